@@ -1,0 +1,232 @@
+/* q38.h — C ABI of the MI355X (gfx950) MTP verification round.
+ *
+ * This is the drop-in boundary: plain C types, device pointers and sizes, no C++ or
+ * torch types. The C++20 host mirror (qwen38::SparseMoe, verify/commit, run round)
+ * sits on top of it; a ctypes binding sits beside it. Every entry point names the
+ * reference interface it replaces (paths relative to the reference checkout).
+ *
+ * Conventions
+ *   - Return 0 on success, a negative Q38_E* code otherwise; q38_last_error() gives a
+ *     thread-local message. No C++ exception crosses this ABI. A failed validation
+ *     leaves every output and state untouched.
+ *   - Tensors are row-major. bf16 / fp16 values travel as uint16_t bit patterns.
+ *   - Pointers documented as "device" are HBM addresses; all device work is ordered on
+ *     the caller's stream (a hipStream_t passed as void*; NULL = the null stream). The
+ *     only host synchronisation is where the reference reads back token ids.
+ *   - Handles own the memory they allocate; callers own their I/O buffers.
+ *   - One layer / head handle may be used by one stream at a time.
+ */
+#ifndef Q38_H
+#define Q38_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    Q38_OK = 0,
+    Q38_EINVAL = -1,  /* bad argument / shape                 (std::runtime_error) */
+    Q38_ERANGE = -2,  /* out of range (short packed buffer)   (std::out_of_range)  */
+    Q38_EHIP = -3,    /* HIP runtime failure */
+    Q38_ENOMEM = -4,  /* allocation failure */
+    Q38_ESTATE = -5,  /* invalid lifecycle / commit request   (std::runtime_error) */
+    Q38_ESPACE = -6   /* workspace too small */
+};
+
+typedef struct q38_ctx q38_ctx;
+typedef struct q38_moe_layer q38_moe_layer;
+typedef struct q38_head q38_head;
+typedef struct q38_slot q38_slot;
+
+/* Codebook storage formats. */
+enum { Q38_CB_FP16 = 0, Q38_CB_INT8_SCALED = 1 };
+
+/* Layer description. Mirrors the SparseMoe constructor arguments
+ * (include/qwen38/sparse_moe.hpp:48-55) plus the VQ geometry of the projection tensors
+ * (src/sparse_moe.cpp:618-661, include/qwen38/quantization_geometry.hpp:12-17). */
+typedef struct q38_moe_desc {
+    int32_t hidden;        /* H, multiple of 512 (2048; 2560 in the reference family) */
+    int32_t inter;         /* I, expert intermediate, multiple of 128 (512; 640)      */
+    int32_t experts;       /* E routed experts, multiple of 64, <= 1024 (512)         */
+    int32_t top_k;         /* experts per token, <= 16 (10)                           */
+    int32_t gu_dim, gu_bits;     /* gate/up VQ geometry: (8,14) or (4,8)              */
+    int32_t down_dim, down_bits; /* down VQ geometry:    (8,14) or (4,8)              */
+    int32_t gu_group, down_group;/* scale group along the input; == input = per row   */
+    int32_t normalize_topk;      /* normalize_topk_probability                        */
+    int32_t has_shared;          /* shared expert (expert index E) + sigmoid gate     */
+    int32_t mixed;               /* 1: even experts d4/8-bit FP16 books, odd experts
+                                    d8/14-bit INT8 books with one FP16 scale each     */
+    int32_t reserved;
+} q38_moe_desc;
+
+/* Device tensors of one layer (uniform geometry). The layer adopts the pointers; the
+ * caller keeps them alive for the layer's lifetime. Expert index E is the shared expert.
+ *   router       [E, H] bf16                      (SparseMoe::router_,  sparse_moe.hpp:201)
+ *   shared_gate  [H] bf16 (w_sg)                  (shared_router_,       sparse_moe.hpp:209)
+ *   codes[p]     [E+1, OUT_p, words_p] u32, words_p = ceil(IN_p/D/32)*BITS
+ *   scales[p]    [E+1, OUT_p, IN_p/G_p] fp16
+ *   books[p]     [2^BITS, D] fp16
+ * p = 0 gate, 1 up, 2 down. */
+typedef struct q38_moe_weights {
+    const uint16_t* router;
+    const uint16_t* shared_gate;
+    const uint32_t* codes[3];
+    const uint16_t* scales[3];
+    const uint16_t* books[3];
+} q38_moe_weights;
+
+/* Routing outputs (optional, device). */
+typedef struct q38_route_out {
+    int32_t* experts;   /* [rows*k] ids in rank order                                  */
+    float* weights;     /* [rows*k]                                                    */
+    float* logits;      /* [rows*E] router logits (BF16 values widened to float)       */
+    int32_t* plan;      /* [1 + 4*rows*k + 1]: n_unique, uexp[rows*k], uoff[rows*k+1],
+                           route_list[rows*k], route_pos[rows*k]                       */
+    uint16_t* x_norm;   /* [rows*H] the normalised layer input (chain mode)            */
+} q38_route_out;
+
+/* ------------------------------------------------------------------ context */
+int q38_ctx_create(int hip_device, q38_ctx** out);
+void q38_ctx_destroy(q38_ctx* ctx);
+const char* q38_last_error(void);
+const char* q38_version(void);
+
+/* ------------------------------------------------------------------ geometry (host)
+ * packed_vq_word_count / unpack_vq_code: src/quantization_geometry.cpp:37-67.
+ * supports_segmented_vq: include/qwen38/quantization_geometry.hpp:12-17. */
+int64_t q38_packed_vq_word_count(int64_t code_count, int bits_per_code);
+int q38_unpack_vq_code(const uint32_t* words, int64_t n_words, int64_t code_index, int bits_per_code,
+                       uint32_t* out);
+int q38_supports_segmented_vq(int dimension, int packed_bits);
+
+/* ------------------------------------------------------------------ MoE layer
+ * Replaces SparseMoe (include/qwen38/sparse_moe.hpp:46-214). */
+int q38_moe_layer_create(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_weights* weights,
+                         q38_moe_layer** out);
+/* Library-owned synthetic layer: every tensor generated from (seed, layer_index) by the
+ * counter-based generator, on the device. */
+int q38_moe_layer_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, uint64_t seed,
+                                   int32_t layer_index, q38_moe_layer** out);
+void q38_moe_layer_destroy(q38_moe_layer* layer);
+/* Device pointers of a layer's tensors (uniform geometry) for inspection. */
+int q38_moe_layer_weights(const q38_moe_layer* layer, q38_moe_weights* out);
+/* Algorithmic HBM bytes of one forward that touches n_unique routed experts. */
+int64_t q38_moe_layer_bytes(const q38_moe_layer* layer, int32_t n_unique, int32_t rows);
+/* Workspace bytes needed by q38_moe_forward / q38_verify_chain for up to max_rows rows. */
+size_t q38_moe_workspace_size(const q38_moe_desc* desc, int32_t max_rows);
+
+/* Router only (R1-R3): SparseMoe::route_decode_batch (src/sparse_moe.cpp:1032-1086) and
+ * the gather-by-expert plan (src/sparse_moe.cpp:2260-2364). x: device [rows, H] bf16. */
+int q38_moe_route(q38_moe_layer* layer, const uint16_t* x, int32_t rows, const q38_route_out* routes,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* SparseMoe::forward_verify (src/sparse_moe.cpp:1953-2171, 2199-2624): y = routed + shared
+ * for rows 1..16 of x. x, y: device [rows, H] bf16 (may not alias). */
+int q38_moe_forward(q38_moe_layer* layer, const uint16_t* x, int32_t rows, uint16_t* y,
+                    const q38_route_out* routes, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The verify pass through a stack of MoE layers (QwenModel::forward_verify_layer_major_
+ * reference, src/model.cpp:386-441, with the HyperConnection/attention parts replaced by
+ * a pre-norm residual): for each layer h <- h + MoE(RMSNorm(h)). h: device [rows, H]
+ * bf16, updated in place. traces (optional): per-layer route outputs, array of n_layers. */
+int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows,
+                     float eps, const q38_route_out* traces, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* Phase timings of a profiled verify pass (MoeVerifyTimings, include/qwen38/sparse_moe.hpp:
+ * 30-36), summed over layers, in milliseconds of device time between HIP events placed
+ * around each launch (the events serialise the phases; use for attribution only). */
+typedef struct q38_moe_timings {
+    double routing_ms;   /* RMSNorm + router logits + top-k + plan */
+    double gate_up_ms;
+    double down_ms;
+    double merge_ms;     /* ordered route reduction + shared gate + residual */
+    int32_t layers;
+    int32_t reserved;
+} q38_moe_timings;
+int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows,
+                              float eps, const q38_route_out* traces, void* workspace, size_t workspace_bytes,
+                              q38_moe_timings* timings, void* stream);
+
+/* RMSNorm with unit gamma, y = T(x / sqrt(mean(x^2) + eps)); device [rows, H] bf16. */
+int q38_rmsnorm(const uint16_t* x, int32_t rows, int32_t hidden, float eps, uint16_t* y, void* stream);
+
+/* Synthetic token embedding (stands in for QwenModel::embed, src/model.cpp:410-414):
+ * row r = N(0,1) bf16 values keyed by (seed, token r). h: device [n, H]. */
+int q38_embed_synthetic(uint64_t seed, const uint32_t* tokens_host, int32_t n, int32_t hidden, uint16_t* h,
+                        void* stream);
+
+/* ------------------------------------------------------------------ LM heads
+ * Target head (src/model.cpp:466-492): symmetric int8 [V, H] + one FP16 scale per row.
+ * Draft head (devtools/build_mtp_lm_head_q4.py:60-92): signed int4 (two per byte, low
+ * nibble first) [V, H/2] + FP16 scales [V, H/64]. */
+enum { Q38_HEAD_Q8 = 0, Q38_HEAD_Q4G64 = 1 };
+int q38_head_create(q38_ctx* ctx, int kind, int64_t vocab, int32_t hidden, const void* weights,
+                    const uint16_t* scales, q38_head** out);
+int q38_head_create_synthetic(q38_ctx* ctx, int kind, int64_t vocab, int32_t hidden, uint64_t seed,
+                              q38_head** out);
+void q38_head_destroy(q38_head* head);
+int q38_head_weights(const q38_head* head, const void** weights, const uint16_t** scales);
+int64_t q38_head_bytes(const q38_head* head);
+size_t q38_head_workspace_size(const q38_head* head, int32_t max_rows);
+
+/* greedy_batch_from_logits (src/mtp_verifier.cpp:30-55): per row the argmax (lowest index
+ * on ties) of the exact logit contract, and that logit. h: device [rows, H] bf16 (rows
+ * <= 16); argmax, logit: device [rows]. Q8 heads only. */
+int q38_head_greedy(q38_head* head, const uint16_t* h, int32_t rows, uint32_t* argmax, float* logit,
+                    void* workspace, size_t workspace_bytes, void* stream);
+/* Raw logits (fast path, float) of either head: device [rows, V]. */
+int q38_head_logits(q38_head* head, const uint16_t* h, int32_t rows, float* logits, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ acceptance
+ * decide_mtp_greedy (src/mtp_lifecycle.cpp:75-97), host. */
+typedef struct q38_greedy_decision {
+    int64_t accepted;
+    int64_t correction_row;
+    uint32_t next_token;
+} q38_greedy_decision;
+int q38_mtp_decide_greedy(const uint32_t* drafts, int64_t k, const uint32_t* target_rows, int64_t n_target,
+                          const uint32_t* stop_tokens, int64_t n_stop, q38_greedy_decision* out);
+
+/* plan_mtp_commit (src/mtp_lifecycle.cpp:57-73), host. out: {truncate_head_to,
+ * target_rows_to_keep, stash_rows, committed_boundary}. */
+int q38_plan_mtp_commit(uint64_t round_offset, uint64_t drafted, uint64_t accepted, uint64_t* out);
+
+/* Rejection-sampling acceptance on the device (no counterpart in the reference, which
+ * bypasses MTP when sampling: src/native_engine.cpp:943-945). target_logits [k+1, V],
+ * draft_logits [k, V] (device float), drafts (device u32 [k]); uniforms from
+ * Philox4x32-10 keyed by (seed; position, round, slot). out: device int64 [2] =
+ * {accepted, next_token}. */
+int q38_mtp_accept_sampled(const float* target_logits, const float* draft_logits, const uint32_t* drafts,
+                           int32_t k, int64_t vocab, float temperature, uint64_t seed, uint64_t slot,
+                           uint64_t round, int64_t* out, void* stream);
+/* Philox4x32-10 (host), for checking the device stream. */
+void q38_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
+/* ------------------------------------------------------------------ per-slot state
+ * The slot keeps the committed length and the committed hidden row of a request;
+ * verification rows are its speculative checkpoints (MtpTargetVerification,
+ * include/qwen38/mtp_verifier.hpp:15-25). */
+int q38_slot_create(q38_ctx* ctx, int32_t hidden, int32_t max_rows, uint64_t token_count, q38_slot** out);
+void q38_slot_destroy(q38_slot* slot);
+/* Record a verification of draft_count drafts: rows = draft_count + 1 checkpoints whose
+ * hidden rows are h (device [rows, H] bf16, copied on stream). */
+int q38_slot_stage(q38_slot* slot, int32_t draft_count, const uint16_t* h, void* stream);
+/* commit_mtp_target_verification (src/mtp_verifier.cpp:129-145): keep checkpoint
+ * `accepted`; token_count becomes origin + accepted + 1; all staged rows are released.
+ * Invalid counts return Q38_ESTATE and leave the slot untouched. */
+int q38_slot_commit(q38_slot* slot, int64_t accepted, void* stream);
+/* Drop the staged rows, keeping the committed state. */
+int q38_slot_rollback(q38_slot* slot);
+int q38_slot_info(const q38_slot* slot, uint64_t* token_count, int32_t* staged_rows, int32_t* draft_count);
+/* Committed hidden row (device [H] bf16), valid after the first commit. */
+const uint16_t* q38_slot_hidden(const q38_slot* slot);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q38_H */

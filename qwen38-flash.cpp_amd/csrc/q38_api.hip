@@ -1,0 +1,675 @@
+// q38_api.hip — the C ABI (include/q38.h): handle lifetime, validation, workspace
+// carving and kernel launches. No exception crosses the ABI; every failure returns a
+// Q38_E* code and leaves outputs untouched.
+#include "q38.h"
+
+#include "q38_device.hpp"
+#include "q38_internal.hpp"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace q38;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+int hip_fail(hipError_t e, const char* where) {
+    g_error = std::string(where) + ": " + hipGetErrorString(e);
+    return Q38_EHIP;
+}
+#define Q38_HIP(expr)                                   \
+    do {                                                \
+        const hipError_t e_ = (expr);                   \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr); \
+    } while (0)
+
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+int64_t words_for(int64_t n, int bits) { return ((n + 31) / 32) * bits; }
+
+} // namespace
+
+struct q38_ctx {
+    int device;
+};
+
+struct q38_moe_layer {
+    q38_ctx* ctx;
+    q38_moe_desc desc;
+    LayerDev dev;
+    void* owned = nullptr;
+    size_t owned_bytes = 0;
+};
+
+struct q38_head {
+    q38_ctx* ctx;
+    HeadDev dev;
+    void* owned = nullptr;
+    size_t owned_bytes = 0;
+};
+
+struct q38_slot {
+    q38_ctx* ctx;
+    int hidden, max_rows;
+    uint64_t token_count;
+    int staged_rows = 0;
+    int draft_count = 0;
+    bool has_hidden = false;
+    uint16_t* committed = nullptr;  // [H]
+    uint16_t* staged = nullptr;     // [max_rows, H]
+};
+
+extern "C" {
+
+const char* q38_last_error(void) { return g_error.c_str(); }
+const char* q38_version(void) { return "q38 0.1 gfx950"; }
+
+int q38_ctx_create(int hip_device, q38_ctx** out) {
+    if (!out) return fail(Q38_EINVAL, "q38_ctx_create: null output");
+    int n = 0;
+    Q38_HIP(hipGetDeviceCount(&n));
+    if (hip_device < 0 || hip_device >= n) return fail(Q38_EINVAL, "q38_ctx_create: no such HIP device");
+    Q38_HIP(hipSetDevice(hip_device));
+    *out = new q38_ctx{hip_device};
+    return Q38_OK;
+}
+void q38_ctx_destroy(q38_ctx* ctx) { delete ctx; }
+
+// ------------------------------------------------------------------ geometry
+int64_t q38_packed_vq_word_count(int64_t code_count, int bits) {
+    if (bits <= 0 || bits > 31 || code_count < 0) {
+        g_error = "packed VQ codes must use 1 to 31 bits";
+        return Q38_EINVAL;
+    }
+    return words_for(code_count, bits);
+}
+int q38_unpack_vq_code(const uint32_t* words, int64_t n_words, int64_t index, int bits, uint32_t* out) {
+    if (bits <= 0 || bits > 31 || index < 0 || !out || (!words && n_words > 0))
+        return fail(Q38_EINVAL, "packed VQ codes must use 1 to 31 bits");
+    if (n_words < words_for(index + 1, bits)) return fail(Q38_ERANGE, "packed VQ code is out of range");
+    const int64_t bit = (index % 32) * bits;
+    const int64_t w = (index / 32) * bits + bit / 32;
+    const int sh = static_cast<int>(bit % 32);
+    uint64_t v = static_cast<uint64_t>(words[w]) >> sh;
+    if (sh + bits > 32) v |= static_cast<uint64_t>(words[w + 1]) << (32 - sh);
+    *out = static_cast<uint32_t>(v & ((uint64_t{1} << bits) - 1));
+    return Q38_OK;
+}
+int q38_supports_segmented_vq(int d, int bits) {
+    return (d == 2 && bits == 0) || (d == 4 && bits == 8) || (d == 8 && bits == 14);
+}
+
+// ------------------------------------------------------------------ MoE layer
+static int validate_desc(const q38_moe_desc* d) {
+    if (!d) return fail(Q38_EINVAL, "null layer description");
+    if (d->hidden <= 0 || d->hidden % 512) return fail(Q38_EINVAL, "hidden size must be a positive multiple of 512");
+    if (d->inter <= 0 || d->inter % 128) return fail(Q38_EINVAL, "expert intermediate size must be a positive multiple of 128");
+    if (d->experts < 64 || d->experts > 1024 || d->experts % 64)
+        return fail(Q38_EINVAL, "routed expert count must be a multiple of 64 in [64, 1024]");
+    if (d->top_k < 1 || d->top_k > kMaxTopK || d->top_k > d->experts)
+        return fail(Q38_EINVAL, "experts per token must be in [1, 16]");
+    if (d->mixed) return fail(Q38_EINVAL, "mixed VQ geometry is not supported by this build");
+    const int geo[2][2] = {{d->gu_dim, d->gu_bits}, {d->down_dim, d->down_bits}};
+    for (auto& g : geo)
+        if (!((g[0] == 8 && g[1] == 14) || (g[0] == 4 && g[1] == 8)))
+            return fail(Q38_EINVAL, "VQ geometry must be d8/14-bit or d4/8-bit");
+    // scale groups: one per row, or groups that tile 16-code lane spans
+    const int ins[2] = {d->hidden, d->inter};
+    const int grp[2] = {d->gu_group, d->down_group};
+    for (int p = 0; p < 2; ++p) {
+        const int G = grp[p], D = geo[p][0];
+        if (G <= 0 || ins[p] % G) return fail(Q38_EINVAL, "scale group must divide the projection input");
+        if (G != ins[p] && (G % D || 16 % (G / D))) return fail(Q38_EINVAL, "unsupported scale group size");
+    }
+    return Q38_OK;
+}
+
+static void fill_dev(q38_moe_layer* L, const q38_moe_weights* w) {
+    const q38_moe_desc& d = L->desc;
+    LayerDev& v = L->dev;
+    v.router = w->router;
+    v.wsg = w->shared_gate;
+    v.H = d.hidden;
+    v.I = d.inter;
+    v.E = d.experts;
+    v.K = d.top_k;
+    v.normalize = d.normalize_topk;
+    v.has_shared = d.has_shared;
+    for (int p = 0; p < 3; ++p) {
+        const int in = p < 2 ? d.hidden : d.inter;
+        const int dim = p < 2 ? d.gu_dim : d.down_dim;
+        const int bits = p < 2 ? d.gu_bits : d.down_bits;
+        const int grp = p < 2 ? d.gu_group : d.down_group;
+        v.p[p].codes = w->codes[p];
+        v.p[p].scales = w->scales[p];
+        v.p[p].book = w->books[p];
+        v.p[p].words = static_cast<int>(words_for(in / dim, bits));
+        v.p[p].ngrp = in / grp;
+        v.p[p].dim = dim;
+        v.p[p].bits = bits;
+    }
+}
+
+int q38_moe_layer_create(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_weights* weights,
+                         q38_moe_layer** out) {
+    if (!ctx || !out || !weights) return fail(Q38_EINVAL, "q38_moe_layer_create: null argument");
+    if (int rc = validate_desc(desc)) return rc;
+    if (!weights->router || (desc->has_shared && !weights->shared_gate))
+        return fail(Q38_EINVAL, "router / shared gate tensors are required");
+    for (int p = 0; p < 3; ++p)
+        if (!weights->codes[p] || !weights->scales[p] || !weights->books[p])
+            return fail(Q38_EINVAL, "every projection needs codes, scales and a codebook");
+    auto* L = new q38_moe_layer{ctx, *desc, {}, nullptr, 0};
+    fill_dev(L, weights);
+    *out = L;
+    return Q38_OK;
+}
+
+struct SynthLayout {
+    size_t router, wsg, book[3], codes[3], scales[3], total;
+};
+static SynthLayout synth_layout(const q38_moe_desc& d) {
+    SynthLayout s{};
+    size_t off = 0;
+    const int E1 = d.experts + 1;
+    s.router = off; off += align256(static_cast<size_t>(d.experts) * d.hidden * 2);
+    s.wsg = off; off += align256(static_cast<size_t>(d.hidden) * 2);
+    for (int p = 0; p < 3; ++p) {
+        const int in = p < 2 ? d.hidden : d.inter, outd = p < 2 ? d.inter : d.hidden;
+        const int dim = p < 2 ? d.gu_dim : d.down_dim, bits = p < 2 ? d.gu_bits : d.down_bits;
+        const int grp = p < 2 ? d.gu_group : d.down_group;
+        s.book[p] = off; off += align256((static_cast<size_t>(1) << bits) * dim * 2);
+        s.codes[p] = off; off += align256(static_cast<size_t>(E1) * outd * words_for(in / dim, bits) * 4);
+        s.scales[p] = off; off += align256(static_cast<size_t>(E1) * outd * (in / grp) * 2);
+    }
+    s.total = off;
+    return s;
+}
+
+int q38_moe_layer_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, uint64_t seed, int32_t layer_index,
+                                   q38_moe_layer** out) {
+    if (!ctx || !out) return fail(Q38_EINVAL, "q38_moe_layer_create_synthetic: null argument");
+    if (int rc = validate_desc(desc)) return rc;
+    const q38_moe_desc& d = *desc;
+    const SynthLayout s = synth_layout(d);
+    char* base = nullptr;
+    if (hipMalloc(&base, s.total) != hipSuccess) return fail(Q38_ENOMEM, "hipMalloc failed for a synthetic layer");
+    const hipStream_t st = nullptr;
+    const uint64_t layer = static_cast<uint64_t>(layer_index);
+    auto* r = reinterpret_cast<uint16_t*>(base + s.router);
+    auto* ws = reinterpret_cast<uint16_t*>(base + s.wsg);
+    hipError_t e = launch_gen_normal(stream_key(seed, layer, T_ROUTER), static_cast<int64_t>(d.experts) * d.hidden,
+                                     0.02, 0, r, st);
+    if (e == hipSuccess) e = launch_gen_normal(stream_key(seed, layer, T_WSG), d.hidden, 0.02, 0, ws, st);
+    const uint64_t tb[3] = {T_CB_GATE, T_CB_UP, T_CB_DOWN};
+    const uint64_t tc[3] = {T_CODES_GATE, T_CODES_UP, T_CODES_DOWN};
+    const uint64_t ts[3] = {T_SCALE_GATE, T_SCALE_UP, T_SCALE_DOWN};
+    q38_moe_weights w{};
+    w.router = r;
+    w.shared_gate = ws;
+    for (int p = 0; p < 3 && e == hipSuccess; ++p) {
+        const int in = p < 2 ? d.hidden : d.inter, outd = p < 2 ? d.inter : d.hidden;
+        const int dim = p < 2 ? d.gu_dim : d.down_dim, bits = p < 2 ? d.gu_bits : d.down_bits;
+        const int grp = p < 2 ? d.gu_group : d.down_group;
+        auto* book = reinterpret_cast<uint16_t*>(base + s.book[p]);
+        auto* codes = reinterpret_cast<uint32_t*>(base + s.codes[p]);
+        auto* scales = reinterpret_cast<uint16_t*>(base + s.scales[p]);
+        e = launch_gen_normal(stream_key(seed, layer, tb[p]), (int64_t{1} << bits) * dim, 1.0, 1, book, st);
+        if (e == hipSuccess)
+            e = launch_gen_codes(stream_key(seed, layer, tc[p]), 0, d.experts + 1, outd, in / dim, bits,
+                                 static_cast<int>(words_for(in / dim, bits)), codes, st);
+        if (e == hipSuccess)
+            e = launch_gen_uniform_f16(stream_key(seed, layer, ts[p]), 0,
+                                       static_cast<int64_t>(d.experts + 1) * outd * (in / grp), 0.005, 0.02, scales,
+                                       st);
+        w.codes[p] = codes;
+        w.scales[p] = scales;
+        w.books[p] = book;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        (void)hipFree(base);
+        return hip_fail(e, "synthetic layer generation");
+    }
+    auto* L = new q38_moe_layer{ctx, d, {}, base, s.total};
+    fill_dev(L, &w);
+    *out = L;
+    return Q38_OK;
+}
+
+void q38_moe_layer_destroy(q38_moe_layer* layer) {
+    if (!layer) return;
+    if (layer->owned) (void)hipFree(layer->owned);
+    delete layer;
+}
+
+int q38_moe_layer_weights(const q38_moe_layer* L, q38_moe_weights* out) {
+    if (!L || !out) return fail(Q38_EINVAL, "null argument");
+    out->router = L->dev.router;
+    out->shared_gate = L->dev.wsg;
+    for (int p = 0; p < 3; ++p) {
+        out->codes[p] = L->dev.p[p].codes;
+        out->scales[p] = L->dev.p[p].scales;
+        out->books[p] = L->dev.p[p].book;
+    }
+    return Q38_OK;
+}
+
+int64_t q38_moe_layer_bytes(const q38_moe_layer* L, int32_t n_unique, int32_t rows) {
+    if (!L) return Q38_EINVAL;
+    const LayerDev& v = L->dev;
+    int64_t per_expert = 0, books = 0;
+    for (int p = 0; p < 3; ++p) {
+        const int outd = p < 2 ? v.I : v.H;
+        per_expert += static_cast<int64_t>(outd) * v.p[p].words * 4 + static_cast<int64_t>(outd) * v.p[p].ngrp * 2;
+        books += (int64_t{1} << v.p[p].bits) * v.p[p].dim * 2;
+    }
+    const int64_t experts = static_cast<int64_t>(n_unique) + (v.has_shared ? 1 : 0);
+    return experts * per_expert + books + static_cast<int64_t>(v.E) * v.H * 2 + (v.has_shared ? v.H * 2 : 0) +
+           static_cast<int64_t>(2) * rows * v.H * 2;
+}
+
+struct MoeWork {
+    uint16_t* xn;
+    float* logits;
+    float* sgate;
+    int32_t* experts;
+    float* weights;
+    int32_t* plan;
+    uint16_t* hbuf;
+    uint16_t* dbuf;
+};
+static size_t moe_ws(const q38_moe_desc& d, int M, MoeWork* w, void* base) {
+    const int MK = M * d.top_k;
+    size_t off = 0;
+    char* b = static_cast<char*>(base);
+    auto take = [&](size_t bytes) {
+        char* p = b ? b + off : nullptr;
+        off += align256(bytes);
+        return p;
+    };
+    MoeWork t{};
+    t.xn = reinterpret_cast<uint16_t*>(take(static_cast<size_t>(M) * d.hidden * 2));
+    t.logits = reinterpret_cast<float*>(take(static_cast<size_t>(M) * d.experts * 4));
+    t.sgate = reinterpret_cast<float*>(take(static_cast<size_t>(M) * 4));
+    t.experts = reinterpret_cast<int32_t*>(take(static_cast<size_t>(MK) * 4));
+    t.weights = reinterpret_cast<float*>(take(static_cast<size_t>(MK) * 4));
+    t.plan = reinterpret_cast<int32_t*>(take(static_cast<size_t>(2 + 4 * MK) * 4));
+    t.hbuf = reinterpret_cast<uint16_t*>(take(static_cast<size_t>(MK + M) * d.inter * 2));
+    t.dbuf = reinterpret_cast<uint16_t*>(take(static_cast<size_t>(MK + M) * d.hidden * 2));
+    if (w) *w = t;
+    return off;
+}
+
+size_t q38_moe_workspace_size(const q38_moe_desc* desc, int32_t max_rows) {
+    if (!desc || max_rows < 1 || max_rows > kMaxRows) return 0;
+    return moe_ws(*desc, max_rows, nullptr, nullptr);
+}
+
+static int check_rows(int rows) {
+    if (rows < 1 || rows > kMaxRows) return fail(Q38_EINVAL, "verify rows must be between 1 and 16");
+    return Q38_OK;
+}
+
+static int copy_routes(const q38_moe_layer* L, int M, const MoeWork& w, const q38_route_out* r, hipStream_t st) {
+    if (!r) return Q38_OK;
+    const int MK = M * L->desc.top_k;
+    if (r->experts) Q38_HIP(hipMemcpyAsync(r->experts, w.experts, MK * 4, hipMemcpyDeviceToDevice, st));
+    if (r->weights) Q38_HIP(hipMemcpyAsync(r->weights, w.weights, MK * 4, hipMemcpyDeviceToDevice, st));
+    if (r->logits)
+        Q38_HIP(hipMemcpyAsync(r->logits, w.logits, static_cast<size_t>(M) * L->desc.experts * 4,
+                               hipMemcpyDeviceToDevice, st));
+    if (r->plan) Q38_HIP(hipMemcpyAsync(r->plan, w.plan, (2 + 4 * MK) * 4, hipMemcpyDeviceToDevice, st));
+    if (r->x_norm)
+        Q38_HIP(hipMemcpyAsync(r->x_norm, w.xn, static_cast<size_t>(M) * L->desc.hidden * 2,
+                               hipMemcpyDeviceToDevice, st));
+    return Q38_OK;
+}
+
+int q38_moe_route(q38_moe_layer* L, const uint16_t* x, int32_t rows, const q38_route_out* routes, void* ws,
+                  size_t ws_bytes, void* stream) {
+    if (!L || !x) return fail(Q38_EINVAL, "q38_moe_route: null argument");
+    if (int rc = check_rows(rows)) return rc;
+    MoeWork w{};
+    if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    Q38_HIP(launch_router(L->dev, x, rows, 0, 0.0f, nullptr, w.logits, w.sgate, st));
+    Q38_HIP(launch_topk_plan(L->dev, w.logits, rows, w.experts, w.weights, w.plan, st));
+    return copy_routes(L, rows, w, routes, st);
+}
+
+int q38_moe_forward(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t* y, const q38_route_out* routes,
+                    void* ws, size_t ws_bytes, void* stream) {
+    if (!L || !x || !y) return fail(Q38_EINVAL, "q38_moe_forward: null argument");
+    if (x == y) return fail(Q38_EINVAL, "q38_moe_forward: input and output must not alias");
+    if (int rc = check_rows(rows)) return rc;
+    MoeWork w{};
+    if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    Q38_HIP(launch_router(L->dev, x, rows, 0, 0.0f, nullptr, w.logits, w.sgate, st));
+    Q38_HIP(launch_topk_plan(L->dev, w.logits, rows, w.experts, w.weights, w.plan, st));
+    Q38_HIP(launch_gate_up(L->dev, x, rows, w.plan, w.hbuf, st));
+    Q38_HIP(launch_down(L->dev, rows, w.plan, w.hbuf, w.dbuf, st));
+    Q38_HIP(launch_combine(L->dev, rows, w.plan, w.weights, w.sgate, w.dbuf, nullptr, y, st));
+    return copy_routes(L, rows, w, routes, st);
+}
+
+int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows, float eps,
+                     const q38_route_out* traces, void* ws, size_t ws_bytes, void* stream) {
+    if (!layers || n_layers < 1 || !h) return fail(Q38_EINVAL, "q38_verify_chain: bad arguments");
+    if (int rc = check_rows(rows)) return rc;
+    size_t need = 0;
+    for (int l = 0; l < n_layers; ++l) {
+        if (!layers[l]) return fail(Q38_EINVAL, "q38_verify_chain: null layer");
+        if (layers[l]->desc.hidden != layers[0]->desc.hidden)
+            return fail(Q38_EINVAL, "q38_verify_chain: layers disagree on the hidden size");
+        need = std::max(need, moe_ws(layers[l]->desc, rows, nullptr, nullptr));
+    }
+    if (!ws || ws_bytes < need) return fail(Q38_ESPACE, "workspace too small");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    for (int l = 0; l < n_layers; ++l) {
+        q38_moe_layer* L = layers[l];
+        MoeWork w{};
+        moe_ws(L->desc, rows, &w, ws);
+        Q38_HIP(launch_router(L->dev, h, rows, 1, eps, w.xn, w.logits, w.sgate, st));
+        Q38_HIP(launch_topk_plan(L->dev, w.logits, rows, w.experts, w.weights, w.plan, st));
+        Q38_HIP(launch_gate_up(L->dev, w.xn, rows, w.plan, w.hbuf, st));
+        Q38_HIP(launch_down(L->dev, rows, w.plan, w.hbuf, w.dbuf, st));
+        Q38_HIP(launch_combine(L->dev, rows, w.plan, w.weights, w.sgate, w.dbuf, h, h, st));
+        if (traces)
+            if (int rc = copy_routes(L, rows, w, &traces[l], st)) return rc;
+    }
+    return Q38_OK;
+}
+
+int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows, float eps,
+                              const q38_route_out* traces, void* ws, size_t ws_bytes, q38_moe_timings* tm,
+                              void* stream) {
+    if (!tm) return fail(Q38_EINVAL, "q38_verify_chain_profiled: null timings");
+    if (!layers || n_layers < 1 || !h) return fail(Q38_EINVAL, "q38_verify_chain_profiled: bad arguments");
+    if (int rc = check_rows(rows)) return rc;
+    size_t need = 0;
+    for (int l = 0; l < n_layers; ++l) {
+        if (!layers[l]) return fail(Q38_EINVAL, "q38_verify_chain_profiled: null layer");
+        need = std::max(need, moe_ws(layers[l]->desc, rows, nullptr, nullptr));
+    }
+    if (!ws || ws_bytes < need) return fail(Q38_ESPACE, "workspace too small");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    std::vector<hipEvent_t> ev(static_cast<size_t>(n_layers) * 5, nullptr);
+    for (auto& e : ev) Q38_HIP(hipEventCreate(&e));
+    int rc = Q38_OK;
+    for (int l = 0; l < n_layers && rc == Q38_OK; ++l) {
+        q38_moe_layer* L = layers[l];
+        MoeWork w{};
+        moe_ws(L->desc, rows, &w, ws);
+        hipEvent_t* E = &ev[static_cast<size_t>(l) * 5];
+        hipError_t e = hipEventRecord(E[0], st);
+        if (e == hipSuccess) e = launch_router(L->dev, h, rows, 1, eps, w.xn, w.logits, w.sgate, st);
+        if (e == hipSuccess) e = launch_topk_plan(L->dev, w.logits, rows, w.experts, w.weights, w.plan, st);
+        if (e == hipSuccess) e = hipEventRecord(E[1], st);
+        if (e == hipSuccess) e = launch_gate_up(L->dev, w.xn, rows, w.plan, w.hbuf, st);
+        if (e == hipSuccess) e = hipEventRecord(E[2], st);
+        if (e == hipSuccess) e = launch_down(L->dev, rows, w.plan, w.hbuf, w.dbuf, st);
+        if (e == hipSuccess) e = hipEventRecord(E[3], st);
+        if (e == hipSuccess) e = launch_combine(L->dev, rows, w.plan, w.weights, w.sgate, w.dbuf, h, h, st);
+        if (e == hipSuccess) e = hipEventRecord(E[4], st);
+        if (e != hipSuccess) rc = hip_fail(e, "profiled verify pass");
+        if (rc == Q38_OK && traces) rc = copy_routes(L, rows, w, &traces[l], st);
+    }
+    if (rc == Q38_OK) {
+        hipError_t e = hipEventSynchronize(ev.back());
+        q38_moe_timings t{};
+        for (int l = 0; l < n_layers && e == hipSuccess; ++l) {
+            hipEvent_t* E = &ev[static_cast<size_t>(l) * 5];
+            float ms[4];
+            for (int i = 0; i < 4 && e == hipSuccess; ++i) e = hipEventElapsedTime(&ms[i], E[i], E[i + 1]);
+            t.routing_ms += ms[0];
+            t.gate_up_ms += ms[1];
+            t.down_ms += ms[2];
+            t.merge_ms += ms[3];
+        }
+        t.layers = n_layers;
+        if (e != hipSuccess) rc = hip_fail(e, "profiled verify timings");
+        else *tm = t;
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    return rc;
+}
+
+int q38_rmsnorm(const uint16_t* x, int32_t rows, int32_t hidden, float eps, uint16_t* y, void* stream) {
+    if (!x || !y || rows < 1 || hidden < 1) return fail(Q38_EINVAL, "q38_rmsnorm: bad arguments");
+    Q38_HIP(launch_rmsnorm(x, rows, hidden, eps, y, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+int q38_embed_synthetic(uint64_t seed, const uint32_t* tokens, int32_t n, int32_t hidden, uint16_t* h,
+                        void* stream) {
+    if (!tokens || !h || n < 1 || n > 32 || hidden < 1) return fail(Q38_EINVAL, "q38_embed_synthetic: bad arguments");
+    Q38_HIP(launch_gen_embed(seed, tokens, n, hidden, h, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+// ------------------------------------------------------------------ heads
+static int head_validate(int kind, int64_t vocab, int hidden) {
+    if (kind != Q38_HEAD_Q8 && kind != Q38_HEAD_Q4G64) return fail(Q38_EINVAL, "unknown head kind");
+    if (vocab < 1 || vocab > (int64_t{1} << 31) - 2) return fail(Q38_EINVAL, "vocab out of range");
+    if (kind == Q38_HEAD_Q8 && hidden != 1024 && hidden != 2048 && hidden != 2560)
+        return fail(Q38_EINVAL, "Q8 head hidden size must be 1024, 2048 or 2560");
+    if (kind == Q38_HEAD_Q4G64 && hidden != 2048) return fail(Q38_EINVAL, "Q4 head hidden size must be 2048");
+    return Q38_OK;
+}
+
+static int head_finish(q38_head* hd) {
+    float* d = nullptr;
+    Q38_HIP(hipMalloc(&d, sizeof(float)));
+    const int64_t ns = hd->dev.kind == 0 ? hd->dev.V : hd->dev.V * (hd->dev.H / 64);
+    hipError_t e = launch_scale_absmax(hd->dev.scales, ns, d, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(&hd->dev.s_max, d, sizeof(float), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return hip_fail(e, "head scale scan");
+    return Q38_OK;
+}
+
+int q38_head_create(q38_ctx* ctx, int kind, int64_t vocab, int32_t hidden, const void* weights,
+                    const uint16_t* scales, q38_head** out) {
+    if (!ctx || !out || !weights || !scales) return fail(Q38_EINVAL, "q38_head_create: null argument");
+    if (int rc = head_validate(kind, vocab, hidden)) return rc;
+    auto* hd = new q38_head{ctx, {}, nullptr, 0};
+    hd->dev = HeadDev{static_cast<const int8_t*>(weights), scales, vocab, hidden, kind, 0.0f};
+    if (int rc = head_finish(hd)) {
+        delete hd;
+        return rc;
+    }
+    *out = hd;
+    return Q38_OK;
+}
+
+int q38_head_create_synthetic(q38_ctx* ctx, int kind, int64_t vocab, int32_t hidden, uint64_t seed, q38_head** out) {
+    if (!ctx || !out) return fail(Q38_EINVAL, "q38_head_create_synthetic: null argument");
+    if (int rc = head_validate(kind, vocab, hidden)) return rc;
+    const size_t wbytes = kind == 0 ? static_cast<size_t>(vocab) * hidden : static_cast<size_t>(vocab) * hidden / 2;
+    const size_t sbytes = kind == 0 ? static_cast<size_t>(vocab) * 2 : static_cast<size_t>(vocab) * (hidden / 64) * 2;
+    char* base = nullptr;
+    if (hipMalloc(&base, align256(wbytes) + align256(sbytes)) != hipSuccess)
+        return fail(Q38_ENOMEM, "hipMalloc failed for a synthetic head");
+    auto* w = reinterpret_cast<int8_t*>(base);
+    auto* s = reinterpret_cast<uint16_t*>(base + align256(wbytes));
+    auto* hd = new q38_head{ctx, HeadDev{w, s, vocab, hidden, kind, 0.0f}, base, align256(wbytes) + align256(sbytes)};
+    hipError_t e = launch_gen_head(hd->dev, seed, w, s, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(base);
+        delete hd;
+        return hip_fail(e, "synthetic head generation");
+    }
+    if (int rc = head_finish(hd)) {
+        (void)hipFree(base);
+        delete hd;
+        return rc;
+    }
+    *out = hd;
+    return Q38_OK;
+}
+
+void q38_head_destroy(q38_head* hd) {
+    if (!hd) return;
+    if (hd->owned) (void)hipFree(hd->owned);
+    delete hd;
+}
+
+int q38_head_weights(const q38_head* hd, const void** weights, const uint16_t** scales) {
+    if (!hd) return fail(Q38_EINVAL, "null head");
+    if (weights) *weights = hd->dev.w;
+    if (scales) *scales = hd->dev.scales;
+    return Q38_OK;
+}
+
+int64_t q38_head_bytes(const q38_head* hd) {
+    if (!hd) return Q38_EINVAL;
+    if (hd->dev.kind == 0) return hd->dev.V * hd->dev.H + hd->dev.V * 2;
+    return hd->dev.V * hd->dev.H / 2 + hd->dev.V * (hd->dev.H / 64) * 2;
+}
+
+size_t q38_head_workspace_size(const q38_head* hd, int32_t max_rows) {
+    if (!hd || max_rows < 1 || max_rows > 4) return 0;
+    return head_work_bytes(hd->dev.V, max_rows);
+}
+
+int q38_head_greedy(q38_head* hd, const uint16_t* h, int32_t rows, uint32_t* argmax, float* logit, void* ws,
+                    size_t ws_bytes, void* stream) {
+    if (!hd || !h || !argmax || !logit) return fail(Q38_EINVAL, "q38_head_greedy: null argument");
+    if (hd->dev.kind != Q38_HEAD_Q8) return fail(Q38_EINVAL, "greedy argmax needs a Q8 head");
+    if (rows < 1 || rows > 4) return fail(Q38_EINVAL, "head rows must be between 1 and 4 per call");
+    if (!ws || ws_bytes < head_work_bytes(hd->dev.V, rows)) return fail(Q38_ESPACE, "workspace too small");
+    const HeadWork w = head_work_carve(ws, hd->dev.V, rows);
+    Q38_HIP(launch_head_greedy(hd->dev, h, rows, w, argmax, logit, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+int q38_head_logits(q38_head* hd, const uint16_t* h, int32_t rows, float* logits, void* ws, size_t ws_bytes,
+                    void* stream) {
+    (void)ws;
+    (void)ws_bytes;
+    if (!hd || !h || !logits) return fail(Q38_EINVAL, "q38_head_logits: null argument");
+    if (rows < 1 || rows > 4) return fail(Q38_EINVAL, "head rows must be between 1 and 4 per call");
+    Q38_HIP(launch_head_logits(hd->dev, h, rows, logits, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+// ------------------------------------------------------------------ acceptance
+int q38_mtp_decide_greedy(const uint32_t* drafts, int64_t k, const uint32_t* target, int64_t n_target,
+                          const uint32_t* stop, int64_t n_stop, q38_greedy_decision* out) {
+    if (!out) return fail(Q38_EINVAL, "null output");
+    if (k <= 0 || !drafts) return fail(Q38_EINVAL, "MTP verification requires at least one draft");
+    if (n_target != k + 1 || !target) return fail(Q38_EINVAL, "MTP target verification must include the bonus row");
+    if (n_stop > 0 && !stop) return fail(Q38_EINVAL, "null stop-token list");
+    int64_t a = 0;
+    while (a < k && drafts[a] == target[a]) {
+        bool is_stop = false;
+        for (int64_t s = 0; s < n_stop; ++s) is_stop |= stop[s] == drafts[a];
+        if (is_stop) break;
+        ++a;
+    }
+    out->accepted = a;
+    out->correction_row = a;
+    out->next_token = target[a];
+    return Q38_OK;
+}
+
+int q38_plan_mtp_commit(uint64_t round_offset, uint64_t drafted, uint64_t accepted, uint64_t* out) {
+    if (!out) return fail(Q38_EINVAL, "null output");
+    if (accepted > drafted) return fail(Q38_ESTATE, "MTP accepted count exceeds drafted count");
+    if (accepted == UINT64_MAX || round_offset > UINT64_MAX - (accepted + 1))
+        return fail(Q38_ESTATE, "MTP committed boundary overflow");
+    out[0] = round_offset;
+    out[1] = 1 + accepted;
+    out[2] = 1 + accepted;
+    out[3] = round_offset + 1 + accepted;
+    return Q38_OK;
+}
+
+void q38_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    philox4x32_10(ctr, key, out);
+}
+
+int q38_mtp_accept_sampled(const float* tl, const float* dl, const uint32_t* drafts, int32_t k, int64_t vocab,
+                           float temperature, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out,
+                           void* stream) {
+    if (!tl || !dl || !drafts || !out) return fail(Q38_EINVAL, "q38_mtp_accept_sampled: null argument");
+    if (k < 1 || k > 24 || vocab < 1) return fail(Q38_EINVAL, "q38_mtp_accept_sampled: bad sizes");
+    if (!(temperature > 0.0f)) return fail(Q38_EINVAL, "temperature must be positive");
+    Q38_HIP(launch_accept_sampled(tl, dl, drafts, k, vocab, temperature, seed, slot, round, out,
+                                  static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+// ------------------------------------------------------------------ slots
+int q38_slot_create(q38_ctx* ctx, int32_t hidden, int32_t max_rows, uint64_t token_count, q38_slot** out) {
+    if (!ctx || !out || hidden < 1 || max_rows < 2 || max_rows > 25)
+        return fail(Q38_EINVAL, "q38_slot_create: bad arguments");
+    auto* s = new q38_slot{ctx, hidden, max_rows, token_count};
+    if (hipMalloc(&s->committed, static_cast<size_t>(hidden) * 2) != hipSuccess ||
+        hipMalloc(&s->staged, static_cast<size_t>(max_rows) * hidden * 2) != hipSuccess) {
+        (void)hipFree(s->committed);
+        delete s;
+        return fail(Q38_ENOMEM, "hipMalloc failed for a slot");
+    }
+    *out = s;
+    return Q38_OK;
+}
+void q38_slot_destroy(q38_slot* s) {
+    if (!s) return;
+    (void)hipFree(s->committed);
+    (void)hipFree(s->staged);
+    delete s;
+}
+int q38_slot_stage(q38_slot* s, int32_t draft_count, const uint16_t* h, void* stream) {
+    if (!s || !h) return fail(Q38_EINVAL, "q38_slot_stage: null argument");
+    if (draft_count < 1 || draft_count + 1 > s->max_rows)
+        return fail(Q38_EINVAL, "staged verification exceeds the slot's row capacity");
+    Q38_HIP(hipMemcpyAsync(s->staged, h, static_cast<size_t>(draft_count + 1) * s->hidden * 2,
+                           hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
+    s->staged_rows = draft_count + 1;
+    s->draft_count = draft_count;
+    return Q38_OK;
+}
+int q38_slot_commit(q38_slot* s, int64_t accepted, void* stream) {
+    if (!s) return fail(Q38_EINVAL, "null slot");
+    if (s->staged_rows == 0 || s->staged_rows != s->draft_count + 1)
+        return fail(Q38_ESTATE, "MTP verification row count is invalid");
+    if (accepted < 0 || accepted > s->draft_count)
+        return fail(Q38_ESTATE, "MTP accepted count exceeds verified draft count");
+    Q38_HIP(hipMemcpyAsync(s->committed, s->staged + static_cast<size_t>(accepted) * s->hidden,
+                           static_cast<size_t>(s->hidden) * 2, hipMemcpyDeviceToDevice,
+                           static_cast<hipStream_t>(stream)));
+    s->token_count += static_cast<uint64_t>(accepted) + 1;
+    s->staged_rows = 0;
+    s->draft_count = 0;
+    s->has_hidden = true;
+    return Q38_OK;
+}
+int q38_slot_rollback(q38_slot* s) {
+    if (!s) return fail(Q38_EINVAL, "null slot");
+    s->staged_rows = 0;
+    s->draft_count = 0;
+    return Q38_OK;
+}
+int q38_slot_info(const q38_slot* s, uint64_t* token_count, int32_t* staged_rows, int32_t* draft_count) {
+    if (!s) return fail(Q38_EINVAL, "null slot");
+    if (token_count) *token_count = s->token_count;
+    if (staged_rows) *staged_rows = s->staged_rows;
+    if (draft_count) *draft_count = s->draft_count;
+    return Q38_OK;
+}
+const uint16_t* q38_slot_hidden(const q38_slot* s) { return s && s->has_hidden ? s->committed : nullptr; }
+
+} // extern "C"

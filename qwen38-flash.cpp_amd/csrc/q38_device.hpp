@@ -1,0 +1,177 @@
+// q38_device.hpp — device-side building blocks shared by the gfx950 kernels: number
+// formats, the counter-based synthetic generator, the packed-VQ code reader, the exp
+// contract of the router softmax, and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q38 {
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ number formats
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t x = __float_as_uint(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((x >> 16) | 0x40u);
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return static_cast<uint16_t>(x >> 16);
+}
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+// Two bf16 packed in a u32 -> floats (low half first).
+__device__ __forceinline__ float bflo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// ------------------------------------------------------------------ generator
+// splitmix64 streams keyed by (seed, layer, tensor); element i = mix64(key + golden*(i+1)).
+constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ull;
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__host__ __device__ __forceinline__ uint64_t stream_key(uint64_t seed, uint64_t layer, uint64_t tensor) {
+    return mix64(mix64(mix64(seed) + kGolden * (layer + 1)) + kGolden * (tensor + 1));
+}
+__host__ __device__ __forceinline__ uint64_t bits_at(uint64_t key, uint64_t i) { return mix64(key + kGolden * (i + 1)); }
+
+enum Tensor : uint64_t {
+    T_ROUTER = 1, T_WSG = 2, T_CB_GATE = 3, T_CB_UP = 4, T_CB_DOWN = 5,
+    T_CODES_GATE = 6, T_CODES_UP = 7, T_CODES_DOWN = 8,
+    T_SCALE_GATE = 9, T_SCALE_UP = 10, T_SCALE_DOWN = 11,
+    T_CB4_GATE = 12, T_CB4_UP = 13, T_CB4_DOWN = 14,
+    T_X = 20, T_EMBED = 21,
+    T_HEAD_W = 30, T_HEAD_S = 31, T_DRAFT_W = 32, T_DRAFT_S = 33,
+};
+constexpr uint64_t kEmbedLayer = 0xFFFF, kHeadLayer = 0xFFFE, kDraftLayer = 0xFFFD;
+
+// Box-Muller in double from two stream elements.
+__device__ __forceinline__ double normal_at(uint64_t key, uint64_t i) {
+    const double u1 = static_cast<double>((bits_at(key, 2 * i) >> 11) + 1) * 0x1.0p-53;
+    const double u2 = static_cast<double>(bits_at(key, 2 * i + 1) >> 11) * 0x1.0p-53;
+    const double rad = sqrt(-2.0 * log(u1));
+    const double ang = cos(6.283185307179586 * u2);
+    return rad * ang;
+}
+__device__ __forceinline__ float uniform_f32(uint64_t key, uint64_t i, double lo, double hi) {
+#pragma clang fp contract(off)
+    const double u = static_cast<double>(bits_at(key, i) >> 11) * 0x1.0p-53;
+    const double span = hi - lo;
+    const double prod = u * span;
+    const double v = lo + prod;
+    return static_cast<float>(v);
+}
+
+// ------------------------------------------------------------------ packed VQ codes
+// Row layout (src/quantization_geometry.cpp:50-67): 32-code blocks of BITS words,
+// code q of a block at bit q*BITS, LSB-first.
+template <int BITS>
+__device__ __forceinline__ uint32_t code_from(const uint32_t* w, int q) {
+    // w: words of the 16-code half-block (or whole block) that holds code q; bit offset
+    // q*BITS is a compile-time constant after unrolling.
+    const int bit = q * BITS;
+    const int wi = bit >> 5, sh = bit & 31;
+    uint32_t v = w[wi] >> sh;
+    if (sh + BITS > 32) v |= w[wi + 1] << (32 - sh);
+    return v & ((1u << BITS) - 1u);
+}
+
+// ------------------------------------------------------------------ exp contract
+// Cody-Waite reduction + degree-7 Taylor polynomial, evaluated with explicit fmaf so the
+// float operations are identical to the CPU restatement; results below 2^-125 flush to 0.
+__device__ __forceinline__ float exp_contract(float d) {
+    if (!(d > -87.0f)) return 0.0f;
+    const float kf = rintf(d * 1.44269504088896341f);
+    float r = __builtin_fmaf(kf, -0.693145751953125f, d);
+    r = __builtin_fmaf(kf, -1.42860682030941723212e-06f, r);
+    float p = 1.0f / 5040.0f;
+    p = __builtin_fmaf(p, r, 1.0f / 720.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int k = static_cast<int>(kf);
+    if (k < -125) return 0.0f;
+    return ldexpf(p, k);
+}
+
+// ------------------------------------------------------------------ wave reductions
+// xor butterfly: every lane ends with the same value, equal to the pairwise tree
+// ((l, l^32), then ^16, ...) that the CPU restatement reproduces.
+__device__ __forceinline__ float wave_sum_xor(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_xor(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+    return v;
+}
+template <int WIDTH>
+__device__ __forceinline__ float group_sum_xor(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint64_t o = __shfl_xor(v, off, kWave);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// ------------------------------------------------------------------ Philox4x32-10
+// Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3" (SC'11).
+__host__ __device__ __forceinline__ void philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int round = 0; round < 10; ++round) {
+        const uint64_t p0 = static_cast<uint64_t>(0xD2511F53u) * c0;
+        const uint64_t p1 = static_cast<uint64_t>(0xCD9E8D57u) * c2;
+        const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n1 = static_cast<uint32_t>(p1);
+        const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c3 ^ k1;
+        const uint32_t n3 = static_cast<uint32_t>(p0);
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+// Acceptance / resample uniforms of (seed, slot, round, position): counter {position,
+// round lo, round hi, slot}, key {seed lo, seed hi}; u = (x0 >> 8) 2^-24, v = (x1 >> 8) 2^-24.
+__host__ __device__ __forceinline__ void round_uniforms(uint64_t seed, uint64_t slot, uint64_t round, uint32_t pos,
+                                                        float* u, float* v) {
+    const uint32_t ctr[4] = {pos, static_cast<uint32_t>(round), static_cast<uint32_t>(round >> 32),
+                             static_cast<uint32_t>(slot)};
+    const uint32_t key[2] = {static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)};
+    uint32_t out[4];
+    philox4x32_10(ctr, key, out);
+    *u = static_cast<float>(out[0] >> 8) * 0x1.0p-24f;
+    *v = static_cast<float>(out[1] >> 8) * 0x1.0p-24f;
+}
+
+// Total order on float bit patterns (larger float -> larger key).
+__device__ __forceinline__ uint32_t orderable(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_orderable(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+} // namespace q38

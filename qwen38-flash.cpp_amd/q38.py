@@ -1,0 +1,193 @@
+"""ctypes binding of libq38.so (include/q38.h), the C ABI of the gfx950 verify round.
+
+This module is plumbing for tests and the benchmark: it loads the in-tree shared library
+and exposes the ABI's structs and functions. It has no fallback: if libq38.so is missing
+or fails to load, importing it raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libq38.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"libq38.so is not built at {LIB_PATH}; run __graft_entry__.build()")
+lib = C.CDLL(LIB_PATH)
+
+Q38_OK, Q38_EINVAL, Q38_ERANGE, Q38_EHIP, Q38_ENOMEM, Q38_ESTATE, Q38_ESPACE = 0, -1, -2, -3, -4, -5, -6
+Q38_HEAD_Q8, Q38_HEAD_Q4G64 = 0, 1
+
+
+class Q38Error(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"q38 error {code}: {msg}")
+        self.code = code
+
+
+class MoeDesc(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "hidden", "inter", "experts", "top_k", "gu_dim", "gu_bits", "down_dim", "down_bits",
+        "gu_group", "down_group", "normalize_topk", "has_shared", "mixed", "reserved")]
+
+
+class MoeWeights(C.Structure):
+    _fields_ = [("router", C.c_void_p), ("shared_gate", C.c_void_p),
+                ("codes", C.c_void_p * 3), ("scales", C.c_void_p * 3), ("books", C.c_void_p * 3)]
+
+
+class RouteOut(C.Structure):
+    _fields_ = [("experts", C.c_void_p), ("weights", C.c_void_p), ("logits", C.c_void_p),
+                ("plan", C.c_void_p), ("x_norm", C.c_void_p)]
+
+
+class MoeTimings(C.Structure):
+    _fields_ = [("routing_ms", C.c_double), ("gate_up_ms", C.c_double), ("down_ms", C.c_double),
+                ("merge_ms", C.c_double), ("layers", C.c_int32), ("reserved", C.c_int32)]
+
+
+class GreedyDecision(C.Structure):
+    _fields_ = [("accepted", C.c_int64), ("correction_row", C.c_int64), ("next_token", C.c_uint32)]
+
+
+def _sig(name, res, *args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+    return f
+
+
+P, I32, I64, U32, U64, SZ, F32 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_size_t, C.c_float
+_sig("q38_last_error", C.c_char_p)
+_sig("q38_version", C.c_char_p)
+_sig("q38_ctx_create", C.c_int, C.c_int, C.POINTER(P))
+_sig("q38_ctx_destroy", None, P)
+_sig("q38_packed_vq_word_count", I64, I64, C.c_int)
+_sig("q38_unpack_vq_code", C.c_int, P, I64, I64, C.c_int, C.POINTER(U32))
+_sig("q38_supports_segmented_vq", C.c_int, C.c_int, C.c_int)
+_sig("q38_moe_layer_create", C.c_int, P, C.POINTER(MoeDesc), C.POINTER(MoeWeights), C.POINTER(P))
+_sig("q38_moe_layer_create_synthetic", C.c_int, P, C.POINTER(MoeDesc), U64, I32, C.POINTER(P))
+_sig("q38_moe_layer_destroy", None, P)
+_sig("q38_moe_layer_weights", C.c_int, P, C.POINTER(MoeWeights))
+_sig("q38_moe_layer_bytes", I64, P, I32, I32)
+_sig("q38_moe_workspace_size", SZ, C.POINTER(MoeDesc), I32)
+_sig("q38_moe_route", C.c_int, P, P, I32, C.POINTER(RouteOut), P, SZ, P)
+_sig("q38_moe_forward", C.c_int, P, P, I32, P, C.POINTER(RouteOut), P, SZ, P)
+_sig("q38_verify_chain", C.c_int, C.POINTER(P), I32, P, I32, F32, C.POINTER(RouteOut), P, SZ, P)
+_sig("q38_verify_chain_profiled", C.c_int, C.POINTER(P), I32, P, I32, F32, C.POINTER(RouteOut), P, SZ,
+     C.POINTER(MoeTimings), P)
+_sig("q38_rmsnorm", C.c_int, P, I32, I32, F32, P, P)
+_sig("q38_embed_synthetic", C.c_int, U64, C.POINTER(U32), I32, I32, P, P)
+_sig("q38_head_create", C.c_int, P, C.c_int, I64, I32, P, P, C.POINTER(P))
+_sig("q38_head_create_synthetic", C.c_int, P, C.c_int, I64, I32, U64, C.POINTER(P))
+_sig("q38_head_destroy", None, P)
+_sig("q38_head_weights", C.c_int, P, C.POINTER(P), C.POINTER(P))
+_sig("q38_head_bytes", I64, P)
+_sig("q38_head_workspace_size", SZ, P, I32)
+_sig("q38_head_greedy", C.c_int, P, P, I32, P, P, P, SZ, P)
+_sig("q38_head_logits", C.c_int, P, P, I32, P, P, SZ, P)
+_sig("q38_mtp_decide_greedy", C.c_int, C.POINTER(U32), I64, C.POINTER(U32), I64, C.POINTER(U32), I64,
+     C.POINTER(GreedyDecision))
+_sig("q38_plan_mtp_commit", C.c_int, U64, U64, U64, C.POINTER(U64))
+_sig("q38_mtp_accept_sampled", C.c_int, P, P, P, I32, I64, F32, U64, U64, U64, P, P)
+_sig("q38_philox4x32_10", None, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32))
+_sig("q38_slot_create", C.c_int, P, I32, I32, U64, C.POINTER(P))
+_sig("q38_slot_destroy", None, P)
+_sig("q38_slot_stage", C.c_int, P, I32, P, P)
+_sig("q38_slot_commit", C.c_int, P, I64, P)
+_sig("q38_slot_rollback", C.c_int, P)
+_sig("q38_slot_info", C.c_int, P, C.POINTER(U64), C.POINTER(I32), C.POINTER(I32))
+_sig("q38_slot_hidden", P, P)
+
+
+def check(rc: int) -> int:
+    if rc != Q38_OK:
+        raise Q38Error(rc, lib.q38_last_error().decode())
+    return rc
+
+
+def last_error() -> str:
+    return lib.q38_last_error().decode()
+
+
+def desc(hidden=2048, inter=512, experts=512, top_k=10, gu=(8, 14), down=(8, 14), gu_group=None,
+         down_group=None, normalize=1, shared=1, mixed=0) -> MoeDesc:
+    """Layer description; groups default to one scale per output row."""
+    return MoeDesc(hidden, inter, experts, top_k, gu[0], gu[1], down[0], down[1],
+                   gu_group or hidden, down_group or inter, normalize, shared, mixed, 0)
+
+
+def words_per_row(n_in: int, dim: int, bits: int) -> int:
+    return ((n_in // dim + 31) // 32) * bits
+
+
+def ptr(t) -> int:
+    """Device/host address of a torch tensor (or an int address)."""
+    return t if isinstance(t, int) else t.data_ptr()
+
+
+class Ctx:
+    def __init__(self, device: int = 0):
+        h = P()
+        check(lib.q38_ctx_create(device, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib.q38_ctx_destroy(self.h)
+            self.h = None
+
+
+class MoeLayer:
+    def __init__(self, ctx: Ctx, d: MoeDesc, seed: int | None = None, layer: int = 0,
+                 weights: MoeWeights | None = None):
+        h = P()
+        self.desc = d
+        if weights is None:
+            check(lib.q38_moe_layer_create_synthetic(ctx.h, C.byref(d), seed, layer, C.byref(h)))
+        else:
+            check(lib.q38_moe_layer_create(ctx.h, C.byref(d), C.byref(weights), C.byref(h)))
+        self.h = h
+
+    def weights(self) -> MoeWeights:
+        w = MoeWeights()
+        check(lib.q38_moe_layer_weights(self.h, C.byref(w)))
+        return w
+
+    def bytes(self, n_unique: int, rows: int) -> int:
+        return lib.q38_moe_layer_bytes(self.h, n_unique, rows)
+
+    def close(self):
+        if self.h:
+            lib.q38_moe_layer_destroy(self.h)
+            self.h = None
+
+
+class Head:
+    def __init__(self, ctx: Ctx, kind: int, vocab: int, hidden: int, seed: int | None = None,
+                 weights=None, scales=None):
+        h = P()
+        if weights is None:
+            check(lib.q38_head_create_synthetic(ctx.h, kind, vocab, hidden, seed, C.byref(h)))
+        else:
+            check(lib.q38_head_create(ctx.h, kind, vocab, hidden, ptr(weights), ptr(scales), C.byref(h)))
+        self.h, self.kind, self.vocab, self.hidden = h, kind, vocab, hidden
+
+    def workspace_size(self, rows: int) -> int:
+        return lib.q38_head_workspace_size(self.h, rows)
+
+    def device_weights(self):
+        w, s = P(), P()
+        check(lib.q38_head_weights(self.h, C.byref(w), C.byref(s)))
+        return w.value, s.value
+
+    def close(self):
+        if self.h:
+            lib.q38_head_destroy(self.h)
+            self.h = None
+
+
+def routes(experts=None, weights=None, logits=None, plan=None, x_norm=None) -> RouteOut:
+    f = lambda t: None if t is None else ptr(t)
+    return RouteOut(f(experts), f(weights), f(logits), f(plan), f(x_norm))

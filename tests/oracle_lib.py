@@ -1,0 +1,323 @@
+"""ctypes loader of the CPU oracle (oracle/_build/libq38_oracle.so) — test infrastructure.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "libq38_oracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libq38_ref.so")
+
+P, I32, I64, U32, U64, F32, F64 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float, C.c_double
+
+
+class Desc(C.Structure):  # field order of oracle/q38_oracle.cpp Desc
+    _fields_ = [(n, C.c_int32) for n in (
+        "hidden", "inter", "experts", "top_k", "gu_dim", "gu_bits", "down_dim", "down_bits",
+        "gu_group", "down_group", "normalize", "has_shared", "mixed", "pad")]
+
+
+def make_desc(hidden=2048, inter=512, experts=512, top_k=10, gu=(8, 14), down=(8, 14), gu_group=None,
+              down_group=None, normalize=1, shared=1, mixed=0) -> Desc:
+    return Desc(hidden, inter, experts, top_k, gu[0], gu[1], down[0], down[1], gu_group or hidden,
+                down_group or inter, normalize, shared, mixed, 0)
+
+
+def _a(x):
+    return x.ctypes.data_as(P)
+
+
+class Oracle:
+    def __init__(self, path=ORACLE_SO):
+        if not os.path.exists(path):
+            subprocess.check_call(["make", "-C", os.path.join(ROOT, "oracle"), "-s"])
+        self.lib = L = C.CDLL(path)
+        sig = lambda n, r, *a: (setattr(getattr(L, n), "restype", r), setattr(getattr(L, n), "argtypes", list(a)))
+        sig("orc_f32_to_bf16", C.c_uint16, F32)
+        sig("orc_f32_to_f16", C.c_uint16, F32)
+        sig("orc_f16_to_f32", F32, C.c_uint16)
+        sig("orc_exp_contract", F32, F32)
+        sig("orc_stream_key", U64, U64, U64, U64)
+        sig("orc_bits_at", U64, U64, U64)
+        sig("orc_gen_normal", None, U64, U64, U64, F64, C.c_int, P)
+        sig("orc_gen_uniform_f16", None, U64, U64, U64, F64, F64, P)
+        sig("orc_gen_int8", None, U64, U64, U64, P)
+        sig("orc_gen_int4", None, U64, U64, U64, P)
+        sig("orc_gen_code_rows", None, U64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P)
+        sig("orc_gen_book", None, U64, C.c_int, C.c_int, C.c_int, P, P, P)
+        sig("orc_gen_embed", None, U64, P, C.c_int, C.c_int, P)
+        sig("orc_packed_word_count", I64, I64, C.c_int)
+        sig("orc_pack_row", C.c_int, P, I64, C.c_int, P)
+        sig("orc_unpack_code", C.c_int, P, I64, I64, C.c_int, P)
+        sig("orc_router_logits", None, P, C.c_int, C.c_int, P, C.c_int, P)
+        sig("orc_dot_contract", F32, P, P, C.c_int)
+        sig("orc_route", None, P, C.c_int, C.c_int, C.c_int, C.c_int, P, P)
+        sig("orc_route_plan", C.c_int, P, C.c_int, C.c_int, C.c_int, P, P, P, P, P)
+        sig("orc_moe_layer_synth", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, P, P, C.c_int)
+        sig("orc_moe_layer_synth_timed", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, C.c_int,
+            C.POINTER(C.c_double))
+        sig("orc_moe_layer_dense", C.c_int, C.POINTER(Desc), P, P, C.POINTER(P), C.POINTER(P), C.POINTER(P),
+            P, C.c_int, P, P, P, P, C.c_int)
+        sig("orc_expert_dense", C.c_int, C.POINTER(Desc), C.POINTER(P), C.POINTER(P), C.POINTER(P), C.c_int, P,
+            C.c_int, P)
+        sig("orc_rmsnorm", None, P, C.c_int, C.c_int, F64, P)
+        sig("orc_residual_add", None, P, P, I64, P)
+        sig("orc_head_q8_synth_logits", None, U64, C.c_int, I64, I64, P, C.c_int, P, C.c_int)
+        sig("orc_head_q8_logits", None, P, P, I64, C.c_int, P, C.c_int, P, C.c_int)
+        sig("orc_argmax", None, P, C.c_int, I64, P, P)
+        sig("orc_head_q4_synth_logits", None, U64, C.c_int, I64, I64, P, C.c_int, P, C.c_int)
+        sig("orc_decide_greedy", C.c_int, P, I64, P, I64, P, I64, P, P, P)
+        sig("orc_plan_commit", C.c_int, U64, U64, U64, P)
+        sig("orc_philox4x32_10", None, P, P, P)
+        sig("orc_round_uniforms", None, U64, U64, U64, U32, P, P)
+        sig("orc_accept_sampled", C.c_int, P, P, P, C.c_int, I64, F32, U64, U64, U64, P, P)
+
+    # ---- formats
+    def bf16(self, x):
+        f = np.ascontiguousarray(x, dtype=np.float32)
+        u = f.view(np.uint32)
+        out = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        nan = (u & 0x7FFFFFFF) > 0x7F800000
+        out[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+        return out
+
+    @staticmethod
+    def bf16_to_f32(u16):
+        return (np.asarray(u16, dtype=np.uint32) << 16).view(np.float32)
+
+    # ---- generator
+    def key(self, seed, layer, tensor):
+        return self.lib.orc_stream_key(seed, layer, tensor)
+
+    def normal(self, key, start, count, sd, f16=False):
+        out = np.empty(count, np.uint16)
+        self.lib.orc_gen_normal(key, start, count, sd, int(f16), _a(out))
+        return out
+
+    def uniform_f16(self, key, start, count, lo, hi):
+        out = np.empty(count, np.uint16)
+        self.lib.orc_gen_uniform_f16(key, start, count, lo, hi, _a(out))
+        return out
+
+    def code_rows(self, key, e, out_dim, o0, nrows, nsub, bits):
+        words = ((nsub + 31) // 32) * bits
+        out = np.empty(nrows * words, np.uint32)
+        self.lib.orc_gen_code_rows(key, e, out_dim, o0, nrows, nsub, bits, _a(out))
+        return out.reshape(nrows, words)
+
+    def embed(self, seed, tokens, H):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty((len(t), H), np.uint16)
+        self.lib.orc_gen_embed(seed, _a(t), len(t), H, _a(out))
+        return out
+
+    # ---- geometry
+    def word_count(self, n, bits):
+        return self.lib.orc_packed_word_count(n, bits)
+
+    def pack_row(self, codes, bits):
+        c = np.ascontiguousarray(codes, dtype=np.uint32)
+        out = np.zeros(max(self.word_count(len(c), bits), 1), np.uint32)
+        assert self.lib.orc_pack_row(_a(c), len(c), bits, _a(out)) == 0
+        return out[: self.word_count(len(c), bits)]
+
+    def unpack(self, words, index, bits):
+        w = np.ascontiguousarray(words, dtype=np.uint32)
+        out = np.zeros(1, np.uint32)
+        rc = self.lib.orc_unpack_code(_a(w), len(w), index, bits, _a(out))
+        return rc, int(out[0])
+
+    # ---- router
+    def router_logits(self, x, W):
+        x = np.ascontiguousarray(x, np.uint16)
+        W = np.ascontiguousarray(W, np.uint16)
+        M, H = x.shape
+        E = W.shape[0]
+        out = np.empty((M, E), np.float32)
+        self.lib.orc_router_logits(_a(x), M, H, _a(W), E, _a(out))
+        return out
+
+    def route(self, logits, k, normalize=1):
+        lg = np.ascontiguousarray(logits, np.float32)
+        M, E = lg.shape
+        ex = np.empty((M, k), np.int32)
+        wt = np.empty((M, k), np.float32)
+        self.lib.orc_route(_a(lg), M, E, k, normalize, _a(ex), _a(wt))
+        return ex, wt
+
+    def plan(self, experts, E):
+        ex = np.ascontiguousarray(experts, np.int32)
+        M, k = ex.shape
+        MK = M * k
+        nu = np.zeros(1, np.int32)
+        uexp = np.zeros(MK, np.int32)
+        uoff = np.zeros(MK + 1, np.int32)
+        rl = np.zeros(MK, np.int32)
+        rp = np.zeros(MK, np.int32)
+        assert self.lib.orc_route_plan(_a(ex), M, k, E, _a(nu), _a(uexp), _a(uoff), _a(rl), _a(rp)) == 0
+        n = int(nu[0])
+        return n, uexp[:n], uoff[: n + 1], rl, rp
+
+    # ---- MoE
+    def moe_layer_synth(self, d: Desc, seed, layer, x, threads=8):
+        x = np.ascontiguousarray(x, np.uint16)
+        M = x.shape[0]
+        y = np.empty_like(x)
+        ex = np.empty((M, d.top_k), np.int32)
+        wt = np.empty((M, d.top_k), np.float32)
+        lg = np.empty((M, d.experts), np.float32)
+        rc = self.lib.orc_moe_layer_synth(C.byref(d), seed, layer, _a(x), M, _a(y), _a(ex), _a(wt), _a(lg), threads)
+        assert rc == 0
+        return y, ex, wt, lg
+
+    def moe_layer_synth_timed(self, d: Desc, seed, layer, x, threads=8):
+        x = np.ascontiguousarray(x, np.uint16)
+        y = np.empty_like(x)
+        sec = C.c_double()
+        assert self.lib.orc_moe_layer_synth_timed(C.byref(d), seed, layer, _a(x), x.shape[0], _a(y), threads,
+                                                  C.byref(sec)) == 0
+        return y, sec.value
+
+    def moe_layer_dense(self, d: Desc, router, wsg, codes, scales, books, x, threads=8):
+        x = np.ascontiguousarray(x, np.uint16)
+        M = x.shape[0]
+        y = np.empty_like(x)
+        ex = np.empty((M, d.top_k), np.int32)
+        wt = np.empty((M, d.top_k), np.float32)
+        lg = np.empty((M, d.experts), np.float32)
+        keep = [np.ascontiguousarray(a) for a in (router, wsg, *codes, *scales, *books)]
+        arr = lambda xs: (P * 3)(*[_a(a).value for a in xs])
+        rc = self.lib.orc_moe_layer_dense(C.byref(d), _a(keep[0]), _a(keep[1]), arr(keep[2:5]), arr(keep[5:8]),
+                                          arr(keep[8:11]), _a(x), M, _a(y), _a(ex), _a(wt), _a(lg), threads)
+        assert rc == 0
+        return y, ex, wt, lg
+
+    def rmsnorm(self, h, eps=1e-6):
+        h = np.ascontiguousarray(h, np.uint16)
+        out = np.empty_like(h)
+        self.lib.orc_rmsnorm(_a(h), h.shape[0], h.shape[1], eps, _a(out))
+        return out
+
+    def residual_add(self, h, y):
+        h = np.ascontiguousarray(h, np.uint16)
+        y = np.ascontiguousarray(y, np.uint16)
+        out = np.empty_like(h)
+        self.lib.orc_residual_add(_a(h), _a(y), h.size, _a(out))
+        return out
+
+    # ---- heads
+    def head_q8_synth_logits(self, seed, H, h, v0=0, nv=151936, threads=8):
+        h = np.ascontiguousarray(h, np.uint16)
+        out = np.empty((h.shape[0], nv), np.float32)
+        self.lib.orc_head_q8_synth_logits(seed, H, v0, nv, _a(h), h.shape[0], _a(out), threads)
+        return out
+
+    def head_q8_logits(self, W, s, h, threads=8):
+        W = np.ascontiguousarray(W, np.int8)
+        s = np.ascontiguousarray(s, np.uint16)
+        h = np.ascontiguousarray(h, np.uint16)
+        V, H = W.shape
+        out = np.empty((h.shape[0], V), np.float32)
+        self.lib.orc_head_q8_logits(_a(W), _a(s), V, H, _a(h), h.shape[0], _a(out), threads)
+        return out
+
+    def head_q4_synth_logits(self, seed, H, h, v0=0, nv=151936, threads=8):
+        h = np.ascontiguousarray(h, np.uint16)
+        out = np.empty((h.shape[0], nv), np.float32)
+        self.lib.orc_head_q4_synth_logits(seed, H, v0, nv, _a(h), h.shape[0], _a(out), threads)
+        return out
+
+    def argmax(self, logits):
+        lg = np.ascontiguousarray(logits, np.float32)
+        M, V = lg.shape
+        idx = np.empty(M, np.uint32)
+        val = np.empty(M, np.float32)
+        self.lib.orc_argmax(_a(lg), M, V, _a(idx), _a(val))
+        return idx, val
+
+    # ---- acceptance
+    def decide_greedy(self, drafts, target, stop=()):
+        d = np.ascontiguousarray(drafts, np.uint32)
+        t = np.ascontiguousarray(target, np.uint32)
+        s = np.ascontiguousarray(stop if len(stop) else [0], np.uint32)
+        a, r, n = np.zeros(1, np.int64), np.zeros(1, np.int64), np.zeros(1, np.uint32)
+        rc = self.lib.orc_decide_greedy(_a(d), len(d), _a(t), len(t), _a(s), len(stop), _a(a), _a(r), _a(n))
+        return rc, int(a[0]), int(r[0]), int(n[0])
+
+    def plan_commit(self, off, drafted, accepted):
+        out = np.zeros(4, np.uint64)
+        rc = self.lib.orc_plan_commit(off, drafted, accepted, _a(out))
+        return rc, [int(v) for v in out]
+
+    def philox(self, ctr, key):
+        c = np.ascontiguousarray(ctr, np.uint32)
+        k = np.ascontiguousarray(key, np.uint32)
+        out = np.zeros(4, np.uint32)
+        self.lib.orc_philox4x32_10(_a(c), _a(k), _a(out))
+        return [int(v) for v in out]
+
+    def round_uniforms(self, seed, slot, rnd, pos):
+        u, v = np.zeros(1, np.float32), np.zeros(1, np.float32)
+        self.lib.orc_round_uniforms(seed, slot, rnd, pos, _a(u), _a(v))
+        return float(u[0]), float(v[0])
+
+    def accept_sampled(self, tl, dl, drafts, T, seed, slot, rnd):
+        tl = np.ascontiguousarray(tl, np.float32)
+        dl = np.ascontiguousarray(dl, np.float32)
+        d = np.ascontiguousarray(drafts, np.uint32)
+        a, n = np.zeros(1, np.int64), np.zeros(1, np.uint32)
+        rc = self.lib.orc_accept_sampled(_a(tl), _a(dl), _a(d), len(d), tl.shape[1], T, seed, slot, rnd, _a(a), _a(n))
+        assert rc == 0
+        return int(a[0]), int(n[0])
+
+
+class RefCore:
+    """The reference's own model-free sources compiled by oracle/Makefile (oracle/_ref)."""
+
+    def __init__(self, path=REF_SO):
+        self.lib = L = C.CDLL(path)
+        sig = lambda n, r, *a: (setattr(getattr(L, n), "restype", r), setattr(getattr(L, n), "argtypes", list(a)))
+        sig("ref_packed_vq_word_count", I64, I64, C.c_int)
+        sig("ref_unpack_vq_code", C.c_int, P, I64, I64, C.c_int, P)
+        sig("ref_supports_segmented_vq", C.c_int, C.c_int, C.c_int)
+        sig("ref_decide_greedy", C.c_int, P, I64, P, I64, P, I64, P, P, P)
+        sig("ref_plan_commit", C.c_int, U64, U64, U64, P)
+
+    def unpack(self, words, index, bits):
+        w = np.ascontiguousarray(words, dtype=np.uint32)
+        out = np.zeros(1, np.uint32)
+        rc = self.lib.ref_unpack_vq_code(_a(w), len(w), index, bits, _a(out))
+        return rc, int(out[0])
+
+    def decide_greedy(self, drafts, target, stop=()):
+        d = np.ascontiguousarray(drafts, np.uint32)
+        t = np.ascontiguousarray(target, np.uint32)
+        s = np.ascontiguousarray(stop if len(stop) else [0], np.uint32)
+        a, r, n = np.zeros(1, np.int64), np.zeros(1, np.int64), np.zeros(1, np.uint32)
+        rc = self.lib.ref_decide_greedy(_a(d), len(d), _a(t), len(t), _a(s), len(stop), _a(a), _a(r), _a(n))
+        return rc, int(a[0]), int(r[0]), int(n[0])
+
+    def plan_commit(self, off, drafted, accepted):
+        out = np.zeros(4, np.uint64)
+        rc = self.lib.ref_plan_commit(off, drafted, accepted, _a(out))
+        return rc, [int(v) for v in out]
+
+
+_ORACLE = None
+
+
+def load() -> Oracle:
+    global _ORACLE
+    if _ORACLE is None:
+        _ORACLE = Oracle()
+    return _ORACLE
+
+
+def load_ref():
+    return RefCore() if os.path.exists(REF_SO) else None

@@ -1,0 +1,117 @@
+"""Verify tail on the GPU: exact greedy argmax + logit of the Q8 head, fast logits, and
+the Q4/g64 draft head, against the CPU oracle."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import gpu_util as G
+from moe_cases import SEED, f16
+
+pytestmark = pytest.mark.gpu
+
+
+def greedy(q38, hd, h_np):
+    M = h_np.shape[0]
+    h = G.to_dev(h_np)
+    am = G.empty(M, np.int32)
+    lg = G.empty(M, np.float32)
+    ws = G.workspace(hd.workspace_size(M))
+    q38.check(q38.lib.q38_head_greedy(hd.h, h.data_ptr(), M, am.data_ptr(), lg.data_ptr(), ws.data_ptr(),
+                                      ws.numel(), G.stream()))
+    return G.to_host(am).astype(np.uint32), G.to_host(lg)
+
+
+def logits(q38, hd, h_np):
+    M = h_np.shape[0]
+    h = G.to_dev(h_np)
+    out = G.empty((M, hd.vocab), np.float32)
+    q38.check(q38.lib.q38_head_logits(hd.h, h.data_ptr(), M, out.data_ptr(), None, 0, G.stream()))
+    return G.to_host(out)
+
+
+def explicit_head(q38, gpu, W, s):
+    Wd, sd = G.to_dev(W), G.to_dev(s)
+    hd = q38.Head(gpu, q38.Q38_HEAD_Q8, W.shape[0], W.shape[1], weights=Wd, scales=sd)
+    hd._keep = (Wd, sd)
+    return hd
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_explicit_head_exact(gpu, q38, orc, M):
+    rng = np.random.default_rng(M)
+    V, H = 5000, 2048
+    W = rng.integers(-127, 128, (V, H)).astype(np.int8)
+    s = f16(rng.uniform(1e-4, 1e-3, V))
+    h = orc.bf16(rng.normal(0, 1, (M, H)))
+    hd = explicit_head(q38, gpu, W, s)
+    try:
+        am, lg = greedy(q38, hd, h)
+        want = orc.head_q8_logits(W, s, h)
+        wi, wv = orc.argmax(want)
+        assert np.array_equal(am, wi) and np.array_equal(lg, wv)
+        fast = logits(q38, hd, h)
+        assert np.allclose(fast, want, rtol=1e-4, atol=1e-5)
+    finally:
+        hd.close()
+
+
+def test_head_near_ties(gpu, q38, orc):
+    rng = np.random.default_rng(11)
+    V, H = 4096, 2048
+    W = rng.integers(-127, 128, (V, H)).astype(np.int8)
+    s = f16(np.full(V, 5e-4))
+    h = orc.bf16(rng.normal(0, 1, (4, H)))
+    base = orc.head_q8_logits(W, s, h)
+    for r in range(4):
+        b = int(np.argmax(base[r]))
+        dup = (b + 1000 * (r + 1)) % V
+        W[dup] = W[b]                         # exact tie: the lower index must win
+    W[3000, :] = W[int(np.argmax(base[0]))]
+    W[3000, 0] = W[3000, 0] + (1 if W[3000, 0] < 127 else -1)   # a one-step neighbour
+    hd = explicit_head(q38, gpu, W, s)
+    try:
+        am, lg = greedy(q38, hd, h)
+        want = orc.head_q8_logits(W, s, h)
+        wi, wv = orc.argmax(want)
+        assert np.array_equal(am, wi) and np.array_equal(lg, wv)
+    finally:
+        hd.close()
+
+
+def test_all_equal_logits_full_fallback(gpu, q38, orc):
+    """h = 0 makes every logit 0: all rows are candidates (overflow path), argmax 0."""
+    rng = np.random.default_rng(12)
+    V, H = 3000, 2048
+    W = rng.integers(-127, 128, (V, H)).astype(np.int8)
+    s = f16(rng.uniform(1e-4, 1e-3, V))
+    hd = explicit_head(q38, gpu, W, s)
+    try:
+        am, lg = greedy(q38, hd, np.zeros((2, H), np.uint16))
+        assert am.tolist() == [0, 0] and lg.tolist() == [0.0, 0.0]
+    finally:
+        hd.close()
+
+
+def test_synthetic_full_vocab_exact(gpu, q38, orc):
+    hd = q38.Head(gpu, q38.Q38_HEAD_Q8, 151936, 2048, seed=SEED)
+    try:
+        h = orc.rmsnorm(orc.embed(SEED, [1, 2, 3, 4], 2048))
+        am, lg = greedy(q38, hd, h)
+        want = orc.head_q8_synth_logits(SEED, 2048, h)
+        wi, wv = orc.argmax(want)
+        assert np.array_equal(am, wi) and np.array_equal(lg, wv)
+    finally:
+        hd.close()
+
+
+def test_q4_draft_head(gpu, q38, orc):
+    hd = q38.Head(gpu, q38.Q38_HEAD_Q4G64, 151936, 2048, seed=SEED)
+    try:
+        h = orc.rmsnorm(orc.embed(SEED, [5, 6, 7], 2048))
+        got = logits(q38, hd, h)
+        want = orc.head_q4_synth_logits(SEED, 2048, h)
+        err = np.abs(got - want)
+        assert err.max() <= 1e-4 * np.abs(want).max() + 1e-5
+    finally:
+        hd.close()
