@@ -140,8 +140,8 @@ int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h
  * 30-36), summed over layers, in milliseconds of device time between HIP events placed
  * around each launch (the events serialise the phases; use for attribution only). */
 typedef struct q38_moe_timings {
-    double routing_ms;   /* RMSNorm + router logits + top-k + plan */
-    double gate_up_ms;
+    double routing_ms;   /* RMSNorm + router logits (+ top-k + plan on the grouped path) */
+    double gate_up_ms;   /* gate/up projections (+ top-k + plan on the MFMA path) */
     double down_ms;
     double merge_ms;     /* ordered route reduction + shared gate + residual */
     int32_t layers;
@@ -158,6 +158,11 @@ int q38_rmsnorm(const uint16_t* x, int32_t rows, int32_t hidden, float eps, uint
  * row r = N(0,1) bf16 values keyed by (seed, token r). h: device [n, H]. */
 int q38_embed_synthetic(uint64_t seed, const uint32_t* tokens_host, int32_t n, int32_t hidden, uint16_t* h,
                         void* stream);
+
+/* The same embedding with the token ids in device memory (device u32 [n]), so a captured
+ * graph can be replayed with new tokens. */
+int q38_embed_synthetic_dev(uint64_t seed, const uint32_t* tokens, int32_t n, int32_t hidden, uint16_t* h,
+                            void* stream);
 
 /* ------------------------------------------------------------------ LM heads
  * Target head (src/model.cpp:466-492): symmetric int8 [V, H] + one FP16 scale per row.
@@ -218,7 +223,8 @@ void q38_slot_destroy(q38_slot* slot);
 int q38_slot_stage(q38_slot* slot, int32_t draft_count, const uint16_t* h, void* stream);
 /* commit_mtp_target_verification (src/mtp_verifier.cpp:129-145): keep checkpoint
  * `accepted`; token_count becomes origin + accepted + 1; all staged rows are released.
- * Invalid counts return Q38_ESTATE and leave the slot untouched. */
+ * Invalid counts return Q38_ESTATE and leave the slot untouched. The slot double-buffers
+ * its checkpoints, so a commit moves no data (the reference moves state_after, :139). */
 int q38_slot_commit(q38_slot* slot, int64_t accepted, void* stream);
 /* Drop the staged rows, keeping the committed state. */
 int q38_slot_rollback(q38_slot* slot);

@@ -46,8 +46,9 @@ struct q38_moe_layer {
     q38_ctx* ctx;
     q38_moe_desc desc;
     LayerDev dev;
-    void* owned = nullptr;
+    void* owned = nullptr;      // synthetic tensors
     size_t owned_bytes = 0;
+    void* prepared = nullptr;   // codebooks split into 4-dim chunks
 };
 
 struct q38_head {
@@ -64,8 +65,9 @@ struct q38_slot {
     int staged_rows = 0;
     int draft_count = 0;
     bool has_hidden = false;
-    uint16_t* committed = nullptr;  // [H]
-    uint16_t* staged = nullptr;     // [max_rows, H]
+    uint16_t* rows[2] = {nullptr, nullptr};  // two [max_rows, H] checkpoint buffers
+    int stage_buf = 0;                       // buffer the next stage writes
+    const uint16_t* committed = nullptr;     // row of the committed checkpoint
 };
 
 extern "C" {
@@ -159,6 +161,30 @@ static void fill_dev(q38_moe_layer* L, const q38_moe_weights* w) {
     }
 }
 
+// Codebooks split into 4-dim chunks ([dim/4][entries][4]) for the LDS-resident MFMA path.
+static int prepare_layer(q38_moe_layer* L) {
+    size_t total = 0, off[3];
+    for (int p = 0; p < 3; ++p) {
+        off[p] = total;
+        total += align256((static_cast<size_t>(1) << L->dev.p[p].bits) * L->dev.p[p].dim * 2);
+    }
+    char* base = nullptr;
+    if (hipMalloc(&base, total) != hipSuccess) return fail(Q38_ENOMEM, "hipMalloc failed for prepared codebooks");
+    hipError_t e = hipSuccess;
+    for (int p = 0; p < 3 && e == hipSuccess; ++p) {
+        auto* dst = reinterpret_cast<uint16_t*>(base + off[p]);
+        e = launch_split_book(L->dev.p[p].book, 1 << L->dev.p[p].bits, L->dev.p[p].dim, dst, nullptr);
+        L->dev.p[p].book4 = dst;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        (void)hipFree(base);
+        return hip_fail(e, "codebook preparation");
+    }
+    L->prepared = base;
+    return Q38_OK;
+}
+
 int q38_moe_layer_create(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_weights* weights,
                          q38_moe_layer** out) {
     if (!ctx || !out || !weights) return fail(Q38_EINVAL, "q38_moe_layer_create: null argument");
@@ -168,8 +194,12 @@ int q38_moe_layer_create(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_w
     for (int p = 0; p < 3; ++p)
         if (!weights->codes[p] || !weights->scales[p] || !weights->books[p])
             return fail(Q38_EINVAL, "every projection needs codes, scales and a codebook");
-    auto* L = new q38_moe_layer{ctx, *desc, {}, nullptr, 0};
+    auto* L = new q38_moe_layer{ctx, *desc, {}, nullptr, 0, nullptr};
     fill_dev(L, weights);
+    if (int rc = prepare_layer(L)) {
+        delete L;
+        return rc;
+    }
     *out = L;
     return Q38_OK;
 }
@@ -240,8 +270,13 @@ int q38_moe_layer_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, uint6
         (void)hipFree(base);
         return hip_fail(e, "synthetic layer generation");
     }
-    auto* L = new q38_moe_layer{ctx, d, {}, base, s.total};
+    auto* L = new q38_moe_layer{ctx, d, {}, base, s.total, nullptr};
     fill_dev(L, &w);
+    if (int rc = prepare_layer(L)) {
+        (void)hipFree(base);
+        delete L;
+        return rc;
+    }
     *out = L;
     return Q38_OK;
 }
@@ -249,6 +284,7 @@ int q38_moe_layer_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, uint6
 void q38_moe_layer_destroy(q38_moe_layer* layer) {
     if (!layer) return;
     if (layer->owned) (void)hipFree(layer->owned);
+    if (layer->prepared) (void)hipFree(layer->prepared);
     delete layer;
 }
 
@@ -278,17 +314,7 @@ int64_t q38_moe_layer_bytes(const q38_moe_layer* L, int32_t n_unique, int32_t ro
            static_cast<int64_t>(2) * rows * v.H * 2;
 }
 
-struct MoeWork {
-    uint16_t* xn;
-    float* logits;
-    float* sgate;
-    int32_t* experts;
-    float* weights;
-    int32_t* plan;
-    uint16_t* hbuf;
-    uint16_t* dbuf;
-};
-static size_t moe_ws(const q38_moe_desc& d, int M, MoeWork* w, void* base) {
+static size_t moe_ws(const q38_moe_desc& d, int M, MoeBufs* w, void* base) {
     const int MK = M * d.top_k;
     size_t off = 0;
     char* b = static_cast<char*>(base);
@@ -297,15 +323,20 @@ static size_t moe_ws(const q38_moe_desc& d, int M, MoeWork* w, void* base) {
         off += align256(bytes);
         return p;
     };
-    MoeWork t{};
-    t.xn = reinterpret_cast<uint16_t*>(take(static_cast<size_t>(M) * d.hidden * 2));
+    MoeBufs t{};
+    t.x = reinterpret_cast<uint16_t*>(take(static_cast<size_t>(M) * d.hidden * 2));
+    t.x16 = reinterpret_cast<uint16_t*>(take(static_cast<size_t>(M) * d.hidden * 2));
     t.logits = reinterpret_cast<float*>(take(static_cast<size_t>(M) * d.experts * 4));
     t.sgate = reinterpret_cast<float*>(take(static_cast<size_t>(M) * 4));
     t.experts = reinterpret_cast<int32_t*>(take(static_cast<size_t>(MK) * 4));
     t.weights = reinterpret_cast<float*>(take(static_cast<size_t>(MK) * 4));
     t.plan = reinterpret_cast<int32_t*>(take(static_cast<size_t>(2 + 4 * MK) * 4));
-    t.hbuf = reinterpret_cast<uint16_t*>(take(static_cast<size_t>(MK + M) * d.inter * 2));
-    t.dbuf = reinterpret_cast<uint16_t*>(take(static_cast<size_t>(MK + M) * d.hidden * 2));
+    const size_t gu = static_cast<size_t>(MK + M) * d.inter, dn = static_cast<size_t>(MK + M) * d.hidden;
+    char* acc = take((2 * gu + dn) * 4);
+    t.g = reinterpret_cast<float*>(acc);
+    t.u = acc ? t.g + gu : nullptr;
+    t.d = acc ? t.g + 2 * gu : nullptr;
+    t.zero_floats = 2 * gu + dn;
     if (w) *w = t;
     return off;
 }
@@ -320,7 +351,7 @@ static int check_rows(int rows) {
     return Q38_OK;
 }
 
-static int copy_routes(const q38_moe_layer* L, int M, const MoeWork& w, const q38_route_out* r, hipStream_t st) {
+static int copy_routes(const q38_moe_layer* L, int M, const MoeBufs& w, const q38_route_out* r, hipStream_t st) {
     if (!r) return Q38_OK;
     const int MK = M * L->desc.top_k;
     if (r->experts) Q38_HIP(hipMemcpyAsync(r->experts, w.experts, MK * 4, hipMemcpyDeviceToDevice, st));
@@ -330,7 +361,7 @@ static int copy_routes(const q38_moe_layer* L, int M, const MoeWork& w, const q3
                                hipMemcpyDeviceToDevice, st));
     if (r->plan) Q38_HIP(hipMemcpyAsync(r->plan, w.plan, (2 + 4 * MK) * 4, hipMemcpyDeviceToDevice, st));
     if (r->x_norm)
-        Q38_HIP(hipMemcpyAsync(r->x_norm, w.xn, static_cast<size_t>(M) * L->desc.hidden * 2,
+        Q38_HIP(hipMemcpyAsync(r->x_norm, w.x, static_cast<size_t>(M) * L->desc.hidden * 2,
                                hipMemcpyDeviceToDevice, st));
     return Q38_OK;
 }
@@ -339,12 +370,33 @@ int q38_moe_route(q38_moe_layer* L, const uint16_t* x, int32_t rows, const q38_r
                   size_t ws_bytes, void* stream) {
     if (!L || !x) return fail(Q38_EINVAL, "q38_moe_route: null argument");
     if (int rc = check_rows(rows)) return rc;
-    MoeWork w{};
+    MoeBufs w{};
     if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    Q38_HIP(launch_router(L->dev, x, rows, 0, 0.0f, nullptr, w.logits, w.sgate, st));
-    Q38_HIP(launch_topk_plan(L->dev, w.logits, rows, w.experts, w.weights, w.plan, st));
+    Q38_HIP(launch_router(L->dev, w, rows, x, 0, 0.0f, st));
+    Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
     return copy_routes(L, rows, w, routes, st);
+}
+
+// One layer: router (+ RMSNorm of h_in when do_norm), routing plan (fused into the MFMA
+// gate/up kernel, a separate kernel otherwise), gate/up, down, combine. Chain mode
+// (h_chain) adds the residual in place; otherwise y receives the layer output. ev, when
+// given, holds 5 events recorded around the phases.
+static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* h_in, int do_norm, float eps,
+                     uint16_t* h_chain, uint16_t* y, const q38_route_out* trace, hipEvent_t* ev, hipStream_t st) {
+    if (ev) Q38_HIP(hipEventRecord(ev[0], st));
+    Q38_HIP(launch_router(L->dev, w, rows, h_in, do_norm, eps, st));
+    if (!moe_uses_mfma(L->dev)) Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
+    if (ev) Q38_HIP(hipEventRecord(ev[1], st));
+    Q38_HIP(launch_gate_up(L->dev, w, rows, st));
+    if (ev) Q38_HIP(hipEventRecord(ev[2], st));
+    if (trace)
+        if (int rc = copy_routes(L, rows, w, trace, st)) return rc;
+    Q38_HIP(launch_down(L->dev, w, rows, st));
+    if (ev) Q38_HIP(hipEventRecord(ev[3], st));
+    Q38_HIP(launch_combine(L->dev, w, rows, h_chain, y, st));
+    if (ev) Q38_HIP(hipEventRecord(ev[4], st));
+    return Q38_OK;
 }
 
 int q38_moe_forward(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t* y, const q38_route_out* routes,
@@ -352,41 +404,35 @@ int q38_moe_forward(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t*
     if (!L || !x || !y) return fail(Q38_EINVAL, "q38_moe_forward: null argument");
     if (x == y) return fail(Q38_EINVAL, "q38_moe_forward: input and output must not alias");
     if (int rc = check_rows(rows)) return rc;
-    MoeWork w{};
+    MoeBufs w{};
     if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    Q38_HIP(launch_router(L->dev, x, rows, 0, 0.0f, nullptr, w.logits, w.sgate, st));
-    Q38_HIP(launch_topk_plan(L->dev, w.logits, rows, w.experts, w.weights, w.plan, st));
-    Q38_HIP(launch_gate_up(L->dev, x, rows, w.plan, w.hbuf, st));
-    Q38_HIP(launch_down(L->dev, rows, w.plan, w.hbuf, w.dbuf, st));
-    Q38_HIP(launch_combine(L->dev, rows, w.plan, w.weights, w.sgate, w.dbuf, nullptr, y, st));
-    return copy_routes(L, rows, w, routes, st);
+    return run_layer(L, w, rows, x, 0, 0.0f, nullptr, y, routes, nullptr, static_cast<hipStream_t>(stream));
+}
+
+static int chain_check(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows, void* ws,
+                       size_t ws_bytes) {
+    if (!layers || n_layers < 1 || !h) return fail(Q38_EINVAL, "verify chain: bad arguments");
+    if (int rc = check_rows(rows)) return rc;
+    size_t need = 0;
+    for (int l = 0; l < n_layers; ++l) {
+        if (!layers[l]) return fail(Q38_EINVAL, "verify chain: null layer");
+        if (layers[l]->desc.hidden != layers[0]->desc.hidden)
+            return fail(Q38_EINVAL, "verify chain: layers disagree on the hidden size");
+        need = std::max(need, moe_ws(layers[l]->desc, rows, nullptr, nullptr));
+    }
+    if (!ws || ws_bytes < need) return fail(Q38_ESPACE, "workspace too small");
+    return Q38_OK;
 }
 
 int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows, float eps,
                      const q38_route_out* traces, void* ws, size_t ws_bytes, void* stream) {
-    if (!layers || n_layers < 1 || !h) return fail(Q38_EINVAL, "q38_verify_chain: bad arguments");
-    if (int rc = check_rows(rows)) return rc;
-    size_t need = 0;
-    for (int l = 0; l < n_layers; ++l) {
-        if (!layers[l]) return fail(Q38_EINVAL, "q38_verify_chain: null layer");
-        if (layers[l]->desc.hidden != layers[0]->desc.hidden)
-            return fail(Q38_EINVAL, "q38_verify_chain: layers disagree on the hidden size");
-        need = std::max(need, moe_ws(layers[l]->desc, rows, nullptr, nullptr));
-    }
-    if (!ws || ws_bytes < need) return fail(Q38_ESPACE, "workspace too small");
+    if (int rc = chain_check(layers, n_layers, h, rows, ws, ws_bytes)) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     for (int l = 0; l < n_layers; ++l) {
-        q38_moe_layer* L = layers[l];
-        MoeWork w{};
-        moe_ws(L->desc, rows, &w, ws);
-        Q38_HIP(launch_router(L->dev, h, rows, 1, eps, w.xn, w.logits, w.sgate, st));
-        Q38_HIP(launch_topk_plan(L->dev, w.logits, rows, w.experts, w.weights, w.plan, st));
-        Q38_HIP(launch_gate_up(L->dev, w.xn, rows, w.plan, w.hbuf, st));
-        Q38_HIP(launch_down(L->dev, rows, w.plan, w.hbuf, w.dbuf, st));
-        Q38_HIP(launch_combine(L->dev, rows, w.plan, w.weights, w.sgate, w.dbuf, h, h, st));
-        if (traces)
-            if (int rc = copy_routes(L, rows, w, &traces[l], st)) return rc;
+        MoeBufs w{};
+        moe_ws(layers[l]->desc, rows, &w, ws);
+        if (int rc = run_layer(layers[l], w, rows, h, 1, eps, h, nullptr, traces ? &traces[l] : nullptr, nullptr, st))
+            return rc;
     }
     return Q38_OK;
 }
@@ -395,35 +441,16 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
                               const q38_route_out* traces, void* ws, size_t ws_bytes, q38_moe_timings* tm,
                               void* stream) {
     if (!tm) return fail(Q38_EINVAL, "q38_verify_chain_profiled: null timings");
-    if (!layers || n_layers < 1 || !h) return fail(Q38_EINVAL, "q38_verify_chain_profiled: bad arguments");
-    if (int rc = check_rows(rows)) return rc;
-    size_t need = 0;
-    for (int l = 0; l < n_layers; ++l) {
-        if (!layers[l]) return fail(Q38_EINVAL, "q38_verify_chain_profiled: null layer");
-        need = std::max(need, moe_ws(layers[l]->desc, rows, nullptr, nullptr));
-    }
-    if (!ws || ws_bytes < need) return fail(Q38_ESPACE, "workspace too small");
+    if (int rc = chain_check(layers, n_layers, h, rows, ws, ws_bytes)) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     std::vector<hipEvent_t> ev(static_cast<size_t>(n_layers) * 5, nullptr);
     for (auto& e : ev) Q38_HIP(hipEventCreate(&e));
     int rc = Q38_OK;
     for (int l = 0; l < n_layers && rc == Q38_OK; ++l) {
-        q38_moe_layer* L = layers[l];
-        MoeWork w{};
-        moe_ws(L->desc, rows, &w, ws);
-        hipEvent_t* E = &ev[static_cast<size_t>(l) * 5];
-        hipError_t e = hipEventRecord(E[0], st);
-        if (e == hipSuccess) e = launch_router(L->dev, h, rows, 1, eps, w.xn, w.logits, w.sgate, st);
-        if (e == hipSuccess) e = launch_topk_plan(L->dev, w.logits, rows, w.experts, w.weights, w.plan, st);
-        if (e == hipSuccess) e = hipEventRecord(E[1], st);
-        if (e == hipSuccess) e = launch_gate_up(L->dev, w.xn, rows, w.plan, w.hbuf, st);
-        if (e == hipSuccess) e = hipEventRecord(E[2], st);
-        if (e == hipSuccess) e = launch_down(L->dev, rows, w.plan, w.hbuf, w.dbuf, st);
-        if (e == hipSuccess) e = hipEventRecord(E[3], st);
-        if (e == hipSuccess) e = launch_combine(L->dev, rows, w.plan, w.weights, w.sgate, w.dbuf, h, h, st);
-        if (e == hipSuccess) e = hipEventRecord(E[4], st);
-        if (e != hipSuccess) rc = hip_fail(e, "profiled verify pass");
-        if (rc == Q38_OK && traces) rc = copy_routes(L, rows, w, &traces[l], st);
+        MoeBufs w{};
+        moe_ws(layers[l]->desc, rows, &w, ws);
+        rc = run_layer(layers[l], w, rows, h, 1, eps, h, nullptr, traces ? &traces[l] : nullptr,
+                       &ev[static_cast<size_t>(l) * 5], st);
     }
     if (rc == Q38_OK) {
         hipError_t e = hipEventSynchronize(ev.back());
@@ -441,13 +468,20 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
         if (e != hipSuccess) rc = hip_fail(e, "profiled verify timings");
         else *tm = t;
     }
-    for (auto& e : ev) (void)hipEventDestroy(e);
+    for (auto& x : ev) (void)hipEventDestroy(x);
     return rc;
 }
 
 int q38_rmsnorm(const uint16_t* x, int32_t rows, int32_t hidden, float eps, uint16_t* y, void* stream) {
     if (!x || !y || rows < 1 || hidden < 1) return fail(Q38_EINVAL, "q38_rmsnorm: bad arguments");
     Q38_HIP(launch_rmsnorm(x, rows, hidden, eps, y, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+int q38_embed_synthetic_dev(uint64_t seed, const uint32_t* tokens, int32_t n, int32_t hidden, uint16_t* h,
+                            void* stream) {
+    if (!tokens || !h || n < 1 || hidden < 1) return fail(Q38_EINVAL, "q38_embed_synthetic_dev: bad arguments");
+    Q38_HIP(launch_gen_embed_dev(seed, tokens, n, hidden, h, static_cast<hipStream_t>(stream)));
     return Q38_OK;
 }
 
@@ -617,40 +651,41 @@ int q38_slot_create(q38_ctx* ctx, int32_t hidden, int32_t max_rows, uint64_t tok
     if (!ctx || !out || hidden < 1 || max_rows < 2 || max_rows > 25)
         return fail(Q38_EINVAL, "q38_slot_create: bad arguments");
     auto* s = new q38_slot{ctx, hidden, max_rows, token_count};
-    if (hipMalloc(&s->committed, static_cast<size_t>(hidden) * 2) != hipSuccess ||
-        hipMalloc(&s->staged, static_cast<size_t>(max_rows) * hidden * 2) != hipSuccess) {
-        (void)hipFree(s->committed);
-        delete s;
-        return fail(Q38_ENOMEM, "hipMalloc failed for a slot");
-    }
+    for (auto& r : s->rows)
+        if (hipMalloc(&r, static_cast<size_t>(max_rows) * hidden * 2) != hipSuccess) {
+            for (auto& q : s->rows) (void)hipFree(q);
+            delete s;
+            return fail(Q38_ENOMEM, "hipMalloc failed for a slot");
+        }
     *out = s;
     return Q38_OK;
 }
 void q38_slot_destroy(q38_slot* s) {
     if (!s) return;
-    (void)hipFree(s->committed);
-    (void)hipFree(s->staged);
+    for (auto& r : s->rows) (void)hipFree(r);
     delete s;
 }
+// Stages into the buffer that does not hold the committed row, so commit is a pointer
+// update and the committed checkpoint survives a later stage + rollback.
 int q38_slot_stage(q38_slot* s, int32_t draft_count, const uint16_t* h, void* stream) {
     if (!s || !h) return fail(Q38_EINVAL, "q38_slot_stage: null argument");
     if (draft_count < 1 || draft_count + 1 > s->max_rows)
         return fail(Q38_EINVAL, "staged verification exceeds the slot's row capacity");
-    Q38_HIP(hipMemcpyAsync(s->staged, h, static_cast<size_t>(draft_count + 1) * s->hidden * 2,
+    Q38_HIP(hipMemcpyAsync(s->rows[s->stage_buf], h, static_cast<size_t>(draft_count + 1) * s->hidden * 2,
                            hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
     s->staged_rows = draft_count + 1;
     s->draft_count = draft_count;
     return Q38_OK;
 }
 int q38_slot_commit(q38_slot* s, int64_t accepted, void* stream) {
+    (void)stream;
     if (!s) return fail(Q38_EINVAL, "null slot");
     if (s->staged_rows == 0 || s->staged_rows != s->draft_count + 1)
         return fail(Q38_ESTATE, "MTP verification row count is invalid");
     if (accepted < 0 || accepted > s->draft_count)
         return fail(Q38_ESTATE, "MTP accepted count exceeds verified draft count");
-    Q38_HIP(hipMemcpyAsync(s->committed, s->staged + static_cast<size_t>(accepted) * s->hidden,
-                           static_cast<size_t>(s->hidden) * 2, hipMemcpyDeviceToDevice,
-                           static_cast<hipStream_t>(stream)));
+    s->committed = s->rows[s->stage_buf] + static_cast<size_t>(accepted) * s->hidden;
+    s->stage_buf ^= 1;
     s->token_count += static_cast<uint64_t>(accepted) + 1;
     s->staged_rows = 0;
     s->draft_count = 0;

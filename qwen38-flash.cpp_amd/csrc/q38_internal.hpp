@@ -15,7 +15,23 @@ struct ProjDev {
     const uint32_t* codes;   // [E+1, OUT, words]
     const uint16_t* scales;  // [E+1, OUT, ngrp] fp16
     const uint16_t* book;    // [2^bits, dim] fp16
+    const uint16_t* book4;   // [dim/4, 2^bits, 4] fp16: the codebook split into 4-dim chunks
     int words, ngrp, dim, bits;
+};
+
+// Workspace views of one MoE call (rows <= kMaxRows).
+struct MoeBufs {
+    uint16_t* x;       // [M, H] bf16 normalised layer input
+    uint16_t* x16;     // [M, H] fp16 copy of x (MFMA operand)
+    float* logits;     // [M, E]
+    float* sgate;      // [M] sigmoid(x . w_sg) rounded to bf16
+    int32_t* experts;  // [M*K]
+    float* weights;    // [M*K]
+    int32_t* plan;     // [2 + 4*M*K]
+    float* g;          // [M*K + M, I] gate projections (sorted route order; shared rows last)
+    float* u;          // [M*K + M, I] up projections
+    float* d;          // [M*K + M, H] down projections
+    size_t zero_floats;  // g, u, d are one contiguous region of this many floats
 };
 
 struct LayerDev {
@@ -33,18 +49,18 @@ struct HeadDev {
     float s_max;             // max |scale| over the head (exact-pass window)
 };
 
-// MoE layer
-hipError_t launch_router(const LayerDev& L, const uint16_t* hin, int M, int do_norm, float eps, uint16_t* xn,
-                         float* logits, float* sgate, hipStream_t st);
-hipError_t launch_topk_plan(const LayerDev& L, const float* logits, int M, int32_t* experts, float* weights,
-                            int32_t* plan, hipStream_t st);
-hipError_t launch_gate_up(const LayerDev& L, const uint16_t* xn, int M, const int32_t* plan, uint16_t* hbuf,
-                          hipStream_t st);
-hipError_t launch_down(const LayerDev& L, int M, const int32_t* plan, const uint16_t* hbuf, uint16_t* dbuf,
-                       hipStream_t st);
-hipError_t launch_combine(const LayerDev& L, int M, const int32_t* plan, const float* weights, const float* sgate,
-                          const uint16_t* dbuf, const uint16_t* hin, uint16_t* out, hipStream_t st);
+// MoE layer (rows M <= kMaxRows)
+// Router logits (+ RMSNorm of h when do_norm; otherwise h is the normalised input).
+hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* h, int do_norm, float eps,
+                         hipStream_t st);
+hipError_t launch_topk_plan(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+// chain: h <- h + y (in place); otherwise out <- y.
+hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st);
+hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_t* book4, hipStream_t st);
+bool moe_uses_mfma(const LayerDev& L);
 
 // generators
 hipError_t launch_gen_codes(uint64_t key, int e0, int n_experts, int out_dim, int nsub, int bits, int words,
@@ -53,6 +69,8 @@ hipError_t launch_gen_uniform_f16(uint64_t key, int64_t idx0, int64_t n, double 
                                   hipStream_t st);
 hipError_t launch_gen_normal(uint64_t key, int64_t n, double sd, int f16, uint16_t* out, hipStream_t st);
 hipError_t launch_gen_embed(uint64_t seed, const uint32_t* tokens, int n, int H, uint16_t* out, hipStream_t st);
+hipError_t launch_gen_embed_dev(uint64_t seed, const uint32_t* tokens_dev, int n, int H, uint16_t* out,
+                                hipStream_t st);
 hipError_t launch_book_to_int8(const uint16_t* book16, int n, int8_t* q8, uint16_t* scale, hipStream_t st);
 hipError_t launch_gen_head(const HeadDev& hd, uint64_t seed, int8_t* w, uint16_t* scales, hipStream_t st);
 hipError_t launch_scale_absmax(const uint16_t* scales, int64_t n, float* out, hipStream_t st);

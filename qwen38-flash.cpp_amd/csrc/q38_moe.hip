@@ -2,18 +2,19 @@
 // (rows <= 16), plus the synthetic-weight generators.
 //
 // Per layer the launch sequence is
-//   k_router      RMSNorm (chain mode) + router logits with the fixed-order contract
-//                 (R1) + the shared-expert gate logit; one wave per expert row of Wr.
-//   k_topk_plan   softmax/top-k/normalise per row (R2) and the gather-by-expert plan
+//   k_router      router logits with the fixed-order contract (R1) + the shared-expert
+//                 gate logit, one wave per row of Wr; clears this layer's accumulators.
+//   k_topk_plan   softmax / top-k / normalise per row (R2) and the gather-by-expert plan
 //                 (R3): unique experts ascending, each with its routes in (row, slot)
 //                 order; one workgroup.
-//   k_gate_up     per (unique expert, 64 output rows): every packed code row is read
-//                 once and applied to all rows routed to that expert (R4, R5, R7);
-//                 SwiGLU epilogue with the reference's rounding points.
-//   k_down        per (unique expert, 128 output rows): down projection of the expert's
-//                 SwiGLU rows, rounded to BF16 per route (R8).
+//   k_gu_mfma     gate and up projections (R4, R5, R7): persistent workgroups, each with
+//                 one 4-dim chunk of one codebook resident in LDS, MFMA tiles over every
+//                 routed row of an expert, so each packed code row is read once per chunk.
+//   k_down_mfma   SwiGLU of the gate/up sums + down projection (R7, R8), same scheme.
 //   k_combine     ordered route reduction (slot order) + shared expert x sigmoid gate +
-//                 merge (R8, R10, R11), and in chain mode the residual add.
+//                 merge (R8, R10, R11); in chain mode the residual add and the next
+//                 layer's RMSNorm.
+// Layers with per-64-input scale groups use the k_*_grouped VALU kernels instead.
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
 
@@ -79,6 +80,17 @@ __global__ void k_gen_embed(uint64_t key, TokenList toks, int n, int H, uint16_t
     }
 }
 
+__global__ void k_gen_embed_dev(uint64_t key, const uint32_t* __restrict__ toks, int n, int H,
+                                uint16_t* __restrict__ out) {
+    const int64_t total = static_cast<int64_t>(n) * H;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int r = static_cast<int>(i / H), c = static_cast<int>(i % H);
+        const double z = normal_at(key, static_cast<uint64_t>(toks[r]) * H + c);
+        out[i] = f2bf(static_cast<float>(z));
+    }
+}
+
 // Approximate INT8 codebook with one FP16 scale per codebook: scale = f16(max|v| / 127),
 // q = clamp(rint(v / scale), -127, 127). One workgroup; v = the FP16 N(0,1) book.
 __global__ void k_book_to_int8(const uint16_t* __restrict__ book16, int n, int8_t* __restrict__ q8,
@@ -101,77 +113,151 @@ __global__ void k_book_to_int8(const uint16_t* __restrict__ book16, int n, int8_
     }
 }
 
+// ============================================================== DPP wave reductions
+// Order-independent reductions (max) use DPP row operations and readlane; the summations
+// whose order is part of a contract keep the xor butterfly of q38_device.hpp.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xF,
+                                                             0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t max_step_u64(uint64_t k) {
+    const uint32_t h = dpp32<CTRL>(static_cast<uint32_t>(k >> 32));
+    const uint32_t l = dpp32<CTRL>(static_cast<uint32_t>(k));
+    const uint64_t o = (static_cast<uint64_t>(h) << 32) | l;
+    return o > k ? o : k;
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t k, int lane) {
+    const uint32_t h = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(k >> 32), lane));
+    const uint32_t l = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(k), lane));
+    return (static_cast<uint64_t>(h) << 32) | l;
+}
+// quad_perm(1,0,3,2), quad_perm(2,3,0,1), row_half_mirror, row_mirror, then rows via readlane.
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t k) {
+    k = max_step_u64<0xB1>(k);
+    k = max_step_u64<0x4E>(k);
+    k = max_step_u64<0x141>(k);
+    k = max_step_u64<0x140>(k);
+    uint64_t m = readlane_u64(k, 0);
+    const uint64_t a = readlane_u64(k, 16), b = readlane_u64(k, 32), c = readlane_u64(k, 48);
+    m = a > m ? a : m;
+    m = b > m ? b : m;
+    m = c > m ? c : m;
+    return m;
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    auto step = [](float x, uint32_t o) { return fmaxf(x, __uint_as_float(o)); };
+    v = step(v, dpp32<0xB1>(__float_as_uint(v)));
+    v = step(v, dpp32<0x4E>(__float_as_uint(v)));
+    v = step(v, dpp32<0x141>(__float_as_uint(v)));
+    v = step(v, dpp32<0x140>(__float_as_uint(v)));
+    float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48)));
+    return m;
+}
+
 // ============================================================== router (R1)
-// One wave per row of Wr (plus one for w_sg). Lane l accumulates c = 512t + 8l + j
-// (t outer, j inner) with fmaf, then the xor butterfly; rounded to BF16.
+// One wave per row of Wr (plus one for w_sg). In chain mode every wave first forms the
+// layer input x = T(h / sqrt(mean(h^2) + eps)) from its own loads of h: lane l holds the
+// columns c = 512t + 8l + j, so the wave covers whole rows and computes each row's sum of
+// squares (lane partials, xor butterfly) identically in every wave. Logit contract: lane
+// l accumulates x*w over its columns (t outer, j inner) with fmaf, xor butterfly, BF16.
+// Workgroup 0 stores x (bf16) and x16 (fp16, the MFMA operand); all workgroups clear the
+// layer's g/u/d accumulators.
 template <int MAXM>
-__global__ __launch_bounds__(256) void k_router(LayerDev L, const uint16_t* __restrict__ hin, int M, int do_norm,
-                                                float eps, uint16_t* __restrict__ xn_out,
-                                                float* __restrict__ logits, float* __restrict__ sgate) {
-    extern __shared__ __align__(16) uint16_t xs[];  // [M][H]
-    __shared__ float red[4][MAXM];
-    const int H = L.H;
+__global__ __launch_bounds__(256) void k_router(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ hin,
+                                                int do_norm, float eps) {
+    const int H = L.H, T = H / 512;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (do_norm) {
-#pragma unroll
-        for (int r = 0; r < MAXM; ++r) {
-            if (r < M) {
-                float ss = 0.0f;
-                for (int c = tid; c < H; c += 256) {
-                    const float v = bf2f(hin[r * H + c]);
-                    ss = fmaf(v, v, ss);
-                }
-                ss = wave_sum_xor(ss);
-                if (lane == 0) red[wave][r] = ss;
-            }
-        }
-        __syncthreads();
-        for (int i = tid; i < M * H; i += 256) {
-            const int r = i / H;
-            const float ss = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
-            const float inv = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
-            const uint16_t x = f2bf(bf2f(hin[i]) * inv);
-            xs[i] = x;
-            if (blockIdx.x == 0 && xn_out) xn_out[i] = x;
-        }
-    } else {
-        const uint4* src = reinterpret_cast<const uint4*>(hin);
-        uint4* dst = reinterpret_cast<uint4*>(xs);
-        for (int i = tid; i < M * H / 8; i += 256) dst[i] = src[i];
+    {
+        const size_t gt = blockIdx.x * 256 + tid, gs = gridDim.x * 256;
+        float4* z = reinterpret_cast<float4*>(B.g);
+        for (size_t i = gt; i < B.zero_floats / 4; i += gs) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    __syncthreads();
     const int e = blockIdx.x * 4 + wave;
     const int n_rows = L.E + (L.has_shared ? 1 : 0);
-    if (e >= n_rows) return;
+    const bool store_x = blockIdx.x == 0 && wave == 0;
+    if (e >= n_rows && !store_x) return;
     const uint16_t* w = e < L.E ? L.router + static_cast<size_t>(e) * H : L.wsg;
-    float acc[MAXM];
+    constexpr int MAXT = 5;  // H <= 2560
+    uint4 wv[MAXT];
 #pragma unroll
-    for (int r = 0; r < MAXM; ++r) acc[r] = 0.0f;
-    for (int t = 0; t < H / 512; ++t) {
-        const uint4 wv = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
-        const float wf[8] = {bflo(wv.x), bfhi(wv.x), bflo(wv.y), bfhi(wv.y),
-                             bflo(wv.z), bfhi(wv.z), bflo(wv.w), bfhi(wv.w)};
-#pragma unroll
-        for (int r = 0; r < MAXM; ++r) {
-            if (r < M) {
-                const uint4 xv = *reinterpret_cast<const uint4*>(xs + r * H + 512 * t + 8 * lane);
-                const float xf[8] = {bflo(xv.x), bfhi(xv.x), bflo(xv.y), bfhi(xv.y),
-                                     bflo(xv.z), bfhi(xv.z), bflo(xv.w), bfhi(xv.w)};
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[r] = __builtin_fmaf(xf[j], wf[j], acc[r]);
-            }
-        }
-    }
+    for (int t = 0; t < MAXT; ++t)
+        if (t < T && e < n_rows) wv[t] = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
 #pragma unroll
     for (int r = 0; r < MAXM; ++r) {
-        if (r < M) {
-            const float s = wave_sum_xor(acc[r]);
+        if (r >= M) break;
+        uint4 xv[MAXT];
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t)
+            if (t < T) xv[t] = *reinterpret_cast<const uint4*>(hin + r * H + 512 * t + 8 * lane);
+        if (do_norm) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int t = 0; t < MAXT; ++t) {
+                if (t < T) {
+                    const uint32_t q[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        ss = fmaf(bflo(q[k]), bflo(q[k]), ss);
+                        ss = fmaf(bfhi(q[k]), bfhi(q[k]), ss);
+                    }
+                }
+            }
+            ss = wave_sum_xor(ss);
+            const float inv = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+#pragma unroll
+            for (int t = 0; t < MAXT; ++t) {
+                if (t < T) {
+                    uint32_t q[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t lo = f2bf(bflo(q[k]) * inv), hi = f2bf(bfhi(q[k]) * inv);
+                        q[k] = lo | (hi << 16);
+                    }
+                    xv[t] = make_uint4(q[0], q[1], q[2], q[3]);
+                }
+            }
+        }
+        if (store_x) {
+#pragma unroll
+            for (int t = 0; t < MAXT; ++t) {
+                if (t < T) {
+                    const size_t at = static_cast<size_t>(r) * H + 512 * t + 8 * lane;
+                    *reinterpret_cast<uint4*>(B.x + at) = xv[t];
+                    const uint32_t q[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+                    uint32_t hq[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        hq[k] = static_cast<uint32_t>(f2h(bflo(q[k]))) | (static_cast<uint32_t>(f2h(bfhi(q[k]))) << 16);
+                    *reinterpret_cast<uint4*>(B.x16 + at) = make_uint4(hq[0], hq[1], hq[2], hq[3]);
+                }
+            }
+        }
+        if (e < n_rows) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < MAXT; ++t) {
+                if (t < T) {
+                    const uint32_t xq[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+                    const uint32_t wq[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        acc = __builtin_fmaf(bflo(xq[k]), bflo(wq[k]), acc);
+                        acc = __builtin_fmaf(bfhi(xq[k]), bfhi(wq[k]), acc);
+                    }
+                }
+            }
+            const float s = wave_sum_xor(acc);
             if (lane == 0) {
                 if (e < L.E) {
-                    logits[r * L.E + e] = rbf(s);
+                    B.logits[r * L.E + e] = rbf(s);
                 } else {
                     const float lg = rbf(s);
-                    sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
+                    B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
                 }
             }
         }
@@ -179,29 +265,39 @@ __global__ __launch_bounds__(256) void k_router(LayerDev L, const uint16_t* __re
 }
 
 // ============================================================== top-k + plan (R2, R3)
-// One workgroup of 1024 threads; wave r handles row r (rows <= 16). Lane l owns experts
-// i = 64j + l. Plan: per expert (one thread each) count its routes, scan, and list them
-// in (row, slot) order.
-__global__ __launch_bounds__(1024) void k_topk_plan(const float* __restrict__ logits, int M, int E, int K,
-                                                    int normalize, int32_t* __restrict__ experts,
-                                                    float* __restrict__ weights, int32_t* __restrict__ plan) {
-    __shared__ int32_t ex_s[kMaxRows * kMaxTopK];
-    __shared__ int32_t sc_a[1024], sc_b[1024];
-    const int tid = threadIdx.x, lane = tid & 63, r = tid >> 6;
+// Block-level routine (any block of >= 256 threads). Wave w takes rows w, w + waves, ...:
+// lane l owns experts 64j + l as (p bits << 32 | ~index) keys; K rounds of a DPP wave max
+// pick (p desc, index asc). The plan is built by counting: route i lands at
+// #{routes (e, i') < (e_i, i)}; expert groups are marked with a ballot. The plan is left
+// in `plan` (LDS or global); `global_out` also receives experts and weights.
+struct TopkLds {
+    int32_t ex[kMaxRows * kMaxTopK];
+    int32_t sorted_e[kMaxRows * kMaxTopK];
+    int32_t wave_cnt[16];
+};
+
+// Rows are taken by waves [row_wave0, waves); the other waves may do unrelated work
+// (the MFMA gate/up kernel fills its codebook with them) before the first barrier.
+__device__ __forceinline__ void topk_plan_block(const LayerDev& L, const MoeBufs& B, int M, bool global_out, int32_t* plan,
+                                                TopkLds& t, int row_wave0) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int waves = blockDim.x >> 6;
+    const int E = L.E, K = L.K, MK = M * K;
     const int NJ = E / 64;
-    if (r < M) {
-        float lg[16];
+    for (int r = wave - row_wave0; wave >= row_wave0 && r < M; r += waves - row_wave0) {
         float mx = -INFINITY;
+        float lg[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            lg[j] = j < NJ ? logits[r * E + 64 * j + lane] : -INFINITY;
+            lg[j] = j < NJ ? B.logits[r * E + 64 * j + lane] : -INFINITY;
             mx = fmaxf(mx, lg[j]);
         }
-        mx = wave_max(mx);
-        float ev[16];
+        mx = wave_max_dpp(mx);
         double ds = 0.0;
+        float ev[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
+            ev[j] = 0.0f;
             if (j < NJ) {
                 ev[j] = exp_contract(lg[j] - mx);
                 ds += static_cast<double>(ev[j]);
@@ -211,81 +307,318 @@ __global__ __launch_bounds__(1024) void k_topk_plan(const float* __restrict__ lo
         uint64_t key[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
+            key[j] = 0;
             if (j < NJ) {
                 const float p = static_cast<float>(static_cast<double>(ev[j]) / ds);
                 key[j] = (static_cast<uint64_t>(__float_as_uint(p)) << 32) |
                          static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(64 * j + lane));
-            } else {
-                key[j] = 0;
             }
         }
-        float psel[kMaxTopK];
-        int isel[kMaxTopK];
+        float psel = 0.0f, sum = 0.0f;
+        int isel = 0;
         for (int s = 0; s < K; ++s) {
-            uint64_t best = 0;
+            uint64_t lm = key[0];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) best = key[j] > best ? key[j] : best;
-            best = wave_max_u64(best);
+            for (int j = 1; j < 16; ++j) lm = key[j] > lm ? key[j] : lm;
+            const uint64_t best = wave_max_u64_dpp(lm);
 #pragma unroll
             for (int j = 0; j < 16; ++j)
                 if (key[j] == best) key[j] = 0;
-            psel[s] = __uint_as_float(static_cast<uint32_t>(best >> 32));
-            isel[s] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+            const float p = __uint_as_float(static_cast<uint32_t>(best >> 32));
+            sum += p;
+            if (lane == s) {
+                psel = p;
+                isel = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+            }
         }
-        if (lane == 0) {
-            float sum = 0.0f;
-            for (int s = 0; s < K; ++s) sum += psel[s];
-            for (int s = 0; s < K; ++s) {
-                experts[r * K + s] = isel[s];
-                weights[r * K + s] = normalize ? psel[s] / sum : psel[s];
-                ex_s[r * K + s] = isel[s];
+        if (lane < K) {
+            t.ex[r * K + lane] = isel;
+            if (global_out) {
+                B.experts[r * K + lane] = isel;
+                B.weights[r * K + lane] = L.normalize ? psel / sum : psel;
             }
         }
     }
     __syncthreads();
-    const int MK = M * K;
-    int cnt = 0;
-    if (tid < E)
-        for (int i = 0; i < MK; ++i) cnt += ex_s[i] == tid;
-    // inclusive scans of cnt (offsets) and of (cnt > 0) (ranks)
-    sc_a[tid] = cnt;
-    sc_b[tid] = cnt > 0;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const int a = tid >= off ? sc_a[tid - off] : 0;
-        const int b = tid >= off ? sc_b[tid - off] : 0;
-        __syncthreads();
-        sc_a[tid] += a;
-        sc_b[tid] += b;
-        __syncthreads();
+    if (tid < MK) {
+        const int my_e = t.ex[tid];
+        const int my_key = (my_e << 8) | tid;
+        int pos = 0;
+        for (int j = 0; j < MK; ++j) pos += ((t.ex[j] << 8) | j) < my_key;
+        t.sorted_e[pos] = my_e;
+        plan[2 + 2 * MK + pos] = tid;   // route_list
+        plan[2 + 3 * MK + tid] = pos;   // route_pos
     }
-    int32_t* uexp = plan + 1;
-    int32_t* uoff = plan + 1 + MK;
-    int32_t* rlist = plan + 2 + 2 * MK;
-    int32_t* rpos = plan + 2 + 3 * MK;
-    if (tid < E && cnt > 0) {
-        const int off = sc_a[tid] - cnt;
-        const int rank = sc_b[tid] - 1;
-        uexp[rank] = tid;
-        uoff[rank] = off;
-        int n = 0;
-        for (int i = 0; i < MK; ++i)
-            if (ex_s[i] == tid) {
-                rlist[off + n] = i;
-                rpos[i] = off + n;
-                ++n;
-            }
+    __syncthreads();
+    const bool start = tid < MK && (tid == 0 || t.sorted_e[tid - 1] != t.sorted_e[tid]);
+    const uint64_t bal = __ballot(start);
+    if (lane == 0) t.wave_cnt[wave] = __popcll(bal);
+    __syncthreads();
+    int rank = __popcll(bal & ((1ull << lane) - 1ull));
+    for (int w = 0; w < wave; ++w) rank += t.wave_cnt[w];
+    if (start) {
+        plan[1 + rank] = t.sorted_e[tid];
+        plan[1 + MK + rank] = tid;
     }
     if (tid == 0) {
-        const int nu = sc_b[1023];
+        int nu = 0;
+        for (int w = 0; w < waves; ++w) nu += t.wave_cnt[w];
         plan[0] = nu;
-        uoff[nu] = MK;
+        plan[1 + MK + nu] = MK;
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void k_topk_plan(LayerDev L, MoeBufs B, int M) {
+    __shared__ TopkLds t;
+    topk_plan_block(L, B, M, true, B.plan, t, 0);
+}
+
+// Rows of unique-expert slot ui: the routed experts in ascending id, then the shared
+// expert (all M rows). Returns false for an empty slot.
+__device__ __forceinline__ bool slot_rows(const int32_t* plan, int M, int K, int has_shared, int ui, int E,
+                                          int* expert, int* n, int* first_pos) {
+    const int nu = plan[0];
+    const int MK = M * K;
+    if (ui < nu) {
+        *expert = plan[1 + ui];
+        const int a = plan[1 + MK + ui], b = plan[1 + MK + ui + 1];
+        *n = b - a;
+        *first_pos = a;
+        return true;
+    }
+    if (ui == nu && has_shared) {
+        *expert = E;
+        *n = M;
+        *first_pos = MK;
+        return true;
+    }
+    return false;
+}
+// The request row of the j-th route of slot ui.
+__device__ __forceinline__ int route_row(const int32_t* plan, int M, int K, int pos0, int j, bool shared) {
+    return shared ? j : plan[2 + 2 * M * K + pos0 + j] / K;
+}
+
+// ============================================================== MFMA expert projections
+// A workgroup holds one 4-dim chunk of one projection's codebook in LDS (128 KiB for
+// d8/14-bit) for the whole launch and walks its share of (expert slot, 128-row tile)
+// items. A wave computes a 16-row x (up to 8 routed rows) tile with
+// v_mfma_f32_16x16x32_f16: A = codebook entries looked up in LDS by the packed codes of
+// the 16 rows (lane (r, q) decodes the codes of row r for subvectors [q*S4, (q+1)*S4)),
+// B = the chunk's dims of the routed rows' inputs (fp16, staged in LDS). Every code row
+// is read once per chunk; the next item's code words are loaded while the current item
+// computes. Chunk partial sums (times the row scale) are added into fp32 accumulators,
+// two addends each for d8 (order-independent).
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaThreads = 512;       // 8 waves
+constexpr int kMfmaRowsPerItem = 128;   // 8 waves x 16 rows
+constexpr int kMfmaMaxCols = 8;         // routed rows staged per pass
+constexpr int kPlanInts = 2 + 4 * kMaxRows * kMaxTopK;
+
+template <int BITS, int NSUB>
+__device__ __forceinline__ void load_lane_words(const uint32_t* src, uint32_t* w) {
+    constexpr int WPL = (NSUB / 4) * BITS / 32;
+    if constexpr (WPL % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < WPL / 4; ++i) {
+            const uint4 v = reinterpret_cast<const uint4*>(src)[i];
+            w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < WPL; ++i) w[i] = src[i];
+    }
+    w[WPL] = 0;
+}
+
+// One 16-row MFMA tile over all subvectors of one chunk.
+template <int BITS, int NSUB>
+__device__ __forceinline__ f4_t mfma_tile(const uint32_t* w, const uint2* book, const uint4* xs, int col, int q,
+                                          bool col_active) {
+    constexpr int S4 = NSUB / 4;
+    f4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < S4 / 2; ++t) {
+        const uint32_t c1 = code_from<BITS>(w, 2 * t);
+        const uint32_t c2 = code_from<BITS>(w, 2 * t + 1);
+        const uint2 a1 = book[c1];
+        const uint2 a2 = book[c2];
+        const uint4 av = make_uint4(a1.x, a1.y, a2.x, a2.y);
+        uint4 bv = make_uint4(0u, 0u, 0u, 0u);
+        if (col_active) bv = xs[(col * NSUB + q * S4 + 2 * t) / 2];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, av), __builtin_bit_cast(h8_t, bv),
+                                                     acc, 0, 0, 0);
+    }
+    return acc;
+}
+
+// Codebook chunk -> LDS, by threads [t0, t0 + nthreads) of the workgroup.
+template <int KENT>
+__device__ __forceinline__ void fill_book(const uint16_t* src4, unsigned char* lds, int t, int nthreads) {
+    const uint4* src = reinterpret_cast<const uint4*>(src4);
+    uint4* dst = reinterpret_cast<uint4*>(lds);
+    constexpr int N = KENT / 2;  // uint4 entries
+    int i = t;
+    for (; i + 3 * nthreads < N; i += 4 * nthreads) {
+        const uint4 a = src[i], b = src[i + nthreads], c = src[i + 2 * nthreads], d = src[i + 3 * nthreads];
+        dst[i] = a;
+        dst[i + nthreads] = b;
+        dst[i + 2 * nthreads] = c;
+        dst[i + 3 * nthreads] = d;
+    }
+    for (; i < N; i += nthreads) dst[i] = src[i];
+}
+
+template <int BITS, int NSUB, int NCHUNK>
+__global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ TopkLds tk;
+    __shared__ int32_t plan[kPlanInts];
+    constexpr int KENT = 1 << BITS;
+    const uint2* book = reinterpret_cast<const uint2*>(lds);       // [KENT] x 4 fp16
+    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);          // [8][NSUB][4] fp16
+    constexpr int TYPES = 2 * NCHUNK;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
+    const int type = kk % TYPES;
+    const int proj = type / NCHUNK, chunk = type % NCHUNK;
+    const int per_type = (gridDim.x / (8 * TYPES)) * 8;
+    const int idx = (kk / TYPES) * 8 + x8;
+    const ProjDev& P = L.p[proj];
+    // waves 0-3 load the codebook chunk while waves 4-7 route; every workgroup derives
+    // the same plan and workgroup 0 publishes it
+    if (wave < 4) fill_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, tid, 256);
+    topk_plan_block(L, B, M, blockIdx.x == 0, plan, tk, 4);
+    if (blockIdx.x == 0)
+        for (int i = tid; i < 2 + 4 * M * L.K; i += kMfmaThreads) B.plan[i] = plan[i];
+    const int H = L.H, I = L.I, K = L.K;
+    const int nu = plan[0];
+    const int n_items = (nu + (L.has_shared ? 1 : 0)) * (I / kMfmaRowsPerItem);
+    const int tiles = I / kMfmaRowsPerItem;
+    float* out = proj == 0 ? B.g : B.u;
+    const int r16 = lane & 15, q = lane >> 4;
+    constexpr int S4 = NSUB / 4;
+    constexpr int WPL = S4 * BITS / 32;
+    auto code_src = [&](int item) {
+        int expert, n, pos0;
+        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
+        const size_t rowi = static_cast<size_t>(expert) * I + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
+        return P.codes + rowi * P.words + q * WPL;
+    };
+    uint32_t w[WPL + 1], wn[WPL + 1];
+    if (idx < n_items) load_lane_words<BITS, NSUB>(code_src(idx), w);
+    for (int item = idx; item < n_items; item += per_type) {
+        if (item + per_type < n_items) load_lane_words<BITS, NSUB>(code_src(item + per_type), wn);
+        const int ui = item / tiles, tile = item % tiles;
+        int expert, n, pos0;
+        slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
+        const bool shared = ui == nu;
+        const int o0 = tile * kMfmaRowsPerItem + wave * 16;
+        for (int j0 = 0; j0 < n; j0 += kMfmaMaxCols) {
+            const int nj = n - j0 < kMfmaMaxCols ? n - j0 : kMfmaMaxCols;
+            __syncthreads();
+            for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
+                const int j = i / NSUB, s = i % NSUB;
+                const int row = route_row(plan, M, K, pos0, j0 + j, shared);
+                reinterpret_cast<uint2*>(xs)[j * NSUB + s] =
+                    *reinterpret_cast<const uint2*>(B.x16 + static_cast<size_t>(row) * H + s * (4 * NCHUNK) + 4 * chunk);
+            }
+            __syncthreads();
+            const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs, r16, q, r16 < nj);
+            if (r16 < nj) {
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int o = o0 + 4 * q + rr;
+                    const float sc = h2f(P.scales[static_cast<size_t>(expert) * I + o]);
+                    atomicAdd(&out[static_cast<size_t>(pos0 + j0 + r16) * I + o], sc * acc[rr]);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i <= WPL; ++i) w[i] = wn[i];
     }
 }
 
-// ============================================================== expert projections
-// Lane mapping: a lane owns 16 consecutive codes of a row (a half 32-code block: BITS/2
-// words); LPR lanes (power of two, padded) cover one row; 64/LPR rows per wave.
+// SwiGLU with the reference's rounding points (src/vq_metal_kernels.hpp:589-595):
+// h = T(T(silu(T(g))) * T(u)).
+__device__ __forceinline__ float swiglu(float g, float u) {
+    const float gt = rbf(g);
+    const float s = rbf(gt / (1.0f + expf(-gt)));
+    return rbf(s * rbf(u));
+}
+
+template <int BITS, int NSUB, int NCHUNK>
+__global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ int32_t plan[kPlanInts];
+    constexpr int KENT = 1 << BITS;
+    const uint2* book = reinterpret_cast<const uint2*>(lds);
+    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
+    const int chunk = kk % NCHUNK;
+    const int per_type = (gridDim.x / (8 * NCHUNK)) * 8;
+    const int idx = (kk / NCHUNK) * 8 + x8;
+    const ProjDev& P = L.p[2];
+    const int H = L.H, I = L.I, K = L.K;
+    for (int i = tid; i < 2 + 4 * M * K; i += kMfmaThreads) plan[i] = B.plan[i];
+    fill_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, tid, kMfmaThreads);
+    __syncthreads();
+    const int nu = plan[0];
+    const int tiles = H / kMfmaRowsPerItem;
+    const int n_items = (nu + (L.has_shared ? 1 : 0)) * tiles;
+    const int r16 = lane & 15, q = lane >> 4;
+    constexpr int S4 = NSUB / 4;
+    constexpr int WPL = S4 * BITS / 32;
+    auto code_src = [&](int item) {
+        int expert, n, pos0;
+        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
+        const size_t rowi = static_cast<size_t>(expert) * H + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
+        return P.codes + rowi * P.words + q * WPL;
+    };
+    uint32_t w[WPL + 1], wn[WPL + 1];
+    if (idx < n_items) load_lane_words<BITS, NSUB>(code_src(idx), w);
+    for (int item = idx; item < n_items; item += per_type) {
+        if (item + per_type < n_items) load_lane_words<BITS, NSUB>(code_src(item + per_type), wn);
+        const int ui = item / tiles, tile = item % tiles;
+        int expert, n, pos0;
+        slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
+        const int o0 = tile * kMfmaRowsPerItem + wave * 16;
+        for (int j0 = 0; j0 < n; j0 += kMfmaMaxCols) {
+            const int nj = n - j0 < kMfmaMaxCols ? n - j0 : kMfmaMaxCols;
+            __syncthreads();
+            for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
+                const int j = i / NSUB, s = i % NSUB;
+                const size_t base = static_cast<size_t>(pos0 + j0 + j) * I + s * (4 * NCHUNK) + 4 * chunk;
+                const float4 gv = *reinterpret_cast<const float4*>(B.g + base);
+                const float4 uv = *reinterpret_cast<const float4*>(B.u + base);
+                const uint32_t h0 = f2h(swiglu(gv.x, uv.x)), h1 = f2h(swiglu(gv.y, uv.y));
+                const uint32_t h2 = f2h(swiglu(gv.z, uv.z)), h3 = f2h(swiglu(gv.w, uv.w));
+                reinterpret_cast<uint2*>(xs)[j * NSUB + s] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+            }
+            __syncthreads();
+            const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs, r16, q, r16 < nj);
+            if (r16 < nj) {
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int o = o0 + 4 * q + rr;
+                    const float sc = h2f(P.scales[static_cast<size_t>(expert) * H + o]);
+                    atomicAdd(&B.d[static_cast<size_t>(pos0 + j0 + r16) * H + o], sc * acc[rr]);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i <= WPL; ++i) w[i] = wn[i];
+    }
+}
+
+// ============================================================== grouped-scale path
+// Layers whose scales are per 64-input group (the reference checkpoint layout,
+// src/sparse_moe.cpp:641-647) take this path: VALU dot products with codebook reads
+// through the cache, per-group scaling in the lane. Same fp32 g/u/d outputs.
 template <int D>
 struct Vec;
 template <>
@@ -299,11 +632,6 @@ struct Vec<8> {
             v[2 * i + 1] = h2f(static_cast<uint16_t>(w[i] >> 16));
         }
     }
-    static __device__ __forceinline__ void load_x(const uint16_t* x, float* v) {
-        const uint4 b = *reinterpret_cast<const uint4*>(x);
-        v[0] = bflo(b.x); v[1] = bfhi(b.x); v[2] = bflo(b.y); v[3] = bfhi(b.y);
-        v[4] = bflo(b.z); v[5] = bfhi(b.z); v[6] = bflo(b.w); v[7] = bfhi(b.w);
-    }
 };
 template <>
 struct Vec<4> {
@@ -314,171 +642,33 @@ struct Vec<4> {
         v[2] = h2f(static_cast<uint16_t>(b.y));
         v[3] = h2f(static_cast<uint16_t>(b.y >> 16));
     }
-    static __device__ __forceinline__ void load_x(const uint16_t* x, float* v) {
-        const uint2 b = *reinterpret_cast<const uint2*>(x);
-        v[0] = bflo(b.x); v[1] = bfhi(b.x); v[2] = bflo(b.y); v[3] = bfhi(b.y);
-    }
 };
-
-// Resolve the rows of unique-expert slot ui. Returns false when the slot is empty.
-__device__ __forceinline__ bool slot_rows(const int32_t* plan, int M, int K, int has_shared, int ui, int E,
-                                          int* expert, int* n, int* first_pos, bool* shared) {
-    const int nu = plan[0];
-    const int MK = M * K;
-    if (ui < nu) {
-        *expert = plan[1 + ui];
-        const int a = plan[1 + MK + ui], b = plan[1 + MK + ui + 1];
-        *n = b - a;
-        *first_pos = a;
-        *shared = false;
-        return true;
-    }
-    if (ui == nu && has_shared) {
-        *expert = E;
-        *n = M;
-        *first_pos = MK;
-        *shared = true;
-        return true;
-    }
-    return false;
-}
 
 constexpr int kGuRowsPerBlock = 64;
 constexpr int kDownRowsPerBlock = 128;
 
+// Lane mapping: a lane owns 16 consecutive codes of a row (BITS/2 words); LPR lanes
+// (power of two, padded) cover one row; 64/LPR rows per wave. in_f: [n][IN] floats.
 template <int D, int BITS, int LPR, int MAXN>
-__global__ __launch_bounds__(256) void k_gate_up(LayerDev L, const uint16_t* __restrict__ xn, int M,
-                                                 const int32_t* __restrict__ plan, uint16_t* __restrict__ hbuf) {
-    extern __shared__ __align__(16) uint16_t xs[];  // [n][H]
-    int expert, n, pos0;
-    bool shared;
-    if (!slot_rows(plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0, &shared)) return;
-    const int H = L.H, I = L.I, MK = M * L.K;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // stage the expert's input rows
-    for (int i = tid; i < n * H / 8; i += 256) {
-        const int j = i / (H / 8), c8 = i % (H / 8);
-        const int row = shared ? j : plan[2 + 2 * MK + pos0 + j] / L.K;
-        reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(xn + static_cast<size_t>(row) * H)[c8];
-    }
-    __syncthreads();
-    const ProjDev& G = L.p[0];
-    const ProjDev& U = L.p[1];
-    const int nsub = H / D;
-    const int lanes_used = nsub / 16;
-    const int sub_lane = lane % LPR;
-    const bool active = sub_lane < lanes_used;
-    const int s0 = sub_lane * 16;
-    const bool row_scale = G.ngrp == 1;
-    const int spg = H / G.ngrp / D;  // subvectors per scale group
-    constexpr int WPL = BITS / 2;    // words per 16 codes
-    constexpr int RPW = 64 / LPR;
-    for (int it = 0; it < kGuRowsPerBlock / (4 * RPW); ++it) {
-        const int o = blockIdx.x * kGuRowsPerBlock + it * 4 * RPW + wave * RPW + lane / LPR;
-        float ga[MAXN], ua[MAXN];
-#pragma unroll
-        for (int j = 0; j < MAXN; ++j) { ga[j] = 0.0f; ua[j] = 0.0f; }
-        if (active && o < I) {
-            const size_t rowi = static_cast<size_t>(expert) * I + o;
-            const uint32_t* gw = G.codes + rowi * G.words + (s0 / 32) * BITS + ((s0 % 32) / 16) * WPL;
-            const uint32_t* uw = U.codes + rowi * U.words + (s0 / 32) * BITS + ((s0 % 32) / 16) * WPL;
-            uint32_t gwr[WPL + 1], uwr[WPL + 1];
-#pragma unroll
-            for (int i = 0; i < WPL; ++i) { gwr[i] = gw[i]; uwr[i] = uw[i]; }
-            gwr[WPL] = 0; uwr[WPL] = 0;
-            float gp[MAXN], up[MAXN];
-#pragma unroll
-            for (int j = 0; j < MAXN; ++j) { gp[j] = 0.0f; up[j] = 0.0f; }
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const uint32_t gc = code_from<BITS>(gwr, q);
-                const uint32_t uc = code_from<BITS>(uwr, q);
-                float gb[D], ub[D];
-                Vec<D>::load_book(G.book, gc, gb);
-                Vec<D>::load_book(U.book, uc, ub);
-                const int s = s0 + q;
-#pragma unroll
-                for (int j = 0; j < MAXN; ++j) {
-                    if (j < n) {
-                        float xv[D];
-                        Vec<D>::load_x(xs + j * H + s * D, xv);
-#pragma unroll
-                        for (int d = 0; d < D; ++d) {
-                            gp[j] = fmaf(xv[d], gb[d], gp[j]);
-                            up[j] = fmaf(xv[d], ub[d], up[j]);
-                        }
-                    }
-                }
-                if (!row_scale && ((s + 1) % spg) == 0) {
-                    const int g = s / spg;
-                    const float gs = h2f(G.scales[rowi * G.ngrp + g]);
-                    const float us = h2f(U.scales[rowi * U.ngrp + g]);
-#pragma unroll
-                    for (int j = 0; j < MAXN; ++j) {
-                        ga[j] = fmaf(gs, gp[j], ga[j]);
-                        ua[j] = fmaf(us, up[j], ua[j]);
-                        gp[j] = 0.0f;
-                        up[j] = 0.0f;
-                    }
-                }
-            }
-            if (row_scale) {
-#pragma unroll
-                for (int j = 0; j < MAXN; ++j) { ga[j] = gp[j]; ua[j] = up[j]; }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < MAXN; ++j) {
-            ga[j] = group_sum_xor<LPR>(ga[j]);
-            ua[j] = group_sum_xor<LPR>(ua[j]);
-        }
-        if (sub_lane == 0 && o < I) {
-            const size_t rowi = static_cast<size_t>(expert) * I + o;
-            const float gsc = row_scale ? h2f(G.scales[rowi]) : 1.0f;
-            const float usc = row_scale ? h2f(U.scales[rowi]) : 1.0f;
-#pragma unroll
-            for (int j = 0; j < MAXN; ++j) {
-                if (j < n) {
-                    const float g = rbf(ga[j] * gsc);
-                    const float u = rbf(ua[j] * usc);
-                    const float s = rbf(g / (1.0f + expf(-g)));
-                    hbuf[static_cast<size_t>(pos0 + j) * I + o] = f2bf(s * u);
-                }
-            }
-        }
-    }
-    (void)MK;
-}
-
-template <int D, int BITS, int LPR, int MAXN>
-__global__ __launch_bounds__(256) void k_down(LayerDev L, int M, const int32_t* __restrict__ plan,
-                                              const uint16_t* __restrict__ hbuf, uint16_t* __restrict__ dbuf) {
-    extern __shared__ __align__(16) uint16_t hs[];  // [n][I]
-    int expert, n, pos0;
-    bool shared;
-    if (!slot_rows(plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0, &shared)) return;
-    const int H = L.H, I = L.I;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < n * I / 8; i += 256)
-        reinterpret_cast<uint4*>(hs)[i] = reinterpret_cast<const uint4*>(hbuf + static_cast<size_t>(pos0) * I)[i];
-    __syncthreads();
-    const ProjDev& P = L.p[2];
-    const int nsub = I / D;
+__device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int IN, int OUT, int o_base,
+                                             int rows_per_block, const float* in_f, int n, float* out,
+                                             int pos0, int wave, int lane) {
+    const int nsub = IN / D;
     const int lanes_used = (nsub + 15) / 16;
     const int sub_lane = lane % LPR;
     const bool active = sub_lane < lanes_used;
     const int s0 = sub_lane * 16;
+    const int spg = IN / P.ngrp / D;
     const bool row_scale = P.ngrp == 1;
-    const int spg = I / P.ngrp / D;
     constexpr int WPL = BITS / 2;
     constexpr int RPW = 64 / LPR;
-    for (int it = 0; it < kDownRowsPerBlock / (4 * RPW); ++it) {
-        const int o = blockIdx.x * kDownRowsPerBlock + it * 4 * RPW + wave * RPW + lane / LPR;
+    for (int it = 0; it < rows_per_block / (4 * RPW); ++it) {
+        const int o = o_base + it * 4 * RPW + wave * RPW + lane / LPR;
         float acc[MAXN];
 #pragma unroll
         for (int j = 0; j < MAXN; ++j) acc[j] = 0.0f;
-        if (active && o < H) {
-            const size_t rowi = static_cast<size_t>(expert) * H + o;
+        if (active && o < OUT) {
+            const size_t rowi = static_cast<size_t>(expert) * OUT + o;
             const uint32_t* pw = P.codes + rowi * P.words + (s0 / 32) * BITS + ((s0 % 32) / 16) * WPL;
             uint32_t wr[WPL + 1];
 #pragma unroll
@@ -488,20 +678,16 @@ __global__ __launch_bounds__(256) void k_down(LayerDev L, int M, const int32_t* 
 #pragma unroll
             for (int j = 0; j < MAXN; ++j) pp[j] = 0.0f;
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const int s = s0 + q;
-                const uint32_t c = code_from<BITS>(wr, q);
-                float b[D];
-                Vec<D>::load_book(P.book, c, b);
+            for (int qq = 0; qq < 16; ++qq) {
+                const int s = s0 + qq;
+                const uint32_t c = code_from<BITS>(wr, qq);
+                float bk[D];
+                Vec<D>::load_book(P.book, c, bk);
 #pragma unroll
-                for (int j = 0; j < MAXN; ++j) {
-                    if (j < n) {
-                        float xv[D];
-                        Vec<D>::load_x(hs + j * I + s * D, xv);
+                for (int j = 0; j < MAXN; ++j)
+                    if (j < n)
 #pragma unroll
-                        for (int d = 0; d < D; ++d) pp[j] = fmaf(xv[d], b[d], pp[j]);
-                    }
-                }
+                        for (int dd = 0; dd < D; ++dd) pp[j] = fmaf(in_f[j * IN + s * D + dd], bk[dd], pp[j]);
                 if (!row_scale && ((s + 1) % spg) == 0) {
                     const float sc = h2f(P.scales[rowi * P.ngrp + s / spg]);
 #pragma unroll
@@ -518,36 +704,70 @@ __global__ __launch_bounds__(256) void k_down(LayerDev L, int M, const int32_t* 
         }
 #pragma unroll
         for (int j = 0; j < MAXN; ++j) acc[j] = group_sum_xor<LPR>(acc[j]);
-        if (sub_lane == 0 && o < H) {
-            const size_t rowi = static_cast<size_t>(expert) * H + o;
-            const float sc = row_scale ? h2f(P.scales[rowi]) : 1.0f;
+        if (sub_lane == 0 && o < OUT) {
+            const float sc = row_scale ? h2f(P.scales[static_cast<size_t>(expert) * OUT + o]) : 1.0f;
 #pragma unroll
             for (int j = 0; j < MAXN; ++j)
-                if (j < n) dbuf[static_cast<size_t>(pos0 + j) * H + o] = f2bf(acc[j] * sc);
+                if (j < n) out[static_cast<size_t>(pos0 + j) * OUT + o] = acc[j] * sc;
         }
     }
 }
 
+template <int D, int BITS, int LPR>
+__global__ __launch_bounds__(256) void k_gu_grouped(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) float fin[];  // [n][H]
+    int expert, n, pos0;
+    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
+    const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
+    const int H = L.H, I = L.I;
+    for (int i = threadIdx.x; i < n * H; i += 256) {
+        const int j = i / H, c = i % H;
+        fin[i] = bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]);
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int o_base = blockIdx.x * kGuRowsPerBlock;
+    grouped_rows<D, BITS, LPR, kMaxRows>(L.p[0], expert, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave, lane);
+    grouped_rows<D, BITS, LPR, kMaxRows>(L.p[1], expert, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave, lane);
+}
+
+template <int D, int BITS, int LPR>
+__global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) float fin[];  // [n][I]
+    int expert, n, pos0;
+    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
+    const int H = L.H, I = L.I;
+    for (int i = threadIdx.x; i < n * I; i += 256) {
+        const size_t at = static_cast<size_t>(pos0) * I + i;
+        fin[i] = swiglu(B.g[at], B.u[at]);
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    grouped_rows<D, BITS, LPR, kMaxRows>(L.p[2], expert, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
+                                         fin, n, B.d, pos0, wave, lane);
+}
+
 // ============================================================== combine (R8, R10, R11)
-__global__ __launch_bounds__(256) void k_combine(LayerDev L, int M, const int32_t* __restrict__ plan,
-                                                 const float* __restrict__ weights, const float* __restrict__ sgate,
-                                                 const uint16_t* __restrict__ dbuf, const uint16_t* hin,
-                                                 uint16_t* out) {
+// One thread per (row, column): routed = T(sum_slot w_slot * T(d_slot)) in slot order,
+// shared = T(T(d_shared) * gate), y = T(routed + shared); chain mode adds the residual in
+// place (h <- T(h + y)), otherwise out <- y.
+__global__ __launch_bounds__(256) void k_combine(LayerDev L, MoeBufs B, int M, uint16_t* h, uint16_t* out) {
     const int r = blockIdx.y;
     const int o = blockIdx.x * 256 + threadIdx.x;
     const int H = L.H, K = L.K, MK = M * K;
     if (o >= H) return;
-    const int32_t* rpos = plan + 2 + 3 * MK;
+    const int32_t* rpos = B.plan + 2 + 3 * MK;
     float routed = 0.0f;
     for (int s = 0; s < K; ++s)
-        routed = fmaf(weights[r * K + s], bf2f(dbuf[static_cast<size_t>(rpos[r * K + s]) * H + o]), routed);
+        routed = fmaf(B.weights[r * K + s], rbf(B.d[static_cast<size_t>(rpos[r * K + s]) * H + o]), routed);
     float y = rbf(routed);
     if (L.has_shared) {
-        const float sh = rbf(bf2f(dbuf[static_cast<size_t>(MK + r) * H + o]) * sgate[r]);
+        const float sh = rbf(rbf(B.d[static_cast<size_t>(MK + r) * H + o]) * B.sgate[r]);
         y = rbf(y + sh);
     }
     const size_t i = static_cast<size_t>(r) * H + o;
-    out[i] = hin ? f2bf(bf2f(hin[i]) + y) : f2bf(y);
+    if (h) h[i] = f2bf(rbf(bf2f(h[i]) + y));
+    else out[i] = f2bf(y);
 }
 
 __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x, int H, float eps,
@@ -568,120 +788,182 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x,
         y[static_cast<size_t>(r) * H + c] = f2bf(bf2f(x[static_cast<size_t>(r) * H + c]) * inv);
 }
 
+// Split a [entries, dim] fp16 codebook into [dim/4][entries][4] chunks.
+__global__ void k_split_book(const uint16_t* __restrict__ book, int entries, int dim, uint16_t* __restrict__ out) {
+    const int n = entries * dim;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const int e = i / dim, d = i % dim;
+        out[(static_cast<size_t>(d / 4) * entries + e) * 4 + d % 4] = book[i];
+    }
+}
+
 // ============================================================== launchers
 namespace {
-template <int MAXM>
-hipError_t launch_router_m(const LayerDev& L, const uint16_t* hin, int M, int do_norm, float eps, uint16_t* xn,
-                           float* logits, float* sgate, hipStream_t st) {
-    const int rows = L.E + (L.has_shared ? 1 : 0);
-    const size_t lds = static_cast<size_t>(M) * L.H * 2;
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_router<MAXM>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
-        attr = true;
-    }
-    hipLaunchKernelGGL(k_router<MAXM>, dim3((rows + 3) / 4), dim3(256), lds, st, L, hin, M, do_norm, eps, xn,
-                       logits, sgate);
-    return hipGetLastError();
-}
-
-template <int D, int BITS, int LPR>
-hipError_t launch_gate_up_g(const LayerDev& L, const uint16_t* xn, int M, const int32_t* plan, uint16_t* hbuf,
-                            hipStream_t st) {
-    const dim3 grid((L.I + kGuRowsPerBlock - 1) / kGuRowsPerBlock, M * L.K + 1);
-    const size_t lds = static_cast<size_t>(M) * L.H * 2;
-    if (M <= 4) {
-        static bool attr = false;
-        if (!attr) { (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gate_up<D, BITS, LPR, 4>), hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024); attr = true; }
-        hipLaunchKernelGGL((k_gate_up<D, BITS, LPR, 4>), grid, dim3(256), lds, st, L, xn, M, plan, hbuf);
-    } else {
-        static bool attr = false;
-        if (!attr) { (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gate_up<D, BITS, LPR, 16>), hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024); attr = true; }
-        hipLaunchKernelGGL((k_gate_up<D, BITS, LPR, 16>), grid, dim3(256), lds, st, L, xn, M, plan, hbuf);
-    }
-    return hipGetLastError();
-}
-
-template <int D, int BITS, int LPR>
-hipError_t launch_down_g(const LayerDev& L, int M, const int32_t* plan, const uint16_t* hbuf, uint16_t* dbuf,
-                         hipStream_t st) {
-    const dim3 grid((L.H + kDownRowsPerBlock - 1) / kDownRowsPerBlock, M * L.K + 1);
-    const size_t lds = static_cast<size_t>(M) * L.I * 2;
-    if (M <= 4)
-        hipLaunchKernelGGL((k_down<D, BITS, LPR, 4>), grid, dim3(256), lds, st, L, M, plan, hbuf, dbuf);
-    else
-        hipLaunchKernelGGL((k_down<D, BITS, LPR, 16>), grid, dim3(256), lds, st, L, M, plan, hbuf, dbuf);
-    return hipGetLastError();
-}
-
 int next_pow2(int v) {
     int p = 1;
     while (p < v) p <<= 1;
     return p;
 }
-} // namespace
+int g_mfma_grid = 256;  // one persistent workgroup per CU (set from the device at first use)
 
-hipError_t launch_router(const LayerDev& L, const uint16_t* hin, int M, int do_norm, float eps, uint16_t* xn,
-                         float* logits, float* sgate, hipStream_t st) {
-    if (M <= 1) return launch_router_m<1>(L, hin, M, do_norm, eps, xn, logits, sgate, st);
-    if (M <= 2) return launch_router_m<2>(L, hin, M, do_norm, eps, xn, logits, sgate, st);
-    if (M <= 4) return launch_router_m<4>(L, hin, M, do_norm, eps, xn, logits, sgate, st);
-    if (M <= 8) return launch_router_m<8>(L, hin, M, do_norm, eps, xn, logits, sgate, st);
-    return launch_router_m<16>(L, hin, M, do_norm, eps, xn, logits, sgate, st);
+void init_grid() {
+    static bool done = false;
+    if (done) return;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus >= 64)
+        g_mfma_grid = cus / 32 * 32;
+    done = true;
 }
 
-hipError_t launch_topk_plan(const LayerDev& L, const float* logits, int M, int32_t* experts, float* weights,
-                            int32_t* plan, hipStream_t st) {
-    hipLaunchKernelGGL(k_topk_plan, dim3(1), dim3(1024), 0, st, logits, M, L.E, L.K, L.normalize, experts, weights,
-                       plan);
+template <int MAXM>
+hipError_t launch_router_m(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* h, int do_norm, float eps,
+                           hipStream_t st) {
+    const int rows = L.E + (L.has_shared ? 1 : 0);
+    hipLaunchKernelGGL(k_router<MAXM>, dim3((rows + 3) / 4), dim3(256), 0, st, L, B, M, h, do_norm, eps);
     return hipGetLastError();
 }
 
-hipError_t launch_gate_up(const LayerDev& L, const uint16_t* xn, int M, const int32_t* plan, uint16_t* hbuf,
-                          hipStream_t st) {
-    const int D = L.p[0].dim, B = L.p[0].bits;
+template <typename Kern>
+hipError_t set_lds(Kern k, size_t bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(bytes));
+}
+
+template <int BITS, int NSUB, int NCHUNK>
+hipError_t launch_gu_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kMfmaMaxCols) * NSUB * 8;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = set_lds(&k_gu_mfma<BITS, NSUB, NCHUNK>, lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_gu_mfma<BITS, NSUB, NCHUNK>), dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
+    return hipGetLastError();
+}
+template <int BITS, int NSUB, int NCHUNK>
+hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kMfmaMaxCols) * NSUB * 8;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = set_lds(&k_down_mfma<BITS, NSUB, NCHUNK>, lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_down_mfma<BITS, NSUB, NCHUNK>), dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
+    return hipGetLastError();
+}
+
+template <int D, int BITS, int LPR>
+hipError_t launch_gu_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    const size_t lds = static_cast<size_t>(M) * L.H * 4;
+    if (lds > 128 * 1024) return hipErrorInvalidValue;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = set_lds(&k_gu_grouped<D, BITS, LPR>, 128 * 1024);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_gu_grouped<D, BITS, LPR>), dim3(L.I / kGuRowsPerBlock, M * L.K + 1), dim3(256), lds, st, L,
+                       B, M);
+    return hipGetLastError();
+}
+template <int D, int BITS, int LPR>
+hipError_t launch_down_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    const size_t lds = static_cast<size_t>(M) * L.I * 4;
+    hipLaunchKernelGGL((k_down_grouped<D, BITS, LPR>), dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256), lds, st,
+                       L, B, M);
+    return hipGetLastError();
+}
+} // namespace
+
+bool moe_uses_mfma(const LayerDev& L) {
+    // MFMA tiles: per-row scales, 128-row tiles, and lane code spans of whole 16-code
+    // half-blocks (gate/up: d8 with H/8 in {256, 320} or d4 with H/4 = 512; down: d8 with
+    // I/8 = 64 or d4 with I/4 = 128).
+    if (L.p[0].ngrp != 1 || L.p[1].ngrp != 1 || L.p[2].ngrp != 1) return false;
+    if (L.I % kMfmaRowsPerItem || L.H % kMfmaRowsPerItem) return false;
+    const int gd = L.p[0].dim, gb = L.p[0].bits, dd = L.p[2].dim, db = L.p[2].bits;
+    const bool gu_ok = (gd == 8 && gb == 14 && (L.H == 2048 || L.H == 2560)) || (gd == 4 && gb == 8 && L.H == 2048);
+    const bool dn_ok = (dd == 8 && db == 14 && L.I == 512) || (dd == 4 && db == 8 && L.I == 512);
+    return gu_ok && dn_ok;
+}
+
+hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* h, int do_norm, float eps,
+                         hipStream_t st) {
+    if (M <= 1) return launch_router_m<1>(L, B, M, h, do_norm, eps, st);
+    if (M <= 2) return launch_router_m<2>(L, B, M, h, do_norm, eps, st);
+    if (M <= 4) return launch_router_m<4>(L, B, M, h, do_norm, eps, st);
+    if (M <= 8) return launch_router_m<8>(L, B, M, h, do_norm, eps, st);
+    return launch_router_m<16>(L, B, M, h, do_norm, eps, st);
+}
+
+hipError_t launch_topk_plan(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    hipLaunchKernelGGL(k_topk_plan, dim3(1), dim3(1024), 0, st, L, B, M);
+    return hipGetLastError();
+}
+
+hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    init_grid();
+    const int D = L.p[0].dim, BT = L.p[0].bits;
+    if (moe_uses_mfma(L)) {
+        const int nsub = L.H / D;
+        if (D == 8 && nsub == 256) return launch_gu_mfma_g<14, 256, 2>(L, B, M, st);
+        if (D == 8 && nsub == 320) return launch_gu_mfma_g<14, 320, 2>(L, B, M, st);
+        if (D == 4 && nsub == 512) return launch_gu_mfma_g<8, 512, 1>(L, B, M, st);
+        return hipErrorInvalidValue;
+    }
     const int lpr = next_pow2((L.H / D + 15) / 16);
-    if (D == 8 && B == 14) {
-        if (lpr == 16) return launch_gate_up_g<8, 14, 16>(L, xn, M, plan, hbuf, st);
-        if (lpr == 32) return launch_gate_up_g<8, 14, 32>(L, xn, M, plan, hbuf, st);
-        if (lpr == 8) return launch_gate_up_g<8, 14, 8>(L, xn, M, plan, hbuf, st);
-        if (lpr <= 4) return launch_gate_up_g<8, 14, 4>(L, xn, M, plan, hbuf, st);
-    } else if (D == 4 && B == 8) {
-        if (lpr == 32) return launch_gate_up_g<4, 8, 32>(L, xn, M, plan, hbuf, st);
-        if (lpr == 64) return launch_gate_up_g<4, 8, 64>(L, xn, M, plan, hbuf, st);
-        if (lpr == 16) return launch_gate_up_g<4, 8, 16>(L, xn, M, plan, hbuf, st);
-        if (lpr <= 8) return launch_gate_up_g<4, 8, 8>(L, xn, M, plan, hbuf, st);
+    if (D == 8 && BT == 14) {
+        if (lpr == 16) return launch_gu_grouped_g<8, 14, 16>(L, B, M, st);
+        if (lpr == 32) return launch_gu_grouped_g<8, 14, 32>(L, B, M, st);
+        if (lpr == 8) return launch_gu_grouped_g<8, 14, 8>(L, B, M, st);
+        if (lpr <= 4) return launch_gu_grouped_g<8, 14, 4>(L, B, M, st);
+    } else if (D == 4 && BT == 8) {
+        if (lpr == 32) return launch_gu_grouped_g<4, 8, 32>(L, B, M, st);
+        if (lpr == 64) return launch_gu_grouped_g<4, 8, 64>(L, B, M, st);
+        if (lpr == 16) return launch_gu_grouped_g<4, 8, 16>(L, B, M, st);
+        if (lpr <= 8) return launch_gu_grouped_g<4, 8, 8>(L, B, M, st);
     }
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_down(const LayerDev& L, int M, const int32_t* plan, const uint16_t* hbuf, uint16_t* dbuf,
-                       hipStream_t st) {
-    const int D = L.p[2].dim, B = L.p[2].bits;
+hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    init_grid();
+    const int D = L.p[2].dim, BT = L.p[2].bits;
+    if (moe_uses_mfma(L)) {
+        const int nsub = L.I / D;
+        if (D == 8 && nsub == 64) return launch_down_mfma_g<14, 64, 2>(L, B, M, st);
+        if (D == 4 && nsub == 128) return launch_down_mfma_g<8, 128, 1>(L, B, M, st);
+        return hipErrorInvalidValue;
+    }
     const int lpr = next_pow2((L.I / D + 15) / 16);
-    if (D == 8 && B == 14) {
-        if (lpr == 4) return launch_down_g<8, 14, 4>(L, M, plan, hbuf, dbuf, st);
-        if (lpr == 8) return launch_down_g<8, 14, 8>(L, M, plan, hbuf, dbuf, st);
-        if (lpr <= 2) return launch_down_g<8, 14, 2>(L, M, plan, hbuf, dbuf, st);
-    } else if (D == 4 && B == 8) {
-        if (lpr == 8) return launch_down_g<4, 8, 8>(L, M, plan, hbuf, dbuf, st);
-        if (lpr == 16) return launch_down_g<4, 8, 16>(L, M, plan, hbuf, dbuf, st);
-        if (lpr == 4) return launch_down_g<4, 8, 4>(L, M, plan, hbuf, dbuf, st);
-        if (lpr <= 2) return launch_down_g<4, 8, 2>(L, M, plan, hbuf, dbuf, st);
+    if (D == 8 && BT == 14) {
+        if (lpr == 4) return launch_down_grouped_g<8, 14, 4>(L, B, M, st);
+        if (lpr == 8) return launch_down_grouped_g<8, 14, 8>(L, B, M, st);
+        if (lpr <= 2) return launch_down_grouped_g<8, 14, 2>(L, B, M, st);
+    } else if (D == 4 && BT == 8) {
+        if (lpr == 8) return launch_down_grouped_g<4, 8, 8>(L, B, M, st);
+        if (lpr == 16) return launch_down_grouped_g<4, 8, 16>(L, B, M, st);
+        if (lpr == 4) return launch_down_grouped_g<4, 8, 4>(L, B, M, st);
+        if (lpr <= 2) return launch_down_grouped_g<4, 8, 2>(L, B, M, st);
     }
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_combine(const LayerDev& L, int M, const int32_t* plan, const float* weights, const float* sgate,
-                          const uint16_t* dbuf, const uint16_t* hin, uint16_t* out, hipStream_t st) {
-    hipLaunchKernelGGL(k_combine, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, M, plan, weights, sgate, dbuf,
-                       hin, out);
+hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
+    hipLaunchKernelGGL(k_combine, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
     return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st) {
     hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, st, x, H, eps, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_t* book4, hipStream_t st) {
+    hipLaunchKernelGGL(k_split_book, dim3(512), dim3(256), 0, st, book, entries, dim, book4);
     return hipGetLastError();
 }
 
@@ -706,6 +988,11 @@ hipError_t launch_gen_embed(uint64_t seed, const uint32_t* tokens, int n, int H,
     for (int i = 0; i < n; ++i) tl.t[i] = tokens[i];
     hipLaunchKernelGGL(k_gen_embed, dim3((n * H + 255) / 256), dim3(256), 0, st,
                        stream_key(seed, kEmbedLayer, T_EMBED), tl, n, H, out);
+    return hipGetLastError();
+}
+hipError_t launch_gen_embed_dev(uint64_t seed, const uint32_t* tokens, int n, int H, uint16_t* out, hipStream_t st) {
+    hipLaunchKernelGGL(k_gen_embed_dev, dim3((n * H + 255) / 256), dim3(256), 0, st,
+                       stream_key(seed, kEmbedLayer, T_EMBED), tokens, n, H, out);
     return hipGetLastError();
 }
 hipError_t launch_book_to_int8(const uint16_t* book16, int n, int8_t* q8, uint16_t* scale, hipStream_t st) {

@@ -79,6 +79,7 @@ _sig("q38_verify_chain_profiled", C.c_int, C.POINTER(P), I32, P, I32, F32, C.POI
      C.POINTER(MoeTimings), P)
 _sig("q38_rmsnorm", C.c_int, P, I32, I32, F32, P, P)
 _sig("q38_embed_synthetic", C.c_int, U64, C.POINTER(U32), I32, I32, P, P)
+_sig("q38_embed_synthetic_dev", C.c_int, U64, P, I32, I32, P, P)
 _sig("q38_head_create", C.c_int, P, C.c_int, I64, I32, P, P, C.POINTER(P))
 _sig("q38_head_create_synthetic", C.c_int, P, C.c_int, I64, I32, U64, C.POINTER(P))
 _sig("q38_head_destroy", None, P)

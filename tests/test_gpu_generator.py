@@ -40,6 +40,10 @@ def test_embed_matches_oracle(gpu, q38, orc):
     arr = (C.c_uint32 * 4)(*toks)
     q38.check(q38.lib.q38_embed_synthetic(SEED, arr, 4, 2048, h.data_ptr(), G.stream()))
     assert np.array_equal(G.to_host(h, np.uint16), orc.embed(SEED, toks, 2048))
+    h2 = G.empty((4, 2048), np.uint16)
+    td = G.to_dev(np.array(toks, np.uint32))
+    q38.check(q38.lib.q38_embed_synthetic_dev(SEED, td.data_ptr(), 4, 2048, h2.data_ptr(), G.stream()))
+    assert np.array_equal(G.to_host(h2, np.uint16), orc.embed(SEED, toks, 2048))
 
 
 def test_head_tensors_match_oracle(gpu, q38, orc):
