@@ -159,6 +159,9 @@ static void fill_dev(q38_moe_layer* L, const q38_moe_weights* w) {
         v.p[p].dim = dim;
         v.p[p].bits = bits;
     }
+    const bool mfma = moe_uses_mfma(v);
+    v.gu_parts = mfma ? d.gu_dim / 4 : 1;
+    v.d_parts = mfma ? d.down_dim / 4 : 1;
 }
 
 // Codebooks split into 4-dim chunks ([dim/4][entries][4]) for the LDS-resident MFMA path.
@@ -332,11 +335,11 @@ static size_t moe_ws(const q38_moe_desc& d, int M, MoeBufs* w, void* base) {
     t.weights = reinterpret_cast<float*>(take(static_cast<size_t>(MK) * 4));
     t.plan = reinterpret_cast<int32_t*>(take(static_cast<size_t>(2 + 4 * MK) * 4));
     const size_t gu = static_cast<size_t>(MK + M) * d.inter, dn = static_cast<size_t>(MK + M) * d.hidden;
-    char* acc = take((2 * gu + dn) * 4);
-    t.g = reinterpret_cast<float*>(acc);
-    t.u = acc ? t.g + gu : nullptr;
-    t.d = acc ? t.g + 2 * gu : nullptr;
-    t.zero_floats = 2 * gu + dn;
+    t.g = reinterpret_cast<float*>(take(2 * gu * 4));
+    t.u = reinterpret_cast<float*>(take(2 * gu * 4));
+    t.d = reinterpret_cast<float*>(take(2 * dn * 4));
+    t.gu_plane = gu;
+    t.d_plane = dn;
     if (w) *w = t;
     return off;
 }

@@ -134,10 +134,100 @@ __global__ __launch_bounds__(256) void k_head_fast(HeadDev hd, const uint16_t* _
     }
 }
 
+// MFMA fast pass (v_mfma_f32_16x16x32_bf16). A wave owns 16-row vocab tiles; lane
+// (i = l % 16, q = l / 16) loads 16 weight bytes of row i per 64-column superstep s
+// (columns 64s + 16q .. +15) and feeds them to two MFMAs as bf16 (u = w ^ 0x80 = w + 128 is
+// exact in bf16); B holds the same columns of the request rows, from LDS. The bias is
+// removed per request row with 128 * sum(h). Output lane (i' = 4q + r, j = l % 16).
+typedef __bf16 bh8_t __attribute__((ext_vector_type(8)));
+typedef float hf4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pack_bf16_hi(float lo, float hi) {
+    return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+}
+
+template <int H>
+__global__ __launch_bounds__(256) void k_head_mfma(HeadDev hd, const uint16_t* __restrict__ h, int M, HeadWork w,
+                                                   float* __restrict__ out_logits) {
+    __shared__ __align__(16) uint16_t hs[5 * H];   // request rows 0..3, then a zero row
+    __shared__ float hsum_s[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < 5 * H / 8; i += 256) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (i < M * H / 8) v = reinterpret_cast<const uint4*>(h)[i];
+        reinterpret_cast<uint4*>(hs)[i] = v;
+    }
+    if (wave < M) {
+        float sacc = 0.0f;
+        for (int c = lane; c < H; c += 64) sacc += bf2f(h[wave * H + c]);
+        sacc = wave_sum_xor(sacc);
+        if (lane == 0) hsum_s[wave] = sacc;
+    }
+    __syncthreads();
+    const int i16 = lane & 15, q = lane >> 4;
+    const int j = i16;                       // request row of this lane's B / D column
+    const bool jact = j < M;
+    const float hsum = jact ? hsum_s[j] : 0.0f;
+    const uint4* hrow = reinterpret_cast<const uint4*>(hs + (jact ? j : 4) * H) + 2 * q;  // branch-free B
+    float* dst = out_logits ? out_logits : w.fast;
+    const int64_t tiles = (hd.V + 15) / 16;
+    float mx = -INFINITY;
+    constexpr int S = H / 64;
+    constexpr int BATCH = 8;
+    for (int64_t t = blockIdx.x * 4 + wave; t < tiles; t += gridDim.x * 4) {
+        const int64_t v0 = t * 16;
+        int64_t vr = v0 + i16;
+        if (vr >= hd.V) vr = hd.V - 1;       // ragged last tile: recompute a valid row, not stored
+        const uint4* wrow = reinterpret_cast<const uint4*>(hd.w + vr * H) + q;
+        hf4_t acc = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < S; s0 += BATCH) {
+            uint4 wv[BATCH];
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) wv[k] = wrow[4 * (s0 + k)];
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) {
+                const uint32_t b4[4] = {wv[k].x ^ 0x80808080u, wv[k].y ^ 0x80808080u, wv[k].z ^ 0x80808080u,
+                                        wv[k].w ^ 0x80808080u};
+                uint32_t a[8];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const float f0 = static_cast<float>(b4[m] & 0xffu), f1 = static_cast<float>((b4[m] >> 8) & 0xffu);
+                    const float f2 = static_cast<float>((b4[m] >> 16) & 0xffu), f3 = static_cast<float>(b4[m] >> 24);
+                    a[2 * m] = pack_bf16_hi(f0, f1);
+                    a[2 * m + 1] = pack_bf16_hi(f2, f3);
+                }
+                const uint4 b0 = hrow[8 * (s0 + k)];
+                const uint4 b1 = hrow[8 * (s0 + k) + 1];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bh8_t, make_uint4(a[0], a[1], a[2], a[3])), __builtin_bit_cast(bh8_t, b0), acc,
+                    0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bh8_t, make_uint4(a[4], a[5], a[6], a[7])), __builtin_bit_cast(bh8_t, b1), acc,
+                    0, 0, 0);
+            }
+        }
+        if (jact) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t v = v0 + 4 * q + r;
+                if (v < hd.V) {
+                    const float lg = fmaf(-128.0f, hsum, acc[r]) * h2f(hd.scales[v]);
+                    mx = fmaxf(mx, lg);
+                    dst[static_cast<size_t>(j) * hd.V + v] = lg;
+                }
+            }
+        }
+    }
+    if (jact && !out_logits) atomicMax(&w.rowmax[j], orderable(mx));
+}
+
 // Window: fast >= max - 2E, E = 2 * s_max * 383 * sum|h| * 80 * 2^-24 + 1e-30 (the float
 // error bound of the fast pass and of the contract's own rounding, with a factor 2).
+// Window: fast >= max - 2E with E a bound on |fast - contract|: the fast pass sums 2048
+// terms |u*h| <= 255|h| (plus the 128*sum(h) correction) in float in an unspecified order,
+// so |error| <= 2^-24 * s_max * sum|h| * (2047 * 383 + 2 * 383); taken with a factor 4.
 __device__ __forceinline__ float head_window(const HeadDev& hd, const HeadWork& w, int r) {
-    const float E = 2.0f * hd.s_max * 383.0f * w.tsum[r] * 80.0f * 0x1.0p-24f + 1e-30f;
+    const float E = 4.0f * hd.s_max * w.tsum[r] * 0x1.0p-24f * (2047.0f * 383.0f + 766.0f) + 1e-30f;
     return from_orderable(w.rowmax[r]) - 2.0f * E;
 }
 
@@ -416,6 +506,13 @@ hipError_t launch_fast_m(const HeadDev& hd, const uint16_t* h, const HeadWork& w
     return hipGetLastError();
 }
 hipError_t launch_fast(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, float* out, hipStream_t st) {
+    if (M >= 1 && M <= 4 && (hd.H == 2048 || hd.H == 1024)) {
+        if (hd.H == 2048)
+            hipLaunchKernelGGL(k_head_mfma<2048>, dim3(256 * 4), dim3(256), 0, st, hd, h, M, w, out);
+        else
+            hipLaunchKernelGGL(k_head_mfma<1024>, dim3(256 * 4), dim3(256), 0, st, hd, h, M, w, out);
+        return hipGetLastError();
+    }
     switch (M) {
         case 1: return launch_fast_m<1>(hd, h, w, out, st);
         case 2: return launch_fast_m<2>(hd, h, w, out, st);

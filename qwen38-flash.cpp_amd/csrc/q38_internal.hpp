@@ -28,10 +28,13 @@ struct MoeBufs {
     int32_t* experts;  // [M*K]
     float* weights;    // [M*K]
     int32_t* plan;     // [2 + 4*M*K]
-    float* g;          // [M*K + M, I] gate projections (sorted route order; shared rows last)
-    float* u;          // [M*K + M, I] up projections
-    float* d;          // [M*K + M, H] down projections
-    size_t zero_floats;  // g, u, d are one contiguous region of this many floats
+    // Projection partial sums, one plane per codebook chunk (summed chunk 0 + chunk 1 by the
+    // consumer): rows in sorted route order, shared-expert rows last.
+    float* g;          // [2][M*K + M, I] gate
+    float* u;          // [2][M*K + M, I] up
+    float* d;          // [2][M*K + M, H] down
+    size_t gu_plane;   // floats between the chunk planes of g and u
+    size_t d_plane;    // floats between the chunk planes of d
 };
 
 struct LayerDev {
@@ -39,6 +42,7 @@ struct LayerDev {
     const uint16_t* wsg;     // [H] bf16
     ProjDev p[3];            // gate, up, down
     int H, I, E, K, normalize, has_shared;
+    int gu_parts, d_parts;   // chunk planes written by the gate/up and down kernels (1 or 2)
 };
 
 struct HeadDev {

@@ -165,70 +165,63 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
 // columns c = 512t + 8l + j, so the wave covers whole rows and computes each row's sum of
 // squares (lane partials, xor butterfly) identically in every wave. Logit contract: lane
 // l accumulates x*w over its columns (t outer, j inner) with fmaf, xor butterfly, BF16.
-// Workgroup 0 stores x (bf16) and x16 (fp16, the MFMA operand); all workgroups clear the
-// layer's g/u/d accumulators.
-template <int MAXM>
+// Workgroup 0 stores x (bf16) and x16 (fp16, the MFMA operand).
+template <int T>
 __global__ __launch_bounds__(256) void k_router(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ hin,
                                                 int do_norm, float eps) {
-    const int H = L.H, T = H / 512;
+    constexpr int H = 512 * T;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    {
-        const size_t gt = blockIdx.x * 256 + tid, gs = gridDim.x * 256;
-        float4* z = reinterpret_cast<float4*>(B.g);
-        for (size_t i = gt; i < B.zero_floats / 4; i += gs) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
     const int e = blockIdx.x * 4 + wave;
     const int n_rows = L.E + (L.has_shared ? 1 : 0);
     const bool store_x = blockIdx.x == 0 && wave == 0;
     if (e >= n_rows && !store_x) return;
+    const bool has_row = e < n_rows;
     const uint16_t* w = e < L.E ? L.router + static_cast<size_t>(e) * H : L.wsg;
-    constexpr int MAXT = 5;  // H <= 2560
-    uint4 wv[MAXT];
+    uint4 wv[T];
 #pragma unroll
-    for (int t = 0; t < MAXT; ++t)
-        if (t < T && e < n_rows) wv[t] = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
+    for (int t = 0; t < T; ++t)
+        if (has_row) wv[t] = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
+    for (int r0 = 0; r0 < M; r0 += 4) {
+        uint4 xv[4][T];
 #pragma unroll
-    for (int r = 0; r < MAXM; ++r) {
-        if (r >= M) break;
-        uint4 xv[MAXT];
+        for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
-        for (int t = 0; t < MAXT; ++t)
-            if (t < T) xv[t] = *reinterpret_cast<const uint4*>(hin + r * H + 512 * t + 8 * lane);
-        if (do_norm) {
-            float ss = 0.0f;
+            for (int t = 0; t < T; ++t)
+                if (r0 + rr < M) xv[rr][t] = *reinterpret_cast<const uint4*>(hin + (r0 + rr) * H + 512 * t + 8 * lane);
 #pragma unroll
-            for (int t = 0; t < MAXT; ++t) {
-                if (t < T) {
-                    const uint32_t q[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+        for (int rr = 0; rr < 4; ++rr) {
+            const int r = r0 + rr;
+            if (r >= M) break;
+            if (do_norm) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const uint32_t q[4] = {xv[rr][t].x, xv[rr][t].y, xv[rr][t].z, xv[rr][t].w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         ss = fmaf(bflo(q[k]), bflo(q[k]), ss);
                         ss = fmaf(bfhi(q[k]), bfhi(q[k]), ss);
                     }
                 }
-            }
-            ss = wave_sum_xor(ss);
-            const float inv = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+                ss = wave_sum_xor(ss);
+                const float inv = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
 #pragma unroll
-            for (int t = 0; t < MAXT; ++t) {
-                if (t < T) {
-                    uint32_t q[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+                for (int t = 0; t < T; ++t) {
+                    uint32_t q[4] = {xv[rr][t].x, xv[rr][t].y, xv[rr][t].z, xv[rr][t].w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         const uint32_t lo = f2bf(bflo(q[k]) * inv), hi = f2bf(bfhi(q[k]) * inv);
                         q[k] = lo | (hi << 16);
                     }
-                    xv[t] = make_uint4(q[0], q[1], q[2], q[3]);
+                    xv[rr][t] = make_uint4(q[0], q[1], q[2], q[3]);
                 }
             }
-        }
-        if (store_x) {
+            if (store_x) {
 #pragma unroll
-            for (int t = 0; t < MAXT; ++t) {
-                if (t < T) {
+                for (int t = 0; t < T; ++t) {
                     const size_t at = static_cast<size_t>(r) * H + 512 * t + 8 * lane;
-                    *reinterpret_cast<uint4*>(B.x + at) = xv[t];
-                    const uint32_t q[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+                    *reinterpret_cast<uint4*>(B.x + at) = xv[rr][t];
+                    const uint32_t q[4] = {xv[rr][t].x, xv[rr][t].y, xv[rr][t].z, xv[rr][t].w};
                     uint32_t hq[4];
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
@@ -236,13 +229,11 @@ __global__ __launch_bounds__(256) void k_router(LayerDev L, MoeBufs B, int M, co
                     *reinterpret_cast<uint4*>(B.x16 + at) = make_uint4(hq[0], hq[1], hq[2], hq[3]);
                 }
             }
-        }
-        if (e < n_rows) {
-            float acc = 0.0f;
+            if (has_row) {
+                float acc = 0.0f;
 #pragma unroll
-            for (int t = 0; t < MAXT; ++t) {
-                if (t < T) {
-                    const uint32_t xq[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+                for (int t = 0; t < T; ++t) {
+                    const uint32_t xq[4] = {xv[rr][t].x, xv[rr][t].y, xv[rr][t].z, xv[rr][t].w};
                     const uint32_t wq[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
@@ -250,14 +241,14 @@ __global__ __launch_bounds__(256) void k_router(LayerDev L, MoeBufs B, int M, co
                         acc = __builtin_fmaf(bfhi(xq[k]), bfhi(wq[k]), acc);
                     }
                 }
-            }
-            const float s = wave_sum_xor(acc);
-            if (lane == 0) {
-                if (e < L.E) {
-                    B.logits[r * L.E + e] = rbf(s);
-                } else {
-                    const float lg = rbf(s);
-                    B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
+                const float sres = wave_sum_xor(acc);
+                if (lane == 0) {
+                    if (e < L.E) {
+                        B.logits[r * L.E + e] = rbf(sres);
+                    } else {
+                        const float lg = rbf(sres);
+                        B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
+                    }
                 }
             }
         }
@@ -434,10 +425,10 @@ __device__ __forceinline__ void load_lane_words(const uint32_t* src, uint32_t* w
     w[WPL] = 0;
 }
 
-// One 16-row MFMA tile over all subvectors of one chunk.
+// One 16-row MFMA tile over all subvectors of one chunk. xlane: this lane's B row in LDS
+// (a zeroed row for lanes without a routed row), already offset to its q block.
 template <int BITS, int NSUB>
-__device__ __forceinline__ f4_t mfma_tile(const uint32_t* w, const uint2* book, const uint4* xs, int col, int q,
-                                          bool col_active) {
+__device__ __forceinline__ f4_t mfma_tile(const uint32_t* w, const uint2* book, const uint4* xlane) {
     constexpr int S4 = NSUB / 4;
     f4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -447,27 +438,32 @@ __device__ __forceinline__ f4_t mfma_tile(const uint32_t* w, const uint2* book, 
         const uint2 a1 = book[c1];
         const uint2 a2 = book[c2];
         const uint4 av = make_uint4(a1.x, a1.y, a2.x, a2.y);
-        uint4 bv = make_uint4(0u, 0u, 0u, 0u);
-        if (col_active) bv = xs[(col * NSUB + q * S4 + 2 * t) / 2];
+        const uint4 bv = xlane[t];
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, av), __builtin_bit_cast(h8_t, bv),
                                                      acc, 0, 0, 0);
     }
     return acc;
 }
+// B row base for lane (row xrow, block q) or the zero row when inactive.
+template <int NSUB>
+__device__ __forceinline__ const uint4* xs_lane(const uint4* xs, int xrow, int zero_row, int q, bool active) {
+    return xs + ((active ? xrow : zero_row) * NSUB + q * (NSUB / 4)) / 2;
+}
 
-// Codebook chunk -> LDS, by threads [t0, t0 + nthreads) of the workgroup.
+// Codebook chunk -> LDS by threads [0, nthreads): 16 loads in flight per thread.
 template <int KENT>
 __device__ __forceinline__ void fill_book(const uint16_t* src4, unsigned char* lds, int t, int nthreads) {
     const uint4* src = reinterpret_cast<const uint4*>(src4);
     uint4* dst = reinterpret_cast<uint4*>(lds);
     constexpr int N = KENT / 2;  // uint4 entries
+    constexpr int G = 16;
     int i = t;
-    for (; i + 3 * nthreads < N; i += 4 * nthreads) {
-        const uint4 a = src[i], b = src[i + nthreads], c = src[i + 2 * nthreads], d = src[i + 3 * nthreads];
-        dst[i] = a;
-        dst[i + nthreads] = b;
-        dst[i + 2 * nthreads] = c;
-        dst[i + 3 * nthreads] = d;
+    for (; i + (G - 1) * nthreads < N; i += G * nthreads) {
+        uint4 v[G];
+#pragma unroll
+        for (int k = 0; k < G; ++k) v[k] = src[i + k * nthreads];
+#pragma unroll
+        for (int k = 0; k < G; ++k) dst[i + k * nthreads] = v[k];
     }
     for (; i < N; i += nthreads) dst[i] = src[i];
 }
@@ -479,7 +475,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     __shared__ int32_t plan[kPlanInts];
     constexpr int KENT = 1 << BITS;
     const uint2* book = reinterpret_cast<const uint2*>(lds);       // [KENT] x 4 fp16
-    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);          // [8][NSUB][4] fp16
+    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);          // [8 + 1 zero][NSUB][4] fp16
     constexpr int TYPES = 2 * NCHUNK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
@@ -498,10 +494,22 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     const int nu = plan[0];
     const int n_items = (nu + (L.has_shared ? 1 : 0)) * (I / kMfmaRowsPerItem);
     const int tiles = I / kMfmaRowsPerItem;
-    float* out = proj == 0 ? B.g : B.u;
+    float* out = (proj == 0 ? B.g : B.u) + chunk * B.gu_plane;
     const int r16 = lane & 15, q = lane >> 4;
     constexpr int S4 = NSUB / 4;
     constexpr int WPL = S4 * BITS / 32;
+    // Verify widths (M <= 8): the chunk's dims of every request row are staged once.
+    const bool stage_all = M <= kMfmaMaxCols;
+    if (stage_all) {
+        for (int i = tid; i < M * NSUB; i += kMfmaThreads) {
+            const int row = i / NSUB, sv = i % NSUB;
+            reinterpret_cast<uint2*>(xs)[i] =
+                *reinterpret_cast<const uint2*>(B.x16 + static_cast<size_t>(row) * H + sv * (4 * NCHUNK) + 4 * chunk);
+        }
+    }
+    for (int i = tid; i < NSUB; i += kMfmaThreads)
+        reinterpret_cast<uint2*>(xs)[kMfmaMaxCols * NSUB + i] = make_uint2(0u, 0u);
+    __syncthreads();
     auto code_src = [&](int item) {
         int expert, n, pos0;
         slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
@@ -519,21 +527,26 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
         const int o0 = tile * kMfmaRowsPerItem + wave * 16;
         for (int j0 = 0; j0 < n; j0 += kMfmaMaxCols) {
             const int nj = n - j0 < kMfmaMaxCols ? n - j0 : kMfmaMaxCols;
-            __syncthreads();
-            for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
-                const int j = i / NSUB, s = i % NSUB;
-                const int row = route_row(plan, M, K, pos0, j0 + j, shared);
-                reinterpret_cast<uint2*>(xs)[j * NSUB + s] =
-                    *reinterpret_cast<const uint2*>(B.x16 + static_cast<size_t>(row) * H + s * (4 * NCHUNK) + 4 * chunk);
+            int xrow = r16;
+            if (stage_all) {
+                if (r16 < nj) xrow = route_row(plan, M, K, pos0, j0 + r16, shared);
+            } else {
+                __syncthreads();
+                for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
+                    const int jj = i / NSUB, sv = i % NSUB;
+                    const int row = route_row(plan, M, K, pos0, j0 + jj, shared);
+                    reinterpret_cast<uint2*>(xs)[jj * NSUB + sv] = *reinterpret_cast<const uint2*>(
+                        B.x16 + static_cast<size_t>(row) * H + sv * (4 * NCHUNK) + 4 * chunk);
+                }
+                __syncthreads();
             }
-            __syncthreads();
-            const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs, r16, q, r16 < nj);
+            const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs_lane<NSUB>(xs, xrow, kMfmaMaxCols, q, r16 < nj));
             if (r16 < nj) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int o = o0 + 4 * q + rr;
                     const float sc = h2f(P.scales[static_cast<size_t>(expert) * I + o]);
-                    atomicAdd(&out[static_cast<size_t>(pos0 + j0 + r16) * I + o], sc * acc[rr]);
+                    out[static_cast<size_t>(pos0 + j0 + r16) * I + o] = sc * acc[rr];
                 }
             }
         }
@@ -550,13 +563,15 @@ __device__ __forceinline__ float swiglu(float g, float u) {
     return rbf(s * rbf(u));
 }
 
+constexpr int kDownStageRoutes = 48;  // routes whose SwiGLU rows are staged once (M <= 4 with k = 10)
+
 template <int BITS, int NSUB, int NCHUNK>
 __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs B, int M) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int32_t plan[kPlanInts];
     constexpr int KENT = 1 << BITS;
     const uint2* book = reinterpret_cast<const uint2*>(lds);
-    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);
+    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);   // [routes][NSUB][4] fp16 SwiGLU rows
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
     const int chunk = kk % NCHUNK;
@@ -564,9 +579,33 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
     const int idx = (kk / NCHUNK) * 8 + x8;
     const ProjDev& P = L.p[2];
     const int H = L.H, I = L.I, K = L.K;
+    const int n_routes = M * K + (L.has_shared ? M : 0);
     for (int i = tid; i < 2 + 4 * M * K; i += kMfmaThreads) plan[i] = B.plan[i];
     fill_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, tid, kMfmaThreads);
+    // SwiGLU rows of every route, once (verify widths)
+    const bool stage_all = n_routes <= kDownStageRoutes;
+    auto stage = [&](int r0, int nr) {
+        for (int i = tid; i < nr * NSUB; i += kMfmaThreads) {
+            const int j = i / NSUB, sv = i % NSUB;
+            const size_t base = static_cast<size_t>(r0 + j) * I + sv * (4 * NCHUNK) + 4 * chunk;
+            float4 gv = *reinterpret_cast<const float4*>(B.g + base);
+            float4 uv = *reinterpret_cast<const float4*>(B.u + base);
+            if (L.gu_parts == 2) {
+                const float4 g1 = *reinterpret_cast<const float4*>(B.g + B.gu_plane + base);
+                const float4 u1 = *reinterpret_cast<const float4*>(B.u + B.gu_plane + base);
+                gv = make_float4(gv.x + g1.x, gv.y + g1.y, gv.z + g1.z, gv.w + g1.w);
+                uv = make_float4(uv.x + u1.x, uv.y + u1.y, uv.z + u1.z, uv.w + u1.w);
+            }
+            const uint32_t h0 = f2h(swiglu(gv.x, uv.x)), h1 = f2h(swiglu(gv.y, uv.y));
+            const uint32_t h2 = f2h(swiglu(gv.z, uv.z)), h3 = f2h(swiglu(gv.w, uv.w));
+            reinterpret_cast<uint2*>(xs)[j * NSUB + sv] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+        }
+    };
+    if (stage_all) stage(0, n_routes);
+    for (int i = tid; i < NSUB; i += kMfmaThreads)
+        reinterpret_cast<uint2*>(xs)[kDownStageRoutes * NSUB + i] = make_uint2(0u, 0u);
     __syncthreads();
+    float* dout = B.d + chunk * B.d_plane;
     const int nu = plan[0];
     const int tiles = H / kMfmaRowsPerItem;
     const int n_items = (nu + (L.has_shared ? 1 : 0)) * tiles;
@@ -589,24 +628,21 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
         const int o0 = tile * kMfmaRowsPerItem + wave * 16;
         for (int j0 = 0; j0 < n; j0 += kMfmaMaxCols) {
             const int nj = n - j0 < kMfmaMaxCols ? n - j0 : kMfmaMaxCols;
-            __syncthreads();
-            for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
-                const int j = i / NSUB, s = i % NSUB;
-                const size_t base = static_cast<size_t>(pos0 + j0 + j) * I + s * (4 * NCHUNK) + 4 * chunk;
-                const float4 gv = *reinterpret_cast<const float4*>(B.g + base);
-                const float4 uv = *reinterpret_cast<const float4*>(B.u + base);
-                const uint32_t h0 = f2h(swiglu(gv.x, uv.x)), h1 = f2h(swiglu(gv.y, uv.y));
-                const uint32_t h2 = f2h(swiglu(gv.z, uv.z)), h3 = f2h(swiglu(gv.w, uv.w));
-                reinterpret_cast<uint2*>(xs)[j * NSUB + s] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+            int xrow = r16;
+            if (stage_all) {
+                xrow = pos0 + j0 + r16;
+            } else {
+                __syncthreads();
+                stage(pos0 + j0, nj);
+                __syncthreads();
             }
-            __syncthreads();
-            const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs, r16, q, r16 < nj);
+            const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs_lane<NSUB>(xs, xrow, kDownStageRoutes, q, r16 < nj));
             if (r16 < nj) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int o = o0 + 4 * q + rr;
                     const float sc = h2f(P.scales[static_cast<size_t>(expert) * H + o]);
-                    atomicAdd(&B.d[static_cast<size_t>(pos0 + j0 + r16) * H + o], sc * acc[rr]);
+                    dout[static_cast<size_t>(pos0 + j0 + r16) * H + o] = sc * acc[rr];
                 }
             }
         }
@@ -739,7 +775,12 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
     const int H = L.H, I = L.I;
     for (int i = threadIdx.x; i < n * I; i += 256) {
         const size_t at = static_cast<size_t>(pos0) * I + i;
-        fin[i] = swiglu(B.g[at], B.u[at]);
+        float g = B.g[at], u = B.u[at];
+        if (L.gu_parts == 2) {
+            g += B.g[B.gu_plane + at];
+            u += B.u[B.gu_plane + at];
+        }
+        fin[i] = swiglu(g, u);
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -757,12 +798,16 @@ __global__ __launch_bounds__(256) void k_combine(LayerDev L, MoeBufs B, int M, u
     const int H = L.H, K = L.K, MK = M * K;
     if (o >= H) return;
     const int32_t* rpos = B.plan + 2 + 3 * MK;
+    const bool two = L.d_parts == 2;
+    auto dsum = [&](int route) {
+        const size_t at = static_cast<size_t>(route) * H + o;
+        return two ? B.d[at] + B.d[B.d_plane + at] : B.d[at];
+    };
     float routed = 0.0f;
-    for (int s = 0; s < K; ++s)
-        routed = fmaf(B.weights[r * K + s], rbf(B.d[static_cast<size_t>(rpos[r * K + s]) * H + o]), routed);
+    for (int s = 0; s < K; ++s) routed = fmaf(B.weights[r * K + s], rbf(dsum(rpos[r * K + s])), routed);
     float y = rbf(routed);
     if (L.has_shared) {
-        const float sh = rbf(rbf(B.d[static_cast<size_t>(MK + r) * H + o]) * B.sgate[r]);
+        const float sh = rbf(rbf(dsum(MK + r)) * B.sgate[r]);
         y = rbf(y + sh);
     }
     const size_t i = static_cast<size_t>(r) * H + o;
@@ -816,11 +861,11 @@ void init_grid() {
     done = true;
 }
 
-template <int MAXM>
-hipError_t launch_router_m(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* h, int do_norm, float eps,
+template <int T>
+hipError_t launch_router_t(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* h, int do_norm, float eps,
                            hipStream_t st) {
     const int rows = L.E + (L.has_shared ? 1 : 0);
-    hipLaunchKernelGGL(k_router<MAXM>, dim3((rows + 3) / 4), dim3(256), 0, st, L, B, M, h, do_norm, eps);
+    hipLaunchKernelGGL(k_router<T>, dim3((rows + 3) / 4), dim3(256), 0, st, L, B, M, h, do_norm, eps);
     return hipGetLastError();
 }
 
@@ -832,7 +877,7 @@ hipError_t set_lds(Kern k, size_t bytes) {
 
 template <int BITS, int NSUB, int NCHUNK>
 hipError_t launch_gu_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kMfmaMaxCols) * NSUB * 8;
+    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kMfmaMaxCols + 1) * NSUB * 8;
     static bool attr = false;
     if (!attr) {
         const hipError_t e = set_lds(&k_gu_mfma<BITS, NSUB, NCHUNK>, lds);
@@ -844,7 +889,7 @@ hipError_t launch_gu_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStrea
 }
 template <int BITS, int NSUB, int NCHUNK>
 hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kMfmaMaxCols) * NSUB * 8;
+    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kDownStageRoutes + 1) * NSUB * 8;
     static bool attr = false;
     if (!attr) {
         const hipError_t e = set_lds(&k_down_mfma<BITS, NSUB, NCHUNK>, lds);
@@ -892,11 +937,16 @@ bool moe_uses_mfma(const LayerDev& L) {
 
 hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* h, int do_norm, float eps,
                          hipStream_t st) {
-    if (M <= 1) return launch_router_m<1>(L, B, M, h, do_norm, eps, st);
-    if (M <= 2) return launch_router_m<2>(L, B, M, h, do_norm, eps, st);
-    if (M <= 4) return launch_router_m<4>(L, B, M, h, do_norm, eps, st);
-    if (M <= 8) return launch_router_m<8>(L, B, M, h, do_norm, eps, st);
-    return launch_router_m<16>(L, B, M, h, do_norm, eps, st);
+    switch (L.H / 512) {
+        case 1: return launch_router_t<1>(L, B, M, h, do_norm, eps, st);
+        case 2: return launch_router_t<2>(L, B, M, h, do_norm, eps, st);
+        case 3: return launch_router_t<3>(L, B, M, h, do_norm, eps, st);
+        case 4: return launch_router_t<4>(L, B, M, h, do_norm, eps, st);
+        case 5: return launch_router_t<5>(L, B, M, h, do_norm, eps, st);
+        case 6: return launch_router_t<6>(L, B, M, h, do_norm, eps, st);
+        case 8: return launch_router_t<8>(L, B, M, h, do_norm, eps, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_topk_plan(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
