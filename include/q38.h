@@ -176,14 +176,19 @@ int q38_head_create_synthetic(q38_ctx* ctx, int kind, int64_t vocab, int32_t hid
 void q38_head_destroy(q38_head* head);
 int q38_head_weights(const q38_head* head, const void** weights, const uint16_t** scales);
 int64_t q38_head_bytes(const q38_head* head);
+/* Device workspace bytes for q38_head_greedy / q38_head_logits with up to max_rows rows
+ * (Q8: 1..16; Q4: 1..4); 0 for an invalid count. */
 size_t q38_head_workspace_size(const q38_head* head, int32_t max_rows);
 
 /* greedy_batch_from_logits (src/mtp_verifier.cpp:30-55): per row the argmax (lowest index
  * on ties) of the exact logit contract, and that logit. h: device [rows, H] bf16 (rows
- * <= 16); argmax, logit: device [rows]. Q8 heads only. */
+ * 1..16, one pass over the weights for all rows); argmax, logit: device [rows]. Q8 heads
+ * only. */
 int q38_head_greedy(q38_head* head, const uint16_t* h, int32_t rows, uint32_t* argmax, float* logit,
                     void* workspace, size_t workspace_bytes, void* stream);
-/* Raw logits (fast path, float) of either head: device [rows, V]. */
+/* Logits of either head: device [rows, V] float. Q8: the fast pass (rows 1..16, needs the
+ * workspace), the float rounding of scale * (w . h^) with h^ the int8-plane form of h (equal
+ * to h for every element with |h| >= max|h| * 2^-12). Q4: rows 1..4, no workspace. */
 int q38_head_logits(q38_head* head, const uint16_t* h, int32_t rows, float* logits, void* workspace,
                     size_t workspace_bytes, void* stream);
 

@@ -506,6 +506,7 @@ static int head_validate(int kind, int64_t vocab, int hidden) {
 }
 
 static int head_finish(q38_head* hd) {
+    Q38_HIP(head_init_attrs());
     float* d = nullptr;
     Q38_HIP(hipMalloc(&d, sizeof(float)));
     const int64_t ns = hd->dev.kind == 0 ? hd->dev.V : hd->dev.V * (hd->dev.H / 64);
@@ -577,28 +578,34 @@ int64_t q38_head_bytes(const q38_head* hd) {
 }
 
 size_t q38_head_workspace_size(const q38_head* hd, int32_t max_rows) {
-    if (!hd || max_rows < 1 || max_rows > 4) return 0;
-    return head_work_bytes(hd->dev.V, max_rows);
+    if (!hd || max_rows < 1 || max_rows > kHeadMaxRows) return 0;
+    if (hd->dev.kind != Q38_HEAD_Q8) return max_rows <= 4 ? 256 : 0;
+    return head_work_bytes(hd->dev, max_rows, true);
 }
 
 int q38_head_greedy(q38_head* hd, const uint16_t* h, int32_t rows, uint32_t* argmax, float* logit, void* ws,
                     size_t ws_bytes, void* stream) {
     if (!hd || !h || !argmax || !logit) return fail(Q38_EINVAL, "q38_head_greedy: null argument");
     if (hd->dev.kind != Q38_HEAD_Q8) return fail(Q38_EINVAL, "greedy argmax needs a Q8 head");
-    if (rows < 1 || rows > 4) return fail(Q38_EINVAL, "head rows must be between 1 and 4 per call");
-    if (!ws || ws_bytes < head_work_bytes(hd->dev.V, rows)) return fail(Q38_ESPACE, "workspace too small");
-    const HeadWork w = head_work_carve(ws, hd->dev.V, rows);
+    if (rows < 1 || rows > kHeadMaxRows) return fail(Q38_EINVAL, "head rows must be between 1 and 16 per call");
+    if (!ws || ws_bytes < head_work_bytes(hd->dev, rows, true)) return fail(Q38_ESPACE, "workspace too small");
+    const HeadWork w = head_work_carve(ws, hd->dev, rows, true);
     Q38_HIP(launch_head_greedy(hd->dev, h, rows, w, argmax, logit, static_cast<hipStream_t>(stream)));
     return Q38_OK;
 }
 
 int q38_head_logits(q38_head* hd, const uint16_t* h, int32_t rows, float* logits, void* ws, size_t ws_bytes,
                     void* stream) {
-    (void)ws;
-    (void)ws_bytes;
     if (!hd || !h || !logits) return fail(Q38_EINVAL, "q38_head_logits: null argument");
-    if (rows < 1 || rows > 4) return fail(Q38_EINVAL, "head rows must be between 1 and 4 per call");
-    Q38_HIP(launch_head_logits(hd->dev, h, rows, logits, static_cast<hipStream_t>(stream)));
+    HeadWork w{};
+    if (hd->dev.kind == Q38_HEAD_Q8) {
+        if (rows < 1 || rows > kHeadMaxRows) return fail(Q38_EINVAL, "head rows must be between 1 and 16 per call");
+        if (!ws || ws_bytes < head_work_bytes(hd->dev, rows, false)) return fail(Q38_ESPACE, "workspace too small");
+        w = head_work_carve(ws, hd->dev, rows, false);
+    } else if (rows < 1 || rows > 4) {
+        return fail(Q38_EINVAL, "Q4 head rows must be between 1 and 4 per call");
+    }
+    Q38_HIP(launch_head_logits(hd->dev, h, rows, w, logits, static_cast<hipStream_t>(stream)));
     return Q38_OK;
 }
 

@@ -6,228 +6,193 @@
 // (src/model.cpp:470-480, src/mtp_verifier.cpp:30-55). Greedy acceptance must be
 // bit-exact, so the argmax is defined on an exact logit contract (double partial sums in
 // a fixed order, see oracle/q38_oracle.cpp head_q8_logit) and computed in two passes:
-//   1. k_head_fast: the bandwidth pass. Every int8 row is read once and dotted with all
-//      rows of h in float; per-row maxima are kept.
-//   2. k_head_cand + k_head_exact: every vocab row whose fast logit lies within twice the
-//      proven float error bound of the row maximum is recomputed under the contract and
-//      the best (logit desc, index asc) key wins. The true contract argmax always lies in
-//      that window, so the result equals the contract argmax; the window holds one or a
-//      few rows in practice. More than kHeadCap candidates fall back to recomputing all
-//      rows of that request row.
+//   1. k_head_i8: the bandwidth pass. Every int8 vocab row is read once and multiplied
+//      with all request rows on the int8 matrix cores; per-row maxima are kept.
+//   2. k_head_cand + k_head_exact: every vocab row whose fast logit lies within twice a
+//      proven bound of the fast pass's error of the row maximum is recomputed under the
+//      contract and the best (logit desc, index asc) key wins. The true contract argmax
+//      always lies in that window, so the result equals the contract argmax; the window
+//      holds one or a few rows in practice. More than kHeadCap candidates fall back to
+//      recomputing all rows of that request row.
+//
+// Fast pass arithmetic. k_head_prep writes each request row h (bf16) as three int8
+// planes, h ~= s * (a + b / 2^7 + c / 2^14), s = 2^(e-6) with max|h| = f * 2^e, so that
+// |a|, |b|, |c| <= 64 and the planes are exact for every element with
+// |h| >= s * 2^-6; R = sum |h - s (a + b/2^7 + c/2^14)| is measured exactly (double).
+// The MFMA sums sum_k w_k a_k (etc.) are exact int32; A * 2^14 + B * 2^7 + C is exact in
+// int64 and, scaled by s * 2^-14 and the fp16 row scale, exact in double, so the fast
+// logit is the float rounding of scale_v * sum_k w_k h^_k, and
+//   |fast_v - contract_v| <= s_max * 128 * (R + 2^-22 * (sum|h| + R)),
+// which head_window doubles.
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
 
 namespace q38 {
 
-size_t head_work_bytes(int64_t V, int M) {
-    size_t b = 0;
-    b += static_cast<size_t>(M) * V * 4;            // fast
-    b += 256;                                        // rowmax
-    b += 256;                                        // tsum
-    b += 256;                                        // cnt
-    b += static_cast<size_t>(M) * kHeadCap * 4;     // cand
-    b += 256;                                        // best
-    return b + 1024;
+namespace {
+constexpr size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 }
-HeadWork head_work_carve(void* base, int64_t V, int M) {
+
+size_t head_work_bytes(const HeadDev& hd, int M, bool greedy) {
+    size_t b = al256(3ull * M * hd.H) + 7 * 256;  // planes; hscale, res, tsum, rowmax, cnt, best
+    if (greedy) b += al256(static_cast<size_t>(M) * kHeadCap * 4) + al256(static_cast<size_t>(M) * hd.V * 4);
+    return b;
+}
+HeadWork head_work_carve(void* base, const HeadDev& hd, int M, bool greedy) {
     char* p = static_cast<char*>(base);
     HeadWork w{};
-    w.fast = reinterpret_cast<float*>(p);
-    p += (static_cast<size_t>(M) * V * 4 + 255) / 256 * 256;
-    w.rowmax = reinterpret_cast<uint32_t*>(p); p += 256;
+    w.planes = reinterpret_cast<int8_t*>(p); p += al256(3ull * M * hd.H);
+    w.hscale = reinterpret_cast<float*>(p); p += 256;
+    w.res = reinterpret_cast<float*>(p); p += 256;
     w.tsum = reinterpret_cast<float*>(p); p += 256;
+    w.rowmax = reinterpret_cast<uint32_t*>(p); p += 256;
     w.cnt = reinterpret_cast<int32_t*>(p); p += 256;
-    w.cand = reinterpret_cast<int32_t*>(p); p += (static_cast<size_t>(M) * kHeadCap * 4 + 255) / 256 * 256;
-    w.best = reinterpret_cast<unsigned long long*>(p);
+    w.best = reinterpret_cast<unsigned long long*>(p); p += 256;
+    if (greedy) {
+        w.cand = reinterpret_cast<int32_t*>(p); p += al256(static_cast<size_t>(M) * kHeadCap * 4);
+        w.fast = reinterpret_cast<float*>(p);
+    }
     return w;
 }
 
-// Per request row: sum |h| (fixed order) and reset of the pass state (no memset nodes,
-// so the sequence can be captured in a graph).
-__global__ void k_head_prep(const uint16_t* __restrict__ h, int H, HeadWork w) {
-    __shared__ float red[4];
-    const int r = blockIdx.x, tid = threadIdx.x;
-    float s = 0.0f;
-    for (int c = tid; c < H; c += 256) s += fabsf(bf2f(h[static_cast<size_t>(r) * H + c]));
-    s = wave_sum_xor(s);
-    if ((tid & 63) == 0) red[tid >> 6] = s;
+// One block per request row: the int8 planes of h, its plane scale, the residual R and
+// sum|h| (double, fixed order), and the reset of the pass state (kernel stores, no memset
+// nodes, so the sequence can be captured in a graph).
+__global__ __launch_bounds__(256) void k_head_prep(const uint16_t* __restrict__ h, int H, int M, HeadWork w) {
+    __shared__ float redm[4];
+    __shared__ double redt[4], redr[4];
+    const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint16_t* hr = h + static_cast<size_t>(r) * H;
+    float m = 0.0f;
+    for (int c = tid; c < H; c += 256) m = fmaxf(m, fabsf(bf2f(hr[c])));
+    m = wave_max(m);
+    if (lane == 0) redm[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
+    int e = 0;
+    (void)frexpf(m, &e);
+    const float s = m > 0.0f ? ldexpf(1.0f, e - 6) : 1.0f;
+    const double sd = s;
+    double tsum = 0.0, res = 0.0;
+    for (int c = tid; c < H; c += 256) {
+        const double x = bf2f(hr[c]);
+        const double y = x / sd;                  // exact: power-of-two scale, |y| < 64
+        const double a = rint(y);
+        const double t1 = (y - a) * 128.0;        // |t1| <= 64
+        const double b = rint(t1);
+        const double t2 = (t1 - b) * 128.0;
+        const double cc = rint(t2);
+        w.planes[(static_cast<size_t>(0) * M + r) * H + c] = static_cast<int8_t>(a);
+        w.planes[(static_cast<size_t>(1) * M + r) * H + c] = static_cast<int8_t>(b);
+        w.planes[(static_cast<size_t>(2) * M + r) * H + c] = static_cast<int8_t>(cc);
+        tsum += fabs(x);
+        res += fabs(x - sd * (a + b * 0x1.0p-7 + cc * 0x1.0p-14));
+    }
+    tsum = wave_sum_xor(tsum);
+    res = wave_sum_xor(res);
+    if (lane == 0) { redt[wv] = tsum; redr[wv] = res; }
     __syncthreads();
     if (tid == 0) {
-        w.tsum[r] = (red[0] + red[1]) + (red[2] + red[3]);
+        // rounded up so that the window bound stays an upper bound
+        w.tsum[r] = static_cast<float>(((redt[0] + redt[1]) + (redt[2] + redt[3])) * (1.0 + 0x1.0p-20));
+        w.res[r] = static_cast<float>(((redr[0] + redr[1]) + (redr[2] + redr[3])) * (1.0 + 0x1.0p-20));
+        w.hscale[r] = s;
         w.rowmax[r] = 0u;
         w.cnt[r] = 0;
         w.best[r] = 0ull;
     }
 }
 
-// Fast pass. Lane l owns columns [CPL*l, CPL*l + CPL); the int8 weights are biased by
-// 128 (w ^ 0x80 -> u in [1, 255], converted exactly by v_cvt_f32_ubyte*) and the bias
-// is removed with the lane's column sum of h.
-template <int M, int CPL>
-__global__ __launch_bounds__(256) void k_head_fast(HeadDev hd, const uint16_t* __restrict__ h, HeadWork w,
-                                                   float* __restrict__ out_logits) {
-    const int lane = threadIdx.x & 63;
-    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int nw = gridDim.x * 4;
-    const int H = hd.H;
-    float hr[M][CPL];
-    float hs[M];
-#pragma unroll
-    for (int r = 0; r < M; ++r) {
-        hs[r] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            hr[r][c] = bf2f(h[static_cast<size_t>(r) * H + CPL * lane + c]);
-            hs[r] += hr[r][c];
-        }
-    }
-    float mx[M];
-#pragma unroll
-    for (int r = 0; r < M; ++r) mx[r] = -INFINITY;
-    float* dst = out_logits ? out_logits : w.fast;
-    for (int64_t v = gw; v < hd.V; v += nw) {
-        const int8_t* row = hd.w + v * H + CPL * lane;
-        uint32_t wd[CPL / 4];
-        if constexpr ((CPL % 16) == 0) {
-#pragma unroll
-            for (int i = 0; i < CPL / 16; ++i) {
-                const uint4 q = reinterpret_cast<const uint4*>(row)[i];
-                wd[4 * i] = q.x; wd[4 * i + 1] = q.y; wd[4 * i + 2] = q.z; wd[4 * i + 3] = q.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < CPL / 8; ++i) {
-                const uint2 q = reinterpret_cast<const uint2*>(row)[i];
-                wd[2 * i] = q.x; wd[2 * i + 1] = q.y;
-            }
-        }
-        float acc[M];
-#pragma unroll
-        for (int r = 0; r < M; ++r) acc[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < CPL / 4; ++i) {
-            const uint32_t b = wd[i] ^ 0x80808080u;
-            const float u0 = static_cast<float>(b & 0xffu);
-            const float u1 = static_cast<float>((b >> 8) & 0xffu);
-            const float u2 = static_cast<float>((b >> 16) & 0xffu);
-            const float u3 = static_cast<float>(b >> 24);
-#pragma unroll
-            for (int r = 0; r < M; ++r) {
-                acc[r] = fmaf(u0, hr[r][4 * i], acc[r]);
-                acc[r] = fmaf(u1, hr[r][4 * i + 1], acc[r]);
-                acc[r] = fmaf(u2, hr[r][4 * i + 2], acc[r]);
-                acc[r] = fmaf(u3, hr[r][4 * i + 3], acc[r]);
-            }
-        }
-        const float sc = h2f(hd.scales[v]);
-#pragma unroll
-        for (int r = 0; r < M; ++r) {
-            const float s = wave_sum_xor(fmaf(-128.0f, hs[r], acc[r]));
-            const float lg = s * sc;
-            mx[r] = fmaxf(mx[r], lg);
-            if (lane == 0) dst[static_cast<size_t>(r) * hd.V + v] = lg;
-        }
-    }
-    if (lane == 0 && !out_logits) {
-#pragma unroll
-        for (int r = 0; r < M; ++r) atomicMax(&w.rowmax[r], orderable(mx[r]));
-    }
-}
+// Fast pass on v_mfma_i32_16x16x64_i8. A tile is 16 vocab rows; the TB groups of four
+// waves of a block take one tile each, and the four waves of a group split the tile's K
+// range into quarters. Lane (i = l % 16, q = l / 16) of wave wq loads, for step s, the 16
+// weight bytes of row i at columns wq * H/4 + 64 s + 16 q (the MFMA A operand, used as
+// loaded); B is the same columns of the request planes, from LDS in the layout
+// [plane][column / 16][row MR][16 bytes] (conflict-free: the 16 lanes of a row group read
+// 16 consecutive 16-byte chunks). The weights of the group's next tile are loaded before
+// the cross-wave reduction of the current one. Output lane (vocab 4q + r, request row i).
+typedef int i4_t __attribute__((ext_vector_type(4)));
 
-// MFMA fast pass (v_mfma_f32_16x16x32_bf16). A wave owns 16-row vocab tiles; lane
-// (i = l % 16, q = l / 16) loads 16 weight bytes of row i per 64-column superstep s
-// (columns 64s + 16q .. +15) and feeds them to two MFMAs as bf16 (u = w ^ 0x80 = w + 128 is
-// exact in bf16); B holds the same columns of the request rows, from LDS. The bias is
-// removed per request row with 128 * sum(h). Output lane (i' = 4q + r, j = l % 16).
-typedef __bf16 bh8_t __attribute__((ext_vector_type(8)));
-typedef float hf4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint32_t pack_bf16_hi(float lo, float hi) {
-    return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
-}
-
-template <int H>
-__global__ __launch_bounds__(256) void k_head_mfma(HeadDev hd, const uint16_t* __restrict__ h, int M, HeadWork w,
-                                                   float* __restrict__ out_logits) {
-    __shared__ __align__(16) uint16_t hs[5 * H];   // request rows 0..3, then a zero row
-    __shared__ float hsum_s[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < 5 * H / 8; i += 256) {
+template <int NS, int MR, int TB>
+__global__ __launch_bounds__(256 * TB) void k_head_i8(HeadDev hd, int M, HeadWork w, float* __restrict__ out_logits) {
+    constexpr int H = 256 * NS;
+    extern __shared__ __align__(16) int8_t hp[];  // [3][H/16][MR][16]
+    __shared__ long long red[2][TB][4][4][MR][4];  // [buffer][group][wave][q][row][r]
+    const int tid = threadIdx.x;
+    for (int c = tid; c < 3 * (H / 16) * MR; c += 256 * TB) {
+        const int p = c / ((H / 16) * MR), rem = c - p * ((H / 16) * MR), kc = rem / MR, j = rem % MR;
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (i < M * H / 8) v = reinterpret_cast<const uint4*>(h)[i];
-        reinterpret_cast<uint4*>(hs)[i] = v;
-    }
-    if (wave < M) {
-        float sacc = 0.0f;
-        for (int c = lane; c < H; c += 64) sacc += bf2f(h[wave * H + c]);
-        sacc = wave_sum_xor(sacc);
-        if (lane == 0) hsum_s[wave] = sacc;
+        if (j < M) v = *reinterpret_cast<const uint4*>(w.planes + (static_cast<size_t>(p) * M + j) * H + 16 * kc);
+        reinterpret_cast<uint4*>(hp)[c] = v;
     }
     __syncthreads();
-    const int i16 = lane & 15, q = lane >> 4;
-    const int j = i16;                       // request row of this lane's B / D column
-    const bool jact = j < M;
-    const float hsum = jact ? hsum_s[j] : 0.0f;
-    const uint4* hrow = reinterpret_cast<const uint4*>(hs + (jact ? j : 4) * H) + 2 * q;  // branch-free B
+    const int lane = tid & 63, wave = (tid >> 6) & 3, grp = tid >> 8, i16 = lane & 15, q = lane >> 4;
+    const int jj = i16 < M ? i16 : 0;
+    const int8_t* bp = hp + ((wave * 4 * NS + q) * MR + jj) * 16;
+    constexpr int kPlane = H * MR;
+    const int64_t V = hd.V;
+    const int64_t tiles = (V + 15) / 16;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * TB;
+    uint4 wv[NS];
+    auto load = [&](int64_t tt) {
+        int64_t vr = tt * 16 + i16;
+        if (vr >= V) vr = V - 1;  // ragged last tile: a valid row, never stored
+        const uint4* src = reinterpret_cast<const uint4*>(hd.w + vr * H + wave * (H / 4)) + q;
+#pragma unroll
+        for (int k = 0; k < NS; ++k) wv[k] = src[4 * k];
+    };
+    int64_t base = static_cast<int64_t>(blockIdx.x) * TB;
+    if (base + grp < tiles) load(base + grp);
+    const bool jact = i16 < M;
+    const double hsc = jact ? static_cast<double>(w.hscale[i16]) * 0x1.0p-14 : 0.0;
     float* dst = out_logits ? out_logits : w.fast;
-    const int64_t tiles = (hd.V + 15) / 16;
     float mx = -INFINITY;
-    constexpr int S = H / 64;
-    constexpr int BATCH = 8;
-    for (int64_t t = blockIdx.x * 4 + wave; t < tiles; t += gridDim.x * 4) {
-        const int64_t v0 = t * 16;
-        int64_t vr = v0 + i16;
-        if (vr >= hd.V) vr = hd.V - 1;       // ragged last tile: recompute a valid row, not stored
-        const uint4* wrow = reinterpret_cast<const uint4*>(hd.w + vr * H) + q;
-        hf4_t acc = {0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < S; s0 += BATCH) {
-            uint4 wv[BATCH];
+    int buf = 0;
+    for (; base < tiles; base += stride) {  // trip count uniform over the block
+        const int64_t t = base + grp;
+        i4_t a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0};
+        if (t < tiles) {
 #pragma unroll
-            for (int k = 0; k < BATCH; ++k) wv[k] = wrow[4 * (s0 + k)];
-#pragma unroll
-            for (int k = 0; k < BATCH; ++k) {
-                const uint32_t b4[4] = {wv[k].x ^ 0x80808080u, wv[k].y ^ 0x80808080u, wv[k].z ^ 0x80808080u,
-                                        wv[k].w ^ 0x80808080u};
-                uint32_t a[8];
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    const float f0 = static_cast<float>(b4[m] & 0xffu), f1 = static_cast<float>((b4[m] >> 8) & 0xffu);
-                    const float f2 = static_cast<float>((b4[m] >> 16) & 0xffu), f3 = static_cast<float>(b4[m] >> 24);
-                    a[2 * m] = pack_bf16_hi(f0, f1);
-                    a[2 * m + 1] = pack_bf16_hi(f2, f3);
-                }
-                const uint4 b0 = hrow[8 * (s0 + k)];
-                const uint4 b1 = hrow[8 * (s0 + k) + 1];
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(bh8_t, make_uint4(a[0], a[1], a[2], a[3])), __builtin_bit_cast(bh8_t, b0), acc,
-                    0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(bh8_t, make_uint4(a[4], a[5], a[6], a[7])), __builtin_bit_cast(bh8_t, b1), acc,
-                    0, 0, 0);
+            for (int k = 0; k < NS; ++k) {
+                const i4_t av = __builtin_bit_cast(i4_t, wv[k]);
+                const int8_t* b = bp + 64 * MR * k;
+                a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, *reinterpret_cast<const i4_t*>(b), a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, *reinterpret_cast<const i4_t*>(b + kPlane), a1, 0, 0, 0);
+                a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, *reinterpret_cast<const i4_t*>(b + 2 * kPlane), a2, 0,
+                                                           0, 0);
             }
+            if (t + stride < tiles) load(t + stride);
         }
-        if (jact) {
+        if (i16 < MR) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                red[buf][grp][wave][q][i16][r] = static_cast<long long>(a0[r]) * 16384 +
+                                                 static_cast<long long>(a1[r]) * 128 + a2[r];
+        }
+        __syncthreads();
+        if (wave == 0 && jact && t < tiles) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t v = v0 + 4 * q + r;
-                if (v < hd.V) {
-                    const float lg = fmaf(-128.0f, hsum, acc[r]) * h2f(hd.scales[v]);
+                const int64_t v = t * 16 + 4 * q + r;
+                if (v < V) {
+                    const long long acc = (red[buf][grp][0][q][i16][r] + red[buf][grp][1][q][i16][r]) +
+                                          (red[buf][grp][2][q][i16][r] + red[buf][grp][3][q][i16][r]);
+                    const float lg = static_cast<float>(static_cast<double>(h2f(hd.scales[v])) *
+                                                        (static_cast<double>(acc) * hsc));
                     mx = fmaxf(mx, lg);
-                    dst[static_cast<size_t>(j) * hd.V + v] = lg;
+                    dst[static_cast<size_t>(i16) * V + v] = lg;
                 }
             }
         }
+        buf ^= 1;  // the other buffer is free: its readers passed this iteration's barrier
     }
-    if (jact && !out_logits) atomicMax(&w.rowmax[j], orderable(mx));
+    if (wave == 0 && jact && !out_logits) atomicMax(&w.rowmax[i16], orderable(mx));
 }
 
-// Window: fast >= max - 2E, E = 2 * s_max * 383 * sum|h| * 80 * 2^-24 + 1e-30 (the float
-// error bound of the fast pass and of the contract's own rounding, with a factor 2).
-// Window: fast >= max - 2E with E a bound on |fast - contract|: the fast pass sums 2048
-// terms |u*h| <= 255|h| (plus the 128*sum(h) correction) in float in an unspecified order,
-// so |error| <= 2^-24 * s_max * sum|h| * (2047 * 383 + 2 * 383); taken with a factor 4.
+// Window: fast >= max - 2E with E = 2 * s_max * 128 * (R + 2^-22 (sum|h| + R)), twice the
+// bound on |fast - contract| derived above (|w| <= 128 for int8 weights).
 __device__ __forceinline__ float head_window(const HeadDev& hd, const HeadWork& w, int r) {
-    const float E = 4.0f * hd.s_max * w.tsum[r] * 0x1.0p-24f * (2047.0f * 383.0f + 766.0f) + 1e-30f;
+    const float E = 2.0f * hd.s_max * 128.0f * (w.res[r] + 0x1.0p-22f * (w.tsum[r] + w.res[r])) + 1e-30f;
     return from_orderable(w.rowmax[r]) - 2.0f * E;
 }
 
@@ -493,31 +458,41 @@ __global__ __launch_bounds__(kSampThreads) void k_accept_sampled(const float* __
 namespace {
 int head_grid() { return 256 * 8; }
 
-template <int M>
-hipError_t launch_fast_m(const HeadDev& hd, const uint16_t* h, const HeadWork& w, float* out, hipStream_t st) {
-    if (hd.H == 2048)
-        hipLaunchKernelGGL((k_head_fast<M, 32>), dim3(head_grid()), dim3(256), 0, st, hd, h, w, out);
-    else if (hd.H == 2560)
-        hipLaunchKernelGGL((k_head_fast<M, 40>), dim3(head_grid()), dim3(256), 0, st, hd, h, w, out);
-    else if (hd.H == 1024)
-        hipLaunchKernelGGL((k_head_fast<M, 16>), dim3(head_grid()), dim3(256), 0, st, hd, h, w, out);
-    else
-        return hipErrorInvalidValue;
+int cu_count() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+        n = 256;
+    return n;
+}
+
+template <int NS, int MR, int TB>
+constexpr size_t i8_lds() { return 3ull * MR * 256 * NS; }
+
+template <int NS, int MR, int TB>
+hipError_t set_i8_attr() {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&k_head_i8<NS, MR, TB>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(i8_lds<NS, MR, TB>()));
+}
+
+// Request rows <= 4: one tile per block, four blocks per CU. Up to 16 rows: two tiles per
+// block sharing the 16-row planes, one block per CU.
+template <int NS, int MR, int TB>
+hipError_t launch_i8_t(const HeadDev& hd, int M, const HeadWork& w, float* out, hipStream_t st) {
+    const int64_t tiles = (hd.V + 15) / 16;
+    int64_t grid = static_cast<int64_t>(cu_count()) * (MR == 4 ? 4 : 1);
+    if (grid > (tiles + TB - 1) / TB) grid = (tiles + TB - 1) / TB;
+    constexpr size_t lds = i8_lds<NS, MR, TB>();
+    hipLaunchKernelGGL((k_head_i8<NS, MR, TB>), dim3(static_cast<unsigned>(grid)), dim3(256 * TB), lds, st, hd, M, w,
+                       out);
     return hipGetLastError();
 }
-hipError_t launch_fast(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, float* out, hipStream_t st) {
-    if (M >= 1 && M <= 4 && (hd.H == 2048 || hd.H == 1024)) {
-        if (hd.H == 2048)
-            hipLaunchKernelGGL(k_head_mfma<2048>, dim3(256 * 4), dim3(256), 0, st, hd, h, M, w, out);
-        else
-            hipLaunchKernelGGL(k_head_mfma<1024>, dim3(256 * 4), dim3(256), 0, st, hd, h, M, w, out);
-        return hipGetLastError();
-    }
-    switch (M) {
-        case 1: return launch_fast_m<1>(hd, h, w, out, st);
-        case 2: return launch_fast_m<2>(hd, h, w, out, st);
-        case 3: return launch_fast_m<3>(hd, h, w, out, st);
-        case 4: return launch_fast_m<4>(hd, h, w, out, st);
+hipError_t launch_i8(const HeadDev& hd, int M, const HeadWork& w, float* out, hipStream_t st) {
+    const bool wide = M > 4;
+    switch (hd.H) {
+        case 1024: return wide ? launch_i8_t<4, 16, 2>(hd, M, w, out, st) : launch_i8_t<4, 4, 1>(hd, M, w, out, st);
+        case 2048: return wide ? launch_i8_t<8, 16, 2>(hd, M, w, out, st) : launch_i8_t<8, 4, 1>(hd, M, w, out, st);
+        case 2560: return wide ? launch_i8_t<10, 16, 2>(hd, M, w, out, st) : launch_i8_t<10, 4, 1>(hd, M, w, out, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -528,12 +503,20 @@ hipError_t launch_q4_m(const HeadDev& hd, const uint16_t* h, float* out, hipStre
 }
 } // namespace
 
+hipError_t head_init_attrs() {
+    hipError_t e = hipSuccess;
+    for (hipError_t x : {set_i8_attr<4, 4, 1>(), set_i8_attr<4, 16, 2>(), set_i8_attr<8, 4, 1>(),
+                         set_i8_attr<8, 16, 2>(), set_i8_attr<10, 4, 1>(), set_i8_attr<10, 16, 2>()})
+        if (x != hipSuccess) e = x;
+    return e;
+}
+
 hipError_t launch_head_greedy(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, uint32_t* argmax,
                               float* logit, hipStream_t st) {
-    hipLaunchKernelGGL(k_head_prep, dim3(M), dim3(256), 0, st, h, hd.H, w);
+    hipLaunchKernelGGL(k_head_prep, dim3(M), dim3(256), 0, st, h, hd.H, M, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if ((e = launch_fast(hd, h, M, w, nullptr, st)) != hipSuccess) return e;
+    if ((e = launch_i8(hd, M, w, nullptr, st)) != hipSuccess) return e;
     hipLaunchKernelGGL(k_head_cand, dim3(2048), dim3(256), 0, st, hd, M, w);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_head_exact, dim3(16, M), dim3(256), 0, st, hd, h, w);
@@ -542,10 +525,13 @@ hipError_t launch_head_greedy(const HeadDev& hd, const uint16_t* h, int M, const
     return hipGetLastError();
 }
 
-hipError_t launch_head_logits(const HeadDev& hd, const uint16_t* h, int M, float* logits, hipStream_t st) {
+hipError_t launch_head_logits(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, float* logits,
+                              hipStream_t st) {
     if (hd.kind == 0) {
-        HeadWork dummy{};
-        return launch_fast(hd, h, M, dummy, logits, st);
+        hipLaunchKernelGGL(k_head_prep, dim3(M), dim3(256), 0, st, h, hd.H, M, w);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_i8(hd, M, w, logits, st);
     }
     if (hd.H != 2048) return hipErrorInvalidValue;
     switch (M) {

@@ -80,19 +80,26 @@ hipError_t launch_gen_head(const HeadDev& hd, uint64_t seed, int8_t* w, uint16_t
 hipError_t launch_scale_absmax(const uint16_t* scales, int64_t n, float* out, hipStream_t st);
 
 // heads
+// Head workspace; the logits path uses the leading part (planes .. best) only.
 struct HeadWork {
-    float* fast;        // [M, V]
-    uint32_t* rowmax;   // [M] orderable
+    int8_t* planes;     // [3, M, H] int8 planes of the request rows
+    float* hscale;      // [M] plane scale (a power of two)
+    float* res;         // [M] sum |h - plane reconstruction|
     float* tsum;        // [M] sum |h|
+    uint32_t* rowmax;   // [M] orderable
     int32_t* cnt;       // [M]
-    int32_t* cand;      // [M, kHeadCap]
     unsigned long long* best;  // [M]
+    int32_t* cand;      // [M, kHeadCap] (greedy)
+    float* fast;        // [M, V] (greedy)
 };
-size_t head_work_bytes(int64_t V, int M);
-HeadWork head_work_carve(void* base, int64_t V, int M);
+constexpr int kHeadMaxRows = 16;
+size_t head_work_bytes(const HeadDev& hd, int M, bool greedy);
+HeadWork head_work_carve(void* base, const HeadDev& hd, int M, bool greedy);
+hipError_t head_init_attrs();
 hipError_t launch_head_greedy(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, uint32_t* argmax,
                               float* logit, hipStream_t st);
-hipError_t launch_head_logits(const HeadDev& hd, const uint16_t* h, int M, float* logits, hipStream_t st);
+hipError_t launch_head_logits(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, float* logits,
+                              hipStream_t st);
 
 // acceptance
 hipError_t launch_accept_sampled(const float* tl, const float* dl, const uint32_t* drafts, int k, int64_t V,

@@ -26,7 +26,9 @@ def logits(q38, hd, h_np):
     M = h_np.shape[0]
     h = G.to_dev(h_np)
     out = G.empty((M, hd.vocab), np.float32)
-    q38.check(q38.lib.q38_head_logits(hd.h, h.data_ptr(), M, out.data_ptr(), None, 0, G.stream()))
+    ws = G.workspace(hd.workspace_size(M))
+    q38.check(q38.lib.q38_head_logits(hd.h, h.data_ptr(), M, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                      G.stream()))
     return G.to_host(out)
 
 
@@ -37,10 +39,14 @@ def explicit_head(q38, gpu, W, s):
     return hd
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
-def test_explicit_head_exact(gpu, q38, orc, M):
-    rng = np.random.default_rng(M)
-    V, H = 5000, 2048
+@pytest.mark.parametrize("M,H", [(1, 2048), (2, 2048), (3, 2048), (4, 2048), (5, 2048), (8, 2048),
+                                 (16, 2048), (3, 1024), (16, 1024), (4, 2560), (11, 2560)])
+def test_explicit_head_exact(gpu, q38, orc, M, H):
+    """Greedy argmax + logit bit-exact against the contract; fast logits within float
+    tolerance. Rows 1-4 take the 4-row kernel, 5-16 the 16-row kernel (two tiles per block);
+    V = 5000 leaves a ragged last tile."""
+    rng = np.random.default_rng(M * 7 + H)
+    V = 5000
     W = rng.integers(-127, 128, (V, H)).astype(np.int8)
     s = f16(rng.uniform(1e-4, 1e-3, V))
     h = orc.bf16(rng.normal(0, 1, (M, H)))
@@ -113,5 +119,40 @@ def test_q4_draft_head(gpu, q38, orc):
         want = orc.head_q4_synth_logits(SEED, 2048, h)
         err = np.abs(got - want)
         assert err.max() <= 1e-4 * np.abs(want).max() + 1e-5
+    finally:
+        hd.close()
+
+
+def test_head_rows_beyond_limit_rejected(gpu, q38):
+    hd = q38.Head(gpu, q38.Q38_HEAD_Q8, 64, 2048, seed=SEED)
+    try:
+        assert hd.workspace_size(17) == 0
+        h = G.empty((17, 2048), np.uint16)
+        out = G.empty((17, 64), np.float32)
+        ws = G.workspace(hd.workspace_size(16))
+        rc = q38.lib.q38_head_logits(hd.h, h.data_ptr(), 17, out.data_ptr(), ws.data_ptr(), ws.numel(), G.stream())
+        assert rc == q38.Q38_EINVAL
+        rc = q38.lib.q38_head_logits(hd.h, h.data_ptr(), 4, out.data_ptr(), ws.data_ptr(), 16, G.stream())
+        assert rc == q38.Q38_ESPACE
+    finally:
+        hd.close()
+
+
+def test_head_planes_wide_dynamic_range(gpu, q38, orc):
+    """Rows mixing large and tiny magnitudes (the planes cannot hold the tiny ones
+    exactly): the measured residual widens the window and the argmax stays exact."""
+    rng = np.random.default_rng(21)
+    V, H = 4096, 2048
+    W = rng.integers(-128, 128, (V, H)).astype(np.int8)
+    s = f16(rng.uniform(1e-4, 1e-3, V))
+    x = rng.normal(0, 1, (4, H)) * np.exp(rng.uniform(-18, 0, (4, H)))
+    x[:, :4] = 40.0
+    h = orc.bf16(x)
+    hd = explicit_head(q38, gpu, W, s)
+    try:
+        am, lg = greedy(q38, hd, h)
+        want = orc.head_q8_logits(W, s, h)
+        wi, wv = orc.argmax(want)
+        assert np.array_equal(am, wi) and np.array_equal(lg, wv)
     finally:
         hd.close()
