@@ -376,19 +376,21 @@ int q38_moe_route(q38_moe_layer* L, const uint16_t* x, int32_t rows, const q38_r
     MoeBufs w{};
     if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    Q38_HIP(launch_router(L->dev, w, rows, x, 0, 0.0f, st));
+    Q38_HIP(launch_router(L->dev, w, rows, x, st));
     Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
     return copy_routes(L, rows, w, routes, st);
 }
 
-// One layer: router (+ RMSNorm of h_in when do_norm), routing plan (fused into the MFMA
-// gate/up kernel, a separate kernel otherwise), gate/up, down, combine. Chain mode
-// (h_chain) adds the residual in place; otherwise y receives the layer output. ev, when
-// given, holds 5 events recorded around the phases.
-static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* h_in, int do_norm, float eps,
+// One layer: router logits, routing plan (fused into the MFMA gate/up kernel, a separate
+// kernel otherwise), gate/up, down, combine. Chain mode (h_chain): x_in is the workspace
+// copy B.x formed by k_xnorm (first layer) or by the previous layer's combine, and the
+// combine adds the residual to h_chain in place and forms the next layer's input;
+// otherwise y receives the layer output. ev, when given, holds 5 events recorded around
+// the phases.
+static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* x_in, float eps,
                      uint16_t* h_chain, uint16_t* y, const q38_route_out* trace, hipEvent_t* ev, hipStream_t st) {
     if (ev) Q38_HIP(hipEventRecord(ev[0], st));
-    Q38_HIP(launch_router(L->dev, w, rows, h_in, do_norm, eps, st));
+    Q38_HIP(launch_router(L->dev, w, rows, x_in, st));
     if (!moe_uses_mfma(L->dev)) Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[1], st));
     Q38_HIP(launch_gate_up(L->dev, w, rows, st));
@@ -397,7 +399,8 @@ static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_
         if (int rc = copy_routes(L, rows, w, trace, st)) return rc;
     Q38_HIP(launch_down(L->dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[3], st));
-    Q38_HIP(launch_combine(L->dev, w, rows, h_chain, y, st));
+    if (h_chain) Q38_HIP(launch_combine_norm(L->dev, w, rows, h_chain, eps, st));
+    else Q38_HIP(launch_combine(L->dev, w, rows, nullptr, y, st));
     if (ev) Q38_HIP(hipEventRecord(ev[4], st));
     return Q38_OK;
 }
@@ -409,7 +412,7 @@ int q38_moe_forward(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t*
     if (int rc = check_rows(rows)) return rc;
     MoeBufs w{};
     if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
-    return run_layer(L, w, rows, x, 0, 0.0f, nullptr, y, routes, nullptr, static_cast<hipStream_t>(stream));
+    return run_layer(L, w, rows, x, 0.0f, nullptr, y, routes, nullptr, static_cast<hipStream_t>(stream));
 }
 
 static int chain_check(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows, void* ws,
@@ -434,7 +437,8 @@ int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h
     for (int l = 0; l < n_layers; ++l) {
         MoeBufs w{};
         moe_ws(layers[l]->desc, rows, &w, ws);
-        if (int rc = run_layer(layers[l], w, rows, h, 1, eps, h, nullptr, traces ? &traces[l] : nullptr, nullptr, st))
+        if (l == 0) Q38_HIP(launch_xnorm(h, rows, layers[0]->desc.hidden, eps, w.x, w.x16, st));
+        if (int rc = run_layer(layers[l], w, rows, w.x, eps, h, nullptr, traces ? &traces[l] : nullptr, nullptr, st))
             return rc;
     }
     return Q38_OK;
@@ -452,7 +456,11 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
     for (int l = 0; l < n_layers && rc == Q38_OK; ++l) {
         MoeBufs w{};
         moe_ws(layers[l]->desc, rows, &w, ws);
-        rc = run_layer(layers[l], w, rows, h, 1, eps, h, nullptr, traces ? &traces[l] : nullptr,
+        if (l == 0 && launch_xnorm(h, rows, layers[0]->desc.hidden, eps, w.x, w.x16, st) != hipSuccess) {
+            rc = fail(Q38_EHIP, "verify chain: RMSNorm launch failed");
+            break;
+        }
+        rc = run_layer(layers[l], w, rows, w.x, eps, h, nullptr, traces ? &traces[l] : nullptr,
                        &ev[static_cast<size_t>(l) * 5], st);
     }
     if (rc == Q38_OK) {

@@ -104,12 +104,66 @@ __device__ __forceinline__ float exp_contract(float d) {
 // ------------------------------------------------------------------ wave reductions
 // xor butterfly: every lane ends with the same value, equal to the pairwise tree
 // ((l, l^32), then ^16, ...) that the CPU restatement reproduces.
+// Value of lane l ^ M. M = 1, 2: DPP quad permutations; M = 4, 8: a row shift for the
+// lanes whose bit is clear and the opposite shift for the others (bank masks select the
+// lanes, every source lies in the same row); M = 16: ds_swizzle xor mode (32-lane groups);
+// M = 32: lane permute.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (M == 1) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false));
+    } else if constexpr (M == 2) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false));
+    } else if constexpr (M == 4 || M == 8) {
+        constexpr int lo_banks = M == 4 ? 0x5 : 0x3;  // lanes with bit M clear: read l + M
+        const int t = __builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0x100 + M, 0xF, lo_banks,
+                                                  false);
+        return static_cast<uint32_t>(
+            __builtin_amdgcn_update_dpp(t, static_cast<int>(v), 0x110 + M, 0xF, 0xF ^ lo_banks, false));
+    } else if constexpr (M == 16) {
+        return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), (16 << 10) | 0x1F));
+    } else {
+        return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), M, kWave));
+    }
+}
+template <int M>
+__device__ __forceinline__ float xor_lane_f(float v) {
+    return __uint_as_float(xor_lane<M>(__float_as_uint(v)));
+}
+template <int M>
+__device__ __forceinline__ double xor_lane_d(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t r = (static_cast<uint64_t>(xor_lane<M>(static_cast<uint32_t>(b >> 32))) << 32) |
+                       xor_lane<M>(static_cast<uint32_t>(b));
+    return __builtin_bit_cast(double, r);
+}
+// Butterfly sum (offsets 32, 16, ..., 1; v = v + v[l ^ off]): every lane ends with the
+// same total, in an order the CPU restatement repeats.
 __device__ __forceinline__ float wave_sum_xor(float v) {
+    v = v + xor_lane_f<32>(v);
+    v = v + xor_lane_f<16>(v);
+    v = v + xor_lane_f<8>(v);
+    v = v + xor_lane_f<4>(v);
+    v = v + xor_lane_f<2>(v);
+    v = v + xor_lane_f<1>(v);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_xor(double v) {
+    v = v + xor_lane_d<32>(v);
+    v = v + xor_lane_d<16>(v);
+    v = v + xor_lane_d<8>(v);
+    v = v + xor_lane_d<4>(v);
+    v = v + xor_lane_d<2>(v);
+    v = v + xor_lane_d<1>(v);
+    return v;
+}
+// The same butterfly through lane permutes only (the reference form of the exchanges).
+__device__ __forceinline__ float wave_sum_xor_shfl(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
     return v;
 }
-__device__ __forceinline__ double wave_sum_xor(double v) {
+__device__ __forceinline__ double wave_sum_xor_shfl(double v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
     return v;

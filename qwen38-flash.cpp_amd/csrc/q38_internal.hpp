@@ -54,17 +54,25 @@ struct HeadDev {
 };
 
 // MoE layer (rows M <= kMaxRows)
-// Router logits (+ RMSNorm of h when do_norm; otherwise h is the normalised input).
-hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* h, int do_norm, float eps,
-                         hipStream_t st);
+// Router logits of the normalised input x (copied to B.x / B.x16 unless x is B.x).
+hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st);
 hipError_t launch_topk_plan(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 // chain: h <- h + y (in place); otherwise out <- y.
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st);
+// Verify chain: x = RMSNorm(h) of the first layer into B.x / B.x16, and the combine that
+// updates h in place and forms the next layer's x (same norm routine).
+hipError_t launch_xnorm(const uint16_t* h, int M, int H, float eps, uint16_t* x, uint16_t* x16, hipStream_t st);
+hipError_t launch_combine_norm(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, float eps, hipStream_t st);
 hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_t* book4, hipStream_t st);
 bool moe_uses_mfma(const LayerDev& L);
+// Verify widths of up to 4 rows on the 4x4x4 MFMA kernels (q38_moe4.hip).
+bool moe_uses_narrow(const LayerDev& L, int M);
+hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+int mfma_grid();  // persistent workgroups of the expert kernels (a multiple of 32)
 
 // generators
 hipError_t launch_gen_codes(uint64_t key, int e0, int n_experts, int out_dim, int nsub, int bits, int words,

@@ -2,8 +2,8 @@
 // (rows <= 16), plus the synthetic-weight generators.
 //
 // Per layer the launch sequence is
-//   k_router      router logits with the fixed-order contract (R1) + the shared-expert
-//                 gate logit, one wave per row of Wr; clears this layer's accumulators.
+//   k_logits      router logits with the fixed-order contract (R1) + the shared-expert
+//                 gate logit; one workgroup per row of Wr, one wave per request row.
 //   k_topk_plan   softmax / top-k / normalise per row (R2) and the gather-by-expert plan
 //                 (R3): unique experts ascending, each with its routes in (row, slot)
 //                 order; one workgroup.
@@ -12,11 +12,13 @@
 //                 routed row of an expert, so each packed code row is read once per chunk.
 //   k_down_mfma   SwiGLU of the gate/up sums + down projection (R7, R8), same scheme.
 //   k_combine     ordered route reduction (slot order) + shared expert x sigmoid gate +
-//                 merge (R8, R10, R11); in chain mode the residual add and the next
-//                 layer's RMSNorm.
+//                 merge (R8, R10, R11); k_combine_norm adds the residual in place (chain)
+//                 and forms the next layer's RMSNorm input; k_xnorm is that RMSNorm for
+//                 the first layer of a chain.
 // Layers with per-64-input scale groups use the k_*_grouped VALU kernels instead.
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
+#include "q38_moe_dev.hpp"
 
 namespace q38 {
 
@@ -113,282 +115,65 @@ __global__ void k_book_to_int8(const uint16_t* __restrict__ book16, int n, int8_
     }
 }
 
-// ============================================================== DPP wave reductions
-// Order-independent reductions (max) use DPP row operations and readlane; the summations
-// whose order is part of a contract keep the xor butterfly of q38_device.hpp.
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xF,
-                                                             0xF, false));
-}
-template <int CTRL>
-__device__ __forceinline__ uint64_t max_step_u64(uint64_t k) {
-    const uint32_t h = dpp32<CTRL>(static_cast<uint32_t>(k >> 32));
-    const uint32_t l = dpp32<CTRL>(static_cast<uint32_t>(k));
-    const uint64_t o = (static_cast<uint64_t>(h) << 32) | l;
-    return o > k ? o : k;
-}
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t k, int lane) {
-    const uint32_t h = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(k >> 32), lane));
-    const uint32_t l = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(k), lane));
-    return (static_cast<uint64_t>(h) << 32) | l;
-}
-// quad_perm(1,0,3,2), quad_perm(2,3,0,1), row_half_mirror, row_mirror, then rows via readlane.
-__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t k) {
-    k = max_step_u64<0xB1>(k);
-    k = max_step_u64<0x4E>(k);
-    k = max_step_u64<0x141>(k);
-    k = max_step_u64<0x140>(k);
-    uint64_t m = readlane_u64(k, 0);
-    const uint64_t a = readlane_u64(k, 16), b = readlane_u64(k, 32), c = readlane_u64(k, 48);
-    m = a > m ? a : m;
-    m = b > m ? b : m;
-    m = c > m ? c : m;
-    return m;
-}
-__device__ __forceinline__ float wave_max_dpp(float v) {
-    auto step = [](float x, uint32_t o) { return fmaxf(x, __uint_as_float(o)); };
-    v = step(v, dpp32<0xB1>(__float_as_uint(v)));
-    v = step(v, dpp32<0x4E>(__float_as_uint(v)));
-    v = step(v, dpp32<0x141>(__float_as_uint(v)));
-    v = step(v, dpp32<0x140>(__float_as_uint(v)));
-    float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)));
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48)));
-    return m;
-}
-
 // ============================================================== router (R1)
-// One wave per row of Wr (plus one for w_sg). In chain mode every wave first forms the
-// layer input x = T(h / sqrt(mean(h^2) + eps)) from its own loads of h: lane l holds the
-// columns c = 512t + 8l + j, so the wave covers whole rows and computes each row's sum of
-// squares (lane partials, xor butterfly) identically in every wave. Logit contract: lane
-// l accumulates x*w over its columns (t outer, j inner) with fmaf, xor butterfly, BF16.
-// Workgroup 0 stores x (bf16) and x16 (fp16, the MFMA operand).
+// One workgroup per row of Wr (the last one: w_sg), one wave per request row (rows w,
+// w + waves, ...). x is the normalised layer input (bf16). Logit contract: lane l holds
+// the columns c = 512t + 8l + j and accumulates x*w over them (t outer, j inner) with
+// fmaf, then the xor butterfly and BF16 rounding. When x is not already the workspace
+// copy, workgroup 0 stores it there (bf16) with its fp16 copy (the MFMA operand).
 template <int T>
-__global__ __launch_bounds__(256) void k_router(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ hin,
-                                                int do_norm, float eps) {
+__global__ __launch_bounds__(256) void k_logits(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ x) {
     constexpr int H = 512 * T;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int e = blockIdx.x * 4 + wave;
-    const int n_rows = L.E + (L.has_shared ? 1 : 0);
-    const bool store_x = blockIdx.x == 0 && wave == 0;
-    if (e >= n_rows && !store_x) return;
-    const bool has_row = e < n_rows;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const int e = blockIdx.x;
     const uint16_t* w = e < L.E ? L.router + static_cast<size_t>(e) * H : L.wsg;
     uint4 wv[T];
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-        if (has_row) wv[t] = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
-    for (int r0 = 0; r0 < M; r0 += 4) {
-        uint4 xv[4][T];
+    for (int t = 0; t < T; ++t) wv[t] = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
+    const bool store_x = e == 0 && x != B.x;
+    for (int r = wave; r < M; r += waves) {
+        uint4 xv[T];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
+        for (int t = 0; t < T; ++t) xv[t] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(r) * H + 512 * t + 8 * lane);
+        float acc = 0.0f;
 #pragma unroll
-            for (int t = 0; t < T; ++t)
-                if (r0 + rr < M) xv[rr][t] = *reinterpret_cast<const uint4*>(hin + (r0 + rr) * H + 512 * t + 8 * lane);
+        for (int t = 0; t < T; ++t) {
+            const uint32_t xq[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+            const uint32_t wq[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const int r = r0 + rr;
-            if (r >= M) break;
-            if (do_norm) {
-                float ss = 0.0f;
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const uint32_t q[4] = {xv[rr][t].x, xv[rr][t].y, xv[rr][t].z, xv[rr][t].w};
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        ss = fmaf(bflo(q[k]), bflo(q[k]), ss);
-                        ss = fmaf(bfhi(q[k]), bfhi(q[k]), ss);
-                    }
-                }
-                ss = wave_sum_xor(ss);
-                const float inv = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    uint32_t q[4] = {xv[rr][t].x, xv[rr][t].y, xv[rr][t].z, xv[rr][t].w};
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const uint32_t lo = f2bf(bflo(q[k]) * inv), hi = f2bf(bfhi(q[k]) * inv);
-                        q[k] = lo | (hi << 16);
-                    }
-                    xv[rr][t] = make_uint4(q[0], q[1], q[2], q[3]);
-                }
+            for (int k = 0; k < 4; ++k) {
+                acc = __builtin_fmaf(bflo(xq[k]), bflo(wq[k]), acc);
+                acc = __builtin_fmaf(bfhi(xq[k]), bfhi(wq[k]), acc);
             }
-            if (store_x) {
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const size_t at = static_cast<size_t>(r) * H + 512 * t + 8 * lane;
-                    *reinterpret_cast<uint4*>(B.x + at) = xv[rr][t];
-                    const uint32_t q[4] = {xv[rr][t].x, xv[rr][t].y, xv[rr][t].z, xv[rr][t].w};
-                    uint32_t hq[4];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        hq[k] = static_cast<uint32_t>(f2h(bflo(q[k]))) | (static_cast<uint32_t>(f2h(bfhi(q[k]))) << 16);
-                    *reinterpret_cast<uint4*>(B.x16 + at) = make_uint4(hq[0], hq[1], hq[2], hq[3]);
-                }
+        }
+        const float sres = wave_sum_xor(acc);
+        if (lane == 0) {
+            if (e < L.E) {
+                B.logits[r * L.E + e] = rbf(sres);
+            } else {
+                const float lg = rbf(sres);
+                B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
             }
-            if (has_row) {
-                float acc = 0.0f;
+        }
+        if (store_x) {
 #pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const uint32_t xq[4] = {xv[rr][t].x, xv[rr][t].y, xv[rr][t].z, xv[rr][t].w};
-                    const uint32_t wq[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
+            for (int t = 0; t < T; ++t) {
+                const size_t at = static_cast<size_t>(r) * H + 512 * t + 8 * lane;
+                *reinterpret_cast<uint4*>(B.x + at) = xv[t];
+                const uint32_t q[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+                uint32_t hq[4];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        acc = __builtin_fmaf(bflo(xq[k]), bflo(wq[k]), acc);
-                        acc = __builtin_fmaf(bfhi(xq[k]), bfhi(wq[k]), acc);
-                    }
-                }
-                const float sres = wave_sum_xor(acc);
-                if (lane == 0) {
-                    if (e < L.E) {
-                        B.logits[r * L.E + e] = rbf(sres);
-                    } else {
-                        const float lg = rbf(sres);
-                        B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
-                    }
-                }
+                for (int k = 0; k < 4; ++k)
+                    hq[k] = static_cast<uint32_t>(f2h(bflo(q[k]))) | (static_cast<uint32_t>(f2h(bfhi(q[k]))) << 16);
+                *reinterpret_cast<uint4*>(B.x16 + at) = make_uint4(hq[0], hq[1], hq[2], hq[3]);
             }
         }
     }
-}
-
-// ============================================================== top-k + plan (R2, R3)
-// Block-level routine (any block of >= 256 threads). Wave w takes rows w, w + waves, ...:
-// lane l owns experts 64j + l as (p bits << 32 | ~index) keys; K rounds of a DPP wave max
-// pick (p desc, index asc). The plan is built by counting: route i lands at
-// #{routes (e, i') < (e_i, i)}; expert groups are marked with a ballot. The plan is left
-// in `plan` (LDS or global); `global_out` also receives experts and weights.
-struct TopkLds {
-    int32_t ex[kMaxRows * kMaxTopK];
-    int32_t sorted_e[kMaxRows * kMaxTopK];
-    int32_t wave_cnt[16];
-};
-
-// Rows are taken by waves [row_wave0, waves); the other waves may do unrelated work
-// (the MFMA gate/up kernel fills its codebook with them) before the first barrier.
-__device__ __forceinline__ void topk_plan_block(const LayerDev& L, const MoeBufs& B, int M, bool global_out, int32_t* plan,
-                                                TopkLds& t, int row_wave0) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int waves = blockDim.x >> 6;
-    const int E = L.E, K = L.K, MK = M * K;
-    const int NJ = E / 64;
-    for (int r = wave - row_wave0; wave >= row_wave0 && r < M; r += waves - row_wave0) {
-        float mx = -INFINITY;
-        float lg[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            lg[j] = j < NJ ? B.logits[r * E + 64 * j + lane] : -INFINITY;
-            mx = fmaxf(mx, lg[j]);
-        }
-        mx = wave_max_dpp(mx);
-        double ds = 0.0;
-        float ev[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            ev[j] = 0.0f;
-            if (j < NJ) {
-                ev[j] = exp_contract(lg[j] - mx);
-                ds += static_cast<double>(ev[j]);
-            }
-        }
-        ds = wave_sum_xor(ds);
-        uint64_t key[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            key[j] = 0;
-            if (j < NJ) {
-                const float p = static_cast<float>(static_cast<double>(ev[j]) / ds);
-                key[j] = (static_cast<uint64_t>(__float_as_uint(p)) << 32) |
-                         static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(64 * j + lane));
-            }
-        }
-        float psel = 0.0f, sum = 0.0f;
-        int isel = 0;
-        for (int s = 0; s < K; ++s) {
-            uint64_t lm = key[0];
-#pragma unroll
-            for (int j = 1; j < 16; ++j) lm = key[j] > lm ? key[j] : lm;
-            const uint64_t best = wave_max_u64_dpp(lm);
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-                if (key[j] == best) key[j] = 0;
-            const float p = __uint_as_float(static_cast<uint32_t>(best >> 32));
-            sum += p;
-            if (lane == s) {
-                psel = p;
-                isel = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
-            }
-        }
-        if (lane < K) {
-            t.ex[r * K + lane] = isel;
-            if (global_out) {
-                B.experts[r * K + lane] = isel;
-                B.weights[r * K + lane] = L.normalize ? psel / sum : psel;
-            }
-        }
-    }
-    __syncthreads();
-    if (tid < MK) {
-        const int my_e = t.ex[tid];
-        const int my_key = (my_e << 8) | tid;
-        int pos = 0;
-        for (int j = 0; j < MK; ++j) pos += ((t.ex[j] << 8) | j) < my_key;
-        t.sorted_e[pos] = my_e;
-        plan[2 + 2 * MK + pos] = tid;   // route_list
-        plan[2 + 3 * MK + tid] = pos;   // route_pos
-    }
-    __syncthreads();
-    const bool start = tid < MK && (tid == 0 || t.sorted_e[tid - 1] != t.sorted_e[tid]);
-    const uint64_t bal = __ballot(start);
-    if (lane == 0) t.wave_cnt[wave] = __popcll(bal);
-    __syncthreads();
-    int rank = __popcll(bal & ((1ull << lane) - 1ull));
-    for (int w = 0; w < wave; ++w) rank += t.wave_cnt[w];
-    if (start) {
-        plan[1 + rank] = t.sorted_e[tid];
-        plan[1 + MK + rank] = tid;
-    }
-    if (tid == 0) {
-        int nu = 0;
-        for (int w = 0; w < waves; ++w) nu += t.wave_cnt[w];
-        plan[0] = nu;
-        plan[1 + MK + nu] = MK;
-    }
-    __syncthreads();
 }
 
 __global__ __launch_bounds__(1024) void k_topk_plan(LayerDev L, MoeBufs B, int M) {
     __shared__ TopkLds t;
     topk_plan_block(L, B, M, true, B.plan, t, 0);
-}
-
-// Rows of unique-expert slot ui: the routed experts in ascending id, then the shared
-// expert (all M rows). Returns false for an empty slot.
-__device__ __forceinline__ bool slot_rows(const int32_t* plan, int M, int K, int has_shared, int ui, int E,
-                                          int* expert, int* n, int* first_pos) {
-    const int nu = plan[0];
-    const int MK = M * K;
-    if (ui < nu) {
-        *expert = plan[1 + ui];
-        const int a = plan[1 + MK + ui], b = plan[1 + MK + ui + 1];
-        *n = b - a;
-        *first_pos = a;
-        return true;
-    }
-    if (ui == nu && has_shared) {
-        *expert = E;
-        *n = M;
-        *first_pos = MK;
-        return true;
-    }
-    return false;
-}
-// The request row of the j-th route of slot ui.
-__device__ __forceinline__ int route_row(const int32_t* plan, int M, int K, int pos0, int j, bool shared) {
-    return shared ? j : plan[2 + 2 * M * K + pos0 + j] / K;
 }
 
 // ============================================================== MFMA expert projections
@@ -407,7 +192,6 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 constexpr int kMfmaThreads = 512;       // 8 waves
 constexpr int kMfmaRowsPerItem = 128;   // 8 waves x 16 rows
 constexpr int kMfmaMaxCols = 8;         // routed rows staged per pass
-constexpr int kPlanInts = 2 + 4 * kMaxRows * kMaxTopK;
 
 template <int BITS, int NSUB>
 __device__ __forceinline__ void load_lane_words(const uint32_t* src, uint32_t* w) {
@@ -448,24 +232,6 @@ __device__ __forceinline__ f4_t mfma_tile(const uint32_t* w, const uint2* book, 
 template <int NSUB>
 __device__ __forceinline__ const uint4* xs_lane(const uint4* xs, int xrow, int zero_row, int q, bool active) {
     return xs + ((active ? xrow : zero_row) * NSUB + q * (NSUB / 4)) / 2;
-}
-
-// Codebook chunk -> LDS by threads [0, nthreads): 16 loads in flight per thread.
-template <int KENT>
-__device__ __forceinline__ void fill_book(const uint16_t* src4, unsigned char* lds, int t, int nthreads) {
-    const uint4* src = reinterpret_cast<const uint4*>(src4);
-    uint4* dst = reinterpret_cast<uint4*>(lds);
-    constexpr int N = KENT / 2;  // uint4 entries
-    constexpr int G = 16;
-    int i = t;
-    for (; i + (G - 1) * nthreads < N; i += G * nthreads) {
-        uint4 v[G];
-#pragma unroll
-        for (int k = 0; k < G; ++k) v[k] = src[i + k * nthreads];
-#pragma unroll
-        for (int k = 0; k < G; ++k) dst[i + k * nthreads] = v[k];
-    }
-    for (; i < N; i += nthreads) dst[i] = src[i];
 }
 
 template <int BITS, int NSUB, int NCHUNK>
@@ -553,14 +319,6 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
 #pragma unroll
         for (int i = 0; i <= WPL; ++i) w[i] = wn[i];
     }
-}
-
-// SwiGLU with the reference's rounding points (src/vq_metal_kernels.hpp:589-595):
-// h = T(T(silu(T(g))) * T(u)).
-__device__ __forceinline__ float swiglu(float g, float u) {
-    const float gt = rbf(g);
-    const float s = rbf(gt / (1.0f + expf(-gt)));
-    return rbf(s * rbf(u));
 }
 
 constexpr int kDownStageRoutes = 48;  // routes whose SwiGLU rows are staged once (M <= 4 with k = 10)
@@ -815,6 +573,96 @@ __global__ __launch_bounds__(256) void k_combine(LayerDev L, MoeBufs B, int M, u
     else out[i] = f2bf(y);
 }
 
+// RMSNorm of one row for the verify chain, with a fixed order: a block of H/4 threads,
+// thread t owns columns t + (H/4) i for i < 4 and accumulates fmaf(v, v, .) in i order;
+// waves join with the xor butterfly, the wave totals are added in wave order. Returns
+// 1 / sqrt(mean(v^2) + eps). red: >= 16 floats of LDS.
+__device__ __forceinline__ float row_inv_rms(const float (&v)[4], float* red, int H, float eps) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss = fmaf(v[i], v[i], ss);
+    ss = wave_sum_xor(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float t = 0.0f;
+    for (int w = 0; w < waves; ++w) t += red[w];
+    return 1.0f / sqrtf(t / static_cast<float>(H) + eps);
+}
+__device__ __forceinline__ void store_xnorm(const float (&v)[4], float inv, int r, int H, uint16_t* x, uint16_t* x16) {
+    const int nt = blockDim.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const size_t at = static_cast<size_t>(r) * H + threadIdx.x + nt * i;
+        const uint16_t b = f2bf(v[i] * inv);
+        x[at] = b;
+        x16[at] = f2h(bf2f(b));
+    }
+}
+
+// x = T(h * inv_rms(h)) for the first layer of a chain (block = H/4 threads per row).
+__global__ __launch_bounds__(1024) void k_xnorm(const uint16_t* __restrict__ h, int H, float eps, uint16_t* x,
+                                                uint16_t* x16) {
+    __shared__ float red[16];
+    const int r = blockIdx.x, nt = blockDim.x;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = bf2f(h[static_cast<size_t>(r) * H + threadIdx.x + nt * i]);
+    const float inv = row_inv_rms(v, red, H, eps);
+    store_xnorm(v, inv, r, H, x, x16);
+}
+
+// Chain combine: one block of H/4 threads per request row. y as in k_combine, h <- T(h + y)
+// in place, then the next layer's input x = T(h * inv_rms(h)) into the workspace (the same
+// routine as k_xnorm, so a chain and its layer-by-layer replay agree bit for bit). All
+// loads of a thread's four columns are issued before the reductions (KT = top-k).
+template <int KT>
+__global__ __launch_bounds__(1024) void k_combine_norm(LayerDev L, MoeBufs B, int M, uint16_t* h, float eps) {
+    __shared__ float red[16];
+    __shared__ float wsl[KT];
+    __shared__ int psl[KT];
+    __shared__ float sg;
+    const int r = blockIdx.x, nt = blockDim.x, tid = threadIdx.x;
+    const int H = L.H, MK = M * KT;
+    if (tid < KT) {
+        wsl[tid] = B.weights[r * KT + tid];
+        psl[tid] = B.plan[2 + 3 * MK + r * KT + tid];
+    }
+    if (tid == KT) sg = L.has_shared ? B.sgate[r] : 0.0f;
+    __syncthreads();
+    const bool two = L.d_parts == 2;
+    const bool shared = L.has_shared;
+    float hv[4], dv[4][KT + 1][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int o = tid + nt * i;
+        hv[i] = bf2f(h[static_cast<size_t>(r) * H + o]);
+#pragma unroll
+        for (int s = 0; s <= KT; ++s) {
+            dv[i][s][0] = dv[i][s][1] = 0.0f;
+            if (s == KT && !shared) continue;
+            const int route = s < KT ? psl[s] : MK + r;
+            const size_t at = static_cast<size_t>(route) * H + o;
+            dv[i][s][0] = B.d[at];
+            if (two) dv[i][s][1] = B.d[B.d_plane + at];
+        }
+    }
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float routed = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KT; ++s) routed = fmaf(wsl[s], rbf(two ? dv[i][s][0] + dv[i][s][1] : dv[i][s][0]), routed);
+        float y = rbf(routed);
+        if (shared) y = rbf(y + rbf(rbf(two ? dv[i][KT][0] + dv[i][KT][1] : dv[i][KT][0]) * sg));
+        const uint16_t hb = f2bf(rbf(hv[i] + y));
+        h[static_cast<size_t>(r) * H + tid + nt * i] = hb;
+        v[i] = bf2f(hb);
+    }
+    const float inv = row_inv_rms(v, red, H, eps);
+    store_xnorm(v, inv, r, H, B.x, B.x16);
+}
+
 __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x, int H, float eps,
                                                  uint16_t* __restrict__ y) {
     __shared__ float red[4];
@@ -862,10 +710,10 @@ void init_grid() {
 }
 
 template <int T>
-hipError_t launch_router_t(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* h, int do_norm, float eps,
-                           hipStream_t st) {
+hipError_t launch_router_t(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st) {
     const int rows = L.E + (L.has_shared ? 1 : 0);
-    hipLaunchKernelGGL(k_router<T>, dim3((rows + 3) / 4), dim3(256), 0, st, L, B, M, h, do_norm, eps);
+    const int waves = M < 4 ? M : 4;
+    hipLaunchKernelGGL(k_logits<T>, dim3(rows), dim3(64 * waves), 0, st, L, B, M, x);
     return hipGetLastError();
 }
 
@@ -935,16 +783,15 @@ bool moe_uses_mfma(const LayerDev& L) {
     return gu_ok && dn_ok;
 }
 
-hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* h, int do_norm, float eps,
-                         hipStream_t st) {
+hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st) {
     switch (L.H / 512) {
-        case 1: return launch_router_t<1>(L, B, M, h, do_norm, eps, st);
-        case 2: return launch_router_t<2>(L, B, M, h, do_norm, eps, st);
-        case 3: return launch_router_t<3>(L, B, M, h, do_norm, eps, st);
-        case 4: return launch_router_t<4>(L, B, M, h, do_norm, eps, st);
-        case 5: return launch_router_t<5>(L, B, M, h, do_norm, eps, st);
-        case 6: return launch_router_t<6>(L, B, M, h, do_norm, eps, st);
-        case 8: return launch_router_t<8>(L, B, M, h, do_norm, eps, st);
+        case 1: return launch_router_t<1>(L, B, M, x, st);
+        case 2: return launch_router_t<2>(L, B, M, x, st);
+        case 3: return launch_router_t<3>(L, B, M, x, st);
+        case 4: return launch_router_t<4>(L, B, M, x, st);
+        case 5: return launch_router_t<5>(L, B, M, x, st);
+        case 6: return launch_router_t<6>(L, B, M, x, st);
+        case 8: return launch_router_t<8>(L, B, M, x, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -954,8 +801,14 @@ hipError_t launch_topk_plan(const LayerDev& L, const MoeBufs& B, int M, hipStrea
     return hipGetLastError();
 }
 
+int mfma_grid() {
+    init_grid();
+    return g_mfma_grid;
+}
+
 hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     init_grid();
+    if (moe_uses_narrow(L, M)) return launch_gate_up4(L, B, M, st);
     const int D = L.p[0].dim, BT = L.p[0].bits;
     if (moe_uses_mfma(L)) {
         const int nsub = L.H / D;
@@ -981,6 +834,7 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
 
 hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     init_grid();
+    if (moe_uses_narrow(L, M)) return launch_down4(L, B, M, st);
     const int D = L.p[2].dim, BT = L.p[2].bits;
     if (moe_uses_mfma(L)) {
         const int nsub = L.I / D;
@@ -1005,6 +859,41 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
     hipLaunchKernelGGL(k_combine, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
     return hipGetLastError();
+}
+
+hipError_t launch_xnorm(const uint16_t* h, int M, int H, float eps, uint16_t* x, uint16_t* x16, hipStream_t st) {
+    if (H % 256 || H / 4 > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_xnorm, dim3(M), dim3(H / 4), 0, st, h, H, eps, x, x16);
+    return hipGetLastError();
+}
+
+template <int KT>
+hipError_t launch_combine_norm_k(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, float eps, hipStream_t st) {
+    hipLaunchKernelGGL(k_combine_norm<KT>, dim3(M), dim3(L.H / 4), 0, st, L, B, M, h, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine_norm(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, float eps, hipStream_t st) {
+    if (L.H % 256 || L.H / 4 > 1024) return hipErrorInvalidValue;
+    switch (L.K) {
+        case 1: return launch_combine_norm_k<1>(L, B, M, h, eps, st);
+        case 2: return launch_combine_norm_k<2>(L, B, M, h, eps, st);
+        case 3: return launch_combine_norm_k<3>(L, B, M, h, eps, st);
+        case 4: return launch_combine_norm_k<4>(L, B, M, h, eps, st);
+        case 5: return launch_combine_norm_k<5>(L, B, M, h, eps, st);
+        case 6: return launch_combine_norm_k<6>(L, B, M, h, eps, st);
+        case 7: return launch_combine_norm_k<7>(L, B, M, h, eps, st);
+        case 8: return launch_combine_norm_k<8>(L, B, M, h, eps, st);
+        case 9: return launch_combine_norm_k<9>(L, B, M, h, eps, st);
+        case 10: return launch_combine_norm_k<10>(L, B, M, h, eps, st);
+        case 11: return launch_combine_norm_k<11>(L, B, M, h, eps, st);
+        case 12: return launch_combine_norm_k<12>(L, B, M, h, eps, st);
+        case 13: return launch_combine_norm_k<13>(L, B, M, h, eps, st);
+        case 14: return launch_combine_norm_k<14>(L, B, M, h, eps, st);
+        case 15: return launch_combine_norm_k<15>(L, B, M, h, eps, st);
+        case 16: return launch_combine_norm_k<16>(L, B, M, h, eps, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st) {

@@ -1,0 +1,289 @@
+// q38_moe_dev.hpp — device routines shared by the MoE kernels: DPP wave reductions, the
+// top-k routing + gather-by-expert plan (R2, R3), the plan accessors, codebook fills and
+// the SwiGLU rounding contract.
+#pragma once
+
+#include "q38_device.hpp"
+#include "q38_internal.hpp"
+
+namespace q38 {
+
+constexpr int kPlanInts = 2 + 4 * kMaxRows * kMaxTopK;
+
+// ============================================================== DPP wave reductions
+// Order-independent reductions (max) use DPP row operations and readlane; the summations
+// whose order is part of a contract keep the xor butterfly of q38_device.hpp.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xF,
+                                                             0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t max_step_u64(uint64_t k) {
+    const uint32_t h = dpp32<CTRL>(static_cast<uint32_t>(k >> 32));
+    const uint32_t l = dpp32<CTRL>(static_cast<uint32_t>(k));
+    const uint64_t o = (static_cast<uint64_t>(h) << 32) | l;
+    return o > k ? o : k;
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t k, int lane) {
+    const uint32_t h = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(k >> 32), lane));
+    const uint32_t l = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(k), lane));
+    return (static_cast<uint64_t>(h) << 32) | l;
+}
+// quad_perm(1,0,3,2), quad_perm(2,3,0,1), row_half_mirror, row_mirror, then rows via readlane.
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t k) {
+    k = max_step_u64<0xB1>(k);
+    k = max_step_u64<0x4E>(k);
+    k = max_step_u64<0x141>(k);
+    k = max_step_u64<0x140>(k);
+    uint64_t m = readlane_u64(k, 0);
+    const uint64_t a = readlane_u64(k, 16), b = readlane_u64(k, 32), c = readlane_u64(k, 48);
+    m = a > m ? a : m;
+    m = b > m ? b : m;
+    m = c > m ? c : m;
+    return m;
+}
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+    auto step = [](uint32_t x, uint32_t o) { return x > o ? x : o; };
+    v = step(v, dpp32<0xB1>(v));
+    v = step(v, dpp32<0x4E>(v));
+    v = step(v, dpp32<0x141>(v));
+    v = step(v, dpp32<0x140>(v));
+    uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0));
+    const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16));
+    const uint32_t b = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
+    const uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 48));
+    m = a > m ? a : m;
+    m = b > m ? b : m;
+    m = c > m ? c : m;
+    return m;
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    auto step = [](float x, uint32_t o) { return fmaxf(x, __uint_as_float(o)); };
+    v = step(v, dpp32<0xB1>(__float_as_uint(v)));
+    v = step(v, dpp32<0x4E>(__float_as_uint(v)));
+    v = step(v, dpp32<0x141>(__float_as_uint(v)));
+    v = step(v, dpp32<0x140>(__float_as_uint(v)));
+    float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48)));
+    return m;
+}
+
+// ============================================================== top-k + plan (R2, R3)
+// Block-level routine (any block of >= 256 threads). Wave w takes rows w, w + waves, ...:
+// lane l owns experts 64j + l as (p bits << 32 | ~index) keys; K rounds of a DPP wave max
+// pick (p desc, index asc). The plan is built by counting: route i lands at
+// #{routes (e, i') < (e_i, i)}; expert groups are marked with a ballot. The plan is left
+// in `plan` (LDS or global); `global_out` also receives experts and weights.
+struct TopkLds {
+    int32_t ex[kMaxRows * kMaxTopK];
+    int32_t sorted_e[kMaxRows * kMaxTopK];
+    int32_t wave_cnt[16];
+};
+
+// Logits of request row r, lane l holding experts 64j + l (j < NJ; E = 64 NJ when EXACT).
+template <int NJ, bool EXACT>
+__device__ __forceinline__ void topk_load_row_t(const LayerDev& L, const MoeBufs& B, int r, float* lg) {
+    const int lane = threadIdx.x & 63;
+    const int E = EXACT ? 64 * NJ : L.E, nj = E / 64;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) lg[j] = EXACT || j < nj ? B.logits[r * E + 64 * j + lane] : -INFINITY;
+}
+__device__ __forceinline__ void topk_load_row(const LayerDev& L, const MoeBufs& B, int r, float* lg) {
+    topk_load_row_t<16, false>(L, B, r, lg);
+}
+
+// Softmax (exp contract, double denominator) and top-k of one row by one wave, for
+// E <= 64 * NJ experts. Keys (p bits << 32 | ~index) are unique; each lane sorts its NJ keys
+// (bitonic network), then K rounds take the DPP wave maximum of the lane heads and the
+// winning lane advances its list, which yields the keys in (p desc, index asc) order.
+template <int NJ, bool EXACT>
+__device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
+                                                  TopkLds& t, bool global_out) {
+    const int lane = threadIdx.x & 63;
+    const int K = L.K, nj = EXACT ? NJ : L.E / 64;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) mx = fmaxf(mx, lg[j]);
+    mx = wave_max_dpp(mx);
+    double ds = 0.0;
+    float ev[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        ev[j] = 0.0f;
+        if (EXACT || j < nj) {
+            ev[j] = exp_contract(lg[j] - mx);
+            ds += static_cast<double>(ev[j]);
+        }
+    }
+    ds = wave_sum_xor(ds);
+    uint64_t key[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        key[j] = 0;
+        if (EXACT || j < nj) {
+            const float p = static_cast<float>(static_cast<double>(ev[j]) / ds);
+            key[j] = (static_cast<uint64_t>(__float_as_uint(p)) << 32) |
+                     static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(64 * j + lane));
+        }
+    }
+#pragma unroll
+    for (int k = 2; k <= NJ; k <<= 1) {
+#pragma unroll
+        for (int h = k >> 1; h > 0; h >>= 1) {
+#pragma unroll
+            for (int i = 0; i < NJ; ++i) {
+                const int m = i ^ h;
+                if (m > i) {
+                    const uint64_t x = key[i], y = key[m];
+                    const bool sw = (i & k) == 0 ? x < y : x > y;  // descending overall
+                    key[i] = sw ? y : x;
+                    key[m] = sw ? x : y;
+                }
+            }
+        }
+    }
+    // A round reduces the p word of the lane heads; the lanes holding the maximum are
+    // balloted and, only when several tie, the index word breaks the tie (largest ~index).
+    float psel = 0.0f, sum = 0.0f;
+    int isel = 0;
+    for (int s = 0; s < K; ++s) {
+        const uint32_t hi = static_cast<uint32_t>(key[0] >> 32), lo = static_cast<uint32_t>(key[0]);
+        const uint32_t mhi = wave_max_u32_dpp(hi);
+        uint64_t tie = __ballot(hi == mhi);
+        if (__popcll(tie) > 1) {
+            const uint32_t mlo = wave_max_u32_dpp(hi == mhi ? lo : 0u);
+            tie = __ballot(hi == mhi && lo == mlo);
+        }
+        const int win = __ffsll(static_cast<long long>(tie)) - 1;
+        const uint32_t wlo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), win));
+        if (lane == win) {
+#pragma unroll
+            for (int i = 0; i + 1 < NJ; ++i) key[i] = key[i + 1];
+            key[NJ - 1] = 0;
+        }
+        const float p = __uint_as_float(mhi);
+        sum += p;
+        if (lane == s) {
+            psel = p;
+            isel = static_cast<int>(0xFFFFFFFFu - wlo);
+        }
+    }
+    if (lane < K) {
+        t.ex[r * K + lane] = isel;
+        if (global_out) {
+            B.experts[r * K + lane] = isel;
+            B.weights[r * K + lane] = L.normalize ? psel / sum : psel;
+        }
+    }
+}
+__device__ __forceinline__ void topk_select_row(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
+                                                TopkLds& t, bool global_out) {
+    if (L.E <= 512) topk_select_row_t<8, false>(L, B, r, lg, t, global_out);
+    else topk_select_row_t<16, false>(L, B, r, lg, t, global_out);
+}
+
+// Gather-by-expert plan from t.ex (all rows selected); every thread of the block calls it.
+__device__ __forceinline__ void topk_build_plan(int M, int K, int32_t* plan, TopkLds& t) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int waves = blockDim.x >> 6;
+    const int MK = M * K;
+    __syncthreads();
+    if (tid < MK) {
+        const int my_e = t.ex[tid];
+        const int my_key = (my_e << 8) | tid;
+        int pos = 0;
+        for (int j = 0; j < MK; ++j) pos += ((t.ex[j] << 8) | j) < my_key;
+        t.sorted_e[pos] = my_e;
+        plan[2 + 2 * MK + pos] = tid;   // route_list
+        plan[2 + 3 * MK + tid] = pos;   // route_pos
+    }
+    __syncthreads();
+    const bool start = tid < MK && (tid == 0 || t.sorted_e[tid - 1] != t.sorted_e[tid]);
+    const uint64_t bal = __ballot(start);
+    if (lane == 0) t.wave_cnt[wave] = __popcll(bal);
+    __syncthreads();
+    int rank = __popcll(bal & ((1ull << lane) - 1ull));
+    for (int w = 0; w < wave; ++w) rank += t.wave_cnt[w];
+    if (start) {
+        plan[1 + rank] = t.sorted_e[tid];
+        plan[1 + MK + rank] = tid;
+    }
+    if (tid == 0) {
+        int nu = 0;
+        for (int w = 0; w < waves; ++w) nu += t.wave_cnt[w];
+        plan[0] = nu;
+        plan[1 + MK + nu] = MK;
+    }
+    __syncthreads();
+}
+
+// Rows are taken by waves [row_wave0, waves); the other waves may do unrelated work
+// (the MFMA gate/up kernel fills its codebook with them) before the first barrier.
+__device__ __forceinline__ void topk_plan_block(const LayerDev& L, const MoeBufs& B, int M, bool global_out, int32_t* plan,
+                                                TopkLds& t, int row_wave0) {
+    const int wave = threadIdx.x >> 6;
+    const int waves = blockDim.x >> 6;
+    for (int r = wave - row_wave0; wave >= row_wave0 && r < M; r += waves - row_wave0) {
+        float lg[16];
+        topk_load_row(L, B, r, lg);
+        topk_select_row(L, B, r, lg, t, global_out);
+    }
+    topk_build_plan(M, L.K, plan, t);
+}
+
+// Rows of unique-expert slot ui: the routed experts in ascending id, then the shared
+// expert (all M rows). Returns false for an empty slot.
+__device__ __forceinline__ bool slot_rows(const int32_t* plan, int M, int K, int has_shared, int ui, int E,
+                                          int* expert, int* n, int* first_pos) {
+    const int nu = plan[0];
+    const int MK = M * K;
+    if (ui < nu) {
+        *expert = plan[1 + ui];
+        const int a = plan[1 + MK + ui], b = plan[1 + MK + ui + 1];
+        *n = b - a;
+        *first_pos = a;
+        return true;
+    }
+    if (ui == nu && has_shared) {
+        *expert = E;
+        *n = M;
+        *first_pos = MK;
+        return true;
+    }
+    return false;
+}
+// The request row of the j-th route of slot ui.
+__device__ __forceinline__ int route_row(const int32_t* plan, int M, int K, int pos0, int j, bool shared) {
+    return shared ? j : plan[2 + 2 * M * K + pos0 + j] / K;
+}
+
+// Codebook chunk -> LDS by threads [0, nthreads): 16 loads in flight per thread.
+template <int KENT>
+__device__ __forceinline__ void fill_book(const uint16_t* src4, unsigned char* lds, int t, int nthreads) {
+    const uint4* src = reinterpret_cast<const uint4*>(src4);
+    uint4* dst = reinterpret_cast<uint4*>(lds);
+    constexpr int N = KENT / 2;  // uint4 entries
+    constexpr int G = 16;
+    int i = t;
+    for (; i + (G - 1) * nthreads < N; i += G * nthreads) {
+        uint4 v[G];
+#pragma unroll
+        for (int k = 0; k < G; ++k) v[k] = src[i + k * nthreads];
+#pragma unroll
+        for (int k = 0; k < G; ++k) dst[i + k * nthreads] = v[k];
+    }
+    for (; i < N; i += nthreads) dst[i] = src[i];
+}
+
+// SwiGLU with the reference's rounding points (src/vq_metal_kernels.hpp:589-595):
+// h = T(T(silu(T(g))) * T(u)).
+__device__ __forceinline__ float swiglu(float g, float u) {
+    const float gt = rbf(g);
+    const float s = rbf(gt / (1.0f + expf(-gt)));
+    return rbf(s * rbf(u));
+}
+
+} // namespace q38
