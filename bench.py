@@ -10,7 +10,8 @@ synthetic (seeded, random-init) and resident in HBM before timing.
 Also reported (in "config"): per-layer microseconds and HBM GB/s of the 48-layer MoE chain for
 M = 1..4 rows, the phase split of a profiled pass, and the roofline of the dominant kernel.
 The CPU baseline is the C++ oracle (oracle/q38_oracle.cpp) timed on this host's cores on a
-bounded sample (two MoE layers at M=4 and a 16384-row slice of the head), scaled to a round.
+bounded sample (as many MoE layers at M=4 as fit in --cpu-seconds, and a 65536-row slice of
+the head), scaled to a round.
 """
 from __future__ import annotations
 
@@ -41,7 +42,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="wall-time budget of the CPU baseline sample")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel from the host")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 256 MiB device copy (reference kernel for HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
@@ -195,34 +199,53 @@ def main():
                     "mean_unique_experts": float(np.mean(uniq)), "bytes_per_layer": nbytes / len(layers)}
         log(f"M={M}: {per_m[M]['layer_us']:.2f} us/layer, {per_m[M]['gbps']:.1f} GB/s, U={np.mean(uniq):.1f}")
 
-    # ---------------------------------------------------------------- profiled phases (M=4)
+    # ---------------------------------------------------------------- profiled kernels (M=4)
+    # Kernel-accurate times: the profiled chain launches each phase's kernel with start/stop
+    # events that carry the kernel's own begin and end (the interval a kernel trace reports).
     M = 4
     plans = [torch.empty(2 + 4 * M * K, dtype=torch.int32, device=dev) for _ in layers]
     tr = (q38.RouteOut * len(layers))(*[q38.routes(plan=p) for p in plans])
     toks = (C.c_uint32 * M)(*[11 + 7 * r for r in range(M)])
     q38.check(q38.lib.q38_embed_synthetic(SEED, toks, M, H, h.data_ptr(), sp))
     tm = q38.MoeTimings()
-    if chain_graphs:            # keep the GPU busy so the profiled launches queue up back to back
-        for _ in range(6):
-            chain_graphs[4].replay()
     q38.check(q38.lib.q38_verify_chain_profiled(larr, len(layers), h.data_ptr(), M, 1e-6, tr, ws.data_ptr(),
                                                 ws.numel(), C.byref(tm), sp))
     torch.cuda.synchronize()
     uniq = [int(p[0].item()) for p in plans]
-    gu_words, d_words = (H // 8 // 32) * 14, (I // 8 // 32) * 14
+    nl = len(layers)
+    MK = M * K
+    # algorithmic bytes per launch (per-expert figures of the packed layout: gate/up codes
+    # 2 x 512 rows x 448 B, down 2048 rows x 112 B, one fp16 scale per row; fp16 d8 codebooks)
     book = 16384 * 8 * 2
-    gu_bytes = sum((u + 1) * 2 * (I * gu_words * 4 + I * 2) + 2 * book + M * H * 2 + (M * K + M) * I * 2
-                   for u in uniq)
-    dn_bytes = sum((u + 1) * (H * d_words * 4 + H * 2) + book + (M * K + M) * (I + H) * 2 for u in uniq)
-    rt_bytes = len(layers) * (E * H * 2 + H * 2 + 2 * M * H * 2 + M * E * 4)
-    phases = {"gate_up": (tm.gate_up_ms, gu_bytes), "down": (tm.down_ms, dn_bytes),
-              "routing": (tm.routing_ms, rt_bytes)}
-    dom = max(phases, key=lambda k: phases[k][0])
-    dom_ms, dom_bytes = phases[dom]
-    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    log("profiled phases (ms over 48 layers): " + ", ".join(
-        f"{k}={v:.3f}" for k, v in (("routing", tm.routing_ms), ("gate_up", tm.gate_up_ms), ("down", tm.down_ms),
-                                    ("merge", tm.merge_ms))))
+    gu_bytes = sum((u + 1) * (2 * I * 448 + 2 * I * 2) + 2 * book + M * H * 2 + (MK + M) * I * 2 for u in uniq) / nl
+    dn_bytes = sum((u + 1) * (H * 112 + H * 2) + book + (MK + M) * I * 2 + M * H * 2 for u in uniq) / nl
+    rt_bytes = E * H * 2 + H * 2 + M * H * 2 + M * E * 4
+    mg_bytes = (MK + M) * H * 2 + 2 * M * H * 2 + M * H * 2 * 2
+    kernels = {"k_gu4 (gate/up, top-k, plan)": (tm.gate_up_ms, gu_bytes),
+               "k_dn4 (SwiGLU, down)": (tm.down_ms, dn_bytes),
+               "k_logits (router)": (tm.routing_ms, rt_bytes),
+               "k_combine_norm (reduce, residual, RMSNorm)": (tm.merge_ms, mg_bytes)}
+    dom = max(kernels, key=lambda k: kernels[k][0])
+    dom_us = 1e3 * kernels[dom][0] / nl
+    dom_bytes = kernels[dom][1]
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    log("kernel time per launch (us): " + ", ".join(f"{k.split()[0]}={1e3 * v[0] / nl:.2f}" for k, v in kernels.items()))
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_k_gu4_m4.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tj = json.load(f)
+        traffic = tj.get("hbm_bytes_per_launch")
+
+    if args.copy_calibration:
+        # a plain device copy of known size for the FETCH_SIZE / WRITE_SIZE calibration runs
+        nb = 256 << 20
+        src = torch.ones(nb // 4, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: 4 x {nb} bytes read and written")
 
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
@@ -234,10 +257,11 @@ def main():
         x = orc.rmsnorm(orc.embed(SEED, [11, 18, 25, 32], H))
         od = oracle_lib.make_desc()
         lay_s = []
-        for l in (0, 1):
-            _, sec = orc.moe_layer_synth_timed(od, SEED, l, x, threads)
+        t_start = time.perf_counter()
+        while len(lay_s) < 2 or time.perf_counter() - t_start < args.cpu_seconds:
+            _, sec = orc.moe_layer_synth_timed(od, SEED, len(lay_s) % LAYERS, x, threads)
             lay_s.append(sec)
-        nv = 16384
+        nv = 65536
         Wh = np.empty(nv * H, np.int8)
         orc.lib.orc_gen_int8(orc.key(SEED, 0xFFFE, 30), 0, nv * H, Wh.ctypes.data)
         sh = orc.uniform_f16(orc.key(SEED, 0xFFFE, 31), 0, nv, 1e-4, 1e-3)
@@ -246,9 +270,9 @@ def main():
         head_s = (time.perf_counter() - t0c) * V / nv
         round_s = LAYERS * float(np.mean(lay_s)) + head_s
         cpu = {"value": (mean_acc + 1) / round_s, "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"C++ oracle on {threads} host threads: 2 MoE layers at M=4 ({1e3 * np.mean(lay_s):.1f} ms/layer)"
-                         f" x48 + Q8 head on a {nv}-row slice scaled to {V} rows ({1e3 * head_s:.1f} ms); "
-                         f"same accepted-length mean as the GPU run"}
+               "sample": f"C++ oracle on {threads} host threads: {len(lay_s)} MoE layers at M=4 (layers 0.., "
+                         f"{1e3 * np.mean(lay_s):.1f} ms/layer arithmetic) x48 + Q8 head on a {nv}-row slice "
+                         f"scaled to {V} rows ({1e3 * head_s:.1f} ms); same accepted-length mean as the GPU run"}
         log(f"CPU baseline {cpu['value']:.3f} tok/s ({round_s * 1e3:.1f} ms/round on {threads} threads)")
 
     m4 = per_m[4]
@@ -276,13 +300,12 @@ def main():
             "moe_layer_us": {str(k): v["layer_us"] for k, v in per_m.items()},
             "moe_layer_gbps": {str(k): v["gbps"] for k, v in per_m.items()},
             "mean_unique_experts": {str(k): v["mean_unique_experts"] for k, v in per_m.items()},
-            "phase_ms_48_layers_m4": {"routing": tm.routing_ms, "gate_up": tm.gate_up_ms, "down": tm.down_ms,
-                                      "merge": tm.merge_ms},
+            "kernel_us_per_launch_m4": {k.split()[0]: 1e3 * v[0] / nl for k, v in kernels.items()},
+            "algorithmic_bytes_per_launch_m4": {k.split()[0]: v[1] for k, v in kernels.items()},
         },
-        "roofline": {"bound": "hbm", "kernel": f"k_{dom}" if dom != "routing" else "k_router+k_topk_plan",
-                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None, "launch_avg_us": 1e3 * dom_ms / len(layers),
-                     "algorithmic_bytes_per_launch": dom_bytes / len(layers)},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "launch_avg_us": dom_us,
+                     "algorithmic_bytes_per_launch": dom_bytes},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -137,13 +137,14 @@ int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h
                      void* stream);
 
 /* Phase timings of a profiled verify pass (MoeVerifyTimings, include/qwen38/sparse_moe.hpp:
- * 30-36), summed over layers, in milliseconds of device time between HIP events placed
- * around each launch (the events serialise the phases; use for attribution only). */
+ * 30-36), summed over layers, in milliseconds: the execution time of each phase's kernel,
+ * from start/stop events the runtime records at the kernel's own begin and end (the
+ * interval a kernel trace reports; launch gaps are not included). */
 typedef struct q38_moe_timings {
-    double routing_ms;   /* RMSNorm + router logits (+ top-k + plan on the grouped path) */
+    double routing_ms;   /* router logits kernel */
     double gate_up_ms;   /* gate/up projections (+ top-k + plan on the MFMA path) */
-    double down_ms;
-    double merge_ms;     /* ordered route reduction + shared gate + residual */
+    double down_ms;      /* down projection (+ SwiGLU on the narrow path) */
+    double merge_ms;     /* ordered route reduction + shared gate + residual + next RMSNorm */
     int32_t layers;
     int32_t reserved;
 } q38_moe_timings;

@@ -450,9 +450,12 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
     if (!tm) return fail(Q38_EINVAL, "q38_verify_chain_profiled: null timings");
     if (int rc = chain_check(layers, n_layers, h, rows, ws, ws_bytes)) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    std::vector<hipEvent_t> ev(static_cast<size_t>(n_layers) * 5, nullptr);
-    for (auto& e : ev) Q38_HIP(hipEventCreate(&e));
+    // per layer and phase (router, gate/up, down, combine): start/stop of the phase's kernel
+    std::vector<hipEvent_t> ev(static_cast<size_t>(n_layers) * 8, nullptr);
     int rc = Q38_OK;
+    for (auto& e : ev)
+        if (hipEventCreate(&e) != hipSuccess) rc = fail(Q38_EHIP, "hipEventCreate failed");
+    KernelTimer& kt = kernel_timer();
     for (int l = 0; l < n_layers && rc == Q38_OK; ++l) {
         MoeBufs w{};
         moe_ws(layers[l]->desc, rows, &w, ws);
@@ -460,26 +463,47 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
             rc = fail(Q38_EHIP, "verify chain: RMSNorm launch failed");
             break;
         }
-        rc = run_layer(layers[l], w, rows, w.x, eps, h, nullptr, traces ? &traces[l] : nullptr,
-                       &ev[static_cast<size_t>(l) * 5], st);
+        hipEvent_t* E = &ev[static_cast<size_t>(l) * 8];
+        const q38_moe_layer* L = layers[l];
+        hipError_t e = hipSuccess;
+        kt = {E[0], E[1]};
+        e = launch_router(L->dev, w, rows, w.x, st);
+        if (e == hipSuccess && !moe_uses_mfma(L->dev)) e = launch_topk_plan(L->dev, w, rows, st);
+        if (e == hipSuccess) {
+            kt = {E[2], E[3]};
+            e = launch_gate_up(L->dev, w, rows, st);
+        }
+        if (e == hipSuccess && traces)
+            if (copy_routes(L, rows, w, &traces[l], st) != Q38_OK) e = hipErrorUnknown;
+        if (e == hipSuccess) {
+            kt = {E[4], E[5]};
+            e = launch_down(L->dev, w, rows, st);
+        }
+        if (e == hipSuccess) {
+            kt = {E[6], E[7]};
+            e = launch_combine_norm(L->dev, w, rows, h, eps, st);
+        }
+        kt = {};
+        if (e != hipSuccess) rc = hip_fail(e, "profiled verify chain");
     }
     if (rc == Q38_OK) {
-        hipError_t e = hipEventSynchronize(ev.back());
+        hipError_t e = hipStreamSynchronize(st);
         q38_moe_timings t{};
         for (int l = 0; l < n_layers && e == hipSuccess; ++l) {
-            hipEvent_t* E = &ev[static_cast<size_t>(l) * 5];
+            hipEvent_t* E = &ev[static_cast<size_t>(l) * 8];
             float ms[4];
-            for (int i = 0; i < 4 && e == hipSuccess; ++i) e = hipEventElapsedTime(&ms[i], E[i], E[i + 1]);
+            for (int i = 0; i < 4 && e == hipSuccess; ++i) e = hipEventElapsedTime(&ms[i], E[2 * i], E[2 * i + 1]);
             t.routing_ms += ms[0];
             t.gate_up_ms += ms[1];
             t.down_ms += ms[2];
             t.merge_ms += ms[3];
         }
         t.layers = n_layers;
-        if (e != hipSuccess) rc = hip_fail(e, "profiled verify timings");
+        if (e != hipSuccess) rc = hip_fail(e, "profiled chain timing");
         else *tm = t;
     }
-    for (auto& x : ev) (void)hipEventDestroy(x);
+    for (auto& e : ev)
+        if (e) (void)hipEventDestroy(e);
     return rc;
 }
 

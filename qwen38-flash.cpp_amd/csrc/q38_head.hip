@@ -107,42 +107,55 @@ __global__ __launch_bounds__(256) void k_head_prep(const uint16_t* __restrict__ 
 // waves of a block take one tile each, and the four waves of a group split the tile's K
 // range into quarters. Lane (i = l % 16, q = l / 16) of wave wq loads, for step s, the 16
 // weight bytes of row i at columns wq * H/4 + 64 s + 16 q (the MFMA A operand, used as
-// loaded); B is the same columns of the request planes, from LDS in the layout
-// [plane][column / 16][row MR][16 bytes] (conflict-free: the 16 lanes of a row group read
-// 16 consecutive 16-byte chunks). The weights of the group's next tile are loaded before
-// the cross-wave reduction of the current one. Output lane (vocab 4q + r, request row i).
+// loaded); B is the same columns of the three request planes, the same for every tile, so
+// each lane holds its B operands in registers for the whole launch. The weights and row
+// scales of the group's next tile are loaded before the cross-wave reduction of the
+// current one. Output lane (vocab 4q + r, request row i).
 typedef int i4_t __attribute__((ext_vector_type(4)));
 
+// Two blocks per CU (2 waves per SIMD): room for the B operands in registers, and 8 tiles of
+// weight loads in flight per CU.
+constexpr int kHeadBlocksPerCu = 2;
+
 template <int NS, int MR, int TB>
-__global__ __launch_bounds__(256 * TB) void k_head_i8(HeadDev hd, int M, HeadWork w, float* __restrict__ out_logits) {
+__global__ __launch_bounds__(256 * TB) __attribute__((amdgpu_waves_per_eu(MR == 4 ? kHeadBlocksPerCu : 2)))
+void k_head_i8(HeadDev hd, int M, HeadWork w, float* __restrict__ out_logits) {
     constexpr int H = 256 * NS;
-    extern __shared__ __align__(16) int8_t hp[];  // [3][H/16][MR][16]
     __shared__ long long red[2][TB][4][4][MR][4];  // [buffer][group][wave][q][row][r]
     const int tid = threadIdx.x;
-    for (int c = tid; c < 3 * (H / 16) * MR; c += 256 * TB) {
-        const int p = c / ((H / 16) * MR), rem = c - p * ((H / 16) * MR), kc = rem / MR, j = rem % MR;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (j < M) v = *reinterpret_cast<const uint4*>(w.planes + (static_cast<size_t>(p) * M + j) * H + 16 * kc);
-        reinterpret_cast<uint4*>(hp)[c] = v;
-    }
-    __syncthreads();
     const int lane = tid & 63, wave = (tid >> 6) & 3, grp = tid >> 8, i16 = lane & 15, q = lane >> 4;
     const int jj = i16 < M ? i16 : 0;
-    const int8_t* bp = hp + ((wave * 4 * NS + q) * MR + jj) * 16;
-    constexpr int kPlane = H * MR;
     const int64_t V = hd.V;
     const int64_t tiles = (V + 15) / 16;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * TB;
     uint4 wv[NS];
+    uint16_t sv[4];  // raw fp16 row scales of vocab rows 4q + r of the tile
     auto load = [&](int64_t tt) {
         int64_t vr = tt * 16 + i16;
         if (vr >= V) vr = V - 1;  // ragged last tile: a valid row, never stored
         const uint4* src = reinterpret_cast<const uint4*>(hd.w + vr * H + wave * (H / 4)) + q;
 #pragma unroll
         for (int k = 0; k < NS; ++k) wv[k] = src[4 * k];
+        if (wave == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int64_t v = tt * 16 + 4 * q + r;
+                if (v >= V) v = V - 1;
+                sv[r] = hd.scales[v];
+            }
+        }
     };
     int64_t base = static_cast<int64_t>(blockIdx.x) * TB;
     if (base + grp < tiles) load(base + grp);
+    i4_t bq[NS][3];
+    {
+        const int8_t* pb = w.planes + static_cast<size_t>(jj) * H + wave * (H / 4) + 16 * q;
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+                bq[k][p] = *reinterpret_cast<const i4_t*>(pb + static_cast<size_t>(p) * M * H + 64 * k);
+    }
     const bool jact = i16 < M;
     const double hsc = jact ? static_cast<double>(w.hscale[i16]) * 0x1.0p-14 : 0.0;
     float* dst = out_logits ? out_logits : w.fast;
@@ -155,14 +168,15 @@ __global__ __launch_bounds__(256 * TB) void k_head_i8(HeadDev hd, int M, HeadWor
 #pragma unroll
             for (int k = 0; k < NS; ++k) {
                 const i4_t av = __builtin_bit_cast(i4_t, wv[k]);
-                const int8_t* b = bp + 64 * MR * k;
-                a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, *reinterpret_cast<const i4_t*>(b), a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, *reinterpret_cast<const i4_t*>(b + kPlane), a1, 0, 0, 0);
-                a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, *reinterpret_cast<const i4_t*>(b + 2 * kPlane), a2, 0,
-                                                           0, 0);
+                a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bq[k][0], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bq[k][1], a1, 0, 0, 0);
+                a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bq[k][2], a2, 0, 0, 0);
             }
-            if (t + stride < tiles) load(t + stride);
         }
+        uint16_t sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] = sv[r];
+        if (t < tiles && t + stride < tiles) load(t + stride);
         if (i16 < MR) {
 #pragma unroll
             for (int r = 0; r < 4; ++r)
@@ -177,8 +191,8 @@ __global__ __launch_bounds__(256 * TB) void k_head_i8(HeadDev hd, int M, HeadWor
                 if (v < V) {
                     const long long acc = (red[buf][grp][0][q][i16][r] + red[buf][grp][1][q][i16][r]) +
                                           (red[buf][grp][2][q][i16][r] + red[buf][grp][3][q][i16][r]);
-                    const float lg = static_cast<float>(static_cast<double>(h2f(hd.scales[v])) *
-                                                        (static_cast<double>(acc) * hsc));
+                    const float lg =
+                        static_cast<float>(static_cast<double>(h2f(sc[r])) * (static_cast<double>(acc) * hsc));
                     mx = fmaxf(mx, lg);
                     dst[static_cast<size_t>(i16) * V + v] = lg;
                 }
@@ -466,26 +480,13 @@ int cu_count() {
     return n;
 }
 
-template <int NS, int MR, int TB>
-constexpr size_t i8_lds() { return 3ull * MR * 256 * NS; }
-
-template <int NS, int MR, int TB>
-hipError_t set_i8_attr() {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&k_head_i8<NS, MR, TB>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(i8_lds<NS, MR, TB>()));
-}
-
-// Request rows <= 4: one tile per block, four blocks per CU. Up to 16 rows: two tiles per
-// block sharing the 16-row planes, one block per CU.
+// Request rows <= 4: one tile per block; up to 16 rows: two tiles per block (16-row B).
 template <int NS, int MR, int TB>
 hipError_t launch_i8_t(const HeadDev& hd, int M, const HeadWork& w, float* out, hipStream_t st) {
     const int64_t tiles = (hd.V + 15) / 16;
-    int64_t grid = static_cast<int64_t>(cu_count()) * (MR == 4 ? 4 : 1);
+    int64_t grid = static_cast<int64_t>(cu_count()) * (MR == 4 ? kHeadBlocksPerCu : 1);
     if (grid > (tiles + TB - 1) / TB) grid = (tiles + TB - 1) / TB;
-    constexpr size_t lds = i8_lds<NS, MR, TB>();
-    hipLaunchKernelGGL((k_head_i8<NS, MR, TB>), dim3(static_cast<unsigned>(grid)), dim3(256 * TB), lds, st, hd, M, w,
-                       out);
-    return hipGetLastError();
+    return launch(k_head_i8<NS, MR, TB>, dim3(static_cast<unsigned>(grid)), dim3(256 * TB), 0, st, hd, M, w, out);
 }
 hipError_t launch_i8(const HeadDev& hd, int M, const HeadWork& w, float* out, hipStream_t st) {
     const bool wide = M > 4;
@@ -503,13 +504,7 @@ hipError_t launch_q4_m(const HeadDev& hd, const uint16_t* h, float* out, hipStre
 }
 } // namespace
 
-hipError_t head_init_attrs() {
-    hipError_t e = hipSuccess;
-    for (hipError_t x : {set_i8_attr<4, 4, 1>(), set_i8_attr<4, 16, 2>(), set_i8_attr<8, 4, 1>(),
-                         set_i8_attr<8, 16, 2>(), set_i8_attr<10, 4, 1>(), set_i8_attr<10, 16, 2>()})
-        if (x != hipSuccess) e = x;
-    return e;
-}
+hipError_t head_init_attrs() { return hipSuccess; }
 
 hipError_t launch_head_greedy(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, uint32_t* argmax,
                               float* logit, hipStream_t st) {

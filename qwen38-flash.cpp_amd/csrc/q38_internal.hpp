@@ -2,10 +2,31 @@
 // the kernel translation units and the C ABI implementation.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace q38 {
+
+// Kernel timing for the profiled entry points: when start is set, the next launch made
+// through launch() records start/stop at the kernel's own begin and end (the interval a
+// kernel trace reports), then the timer is cleared. One timer per host thread.
+struct KernelTimer {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+KernelTimer& kernel_timer();
+
+template <typename F, typename... Args>
+hipError_t launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
+    KernelTimer& t = kernel_timer();
+    if (t.start) {
+        hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), st, t.start, t.stop, 0, args...);
+        t.start = t.stop = nullptr;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+    }
+    return hipGetLastError();
+}
 
 constexpr int kMaxRows = 16;   // verify rows per MoE call (4 slots x (1 + 3 drafts))
 constexpr int kMaxTopK = 16;

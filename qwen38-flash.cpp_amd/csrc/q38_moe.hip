@@ -713,8 +713,7 @@ template <int T>
 hipError_t launch_router_t(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st) {
     const int rows = L.E + (L.has_shared ? 1 : 0);
     const int waves = M < 4 ? M : 4;
-    hipLaunchKernelGGL(k_logits<T>, dim3(rows), dim3(64 * waves), 0, st, L, B, M, x);
-    return hipGetLastError();
+    return launch(k_logits<T>, dim3(rows), dim3(64 * waves), 0, st, L, B, M, x);
 }
 
 template <typename Kern>
@@ -732,8 +731,7 @@ hipError_t launch_gu_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStrea
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((k_gu_mfma<BITS, NSUB, NCHUNK>), dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
-    return hipGetLastError();
+    return launch(k_gu_mfma<BITS, NSUB, NCHUNK>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
 template <int BITS, int NSUB, int NCHUNK>
 hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
@@ -744,8 +742,7 @@ hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStr
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((k_down_mfma<BITS, NSUB, NCHUNK>), dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
-    return hipGetLastError();
+    return launch(k_down_mfma<BITS, NSUB, NCHUNK>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
 
 template <int D, int BITS, int LPR>
@@ -799,6 +796,11 @@ hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint1
 hipError_t launch_topk_plan(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     hipLaunchKernelGGL(k_topk_plan, dim3(1), dim3(1024), 0, st, L, B, M);
     return hipGetLastError();
+}
+
+KernelTimer& kernel_timer() {
+    static thread_local KernelTimer t;
+    return t;
 }
 
 int mfma_grid() {
@@ -857,8 +859,7 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
 }
 
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
-    hipLaunchKernelGGL(k_combine, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
-    return hipGetLastError();
+    return launch(k_combine, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
 }
 
 hipError_t launch_xnorm(const uint16_t* h, int M, int H, float eps, uint16_t* x, uint16_t* x16, hipStream_t st) {
@@ -869,8 +870,7 @@ hipError_t launch_xnorm(const uint16_t* h, int M, int H, float eps, uint16_t* x,
 
 template <int KT>
 hipError_t launch_combine_norm_k(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, float eps, hipStream_t st) {
-    hipLaunchKernelGGL(k_combine_norm<KT>, dim3(M), dim3(L.H / 4), 0, st, L, B, M, h, eps);
-    return hipGetLastError();
+    return launch(k_combine_norm<KT>, dim3(M), dim3(L.H / 4), 0, st, L, B, M, h, eps);
 }
 
 hipError_t launch_combine_norm(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, float eps, hipStream_t st) {

@@ -298,8 +298,7 @@ hipError_t launch_gu4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t 
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((k_gu4<BITS, NSUB, NCHUNK>), dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
-    return hipGetLastError();
+    return launch(k_gu4<BITS, NSUB, NCHUNK>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
 }
 template <int BITS, int NSUB, int NCHUNK>
 hipError_t launch_dn4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
@@ -311,8 +310,7 @@ hipError_t launch_dn4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t 
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((k_dn4<BITS, NSUB, NCHUNK>), dim3(mfma_grid()), dim3(512), lds, st, L, B, M);
-    return hipGetLastError();
+    return launch(k_dn4<BITS, NSUB, NCHUNK>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M);
 }
 } // namespace
 
