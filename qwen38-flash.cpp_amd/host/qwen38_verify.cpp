@@ -1,0 +1,383 @@
+// qwen38_verify.cpp — C++20 host interface of the verify round over the C ABI (q38.h).
+// Every device operation goes through libq38's HIP kernels; this file only orders them,
+// owns buffers and converts error codes to the reference's exception types.
+#include "qwen38_verify.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <mutex>
+#include <stdexcept>
+
+namespace qwen38 {
+namespace {
+
+void check(int rc, const char* what) {
+    if (rc == Q38_OK) return;
+    std::string msg = std::string(what) + ": " + q38_last_error();
+    if (rc == Q38_ERANGE) throw std::out_of_range(msg);
+    throw std::runtime_error(msg);
+}
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+std::size_t rows_of(const DeviceTensor& t, std::size_t hidden) {
+    const auto& s = t.shape();
+    if (t.dtype() != DType::bf16 || s.empty() || s.back() != hidden)
+        throw std::runtime_error("expected a bf16 tensor whose last dimension is the hidden size");
+    std::size_t rows = 1;
+    for (std::size_t i = 0; i + 1 < s.size(); ++i) rows *= s[i];
+    return rows;
+}
+
+std::mutex g_ws_mutex;  // lazily sized workspaces of logically const objects
+
+} // namespace
+
+// ------------------------------------------------------------------ Context / tensors
+Context::Context(int hip_device) {
+    check(q38_ctx_create(hip_device, &ctx_), "q38_ctx_create");
+    hipStream_t s = nullptr;
+    const hipError_t e = hipStreamCreate(&s);  // default priority
+    if (e != hipSuccess) {
+        q38_ctx_destroy(ctx_);
+        check_hip(e, "hipStreamCreate");
+    }
+    stream_ = s;
+}
+Context::~Context() {
+    if (stream_) (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
+    q38_ctx_destroy(ctx_);
+}
+void Context::synchronize() const { check_hip(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "sync"); }
+
+std::size_t dtype_size(DType t) noexcept {
+    switch (t) {
+        case DType::bf16:
+        case DType::f16: return 2;
+        default: return 4;
+    }
+}
+
+DeviceTensor::DeviceTensor(std::vector<std::size_t> shape, DType dtype) : shape_(std::move(shape)), dtype_(dtype) {
+    const std::size_t n = std::max<std::size_t>(nbytes(), 1);
+    void* p = nullptr;
+    check_hip(hipMalloc(&p, n), "hipMalloc");
+    buf_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
+}
+DeviceTensor DeviceTensor::share() const {
+    DeviceTensor t;
+    t.buf_ = buf_;
+    t.shape_ = shape_;
+    t.dtype_ = dtype_;
+    return t;
+}
+std::size_t DeviceTensor::numel() const noexcept {
+    std::size_t n = 1;
+    for (std::size_t d : shape_) n *= d;
+    return n;
+}
+void DeviceTensor::upload(const void* host, std::size_t bytes) {
+    if (bytes > nbytes()) throw std::runtime_error("upload larger than the tensor");
+    check_hip(hipMemcpy(data(), host, bytes, hipMemcpyHostToDevice), "upload");
+}
+void DeviceTensor::download(void* host, std::size_t bytes) const {
+    if (bytes > nbytes()) throw std::runtime_error("download larger than the tensor");
+    check_hip(hipMemcpy(host, data(), bytes, hipMemcpyDeviceToHost), "download");
+}
+
+// ------------------------------------------------------------------ SparseMoe
+static q38_moe_desc make_desc(std::size_t experts, std::size_t top_k, bool normalize, const MoeGeometry& g,
+                              std::size_t group) {
+    q38_moe_desc d{};
+    d.hidden = static_cast<int32_t>(g.hidden);
+    d.inter = static_cast<int32_t>(g.intermediate);
+    d.experts = static_cast<int32_t>(experts);
+    d.top_k = static_cast<int32_t>(top_k);
+    d.gu_dim = static_cast<int32_t>(g.gate_up_dimension);
+    d.gu_bits = static_cast<int32_t>(g.gate_up_bits);
+    d.down_dim = static_cast<int32_t>(g.down_dimension);
+    d.down_bits = static_cast<int32_t>(g.down_bits);
+    d.gu_group = static_cast<int32_t>(group ? group : g.hidden);
+    d.down_group = static_cast<int32_t>(group ? group : g.intermediate);
+    d.normalize_topk = normalize ? 1 : 0;
+    d.has_shared = g.shared_expert ? 1 : 0;
+    return d;
+}
+
+SparseMoe::SparseMoe(const Context& ctx, const q38_moe_weights& tensors, std::size_t expert_count,
+                     std::size_t experts_per_token, std::size_t quantization_bits,
+                     std::size_t quantization_group_size, bool normalize_topk_probability, const MoeGeometry& geometry)
+    : ctx_(&ctx) {
+    if (quantization_bits != geometry.gate_up_bits)
+        throw std::runtime_error("quantization_bits must equal the gate/up VQ code width");
+    desc_ = make_desc(expert_count, experts_per_token, normalize_topk_probability, geometry, quantization_group_size);
+    check(q38_moe_layer_create(ctx.handle(), &desc_, &tensors, &layer_), "SparseMoe");
+}
+SparseMoe::SparseMoe(const Context& ctx, std::uint64_t seed, int layer_index, std::size_t expert_count,
+                     std::size_t experts_per_token, bool normalize_topk_probability, const MoeGeometry& geometry)
+    : ctx_(&ctx) {
+    desc_ = make_desc(expert_count, experts_per_token, normalize_topk_probability, geometry, 0);
+    check(q38_moe_layer_create_synthetic(ctx.handle(), &desc_, seed, layer_index, &layer_), "SparseMoe");
+}
+SparseMoe::~SparseMoe() { q38_moe_layer_destroy(layer_); }
+SparseMoe::SparseMoe(SparseMoe&& o) noexcept
+    : ctx_(o.ctx_), layer_(o.layer_), desc_(o.desc_), workspace_(std::move(o.workspace_)) {
+    o.layer_ = nullptr;
+}
+SparseMoe& SparseMoe::operator=(SparseMoe&& o) noexcept {
+    if (this != &o) {
+        q38_moe_layer_destroy(layer_);
+        ctx_ = o.ctx_;
+        layer_ = o.layer_;
+        desc_ = o.desc_;
+        workspace_ = std::move(o.workspace_);
+        o.layer_ = nullptr;
+    }
+    return *this;
+}
+
+std::vector<RouterSelection> SparseMoe::route_decode_batch(const DeviceTensor& input) const {
+    const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
+    if (rows < 1 || rows > 16) throw std::runtime_error("route_decode: rows must be between 1 and 16");
+    const std::size_t k = experts_per_token();
+    DeviceTensor ex({rows * k}, DType::i32), wt({rows * k}, DType::f32);
+    {
+        std::lock_guard<std::mutex> lk(g_ws_mutex);
+        const std::size_t need = q38_moe_workspace_size(&desc_, 16);
+        if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
+    }
+    q38_route_out r{static_cast<int32_t*>(ex.data()), static_cast<float*>(wt.data()), nullptr, nullptr, nullptr};
+    check(q38_moe_route(layer_, static_cast<const uint16_t*>(input.data()), static_cast<int32_t>(rows), &r,
+                        workspace_.data(), workspace_.nbytes(), ctx_->stream()),
+          "route_decode");
+    ctx_->synchronize();
+    const auto e = ex.to_host<int32_t>();
+    const auto w = wt.to_host<float>();
+    std::vector<RouterSelection> out(rows);
+    for (std::size_t i = 0; i < rows; ++i) {
+        for (std::size_t s = 0; s < k; ++s) {
+            out[i].experts.push_back(static_cast<std::size_t>(e[i * k + s]));
+            out[i].weights.push_back(w[i * k + s]);
+        }
+    }
+    return out;
+}
+RouterSelection SparseMoe::route_decode(const DeviceTensor& input) const {
+    auto all = route_decode_batch(input);
+    if (all.size() != 1) throw std::runtime_error("route_decode expects one row");
+    return std::move(all.front());
+}
+
+DeviceTensor SparseMoe::forward_verify(const DeviceTensor& input) const {
+    const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
+    if (rows < 1 || rows > 16) throw std::runtime_error("forward_verify: rows must be between 1 and 16");
+    DeviceTensor out(input.shape(), DType::bf16);
+    {
+        std::lock_guard<std::mutex> lk(g_ws_mutex);
+        const std::size_t need = q38_moe_workspace_size(&desc_, 16);
+        if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
+    }
+    check(q38_moe_forward(layer_, static_cast<const uint16_t*>(input.data()), static_cast<int32_t>(rows),
+                          static_cast<uint16_t*>(out.data()), nullptr, workspace_.data(), workspace_.nbytes(),
+                          ctx_->stream()),
+          "forward_verify");
+    return out;
+}
+
+// ------------------------------------------------------------------ QwenModel (verify path)
+QwenModel::QwenModel(const Context& ctx, std::uint64_t seed, std::size_t layer_count, std::size_t vocab,
+                     const MoeGeometry& geometry, std::size_t expert_count, std::size_t experts_per_token,
+                     float rms_eps)
+    : ctx_(&ctx), geometry_(geometry), seed_(seed), vocab_(vocab), eps_(rms_eps) {
+    if (layer_count < 1) throw std::runtime_error("QwenModel needs at least one layer");
+    layers_.reserve(layer_count);
+    for (std::size_t l = 0; l < layer_count; ++l)
+        layers_.emplace_back(ctx, seed, static_cast<int>(l), expert_count, experts_per_token, true, geometry);
+    check(q38_head_create_synthetic(ctx.handle(), Q38_HEAD_Q8, static_cast<int64_t>(vocab),
+                                    static_cast<int32_t>(geometry.hidden), seed, &head_),
+          "LM head");
+    moe_ws_ = DeviceTensor({q38_moe_workspace_size(&layers_.front().desc(), 16)}, DType::u32);
+    head_ws_ = DeviceTensor({q38_head_workspace_size(head_, 16)}, DType::u32);
+    tokens_dev_ = DeviceTensor({16}, DType::u32);
+    h_ = DeviceTensor({16, geometry.hidden}, DType::bf16);
+}
+QwenModel::~QwenModel() { q38_head_destroy(head_); }
+
+void QwenModel::forward_verify_layer_major(std::span<const std::uint32_t> tokens, DeviceTensor& final_mixed,
+                                           std::vector<GreedyStep>& greedy, MoeVerifyTimings* timings) const {
+    const std::size_t rows = tokens.size();
+    if (rows < 1 || rows > 16) throw std::runtime_error("verify rows must be between 1 and 16");
+    for (std::uint32_t t : tokens)
+        if (t >= vocab_) throw std::runtime_error("token id outside the vocabulary");
+    void* st = ctx_->stream();
+    const auto H = static_cast<int32_t>(geometry_.hidden);
+    const auto n = static_cast<int32_t>(rows);
+    check_hip(hipMemcpyAsync(tokens_dev_.data(), tokens.data(), rows * 4, hipMemcpyHostToDevice,
+                             static_cast<hipStream_t>(st)),
+              "tokens");
+    check(q38_embed_synthetic_dev(seed_, static_cast<const uint32_t*>(tokens_dev_.data()), n, H,
+                                  static_cast<uint16_t*>(h_.data()), st),
+          "embedding");
+    std::vector<q38_moe_layer*> hs;
+    for (const SparseMoe& L : layers_) hs.push_back(L.handle());
+    if (timings) {
+        q38_moe_timings t{};
+        check(q38_verify_chain_profiled(hs.data(), static_cast<int32_t>(hs.size()), static_cast<uint16_t*>(h_.data()),
+                                        n, eps_, nullptr, moe_ws_.data(), moe_ws_.nbytes(), &t, st),
+              "verify chain");
+        *timings = MoeVerifyTimings{t.routing_ms, t.gate_up_ms, t.down_ms, 0.0, t.merge_ms};
+    } else {
+        check(q38_verify_chain(hs.data(), static_cast<int32_t>(hs.size()), static_cast<uint16_t*>(h_.data()), n, eps_,
+                               nullptr, moe_ws_.data(), moe_ws_.nbytes(), st),
+              "verify chain");
+    }
+    final_mixed = DeviceTensor({1, rows, geometry_.hidden}, DType::bf16);
+    check(q38_rmsnorm(static_cast<const uint16_t*>(h_.data()), n, H, eps_, static_cast<uint16_t*>(final_mixed.data()),
+                      st),
+          "final norm");
+    DeviceTensor am({rows}, DType::u32), lg({rows}, DType::f32);
+    check(q38_head_greedy(head_, static_cast<const uint16_t*>(final_mixed.data()), n, static_cast<uint32_t*>(am.data()),
+                          static_cast<float*>(lg.data()), head_ws_.data(), head_ws_.nbytes(), st),
+          "LM head");
+    ctx_->synchronize();
+    const auto a = am.to_host<uint32_t>();
+    const auto l = lg.to_host<float>();
+    greedy.resize(rows);
+    for (std::size_t i = 0; i < rows; ++i) greedy[i] = GreedyStep{a[i], l[i]};
+}
+
+// ------------------------------------------------------------------ decode state / verify / commit
+ModelDecodeState::ModelDecodeState(const QwenModel& model, std::size_t token_count, std::size_t max_rows) {
+    check(q38_slot_create(model.context().handle(), static_cast<int32_t>(model.hidden()),
+                          static_cast<int32_t>(max_rows), token_count, &slot_),
+          "decode state");
+}
+ModelDecodeState::~ModelDecodeState() { q38_slot_destroy(slot_); }
+std::size_t ModelDecodeState::token_count() const {
+    uint64_t tc = 0;
+    int32_t staged = 0, drafts = 0;
+    check(q38_slot_info(slot_, &tc, &staged, &drafts), "decode state");
+    return static_cast<std::size_t>(tc);
+}
+
+MtpTargetVerification verify_mtp_target_layer_major_reference(const QwenModel& model, std::uint32_t current_token,
+                                                               std::span<const std::uint32_t> drafts,
+                                                               ModelDecodeState& origin) {
+    if (drafts.empty()) throw std::runtime_error("MTP verification requires at least one draft");
+    std::vector<std::uint32_t> tokens;
+    tokens.reserve(drafts.size() + 1);
+    tokens.push_back(current_token);
+    tokens.insert(tokens.end(), drafts.begin(), drafts.end());
+    DeviceTensor final_mixed;
+    std::vector<GreedyStep> greedy;
+    model.forward_verify_layer_major(tokens, final_mixed, greedy);
+    const std::size_t base = origin.token_count();
+    check(q38_slot_stage(origin.slot(), static_cast<int32_t>(drafts.size()),
+                         static_cast<const uint16_t*>(final_mixed.data()), model.context().stream()),
+          "verification checkpoints");
+    MtpTargetVerification v;
+    v.draft_count = drafts.size();
+    v.origin = &origin;
+    const std::size_t H = model.hidden();
+    for (std::size_t i = 0; i < tokens.size(); ++i) {
+        MtpTargetVerifyRow row;
+        row.greedy = greedy[i];
+        row.final_mixed = DeviceTensor({1, 1, H}, DType::bf16);
+        check_hip(hipMemcpyAsync(row.final_mixed.data(), static_cast<const char*>(final_mixed.data()) + i * H * 2,
+                                 H * 2, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(model.context().stream())),
+                  "verification row");
+        row.state_after = base + i + 1;
+        v.rows.push_back(std::move(row));
+    }
+    model.context().synchronize();
+    return v;
+}
+
+void commit_mtp_target_verification(MtpTargetVerification&& verification, std::size_t accepted,
+                                    ModelDecodeState& destination) {
+    if (verification.rows.size() != verification.draft_count + 1)
+        throw std::runtime_error("MTP verification row count is invalid");
+    if (accepted > verification.draft_count)
+        throw std::runtime_error("MTP accepted count exceeds verified draft count");
+    if (verification.origin != &destination)
+        throw std::runtime_error("MTP verification belongs to another decode state");
+    check(q38_slot_commit(destination.slot(), static_cast<int64_t>(accepted), nullptr), "commit");
+    verification.rows.clear();
+    verification.draft_count = 0;
+}
+
+// ------------------------------------------------------------------ lifecycle (host, via the ABI)
+MtpCommitPlan plan_mtp_commit(std::size_t round_offset, std::size_t drafted, std::size_t accepted) {
+    uint64_t out[4] = {0, 0, 0, 0};
+    check(q38_plan_mtp_commit(round_offset, drafted, accepted, out), "plan_mtp_commit");
+    return MtpCommitPlan{static_cast<std::size_t>(out[0]), static_cast<std::size_t>(out[1]),
+                         static_cast<std::size_t>(out[2]), static_cast<std::size_t>(out[3])};
+}
+
+MtpGreedyDecision decide_mtp_greedy(std::span<const std::uint32_t> drafts,
+                                    std::span<const std::uint32_t> target_argmax_rows,
+                                    std::span<const std::uint32_t> stop_tokens) {
+    q38_greedy_decision d{};
+    check(q38_mtp_decide_greedy(drafts.data(), static_cast<int64_t>(drafts.size()), target_argmax_rows.data(),
+                                static_cast<int64_t>(target_argmax_rows.size()), stop_tokens.data(),
+                                static_cast<int64_t>(stop_tokens.size()), &d),
+          "decide_mtp_greedy");
+    return MtpGreedyDecision{static_cast<std::size_t>(d.accepted), static_cast<std::size_t>(d.correction_row),
+                             d.next_token};
+}
+
+std::size_t packed_vq_word_count(std::size_t code_count, std::size_t bits_per_code) {
+    const int64_t n = q38_packed_vq_word_count(static_cast<int64_t>(code_count), static_cast<int>(bits_per_code));
+    if (n < 0) check(static_cast<int>(n), "packed_vq_word_count");
+    return static_cast<std::size_t>(n);
+}
+std::uint32_t unpack_vq_code(std::span<const std::uint32_t> words, std::size_t code_index, std::size_t bits_per_code) {
+    uint32_t out = 0;
+    check(q38_unpack_vq_code(words.data(), static_cast<int64_t>(words.size()), static_cast<int64_t>(code_index),
+                             static_cast<int>(bits_per_code), &out),
+          "unpack_vq_code");
+    return out;
+}
+bool supports_segmented_vq(std::size_t dimension, std::size_t packed_bits) noexcept {
+    return q38_supports_segmented_vq(static_cast<int>(dimension), static_cast<int>(packed_bits)) != 0;
+}
+
+// ------------------------------------------------------------------ round
+MtpRoundStep run_greedy_external_draft_round_reference(const QwenModel& target, std::uint32_t current_token,
+                                                       std::size_t query_position, std::vector<std::uint32_t> drafts,
+                                                       ModelDecodeState& target_state,
+                                                       std::span<const std::uint32_t> stop_tokens) {
+    if (target_state.token_count() != query_position)
+        throw std::runtime_error("MTP target state is not at the query position");
+    const auto t0 = std::chrono::steady_clock::now();
+    MtpTargetVerification verification =
+        verify_mtp_target_layer_major_reference(target, current_token, drafts, target_state);
+    const auto t1 = std::chrono::steady_clock::now();
+    std::vector<std::uint32_t> target_rows;
+    target_rows.reserve(verification.rows.size());
+    for (const MtpTargetVerifyRow& row : verification.rows) target_rows.push_back(row.greedy.token);
+    const MtpGreedyDecision decision = decide_mtp_greedy(drafts, target_rows, stop_tokens);
+    commit_mtp_target_verification(std::move(verification), decision.accepted, target_state);
+    const std::size_t next_query_position = query_position + decision.accepted + 1;
+    if (target_state.token_count() != next_query_position)
+        throw std::runtime_error("MTP committed target length mismatch");
+    const auto t2 = std::chrono::steady_clock::now();
+    std::vector<std::uint32_t> emitted;
+    emitted.reserve(decision.accepted + 1);
+    for (std::size_t i = 0; i < decision.accepted; ++i) emitted.push_back(drafts[i]);
+    emitted.push_back(decision.next_token);
+    MtpRoundStep step;
+    step.emitted_tokens = std::move(emitted);
+    step.draft_tokens = std::move(drafts);
+    step.accepted = decision.accepted;
+    step.next_current_token = decision.next_token;
+    step.next_query_position = next_query_position;
+    step.verify_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    step.commit_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    return step;
+}
+
+} // namespace qwen38

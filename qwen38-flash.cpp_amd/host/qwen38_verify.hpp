@@ -1,0 +1,264 @@
+// qwen38_verify.hpp — C++20 host interface of the MI355X MTP verification round.
+//
+// It mirrors the reference's interfaces for this path (same names, argument meaning and
+// error behaviour) on top of the C ABI in include/q38.h:
+//   SparseMoe, RouterSelection, MoeVerifyTimings   include/qwen38/sparse_moe.hpp:12-36, 46-214
+//   GreedyStep                                     include/qwen38/model.hpp:24-27
+//   MtpTargetVerifyRow / MtpTargetVerification      include/qwen38/mtp_verifier.hpp:15-25
+//   verify_mtp_target_layer_major_reference,
+//   commit_mtp_target_verification                  include/qwen38/mtp_verifier.hpp:33-47
+//   MtpCommitPlan / plan_mtp_commit, MtpGreedyDecision / decide_mtp_greedy
+//                                                   include/qwen38/mtp_lifecycle.hpp:38-59
+//   MtpRoundStep / run_greedy_external_draft_round_reference
+//                                                   include/qwen38/mtp_runner.hpp:19-60
+// DeviceTensor (an owning HBM buffer with shape, dtype and stream) takes the place of
+// MlxArray. Errors are thrown as std::runtime_error (std::out_of_range for packed-code
+// lookups past the buffer); a failed validation leaves its arguments untouched.
+#pragma once
+
+#include "q38.h"
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <span>
+#include <string>
+#include <vector>
+
+namespace qwen38 {
+
+// ------------------------------------------------------------------ device plumbing
+class Context {
+public:
+    explicit Context(int hip_device = 0);
+    ~Context();
+    Context(const Context&) = delete;
+    Context& operator=(const Context&) = delete;
+    [[nodiscard]] q38_ctx* handle() const noexcept { return ctx_; }
+    [[nodiscard]] void* stream() const noexcept { return stream_; }  // hipStream_t
+    void synchronize() const;
+
+private:
+    q38_ctx* ctx_ = nullptr;
+    void* stream_ = nullptr;
+};
+
+enum class DType { bf16, f16, f32, i32, u32 };
+[[nodiscard]] std::size_t dtype_size(DType t) noexcept;
+
+// Owning device tensor. Move-only; share() hands out another owner of the same buffer
+// (as MlxArray::share does).
+class DeviceTensor {
+public:
+    DeviceTensor() = default;
+    DeviceTensor(std::vector<std::size_t> shape, DType dtype);
+    DeviceTensor(DeviceTensor&&) noexcept = default;
+    DeviceTensor& operator=(DeviceTensor&&) noexcept = default;
+    DeviceTensor(const DeviceTensor&) = delete;
+    DeviceTensor& operator=(const DeviceTensor&) = delete;
+
+    [[nodiscard]] DeviceTensor share() const;
+    [[nodiscard]] const std::vector<std::size_t>& shape() const noexcept { return shape_; }
+    [[nodiscard]] DType dtype() const noexcept { return dtype_; }
+    [[nodiscard]] std::size_t numel() const noexcept;
+    [[nodiscard]] std::size_t nbytes() const noexcept { return numel() * dtype_size(dtype_); }
+    [[nodiscard]] void* data() const noexcept { return buf_.get(); }
+    [[nodiscard]] bool empty() const noexcept { return !buf_; }
+
+    // Synchronous host transfers (the reference's readback points).
+    void upload(const void* host, std::size_t bytes);
+    void download(void* host, std::size_t bytes) const;
+    template <typename T>
+    [[nodiscard]] std::vector<T> to_host() const {
+        std::vector<T> out(nbytes() / sizeof(T));
+        download(out.data(), out.size() * sizeof(T));
+        return out;
+    }
+
+private:
+    std::shared_ptr<void> buf_;
+    std::vector<std::size_t> shape_;
+    DType dtype_ = DType::bf16;
+};
+
+// ------------------------------------------------------------------ sparse MoE
+struct RouterSelection {
+    std::vector<std::size_t> experts;
+    std::vector<float> weights;
+};
+
+struct MoeVerifyTimings {
+    double routing_ms{0.0};
+    double gate_up_ms{0.0};
+    double down_ms{0.0};
+    double shared_expert_ms{0.0};  // the shared expert runs inside the projection kernels
+    double merge_ms{0.0};
+};
+
+// VQ geometry of the projection tensors (the reference reads it from the checkpoint's
+// tensor shapes, src/sparse_moe.cpp:618-661).
+struct MoeGeometry {
+    std::size_t hidden{2048};
+    std::size_t intermediate{512};
+    std::size_t gate_up_dimension{8}, gate_up_bits{14};
+    std::size_t down_dimension{8}, down_bits{14};
+    bool shared_expert{true};
+};
+
+class SparseMoe final {
+public:
+    // Adopts device tensors in the reference layout. Arguments as SparseMoe's constructor
+    // (include/qwen38/sparse_moe.hpp:48-55): quantization_bits / quantization_group_size
+    // describe the scale groups along the input (group size == input: one scale per row).
+    SparseMoe(const Context& ctx, const q38_moe_weights& tensors, std::size_t expert_count,
+              std::size_t experts_per_token, std::size_t quantization_bits, std::size_t quantization_group_size,
+              bool normalize_topk_probability, const MoeGeometry& geometry = {});
+    // Seeded random-init layer generated on the device.
+    SparseMoe(const Context& ctx, std::uint64_t seed, int layer_index, std::size_t expert_count,
+              std::size_t experts_per_token, bool normalize_topk_probability, const MoeGeometry& geometry = {});
+    ~SparseMoe();
+    SparseMoe(SparseMoe&&) noexcept;
+    SparseMoe& operator=(SparseMoe&&) noexcept;
+    SparseMoe(const SparseMoe&) = delete;
+    SparseMoe& operator=(const SparseMoe&) = delete;
+
+    // input [1, S, H] bf16 (normalised). Selections per row, read back to the host.
+    [[nodiscard]] RouterSelection route_decode(const DeviceTensor& input) const;
+    [[nodiscard]] std::vector<RouterSelection> route_decode_batch(const DeviceTensor& input) const;
+    // forward_verify (src/sparse_moe.cpp:1953-2171): input [1, S, H] bf16, S in 1..16; output
+    // the same shape and dtype.
+    [[nodiscard]] DeviceTensor forward_verify(const DeviceTensor& input) const;
+
+    [[nodiscard]] q38_moe_layer* handle() const noexcept { return layer_; }
+    [[nodiscard]] const q38_moe_desc& desc() const noexcept { return desc_; }
+    [[nodiscard]] std::size_t experts_per_token() const noexcept { return static_cast<std::size_t>(desc_.top_k); }
+
+private:
+    const Context* ctx_ = nullptr;
+    q38_moe_layer* layer_ = nullptr;
+    q38_moe_desc desc_{};
+    mutable DeviceTensor workspace_;
+};
+
+// ------------------------------------------------------------------ verify model
+struct GreedyStep {
+    std::uint32_t token{0};
+    float logit{0.0F};
+};
+
+// The verify-path model: seeded embedding, a stack of SparseMoe layers applied as
+// h <- h + MoE(RMSNorm(h)), a final RMSNorm and the Q8 LM head (exact greedy argmax).
+class QwenModel final {
+public:
+    QwenModel(const Context& ctx, std::uint64_t seed, std::size_t layer_count, std::size_t vocab,
+              const MoeGeometry& geometry = {}, std::size_t expert_count = 512, std::size_t experts_per_token = 10,
+              float rms_eps = 1e-6F);
+    ~QwenModel();
+    QwenModel(const QwenModel&) = delete;
+    QwenModel& operator=(const QwenModel&) = delete;
+
+    [[nodiscard]] const Context& context() const noexcept { return *ctx_; }
+    [[nodiscard]] std::size_t hidden() const noexcept { return geometry_.hidden; }
+    [[nodiscard]] std::size_t vocab() const noexcept { return vocab_; }
+    [[nodiscard]] std::size_t layer_count() const noexcept { return layers_.size(); }
+
+    // Layer-major verify of the given tokens (rows 1..16): returns the final hidden rows
+    // (after the final RMSNorm) and each row's greedy step.
+    void forward_verify_layer_major(std::span<const std::uint32_t> tokens, DeviceTensor& final_mixed,
+                                    std::vector<GreedyStep>& greedy,
+                                    MoeVerifyTimings* timings = nullptr) const;
+
+private:
+    const Context* ctx_ = nullptr;
+    MoeGeometry geometry_;
+    std::uint64_t seed_ = 0;
+    std::size_t vocab_ = 0;
+    float eps_ = 1e-6F;
+    std::vector<SparseMoe> layers_;
+    q38_head* head_ = nullptr;
+    mutable DeviceTensor moe_ws_, head_ws_, tokens_dev_, h_;
+};
+
+// Per-request decode state of the verify path: the committed length and the committed
+// hidden row, with the verification rows as speculative checkpoints (a q38 slot).
+class ModelDecodeState final {
+public:
+    ModelDecodeState(const QwenModel& model, std::size_t token_count, std::size_t max_rows = 8);
+    ~ModelDecodeState();
+    ModelDecodeState(const ModelDecodeState&) = delete;
+    ModelDecodeState& operator=(const ModelDecodeState&) = delete;
+    [[nodiscard]] std::size_t token_count() const;
+    [[nodiscard]] q38_slot* slot() const noexcept { return slot_; }
+
+private:
+    q38_slot* slot_ = nullptr;
+};
+
+struct MtpTargetVerifyRow {
+    GreedyStep greedy;
+    DeviceTensor final_mixed;    // [1, 1, H] bf16 final hidden of the row
+    std::size_t state_after{0};  // token count of the state after this row
+};
+
+struct MtpTargetVerification {
+    std::size_t draft_count{0};
+    std::vector<MtpTargetVerifyRow> rows;
+    ModelDecodeState* origin = nullptr;  // the state whose slot holds the staged checkpoints
+};
+
+[[nodiscard]] MtpTargetVerification verify_mtp_target_layer_major_reference(const QwenModel& model,
+                                                                           std::uint32_t current_token,
+                                                                           std::span<const std::uint32_t> drafts,
+                                                                           ModelDecodeState& origin);
+
+// accepted = N keeps the checkpoint after current_token plus N accepted drafts. Consumes
+// all verification rows on success; validation failures leave verification and
+// destination intact.
+void commit_mtp_target_verification(MtpTargetVerification&& verification, std::size_t accepted,
+                                    ModelDecodeState& destination);
+
+// ------------------------------------------------------------------ lifecycle (host)
+struct MtpCommitPlan {
+    std::size_t truncate_head_to{0};
+    std::size_t target_rows_to_keep{0};
+    std::size_t stash_rows{0};
+    std::size_t committed_boundary{0};
+};
+[[nodiscard]] MtpCommitPlan plan_mtp_commit(std::size_t round_offset, std::size_t drafted, std::size_t accepted);
+
+struct MtpGreedyDecision {
+    std::size_t accepted{0};
+    std::size_t correction_row{0};
+    std::uint32_t next_token{0};
+};
+[[nodiscard]] MtpGreedyDecision decide_mtp_greedy(std::span<const std::uint32_t> drafts,
+                                                  std::span<const std::uint32_t> target_argmax_rows,
+                                                  std::span<const std::uint32_t> stop_tokens = {});
+
+// Packed-VQ geometry (src/quantization_geometry.cpp:37-67).
+[[nodiscard]] std::size_t packed_vq_word_count(std::size_t code_count, std::size_t bits_per_code);
+[[nodiscard]] std::uint32_t unpack_vq_code(std::span<const std::uint32_t> words, std::size_t code_index,
+                                           std::size_t bits_per_code);
+[[nodiscard]] bool supports_segmented_vq(std::size_t dimension, std::size_t packed_bits) noexcept;
+
+// ------------------------------------------------------------------ round
+struct MtpRoundStep {
+    std::vector<std::uint32_t> emitted_tokens;
+    std::vector<std::uint32_t> draft_tokens;
+    std::size_t accepted{0};
+    std::uint32_t next_current_token{0};
+    std::size_t next_query_position{0};
+    double verify_ms{0.0};
+    double commit_ms{0.0};
+};
+
+// One greedy round with externally proposed drafts: verify [current, drafts...], decide,
+// commit. current_token has been emitted but is not yet in target_state.
+[[nodiscard]] MtpRoundStep run_greedy_external_draft_round_reference(const QwenModel& target,
+                                                                     std::uint32_t current_token,
+                                                                     std::size_t query_position,
+                                                                     std::vector<std::uint32_t> drafts,
+                                                                     ModelDecodeState& target_state,
+                                                                     std::span<const std::uint32_t> stop_tokens = {});
+
+} // namespace qwen38

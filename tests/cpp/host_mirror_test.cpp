@@ -1,0 +1,170 @@
+// host_mirror_test.cpp — tests of the C++20 host interface (qwen38-flash.cpp_amd/host/),
+// written like the reference's own tests:
+//   host section   KATs restated from tests/quantization_geometry_test.cpp:48-84 and
+//                  tests/mtp_lifecycle_test.cpp:39-71, and the exception types of
+//                  include/qwen38/mtp_verifier.hpp:39-47 / quantization_geometry.hpp.
+//   --gpu section  a verify model on the device: SparseMoe routes and outputs through the
+//                  C++ interface equal the C ABI's, a verify + commit round keeps the
+//                  reference's lifecycle (rows = k + 1, accepted <= k, token_count =
+//                  q + accepted + 1, failed validation leaves state intact).
+// Prints one line per section and exits non-zero on the first failed check.
+#include "qwen38_verify.hpp"
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <stdexcept>
+#include <vector>
+
+#define CHECK(cond)                                                             \
+    do {                                                                        \
+        if (!(cond)) {                                                          \
+            std::fprintf(stderr, "check failed %s:%d: %s\n", __FILE__, __LINE__, #cond); \
+            std::exit(1);                                                       \
+        }                                                                       \
+    } while (0)
+
+template <typename E, typename F>
+bool throws(F&& f) {
+    try {
+        f();
+    } catch (const E&) {
+        return true;
+    } catch (...) {
+        return false;
+    }
+    return false;
+}
+
+static void host_tests() {
+    // packed-VQ geometry (tests/quantization_geometry_test.cpp:48-84)
+    constexpr std::size_t bits = 14;
+    std::vector<std::uint32_t> expected(67);
+    for (std::size_t i = 0; i < expected.size(); ++i) expected[i] = static_cast<std::uint32_t>((i * 997 + 17) & 0x3FFF);
+    std::vector<std::uint32_t> packed(qwen38::packed_vq_word_count(expected.size(), bits), 0);
+    for (std::size_t i = 0; i < expected.size(); ++i) {
+        const std::size_t off = (i % 32) * bits, word = (i / 32) * bits + off / 32, sh = off % 32;
+        const std::uint64_t v = static_cast<std::uint64_t>(expected[i]) << sh;
+        packed[word] |= static_cast<std::uint32_t>(v);
+        if (sh + bits > 32) packed[word + 1] |= static_cast<std::uint32_t>(v >> 32);
+    }
+    CHECK(packed.size() == 42);
+    for (std::size_t i = 0; i < expected.size(); ++i) CHECK(qwen38::unpack_vq_code(packed, i, bits) == expected[i]);
+    CHECK(throws<std::out_of_range>([&] {
+        (void)qwen38::unpack_vq_code(std::span<const std::uint32_t>(packed.data(), 13), 31, bits);
+    }));
+    std::vector<std::uint32_t> packed8(qwen38::packed_vq_word_count(160, 8));
+    for (std::size_t i = 0; i < 160; ++i)
+        packed8[i / 4] |= static_cast<std::uint32_t>((i * 17 + 255) % 256) << ((i % 4) * 8);
+    CHECK(packed8.size() == 40);
+    for (std::size_t i = 0; i < 160; ++i) CHECK(qwen38::unpack_vq_code(packed8, i, 8) == (i * 17 + 255) % 256);
+    CHECK(qwen38::supports_segmented_vq(8, 14) && qwen38::supports_segmented_vq(4, 8));
+
+    // lifecycle (tests/mtp_lifecycle_test.cpp:39-71)
+    const auto partial = qwen38::plan_mtp_commit(12, 3, 1);
+    CHECK(partial.truncate_head_to == 12 && partial.target_rows_to_keep == 2 && partial.stash_rows == 2 &&
+          partial.committed_boundary == 14);
+    CHECK(throws<std::runtime_error>([] { (void)qwen38::plan_mtp_commit(0, 1, 2); }));
+    const std::vector<std::uint32_t> drafts{10, 20, 30};
+    const auto zero = qwen38::decide_mtp_greedy(drafts, std::vector<std::uint32_t>{11, 20, 30, 40});
+    CHECK(zero.accepted == 0 && zero.correction_row == 0 && zero.next_token == 11);
+    const auto part = qwen38::decide_mtp_greedy(drafts, std::vector<std::uint32_t>{10, 20, 31, 40});
+    CHECK(part.accepted == 2 && part.correction_row == 2 && part.next_token == 31);
+    const auto full = qwen38::decide_mtp_greedy(drafts, std::vector<std::uint32_t>{10, 20, 30, 40});
+    CHECK(full.accepted == 3 && full.correction_row == 3 && full.next_token == 40);
+    const auto stopped = qwen38::decide_mtp_greedy(drafts, std::vector<std::uint32_t>{10, 20, 30, 40},
+                                                   std::vector<std::uint32_t>{20, 99});
+    CHECK(stopped.accepted == 1 && stopped.correction_row == 1 && stopped.next_token == 20);
+    CHECK(throws<std::runtime_error>(
+        [&] { (void)qwen38::decide_mtp_greedy(drafts, std::vector<std::uint32_t>{10, 20, 30}); }));
+    std::printf("host section: ok\n");
+}
+
+static void gpu_tests() {
+    qwen38::Context ctx(0);
+    const std::uint64_t seed = 0x51A5EED;
+    qwen38::MoeGeometry g;  // config-0 shapes
+    // one layer through the C++ interface against the C ABI on the same input
+    qwen38::SparseMoe moe(ctx, seed, 0, 512, 10, true, g);
+    qwen38::DeviceTensor x({1, 4, 2048}, qwen38::DType::bf16);
+    {
+        const std::uint32_t toks[4] = {1, 2, 3, 4};
+        qwen38::DeviceTensor h({4, 2048}, qwen38::DType::bf16);
+        CHECK(q38_embed_synthetic(seed, toks, 4, 2048, static_cast<uint16_t*>(h.data()), ctx.stream()) == Q38_OK);
+        CHECK(q38_rmsnorm(static_cast<const uint16_t*>(h.data()), 4, 2048, 1e-6F, static_cast<uint16_t*>(x.data()),
+                          ctx.stream()) == Q38_OK);
+        ctx.synchronize();
+    }
+    const auto sel = moe.route_decode_batch(x);
+    CHECK(sel.size() == 4);
+    std::vector<int32_t> ex(40);
+    {
+        qwen38::DeviceTensor ed({40}, qwen38::DType::i32), ws({q38_moe_workspace_size(&moe.desc(), 4)},
+                                                              qwen38::DType::u32);
+        q38_route_out r{static_cast<int32_t*>(ed.data()), nullptr, nullptr, nullptr, nullptr};
+        CHECK(q38_moe_route(moe.handle(), static_cast<const uint16_t*>(x.data()), 4, &r, ws.data(), ws.nbytes(),
+                            ctx.stream()) == Q38_OK);
+        ctx.synchronize();
+        ed.download(ex.data(), ex.size() * 4);
+    }
+    for (std::size_t r = 0; r < 4; ++r) {
+        CHECK(sel[r].experts.size() == 10 && sel[r].weights.size() == 10);
+        float wsum = 0.0F;
+        for (std::size_t s = 0; s < 10; ++s) {
+            CHECK(sel[r].experts[s] == static_cast<std::size_t>(ex[r * 10 + s]));
+            wsum += sel[r].weights[s];
+        }
+        CHECK(wsum > 0.999F && wsum < 1.001F);
+    }
+    const auto y1 = moe.forward_verify(x).to_host<std::uint16_t>();
+    const auto y2 = moe.forward_verify(x).to_host<std::uint16_t>();
+    CHECK(y1 == y2);  // deterministic
+    CHECK(throws<std::runtime_error>([&] {
+        qwen38::DeviceTensor bad({1, 17, 2048}, qwen38::DType::bf16);
+        (void)moe.forward_verify(bad);
+    }));
+
+    // verify round + commit lifecycle on a 2-layer model with a small vocabulary
+    qwen38::QwenModel model(ctx, seed, 2, 4096, g);
+    qwen38::ModelDecodeState state(model, 100);
+    const std::vector<std::uint32_t> drafts{7, 8, 9};
+    auto v = qwen38::verify_mtp_target_layer_major_reference(model, 5, drafts, state);
+    CHECK(v.draft_count == 3 && v.rows.size() == 4);
+    for (std::size_t i = 0; i < 4; ++i) CHECK(v.rows[i].state_after == 101 + i && v.rows[i].greedy.token < 4096);
+    // the same tokens through the model directly give the same greedy rows
+    qwen38::DeviceTensor fm;
+    std::vector<qwen38::GreedyStep> gs;
+    const std::vector<std::uint32_t> toks{5, 7, 8, 9};
+    model.forward_verify_layer_major(toks, fm, gs);
+    for (std::size_t i = 0; i < 4; ++i)
+        CHECK(gs[i].token == v.rows[i].greedy.token && gs[i].logit == v.rows[i].greedy.logit);
+    // validation failures leave the verification and the state intact
+    CHECK(throws<std::runtime_error>([&] { qwen38::commit_mtp_target_verification(std::move(v), 4, state); }));
+    CHECK(v.rows.size() == 4 && state.token_count() == 100);
+    qwen38::commit_mtp_target_verification(std::move(v), 2, state);
+    CHECK(v.rows.empty() && state.token_count() == 103);
+
+    // a full external-draft round with the target's own greedy continuation as drafts
+    const std::uint32_t cur = 11;
+    std::vector<std::uint32_t> greedy_drafts;
+    std::uint32_t prev = cur;
+    for (int i = 0; i < 3; ++i) {
+        qwen38::DeviceTensor f1;
+        std::vector<qwen38::GreedyStep> g1;
+        model.forward_verify_layer_major(std::vector<std::uint32_t>{prev}, f1, g1);
+        greedy_drafts.push_back(g1[0].token);
+        prev = g1[0].token;
+    }
+    const std::size_t q = state.token_count();
+    const auto step = qwen38::run_greedy_external_draft_round_reference(model, cur, q, greedy_drafts, state);
+    CHECK(step.emitted_tokens.size() == step.accepted + 1);
+    CHECK(step.next_query_position == q + step.accepted + 1 && state.token_count() == step.next_query_position);
+    CHECK(step.emitted_tokens.back() == step.next_current_token);
+    std::printf("gpu section: ok (accepted %zu of 3 self-drafts)\n", step.accepted);
+}
+
+int main(int argc, char** argv) {
+    host_tests();
+    if (argc > 1 && std::strcmp(argv[1], "--gpu") == 0) gpu_tests();
+    return 0;
+}
