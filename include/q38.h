@@ -78,6 +78,30 @@ typedef struct q38_moe_weights {
     const uint16_t* books[3];
 } q38_moe_weights;
 
+/* Device tensors of a mixed-geometry layer (desc->mixed = 1; hidden 2048, inter 512,
+ * one scale per output row). Expert e uses bank e % 2 at index e / 2; the shared expert
+ * (index E, even) is the last entry of bank 0.
+ *   bank 0 (even): codes_d4[p] [E/2+1, OUT_p, ceil(IN_p/4/32)*8] u32 (8-bit codes),
+ *                  scales_d4[p] [E/2+1, OUT_p] fp16, books_d4[p] [256, 4] fp16
+ *   bank 1 (odd):  codes_d8[p] [E/2, OUT_p, ceil(IN_p/8/32)*14] u32 (14-bit codes),
+ *                  scales_d8[p] [E/2, OUT_p] fp16, books_d8[p] [16384, 8] int8 with one
+ *                  fp16 scale per codebook, book_scales_d8[p] (value = q * scale)
+ * (the per-expert geometry of the reference's mixed VQ v2 layers, src/sparse_moe.cpp:
+ * 539-544, 2249-2258; INT8 codebooks as in SparseMoe::prepare_u8_codebook,
+ * src/sparse_moe.cpp:750-804, with one scale per codebook). */
+typedef struct q38_moe_mixed_weights {
+    const uint16_t* router;
+    const uint16_t* shared_gate;
+    const uint32_t* codes_d4[3];
+    const uint16_t* scales_d4[3];
+    const uint16_t* books_d4[3];
+    const uint32_t* codes_d8[3];
+    const uint16_t* scales_d8[3];
+    const int8_t* books_d8[3];
+    uint16_t book_scales_d8[3];
+    uint16_t reserved;
+} q38_moe_mixed_weights;
+
 /* Routing outputs (optional, device). */
 typedef struct q38_route_out {
     int32_t* experts;   /* [rows*k] ids in rank order                                  */
@@ -106,8 +130,11 @@ int q38_supports_segmented_vq(int dimension, int packed_bits);
  * Replaces SparseMoe (include/qwen38/sparse_moe.hpp:46-214). */
 int q38_moe_layer_create(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_weights* weights,
                          q38_moe_layer** out);
+/* Mixed-geometry layer (desc->mixed = 1) over caller-owned tensors. */
+int q38_moe_layer_create_mixed(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_mixed_weights* weights,
+                               q38_moe_layer** out);
 /* Library-owned synthetic layer: every tensor generated from (seed, layer_index) by the
- * counter-based generator, on the device. */
+ * counter-based generator, on the device (uniform or, with desc->mixed, mixed geometry). */
 int q38_moe_layer_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, uint64_t seed,
                                    int32_t layer_index, q38_moe_layer** out);
 void q38_moe_layer_destroy(q38_moe_layer* layer);

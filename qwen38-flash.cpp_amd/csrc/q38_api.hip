@@ -119,7 +119,14 @@ static int validate_desc(const q38_moe_desc* d) {
         return fail(Q38_EINVAL, "routed expert count must be a multiple of 64 in [64, 1024]");
     if (d->top_k < 1 || d->top_k > kMaxTopK || d->top_k > d->experts)
         return fail(Q38_EINVAL, "experts per token must be in [1, 16]");
-    if (d->mixed) return fail(Q38_EINVAL, "mixed VQ geometry is not supported by this build");
+    if (d->mixed) {
+        if (d->hidden != 2048 || d->inter != 512)
+            return fail(Q38_EINVAL, "mixed VQ layers need hidden 2048 and expert intermediate 512");
+        if (d->gu_group != d->hidden || d->down_group != d->inter)
+            return fail(Q38_EINVAL, "mixed VQ layers use one scale per output row");
+        if (d->experts % 2) return fail(Q38_EINVAL, "mixed VQ layers need an even expert count");
+        return Q38_OK;
+    }
     const int geo[2][2] = {{d->gu_dim, d->gu_bits}, {d->down_dim, d->down_bits}};
     for (auto& g : geo)
         if (!((g[0] == 8 && g[1] == 14) || (g[0] == 4 && g[1] == 8)))
@@ -228,10 +235,14 @@ static SynthLayout synth_layout(const q38_moe_desc& d) {
     return s;
 }
 
+static int create_synthetic_mixed(q38_ctx* ctx, const q38_moe_desc& d, uint64_t seed, int32_t layer_index,
+                                  q38_moe_layer** out);
+
 int q38_moe_layer_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, uint64_t seed, int32_t layer_index,
                                    q38_moe_layer** out) {
     if (!ctx || !out) return fail(Q38_EINVAL, "q38_moe_layer_create_synthetic: null argument");
     if (int rc = validate_desc(desc)) return rc;
+    if (desc->mixed) return create_synthetic_mixed(ctx, *desc, seed, layer_index, out);
     const q38_moe_desc& d = *desc;
     const SynthLayout s = synth_layout(d);
     char* base = nullptr;
@@ -258,7 +269,7 @@ int q38_moe_layer_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, uint6
         auto* scales = reinterpret_cast<uint16_t*>(base + s.scales[p]);
         e = launch_gen_normal(stream_key(seed, layer, tb[p]), (int64_t{1} << bits) * dim, 1.0, 1, book, st);
         if (e == hipSuccess)
-            e = launch_gen_codes(stream_key(seed, layer, tc[p]), 0, d.experts + 1, outd, in / dim, bits,
+            e = launch_gen_codes(stream_key(seed, layer, tc[p]), 0, 1, d.experts + 1, outd, in / dim, bits,
                                  static_cast<int>(words_for(in / dim, bits)), codes, st);
         if (e == hipSuccess)
             e = launch_gen_uniform_f16(stream_key(seed, layer, ts[p]), 0,
@@ -284,6 +295,146 @@ int q38_moe_layer_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, uint6
     return Q38_OK;
 }
 
+// ------------------------------------------------------------------ mixed geometry
+static float h2f_host(uint16_t h) {
+    _Float16 v;
+    std::memcpy(&v, &h, 2);
+    return static_cast<float>(v);
+}
+
+static void fill_dev_mixed(q38_moe_layer* L, const q38_moe_mixed_weights* w) {
+    const q38_moe_desc& d = L->desc;
+    LayerDev& v = L->dev;
+    v = LayerDev{};
+    v.router = w->router;
+    v.wsg = w->shared_gate;
+    v.H = d.hidden;
+    v.I = d.inter;
+    v.E = d.experts;
+    v.K = d.top_k;
+    v.normalize = d.normalize_topk;
+    v.has_shared = d.has_shared;
+    v.mixed = 1;
+    for (int p = 0; p < 3; ++p) {
+        const int in = p < 2 ? d.hidden : d.inter;
+        ProjDev a{};
+        a.codes = w->codes_d4[p];
+        a.scales = w->scales_d4[p];
+        a.book = w->books_d4[p];
+        a.words = static_cast<int>(words_for(in / 4, 8));
+        a.ngrp = 1;
+        a.dim = 4;
+        a.bits = 8;
+        ProjDev b{};
+        b.codes = w->codes_d8[p];
+        b.scales = w->scales_d8[p];
+        b.book_i8 = w->books_d8[p];
+        b.book_scale = h2f_host(w->book_scales_d8[p]);
+        b.words = static_cast<int>(words_for(in / 8, 14));
+        b.ngrp = 1;
+        b.dim = 8;
+        b.bits = 14;
+        v.pb[p][0] = a;
+        v.pb[p][1] = b;
+        v.p[p] = b;
+    }
+    v.gu_parts = v.d_parts = 1;
+}
+
+int q38_moe_layer_create_mixed(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_mixed_weights* w,
+                               q38_moe_layer** out) {
+    if (!ctx || !out || !w) return fail(Q38_EINVAL, "q38_moe_layer_create_mixed: null argument");
+    if (!desc || !desc->mixed) return fail(Q38_EINVAL, "q38_moe_layer_create_mixed: desc->mixed must be 1");
+    if (int rc = validate_desc(desc)) return rc;
+    if (!w->router || (desc->has_shared && !w->shared_gate))
+        return fail(Q38_EINVAL, "router / shared gate tensors are required");
+    for (int p = 0; p < 3; ++p)
+        if (!w->codes_d4[p] || !w->scales_d4[p] || !w->books_d4[p] || !w->codes_d8[p] || !w->scales_d8[p] ||
+            !w->books_d8[p])
+            return fail(Q38_EINVAL, "mixed layer tensors are required for all three projections");
+    auto* L = new q38_moe_layer{ctx, *desc, {}, nullptr, 0, nullptr};
+    fill_dev_mixed(L, w);
+    *out = L;
+    return Q38_OK;
+}
+
+static int create_synthetic_mixed(q38_ctx* ctx, const q38_moe_desc& d, uint64_t seed, int32_t layer_index,
+                                  q38_moe_layer** out) {
+    const int nA = d.experts / 2 + 1, nB = d.experts / 2;  // bank 0 holds the shared expert
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += align256(bytes);
+        return at;
+    };
+    const size_t o_router = take(static_cast<size_t>(d.experts) * d.hidden * 2), o_wsg = take(d.hidden * 2);
+    size_t o_bA[3], o_cA[3], o_sA[3], o_b16[3], o_bB[3], o_bs[3], o_cB[3], o_sB[3];
+    for (int p = 0; p < 3; ++p) {
+        const int in = p < 2 ? d.hidden : d.inter, outd = p < 2 ? d.inter : d.hidden;
+        o_bA[p] = take(256 * 4 * 2);
+        o_cA[p] = take(static_cast<size_t>(nA) * outd * words_for(in / 4, 8) * 4);
+        o_sA[p] = take(static_cast<size_t>(nA) * outd * 2);
+        o_b16[p] = take(16384 * 8 * 2);
+        o_bB[p] = take(16384 * 8);
+        o_bs[p] = take(2);
+        o_cB[p] = take(static_cast<size_t>(nB) * outd * words_for(in / 8, 14) * 4);
+        o_sB[p] = take(static_cast<size_t>(nB) * outd * 2);
+    }
+    char* base = nullptr;
+    if (hipMalloc(&base, off) != hipSuccess) return fail(Q38_ENOMEM, "hipMalloc failed for a synthetic layer");
+    const hipStream_t st = nullptr;
+    const uint64_t layer = static_cast<uint64_t>(layer_index);
+    q38_moe_mixed_weights w{};
+    w.router = reinterpret_cast<uint16_t*>(base + o_router);
+    w.shared_gate = reinterpret_cast<uint16_t*>(base + o_wsg);
+    hipError_t e = launch_gen_normal(stream_key(seed, layer, T_ROUTER), static_cast<int64_t>(d.experts) * d.hidden,
+                                     0.02, 0, const_cast<uint16_t*>(w.router), st);
+    if (e == hipSuccess)
+        e = launch_gen_normal(stream_key(seed, layer, T_WSG), d.hidden, 0.02, 0, const_cast<uint16_t*>(w.shared_gate),
+                              st);
+    const uint64_t tb[3] = {T_CB_GATE, T_CB_UP, T_CB_DOWN}, tb4[3] = {T_CB4_GATE, T_CB4_UP, T_CB4_DOWN};
+    const uint64_t tc[3] = {T_CODES_GATE, T_CODES_UP, T_CODES_DOWN};
+    const uint64_t ts[3] = {T_SCALE_GATE, T_SCALE_UP, T_SCALE_DOWN};
+    for (int p = 0; p < 3 && e == hipSuccess; ++p) {
+        const int in = p < 2 ? d.hidden : d.inter, outd = p < 2 ? d.inter : d.hidden;
+        auto* bA = reinterpret_cast<uint16_t*>(base + o_bA[p]);
+        auto* cA = reinterpret_cast<uint32_t*>(base + o_cA[p]);
+        auto* sA = reinterpret_cast<uint16_t*>(base + o_sA[p]);
+        auto* b16 = reinterpret_cast<uint16_t*>(base + o_b16[p]);
+        auto* bB = reinterpret_cast<int8_t*>(base + o_bB[p]);
+        auto* bs = reinterpret_cast<uint16_t*>(base + o_bs[p]);
+        auto* cB = reinterpret_cast<uint32_t*>(base + o_cB[p]);
+        auto* sB = reinterpret_cast<uint16_t*>(base + o_sB[p]);
+        e = launch_gen_normal(stream_key(seed, layer, tb4[p]), 256 * 4, 1.0, 1, bA, st);
+        if (e == hipSuccess) e = launch_gen_normal(stream_key(seed, layer, tb[p]), 16384 * 8, 1.0, 1, b16, st);
+        if (e == hipSuccess) e = launch_book_to_int8(b16, 16384 * 8, bB, bs, st);
+        if (e == hipSuccess)
+            e = launch_gen_codes(stream_key(seed, layer, tc[p]), 0, 2, nA, outd, in / 4, 8,
+                                 static_cast<int>(words_for(in / 4, 8)), cA, st);
+        if (e == hipSuccess)
+            e = launch_gen_codes(stream_key(seed, layer, tc[p]), 1, 2, nB, outd, in / 8, 14,
+                                 static_cast<int>(words_for(in / 8, 14)), cB, st);
+        if (e == hipSuccess) e = launch_gen_scales(stream_key(seed, layer, ts[p]), 0, 2, nA, outd, 0.005, 0.02, sA, st);
+        if (e == hipSuccess) e = launch_gen_scales(stream_key(seed, layer, ts[p]), 1, 2, nB, outd, 0.005, 0.02, sB, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(&w.book_scales_d8[p], bs, 2, hipMemcpyDeviceToHost, st);
+        w.codes_d4[p] = cA;
+        w.scales_d4[p] = sA;
+        w.books_d4[p] = bA;
+        w.codes_d8[p] = cB;
+        w.scales_d8[p] = sB;
+        w.books_d8[p] = bB;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        (void)hipFree(base);
+        return hip_fail(e, "synthetic mixed layer generation");
+    }
+    auto* L = new q38_moe_layer{ctx, d, {}, base, off, nullptr};
+    fill_dev_mixed(L, &w);
+    *out = L;
+    return Q38_OK;
+}
+
 void q38_moe_layer_destroy(q38_moe_layer* layer) {
     if (!layer) return;
     if (layer->owned) (void)hipFree(layer->owned);
@@ -293,6 +444,7 @@ void q38_moe_layer_destroy(q38_moe_layer* layer) {
 
 int q38_moe_layer_weights(const q38_moe_layer* L, q38_moe_weights* out) {
     if (!L || !out) return fail(Q38_EINVAL, "null argument");
+    if (L->dev.mixed) return fail(Q38_EINVAL, "a mixed layer has per-bank tensors (q38_moe_mixed_weights)");
     out->router = L->dev.router;
     out->shared_gate = L->dev.wsg;
     for (int p = 0; p < 3; ++p) {
@@ -306,6 +458,18 @@ int q38_moe_layer_weights(const q38_moe_layer* L, q38_moe_weights* out) {
 int64_t q38_moe_layer_bytes(const q38_moe_layer* L, int32_t n_unique, int32_t rows) {
     if (!L) return Q38_EINVAL;
     const LayerDev& v = L->dev;
+    if (v.mixed) {  // half the routed experts of each geometry on average; shared expert d4
+        int64_t pe[2] = {0, 0}, books = 0;
+        for (int b = 0; b < 2; ++b)
+            for (int p = 0; p < 3; ++p) {
+                const int outd = p < 2 ? v.I : v.H;
+                pe[b] += static_cast<int64_t>(outd) * v.pb[p][b].words * 4 + static_cast<int64_t>(outd) * 2;
+            }
+        books = 3 * (256 * 4 * 2 + 16384 * 8);
+        return static_cast<int64_t>(n_unique) * (pe[0] + pe[1]) / 2 + (v.has_shared ? pe[0] : 0) + books +
+               static_cast<int64_t>(v.E) * v.H * 2 + (v.has_shared ? v.H * 2 : 0) +
+               static_cast<int64_t>(2) * rows * v.H * 2;
+    }
     int64_t per_expert = 0, books = 0;
     for (int p = 0; p < 3; ++p) {
         const int outd = p < 2 ? v.I : v.H;

@@ -33,11 +33,13 @@ constexpr int kMaxTopK = 16;
 constexpr int kHeadCap = 256;  // exact-pass candidates kept per row before the full fallback
 
 struct ProjDev {
-    const uint32_t* codes;   // [E+1, OUT, words]
-    const uint16_t* scales;  // [E+1, OUT, ngrp] fp16
-    const uint16_t* book;    // [2^bits, dim] fp16
+    const uint32_t* codes;   // [experts, OUT, words]
+    const uint16_t* scales;  // [experts, OUT, ngrp] fp16
+    const uint16_t* book;    // [2^bits, dim] fp16 (null for an INT8 codebook)
     const uint16_t* book4;   // [dim/4, 2^bits, 4] fp16: the codebook split into 4-dim chunks
     int words, ngrp, dim, bits;
+    const int8_t* book_i8;   // [2^bits, dim] int8 codebook (value = q * book_scale), or null
+    float book_scale;
 };
 
 // Workspace views of one MoE call (rows <= kMaxRows).
@@ -64,6 +66,11 @@ struct LayerDev {
     ProjDev p[3];            // gate, up, down
     int H, I, E, K, normalize, has_shared;
     int gu_parts, d_parts;   // chunk planes written by the gate/up and down kernels (1 or 2)
+    // Mixed geometry: pb[p][0] holds the even experts (index e/2; the shared expert E is
+    // even) as d4/8-bit with an fp16 codebook, pb[p][1] the odd experts (index e/2) as
+    // d8/14-bit with an INT8 codebook.
+    int mixed;
+    ProjDev pb[3][2];
 };
 
 struct HeadDev {
@@ -96,8 +103,12 @@ hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t 
 int mfma_grid();  // persistent workgroups of the expert kernels (a multiple of 32)
 
 // generators
-hipError_t launch_gen_codes(uint64_t key, int e0, int n_experts, int out_dim, int nsub, int bits, int words,
-                            uint32_t* codes, hipStream_t st);
+// codes of experts e0, e0 + e_stride, ... (n_experts of them), stored contiguously
+hipError_t launch_gen_codes(uint64_t key, int e0, int e_stride, int n_experts, int out_dim, int nsub, int bits,
+                            int words, uint32_t* codes, hipStream_t st);
+// per-row scales of experts e0, e0 + e_stride, ...: out[i * out_dim + o] = uniform at (e * out_dim + o)
+hipError_t launch_gen_scales(uint64_t key, int e0, int e_stride, int n_experts, int out_dim, double lo, double hi,
+                             uint16_t* out, hipStream_t st);
 hipError_t launch_gen_uniform_f16(uint64_t key, int64_t idx0, int64_t n, double lo, double hi, uint16_t* out,
                                   hipStream_t st);
 hipError_t launch_gen_normal(uint64_t key, int64_t n, double sd, int f16, uint16_t* out, hipStream_t st);

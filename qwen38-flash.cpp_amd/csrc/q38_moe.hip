@@ -23,8 +23,8 @@
 namespace q38 {
 
 // ============================================================== generators
-__global__ void k_gen_codes(uint64_t key, int e0, int n_experts, int out_dim, int nsub, int bits, int words,
-                            uint32_t* __restrict__ codes) {
+__global__ void k_gen_codes(uint64_t key, int e0, int e_stride, int n_experts, int out_dim, int nsub, int bits,
+                            int words, uint32_t* __restrict__ codes) {
     // one thread per (expert, row, 32-code block)
     const int nblk = (nsub + 31) / 32;
     const int64_t total = static_cast<int64_t>(n_experts) * out_dim * nblk;
@@ -33,7 +33,7 @@ __global__ void k_gen_codes(uint64_t key, int e0, int n_experts, int out_dim, in
         const int blk = static_cast<int>(t % nblk);
         const int64_t row = t / nblk;  // local (expert, o)
         const int o = static_cast<int>(row % out_dim);
-        const int e = e0 + static_cast<int>(row / out_dim);
+        const int e = e0 + e_stride * static_cast<int>(row / out_dim);
         uint32_t w[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) w[i] = 0;
@@ -59,6 +59,16 @@ __global__ void k_gen_uniform_f16(uint64_t key, int64_t idx0, int64_t n, double 
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x)
         out[i] = f2h(uniform_f32(key, static_cast<uint64_t>(idx0 + i), lo, hi));
+}
+
+__global__ void k_gen_scales(uint64_t key, int e0, int e_stride, int n_experts, int out_dim, double lo, double hi,
+                             uint16_t* __restrict__ out) {
+    const int64_t n = static_cast<int64_t>(n_experts) * out_dim;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t e = e0 + static_cast<int64_t>(e_stride) * (i / out_dim);
+        out[i] = f2h(uniform_f32(key, static_cast<uint64_t>(e * out_dim + i % out_dim), lo, hi));
+    }
 }
 
 __global__ void k_gen_normal(uint64_t key, int64_t n, double sd, int f16, uint16_t* __restrict__ out) {
@@ -417,8 +427,17 @@ template <int D>
 struct Vec;
 template <>
 struct Vec<8> {
-    static __device__ __forceinline__ void load_book(const uint16_t* book, uint32_t code, float* v) {
-        const uint4 b = *reinterpret_cast<const uint4*>(book + code * 8);
+    // fp16 codebook, or INT8 codebook x one fp16 scale (value = q * scale, exact in float)
+    static __device__ __forceinline__ void load_book(const ProjDev& P, uint32_t code, float* v) {
+        if (P.book_i8) {
+            const uint2 b = *reinterpret_cast<const uint2*>(P.book_i8 + code * 8);
+            const uint32_t w[2] = {b.x, b.y};
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                v[i] = static_cast<float>(static_cast<int8_t>(w[i >> 2] >> (8 * (i & 3)))) * P.book_scale;
+            return;
+        }
+        const uint4 b = *reinterpret_cast<const uint4*>(P.book + code * 8);
         const uint32_t w[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -429,8 +448,8 @@ struct Vec<8> {
 };
 template <>
 struct Vec<4> {
-    static __device__ __forceinline__ void load_book(const uint16_t* book, uint32_t code, float* v) {
-        const uint2 b = *reinterpret_cast<const uint2*>(book + code * 4);
+    static __device__ __forceinline__ void load_book(const ProjDev& P, uint32_t code, float* v) {
+        const uint2 b = *reinterpret_cast<const uint2*>(P.book + code * 4);
         v[0] = h2f(static_cast<uint16_t>(b.x));
         v[1] = h2f(static_cast<uint16_t>(b.x >> 16));
         v[2] = h2f(static_cast<uint16_t>(b.y));
@@ -476,7 +495,7 @@ __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int I
                 const int s = s0 + qq;
                 const uint32_t c = code_from<BITS>(wr, qq);
                 float bk[D];
-                Vec<D>::load_book(P.book, c, bk);
+                Vec<D>::load_book(P, c, bk);
 #pragma unroll
                 for (int j = 0; j < MAXN; ++j)
                     if (j < n)
@@ -544,6 +563,56 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     grouped_rows<D, BITS, LPR, kMaxRows>(L.p[2], expert, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
                                          fin, n, B.d, pos0, wave, lane);
+}
+
+// Mixed geometry (even experts d4/8-bit fp16 books, odd experts d8/14-bit INT8 books):
+// the same per-slot kernels with the decoder chosen by the slot's expert (uniform per
+// block). LA / LB: lanes per row of the d4 and d8 geometries.
+template <int LA, int LB>
+__global__ __launch_bounds__(256) void k_gu_mixed(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) float fin[];  // [n][H]
+    int expert, n, pos0;
+    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
+    const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
+    const int H = L.H, I = L.I;
+    for (int i = threadIdx.x; i < n * H; i += 256) {
+        const int j = i / H, c = i % H;
+        fin[i] = bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]);
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int o_base = blockIdx.x * kGuRowsPerBlock;
+    const int idx = expert >> 1;
+    if ((expert & 1) == 0) {
+        grouped_rows<4, 8, LA, kMaxRows>(L.pb[0][0], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave, lane);
+        grouped_rows<4, 8, LA, kMaxRows>(L.pb[1][0], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave, lane);
+    } else {
+        grouped_rows<8, 14, LB, kMaxRows>(L.pb[0][1], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave,
+                                          lane);
+        grouped_rows<8, 14, LB, kMaxRows>(L.pb[1][1], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave,
+                                          lane);
+    }
+}
+
+template <int LA, int LB>
+__global__ __launch_bounds__(256) void k_down_mixed(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) float fin[];  // [n][I]
+    int expert, n, pos0;
+    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
+    const int H = L.H, I = L.I;
+    for (int i = threadIdx.x; i < n * I; i += 256) {
+        const size_t at = static_cast<size_t>(pos0) * I + i;
+        fin[i] = swiglu(B.g[at], B.u[at]);
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int idx = expert >> 1;
+    if ((expert & 1) == 0)
+        grouped_rows<4, 8, LA, kMaxRows>(L.pb[2][0], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
+                                         fin, n, B.d, pos0, wave, lane);
+    else
+        grouped_rows<8, 14, LB, kMaxRows>(L.pb[2][1], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
+                                          fin, n, B.d, pos0, wave, lane);
 }
 
 // ============================================================== combine (R8, R10, R11)
@@ -769,6 +838,7 @@ hipError_t launch_down_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hip
 } // namespace
 
 bool moe_uses_mfma(const LayerDev& L) {
+    if (L.mixed) return false;
     // MFMA tiles: per-row scales, 128-row tiles, and lane code spans of whole 16-code
     // half-blocks (gate/up: d8 with H/8 in {256, 320} or d4 with H/4 = 512; down: d8 with
     // I/8 = 64 or d4 with I/4 = 128).
@@ -810,6 +880,17 @@ int mfma_grid() {
 
 hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     init_grid();
+    if (L.mixed) {  // d4: H/4 = 512 subvectors -> 32 lanes per row; d8: 256 -> 16
+        if (L.H != 2048 || L.I != 512) return hipErrorInvalidValue;
+        static bool attr = false;
+        if (!attr) {
+            const hipError_t e = set_lds(&k_gu_mixed<32, 16>, 128 * 1024);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+        return launch(k_gu_mixed<32, 16>, dim3(L.I / kGuRowsPerBlock, M * L.K + 1), dim3(256),
+                      static_cast<size_t>(M) * L.H * 4, st, L, B, M);
+    }
     if (moe_uses_narrow(L, M)) return launch_gate_up4(L, B, M, st);
     const int D = L.p[0].dim, BT = L.p[0].bits;
     if (moe_uses_mfma(L)) {
@@ -836,6 +917,11 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
 
 hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     init_grid();
+    if (L.mixed) {  // d4: I/4 = 128 subvectors -> 8 lanes per row; d8: 64 -> 4
+        if (L.H != 2048 || L.I != 512) return hipErrorInvalidValue;
+        return launch(k_down_mixed<8, 4>, dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256),
+                      static_cast<size_t>(M) * L.I * 4, st, L, B, M);
+    }
     if (moe_uses_narrow(L, M)) return launch_down4(L, B, M, st);
     const int D = L.p[2].dim, BT = L.p[2].bits;
     if (moe_uses_mfma(L)) {
@@ -906,10 +992,15 @@ hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_
     return hipGetLastError();
 }
 
-hipError_t launch_gen_codes(uint64_t key, int e0, int n_experts, int out_dim, int nsub, int bits, int words,
-                            uint32_t* codes, hipStream_t st) {
-    hipLaunchKernelGGL(k_gen_codes, dim3(4096), dim3(256), 0, st, key, e0, n_experts, out_dim, nsub, bits, words,
-                       codes);
+hipError_t launch_gen_codes(uint64_t key, int e0, int e_stride, int n_experts, int out_dim, int nsub, int bits,
+                            int words, uint32_t* codes, hipStream_t st) {
+    hipLaunchKernelGGL(k_gen_codes, dim3(4096), dim3(256), 0, st, key, e0, e_stride, n_experts, out_dim, nsub, bits,
+                       words, codes);
+    return hipGetLastError();
+}
+hipError_t launch_gen_scales(uint64_t key, int e0, int e_stride, int n_experts, int out_dim, double lo, double hi,
+                             uint16_t* out, hipStream_t st) {
+    hipLaunchKernelGGL(k_gen_scales, dim3(2048), dim3(256), 0, st, key, e0, e_stride, n_experts, out_dim, lo, hi, out);
     return hipGetLastError();
 }
 hipError_t launch_gen_uniform_f16(uint64_t key, int64_t idx0, int64_t n, double lo, double hi, uint16_t* out,

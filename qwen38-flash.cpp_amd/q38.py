@@ -3,6 +3,10 @@
 This module is plumbing for tests and the benchmark: it loads the in-tree shared library
 and exposes the ABI's structs and functions. It has no fallback: if libq38.so is missing
 or fails to load, importing it raises.
+
+libq38.so links libamdhip64 by soname. A PyTorch build for ROCm carries its own copy: when
+both are used in one process, import torch first, so that the library binds to the runtime
+torch already loaded and the process holds a single HIP runtime.
 """
 from __future__ import annotations
 

@@ -110,3 +110,55 @@ def test_moe_layer_vs_numpy(orc):
     got = orc.bf16_to_f32(y).astype(np.float64)
     rel = np.linalg.norm(got - want) / np.linalg.norm(want)
     assert rel < 2e-3 and np.abs(got - want).max() < 2e-3, rel
+
+
+def test_mixed_layer_vs_numpy(orc):
+    """Mixed geometry (config 4): even experts (and the shared expert E) d4/8-bit with an
+    fp16 [256, 4] book, odd experts d8/14-bit with an INT8 [16384, 8] book and one fp16
+    scale per book (q = clamp(rint(v / s), -127, 127), value q * s). The oracle's synthetic
+    layer against a float64 numpy recomputation from the generator streams."""
+    H, I, E, k, seed, layer = 512, 128, 64, 4, 77, 3
+    desc = oracle_lib.make_desc(hidden=H, inter=I, experts=E, top_k=k, mixed=1)
+    K = lambda t: orc.key(seed, layer, t)
+    x = orc.bf16(np.random.default_rng(9).normal(0, 1, (2, H)))
+    y, ex, wt, lg = orc.moe_layer_synth(desc, seed, layer, x)
+    outs, ins = (I, I, H), (H, H, I)
+    book4 = [orc.normal(K(12 + p), 0, 256 * 4, 1.0, f16=True).view(np.float16).astype(np.float64).reshape(256, 4)
+             for p in range(3)]
+    book8 = []
+    for p in range(3):
+        v = orc.normal(K(3 + p), 0, 16384 * 8, 1.0, f16=True).view(np.float16).astype(np.float32)
+        s = np.float32(np.float16(np.abs(v).max() / np.float32(127)))
+        q = np.clip(np.rint(v / s), -127, 127)
+        assert q.min() >= -127 and q.max() <= 127 and np.abs(q).max() == 127
+        book8.append((q.astype(np.float64) * np.float64(s)).reshape(16384, 8))
+
+    def unpack_rows(words, n, bits):  # LSB-first 32-code blocks of `bits` words
+        i = np.arange(n)
+        bit = (i % 32) * bits
+        w = (i // 32) * bits + bit // 32
+        sh = (bit % 32).astype(np.uint64)
+        wp = np.concatenate([words, np.zeros((words.shape[0], 1), np.uint32)], 1).astype(np.uint64)
+        v = (wp[:, w] >> sh) | (wp[:, w + 1] << (np.uint64(32) - sh))
+        return (v & np.uint64((1 << bits) - 1)).astype(np.int64)
+
+    def dense(p, e):
+        d4 = e % 2 == 0
+        dim, bits, book = (4, 8, book4[p]) if d4 else (8, 14, book8[p])
+        codes = unpack_rows(orc.code_rows(K(6 + p), e, outs[p], 0, outs[p], ins[p] // dim, bits), ins[p] // dim, bits)
+        sc = orc.uniform_f16(K(9 + p), e * outs[p], outs[p], 0.005, 0.02).view(np.float16).astype(np.float64)
+        return book[codes].reshape(outs[p], -1) * sc[:, None]
+
+    wsg = orc.bf16_to_f32(orc.normal(K(2), 0, H, 0.02))
+    xf = orc.bf16_to_f32(x).astype(np.float64)
+    want = np.zeros((2, H))
+    for r in range(2):
+        routed = sum(wt[r, s] * np_expert(orc, dense(0, ex[r, s]), dense(1, ex[r, s]), dense(2, ex[r, s]), xf[r])
+                     for s in range(k))
+        sh_out = np_expert(orc, dense(0, E), dense(1, E), dense(2, E), xf[r])
+        g = rb(orc, 1 / (1 + np.exp(-rb(orc, xf[r] @ wsg))))
+        want[r] = rb(orc, rb(orc, routed) + rb(orc, sh_out * g))
+    assert {e % 2 for e in ex.reshape(-1)} == {0, 1}  # both geometries routed
+    got = orc.bf16_to_f32(y).astype(np.float64)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel < 2e-3 and np.abs(got - want).max() < 2e-3, rel
