@@ -142,18 +142,37 @@ void q38_moe_layer_destroy(q38_moe_layer* layer);
 int q38_moe_layer_weights(const q38_moe_layer* layer, q38_moe_weights* out);
 /* Algorithmic HBM bytes of one forward that touches n_unique routed experts. */
 int64_t q38_moe_layer_bytes(const q38_moe_layer* layer, int32_t n_unique, int32_t rows);
-/* Workspace bytes needed by q38_moe_forward / q38_verify_chain for up to max_rows rows. */
+/* Workspace bytes needed by q38_moe_forward / q38_verify_chain for up to max_rows rows
+ * (1..2048). */
 size_t q38_moe_workspace_size(const q38_moe_desc* desc, int32_t max_rows);
 
 /* Router only (R1-R3): SparseMoe::route_decode_batch (src/sparse_moe.cpp:1032-1086) and
- * the gather-by-expert plan (src/sparse_moe.cpp:2260-2364). x: device [rows, H] bf16. */
+ * the gather-by-expert plan (src/sparse_moe.cpp:2260-2364), rows 1..2048. x: device
+ * [rows, H] bf16. */
 int q38_moe_route(q38_moe_layer* layer, const uint16_t* x, int32_t rows, const q38_route_out* routes,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* SparseMoe::forward_verify (src/sparse_moe.cpp:1953-2171, 2199-2624): y = routed + shared
- * for rows 1..16 of x. x, y: device [rows, H] bf16 (may not alias). */
+/* SparseMoe::forward_verify / forward_prefill (src/sparse_moe.cpp:1953-2171, 2199-2624):
+ * y = routed + shared for rows 1..2048 of x. Rows 1..16 take the verify kernels; wider
+ * calls (SparseMoe::forward_prefill, include/qwen38/sparse_moe.hpp:68, S <= 2048) take the
+ * segmented-GEMM kernels, which need d8/14-bit projections with per-row scales and
+ * rows * top_k <= 32768. x, y: device [rows, H] bf16 (may not alias). */
 int q38_moe_forward(q38_moe_layer* layer, const uint16_t* x, int32_t rows, uint16_t* y,
                     const q38_route_out* routes, void* workspace, size_t workspace_bytes, void* stream);
+
+/* SparseMoe::forward_prefill_profiled (include/qwen38/sparse_moe.hpp:69-71) for rows
+ * 17..2048: the same call as q38_moe_forward, synchronised, with the execution time of each
+ * kernel in milliseconds: kernel_ms[7] = router logits, top-k, route plan, gate/up,
+ * SwiGLU, down, combine. */
+int q38_moe_forward_prefill_profiled(q38_moe_layer* layer, const uint16_t* x, int32_t rows, uint16_t* y,
+                                     const q38_route_out* routes, void* workspace, size_t workspace_bytes,
+                                     float* kernel_ms, void* stream);
+
+/* Additive router-logit bias: logits[r, e] = T(x_r . Wr_e) + bias[e] (float), before the
+ * softmax. bias: device [E] float kept by the layer (not copied), or null to clear. No
+ * counterpart in the reference: it is the hook a prefill benchmark uses to skew expert
+ * popularity (and a mask, with -inf entries). */
+int q38_moe_layer_set_router_bias(q38_moe_layer* layer, const float* bias);
 
 /* The verify pass through a stack of MoE layers (QwenModel::forward_verify_layer_major_
  * reference, src/model.cpp:386-441, with the HyperConnection/attention parts replaced by

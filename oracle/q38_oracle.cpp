@@ -357,15 +357,17 @@ void parallel_for(int n, int threads, F&& f) {
 // Rounding points: routed = T(sum_slot w_slot * T(down_slot)) in slot order (accumulated in
 // double here), shared = T(T(down_shared) * T(sigmoid(T(x . w_sg)))), y = T(routed + shared).
 int moe_layer(const Desc& d, LayerSource& src, const uint16_t* x, int M, uint16_t* y,
-              int32_t* experts_out, float* weights_out, float* logits_out, int threads) {
+              int32_t* experts_out, float* weights_out, float* logits_out, int threads,
+              const float* bias = nullptr) {
     const int H = d.hidden, E = d.experts, k = d.top_k;
     if (H % 512 != 0 || E % 64 != 0 || k < 1 || k > E || M < 1) return -1;
     const uint16_t* Wr = src.router();
     std::vector<float> logits(static_cast<size_t>(M) * E);
     parallel_for(E, threads, [&](int e) {
-        for (int r = 0; r < M; ++r)
-            logits[static_cast<size_t>(r) * E + e] =
-                rbf16(dot_contract(x + static_cast<size_t>(r) * H, Wr + static_cast<size_t>(e) * H, H));
+        for (int r = 0; r < M; ++r) {
+            const float lg = rbf16(dot_contract(x + static_cast<size_t>(r) * H, Wr + static_cast<size_t>(e) * H, H));
+            logits[static_cast<size_t>(r) * E + e] = bias ? lg + bias[e] : lg;
+        }
     });
     std::vector<int32_t> ex(static_cast<size_t>(M) * k);
     std::vector<float> wt(static_cast<size_t>(M) * k);
@@ -791,6 +793,12 @@ int orc_moe_layer_synth(const Desc* d, uint64_t seed, int layer, const uint16_t*
                         int32_t* experts, float* weights, float* logits, int threads) {
     SynthSource src(*d, seed, static_cast<uint64_t>(layer));
     return moe_layer(*d, src, x, M, y, experts, weights, logits, threads);
+}
+// orc_moe_layer_synth with an additive router-logit bias (float, added to the BF16 logit).
+int orc_moe_layer_synth_bias(const Desc* d, uint64_t seed, int layer, const uint16_t* x, int M, const float* bias,
+                             uint16_t* y, int32_t* experts, float* weights, float* logits, int threads) {
+    SynthSource src(*d, seed, static_cast<uint64_t>(layer));
+    return moe_layer(*d, src, x, M, y, experts, weights, logits, threads, bias);
 }
 // Same as orc_moe_layer_synth, but the tensors are materialised by an untimed first pass
 // and *seconds receives the wall time of a second, arithmetic-only pass (CPU baseline).

@@ -502,6 +502,7 @@ static size_t moe_ws(const q38_moe_desc& d, int M, MoeBufs* w, void* base) {
     t.g = reinterpret_cast<float*>(take(2 * gu * 4));
     t.u = reinterpret_cast<float*>(take(2 * gu * 4));
     t.d = reinterpret_cast<float*>(take(2 * dn * 4));
+    t.h16 = reinterpret_cast<uint16_t*>(take(gu * 2));
     t.gu_plane = gu;
     t.d_plane = dn;
     if (w) *w = t;
@@ -509,7 +510,7 @@ static size_t moe_ws(const q38_moe_desc& d, int M, MoeBufs* w, void* base) {
 }
 
 size_t q38_moe_workspace_size(const q38_moe_desc* desc, int32_t max_rows) {
-    if (!desc || max_rows < 1 || max_rows > kMaxRows) return 0;
+    if (!desc || max_rows < 1 || max_rows > kMaxPrefillRows) return 0;
     return moe_ws(*desc, max_rows, nullptr, nullptr);
 }
 
@@ -533,16 +534,65 @@ static int copy_routes(const q38_moe_layer* L, int M, const MoeBufs& w, const q3
     return Q38_OK;
 }
 
+// Rows beyond the verify width take the prefill kernels (one plane per projection).
+static int check_forward_rows(const q38_moe_layer* L, int rows) {
+    if (rows >= 1 && rows <= kMaxRows) return Q38_OK;
+    if (rows < 1 || rows > kMaxPrefillRows) return fail(Q38_EINVAL, "rows must be between 1 and 2048");
+    if (L->desc.top_k * rows > 32768) return fail(Q38_EINVAL, "rows x top_k must not exceed 32768");
+    if (!moe_supports_prefill(L->dev))
+        return fail(Q38_EINVAL, "prefill widths (rows > 16) need a d8/14-bit layer with per-row scales");
+    return Q38_OK;
+}
+
+static int route_prefill(const q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* x, hipStream_t st,
+                         hipEvent_t* ev) {
+    KernelTimer& kt = kernel_timer();
+    if (ev) kt = {ev[0], ev[1]};
+    Q38_HIP(launch_router_rows(L->dev, w, rows, x, st));
+    if (ev) kt = {ev[2], ev[3]};
+    Q38_HIP(launch_topk_rows(L->dev, w, rows, st));
+    if (ev) kt = {ev[4], ev[5]};
+    Q38_HIP(launch_plan_sort(L->dev, w, rows, st));
+    return Q38_OK;
+}
+
 int q38_moe_route(q38_moe_layer* L, const uint16_t* x, int32_t rows, const q38_route_out* routes, void* ws,
                   size_t ws_bytes, void* stream) {
     if (!L || !x) return fail(Q38_EINVAL, "q38_moe_route: null argument");
-    if (int rc = check_rows(rows)) return rc;
+    if (int rc = check_forward_rows(L, rows)) return rc;
     MoeBufs w{};
     if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    Q38_HIP(launch_router(L->dev, w, rows, x, st));
-    Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
+    if (rows > kMaxRows) {
+        if (int rc = route_prefill(L, w, rows, x, st, nullptr)) return rc;
+    } else {
+        Q38_HIP(launch_router(L->dev, w, rows, x, st));
+        Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
+    }
     return copy_routes(L, rows, w, routes, st);
+}
+
+// Prefill widths (SparseMoe::forward_prefill_impl, src/sparse_moe.cpp:2252-2505): logits,
+// top-k, sorted plan, segmented gate/up, SwiGLU, segmented down, combine. ev, when given,
+// holds 14 events: start/stop of each of the 7 kernels in that order.
+static int run_prefill(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* x, uint16_t* y,
+                       const q38_route_out* trace, hipEvent_t* ev, hipStream_t st) {
+    if (int rc = route_prefill(L, w, rows, x, st, ev)) return rc;
+    LayerDev one = L->dev;  // the prefill kernels write a single plane per projection
+    one.gu_parts = one.d_parts = 1;
+    KernelTimer& kt = kernel_timer();
+    if (ev) kt = {ev[6], ev[7]};
+    Q38_HIP(launch_gate_up_pf(one, w, rows, st));
+    if (trace)
+        if (int rc = copy_routes(L, rows, w, trace, st)) return rc;
+    if (ev) kt = {ev[8], ev[9]};
+    Q38_HIP(launch_swiglu_pf(one, w, rows, st));
+    if (ev) kt = {ev[10], ev[11]};
+    Q38_HIP(launch_down_pf(one, w, rows, st));
+    if (ev) kt = {ev[12], ev[13]};
+    Q38_HIP(launch_combine(one, w, rows, nullptr, y, st));
+    kt = {};
+    return Q38_OK;
 }
 
 // One layer: router logits, routing plan (fused into the MFMA gate/up kernel, a separate
@@ -573,10 +623,43 @@ int q38_moe_forward(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t*
                     void* ws, size_t ws_bytes, void* stream) {
     if (!L || !x || !y) return fail(Q38_EINVAL, "q38_moe_forward: null argument");
     if (x == y) return fail(Q38_EINVAL, "q38_moe_forward: input and output must not alias");
-    if (int rc = check_rows(rows)) return rc;
+    if (int rc = check_forward_rows(L, rows)) return rc;
     MoeBufs w{};
     if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
+    if (rows > kMaxRows) return run_prefill(L, w, rows, x, y, routes, nullptr, static_cast<hipStream_t>(stream));
     return run_layer(L, w, rows, x, 0.0f, nullptr, y, routes, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int q38_moe_forward_prefill_profiled(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t* y,
+                                     const q38_route_out* routes, void* ws, size_t ws_bytes, float* kernel_ms,
+                                     void* stream) {
+    if (!L || !x || !y || !kernel_ms) return fail(Q38_EINVAL, "q38_moe_forward_prefill_profiled: null argument");
+    if (x == y) return fail(Q38_EINVAL, "q38_moe_forward_prefill_profiled: input and output must not alias");
+    if (rows <= kMaxRows) return fail(Q38_EINVAL, "profiled prefill needs rows > 16");
+    if (int rc = check_forward_rows(L, rows)) return rc;
+    MoeBufs w{};
+    if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipEvent_t ev[14] = {};
+    int rc = Q38_OK;
+    for (auto& e : ev)
+        if (rc == Q38_OK && hipEventCreate(&e) != hipSuccess) rc = fail(Q38_EHIP, "hipEventCreate failed");
+    if (rc == Q38_OK) rc = run_prefill(L, w, rows, x, y, routes, ev, st);
+    kernel_timer() = {};
+    if (rc == Q38_OK) {
+        hipError_t e = hipStreamSynchronize(st);
+        for (int k = 0; k < 7 && e == hipSuccess; ++k) e = hipEventElapsedTime(&kernel_ms[k], ev[2 * k], ev[2 * k + 1]);
+        if (e != hipSuccess) rc = hip_fail(e, "profiled prefill timings");
+    }
+    for (auto& e : ev)
+        if (e) (void)hipEventDestroy(e);
+    return rc;
+}
+
+int q38_moe_layer_set_router_bias(q38_moe_layer* L, const float* bias) {
+    if (!L) return fail(Q38_EINVAL, "q38_moe_layer_set_router_bias: null layer");
+    L->dev.rbias = bias;
+    return Q38_OK;
 }
 
 static int chain_check(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows, void* ws,
@@ -686,8 +769,10 @@ int q38_embed_synthetic_dev(uint64_t seed, const uint32_t* tokens, int32_t n, in
 
 int q38_embed_synthetic(uint64_t seed, const uint32_t* tokens, int32_t n, int32_t hidden, uint16_t* h,
                         void* stream) {
-    if (!tokens || !h || n < 1 || n > 32 || hidden < 1) return fail(Q38_EINVAL, "q38_embed_synthetic: bad arguments");
-    Q38_HIP(launch_gen_embed(seed, tokens, n, hidden, h, static_cast<hipStream_t>(stream)));
+    if (!tokens || !h || n < 1 || hidden < 1) return fail(Q38_EINVAL, "q38_embed_synthetic: bad arguments");
+    for (int r = 0; r < n; r += 32)  // token ids travel as kernel arguments, 32 per launch
+        Q38_HIP(launch_gen_embed(seed, tokens + r, std::min(32, n - r), hidden, h + static_cast<size_t>(r) * hidden,
+                                 static_cast<hipStream_t>(stream)));
     return Q38_OK;
 }
 

@@ -29,6 +29,7 @@ hipError_t launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, A
 }
 
 constexpr int kMaxRows = 16;   // verify rows per MoE call (4 slots x (1 + 3 drafts))
+constexpr int kMaxPrefillRows = 2048;  // prefill-width rows per MoE call
 constexpr int kMaxTopK = 16;
 constexpr int kHeadCap = 256;  // exact-pass candidates kept per row before the full fallback
 
@@ -56,6 +57,7 @@ struct MoeBufs {
     float* g;          // [2][M*K + M, I] gate
     float* u;          // [2][M*K + M, I] up
     float* d;          // [2][M*K + M, H] down
+    uint16_t* h16;     // [M*K + M, I] fp16 SwiGLU rows (prefill path)
     size_t gu_plane;   // floats between the chunk planes of g and u
     size_t d_plane;    // floats between the chunk planes of d
 };
@@ -71,6 +73,7 @@ struct LayerDev {
     // d8/14-bit with an INT8 codebook.
     int mixed;
     ProjDev pb[3][2];
+    const float* rbias;      // [E] additive router-logit bias (device) or null
 };
 
 struct HeadDev {
@@ -101,6 +104,16 @@ bool moe_uses_narrow(const LayerDev& L, int M);
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 int mfma_grid();  // persistent workgroups of the expert kernels (a multiple of 32)
+// Prefill widths, kMaxRows < M <= kMaxPrefillRows (q38_moe_pf.hip), one kernel each:
+// router logits, per-row top-k, sorted plan, segmented gate/up, SwiGLU, segmented down
+// (gate/up/down write one plane each).
+bool moe_supports_prefill(const LayerDev& L);
+hipError_t launch_router_rows(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st);
+hipError_t launch_topk_rows(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+hipError_t launch_plan_sort(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+hipError_t launch_gate_up_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+hipError_t launch_swiglu_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+hipError_t launch_down_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 
 // generators
 // codes of experts e0, e0 + e_stride, ... (n_experts of them), stored contiguously

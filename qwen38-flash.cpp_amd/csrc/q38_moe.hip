@@ -129,7 +129,8 @@ __global__ void k_book_to_int8(const uint16_t* __restrict__ book16, int n, int8_
 // One workgroup per row of Wr (the last one: w_sg), one wave per request row (rows w,
 // w + waves, ...). x is the normalised layer input (bf16). Logit contract: lane l holds
 // the columns c = 512t + 8l + j and accumulates x*w over them (t outer, j inner) with
-// fmaf, then the xor butterfly and BF16 rounding. When x is not already the workspace
+// fmaf, then the xor butterfly and BF16 rounding; a router bias, when set, is added to the
+// rounded logit in float. When x is not already the workspace
 // copy, workgroup 0 stores it there (bf16) with its fp16 copy (the MFMA operand).
 template <int T>
 __global__ __launch_bounds__(256) void k_logits(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ x) {
@@ -159,7 +160,7 @@ __global__ __launch_bounds__(256) void k_logits(LayerDev L, MoeBufs B, int M, co
         const float sres = wave_sum_xor(acc);
         if (lane == 0) {
             if (e < L.E) {
-                B.logits[r * L.E + e] = rbf(sres);
+                B.logits[r * L.E + e] = L.rbias ? rbf(sres) + L.rbias[e] : rbf(sres);
             } else {
                 const float lg = rbf(sres);
                 B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));

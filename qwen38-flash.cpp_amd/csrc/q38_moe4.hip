@@ -107,7 +107,7 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
 #pragma unroll
         for (int t = 0; t < 32; ++t) xb[t] = *reinterpret_cast<const uint2*>(xr + t * 4 * NCHUNK);
     }
-    if (wave < M) topk_select_row_t<8, true>(L, B, wave, lg, tk, blockIdx.x == 0);
+    if (wave < M) topk_select_row_t<8, true>(L, B, wave, lg, tk.ex, blockIdx.x == 0);
     topk_build_plan(M, K, plan, tk);  // barriers on entry and exit
 
     const int tiles = I / 64;

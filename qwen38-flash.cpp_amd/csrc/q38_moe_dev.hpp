@@ -101,7 +101,7 @@ __device__ __forceinline__ void topk_load_row(const LayerDev& L, const MoeBufs& 
 // winning lane advances its list, which yields the keys in (p desc, index asc) order.
 template <int NJ, bool EXACT>
 __device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
-                                                  TopkLds& t, bool global_out) {
+                                                  int32_t* ex_lds, bool global_out) {
     const int lane = threadIdx.x & 63;
     const int K = L.K, nj = EXACT ? NJ : L.E / 64;
     float mx = -INFINITY;
@@ -172,7 +172,7 @@ __device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBu
         }
     }
     if (lane < K) {
-        t.ex[r * K + lane] = isel;
+        if (ex_lds) ex_lds[r * K + lane] = isel;
         if (global_out) {
             B.experts[r * K + lane] = isel;
             B.weights[r * K + lane] = L.normalize ? psel / sum : psel;
@@ -180,9 +180,9 @@ __device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBu
     }
 }
 __device__ __forceinline__ void topk_select_row(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
-                                                TopkLds& t, bool global_out) {
-    if (L.E <= 512) topk_select_row_t<8, false>(L, B, r, lg, t, global_out);
-    else topk_select_row_t<16, false>(L, B, r, lg, t, global_out);
+                                                int32_t* ex_lds, bool global_out) {
+    if (L.E <= 512) topk_select_row_t<8, false>(L, B, r, lg, ex_lds, global_out);
+    else topk_select_row_t<16, false>(L, B, r, lg, ex_lds, global_out);
 }
 
 // Gather-by-expert plan from t.ex (all rows selected); every thread of the block calls it.
@@ -229,7 +229,7 @@ __device__ __forceinline__ void topk_plan_block(const LayerDev& L, const MoeBufs
     for (int r = wave - row_wave0; wave >= row_wave0 && r < M; r += waves - row_wave0) {
         float lg[16];
         topk_load_row(L, B, r, lg);
-        topk_select_row(L, B, r, lg, t, global_out);
+        topk_select_row(L, B, r, lg, t.ex, global_out);
     }
     topk_build_plan(M, L.K, plan, t);
 }

@@ -187,6 +187,51 @@ DeviceTensor SparseMoe::forward_verify(const DeviceTensor& input) const {
     return out;
 }
 
+DeviceTensor SparseMoe::forward_prefill(const DeviceTensor& input) const {
+    const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
+    if (rows < 1 || rows > 2048) throw std::runtime_error("MoE prefill requires shape [1,S,hidden], S=1..2048");
+    DeviceTensor out(input.shape(), DType::bf16);
+    std::lock_guard<std::mutex> lk(g_ws_mutex);
+    const std::size_t need = q38_moe_workspace_size(&desc_, static_cast<int32_t>(rows));
+    if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
+    check(q38_moe_forward(layer_, static_cast<const uint16_t*>(input.data()), static_cast<int32_t>(rows),
+                          static_cast<uint16_t*>(out.data()), nullptr, workspace_.data(), workspace_.nbytes(),
+                          ctx_->stream()),
+          "forward_prefill");
+    return out;
+}
+
+DeviceTensor SparseMoe::forward_prefill_profiled(const DeviceTensor& input, MoePrefillTimings& timings) const {
+    const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
+    if (rows < 17 || rows > 2048) throw std::runtime_error("profiled MoE prefill requires S=17..2048");
+    DeviceTensor out(input.shape(), DType::bf16);
+    std::lock_guard<std::mutex> lk(g_ws_mutex);
+    const std::size_t need = q38_moe_workspace_size(&desc_, static_cast<int32_t>(rows));
+    if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
+    float ms[7] = {};
+    check(q38_moe_forward_prefill_profiled(layer_, static_cast<const uint16_t*>(input.data()),
+                                           static_cast<int32_t>(rows), static_cast<uint16_t*>(out.data()), nullptr,
+                                           workspace_.data(), workspace_.nbytes(), ms, ctx_->stream()),
+          "forward_prefill_profiled");
+    timings = MoePrefillTimings{};
+    timings.routing_ms = static_cast<double>(ms[0]) + ms[1] + ms[2];
+    timings.gate_up_ms = ms[3];
+    timings.swiglu_ms = ms[4];
+    timings.down_qmm_ms = ms[5];
+    timings.merge_ms = ms[6];
+    return out;
+}
+
+void SparseMoe::set_router_bias(const DeviceTensor& bias) {
+    if (bias.empty()) {
+        check(q38_moe_layer_set_router_bias(layer_, nullptr), "set_router_bias");
+        return;
+    }
+    if (bias.dtype() != DType::f32 || bias.numel() != static_cast<std::size_t>(desc_.experts))
+        throw std::runtime_error("router bias must be an f32 tensor of expert_count values");
+    check(q38_moe_layer_set_router_bias(layer_, static_cast<const float*>(bias.data())), "set_router_bias");
+}
+
 // ------------------------------------------------------------------ QwenModel (verify path)
 QwenModel::QwenModel(const Context& ctx, std::uint64_t seed, std::size_t layer_count, std::size_t vocab,
                      const MoeGeometry& geometry, std::size_t expert_count, std::size_t experts_per_token,

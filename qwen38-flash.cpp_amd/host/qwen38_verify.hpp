@@ -95,6 +95,23 @@ struct MoeVerifyTimings {
     double merge_ms{0.0};
 };
 
+// MoePrefillTimings (include/qwen38/sparse_moe.hpp:17-28): kernel execution times of one
+// prefill call in milliseconds. Gate and up run in one kernel (gate_up_ms; gate_qmm_ms and
+// up_qmm_ms stay 0), the down kernel reduces nothing (down_qmm_ms; down_reduce_ms 0), and
+// the route reduction, shared-expert gate and output form one kernel (merge_ms).
+struct MoePrefillTimings {
+    double routing_ms{0.0};
+    double gate_up_ms{0.0};
+    double gate_qmm_ms{0.0};
+    double up_qmm_ms{0.0};
+    double swiglu_ms{0.0};
+    double down_reduce_ms{0.0};
+    double down_qmm_ms{0.0};
+    double route_reduce_ms{0.0};
+    double shared_expert_ms{0.0};
+    double merge_ms{0.0};
+};
+
 // VQ geometry of the projection tensors (the reference reads it from the checkpoint's
 // tensor shapes, src/sparse_moe.cpp:618-661).
 struct MoeGeometry {
@@ -128,6 +145,14 @@ public:
     // forward_verify (src/sparse_moe.cpp:1953-2171): input [1, S, H] bf16, S in 1..16; output
     // the same shape and dtype.
     [[nodiscard]] DeviceTensor forward_verify(const DeviceTensor& input) const;
+    // forward_prefill (src/sparse_moe.cpp:2199-2624): input [1, S, H] bf16, S in 1..2048;
+    // S > 16 takes the segmented-GEMM kernels.
+    [[nodiscard]] DeviceTensor forward_prefill(const DeviceTensor& input) const;
+    // forward_prefill_profiled: the same for S in 17..2048, synchronised, with kernel times.
+    [[nodiscard]] DeviceTensor forward_prefill_profiled(const DeviceTensor& input, MoePrefillTimings& timings) const;
+    // Additive router-logit bias (device [E] float, kept by reference, or an empty tensor to
+    // clear): a benchmark hook with no counterpart in the reference.
+    void set_router_bias(const DeviceTensor& bias);
 
     [[nodiscard]] q38_moe_layer* handle() const noexcept { return layer_; }
     [[nodiscard]] const q38_moe_desc& desc() const noexcept { return desc_; }

@@ -123,6 +123,37 @@ static void gpu_tests() {
         qwen38::DeviceTensor bad({1, 17, 2048}, qwen38::DType::bf16);
         (void)moe.forward_verify(bad);
     }));
+    // prefill widths: S <= 16 is the verify call, S = 64 the segmented kernels, profiled or not
+    CHECK(moe.forward_prefill(x).to_host<std::uint16_t>() == y1);
+    {
+        std::vector<std::uint32_t> toks(64);
+        for (std::size_t i = 0; i < toks.size(); ++i) toks[i] = static_cast<std::uint32_t>(1000 + 7 * i);
+        qwen38::DeviceTensor h({64, 2048}, qwen38::DType::bf16), xp({1, 64, 2048}, qwen38::DType::bf16);
+        CHECK(q38_embed_synthetic(seed, toks.data(), 64, 2048, static_cast<uint16_t*>(h.data()), ctx.stream()) ==
+              Q38_OK);
+        CHECK(q38_rmsnorm(static_cast<const uint16_t*>(h.data()), 64, 2048, 1e-6F, static_cast<uint16_t*>(xp.data()),
+                          ctx.stream()) == Q38_OK);
+        const auto p1 = moe.forward_prefill(xp).to_host<std::uint16_t>();
+        qwen38::MoePrefillTimings t;
+        const auto p2 = moe.forward_prefill_profiled(xp, t).to_host<std::uint16_t>();
+        CHECK(p1 == p2 && p1.size() == 64 * 2048);
+        CHECK(t.routing_ms > 0.0 && t.gate_up_ms > 0.0 && t.swiglu_ms > 0.0 && t.down_qmm_ms > 0.0 && t.merge_ms > 0.0);
+        CHECK(throws<std::runtime_error>([&] { (void)moe.forward_prefill_profiled(x, t); }));
+        // a bias of +100 on experts 0..9 routes every row to exactly those experts
+        std::vector<float> b(512, 0.0F);
+        for (int e = 0; e < 10; ++e) b[e] = 100.0F;
+        qwen38::DeviceTensor bias({512}, qwen38::DType::f32);
+        bias.upload(b.data(), b.size() * 4);
+        moe.set_router_bias(bias);
+        for (const auto& s : moe.route_decode_batch(x))
+            for (std::size_t e : s.experts) CHECK(e < 10);
+        moe.set_router_bias(qwen38::DeviceTensor{});
+        CHECK(moe.forward_verify(x).to_host<std::uint16_t>() == y1);
+    }
+    CHECK(throws<std::runtime_error>([&] {
+        qwen38::DeviceTensor bad({1, 2049, 2048}, qwen38::DType::bf16);
+        (void)moe.forward_prefill(bad);
+    }));
 
     // verify round + commit lifecycle on a 2-layer model with a small vocabulary
     qwen38::QwenModel model(ctx, seed, 2, 4096, g);

@@ -60,6 +60,8 @@ class Oracle:
         sig("orc_route", None, P, C.c_int, C.c_int, C.c_int, C.c_int, P, P)
         sig("orc_route_plan", C.c_int, P, C.c_int, C.c_int, C.c_int, P, P, P, P, P)
         sig("orc_moe_layer_synth", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, P, P, C.c_int)
+        sig("orc_moe_layer_synth_bias", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, P, P, P,
+            C.c_int)
         sig("orc_moe_layer_synth_timed", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, C.c_int,
             C.POINTER(C.c_double))
         sig("orc_moe_layer_dense", C.c_int, C.POINTER(Desc), P, P, C.POINTER(P), C.POINTER(P), C.POINTER(P),
@@ -165,14 +167,22 @@ class Oracle:
         return n, uexp[:n], uoff[: n + 1], rl, rp
 
     # ---- MoE
-    def moe_layer_synth(self, d: Desc, seed, layer, x, threads=8):
+    def moe_layer_synth(self, d: Desc, seed, layer, x, threads=8, bias=None):
+        """Synthetic layer (seed, layer) on x; bias: optional [E] float32 router-logit bias."""
         x = np.ascontiguousarray(x, np.uint16)
         M = x.shape[0]
         y = np.empty_like(x)
         ex = np.empty((M, d.top_k), np.int32)
         wt = np.empty((M, d.top_k), np.float32)
         lg = np.empty((M, d.experts), np.float32)
-        rc = self.lib.orc_moe_layer_synth(C.byref(d), seed, layer, _a(x), M, _a(y), _a(ex), _a(wt), _a(lg), threads)
+        if bias is None:
+            rc = self.lib.orc_moe_layer_synth(C.byref(d), seed, layer, _a(x), M, _a(y), _a(ex), _a(wt), _a(lg),
+                                              threads)
+        else:
+            b = np.ascontiguousarray(bias, np.float32)
+            assert b.shape == (d.experts,)
+            rc = self.lib.orc_moe_layer_synth_bias(C.byref(d), seed, layer, _a(x), M, _a(b), _a(y), _a(ex), _a(wt),
+                                                   _a(lg), threads)
         assert rc == 0
         return y, ex, wt, lg
 

@@ -37,4 +37,6 @@ def test_workspace_sizes(q38):
     ws1 = q38.lib.q38_moe_workspace_size(C.byref(d), 1)
     ws4 = q38.lib.q38_moe_workspace_size(C.byref(d), 4)
     assert 0 < ws1 < ws4
-    assert q38.lib.q38_moe_workspace_size(C.byref(d), 17) == 0
+    ws512 = q38.lib.q38_moe_workspace_size(C.byref(d), 512)
+    assert ws4 < q38.lib.q38_moe_workspace_size(C.byref(d), 17) < ws512   # prefill widths
+    assert q38.lib.q38_moe_workspace_size(C.byref(d), 2049) == 0

@@ -111,3 +111,33 @@ def test_plan_closed_form(orc):
             assert (rp[members] == np.arange(uoff[u], uoff[u + 1])).all()
         # stable sort by expert id == the plan's route list
         assert rl.tolist() == sorted(range(M * 10), key=lambda i: (flat[i], i))
+
+
+def test_router_bias(orc):
+    """The additive router bias of the prefill workload: zero bias changes nothing, +100 on
+    ten experts selects exactly those, -inf masks an expert; logits = T(x.w) + bias."""
+    import oracle_lib
+    d = oracle_lib.make_desc(hidden=512, inter=128, experts=64, top_k=4)
+    x = orc.rmsnorm(orc.embed(5, list(range(6)), 512))
+    y0, ex0, wt0, lg0 = orc.moe_layer_synth(d, 9, 0, x)
+    y1, ex1, wt1, lg1 = orc.moe_layer_synth(d, 9, 0, x, bias=np.zeros(64, np.float32))
+    assert np.array_equal(lg0.view(np.uint32), lg1.view(np.uint32)) and np.array_equal(y0, y1)
+    b = np.zeros(64, np.float32)
+    hot = [3, 17, 40, 63]
+    b[hot] = 100.0
+    _, ex2, _, lg2 = orc.moe_layer_synth(d, 9, 0, x, bias=b)
+    assert all(sorted(r) == hot for r in ex2.tolist())
+    assert np.array_equal(lg2, lg0 + b)
+    m = np.zeros(64, np.float32)
+    m[ex0[:, 0]] = -np.inf
+    _, ex3, _, _ = orc.moe_layer_synth(d, 9, 0, x, bias=m)
+    assert not np.isin(ex3, ex0[:, 0]).any()
+
+
+def test_zipf_workload_shape():
+    """Zipf(1.1) bias: a permutation of -s tau ln(rank) over all experts."""
+    from workloads import zipf_router_bias
+    b = zipf_router_bias(512, 7)
+    assert b.dtype == np.float32 and b.shape == (512,)
+    assert np.allclose(np.sort(b)[::-1], -1.1 * 0.28 * np.log(np.arange(1, 513)), atol=1e-6)
+    assert np.array_equal(b, zipf_router_bias(512, 7)) and not np.array_equal(b, zipf_router_bias(512, 8))
