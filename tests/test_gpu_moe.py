@@ -97,8 +97,13 @@ def test_invalid_shapes_rejected(layer0, q38):
     ws = G.workspace(1 << 20)
     x = G.empty((17, 2048), np.uint16)
     y = G.empty((17, 2048), np.uint16)
+    # 17 rows is a prefill width: valid, but it needs a larger workspace
     rc = q38.lib.q38_moe_forward(layer0.h, x.data_ptr(), 17, y.data_ptr(), None, ws.data_ptr(), ws.numel(), G.stream())
-    assert rc == q38.Q38_EINVAL
+    assert rc == q38.Q38_ESPACE
+    for rows in (0, -1, 2049):
+        rc = q38.lib.q38_moe_forward(layer0.h, x.data_ptr(), rows, y.data_ptr(), None, ws.data_ptr(), ws.numel(),
+                                     G.stream())
+        assert rc == q38.Q38_EINVAL
     rc = q38.lib.q38_moe_forward(layer0.h, x.data_ptr(), 4, y.data_ptr(), None, ws.data_ptr(), 16, G.stream())
     assert rc == q38.Q38_ESPACE
     rc = q38.lib.q38_moe_forward(layer0.h, x.data_ptr(), 4, x.data_ptr(), None, ws.data_ptr(), ws.numel(), G.stream())
