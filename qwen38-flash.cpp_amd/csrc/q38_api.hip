@@ -566,7 +566,7 @@ int q38_moe_route(q38_moe_layer* L, const uint16_t* x, int32_t rows, const q38_r
     if (rows > kMaxRows) {
         if (int rc = route_prefill(L, w, rows, x, st, nullptr)) return rc;
     } else {
-        Q38_HIP(launch_router(L->dev, w, rows, x, st));
+        Q38_HIP(launch_router(L->dev, w, rows, x, false, 0.0f, st));
         Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
     }
     return copy_routes(L, rows, w, routes, st);
@@ -595,16 +595,15 @@ static int run_prefill(q38_moe_layer* L, const MoeBufs& w, int rows, const uint1
     return Q38_OK;
 }
 
-// One layer: router logits, routing plan (fused into the MFMA gate/up kernel, a separate
-// kernel otherwise), gate/up, down, combine. Chain mode (h_chain): x_in is the workspace
-// copy B.x formed by k_xnorm (first layer) or by the previous layer's combine, and the
-// combine adds the residual to h_chain in place and forms the next layer's input;
-// otherwise y receives the layer output. ev, when given, holds 5 events recorded around
-// the phases.
-static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* x_in, float eps,
+// One layer: router logits (with the layer-input RMSNorm of h when norm is set), routing
+// plan (fused into the MFMA gate/up kernels, a separate kernel otherwise), gate/up, down,
+// combine. Chain mode (h_chain): src is h_chain, and the combine adds the residual to it in
+// place; otherwise src is x and y receives the layer output. ev, when given, holds 5
+// events recorded around the phases.
+static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* src, bool norm, float eps,
                      uint16_t* h_chain, uint16_t* y, const q38_route_out* trace, hipEvent_t* ev, hipStream_t st) {
     if (ev) Q38_HIP(hipEventRecord(ev[0], st));
-    Q38_HIP(launch_router(L->dev, w, rows, x_in, st));
+    Q38_HIP(launch_router(L->dev, w, rows, src, norm, eps, st));
     if (!moe_uses_mfma(L->dev)) Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[1], st));
     Q38_HIP(launch_gate_up(L->dev, w, rows, st));
@@ -613,8 +612,7 @@ static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_
         if (int rc = copy_routes(L, rows, w, trace, st)) return rc;
     Q38_HIP(launch_down(L->dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[3], st));
-    if (h_chain) Q38_HIP(launch_combine_norm(L->dev, w, rows, h_chain, eps, st));
-    else Q38_HIP(launch_combine(L->dev, w, rows, nullptr, y, st));
+    Q38_HIP(launch_combine(L->dev, w, rows, h_chain, y, st));
     if (ev) Q38_HIP(hipEventRecord(ev[4], st));
     return Q38_OK;
 }
@@ -627,7 +625,7 @@ int q38_moe_forward(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t*
     MoeBufs w{};
     if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
     if (rows > kMaxRows) return run_prefill(L, w, rows, x, y, routes, nullptr, static_cast<hipStream_t>(stream));
-    return run_layer(L, w, rows, x, 0.0f, nullptr, y, routes, nullptr, static_cast<hipStream_t>(stream));
+    return run_layer(L, w, rows, x, false, 0.0f, nullptr, y, routes, nullptr, static_cast<hipStream_t>(stream));
 }
 
 int q38_moe_forward_prefill_profiled(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t* y,
@@ -684,8 +682,7 @@ int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h
     for (int l = 0; l < n_layers; ++l) {
         MoeBufs w{};
         moe_ws(layers[l]->desc, rows, &w, ws);
-        if (l == 0) Q38_HIP(launch_xnorm(h, rows, layers[0]->desc.hidden, eps, w.x, w.x16, st));
-        if (int rc = run_layer(layers[l], w, rows, w.x, eps, h, nullptr, traces ? &traces[l] : nullptr, nullptr, st))
+        if (int rc = run_layer(layers[l], w, rows, h, true, eps, h, nullptr, traces ? &traces[l] : nullptr, nullptr, st))
             return rc;
     }
     return Q38_OK;
@@ -706,15 +703,11 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
     for (int l = 0; l < n_layers && rc == Q38_OK; ++l) {
         MoeBufs w{};
         moe_ws(layers[l]->desc, rows, &w, ws);
-        if (l == 0 && launch_xnorm(h, rows, layers[0]->desc.hidden, eps, w.x, w.x16, st) != hipSuccess) {
-            rc = fail(Q38_EHIP, "verify chain: RMSNorm launch failed");
-            break;
-        }
         hipEvent_t* E = &ev[static_cast<size_t>(l) * 8];
         const q38_moe_layer* L = layers[l];
         hipError_t e = hipSuccess;
         kt = {E[0], E[1]};
-        e = launch_router(L->dev, w, rows, w.x, st);
+        e = launch_router(L->dev, w, rows, h, true, eps, st);
         if (e == hipSuccess && !moe_uses_mfma(L->dev)) e = launch_topk_plan(L->dev, w, rows, st);
         if (e == hipSuccess) {
             kt = {E[2], E[3]};
@@ -728,7 +721,7 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
         }
         if (e == hipSuccess) {
             kt = {E[6], E[7]};
-            e = launch_combine_norm(L->dev, w, rows, h, eps, st);
+            e = launch_combine(L->dev, w, rows, h, nullptr, st);
         }
         kt = {};
         if (e != hipSuccess) rc = hip_fail(e, "profiled verify chain");
@@ -999,3 +992,15 @@ int q38_slot_info(const q38_slot* s, uint64_t* token_count, int32_t* staged_rows
 const uint16_t* q38_slot_hidden(const q38_slot* s) { return s && s->has_hidden ? s->committed : nullptr; }
 
 } // extern "C"
+
+#ifdef Q38_TRACE
+// Phase stamps of the Q38_TRACE build (see q38_moe_dev.hpp).
+namespace q38 {
+__device__ unsigned long long g_trace[32768];
+}
+extern "C" int q38_trace_read(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(q38::g_trace), sizeof(unsigned long long) * 32768) == hipSuccess
+               ? 0
+               : -1;
+}
+#endif

@@ -10,6 +10,23 @@ namespace q38 {
 
 constexpr int kWave = 64;
 
+// ------------------------------------------------------------------ workgroup barrier
+// A barrier that orders LDS only. __syncthreads() fences every address space, which on
+// gfx950 waits for all of the wave's outstanding global loads (vmcnt(0)) before s_barrier
+// and so drains any prefetch in flight. Kernels that share data through LDS only use this
+// one; data that arrives in LDS over the direct global-to-LDS path is covered by an
+// explicit vmcnt wait of the issuing wave before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+// The same for a phase in which direct global-to-LDS copies are still in flight: the LDS
+// fence above also waits for those (they count as LDS writes), so this barrier waits only
+// for the wave's own LDS instructions (lgkmcnt) and leaves the copies running. Only data
+// written with ds_* instructions may be read after it.
+__device__ __forceinline__ void lds_barrier_dma_pending() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ------------------------------------------------------------------ number formats
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 __device__ __forceinline__ uint16_t f2bf(float f) {
@@ -156,6 +173,23 @@ __device__ __forceinline__ double wave_sum_xor(double v) {
     v = v + xor_lane_d<2>(v);
     v = v + xor_lane_d<1>(v);
     return v;
+}
+// wave_sum_xor of N independent values, step by step across all of them (the exchanges of
+// one step are in flight together); each result equals wave_sum_xor of that value alone.
+template <int N>
+__device__ __forceinline__ void wave_sum_xor_n(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + xor_lane_f<32>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + xor_lane_f<16>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + xor_lane_f<8>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + xor_lane_f<4>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + xor_lane_f<2>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + xor_lane_f<1>(v[i]);
 }
 // The same butterfly through lane permutes only (the reference form of the exchanges).
 __device__ __forceinline__ float wave_sum_xor_shfl(float v) {

@@ -53,7 +53,8 @@ struct MoeBufs {
     float* weights;    // [M*K]
     int32_t* plan;     // [2 + 4*M*K]
     // Projection partial sums, one plane per codebook chunk (summed chunk 0 + chunk 1 by the
-    // consumer): rows in sorted route order, shared-expert rows last.
+    // consumer). g / u rows in sorted route order, d rows at the route index (row * K +
+    // slot); shared-expert rows last (M*K + row).
     float* g;          // [2][M*K + M, I] gate
     float* u;          // [2][M*K + M, I] up
     float* d;          // [2][M*K + M, H] down
@@ -85,18 +86,17 @@ struct HeadDev {
 };
 
 // MoE layer (rows M <= kMaxRows)
-// Router logits of the normalised input x (copied to B.x / B.x16 unless x is B.x).
-hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st);
+// Router logits of the layer input: norm = false: src is x (copied to B.x / B.x16 unless it
+// is B.x); norm = true: src is the residual stream h and x = RMSNorm(h) (eps) is formed
+// first (the verify chain).
+hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* src, bool norm, float eps,
+                         hipStream_t st);
 hipError_t launch_topk_plan(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
-// chain: h <- h + y (in place); otherwise out <- y.
+// chain: h <- h + y (in place); otherwise out <- y. Down rows are read at the route index.
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st);
-// Verify chain: x = RMSNorm(h) of the first layer into B.x / B.x16, and the combine that
-// updates h in place and forms the next layer's x (same norm routine).
-hipError_t launch_xnorm(const uint16_t* h, int M, int H, float eps, uint16_t* x, uint16_t* x16, hipStream_t st);
-hipError_t launch_combine_norm(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, float eps, hipStream_t st);
 hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_t* book4, hipStream_t st);
 bool moe_uses_mfma(const LayerDev& L);
 // Verify widths of up to 4 rows on the 4x4x4 MFMA kernels (q38_moe4.hip).

@@ -2,8 +2,9 @@
 // (rows <= 16), plus the synthetic-weight generators.
 //
 // Per layer the launch sequence is
-//   k_logits      router logits with the fixed-order contract (R1) + the shared-expert
-//                 gate logit; one workgroup per row of Wr, one wave per request row.
+//   k_route_norm  router logits with the fixed-order contract (R1) + the shared-expert
+//                 gate logit, with the layer-input RMSNorm of the verify chain folded in;
+//                 one wave per row of Wr, H/4 threads per workgroup.
 //   k_topk_plan   softmax / top-k / normalise per row (R2) and the gather-by-expert plan
 //                 (R3): unique experts ascending, each with its routes in (row, slot)
 //                 order; one workgroup.
@@ -12,9 +13,7 @@
 //                 routed row of an expert, so each packed code row is read once per chunk.
 //   k_down_mfma   SwiGLU of the gate/up sums + down projection (R7, R8), same scheme.
 //   k_combine     ordered route reduction (slot order) + shared expert x sigmoid gate +
-//                 merge (R8, R10, R11); k_combine_norm adds the residual in place (chain)
-//                 and forms the next layer's RMSNorm input; k_xnorm is that RMSNorm for
-//                 the first layer of a chain.
+//                 merge (R8, R10, R11); in a chain it adds the residual in place.
 // Layers with per-64-input scale groups use the k_*_grouped VALU kernels instead.
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
@@ -125,40 +124,120 @@ __global__ void k_book_to_int8(const uint16_t* __restrict__ book16, int n, int8_
     }
 }
 
-// ============================================================== router (R1)
-// One workgroup per row of Wr (the last one: w_sg), one wave per request row (rows w,
-// w + waves, ...). x is the normalised layer input (bf16). Logit contract: lane l holds
-// the columns c = 512t + 8l + j and accumulates x*w over them (t outer, j inner) with
-// fmaf, then the xor butterfly and BF16 rounding; a router bias, when set, is added to the
-// rounded logit in float. When x is not already the workspace
-// copy, workgroup 0 stores it there (bf16) with its fp16 copy (the MFMA operand).
-template <int T>
-__global__ __launch_bounds__(256) void k_logits(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ x) {
-    constexpr int H = 512 * T;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    const int e = blockIdx.x;
-    const uint16_t* w = e < L.E ? L.router + static_cast<size_t>(e) * H : L.wsg;
+// ============================================================== router (R1) + layer-input RMSNorm
+// One workgroup of H/4 threads per NW = H/256 router rows (wave w: row blockIdx.x * NW + w;
+// row E is w_sg). The router rows are requested first: they do not depend on the previous
+// kernel. NORM: the layer input is x = T(h * inv_rms(h)) of the residual stream h, formed
+// in every workgroup in one fixed order: thread t owns columns t + (H/4) i (i < 4) and
+// accumulates fmaf(v, v) in i order; the waves' xor-butterfly totals are added in wave
+// order; inv_rms = 1 / sqrt(total / H + eps). Otherwise src is x itself.
+// Logit contract: lane l holds the columns c = 512t + 8l + j and accumulates x*w over them
+// (t outer, j inner) with fmaf, then the xor butterfly and BF16 rounding; a router bias,
+// when set, is added to the rounded logit in float. Workgroup 0 stores x in the workspace
+// (bf16) with its fp16 copy (the MFMA operand) unless src already is that copy.
+template <int T, bool NORM, int MR>
+__global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ src,
+                                                        float eps) {
+    constexpr int H = 512 * T, NT = 128 * T, NW = NT / 64;
+    extern __shared__ __align__(16) uint16_t xs[];  // [M][H] bf16
+    __shared__ float red[MR][NW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nr = L.E + (L.has_shared ? 1 : 0);
+    const int e = blockIdx.x * NW + wave;
+    Q38_STAMP(0, 0);
+    const bool store = blockIdx.x == 0 && src != B.x;
+    // The layer input is requested first (it gates the norm); the router rows are needed
+    // only for the dot products and stream in behind it. MR >= M rows are loaded without
+    // branches (rows past M repeat row M - 1) so that every load is in flight at once.
+    float v[NORM ? MR : 1][4];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            const int rr = r < M ? r : M - 1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[r][i] = bf2f(src[static_cast<size_t>(rr) * H + tid + NT * i]);
+        }
+    }
     uint4 wv[T];
+    {
+        const int ew = e < nr ? e : nr - 1;
+        const uint16_t* w = ew < L.E ? L.router + static_cast<size_t>(ew) * H : L.wsg;
 #pragma unroll
-    for (int t = 0; t < T; ++t) wv[t] = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
-    const bool store_x = e == 0 && x != B.x;
-    for (int r = wave; r < M; r += waves) {
-        uint4 xv[T];
+        for (int t = 0; t < T; ++t) wv[t] = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
+    }
+    if constexpr (NORM) {
+        Q38_STAMPV(0, 1, v[0][0]);
+        float ss[MR];
 #pragma unroll
-        for (int t = 0; t < T; ++t) xv[t] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(r) * H + 512 * t + 8 * lane);
-        float acc = 0.0f;
+        for (int r = 0; r < MR; ++r) {
+            ss[r] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ss[r] = fmaf(v[r][i], v[r][i], ss[r]);
+        }
+        wave_sum_xor_n<MR>(ss);
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+            if (lane == 0) red[r][wave] = ss[r];
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+            if (r < M) {
+                float t = 0.0f;
+                for (int w = 0; w < NW; ++w) t += red[r][w];
+                const float inv = 1.0f / sqrtf(t / static_cast<float>(H) + eps);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const size_t at = static_cast<size_t>(r) * H + tid + NT * i;
+                    const uint16_t b = f2bf(v[r][i] * inv);
+                    xs[at] = b;
+                    if (store) {
+                        B.x[at] = b;
+                        B.x16[at] = f2h(bf2f(b));
+                    }
+                }
+            }
+    } else {
+        const uint4* s4 = reinterpret_cast<const uint4*>(src);
+        for (int i = tid; i < M * H / 8; i += NT) {
+            const uint4 q4 = s4[i];
+            reinterpret_cast<uint4*>(xs)[i] = q4;
+            if (store) {
+                reinterpret_cast<uint4*>(B.x)[i] = q4;
+                const uint32_t q[4] = {q4.x, q4.y, q4.z, q4.w};
+                uint32_t hq[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    hq[k] = static_cast<uint32_t>(f2h(bflo(q[k]))) | (static_cast<uint32_t>(f2h(bfhi(q[k]))) << 16);
+                reinterpret_cast<uint4*>(B.x16)[i] = make_uint4(hq[0], hq[1], hq[2], hq[3]);
+            }
+        }
+    }
+    lds_barrier();
+    Q38_STAMP(0, 2);
+    if (e >= nr) return;
+    // all rows' products first (independent chains), then the butterflies
+    float acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        acc[r] = 0.0f;
+        const int rr = r < M ? r : 0;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const uint32_t xq[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+            const uint4 xv = *reinterpret_cast<const uint4*>(xs + static_cast<size_t>(rr) * H + 512 * t + 8 * lane);
+            const uint32_t xq[4] = {xv.x, xv.y, xv.z, xv.w};
             const uint32_t wq[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                acc = __builtin_fmaf(bflo(xq[k]), bflo(wq[k]), acc);
-                acc = __builtin_fmaf(bfhi(xq[k]), bfhi(wq[k]), acc);
+                acc[r] = __builtin_fmaf(bflo(xq[k]), bflo(wq[k]), acc[r]);
+                acc[r] = __builtin_fmaf(bfhi(xq[k]), bfhi(wq[k]), acc[r]);
             }
         }
-        const float sres = wave_sum_xor(acc);
-        if (lane == 0) {
+    }
+    wave_sum_xor_n<MR>(acc);
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        const float sres = acc[r];
+        if (lane == 0 && r < M) {
             if (e < L.E) {
                 B.logits[r * L.E + e] = L.rbias ? rbf(sres) + L.rbias[e] : rbf(sres);
             } else {
@@ -166,20 +245,8 @@ __global__ __launch_bounds__(256) void k_logits(LayerDev L, MoeBufs B, int M, co
                 B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
             }
         }
-        if (store_x) {
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const size_t at = static_cast<size_t>(r) * H + 512 * t + 8 * lane;
-                *reinterpret_cast<uint4*>(B.x + at) = xv[t];
-                const uint32_t q[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-                uint32_t hq[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    hq[k] = static_cast<uint32_t>(f2h(bflo(q[k]))) | (static_cast<uint32_t>(f2h(bfhi(q[k]))) << 16);
-                *reinterpret_cast<uint4*>(B.x16 + at) = make_uint4(hq[0], hq[1], hq[2], hq[3]);
-            }
-        }
     }
+    Q38_STAMP(0, 3);
 }
 
 __global__ __launch_bounds__(1024) void k_topk_plan(LayerDev L, MoeBufs B, int M) {
@@ -286,7 +353,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     }
     for (int i = tid; i < NSUB; i += kMfmaThreads)
         reinterpret_cast<uint2*>(xs)[kMfmaMaxCols * NSUB + i] = make_uint2(0u, 0u);
-    __syncthreads();
+    lds_barrier();
     auto code_src = [&](int item) {
         int expert, n, pos0;
         slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
@@ -308,14 +375,14 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
             if (stage_all) {
                 if (r16 < nj) xrow = route_row(plan, M, K, pos0, j0 + r16, shared);
             } else {
-                __syncthreads();
+                lds_barrier();
                 for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
                     const int jj = i / NSUB, sv = i % NSUB;
                     const int row = route_row(plan, M, K, pos0, j0 + jj, shared);
                     reinterpret_cast<uint2*>(xs)[jj * NSUB + sv] = *reinterpret_cast<const uint2*>(
                         B.x16 + static_cast<size_t>(row) * H + sv * (4 * NCHUNK) + 4 * chunk);
                 }
-                __syncthreads();
+                lds_barrier();
             }
             const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs_lane<NSUB>(xs, xrow, kMfmaMaxCols, q, r16 < nj));
             if (r16 < nj) {
@@ -373,7 +440,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
     if (stage_all) stage(0, n_routes);
     for (int i = tid; i < NSUB; i += kMfmaThreads)
         reinterpret_cast<uint2*>(xs)[kDownStageRoutes * NSUB + i] = make_uint2(0u, 0u);
-    __syncthreads();
+    lds_barrier();
     float* dout = B.d + chunk * B.d_plane;
     const int nu = plan[0];
     const int tiles = H / kMfmaRowsPerItem;
@@ -401,9 +468,9 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
             if (stage_all) {
                 xrow = pos0 + j0 + r16;
             } else {
-                __syncthreads();
+                lds_barrier();
                 stage(pos0 + j0, nj);
-                __syncthreads();
+                lds_barrier();
             }
             const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs_lane<NSUB>(xs, xrow, kDownStageRoutes, q, r16 < nj));
             if (r16 < nj) {
@@ -411,7 +478,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
                 for (int rr = 0; rr < 4; ++rr) {
                     const int o = o0 + 4 * q + rr;
                     const float sc = h2f(P.scales[static_cast<size_t>(expert) * H + o]);
-                    dout[static_cast<size_t>(pos0 + j0 + r16) * H + o] = sc * acc[rr];
+                    dout[static_cast<size_t>(route_of_pos(plan, M * K, pos0 + j0 + r16)) * H + o] = sc * acc[rr];
                 }
             }
         }
@@ -462,11 +529,13 @@ constexpr int kGuRowsPerBlock = 64;
 constexpr int kDownRowsPerBlock = 128;
 
 // Lane mapping: a lane owns 16 consecutive codes of a row (BITS/2 words); LPR lanes
-// (power of two, padded) cover one row; 64/LPR rows per wave. in_f: [n][IN] floats.
+// (power of two, padded) cover one row; 64/LPR rows per wave. in_f: [n][IN] floats. Output row
+// pos0 + j, or its route index when rplan (the plan) is given (down projections).
 template <int D, int BITS, int LPR, int MAXN>
 __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int IN, int OUT, int o_base,
                                              int rows_per_block, const float* in_f, int n, float* out,
-                                             int pos0, int wave, int lane) {
+                                             int pos0, int wave, int lane, const int32_t* rplan = nullptr,
+                                             int MK = 0) {
     const int nsub = IN / D;
     const int lanes_used = (nsub + 15) / 16;
     const int sub_lane = lane % LPR;
@@ -522,7 +591,7 @@ __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int I
             const float sc = row_scale ? h2f(P.scales[static_cast<size_t>(expert) * OUT + o]) : 1.0f;
 #pragma unroll
             for (int j = 0; j < MAXN; ++j)
-                if (j < n) out[static_cast<size_t>(pos0 + j) * OUT + o] = acc[j] * sc;
+                if (j < n) out[static_cast<size_t>(rplan ? route_of_pos(rplan, MK, pos0 + j) : pos0 + j) * OUT + o] = acc[j] * sc;
         }
     }
 }
@@ -563,7 +632,7 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     grouped_rows<D, BITS, LPR, kMaxRows>(L.p[2], expert, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
-                                         fin, n, B.d, pos0, wave, lane);
+                                         fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
 }
 
 // Mixed geometry (even experts d4/8-bit fp16 books, odd experts d8/14-bit INT8 books):
@@ -610,127 +679,48 @@ __global__ __launch_bounds__(256) void k_down_mixed(LayerDev L, MoeBufs B, int M
     const int idx = expert >> 1;
     if ((expert & 1) == 0)
         grouped_rows<4, 8, LA, kMaxRows>(L.pb[2][0], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
-                                         fin, n, B.d, pos0, wave, lane);
+                                         fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
     else
         grouped_rows<8, 14, LB, kMaxRows>(L.pb[2][1], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
-                                          fin, n, B.d, pos0, wave, lane);
+                                          fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
 }
 
 // ============================================================== combine (R8, R10, R11)
 // One thread per (row, column): routed = T(sum_slot w_slot * T(d_slot)) in slot order,
 // shared = T(T(d_shared) * gate), y = T(routed + shared); chain mode adds the residual in
-// place (h <- T(h + y)), otherwise out <- y.
+// place (h <- T(h + y)), otherwise out <- y. The down kernels write route r * k + s at row
+// r * k + s and the shared expert's row r at M * k + r, so every load here is independent
+// of the plan and all of them are issued before the first use.
+template <int KT>
 __global__ __launch_bounds__(256) void k_combine(LayerDev L, MoeBufs B, int M, uint16_t* h, uint16_t* out) {
     const int r = blockIdx.y;
     const int o = blockIdx.x * 256 + threadIdx.x;
-    const int H = L.H, K = L.K, MK = M * K;
+    const int H = L.H, MK = M * KT;
+    Q38_STAMP(24576, 0);
     if (o >= H) return;
-    const int32_t* rpos = B.plan + 2 + 3 * MK;
     const bool two = L.d_parts == 2;
-    auto dsum = [&](int route) {
+    const bool shared = L.has_shared;
+    float dv[KT + 1][2];
+#pragma unroll
+    for (int s = 0; s <= KT; ++s) {
+        const int route = s < KT ? r * KT + s : (shared ? MK + r : r * KT);
         const size_t at = static_cast<size_t>(route) * H + o;
-        return two ? B.d[at] + B.d[B.d_plane + at] : B.d[at];
-    };
+        dv[s][0] = B.d[at];
+        dv[s][1] = two ? B.d[B.d_plane + at] : 0.0f;
+    }
+    const float hv = h ? bf2f(h[static_cast<size_t>(r) * H + o]) : 0.0f;
     float routed = 0.0f;
-    for (int s = 0; s < K; ++s) routed = fmaf(B.weights[r * K + s], rbf(dsum(rpos[r * K + s])), routed);
+#pragma unroll
+    for (int s = 0; s < KT; ++s) routed = fmaf(B.weights[r * KT + s], rbf(two ? dv[s][0] + dv[s][1] : dv[s][0]), routed);
     float y = rbf(routed);
-    if (L.has_shared) {
-        const float sh = rbf(rbf(dsum(MK + r)) * B.sgate[r]);
+    if (shared) {
+        const float sh = rbf(rbf(two ? dv[KT][0] + dv[KT][1] : dv[KT][0]) * B.sgate[r]);
         y = rbf(y + sh);
     }
     const size_t i = static_cast<size_t>(r) * H + o;
-    if (h) h[i] = f2bf(rbf(bf2f(h[i]) + y));
+    if (h) h[i] = f2bf(rbf(hv + y));
     else out[i] = f2bf(y);
-}
-
-// RMSNorm of one row for the verify chain, with a fixed order: a block of H/4 threads,
-// thread t owns columns t + (H/4) i for i < 4 and accumulates fmaf(v, v, .) in i order;
-// waves join with the xor butterfly, the wave totals are added in wave order. Returns
-// 1 / sqrt(mean(v^2) + eps). red: >= 16 floats of LDS.
-__device__ __forceinline__ float row_inv_rms(const float (&v)[4], float* red, int H, float eps) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ss = fmaf(v[i], v[i], ss);
-    ss = wave_sum_xor(ss);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float t = 0.0f;
-    for (int w = 0; w < waves; ++w) t += red[w];
-    return 1.0f / sqrtf(t / static_cast<float>(H) + eps);
-}
-__device__ __forceinline__ void store_xnorm(const float (&v)[4], float inv, int r, int H, uint16_t* x, uint16_t* x16) {
-    const int nt = blockDim.x;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const size_t at = static_cast<size_t>(r) * H + threadIdx.x + nt * i;
-        const uint16_t b = f2bf(v[i] * inv);
-        x[at] = b;
-        x16[at] = f2h(bf2f(b));
-    }
-}
-
-// x = T(h * inv_rms(h)) for the first layer of a chain (block = H/4 threads per row).
-__global__ __launch_bounds__(1024) void k_xnorm(const uint16_t* __restrict__ h, int H, float eps, uint16_t* x,
-                                                uint16_t* x16) {
-    __shared__ float red[16];
-    const int r = blockIdx.x, nt = blockDim.x;
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = bf2f(h[static_cast<size_t>(r) * H + threadIdx.x + nt * i]);
-    const float inv = row_inv_rms(v, red, H, eps);
-    store_xnorm(v, inv, r, H, x, x16);
-}
-
-// Chain combine: one block of H/4 threads per request row. y as in k_combine, h <- T(h + y)
-// in place, then the next layer's input x = T(h * inv_rms(h)) into the workspace (the same
-// routine as k_xnorm, so a chain and its layer-by-layer replay agree bit for bit). All
-// loads of a thread's four columns are issued before the reductions (KT = top-k).
-template <int KT>
-__global__ __launch_bounds__(1024) void k_combine_norm(LayerDev L, MoeBufs B, int M, uint16_t* h, float eps) {
-    __shared__ float red[16];
-    __shared__ float wsl[KT];
-    __shared__ int psl[KT];
-    __shared__ float sg;
-    const int r = blockIdx.x, nt = blockDim.x, tid = threadIdx.x;
-    const int H = L.H, MK = M * KT;
-    if (tid < KT) {
-        wsl[tid] = B.weights[r * KT + tid];
-        psl[tid] = B.plan[2 + 3 * MK + r * KT + tid];
-    }
-    if (tid == KT) sg = L.has_shared ? B.sgate[r] : 0.0f;
-    __syncthreads();
-    const bool two = L.d_parts == 2;
-    const bool shared = L.has_shared;
-    float hv[4], dv[4][KT + 1][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int o = tid + nt * i;
-        hv[i] = bf2f(h[static_cast<size_t>(r) * H + o]);
-#pragma unroll
-        for (int s = 0; s <= KT; ++s) {
-            dv[i][s][0] = dv[i][s][1] = 0.0f;
-            if (s == KT && !shared) continue;
-            const int route = s < KT ? psl[s] : MK + r;
-            const size_t at = static_cast<size_t>(route) * H + o;
-            dv[i][s][0] = B.d[at];
-            if (two) dv[i][s][1] = B.d[B.d_plane + at];
-        }
-    }
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float routed = 0.0f;
-#pragma unroll
-        for (int s = 0; s < KT; ++s) routed = fmaf(wsl[s], rbf(two ? dv[i][s][0] + dv[i][s][1] : dv[i][s][0]), routed);
-        float y = rbf(routed);
-        if (shared) y = rbf(y + rbf(rbf(two ? dv[i][KT][0] + dv[i][KT][1] : dv[i][KT][0]) * sg));
-        const uint16_t hb = f2bf(rbf(hv[i] + y));
-        h[static_cast<size_t>(r) * H + tid + nt * i] = hb;
-        v[i] = bf2f(hb);
-    }
-    const float inv = row_inv_rms(v, red, H, eps);
-    store_xnorm(v, inv, r, H, B.x, B.x16);
+    Q38_STAMP(24576, 1);
 }
 
 __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x, int H, float eps,
@@ -779,11 +769,35 @@ void init_grid() {
     done = true;
 }
 
-template <int T>
-hipError_t launch_router_t(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st) {
+template <int T, bool NORM, int MR>
+hipError_t launch_route_norm_t(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* src, float eps,
+                               hipStream_t st) {
+    constexpr int NW = 2 * T;  // waves of H/4 threads
+    const size_t lds = static_cast<size_t>(M) * 512 * T * 2;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e =
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&k_route_norm<T, NORM, MR>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(MR * 512 * T * 2));
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
     const int rows = L.E + (L.has_shared ? 1 : 0);
-    const int waves = M < 4 ? M : 4;
-    return launch(k_logits<T>, dim3(rows), dim3(64 * waves), 0, st, L, B, M, x);
+    return launch(k_route_norm<T, NORM, MR>, dim3((rows + NW - 1) / NW), dim3(128 * T), lds, st, L, B, M, src, eps);
+}
+template <int T, bool NORM>
+hipError_t launch_route_norm_m(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* src, float eps,
+                               hipStream_t st) {
+    if (M <= 1) return launch_route_norm_t<T, NORM, 1>(L, B, M, src, eps, st);
+    if (M <= 2) return launch_route_norm_t<T, NORM, 2>(L, B, M, src, eps, st);
+    if (M <= 4) return launch_route_norm_t<T, NORM, 4>(L, B, M, src, eps, st);
+    if (M <= 8) return launch_route_norm_t<T, NORM, 8>(L, B, M, src, eps, st);
+    return launch_route_norm_t<T, NORM, 16>(L, B, M, src, eps, st);
+}
+template <int T>
+hipError_t launch_route_norm_h(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* src, bool norm, float eps,
+                               hipStream_t st) {
+    return norm ? launch_route_norm_m<T, true>(L, B, M, src, eps, st) : launch_route_norm_m<T, false>(L, B, M, src, eps, st);
 }
 
 template <typename Kern>
@@ -851,15 +865,17 @@ bool moe_uses_mfma(const LayerDev& L) {
     return gu_ok && dn_ok;
 }
 
-hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st) {
+hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* src, bool norm, float eps,
+                         hipStream_t st) {
+    if (M < 1 || M > kMaxRows) return hipErrorInvalidValue;
     switch (L.H / 512) {
-        case 1: return launch_router_t<1>(L, B, M, x, st);
-        case 2: return launch_router_t<2>(L, B, M, x, st);
-        case 3: return launch_router_t<3>(L, B, M, x, st);
-        case 4: return launch_router_t<4>(L, B, M, x, st);
-        case 5: return launch_router_t<5>(L, B, M, x, st);
-        case 6: return launch_router_t<6>(L, B, M, x, st);
-        case 8: return launch_router_t<8>(L, B, M, x, st);
+        case 1: return launch_route_norm_h<1>(L, B, M, src, norm, eps, st);
+        case 2: return launch_route_norm_h<2>(L, B, M, src, norm, eps, st);
+        case 3: return launch_route_norm_h<3>(L, B, M, src, norm, eps, st);
+        case 4: return launch_route_norm_h<4>(L, B, M, src, norm, eps, st);
+        case 5: return launch_route_norm_h<5>(L, B, M, src, norm, eps, st);
+        case 6: return launch_route_norm_h<6>(L, B, M, src, norm, eps, st);
+        case 8: return launch_route_norm_h<8>(L, B, M, src, norm, eps, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -945,40 +961,29 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
-    return launch(k_combine, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
-}
-
-hipError_t launch_xnorm(const uint16_t* h, int M, int H, float eps, uint16_t* x, uint16_t* x16, hipStream_t st) {
-    if (H % 256 || H / 4 > 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_xnorm, dim3(M), dim3(H / 4), 0, st, h, H, eps, x, x16);
-    return hipGetLastError();
-}
-
 template <int KT>
-hipError_t launch_combine_norm_k(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, float eps, hipStream_t st) {
-    return launch(k_combine_norm<KT>, dim3(M), dim3(L.H / 4), 0, st, L, B, M, h, eps);
+hipError_t launch_combine_k(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
+    return launch(k_combine<KT>, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
 }
 
-hipError_t launch_combine_norm(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, float eps, hipStream_t st) {
-    if (L.H % 256 || L.H / 4 > 1024) return hipErrorInvalidValue;
+hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
     switch (L.K) {
-        case 1: return launch_combine_norm_k<1>(L, B, M, h, eps, st);
-        case 2: return launch_combine_norm_k<2>(L, B, M, h, eps, st);
-        case 3: return launch_combine_norm_k<3>(L, B, M, h, eps, st);
-        case 4: return launch_combine_norm_k<4>(L, B, M, h, eps, st);
-        case 5: return launch_combine_norm_k<5>(L, B, M, h, eps, st);
-        case 6: return launch_combine_norm_k<6>(L, B, M, h, eps, st);
-        case 7: return launch_combine_norm_k<7>(L, B, M, h, eps, st);
-        case 8: return launch_combine_norm_k<8>(L, B, M, h, eps, st);
-        case 9: return launch_combine_norm_k<9>(L, B, M, h, eps, st);
-        case 10: return launch_combine_norm_k<10>(L, B, M, h, eps, st);
-        case 11: return launch_combine_norm_k<11>(L, B, M, h, eps, st);
-        case 12: return launch_combine_norm_k<12>(L, B, M, h, eps, st);
-        case 13: return launch_combine_norm_k<13>(L, B, M, h, eps, st);
-        case 14: return launch_combine_norm_k<14>(L, B, M, h, eps, st);
-        case 15: return launch_combine_norm_k<15>(L, B, M, h, eps, st);
-        case 16: return launch_combine_norm_k<16>(L, B, M, h, eps, st);
+        case 1: return launch_combine_k<1>(L, B, M, h, out, st);
+        case 2: return launch_combine_k<2>(L, B, M, h, out, st);
+        case 3: return launch_combine_k<3>(L, B, M, h, out, st);
+        case 4: return launch_combine_k<4>(L, B, M, h, out, st);
+        case 5: return launch_combine_k<5>(L, B, M, h, out, st);
+        case 6: return launch_combine_k<6>(L, B, M, h, out, st);
+        case 7: return launch_combine_k<7>(L, B, M, h, out, st);
+        case 8: return launch_combine_k<8>(L, B, M, h, out, st);
+        case 9: return launch_combine_k<9>(L, B, M, h, out, st);
+        case 10: return launch_combine_k<10>(L, B, M, h, out, st);
+        case 11: return launch_combine_k<11>(L, B, M, h, out, st);
+        case 12: return launch_combine_k<12>(L, B, M, h, out, st);
+        case 13: return launch_combine_k<13>(L, B, M, h, out, st);
+        case 14: return launch_combine_k<14>(L, B, M, h, out, st);
+        case 15: return launch_combine_k<15>(L, B, M, h, out, st);
+        case 16: return launch_combine_k<16>(L, B, M, h, out, st);
         default: return hipErrorInvalidValue;
     }
 }

@@ -1,4 +1,4 @@
-// q38_moe4.hip — expert projections for verify widths of up to four rows (R4, R5, R7, R8)
+// q38_moe4.hip — expert projections for verify widths of up to four rows (R2-R5, R7, R8)
 // on v_mfma_f32_4x4x4_16b_f16.
 //
 // Operand layout of the 16-block 4x4x4 instruction: A lane 4b + i holds row i of block b
@@ -10,11 +10,19 @@
 // 32-subvector K slice (one whole 32-code block of each of its rows, one contiguous code
 // span per lane); the slices are summed across waves through LDS in a fixed order.
 //
-// Each workgroup keeps one 4-dim chunk of one codebook in LDS for the whole launch (as in
-// the wide-row kernels) and walks its share of (expert slot, tile) items. The prologue
-// issues every independent load before it waits on any: the routing wave's logits, the
-// codebook chunk, the input operand; the first item's code span is requested as soon as
-// the plan exists, and each item's span is prefetched while the previous item computes.
+// Each workgroup keeps one 4-dim chunk of one codebook in LDS for the whole launch and
+// walks its share of (expert slot, tile) items. The kernels are built around the latency
+// chain of a verify layer:
+//   k_gu4  the routing waves (one per request row) load only their logits, so nothing else
+//          queues ahead of them; once the logits are in, the other waves stream the
+//          codebook chunk into LDS over the direct global-to-LDS path while the routing
+//          waves run softmax + top-k; one wave turns the rows' experts into the plan, and
+//          every wave then issues the code spans of all its items (a ring of D in flight).
+//   k_dn4  the plan is read first; the codebook chunk (into registers) and the code spans,
+//          gate/up partial sums and scales of the first D items follow as soon as the plan is
+//          in LDS; the chunk is stored to LDS behind them.
+//          Down outputs are written at the route index (request row * k + slot; the
+//          shared expert's rows after the routed ones), so the combine needs no plan.
 #include "q38_moe_dev.hpp"
 
 namespace q38 {
@@ -22,8 +30,10 @@ namespace {
 
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kNarrow = 4;  // input rows per instruction (the B columns)
+constexpr int kNarrowPlan = 2 + 4 * kNarrow * kMaxTopK;
 
 // One 32-code block (BITS words) plus a zero pad word for code_from.
 template <int BITS>
@@ -47,18 +57,24 @@ __device__ __forceinline__ void load_code_block(const uint32_t* src, uint32_t* w
     w[BITS] = 0;
 }
 
-// 32 steps of one K slice: A = codebook entries of the lane's row, B = bops[t].
+// 32 steps of one K slice: A = codebook entries of the lane's row, B = bops[t]. Even and
+// odd steps accumulate separately (two independent MFMA chains), added at the end.
 template <int BITS>
 __device__ __forceinline__ v4f_t slice_mfma(const uint32_t* cw, const uint2* book, const uint2* bops) {
-    v4f_t acc = {0.f, 0.f, 0.f, 0.f};
+    v4f_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < 32; ++t) {
-        const uint2 a = book[code_from<BITS>(cw, t)];
-        acc = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4_t, a), __builtin_bit_cast(h4_t, bops[t]), acc,
-                                                  0, 0, 0);
+    for (int t = 0; t < 32; t += 2) {
+        const uint2 a0 = book[code_from<BITS>(cw, t)];
+        const uint2 a1 = book[code_from<BITS>(cw, t + 1)];
+        acc0 = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4_t, a0), __builtin_bit_cast(h4_t, bops[t]), acc0,
+                                                   0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4_t, a1), __builtin_bit_cast(h4_t, bops[t + 1]),
+                                                   acc1, 0, 0, 0);
     }
-    return acc;
+    return acc0 + acc1;
 }
+
+__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Gate and up projections. Workgroup type = (projection, codebook chunk); waves = K slices.
 // Items are 64-row tiles of I; the 4 B columns are the request rows (rows not routed to the
@@ -66,19 +82,26 @@ __device__ __forceinline__ v4f_t slice_mfma(const uint32_t* cw, const uint2* boo
 // row scale, at the route's sorted position (the gate/up chunk planes).
 // One workgroup per CU (the LDS codebook chunk), so a SIMD runs at most ceil(waves / 4)
 // of its waves: the register budget is set by that, not by a higher occupancy target.
+// LDS: codebook chunk [KENT][4] fp16, cross-wave partial sums [2][KS][64][4] f32, the
+// chunk's dims of the request rows [4][NSUB][4] fp16.
 template <int BITS, int NSUB, int NCHUNK>
+constexpr size_t gu4_lds_bytes() {
+    return (size_t{1} << BITS) * 8 + 2 * (NSUB / 32) * 64 * 16 + kNarrow * NSUB * 8;
+}
+template <int BITS, int NSUB, int NCHUNK, int D>
 __global__ __launch_bounds__(2 * NSUB) __attribute__((amdgpu_waves_per_eu(1, (NSUB / 32 + 3) / 4)))
 void k_gu4(LayerDev L, MoeBufs B, int M) {
     constexpr int KS = NSUB / 32;
     constexpr int NT = 64 * KS;
     constexpr int KENT = 1 << BITS;
     constexpr int TYPES = 2 * NCHUNK;
-    constexpr int NF = (KENT / 2 + NT - 1) / NT;  // codebook uint4 per thread
     extern __shared__ __align__(16) unsigned char lds[];
-    __shared__ TopkLds tk;
-    __shared__ int32_t plan[kPlanInts];
+    __shared__ int32_t ex[kNarrowMaxRoutes];
+    __shared__ int32_t plan[kNarrowPlan];
+    __shared__ int32_t slot_pos[(kNarrowMaxRoutes + 1) * 4];
     const uint2* book = reinterpret_cast<const uint2*>(lds);
     float* red = reinterpret_cast<float*>(lds + KENT * 8);  // [2][KS][64][4]
+    uint2* xs = reinterpret_cast<uint2*>(lds + KENT * 8 + 2 * KS * 64 * 16);  // [4][NSUB]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
     const int type = kk % TYPES;
@@ -86,100 +109,150 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     const int per_type = (gridDim.x / (8 * TYPES)) * 8;
     const int idx = (kk / TYPES) * 8 + x8;  // items of one index run on one XCD for all types
     const ProjDev& P = L.p[proj];
-    const int H = L.H, I = L.I, K = L.K;
+    const int H = L.H, I = L.I, K = L.K, MK = M * K;
 
-    // Loads in the order they are consumed (a wave's vector loads complete in order).
-    // E = 512: 64 lanes x 8 keys, branch-free routing code (moe_uses_narrow checks E).
+    // 1. The routing waves load their row's logits (E = 512: 64 lanes x 8) and wait for them.
+    Q38_STAMP(8192, 0);
     float lg[8];
-    if (wave < M) topk_load_row_t<8, true>(L, B, wave, lg);
-    uint4 fv[NF];
-    const uint4* fsrc = reinterpret_cast<const uint4*>(P.book4 + static_cast<size_t>(chunk) * KENT * 4);
+    if (wave < M) {
+        topk_load_row_t<8, true>(L, B, wave, lg);
 #pragma unroll
-    for (int k = 0; k < NF; ++k) {
-        const int i = tid + k * NT;
-        fv[k] = (KENT / 2) % NT == 0 || i < KENT / 2 ? fsrc[i] : make_uint4(0u, 0u, 0u, 0u);
+        for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(lg[j]));
+        Q38_STAMP(8192, 1);
     }
-    uint2 xb[32];
-    {
-        const int jx = (lane & 3) < M ? (lane & 3) : 0;
-        const uint16_t* xr =
-            B.x16 + static_cast<size_t>(jx) * H + static_cast<size_t>(wave) * 32 * (4 * NCHUNK) + 4 * chunk;
+    lds_barrier();
+    Q38_STAMP(8192, 2);
+    // 2. Every wave requests its share of the chunk's dims of the request rows (two 8-byte
+    //    loads per thread), then the non-routing waves stream the codebook chunk into LDS and
+    //    the routing waves select their row's experts.
+    constexpr int XPT = (kNarrow * NSUB + NT - 1) / NT;
+    uint2 xv[XPT];
 #pragma unroll
-        for (int t = 0; t < 32; ++t) xb[t] = *reinterpret_cast<const uint2*>(xr + t * 4 * NCHUNK);
+    for (int q = 0; q < XPT; ++q) {
+        const int i = tid + q * NT, row = i / NSUB, sv = i % NSUB;
+        const int rr = row < M ? row : 0;
+        xv[q] = *reinterpret_cast<const uint2*>(B.x16 + static_cast<size_t>(rr) * H + sv * (4 * NCHUNK) + 4 * chunk);
     }
-    if (wave < M) topk_select_row_t<8, true>(L, B, wave, lg, tk.ex, blockIdx.x == 0);
-    topk_build_plan(M, K, plan, tk);  // barriers on entry and exit
+    // (a wave's loads complete in order, so the non-routing waves store theirs before
+    // issuing the codebook copy)
+    if (wave < M) topk_select_row_t<8, true>(L, B, wave, lg, ex, blockIdx.x == 0);
+#pragma unroll
+    for (int q = 0; q < XPT; ++q)
+        if (tid + q * NT < kNarrow * NSUB) xs[tid + q * NT] = xv[q];
+    if (wave >= M) dma_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, wave - M, KS - M);
+    Q38_STAMP(8192, 3);
+    // the copy (~1.5 us) is over by the time the routing waves are done
+    wait_vm_all();
+    lds_barrier();
+    // 3. The plan of every row's routes (R3), published by workgroup 0.
+    if (wave == 0) plan_wave(M, K, ex, plan, slot_pos);
+    lds_barrier();
+    Q38_STAMP(8192, 4);
+    if (blockIdx.x == 0)
+        for (int i = tid; i < 2 + 4 * MK; i += NT) B.plan[i] = plan[i];
 
+    // 4. The code spans and row scales of this workgroup's first D items and the B operand
+    //    from LDS (lane 4b + j: the 4 chunk dims of request row j for each of the wave's 32
+    //    subvectors). Item k waits only for its own loads (they complete in order).
     const int tiles = I / 64;
     const int nu = plan[0];
     const int n_items = (nu + (L.has_shared ? 1 : 0)) * tiles;
-    auto code_src = [&](int item) {
-        int expert, n, pos0;
-        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
-        const size_t row = static_cast<size_t>(expert) * I + (item % tiles) * 64 + lane;
-        return P.codes + row * P.words + wave * BITS;
+    const int r_out = (tid >> 2) & 63;  // output role (tid < 256): weight row of the tile
+    const int E = L.E;
+    // (the plan entry is read from LDS before the value select, so that the compiler cannot
+    // turn it into one generic load from either LDS or the kernel arguments)
+    auto item_expert = [&](int item) {
+        const int ui = item / tiles;
+        const int pe = plan[1 + (ui < nu ? ui : 0)];
+        return ui < nu ? pe : E;
     };
-    uint32_t cw[BITS + 1], cn[BITS + 1];
-    if (idx < n_items) load_code_block<BITS>(code_src(idx), cw);
-    uint4* bdst = reinterpret_cast<uint4*>(lds);
+    // This workgroup's items are idx + j * per_type, j < my_n. The loads of items 0..D-1 go
+    // to ring slots 0..D-1, all issued here and unconditionally (slots past the end repeat the
+    // last item, an L2 hit), so the compiler counts them exactly and item k waits only for
+    // its own.
+    const int my_n = n_items > idx ? (n_items - idx + per_type - 1) / per_type : 0;
+    auto load_item = [&](int j, uint32_t* cw, uint32_t& sc) {
+        const int item = my_n > 0 ? idx + (j < my_n ? j : my_n - 1) * per_type : 0;
+        const int expert = item_expert(item);
+        const size_t row = static_cast<size_t>(expert) * I + (item % tiles) * 64;
+        load_code_block<BITS>(P.codes + (row + lane) * P.words + wave * BITS, cw);
+        // the aligned 32-bit word holding the row's fp16 scale (no 16-bit load to widen)
+        sc = *reinterpret_cast<const uint32_t*>(P.scales + ((row + r_out) & ~size_t{1}));
+    };
+    uint32_t cw[D][BITS + 1];
+    uint32_t sc[D];
 #pragma unroll
-    for (int k = 0; k < NF; ++k) {
-        const int i = tid + k * NT;
-        if ((KENT / 2) % NT == 0 || i < KENT / 2) bdst[i] = fv[k];
+    for (int k = 0; k < D; ++k) load_item(k, cw[k], sc[k]);  // (no items: item 0, unused)
+    uint2 xb[32];
+    {
+        const int jx = (lane & 3) < M ? (lane & 3) : 0;
+#pragma unroll
+        for (int t = 0; t < 32; ++t) xb[t] = xs[jx * NSUB + wave * 32 + t];
     }
-    if (blockIdx.x == 0)
-        for (int i = tid; i < 2 + 4 * M * K; i += NT) B.plan[i] = plan[i];
-    __syncthreads();
+    Q38_STAMP(8192, 5);
 
+    // 5. Items. The first D run straight from the ring with no memory instructions between
+    //    them (results stay in registers until all are done), so item k waits only for its
+    //    own loads; items past the ring (more than D per workgroup) take a plain loop.
+    //    Output thread tid < 256: weight row r_out of the tile x request row tid & 3.
     float* out = (proj == 0 ? B.g : B.u) + chunk * B.gu_plane;
-    int buf = 0;
-    for (int item = idx; item < n_items; item += per_type) {
-        if (item + per_type < n_items) load_code_block<BITS>(code_src(item + per_type), cn);
-        const v4f_t acc = slice_mfma<BITS>(cw, book, xb);
+    auto item_compute = [&](int j, const uint32_t* cwj, uint32_t scj, float& ov, int& oat) {
+        const int item = idx + j * per_type;
+        const int buf = j & 1;
+        const v4f_t acc = slice_mfma<BITS>(cwj, book, xb);
         reinterpret_cast<v4f_t*>(red)[(buf * KS + wave) * 64 + lane] = acc;
-        __syncthreads();
+        lds_barrier();  // (the other buffer's readers passed the previous item's barrier)
+        oat = -1;
         if (tid < 64 * kNarrow) {
-            const int r = tid >> 2, j = tid & 3;  // weight row of the tile, request row
-            const int ui = item / tiles;
-            int expert, n, pos0;
-            slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
-            int pos = -1;
-            if (j < M) {
-                if (ui == nu) {
-                    pos = pos0 + j;
-                } else {
-                    for (int p = 0; p < n; ++p)
-                        if (route_row(plan, M, K, pos0, p, false) == j) pos = pos0 + p;
-                }
-            }
+            const int jr = tid & 3;  // request row
+            const int pos = jr < M ? slot_pos[(item / tiles) * 4 + jr] : -1;
             if (pos >= 0) {
-                const int src = (r & ~3) | j, reg = r & 3;
+                const int src = (r_out & ~3) | jr, reg = r_out & 3;
                 float s = 0.0f;
 #pragma unroll
                 for (int w = 0; w < KS; ++w) s += red[((buf * KS + w) * 64 + src) * 4 + reg];
-                const int o = (item % tiles) * 64 + r;
-                out[static_cast<size_t>(pos) * I + o] = h2f(P.scales[static_cast<size_t>(expert) * I + o]) * s;
+                ov = h2f(static_cast<uint16_t>(scj >> (16 * (r_out & 1)))) * s;
+                oat = pos * I + (item % tiles) * 64 + r_out;
             }
         }
-        buf ^= 1;  // the other buffer's readers have passed this item's barrier
+    };
+    float ov[D];
+    int oat[D];
 #pragma unroll
-        for (int i = 0; i <= BITS; ++i) cw[i] = cn[i];
+    for (int k = 0; k < D; ++k) {
+        oat[k] = -1;
+        if (k < my_n) item_compute(k, cw[k], sc[k], ov[k], oat[k]);
+        if (k == 0) Q38_STAMP(8192, 8);
     }
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        if (oat[k] >= 0) out[oat[k]] = ov[k];
+    for (int jj = D; jj < my_n; ++jj) {
+        uint32_t c1[BITS + 1], s1;
+        load_item(jj, c1, s1);
+        float o1;
+        int a1;
+        item_compute(jj, c1, s1, o1, a1);
+        if (a1 >= 0) out[a1] = o1;
+    }
+    Q38_STAMP(8192, 9);
+#ifdef Q38_TRACE
+    if (threadIdx.x == 0) g_trace[8192 + 16 * blockIdx.x + 10] = my_n;
+#endif
 }
 
 // Down projection. Workgroup type = codebook chunk; 8 waves = KS K slices x RG row groups,
 // items are (slot, TR = 64 RG rows of H). The B columns are the slot's routes: their SwiGLU
 // rows (this chunk's dims, fp16) are formed per item from the gate/up chunk planes, which
-// are prefetched one item ahead with the code spans.
-template <int BITS, int NSUB, int NCHUNK>
+// are requested with the item's code spans, D items ahead.
+template <int BITS, int NSUB, int NCHUNK, int D>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_dn4(LayerDev L, MoeBufs B, int M) {
     constexpr int KS = NSUB / 32, RG = 8 / KS, TR = 64 * RG;
     constexpr int NT = 512, KENT = 1 << BITS;
-    constexpr int NF = (KENT / 2 + NT - 1) / NT;
     static_assert(KS * RG == 8, "8 waves");
     static_assert(kNarrow * NSUB <= NT, "one SwiGLU quad per thread");
     extern __shared__ __align__(16) unsigned char lds[];
-    __shared__ int32_t plan[kPlanInts];
+    __shared__ int32_t plan[kNarrowPlan];
     __shared__ __align__(16) uint2 hs[kNarrow][NSUB];  // SwiGLU rows of the item's routes (fp16)
     const uint2* book = reinterpret_cast<const uint2*>(lds);
     float* red = reinterpret_cast<float*>(lds + KENT * 8);  // [RG][KS-1][64][4]
@@ -192,19 +265,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int H = L.H, I = L.I, K = L.K, MK = M * K;
     const int kh = wave % KS, rg = wave / KS;
 
-    int32_t pv = 0;
+    // 1. The plan (written by the gate/up kernel) into LDS, then the codebook chunk loads
+    //    into registers (a wave's loads complete in order: the plan must not queue behind
+    //    them). The chunk is stored to LDS after the item loads below have been issued, so
+    //    every wait is on registers and the compiler counts it exactly.
     const int plan_n = 2 + 4 * MK;
-    if (tid < plan_n) pv = B.plan[tid];
-    uint4 fv[NF];
-    const uint4* fsrc = reinterpret_cast<const uint4*>(P.book4 + static_cast<size_t>(chunk) * KENT * 4);
+    Q38_STAMP(16384, 0);
+    if (tid < plan_n) plan[tid] = B.plan[tid];
+    constexpr int NG = KENT / 2;  // 16-byte granules of the chunk
+    constexpr int NFILL = (NG + NT - 1) / NT;
+    u4_t fv[NFILL];
+    {
+        const u4_t* src = reinterpret_cast<const u4_t*>(P.book4 + static_cast<size_t>(chunk) * KENT * 4);
 #pragma unroll
-    for (int k = 0; k < NF; ++k) {
-        const int i = tid + k * NT;
-        fv[k] = (KENT / 2) % NT == 0 || i < KENT / 2 ? fsrc[i] : make_uint4(0u, 0u, 0u, 0u);
+        for (int q = 0; q < NFILL; ++q) {
+            const int i = tid + q * NT;
+            fv[q] = src[i < NG ? i : NG - 1];
+        }
     }
-    if (tid < plan_n) plan[tid] = pv;
-    __syncthreads();
+    lds_barrier();
+    Q38_STAMP(16384, 1);
 
+    // 2. Code spans and gate/up quads of the first D items.
     const int nu = plan[0];
     const int tiles = H / TR;
     const int n_items = (nu + (L.has_shared ? 1 : 0)) * tiles;
@@ -216,71 +298,126 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         return P.codes + row * P.words + kh * BITS;
     };
     // gate/up chunk-plane quads of SwiGLU element (route tid / NSUB, subvector tid % NSUB)
-    float4 gq[2], uq[2];
-    auto load_gu = [&](int item) {
+    // (loads are unconditional: threads past the slot's routes repeat its last route, so the
+    // compiler counts every load)
+    auto load_gu = [&](int item, float4 (&g)[2], float4 (&u)[2]) {
         int expert, n, pos0;
         slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
-        if (tid < n * NSUB) {
-            const size_t at = static_cast<size_t>(pos0 + tid / NSUB) * I + (tid % NSUB) * (4 * NCHUNK) + 4 * chunk;
-            gq[0] = *reinterpret_cast<const float4*>(B.g + at);
-            uq[0] = *reinterpret_cast<const float4*>(B.u + at);
-            if (two) {
-                gq[1] = *reinterpret_cast<const float4*>(B.g + B.gu_plane + at);
-                uq[1] = *reinterpret_cast<const float4*>(B.u + B.gu_plane + at);
-            }
-        }
+        const int j = tid / NSUB < n ? tid / NSUB : n - 1;
+        const size_t at = static_cast<size_t>(pos0 + j) * I + (tid % NSUB) * (4 * NCHUNK) + 4 * chunk;
+        g[0] = *reinterpret_cast<const float4*>(B.g + at);
+        u[0] = *reinterpret_cast<const float4*>(B.u + at);
+        g[1] = *reinterpret_cast<const float4*>(B.g + (two ? B.gu_plane : 0) + at);
+        u[1] = *reinterpret_cast<const float4*>(B.u + (two ? B.gu_plane : 0) + at);
     };
-    uint32_t cw[BITS + 1], cn[BITS + 1];
-    if (idx < n_items) {
-        load_code_block<BITS>(code_src(idx), cw);
-        load_gu(idx);
-    }
-    uint4* bdst = reinterpret_cast<uint4*>(lds);
+    // row scales of the output lanes (kh == 0): rows (lane & ~3) + 0..3 of the row group
+    auto load_sc = [&](int item, uint2& sc) {
+        const int ui = item / tiles;
+        const int expert = ui < nu ? plan[1 + ui] : L.E;
+        sc = *reinterpret_cast<const uint2*>(P.scales + static_cast<size_t>(expert) * H + (item % tiles) * TR +
+                                             rg * 64 + (lane & ~3));
+    };
+    // Ring of D items as in k_gu4: items j = idx + j * per_type (j < D) in slot j, all loaded
+    // here and unconditionally (past the end: the last item again).
+    const int my_n = n_items > idx ? (n_items - idx + per_type - 1) / per_type : 0;
+    auto item_of = [&](int j) { return my_n > 0 ? idx + (j < my_n ? j : my_n - 1) * per_type : 0; };
+    uint32_t cw[D][BITS + 1];
+    float4 gq[D][2], uq[D][2];
+    uint2 sc[D];
 #pragma unroll
-    for (int k = 0; k < NF; ++k) {
-        const int i = tid + k * NT;
-        if ((KENT / 2) % NT == 0 || i < KENT / 2) bdst[i] = fv[k];
+    for (int k = 0; k < D; ++k) {  // (no items: item 0, unused)
+        const int it = item_of(k);
+        load_code_block<BITS>(code_src(it), cw[k]);
+        load_gu(it, gq[k], uq[k]);
+        load_sc(it, sc[k]);
     }
+#pragma unroll
+    for (int q = 0; q < NFILL; ++q) {
+        const int i = tid + q * NT;
+        if (NG % NT == 0 || i < NG) reinterpret_cast<u4_t*>(lds)[i] = fv[q];
+    }
+    Q38_STAMP(16384, 2);
 
+    // 3. Items: the first D straight from the ring with no memory instructions between them
+    //    (results stay in registers), items past the ring in a plain loop. Output lanes
+    //    (kh == 0): weight rows (lane & ~3) + 0..3 of the row group x route lane & 3.
     float* dout = B.d + chunk * B.d_plane;
-    for (int item = idx; item < n_items; item += per_type) {
+    auto item_compute = [&](int jj, const uint32_t* cwj, const float4 (&g2)[2], const float4 (&u2)[2], uint2 scj,
+                            float (&o4)[4], int& oroute, int& obase) {
+        const int item = idx + jj * per_type;
         int expert, n, pos0;
-        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
+        const int ui = item / tiles;
+        slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
         if (tid < n * NSUB) {
-            float4 g = gq[0], u = uq[0];
+            float4 g = g2[0], u = u2[0];
             if (two) {
-                g = make_float4(g.x + gq[1].x, g.y + gq[1].y, g.z + gq[1].z, g.w + gq[1].w);
-                u = make_float4(u.x + uq[1].x, u.y + uq[1].y, u.z + uq[1].z, u.w + uq[1].w);
+                g = make_float4(g.x + g2[1].x, g.y + g2[1].y, g.z + g2[1].z, g.w + g2[1].w);
+                u = make_float4(u.x + u2[1].x, u.y + u2[1].y, u.z + u2[1].z, u.w + u2[1].w);
             }
             const uint32_t h0 = f2h(swiglu(g.x, u.x)), h1 = f2h(swiglu(g.y, u.y));
             const uint32_t h2 = f2h(swiglu(g.z, u.z)), h3 = f2h(swiglu(g.w, u.w));
             hs[tid / NSUB][tid % NSUB] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
         }
-        if (item + per_type < n_items) {
-            load_code_block<BITS>(code_src(item + per_type), cn);
-            load_gu(item + per_type);
-        }
-        __syncthreads();  // SwiGLU rows (and, the first time, the codebook) in LDS
+        lds_barrier();  // SwiGLU rows (and, the first time, the codebook chunk) in LDS
         const int jb = (lane & 3) < n ? (lane & 3) : 0;
-        v4f_t acc = slice_mfma<BITS>(cw, book, &hs[jb][kh * 32]);
+        uint2 bop[32];
+#pragma unroll
+        for (int t = 0; t < 32; t += 2) {
+            const uint4 v2 = *reinterpret_cast<const uint4*>(&hs[jb][kh * 32 + t]);
+            bop[t] = make_uint2(v2.x, v2.y);
+            bop[t + 1] = make_uint2(v2.z, v2.w);
+        }
+        v4f_t acc = slice_mfma<BITS>(cwj, book, bop);
         if (kh > 0) reinterpret_cast<v4f_t*>(red)[(rg * (KS - 1) + kh - 1) * 64 + lane] = acc;
-        __syncthreads();
+        lds_barrier();  // (the next item's SwiGLU rows are written after this barrier)
+        oroute = -1;
         if (kh == 0) {
 #pragma unroll
-            for (int w = 1; w < KS; ++w) acc += reinterpret_cast<const v4f_t*>(red)[(rg * (KS - 1) + w - 1) * 64 + lane];
-            const int j = lane & 3;
-            if (j < n) {
+            for (int w = 1; w < KS; ++w)
+                acc += reinterpret_cast<const v4f_t*>(red)[(rg * (KS - 1) + w - 1) * 64 + lane];
+            const int jr = lane & 3;
+            if (jr < n) {
+                oroute = ui == nu ? MK + jr : plan[2 + 2 * MK + pos0 + jr];
+                obase = (item % tiles) * TR + rg * 64 + (lane & ~3);
+                const uint16_t s4[4] = {static_cast<uint16_t>(scj.x), static_cast<uint16_t>(scj.x >> 16),
+                                        static_cast<uint16_t>(scj.y), static_cast<uint16_t>(scj.y >> 16)};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int o = (item % tiles) * TR + rg * 64 + (lane & ~3) + r;
-                    dout[static_cast<size_t>(pos0 + j) * H + o] =
-                        h2f(P.scales[static_cast<size_t>(expert) * H + o]) * acc[r];
-                }
+                for (int r = 0; r < 4; ++r) o4[r] = h2f(s4[r]) * acc[r];
             }
         }
+    };
+    float o4[D][4];
+    int oroute[D], obase[D];
 #pragma unroll
-        for (int i = 0; i <= BITS; ++i) cw[i] = cn[i];
+    for (int k = 0; k < D; ++k) {
+        oroute[k] = -1;
+        if (k < my_n) item_compute(k, cw[k], gq[k], uq[k], sc[k], o4[k], oroute[k], obase[k]);
+        if (k == 0) Q38_STAMP(16384, 3);
     }
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        if (oroute[k] >= 0)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dout[static_cast<size_t>(oroute[k]) * H + obase[k] + r] = o4[k][r];
+    for (int jj = D; jj < my_n; ++jj) {
+        const int it = item_of(jj);
+        uint32_t c1[BITS + 1];
+        float4 g1[2], u1[2];
+        uint2 s1;
+        load_code_block<BITS>(code_src(it), c1);
+        load_gu(it, g1, u1);
+        load_sc(it, s1);
+        float p4[4];
+        int rt, bs;
+        item_compute(jj, c1, g1, u1, s1, p4, rt, bs);
+        if (rt >= 0)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dout[static_cast<size_t>(rt) * H + bs + r] = p4[r];
+    }
+    Q38_STAMP(16384, 4);
+#ifdef Q38_TRACE
+    if (threadIdx.x == 0) g_trace[16384 + 16 * blockIdx.x + 10] = my_n;
+#endif
 }
 
 template <typename Kern>
@@ -289,51 +426,86 @@ hipError_t set_lds4(Kern k, size_t bytes) {
                                static_cast<int>(bytes));
 }
 
-template <int BITS, int NSUB, int NCHUNK>
+template <int BITS, int NSUB, int NCHUNK, int D>
 hipError_t launch_gu4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    constexpr size_t lds = (size_t{1} << BITS) * 8 + 2 * (NSUB / 32) * 64 * 16;
+    constexpr size_t lds = gu4_lds_bytes<BITS, NSUB, NCHUNK>();
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = set_lds4(&k_gu4<BITS, NSUB, NCHUNK>, lds);
+        const hipError_t e = set_lds4(&k_gu4<BITS, NSUB, NCHUNK, D>, lds);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    return launch(k_gu4<BITS, NSUB, NCHUNK>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
+    return launch(k_gu4<BITS, NSUB, NCHUNK, D>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
 }
-template <int BITS, int NSUB, int NCHUNK>
+template <int BITS, int NSUB, int NCHUNK, int D>
 hipError_t launch_dn4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     constexpr int KS = NSUB / 32, RG = 8 / KS;
     constexpr size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(RG) * (KS - 1) * 64 * 16;
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = set_lds4(&k_dn4<BITS, NSUB, NCHUNK>, lds);
+        const hipError_t e = set_lds4(&k_dn4<BITS, NSUB, NCHUNK, D>, lds);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    return launch(k_dn4<BITS, NSUB, NCHUNK>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M);
+    return launch(k_dn4<BITS, NSUB, NCHUNK, D>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M);
 }
 } // namespace
 
 bool moe_uses_narrow(const LayerDev& L, int M) {
     if (M < 1 || M > kNarrow || L.E != 512 || !moe_uses_mfma(L)) return false;
+    if (M * L.K > 64) return false;  // the plan is built by one wave
     const int gn = L.H / L.p[0].dim, dn = L.I / L.p[2].dim;
     const bool gu = (L.p[0].dim == 8 && (gn == 256 || gn == 320)) || (L.p[0].dim == 4 && gn == 512);
     const bool dw = (L.p[2].dim == 8 && dn == 64) || (L.p[2].dim == 4 && dn == 128);
     return gu && dw && L.I % 64 == 0 && L.H % 256 == 0;
 }
 
+// Ring depth: the most items one workgroup can get (every route on its own expert, plus the
+// shared expert), so that the item loads are all in flight before the first item; deeper
+// rings cost registers (8 waves: 256 VGPRs a wave; 10 or 16 waves: fewer), so they stop at
+// 6 (4 for the wider workgroups) and further items take the loop.
+static int ring_items(const LayerDev& L, int M, int tiles, int per_type) {
+    return ((M * L.K + 1) * tiles + per_type - 1) / per_type;
+}
+
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const int nsub = L.H / L.p[0].dim;
-    if (L.p[0].dim == 8 && nsub == 256) return launch_gu4_t<14, 256, 2>(L, B, M, st);
-    if (L.p[0].dim == 8 && nsub == 320) return launch_gu4_t<14, 320, 2>(L, B, M, st);
-    if (L.p[0].dim == 4 && nsub == 512) return launch_gu4_t<8, 512, 1>(L, B, M, st);
+    const int grid = mfma_grid();
+    if (L.p[0].dim == 8 && nsub == 256) {
+        const int c = ring_items(L, M, L.I / 64, grid / 32 * 8);
+        if (c <= 2) return launch_gu4_t<14, 256, 2, 2>(L, B, M, st);
+        if (c <= 3) return launch_gu4_t<14, 256, 2, 3>(L, B, M, st);
+        if (c <= 4) return launch_gu4_t<14, 256, 2, 4>(L, B, M, st);
+        return launch_gu4_t<14, 256, 2, 6>(L, B, M, st);
+    }
+    if (L.p[0].dim == 8 && nsub == 320) {
+        const int c = ring_items(L, M, L.I / 64, grid / 32 * 8);
+        if (c <= 2) return launch_gu4_t<14, 320, 2, 2>(L, B, M, st);
+        return launch_gu4_t<14, 320, 2, 4>(L, B, M, st);
+    }
+    if (L.p[0].dim == 4 && nsub == 512) {
+        const int c = ring_items(L, M, L.I / 64, grid / 16 * 8);
+        if (c <= 2) return launch_gu4_t<8, 512, 1, 2>(L, B, M, st);
+        return launch_gu4_t<8, 512, 1, 4>(L, B, M, st);
+    }
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const int nsub = L.I / L.p[2].dim;
-    if (L.p[2].dim == 8 && nsub == 64) return launch_dn4_t<14, 64, 2>(L, B, M, st);
-    if (L.p[2].dim == 4 && nsub == 128) return launch_dn4_t<8, 128, 1>(L, B, M, st);
+    const int grid = mfma_grid();
+    if (L.p[2].dim == 8 && nsub == 64) {
+        const int c = ring_items(L, M, L.H / 256, grid / 16 * 8);
+        if (c <= 1) return launch_dn4_t<14, 64, 2, 1>(L, B, M, st);
+        if (c <= 2) return launch_dn4_t<14, 64, 2, 2>(L, B, M, st);
+        return launch_dn4_t<14, 64, 2, 3>(L, B, M, st);
+    }
+    if (L.p[2].dim == 4 && nsub == 128) {
+        const int c = ring_items(L, M, L.H / 128, grid / 8 * 8);
+        if (c <= 1) return launch_dn4_t<8, 128, 1, 1>(L, B, M, st);
+        if (c <= 2) return launch_dn4_t<8, 128, 1, 2>(L, B, M, st);
+        return launch_dn4_t<8, 128, 1, 3>(L, B, M, st);
+    }
     return hipErrorInvalidValue;
 }
 

@@ -6,8 +6,37 @@
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
 
+// Phase stamps for timing a kernel from the inside: with Q38_TRACE defined (a separate
+// relocatable-device-code build), thread 0 of each workgroup records the 100 MHz real-time
+// counter at a numbered point into q38::g_trace[base + 16 * workgroup + i]; Q38_STAMPV
+// first waits for value v. Without Q38_TRACE they compile to nothing.
+#ifdef Q38_TRACE
+namespace q38 {
+extern __device__ unsigned long long g_trace[32768];
+}
+#define Q38_STAMP(base, i)                                                                                    \
+    do {                                                                                                      \
+        if (threadIdx.x == 0)                                                                                 \
+            ::q38::g_trace[(base) + 16 * (blockIdx.y * gridDim.x + blockIdx.x) + (i)] =                       \
+                __builtin_amdgcn_s_memrealtime();                                                             \
+    } while (0)
+#define Q38_STAMPV(base, i, v)          \
+    do {                                \
+        asm volatile("" ::"v"(v));      \
+        Q38_STAMP(base, i);             \
+    } while (0)
+#else
+#define Q38_STAMP(base, i) \
+    do {                   \
+    } while (0)
+#define Q38_STAMPV(base, i, v) \
+    do {                       \
+    } while (0)
+#endif
+
 namespace q38 {
 
+constexpr int kNarrowMaxRoutes = 64;  // routes of the one-wave plan (4 rows x 16)
 constexpr int kPlanInts = 2 + 4 * kMaxRows * kMaxTopK;
 
 // ============================================================== DPP wave reductions
@@ -190,7 +219,7 @@ __device__ __forceinline__ void topk_build_plan(int M, int K, int32_t* plan, Top
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int waves = blockDim.x >> 6;
     const int MK = M * K;
-    __syncthreads();
+    lds_barrier();
     if (tid < MK) {
         const int my_e = t.ex[tid];
         const int my_key = (my_e << 8) | tid;
@@ -200,11 +229,11 @@ __device__ __forceinline__ void topk_build_plan(int M, int K, int32_t* plan, Top
         plan[2 + 2 * MK + pos] = tid;   // route_list
         plan[2 + 3 * MK + tid] = pos;   // route_pos
     }
-    __syncthreads();
+    lds_barrier();
     const bool start = tid < MK && (tid == 0 || t.sorted_e[tid - 1] != t.sorted_e[tid]);
     const uint64_t bal = __ballot(start);
     if (lane == 0) t.wave_cnt[wave] = __popcll(bal);
-    __syncthreads();
+    lds_barrier();
     int rank = __popcll(bal & ((1ull << lane) - 1ull));
     for (int w = 0; w < wave; ++w) rank += t.wave_cnt[w];
     if (start) {
@@ -217,7 +246,7 @@ __device__ __forceinline__ void topk_build_plan(int M, int K, int32_t* plan, Top
         plan[0] = nu;
         plan[1 + MK + nu] = MK;
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Rows are taken by waves [row_wave0, waves); the other waves may do unrelated work
@@ -232,6 +261,116 @@ __device__ __forceinline__ void topk_plan_block(const LayerDev& L, const MoeBufs
         topk_select_row(L, B, r, lg, t.ex, global_out);
     }
     topk_build_plan(M, L.K, plan, t);
+}
+
+// Gather-by-expert plan (R3) of up to 4 rows x K <= 16 routes over E <= 512 experts, built
+// by one whole wave without loops over the routes (every lane calls it). ex: [M*K] expert
+// ids in route order (route i = row * K + slot; the experts of one row are distinct). Same
+// layout as topk_build_plan: routes sorted by (expert, route index), unique experts
+// ascending. Lane 16 r + w builds the 32-bit mask of row r's experts in [32 w, 32 w + 32)
+// and the exclusive prefix count of row r's experts below 32 w (a DPP scan within the 16-lane
+// row); the union of the rows' masks gives the unique-expert ranks the same way. Route i
+// (row r, expert e) then sits at sorted position #{routes with expert < e} + #{rows r' < r
+// that chose e}, and opens its expert's group when no earlier row chose e. slot_pos, when
+// given ([65][4] ints), receives the sorted position of row r's route in unique slot u at
+// [4 u + r] (-1 where row r did not choose that expert; slot nu: the shared expert).
+__device__ __forceinline__ uint32_t row_scan_incl(uint32_t x) {  // inclusive scan in 16-lane rows
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x111, 0xF, 0xF, false));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x112, 0xF, 0xF, false));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x114, 0xF, 0xF, false));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x118, 0xF, 0xF, false));
+    return x;
+}
+__device__ __forceinline__ void plan_wave(int M, int K, const int32_t* ex, int32_t* plan, int32_t* slot_pos = nullptr) {
+    const int lane = threadIdx.x & 63;
+    const int MK = M * K;
+    if (slot_pos)
+        for (int i = lane; i < (kNarrowMaxRoutes + 1) * 4; i += 64) slot_pos[i] = -1;
+    // 1. row masks: lane 16 r + w
+    const int mr = lane >> 4, mw = lane & 15;
+    uint32_t m = 0;
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s) {  // slots past K repeat slot K - 1 (same bits)
+        const int e = ex[(mr < M ? mr : 0) * K + (s < K ? s : K - 1)];
+        m |= (e >> 5) == mw ? 1u << (e & 31) : 0u;
+    }
+    if (mr >= M) m = 0;
+    const uint32_t pc = static_cast<uint32_t>(__popc(m));
+    const uint32_t pref = row_scan_incl(pc) - pc;  // row mr's experts below 32 mw
+    // 2. union of the rows' masks (every row of lanes ends with U[w]) and its prefix counts
+    uint32_t u = m | static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 16, 64));
+    u |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(u), 32, 64));
+    const uint32_t uc = static_cast<uint32_t>(__popc(u));
+    const uint32_t upref = row_scan_incl(uc) - uc;
+    const int nu = static_cast<int>(__builtin_amdgcn_readlane(static_cast<int>(upref + uc), 15));
+    // 3. one lane per route
+    const bool act = lane < MK;
+    const int e = act ? ex[lane] : 0;
+    const int r = (lane >= K ? 1 : 0) + (lane >= 2 * K ? 1 : 0) + (lane >= 3 * K ? 1 : 0);
+    const int w = e >> 5, b = e & 31;
+    const uint32_t low = (1u << b) - 1u;
+    int below = 0, rank = 0;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        const uint32_t mk = static_cast<uint32_t>(__shfl(static_cast<int>(m), rr * 16 + w, 64));
+        const uint32_t pk = static_cast<uint32_t>(__shfl(static_cast<int>(pref), rr * 16 + w, 64));
+        if (rr < M) {
+            below += static_cast<int>(pk) + __popc(mk & low);
+            rank += (rr < r && ((mk >> b) & 1u)) ? 1 : 0;
+        }
+    }
+    const uint32_t uw = static_cast<uint32_t>(__shfl(static_cast<int>(u), w, 64));
+    const uint32_t upw = static_cast<uint32_t>(__shfl(static_cast<int>(upref), w, 64));
+    const int pos = below + rank;
+    const int urank = static_cast<int>(upw) + __popc(uw & low);
+    if (act) {
+        plan[2 + 2 * MK + pos] = lane;  // route at sorted position pos
+        plan[2 + 3 * MK + lane] = pos;  // sorted position of route lane
+        if (rank == 0) {
+            plan[1 + urank] = e;
+            plan[1 + MK + urank] = pos;
+        }
+        if (slot_pos) slot_pos[urank * 4 + r] = pos;
+    }
+    if (lane == 0) {
+        plan[0] = nu;
+        plan[1 + MK + nu] = MK;
+    }
+    if (slot_pos && lane < M) slot_pos[nu * 4 + lane] = MK + lane;  // the shared expert's slot
+}
+
+// The route index of sorted position pos (shared-expert rows, pos >= MK, keep theirs).
+__device__ __forceinline__ int route_of_pos(const int32_t* plan, int MK, int pos) {
+    return pos < MK ? plan[2 + 2 * MK + pos] : pos;
+}
+
+// Codebook chunk -> LDS over the direct global-to-LDS path (no VGPR staging): waves
+// w = 0..nw-1 of the caller copy KENT * 8 bytes, 1 KiB per wave instruction. The data is in
+// LDS once the issuing wave's vmcnt drains; wait for that before the barrier that
+// publishes it.
+// The same copy by all NW waves of the workgroup with a compile-time instruction count per
+// wave (unrolled), so the compiler can count the copy's vmcnt events exactly.
+template <int KENT, int NW>
+__device__ __forceinline__ void dma_book_all(const uint16_t* src4, unsigned char* lds) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint4* src = reinterpret_cast<const uint4*>(src4);
+    constexpr int N = KENT / 2;
+    constexpr int PER = (N + 64 * NW - 1) / (64 * NW);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = (k * NW + w) * 64;
+        if (N % (64 * NW) == 0 || i < N)
+            __builtin_amdgcn_global_load_lds(src + i + lane, reinterpret_cast<uint4*>(lds) + i, 16, 0, 0);
+    }
+}
+
+template <int KENT>
+__device__ __forceinline__ void dma_book(const uint16_t* src4, unsigned char* lds, int w, int nw) {
+    const int lane = threadIdx.x & 63;
+    const uint4* src = reinterpret_cast<const uint4*>(src4);
+    constexpr int N = KENT / 2;  // 16-byte granules
+    for (int i = w * 64; i < N; i += nw * 64)
+        __builtin_amdgcn_global_load_lds(src + i + lane, reinterpret_cast<uint4*>(lds) + i, 16, 0, 0);
 }
 
 // Rows of unique-expert slot ui: the routed experts in ascending id, then the shared

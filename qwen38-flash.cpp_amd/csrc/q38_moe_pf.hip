@@ -243,9 +243,11 @@ __device__ __forceinline__ void pf_pass(const ProjDev& P, int expert, int OUT, i
 }
 
 // D lane (c16 = l % 16, q = l / 16) register r of acc[i]: row 16 wave + 4q + r, route
-// 64 (i / 4) + 16 (i % 4) + c16 of the pass; out row = sorted position pos0 + p0 + route.
+// 64 (i / 4) + 16 (i % 4) + c16 of the pass; out row = sorted position pos0 + p0 + route, or
+// that position's route index when rplan (the plan) is given (the down projection).
 __device__ __forceinline__ void pf_store(const ProjDev& P, int expert, int OUT, int o0, int p0, int np, int pos0,
-                                         const f4_t (&acc)[4 * kPfChunks], float* out) {
+                                         const f4_t (&acc)[4 * kPfChunks], float* out, const int32_t* rplan = nullptr,
+                                         int MK = 0) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, c16 = lane & 15, q = lane >> 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -254,7 +256,10 @@ __device__ __forceinline__ void pf_store(const ProjDev& P, int expert, int OUT, 
 #pragma unroll
         for (int i = 0; i < 4 * kPfChunks; ++i) {
             const int j = (i >> 2) * kPfRoutes + (i & 3) * 16 + c16;
-            if (j < np) out[static_cast<size_t>(pos0 + p0 + j) * OUT + o] = sc * acc[i][r];
+            if (j < np) {
+                const int row = pos0 + p0 + j;
+                out[static_cast<size_t>(rplan ? route_of_pos(rplan, MK, row) : row) * OUT + o] = sc * acc[i][r];
+            }
         }
     }
 }
@@ -313,7 +318,7 @@ __global__ __launch_bounds__(256) void k_dn_pf(LayerDev L, MoeBufs B, int M) {
         pf_pass(P, expert, L.H, L.I, o0, np, As, Bs, acc, [&](int kb, int ch, Tile* Bt) {
             stage_rows(B.h16, L.I, kb, ch, np, Bt, [&](int j) { return pos0 + p0 + j; });
         });
-        pf_store(P, expert, L.H, o0, p0, np, pos0, acc, B.d);
+        pf_store(P, expert, L.H, o0, p0, np, pos0, acc, B.d, B.plan, M * L.K);
     }
 }
 
