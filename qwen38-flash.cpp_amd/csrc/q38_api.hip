@@ -171,12 +171,21 @@ static void fill_dev(q38_moe_layer* L, const q38_moe_weights* w) {
     v.d_parts = mfma ? d.down_dim / 4 : 1;
 }
 
-// Codebooks split into 4-dim chunks ([dim/4][entries][4]) for the LDS-resident MFMA path.
+// Codebooks split into 4-dim chunks ([dim/4][entries][4]) for the LDS-resident MFMA path,
+// and, for layers the four-row verify kernels serve, the codes in the tiled layout those
+// kernels load from (one more copy of the codes: HBM traded for coalesced loads).
 static int prepare_layer(q38_moe_layer* L) {
-    size_t total = 0, off[3];
+    size_t total = 0, off[3], toff[3];
+    const bool tiled = moe_uses_narrow(L->dev, 1);
     for (int p = 0; p < 3; ++p) {
         off[p] = total;
         total += align256((static_cast<size_t>(1) << L->dev.p[p].bits) * L->dev.p[p].dim * 2);
+    }
+    int64_t rows[3] = {0, 0, 0};
+    for (int p = 0; p < 3 && tiled; ++p) {
+        rows[p] = static_cast<int64_t>(L->desc.experts + 1) * (p < 2 ? L->desc.inter : L->desc.hidden);
+        toff[p] = total;
+        total += align256(static_cast<size_t>(rows[p]) * L->dev.p[p].words * 4);
     }
     char* base = nullptr;
     if (hipMalloc(&base, total) != hipSuccess) return fail(Q38_ENOMEM, "hipMalloc failed for prepared codebooks");
@@ -185,6 +194,12 @@ static int prepare_layer(q38_moe_layer* L) {
         auto* dst = reinterpret_cast<uint16_t*>(base + off[p]);
         e = launch_split_book(L->dev.p[p].book, 1 << L->dev.p[p].bits, L->dev.p[p].dim, dst, nullptr);
         L->dev.p[p].book4 = dst;
+        L->dev.p[p].codes_t = nullptr;
+        if (tiled && e == hipSuccess) {
+            auto* ct = reinterpret_cast<uint32_t*>(base + toff[p]);
+            e = launch_tile_codes(L->dev.p[p].codes, rows[p], L->dev.p[p].words, L->dev.p[p].bits, ct, nullptr);
+            L->dev.p[p].codes_t = ct;
+        }
     }
     if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
     if (e != hipSuccess) {

@@ -29,11 +29,13 @@ __device__ __forceinline__ void lds_barrier_dma_pending() { asm volatile("s_wait
 
 // ------------------------------------------------------------------ number formats
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+// Round to nearest even; NaN keeps its sign and top mantissa bits and becomes quiet. Written
+// as a value select (no branch): every float store of the kernels goes through it.
 __device__ __forceinline__ uint16_t f2bf(float f) {
-    uint32_t x = __float_as_uint(f);
-    if ((x & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((x >> 16) | 0x40u);
-    x += 0x7fffu + ((x >> 16) & 1u);
-    return static_cast<uint16_t>(x >> 16);
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t rounded = (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
+    const uint32_t quiet = (x >> 16) | 0x40u;
+    return static_cast<uint16_t>((x & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 __device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }

@@ -41,6 +41,11 @@ struct ProjDev {
     int words, ngrp, dim, bits;
     const int8_t* book_i8;   // [2^bits, dim] int8 codebook (value = q * book_scale), or null
     float book_scale;
+    // The codes again, tiled for the verify kernels (or null): 64-row tiles of the flattened
+    // [experts * OUT] rows; per (tile, 32-code block) the 64 rows' BITS words are stored as
+    // chunks of 4 words (the last chunk BITS % 4 wide when not 0) with the 64 rows
+    // interleaved inside each chunk, so one 16-byte load per lane reads 1 KiB contiguously.
+    const uint32_t* codes_t;
 };
 
 // Workspace views of one MoE call (rows <= kMaxRows).
@@ -98,6 +103,8 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st);
 hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_t* book4, hipStream_t st);
+// codes [rows, words] (rows a multiple of 64) -> the tiled layout of ProjDev::codes_t
+hipError_t launch_tile_codes(const uint32_t* codes, int64_t rows, int words, int bits, uint32_t* out, hipStream_t st);
 bool moe_uses_mfma(const LayerDev& L);
 // Verify widths of up to 4 rows on the 4x4x4 MFMA kernels (q38_moe4.hip).
 bool moe_uses_narrow(const LayerDev& L, int M);

@@ -174,11 +174,14 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
 #pragma unroll
             for (int i = 0; i < 4; ++i) ss[r] = fmaf(v[r][i], v[r][i], ss[r]);
         }
+        Q38_STAMPV(0, 4, ss[MR - 1]);
         wave_sum_xor_n<MR>(ss);
 #pragma unroll
         for (int r = 0; r < MR; ++r)
             if (lane == 0) red[r][wave] = ss[r];
+        Q38_STAMPV(0, 5, ss[MR - 1]);
         lds_barrier();
+        Q38_STAMP(0, 6);
 #pragma unroll
         for (int r = 0; r < MR; ++r)
             if (r < M) {
@@ -196,6 +199,7 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
                     }
                 }
             }
+        Q38_STAMP(0, 7);
     } else {
         const uint4* s4 = reinterpret_cast<const uint4*>(src);
         for (int i = tid; i < M * H / 8; i += NT) {
@@ -750,6 +754,27 @@ __global__ void k_split_book(const uint16_t* __restrict__ book, int entries, int
     }
 }
 
+// Tiled copy of packed codes (the layout of ProjDev::codes_t): one thread per (64-row tile,
+// 32-code block, row of the tile).
+__global__ void k_tile_codes(const uint32_t* __restrict__ codes, int64_t n_tiles, int words, int bits,
+                             uint32_t* __restrict__ out) {
+    const int nblk = words / bits;
+    const int64_t total = n_tiles * nblk * 64;
+    for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
+         t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int lane = static_cast<int>(t % 64);
+        const int64_t tw = t / 64;
+        const int w = static_cast<int>(tw % nblk);
+        const int64_t tile = tw / nblk;
+        const uint32_t* src = codes + (tile * 64 + lane) * words + static_cast<int64_t>(w) * bits;
+        uint32_t* blk = out + (tile * nblk + w) * bits * 64;
+        for (int q = 0; q < bits; ++q) {
+            const int c = q / 4, cw = bits - 4 * c < 4 ? bits - 4 * c : 4;
+            blk[c * 256 + lane * cw + q % 4] = src[q];
+        }
+    }
+}
+
 // ============================================================== launchers
 namespace {
 int next_pow2(int v) {
@@ -990,6 +1015,12 @@ hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* 
 
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st) {
     hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, st, x, H, eps, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_codes(const uint32_t* codes, int64_t rows, int words, int bits, uint32_t* out, hipStream_t st) {
+    if (rows % 64 || words % bits) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_tile_codes, dim3(4096), dim3(256), 0, st, codes, rows / 64, words, bits, out);
     return hipGetLastError();
 }
 

@@ -35,24 +35,24 @@ typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 constexpr int kNarrow = 4;  // input rows per instruction (the B columns)
 constexpr int kNarrowPlan = 2 + 4 * kNarrow * kMaxTopK;
 
-// One 32-code block (BITS words) plus a zero pad word for code_from.
+// One 32-code block (BITS words) of the lane's row plus a zero pad word for code_from, from
+// the tiled copy (ProjDev::codes_t): blk is the (64-row tile, block) base; chunk c holds
+// words 4c.. of the 64 rows interleaved, so each load is contiguous across the wave.
 template <int BITS>
-__device__ __forceinline__ void load_code_block(const uint32_t* src, uint32_t* w) {
-    if constexpr (BITS % 4 == 0) {
+__device__ __forceinline__ void load_code_block_tiled(const uint32_t* blk, int lane, uint32_t* w) {
 #pragma unroll
-        for (int i = 0; i < BITS / 4; ++i) {
-            const uint4 v = reinterpret_cast<const uint4*>(src)[i];
-            w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    for (int c = 0; c < (BITS + 3) / 4; ++c) {
+        const int cw = BITS - 4 * c < 4 ? BITS - 4 * c : 4;
+        const uint32_t* src = blk + c * 256 + lane * cw;
+        if (cw == 4) {
+            const uint4 v = *reinterpret_cast<const uint4*>(src);
+            w[4 * c] = v.x; w[4 * c + 1] = v.y; w[4 * c + 2] = v.z; w[4 * c + 3] = v.w;
+        } else if (cw == 2) {
+            const uint2 v = *reinterpret_cast<const uint2*>(src);
+            w[4 * c] = v.x; w[4 * c + 1] = v.y;
+        } else {
+            for (int i = 0; i < cw; ++i) w[4 * c + i] = src[i];
         }
-    } else if constexpr (BITS % 2 == 0) {
-#pragma unroll
-        for (int i = 0; i < BITS / 2; ++i) {
-            const uint2 v = reinterpret_cast<const uint2*>(src)[i];
-            w[2 * i] = v.x; w[2 * i + 1] = v.y;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < BITS; ++i) w[i] = src[i];
     }
     w[BITS] = 0;
 }
@@ -82,12 +82,16 @@ __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)
 // row scale, at the route's sorted position (the gate/up chunk planes).
 // One workgroup per CU (the LDS codebook chunk), so a SIMD runs at most ceil(waves / 4)
 // of its waves: the register budget is set by that, not by a higher occupancy target.
-// LDS: codebook chunk [KENT][4] fp16, cross-wave partial sums [2][KS][64][4] f32, the
-// chunk's dims of the request rows [4][NSUB][4] fp16.
+// LDS: codebook chunk [KENT][4] fp16, cross-wave partial sums [2][KS][64][4] f32; before
+// the items, the chunk's dims of the request rows [4][NSUB][4] fp16 and the routing waves'
+// top-k candidates [4][64] u64 share the partial-sum area.
+// (the x staging and the routing waves' candidate lists live inside the partial-sum area,
+// which the items use only after both are consumed)
 template <int BITS, int NSUB, int NCHUNK>
 constexpr size_t gu4_lds_bytes() {
-    return (size_t{1} << BITS) * 8 + 2 * (NSUB / 32) * 64 * 16 + kNarrow * NSUB * 8;
+    return (size_t{1} << BITS) * 8 + 2 * (NSUB / 32) * 64 * 16;
 }
+
 template <int BITS, int NSUB, int NCHUNK, int D>
 __global__ __launch_bounds__(2 * NSUB) __attribute__((amdgpu_waves_per_eu(1, (NSUB / 32 + 3) / 4)))
 void k_gu4(LayerDev L, MoeBufs B, int M) {
@@ -99,9 +103,11 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     __shared__ int32_t ex[kNarrowMaxRoutes];
     __shared__ int32_t plan[kNarrowPlan];
     __shared__ int32_t slot_pos[(kNarrowMaxRoutes + 1) * 4];
+    static_assert(kNarrow * NSUB * 8 + kNarrow * 64 * 8 <= 2 * KS * 64 * 16, "staging fits the partial sums");
     const uint2* book = reinterpret_cast<const uint2*>(lds);
     float* red = reinterpret_cast<float*>(lds + KENT * 8);  // [2][KS][64][4]
-    uint2* xs = reinterpret_cast<uint2*>(lds + KENT * 8 + 2 * KS * 64 * 16);  // [4][NSUB]
+    uint2* xs = reinterpret_cast<uint2*>(lds + KENT * 8);                       // [4][NSUB], in red
+    uint64_t* cand = reinterpret_cast<uint64_t*>(lds + KENT * 8 + kNarrow * NSUB * 8);  // [4][64], in red
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
     const int type = kk % TYPES;
@@ -135,7 +141,7 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     }
     // (a wave's loads complete in order, so the non-routing waves store theirs before
     // issuing the codebook copy)
-    if (wave < M) topk_select_row_t<8, true>(L, B, wave, lg, ex, blockIdx.x == 0);
+    if (wave < M) topk_select_row_fast<8>(L, B, wave, lg, ex, blockIdx.x == 0, cand + 64 * wave);
 #pragma unroll
     for (int q = 0; q < XPT; ++q)
         if (tid + q * NT < kNarrow * NSUB) xs[tid + q * NT] = xv[q];
@@ -175,7 +181,7 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
         const int item = my_n > 0 ? idx + (j < my_n ? j : my_n - 1) * per_type : 0;
         const int expert = item_expert(item);
         const size_t row = static_cast<size_t>(expert) * I + (item % tiles) * 64;
-        load_code_block<BITS>(P.codes + (row + lane) * P.words + wave * BITS, cw);
+        load_code_block_tiled<BITS>(P.codes_t + ((row >> 6) * KS + wave) * (BITS * 64), lane, cw);
         // the aligned 32-bit word holding the row's fp16 scale (no 16-bit load to widen)
         sc = *reinterpret_cast<const uint32_t*>(P.scales + ((row + r_out) & ~size_t{1}));
     };
@@ -189,6 +195,7 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
 #pragma unroll
         for (int t = 0; t < 32; ++t) xb[t] = xs[jx * NSUB + wave * 32 + t];
     }
+    lds_barrier();  // every wave has its B operand before the items overwrite the staging
     Q38_STAMP(8192, 5);
 
     // 5. Items. The first D run straight from the ring with no memory instructions between
@@ -250,7 +257,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     constexpr int KS = NSUB / 32, RG = 8 / KS, TR = 64 * RG;
     constexpr int NT = 512, KENT = 1 << BITS;
     static_assert(KS * RG == 8, "8 waves");
-    static_assert(kNarrow * NSUB <= NT, "one SwiGLU quad per thread");
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int32_t plan[kNarrowPlan];
     __shared__ __align__(16) uint2 hs[kNarrow][NSUB];  // SwiGLU rows of the item's routes (fp16)
@@ -291,24 +297,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int tiles = H / TR;
     const int n_items = (nu + (L.has_shared ? 1 : 0)) * tiles;
     const bool two = L.gu_parts == 2;
-    auto code_src = [&](int item) {
+    auto code_src = [&](int item) {  // this wave's (64-row tile, block) in the tiled codes
         int expert, n, pos0;
         slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
-        const size_t row = static_cast<size_t>(expert) * H + (item % tiles) * TR + rg * 64 + lane;
-        return P.codes + row * P.words + kh * BITS;
+        const size_t row0 = static_cast<size_t>(expert) * H + (item % tiles) * TR + rg * 64;
+        return P.codes_t + ((row0 >> 6) * KS + kh) * (BITS * 64);
     };
-    // gate/up chunk-plane quads of SwiGLU element (route tid / NSUB, subvector tid % NSUB)
-    // (loads are unconditional: threads past the slot's routes repeat its last route, so the
-    // compiler counts every load)
-    auto load_gu = [&](int item, float4 (&g)[2], float4 (&u)[2]) {
+    // Gate/up chunk-plane values of the SwiGLU elements this thread forms: element e = tid
+    // + 512 q (q < GQ) of the slot's n routes x NSUB subvectors x 4 chunk dims (route e /
+    // (4 NSUB), subvector e / 4 % NSUB, dim e % 4). Loads are unconditional: elements past
+    // the slot's routes repeat its last element, so the compiler counts every load.
+    constexpr int GQ = (kNarrow * NSUB * 4 + NT - 1) / NT;
+    auto load_gu = [&](int item, float (&g)[GQ][2], float (&u)[GQ][2]) {
         int expert, n, pos0;
         slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
-        const int j = tid / NSUB < n ? tid / NSUB : n - 1;
-        const size_t at = static_cast<size_t>(pos0 + j) * I + (tid % NSUB) * (4 * NCHUNK) + 4 * chunk;
-        g[0] = *reinterpret_cast<const float4*>(B.g + at);
-        u[0] = *reinterpret_cast<const float4*>(B.u + at);
-        g[1] = *reinterpret_cast<const float4*>(B.g + (two ? B.gu_plane : 0) + at);
-        u[1] = *reinterpret_cast<const float4*>(B.u + (two ? B.gu_plane : 0) + at);
+#pragma unroll
+        for (int q = 0; q < GQ; ++q) {
+            const int e = tid + NT * q < n * NSUB * 4 ? tid + NT * q : n * NSUB * 4 - 1;
+            const size_t at = static_cast<size_t>(pos0 + e / (4 * NSUB)) * I + (e / 4 % NSUB) * (4 * NCHUNK) +
+                              4 * chunk + (e & 3);
+            g[q][0] = B.g[at];
+            u[q][0] = B.u[at];
+            g[q][1] = B.g[(two ? B.gu_plane : 0) + at];
+            u[q][1] = B.u[(two ? B.gu_plane : 0) + at];
+        }
     };
     // row scales of the output lanes (kh == 0): rows (lane & ~3) + 0..3 of the row group
     auto load_sc = [&](int item, uint2& sc) {
@@ -322,12 +334,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int my_n = n_items > idx ? (n_items - idx + per_type - 1) / per_type : 0;
     auto item_of = [&](int j) { return my_n > 0 ? idx + (j < my_n ? j : my_n - 1) * per_type : 0; };
     uint32_t cw[D][BITS + 1];
-    float4 gq[D][2], uq[D][2];
+    float gq[D][GQ][2], uq[D][GQ][2];
     uint2 sc[D];
 #pragma unroll
     for (int k = 0; k < D; ++k) {  // (no items: item 0, unused)
         const int it = item_of(k);
-        load_code_block<BITS>(code_src(it), cw[k]);
+        load_code_block_tiled<BITS>(code_src(it), lane, cw[k]);
         load_gu(it, gq[k], uq[k]);
         load_sc(it, sc[k]);
     }
@@ -342,21 +354,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     //    (results stay in registers), items past the ring in a plain loop. Output lanes
     //    (kh == 0): weight rows (lane & ~3) + 0..3 of the row group x route lane & 3.
     float* dout = B.d + chunk * B.d_plane;
-    auto item_compute = [&](int jj, const uint32_t* cwj, const float4 (&g2)[2], const float4 (&u2)[2], uint2 scj,
-                            float (&o4)[4], int& oroute, int& obase) {
+    auto item_compute = [&](int jj, const uint32_t* cwj, const float (&g2)[GQ][2], const float (&u2)[GQ][2],
+                            uint2 scj, float (&o4)[4], int& oroute, int& obase) {
         const int item = idx + jj * per_type;
         int expert, n, pos0;
         const int ui = item / tiles;
         slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
-        if (tid < n * NSUB) {
-            float4 g = g2[0], u = u2[0];
-            if (two) {
-                g = make_float4(g.x + g2[1].x, g.y + g2[1].y, g.z + g2[1].z, g.w + g2[1].w);
-                u = make_float4(u.x + u2[1].x, u.y + u2[1].y, u.z + u2[1].z, u.w + u2[1].w);
+#pragma unroll
+        for (int q = 0; q < GQ; ++q) {
+            const int e = tid + NT * q;
+            if (e < n * NSUB * 4) {
+                const float g = two ? g2[q][0] + g2[q][1] : g2[q][0];
+                const float u = two ? u2[q][0] + u2[q][1] : u2[q][0];
+                reinterpret_cast<uint16_t*>(&hs[0][0])[e] = f2h(swiglu(g, u));
             }
-            const uint32_t h0 = f2h(swiglu(g.x, u.x)), h1 = f2h(swiglu(g.y, u.y));
-            const uint32_t h2 = f2h(swiglu(g.z, u.z)), h3 = f2h(swiglu(g.w, u.w));
-            hs[tid / NSUB][tid % NSUB] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
         }
         lds_barrier();  // SwiGLU rows (and, the first time, the codebook chunk) in LDS
         const int jb = (lane & 3) < n ? (lane & 3) : 0;
@@ -402,9 +413,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     for (int jj = D; jj < my_n; ++jj) {
         const int it = item_of(jj);
         uint32_t c1[BITS + 1];
-        float4 g1[2], u1[2];
+        float g1[GQ][2], u1[GQ][2];
         uint2 s1;
-        load_code_block<BITS>(code_src(it), c1);
+        load_code_block_tiled<BITS>(code_src(it), lane, c1);
         load_gu(it, g1, u1);
         load_sc(it, s1);
         float p4[4];
@@ -470,6 +481,7 @@ static int ring_items(const LayerDev& L, int M, int tiles, int per_type) {
 
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const int nsub = L.H / L.p[0].dim;
+    if (!L.p[0].codes_t || !L.p[1].codes_t) return hipErrorInvalidValue;
     const int grid = mfma_grid();
     if (L.p[0].dim == 8 && nsub == 256) {
         const int c = ring_items(L, M, L.I / 64, grid / 32 * 8);
@@ -493,6 +505,7 @@ hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream
 
 hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const int nsub = L.I / L.p[2].dim;
+    if (!L.p[2].codes_t) return hipErrorInvalidValue;
     const int grid = mfma_grid();
     if (L.p[2].dim == 8 && nsub == 64) {
         const int c = ring_items(L, M, L.H / 256, grid / 16 * 8);

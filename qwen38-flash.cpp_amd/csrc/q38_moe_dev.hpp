@@ -124,15 +124,13 @@ __device__ __forceinline__ void topk_load_row(const LayerDev& L, const MoeBufs& 
     topk_load_row_t<16, false>(L, B, r, lg);
 }
 
-// Softmax (exp contract, double denominator) and top-k of one row by one wave, for
-// E <= 64 * NJ experts. Keys (p bits << 32 | ~index) are unique; each lane sorts its NJ keys
-// (bitonic network), then K rounds take the DPP wave maximum of the lane heads and the
-// winning lane advances its list, which yields the keys in (p desc, index asc) order.
+// Softmax (exp contract, double denominator) of one row by one wave, for E <= 64 * NJ
+// experts (lane l: experts 64j + l): keys (p bits << 32 | ~index), unique, ordered as (p
+// desc, index asc); experts past E get key 0.
 template <int NJ, bool EXACT>
-__device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
-                                                  int32_t* ex_lds, bool global_out) {
+__device__ __forceinline__ void topk_keys_t(const LayerDev& L, const float* lg, uint64_t* key) {
     const int lane = threadIdx.x & 63;
-    const int K = L.K, nj = EXACT ? NJ : L.E / 64;
+    const int nj = EXACT ? NJ : L.E / 64;
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) mx = fmaxf(mx, lg[j]);
@@ -148,7 +146,6 @@ __device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBu
         }
     }
     ds = wave_sum_xor(ds);
-    uint64_t key[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         key[j] = 0;
@@ -158,6 +155,31 @@ __device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBu
                      static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(64 * j + lane));
         }
     }
+}
+
+// Rank-ordered outputs of one row: lane s < K holds the s-th key (weight p / sum of the
+// selected p in rank order when normalising).
+__device__ __forceinline__ void topk_write_row(const LayerDev& L, const MoeBufs& B, int r, int32_t* ex_lds,
+                                               bool global_out, float psel, int isel, float sum) {
+    const int lane = threadIdx.x & 63;
+    const int K = L.K;
+    if (lane < K) {
+        if (ex_lds) ex_lds[r * K + lane] = isel;
+        if (global_out) {
+            B.experts[r * K + lane] = isel;
+            B.weights[r * K + lane] = L.normalize ? psel / sum : psel;
+        }
+    }
+}
+
+// Top-k by tournament: each lane sorts its NJ keys (bitonic network), then K rounds take the
+// DPP wave maximum of the lane heads and the winning lane advances its list, which yields the
+// keys in (p desc, index asc) order. key[] is consumed.
+template <int NJ>
+__device__ __forceinline__ void topk_tournament(const LayerDev& L, const MoeBufs& B, int r, uint64_t* key,
+                                                int32_t* ex_lds, bool global_out) {
+    const int lane = threadIdx.x & 63;
+    const int K = L.K;
 #pragma unroll
     for (int k = 2; k <= NJ; k <<= 1) {
 #pragma unroll
@@ -200,13 +222,98 @@ __device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBu
             isel = static_cast<int>(0xFFFFFFFFu - wlo);
         }
     }
-    if (lane < K) {
-        if (ex_lds) ex_lds[r * K + lane] = isel;
-        if (global_out) {
-            B.experts[r * K + lane] = isel;
-            B.weights[r * K + lane] = L.normalize ? psel / sum : psel;
-        }
+    topk_write_row(L, B, r, ex_lds, global_out, psel, isel, sum);
+}
+
+template <int NJ, bool EXACT>
+__device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
+                                                  int32_t* ex_lds, bool global_out) {
+    uint64_t key[NJ];
+    topk_keys_t<NJ, EXACT>(L, lg, key);
+    topk_tournament<NJ>(L, B, r, key, ex_lds, global_out);
+}
+
+// One step of a bitonic sort of one u64 key per lane (64 lanes, descending overall): the
+// lower lane of each pair keeps the larger key in a descending block of KB lanes.
+template <int KB, int J>
+__device__ __forceinline__ uint64_t wave_bitonic_step(uint64_t key, int lane) {
+    const uint64_t other = (static_cast<uint64_t>(xor_lane<J>(static_cast<uint32_t>(key >> 32))) << 32) |
+                           xor_lane<J>(static_cast<uint32_t>(key));
+    const bool keep_max = ((lane & J) == 0) == ((lane & KB) == 0);
+    const bool gt = other > key;
+    return keep_max == gt ? other : key;
+}
+__device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t key) {
+    const int lane = threadIdx.x & 63;
+    key = wave_bitonic_step<2, 1>(key, lane);
+    key = wave_bitonic_step<4, 2>(key, lane);
+    key = wave_bitonic_step<4, 1>(key, lane);
+    key = wave_bitonic_step<8, 4>(key, lane);
+    key = wave_bitonic_step<8, 2>(key, lane);
+    key = wave_bitonic_step<8, 1>(key, lane);
+    key = wave_bitonic_step<16, 8>(key, lane);
+    key = wave_bitonic_step<16, 4>(key, lane);
+    key = wave_bitonic_step<16, 2>(key, lane);
+    key = wave_bitonic_step<16, 1>(key, lane);
+    key = wave_bitonic_step<32, 16>(key, lane);
+    key = wave_bitonic_step<32, 8>(key, lane);
+    key = wave_bitonic_step<32, 4>(key, lane);
+    key = wave_bitonic_step<32, 2>(key, lane);
+    key = wave_bitonic_step<32, 1>(key, lane);
+    key = wave_bitonic_step<64, 32>(key, lane);
+    key = wave_bitonic_step<64, 16>(key, lane);
+    key = wave_bitonic_step<64, 8>(key, lane);
+    key = wave_bitonic_step<64, 4>(key, lane);
+    key = wave_bitonic_step<64, 2>(key, lane);
+    key = wave_bitonic_step<64, 1>(key, lane);
+    return key;
+}
+
+// The same top-k (E = 512, K <= 64) with a short dependent chain. T = the K-th largest p
+// word among the lane maxima, found bit by bit with ballot counts, is a lower bound of the
+// K-th largest key's p word (the K largest lane maxima are K distinct keys). The keys whose
+// p word is >= T, typically little more than K of them, are compacted through cand (64 u64
+// of this wave's LDS) and sorted across the wave with one bitonic network; lanes 0..K-1
+// then hold the top K in (p desc, index asc) order. More than 64 candidates (many equal p
+// words) take the tournament. The selection and the rank-order weight sum equal
+// topk_select_row_t's bit for bit.
+template <int NJ>
+__device__ __forceinline__ void topk_select_row_fast(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
+                                                     int32_t* ex_lds, bool global_out, uint64_t* cand) {
+    const int lane = threadIdx.x & 63;
+    const int K = L.K;
+    uint64_t key[NJ];
+    topk_keys_t<NJ, true>(L, lg, key);
+    uint64_t lm = key[0];
+#pragma unroll
+    for (int j = 1; j < NJ; ++j) lm = key[j] > lm ? key[j] : lm;
+    const uint32_t mh = static_cast<uint32_t>(lm >> 32);
+    uint32_t t = 0;  // p words are those of floats in [0, 1]: below 2^30
+#pragma unroll
+    for (int b = 29; b >= 0; --b) {
+        const uint32_t c = t | (1u << b);
+        if (__popcll(__ballot(mh >= c)) >= K) t = c;
     }
+    const uint64_t lt = (1ull << lane) - 1ull;
+    int total = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const bool in = static_cast<uint32_t>(key[j] >> 32) >= t;
+        const uint64_t bj = __ballot(in);
+        const int at = total + __popcll(bj & lt);
+        if (in && at < 64) cand[at] = key[j];
+        total += __popcll(bj);
+    }
+    if (total > 64) {
+        topk_tournament<NJ>(L, B, r, key, ex_lds, global_out);
+        return;
+    }
+    const uint64_t ck = wave_sort_desc_u64(lane < total ? cand[lane] : 0ull);
+    const uint32_t pbits = static_cast<uint32_t>(ck >> 32);
+    float sum = 0.0f;
+    for (int s = 0; s < K; ++s) sum += __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pbits), s)));
+    topk_write_row(L, B, r, ex_lds, global_out, __uint_as_float(pbits),
+                   static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck)), sum);
 }
 __device__ __forceinline__ void topk_select_row(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
                                                 int32_t* ex_lds, bool global_out) {

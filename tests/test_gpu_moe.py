@@ -108,3 +108,20 @@ def test_invalid_shapes_rejected(layer0, q38):
     assert rc == q38.Q38_ESPACE
     rc = q38.lib.q38_moe_forward(layer0.h, x.data_ptr(), 4, x.data_ptr(), None, ws.data_ptr(), ws.numel(), G.stream())
     assert rc == q38.Q38_EINVAL
+
+
+@pytest.mark.parametrize("H,I,M", [(2560, 512, 4), (2560, 512, 1), (2560, 640, 4)])
+def test_hidden_2560_layers(gpu, q38, orc, H, I, M):
+    """The reference family's hidden size: 2560 x 512 takes the four-row MFMA kernels with
+    320-subvector K slices (10 waves), 2560 x 640 the general path; both against the oracle."""
+    L = q38.MoeLayer(gpu, q38.desc(hidden=H, inter=I), seed=SEED, layer=7)
+    try:
+        x = orc.normal(orc.key(SEED, 7, 20), 31 * M, M * H, 1.0).reshape(M, H)
+        y, ex, wt, lg, plan = run_forward(q38, L, L.desc, x)
+        wy, wex, wwt, wlg = orc.moe_layer_synth(oracle_lib.make_desc(hidden=H, inter=I), SEED, 7, x)
+        assert np.array_equal(lg, wlg), "router logits"
+        assert np.array_equal(ex, wex) and np.array_equal(wt, wwt), "routing"
+        plan_check(orc, plan, ex, 512)
+        tol_check(orc, y, wy)
+    finally:
+        L.close()
