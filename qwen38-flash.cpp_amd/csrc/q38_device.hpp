@@ -102,10 +102,12 @@ __device__ __forceinline__ uint32_t code_from(const uint32_t* w, int q) {
 // ------------------------------------------------------------------ exp contract
 // Cody-Waite reduction + degree-7 Taylor polynomial, evaluated with explicit fmaf so the
 // float operations are identical to the CPU restatement; results below 2^-125 flush to 0.
+// Branch-free: the argument is clamped (NaN included) before the reduction and the flush
+// is a final select, so a wave never splits.
 __device__ __forceinline__ float exp_contract(float d) {
-    if (!(d > -87.0f)) return 0.0f;
-    const float kf = rintf(d * 1.44269504088896341f);
-    float r = __builtin_fmaf(kf, -0.693145751953125f, d);
+    const float dc = __builtin_fmaxf(d, -88.0f);
+    const float kf = rintf(dc * 1.44269504088896341f);
+    float r = __builtin_fmaf(kf, -0.693145751953125f, dc);
     r = __builtin_fmaf(kf, -1.42860682030941723212e-06f, r);
     float p = 1.0f / 5040.0f;
     p = __builtin_fmaf(p, r, 1.0f / 720.0f);
@@ -116,8 +118,8 @@ __device__ __forceinline__ float exp_contract(float d) {
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
     const int k = static_cast<int>(kf);
-    if (k < -125) return 0.0f;
-    return ldexpf(p, k);
+    const float v = ldexpf(p, k);
+    return d > -87.0f && k >= -125 ? v : 0.0f;
 }
 
 // ------------------------------------------------------------------ wave reductions
@@ -125,8 +127,7 @@ __device__ __forceinline__ float exp_contract(float d) {
 // ((l, l^32), then ^16, ...) that the CPU restatement reproduces.
 // Value of lane l ^ M. M = 1, 2: DPP quad permutations; M = 4, 8: a row shift for the
 // lanes whose bit is clear and the opposite shift for the others (bank masks select the
-// lanes, every source lies in the same row); M = 16: ds_swizzle xor mode (32-lane groups);
-// M = 32: lane permute.
+// lanes, every source lies in the same row); M = 16, 32: permlane swaps (no LDS round trip).
 template <int M>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
     if constexpr (M == 1) {
@@ -139,10 +140,13 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
                                                   false);
         return static_cast<uint32_t>(
             __builtin_amdgcn_update_dpp(t, static_cast<int>(v), 0x110 + M, 0xF, 0xF ^ lo_banks, false));
-    } else if constexpr (M == 16) {
-        return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), (16 << 10) | 0x1F));
     } else {
-        return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), M, kWave));
+        // M = 16, 32: the gfx950 lane swaps. With both operands v, the first result holds the
+        // lower 16-lane row (32-lane half) of each pair in both rows (halves) and the second
+        // the upper one, so lane l takes the one that is not its own.
+        const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(v, v, false, false)
+                               : __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (threadIdx.x & M) ? r[0] : r[1];
     }
 }
 template <int M>

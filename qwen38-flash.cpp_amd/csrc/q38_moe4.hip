@@ -118,10 +118,16 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     const int H = L.H, I = L.I, K = L.K, MK = M * K;
 
     // 1. The routing waves load their row's logits (E = 512: 64 lanes x 8) and wait for them.
+    //    Behind the logits they touch one word per 128-byte line of a share of the down
+    //    projection's codebook (same geometry; the workgroups of an XCD cover it), so the
+    //    down kernel's chunk fills find it in the XCD's L2. The words are dropped.
     Q38_STAMP(8192, 0);
     float lg[8];
+    uint32_t warm = 0;
     if (wave < M) {
         topk_load_row_t<8, true>(L, B, wave, lg);
+        constexpr int kLines = NCHUNK * KENT * 8 / 128;
+        warm = reinterpret_cast<const uint32_t*>(L.p[2].book4)[(((kk * M + wave) * 64 + lane) % kLines) * 32];
 #pragma unroll
         for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(lg[j]));
         Q38_STAMP(8192, 1);
@@ -147,12 +153,14 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
         if (tid + q * NT < kNarrow * NSUB) xs[tid + q * NT] = xv[q];
     if (wave >= M) dma_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, wave - M, KS - M);
     Q38_STAMP(8192, 3);
-    // the copy (~1.5 us) is over by the time the routing waves are done
+    // 3. The plan of every row's routes (R3), published by workgroup 0. Wave 0 (a routing
+    //    wave: no copy of its own in flight) builds it while the copy finishes; the barrier
+    //    before it waits for LDS writes only, the one after it for every wave's copy too.
+    lds_barrier_dma_pending();
+    if (wave == 0) plan_wave(M, K, ex, plan, slot_pos);
     wait_vm_all();
     lds_barrier();
-    // 3. The plan of every row's routes (R3), published by workgroup 0.
-    if (wave == 0) plan_wave(M, K, ex, plan, slot_pos);
-    lds_barrier();
+    asm volatile("" ::"v"(warm));
     Q38_STAMP(8192, 4);
     if (blockIdx.x == 0)
         for (int i = tid; i < 2 + 4 * MK; i += NT) B.plan[i] = plan[i];
@@ -172,10 +180,9 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
         const int pe = plan[1 + (ui < nu ? ui : 0)];
         return ui < nu ? pe : E;
     };
-    // This workgroup's items are idx + j * per_type, j < my_n. The loads of items 0..D-1 go
-    // to ring slots 0..D-1, all issued here and unconditionally (slots past the end repeat the
-    // last item, an L2 hit), so the compiler counts them exactly and item k waits only for
-    // its own.
+    // This workgroup's items are idx + j * per_type, j < my_n. Their loads are issued
+    // unconditionally (past the end: the last item again, an L2 hit), so the compiler counts
+    // them exactly and item k waits only for its own.
     const int my_n = n_items > idx ? (n_items - idx + per_type - 1) / per_type : 0;
     auto load_item = [&](int j, uint32_t* cw, uint32_t& sc) {
         const int item = my_n > 0 ? idx + (j < my_n ? j : my_n - 1) * per_type : 0;
@@ -185,10 +192,11 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
         // the aligned 32-bit word holding the row's fp16 scale (no 16-bit load to widen)
         sc = *reinterpret_cast<const uint32_t*>(P.scales + ((row + r_out) & ~size_t{1}));
     };
-    uint32_t cw[D][BITS + 1];
-    uint32_t sc[D];
+    constexpr int PF = D < 3 ? D : 3;  // items in flight
+    uint32_t cw[PF][BITS + 1];
+    uint32_t sc[PF];
 #pragma unroll
-    for (int k = 0; k < D; ++k) load_item(k, cw[k], sc[k]);  // (no items: item 0, unused)
+    for (int k = 0; k < PF; ++k) load_item(k, cw[k], sc[k]);  // (no items: item 0, unused)
     uint2 xb[32];
     {
         const int jx = (lane & 3) < M ? (lane & 3) : 0;
@@ -198,9 +206,11 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     lds_barrier();  // every wave has its B operand before the items overwrite the staging
     Q38_STAMP(8192, 5);
 
-    // 5. Items. The first D run straight from the ring with no memory instructions between
-    //    them (results stay in registers until all are done), so item k waits only for its
-    //    own loads; items past the ring (more than D per workgroup) take a plain loop.
+    // 5. Items. The first D run as straight-line code over a ring of PF slots: item k's
+    //    compute, then the loads of item k + PF into its slot (unconditional, clamped), with
+    //    no other memory instruction in between (results stay in registers until all D are
+    //    done), so item k waits only for its own loads while later items stream in behind
+    //    the compute. Items past D (more per workgroup than the launch planned) take a loop.
     //    Output thread tid < 256: weight row r_out of the tile x request row tid & 3.
     float* out = (proj == 0 ? B.g : B.u) + chunk * B.gu_plane;
     auto item_compute = [&](int j, const uint32_t* cwj, uint32_t scj, float& ov, int& oat) {
@@ -228,7 +238,8 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
 #pragma unroll
     for (int k = 0; k < D; ++k) {
         oat[k] = -1;
-        if (k < my_n) item_compute(k, cw[k], sc[k], ov[k], oat[k]);
+        if (k < my_n) item_compute(k, cw[k % PF], sc[k % PF], ov[k], oat[k]);
+        if (k + PF < D) load_item(k + PF, cw[k % PF], sc[k % PF]);
         if (k == 0) Q38_STAMP(8192, 8);
     }
 #pragma unroll
@@ -329,20 +340,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         sc = *reinterpret_cast<const uint2*>(P.scales + static_cast<size_t>(expert) * H + (item % tiles) * TR +
                                              rg * 64 + (lane & ~3));
     };
-    // Ring of D items as in k_gu4: items j = idx + j * per_type (j < D) in slot j, all loaded
-    // here and unconditionally (past the end: the last item again).
+    // Items j = idx + j * per_type (j < my_n); loads are unconditional (past the end: the last
+    // item again) so the compiler counts them exactly.
     const int my_n = n_items > idx ? (n_items - idx + per_type - 1) / per_type : 0;
     auto item_of = [&](int j) { return my_n > 0 ? idx + (j < my_n ? j : my_n - 1) * per_type : 0; };
-    uint32_t cw[D][BITS + 1];
-    float gq[D][GQ][2], uq[D][GQ][2];
-    uint2 sc[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) {  // (no items: item 0, unused)
-        const int it = item_of(k);
+    constexpr int PF = D;  // items in flight (all: the item loads are the ones that wait longest)
+    uint32_t cw[PF][BITS + 1];
+    float gq[PF][GQ][2], uq[PF][GQ][2];
+    uint2 sc[PF];
+    auto load_slot = [&](int j, int k) {
+        const int it = item_of(j);
         load_code_block_tiled<BITS>(code_src(it), lane, cw[k]);
         load_gu(it, gq[k], uq[k]);
         load_sc(it, sc[k]);
-    }
+    };
+#pragma unroll
+    for (int k = 0; k < PF; ++k) load_slot(k, k);  // (no items: item 0, unused)
 #pragma unroll
     for (int q = 0; q < NFILL; ++q) {
         const int i = tid + q * NT;
@@ -350,9 +363,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     }
     Q38_STAMP(16384, 2);
 
-    // 3. Items: the first D straight from the ring with no memory instructions between them
-    //    (results stay in registers), items past the ring in a plain loop. Output lanes
-    //    (kh == 0): weight rows (lane & ~3) + 0..3 of the row group x route lane & 3.
+    // 3. Items: the first D as straight-line code over a ring of PF slots (as in k_gu4: item
+    //    k's compute, then item k + PF's loads into its slot; results stay in registers),
+    //    items past D in a plain loop. Output lanes (kh == 0): weight rows (lane & ~3) +
+    //    0..3 of the row group x route lane & 3.
     float* dout = B.d + chunk * B.d_plane;
     auto item_compute = [&](int jj, const uint32_t* cwj, const float (&g2)[GQ][2], const float (&u2)[GQ][2],
                             uint2 scj, float (&o4)[4], int& oroute, int& obase) {
@@ -402,7 +416,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
     for (int k = 0; k < D; ++k) {
         oroute[k] = -1;
-        if (k < my_n) item_compute(k, cw[k], gq[k], uq[k], sc[k], o4[k], oroute[k], obase[k]);
+        if (k < my_n) item_compute(k, cw[k % PF], gq[k % PF], uq[k % PF], sc[k % PF], o4[k], oroute[k], obase[k]);
+        if (k + PF < D) load_slot(k + PF, k % PF);
         if (k == 0) Q38_STAMP(16384, 3);
     }
 #pragma unroll

@@ -233,50 +233,16 @@ __device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBu
     topk_tournament<NJ>(L, B, r, key, ex_lds, global_out);
 }
 
-// One step of a bitonic sort of one u64 key per lane (64 lanes, descending overall): the
-// lower lane of each pair keeps the larger key in a descending block of KB lanes.
-template <int KB, int J>
-__device__ __forceinline__ uint64_t wave_bitonic_step(uint64_t key, int lane) {
-    const uint64_t other = (static_cast<uint64_t>(xor_lane<J>(static_cast<uint32_t>(key >> 32))) << 32) |
-                           xor_lane<J>(static_cast<uint32_t>(key));
-    const bool keep_max = ((lane & J) == 0) == ((lane & KB) == 0);
-    const bool gt = other > key;
-    return keep_max == gt ? other : key;
-}
-__device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t key) {
-    const int lane = threadIdx.x & 63;
-    key = wave_bitonic_step<2, 1>(key, lane);
-    key = wave_bitonic_step<4, 2>(key, lane);
-    key = wave_bitonic_step<4, 1>(key, lane);
-    key = wave_bitonic_step<8, 4>(key, lane);
-    key = wave_bitonic_step<8, 2>(key, lane);
-    key = wave_bitonic_step<8, 1>(key, lane);
-    key = wave_bitonic_step<16, 8>(key, lane);
-    key = wave_bitonic_step<16, 4>(key, lane);
-    key = wave_bitonic_step<16, 2>(key, lane);
-    key = wave_bitonic_step<16, 1>(key, lane);
-    key = wave_bitonic_step<32, 16>(key, lane);
-    key = wave_bitonic_step<32, 8>(key, lane);
-    key = wave_bitonic_step<32, 4>(key, lane);
-    key = wave_bitonic_step<32, 2>(key, lane);
-    key = wave_bitonic_step<32, 1>(key, lane);
-    key = wave_bitonic_step<64, 32>(key, lane);
-    key = wave_bitonic_step<64, 16>(key, lane);
-    key = wave_bitonic_step<64, 8>(key, lane);
-    key = wave_bitonic_step<64, 4>(key, lane);
-    key = wave_bitonic_step<64, 2>(key, lane);
-    key = wave_bitonic_step<64, 1>(key, lane);
-    return key;
-}
-
-// The same top-k (E = 512, K <= 64) with a short dependent chain. T = the K-th largest p
-// word among the lane maxima, found bit by bit with ballot counts, is a lower bound of the
-// K-th largest key's p word (the K largest lane maxima are K distinct keys). The keys whose
-// p word is >= T, typically little more than K of them, are compacted through cand (64 u64
-// of this wave's LDS) and sorted across the wave with one bitonic network; lanes 0..K-1
-// then hold the top K in (p desc, index asc) order. More than 64 candidates (many equal p
-// words) take the tournament. The selection and the rank-order weight sum equal
-// topk_select_row_t's bit for bit.
+// The same top-k (E = 512, K <= 64) with a short dependent chain, by counting instead of
+// sorting the keys. T = the K-th largest p word among the 64 lane maxima is a lower bound of
+// the K-th largest key's p word (the K largest lane maxima are K distinct keys); so is T
+// with its low bits cleared, which a bitwise search with ballot counts finds. The keys whose
+// p word is >= that bound, typically a few more than K, are compacted into cand; each
+// candidate's rank is the number of larger candidates (keys are unique) and a lane permute
+// sends it to lane rank, so lanes 0..K-1 hold the top K in (p desc, index asc) order. More
+// than 64 candidates (many equal p words) take the tournament. The selection and the
+// rank-order weight sum equal topk_select_row_t's bit for bit. cand: 64 u64 of this wave's
+// LDS.
 template <int NJ>
 __device__ __forceinline__ void topk_select_row_fast(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
                                                      int32_t* ex_lds, bool global_out, uint64_t* cand) {
@@ -284,16 +250,20 @@ __device__ __forceinline__ void topk_select_row_fast(const LayerDev& L, const Mo
     const int K = L.K;
     uint64_t key[NJ];
     topk_keys_t<NJ, true>(L, lg, key);
+    Q38_STAMPV(8192, 11, static_cast<uint32_t>(key[0]));
     uint64_t lm = key[0];
 #pragma unroll
     for (int j = 1; j < NJ; ++j) lm = key[j] > lm ? key[j] : lm;
     const uint32_t mh = static_cast<uint32_t>(lm >> 32);
-    uint32_t t = 0;  // p words are those of floats in [0, 1]: below 2^30
+    // p words are those of floats in [0, 1]: below 2^30. Bits 29..17 only: T is then
+    // within ~1/32 of the K-th lane maximum, and the chain is 13 ballots.
+    uint32_t t = 0;
 #pragma unroll
-    for (int b = 29; b >= 0; --b) {
+    for (int b = 29; b >= 17; --b) {
         const uint32_t c = t | (1u << b);
         if (__popcll(__ballot(mh >= c)) >= K) t = c;
     }
+    Q38_STAMPV(8192, 12, t);
     const uint64_t lt = (1ull << lane) - 1ull;
     int total = 0;
 #pragma unroll
@@ -308,12 +278,27 @@ __device__ __forceinline__ void topk_select_row_fast(const LayerDev& L, const Mo
         topk_tournament<NJ>(L, B, r, key, ex_lds, global_out);
         return;
     }
-    const uint64_t ck = wave_sort_desc_u64(lane < total ? cand[lane] : 0ull);
-    const uint32_t pbits = static_cast<uint32_t>(ck >> 32);
+    // zero keys pad the list to a multiple of 16 (a zero key is below every real one); a
+    // wave's LDS operations complete in order, so the reads below see every write
+    const int total16 = (total + 15) & ~15;
+    if (lane >= total && lane < total16) cand[lane] = 0;
+    const uint64_t mine = lane < total ? cand[lane] : 0ull;
+    int rank = 0;
+    for (int i = 0; i < total16; i += 16) {
+        ulonglong2 c[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) c[q] = *reinterpret_cast<const ulonglong2*>(cand + i + 2 * q);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) rank += (c[q].x > mine) + (c[q].y > mine);
+    }
+    // candidates go to lane rank, the other lanes keep their own slot (a bijection)
+    const int dst = (lane < total ? rank : lane) * 4;
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_ds_permute(dst, static_cast<int>(mine >> 32)));
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_ds_permute(dst, static_cast<int>(mine)));
+    Q38_STAMPV(8192, 13, hi);
     float sum = 0.0f;
-    for (int s = 0; s < K; ++s) sum += __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pbits), s)));
-    topk_write_row(L, B, r, ex_lds, global_out, __uint_as_float(pbits),
-                   static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck)), sum);
+    for (int s = 0; s < K; ++s) sum += __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(hi), s)));
+    topk_write_row(L, B, r, ex_lds, global_out, __uint_as_float(hi), static_cast<int>(0xFFFFFFFFu - lo), sum);
 }
 __device__ __forceinline__ void topk_select_row(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
                                                 int32_t* ex_lds, bool global_out) {
