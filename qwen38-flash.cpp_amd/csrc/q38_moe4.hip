@@ -117,40 +117,36 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     const ProjDev& P = L.p[proj];
     const int H = L.H, I = L.I, K = L.K, MK = M * K;
 
-    // 1. The routing waves load their row's logits (E = 512: 64 lanes x 8) and wait for them.
-    //    Behind the logits they touch one word per 128-byte line of a share of the down
-    //    projection's codebook (same geometry; the workgroups of an XCD cover it), so the
-    //    down kernel's chunk fills find it in the XCD's L2. The words are dropped.
+    // 1. The routing waves load their row's logits (E = 512: 64 lanes x 8), behind them their
+    //    row's dims of the chunk (NSUB / 64 8-byte loads per lane) and one word per 128-byte
+    //    line of a share of the down projection's codebook (same geometry; the workgroups of
+    //    an XCD cover it, so the down kernel's chunk fills find it in the XCD's L2; the words
+    //    are dropped), wait for the logits only, select their row's experts and stage their
+    //    row's chunk dims. The non-routing waves skip that block and copy the codebook chunk
+    //    into LDS at once (the copy's block comes second, so no copy is pending in the code
+    //    of the routing waves as the compiler sees it).
+    static_assert(NSUB % 64 == 0, "whole 64-lane passes over the subvectors");
+    constexpr int XPW = NSUB / 64;
     Q38_STAMP(8192, 0);
-    float lg[8];
     uint32_t warm = 0;
     if (wave < M) {
+        float lg[8];
+        uint2 xv[XPW];
         topk_load_row_t<8, true>(L, B, wave, lg);
+#pragma unroll
+        for (int q = 0; q < XPW; ++q)
+            xv[q] = *reinterpret_cast<const uint2*>(B.x16 + static_cast<size_t>(wave) * H +
+                                                    (lane + 64 * q) * (4 * NCHUNK) + 4 * chunk);
         constexpr int kLines = NCHUNK * KENT * 8 / 128;
         warm = reinterpret_cast<const uint32_t*>(L.p[2].book4)[(((kk * M + wave) * 64 + lane) % kLines) * 32];
 #pragma unroll
         for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(lg[j]));
         Q38_STAMP(8192, 1);
-    }
-    lds_barrier();
-    Q38_STAMP(8192, 2);
-    // 2. Every wave requests its share of the chunk's dims of the request rows (two 8-byte
-    //    loads per thread), then the non-routing waves stream the codebook chunk into LDS and
-    //    the routing waves select their row's experts.
-    constexpr int XPT = (kNarrow * NSUB + NT - 1) / NT;
-    uint2 xv[XPT];
+        Q38_STAMP(8192, 2);
+        topk_select_row_fast<8>(L, B, wave, lg, ex, blockIdx.x == 0, cand + 64 * wave);
 #pragma unroll
-    for (int q = 0; q < XPT; ++q) {
-        const int i = tid + q * NT, row = i / NSUB, sv = i % NSUB;
-        const int rr = row < M ? row : 0;
-        xv[q] = *reinterpret_cast<const uint2*>(B.x16 + static_cast<size_t>(rr) * H + sv * (4 * NCHUNK) + 4 * chunk);
+        for (int q = 0; q < XPW; ++q) xs[wave * NSUB + lane + 64 * q] = xv[q];
     }
-    // (a wave's loads complete in order, so the non-routing waves store theirs before
-    // issuing the codebook copy)
-    if (wave < M) topk_select_row_fast<8>(L, B, wave, lg, ex, blockIdx.x == 0, cand + 64 * wave);
-#pragma unroll
-    for (int q = 0; q < XPT; ++q)
-        if (tid + q * NT < kNarrow * NSUB) xs[tid + q * NT] = xv[q];
     if (wave >= M) dma_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, wave - M, KS - M);
     Q38_STAMP(8192, 3);
     // 3. The plan of every row's routes (R3), published by workgroup 0. Wave 0 (a routing
