@@ -214,17 +214,23 @@ def main():
     uniq = [int(p[0].item()) for p in plans]
     nl = len(layers)
     MK = M * K
-    # algorithmic bytes per launch (per-expert figures of the packed layout: gate/up codes
-    # 2 x 512 rows x 448 B, down 2048 rows x 112 B, one fp16 scale per row; fp16 d8 codebooks)
+    # algorithmic bytes per launch: the weights a launch must read once (per-expert figures
+    # of the packed layout: gate/up codes 2 x 512 rows x 448 B, down 2048 rows x 112 B, one
+    # fp16 scale per row; the fp16 d8 codebooks once per launch, not once per CU) plus the
+    # activations it reads and writes as designed (gate/up partial sums and down outputs are
+    # two fp32 chunk planes per route, the router writes x as bf16 and fp16).
     book = 16384 * 8 * 2
-    gu_bytes = sum((u + 1) * (2 * I * 448 + 2 * I * 2) + 2 * book + M * H * 2 + (MK + M) * I * 2 for u in uniq) / nl
-    dn_bytes = sum((u + 1) * (H * 112 + H * 2) + book + (MK + M) * I * 2 + M * H * 2 for u in uniq) / nl
-    rt_bytes = E * H * 2 + H * 2 + M * H * 2 + M * E * 4
-    mg_bytes = (MK + M) * H * 2 + 2 * M * H * 2 + M * H * 2 * 2
-    kernels = {"k_gu4 (gate/up, top-k, plan)": (tm.gate_up_ms, gu_bytes),
+    routes = MK + M  # routed + shared
+    gu_bytes = sum((u + 1) * (2 * I * 448 + 2 * I * 2) + 2 * book + M * E * 4 + M * H * 2 + 2 * 2 * routes * I * 4
+                   for u in uniq) / nl
+    dn_bytes = sum((u + 1) * (H * 112 + H * 2) + book + 2 * 2 * routes * I * 4 + 2 * routes * H * 4
+                   for u in uniq) / nl
+    rt_bytes = E * H * 2 + H * 2 + M * H * 2 + 2 * M * H * 2 + M * (E + 1) * 4
+    mg_bytes = 2 * routes * H * 4 + M * K * 4 + M * 4 + 2 * M * H * 2
+    kernels = {"k_gu4 (top-k, plan, gate/up)": (tm.gate_up_ms, gu_bytes),
                "k_dn4 (SwiGLU, down)": (tm.down_ms, dn_bytes),
-               "k_logits (router)": (tm.routing_ms, rt_bytes),
-               "k_combine_norm (reduce, residual, RMSNorm)": (tm.merge_ms, mg_bytes)}
+               "k_route_norm (RMSNorm, router logits)": (tm.routing_ms, rt_bytes),
+               "k_combine (route-order reduce, shared gate, residual)": (tm.merge_ms, mg_bytes)}
     dom = max(kernels, key=lambda k: kernels[k][0])
     dom_us = 1e3 * kernels[dom][0] / nl
     dom_bytes = kernels[dom][1]

@@ -13,14 +13,16 @@
 // Each workgroup keeps one 4-dim chunk of one codebook in LDS for the whole launch and
 // walks its share of (expert slot, tile) items. The kernels are built around the latency
 // chain of a verify layer:
-//   k_gu4  the routing waves (one per request row) load only their logits, so nothing else
-//          queues ahead of them; once the logits are in, the other waves stream the
-//          codebook chunk into LDS over the direct global-to-LDS path while the routing
-//          waves run softmax + top-k; one wave turns the rows' experts into the plan, and
-//          every wave then issues the code spans of all its items (a ring of D in flight).
-//   k_dn4  the plan is read first; the codebook chunk (into registers) and the code spans,
-//          gate/up partial sums and scales of the first D items follow as soon as the plan is
-//          in LDS; the chunk is stored to LDS behind them.
+//   k_gu4  the non-routing waves start the codebook chunk's copy into LDS (the direct
+//          global-to-LDS path) at kernel entry; the routing waves (one per request row)
+//          load their logits, their row's chunk dims and a share of the down codebook's
+//          lines (so the down kernel finds them in L2), and run softmax + top-k as soon as
+//          the logits are in; wave 0 turns the rows' experts into the plan while the copy
+//          finishes; then every wave walks its items over a ring of three in flight (item
+//          k computes, then item k + 3's code spans are requested into its slot).
+//   k_dn4  the plan is read first; the codebook chunk (into registers) follows at once and
+//          the code spans, gate/up partial sums and scales of the first D items as soon as
+//          the plan is in LDS; the chunk is stored to LDS behind them.
 //          Down outputs are written at the route index (request row * k + slot; the
 //          shared expert's rows after the routed ones), so the combine needs no plan.
 #include "q38_moe_dev.hpp"
