@@ -27,6 +27,23 @@ __device__ __forceinline__ void lds_barrier() {
 // written with ds_* instructions may be read after it.
 __device__ __forceinline__ void lds_barrier_dma_pending() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// ------------------------------------------------------------------ kernel arguments
+// Kernel arguments are read through the scalar cache on first use, so an argument line
+// first needed deep inside a kernel costs a memory round trip at that point. This reads one
+// dword of every 64-byte line of the first BYTES bytes at kernel entry: the reads are issued
+// together and waited for once, and every later argument read hits.
+template <int BYTES>
+__device__ __forceinline__ void touch_kernargs() {
+    typedef const __attribute__((address_space(4))) uint32_t karg_t;
+    karg_t* ka = (karg_t*)(__builtin_amdgcn_kernarg_segment_ptr());
+    constexpr int kLines = (BYTES + 63) / 64;
+    uint32_t v[kLines];
+#pragma unroll
+    for (int i = 0; i < kLines; ++i) v[i] = ka[16 * i];
+#pragma unroll
+    for (int i = 0; i < kLines; ++i) asm volatile("" ::"s"(v[i]));
+}
+
 // ------------------------------------------------------------------ number formats
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 // Round to nearest even; NaN keeps its sign and top mantissa bits and becomes quiet. Written

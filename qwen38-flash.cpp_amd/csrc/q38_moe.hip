@@ -141,6 +141,7 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
     constexpr int H = 512 * T, NT = 128 * T, NW = NT / 64;
     extern __shared__ __align__(16) uint16_t xs[];  // [M][H] bf16
     __shared__ float red[MR][NW];
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + 2 * sizeof(void*) + sizeof(float)>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nr = L.E + (L.has_shared ? 1 : 0);
     const int e = blockIdx.x * NW + wave;
@@ -149,15 +150,16 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
     // The layer input is requested first (it gates the norm); the router rows are needed
     // only for the dot products and stream in behind it. MR >= M rows are loaded without
     // branches (rows past M repeat row M - 1) so that every load is in flight at once.
-    float v[NORM ? MR : 1][4];
+    uint16_t hraw[NORM ? MR : 1][4];
     if constexpr (NORM) {
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
             const int rr = r < M ? r : M - 1;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[r][i] = bf2f(src[static_cast<size_t>(rr) * H + tid + NT * i]);
+            for (int i = 0; i < 4; ++i) hraw[r][i] = src[static_cast<size_t>(rr) * H + tid + NT * i];
         }
     }
+    __builtin_amdgcn_sched_barrier(0);  // (the input's loads stay ahead of the router rows')
     uint4 wv[T];
     {
         const int ew = e < nr ? e : nr - 1;
@@ -165,7 +167,15 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
 #pragma unroll
         for (int t = 0; t < T; ++t) wv[t] = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
     }
+    // (the scheduler would otherwise sink the router-row loads below the norm's wait for
+    // the layer input, and the two memory latencies would add up)
+    __builtin_amdgcn_sched_barrier(0);
+    float v[NORM ? MR : 1][4];
     if constexpr (NORM) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[r][i] = bf2f(hraw[r][i]);
         Q38_STAMPV(0, 1, v[0][0]);
         float ss[MR];
 #pragma unroll
@@ -182,16 +192,26 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
         Q38_STAMPV(0, 5, ss[MR - 1]);
         lds_barrier();
         Q38_STAMP(0, 6);
+        // every row's wave totals at once, then the MR independent rsqrt chains
+        float inv[MR];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            float t = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) t += red[r][w];
+            inv[r] = 1.0f / sqrtf(t / static_cast<float>(H) + eps);
+        }
+        // (all rows' chains side by side: keeps the compiler from sinking each into its
+        // row's guarded stores below, one after another)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) asm volatile("" ::"v"(inv[r]));
 #pragma unroll
         for (int r = 0; r < MR; ++r)
             if (r < M) {
-                float t = 0.0f;
-                for (int w = 0; w < NW; ++w) t += red[r][w];
-                const float inv = 1.0f / sqrtf(t / static_cast<float>(H) + eps);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const size_t at = static_cast<size_t>(r) * H + tid + NT * i;
-                    const uint16_t b = f2bf(v[r][i] * inv);
+                    const uint16_t b = f2bf(v[r][i] * inv[r]);
                     xs[at] = b;
                     if (store) {
                         B.x[at] = b;
@@ -695,30 +715,42 @@ __global__ __launch_bounds__(256) void k_down_mixed(LayerDev L, MoeBufs B, int M
 // place (h <- T(h + y)), otherwise out <- y. The down kernels write route r * k + s at row
 // r * k + s and the shared expert's row r at M * k + r, so every load here is independent
 // of the plan and all of them are issued before the first use.
-template <int KT>
+template <int KT, bool TWO>
 __global__ __launch_bounds__(256) void k_combine(LayerDev L, MoeBufs B, int M, uint16_t* h, uint16_t* out) {
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + 3 * sizeof(void*)>();
     const int r = blockIdx.y;
     const int o = blockIdx.x * 256 + threadIdx.x;
     const int H = L.H, MK = M * KT;
     Q38_STAMP(24576, 0);
     if (o >= H) return;
-    const bool two = L.d_parts == 2;
+    constexpr bool two = TWO;  // L.d_parts == 2
     const bool shared = L.has_shared;
+    // Every load is unconditional and issued up front, the row's route weights and gate
+    // first (each wait below then covers only what it needs): the residual comes from the
+    // output row when there is none, and with no shared expert its read repeats route 0
+    // (that route is opaque to the optimizer, so it cannot split the code on it).
+    float wts[KT + 1];
+#pragma unroll
+    for (int s = 0; s < KT; ++s) wts[s] = B.weights[r * KT + s];
+    wts[KT] = B.sgate[r];
+    const uint16_t hraw = (h ? h : out)[static_cast<size_t>(r) * H + o];
+    int shared_route = shared ? MK + r : r * KT;  // (no shared expert: route 0 again, unused)
+    asm("" : "+s"(shared_route));
     float dv[KT + 1][2];
 #pragma unroll
     for (int s = 0; s <= KT; ++s) {
-        const int route = s < KT ? r * KT + s : (shared ? MK + r : r * KT);
+        const int route = s < KT ? r * KT + s : shared_route;
         const size_t at = static_cast<size_t>(route) * H + o;
         dv[s][0] = B.d[at];
         dv[s][1] = two ? B.d[B.d_plane + at] : 0.0f;
     }
-    const float hv = h ? bf2f(h[static_cast<size_t>(r) * H + o]) : 0.0f;
+    const float hv = h ? bf2f(hraw) : 0.0f;
     float routed = 0.0f;
 #pragma unroll
-    for (int s = 0; s < KT; ++s) routed = fmaf(B.weights[r * KT + s], rbf(two ? dv[s][0] + dv[s][1] : dv[s][0]), routed);
+    for (int s = 0; s < KT; ++s) routed = fmaf(wts[s], rbf(two ? dv[s][0] + dv[s][1] : dv[s][0]), routed);
     float y = rbf(routed);
     if (shared) {
-        const float sh = rbf(rbf(two ? dv[KT][0] + dv[KT][1] : dv[KT][0]) * B.sgate[r]);
+        const float sh = rbf(rbf(two ? dv[KT][0] + dv[KT][1] : dv[KT][0]) * wts[KT]);
         y = rbf(y + sh);
     }
     const size_t i = static_cast<size_t>(r) * H + o;
@@ -988,7 +1020,8 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
 
 template <int KT>
 hipError_t launch_combine_k(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
-    return launch(k_combine<KT>, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
+    if (L.d_parts == 2) return launch(k_combine<KT, true>, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
+    return launch(k_combine<KT, false>, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
 }
 
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {

@@ -110,6 +110,7 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     float* red = reinterpret_cast<float*>(lds + KENT * 8);  // [2][KS][64][4]
     uint2* xs = reinterpret_cast<uint2*>(lds + KENT * 8);                       // [4][NSUB], in red
     uint64_t* cand = reinterpret_cast<uint64_t*>(lds + KENT * 8 + kNarrow * NSUB * 8);  // [4][64], in red
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
     const int type = kk % TYPES;
@@ -271,6 +272,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     __shared__ __align__(16) uint2 hs[kNarrow][NSUB];  // SwiGLU rows of the item's routes (fp16)
     const uint2* book = reinterpret_cast<const uint2*>(lds);
     float* red = reinterpret_cast<float*>(lds + KENT * 8);  // [RG][KS-1][64][4]
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
     const int chunk = kk % NCHUNK;
