@@ -148,8 +148,11 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     tokens = 0
+    round_ms = []
     for cur, drafts, acc, nxt in fixture[args.warmup:]:
+        tr0 = time.perf_counter()
         got = round_fn(cur, drafts)
+        round_ms.append(1e3 * (time.perf_counter() - tr0))
         assert got == (acc, nxt), (got, acc, nxt)
         tokens += got[0] + 1
     torch.cuda.synchronize()
@@ -243,6 +246,82 @@ def main():
             tj = json.load(f)
         traffic = tj.get("hbm_bytes_per_launch")
 
+    # ---------------------------------------------------------------- config 3: prefill width
+    # 512 token rows through one layer whose router logits carry the Zipf(1.1) popularity
+    # bias; the expert GEMMs run on MFMA, so this is reported against the MFMA roofline
+    # (fp16 2.5 PFLOP/s dense) as well as in weight bytes.
+    import workloads
+    Mp = 512
+    Lp = q38.MoeLayer(ctx, d, seed=SEED, layer=3)
+    bias = torch.from_numpy(workloads.zipf_router_bias(E, SEED)).to(dev)
+    q38.check(q38.lib.q38_moe_layer_set_router_bias(Lp.h, bias.data_ptr()))
+    wsp = torch.empty(q38.lib.q38_moe_workspace_size(C.byref(d), Mp), dtype=torch.uint8, device=dev)
+    xp = torch.empty((Mp, H), dtype=torch.int16, device=dev)
+    yp = torch.empty((Mp, H), dtype=torch.int16, device=dev)
+    toks = (C.c_uint32 * Mp)(*[(7919 * r + 11) % V for r in range(Mp)])
+    q38.check(q38.lib.q38_embed_synthetic(SEED, toks, Mp, H, yp.data_ptr(), sp))
+    q38.check(q38.lib.q38_rmsnorm(yp.data_ptr(), Mp, H, 1e-6, xp.data_ptr(), sp))
+    planp = torch.empty(2 + 4 * Mp * K, dtype=torch.int32, device=dev)
+    rp = q38.routes(plan=planp)
+
+    def prefill(r=None):
+        q38.check(q38.lib.q38_moe_forward(Lp.h, xp.data_ptr(), Mp, yp.data_ptr(), C.byref(r) if r else None,
+                                          wsp.data_ptr(), wsp.numel(), sp))
+    prefill(rp)
+    torch.cuda.synchronize()
+    up = int(planp[0].item())
+    pt = []
+    for _ in range(10):
+        ev0.record(stream)
+        prefill()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        pt.append(ev0.elapsed_time(ev1))
+    p_us = 1e3 * float(np.median(pt))
+    p_flop = (Mp * K + Mp) * (4 * H * I + 2 * I * H) + 2 * Mp * H * (E + 1)
+    p_bytes = Lp.bytes(up, Mp)
+    prefill_cfg = {"rows": Mp, "routing": "Zipf(1.1) router bias", "layer_us": p_us, "unique_experts": up,
+                   "flop": p_flop, "tflops": p_flop / (p_us * 1e-6) / 1e12,
+                   "mfma_frac": p_flop / (p_us * 1e-6) / 2.5e15, "weight_bytes": p_bytes,
+                   "gbps": p_bytes / (p_us * 1e-6) / 1e9}
+    log(f"config 3 (512 rows, Zipf): {p_us:.1f} us/layer, {prefill_cfg['tflops']:.1f} TFLOP/s "
+        f"({100 * prefill_cfg['mfma_frac']:.2f}% of 2.5 PFLOP/s), {prefill_cfg['gbps']:.0f} GB/s, U={up}")
+    Lp.close()
+
+    # ---------------------------------------------------------------- config 4: mixed VQ v2
+    # 16 rows (4 slots x 4) through a chain of mixed layers (even experts d4/8-bit fp16 books,
+    # odd experts d8/14-bit INT8 books with one scale per book), uniform routing.
+    Mm, NLm = 16, 4
+    dm = q38.desc(mixed=1)
+    lm = [q38.MoeLayer(ctx, dm, seed=SEED, layer=l) for l in range(NLm)]
+    larm = (C.c_void_p * NLm)(*[L.h.value for L in lm])
+    wsm = torch.empty(q38.lib.q38_moe_workspace_size(C.byref(dm), Mm), dtype=torch.uint8, device=dev)
+    hm = torch.empty((Mm, H), dtype=torch.int16, device=dev)
+    toks = (C.c_uint32 * Mm)(*[11 + 7 * r for r in range(Mm)])
+    q38.check(q38.lib.q38_embed_synthetic(SEED, toks, Mm, H, hm.data_ptr(), sp))
+    hm0 = hm.clone()
+    plm = [torch.empty(2 + 4 * Mm * K, dtype=torch.int32, device=dev) for _ in lm]
+    trm = (q38.RouteOut * NLm)(*[q38.routes(plan=p) for p in plm])
+    q38.check(q38.lib.q38_verify_chain(larm, NLm, hm.data_ptr(), Mm, 1e-6, trm, wsm.data_ptr(), wsm.numel(), sp))
+    torch.cuda.synchronize()
+    um = [int(p[0].item()) for p in plm]
+    mt = []
+    for _ in range(10):
+        hm.copy_(hm0)
+        ev0.record(stream)
+        q38.check(q38.lib.q38_verify_chain(larm, NLm, hm.data_ptr(), Mm, 1e-6, None, wsm.data_ptr(), wsm.numel(),
+                                           sp))
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        mt.append(ev0.elapsed_time(ev1))
+    m_us = 1e3 * float(np.median(mt)) / NLm
+    m_bytes = sum(L.bytes(u, Mm) for L, u in zip(lm, um)) / NLm
+    mixed_cfg = {"rows": Mm, "layers": NLm, "layer_us": m_us, "mean_unique_experts": float(np.mean(um)),
+                 "bytes_per_layer": m_bytes, "gbps": m_bytes / (m_us * 1e-6) / 1e9}
+    log(f"config 4 (mixed VQ v2, 16 rows): {m_us:.1f} us/layer, {mixed_cfg['gbps']:.0f} GB/s, U={np.mean(um):.1f}")
+    for L in lm:
+        L.close()
+
     if args.copy_calibration:
         # a plain device copy of known size for the FETCH_SIZE / WRITE_SIZE calibration runs
         nb = 256 << 20
@@ -306,8 +385,11 @@ def main():
             "moe_layer_us": {str(k): v["layer_us"] for k, v in per_m.items()},
             "moe_layer_gbps": {str(k): v["gbps"] for k, v in per_m.items()},
             "mean_unique_experts": {str(k): v["mean_unique_experts"] for k, v in per_m.items()},
+            "round_ms_p10_p50_p90": [float(np.percentile(round_ms, q)) for q in (10, 50, 90)],
             "kernel_us_per_launch_m4": {k.split()[0]: 1e3 * v[0] / nl for k, v in kernels.items()},
             "algorithmic_bytes_per_launch_m4": {k.split()[0]: v[1] for k, v in kernels.items()},
+            "config3_prefill": prefill_cfg,
+            "config4_mixed": mixed_cfg,
         },
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "launch_avg_us": dom_us,

@@ -552,8 +552,15 @@ struct Vec<4> {
 constexpr int kGuRowsPerBlock = 64;
 constexpr int kDownRowsPerBlock = 128;
 
+// Staged input rows of the grouped kernels: row j, column c at fin_at(j, c, IN). One pad
+// float after every 64 columns, so that the lanes of a row (16 codes each, 64 or 128
+// columns apart) read different LDS banks instead of one.
+__host__ __device__ constexpr int fin_stride(int IN) { return IN + IN / 64; }
+constexpr size_t kFinLdsMax = 136 * 1024;  // 16 rows of H = 2048 (133,120 bytes)
+__device__ __forceinline__ int fin_at(int j, int c, int IN) { return j * fin_stride(IN) + c + c / 64; }
+
 // Lane mapping: a lane owns 16 consecutive codes of a row (BITS/2 words); LPR lanes
-// (power of two, padded) cover one row; 64/LPR rows per wave. in_f: [n][IN] floats. Output row
+// (power of two, padded) cover one row; 64/LPR rows per wave. in_f: n rows staged at fin_at. Output row
 // pos0 + j, or its route index when rplan (the plan) is given (down projections).
 template <int D, int BITS, int LPR, int MAXN>
 __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int IN, int OUT, int o_base,
@@ -594,7 +601,7 @@ __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int I
                 for (int j = 0; j < MAXN; ++j)
                     if (j < n)
 #pragma unroll
-                        for (int dd = 0; dd < D; ++dd) pp[j] = fmaf(in_f[j * IN + s * D + dd], bk[dd], pp[j]);
+                        for (int dd = 0; dd < D; ++dd) pp[j] = fmaf(in_f[fin_at(j, s * D + dd, IN)], bk[dd], pp[j]);
                 if (!row_scale && ((s + 1) % spg) == 0) {
                     const float sc = h2f(P.scales[rowi * P.ngrp + s / spg]);
 #pragma unroll
@@ -622,14 +629,14 @@ __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int I
 
 template <int D, int BITS, int LPR>
 __global__ __launch_bounds__(256) void k_gu_grouped(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) float fin[];  // [n][H]
+    extern __shared__ __align__(16) float fin[];  // n rows of H, at fin_at
     int expert, n, pos0;
     if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
     const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
     const int H = L.H, I = L.I;
     for (int i = threadIdx.x; i < n * H; i += 256) {
         const int j = i / H, c = i % H;
-        fin[i] = bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]);
+        fin[fin_at(j, c, H)] = bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]);
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -640,7 +647,7 @@ __global__ __launch_bounds__(256) void k_gu_grouped(LayerDev L, MoeBufs B, int M
 
 template <int D, int BITS, int LPR>
 __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) float fin[];  // [n][I]
+    extern __shared__ __align__(16) float fin[];  // n rows of I, at fin_at
     int expert, n, pos0;
     if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
     const int H = L.H, I = L.I;
@@ -651,7 +658,7 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
             g += B.g[B.gu_plane + at];
             u += B.u[B.gu_plane + at];
         }
-        fin[i] = swiglu(g, u);
+        fin[fin_at(i / I, i % I, I)] = swiglu(g, u);
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -664,14 +671,14 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
 // block). LA / LB: lanes per row of the d4 and d8 geometries.
 template <int LA, int LB>
 __global__ __launch_bounds__(256) void k_gu_mixed(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) float fin[];  // [n][H]
+    extern __shared__ __align__(16) float fin[];  // n rows of H, at fin_at
     int expert, n, pos0;
     if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
     const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
     const int H = L.H, I = L.I;
     for (int i = threadIdx.x; i < n * H; i += 256) {
         const int j = i / H, c = i % H;
-        fin[i] = bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]);
+        fin[fin_at(j, c, H)] = bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]);
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -690,13 +697,13 @@ __global__ __launch_bounds__(256) void k_gu_mixed(LayerDev L, MoeBufs B, int M) 
 
 template <int LA, int LB>
 __global__ __launch_bounds__(256) void k_down_mixed(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) float fin[];  // [n][I]
+    extern __shared__ __align__(16) float fin[];  // n rows of I, at fin_at
     int expert, n, pos0;
     if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
     const int H = L.H, I = L.I;
     for (int i = threadIdx.x; i < n * I; i += 256) {
         const size_t at = static_cast<size_t>(pos0) * I + i;
-        fin[i] = swiglu(B.g[at], B.u[at]);
+        fin[fin_at(i / I, i % I, I)] = swiglu(B.g[at], B.u[at]);
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -888,11 +895,11 @@ hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStr
 
 template <int D, int BITS, int LPR>
 hipError_t launch_gu_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = static_cast<size_t>(M) * L.H * 4;
-    if (lds > 128 * 1024) return hipErrorInvalidValue;
+    const size_t lds = static_cast<size_t>(M) * fin_stride(L.H) * 4;
+    if (lds > kFinLdsMax) return hipErrorInvalidValue;
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = set_lds(&k_gu_grouped<D, BITS, LPR>, 128 * 1024);
+        const hipError_t e = set_lds(&k_gu_grouped<D, BITS, LPR>, kFinLdsMax);
         if (e != hipSuccess) return e;
         attr = true;
     }
@@ -902,7 +909,7 @@ hipError_t launch_gu_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipSt
 }
 template <int D, int BITS, int LPR>
 hipError_t launch_down_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = static_cast<size_t>(M) * L.I * 4;
+    const size_t lds = static_cast<size_t>(M) * fin_stride(L.I) * 4;
     hipLaunchKernelGGL((k_down_grouped<D, BITS, LPR>), dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256), lds, st,
                        L, B, M);
     return hipGetLastError();
@@ -958,12 +965,12 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
         if (L.H != 2048 || L.I != 512) return hipErrorInvalidValue;
         static bool attr = false;
         if (!attr) {
-            const hipError_t e = set_lds(&k_gu_mixed<32, 16>, 128 * 1024);
+            const hipError_t e = set_lds(&k_gu_mixed<32, 16>, kFinLdsMax);
             if (e != hipSuccess) return e;
             attr = true;
         }
         return launch(k_gu_mixed<32, 16>, dim3(L.I / kGuRowsPerBlock, M * L.K + 1), dim3(256),
-                      static_cast<size_t>(M) * L.H * 4, st, L, B, M);
+                      static_cast<size_t>(M) * fin_stride(L.H) * 4, st, L, B, M);
     }
     if (moe_uses_narrow(L, M)) return launch_gate_up4(L, B, M, st);
     const int D = L.p[0].dim, BT = L.p[0].bits;
@@ -994,7 +1001,7 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
     if (L.mixed) {  // d4: I/4 = 128 subvectors -> 8 lanes per row; d8: 64 -> 4
         if (L.H != 2048 || L.I != 512) return hipErrorInvalidValue;
         return launch(k_down_mixed<8, 4>, dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256),
-                      static_cast<size_t>(M) * L.I * 4, st, L, B, M);
+                      static_cast<size_t>(M) * fin_stride(L.I) * 4, st, L, B, M);
     }
     if (moe_uses_narrow(L, M)) return launch_down4(L, B, M, st);
     const int D = L.p[2].dim, BT = L.p[2].bits;
