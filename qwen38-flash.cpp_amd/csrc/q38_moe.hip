@@ -552,19 +552,23 @@ struct Vec<4> {
 constexpr int kGuRowsPerBlock = 64;
 constexpr int kDownRowsPerBlock = 128;
 
-// Staged input rows of the grouped kernels: row j, column c at fin_at(j, c, IN). One pad
-// float after every 64 columns, so that the lanes of a row (16 codes each, 64 or 128
-// columns apart) read different LDS banks instead of one.
-__host__ __device__ constexpr int fin_stride(int IN) { return IN + IN / 64; }
-constexpr size_t kFinLdsMax = 136 * 1024;  // 16 rows of H = 2048 (133,120 bytes)
-__device__ __forceinline__ int fin_at(int j, int c, int IN) { return j * fin_stride(IN) + c + c / 64; }
+// Staged input rows of the grouped kernels, fp16: row j, column c at fin_at(j, c, IN). Two
+// pad halves (one bank) after every 64 columns, so that the lanes of a row (16 codes each,
+// 64 or 128 columns apart) read different LDS banks instead of one. fp16 keeps 16 rows of
+// H = 2048 at 66.5 KiB, two workgroups per CU. (Inputs are bf16 values or SwiGLU outputs
+// rounded to bf16: fp16 holds them exactly in the normal range; the MFMA paths take the
+// same fp16 operand.)
+typedef _Float16 fin_t;
+__host__ __device__ constexpr int fin_stride(int IN) { return IN + 2 * (IN / 64); }
+constexpr size_t kFinLdsMax = 68 * 1024;  // 16 rows of H = 2048 (68,096 bytes)
+__device__ __forceinline__ int fin_at(int j, int c, int IN) { return j * fin_stride(IN) + c + 2 * (c / 64); }
 
 // Lane mapping: a lane owns 16 consecutive codes of a row (BITS/2 words); LPR lanes
 // (power of two, padded) cover one row; 64/LPR rows per wave. in_f: n rows staged at fin_at. Output row
 // pos0 + j, or its route index when rplan (the plan) is given (down projections).
 template <int D, int BITS, int LPR, int MAXN>
 __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int IN, int OUT, int o_base,
-                                             int rows_per_block, const float* in_f, int n, float* out,
+                                             int rows_per_block, const fin_t* in_f, int n, float* out,
                                              int pos0, int wave, int lane, const int32_t* rplan = nullptr,
                                              int MK = 0) {
     const int nsub = IN / D;
@@ -601,7 +605,7 @@ __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int I
                 for (int j = 0; j < MAXN; ++j)
                     if (j < n)
 #pragma unroll
-                        for (int dd = 0; dd < D; ++dd) pp[j] = fmaf(in_f[fin_at(j, s * D + dd, IN)], bk[dd], pp[j]);
+                        for (int dd = 0; dd < D; ++dd) pp[j] = fmaf(static_cast<float>(in_f[fin_at(j, s * D + dd, IN)]), bk[dd], pp[j]);
                 if (!row_scale && ((s + 1) % spg) == 0) {
                     const float sc = h2f(P.scales[rowi * P.ngrp + s / spg]);
 #pragma unroll
@@ -627,27 +631,45 @@ __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int I
     }
 }
 
+// grouped_rows for a slot of n routes, with the route loop sized for n (1, 2, 4 or up to
+// kMaxRows) rather than always unrolled to kMaxRows with a guard per route (most slots of
+// a 16-row call have one or two routes).
+template <int D, int BITS, int LPR>
+__device__ __forceinline__ void grouped_rows_n(const ProjDev& P, int expert, int IN, int OUT, int o_base,
+                                               int rows_per_block, const fin_t* in_f, int n, float* out, int pos0,
+                                               int wave, int lane, const int32_t* rplan = nullptr, int MK = 0) {
+    if (n <= 1)
+        grouped_rows<D, BITS, LPR, 1>(P, expert, IN, OUT, o_base, rows_per_block, in_f, n, out, pos0, wave, lane, rplan, MK);
+    else if (n <= 2)
+        grouped_rows<D, BITS, LPR, 2>(P, expert, IN, OUT, o_base, rows_per_block, in_f, n, out, pos0, wave, lane, rplan, MK);
+    else if (n <= 4)
+        grouped_rows<D, BITS, LPR, 4>(P, expert, IN, OUT, o_base, rows_per_block, in_f, n, out, pos0, wave, lane, rplan, MK);
+    else
+        grouped_rows<D, BITS, LPR, kMaxRows>(P, expert, IN, OUT, o_base, rows_per_block, in_f, n, out, pos0, wave, lane,
+                                             rplan, MK);
+}
+
 template <int D, int BITS, int LPR>
 __global__ __launch_bounds__(256) void k_gu_grouped(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) float fin[];  // n rows of H, at fin_at
+    extern __shared__ __align__(16) fin_t fin[];  // n rows of H, at fin_at
     int expert, n, pos0;
     if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
     const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
     const int H = L.H, I = L.I;
     for (int i = threadIdx.x; i < n * H; i += 256) {
         const int j = i / H, c = i % H;
-        fin[fin_at(j, c, H)] = bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]);
+        fin[fin_at(j, c, H)] = static_cast<fin_t>(bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]));
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int o_base = blockIdx.x * kGuRowsPerBlock;
-    grouped_rows<D, BITS, LPR, kMaxRows>(L.p[0], expert, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave, lane);
-    grouped_rows<D, BITS, LPR, kMaxRows>(L.p[1], expert, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave, lane);
+    grouped_rows_n<D, BITS, LPR>(L.p[0], expert, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave, lane);
+    grouped_rows_n<D, BITS, LPR>(L.p[1], expert, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave, lane);
 }
 
 template <int D, int BITS, int LPR>
 __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) float fin[];  // n rows of I, at fin_at
+    extern __shared__ __align__(16) fin_t fin[];  // n rows of I, at fin_at
     int expert, n, pos0;
     if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
     const int H = L.H, I = L.I;
@@ -658,11 +680,11 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
             g += B.g[B.gu_plane + at];
             u += B.u[B.gu_plane + at];
         }
-        fin[fin_at(i / I, i % I, I)] = swiglu(g, u);
+        fin[fin_at(i / I, i % I, I)] = static_cast<fin_t>(swiglu(g, u));
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    grouped_rows<D, BITS, LPR, kMaxRows>(L.p[2], expert, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
+    grouped_rows_n<D, BITS, LPR>(L.p[2], expert, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
                                          fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
 }
 
@@ -671,48 +693,48 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
 // block). LA / LB: lanes per row of the d4 and d8 geometries.
 template <int LA, int LB>
 __global__ __launch_bounds__(256) void k_gu_mixed(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) float fin[];  // n rows of H, at fin_at
+    extern __shared__ __align__(16) fin_t fin[];  // n rows of H, at fin_at
     int expert, n, pos0;
     if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
     const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
     const int H = L.H, I = L.I;
     for (int i = threadIdx.x; i < n * H; i += 256) {
         const int j = i / H, c = i % H;
-        fin[fin_at(j, c, H)] = bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]);
+        fin[fin_at(j, c, H)] = static_cast<fin_t>(bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]));
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int o_base = blockIdx.x * kGuRowsPerBlock;
     const int idx = expert >> 1;
     if ((expert & 1) == 0) {
-        grouped_rows<4, 8, LA, kMaxRows>(L.pb[0][0], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave, lane);
-        grouped_rows<4, 8, LA, kMaxRows>(L.pb[1][0], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave, lane);
+        grouped_rows_n<4, 8, LA>(L.pb[0][0], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave, lane);
+        grouped_rows_n<4, 8, LA>(L.pb[1][0], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave, lane);
     } else {
-        grouped_rows<8, 14, LB, kMaxRows>(L.pb[0][1], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave,
+        grouped_rows_n<8, 14, LB>(L.pb[0][1], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave,
                                           lane);
-        grouped_rows<8, 14, LB, kMaxRows>(L.pb[1][1], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave,
+        grouped_rows_n<8, 14, LB>(L.pb[1][1], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave,
                                           lane);
     }
 }
 
 template <int LA, int LB>
 __global__ __launch_bounds__(256) void k_down_mixed(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) float fin[];  // n rows of I, at fin_at
+    extern __shared__ __align__(16) fin_t fin[];  // n rows of I, at fin_at
     int expert, n, pos0;
     if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
     const int H = L.H, I = L.I;
     for (int i = threadIdx.x; i < n * I; i += 256) {
         const size_t at = static_cast<size_t>(pos0) * I + i;
-        fin[fin_at(i / I, i % I, I)] = swiglu(B.g[at], B.u[at]);
+        fin[fin_at(i / I, i % I, I)] = static_cast<fin_t>(swiglu(B.g[at], B.u[at]));
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int idx = expert >> 1;
     if ((expert & 1) == 0)
-        grouped_rows<4, 8, LA, kMaxRows>(L.pb[2][0], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
+        grouped_rows_n<4, 8, LA>(L.pb[2][0], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
                                          fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
     else
-        grouped_rows<8, 14, LB, kMaxRows>(L.pb[2][1], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
+        grouped_rows_n<8, 14, LB>(L.pb[2][1], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
                                           fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
 }
 
@@ -895,7 +917,7 @@ hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStr
 
 template <int D, int BITS, int LPR>
 hipError_t launch_gu_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = static_cast<size_t>(M) * fin_stride(L.H) * 4;
+    const size_t lds = static_cast<size_t>(M) * fin_stride(L.H) * sizeof(fin_t);
     if (lds > kFinLdsMax) return hipErrorInvalidValue;
     static bool attr = false;
     if (!attr) {
@@ -909,7 +931,7 @@ hipError_t launch_gu_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipSt
 }
 template <int D, int BITS, int LPR>
 hipError_t launch_down_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = static_cast<size_t>(M) * fin_stride(L.I) * 4;
+    const size_t lds = static_cast<size_t>(M) * fin_stride(L.I) * sizeof(fin_t);
     hipLaunchKernelGGL((k_down_grouped<D, BITS, LPR>), dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256), lds, st,
                        L, B, M);
     return hipGetLastError();
@@ -970,7 +992,7 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
             attr = true;
         }
         return launch(k_gu_mixed<32, 16>, dim3(L.I / kGuRowsPerBlock, M * L.K + 1), dim3(256),
-                      static_cast<size_t>(M) * fin_stride(L.H) * 4, st, L, B, M);
+                      static_cast<size_t>(M) * fin_stride(L.H) * sizeof(fin_t), st, L, B, M);
     }
     if (moe_uses_narrow(L, M)) return launch_gate_up4(L, B, M, st);
     const int D = L.p[0].dim, BT = L.p[0].bits;
@@ -1001,7 +1023,7 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
     if (L.mixed) {  // d4: I/4 = 128 subvectors -> 8 lanes per row; d8: 64 -> 4
         if (L.H != 2048 || L.I != 512) return hipErrorInvalidValue;
         return launch(k_down_mixed<8, 4>, dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256),
-                      static_cast<size_t>(M) * fin_stride(L.I) * 4, st, L, B, M);
+                      static_cast<size_t>(M) * fin_stride(L.I) * sizeof(fin_t), st, L, B, M);
     }
     if (moe_uses_narrow(L, M)) return launch_down4(L, B, M, st);
     const int D = L.p[2].dim, BT = L.p[2].bits;
