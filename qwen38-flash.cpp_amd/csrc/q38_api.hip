@@ -353,7 +353,35 @@ static void fill_dev_mixed(q38_moe_layer* L, const q38_moe_mixed_weights* w) {
         v.pb[p][1] = b;
         v.p[p] = b;
     }
-    v.gu_parts = v.d_parts = 1;
+    // the odd bank (two codebook chunks) writes two partial-sum planes, the even bank writes
+    // one and clears the second
+    v.gu_parts = v.d_parts = 2;
+}
+
+// Chunked fp16 codebooks of a mixed layer for the MFMA kernels: the d4 books are already in
+// the chunk layout ([1][256][4]); the INT8 d8 books are decoded (q * scale) into
+// [2][16384][4] fp16.
+static int prepare_mixed(q38_moe_layer* L) {
+    const size_t per = align256(static_cast<size_t>(16384) * 8 * 2);
+    char* base = nullptr;
+    if (hipMalloc(&base, 3 * per) != hipSuccess) return fail(Q38_ENOMEM, "hipMalloc failed for prepared codebooks");
+    hipError_t e = hipSuccess;
+    LayerDev& v = L->dev;
+    for (int p = 0; p < 3 && e == hipSuccess; ++p) {
+        auto* dst = reinterpret_cast<uint16_t*>(base + p * per);
+        e = launch_split_book_i8(v.pb[p][1].book_i8, v.pb[p][1].book_scale, 1 << v.pb[p][1].bits, v.pb[p][1].dim, dst,
+                                 nullptr);
+        v.pb[p][0].book4 = v.pb[p][0].book;
+        v.pb[p][1].book4 = dst;
+        v.p[p] = v.pb[p][1];
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        (void)hipFree(base);
+        return hip_fail(e, "mixed codebook preparation");
+    }
+    L->prepared = base;
+    return Q38_OK;
 }
 
 int q38_moe_layer_create_mixed(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_mixed_weights* w,
@@ -369,6 +397,10 @@ int q38_moe_layer_create_mixed(q38_ctx* ctx, const q38_moe_desc* desc, const q38
             return fail(Q38_EINVAL, "mixed layer tensors are required for all three projections");
     auto* L = new q38_moe_layer{ctx, *desc, {}, nullptr, 0, nullptr};
     fill_dev_mixed(L, w);
+    if (int rc = prepare_mixed(L)) {
+        delete L;
+        return rc;
+    }
     *out = L;
     return Q38_OK;
 }
@@ -446,6 +478,11 @@ static int create_synthetic_mixed(q38_ctx* ctx, const q38_moe_desc& d, uint64_t 
     }
     auto* L = new q38_moe_layer{ctx, d, {}, base, off, nullptr};
     fill_dev_mixed(L, &w);
+    if (int rc = prepare_mixed(L)) {
+        (void)hipFree(base);
+        delete L;
+        return rc;
+    }
     *out = L;
     return Q38_OK;
 }
@@ -619,7 +656,7 @@ static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_
                      uint16_t* h_chain, uint16_t* y, const q38_route_out* trace, hipEvent_t* ev, hipStream_t st) {
     if (ev) Q38_HIP(hipEventRecord(ev[0], st));
     Q38_HIP(launch_router(L->dev, w, rows, src, norm, eps, st));
-    if (!moe_uses_mfma(L->dev)) Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
+    if (!moe_plans_in_gate_up(L->dev)) Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[1], st));
     Q38_HIP(launch_gate_up(L->dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[2], st));
@@ -723,7 +760,7 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
         hipError_t e = hipSuccess;
         kt = {E[0], E[1]};
         e = launch_router(L->dev, w, rows, h, true, eps, st);
-        if (e == hipSuccess && !moe_uses_mfma(L->dev)) e = launch_topk_plan(L->dev, w, rows, st);
+        if (e == hipSuccess && !moe_plans_in_gate_up(L->dev)) e = launch_topk_plan(L->dev, w, rows, st);
         if (e == hipSuccess) {
             kt = {E[2], E[3]};
             e = launch_gate_up(L->dev, w, rows, st);

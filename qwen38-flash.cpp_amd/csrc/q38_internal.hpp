@@ -103,9 +103,15 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st);
 hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_t* book4, hipStream_t st);
+hipError_t launch_split_book_i8(const int8_t* book, float scale, int entries, int dim, uint16_t* book4,
+                                hipStream_t st);
 // codes [rows, words] (rows a multiple of 64) -> the tiled layout of ProjDev::codes_t
 hipError_t launch_tile_codes(const uint32_t* codes, int64_t rows, int words, int bits, uint32_t* out, hipStream_t st);
 bool moe_uses_mfma(const LayerDev& L);
+// Mixed layer on the MFMA kernels (both banks prepared); the gate/up kernels of both the
+// uniform and the mixed MFMA paths route and build the plan themselves.
+bool moe_mixed_mfma(const LayerDev& L);
+bool moe_plans_in_gate_up(const LayerDev& L);
 // Verify widths of up to 4 rows on the 4x4x4 MFMA kernels (q38_moe4.hip).
 bool moe_uses_narrow(const LayerDev& L, int M);
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);

@@ -336,11 +336,47 @@ __device__ __forceinline__ const uint4* xs_lane(const uint4* xs, int xrow, int z
     return xs + ((active ? xrow : zero_row) * NSUB + q * (NSUB / 4)) / 2;
 }
 
-template <int BITS, int NSUB, int NCHUNK>
+constexpr int kPlanSlots = kMaxRows * kMaxTopK + 1;  // unique-expert slots + the shared one
+
+// Mixed layers: the index of expert e in its bank (even experts and the shared expert E
+// in bank 0, odd experts in bank 1, both at e / 2); uniform layers: e.
+template <int PAR>
+__device__ __forceinline__ int bank_index(int e) { return PAR < 0 ? e : e >> 1; }
+
+// The plan's slots (unique experts ascending, then the shared expert E, which is even)
+// whose expert has parity par, in slot order, into out; returns their count. Every
+// thread calls it; the list is complete after the block barrier inside.
+__device__ __forceinline__ int parity_slots(const int32_t* plan, int nu, int has_shared, int E, int par,
+                                            int32_t* out) {
+    __shared__ int32_t cnt;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const int ns = nu + (has_shared ? 1 : 0);
+        int base = 0;
+        for (int u0 = 0; u0 < ns; u0 += 64) {
+            const int u = u0 + lane;
+            const int e = u < nu ? plan[1 + u] : E;
+            const bool take = u < ns && (e & 1) == par;
+            const uint64_t m = __ballot(take);
+            if (take) out[base + __popcll(m & ((1ull << lane) - 1ull))] = u;
+            base += __popcll(m);
+        }
+        if (lane == 0) cnt = base;
+    }
+    __syncthreads();
+    return cnt;
+}
+
+// PAR >= 0 (mixed layers): only the slots whose expert has that parity, with the
+// geometry of that bank (L.pb[proj][PAR], expert index e / 2); the even bank (one codebook
+// chunk) also clears plane 1 of its outputs, so a consumer can add both planes for every
+// route.
+template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B, int M) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ TopkLds tk;
     __shared__ int32_t plan[kPlanInts];
+    __shared__ int32_t pslots[PAR < 0 ? 1 : kPlanSlots];
     constexpr int KENT = 1 << BITS;
     const uint2* book = reinterpret_cast<const uint2*>(lds);       // [KENT] x 4 fp16
     uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);          // [8 + 1 zero][NSUB][4] fp16
@@ -351,7 +387,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     const int proj = type / NCHUNK, chunk = type % NCHUNK;
     const int per_type = (gridDim.x / (8 * TYPES)) * 8;
     const int idx = (kk / TYPES) * 8 + x8;
-    const ProjDev& P = L.p[proj];
+    const ProjDev& P = PAR < 0 ? L.p[proj] : L.pb[proj][PAR < 0 ? 0 : PAR];
     // waves 0-3 load the codebook chunk while waves 4-7 route; every workgroup derives
     // the same plan and workgroup 0 publishes it
     if (wave < 4) fill_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, tid, 256);
@@ -360,8 +396,10 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
         for (int i = tid; i < 2 + 4 * M * L.K; i += kMfmaThreads) B.plan[i] = plan[i];
     const int H = L.H, I = L.I, K = L.K;
     const int nu = plan[0];
-    const int n_items = (nu + (L.has_shared ? 1 : 0)) * (I / kMfmaRowsPerItem);
+    const int nslots = PAR < 0 ? nu + (L.has_shared ? 1 : 0) : parity_slots(plan, nu, L.has_shared, L.E, PAR, pslots);
+    const int n_items = nslots * (I / kMfmaRowsPerItem);
     const int tiles = I / kMfmaRowsPerItem;
+    auto slot_of = [&](int item) { return PAR < 0 ? item / tiles : pslots[item / tiles]; };
     float* out = (proj == 0 ? B.g : B.u) + chunk * B.gu_plane;
     const int r16 = lane & 15, q = lane >> 4;
     constexpr int S4 = NSUB / 4;
@@ -380,15 +418,16 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     lds_barrier();
     auto code_src = [&](int item) {
         int expert, n, pos0;
-        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
-        const size_t rowi = static_cast<size_t>(expert) * I + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
+        slot_rows(plan, M, K, L.has_shared, slot_of(item), L.E, &expert, &n, &pos0);
+        const size_t rowi =
+            static_cast<size_t>(bank_index<PAR>(expert)) * I + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
         return P.codes + rowi * P.words + q * WPL;
     };
     uint32_t w[WPL + 1], wn[WPL + 1];
     if (idx < n_items) load_lane_words<BITS, NSUB>(code_src(idx), w);
     for (int item = idx; item < n_items; item += per_type) {
         if (item + per_type < n_items) load_lane_words<BITS, NSUB>(code_src(item + per_type), wn);
-        const int ui = item / tiles, tile = item % tiles;
+        const int ui = slot_of(item), tile = item % tiles;
         int expert, n, pos0;
         slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
         const bool shared = ui == nu;
@@ -413,8 +452,9 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int o = o0 + 4 * q + rr;
-                    const float sc = h2f(P.scales[static_cast<size_t>(expert) * I + o]);
+                    const float sc = h2f(P.scales[static_cast<size_t>(bank_index<PAR>(expert)) * I + o]);
                     out[static_cast<size_t>(pos0 + j0 + r16) * I + o] = sc * acc[rr];
+                    if (PAR >= 0 && NCHUNK == 1) out[B.gu_plane + static_cast<size_t>(pos0 + j0 + r16) * I + o] = 0.0f;
                 }
             }
         }
@@ -425,10 +465,12 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
 
 constexpr int kDownStageRoutes = 48;  // routes whose SwiGLU rows are staged once (M <= 4 with k = 10)
 
-template <int BITS, int NSUB, int NCHUNK>
+// PAR >= 0: one bank of a mixed layer, as in k_gu_mfma (the even bank clears plane 1).
+template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs B, int M) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int32_t plan[kPlanInts];
+    __shared__ int32_t pslots[PAR < 0 ? 1 : kPlanSlots];
     constexpr int KENT = 1 << BITS;
     const uint2* book = reinterpret_cast<const uint2*>(lds);
     uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);   // [routes][NSUB][4] fp16 SwiGLU rows
@@ -437,7 +479,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
     const int chunk = kk % NCHUNK;
     const int per_type = (gridDim.x / (8 * NCHUNK)) * 8;
     const int idx = (kk / NCHUNK) * 8 + x8;
-    const ProjDev& P = L.p[2];
+    const ProjDev& P = PAR < 0 ? L.p[2] : L.pb[2][PAR < 0 ? 0 : PAR];
     const int H = L.H, I = L.I, K = L.K;
     const int n_routes = M * K + (L.has_shared ? M : 0);
     for (int i = tid; i < 2 + 4 * M * K; i += kMfmaThreads) plan[i] = B.plan[i];
@@ -468,21 +510,24 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
     float* dout = B.d + chunk * B.d_plane;
     const int nu = plan[0];
     const int tiles = H / kMfmaRowsPerItem;
-    const int n_items = (nu + (L.has_shared ? 1 : 0)) * tiles;
+    const int nslots = PAR < 0 ? nu + (L.has_shared ? 1 : 0) : parity_slots(plan, nu, L.has_shared, L.E, PAR, pslots);
+    const int n_items = nslots * tiles;
+    auto slot_of = [&](int item) { return PAR < 0 ? item / tiles : pslots[item / tiles]; };
     const int r16 = lane & 15, q = lane >> 4;
     constexpr int S4 = NSUB / 4;
     constexpr int WPL = S4 * BITS / 32;
     auto code_src = [&](int item) {
         int expert, n, pos0;
-        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
-        const size_t rowi = static_cast<size_t>(expert) * H + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
+        slot_rows(plan, M, K, L.has_shared, slot_of(item), L.E, &expert, &n, &pos0);
+        const size_t rowi =
+            static_cast<size_t>(bank_index<PAR>(expert)) * H + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
         return P.codes + rowi * P.words + q * WPL;
     };
     uint32_t w[WPL + 1], wn[WPL + 1];
     if (idx < n_items) load_lane_words<BITS, NSUB>(code_src(idx), w);
     for (int item = idx; item < n_items; item += per_type) {
         if (item + per_type < n_items) load_lane_words<BITS, NSUB>(code_src(item + per_type), wn);
-        const int ui = item / tiles, tile = item % tiles;
+        const int ui = slot_of(item), tile = item % tiles;
         int expert, n, pos0;
         slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
         const int o0 = tile * kMfmaRowsPerItem + wave * 16;
@@ -501,8 +546,10 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int o = o0 + 4 * q + rr;
-                    const float sc = h2f(P.scales[static_cast<size_t>(expert) * H + o]);
-                    dout[static_cast<size_t>(route_of_pos(plan, M * K, pos0 + j0 + r16)) * H + o] = sc * acc[rr];
+                    const float sc = h2f(P.scales[static_cast<size_t>(bank_index<PAR>(expert)) * H + o]);
+                    const size_t at = static_cast<size_t>(route_of_pos(plan, M * K, pos0 + j0 + r16)) * H + o;
+                    dout[at] = sc * acc[rr];
+                    if (PAR >= 0 && NCHUNK == 1) B.d[B.d_plane + at] = 0.0f;
                 }
             }
         }
@@ -688,55 +735,6 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
                                          fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
 }
 
-// Mixed geometry (even experts d4/8-bit fp16 books, odd experts d8/14-bit INT8 books):
-// the same per-slot kernels with the decoder chosen by the slot's expert (uniform per
-// block). LA / LB: lanes per row of the d4 and d8 geometries.
-template <int LA, int LB>
-__global__ __launch_bounds__(256) void k_gu_mixed(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) fin_t fin[];  // n rows of H, at fin_at
-    int expert, n, pos0;
-    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
-    const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
-    const int H = L.H, I = L.I;
-    for (int i = threadIdx.x; i < n * H; i += 256) {
-        const int j = i / H, c = i % H;
-        fin[fin_at(j, c, H)] = static_cast<fin_t>(bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]));
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int o_base = blockIdx.x * kGuRowsPerBlock;
-    const int idx = expert >> 1;
-    if ((expert & 1) == 0) {
-        grouped_rows_n<4, 8, LA>(L.pb[0][0], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave, lane);
-        grouped_rows_n<4, 8, LA>(L.pb[1][0], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave, lane);
-    } else {
-        grouped_rows_n<8, 14, LB>(L.pb[0][1], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave,
-                                          lane);
-        grouped_rows_n<8, 14, LB>(L.pb[1][1], idx, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave,
-                                          lane);
-    }
-}
-
-template <int LA, int LB>
-__global__ __launch_bounds__(256) void k_down_mixed(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) fin_t fin[];  // n rows of I, at fin_at
-    int expert, n, pos0;
-    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
-    const int H = L.H, I = L.I;
-    for (int i = threadIdx.x; i < n * I; i += 256) {
-        const size_t at = static_cast<size_t>(pos0) * I + i;
-        fin[fin_at(i / I, i % I, I)] = static_cast<fin_t>(swiglu(B.g[at], B.u[at]));
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int idx = expert >> 1;
-    if ((expert & 1) == 0)
-        grouped_rows_n<4, 8, LA>(L.pb[2][0], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
-                                         fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
-    else
-        grouped_rows_n<8, 14, LB>(L.pb[2][1], idx, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
-                                          fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
-}
 
 // ============================================================== combine (R8, R10, R11)
 // One thread per (row, column): routed = T(sum_slot w_slot * T(d_slot)) in slot order,
@@ -812,6 +810,17 @@ __global__ void k_split_book(const uint16_t* __restrict__ book, int entries, int
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         const int e = i / dim, d = i % dim;
         out[(static_cast<size_t>(d / 4) * entries + e) * 4 + d % 4] = book[i];
+    }
+}
+
+// The same split of an INT8 codebook, decoded to fp16: value = fp16(q * scale) (the MFMA
+// operand type; q * scale itself is exact in float, the fp16 rounding is the only change).
+__global__ void k_split_book_i8(const int8_t* __restrict__ book, float scale, int entries, int dim,
+                                uint16_t* __restrict__ out) {
+    const int n = entries * dim;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const int e = i / dim, d = i % dim;
+        out[(static_cast<size_t>(d / 4) * entries + e) * 4 + d % 4] = f2h(static_cast<float>(book[i]) * scale);
     }
 }
 
@@ -892,27 +901,27 @@ hipError_t set_lds(Kern k, size_t bytes) {
                                static_cast<int>(bytes));
 }
 
-template <int BITS, int NSUB, int NCHUNK>
+template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 hipError_t launch_gu_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kMfmaMaxCols + 1) * NSUB * 8;
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = set_lds(&k_gu_mfma<BITS, NSUB, NCHUNK>, lds);
+        const hipError_t e = set_lds(&k_gu_mfma<BITS, NSUB, NCHUNK, PAR>, lds);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    return launch(k_gu_mfma<BITS, NSUB, NCHUNK>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
+    return launch(k_gu_mfma<BITS, NSUB, NCHUNK, PAR>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
-template <int BITS, int NSUB, int NCHUNK>
+template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kDownStageRoutes + 1) * NSUB * 8;
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = set_lds(&k_down_mfma<BITS, NSUB, NCHUNK>, lds);
+        const hipError_t e = set_lds(&k_down_mfma<BITS, NSUB, NCHUNK, PAR>, lds);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    return launch(k_down_mfma<BITS, NSUB, NCHUNK>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
+    return launch(k_down_mfma<BITS, NSUB, NCHUNK, PAR>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
 
 template <int D, int BITS, int LPR>
@@ -937,6 +946,18 @@ hipError_t launch_down_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hip
     return hipGetLastError();
 }
 } // namespace
+
+// Mixed layers run their two banks on the MFMA kernels: H = 2048, I = 512, per-row scales,
+// chunked fp16 codebooks prepared for both banks.
+bool moe_mixed_mfma(const LayerDev& L) {
+    if (!L.mixed || L.H != 2048 || L.I != 512) return false;
+    for (int p = 0; p < 3; ++p)
+        for (int b = 0; b < 2; ++b)
+            if (L.pb[p][b].ngrp != 1 || !L.pb[p][b].book4) return false;
+    return true;
+}
+
+bool moe_plans_in_gate_up(const LayerDev& L) { return moe_uses_mfma(L) || moe_mixed_mfma(L); }
 
 bool moe_uses_mfma(const LayerDev& L) {
     if (L.mixed) return false;
@@ -983,16 +1004,11 @@ int mfma_grid() {
 
 hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     init_grid();
-    if (L.mixed) {  // d4: H/4 = 512 subvectors -> 32 lanes per row; d8: 256 -> 16
-        if (L.H != 2048 || L.I != 512) return hipErrorInvalidValue;
-        static bool attr = false;
-        if (!attr) {
-            const hipError_t e = set_lds(&k_gu_mixed<32, 16>, kFinLdsMax);
-            if (e != hipSuccess) return e;
-            attr = true;
-        }
-        return launch(k_gu_mixed<32, 16>, dim3(L.I / kGuRowsPerBlock, M * L.K + 1), dim3(256),
-                      static_cast<size_t>(M) * fin_stride(L.H) * sizeof(fin_t), st, L, B, M);
+    if (L.mixed) {  // the two banks on the MFMA kernels: even experts d4/8-bit, odd d8/14-bit
+        if (!moe_mixed_mfma(L)) return hipErrorInvalidValue;
+        const hipError_t e = launch_gu_mfma_g<8, 512, 1, 0>(L, B, M, st);
+        if (e != hipSuccess) return e;
+        return launch_gu_mfma_g<14, 256, 2, 1>(L, B, M, st);
     }
     if (moe_uses_narrow(L, M)) return launch_gate_up4(L, B, M, st);
     const int D = L.p[0].dim, BT = L.p[0].bits;
@@ -1020,10 +1036,11 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
 
 hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     init_grid();
-    if (L.mixed) {  // d4: I/4 = 128 subvectors -> 8 lanes per row; d8: 64 -> 4
-        if (L.H != 2048 || L.I != 512) return hipErrorInvalidValue;
-        return launch(k_down_mixed<8, 4>, dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256),
-                      static_cast<size_t>(M) * fin_stride(L.I) * sizeof(fin_t), st, L, B, M);
+    if (L.mixed) {
+        if (!moe_mixed_mfma(L)) return hipErrorInvalidValue;
+        const hipError_t e = launch_down_mfma_g<8, 128, 1, 0>(L, B, M, st);
+        if (e != hipSuccess) return e;
+        return launch_down_mfma_g<14, 64, 2, 1>(L, B, M, st);
     }
     if (moe_uses_narrow(L, M)) return launch_down4(L, B, M, st);
     const int D = L.p[2].dim, BT = L.p[2].bits;
@@ -1088,6 +1105,11 @@ hipError_t launch_tile_codes(const uint32_t* codes, int64_t rows, int words, int
 
 hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_t* book4, hipStream_t st) {
     hipLaunchKernelGGL(k_split_book, dim3(512), dim3(256), 0, st, book, entries, dim, book4);
+    return hipGetLastError();
+}
+hipError_t launch_split_book_i8(const int8_t* book, float scale, int entries, int dim, uint16_t* book4,
+                                hipStream_t st) {
+    hipLaunchKernelGGL(k_split_book_i8, dim3(512), dim3(256), 0, st, book, scale, entries, dim, book4);
     return hipGetLastError();
 }
 
