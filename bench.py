@@ -264,16 +264,24 @@ def main():
     planp = torch.empty(2 + 4 * Mp * K, dtype=torch.int32, device=dev)
     rp = q38.routes(plan=planp)
 
-    def prefill(r=None):
+    def prefill(sp_, r=None):
         q38.check(q38.lib.q38_moe_forward(Lp.h, xp.data_ptr(), Mp, yp.data_ptr(), C.byref(r) if r else None,
-                                          wsp.data_ptr(), wsp.numel(), sp))
-    prefill(rp)
+                                          wsp.data_ptr(), wsp.numel(), sp_))
+    prefill(sp, rp)
     torch.cuda.synchronize()
     up = int(planp[0].item())
+    gp = None
+    if not args.no_graph:
+        gp = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gp):
+            prefill(torch.cuda.current_stream().cuda_stream)
     pt = []
     for _ in range(10):
         ev0.record(stream)
-        prefill()
+        if gp is not None:
+            gp.replay()
+        else:
+            prefill(sp)
         ev1.record(stream)
         torch.cuda.synchronize()
         pt.append(ev0.elapsed_time(ev1))
@@ -305,12 +313,23 @@ def main():
     q38.check(q38.lib.q38_verify_chain(larm, NLm, hm.data_ptr(), Mm, 1e-6, trm, wsm.data_ptr(), wsm.numel(), sp))
     torch.cuda.synchronize()
     um = [int(p[0].item()) for p in plm]
+
+    def mixed_chain(sp_):
+        q38.check(q38.lib.q38_verify_chain(larm, NLm, hm.data_ptr(), Mm, 1e-6, None, wsm.data_ptr(), wsm.numel(),
+                                           sp_))
+    gm = None
+    if not args.no_graph:
+        gm = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gm):
+            mixed_chain(torch.cuda.current_stream().cuda_stream)
     mt = []
     for _ in range(10):
         hm.copy_(hm0)
         ev0.record(stream)
-        q38.check(q38.lib.q38_verify_chain(larm, NLm, hm.data_ptr(), Mm, 1e-6, None, wsm.data_ptr(), wsm.numel(),
-                                           sp))
+        if gm is not None:
+            gm.replay()
+        else:
+            mixed_chain(sp)
         ev1.record(stream)
         torch.cuda.synchronize()
         mt.append(ev0.elapsed_time(ev1))
