@@ -130,7 +130,8 @@ int q38_supports_segmented_vq(int dimension, int packed_bits);
  * Replaces SparseMoe (include/qwen38/sparse_moe.hpp:46-214). */
 int q38_moe_layer_create(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_weights* weights,
                          q38_moe_layer** out);
-/* Mixed-geometry layer (desc->mixed = 1) over caller-owned tensors. */
+/* Mixed-geometry layer (desc->mixed = 1) over caller-owned tensors. Allocates the INT8
+ * books decoded to fp16 chunks (3 x 256 KiB) for the MFMA kernels. */
 int q38_moe_layer_create_mixed(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_mixed_weights* weights,
                                q38_moe_layer** out);
 /* Library-owned synthetic layer: every tensor generated from (seed, layer_index) by the

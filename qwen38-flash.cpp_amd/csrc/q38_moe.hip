@@ -14,7 +14,9 @@
 //   k_down_mfma   SwiGLU of the gate/up sums + down projection (R7, R8), same scheme.
 //   k_combine     ordered route reduction (slot order) + shared expert x sigmoid gate +
 //                 merge (R8, R10, R11); in a chain it adds the residual in place.
-// Layers with per-64-input scale groups use the k_*_grouped VALU kernels instead.
+// Rows <= 4 take the narrow kernels of q38_moe4.hip instead of k_topk_plan + k_*_mfma.
+// Mixed layers (two codebook geometries by expert parity) run k_gu_mfma / k_down_mfma once
+// per bank. Layers with per-64-input scale groups use the k_*_grouped VALU kernels.
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
 #include "q38_moe_dev.hpp"
