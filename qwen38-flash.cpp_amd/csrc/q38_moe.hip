@@ -372,7 +372,8 @@ __device__ __forceinline__ int parity_slots(const int32_t* plan, int nu, int has
 // PAR >= 0 (mixed layers): only the slots whose expert has that parity, with the
 // geometry of that bank (L.pb[proj][PAR], expert index e / 2); the even bank (one codebook
 // chunk) also clears plane 1 of its outputs, so a consumer can add both planes for every
-// route.
+// route. The even bank's launch routes and publishes the plan; the odd bank's launch,
+// which follows it, reads the plan.
 template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B, int M) {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -392,10 +393,18 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     const ProjDev& P = PAR < 0 ? L.p[proj] : L.pb[proj][PAR < 0 ? 0 : PAR];
     // waves 0-3 load the codebook chunk while waves 4-7 route; every workgroup derives
     // the same plan and workgroup 0 publishes it
-    if (wave < 4) fill_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, tid, 256);
-    topk_plan_block(L, B, M, blockIdx.x == 0, plan, tk, 4);
-    if (blockIdx.x == 0)
-        for (int i = tid; i < 2 + 4 * M * L.K; i += kMfmaThreads) B.plan[i] = plan[i];
+    if (PAR == 1) {
+        // the odd bank runs right after the even bank's launch, which routed and published
+        // the plan (and the routes) on the same stream
+        for (int i = tid; i < 2 + 4 * M * L.K; i += kMfmaThreads) plan[i] = B.plan[i];
+        fill_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, tid, kMfmaThreads);
+        __syncthreads();
+    } else {
+        if (wave < 4) fill_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, tid, 256);
+        topk_plan_block(L, B, M, blockIdx.x == 0, plan, tk, 4);
+        if (blockIdx.x == 0)
+            for (int i = tid; i < 2 + 4 * M * L.K; i += kMfmaThreads) B.plan[i] = plan[i];
+    }
     const int H = L.H, I = L.I, K = L.K;
     const int nu = plan[0];
     const int nslots = PAR < 0 ? nu + (L.has_shared ? 1 : 0) : parity_slots(plan, nu, L.has_shared, L.E, PAR, pslots);
