@@ -194,19 +194,19 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
         Q38_STAMPV(0, 5, ss[MR - 1]);
         lds_barrier();
         Q38_STAMP(0, 6);
-        // every row's wave totals at once, then the MR independent rsqrt chains
+        // Lane r forms row r's total (wave totals in wave order) and 1 / rms, one chain for
+        // all rows instead of MR chains in every lane (the phase is VALU-bound); the results
+        // are read back from lanes 0..MR-1.
         float inv[MR];
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
+        {
+            const int rl = lane < MR ? lane : 0;
             float t = 0.0f;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) t += red[r][w];
-            inv[r] = 1.0f / sqrtf(t / static_cast<float>(H) + eps);
-        }
-        // (all rows' chains side by side: keeps the compiler from sinking each into its
-        // row's guarded stores below, one after another)
+            for (int w = 0; w < NW; ++w) t += red[rl][w];
+            const float il = 1.0f / sqrtf(t / static_cast<float>(H) + eps);
 #pragma unroll
-        for (int r = 0; r < MR; ++r) asm volatile("" ::"v"(inv[r]));
+            for (int r = 0; r < MR; ++r) inv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(il), r));
+        }
 #pragma unroll
         for (int r = 0; r < MR; ++r)
             if (r < M) {
