@@ -179,62 +179,116 @@ constexpr int kPfLd = kPfK + 8; // fp16 row pitch of the LDS tiles
 
 typedef _Float16 Tile[kPfLd];
 
-// Decode the 64 x 256 fp16 weight tile of rows [o0, o0 + 64) of `expert`, K block kb, into
-// As: thread t decodes codes [8 (t % 4), 8 (t % 4) + 8) of row t / 4 (fp16 codebook
-// entries, 16 bytes each, read through the cache).
-__device__ __forceinline__ void decode_tile(const ProjDev& P, int expert, int OUT, int o0, int kb, Tile* As) {
-    const int t = threadIdx.x, row = t >> 2, qq = t & 3;
+// The 64 x 256 fp16 weight tile of rows [o0, o0 + 64) of `expert`, K block kb, is decoded
+// into As in two steps so that the code words of block kb + 1 can be in flight while block
+// kb is decoded and multiplied: load_codes reads the 14 packed words (32 d8 codes) of row
+// t / 4 into registers; decode_gather picks codes [8 (t % 4), 8 (t % 4) + 8) out of them and
+// issues their fp16 codebook entries (16 bytes each, read through the cache); store_tile
+// writes the entries to As.
+__device__ __forceinline__ void load_codes(const ProjDev& P, int expert, int OUT, int o0, int kb,
+                                           uint32_t (&w)[14]) {
+    const int row = threadIdx.x >> 2;
     const uint32_t* src = P.codes + (static_cast<size_t>(expert) * OUT + o0 + row) * P.words + kb * 14;
-    uint32_t w[15];
 #pragma unroll
     for (int i = 0; i < 7; ++i) {
         const uint2 v = reinterpret_cast<const uint2*>(src)[i];
         w[2 * i] = v.x;
         w[2 * i + 1] = v.y;
     }
+}
+
+__device__ __forceinline__ void decode_gather(const ProjDev& P, const uint32_t (&wc)[14], uint4 (&e)[8]) {
+    const int qq = threadIdx.x & 3;
+    uint32_t w[15];
+#pragma unroll
+    for (int i = 0; i < 14; ++i) w[i] = wc[i];
     w[14] = 0;
-    uint32_t c[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint32_t c0 = code_from<14>(w, i), c1 = code_from<14>(w, 8 + i);
         const uint32_t c2 = code_from<14>(w, 16 + i), c3 = code_from<14>(w, 24 + i);
-        c[i] = qq == 0 ? c0 : qq == 1 ? c1 : qq == 2 ? c2 : c3;
+        const uint32_t c = qq == 0 ? c0 : qq == 1 ? c1 : qq == 2 ? c2 : c3;
+        e[i] = *reinterpret_cast<const uint4*>(P.book + static_cast<size_t>(c) * 8);
     }
-    uint4 e[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = *reinterpret_cast<const uint4*>(P.book + static_cast<size_t>(c[i]) * 8);
+}
+
+__device__ __forceinline__ void store_tile(const uint4 (&e)[8], Tile* As) {
+    const int t = threadIdx.x, row = t >> 2, qq = t & 3;
 #pragma unroll
     for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(&As[row][64 * qq + 8 * i]) = e[i];
 }
 
+// Stage routes [64 ch, 64 ch + 64) of the pass (K block kb) in two steps, loads then LDS
+// stores: thread t moves 8 fp16 of columns 8 (t % 32) for routes t / 32 + 8 m (m < 8); rows
+// past np are zeros. src_row(j) gives the source row of pass route j in `src` ([*, IN] fp16).
+template <typename SrcRow>
+__device__ __forceinline__ void stage_load(const uint16_t* src, int IN, int kb, int ch, int np, uint4 (&v)[8],
+                                           SrcRow src_row) {
+    const int j0 = threadIdx.x >> 5, c8 = threadIdx.x & 31;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int route = ch * kPfRoutes + j0 + 8 * m;
+        v[m] = make_uint4(0u, 0u, 0u, 0u);
+        if (route < np)
+            v[m] = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(src_row(route)) * IN + kb * kPfK + 8 * c8);
+    }
+}
+
+__device__ __forceinline__ void stage_store(const uint4 (&v)[8], Tile* Bt) {
+    const int j0 = threadIdx.x >> 5, c8 = threadIdx.x & 31;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) *reinterpret_cast<uint4*>(&Bt[j0 + 8 * m][8 * c8]) = v[m];
+}
+
 // One accumulation pass over all K blocks for routes [0, np) of the pass (np <= kPfPass):
-// acc[4 ch + t] = rows 16 wave + (0..15) x routes 64 ch + 16 t + (0..15).
-template <typename StageB>
+// acc[4 ch + t] = rows 16 wave + (0..15) x routes 64 ch + 16 t + (0..15). Per K block: the
+// codebook gathers of the block and the loads of its first B tile are issued together, then
+// the next block's code words (clamped to the last block: always in bounds), which stay in
+// flight through the block's MFMAs. The barriers wait only for LDS traffic, so they do not
+// drain those prefetches. 16-route B sub-tiles with no route are skipped.
+template <typename StageLoad>
 __device__ __forceinline__ void pf_pass(const ProjDev& P, int expert, int OUT, int IN, int o0, int np, Tile* As,
-                                        Tile* Bs, f4_t (&acc)[4 * kPfChunks], StageB stage_b) {
+                                        Tile* Bs, f4_t (&acc)[4 * kPfChunks], StageLoad stage_b) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, q = lane >> 4;
 #pragma unroll
     for (int i = 0; i < 4 * kPfChunks; ++i) acc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
     const int nch = (np + kPfRoutes - 1) / kPfRoutes;
-    for (int kb = 0; kb < IN / kPfK; ++kb) {
-        __syncthreads();  // the previous K block's tiles are consumed
-        decode_tile(P, expert, OUT, o0, kb, As);
-        __syncthreads();
+    const int nkb = IN / kPfK;
+    uint32_t w[14];
+    load_codes(P, expert, OUT, o0, 0, w);
+    for (int kb = 0; kb < nkb; ++kb) {
+        lds_barrier_dma_pending();  // the previous K block's tiles are consumed
+        {
+            uint4 e[8], bv[8];
+            decode_gather(P, w, e);
+            stage_b(kb, 0, bv);
+            load_codes(P, expert, OUT, o0, kb + 1 < nkb ? kb + 1 : kb, w);
+            store_tile(e, As);
+            stage_store(bv, Bs);
+        }
+        lds_barrier_dma_pending();
         h8_t af[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) af[s] = *reinterpret_cast<const h8_t*>(&As[16 * wave + r16][32 * s + 8 * q]);
 #pragma unroll
         for (int ch = 0; ch < kPfChunks; ++ch) {
             if (ch < nch) {  // workgroup-uniform
-                if (ch) __syncthreads();
-                stage_b(kb, ch, Bs);
-                __syncthreads();
+                if (ch) {
+                    uint4 bv[8];
+                    stage_b(kb, ch, bv);
+                    lds_barrier_dma_pending();  // the previous B tile is consumed
+                    stage_store(bv, Bs);
+                    lds_barrier_dma_pending();
+                }
+                const int nv = np - ch * kPfRoutes;  // routes of this B tile (> 0)
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
+                    if (16 * t < nv) {  // workgroup-uniform
 #pragma unroll
-                    for (int s = 0; s < 8; ++s) {
-                        const h8_t bf = *reinterpret_cast<const h8_t*>(&Bs[16 * t + r16][32 * s + 8 * q]);
-                        acc[4 * ch + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bf, acc[4 * ch + t], 0, 0, 0);
+                        for (int s = 0; s < 8; ++s) {
+                            const h8_t bf = *reinterpret_cast<const h8_t*>(&Bs[16 * t + r16][32 * s + 8 * q]);
+                            acc[4 * ch + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], bf, acc[4 * ch + t], 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -264,24 +318,10 @@ __device__ __forceinline__ void pf_store(const ProjDev& P, int expert, int OUT, 
     }
 }
 
-// Stage routes [64 ch, 64 ch + 64) of the pass into Bt: 8 fp16 per thread-step, zero rows
-// past np. src_row(j) gives the source row of pass route j in `src` ([*, IN] fp16).
-template <typename SrcRow>
-__device__ __forceinline__ void stage_rows(const uint16_t* src, int IN, int kb, int ch, int np, Tile* Bt,
-                                           SrcRow src_row) {
-    for (int i = threadIdx.x; i < kPfRoutes * (kPfK / 8); i += 256) {
-        const int j = i / (kPfK / 8), c8 = i % (kPfK / 8);
-        const int route = ch * kPfRoutes + j;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (route < np)
-            v = *reinterpret_cast<const uint4*>(src + static_cast<size_t>(src_row(route)) * IN + kb * kPfK + 8 * c8);
-        *reinterpret_cast<uint4*>(&Bt[j][8 * c8]) = v;
-    }
-}
-
-__global__ __launch_bounds__(256) void k_gu_pf(LayerDev L, MoeBufs B, int M) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gu_pf(LayerDev L, MoeBufs B, int M) {
     __shared__ __align__(16) Tile As[kPfRows];
     __shared__ __align__(16) Tile Bs[kPfRoutes];
+    __shared__ int src_rows[kPfPass];  // source row of each route of the pass
     int expert, n, pos0;
     if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
     const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
@@ -292,9 +332,11 @@ __global__ __launch_bounds__(256) void k_gu_pf(LayerDev L, MoeBufs B, int M) {
     f4_t acc[4 * kPfChunks];
     for (int p0 = 0; p0 < n; p0 += kPfPass) {
         const int np = n - p0 < kPfPass ? n - p0 : kPfPass;
-        pf_pass(P, expert, L.I, L.H, o0, np, As, Bs, acc, [&](int kb, int ch, Tile* Bt) {
-            stage_rows(B.x16, L.H, kb, ch, np, Bt,
-                       [&](int j) { return route_row(B.plan, M, L.K, pos0, p0 + j, shared); });
+        lds_barrier();  // the previous pass's row table is consumed
+        for (int j = threadIdx.x; j < np; j += 256) src_rows[j] = route_row(B.plan, M, L.K, pos0, p0 + j, shared);
+        // (published by the first barrier of the pass)
+        pf_pass(P, expert, L.I, L.H, o0, np, As, Bs, acc, [&](int kb, int ch, uint4 (&v)[8]) {
+            stage_load(B.x16, L.H, kb, ch, np, v, [&](int j) { return src_rows[j]; });
         });
         pf_store(P, expert, L.I, o0, p0, np, pos0, acc, out);
     }
@@ -305,7 +347,7 @@ __global__ __launch_bounds__(256) void k_swiglu_pf(MoeBufs B, int64_t total) {
         B.h16[i] = f2h(swiglu(B.g[i], B.u[i]));
 }
 
-__global__ __launch_bounds__(256) void k_dn_pf(LayerDev L, MoeBufs B, int M) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_dn_pf(LayerDev L, MoeBufs B, int M) {
     __shared__ __align__(16) Tile As[kPfRows];
     __shared__ __align__(16) Tile Bs[kPfRoutes];
     int expert, n, pos0;
@@ -315,8 +357,8 @@ __global__ __launch_bounds__(256) void k_dn_pf(LayerDev L, MoeBufs B, int M) {
     f4_t acc[4 * kPfChunks];
     for (int p0 = 0; p0 < n; p0 += kPfPass) {
         const int np = n - p0 < kPfPass ? n - p0 : kPfPass;
-        pf_pass(P, expert, L.H, L.I, o0, np, As, Bs, acc, [&](int kb, int ch, Tile* Bt) {
-            stage_rows(B.h16, L.I, kb, ch, np, Bt, [&](int j) { return pos0 + p0 + j; });
+        pf_pass(P, expert, L.H, L.I, o0, np, As, Bs, acc, [&](int kb, int ch, uint4 (&v)[8]) {
+            stage_load(B.h16, L.I, kb, ch, np, v, [&](int j) { return pos0 + p0 + j; });
         });
         pf_store(P, expert, L.H, o0, p0, np, pos0, acc, B.d, B.plan, M * L.K);
     }
