@@ -110,62 +110,98 @@ constexpr int kSortMax = 32768;  // routes per call (rows x k); route ids fit 16
 // Plan layout (shared with the verify kernels): [0] unique experts nu, [1 + u] expert of
 // slot u, [1 + MK + u] first sorted position of slot u (u <= nu, the last is MK),
 // [2 + 2MK + i] route at sorted position i, [2 + 3MK + route] its sorted position.
-__global__ __launch_bounds__(1024) void k_plan_sort(MoeBufs B, int MK) {
-    __shared__ uint32_t key[kSortMax];
-    __shared__ int scan[1024];
-    const int tid = threadIdx.x;
-    int NP = 1;
-    while (NP < MK) NP <<= 1;
-    for (int i = tid; i < NP; i += 1024)
-        key[i] = i < MK ? (static_cast<uint32_t>(B.experts[i]) << 16) | static_cast<uint32_t>(i) : 0xFFFFFFFFu;
-    __syncthreads();
-    for (int k = 2; k <= NP; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = tid; i < NP; i += 1024) {
-                const int l = i ^ j;
-                if (l > i) {
-                    const uint32_t a = key[i], b = key[l];
-                    if ((a > b) == ((i & k) == 0)) {
-                        key[i] = b;
-                        key[l] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
+//
+// The plan is a stable counting sort of the routes by expert (routes keep ascending order
+// within an expert), in one workgroup of 16 waves. Wave w owns the contiguous routes
+// [w c, w c + c) and walks them 64 at a time in order; within such a batch, lanes with the
+// same expert find each other with one ballot per expert-id bit, and a lane's rank is the
+// number of lower lanes in its group.
+//   A: every group's last lane adds the group size to cnt[w][e];
+//   B: per expert, a scan over experts of the totals (and of the nonzero flags: the slot
+//      numbers) gives its first position, and a scan over waves turns cnt[w][e] into wave
+//      w's first position within the expert;
+//   C: the walk again: position = cnt[w][e] + rank, the group's last lane advances cnt.
+// Counts and positions are below 2^16 (MK <= kSortMax), so cnt holds 16-bit values.
+constexpr int kPlanWaves = 16;
+constexpr int kPlanExperts = 1024;  // expert ids < 2^10
+
+__device__ __forceinline__ void plan_group(int e, bool valid, int lane, int& rank, int& cnt) {
+    uint64_t same = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 10; ++bit) {
+        const bool on = (e >> bit) & 1;
+        const uint64_t bal = __ballot(on);
+        same &= on ? bal : ~bal;
     }
-    int32_t* plan = B.plan;
-    const int chunk = (MK + 1023) / 1024;
-    const int a = tid * chunk < MK ? tid * chunk : MK;
-    const int b = a + chunk < MK ? a + chunk : MK;
-    int c = 0;
-    for (int i = a; i < b; ++i) {
-        const uint32_t kk = key[i];
-        const int route = static_cast<int>(kk & 0xFFFFu);
-        plan[2 + 2 * MK + i] = route;
-        plan[2 + 3 * MK + route] = i;
-        if (i == 0 || (key[i - 1] >> 16) != (kk >> 16)) ++c;
-    }
-    scan[tid] = c;
+    rank = __popcll(same & ((1ull << lane) - 1ull));
+    cnt = __popcll(same);
+}
+
+__global__ __launch_bounds__(1024) void k_plan_sort(MoeBufs B, int MK, int E) {
+    __shared__ uint16_t cnt[kPlanWaves][kPlanExperts];
+    __shared__ uint32_t scan[kPlanExperts];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    for (int i = tid; i < kPlanWaves * kPlanExperts; i += 1024) (&cnt[0][0])[i] = 0;
     __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {  // inclusive scan of the group starts
-        const int t = tid >= off ? scan[tid - off] : 0;
+    const int c = (MK + kPlanWaves - 1) / kPlanWaves;
+    const int r0 = w * c < MK ? w * c : MK, r1 = r0 + c < MK ? r0 + c : MK;
+    for (int b = r0; b < r1; b += 64) {  // A
+        const int i = b + lane;
+        const bool valid = i < r1;
+        const int e = valid ? B.experts[i] : 0;
+        int rank, n;
+        plan_group(e, valid, lane, rank, n);
+        if (valid && rank == n - 1) cnt[w][e] = static_cast<uint16_t>(cnt[w][e] + n);
+    }
+    __syncthreads();
+    // B: tid = expert. scan holds total | (total > 0) << 16 (totals sum to MK < 2^16).
+    uint32_t tot = 0;
+    if (tid < E)
+        for (int v = 0; v < kPlanWaves; ++v) tot += cnt[v][tid];
+    const uint32_t own = tot | (tot ? 1u << 16 : 0u);
+    scan[tid] = own;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {  // inclusive scan
+        const uint32_t t = tid >= off ? scan[tid - off] : 0u;
         __syncthreads();
         scan[tid] += t;
         __syncthreads();
     }
-    int rank = scan[tid] - c;
-    for (int i = a; i < b; ++i) {
-        const uint32_t kk = key[i];
-        if (i == 0 || (key[i - 1] >> 16) != (kk >> 16)) {
-            plan[1 + rank] = static_cast<int32_t>(kk >> 16);
-            plan[1 + MK + rank] = i;
-            ++rank;
-        }
+    const uint32_t excl = scan[tid] - own;
+    int32_t* plan = B.plan;
+    if (tid < E && tot) {
+        const int slot = static_cast<int>(excl >> 16);
+        plan[1 + slot] = tid;
+        plan[1 + MK + slot] = static_cast<int>(excl & 0xFFFFu);
     }
     if (tid == 1023) {
-        plan[0] = scan[1023];
-        plan[1 + MK + scan[1023]] = MK;
+        const int nu = static_cast<int>(scan[1023] >> 16);
+        plan[0] = nu;
+        plan[1 + MK + nu] = MK;
+    }
+    if (tid < E) {
+        uint32_t run = excl & 0xFFFFu;
+        for (int v = 0; v < kPlanWaves; ++v) {
+            const uint32_t n = cnt[v][tid];
+            cnt[v][tid] = static_cast<uint16_t>(run);
+            run += n;
+        }
+    }
+    __syncthreads();
+    for (int b = r0; b < r1; b += 64) {  // C
+        const int i = b + lane;
+        const bool valid = i < r1;
+        const int e = valid ? B.experts[i] : 0;
+        int rank, n;
+        plan_group(e, valid, lane, rank, n);
+        if (valid) {
+            const int pos = cnt[w][e] + rank;
+            plan[2 + 2 * MK + pos] = i;
+            plan[2 + 3 * MK + i] = pos;
+        }
+        // every lane has read cnt before the group's last lane advances it
+        __builtin_amdgcn_wave_barrier();
+        if (valid && rank == n - 1) cnt[w][e] = static_cast<uint16_t>(cnt[w][e] + n);
     }
 }
 
@@ -401,8 +437,8 @@ hipError_t launch_topk_rows(const LayerDev& L, const MoeBufs& B, int M, hipStrea
 }
 
 hipError_t launch_plan_sort(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    if (M * L.K > kSortMax) return hipErrorInvalidValue;
-    return launch(k_plan_sort, dim3(1), dim3(1024), 0, st, B, M * L.K);
+    if (M * L.K > kSortMax || L.E > kPlanExperts) return hipErrorInvalidValue;
+    return launch(k_plan_sort, dim3(1), dim3(1024), 0, st, B, M * L.K, L.E);
 }
 
 static int pf_slots(const LayerDev& L, int M) {
