@@ -296,6 +296,10 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 constexpr int kMfmaThreads = 512;       // 8 waves
 constexpr int kMfmaRowsPerItem = 128;   // 8 waves x 16 rows
 constexpr int kMfmaMaxCols = 8;         // routed rows staged per pass
+// Gate/up: routed rows staged per pass. With an 8-bit codebook (2 KiB) the LDS holds all 16
+// B columns of the MFMA tile, so up to 16 request rows are staged once per workgroup; a
+// 14-bit codebook chunk (128 KiB) leaves room for 8.
+__host__ __device__ constexpr int gu_mfma_cols(int bits) { return bits <= 8 ? 16 : kMfmaMaxCols; }
 
 template <int BITS, int NSUB>
 __device__ __forceinline__ void load_lane_words(const uint32_t* src, uint32_t* w) {
@@ -381,6 +385,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     __shared__ int32_t plan[kPlanInts];
     __shared__ int32_t pslots[PAR < 0 ? 1 : kPlanSlots];
     constexpr int KENT = 1 << BITS;
+    constexpr int MAXC = gu_mfma_cols(BITS);
     const uint2* book = reinterpret_cast<const uint2*>(lds);       // [KENT] x 4 fp16
     uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);          // [8 + 1 zero][NSUB][4] fp16
     constexpr int TYPES = 2 * NCHUNK;
@@ -415,8 +420,8 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     const int r16 = lane & 15, q = lane >> 4;
     constexpr int S4 = NSUB / 4;
     constexpr int WPL = S4 * BITS / 32;
-    // Verify widths (M <= 8): the chunk's dims of every request row are staged once.
-    const bool stage_all = M <= kMfmaMaxCols;
+    // Verify widths (M <= MAXC): the chunk's dims of every request row are staged once.
+    const bool stage_all = M <= MAXC;
     if (stage_all) {
         for (int i = tid; i < M * NSUB; i += kMfmaThreads) {
             const int row = i / NSUB, sv = i % NSUB;
@@ -425,7 +430,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
         }
     }
     for (int i = tid; i < NSUB; i += kMfmaThreads)
-        reinterpret_cast<uint2*>(xs)[kMfmaMaxCols * NSUB + i] = make_uint2(0u, 0u);
+        reinterpret_cast<uint2*>(xs)[MAXC * NSUB + i] = make_uint2(0u, 0u);
     lds_barrier();
     auto code_src = [&](int item) {
         int expert, n, pos0;
@@ -443,8 +448,8 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
         slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
         const bool shared = ui == nu;
         const int o0 = tile * kMfmaRowsPerItem + wave * 16;
-        for (int j0 = 0; j0 < n; j0 += kMfmaMaxCols) {
-            const int nj = n - j0 < kMfmaMaxCols ? n - j0 : kMfmaMaxCols;
+        for (int j0 = 0; j0 < n; j0 += MAXC) {
+            const int nj = n - j0 < MAXC ? n - j0 : MAXC;
             int xrow = r16;
             if (stage_all) {
                 if (r16 < nj) xrow = route_row(plan, M, K, pos0, j0 + r16, shared);
@@ -458,7 +463,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
                 }
                 lds_barrier();
             }
-            const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs_lane<NSUB>(xs, xrow, kMfmaMaxCols, q, r16 < nj));
+            const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs_lane<NSUB>(xs, xrow, MAXC, q, r16 < nj));
             if (r16 < nj) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
@@ -914,7 +919,7 @@ hipError_t set_lds(Kern k, size_t bytes) {
 
 template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 hipError_t launch_gu_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kMfmaMaxCols + 1) * NSUB * 8;
+    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(gu_mfma_cols(BITS) + 1) * NSUB * 8;
     static bool attr = false;
     if (!attr) {
         const hipError_t e = set_lds(&k_gu_mfma<BITS, NSUB, NCHUNK, PAR>, lds);
