@@ -5,14 +5,16 @@
 //                  64 request rows (the per-lane summation contract of the verify router)
 //   k_topk_rows    softmax + top-k of every row (one wave per row, R2)
 //   k_plan_sort    gather-by-expert plan of all routes (R3, the stable sort of
-//                  src/sparse_moe.cpp:2260-2271): a bitonic sort of the unique keys
-//                  (expert << 16 | route) in LDS, so every expert's routes come out in route
-//                  order; unique experts and their offsets by a block scan
+//                  src/sparse_moe.cpp:2260-2271): a counting sort by expert in one
+//                  workgroup, ranks within 64-route batches from wave ballots, so every
+//                  expert's routes come out in route order; unique experts and their
+//                  offsets by a block scan
 //   k_gu_pf        gate / up segmented GEMM (R9): one workgroup per (64-row output tile,
 //                  expert slot, projection). Per 256-input K block the VQ weight tile
 //                  (64 x 256) is decoded once into LDS as fp16 and used for every route of
 //                  the slot, 64 routes at a time, on v_mfma_f32_16x16x32_f16 (B = the
-//                  routes' fp16 inputs staged in LDS)
+//                  routes' fp16 inputs staged in LDS); the next K block's code words are
+//                  loaded while the current block is decoded and multiplied
 //   k_swiglu_pf    SwiGLU of every route with the reference's rounding points, fp16
 //   k_dn_pf        down segmented GEMM over the SwiGLU rows, same scheme
 // Row scales multiply the accumulated tile at the end. Layers: d8/14-bit, one scale per
