@@ -405,8 +405,10 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
         fill_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, tid, kMfmaThreads);
         __syncthreads();
     } else {
+        // an 8-bit book (2 KiB) is one load per thread of waves 0-3, which then route too
+        constexpr int route_wave0 = KENT <= 256 ? 0 : 4;
         if (wave < 4) fill_book<KENT>(P.book4 + static_cast<size_t>(chunk) * KENT * 4, lds, tid, 256);
-        topk_plan_block(L, B, M, blockIdx.x == 0, plan, tk, 4);
+        topk_plan_block(L, B, M, blockIdx.x == 0, plan, tk, route_wave0);
         if (blockIdx.x == 0)
             for (int i = tid; i < 2 + 4 * M * L.K; i += kMfmaThreads) B.plan[i] = plan[i];
     }
