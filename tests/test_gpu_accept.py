@@ -23,7 +23,7 @@ def test_sampled_decisions_match(gpu, q38, orc):
     rng = np.random.default_rng(0)
     V, k, T = 1000, 3, 0.7
     same = 0
-    n = 400
+    n = 2000  # the bar: >= 99.9% identical decisions, i.e. at most n // 1000 differences
     for rnd in range(n):
         tl = rng.normal(0, 2, (k + 1, V)).astype(np.float32)
         dl = (tl[:k] + rng.normal(0, 1, (k, V))).astype(np.float32)
@@ -31,7 +31,8 @@ def test_sampled_decisions_match(gpu, q38, orc):
         q /= q.sum(1, keepdims=True)
         drafts = [int(rng.choice(V, p=q[i])) for i in range(k)]
         same += gpu_accept(q38, tl, dl, drafts, T, 77, 1, rnd) == orc.accept_sampled(tl, dl, drafts, T, 77, 1, rnd)
-    assert same >= n - 1, same
+    print(f"sampled acceptance: {same}/{n} rounds identical to the oracle")
+    assert same >= n - n // 1000, same
 
 
 def test_sampled_full_vocab(gpu, q38, orc):
