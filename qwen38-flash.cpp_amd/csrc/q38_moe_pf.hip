@@ -48,11 +48,23 @@ __global__ __launch_bounds__(256) void k_logits_rows(LayerDev L, MoeBufs B, int 
     }
     const bool store_x = blockIdx.x == 0 && x != B.x;
     const int r1 = (static_cast<int>(blockIdx.y) + 1) * 64 < M ? (blockIdx.y + 1) * 64 : M;
+    // the next request row's inputs are loaded while this row's dot products run (the
+    // prefetch of the last row repeats it: always in bounds)
+    uint4 xn[T];
+    {
+        const int r0 = blockIdx.y * 64 + wave < r1 ? blockIdx.y * 64 + wave : r1 - 1;
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            xn[t] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(r0) * H + 512 * t + 8 * lane);
+    }
     for (int r = blockIdx.y * 64 + wave; r < r1; r += 4) {
         uint4 xv[T];
 #pragma unroll
+        for (int t = 0; t < T; ++t) xv[t] = xn[t];
+        const int rn = r + 4 < r1 ? r + 4 : r;
+#pragma unroll
         for (int t = 0; t < T; ++t)
-            xv[t] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(r) * H + 512 * t + 8 * lane);
+            xn[t] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(rn) * H + 512 * t + 8 * lane);
         float acc[NE];
 #pragma unroll
         for (int n = 0; n < NE; ++n) acc[n] = 0.0f;
