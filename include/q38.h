@@ -284,6 +284,11 @@ int q38_slot_rollback(q38_slot* slot);
 int q38_slot_info(const q38_slot* slot, uint64_t* token_count, int32_t* staged_rows, int32_t* draft_count);
 /* Committed hidden row (device [H] bf16), valid after the first commit. */
 const uint16_t* q38_slot_hidden(const q38_slot* slot);
+/* Generation of the staged verification: a number that every q38_slot_stage call makes
+ * new (1, 2, ...), or 0 when nothing is staged. A caller that holds a verification keeps
+ * the generation of its stage and commits only while the slot still reports it (the
+ * reference consumes the verification's own rows, src/mtp_verifier.cpp:129-145). */
+uint64_t q38_slot_generation(const q38_slot* slot);
 
 #ifdef __cplusplus
 }

@@ -881,8 +881,42 @@ void orc_argmax(const float* logits, int M, int64_t V, uint32_t* idx, float* val
         val[r] = l[best];
     }
 }
-// Q4 draft head: signed int4 [-8,7], one FP16 scale per 64 inputs; logit in double:
-// sum_g scale[v,g] * sum_{k in g} w*h. Synthetic weights only.
+// Q4 draft head logit of one vocab row (same arithmetic for explicit and synthetic weights):
+// signed int4 w[c] in [-8, 7], one FP16 scale per 64 inputs, in double:
+// sum_g scale[v, g] * sum_{c in g} w[c] * h[c] (groups in order, inputs in order).
+inline float head_q4_logit(const int8_t* w, const float* h, int H, const uint16_t* s_row) {
+    double acc = 0.0;
+    for (int g = 0; g < H / 64; ++g) {
+        double ga = 0.0;
+        for (int c = g * 64; c < g * 64 + 64; ++c) ga += static_cast<double>(w[c]) * h[c];
+        acc += static_cast<double>(f16_to_f32(s_row[g])) * ga;
+    }
+    return static_cast<float>(acc);
+}
+// Explicit Q4 head: Wp [V, H/2] bytes, input 2i in the low nibble and 2i + 1 in the high
+// nibble, each a signed (two's-complement) int4; s [V, H/64] fp16. This is the device
+// head's tensor contract (q38_head_create, Q38_HEAD_Q4G64).
+void orc_head_q4_logits(const uint8_t* Wp, const uint16_t* s, int64_t V, int H, const uint16_t* h, int M,
+                        float* logits, int threads) {
+    std::vector<float> hf(static_cast<size_t>(M) * H);
+    for (size_t i = 0; i < hf.size(); ++i) hf[i] = bf16_to_f32(h[i]);
+    const int chunks = static_cast<int>((V + 255) / 256);
+    parallel_for(chunks, threads, [&](int ch) {
+        std::vector<int8_t> w(H);
+        for (int64_t v = static_cast<int64_t>(ch) * 256; v < std::min(V, static_cast<int64_t>(ch + 1) * 256); ++v) {
+            const uint8_t* row = Wp + v * (H / 2);
+            for (int i = 0; i < H / 2; ++i) {
+                w[2 * i] = static_cast<int8_t>(static_cast<int>(row[i] & 0xF) - ((row[i] & 0x8) ? 16 : 0));
+                w[2 * i + 1] = static_cast<int8_t>(static_cast<int>(row[i] >> 4) - ((row[i] & 0x80) ? 16 : 0));
+            }
+            for (int r = 0; r < M; ++r)
+                logits[static_cast<size_t>(r) * V + v] =
+                    head_q4_logit(w.data(), hf.data() + static_cast<size_t>(r) * H, H, s + v * (H / 64));
+        }
+    });
+}
+// Q4 draft head with synthetic weights: w = draft_w_at (T_DRAFT_W stream), scales ~
+// U(1.6e-3, 1.6e-2) (T_DRAFT_S stream, index v * H/64 + g).
 void orc_head_q4_synth_logits(uint64_t seed, int H, int64_t v0, int64_t nv, const uint16_t* h, int M,
                               float* logits, int threads) {
     const uint64_t wk = stream_key(seed, kDraftLayer, T_DRAFT_W), sk = stream_key(seed, kDraftLayer, T_DRAFT_S);
@@ -892,17 +926,13 @@ void orc_head_q4_synth_logits(uint64_t seed, int H, int64_t v0, int64_t nv, cons
     const int chunks = static_cast<int>((nv + 255) / 256);
     parallel_for(chunks, threads, [&](int ch) {
         std::vector<int8_t> w(H);
+        std::vector<uint16_t> srow(G);
         for (int64_t v = v0 + static_cast<int64_t>(ch) * 256; v < std::min(v0 + nv, v0 + static_cast<int64_t>(ch + 1) * 256); ++v) {
             for (int c = 0; c < H; ++c) w[c] = draft_w_at(wk, static_cast<uint64_t>(v) * H + c);
-            for (int r = 0; r < M; ++r) {
-                double acc = 0.0;
-                for (int g = 0; g < G; ++g) {
-                    double ga = 0.0;
-                    for (int c = g * 64; c < g * 64 + 64; ++c) ga += static_cast<double>(w[c]) * hf[static_cast<size_t>(r) * H + c];
-                    acc += static_cast<double>(f16_to_f32(uniform_f16(sk, static_cast<uint64_t>(v) * G + g, 1.6e-3, 1.6e-2))) * ga;
-                }
-                logits[static_cast<size_t>(r) * nv + (v - v0)] = static_cast<float>(acc);
-            }
+            for (int g = 0; g < G; ++g) srow[g] = uniform_f16(sk, static_cast<uint64_t>(v) * G + g, 1.6e-3, 1.6e-2);
+            for (int r = 0; r < M; ++r)
+                logits[static_cast<size_t>(r) * nv + (v - v0)] =
+                    head_q4_logit(w.data(), hf.data() + static_cast<size_t>(r) * H, H, srow.data());
         }
     });
 }

@@ -68,6 +68,7 @@ struct q38_slot {
     uint16_t* rows[2] = {nullptr, nullptr};  // two [max_rows, H] checkpoint buffers
     int stage_buf = 0;                       // buffer the next stage writes
     const uint16_t* committed = nullptr;     // row of the committed checkpoint
+    uint64_t stages = 0;                     // verifications staged so far
 };
 
 extern "C" {
@@ -213,6 +214,9 @@ static int prepare_layer(q38_moe_layer* L) {
 int q38_moe_layer_create(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_weights* weights,
                          q38_moe_layer** out) {
     if (!ctx || !out || !weights) return fail(Q38_EINVAL, "q38_moe_layer_create: null argument");
+    if (desc && desc->mixed)
+        return fail(Q38_EINVAL, "q38_moe_layer_create: a mixed-geometry layer (desc->mixed = 1) takes per-bank "
+                                "tensors; use q38_moe_layer_create_mixed");
     if (int rc = validate_desc(desc)) return rc;
     if (!weights->router || (desc->has_shared && !weights->shared_gate))
         return fail(Q38_EINVAL, "router / shared gate tensors are required");
@@ -1011,6 +1015,7 @@ int q38_slot_stage(q38_slot* s, int32_t draft_count, const uint16_t* h, void* st
                            hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
     s->staged_rows = draft_count + 1;
     s->draft_count = draft_count;
+    s->stages += 1;
     return Q38_OK;
 }
 int q38_slot_commit(q38_slot* s, int64_t accepted, void* stream) {
@@ -1042,6 +1047,7 @@ int q38_slot_info(const q38_slot* s, uint64_t* token_count, int32_t* staged_rows
     return Q38_OK;
 }
 const uint16_t* q38_slot_hidden(const q38_slot* s) { return s && s->has_hidden ? s->committed : nullptr; }
+uint64_t q38_slot_generation(const q38_slot* s) { return s && s->staged_rows > 0 ? s->stages : 0; }
 
 } // extern "C"
 

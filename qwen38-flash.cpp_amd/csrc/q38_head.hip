@@ -499,8 +499,7 @@ hipError_t launch_i8(const HeadDev& hd, int M, const HeadWork& w, float* out, hi
 }
 template <int M>
 hipError_t launch_q4_m(const HeadDev& hd, const uint16_t* h, float* out, hipStream_t st) {
-    hipLaunchKernelGGL((k_head_q4<M>), dim3(head_grid()), dim3(256), 0, st, hd, h, out);
-    return hipGetLastError();
+    return launch(k_head_q4<M>, dim3(head_grid()), dim3(256), 0, st, hd, h, out);
 }
 } // namespace
 
@@ -508,23 +507,18 @@ hipError_t head_init_attrs() { return hipSuccess; }
 
 hipError_t launch_head_greedy(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, uint32_t* argmax,
                               float* logit, hipStream_t st) {
-    hipLaunchKernelGGL(k_head_prep, dim3(M), dim3(256), 0, st, h, hd.H, M, w);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch(k_head_prep, dim3(M), dim3(256), 0, st, h, hd.H, M, w);
     if (e != hipSuccess) return e;
     if ((e = launch_i8(hd, M, w, nullptr, st)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_head_cand, dim3(2048), dim3(256), 0, st, hd, M, w);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_head_exact, dim3(16, M), dim3(256), 0, st, hd, h, w);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_head_final, dim3(1), dim3(64), 0, st, M, w, argmax, logit);
-    return hipGetLastError();
+    if ((e = launch(k_head_cand, dim3(2048), dim3(256), 0, st, hd, M, w)) != hipSuccess) return e;
+    if ((e = launch(k_head_exact, dim3(16, M), dim3(256), 0, st, hd, h, w)) != hipSuccess) return e;
+    return launch(k_head_final, dim3(1), dim3(64), 0, st, M, w, argmax, logit);
 }
 
 hipError_t launch_head_logits(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, float* logits,
                               hipStream_t st) {
     if (hd.kind == 0) {
-        hipLaunchKernelGGL(k_head_prep, dim3(M), dim3(256), 0, st, h, hd.H, M, w);
-        const hipError_t e = hipGetLastError();
+        const hipError_t e = launch(k_head_prep, dim3(M), dim3(256), 0, st, h, hd.H, M, w);
         if (e != hipSuccess) return e;
         return launch_i8(hd, M, w, logits, st);
     }
@@ -553,9 +547,8 @@ hipError_t launch_scale_absmax(const uint16_t* scales, int64_t n, float* out, hi
 hipError_t launch_accept_sampled(const float* tl, const float* dl, const uint32_t* drafts, int k, int64_t V,
                                  float T, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out,
                                  hipStream_t st) {
-    hipLaunchKernelGGL(k_accept_sampled, dim3(1), dim3(kSampThreads), 0, st, tl, dl, drafts, k, V, T, seed, slot,
-                       round, out);
-    return hipGetLastError();
+    return launch(k_accept_sampled, dim3(1), dim3(kSampThreads), 0, st, tl, dl, drafts, k, V, T, seed, slot, round,
+                  out);
 }
 
 } // namespace q38

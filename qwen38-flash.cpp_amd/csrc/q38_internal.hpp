@@ -6,11 +6,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace q38 {
 
-// Kernel timing for the profiled entry points: when start is set, the next launch made
-// through launch() records start/stop at the kernel's own begin and end (the interval a
-// kernel trace reports), then the timer is cleared. One timer per host thread.
+// Kernel timing for the profiled entry points: while a timer is set, the first launch made
+// through launch() records `start` at its kernel's own begin and every launch records `stop`
+// at its kernel's end, so a phase of one or more kernels spans the first kernel's begin to
+// the last kernel's end (the interval a kernel trace reports); the caller clears the timer
+// after the phase. One timer per host thread. Every kernel launch of the library goes
+// through launch().
 struct KernelTimer {
     hipEvent_t start = nullptr, stop = nullptr;
 };
@@ -19,13 +24,29 @@ KernelTimer& kernel_timer();
 template <typename F, typename... Args>
 hipError_t launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
     KernelTimer& t = kernel_timer();
-    if (t.start) {
+    if (t.stop) {
         hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), st, t.start, t.stop, 0, args...);
-        t.start = t.stop = nullptr;
+        t.start = nullptr;
     } else {
         hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
     }
     return hipGetLastError();
+}
+
+// Dynamic-LDS limit of kernel KERN, raised once per device (thread-safe: a device bit is
+// set only after the attribute call succeeded; a race sets the same value twice).
+template <auto KERN>
+hipError_t ensure_lds(size_t bytes) {
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = uint64_t{1} << (dev & 63);
+    if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(KERN), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(bytes));
+    if (e == hipSuccess) done.fetch_or(bit, std::memory_order_acq_rel);
+    return e;
 }
 
 constexpr int kMaxRows = 16;   // verify rows per MoE call (4 slots x (1 + 3 drafts))

@@ -21,6 +21,8 @@
 #include "q38_internal.hpp"
 #include "q38_moe_dev.hpp"
 
+#include <mutex>
+
 namespace q38 {
 
 // ============================================================== generators
@@ -873,13 +875,15 @@ int next_pow2(int v) {
 int g_mfma_grid = 256;  // one persistent workgroup per CU (set from the device at first use)
 
 void init_grid() {
-    static bool done = false;
-    if (done) return;
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus >= 64)
-        g_mfma_grid = cus / 32 * 32;
-    done = true;
+    // (every device of the process is an MI355X with the same CU count; the value is the
+    // same whichever thread stores it first)
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus >= 64)
+            g_mfma_grid = cus / 32 * 32;
+    });
 }
 
 template <int T, bool NORM, int MR>
@@ -887,14 +891,7 @@ hipError_t launch_route_norm_t(const LayerDev& L, const MoeBufs& B, int M, const
                                hipStream_t st) {
     constexpr int NW = 2 * T;  // waves of H/4 threads
     const size_t lds = static_cast<size_t>(M) * 512 * T * 2;
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e =
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&k_route_norm<T, NORM, MR>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(MR * 512 * T * 2));
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    if (const hipError_t e = ensure_lds<k_route_norm<T, NORM, MR>>(MR * 512 * T * 2); e != hipSuccess) return e;
     const int rows = L.E + (L.has_shared ? 1 : 0);
     return launch(k_route_norm<T, NORM, MR>, dim3((rows + NW - 1) / NW), dim3(128 * T), lds, st, L, B, M, src, eps);
 }
@@ -913,32 +910,16 @@ hipError_t launch_route_norm_h(const LayerDev& L, const MoeBufs& B, int M, const
     return norm ? launch_route_norm_m<T, true>(L, B, M, src, eps, st) : launch_route_norm_m<T, false>(L, B, M, src, eps, st);
 }
 
-template <typename Kern>
-hipError_t set_lds(Kern k, size_t bytes) {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               static_cast<int>(bytes));
-}
-
 template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 hipError_t launch_gu_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(gu_mfma_cols(BITS) + 1) * NSUB * 8;
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e = set_lds(&k_gu_mfma<BITS, NSUB, NCHUNK, PAR>, lds);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    if (const hipError_t e = ensure_lds<k_gu_mfma<BITS, NSUB, NCHUNK, PAR>>(lds); e != hipSuccess) return e;
     return launch(k_gu_mfma<BITS, NSUB, NCHUNK, PAR>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
 template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kDownStageRoutes + 1) * NSUB * 8;
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e = set_lds(&k_down_mfma<BITS, NSUB, NCHUNK, PAR>, lds);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    if (const hipError_t e = ensure_lds<k_down_mfma<BITS, NSUB, NCHUNK, PAR>>(lds); e != hipSuccess) return e;
     return launch(k_down_mfma<BITS, NSUB, NCHUNK, PAR>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
 
@@ -946,22 +927,14 @@ template <int D, int BITS, int LPR>
 hipError_t launch_gu_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const size_t lds = static_cast<size_t>(M) * fin_stride(L.H) * sizeof(fin_t);
     if (lds > kFinLdsMax) return hipErrorInvalidValue;
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e = set_lds(&k_gu_grouped<D, BITS, LPR>, kFinLdsMax);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
-    hipLaunchKernelGGL((k_gu_grouped<D, BITS, LPR>), dim3(L.I / kGuRowsPerBlock, M * L.K + 1), dim3(256), lds, st, L,
-                       B, M);
-    return hipGetLastError();
+    if (const hipError_t e = ensure_lds<k_gu_grouped<D, BITS, LPR>>(kFinLdsMax); e != hipSuccess) return e;
+    return launch(k_gu_grouped<D, BITS, LPR>, dim3(L.I / kGuRowsPerBlock, M * L.K + 1), dim3(256), lds, st, L, B, M);
 }
 template <int D, int BITS, int LPR>
 hipError_t launch_down_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const size_t lds = static_cast<size_t>(M) * fin_stride(L.I) * sizeof(fin_t);
-    hipLaunchKernelGGL((k_down_grouped<D, BITS, LPR>), dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256), lds, st,
-                       L, B, M);
-    return hipGetLastError();
+    return launch(k_down_grouped<D, BITS, LPR>, dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256), lds, st, L, B,
+                  M);
 }
 } // namespace
 
@@ -1006,8 +979,7 @@ hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint1
 }
 
 hipError_t launch_topk_plan(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    hipLaunchKernelGGL(k_topk_plan, dim3(1), dim3(1024), 0, st, L, B, M);
-    return hipGetLastError();
+    return launch(k_topk_plan, dim3(1), dim3(1024), 0, st, L, B, M);
 }
 
 KernelTimer& kernel_timer() {
@@ -1111,8 +1083,7 @@ hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* 
 }
 
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, st, x, H, eps, y);
-    return hipGetLastError();
+    return launch(k_rmsnorm, dim3(M), dim3(256), 0, st, x, H, eps, y);
 }
 
 hipError_t launch_tile_codes(const uint32_t* codes, int64_t rows, int words, int bits, uint32_t* out, hipStream_t st) {

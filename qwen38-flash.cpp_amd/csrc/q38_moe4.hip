@@ -446,33 +446,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #endif
 }
 
-template <typename Kern>
-hipError_t set_lds4(Kern k, size_t bytes) {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               static_cast<int>(bytes));
-}
-
 template <int BITS, int NSUB, int NCHUNK, int D>
 hipError_t launch_gu4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     constexpr size_t lds = gu4_lds_bytes<BITS, NSUB, NCHUNK>();
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e = set_lds4(&k_gu4<BITS, NSUB, NCHUNK, D>, lds);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    if (const hipError_t e = ensure_lds<k_gu4<BITS, NSUB, NCHUNK, D>>(lds); e != hipSuccess) return e;
     return launch(k_gu4<BITS, NSUB, NCHUNK, D>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
 }
 template <int BITS, int NSUB, int NCHUNK, int D>
 hipError_t launch_dn4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     constexpr int KS = NSUB / 32, RG = 8 / KS;
     constexpr size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(RG) * (KS - 1) * 64 * 16;
-    static bool attr = false;
-    if (!attr) {
-        const hipError_t e = set_lds4(&k_dn4<BITS, NSUB, NCHUNK, D>, lds);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    if (const hipError_t e = ensure_lds<k_dn4<BITS, NSUB, NCHUNK, D>>(lds); e != hipSuccess) return e;
     return launch(k_dn4<BITS, NSUB, NCHUNK, D>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M);
 }
 } // namespace

@@ -139,16 +139,18 @@ SparseMoe& SparseMoe::operator=(SparseMoe&& o) noexcept {
     return *this;
 }
 
+void SparseMoe::reserve_workspace(std::size_t rows) const {
+    std::lock_guard<std::mutex> lk(g_ws_mutex);
+    const std::size_t need = q38_moe_workspace_size(&desc_, static_cast<int32_t>(std::max<std::size_t>(rows, 16)));
+    if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
+}
+
 std::vector<RouterSelection> SparseMoe::route_decode_batch(const DeviceTensor& input) const {
     const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
-    if (rows < 1 || rows > 16) throw std::runtime_error("route_decode: rows must be between 1 and 16");
+    if (rows < 1 || rows > 2048) throw std::runtime_error("route_decode: rows must be between 1 and 2048");
     const std::size_t k = experts_per_token();
     DeviceTensor ex({rows * k}, DType::i32), wt({rows * k}, DType::f32);
-    {
-        std::lock_guard<std::mutex> lk(g_ws_mutex);
-        const std::size_t need = q38_moe_workspace_size(&desc_, 16);
-        if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
-    }
+    reserve_workspace(rows);
     q38_route_out r{static_cast<int32_t*>(ex.data()), static_cast<float*>(wt.data()), nullptr, nullptr, nullptr};
     check(q38_moe_route(layer_, static_cast<const uint16_t*>(input.data()), static_cast<int32_t>(rows), &r,
                         workspace_.data(), workspace_.nbytes(), ctx_->stream()),
@@ -171,44 +173,70 @@ RouterSelection SparseMoe::route_decode(const DeviceTensor& input) const {
     return std::move(all.front());
 }
 
-DeviceTensor SparseMoe::forward_verify(const DeviceTensor& input) const {
-    const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
-    if (rows < 1 || rows > 16) throw std::runtime_error("forward_verify: rows must be between 1 and 16");
+// One q38_moe_forward over `rows` rows of input into a new tensor of the input's shape.
+DeviceTensor SparseMoe::forward_rows(const DeviceTensor& input, std::size_t rows, const char* what) const {
     DeviceTensor out(input.shape(), DType::bf16);
-    {
-        std::lock_guard<std::mutex> lk(g_ws_mutex);
-        const std::size_t need = q38_moe_workspace_size(&desc_, 16);
-        if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
-    }
+    reserve_workspace(rows);
+    std::lock_guard<std::mutex> lk(g_ws_mutex);  // the workspace is shared by the calls of this layer
     check(q38_moe_forward(layer_, static_cast<const uint16_t*>(input.data()), static_cast<int32_t>(rows),
                           static_cast<uint16_t*>(out.data()), nullptr, workspace_.data(), workspace_.nbytes(),
                           ctx_->stream()),
-          "forward_verify");
+          what);
     return out;
+}
+
+DeviceTensor SparseMoe::forward_verify(const DeviceTensor& input) const {
+    const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
+    if (input.shape().size() != 3 || input.shape()[0] != 1 || rows < 1 || rows > 1024)
+        throw std::runtime_error("MoE batch requires shape [1,S,hidden], S=1..1024");
+    return forward_rows(input, rows, "forward_verify");
+}
+
+DeviceTensor SparseMoe::forward_decode(const DeviceTensor& input) const {
+    const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
+    if (rows != 1) throw std::runtime_error("MoE decode requires shape [1,1,hidden]");
+    return forward_rows(input, 1, "forward_decode");
+}
+
+std::vector<DeviceTensor> SparseMoe::forward_decode_multi(const std::vector<DeviceTensor>& inputs) const {
+    if (inputs.empty()) throw std::runtime_error("multi-request MoE requires at least one row");
+    const std::size_t H = static_cast<std::size_t>(desc_.hidden);
+    if (inputs.size() > 2048) throw std::runtime_error("multi-request MoE takes at most 2048 rows");
+    for (const DeviceTensor& in : inputs)
+        if (rows_of(in, H) != 1) throw std::runtime_error("multi-request MoE requires [1,1,hidden] rows");
+    const std::size_t n = inputs.size();
+    DeviceTensor batch({1, n, H}, DType::bf16);
+    const auto st = static_cast<hipStream_t>(ctx_->stream());
+    for (std::size_t i = 0; i < n; ++i)
+        check_hip(hipMemcpyAsync(static_cast<char*>(batch.data()) + i * H * 2, inputs[i].data(), H * 2,
+                                 hipMemcpyDeviceToDevice, st),
+                  "gather rows");
+    DeviceTensor out = forward_rows(batch, n, "forward_decode_multi");
+    std::vector<DeviceTensor> rows;
+    rows.reserve(n);
+    for (std::size_t i = 0; i < n; ++i) {
+        DeviceTensor r(inputs[i].shape(), DType::bf16);
+        check_hip(hipMemcpyAsync(r.data(), static_cast<const char*>(out.data()) + i * H * 2, H * 2,
+                                 hipMemcpyDeviceToDevice, st),
+                  "scatter rows");
+        rows.push_back(std::move(r));
+    }
+    return rows;
 }
 
 DeviceTensor SparseMoe::forward_prefill(const DeviceTensor& input) const {
     const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
     if (rows < 1 || rows > 2048) throw std::runtime_error("MoE prefill requires shape [1,S,hidden], S=1..2048");
-    DeviceTensor out(input.shape(), DType::bf16);
-    std::lock_guard<std::mutex> lk(g_ws_mutex);
-    const std::size_t need = q38_moe_workspace_size(&desc_, static_cast<int32_t>(rows));
-    if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
-    check(q38_moe_forward(layer_, static_cast<const uint16_t*>(input.data()), static_cast<int32_t>(rows),
-                          static_cast<uint16_t*>(out.data()), nullptr, workspace_.data(), workspace_.nbytes(),
-                          ctx_->stream()),
-          "forward_prefill");
-    return out;
+    return forward_rows(input, rows, "forward_prefill");
 }
 
 DeviceTensor SparseMoe::forward_prefill_profiled(const DeviceTensor& input, MoePrefillTimings& timings) const {
     const std::size_t rows = rows_of(input, static_cast<std::size_t>(desc_.hidden));
     if (rows < 17 || rows > 2048) throw std::runtime_error("profiled MoE prefill requires S=17..2048");
     DeviceTensor out(input.shape(), DType::bf16);
-    std::lock_guard<std::mutex> lk(g_ws_mutex);
-    const std::size_t need = q38_moe_workspace_size(&desc_, static_cast<int32_t>(rows));
-    if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
     float ms[7] = {};
+    reserve_workspace(rows);
+    std::lock_guard<std::mutex> lk(g_ws_mutex);
     check(q38_moe_forward_prefill_profiled(layer_, static_cast<const uint16_t*>(input.data()),
                                            static_cast<int32_t>(rows), static_cast<uint16_t*>(out.data()), nullptr,
                                            workspace_.data(), workspace_.nbytes(), ms, ctx_->stream()),
@@ -326,6 +354,7 @@ MtpTargetVerification verify_mtp_target_layer_major_reference(const QwenModel& m
     MtpTargetVerification v;
     v.draft_count = drafts.size();
     v.origin = &origin;
+    v.generation = q38_slot_generation(origin.slot());
     const std::size_t H = model.hidden();
     for (std::size_t i = 0; i < tokens.size(); ++i) {
         MtpTargetVerifyRow row;
@@ -349,6 +378,8 @@ void commit_mtp_target_verification(MtpTargetVerification&& verification, std::s
         throw std::runtime_error("MTP accepted count exceeds verified draft count");
     if (verification.origin != &destination)
         throw std::runtime_error("MTP verification belongs to another decode state");
+    if (verification.generation == 0 || q38_slot_generation(destination.slot()) != verification.generation)
+        throw std::runtime_error("MTP verification is stale: the decode state holds a newer verification");
     check(q38_slot_commit(destination.slot(), static_cast<int64_t>(accepted), nullptr), "commit");
     verification.rows.clear();
     verification.draft_count = 0;

@@ -139,11 +139,18 @@ public:
     SparseMoe(const SparseMoe&) = delete;
     SparseMoe& operator=(const SparseMoe&) = delete;
 
-    // input [1, S, H] bf16 (normalised). Selections per row, read back to the host.
+    // input [1, S, H] bf16 (normalised), S in 1..2048. Selections per row, read back to the
+    // host.
     [[nodiscard]] RouterSelection route_decode(const DeviceTensor& input) const;
     [[nodiscard]] std::vector<RouterSelection> route_decode_batch(const DeviceTensor& input) const;
-    // forward_verify (src/sparse_moe.cpp:1953-2171): input [1, S, H] bf16, S in 1..16; output
-    // the same shape and dtype.
+    // forward_decode (src/sparse_moe.cpp:1629-1642): one row, input [1, 1, H] bf16.
+    [[nodiscard]] DeviceTensor forward_decode(const DeviceTensor& input) const;
+    // forward_decode_multi (src/sparse_moe.cpp:1775-1950): one [1, 1, H] row per request,
+    // routed and computed as one batch (rows 1..2048); one output per request.
+    [[nodiscard]] std::vector<DeviceTensor> forward_decode_multi(const std::vector<DeviceTensor>& inputs) const;
+    // forward_verify (src/sparse_moe.cpp:1953-2171): input [1, S, H] bf16, S in 1..1024
+    // (src/sparse_moe.cpp:1974-1976); output the same shape and dtype. S <= 16 takes the
+    // verify-width kernels, wider calls the segmented-GEMM kernels.
     [[nodiscard]] DeviceTensor forward_verify(const DeviceTensor& input) const;
     // forward_prefill (src/sparse_moe.cpp:2199-2624): input [1, S, H] bf16, S in 1..2048;
     // S > 16 takes the segmented-GEMM kernels.
@@ -159,6 +166,9 @@ public:
     [[nodiscard]] std::size_t experts_per_token() const noexcept { return static_cast<std::size_t>(desc_.top_k); }
 
 private:
+    DeviceTensor forward_rows(const DeviceTensor& input, std::size_t rows, const char* what) const;
+    void reserve_workspace(std::size_t rows) const;
+
     const Context* ctx_ = nullptr;
     q38_moe_layer* layer_ = nullptr;
     q38_moe_desc desc_{};
@@ -229,6 +239,7 @@ struct MtpTargetVerification {
     std::size_t draft_count{0};
     std::vector<MtpTargetVerifyRow> rows;
     ModelDecodeState* origin = nullptr;  // the state whose slot holds the staged checkpoints
+    std::uint64_t generation{0};         // the slot's staging generation of these rows
 };
 
 [[nodiscard]] MtpTargetVerification verify_mtp_target_layer_major_reference(const QwenModel& model,
@@ -238,7 +249,8 @@ struct MtpTargetVerification {
 
 // accepted = N keeps the checkpoint after current_token plus N accepted drafts. Consumes
 // all verification rows on success; validation failures leave verification and
-// destination intact.
+// destination intact. A verification whose checkpoints the state has since replaced (a
+// later verification was staged on it) is rejected.
 void commit_mtp_target_verification(MtpTargetVerification&& verification, std::size_t accepted,
                                     ModelDecodeState& destination);
 

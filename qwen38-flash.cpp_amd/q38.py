@@ -106,6 +106,7 @@ _sig("q38_slot_commit", C.c_int, P, I64, P)
 _sig("q38_slot_rollback", C.c_int, P)
 _sig("q38_slot_info", C.c_int, P, C.POINTER(U64), C.POINTER(I32), C.POINTER(I32))
 _sig("q38_slot_hidden", P, P)
+_sig("q38_slot_generation", C.c_uint64, P)
 
 
 def check(rc: int) -> int:

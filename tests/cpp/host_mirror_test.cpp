@@ -10,8 +10,11 @@
 // Prints one line per section and exits non-zero on the first failed check.
 #include "qwen38_verify.hpp"
 
+#include <hip/hip_runtime.h>
+
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <stdexcept>
 #include <vector>
@@ -120,9 +123,33 @@ static void gpu_tests() {
     const auto y2 = moe.forward_verify(x).to_host<std::uint16_t>();
     CHECK(y1 == y2);  // deterministic
     CHECK(throws<std::runtime_error>([&] {
-        qwen38::DeviceTensor bad({1, 17, 2048}, qwen38::DType::bf16);
+        qwen38::DeviceTensor bad({1, 1025, 2048}, qwen38::DType::bf16);
         (void)moe.forward_verify(bad);
     }));
+    // forward_decode / forward_decode_multi: one-row requests batched through one pass equal
+    // the rows of the same batch verified together
+    {
+        std::vector<qwen38::DeviceTensor> reqs;
+        for (std::size_t r = 0; r < 4; ++r) {
+            qwen38::DeviceTensor t({1, 1, 2048}, qwen38::DType::bf16);
+            CHECK(hipMemcpy(t.data(), static_cast<const char*>(x.data()) + r * 4096, 4096, hipMemcpyDeviceToDevice) ==
+                  hipSuccess);
+            reqs.push_back(std::move(t));
+        }
+        const auto outs = moe.forward_decode_multi(reqs);
+        CHECK(outs.size() == 4);
+        for (std::size_t r = 0; r < 4; ++r) {
+            const auto o = outs[r].to_host<std::uint16_t>();
+            CHECK(std::equal(o.begin(), o.end(), y1.begin() + r * 2048));
+        }
+        const auto d0 = moe.forward_decode(reqs[0]).to_host<std::uint16_t>();
+        std::vector<qwen38::DeviceTensor> one;
+        one.push_back(reqs[0].share());
+        const auto m0 = moe.forward_decode_multi(one);
+        CHECK(d0 == m0[0].to_host<std::uint16_t>());
+        CHECK(throws<std::runtime_error>([&] { (void)moe.forward_decode(x); }));
+        CHECK(throws<std::runtime_error>([&] { (void)moe.forward_decode_multi({}); }));
+    }
     // prefill widths: S <= 16 is the verify call, S = 64 the segmented kernels, profiled or not
     CHECK(moe.forward_prefill(x).to_host<std::uint16_t>() == y1);
     {
@@ -150,6 +177,30 @@ static void gpu_tests() {
         moe.set_router_bias(qwen38::DeviceTensor{});
         CHECK(moe.forward_verify(x).to_host<std::uint16_t>() == y1);
     }
+    // forward_verify accepts S = 1..1024 (src/sparse_moe.cpp:1974-1976): S = 17 and 1024 take
+    // the segmented kernels and equal the C ABI call; route_decode_batch agrees with q38_moe_route
+    for (const std::size_t S : {std::size_t{17}, std::size_t{1024}}) {
+        std::vector<std::uint32_t> toks(S);
+        for (std::size_t i = 0; i < S; ++i) toks[i] = static_cast<std::uint32_t>(3 + 11 * i);
+        qwen38::DeviceTensor h({S, 2048}, qwen38::DType::bf16), xs({1, S, 2048}, qwen38::DType::bf16);
+        CHECK(q38_embed_synthetic(seed, toks.data(), static_cast<int32_t>(S), 2048, static_cast<uint16_t*>(h.data()),
+                                  ctx.stream()) == Q38_OK);
+        CHECK(q38_rmsnorm(static_cast<const uint16_t*>(h.data()), static_cast<int32_t>(S), 2048, 1e-6F,
+                          static_cast<uint16_t*>(xs.data()), ctx.stream()) == Q38_OK);
+        const auto yv = moe.forward_verify(xs).to_host<std::uint16_t>();
+        qwen38::DeviceTensor yc({S, 2048}, qwen38::DType::bf16), ed({S * 10}, qwen38::DType::i32);
+        qwen38::DeviceTensor ws({q38_moe_workspace_size(&moe.desc(), static_cast<int32_t>(S))}, qwen38::DType::u32);
+        q38_route_out r{static_cast<int32_t*>(ed.data()), nullptr, nullptr, nullptr, nullptr};
+        CHECK(q38_moe_forward(moe.handle(), static_cast<const uint16_t*>(xs.data()), static_cast<int32_t>(S),
+                              static_cast<uint16_t*>(yc.data()), &r, ws.data(), ws.nbytes(), ctx.stream()) == Q38_OK);
+        ctx.synchronize();
+        CHECK(yv == yc.to_host<std::uint16_t>());
+        const auto exs = ed.to_host<int32_t>();
+        const auto sels = moe.route_decode_batch(xs);
+        CHECK(sels.size() == S);
+        for (std::size_t i = 0; i < S; ++i)
+            for (std::size_t k = 0; k < 10; ++k) CHECK(sels[i].experts[k] == static_cast<std::size_t>(exs[i * 10 + k]));
+    }
     CHECK(throws<std::runtime_error>([&] {
         qwen38::DeviceTensor bad({1, 2049, 2048}, qwen38::DType::bf16);
         (void)moe.forward_prefill(bad);
@@ -172,8 +223,21 @@ static void gpu_tests() {
     // validation failures leave the verification and the state intact
     CHECK(throws<std::runtime_error>([&] { qwen38::commit_mtp_target_verification(std::move(v), 4, state); }));
     CHECK(v.rows.size() == 4 && state.token_count() == 100);
-    qwen38::commit_mtp_target_verification(std::move(v), 2, state);
-    CHECK(v.rows.empty() && state.token_count() == 103);
+    // a second verification staged on the same state makes the first one stale: committing
+    // it is rejected with the state intact, the newer one commits
+    {
+        auto v2 = qwen38::verify_mtp_target_layer_major_reference(model, 5, std::vector<std::uint32_t>{7, 8}, state);
+        CHECK(v2.generation > v.generation);
+        CHECK(throws<std::runtime_error>([&] { qwen38::commit_mtp_target_verification(std::move(v), 1, state); }));
+        CHECK(v.rows.size() == 4 && state.token_count() == 100);
+        qwen38::commit_mtp_target_verification(std::move(v2), 1, state);
+        CHECK(v2.rows.empty() && state.token_count() == 102);
+        CHECK(throws<std::runtime_error>([&] { qwen38::commit_mtp_target_verification(std::move(v), 1, state); }));
+        CHECK(state.token_count() == 102);
+    }
+    auto v3 = qwen38::verify_mtp_target_layer_major_reference(model, 5, drafts, state);
+    qwen38::commit_mtp_target_verification(std::move(v3), 2, state);
+    CHECK(v3.rows.empty() && state.token_count() == 105);
 
     // a full external-draft round with the target's own greedy continuation as drafts
     const std::uint32_t cur = 11;

@@ -14,6 +14,22 @@ def f16(v):
     return np.asarray(v, np.float32).astype(np.float16).view(np.uint16)
 
 
+def pack_q4(w):
+    """[V, H] ints in [-8, 7] -> [V, H/2] bytes: input 2i in the low nibble, 2i + 1 in the
+    high nibble (the Q4/g64 head's tensor contract)."""
+    u = (np.asarray(w, np.int64) & 0xF).astype(np.uint8)
+    return (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8)
+
+
+def bf16_ulps(orc, got, want):
+    """Per-element distance in bf16 units in the last place (bit patterns of finite values,
+    ordered across zero)."""
+    def key(u):
+        u = np.asarray(u, np.uint16).astype(np.int32)
+        return np.where(u & 0x8000, -(u & 0x7FFF), u)
+    return np.abs(key(got) - key(want))
+
+
 class ExplicitLayer:
     """A layer whose tensors are numpy arrays uploaded to the device (q38_moe_layer_create)."""
 

@@ -74,6 +74,7 @@ class Oracle:
         sig("orc_head_q8_logits", None, P, P, I64, C.c_int, P, C.c_int, P, C.c_int)
         sig("orc_argmax", None, P, C.c_int, I64, P, P)
         sig("orc_head_q4_synth_logits", None, U64, C.c_int, I64, I64, P, C.c_int, P, C.c_int)
+        sig("orc_head_q4_logits", None, P, P, I64, C.c_int, P, C.c_int, P, C.c_int)
         sig("orc_decide_greedy", C.c_int, P, I64, P, I64, P, I64, P, P, P)
         sig("orc_plan_commit", C.c_int, U64, U64, U64, P)
         sig("orc_philox4x32_10", None, P, P, P)
@@ -241,6 +242,17 @@ class Oracle:
         h = np.ascontiguousarray(h, np.uint16)
         out = np.empty((h.shape[0], nv), np.float32)
         self.lib.orc_head_q4_synth_logits(seed, H, v0, nv, _a(h), h.shape[0], _a(out), threads)
+        return out
+
+    def head_q4_logits(self, Wp, s, h, threads=8):
+        """Explicit Q4 head: Wp [V, H/2] uint8 (input 2i low nibble, 2i+1 high nibble, signed),
+        s [V, H/64] fp16 bits."""
+        Wp = np.ascontiguousarray(Wp, np.uint8)
+        s = np.ascontiguousarray(s, np.uint16)
+        h = np.ascontiguousarray(h, np.uint16)
+        V, H = Wp.shape[0], 2 * Wp.shape[1]
+        out = np.empty((h.shape[0], V), np.float32)
+        self.lib.orc_head_q4_logits(_a(Wp), _a(s), V, H, _a(h), h.shape[0], _a(out), threads)
         return out
 
     def argmax(self, logits):

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import gpu_util as G
-from moe_cases import SEED, f16
+from moe_cases import SEED, f16, pack_q4
 
 pytestmark = pytest.mark.gpu
 
@@ -121,6 +121,73 @@ def test_q4_draft_head(gpu, q38, orc):
         assert err.max() <= 1e-4 * np.abs(want).max() + 1e-5
     finally:
         hd.close()
+
+
+def test_q4_explicit_head_closed_forms(gpu, q38, orc):
+    """An explicit Q4/g64 head (caller-owned nibbles and scales) against the oracle's
+    explicit-weight path and closed forms: +1/-1 in the low/high nibbles, all -8, one group
+    of 7s, one weight at an odd input, random rows (V = 70 leaves a ragged last pass)."""
+    H, V = 2048, 70
+    rng = np.random.default_rng(41)
+    w = rng.integers(-8, 8, (V, H))
+    s = rng.uniform(1.6e-3, 1.6e-2, (V, H // 64)).astype(np.float32)
+    w[0] = 0
+    w[0, 0::2], w[0, 1::2], s[0] = 1, -1, 1.0
+    w[1], s[1] = -8, 2.0 ** -(np.arange(H // 64) % 4)
+    w[2] = 0
+    w[2, 320:384], s[2] = 7, 0.5
+    w[3] = 0
+    w[3, 1001], s[3] = 3, 0.25
+    s16 = f16(s)
+    Wp = pack_q4(w)
+    h = orc.bf16(rng.normal(0, 1, (4, H)))
+    hf = orc.bf16_to_f32(h).astype(np.float64)
+    Wd, sd = G.to_dev(Wp), G.to_dev(s16)
+    hd = q38.Head(gpu, q38.Q38_HEAD_Q4G64, V, H, weights=Wd, scales=sd)
+    try:
+        got = logits(q38, hd, h)
+        want = orc.head_q4_logits(Wp, s16, h)
+        closed = np.stack([hf[:, 0::2].sum(1) - hf[:, 1::2].sum(1),
+                           -8 * (hf.reshape(4, 32, 64).sum(2) * s16.view(np.float16).astype(np.float64)[1]).sum(1),
+                           3.5 * hf[:, 320:384].sum(1), 0.75 * hf[:, 1001]], 1)
+        assert np.allclose(want[:, :4], closed, rtol=1e-6, atol=1e-6)
+        err = np.abs(got - want)
+        assert err.max() <= 1e-4 * np.abs(want).max() + 1e-5, err.max()
+    finally:
+        hd.close()
+
+
+def test_q4_synthetic_tensors_match_generator(gpu, q38, orc):
+    """The device-generated draft head: nibbles (low first) equal orc_gen_int4 and the g64
+    scales equal the T_DRAFT_S stream, bit for bit, on rows across the vocab."""
+    H, V = 2048, 151936
+    hd = q38.Head(gpu, q38.Q38_HEAD_Q4G64, V, H, seed=SEED)
+    try:
+        wp, sp = hd.device_weights()
+        for v in (0, 1, 77777, V - 1):
+            got = G.d2h(wp + v * (H // 2), H // 2, np.uint8)
+            w = np.empty(H, np.int8)
+            orc.lib.orc_gen_int4(orc.key(SEED, 0xFFFD, 32), v * H, H, w.ctypes.data)
+            assert np.array_equal(got, pack_q4(w[None])[0]), v
+        s = G.d2h(sp, V * (H // 64), np.uint16)
+        assert np.array_equal(s, orc.uniform_f16(orc.key(SEED, 0xFFFD, 33), 0, V * (H // 64), 1.6e-3, 1.6e-2))
+    finally:
+        hd.close()
+
+
+@pytest.mark.parametrize("M,H", [(1, 2048), (4, 2048), (16, 2048), (3, 2560)])
+def test_rmsnorm_vs_oracle(gpu, q38, orc, M, H):
+    """q38_rmsnorm (the head's input norm) against the oracle's float64 RMSNorm: within one
+    bf16 ulp per element (the device sums the squares in float), and exact almost always."""
+    from moe_cases import bf16_ulps
+    rng = np.random.default_rng(M + H)
+    h_np = orc.bf16(rng.normal(0, 1, (M, H)) * np.exp(rng.uniform(-4, 4, (M, 1))))
+    h = G.to_dev(h_np)
+    y = G.empty((M, H), np.uint16)
+    q38.check(q38.lib.q38_rmsnorm(h.data_ptr(), M, H, C.c_float(1e-6), y.data_ptr(), G.stream()))
+    got = G.to_host(y, np.uint16)
+    ulps = bf16_ulps(orc, got, orc.rmsnorm(h_np))
+    assert ulps.max() <= 1 and np.mean(ulps == 0) >= 0.99, (ulps.max(), np.mean(ulps == 0))
 
 
 def test_head_rows_beyond_limit_rejected(gpu, q38):

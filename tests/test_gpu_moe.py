@@ -110,6 +110,17 @@ def test_invalid_shapes_rejected(layer0, q38):
     assert rc == q38.Q38_EINVAL
 
 
+def test_mixed_desc_rejected_by_uniform_create(gpu, q38):
+    """q38_moe_layer_create takes uniform-geometry tensors only: a mixed description is an
+    argument error (it would otherwise read per-bank geometry fields it does not have)."""
+    d = q38.desc(mixed=1)
+    d.gu_dim = d.down_dim = 0
+    w = q38.MoeWeights()
+    h = C.c_void_p()
+    assert q38.lib.q38_moe_layer_create(gpu.h, C.byref(d), C.byref(w), C.byref(h)) == q38.Q38_EINVAL
+    assert b"q38_moe_layer_create_mixed" in q38.lib.q38_last_error()
+
+
 @pytest.mark.parametrize("H,I,M", [(2560, 512, 4), (2560, 512, 1), (2560, 640, 4)])
 def test_hidden_2560_layers(gpu, q38, orc, H, I, M):
     """The reference family's hidden size: 2560 x 512 takes the four-row MFMA kernels with

@@ -96,3 +96,98 @@ def test_sampling_output_follows_target(orc):
         counts[d if a == 1 else nxt] += 1
     chi = stats.chisquare(counts, p * n)
     assert chi.pvalue > 1e-4, (counts, p * n)
+
+
+# ---------------------------------------------------------------- Q4 draft head (R14)
+# Device tensor contract of the Q4/g64 head: [V, H/2] bytes, input 2i in the low nibble and
+# 2i + 1 in the high nibble, both signed int4; [V, H/64] fp16 scales. The logit is
+# sum_g s[v, g] * sum_{c in g} w[c] h[c]. The checks below are chosen so that a swapped
+# nibble order, a missing sign extension or a transposed scale index fails one of them.
+
+def _pack_q4(w):
+    """[V, H] ints in [-8, 7] -> [V, H/2] bytes, low nibble first."""
+    u = (np.asarray(w, np.int64) & 0xF).astype(np.uint8)
+    return (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8)
+
+
+def _np_q4_logits(orc, w, s16, h):
+    hf = orc.bf16_to_f32(h).astype(np.float64)
+    V, H = w.shape
+    s = s16.view(np.float16).astype(np.float64).reshape(V, H // 64)
+    g = (w.astype(np.float64).reshape(V, H // 64, 64)[None] * hf.reshape(-1, 1, H // 64, 64)).sum(-1)
+    return (g * s[None]).sum(-1)
+
+
+def _close_f32(got, want64):
+    want = want64.astype(np.float32)
+    return np.all(np.abs(got.astype(np.float64) - want) <= np.spacing(np.abs(want)).astype(np.float64))
+
+
+def test_q4_explicit_closed_forms(orc):
+    H, V = 2048, 6
+    rng = np.random.default_rng(40)
+    h = orc.bf16(rng.normal(0, 1, (2, H)))
+    hf = orc.bf16_to_f32(h).astype(np.float64)
+    w = np.zeros((V, H), np.int64)
+    s = np.ones((V, H // 64), np.float32)
+    w[0, 0::2], w[0, 1::2] = 1, -1                       # +1 low nibble, -1 high nibble
+    w[1, :] = -8                                          # the most negative nibble
+    s[1] = 2.0 ** -(np.arange(H // 64) % 4)               # a different scale per group
+    w[2, 5 * 64:6 * 64] = 7                               # one group only
+    s[2] = 0.5
+    w[4, 1001] = 3                                        # one weight, odd input (high nibble)
+    s[4] = 0.25
+    w[5] = rng.integers(-8, 8, H)
+    s[5] = rng.uniform(1.6e-3, 1.6e-2, H // 64)
+    s16 = s.astype(np.float16).view(np.uint16)
+    got = orc.head_q4_logits(_pack_q4(w), s16, h)
+    sf = s16.view(np.float16).astype(np.float64)
+    closed = np.stack([
+        hf[:, 0::2].sum(1) - hf[:, 1::2].sum(1),
+        -8 * (hf.reshape(2, H // 64, 64).sum(2) * sf[1]).sum(1),
+        3.5 * hf[:, 5 * 64:6 * 64].sum(1),
+        np.zeros(2),
+        0.75 * hf[:, 1001],
+    ], 1)
+    assert _close_f32(got[:, :5], closed)
+    assert _close_f32(got, _np_q4_logits(orc, w, s16, h))
+
+
+def _mix64(z):
+    z = np.asarray(z, np.uint64)
+    with np.errstate(over="ignore"):
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def _np_stream_key(seed, layer, tensor):
+    g = np.uint64(0x9E3779B97F4A7C15)
+    with np.errstate(over="ignore"):
+        k = _mix64(_mix64(np.uint64(seed)) + g * np.uint64(layer + 1))
+        return _mix64(k + g * np.uint64(tensor + 1))
+
+
+def test_q4_synthetic_vs_numpy(orc):
+    """The synthetic draft head (generator streams T_DRAFT_W / T_DRAFT_S of layer 0xFFFD)
+    regenerated in numpy (an independent splitmix64: w = (bits >> 60) - 8, scale = f16 of
+    1.6e-3 + u * (1.6e-2 - 1.6e-3)), logits recomputed in float64; and the same weights
+    packed as nibbles give the same logits through the explicit-weight path."""
+    seed, H, v0, nv = 0x51A5EED, 2048, 151936 - 300, 300
+    h = orc.rmsnorm(orc.embed(seed, [5, 6, 7], H))
+    got = orc.head_q4_synth_logits(seed, H, h, v0=v0, nv=nv)
+    gk = np.uint64(0x9E3779B97F4A7C15)
+    wk, sk = _np_stream_key(seed, 0xFFFD, 32), _np_stream_key(seed, 0xFFFD, 33)
+    with np.errstate(over="ignore"):
+        idx = np.arange(v0 * H, (v0 + nv) * H, dtype=np.uint64)
+        w = ((_mix64(wk + gk * (idx + np.uint64(1))) >> np.uint64(60)).astype(np.int64) - 8).reshape(nv, H)
+        gi = np.arange(v0 * (H // 64), (v0 + nv) * (H // 64), dtype=np.uint64)
+        u = (_mix64(sk + gk * (gi + np.uint64(1))) >> np.uint64(11)).astype(np.float64) * 2.0 ** -53
+    s16 = (1.6e-3 + u * (1.6e-2 - 1.6e-3)).astype(np.float32).astype(np.float16).view(np.uint16)
+    ref = np.empty(nv * H, np.int8)
+    orc.lib.orc_gen_int4(orc.key(seed, 0xFFFD, 32), v0 * H, nv * H, ref.ctypes.data)
+    assert np.array_equal(ref.reshape(nv, H), w)
+    assert np.array_equal(s16, orc.uniform_f16(orc.key(seed, 0xFFFD, 33), v0 * (H // 64), nv * (H // 64),
+                                                1.6e-3, 1.6e-2))
+    assert _close_f32(got, _np_q4_logits(orc, w, s16, h))
+    assert np.array_equal(orc.head_q4_logits(_pack_q4(w), s16, h), got)
