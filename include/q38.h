@@ -161,6 +161,17 @@ int q38_moe_route(q38_moe_layer* layer, const uint16_t* x, int32_t rows, const q
 int q38_moe_forward(q38_moe_layer* layer, const uint16_t* x, int32_t rows, uint16_t* y,
                     const q38_route_out* routes, void* workspace, size_t workspace_bytes, void* stream);
 
+/* q38_moe_forward for verify widths (rows 1..16) without a workspace argument and without
+ * any allocation: no counterpart in the reference. It is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Scratch is one fixed 8 MiB device array per GPU, held until the process ends; its address
+ * is looked up by q38_ctx_create. Calls needing more (a layer's workspace for `rows`, see
+ * q38_moe_workspace_size) return Q38_ESPACE. Every call on a GPU shares that GPU's array and
+ * leaves its contents behind: calls that overlap on one GPU (two streams, two threads) race.
+ * x, y: device [rows, H] bf16 (may not alias); routes optional as for q38_moe_forward. */
+int q38_moe_forward_static(q38_moe_layer* layer, const uint16_t* x, int32_t rows, uint16_t* y,
+                           const q38_route_out* routes, void* stream);
+
 /* SparseMoe::forward_prefill_profiled (include/qwen38/sparse_moe.hpp:69-71) for rows
  * 17..2048: the same call as q38_moe_forward, synchronised, with the execution time of each
  * kernel in milliseconds: kernel_ms[7] = router logits, top-k, route plan, gate/up,

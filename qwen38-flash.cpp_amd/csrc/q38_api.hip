@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -33,6 +34,34 @@ int hip_fail(hipError_t e, const char* where) {
     } while (0)
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+// Scratch of the allocation-free forward (q38_moe_forward_static): one fixed array per GPU,
+// allocated with the code object and held until the process ends. Host code never passes
+// the array's name to a kernel: it passes the device address that hipGetSymbolAddress
+// returns for the current device, kept per device in g_scratch.
+constexpr size_t kScratchBytes = size_t{8} << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices] = {};
+
+// With `dev` current: look the array's address up once for this device.
+int scratch_init(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) {
+        g_error = "q38: device index beyond the scratch table";
+        return Q38_EINVAL;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mutex);
+    if (g_scratch[dev]) return Q38_OK;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+        g_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+        return Q38_EHIP;
+    }
+    g_scratch[dev] = ptr;
+    return Q38_OK;
+}
 
 int64_t words_for(int64_t n, int bits) { return ((n + 31) / 32) * bits; }
 
@@ -82,6 +111,7 @@ int q38_ctx_create(int hip_device, q38_ctx** out) {
     Q38_HIP(hipGetDeviceCount(&n));
     if (hip_device < 0 || hip_device >= n) return fail(Q38_EINVAL, "q38_ctx_create: no such HIP device");
     Q38_HIP(hipSetDevice(hip_device));
+    if (int rc = scratch_init(hip_device)) return rc;
     *out = new q38_ctx{hip_device};
     return Q38_OK;
 }
@@ -681,6 +711,28 @@ int q38_moe_forward(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t*
     MoeBufs w{};
     if (!ws || ws_bytes < moe_ws(L->desc, rows, &w, ws)) return fail(Q38_ESPACE, "workspace too small");
     if (rows > kMaxRows) return run_prefill(L, w, rows, x, y, routes, nullptr, static_cast<hipStream_t>(stream));
+    return run_layer(L, w, rows, x, false, 0.0f, nullptr, y, routes, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int q38_moe_forward_static(q38_moe_layer* L, const uint16_t* x, int32_t rows, uint16_t* y, const q38_route_out* routes,
+                           void* stream) {
+    if (!L || !x || !y) return fail(Q38_EINVAL, "q38_moe_forward_static: null argument");
+    if (x == y) return fail(Q38_EINVAL, "q38_moe_forward_static: input and output must not alias");
+    if (int rc = check_rows(rows)) return rc;
+    const size_t need = moe_ws(L->desc, rows, nullptr, nullptr);
+    if (need > kScratchBytes)
+        return fail(Q38_ESPACE, "q38_moe_forward_static: the layer needs " + std::to_string(need) +
+                                    " bytes of scratch for this many rows; the fixed scratch holds " +
+                                    std::to_string(kScratchBytes));
+    void* base = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mutex);
+        const int dev = L->ctx->device;
+        base = dev >= 0 && dev < kMaxDevices ? g_scratch[dev] : nullptr;
+    }
+    if (!base) return fail(Q38_ESTATE, "q38_moe_forward_static: no scratch on the layer's device");
+    MoeBufs w{};
+    moe_ws(L->desc, rows, &w, base);
     return run_layer(L, w, rows, x, false, 0.0f, nullptr, y, routes, nullptr, static_cast<hipStream_t>(stream));
 }
 

@@ -78,6 +78,7 @@ _sig("q38_moe_layer_bytes", I64, P, I32, I32)
 _sig("q38_moe_workspace_size", SZ, C.POINTER(MoeDesc), I32)
 _sig("q38_moe_route", C.c_int, P, P, I32, C.POINTER(RouteOut), P, SZ, P)
 _sig("q38_moe_forward", C.c_int, P, P, I32, P, C.POINTER(RouteOut), P, SZ, P)
+_sig("q38_moe_forward_static", C.c_int, P, P, I32, P, C.POINTER(RouteOut), P)
 _sig("q38_moe_forward_prefill_profiled", C.c_int, P, P, I32, P, C.POINTER(RouteOut), P, SZ, C.POINTER(F32), P)
 _sig("q38_moe_layer_set_router_bias", C.c_int, P, P)
 _sig("q38_verify_chain", C.c_int, C.POINTER(P), I32, P, I32, F32, C.POINTER(RouteOut), P, SZ, P)
