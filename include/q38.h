@@ -41,8 +41,13 @@ typedef struct q38_moe_layer q38_moe_layer;
 typedef struct q38_head q38_head;
 typedef struct q38_slot q38_slot;
 
-/* Codebook storage formats. */
-enum { Q38_CB_FP16 = 0, Q38_CB_INT8_SCALED = 1 };
+/* Codebook formats. Q38_CB_FP16: the FP16 books as given. Q38_CB_INT8_SCALED: the mixed
+ * layout's INT8 d8 books with one FP16 scale per book. Q38_CB_U8_PERDIM: the reference's
+ * verify-width books (SparseMoe::prepare_u8_codebook, src/sparse_moe.cpp:528-544, 750-804),
+ * derived at layer creation from the FP16 books of the d8/14-bit projections: per-dimension
+ * min/max, scale = (max - min) / 255, a centred INT8 gate book and affine U8 up/down books
+ * with FP16 scale and bias per dimension, decoded as q * scale (+ bias). */
+enum { Q38_CB_FP16 = 0, Q38_CB_INT8_SCALED = 1, Q38_CB_U8_PERDIM = 2 };
 
 /* Layer description. Mirrors the SparseMoe constructor arguments
  * (include/qwen38/sparse_moe.hpp:48-55) plus the VQ geometry of the projection tensors
@@ -59,7 +64,7 @@ typedef struct q38_moe_desc {
     int32_t has_shared;          /* shared expert (expert index E) + sigmoid gate     */
     int32_t mixed;               /* 1: even experts d4/8-bit FP16 books, odd experts
                                     d8/14-bit INT8 books with one FP16 scale each     */
-    int32_t reserved;
+    int32_t book_format;         /* uniform layers: Q38_CB_FP16 or Q38_CB_U8_PERDIM   */
 } q38_moe_desc;
 
 /* Device tensors of one layer (uniform geometry). The layer adopts the pointers; the
@@ -139,8 +144,17 @@ int q38_moe_layer_create_mixed(q38_ctx* ctx, const q38_moe_desc* desc, const q38
 int q38_moe_layer_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, uint64_t seed,
                                    int32_t layer_index, q38_moe_layer** out);
 void q38_moe_layer_destroy(q38_moe_layer* layer);
-/* Device pointers of a layer's tensors (uniform geometry) for inspection. */
+/* Device pointers of a layer's tensors (uniform geometry, as given at creation) for
+ * inspection. */
 int q38_moe_layer_weights(const q38_moe_layer* layer, q38_moe_weights* out);
+/* The codebook the kernels read for projection p (0 gate, 1 up, 2 down): device [2^BITS, D]
+ * fp16. With Q38_CB_U8_PERDIM and a d8/14-bit projection it is the decoded per-dimension
+ * book (q * scale (+ bias) rounded to fp16, the MFMA operand type), and q (int8 centred for
+ * the gate, uint8 affine otherwise, [2^BITS, D]), scales [D] and biases [D] (fp16) are the
+ * derived tables (the reference's codebook_u8, codebook_u8_scales and codebook_u8_biases);
+ * otherwise the FP16 book as given and null tables. Outputs may be null. */
+int q38_moe_layer_codebook(const q38_moe_layer* layer, int proj, const uint16_t** book, const void** q,
+                           const uint16_t** scales, const uint16_t** biases);
 /* Algorithmic HBM bytes of one forward that touches n_unique routed experts. */
 int64_t q38_moe_layer_bytes(const q38_moe_layer* layer, int32_t n_unique, int32_t rows);
 /* Workspace bytes needed by q38_moe_forward / q38_verify_chain for up to max_rows rows

@@ -25,6 +25,12 @@
 //   rejection sampling     invariants (p == q accepts all; p(d) = 0 rejects) and a
 //                          chi-square test that the emitted token follows p.
 //   exp contract           error bound vs math.exp over the whole reduced range.
+//   per-dim INT8/U8 books  independent numpy restatement (bit-exact tables and decode),
+//                          closed forms (min/max round trip, lround ties away from zero,
+//                          clamps, constant dimension), float64 numpy layer recomputation.
+//   Q4 draft head          closed forms (nibble order, sign, group scales), numpy splitmix64
+//                          regeneration + float64 logits.
+//   RMSNorm                bit-exact float64 numpy restatement, closed forms, invariants.
 
 #include <algorithm>
 #include <atomic>
@@ -32,6 +38,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <limits>
 #include <numeric>
 #include <thread>
 #include <vector>
@@ -277,7 +284,7 @@ struct Desc {  // field order is part of the ctypes contract (tests/oracle.py)
     int32_t gu_group, down_group;   // scale group along IN; == IN means one scale per row
     int32_t normalize, has_shared;
     int32_t mixed;                  // 1: even experts d4/8-bit FP16, odd d8/14-bit INT8 codebook
-    int32_t pad;
+    int32_t book_format;            // 0: FP16 books; 2: per-dimension INT8/U8 books (d8/14 projections)
 };
 
 struct Proj {  // one projection of one expert, host pointers
@@ -470,6 +477,55 @@ void synth_book(uint64_t key, int K, int D, bool int8, std::vector<float>& vals,
     }
 }
 
+// SparseMoe::prepare_u8_codebook (src/sparse_moe.cpp:750-804): per-dimension min/max of the
+// FP16 book (as float), scale = (max - min) / 255 (1 when not > 0); centred (the gate book):
+// q = clamp(lround(v / scale), -128, 127); affine (up, down): q = clamp(lround((v - min) /
+// scale), 0, 255); scales and biases (= min) stored as FP16. The kernels decode in float
+// (src/vq_metal_kernels.hpp:564-579): w = q * f16(scale) (+ f16(min) when affine).
+void prepare_u8_book(const uint16_t* book16, int K, int D, bool centered, std::vector<int32_t>& q,
+                     std::vector<uint16_t>& s16, std::vector<uint16_t>& b16, std::vector<float>& vals) {
+    std::vector<float> mn(D, std::numeric_limits<float>::infinity()), mx(D, -std::numeric_limits<float>::infinity());
+    for (int r = 0; r < K; ++r)
+        for (int d = 0; d < D; ++d) {
+            const float v = f16_to_f32(book16[static_cast<size_t>(r) * D + d]);
+            mn[d] = std::min(mn[d], v);
+            mx[d] = std::max(mx[d], v);
+        }
+    std::vector<float> sc(D);
+    s16.resize(D);
+    b16.resize(D);
+    for (int d = 0; d < D; ++d) {
+        sc[d] = (mx[d] - mn[d]) / 255.0F;
+        if (!(sc[d] > 0.0F)) sc[d] = 1.0F;
+        s16[d] = f32_to_f16(sc[d]);
+        b16[d] = f32_to_f16(mn[d]);
+    }
+    const size_t n = static_cast<size_t>(K) * D;
+    q.resize(n);
+    vals.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+        const int d = static_cast<int>(i % D);
+        const float v = f16_to_f32(book16[i]);
+        const long r = centered ? std::lround(v / sc[d]) : std::lround((v - mn[d]) / sc[d]);
+        q[i] = static_cast<int32_t>(centered ? std::clamp<long>(r, -128, 127) : std::clamp<long>(r, 0, 255));
+        vals[i] = static_cast<float>(q[i]) * f16_to_f32(s16[d]);
+        if (!centered) vals[i] = vals[i] + f16_to_f32(b16[d]);
+    }
+}
+// The book the kernels read for projection p: the FP16 values, or with book_format 2 and a
+// d8/14-bit projection the decoded per-dimension INT8 (gate) / U8 (up, down) book
+// (src/sparse_moe.cpp:528-544).
+void layer_book(const Desc& d, int p, const uint16_t* book16, int K, int D, int bits, std::vector<float>& vals) {
+    if (d.book_format == 2 && D == 8 && bits == 14) {
+        std::vector<int32_t> q;
+        std::vector<uint16_t> s16, b16;
+        prepare_u8_book(book16, K, D, p == 0, q, s16, b16, vals);
+        return;
+    }
+    vals.resize(static_cast<size_t>(K) * D);
+    for (size_t i = 0; i < vals.size(); ++i) vals[i] = f16_to_f32(book16[i]);
+}
+
 struct SynthSource final : LayerSource {
     Desc d;
     uint64_t seed, layer;
@@ -489,8 +545,13 @@ struct SynthSource final : LayerSource {
         } else {
             const int dims[3] = {d.gu_dim, d.gu_dim, d.down_dim};
             const int bits[3] = {d.gu_bits, d.gu_bits, d.down_bits};
-            for (int p = 0; p < 3; ++p)
-                synth_book(stream_key(seed, layer, cbt[p]), 1 << bits[p], dims[p], false, book8[p], nullptr, nullptr, nullptr);
+            for (int p = 0; p < 3; ++p) {
+                std::vector<uint16_t> raw;
+                std::vector<float> fp16_vals;
+                synth_book(stream_key(seed, layer, cbt[p]), 1 << bits[p], dims[p], false, fp16_vals, &raw, nullptr,
+                           nullptr);
+                layer_book(d, p, raw.data(), 1 << bits[p], dims[p], bits[p], book8[p]);
+            }
         }
     }
     const uint16_t* router() override {
@@ -578,9 +639,7 @@ struct DenseSource final : LayerSource {
         for (int p = 0; p < 3; ++p) {
             codes[p] = c[p];
             scales[p] = s[p];
-            const int n = (1 << bits[p]) * dims[p];
-            book[p].resize(n);
-            for (int i = 0; i < n; ++i) book[p][i] = f16_to_f32(b[p][i]);
+            layer_book(d, p, b[p], 1 << bits[p], dims[p], bits[p], book[p]);
         }
     }
     const uint16_t* router() override { return wr; }
@@ -747,6 +806,19 @@ void orc_gen_book(uint64_t key, int K, int D, int int8, uint16_t* f16_out, int8_
     synth_book(key, K, D, int8 != 0, vals, &raw, &raw8, scale_out);
     if (!int8 && f16_out) std::copy(raw.begin(), raw.end(), f16_out);
     if (int8 && i8_out) std::copy(raw8.begin(), raw8.end(), i8_out);
+}
+// Per-dimension INT8/U8 codebook of an FP16 book: q [K*D] int32, scales/biases [D] fp16,
+// decoded values [K*D] float.
+void orc_prepare_u8_book(const uint16_t* book16, int K, int D, int centered, int32_t* q, uint16_t* s16, uint16_t* b16,
+                         float* vals) {
+    std::vector<int32_t> qv;
+    std::vector<uint16_t> sv, bv;
+    std::vector<float> fv;
+    prepare_u8_book(book16, K, D, centered != 0, qv, sv, bv, fv);
+    std::copy(qv.begin(), qv.end(), q);
+    std::copy(sv.begin(), sv.end(), s16);
+    std::copy(bv.begin(), bv.end(), b16);
+    std::copy(fv.begin(), fv.end(), vals);
 }
 void orc_gen_embed(uint64_t seed, const uint32_t* tokens, int n, int H, uint16_t* out) {
     const uint64_t key = stream_key(seed, kEmbedLayer, T_EMBED);

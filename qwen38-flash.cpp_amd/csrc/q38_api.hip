@@ -77,7 +77,12 @@ struct q38_moe_layer {
     LayerDev dev;
     void* owned = nullptr;      // synthetic tensors
     size_t owned_bytes = 0;
-    void* prepared = nullptr;   // codebooks split into 4-dim chunks
+    void* prepared = nullptr;   // codebooks split into 4-dim chunks (+ tiled codes, derived books)
+    const uint16_t* books_in[3] = {nullptr, nullptr, nullptr};  // the FP16 books as given
+    // per-dimension INT8/U8 books (Q38_CB_U8_PERDIM) of d8/14-bit projections, else null
+    const void* u8q[3] = {nullptr, nullptr, nullptr};
+    const uint16_t* u8s[3] = {nullptr, nullptr, nullptr};
+    const uint16_t* u8b[3] = {nullptr, nullptr, nullptr};
 };
 
 struct q38_head {
@@ -150,6 +155,8 @@ static int validate_desc(const q38_moe_desc* d) {
         return fail(Q38_EINVAL, "routed expert count must be a multiple of 64 in [64, 1024]");
     if (d->top_k < 1 || d->top_k > kMaxTopK || d->top_k > d->experts)
         return fail(Q38_EINVAL, "experts per token must be in [1, 16]");
+    if (d->book_format != Q38_CB_FP16 && (d->mixed || d->book_format != Q38_CB_U8_PERDIM))
+        return fail(Q38_EINVAL, "codebook format must be Q38_CB_FP16, or Q38_CB_U8_PERDIM for a uniform layer");
     if (d->mixed) {
         if (d->hidden != 2048 || d->inter != 512)
             return fail(Q38_EINVAL, "mixed VQ layers need hidden 2048 and expert intermediate 512");
@@ -176,6 +183,7 @@ static int validate_desc(const q38_moe_desc* d) {
 static void fill_dev(q38_moe_layer* L, const q38_moe_weights* w) {
     const q38_moe_desc& d = L->desc;
     LayerDev& v = L->dev;
+    for (int p = 0; p < 3; ++p) L->books_in[p] = w->books[p];
     v.router = w->router;
     v.wsg = w->shared_gate;
     v.H = d.hidden;
@@ -205,12 +213,20 @@ static void fill_dev(q38_moe_layer* L, const q38_moe_weights* w) {
 // Codebooks split into 4-dim chunks ([dim/4][entries][4]) for the LDS-resident MFMA path,
 // and, for layers the four-row verify kernels serve, the codes in the tiled layout those
 // kernels load from (one more copy of the codes: HBM traded for coalesced loads).
+// With Q38_CB_U8_PERDIM, the d8/14-bit projections first get their per-dimension INT8/U8
+// books (q, scales, biases) and the decoded book, which every kernel then reads in place of
+// the FP16 book (SparseMoe::prepare_u8_codebook runs at load time too, src/sparse_moe.cpp:
+// 528-544): the gate book centred, up and down affine.
 static int prepare_layer(q38_moe_layer* L) {
-    size_t total = 0, off[3], toff[3];
+    size_t total = 0, off[3], toff[3], uoff[3];
     const bool tiled = moe_uses_narrow(L->dev, 1);
+    bool u8[3];
     for (int p = 0; p < 3; ++p) {
         off[p] = total;
         total += align256((static_cast<size_t>(1) << L->dev.p[p].bits) * L->dev.p[p].dim * 2);
+        u8[p] = L->desc.book_format == Q38_CB_U8_PERDIM && L->dev.p[p].dim == 8 && L->dev.p[p].bits == 14;
+        uoff[p] = total;
+        if (u8[p]) total += align256(size_t{16384} * 8) + 256 + align256(size_t{16384} * 8 * 2);
     }
     int64_t rows[3] = {0, 0, 0};
     for (int p = 0; p < 3 && tiled; ++p) {
@@ -221,6 +237,17 @@ static int prepare_layer(q38_moe_layer* L) {
     char* base = nullptr;
     if (hipMalloc(&base, total) != hipSuccess) return fail(Q38_ENOMEM, "hipMalloc failed for prepared codebooks");
     hipError_t e = hipSuccess;
+    for (int p = 0; p < 3 && e == hipSuccess; ++p) {
+        if (!u8[p]) continue;
+        auto* q = reinterpret_cast<uint8_t*>(base + uoff[p]);
+        auto* sb = reinterpret_cast<uint16_t*>(base + uoff[p] + align256(size_t{16384} * 8));
+        auto* dec = reinterpret_cast<uint16_t*>(base + uoff[p] + align256(size_t{16384} * 8) + 256);
+        e = launch_prepare_u8(L->dev.p[p].book, 16384, p == 0 ? 1 : 0, q, sb, sb + 8, dec, nullptr);
+        L->u8q[p] = q;
+        L->u8s[p] = sb;
+        L->u8b[p] = sb + 8;
+        L->dev.p[p].book = dec;
+    }
     for (int p = 0; p < 3 && e == hipSuccess; ++p) {
         auto* dst = reinterpret_cast<uint16_t*>(base + off[p]);
         e = launch_split_book(L->dev.p[p].book, 1 << L->dev.p[p].bits, L->dev.p[p].dim, dst, nullptr);
@@ -536,8 +563,19 @@ int q38_moe_layer_weights(const q38_moe_layer* L, q38_moe_weights* out) {
     for (int p = 0; p < 3; ++p) {
         out->codes[p] = L->dev.p[p].codes;
         out->scales[p] = L->dev.p[p].scales;
-        out->books[p] = L->dev.p[p].book;
+        out->books[p] = L->books_in[p];
     }
+    return Q38_OK;
+}
+
+int q38_moe_layer_codebook(const q38_moe_layer* L, int proj, const uint16_t** book, const void** q,
+                           const uint16_t** scales, const uint16_t** biases) {
+    if (!L || proj < 0 || proj > 2) return fail(Q38_EINVAL, "q38_moe_layer_codebook: bad arguments");
+    if (L->dev.mixed) return fail(Q38_EINVAL, "a mixed layer has per-bank codebooks");
+    if (book) *book = L->dev.p[proj].book;
+    if (q) *q = L->u8q[proj];
+    if (scales) *scales = L->u8s[proj];
+    if (biases) *biases = L->u8b[proj];
     return Q38_OK;
 }
 

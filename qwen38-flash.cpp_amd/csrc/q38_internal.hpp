@@ -163,6 +163,10 @@ hipError_t launch_gen_embed(uint64_t seed, const uint32_t* tokens, int n, int H,
 hipError_t launch_gen_embed_dev(uint64_t seed, const uint32_t* tokens_dev, int n, int H, uint16_t* out,
                                 hipStream_t st);
 hipError_t launch_book_to_int8(const uint16_t* book16, int n, int8_t* q8, uint16_t* scale, hipStream_t st);
+// Per-dimension INT8 (centred) / U8 (affine) codebook of a [K, 8] fp16 book: q [K*8], scales
+// and biases [8] fp16, and the decoded book [K*8] fp16.
+hipError_t launch_prepare_u8(const uint16_t* book16, int K, int centered, uint8_t* q, uint16_t* s16, uint16_t* b16,
+                             uint16_t* dec, hipStream_t st);
 hipError_t launch_gen_head(const HeadDev& hd, uint64_t seed, int8_t* w, uint16_t* scales, hipStream_t st);
 hipError_t launch_scale_absmax(const uint16_t* scales, int64_t n, float* out, hipStream_t st);
 

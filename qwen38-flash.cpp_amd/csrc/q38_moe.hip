@@ -128,6 +128,74 @@ __global__ void k_book_to_int8(const uint16_t* __restrict__ book16, int n, int8_
     }
 }
 
+// SparseMoe::prepare_u8_codebook (src/sparse_moe.cpp:750-804) of a [K, 8] fp16 book in one
+// workgroup: per-dimension min/max (order-free), scale = (max - min) / 255 (1 when not > 0),
+// centred q = clamp(lround(v / scale), -128, 127) or affine q = clamp(lround((v - min) /
+// scale), 0, 255), fp16 scale and bias (= min). The book the kernels read is the float decode
+// q * f16(scale) (+ f16(min)) (src/vq_metal_kernels.hpp:564-579) rounded to fp16.
+__global__ __launch_bounds__(1024) void k_prepare_u8(const uint16_t* __restrict__ book16, int K, int centered,
+                                                      uint8_t* __restrict__ q, uint16_t* __restrict__ s16,
+                                                      uint16_t* __restrict__ b16, uint16_t* __restrict__ dec) {
+    constexpr int D = 8;
+    __shared__ float red[2][16][D];
+    __shared__ float sc[D], mn[D];
+    float lo[D], hi[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        lo[d] = INFINITY;
+        hi[d] = -INFINITY;
+    }
+    for (int r = threadIdx.x; r < K; r += blockDim.x) {
+        const uint4 v = reinterpret_cast<const uint4*>(book16)[r];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const float x = h2f(static_cast<uint16_t>(w[d / 2] >> (16 * (d & 1))));
+            lo[d] = fminf(lo[d], x);
+            hi[d] = fmaxf(hi[d], x);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        for (int off = 32; off >= 1; off >>= 1) {
+            lo[d] = fminf(lo[d], __shfl_xor(lo[d], off, kWave));
+            hi[d] = fmaxf(hi[d], __shfl_xor(hi[d], off, kWave));
+        }
+        if ((threadIdx.x & 63) == 0) {
+            red[0][threadIdx.x >> 6][d] = lo[d];
+            red[1][threadIdx.x >> 6][d] = hi[d];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < D) {
+        const int d = threadIdx.x;
+        float a = INFINITY, b = -INFINITY;
+        for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) {
+            a = fminf(a, red[0][w][d]);
+            b = fmaxf(b, red[1][w][d]);
+        }
+        float s = (b - a) / 255.0f;
+        if (!(s > 0.0f)) s = 1.0f;
+        sc[d] = s;
+        mn[d] = a;
+        s16[d] = f2h(s);
+        b16[d] = f2h(a);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < K * D; i += blockDim.x) {
+        const int d = i % D;
+        const float v = h2f(book16[i]);
+        const float t = centered ? v / sc[d] : (v - mn[d]) / sc[d];
+        const float r = roundf(t);  // (half away from zero, as lround)
+        const float qf = centered ? fminf(127.0f, fmaxf(-128.0f, r)) : fminf(255.0f, fmaxf(0.0f, r));
+        const int qi = static_cast<int>(qf);
+        q[i] = static_cast<uint8_t>(qi);
+        float wv = static_cast<float>(qi) * h2f(f2h(sc[d]));
+        if (!centered) wv = wv + h2f(f2h(mn[d]));
+        dec[i] = f2h(wv);
+    }
+}
+
 // ============================================================== router (R1) + layer-input RMSNorm
 // One workgroup of H/4 threads per NW = H/256 router rows (wave w: row blockIdx.x * NW + w;
 // row E is w_sg). The router rows are requested first: they do not depend on the previous
@@ -1134,6 +1202,10 @@ hipError_t launch_gen_embed_dev(uint64_t seed, const uint32_t* tokens, int n, in
     hipLaunchKernelGGL(k_gen_embed_dev, dim3((n * H + 255) / 256), dim3(256), 0, st,
                        stream_key(seed, kEmbedLayer, T_EMBED), tokens, n, H, out);
     return hipGetLastError();
+}
+hipError_t launch_prepare_u8(const uint16_t* book16, int K, int centered, uint8_t* q, uint16_t* s16, uint16_t* b16,
+                             uint16_t* dec, hipStream_t st) {
+    return launch(k_prepare_u8, dim3(1), dim3(1024), 0, st, book16, K, centered, q, s16, b16, dec);
 }
 hipError_t launch_book_to_int8(const uint16_t* book16, int n, int8_t* q8, uint16_t* scale, hipStream_t st) {
     hipLaunchKernelGGL(k_book_to_int8, dim3(1), dim3(1024), 0, st, book16, n, q8, scale);

@@ -22,6 +22,7 @@ lib = C.CDLL(LIB_PATH)
 
 Q38_OK, Q38_EINVAL, Q38_ERANGE, Q38_EHIP, Q38_ENOMEM, Q38_ESTATE, Q38_ESPACE = 0, -1, -2, -3, -4, -5, -6
 Q38_HEAD_Q8, Q38_HEAD_Q4G64 = 0, 1
+Q38_CB_FP16, Q38_CB_INT8_SCALED, Q38_CB_U8_PERDIM = 0, 1, 2
 
 
 class Q38Error(RuntimeError):
@@ -33,7 +34,7 @@ class Q38Error(RuntimeError):
 class MoeDesc(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "hidden", "inter", "experts", "top_k", "gu_dim", "gu_bits", "down_dim", "down_bits",
-        "gu_group", "down_group", "normalize_topk", "has_shared", "mixed", "reserved")]
+        "gu_group", "down_group", "normalize_topk", "has_shared", "mixed", "book_format")]
 
 
 class MoeWeights(C.Structure):
@@ -74,6 +75,7 @@ _sig("q38_moe_layer_create", C.c_int, P, C.POINTER(MoeDesc), C.POINTER(MoeWeight
 _sig("q38_moe_layer_create_synthetic", C.c_int, P, C.POINTER(MoeDesc), U64, I32, C.POINTER(P))
 _sig("q38_moe_layer_destroy", None, P)
 _sig("q38_moe_layer_weights", C.c_int, P, C.POINTER(MoeWeights))
+_sig("q38_moe_layer_codebook", C.c_int, P, C.c_int, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P))
 _sig("q38_moe_layer_bytes", I64, P, I32, I32)
 _sig("q38_moe_workspace_size", SZ, C.POINTER(MoeDesc), I32)
 _sig("q38_moe_route", C.c_int, P, P, I32, C.POINTER(RouteOut), P, SZ, P)
@@ -121,10 +123,10 @@ def last_error() -> str:
 
 
 def desc(hidden=2048, inter=512, experts=512, top_k=10, gu=(8, 14), down=(8, 14), gu_group=None,
-         down_group=None, normalize=1, shared=1, mixed=0) -> MoeDesc:
+         down_group=None, normalize=1, shared=1, mixed=0, book_format=0) -> MoeDesc:
     """Layer description; groups default to one scale per output row."""
     return MoeDesc(hidden, inter, experts, top_k, gu[0], gu[1], down[0], down[1],
-                   gu_group or hidden, down_group or inter, normalize, shared, mixed, 0)
+                   gu_group or hidden, down_group or inter, normalize, shared, mixed, book_format)
 
 
 def words_per_row(n_in: int, dim: int, bits: int) -> int:
@@ -163,6 +165,12 @@ class MoeLayer:
         w = MoeWeights()
         check(lib.q38_moe_layer_weights(self.h, C.byref(w)))
         return w
+
+    def codebook(self, proj: int):
+        """Device pointers (book, q, scales, biases) of the codebook the kernels read."""
+        ptrs = [P() for _ in range(4)]
+        check(lib.q38_moe_layer_codebook(self.h, proj, *[C.byref(x) for x in ptrs]))
+        return [x.value for x in ptrs]
 
     def bytes(self, n_unique: int, rows: int) -> int:
         return lib.q38_moe_layer_bytes(self.h, n_unique, rows)

@@ -34,14 +34,14 @@ class ExplicitLayer:
     """A layer whose tensors are numpy arrays uploaded to the device (q38_moe_layer_create)."""
 
     def __init__(self, q38, ctx, orc, H=512, I=128, E=64, k=4, gu=(8, 14), down=(8, 14), gu_group=None,
-                 down_group=None, seed=0, router=None):
+                 down_group=None, seed=0, router=None, book_format=0):
         rng = np.random.default_rng(seed)
         self.H, self.I, self.E, self.k = H, I, E, k
         self.qdesc = q38.desc(hidden=H, inter=I, experts=E, top_k=k, gu=gu, down=down, gu_group=gu_group,
-                              down_group=down_group)
+                              down_group=down_group, book_format=book_format)
         import oracle_lib
         self.odesc = oracle_lib.make_desc(hidden=H, inter=I, experts=E, top_k=k, gu=gu, down=down,
-                                          gu_group=gu_group, down_group=down_group)
+                                          gu_group=gu_group, down_group=down_group, book_format=book_format)
         self.router = router if router is not None else orc.bf16(rng.normal(0, 0.02, (E, H)))
         self.wsg = orc.bf16(rng.normal(0, 0.02, H))
         geo = (gu, gu, down)

@@ -20,13 +20,13 @@ P, I32, I64, U32, U64, F32, F64 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint32, 
 class Desc(C.Structure):  # field order of oracle/q38_oracle.cpp Desc
     _fields_ = [(n, C.c_int32) for n in (
         "hidden", "inter", "experts", "top_k", "gu_dim", "gu_bits", "down_dim", "down_bits",
-        "gu_group", "down_group", "normalize", "has_shared", "mixed", "pad")]
+        "gu_group", "down_group", "normalize", "has_shared", "mixed", "book_format")]
 
 
 def make_desc(hidden=2048, inter=512, experts=512, top_k=10, gu=(8, 14), down=(8, 14), gu_group=None,
-              down_group=None, normalize=1, shared=1, mixed=0) -> Desc:
+              down_group=None, normalize=1, shared=1, mixed=0, book_format=0) -> Desc:
     return Desc(hidden, inter, experts, top_k, gu[0], gu[1], down[0], down[1], gu_group or hidden,
-                down_group or inter, normalize, shared, mixed, 0)
+                down_group or inter, normalize, shared, mixed, book_format)
 
 
 def _a(x):
@@ -52,6 +52,7 @@ class Oracle:
         sig("orc_gen_code_rows", None, U64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P)
         sig("orc_gen_book", None, U64, C.c_int, C.c_int, C.c_int, P, P, P)
         sig("orc_gen_embed", None, U64, P, C.c_int, C.c_int, P)
+        sig("orc_prepare_u8_book", None, P, C.c_int, C.c_int, C.c_int, P, P, P, P)
         sig("orc_packed_word_count", I64, I64, C.c_int)
         sig("orc_pack_row", C.c_int, P, I64, C.c_int, P)
         sig("orc_unpack_code", C.c_int, P, I64, I64, C.c_int, P)
@@ -243,6 +244,17 @@ class Oracle:
         out = np.empty((h.shape[0], nv), np.float32)
         self.lib.orc_head_q4_synth_logits(seed, H, v0, nv, _a(h), h.shape[0], _a(out), threads)
         return out
+
+    def prepare_u8_book(self, book16, K, D, centered):
+        """SparseMoe::prepare_u8_codebook of an FP16 book [K*D] (uint16 bits): (q int32, scales
+        fp16 bits [D], biases fp16 bits [D], decoded float values)."""
+        b = np.ascontiguousarray(book16, np.uint16)
+        q = np.empty(K * D, np.int32)
+        s16 = np.empty(D, np.uint16)
+        b16 = np.empty(D, np.uint16)
+        vals = np.empty(K * D, np.float32)
+        self.lib.orc_prepare_u8_book(_a(b), K, D, int(centered), _a(q), _a(s16), _a(b16), _a(vals))
+        return q, s16, b16, vals
 
     def head_q4_logits(self, Wp, s, h, threads=8):
         """Explicit Q4 head: Wp [V, H/2] uint8 (input 2i low nibble, 2i+1 high nibble, signed),
