@@ -32,13 +32,19 @@
 //                          regeneration + float64 logits.
 //   RMSNorm                bit-exact float64 numpy restatement, closed forms, invariants.
 
+#include <pthread.h>
+#include <sched.h>
+
 #include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cmath>
+#include <condition_variable>
 #include <cstdint>
 #include <cstring>
+#include <functional>
 #include <limits>
+#include <mutex>
 #include <numeric>
 #include <thread>
 #include <vector>
@@ -341,20 +347,106 @@ struct LayerSource {
     virtual ExpertWeights expert(int e) = 0;    // e == E: shared expert
 };
 
+// Persistent worker pool: workers are created on first use, each pinned to one CPU of the
+// process's affinity mask (worker t to the (t+1)-th allowed CPU, the caller's thread runs
+// items too and is not pinned), and wait on a condition variable between jobs. One job at a
+// time (callers serialise on `run_mu`); items are handed out by an atomic counter.
+class Pool {
+public:
+    static Pool& get() {
+        static Pool p;
+        return p;
+    }
+    void run(int n, int threads, const std::function<void(int)>& f) {
+        std::lock_guard<std::mutex> run_lock(run_mu_);
+        const int helpers = std::min(threads, n) - 1;
+        grow(helpers);
+        std::atomic<int> next{0};
+        const std::function<void()> body = [&] {
+            for (int i = next.fetch_add(1); i < n; i = next.fetch_add(1)) f(i);
+        };
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            job_ = &body;
+            active_ = helpers;
+            pending_ = helpers;
+            ++gen_;
+        }
+        cv_.notify_all();
+        body();
+        std::unique_lock<std::mutex> lk(mu_);
+        done_cv_.wait(lk, [&] { return pending_ == 0; });
+        job_ = nullptr;
+    }
+    ~Pool() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+            ++gen_;
+        }
+        cv_.notify_all();
+        for (auto& t : workers_) t.join();
+    }
+
+private:
+    void grow(int want) {
+        while (static_cast<int>(workers_.size()) < want) {
+            const int id = static_cast<int>(workers_.size());
+            workers_.emplace_back([this, id] { loop(id); });
+            pin(workers_.back(), id + 1);
+        }
+    }
+    static void pin(std::thread& t, int ordinal) {
+        cpu_set_t allowed;
+        CPU_ZERO(&allowed);
+        if (sched_getaffinity(0, sizeof(allowed), &allowed) != 0) return;
+        const int n = CPU_COUNT(&allowed);
+        if (n == 0) return;
+        int want = ordinal % n;
+        for (int c = 0; c < CPU_SETSIZE; ++c) {
+            if (!CPU_ISSET(c, &allowed)) continue;
+            if (want-- == 0) {
+                cpu_set_t one;
+                CPU_ZERO(&one);
+                CPU_SET(c, &one);
+                pthread_setaffinity_np(t.native_handle(), sizeof(one), &one);
+                return;
+            }
+        }
+    }
+    void loop(int id) {
+        uint64_t seen = 0;
+        for (;;) {
+            const std::function<void()>* job = nullptr;
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return stop_ || (gen_ != seen && id < active_); });
+                if (stop_) return;
+                seen = gen_;
+                job = job_;
+            }
+            (*job)();
+            std::lock_guard<std::mutex> lk(mu_);
+            if (--pending_ == 0) done_cv_.notify_one();
+        }
+    }
+    std::mutex run_mu_, mu_;
+    std::condition_variable cv_, done_cv_;
+    std::vector<std::thread> workers_;
+    const std::function<void()>* job_ = nullptr;
+    int active_ = 0, pending_ = 0;
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+};
+
 template <class F>
 void parallel_for(int n, int threads, F&& f) {
     if (threads <= 1 || n <= 1) {
         for (int i = 0; i < n; ++i) f(i);
         return;
     }
-    std::atomic<int> next{0};
-    std::vector<std::thread> pool;
-    const int nt = std::min(threads, n);
-    for (int t = 0; t < nt; ++t)
-        pool.emplace_back([&] {
-            for (int i = next.fetch_add(1); i < n; i = next.fetch_add(1)) f(i);
-        });
-    for (auto& th : pool) th.join();
+    const std::function<void(int)> fn(std::ref(f));
+    Pool::get().run(n, threads, fn);
 }
 
 // SparseMoe::forward_verify on the fused-VQ path (src/sparse_moe.cpp:2199-2247 routing,
@@ -874,15 +966,22 @@ int orc_moe_layer_synth_bias(const Desc* d, uint64_t seed, int layer, const uint
 }
 // Same as orc_moe_layer_synth, but the tensors are materialised by an untimed first pass
 // and *seconds receives the wall time of a second, arithmetic-only pass (CPU baseline).
-int orc_moe_layer_synth_timed(const Desc* d, uint64_t seed, int layer, const uint16_t* x, int M, uint16_t* y,
-                              int threads, double* seconds) {
+// Repeated timing of one synthetic layer: the layer's experts are generated once (untimed),
+// then for each of the n_cfg thread counts, `warm` untimed passes and `reps` timed passes;
+// seconds[c * reps + r] is pass r at threads[c].
+int orc_moe_layer_synth_reps(const Desc* d, uint64_t seed, int layer, const uint16_t* x, int M, uint16_t* y,
+                             const int* threads, int n_cfg, int warm, int reps, double* seconds) {
     SynthSource src(*d, seed, static_cast<uint64_t>(layer));
     CachingSource cs(src);
-    int rc = moe_layer(*d, cs, x, M, y, nullptr, nullptr, nullptr, threads);
-    if (rc) return rc;
-    const auto t0 = std::chrono::steady_clock::now();
-    rc = moe_layer(*d, cs, x, M, y, nullptr, nullptr, nullptr, threads);
-    *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    int rc = moe_layer(*d, cs, x, M, y, nullptr, nullptr, nullptr, threads[0]);
+    for (int c = 0; c < n_cfg && rc == 0; ++c) {
+        for (int w = 0; w < warm && rc == 0; ++w) rc = moe_layer(*d, cs, x, M, y, nullptr, nullptr, nullptr, threads[c]);
+        for (int r = 0; r < reps && rc == 0; ++r) {
+            const auto t0 = std::chrono::steady_clock::now();
+            rc = moe_layer(*d, cs, x, M, y, nullptr, nullptr, nullptr, threads[c]);
+            seconds[c * reps + r] = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        }
+    }
     return rc;
 }
 // codes/scales/books: arrays of 3 pointers (gate, up, down) in the product layout

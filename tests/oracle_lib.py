@@ -63,8 +63,8 @@ class Oracle:
         sig("orc_moe_layer_synth", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, P, P, C.c_int)
         sig("orc_moe_layer_synth_bias", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, P, P, P,
             C.c_int)
-        sig("orc_moe_layer_synth_timed", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, C.c_int,
-            C.POINTER(C.c_double))
+        sig("orc_moe_layer_synth_reps", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, C.c_int,
+            C.c_int, C.c_int, P)
         sig("orc_moe_layer_dense", C.c_int, C.POINTER(Desc), P, P, C.POINTER(P), C.POINTER(P), C.POINTER(P),
             P, C.c_int, P, P, P, P, C.c_int)
         sig("orc_expert_dense", C.c_int, C.POINTER(Desc), C.POINTER(P), C.POINTER(P), C.POINTER(P), C.c_int, P,
@@ -188,13 +188,15 @@ class Oracle:
         assert rc == 0
         return y, ex, wt, lg
 
-    def moe_layer_synth_timed(self, d: Desc, seed, layer, x, threads=8):
+    def moe_layer_synth_reps(self, d: Desc, seed, layer, x, threads=(8,), warm=2, reps=20):
+        """Seconds per pass, [len(threads), reps], of one synthetic layer (experts generated once)."""
         x = np.ascontiguousarray(x, np.uint16)
         y = np.empty_like(x)
-        sec = C.c_double()
-        assert self.lib.orc_moe_layer_synth_timed(C.byref(d), seed, layer, _a(x), x.shape[0], _a(y), threads,
-                                                  C.byref(sec)) == 0
-        return y, sec.value
+        th = np.asarray(threads, np.int32)
+        sec = np.zeros((len(th), reps), np.float64)
+        assert self.lib.orc_moe_layer_synth_reps(C.byref(d), seed, layer, _a(x), x.shape[0], _a(y), _a(th),
+                                                 len(th), warm, reps, _a(sec)) == 0
+        return y, sec
 
     def moe_layer_dense(self, d: Desc, router, wsg, codes, scales, books, x, threads=8):
         x = np.ascontiguousarray(x, np.uint16)

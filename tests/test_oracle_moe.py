@@ -69,7 +69,7 @@ def test_zero_codebook_gives_zero(orc):
     router = orc.bf16(rng.normal(0, 0.02, (E, H)))
     wsg = orc.bf16(rng.normal(0, 0.02, H))
     codes = [rng.integers(0, 2**32, (E + 1) * n_out * w, dtype=np.uint64).astype(np.uint32)
-             for n_out, w in ((I, 28), (I, 28), (H, 7))]
+             for n_out, w in ((I, 28), (I, 28), (H, 14))]  # 16 codes per down row fill one 14-word block
     scales = [f16(rng.uniform(0.005, 0.02, (E + 1) * n)) for n in (I, I, H)]
     books = [np.zeros(16384 * 8, np.uint16)] * 3
     x = orc.bf16(rng.normal(0, 1, (3, H)))
@@ -162,3 +162,16 @@ def test_mixed_layer_vs_numpy(orc):
     got = orc.bf16_to_f32(y).astype(np.float64)
     rel = np.linalg.norm(got - want) / np.linalg.norm(want)
     assert rel < 2e-3 and np.abs(got - want).max() < 2e-3, rel
+
+
+def test_thread_pool_is_deterministic(orc):
+    """The pooled oracle gives the same bits on 1, 3 and 8 threads, and repeated timed passes
+    reproduce the single-pass result (routes are independent items; the route reduce is serial)."""
+    desc = oracle_lib.make_desc(hidden=512, inter=128, experts=64, top_k=4)
+    x = orc.bf16(np.random.default_rng(9).normal(0, 1, (4, 512)))
+    ref = orc.moe_layer_synth(desc, 7, 2, x, threads=1)[0]
+    for t in (3, 8):
+        assert np.array_equal(orc.moe_layer_synth(desc, 7, 2, x, threads=t)[0], ref)
+    y, sec = orc.moe_layer_synth_reps(desc, 7, 2, x, threads=(8, 1), warm=1, reps=3)
+    assert np.array_equal(y, ref)
+    assert sec.shape == (2, 3) and (sec > 0).all()
