@@ -297,7 +297,8 @@ void q38_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t ou
 int q38_slot_create(q38_ctx* ctx, int32_t hidden, int32_t max_rows, uint64_t token_count, q38_slot** out);
 void q38_slot_destroy(q38_slot* slot);
 /* Record a verification of draft_count drafts: rows = draft_count + 1 checkpoints whose
- * hidden rows are h (device [rows, H] bf16, copied on stream). */
+ * hidden rows are h (device [rows, H] bf16, copied on stream). draft_count 0 stages a
+ * serial decode step (one row, committed with accepted = 0). */
 int q38_slot_stage(q38_slot* slot, int32_t draft_count, const uint16_t* h, void* stream);
 /* commit_mtp_target_verification (src/mtp_verifier.cpp:129-145): keep checkpoint
  * `accepted`; token_count becomes origin + accepted + 1; all staged rows are released.

@@ -1099,7 +1099,7 @@ void q38_slot_destroy(q38_slot* s) {
 // update and the committed checkpoint survives a later stage + rollback.
 int q38_slot_stage(q38_slot* s, int32_t draft_count, const uint16_t* h, void* stream) {
     if (!s || !h) return fail(Q38_EINVAL, "q38_slot_stage: null argument");
-    if (draft_count < 1 || draft_count + 1 > s->max_rows)
+    if (draft_count < 0 || draft_count + 1 > s->max_rows)
         return fail(Q38_EINVAL, "staged verification exceeds the slot's row capacity");
     Q38_HIP(hipMemcpyAsync(s->rows[s->stage_buf], h, static_cast<size_t>(draft_count + 1) * s->hidden * 2,
                            hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));

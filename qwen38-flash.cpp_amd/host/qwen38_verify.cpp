@@ -456,4 +456,42 @@ MtpRoundStep run_greedy_external_draft_round_reference(const QwenModel& target, 
     return step;
 }
 
+// ------------------------------------------------------------------ batched slots
+QwenBatchVerifier::QwenBatchVerifier(const QwenModel& model, std::vector<ModelDecodeState*> slots)
+    : model_(model), slots_(std::move(slots)) {
+    for (ModelDecodeState* s : slots_)
+        if (s == nullptr) throw std::runtime_error("batch verifier slot is null");
+}
+
+std::vector<std::vector<std::uint32_t>> QwenBatchVerifier::verify(std::span<const SlotVerifyRows> batch) {
+    std::vector<std::uint32_t> tokens;
+    for (const SlotVerifyRows& e : batch) {
+        if (e.slot >= slots_.size()) throw std::runtime_error("batch verification names an unknown slot");
+        tokens.push_back(e.current_token);
+        tokens.insert(tokens.end(), e.drafts.begin(), e.drafts.end());
+    }
+    std::vector<GreedyStep> greedy;
+    model_.forward_verify_layer_major(tokens, final_mixed_, greedy);
+    const std::size_t H = model_.hidden();
+    std::vector<std::vector<std::uint32_t>> out;
+    out.reserve(batch.size());
+    std::size_t row = 0;
+    for (const SlotVerifyRows& e : batch) {
+        const std::size_t n = e.drafts.size() + 1;
+        check(q38_slot_stage(slots_[e.slot]->slot(), static_cast<int32_t>(e.drafts.size()),
+                             static_cast<const uint16_t*>(final_mixed_.data()) + row * H, model_.context().stream()),
+              "batched verification checkpoints");
+        std::vector<std::uint32_t> t(n);
+        for (std::size_t i = 0; i < n; ++i) t[i] = greedy[row + i].token;
+        out.push_back(std::move(t));
+        row += n;
+    }
+    return out;
+}
+
+void QwenBatchVerifier::commit(std::size_t slot, std::size_t accepted) {
+    if (slot >= slots_.size()) throw std::runtime_error("commit names an unknown slot");
+    check(q38_slot_commit(slots_[slot]->slot(), static_cast<int64_t>(accepted), model_.context().stream()), "commit");
+}
+
 } // namespace qwen38

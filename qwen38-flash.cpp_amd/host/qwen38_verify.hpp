@@ -17,6 +17,7 @@
 #pragma once
 
 #include "q38.h"
+#include "qwen38_engine.hpp"
 
 #include <cstddef>
 #include <cstdint>
@@ -297,5 +298,24 @@ struct MtpRoundStep {
                                                                      std::vector<std::uint32_t> drafts,
                                                                      ModelDecodeState& target_state,
                                                                      std::span<const std::uint32_t> stop_tokens = {});
+
+// ------------------------------------------------------------------ batched slots
+// BatchVerifier on the GPU: one verification packs every slot's rows [current, drafts...]
+// into one layer-major pass of the model (up to 16 rows) and stages each slot's rows as the
+// checkpoints of its decode state; commit() keeps one of them (q38_slot_commit).
+class QwenBatchVerifier final : public BatchVerifier {
+public:
+    QwenBatchVerifier(const QwenModel& model, std::vector<ModelDecodeState*> slots);
+    [[nodiscard]] std::size_t max_rows() const override { return 16; }
+    [[nodiscard]] std::vector<std::vector<std::uint32_t>> verify(std::span<const SlotVerifyRows> batch) override;
+    void commit(std::size_t slot, std::size_t accepted) override;
+    // Final hidden rows [1, rows, H] of the last verification, in batch order.
+    [[nodiscard]] const DeviceTensor& last_final_mixed() const noexcept { return final_mixed_; }
+
+private:
+    const QwenModel& model_;
+    std::vector<ModelDecodeState*> slots_;
+    DeviceTensor final_mixed_;
+};
 
 } // namespace qwen38

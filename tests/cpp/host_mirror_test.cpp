@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <algorithm>
 #include <cstring>
+#include <memory>
 #include <stdexcept>
 #include <vector>
 
@@ -81,6 +82,122 @@ static void host_tests() {
     CHECK(throws<std::runtime_error>(
         [&] { (void)qwen38::decide_mtp_greedy(drafts, std::vector<std::uint32_t>{10, 20, 30}); }));
     std::printf("host section: ok\n");
+}
+
+// The engine-side round driver over the GPU: 3 requests share each batched verification.
+// Every recorded batch is recomputed row by row in the same kernel family (a row alone when
+// the batch had at most 4 rows, else the row with 4 fixed companions: rows of a batch are
+// independent within a family), so the greedy tokens and logits must match exactly; each
+// state's committed length and hidden row follow the scheduler's commits.
+static void batched_slot_tests(const qwen38::Context& ctx, const qwen38::QwenModel& model) {
+    struct Recording final : qwen38::BatchVerifier {
+        qwen38::QwenBatchVerifier& inner;
+        std::vector<std::vector<qwen38::SlotVerifyRows>> batches;
+        std::vector<std::vector<std::vector<std::uint32_t>>> targets;
+        std::vector<std::vector<std::size_t>> accepted;
+        explicit Recording(qwen38::QwenBatchVerifier& v) : inner(v) {}
+        std::size_t max_rows() const override { return inner.max_rows(); }
+        std::vector<std::vector<std::uint32_t>> verify(std::span<const qwen38::SlotVerifyRows> b) override {
+            auto t = inner.verify(b);
+            batches.emplace_back(b.begin(), b.end());
+            targets.push_back(t);
+            accepted.emplace_back();
+            return t;
+        }
+        void commit(std::size_t slot, std::size_t a) override {
+            inner.commit(slot, a);
+            accepted.back().push_back(a);
+        }
+    };
+    // Drafts from the (token -> target) pairs seen so far; unseen tokens get a made-up successor.
+    struct MemoDrafter final : qwen38::LearnedDrafter {
+        Recording* rec = nullptr;
+        std::size_t vocab = 0;
+        std::vector<std::uint32_t> propose(std::size_t, std::uint32_t cur, std::size_t depth) override {
+            std::vector<std::uint32_t> d;
+            for (std::size_t i = 0; i < depth; ++i) {
+                std::uint32_t nxt = static_cast<std::uint32_t>((cur * 31u + 7u) % vocab);
+                for (std::size_t b = 0; b < rec->batches.size(); ++b)
+                    for (std::size_t e = 0; e < rec->batches[b].size(); ++e) {
+                        const auto& rows = rec->batches[b][e];
+                        if (rows.current_token == cur) nxt = rec->targets[b][e][0];
+                        for (std::size_t j = 0; j < rows.drafts.size(); ++j)
+                            if (rows.drafts[j] == cur) nxt = rec->targets[b][e][j + 1];
+                    }
+                d.push_back(nxt);
+                cur = nxt;
+            }
+            return d;
+        }
+    };
+    std::vector<std::unique_ptr<qwen38::ModelDecodeState>> states;
+    std::vector<qwen38::ModelDecodeState*> ptrs;
+    for (std::size_t i = 0; i < 3; ++i) {
+        states.push_back(std::make_unique<qwen38::ModelDecodeState>(model, 10 + i, 16));
+        ptrs.push_back(states.back().get());
+    }
+    qwen38::QwenBatchVerifier gpu(model, ptrs);
+    Recording rec(gpu);
+    MemoDrafter drafter;
+    drafter.rec = &rec;
+    drafter.vocab = model.vocab();
+    qwen38::MtpSchedulerOptions opt;
+    opt.zero_accept_fallback_rounds = 1000;
+    opt.economic_fallback = false;
+    qwen38::MtpSlotScheduler sched(rec, &drafter, opt);
+    for (std::size_t i = 0; i < 3; ++i) {
+        const std::vector<std::uint32_t> prompt{static_cast<std::uint32_t>(100 + i), static_cast<std::uint32_t>(200 + 3 * i)};
+        sched.add_request(i, prompt, 10 + i, 20);
+    }
+    std::size_t rounds = 0;
+    while (!sched.done() && rounds < 100) {
+        (void)sched.step();
+        ++rounds;
+        // the last verification's committed rows are the slots' committed hidden rows
+        const auto& b = rec.batches.back();
+        const qwen38::DeviceTensor& fm = gpu.last_final_mixed();
+        const std::size_t H = model.hidden();
+        std::vector<std::uint16_t> all(fm.numel()), mine(H);
+        fm.download(all.data(), all.size() * 2);
+        std::size_t row = 0;
+        for (std::size_t e = 0; e < b.size(); ++e) {
+            const std::size_t a = rec.accepted.back()[e];
+            CHECK(hipMemcpy(mine.data(), q38_slot_hidden(ptrs[b[e].slot]->slot()), H * 2, hipMemcpyDeviceToHost) ==
+                  hipSuccess);
+            CHECK(std::equal(mine.begin(), mine.end(), all.begin() + static_cast<std::ptrdiff_t>((row + a) * H)));
+            row += b[e].drafts.size() + 1;
+        }
+    }
+    CHECK(sched.done());
+    std::size_t recomputed = 0, wide = 0, accepted_total = 0;
+    const std::vector<std::uint32_t> companions{3, 1, 4, 1};
+    for (std::size_t bi = 0; bi < rec.batches.size(); ++bi) {
+        std::size_t rows = 0;
+        for (const auto& e : rec.batches[bi]) rows += e.drafts.size() + 1;
+        wide += rows > 4;
+        for (std::size_t e = 0; e < rec.batches[bi].size(); ++e) {
+            const auto& rs = rec.batches[bi][e];
+            std::vector<std::uint32_t> toks{rs.current_token};
+            toks.insert(toks.end(), rs.drafts.begin(), rs.drafts.end());
+            accepted_total += rec.accepted[bi][e];
+            for (std::size_t j = 0; j < toks.size(); ++j) {
+                std::vector<std::uint32_t> alone{toks[j]};
+                if (rows > 4) alone.insert(alone.end(), companions.begin(), companions.end());
+                qwen38::DeviceTensor f1;
+                std::vector<qwen38::GreedyStep> g1;
+                model.forward_verify_layer_major(alone, f1, g1);
+                CHECK(g1[0].token == rec.targets[bi][e][j]);
+                ++recomputed;
+            }
+        }
+    }
+    for (std::size_t i = 0; i < 3; ++i) {
+        CHECK(sched.tokens(i).size() == 20 && sched.stats(i).finish_reason == "length");
+        CHECK(states[i]->token_count() == sched.query_position(i));
+    }
+    CHECK(wide > 0 && accepted_total > 0);
+    std::printf("batched slots: ok (%zu rounds, %zu verifications, %zu wide, %zu rows recomputed, %zu accepted)\n",
+                rounds, rec.batches.size(), wide, recomputed, accepted_total);
 }
 
 static void gpu_tests() {
@@ -256,6 +373,7 @@ static void gpu_tests() {
     CHECK(step.next_query_position == q + step.accepted + 1 && state.token_count() == step.next_query_position);
     CHECK(step.emitted_tokens.back() == step.next_current_token);
     std::printf("gpu section: ok (accepted %zu of 3 self-drafts)\n", step.accepted);
+    batched_slot_tests(ctx, model);
 }
 
 int main(int argc, char** argv) {

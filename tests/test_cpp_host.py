@@ -1,7 +1,8 @@
 """The C++20 host interface (qwen38-flash.cpp_amd/host/qwen38_verify.hpp) through its test
 program tests/cpp/host_mirror_test.cpp, built with the library: host KATs and exception
 types on the CPU, the device section (SparseMoe vs the C ABI, verify + commit lifecycle,
-a greedy round) on the GPU."""
+a greedy round, and the engine-side round driver with 3 requests sharing each batched
+verification, every batch recomputed row by row in the same kernel family) on the GPU."""
 import os
 import subprocess
 
@@ -26,3 +27,4 @@ def test_host_section():
 def test_gpu_section():
     out = run("--gpu")
     assert "gpu section: ok" in out, out
+    assert "batched slots: ok" in out, out
