@@ -265,6 +265,63 @@ int q38_head_greedy(q38_head* head, const uint16_t* h, int32_t rows, uint32_t* a
 int q38_head_logits(q38_head* head, const uint16_t* h, int32_t rows, float* logits, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* greedy_from_logits (src/mtp_verifier.cpp:20-55) on device logits [rows, vocab] float:
+ * per row the argmax, lowest index on ties (src/mlx_backend.cpp:78-85), and its value.
+ * argmax, value: device [rows] (value may be null); rows 1..64; workspace: device, at least
+ * 8 * rows bytes. */
+int q38_argmax_rows(const float* logits, int32_t rows, int64_t vocab, uint32_t* argmax, float* value,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ MTP draft head
+ * QwenMtpHead (include/qwen38/mtp_head.hpp:29-63) on the verify path's model: one draft step
+ * (forward_decode, src/mtp_head.cpp:454-470) for rows independent requests maps the target's
+ * pre-norm residual stream s (device [rows, H] bf16) and the next token t to
+ *   e = embed(t)                          the target's embedding (seeded generator)
+ *   x = T(T(W_e . rms(e)) + T(W_h . rms(s)))   combine_inputs (src/mtp_head.cpp:258-266):
+ *                                         two H x H Q8 projections (q38_head_logits, Q8)
+ *   s' = x + MoE(rms(x))                  the head's decoder block: one SparseMoe layer
+ *                                         (block.mlp as layer 48, src/sparse_moe.cpp:376-381)
+ *   logits = Q4 head(rms(s'))             the draft LM head (R14)
+ * with rms the unit-gain RMSNorm (eps of the head). s' is the step's output stream
+ * (pre_mixer_stream), the input of the next step of a draft chain. Rows 1..4 (the Q4 head's
+ * row limit); hidden 2048. */
+typedef struct q38_mtp_head q38_mtp_head;
+/* Borrowed components (kept alive by the caller): layer (hidden H), fc_embedding and
+ * fc_hidden (Q8 heads, vocab = hidden = H), draft_head (Q4, hidden H). */
+int q38_mtp_head_create(q38_ctx* ctx, q38_moe_layer* layer, q38_head* fc_embedding, q38_head* fc_hidden,
+                        q38_head* draft_head, uint64_t embed_seed, float eps, q38_mtp_head** out);
+/* Seeded random-init head: layer 48 of the seed's synthetic stack (desc), FC projections
+ * from the Q8 generator with seeds seed ^ Q38_MTP_FC_EMBED_SALT / seed ^ Q38_MTP_FC_HIDDEN_SALT,
+ * the Q4 draft head of the seed, the seed's embedding; eps 1e-6. */
+#define Q38_MTP_FC_EMBED_SALT 0x46C0E3BEull
+#define Q38_MTP_FC_HIDDEN_SALT 0x46C0411Dull
+int q38_mtp_head_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, int64_t vocab, uint64_t seed,
+                                  q38_mtp_head** out);
+void q38_mtp_head_destroy(q38_mtp_head* head);
+/* The component handles (owned by the head when it was created synthetic). */
+int q38_mtp_head_parts(const q38_mtp_head* head, q38_moe_layer** layer, q38_head** fc_embedding,
+                       q38_head** fc_hidden, q38_head** draft_head);
+/* Device workspace bytes for up to max_rows rows (1..4); 0 for an invalid count. */
+size_t q38_mtp_workspace_size(const q38_mtp_head* head, int32_t max_rows);
+/* Optional intermediate rows of a step (MtpTrace, include/qwen38/mtp_head.hpp:24-28):
+ * combined = x, final_mixed = rms(s'); device [rows, H] bf16 each, or null. */
+typedef struct q38_mtp_trace {
+    uint16_t* combined;
+    uint16_t* final_mixed;
+} q38_mtp_trace;
+/* One draft step: tokens device u32 [rows]; logits device [rows, V] float (or null);
+ * stream_out device [rows, H] bf16 (or null). */
+int q38_mtp_forward_decode(q38_mtp_head* head, const uint16_t* stream_in, const uint32_t* tokens, int32_t rows,
+                           float* logits, uint16_t* stream_out, const q38_mtp_trace* trace, void* workspace,
+                           size_t workspace_bytes, void* stream);
+/* Greedy draft chain (draft_lazy_chain, src/mtp_runner.cpp:152-211): depth steps, each
+ * feeding its argmax token (q38_argmax_rows) and output stream into the next, all on the
+ * device. drafts: device u32 [rows, depth]; depth 1..24; stream_out (optional) receives
+ * the last step's output stream. No host synchronisation (graph-capturable). */
+int q38_mtp_draft_greedy(q38_mtp_head* head, const uint16_t* stream_in, const uint32_t* tokens, int32_t rows,
+                         int32_t depth, uint32_t* drafts, uint16_t* stream_out, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ acceptance
  * decide_mtp_greedy (src/mtp_lifecycle.cpp:75-97), host. */
 typedef struct q38_greedy_decision {

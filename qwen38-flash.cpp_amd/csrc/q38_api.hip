@@ -1029,6 +1029,208 @@ int q38_head_logits(q38_head* hd, const uint16_t* h, int32_t rows, float* logits
     return Q38_OK;
 }
 
+int q38_argmax_rows(const float* logits, int32_t rows, int64_t vocab, uint32_t* argmax, float* value, void* ws,
+                    size_t ws_bytes, void* stream) {
+    if (!logits || !argmax) return fail(Q38_EINVAL, "q38_argmax_rows: null argument");
+    if (rows < 1 || rows > 64 || vocab < 1 || vocab > (int64_t{1} << 31) - 2)
+        return fail(Q38_EINVAL, "q38_argmax_rows: rows must be 1..64 and vocab positive");
+    if (!ws || ws_bytes < static_cast<size_t>(rows) * 8) return fail(Q38_ESPACE, "workspace too small");
+    Q38_HIP(launch_argmax(logits, rows, vocab, static_cast<unsigned long long*>(ws), true, argmax, value, nullptr, 1,
+                          0, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+// ------------------------------------------------------------------ MTP draft head
+struct q38_mtp_head {
+    q38_ctx* ctx;
+    q38_moe_layer* layer;
+    q38_head* fc_e;
+    q38_head* fc_h;
+    q38_head* draft;
+    uint64_t embed_seed;
+    float eps;
+    bool owned;
+};
+
+namespace {
+constexpr int kMtpMaxRows = 4;
+
+struct MtpWork {
+    uint16_t *e16, *ne, *nh, *x, *f;
+    float *pe, *ph, *logits;
+    unsigned long long* best;
+    uint32_t* tokens;
+    void* head_ws;
+    size_t head_ws_bytes;
+    void* moe_ws;
+    size_t moe_ws_bytes;
+};
+
+size_t mtp_layout(const q38_mtp_head* m, int rows, MtpWork* w, void* base) {
+    const size_t H = static_cast<size_t>(m->layer->desc.hidden);
+    const size_t V = static_cast<size_t>(m->draft->dev.V);
+    char* b = static_cast<char*>(base);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        char* p = b ? b + off : nullptr;
+        off += align256(bytes);
+        return p;
+    };
+    MtpWork t{};
+    t.e16 = reinterpret_cast<uint16_t*>(take(rows * H * 2));
+    t.ne = reinterpret_cast<uint16_t*>(take(rows * H * 2));
+    t.nh = reinterpret_cast<uint16_t*>(take(rows * H * 2));
+    t.x = reinterpret_cast<uint16_t*>(take(rows * H * 2));
+    t.f = reinterpret_cast<uint16_t*>(take(rows * H * 2));
+    t.pe = reinterpret_cast<float*>(take(rows * H * 4));
+    t.ph = reinterpret_cast<float*>(take(rows * H * 4));
+    t.logits = reinterpret_cast<float*>(take(rows * V * 4));
+    t.best = reinterpret_cast<unsigned long long*>(take(rows * 8));
+    t.tokens = reinterpret_cast<uint32_t*>(take(rows * 4));
+    t.head_ws_bytes = std::max(q38_head_workspace_size(m->fc_e, rows), q38_head_workspace_size(m->fc_h, rows));
+    t.head_ws = take(t.head_ws_bytes);
+    t.moe_ws_bytes = q38_moe_workspace_size(&m->layer->desc, rows);
+    t.moe_ws = take(t.moe_ws_bytes);
+    if (w) *w = t;
+    return off;
+}
+
+int mtp_validate(q38_moe_layer* layer, q38_head* fe, q38_head* fh, q38_head* dh) {
+    if (!layer || !fe || !fh || !dh) return fail(Q38_EINVAL, "q38_mtp_head_create: null component");
+    const int H = layer->desc.hidden;
+    if (H != 2048) return fail(Q38_EINVAL, "MTP draft head hidden size must be 2048");
+    for (const q38_head* fc : {fe, fh})
+        if (fc->dev.kind != Q38_HEAD_Q8 || fc->dev.V != H || fc->dev.H != H)
+            return fail(Q38_EINVAL, "MTP FC projections must be Q8 heads with vocab = hidden = the layer's hidden");
+    if (dh->dev.kind != Q38_HEAD_Q4G64 || dh->dev.H != H)
+        return fail(Q38_EINVAL, "MTP draft LM head must be a Q4 head of the layer's hidden size");
+    return Q38_OK;
+}
+
+// One draft step on rows (<= 4) requests; logits into `logits`, the output stream in w.x.
+int mtp_step(q38_mtp_head* m, const MtpWork& w, const uint16_t* stream_in, const uint32_t* tokens, int rows,
+             float* logits, const q38_mtp_trace* trace, hipStream_t st) {
+    const int H = m->layer->desc.hidden;
+    Q38_HIP(launch_gen_embed_dev(m->embed_seed, tokens, rows, H, w.e16, st));
+    Q38_HIP(launch_rmsnorm(w.e16, rows, H, m->eps, w.ne, st));
+    Q38_HIP(launch_rmsnorm(stream_in, rows, H, m->eps, w.nh, st));
+    if (int rc = q38_head_logits(m->fc_e, w.ne, rows, w.pe, w.head_ws, w.head_ws_bytes, st)) return rc;
+    if (int rc = q38_head_logits(m->fc_h, w.nh, rows, w.ph, w.head_ws, w.head_ws_bytes, st)) return rc;
+    Q38_HIP(launch_fc_join(w.pe, w.ph, rows * H, w.x, w.best, rows, st));
+    if (trace && trace->combined)
+        Q38_HIP(hipMemcpyAsync(trace->combined, w.x, static_cast<size_t>(rows) * H * 2, hipMemcpyDeviceToDevice, st));
+    q38_moe_layer* layers[1] = {m->layer};
+    if (int rc = q38_verify_chain(layers, 1, w.x, rows, m->eps, nullptr, w.moe_ws, w.moe_ws_bytes, st)) return rc;
+    Q38_HIP(launch_rmsnorm(w.x, rows, H, m->eps, w.f, st));
+    if (trace && trace->final_mixed)
+        Q38_HIP(hipMemcpyAsync(trace->final_mixed, w.f, static_cast<size_t>(rows) * H * 2, hipMemcpyDeviceToDevice,
+                               st));
+    return q38_head_logits(m->draft, w.f, rows, logits, nullptr, 0, st);
+}
+} // namespace
+
+int q38_mtp_head_create(q38_ctx* ctx, q38_moe_layer* layer, q38_head* fc_embedding, q38_head* fc_hidden,
+                        q38_head* draft_head, uint64_t embed_seed, float eps, q38_mtp_head** out) {
+    if (!ctx || !out) return fail(Q38_EINVAL, "q38_mtp_head_create: null argument");
+    if (int rc = mtp_validate(layer, fc_embedding, fc_hidden, draft_head)) return rc;
+    if (!(eps > 0.0f)) return fail(Q38_EINVAL, "q38_mtp_head_create: eps must be positive");
+    *out = new q38_mtp_head{ctx, layer, fc_embedding, fc_hidden, draft_head, embed_seed, eps, false};
+    return Q38_OK;
+}
+
+int q38_mtp_head_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, int64_t vocab, uint64_t seed,
+                                  q38_mtp_head** out) {
+    if (!ctx || !desc || !out) return fail(Q38_EINVAL, "q38_mtp_head_create_synthetic: null argument");
+    if (desc->hidden != 2048) return fail(Q38_EINVAL, "MTP draft head hidden size must be 2048");
+    q38_moe_layer* layer = nullptr;
+    q38_head *fe = nullptr, *fh = nullptr, *dh = nullptr;
+    int rc = q38_moe_layer_create_synthetic(ctx, desc, seed, 48, &layer);
+    if (rc == Q38_OK)
+        rc = q38_head_create_synthetic(ctx, Q38_HEAD_Q8, desc->hidden, desc->hidden, seed ^ Q38_MTP_FC_EMBED_SALT, &fe);
+    if (rc == Q38_OK)
+        rc = q38_head_create_synthetic(ctx, Q38_HEAD_Q8, desc->hidden, desc->hidden, seed ^ Q38_MTP_FC_HIDDEN_SALT, &fh);
+    if (rc == Q38_OK) rc = q38_head_create_synthetic(ctx, Q38_HEAD_Q4G64, vocab, desc->hidden, seed, &dh);
+    if (rc == Q38_OK) rc = mtp_validate(layer, fe, fh, dh);
+    if (rc != Q38_OK) {
+        const std::string msg = g_error;
+        q38_head_destroy(dh);
+        q38_head_destroy(fh);
+        q38_head_destroy(fe);
+        q38_moe_layer_destroy(layer);
+        return fail(rc, msg);
+    }
+    *out = new q38_mtp_head{ctx, layer, fe, fh, dh, seed, 1e-6f, true};
+    return Q38_OK;
+}
+
+void q38_mtp_head_destroy(q38_mtp_head* m) {
+    if (!m) return;
+    if (m->owned) {
+        q38_head_destroy(m->draft);
+        q38_head_destroy(m->fc_h);
+        q38_head_destroy(m->fc_e);
+        q38_moe_layer_destroy(m->layer);
+    }
+    delete m;
+}
+
+int q38_mtp_head_parts(const q38_mtp_head* m, q38_moe_layer** layer, q38_head** fc_embedding, q38_head** fc_hidden,
+                       q38_head** draft_head) {
+    if (!m) return fail(Q38_EINVAL, "null MTP head");
+    if (layer) *layer = m->layer;
+    if (fc_embedding) *fc_embedding = m->fc_e;
+    if (fc_hidden) *fc_hidden = m->fc_h;
+    if (draft_head) *draft_head = m->draft;
+    return Q38_OK;
+}
+
+size_t q38_mtp_workspace_size(const q38_mtp_head* m, int32_t max_rows) {
+    if (!m || max_rows < 1 || max_rows > kMtpMaxRows) return 0;
+    return mtp_layout(m, max_rows, nullptr, nullptr);
+}
+
+int q38_mtp_forward_decode(q38_mtp_head* m, const uint16_t* stream_in, const uint32_t* tokens, int32_t rows,
+                           float* logits, uint16_t* stream_out, const q38_mtp_trace* trace, void* ws,
+                           size_t ws_bytes, void* stream) {
+    if (!m || !stream_in || !tokens) return fail(Q38_EINVAL, "q38_mtp_forward_decode: null argument");
+    if (rows < 1 || rows > kMtpMaxRows) return fail(Q38_EINVAL, "MTP draft rows must be between 1 and 4 per call");
+    if (!ws || ws_bytes < mtp_layout(m, rows, nullptr, nullptr)) return fail(Q38_ESPACE, "workspace too small");
+    MtpWork w{};
+    mtp_layout(m, rows, &w, ws);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (int rc = mtp_step(m, w, stream_in, tokens, rows, logits ? logits : w.logits, trace, st)) return rc;
+    if (stream_out)
+        Q38_HIP(hipMemcpyAsync(stream_out, w.x, static_cast<size_t>(rows) * m->layer->desc.hidden * 2,
+                               hipMemcpyDeviceToDevice, st));
+    return Q38_OK;
+}
+
+int q38_mtp_draft_greedy(q38_mtp_head* m, const uint16_t* stream_in, const uint32_t* tokens, int32_t rows,
+                         int32_t depth, uint32_t* drafts, uint16_t* stream_out, void* ws, size_t ws_bytes,
+                         void* stream) {
+    if (!m || !stream_in || !tokens || !drafts) return fail(Q38_EINVAL, "q38_mtp_draft_greedy: null argument");
+    if (rows < 1 || rows > kMtpMaxRows) return fail(Q38_EINVAL, "MTP draft rows must be between 1 and 4 per call");
+    if (depth < 1 || depth > 24) return fail(Q38_EINVAL, "MTP draft depth must be between 1 and 24");
+    if (!ws || ws_bytes < mtp_layout(m, rows, nullptr, nullptr)) return fail(Q38_ESPACE, "workspace too small");
+    MtpWork w{};
+    mtp_layout(m, rows, &w, ws);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint16_t* s_in = stream_in;
+    const uint32_t* t_in = tokens;
+    for (int step = 0; step < depth; ++step) {
+        // the step's join clears w.best; its argmax feeds the next step's token and stream
+        if (int rc = mtp_step(m, w, s_in, t_in, rows, w.logits, nullptr, st)) return rc;
+        Q38_HIP(launch_argmax(w.logits, rows, m->draft->dev.V, w.best, false, w.tokens, nullptr, drafts, depth, step,
+                              st));
+        s_in = w.x;
+        t_in = w.tokens;
+    }
+    if (stream_out)
+        Q38_HIP(hipMemcpyAsync(stream_out, w.x, static_cast<size_t>(rows) * m->layer->desc.hidden * 2,
+                               hipMemcpyDeviceToDevice, st));
+    return Q38_OK;
+}
+
 // ------------------------------------------------------------------ acceptance
 int q38_mtp_decide_greedy(const uint32_t* drafts, int64_t k, const uint32_t* target, int64_t n_target,
                           const uint32_t* stop, int64_t n_stop, q38_greedy_decision* out) {

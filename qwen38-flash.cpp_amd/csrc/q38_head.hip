@@ -1,6 +1,6 @@
 // q38_head.hip — gfx950 kernels of the verify tail: the Q8 target LM head with an exact
 // greedy argmax (R12, R13), the Q4/g64 draft head logits (R14), and rejection-sampling
-// acceptance (R16).
+// acceptance (R16), and the row argmax + FC join of the MTP draft head.
 //
 // Greedy argmax. The reference takes argmax_all over MLX quantized_matmul logits
 // (src/model.cpp:470-480, src/mtp_verifier.cpp:30-55). Greedy acceptance must be
@@ -26,6 +26,8 @@
 // which head_window doubles.
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
+
+#include <algorithm>
 
 namespace q38 {
 
@@ -542,6 +544,72 @@ hipError_t launch_gen_head(const HeadDev& hd, uint64_t seed, int8_t* w, uint16_t
 hipError_t launch_scale_absmax(const uint16_t* scales, int64_t n, float* out, hipStream_t st) {
     hipLaunchKernelGGL(k_scale_absmax, dim3(1), dim3(1024), 0, st, scales, n, out);
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- draft head helpers
+// MTP draft head FC join: x = T(T(a) + T(b)) over n values (the embedding and hidden
+// projections, each rounded to bf16, added in bf16: src/mtp_head.cpp:258-266). The sum of two
+// bf16 values is exact in fp32 or below half a bf16 ulp of the larger, so one rounding of the
+// fp32 sum is the correctly rounded bf16 sum. Also clears best[0..M) for the step's argmax.
+__global__ __launch_bounds__(256) void k_fc_join(const float* __restrict__ a, const float* __restrict__ b, int n,
+                                                 uint16_t* __restrict__ x, unsigned long long* __restrict__ best,
+                                                 int M) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = f2bf(rbf(a[i]) + rbf(b[i]));
+    if (best && i < M) best[i] = 0ull;
+}
+
+__global__ void k_fill_u64(unsigned long long* __restrict__ p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0ull;
+}
+
+// Row argmax of logits [M, V], ties to the lowest index (src/mtp_verifier.cpp:20-55 with the
+// tie rule of src/mlx_backend.cpp:78-85): each thread keeps the largest key
+// (orderable(value) << 32 | ~index) of a strided range, the wave reduces, one 64-bit atomic max
+// per wave merges into best[row] (which starts at 0, below every key).
+__global__ __launch_bounds__(256) void k_argmax_rows(const float* __restrict__ logits, int64_t V,
+                                                     unsigned long long* __restrict__ best) {
+    const int r = blockIdx.y;
+    const float* row = logits + static_cast<int64_t>(r) * V;
+    uint64_t k = 0;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < V;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const uint64_t c = (static_cast<uint64_t>(orderable(row[i])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+        k = c > k ? c : k;
+    }
+    k = wave_max_u64(k);
+    if ((threadIdx.x & 63) == 0 && k != 0) atomicMax(&best[r], static_cast<unsigned long long>(k));
+}
+
+// Decodes best[r] into tokens[r] (and values[r]); with drafts, also drafts[r * depth + step].
+__global__ void k_argmax_final(const unsigned long long* __restrict__ best, int M, uint32_t* __restrict__ tokens,
+                               float* __restrict__ values, uint32_t* __restrict__ drafts, int depth, int step) {
+    const int r = threadIdx.x;
+    if (r >= M) return;
+    const unsigned long long b = best[r];
+    const uint32_t t = 0xFFFFFFFFu - static_cast<uint32_t>(b);
+    if (tokens) tokens[r] = t;
+    if (values) values[r] = from_orderable(static_cast<uint32_t>(b >> 32));
+    if (drafts) drafts[static_cast<size_t>(r) * depth + step] = t;
+}
+
+hipError_t launch_fc_join(const float* a, const float* b, int n, uint16_t* x, unsigned long long* best, int M,
+                          hipStream_t st) {
+    return launch(k_fc_join, dim3((n + 255) / 256), dim3(256), 0, st, a, b, n, x, best, M);
+}
+
+hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long long* best, bool clear,
+                         uint32_t* tokens, float* values, uint32_t* drafts, int depth, int step, hipStream_t st) {
+    if (M < 1 || M > 64 || V < 1) return hipErrorInvalidValue;
+    if (clear) {
+        const hipError_t e = launch(k_fill_u64, dim3(1), dim3(256), 0, st, best, M);
+        if (e != hipSuccess) return e;
+    }
+    const int64_t blocks = std::min<int64_t>(128, (V + 255) / 256);
+    hipError_t e = launch(k_argmax_rows, dim3(static_cast<unsigned>(blocks), M), dim3(256), 0, st, logits, V, best);
+    if (e != hipSuccess) return e;
+    return launch(k_argmax_final, dim3(1), dim3(64), 0, st, best, M, tokens, values, drafts, depth, step);
 }
 
 hipError_t launch_accept_sampled(const float* tl, const float* dl, const uint32_t* drafts, int k, int64_t V,

@@ -192,6 +192,15 @@ hipError_t launch_head_greedy(const HeadDev& hd, const uint16_t* h, int M, const
 hipError_t launch_head_logits(const HeadDev& hd, const uint16_t* h, int M, const HeadWork& w, float* logits,
                               hipStream_t st);
 
+// draft head: x = T(T(a) + T(b)) over n values, clearing best[0..M) (best may be null)
+hipError_t launch_fc_join(const float* a, const float* b, int n, uint16_t* x, unsigned long long* best, int M,
+                          hipStream_t st);
+// Row argmax of logits [M, V] (ties to the lowest index) into best[M] (cleared first when
+// `clear`, else it must hold 0), decoded into tokens / values / drafts[r * depth + step]
+// (each may be null). M <= 64.
+hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long long* best, bool clear,
+                         uint32_t* tokens, float* values, uint32_t* drafts, int depth, int step, hipStream_t st);
+
 // acceptance
 hipError_t launch_accept_sampled(const float* tl, const float* dl, const uint32_t* drafts, int k, int64_t V,
                                  float T, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out,

@@ -97,6 +97,22 @@ _sig("q38_head_bytes", I64, P)
 _sig("q38_head_workspace_size", SZ, P, I32)
 _sig("q38_head_greedy", C.c_int, P, P, I32, P, P, P, SZ, P)
 _sig("q38_head_logits", C.c_int, P, P, I32, P, P, SZ, P)
+_sig("q38_argmax_rows", C.c_int, P, I32, I64, P, P, P, SZ, P)
+
+
+class MtpTrace(C.Structure):
+    _fields_ = [("combined", P), ("final_mixed", P)]
+
+
+Q38_MTP_FC_EMBED_SALT = 0x46C0E3BE
+Q38_MTP_FC_HIDDEN_SALT = 0x46C0411D
+_sig("q38_mtp_head_create", C.c_int, P, P, P, P, P, U64, F32, C.POINTER(P))
+_sig("q38_mtp_head_create_synthetic", C.c_int, P, C.POINTER(MoeDesc), I64, U64, C.POINTER(P))
+_sig("q38_mtp_head_destroy", None, P)
+_sig("q38_mtp_head_parts", C.c_int, P, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P))
+_sig("q38_mtp_workspace_size", SZ, P, I32)
+_sig("q38_mtp_forward_decode", C.c_int, P, P, P, I32, P, P, C.POINTER(MtpTrace), P, SZ, P)
+_sig("q38_mtp_draft_greedy", C.c_int, P, P, P, I32, I32, P, P, P, SZ, P)
 _sig("q38_mtp_decide_greedy", C.c_int, C.POINTER(U32), I64, C.POINTER(U32), I64, C.POINTER(U32), I64,
      C.POINTER(GreedyDecision))
 _sig("q38_plan_mtp_commit", C.c_int, U64, U64, U64, C.POINTER(U64))
@@ -202,6 +218,28 @@ class Head:
     def close(self):
         if self.h:
             lib.q38_head_destroy(self.h)
+            self.h = None
+
+
+class MtpHead:
+    """The MTP draft head (q38_mtp_head): synthetic (seeded) with the given MoE geometry."""
+
+    def __init__(self, ctx: Ctx, d: MoeDesc, vocab: int, seed: int):
+        h = P()
+        check(lib.q38_mtp_head_create_synthetic(ctx.h, C.byref(d), vocab, seed, C.byref(h)))
+        self.h, self.desc, self.vocab, self.seed = h, d, vocab, seed
+
+    def workspace_size(self, rows: int) -> int:
+        return lib.q38_mtp_workspace_size(self.h, rows)
+
+    def parts(self):
+        layer, fe, fh, dh = P(), P(), P(), P()
+        check(lib.q38_mtp_head_parts(self.h, C.byref(layer), C.byref(fe), C.byref(fh), C.byref(dh)))
+        return layer.value, fe.value, fh.value, dh.value
+
+    def close(self):
+        if self.h:
+            lib.q38_mtp_head_destroy(self.h)
             self.h = None
 
 

@@ -54,7 +54,8 @@ def test_slot_commit_rollback(gpu, q38):
         assert q38.lib.q38_slot_commit(s, 0, G.stream()) == q38.Q38_ESTATE      # nothing staged
         for accepted in range(5):
             rows = np.repeat(np.arange(5, dtype=np.uint16)[:, None] + 100 * accepted, H, 1)
-            q38.check(q38.lib.q38_slot_stage(s, 4, G.to_dev(rows).data_ptr(), G.stream()))
+            rows_dev = G.to_dev(rows)  # alive until the staging copy ran
+            q38.check(q38.lib.q38_slot_stage(s, 4, rows_dev.data_ptr(), G.stream()))
             q38.check(q38.lib.q38_slot_info(s, C.byref(tc), C.byref(sr), C.byref(dc)))
             before = tc.value
             assert (sr.value, dc.value) == (5, 4)
