@@ -100,11 +100,7 @@ MtpSlotScheduler::Plan MtpSlotScheduler::plan(std::size_t index) {
             return p;
         }
     }
-    std::vector<std::uint32_t> drafts = drafter_->propose(r.slot, r.current, r.depth.depth());
-    if (drafts.size() > std::min(r.depth.depth(), width)) drafts.resize(std::min(r.depth.depth(), width));
-    if (drafts.empty()) return p;  // the drafter had nothing: a serial step
-    p.source = DraftSourceKind::learned;
-    p.drafts = std::move(drafts);
+    p.wants_learned = true;  // filled in by step(), one drafter call for all learned slots
     return p;
 }
 
@@ -211,6 +207,28 @@ std::vector<SlotRound> MtpSlotScheduler::step() {
     std::vector<Plan> plans;
     for (std::size_t i = 0; i < requests_.size(); ++i)
         if (!requests_[i].finished) plans.push_back(plan(i));
+    std::vector<DraftRequest> asks;
+    for (const Plan& p : plans)
+        if (p.wants_learned) {
+            const Request& r = requests_[p.request];
+            asks.push_back(DraftRequest{r.slot, r.current, r.depth.depth()});
+        }
+    if (!asks.empty()) {
+        std::vector<std::vector<std::uint32_t>> got = drafter_->propose_batch(asks);
+        if (got.size() != asks.size()) throw std::runtime_error("learned drafter returned a wrong request count");
+        std::size_t j = 0;
+        const std::size_t width = verifier_.max_rows() - 1;
+        for (Plan& p : plans) {
+            if (!p.wants_learned) continue;
+            std::vector<std::uint32_t>& d = got[j];
+            const std::size_t cap = std::min(asks[j].depth, width);
+            if (d.size() > cap) d.resize(cap);
+            ++j;
+            if (d.empty()) continue;  // the drafter had nothing: a serial step
+            p.source = DraftSourceKind::learned;
+            p.drafts = std::move(d);
+        }
+    }
     std::vector<SlotRound> rounds;
     rounds.reserve(plans.size());
     const std::size_t width = verifier_.max_rows();

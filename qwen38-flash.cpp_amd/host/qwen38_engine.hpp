@@ -45,13 +45,26 @@ public:
     virtual void commit(std::size_t slot, std::size_t accepted) = 0;
 };
 
+struct DraftRequest {
+    std::size_t slot{0};
+    std::uint32_t current_token{0};
+    std::size_t depth{0};
+};
+
 // The learned drafter (the MTP draft head's role): up to `depth` drafts following
-// current_token for the slot.
+// current_token for the slot. propose_batch serves every learned slot of a round at once
+// (by default one propose() per request).
 class LearnedDrafter {
 public:
     virtual ~LearnedDrafter() = default;
     [[nodiscard]] virtual std::vector<std::uint32_t> propose(std::size_t slot, std::uint32_t current_token,
                                                              std::size_t depth) = 0;
+    [[nodiscard]] virtual std::vector<std::vector<std::uint32_t>> propose_batch(std::span<const DraftRequest> requests) {
+        std::vector<std::vector<std::uint32_t>> out;
+        out.reserve(requests.size());
+        for (const DraftRequest& r : requests) out.push_back(propose(r.slot, r.current_token, r.depth));
+        return out;
+    }
 };
 
 enum class DraftSourceKind { serial, learned, history, context_copy };
@@ -131,6 +144,7 @@ private:
         std::size_t request;
         DraftSourceKind source;
         std::vector<std::uint32_t> drafts;
+        bool wants_learned{false};  // learned drafts to be filled in by the round's batch request
     };
 
     [[nodiscard]] const Request& at(std::size_t request) const;

@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdint>
 #include <mutex>
 #include <stdexcept>
 
@@ -280,7 +281,8 @@ QwenModel::QwenModel(const Context& ctx, std::uint64_t seed, std::size_t layer_c
 QwenModel::~QwenModel() { q38_head_destroy(head_); }
 
 void QwenModel::forward_verify_layer_major(std::span<const std::uint32_t> tokens, DeviceTensor& final_mixed,
-                                           std::vector<GreedyStep>& greedy, MoeVerifyTimings* timings) const {
+                                           std::vector<GreedyStep>& greedy, MoeVerifyTimings* timings,
+                                           DeviceTensor* pre_mixer_streams) const {
     const std::size_t rows = tokens.size();
     if (rows < 1 || rows > 16) throw std::runtime_error("verify rows must be between 1 and 16");
     for (std::uint32_t t : tokens)
@@ -306,6 +308,12 @@ void QwenModel::forward_verify_layer_major(std::span<const std::uint32_t> tokens
         check(q38_verify_chain(hs.data(), static_cast<int32_t>(hs.size()), static_cast<uint16_t*>(h_.data()), n, eps_,
                                nullptr, moe_ws_.data(), moe_ws_.nbytes(), st),
               "verify chain");
+    }
+    if (pre_mixer_streams) {
+        *pre_mixer_streams = DeviceTensor({1, rows, geometry_.hidden}, DType::bf16);
+        check_hip(hipMemcpyAsync(pre_mixer_streams->data(), h_.data(), rows * geometry_.hidden * 2,
+                                 hipMemcpyDeviceToDevice, static_cast<hipStream_t>(st)),
+                  "pre-mixer streams");
     }
     final_mixed = DeviceTensor({1, rows, geometry_.hidden}, DType::bf16);
     check(q38_rmsnorm(static_cast<const uint16_t*>(h_.data()), n, H, eps_, static_cast<uint16_t*>(final_mixed.data()),
@@ -344,9 +352,9 @@ MtpTargetVerification verify_mtp_target_layer_major_reference(const QwenModel& m
     tokens.reserve(drafts.size() + 1);
     tokens.push_back(current_token);
     tokens.insert(tokens.end(), drafts.begin(), drafts.end());
-    DeviceTensor final_mixed;
+    DeviceTensor final_mixed, streams;
     std::vector<GreedyStep> greedy;
-    model.forward_verify_layer_major(tokens, final_mixed, greedy);
+    model.forward_verify_layer_major(tokens, final_mixed, greedy, nullptr, &streams);
     const std::size_t base = origin.token_count();
     check(q38_slot_stage(origin.slot(), static_cast<int32_t>(drafts.size()),
                          static_cast<const uint16_t*>(final_mixed.data()), model.context().stream()),
@@ -363,6 +371,10 @@ MtpTargetVerification verify_mtp_target_layer_major_reference(const QwenModel& m
         check_hip(hipMemcpyAsync(row.final_mixed.data(), static_cast<const char*>(final_mixed.data()) + i * H * 2,
                                  H * 2, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(model.context().stream())),
                   "verification row");
+        row.pre_mixer_stream = DeviceTensor({1, 1, H}, DType::bf16);
+        check_hip(hipMemcpyAsync(row.pre_mixer_stream.data(), static_cast<const char*>(streams.data()) + i * H * 2,
+                                 H * 2, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(model.context().stream())),
+                  "verification stream row");
         row.state_after = base + i + 1;
         v.rows.push_back(std::move(row));
     }
@@ -456,6 +468,177 @@ MtpRoundStep run_greedy_external_draft_round_reference(const QwenModel& target, 
     return step;
 }
 
+// ------------------------------------------------------------------ MTP draft head
+MtpDecodeState snapshot_mtp_decode_state(const MtpDecodeState& state) { return state; }
+
+QwenMtpHead::QwenMtpHead(const Context& ctx, std::uint64_t seed, std::size_t vocab, const MoeGeometry& geometry,
+                         std::size_t expert_count, std::size_t experts_per_token)
+    : ctx_(&ctx), hidden_(geometry.hidden), vocab_(vocab) {
+    q38_moe_desc d{};
+    d.hidden = static_cast<int32_t>(geometry.hidden);
+    d.inter = static_cast<int32_t>(geometry.intermediate);
+    d.experts = static_cast<int32_t>(expert_count);
+    d.top_k = static_cast<int32_t>(experts_per_token);
+    d.gu_dim = static_cast<int32_t>(geometry.gate_up_dimension);
+    d.gu_bits = static_cast<int32_t>(geometry.gate_up_bits);
+    d.down_dim = static_cast<int32_t>(geometry.down_dimension);
+    d.down_bits = static_cast<int32_t>(geometry.down_bits);
+    d.gu_group = d.hidden;
+    d.down_group = d.inter;
+    d.normalize_topk = 1;
+    d.has_shared = geometry.shared_expert ? 1 : 0;
+    check(q38_mtp_head_create_synthetic(ctx.handle(), &d, static_cast<int64_t>(vocab), seed, &head_), "MTP head");
+    ws_ = DeviceTensor({q38_mtp_workspace_size(head_, 4)}, DType::u32);
+    tokens_dev_ = DeviceTensor({4}, DType::u32);
+    streams_dev_ = DeviceTensor({4, hidden_}, DType::bf16);
+    drafts_dev_ = DeviceTensor({4, 24}, DType::u32);
+}
+QwenMtpHead::~QwenMtpHead() { q38_mtp_head_destroy(head_); }
+
+void QwenMtpHead::advance(std::size_t query_position, std::size_t rows, MtpDecodeState& state) const {
+    if (!state.position_base.has_value()) state.position_base = query_position;
+    if (query_position != *state.position_base + state.row_count)
+        throw std::runtime_error("MTP query positions must be contiguous");
+    state.row_count += rows;
+}
+
+MtpDecodeStep QwenMtpHead::forward_decode(const DeviceTensor& stream, std::uint32_t next_token,
+                                          std::size_t query_position, MtpDecodeState& state) const {
+    if (stream.shape() != std::vector<std::size_t>{1, 1, hidden_} || stream.dtype() != DType::bf16)
+        throw std::runtime_error("MTP target stream must have shape [1,1,hidden] bf16");
+    if (next_token >= vocab_) throw std::runtime_error("MTP token id is out of range");
+    MtpDecodeState next = state;
+    advance(query_position, 1, next);
+    const hipStream_t st = static_cast<hipStream_t>(ctx_->stream());
+    check_hip(hipMemcpyAsync(tokens_dev_.data(), &next_token, 4, hipMemcpyHostToDevice, st), "MTP token");
+    MtpDecodeStep out{DeviceTensor({1, 1, vocab_}, DType::f32), DeviceTensor({1, 1, hidden_}, DType::bf16)};
+    check(q38_mtp_forward_decode(head_, static_cast<const uint16_t*>(stream.data()),
+                                 static_cast<const uint32_t*>(tokens_dev_.data()), 1, static_cast<float*>(out.logits.data()),
+                                 static_cast<uint16_t*>(out.pre_mixer_stream.data()), nullptr, ws_.data(), ws_.nbytes(),
+                                 ctx_->stream()),
+          "MTP forward_decode");
+    ctx_->synchronize();
+    state = next;
+    return out;
+}
+
+std::vector<std::vector<std::uint32_t>> QwenMtpHead::draft_greedy_rows(std::span<const DeviceTensor* const> streams,
+                                                                       std::span<const std::uint32_t> tokens,
+                                                                       std::size_t depth) const {
+    const std::size_t rows = tokens.size();
+    if (rows < 1 || rows > 4 || streams.size() != rows)
+        throw std::runtime_error("MTP draft rows must be 1..4 matching streams and tokens");
+    if (depth < 1 || depth > 24) throw std::runtime_error("MTP draft depth must be between 1 and 24");
+    const hipStream_t st = static_cast<hipStream_t>(ctx_->stream());
+    for (std::size_t r = 0; r < rows; ++r) {
+        if (streams[r] == nullptr || streams[r]->numel() != hidden_ || streams[r]->dtype() != DType::bf16)
+            throw std::runtime_error("MTP target stream must have shape [1,1,hidden] bf16");
+        if (tokens[r] >= vocab_) throw std::runtime_error("MTP token id is out of range");
+        check_hip(hipMemcpyAsync(static_cast<char*>(streams_dev_.data()) + r * hidden_ * 2, streams[r]->data(),
+                                 hidden_ * 2, hipMemcpyDeviceToDevice, st),
+                  "MTP streams");
+    }
+    check_hip(hipMemcpyAsync(tokens_dev_.data(), tokens.data(), rows * 4, hipMemcpyHostToDevice, st), "MTP tokens");
+    check(q38_mtp_draft_greedy(head_, static_cast<const uint16_t*>(streams_dev_.data()),
+                               static_cast<const uint32_t*>(tokens_dev_.data()), static_cast<int32_t>(rows),
+                               static_cast<int32_t>(depth), static_cast<uint32_t*>(drafts_dev_.data()), nullptr,
+                               ws_.data(), ws_.nbytes(), ctx_->stream()),
+          "MTP draft chain");
+    std::vector<std::uint32_t> flat(rows * depth);
+    check_hip(hipMemcpyAsync(flat.data(), drafts_dev_.data(), flat.size() * 4, hipMemcpyDeviceToHost, st), "drafts");
+    ctx_->synchronize();
+    std::vector<std::vector<std::uint32_t>> out(rows);
+    for (std::size_t r = 0; r < rows; ++r) out[r].assign(flat.begin() + r * depth, flat.begin() + (r + 1) * depth);
+    return out;
+}
+
+std::vector<std::uint32_t> QwenMtpHead::draft_greedy(const DeviceTensor& stream, std::uint32_t current_token,
+                                                     std::size_t query_position, std::size_t depth,
+                                                     MtpDecodeState& state) const {
+    MtpDecodeState next = state;
+    advance(query_position, depth, next);
+    const DeviceTensor* s[1] = {&stream};
+    std::vector<std::uint32_t> d = draft_greedy_rows(s, std::span<const std::uint32_t>(&current_token, 1), depth).front();
+    state = next;
+    return d;
+}
+
+void QwenMtpHead::consume_decode(const DeviceTensor& stream, std::uint32_t next_token, std::size_t query_position,
+                                 MtpDecodeState& state) const {
+    if (stream.numel() != hidden_) throw std::runtime_error("MTP target stream must have shape [1,1,hidden] bf16");
+    if (next_token >= vocab_) throw std::runtime_error("MTP token id is out of range");
+    advance(query_position, 1, state);
+}
+
+namespace {
+// finish_greedy_mtp_round (src/mtp_runner.cpp:213-340) on the verify path.
+MtpRoundStep finish_head_round(const QwenModel& target, const QwenMtpHead& head, std::uint32_t current_token,
+                               const DeviceTensor& previous_target_stream, std::size_t query_position,
+                               std::vector<std::uint32_t> drafts, double draft_ms, MtpDecodeState head_origin,
+                               ModelDecodeState& target_state, MtpDecodeState& head_state,
+                               std::span<const std::uint32_t> stop_tokens) {
+    if (drafts.size() < 2 || drafts.size() > 24)
+        throw std::runtime_error("speculative proposal depth must be between 2 and 24");
+    if (query_position != target_state.token_count())
+        throw std::runtime_error("MTP query position must match target committed length");
+    const auto t0 = std::chrono::steady_clock::now();
+    head_state = std::move(head_origin);  // speculative head rows are never committed
+    MtpTargetVerification verification =
+        verify_mtp_target_layer_major_reference(target, current_token, drafts, target_state);
+    const auto t1 = std::chrono::steady_clock::now();
+    std::vector<std::uint32_t> target_rows;
+    for (const MtpTargetVerifyRow& row : verification.rows) target_rows.push_back(row.greedy.token);
+    const MtpGreedyDecision decision = decide_mtp_greedy(drafts, target_rows, stop_tokens);
+    DeviceTensor next_stream = verification.rows[decision.correction_row].pre_mixer_stream.share();
+    head.consume_decode(previous_target_stream, current_token, query_position, head_state);
+    for (std::size_t i = 0; i < decision.accepted; ++i)
+        head.consume_decode(verification.rows[i].pre_mixer_stream, drafts[i], query_position + i + 1, head_state);
+    commit_mtp_target_verification(std::move(verification), decision.accepted, target_state);
+    const std::size_t next_query_position = query_position + decision.accepted + 1;
+    if (target_state.token_count() != next_query_position)
+        throw std::runtime_error("MTP committed target length mismatch");
+    const auto t2 = std::chrono::steady_clock::now();
+    MtpRoundStep step;
+    step.emitted_tokens.assign(drafts.begin(), drafts.begin() + static_cast<std::ptrdiff_t>(decision.accepted));
+    step.emitted_tokens.push_back(decision.next_token);
+    step.draft_tokens = std::move(drafts);
+    step.accepted = decision.accepted;
+    step.next_current_token = decision.next_token;
+    step.next_query_position = next_query_position;
+    step.next_target_stream = std::move(next_stream);
+    step.draft_ms = draft_ms;
+    step.verify_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    step.commit_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    return step;
+}
+} // namespace
+
+MtpRoundStep run_greedy_mtp_round_reference(const QwenModel& target, const QwenMtpHead& head,
+                                            std::uint32_t current_token, const DeviceTensor& previous_target_stream,
+                                            std::size_t query_position, std::size_t draft_depth,
+                                            ModelDecodeState& target_state, MtpDecodeState& head_state,
+                                            std::span<const std::uint32_t> stop_tokens) {
+    if (draft_depth < 2 || draft_depth > 4) throw std::runtime_error("MTP draft depth must be between 2 and 4");
+    MtpDecodeState head_origin = head.snapshot_state(head_state);
+    const auto t0 = std::chrono::steady_clock::now();
+    std::vector<std::uint32_t> drafts =
+        head.draft_greedy(previous_target_stream, current_token, query_position, draft_depth, head_state);
+    const double draft_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return finish_head_round(target, head, current_token, previous_target_stream, query_position, std::move(drafts),
+                             draft_ms, std::move(head_origin), target_state, head_state, stop_tokens);
+}
+
+MtpRoundStep run_greedy_external_draft_round_reference(const QwenModel& target, const QwenMtpHead& head,
+                                                       std::uint32_t current_token,
+                                                       const DeviceTensor& previous_target_stream,
+                                                       std::size_t query_position, std::vector<std::uint32_t> drafts,
+                                                       ModelDecodeState& target_state, MtpDecodeState& head_state,
+                                                       std::span<const std::uint32_t> stop_tokens) {
+    MtpDecodeState head_origin = head.snapshot_state(head_state);
+    return finish_head_round(target, head, current_token, previous_target_stream, query_position, std::move(drafts),
+                             0.0, std::move(head_origin), target_state, head_state, stop_tokens);
+}
+
 // ------------------------------------------------------------------ batched slots
 QwenBatchVerifier::QwenBatchVerifier(const QwenModel& model, std::vector<ModelDecodeState*> slots)
     : model_(model), slots_(std::move(slots)) {
@@ -471,12 +654,14 @@ std::vector<std::vector<std::uint32_t>> QwenBatchVerifier::verify(std::span<cons
         tokens.insert(tokens.end(), e.drafts.begin(), e.drafts.end());
     }
     std::vector<GreedyStep> greedy;
-    model_.forward_verify_layer_major(tokens, final_mixed_, greedy);
+    model_.forward_verify_layer_major(tokens, final_mixed_, greedy, nullptr, &pre_mixer_);
     const std::size_t H = model_.hidden();
     std::vector<std::vector<std::uint32_t>> out;
     out.reserve(batch.size());
+    row_of_.assign(slots_.size(), SIZE_MAX);
     std::size_t row = 0;
     for (const SlotVerifyRows& e : batch) {
+        row_of_[e.slot] = row;
         const std::size_t n = e.drafts.size() + 1;
         check(q38_slot_stage(slots_[e.slot]->slot(), static_cast<int32_t>(e.drafts.size()),
                              static_cast<const uint16_t*>(final_mixed_.data()) + row * H, model_.context().stream()),
@@ -490,8 +675,52 @@ std::vector<std::vector<std::uint32_t>> QwenBatchVerifier::verify(std::span<cons
 }
 
 void QwenBatchVerifier::commit(std::size_t slot, std::size_t accepted) {
-    if (slot >= slots_.size()) throw std::runtime_error("commit names an unknown slot");
+    if (slot >= slots_.size() || slot >= row_of_.size() || row_of_[slot] == SIZE_MAX)
+        throw std::runtime_error("commit names a slot outside the last verification");
     check(q38_slot_commit(slots_[slot]->slot(), static_cast<int64_t>(accepted), model_.context().stream()), "commit");
+    const std::size_t H = model_.hidden();
+    if (committed_.size() < slots_.size()) committed_.resize(slots_.size());
+    if (committed_[slot].empty()) committed_[slot] = DeviceTensor({1, 1, H}, DType::bf16);
+    check_hip(hipMemcpyAsync(committed_[slot].data(),
+                             static_cast<const char*>(pre_mixer_.data()) + (row_of_[slot] + accepted) * H * 2, H * 2,
+                             hipMemcpyDeviceToDevice, static_cast<hipStream_t>(model_.context().stream())),
+              "committed stream row");
+}
+
+const DeviceTensor& QwenBatchVerifier::committed_stream(std::size_t slot) const {
+    static const DeviceTensor none;
+    return slot < committed_.size() ? committed_[slot] : none;
+}
+
+std::vector<std::uint32_t> MtpHeadDrafter::propose(std::size_t slot, std::uint32_t current_token, std::size_t depth) {
+    const DraftRequest r{slot, current_token, depth};
+    return propose_batch(std::span<const DraftRequest>(&r, 1)).front();
+}
+
+std::vector<std::vector<std::uint32_t>> MtpHeadDrafter::propose_batch(std::span<const DraftRequest> requests) {
+    std::vector<std::vector<std::uint32_t>> out(requests.size());
+    std::vector<std::size_t> ready;  // requests whose slot has a committed stream
+    for (std::size_t i = 0; i < requests.size(); ++i)
+        if (requests[i].depth > 0 && !verifier_.committed_stream(requests[i].slot).empty()) ready.push_back(i);
+    for (std::size_t first = 0; first < ready.size(); first += 4) {
+        const std::size_t n = std::min<std::size_t>(4, ready.size() - first);
+        std::vector<const DeviceTensor*> streams;
+        std::vector<std::uint32_t> tokens;
+        std::size_t depth = 0;
+        for (std::size_t j = 0; j < n; ++j) {
+            const DraftRequest& r = requests[ready[first + j]];
+            streams.push_back(&verifier_.committed_stream(r.slot));
+            tokens.push_back(r.current_token);
+            depth = std::max(depth, r.depth);
+        }
+        std::vector<std::vector<std::uint32_t>> d = head_.draft_greedy_rows(streams, tokens, depth);
+        for (std::size_t j = 0; j < n; ++j) {
+            std::vector<std::uint32_t>& v = d[j];
+            v.resize(std::min(v.size(), requests[ready[first + j]].depth));
+            out[ready[first + j]] = std::move(v);
+        }
+    }
+    return out;
 }
 
 } // namespace qwen38

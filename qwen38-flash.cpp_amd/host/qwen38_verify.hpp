@@ -22,6 +22,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <memory>
+#include <optional>
 #include <span>
 #include <string>
 #include <vector>
@@ -200,9 +201,13 @@ public:
 
     // Layer-major verify of the given tokens (rows 1..16): returns the final hidden rows
     // (after the final RMSNorm) and each row's greedy step.
+    // pre_mixer_streams (optional): the rows' residual streams after the last layer, before
+    // the final norm ([1, rows, H] bf16; the reference's pre_mixer_stream rows).
     void forward_verify_layer_major(std::span<const std::uint32_t> tokens, DeviceTensor& final_mixed,
-                                    std::vector<GreedyStep>& greedy,
-                                    MoeVerifyTimings* timings = nullptr) const;
+                                    std::vector<GreedyStep>& greedy, MoeVerifyTimings* timings = nullptr,
+                                    DeviceTensor* pre_mixer_streams = nullptr) const;
+    [[nodiscard]] std::uint64_t seed() const noexcept { return seed_; }
+    [[nodiscard]] const MoeGeometry& geometry() const noexcept { return geometry_; }
 
 private:
     const Context* ctx_ = nullptr;
@@ -232,7 +237,8 @@ private:
 
 struct MtpTargetVerifyRow {
     GreedyStep greedy;
-    DeviceTensor final_mixed;    // [1, 1, H] bf16 final hidden of the row
+    DeviceTensor final_mixed;       // [1, 1, H] bf16 final hidden of the row
+    DeviceTensor pre_mixer_stream;  // [1, 1, H] bf16 residual stream before the final norm
     std::size_t state_after{0};  // token count of the state after this row
 };
 
@@ -286,6 +292,8 @@ struct MtpRoundStep {
     std::size_t accepted{0};
     std::uint32_t next_current_token{0};
     std::size_t next_query_position{0};
+    DeviceTensor next_target_stream;  // pre_mixer_stream of the correction row (set by the head rounds)
+    double draft_ms{0.0};
     double verify_ms{0.0};
     double commit_ms{0.0};
 };
@@ -299,6 +307,81 @@ struct MtpRoundStep {
                                                                      ModelDecodeState& target_state,
                                                                      std::span<const std::uint32_t> stop_tokens = {});
 
+// ------------------------------------------------------------------ MTP draft head
+// MtpDecodeState (include/qwen38/mtp_head.hpp:14-18): the head's position bookkeeping. The
+// verify path's head block is a SparseMoe layer without attention, so there is no per-row
+// cache to hold; positions must still advance contiguously.
+struct MtpDecodeState {
+    std::size_t row_count{0};
+    std::optional<std::size_t> position_base;
+};
+[[nodiscard]] MtpDecodeState snapshot_mtp_decode_state(const MtpDecodeState& state);
+
+struct MtpDecodeStep {
+    DeviceTensor logits;            // [1, 1, V] float
+    DeviceTensor pre_mixer_stream;  // [1, 1, H] bf16: the step's output stream
+};
+
+// QwenMtpHead (include/qwen38/mtp_head.hpp:29-63) over q38_mtp_head (include/q38.h): the
+// seeded random-init draft head of a QwenModel with the same seed and geometry.
+class QwenMtpHead final {
+public:
+    QwenMtpHead(const Context& ctx, std::uint64_t seed, std::size_t vocab, const MoeGeometry& geometry = {},
+                std::size_t expert_count = 512, std::size_t experts_per_token = 10);
+    ~QwenMtpHead();
+    QwenMtpHead(const QwenMtpHead&) = delete;
+    QwenMtpHead& operator=(const QwenMtpHead&) = delete;
+
+    [[nodiscard]] MtpDecodeState make_state() const { return {}; }
+    [[nodiscard]] MtpDecodeState snapshot_state(const MtpDecodeState& state) const {
+        return snapshot_mtp_decode_state(state);
+    }
+    // forward_decode (src/mtp_head.cpp:454-470): target_pre_mixer_stream [1, 1, H] bf16.
+    [[nodiscard]] MtpDecodeStep forward_decode(const DeviceTensor& target_pre_mixer_stream, std::uint32_t next_token,
+                                               std::size_t query_position, MtpDecodeState& state) const;
+    // The greedy draft chain (draft_lazy_chain, src/mtp_runner.cpp:152-211): depth drafts on
+    // the device, read back once; advances state by depth rows.
+    [[nodiscard]] std::vector<std::uint32_t> draft_greedy(const DeviceTensor& target_pre_mixer_stream,
+                                                          std::uint32_t current_token, std::size_t query_position,
+                                                          std::size_t depth, MtpDecodeState& state) const;
+    // Several requests' chains in one pass per step (rows 1..4): row r starts from
+    // streams[r] ([1, 1, H] each) and tokens[r]; returns drafts[r] (depth each). No state.
+    [[nodiscard]] std::vector<std::vector<std::uint32_t>> draft_greedy_rows(std::span<const DeviceTensor* const> streams,
+                                                                            std::span<const std::uint32_t> tokens,
+                                                                            std::size_t depth) const;
+    // consume_decode (src/mtp_head.cpp): a committed row advances the head's positions.
+    void consume_decode(const DeviceTensor& target_pre_mixer_stream, std::uint32_t next_token,
+                        std::size_t query_position, MtpDecodeState& state) const;
+
+    [[nodiscard]] q38_mtp_head* handle() const noexcept { return head_; }
+    [[nodiscard]] std::size_t vocab() const noexcept { return vocab_; }
+
+private:
+    void advance(std::size_t query_position, std::size_t rows, MtpDecodeState& state) const;
+    const Context* ctx_ = nullptr;
+    q38_mtp_head* head_ = nullptr;
+    std::size_t hidden_ = 0, vocab_ = 0;
+    mutable DeviceTensor ws_, tokens_dev_, streams_dev_, drafts_dev_;
+};
+
+// run_greedy_mtp_round_reference (include/qwen38/mtp_runner.hpp:38-47,
+// src/mtp_runner.cpp:355-406): draft depth (2..4) tokens with the head from the previous
+// target stream, verify them layer-major, decide, commit; the head's state is restored to its
+// origin before verification and advanced over the committed rows.
+[[nodiscard]] MtpRoundStep run_greedy_mtp_round_reference(const QwenModel& target, const QwenMtpHead& head,
+                                                          std::uint32_t current_token,
+                                                          const DeviceTensor& previous_target_stream,
+                                                          std::size_t query_position, std::size_t draft_depth,
+                                                          ModelDecodeState& target_state, MtpDecodeState& head_state,
+                                                          std::span<const std::uint32_t> stop_tokens = {});
+// run_greedy_external_draft_round_reference with the reference's full signature
+// (include/qwen38/mtp_runner.hpp:49-60): externally proposed drafts (2..24), the head's state
+// bookkept as in the learned round.
+[[nodiscard]] MtpRoundStep run_greedy_external_draft_round_reference(
+    const QwenModel& target, const QwenMtpHead& head, std::uint32_t current_token,
+    const DeviceTensor& previous_target_stream, std::size_t query_position, std::vector<std::uint32_t> drafts,
+    ModelDecodeState& target_state, MtpDecodeState& head_state, std::span<const std::uint32_t> stop_tokens = {});
+
 // ------------------------------------------------------------------ batched slots
 // BatchVerifier on the GPU: one verification packs every slot's rows [current, drafts...]
 // into one layer-major pass of the model (up to 16 rows) and stages each slot's rows as the
@@ -311,11 +394,31 @@ public:
     void commit(std::size_t slot, std::size_t accepted) override;
     // Final hidden rows [1, rows, H] of the last verification, in batch order.
     [[nodiscard]] const DeviceTensor& last_final_mixed() const noexcept { return final_mixed_; }
+    // The pre-norm stream row [1, 1, H] of the slot's last committed checkpoint (empty before
+    // its first commit): the next draft chain's input.
+    [[nodiscard]] const DeviceTensor& committed_stream(std::size_t slot) const;
 
 private:
     const QwenModel& model_;
     std::vector<ModelDecodeState*> slots_;
-    DeviceTensor final_mixed_;
+    DeviceTensor final_mixed_, pre_mixer_;
+    std::vector<std::size_t> row_of_;      // first row of each slot in the last verification
+    std::vector<DeviceTensor> committed_;  // per slot
+};
+
+// LearnedDrafter over the draft head: each slot's chain starts from the pre-norm stream of its
+// last committed checkpoint (none before the first commit: no drafts, a serial step), and up
+// to 4 slots share each chain step.
+class MtpHeadDrafter final : public LearnedDrafter {
+public:
+    MtpHeadDrafter(const QwenMtpHead& head, const QwenBatchVerifier& verifier) : head_(head), verifier_(verifier) {}
+    [[nodiscard]] std::vector<std::uint32_t> propose(std::size_t slot, std::uint32_t current_token,
+                                                     std::size_t depth) override;
+    [[nodiscard]] std::vector<std::vector<std::uint32_t>> propose_batch(std::span<const DraftRequest> requests) override;
+
+private:
+    const QwenMtpHead& head_;
+    const QwenBatchVerifier& verifier_;
 };
 
 } // namespace qwen38

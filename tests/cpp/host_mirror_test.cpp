@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <cstring>
 #include <memory>
+#include <optional>
 #include <stdexcept>
 #include <vector>
 
@@ -200,6 +201,111 @@ static void batched_slot_tests(const qwen38::Context& ctx, const qwen38::QwenMod
                 rounds, rec.batches.size(), wide, recomputed, accepted_total);
 }
 
+// The MTP draft head and the learned-draft round (run_greedy_mtp_round_reference): drafts
+// equal the head's chain on the previous target stream and a host replay of single steps;
+// the round keeps the reference's lifecycle (target length q + accepted + 1, head positions
+// advanced over the committed rows only, next stream = the correction row's pre-norm stream);
+// bad depths and positions throw with both states intact; the batched scheduler drafts
+// with the head once a slot has a committed stream.
+static void draft_head_tests(const qwen38::Context& ctx, const qwen38::QwenModel& model) {
+    qwen38::MoeGeometry g;
+    qwen38::QwenMtpHead head(ctx, model.seed(), model.vocab(), g);
+    // a previous target stream: the pre-norm row of verifying one token
+    qwen38::DeviceTensor fm, streams;
+    std::vector<qwen38::GreedyStep> gs;
+    model.forward_verify_layer_major(std::vector<std::uint32_t>{321}, fm, gs, nullptr, &streams);
+    qwen38::DeviceTensor prev({1, 1, model.hidden()}, qwen38::DType::bf16);
+    CHECK(hipMemcpy(prev.data(), streams.data(), model.hidden() * 2, hipMemcpyDeviceToDevice) == hipSuccess);
+    std::uint32_t cur = gs[0].token;
+    // chain = replay of single steps with a host argmax
+    {
+        qwen38::MtpDecodeState st = head.make_state();
+        const auto d = head.draft_greedy(prev, cur, 50, 3, st);
+        CHECK(d.size() == 3 && st.row_count == 3 && st.position_base == std::optional<std::size_t>(50));
+        qwen38::MtpDecodeState rs = head.make_state();
+        qwen38::DeviceTensor s = prev.share();
+        std::uint32_t t = cur;
+        for (std::size_t k = 0; k < 3; ++k) {
+            qwen38::MtpDecodeStep step = head.forward_decode(s, t, 50 + k, rs);
+            const auto lg = step.logits.to_host<float>();
+            t = static_cast<std::uint32_t>(std::max_element(lg.begin(), lg.end()) - lg.begin());
+            CHECK(t == d[k]);
+            s = std::move(step.pre_mixer_stream);
+        }
+        CHECK(throws<std::runtime_error>([&] { (void)head.forward_decode(s, t, 99, rs); }));  // not contiguous
+        CHECK(rs.row_count == 3);
+    }
+    qwen38::ModelDecodeState state(model, 100, 8);
+    qwen38::MtpDecodeState hs = head.make_state();
+    std::size_t q = 100, learned_accepted = 0;
+    CHECK(throws<std::runtime_error>(
+        [&] { (void)qwen38::run_greedy_mtp_round_reference(model, head, cur, prev, q, 1, state, hs); }));
+    CHECK(state.token_count() == 100 && hs.row_count == 0);
+    // A query position that does not match the target is found after drafting, as in the
+    // reference (src/mtp_runner.cpp:227-245 run before the head state is restored): the target
+    // state is intact, the head state holds the speculative rows.
+    CHECK(throws<std::runtime_error>(
+        [&] { (void)qwen38::run_greedy_mtp_round_reference(model, head, cur, prev, q + 1, 3, state, hs); }));
+    CHECK(state.token_count() == 100 && hs.row_count == 3);
+    hs = head.make_state();
+    for (int round = 0; round < 4; ++round) {
+        const std::size_t rows_before = hs.row_count;
+        std::vector<std::uint32_t> expect;
+        {
+            const qwen38::DeviceTensor* s1[1] = {&prev};
+            expect = head.draft_greedy_rows(s1, std::span<const std::uint32_t>(&cur, 1), 3).front();
+        }
+        qwen38::MtpRoundStep step = qwen38::run_greedy_mtp_round_reference(model, head, cur, prev, q, 3, state, hs);
+        CHECK(step.draft_tokens == expect);
+        CHECK(state.token_count() == q + step.accepted + 1 && step.next_query_position == q + step.accepted + 1);
+        CHECK(hs.row_count == rows_before + step.accepted + 1);
+        CHECK(step.emitted_tokens.size() == step.accepted + 1 && step.emitted_tokens.back() == step.next_current_token);
+        // the next stream is the correction row's pre-norm stream of [cur, drafts]
+        std::vector<std::uint32_t> toks{cur};
+        toks.insert(toks.end(), expect.begin(), expect.end());
+        qwen38::DeviceTensor fm2, st2;
+        std::vector<qwen38::GreedyStep> g2;
+        model.forward_verify_layer_major(toks, fm2, g2, nullptr, &st2);
+        std::vector<std::uint16_t> a(model.hidden()), b = step.next_target_stream.to_host<std::uint16_t>();
+        CHECK(hipMemcpy(a.data(), static_cast<const char*>(st2.data()) + step.accepted * model.hidden() * 2,
+                        model.hidden() * 2, hipMemcpyDeviceToHost) == hipSuccess);
+        CHECK(a == b && g2[step.accepted].token == step.next_current_token);
+        learned_accepted += step.accepted;
+        q = step.next_query_position;
+        cur = step.next_current_token;
+        prev = std::move(step.next_target_stream);
+    }
+    // the batched scheduler with the head as its learned drafter
+    std::vector<std::unique_ptr<qwen38::ModelDecodeState>> states;
+    std::vector<qwen38::ModelDecodeState*> ptrs;
+    for (std::size_t i = 0; i < 2; ++i) {
+        states.push_back(std::make_unique<qwen38::ModelDecodeState>(model, 7, 16));
+        ptrs.push_back(states.back().get());
+    }
+    qwen38::QwenBatchVerifier verifier(model, ptrs);
+    qwen38::MtpHeadDrafter drafter(head, verifier);
+    qwen38::MtpSchedulerOptions opt;
+    opt.zero_accept_fallback_rounds = 1000;
+    opt.economic_fallback = false;
+    opt.history_mode = qwen38::HistoryDraftMode::disabled;
+    qwen38::MtpSlotScheduler sched(verifier, &drafter, opt);
+    sched.add_request(0, std::vector<std::uint32_t>{5, 6}, 7, 12);
+    sched.add_request(1, std::vector<std::uint32_t>{8, 9}, 7, 12);
+    std::size_t learned = 0, first_serial = 0;
+    for (int r = 0; r < 40 && !sched.done(); ++r)
+        for (const qwen38::SlotRound& sr : sched.step()) {
+            learned += sr.source == qwen38::DraftSourceKind::learned;
+            if (r == 0) first_serial += sr.source == qwen38::DraftSourceKind::serial;
+            if (sr.source == qwen38::DraftSourceKind::learned)
+                CHECK(sr.draft_tokens.size() == 2 || sr.draft_tokens.size() == 3);  // probe depth, then promoted
+        }
+    CHECK(sched.done() && learned > 0 && first_serial == 2);
+    for (std::size_t i = 0; i < 2; ++i)
+        CHECK(sched.tokens(i).size() == 12 && states[i]->token_count() == sched.query_position(i));
+    std::printf("draft head: ok (learned rounds accepted %zu; scheduler learned rounds %zu)\n", learned_accepted,
+                learned);
+}
+
 static void gpu_tests() {
     qwen38::Context ctx(0);
     const std::uint64_t seed = 0x51A5EED;
@@ -374,6 +480,7 @@ static void gpu_tests() {
     CHECK(step.emitted_tokens.back() == step.next_current_token);
     std::printf("gpu section: ok (accepted %zu of 3 self-drafts)\n", step.accepted);
     batched_slot_tests(ctx, model);
+    draft_head_tests(ctx, model);
 }
 
 int main(int argc, char** argv) {

@@ -2,7 +2,8 @@
 program tests/cpp/host_mirror_test.cpp, built with the library: host KATs and exception
 types on the CPU, the device section (SparseMoe vs the C ABI, verify + commit lifecycle,
 a greedy round, and the engine-side round driver with 3 requests sharing each batched
-verification, every batch recomputed row by row in the same kernel family) on the GPU."""
+verification, every batch recomputed row by row in the same kernel family; the MTP draft head,
+learned-draft rounds and the scheduler drafting with the head) on the GPU."""
 import os
 import subprocess
 
@@ -28,3 +29,4 @@ def test_gpu_section():
     out = run("--gpu")
     assert "gpu section: ok" in out, out
     assert "batched slots: ok" in out, out
+    assert "draft head: ok" in out, out
