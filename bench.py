@@ -8,7 +8,9 @@ fixture of config 2: each equals the target's argmax with probability 0.7. All w
 synthetic (seeded, random-init) and resident in HBM before timing.
 
 Also reported (in "config"): per-layer microseconds and HBM GB/s of the 48-layer MoE chain for
-M = 1..4 rows, the phase split of a profiled pass, and the roofline of the dominant kernel.
+M = 1..4 rows, the phase split of a profiled pass, the roofline of the dominant kernel, config 3
+(512 prefill rows), config 4 (mixed VQ v2, 16 rows), config 2's sampled tail (Q8 logits, Q4 draft
+logits, device rejection sampling) and a round with drafts from the MTP draft head.
 The CPU baseline is the C++ oracle (oracle/q38_oracle.cpp) timed on this host's cores on a
 bounded sample (20 passes per M = 1..4 over 5 layers, and a row slice of the Q8 head + argmax,
 on the process's thread share and on 1 thread), scaled to a round.
@@ -431,6 +433,140 @@ def main():
         torch.cuda.synchronize()
         log(f"calibration copy: 4 x {nb} bytes read and written")
 
+    # ---------------------------------------------------------------- config 2: sampled tail
+    # k = 3 at temperature 0.7: Q8 target logits of the 4 verify rows (fast pass), Q4/g64 draft
+    # logits of the 3 draft rows, then rejection sampling on the device. Each call is timed
+    # with events on the launch stream (median of 20, after a warm-up).
+    head_q4 = q38.Head(ctx, q38.Q38_HEAD_Q4G64, V, H, seed=SEED)
+    tl = torch.empty((4, V), dtype=torch.float32, device=dev)
+    dl = torch.empty((3, V), dtype=torch.float32, device=dev)
+    acc_out = torch.empty(2, dtype=torch.int64, device=dev)
+    sdrafts = torch.tensor([5, 6, 7], dtype=torch.int32, device=dev)
+    toks4 = (C.c_uint32 * 4)(*[1000, 5, 6, 7])
+    q38.check(q38.lib.q38_embed_synthetic(SEED, toks4, 4, H, h.data_ptr(), sp))
+    q38.check(q38.lib.q38_rmsnorm(h.data_ptr(), 4, H, 1e-6, hf.data_ptr(), sp))
+    rnd = [0]
+    calls = {
+        "q8_logits_4rows": lambda: q38.check(q38.lib.q38_head_logits(head.h, hf.data_ptr(), 4, tl.data_ptr(),
+                                                                     wsh.data_ptr(), wsh.numel(), sp)),
+        "q4_draft_logits_3rows": lambda: q38.check(q38.lib.q38_head_logits(head_q4.h, hf.data_ptr(), 3,
+                                                                           dl.data_ptr(), None, 0, sp)),
+        "k_accept_sampled": lambda: q38.check(q38.lib.q38_mtp_accept_sampled(
+            tl.data_ptr(), dl.data_ptr(), sdrafts.data_ptr(), 3, V, 0.7, SEED, 0, rnd[0], acc_out.data_ptr(), sp)),
+    }
+    samp_us = {}
+    for name, fn in calls.items():
+        fn()
+        ts = []
+        for r in range(20):
+            rnd[0] = r
+            ev0.record(stream)
+            fn()
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            ts.append(1e3 * ev0.elapsed_time(ev1))
+        samp_us[name] = float(np.median(ts))
+    q4_bytes = V * H // 2 + V * (H // 64) * 2
+    q8_bytes = V * H + V * 2
+    sampled_cfg = {
+        "temperature": 0.7, "us": samp_us, "total_us": sum(samp_us.values()),
+        "q4_draft_head_gbps": q4_bytes / (samp_us["q4_draft_logits_3rows"] * 1e-6) / 1e9,
+        "q4_draft_head_hbm_frac": q4_bytes / (samp_us["q4_draft_logits_3rows"] * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "q8_logits_gbps": q8_bytes / (samp_us["q8_logits_4rows"] * 1e-6) / 1e9,
+        "accept_input_bytes": 7 * V * 4,
+        "accept_gbps_one_pass": 7 * V * 4 / (samp_us["k_accept_sampled"] * 1e-6) / 1e9,
+    }
+    log("config 2 sampled tail (us): " + ", ".join(f"{k}={v:.1f}" for k, v in samp_us.items()))
+    head_q4.close()
+
+    # ---------------------------------------------------------------- config 2: learned drafts
+    # The MTP draft head (seeded random-init, its block = layer 48) drafts 3 tokens on the
+    # device from the previous round's correction-row stream; the drafts go straight into the
+    # verify rows inside the same graph (one host synchronisation per round). With random
+    # weights the drafts are uncorrelated with the target, so acceptance is near 0: this leg
+    # measures the cost of drafting + verifying, not a speed-up.
+    mtp = q38.MtpHead(ctx, d, V, SEED)
+    wsd = torch.empty(mtp.workspace_size(1), dtype=torch.uint8, device=dev)
+    sbuf = torch.empty((1, H), dtype=torch.int16, device=dev)
+    ddev = torch.empty(3, dtype=torch.int32, device=dev)
+    d_host = torch.empty(3, dtype=torch.int32, pin_memory=True)
+
+    def draft_chain(sp_):
+        q38.check(q38.lib.q38_mtp_draft_greedy(mtp.h, sbuf.data_ptr(), tok_dev.data_ptr(), 1, 3, ddev.data_ptr(),
+                                               None, wsd.data_ptr(), wsd.numel(), sp_))
+
+    def learned_device(sp_):
+        tok_dev[:1].copy_(tok_host[:1], non_blocking=True)
+        draft_chain(sp_)
+        tok_dev[1:4].copy_(ddev)
+        q38.check(q38.lib.q38_embed_synthetic_dev(SEED, tok_dev.data_ptr(), 4, H, h.data_ptr(), sp_))
+        q38.check(q38.lib.q38_verify_chain(larr, len(layers), h.data_ptr(), 4, 1e-6, None, ws.data_ptr(),
+                                           ws.numel(), sp_))
+        q38.check(q38.lib.q38_rmsnorm(h.data_ptr(), 4, H, 1e-6, hf.data_ptr(), sp_))
+        q38.check(q38.lib.q38_head_greedy(head.h, hf.data_ptr(), 4, am.data_ptr(), lg.data_ptr(), wsh.data_ptr(),
+                                          wsh.numel(), sp_))
+        am_host[:4].copy_(am[:4], non_blocking=True)
+        d_host.copy_(ddev, non_blocking=True)
+
+    gl = gd = None
+    if not args.no_graph:
+        learned_device(sp)
+        torch.cuda.synchronize()
+        gl, gd = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gl):
+            learned_device(torch.cuda.current_stream().cuda_stream)
+        with torch.cuda.graph(gd):
+            draft_chain(torch.cuda.current_stream().cuda_stream)
+    cur_l = 1000
+    tgt0 = verify([cur_l])
+    sbuf.copy_(h[:1])
+    cur_l = tgt0[0]
+
+    def learned_round(cur):
+        tok_host[0] = cur
+        if gl is not None:
+            gl.replay()
+        else:
+            learned_device(sp)
+        stream.synchronize()
+        drafts = [int(v) for v in d_host.tolist()]
+        target = [int(v) for v in am_host[:4].tolist()]
+        dec = q38.GreedyDecision()
+        q38.check(q38.lib.q38_mtp_decide_greedy((C.c_uint32 * 3)(*drafts), 3, (C.c_uint32 * 4)(*target), 4, None,
+                                                0, C.byref(dec)))
+        q38.check(q38.lib.q38_slot_stage(slot, 3, h.data_ptr(), sp))
+        q38.check(q38.lib.q38_slot_commit(slot, dec.accepted, sp))
+        sbuf.copy_(h[dec.accepted:dec.accepted + 1])  # the correction row's stream drafts next
+        return dec.accepted, dec.next_token
+
+    for _ in range(args.warmup):
+        _, cur_l = learned_round(cur_l)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    l_tokens = 0
+    for _ in range(args.steps):
+        a, cur_l = learned_round(cur_l)
+        l_tokens += a + 1
+    torch.cuda.synchronize()
+    l_elapsed = time.perf_counter() - t0
+    dts = []
+    for _ in range(20):
+        ev0.record(stream)
+        if gd is not None:
+            gd.replay()
+        else:
+            draft_chain(sp)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        dts.append(1e3 * ev0.elapsed_time(ev1))
+    learned_cfg = {"depth": 3, "draft_chain_us": float(np.median(dts)),
+                   "draft_chain_bytes": 3 * (q4_bytes + 2 * (H * H + H * 2)), "round_ms": 1e3 * l_elapsed / args.steps,
+                   "tok_s": l_tokens / l_elapsed, "mean_accepted": l_tokens / args.steps - 1,
+                   "note": "seeded random-init draft head: drafts are uncorrelated with the target"}
+    log(f"config 2 learned drafts: draft chain {learned_cfg['draft_chain_us']:.1f} us (depth 3), round "
+        f"{learned_cfg['round_ms']:.3f} ms, mean accepted {learned_cfg['mean_accepted']:.2f}")
+    mtp.close()
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu_baseline:
@@ -466,6 +602,8 @@ def main():
             "algorithmic_bytes_per_launch_m4": {k.split()[0]: v[1] for k, v in kernels.items()},
             "config3_prefill": prefill_cfg,
             "config4_mixed": mixed_cfg,
+            "config2_sampled": sampled_cfg,
+            "config2_learned_drafts": learned_cfg,
         },
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "launch_avg_us": dom_us,
