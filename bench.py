@@ -446,13 +446,15 @@ def main():
     q38.check(q38.lib.q38_embed_synthetic(SEED, toks4, 4, H, h.data_ptr(), sp))
     q38.check(q38.lib.q38_rmsnorm(h.data_ptr(), 4, H, 1e-6, hf.data_ptr(), sp))
     rnd = [0]
+    wsa = torch.empty(q38.lib.q38_mtp_accept_workspace_size(3, V), dtype=torch.uint8, device=dev)
     calls = {
         "q8_logits_4rows": lambda: q38.check(q38.lib.q38_head_logits(head.h, hf.data_ptr(), 4, tl.data_ptr(),
                                                                      wsh.data_ptr(), wsh.numel(), sp)),
         "q4_draft_logits_3rows": lambda: q38.check(q38.lib.q38_head_logits(head_q4.h, hf.data_ptr(), 3,
                                                                            dl.data_ptr(), None, 0, sp)),
-        "k_accept_sampled": lambda: q38.check(q38.lib.q38_mtp_accept_sampled(
-            tl.data_ptr(), dl.data_ptr(), sdrafts.data_ptr(), 3, V, 0.7, SEED, 0, rnd[0], acc_out.data_ptr(), sp)),
+        "accept_sampled": lambda: q38.check(q38.lib.q38_mtp_accept_sampled(
+            tl.data_ptr(), dl.data_ptr(), sdrafts.data_ptr(), 3, V, 0.7, SEED, 0, rnd[0], acc_out.data_ptr(),
+            wsa.data_ptr(), wsa.numel(), sp)),
     }
     samp_us = {}
     for name, fn in calls.items():
@@ -474,7 +476,7 @@ def main():
         "q4_draft_head_hbm_frac": q4_bytes / (samp_us["q4_draft_logits_3rows"] * 1e-6) / 1e9 / HBM_PEAK_GBS,
         "q8_logits_gbps": q8_bytes / (samp_us["q8_logits_4rows"] * 1e-6) / 1e9,
         "accept_input_bytes": 7 * V * 4,
-        "accept_gbps_one_pass": 7 * V * 4 / (samp_us["k_accept_sampled"] * 1e-6) / 1e9,
+        "accept_gbps_one_pass": 7 * V * 4 / (samp_us["accept_sampled"] * 1e-6) / 1e9,
     }
     log("config 2 sampled tail (us): " + ", ".join(f"{k}={v:.1f}" for k, v in samp_us.items()))
     head_q4.close()

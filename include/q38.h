@@ -340,10 +340,13 @@ int q38_plan_mtp_commit(uint64_t round_offset, uint64_t drafted, uint64_t accept
  * bypasses MTP when sampling: src/native_engine.cpp:943-945). target_logits [k+1, V],
  * draft_logits [k, V] (device float), drafts (device u32 [k]); uniforms from
  * Philox4x32-10 keyed by (seed; position, round, slot). out: device int64 [2] =
- * {accepted, next_token}. */
+ * {accepted, next_token}. Four launches spread over the chip, no host synchronisation;
+ * workspace: device, q38_mtp_accept_workspace_size(k, vocab) bytes. */
 int q38_mtp_accept_sampled(const float* target_logits, const float* draft_logits, const uint32_t* drafts,
                            int32_t k, int64_t vocab, float temperature, uint64_t seed, uint64_t slot,
-                           uint64_t round, int64_t* out, void* stream);
+                           uint64_t round, int64_t* out, void* workspace, size_t workspace_bytes, void* stream);
+/* Device workspace bytes of q38_mtp_accept_sampled (k 1..24); 0 for invalid sizes. */
+size_t q38_mtp_accept_workspace_size(int32_t k, int64_t vocab);
 /* Philox4x32-10 (host), for checking the device stream. */
 void q38_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 

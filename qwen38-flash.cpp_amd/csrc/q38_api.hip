@@ -1267,13 +1267,20 @@ void q38_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t ou
     philox4x32_10(ctr, key, out);
 }
 
+size_t q38_mtp_accept_workspace_size(int32_t k, int64_t vocab) {
+    if (k < 1 || k > 24 || vocab < 1 || vocab > (int64_t{1} << 31) - 2) return 0;
+    return accept_sampled_workspace(k, vocab);
+}
+
 int q38_mtp_accept_sampled(const float* tl, const float* dl, const uint32_t* drafts, int32_t k, int64_t vocab,
-                           float temperature, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out,
-                           void* stream) {
+                           float temperature, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out, void* ws,
+                           size_t ws_bytes, void* stream) {
     if (!tl || !dl || !drafts || !out) return fail(Q38_EINVAL, "q38_mtp_accept_sampled: null argument");
-    if (k < 1 || k > 24 || vocab < 1) return fail(Q38_EINVAL, "q38_mtp_accept_sampled: bad sizes");
+    if (k < 1 || k > 24 || vocab < 1 || vocab > (int64_t{1} << 31) - 2)
+        return fail(Q38_EINVAL, "q38_mtp_accept_sampled: bad sizes");
     if (!(temperature > 0.0f)) return fail(Q38_EINVAL, "temperature must be positive");
-    Q38_HIP(launch_accept_sampled(tl, dl, drafts, k, vocab, temperature, seed, slot, round, out,
+    if (!ws || ws_bytes < accept_sampled_workspace(k, vocab)) return fail(Q38_ESPACE, "workspace too small");
+    Q38_HIP(launch_accept_sampled(tl, dl, drafts, k, vocab, temperature, seed, slot, round, out, ws,
                                   static_cast<hipStream_t>(stream)));
     return Q38_OK;
 }

@@ -273,47 +273,125 @@ __global__ void k_head_final(int M, HeadWork w, uint32_t* __restrict__ argmax, f
 }
 
 // Q4/g64 draft head logits: signed nibbles (low first), u = nibble ^ 8 = w + 8, bias
-// removed per 64-column group with the group's column sum of h.
+// removed per 32-column lane span with the span's sum of h. The products run on
+// v_dot2_f32_f16: each nibble becomes the fp16 value 1 + u/16 (exact; products with the fp16
+// copy of h are exact in fp32), so sum w h = 16 sum (1 + u/16) h - 24 sum h. Lane l owns columns
+// [32l, 32l + 32) (half a scale group) of every row; a wave takes 8 vocab rows per step and
+// has the next step's 8 rows (weights and scales) in flight while it computes. The 8 x M
+// per-lane partials are reduce-scattered across the wave (each butterfly step halves the
+// values a lane keeps) instead of one full butterfly per (row, request).
+// Reduce-scatter over the wave with DPP / permlane exchanges: at offset O a lane keeps the
+// half of its KEEP values selected by (lane & O) and adds the partner's copy of that half;
+// once one value is left, plain butterfly steps finish the sum.
+template <int O, int KEEP, int NP>
+__device__ __forceinline__ void reduce_scatter(float (&part)[NP]) {
+    if constexpr (O >= 1) {
+        if constexpr (KEEP > 1) {
+            constexpr int half = KEEP / 2;
+            const bool up = (threadIdx.x & O) != 0;
+#pragma unroll
+            for (int i = 0; i < half; ++i) {
+                const float mine = up ? part[half + i] : part[i];
+                const float send = up ? part[i] : part[half + i];
+                part[i] = mine + xor_lane_f<O>(send);
+            }
+            reduce_scatter<O / 2, half, NP>(part);
+        } else {
+            part[0] += xor_lane_f<O>(part[0]);
+            reduce_scatter<O / 2, 1, NP>(part);
+        }
+    }
+}
+
 template <int M>
 __global__ __launch_bounds__(256) void k_head_q4(HeadDev hd, const uint16_t* __restrict__ h,
                                                  float* __restrict__ out_logits) {
-    constexpr int CPL = 32;  // H = 2048: lane l owns columns [32l, 32l+32) = half a group
+    constexpr int CPL = 32, RPS = 8;            // columns per lane, rows per step
+    constexpr int N = RPS * M;                  // partials per lane per step
+    constexpr int NP = N <= 8 ? 8 : N <= 16 ? 16 : 32;  // padded to a power of two
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
     const int lane = threadIdx.x & 63;
-    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int nw = gridDim.x * 4;
+    const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
     const int H = hd.H, G = H / 64;
-    float hr[M][CPL];
+    const int64_t V = hd.V;
+    // h as fp16 pairs in the order the nibbles are paired below: word i of the lane's 16
+    // bytes holds columns 8i..8i+7 (nibble n = column 8i + n); pair k = columns (8i+k, 8i+k+4).
+    half2_t hp[M][16];
     float hs[M];
 #pragma unroll
     for (int r = 0; r < M; ++r) {
+        float t[CPL];
         hs[r] = 0.0f;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            hr[r][c] = bf2f(h[static_cast<size_t>(r) * H + CPL * lane + c]);
-            hs[r] += hr[r][c];
+            t[c] = bf2f(h[static_cast<size_t>(r) * H + CPL * lane + c]);
+            hs[r] += t[c];
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                hp[r][4 * i + k] = half2_t{static_cast<_Float16>(t[8 * i + k]), static_cast<_Float16>(t[8 * i + k + 4])};
     }
-    for (int64_t v = gw; v < hd.V; v += nw) {
-        const uint4 q = reinterpret_cast<const uint4*>(hd.w + v * (H / 2) + (CPL / 2) * lane)[0];
-        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
-        float acc[M];
+    uint4 wq[RPS], wn[RPS];
+    uint16_t sq[RPS], sn[RPS];
+    auto load = [&](int64_t base, uint4 (&w)[RPS], uint16_t (&sc)[RPS]) {
 #pragma unroll
-        for (int r = 0; r < M; ++r) acc[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t b = wd[i] ^ 0x88888888u;
-#pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                const float u = static_cast<float>((b >> (4 * n)) & 0xfu);
-#pragma unroll
-                for (int r = 0; r < M; ++r) acc[r] = fmaf(u, hr[r][8 * i + n], acc[r]);
-            }
+        for (int j = 0; j < RPS; ++j) {
+            const int64_t v = base + j < V ? base + j : V - 1;  // a ragged step reads a valid row
+            w[j] = reinterpret_cast<const uint4*>(hd.w + v * (H / 2) + (CPL / 2) * lane)[0];
+            sc[j] = hd.scales[v * G + lane / 2];
         }
-        const float sc = h2f(hd.scales[v * G + lane / 2]);
+    };
+    int64_t base = gw * RPS;
+    if (base < V) load(base, wq, sq);
+    for (; base < V; base += nw * RPS) {
+        if (base + nw * RPS < V) load(base + nw * RPS, wn, sn);
+        float part[NP];
 #pragma unroll
-        for (int r = 0; r < M; ++r) {
-            const float s = wave_sum_xor(sc * fmaf(-8.0f, hs[r], acc[r]));
-            if (lane == 0) out_logits[static_cast<size_t>(r) * hd.V + v] = s;
+        for (int i = 0; i < NP; ++i) part[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < RPS; ++j) {
+            const uint32_t wd[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
+            float acc[M];
+#pragma unroll
+            for (int r = 0; r < M; ++r) acc[r] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t bw = wd[i] ^ 0x88888888u;  // u = w + 8 in 0..15
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    // nibbles k and k + 4 into bits 6..9 of the two fp16 halves: 1 + u / 16
+                    const uint32_t sh = k < 2 ? bw << (6 - 4 * k) : bw >> (4 * k - 6);
+                    const uint32_t pr = (sh & 0x03C003C0u) | 0x3C003C00u;
+                    const half2_t wv = __builtin_bit_cast(half2_t, pr);
+#pragma unroll
+                    for (int r = 0; r < M; ++r) acc[r] = __builtin_amdgcn_fdot2(wv, hp[r][4 * i + k], acc[r], false);
+                }
+            }
+            // sum (w) h = sum (u - 8) h = 16 sum (1 + u/16) h - 24 sum h
+            const float sc = h2f(sq[j]);
+#pragma unroll
+            for (int r = 0; r < M; ++r) part[j * M + r] = sc * fmaf(16.0f, acc[r], -24.0f * hs[r]);
+        }
+        reduce_scatter<32, NP, NP>(part);
+        // the value index a lane holds: its bits of the halving offsets, high offset first
+        int idx = 0;
+        {
+            int bitv = NP / 2;
+            for (int o = 32; bitv >= 1; o >>= 1, bitv >>= 1)
+                if (lane & o) idx += bitv;
+        }
+        const int lsb = 64 / NP;  // lanes sharing an index: the low log2(64 / NP) lane bits
+        if ((lane & (lsb - 1)) == 0 && idx < N) {
+            const int j = idx / M, r = idx % M;
+            if (base + j < V) out_logits[static_cast<size_t>(r) * V + base + j] = part[0];
+        }
+#pragma unroll
+        for (int j = 0; j < RPS; ++j) {
+            wq[j] = wn[j];
+            sq[j] = sn[j];
         }
     }
 }
@@ -355,120 +433,236 @@ __global__ void k_scale_absmax(const uint16_t* __restrict__ s, int64_t n, float*
 }
 
 // ---------------------------------------------------------------- rejection sampling
-// One workgroup. Row statistics are block reductions in a fixed order; the residual /
-// bonus draw is an inverse CDF over the vocab in index order (chunked prefix sums).
+// Spread over the chip in four launches (graph-capturable, no host round trip):
+//   k_samp_stats   (chunks x rows) workgroups: online softmax partials (max, sum exp) of each
+//                  256-thread chunk of every target row 0..k and draft row 0..k-1;
+//   k_samp_decide  one wave: each row's (max, sum) from its partials in a fixed tree order,
+//                  then the accept test of drafts 0..k-1 in order (u * q(d) < p(d));
+//   k_samp_mass    one workgroup per chunk: the residual mass max(0, p - q) of the first
+//                  rejected position (or p of the bonus row) per chunk, and the chunk's last
+//                  positive index;
+//   k_samp_draw    one workgroup: the chunk where the inclusive prefix first exceeds v * total,
+//                  then the index inside it (thread sub-ranges in index order); when rounding
+//                  leaves no crossing, the last index with positive mass.
+// Every sum runs in a fixed order, so a call is deterministic.
 namespace {
-constexpr int kSampThreads = 1024;
+constexpr int kSampChunks = 64;  // chunks per row (fewer for small vocabularies)
 
-__device__ float block_reduce(float v, float* sh, bool is_max) {
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    if (is_max) v = wave_max(v);
-    else v = wave_sum_xor(v);
+struct SampCtl {
+    int32_t row;       // first rejected position, or k (all accepted: the bonus row)
+    float v;           // the residual draw's uniform
+    float pm, ps;      // target row stats (max, sum exp) of `row`
+    float qm, qs;      // draft row stats (row < k)
+};
+
+__device__ __forceinline__ void softmax_merge(float& m, float& s, float m2, float s2, float invT) {
+    if (m2 == -INFINITY) return;
+    if (m == -INFINITY) { m = m2; s = s2; return; }
+    if (m2 > m) {
+        s = s * expf((m - m2) * invT) + s2;
+        m = m2;
+    } else {
+        s += s2 * expf((m2 - m) * invT);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_samp_stats(const float* __restrict__ tl, const float* __restrict__ dl, int k,
+                                                    int64_t V, int64_t cs, float invT, float2* __restrict__ part) {
+    __shared__ float2 sh[4];
+    const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+    const float* l = r <= k ? tl + static_cast<int64_t>(r) * V : dl + static_cast<int64_t>(r - k - 1) * V;
+    const int64_t a = static_cast<int64_t>(c) * cs, b = a + cs < V ? a + cs : V;
+    float m = -INFINITY, s = 0.0f;
+    for (int64_t x = a + tid; x < b; x += 256) {
+        const float v = l[x];
+        if (!(v > -INFINITY)) continue;  // a -inf logit has probability 0
+        if (v > m) {
+            s = (m == -INFINITY ? 0.0f : s * expf((m - v) * invT)) + 1.0f;
+            m = v;
+        } else {
+            s += expf((v - m) * invT);
+        }
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float m2 = __shfl_xor(m, off, kWave), s2 = __shfl_xor(s, off, kWave);
+        softmax_merge(m, s, m2, s2, invT);
+    }
+    if ((tid & 63) == 0) sh[tid >> 6] = make_float2(m, s);
     __syncthreads();
-    if (lane == 0) sh[wv] = v;
+    if (tid == 0) {
+        float M = sh[0].x, S = sh[0].y;
+        for (int w = 1; w < 4; ++w) softmax_merge(M, S, sh[w].x, sh[w].y, invT);
+        part[static_cast<size_t>(r) * gridDim.x + c] = make_float2(M, S);
+    }
+}
+
+__global__ __launch_bounds__(64) void k_samp_decide(const float* __restrict__ tl, const float* __restrict__ dl,
+                                                    const uint32_t* __restrict__ drafts, int k, int64_t V, int nc,
+                                                    float invT, uint64_t seed, uint64_t slot, uint64_t round,
+                                                    const float2* __restrict__ part, SampCtl* __restrict__ ctl) {
+    __shared__ float2 st[2 * 24 + 1];
+    const int lane = threadIdx.x;
+    for (int r = 0; r < 2 * k + 1; ++r) {
+        float m = -INFINITY, s = 0.0f;
+        if (lane < nc) {
+            const float2 p = part[static_cast<size_t>(r) * nc + lane];
+            m = p.x;
+            s = p.y;
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float m2 = __shfl_xor(m, off, kWave), s2 = __shfl_xor(s, off, kWave);
+            softmax_merge(m, s, m2, s2, invT);
+        }
+        if (lane == 0) st[r] = make_float2(m, s);
+    }
     __syncthreads();
-    float t = sh[0];
-    for (int i = 1; i < kSampThreads / 64; ++i) t = is_max ? fmaxf(t, sh[i]) : t + sh[i];
+    if (lane != 0) return;
+    for (int i = 0; i <= k; ++i) {
+        float u, v;
+        round_uniforms(seed, slot, round, static_cast<uint32_t>(i), &u, &v);
+        const float2 ps = st[i];
+        if (i == k) {
+            *ctl = SampCtl{k, v, ps.x, ps.y, 0.0f, 1.0f};
+            return;
+        }
+        const float2 qs = st[k + 1 + i];
+        const uint32_t d = drafts[i];
+        // an out-of-vocabulary draft is rejected (never read out of bounds)
+        const float pd = d < V ? expf((tl[static_cast<int64_t>(i) * V + d] - ps.x) * invT) / ps.y : 0.0f;
+        const float qd = d < V ? expf((dl[static_cast<int64_t>(i) * V + d] - qs.x) * invT) / qs.y : 1.0f;
+        if (u * qd < pd) continue;
+        *ctl = SampCtl{i, v, ps.x, ps.y, qs.x, qs.y};
+        return;
+    }
+}
+
+// Residual weight of index x under the control block's row.
+__device__ __forceinline__ float samp_weight(const float* tl, const float* dl, int k, int64_t V, const SampCtl& c,
+                                             float invT, int64_t x) {
+    const float p = expf((tl[static_cast<int64_t>(c.row) * V + x] - c.pm) * invT) / c.ps;
+    if (c.row == k) return p;
+    const float q = expf((dl[static_cast<int64_t>(c.row) * V + x] - c.qm) * invT) / c.qs;
+    return fmaxf(0.0f, p - q);
+}
+
+// Thread t of a chunk owns the contiguous sub-range [a + t * sub, a + (t + 1) * sub).
+__device__ __forceinline__ void samp_range(int64_t a, int64_t b, int64_t sub, int t, int64_t& x0, int64_t& x1) {
+    x0 = a + t * sub < b ? a + t * sub : b;
+    x1 = x0 + sub < b ? x0 + sub : b;
+}
+
+__device__ float block_sum_ordered(float v, float* sh) {
+    v = wave_sum_xor(v);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = (sh[0] + sh[1]) + (sh[2] + sh[3]);
     __syncthreads();
     return t;
 }
 
-struct RowStat { float mx, sum; };
-__device__ RowStat row_stat(const float* l, int64_t V, float invT, float* sh) {
-    float m = -INFINITY;
-    for (int64_t i = threadIdx.x; i < V; i += kSampThreads) m = fmaxf(m, l[i]);
-    m = block_reduce(m, sh, true);
+__global__ __launch_bounds__(256) void k_samp_mass(const float* __restrict__ tl, const float* __restrict__ dl, int k,
+                                                   int64_t V, int64_t cs, float invT, const SampCtl* __restrict__ ctl,
+                                                   float* __restrict__ csum, int64_t* __restrict__ clast) {
+    __shared__ float sh[4];
+    __shared__ unsigned long long last;
+    const SampCtl c = *ctl;
+    const int64_t a = static_cast<int64_t>(blockIdx.x) * cs, b = a + cs < V ? a + cs : V;
+    const int64_t sub = (cs + 255) / 256;
+    int64_t x0, x1;
+    samp_range(a, b, sub, threadIdx.x, x0, x1);
+    if (threadIdx.x == 0) last = 0ull;
+    __syncthreads();
     float s = 0.0f;
-    for (int64_t i = threadIdx.x; i < V; i += kSampThreads) s += expf((l[i] - m) * invT);
-    s = block_reduce(s, sh, false);
-    return {m, s};
+    int64_t lp = -1;
+    for (int64_t x = x0; x < x1; ++x) {
+        const float w = samp_weight(tl, dl, k, V, c, invT, x);
+        s += w;
+        if (w > 0.0f) lp = x;
+    }
+    if (lp >= 0) atomicMax(&last, static_cast<unsigned long long>(lp + 1));
+    const float t = block_sum_ordered(s, sh);
+    if (threadIdx.x == 0) {
+        csum[blockIdx.x] = t;
+        clast[blockIdx.x] = static_cast<int64_t>(last) - 1;
+    }
 }
 
-// weight(x) = max(0, p(x) - q(x)) when dl != null, else p(x). Returns the smallest x whose
-// inclusive prefix sum exceeds v * total (thread chunks in index order); when rounding
-// leaves no crossing, the last x with positive weight.
-__device__ int64_t draw_cdf(const float* tl, RowStat ps, const float* dl, RowStat qs, int64_t V, float invT,
-                            float v, float* sh, unsigned long long* found, unsigned long long* lastp) {
+__global__ __launch_bounds__(256) void k_samp_draw(const float* __restrict__ tl, const float* __restrict__ dl, int k,
+                                                   int64_t V, int64_t cs, int nc, float invT,
+                                                   const SampCtl* __restrict__ ctl, const float* __restrict__ csum,
+                                                   const int64_t* __restrict__ clast, int64_t* __restrict__ out) {
+    __shared__ float pre[256];
+    __shared__ int chunk;
+    __shared__ float base, target;
+    __shared__ unsigned long long found;
+    const SampCtl c = *ctl;
     const int tid = threadIdx.x;
-    const int64_t chunk = (V + kSampThreads - 1) / kSampThreads;
-    const int64_t a = tid * chunk < V ? tid * chunk : V;
-    const int64_t b = a + chunk < V ? a + chunk : V;
-    auto wgt = [&](int64_t x) {
-        const float p = expf((tl[x] - ps.mx) * invT) / ps.sum;
-        if (!dl) return p;
-        const float q = expf((dl[x] - qs.mx) * invT) / qs.sum;
-        return fmaxf(0.0f, p - q);
-    };
-    float s = 0.0f;
-    int64_t last = -1;
-    for (int64_t x = a; x < b; ++x) {
-        const float wv = wgt(x);
-        s += wv;
-        if (wv > 0.0f) last = x;
-    }
-    if (tid == 0) { *found = ~0ull; *lastp = 0ull; }
-    sh[tid] = s;
-    __syncthreads();
-    for (int off = 1; off < kSampThreads; off <<= 1) {
-        const float t = tid >= off ? sh[tid - off] : 0.0f;
-        __syncthreads();
-        sh[tid] += t;
-        __syncthreads();
-    }
-    const float incl = sh[tid];
-    const float total = sh[kSampThreads - 1];
-    const float excl = incl - s;
-    const float target = v * total;
-    if (last >= 0) atomicMax(lastp, static_cast<unsigned long long>(last + 1));
-    if (s > 0.0f && excl <= target && target < incl) {
-        float c = excl;
-        int64_t pick = last;
-        for (int64_t x = a; x < b; ++x) {
-            const float wv = wgt(x);
-            c += wv;
-            if (c > target && wv > 0.0f) { pick = x; break; }
+    if (tid == 0) {
+        float total = 0.0f;
+        for (int i = 0; i < nc; ++i) total += csum[i];
+        const float tg = c.v * total;
+        float run = 0.0f;
+        int ch = -1;
+        for (int i = 0; i < nc; ++i) {
+            if (csum[i] > 0.0f && run <= tg && tg < run + csum[i]) {
+                ch = i;
+                break;
+            }
+            run += csum[i];
         }
-        atomicMin(found, static_cast<unsigned long long>(pick));
+        chunk = ch;
+        base = run;
+        target = tg;
+        found = ~0ull;
     }
     __syncthreads();
-    const unsigned long long f = *found, l = *lastp;
-    __syncthreads();
-    if (f != ~0ull) return static_cast<int64_t>(f);
-    return l ? static_cast<int64_t>(l - 1) : 0;
+    int64_t pick = -1;
+    if (chunk >= 0) {
+        const int64_t a = static_cast<int64_t>(chunk) * cs, b = a + cs < V ? a + cs : V;
+        const int64_t sub = (cs + 255) / 256;
+        int64_t x0, x1;
+        samp_range(a, b, sub, tid, x0, x1);
+        float s = 0.0f;
+        for (int64_t x = x0; x < x1; ++x) s += samp_weight(tl, dl, k, V, c, invT, x);
+        pre[tid] = s;
+        __syncthreads();
+        if (tid == 0) {  // exclusive prefix over the threads, in index order
+            float run = base;
+            for (int t = 0; t < 256; ++t) {
+                const float w = pre[t];
+                pre[t] = run;
+                run += w;
+            }
+        }
+        __syncthreads();
+        const float excl = pre[tid];
+        if (s > 0.0f && excl <= target && target < excl + s) {
+            float run = excl;
+            int64_t p = -1;
+            for (int64_t x = x0; x < x1; ++x) {
+                const float w = samp_weight(tl, dl, k, V, c, invT, x);
+                run += w;
+                if (w > 0.0f) p = x;  // the last positive so far: the fallback of this range
+                if (run > target && w > 0.0f) break;
+            }
+            if (p >= 0) atomicMin(&found, static_cast<unsigned long long>(p));
+        }
+        __syncthreads();
+        if (found != ~0ull) pick = static_cast<int64_t>(found);
+    }
+    if (tid == 0) {
+        if (pick < 0) {  // no crossing under rounding: the last index with positive mass
+            int64_t lp = -1;
+            for (int i = 0; i < nc; ++i) lp = clast[i] > lp ? clast[i] : lp;
+            pick = lp < 0 ? 0 : lp;
+        }
+        out[0] = c.row;
+        out[1] = pick;
+    }
 }
 } // namespace
-
-__global__ __launch_bounds__(kSampThreads) void k_accept_sampled(const float* __restrict__ tl,
-                                                                const float* __restrict__ dl,
-                                                                const uint32_t* __restrict__ drafts, int k, int64_t V,
-                                                                float T, uint64_t seed, uint64_t slot, uint64_t round,
-                                                                int64_t* __restrict__ out) {
-    __shared__ float sh[kSampThreads];
-    __shared__ unsigned long long found, lastp;
-    const float invT = 1.0f / T;
-    for (int i = 0; i < k; ++i) {
-        const float* ti = tl + static_cast<size_t>(i) * V;
-        const float* di = dl + static_cast<size_t>(i) * V;
-        const RowStat ps = row_stat(ti, V, invT, sh);
-        const RowStat qs = row_stat(di, V, invT, sh);
-        float u, v;
-        round_uniforms(seed, slot, round, static_cast<uint32_t>(i), &u, &v);
-        const uint32_t d = drafts[i];
-        // an out-of-vocabulary draft is rejected (never read out of bounds)
-        const float pd = d < V ? expf((ti[d] - ps.mx) * invT) / ps.sum : 0.0f;
-        const float qd = d < V ? expf((di[d] - qs.mx) * invT) / qs.sum : 1.0f;
-        if (u * qd < pd) continue;
-        const int64_t x = draw_cdf(ti, ps, di, qs, V, invT, v, sh, &found, &lastp);
-        if (threadIdx.x == 0) { out[0] = i; out[1] = x; }
-        return;
-    }
-    const float* tk = tl + static_cast<size_t>(k) * V;
-    const RowStat ps = row_stat(tk, V, invT, sh);
-    float u, v;
-    round_uniforms(seed, slot, round, static_cast<uint32_t>(k), &u, &v);
-    const int64_t x = draw_cdf(tk, ps, nullptr, ps, V, invT, v, sh, &found, &lastp);
-    if (threadIdx.x == 0) { out[0] = k; out[1] = x; }
-}
 
 // ---------------------------------------------------------------- launchers
 namespace {
@@ -501,7 +695,10 @@ hipError_t launch_i8(const HeadDev& hd, int M, const HeadWork& w, float* out, hi
 }
 template <int M>
 hipError_t launch_q4_m(const HeadDev& hd, const uint16_t* h, float* out, hipStream_t st) {
-    return launch(k_head_q4<M>, dim3(head_grid()), dim3(256), 0, st, hd, h, out);
+    // one resident wave per SIMD slot (the kernel holds 4 waves per SIMD at M = 1, 3 at M = 2
+    // and 3, 2 at M = 4): every wave streams
+    // many 8-row steps, so its prologue (M rows of h) is paid once per ~9 steps
+    return launch(k_head_q4<M>, dim3(cu_count() * (M == 1 ? 4 : M == 4 ? 2 : 3)), dim3(256), 0, st, hd, h, out);
 }
 } // namespace
 
@@ -612,11 +809,55 @@ hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long lo
     return launch(k_argmax_final, dim3(1), dim3(64), 0, st, best, M, tokens, values, drafts, depth, step);
 }
 
+namespace {
+struct SampLayout {
+    int nc;
+    int64_t cs;
+    float2* part;
+    float* csum;
+    int64_t* clast;
+    SampCtl* ctl;
+    size_t bytes;
+};
+size_t a256(size_t v) { return (v + 255) / 256 * 256; }
+SampLayout samp_layout(int k, int64_t V, void* base) {
+    SampLayout L{};
+    L.nc = static_cast<int>(std::min<int64_t>(kSampChunks, (V + 255) / 256));
+    L.cs = (V + L.nc - 1) / L.nc;
+    char* b = static_cast<char*>(base);
+    size_t off = 0;
+    L.part = reinterpret_cast<float2*>(b + off);
+    off += a256(static_cast<size_t>(2 * k + 1) * L.nc * sizeof(float2));
+    L.csum = reinterpret_cast<float*>(b + off);
+    off += a256(static_cast<size_t>(L.nc) * 4);
+    L.clast = reinterpret_cast<int64_t*>(b + off);
+    off += a256(static_cast<size_t>(L.nc) * 8);
+    L.ctl = reinterpret_cast<SampCtl*>(b + off);
+    off += a256(sizeof(SampCtl));
+    L.bytes = off;
+    return L;
+}
+} // namespace
+
+size_t accept_sampled_workspace(int k, int64_t V) { return samp_layout(k, V, nullptr).bytes; }
+
 hipError_t launch_accept_sampled(const float* tl, const float* dl, const uint32_t* drafts, int k, int64_t V,
-                                 float T, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out,
+                                 float T, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out, void* ws,
                                  hipStream_t st) {
-    return launch(k_accept_sampled, dim3(1), dim3(kSampThreads), 0, st, tl, dl, drafts, k, V, T, seed, slot, round,
-                  out);
+    const SampLayout L = samp_layout(k, V, ws);
+    const float invT = 1.0f / T;
+    hipError_t e = launch(k_samp_stats, dim3(L.nc, 2 * k + 1), dim3(256), 0, st, tl, dl, k, V, L.cs, invT, L.part);
+    if (e == hipSuccess)
+        e = launch(k_samp_decide, dim3(1), dim3(64), 0, st, tl, dl, drafts, k, V, L.nc, invT, seed, slot, round,
+                   static_cast<const float2*>(L.part), L.ctl);
+    if (e == hipSuccess)
+        e = launch(k_samp_mass, dim3(L.nc), dim3(256), 0, st, tl, dl, k, V, L.cs, invT,
+                   static_cast<const SampCtl*>(L.ctl), L.csum, L.clast);
+    if (e == hipSuccess)
+        e = launch(k_samp_draw, dim3(1), dim3(256), 0, st, tl, dl, k, V, L.cs, L.nc, invT,
+                   static_cast<const SampCtl*>(L.ctl), static_cast<const float*>(L.csum),
+                   static_cast<const int64_t*>(L.clast), out);
+    return e;
 }
 
 } // namespace q38

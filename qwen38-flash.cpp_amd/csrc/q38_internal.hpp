@@ -202,8 +202,10 @@ hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long lo
                          uint32_t* tokens, float* values, uint32_t* drafts, int depth, int step, hipStream_t st);
 
 // acceptance
+// k <= 24; ws: accept_sampled_workspace(k, V) bytes.
+size_t accept_sampled_workspace(int k, int64_t V);
 hipError_t launch_accept_sampled(const float* tl, const float* dl, const uint32_t* drafts, int k, int64_t V,
-                                 float T, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out,
+                                 float T, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out, void* ws,
                                  hipStream_t st);
 
 } // namespace q38

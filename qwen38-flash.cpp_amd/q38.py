@@ -116,7 +116,8 @@ _sig("q38_mtp_draft_greedy", C.c_int, P, P, P, I32, I32, P, P, P, SZ, P)
 _sig("q38_mtp_decide_greedy", C.c_int, C.POINTER(U32), I64, C.POINTER(U32), I64, C.POINTER(U32), I64,
      C.POINTER(GreedyDecision))
 _sig("q38_plan_mtp_commit", C.c_int, U64, U64, U64, C.POINTER(U64))
-_sig("q38_mtp_accept_sampled", C.c_int, P, P, P, I32, I64, F32, U64, U64, U64, P, P)
+_sig("q38_mtp_accept_sampled", C.c_int, P, P, P, I32, I64, F32, U64, U64, U64, P, P, SZ, P)
+_sig("q38_mtp_accept_workspace_size", SZ, I32, I64)
 _sig("q38_philox4x32_10", None, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32))
 _sig("q38_slot_create", C.c_int, P, I32, I32, U64, C.POINTER(P))
 _sig("q38_slot_destroy", None, P)

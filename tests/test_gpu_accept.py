@@ -13,8 +13,10 @@ pytestmark = pytest.mark.gpu
 def gpu_accept(q38, tl, dl, drafts, T, seed, slot, rnd):
     t, d, dr = G.to_dev(tl), G.to_dev(dl), G.to_dev(np.asarray(drafts, np.uint32))
     out = G.empty(2, np.int64)
+    ws = G.workspace(q38.lib.q38_mtp_accept_workspace_size(len(drafts), tl.shape[1]))
     q38.check(q38.lib.q38_mtp_accept_sampled(t.data_ptr(), d.data_ptr(), dr.data_ptr(), len(drafts), tl.shape[1],
-                                             T, seed, slot, rnd, out.data_ptr(), G.stream()))
+                                             T, seed, slot, rnd, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                             G.stream()))
     o = G.to_host(out)
     return int(o[0]), int(o[1])
 
