@@ -135,6 +135,19 @@ int q38_supports_segmented_vq(int dimension, int packed_bits);
  * Replaces SparseMoe (include/qwen38/sparse_moe.hpp:46-214). */
 int q38_moe_layer_create(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_weights* weights,
                          q38_moe_layer** out);
+/* SparseMoe(MlxTensorStore&, prefix, ...) (include/qwen38/sparse_moe.hpp:48-55) over an
+ * on-disk checkpoint directory: config.json's vq_modules (src/model_manifest.cpp:210-230)
+ * and safetensors tensors prefix.switch_mlp.{gate,up,down}_proj.{codes,codebook,vq_scales}
+ * checked against the reference's tensor contract (src/sparse_moe.cpp:618-661), the BF16
+ * router prefix.gate.weight, and a VQ shared expert (prefix.shared_expert.*_proj with the
+ * routed codebook, prefix.shared_expert_gate.weight) when present. U32 packed codes
+ * (pack_bits 1..31) and byte codes (pack_bits 0: d2/K256) load; top-k and normalisation
+ * come from the config. The layer owns the device copies of its tensors. */
+int q38_moe_layer_load(q38_ctx* ctx, const char* checkpoint_dir, const char* prefix, int32_t book_format,
+                       q38_moe_layer** out);
+/* The layer description a checkpoint gives for prefix, after the same checks, without
+ * device work (book_format left 0). */
+int q38_checkpoint_inspect(const char* checkpoint_dir, const char* prefix, q38_moe_desc* desc);
 /* Mixed-geometry layer (desc->mixed = 1) over caller-owned tensors. Allocates the INT8
  * books decoded to fp16 chunks (3 x 256 KiB) for the MFMA kernels. */
 int q38_moe_layer_create_mixed(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_mixed_weights* weights,

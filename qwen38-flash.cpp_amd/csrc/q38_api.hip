@@ -5,6 +5,7 @@
 
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
+#include "q38_private.h"
 
 #include <algorithm>
 #include <cstdio>
@@ -167,16 +168,20 @@ static int validate_desc(const q38_moe_desc* d) {
     }
     const int geo[2][2] = {{d->gu_dim, d->gu_bits}, {d->down_dim, d->down_bits}};
     for (auto& g : geo)
-        if (!((g[0] == 8 && g[1] == 14) || (g[0] == 4 && g[1] == 8)))
-            return fail(Q38_EINVAL, "VQ geometry must be d8/14-bit or d4/8-bit");
-    // scale groups: one per row, or groups that tile 16-code lane spans
+        if (!((g[0] == 8 && g[1] == 14) || (g[0] == 4 && g[1] == 8) || (g[0] == 2 && g[1] == 8)))
+            return fail(Q38_EINVAL, "VQ geometry must be d8/14-bit, d4/8-bit or d2/8-bit (byte codes)");
+    // scale groups: one per row, or groups whose codes tile 16-code lane spans (or are
+    // whole multiples of them)
     const int ins[2] = {d->hidden, d->inter};
     const int grp[2] = {d->gu_group, d->down_group};
     for (int p = 0; p < 2; ++p) {
         const int G = grp[p], D = geo[p][0];
         if (G <= 0 || ins[p] % G) return fail(Q38_EINVAL, "scale group must divide the projection input");
-        if (G != ins[p] && (G % D || 16 % (G / D))) return fail(Q38_EINVAL, "unsupported scale group size");
+        if (G != ins[p] && (G % D || (16 % (G / D) && (G / D) % 16))) return fail(Q38_EINVAL, "unsupported scale group size");
     }
+    // the grouped kernels cover a row with at most 64 lanes of 16 codes
+    if (d->hidden / d->gu_dim > 1024 || d->inter / d->down_dim > 1024)
+        return fail(Q38_EINVAL, "more than 1024 codes per projection row");
     return Q38_OK;
 }
 
@@ -250,8 +255,13 @@ static int prepare_layer(q38_moe_layer* L) {
     }
     for (int p = 0; p < 3 && e == hipSuccess; ++p) {
         auto* dst = reinterpret_cast<uint16_t*>(base + off[p]);
-        e = launch_split_book(L->dev.p[p].book, 1 << L->dev.p[p].bits, L->dev.p[p].dim, dst, nullptr);
-        L->dev.p[p].book4 = dst;
+        // 4-dim chunks feed the MFMA kernels (d8, d4); d2 books are read whole
+        if (L->dev.p[p].dim % 4 == 0) {
+            e = launch_split_book(L->dev.p[p].book, 1 << L->dev.p[p].bits, L->dev.p[p].dim, dst, nullptr);
+            L->dev.p[p].book4 = dst;
+        } else {
+            L->dev.p[p].book4 = nullptr;
+        }
         L->dev.p[p].codes_t = nullptr;
         if (tiled && e == hipSuccess) {
             auto* ct = reinterpret_cast<uint32_t*>(base + toff[p]);
@@ -1283,6 +1293,12 @@ int q38_mtp_accept_sampled(const float* tl, const float* dl, const uint32_t* dra
     Q38_HIP(launch_accept_sampled(tl, dl, drafts, k, vocab, temperature, seed, slot, round, out, ws,
                                   static_cast<hipStream_t>(stream)));
     return Q38_OK;
+}
+
+// ------------------------------------------------------------------ private hooks
+void q38_private_set_error(const char* msg) { g_error = msg ? msg : ""; }
+void q38_private_layer_adopt(q38_moe_layer* layer, void* block) {
+    if (layer && !layer->owned) layer->owned = block;
 }
 
 // ------------------------------------------------------------------ slots

@@ -666,7 +666,6 @@ __global__ __launch_bounds__(256) void k_samp_draw(const float* __restrict__ tl,
 
 // ---------------------------------------------------------------- launchers
 namespace {
-int head_grid() { return 256 * 8; }
 
 int cu_count() {
     int dev = 0, n = 0;

@@ -684,6 +684,16 @@ struct Vec<4> {
     }
 };
 
+template <>
+struct Vec<2> {
+    // d2/K256: the byte codes of the reference checkpoint's first layers
+    static __device__ __forceinline__ void load_book(const ProjDev& P, uint32_t code, float* v) {
+        const uint32_t b = *reinterpret_cast<const uint32_t*>(P.book + code * 2);
+        v[0] = h2f(static_cast<uint16_t>(b));
+        v[1] = h2f(static_cast<uint16_t>(b >> 16));
+    }
+};
+
 constexpr int kGuRowsPerBlock = 64;
 constexpr int kDownRowsPerBlock = 128;
 
@@ -741,7 +751,8 @@ __device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int I
                     if (j < n)
 #pragma unroll
                         for (int dd = 0; dd < D; ++dd) pp[j] = fmaf(static_cast<float>(in_f[fin_at(j, s * D + dd, IN)]), bk[dd], pp[j]);
-                if (!row_scale && ((s + 1) % spg) == 0) {
+                // a group ends here, or the lane's span ends inside a group of more than 16 codes
+                if (!row_scale && (((s + 1) % spg) == 0 || qq == 15)) {
                     const float sc = h2f(P.scales[rowi * P.ngrp + s / spg]);
 #pragma unroll
                     for (int j = 0; j < MAXN; ++j) {
@@ -1088,6 +1099,10 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
         if (lpr == 64) return launch_gu_grouped_g<4, 8, 64>(L, B, M, st);
         if (lpr == 16) return launch_gu_grouped_g<4, 8, 16>(L, B, M, st);
         if (lpr <= 8) return launch_gu_grouped_g<4, 8, 8>(L, B, M, st);
+    } else if (D == 2 && BT == 8) {
+        if (lpr == 64) return launch_gu_grouped_g<2, 8, 64>(L, B, M, st);
+        if (lpr == 32) return launch_gu_grouped_g<2, 8, 32>(L, B, M, st);
+        if (lpr <= 16) return launch_gu_grouped_g<2, 8, 16>(L, B, M, st);
     }
     return hipErrorInvalidValue;
 }
@@ -1118,6 +1133,10 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
         if (lpr == 16) return launch_down_grouped_g<4, 8, 16>(L, B, M, st);
         if (lpr == 4) return launch_down_grouped_g<4, 8, 4>(L, B, M, st);
         if (lpr <= 2) return launch_down_grouped_g<4, 8, 2>(L, B, M, st);
+    } else if (D == 2 && BT == 8) {
+        if (lpr == 16) return launch_down_grouped_g<2, 8, 16>(L, B, M, st);
+        if (lpr == 32) return launch_down_grouped_g<2, 8, 32>(L, B, M, st);
+        if (lpr <= 8) return launch_down_grouped_g<2, 8, 8>(L, B, M, st);
     }
     return hipErrorInvalidValue;
 }

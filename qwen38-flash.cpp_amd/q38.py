@@ -74,6 +74,8 @@ _sig("q38_supports_segmented_vq", C.c_int, C.c_int, C.c_int)
 _sig("q38_moe_layer_create", C.c_int, P, C.POINTER(MoeDesc), C.POINTER(MoeWeights), C.POINTER(P))
 _sig("q38_moe_layer_create_synthetic", C.c_int, P, C.POINTER(MoeDesc), U64, I32, C.POINTER(P))
 _sig("q38_moe_layer_destroy", None, P)
+_sig("q38_moe_layer_load", C.c_int, P, C.c_char_p, C.c_char_p, I32, C.POINTER(P))
+_sig("q38_checkpoint_inspect", C.c_int, C.c_char_p, C.c_char_p, C.POINTER(MoeDesc))
 _sig("q38_moe_layer_weights", C.c_int, P, C.POINTER(MoeWeights))
 _sig("q38_moe_layer_codebook", C.c_int, P, C.c_int, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P))
 _sig("q38_moe_layer_bytes", I64, P, I32, I32)
