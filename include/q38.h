@@ -68,7 +68,11 @@ typedef struct q38_moe_desc {
 } q38_moe_desc;
 
 /* Device tensors of one layer (uniform geometry). The layer adopts the pointers; the
- * caller keeps them alive for the layer's lifetime. Expert index E is the shared expert.
+ * caller keeps them alive for the layer's lifetime. The tensors must be final when the
+ * layer is created: creation copies the codebooks (re-laid in 4-dim chunks, or derived
+ * per-dimension U8 books) and, for layers the <= 4-row kernels serve, the packed codes
+ * (tiled); those kernels read the copies while wider calls read the originals, so a
+ * later in-place change would make the two disagree. Expert index E is the shared expert.
  *   router       [E, H] bf16                      (SparseMoe::router_,  sparse_moe.hpp:201)
  *   shared_gate  [H] bf16 (w_sg)                  (shared_router_,       sparse_moe.hpp:209)
  *   codes[p]     [E+1, OUT_p, words_p] u32, words_p = ceil(IN_p/D/32)*BITS
