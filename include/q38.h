@@ -164,6 +164,8 @@ void q38_moe_layer_destroy(q38_moe_layer* layer);
 /* Device pointers of a layer's tensors (uniform geometry, as given at creation) for
  * inspection. */
 int q38_moe_layer_weights(const q38_moe_layer* layer, q38_moe_weights* out);
+/* The bank tensors of a mixed layer (as given to q38_moe_layer_create_mixed, or generated). */
+int q38_moe_layer_mixed_weights(const q38_moe_layer* layer, q38_moe_mixed_weights* out);
 /* The codebook the kernels read for projection p (0 gate, 1 up, 2 down): device [2^BITS, D]
  * fp16. With Q38_CB_U8_PERDIM and a d8/14-bit projection it is the decoded per-dimension
  * book (q * scale (+ bias) rounded to fp16, the MFMA operand type), and q (int8 centred for

@@ -84,6 +84,7 @@ struct q38_moe_layer {
     const void* u8q[3] = {nullptr, nullptr, nullptr};
     const uint16_t* u8s[3] = {nullptr, nullptr, nullptr};
     const uint16_t* u8b[3] = {nullptr, nullptr, nullptr};
+    q38_moe_mixed_weights mixed_in{};  // a mixed layer's bank tensors as given
 };
 
 struct q38_head {
@@ -391,6 +392,7 @@ static float h2f_host(uint16_t h) {
 static void fill_dev_mixed(q38_moe_layer* L, const q38_moe_mixed_weights* w) {
     const q38_moe_desc& d = L->desc;
     LayerDev& v = L->dev;
+    L->mixed_in = *w;
     v = LayerDev{};
     v.router = w->router;
     v.wsg = w->shared_gate;
@@ -575,6 +577,13 @@ int q38_moe_layer_weights(const q38_moe_layer* L, q38_moe_weights* out) {
         out->scales[p] = L->dev.p[p].scales;
         out->books[p] = L->books_in[p];
     }
+    return Q38_OK;
+}
+
+int q38_moe_layer_mixed_weights(const q38_moe_layer* L, q38_moe_mixed_weights* out) {
+    if (!L || !out) return fail(Q38_EINVAL, "null argument");
+    if (!L->dev.mixed) return fail(Q38_EINVAL, "a uniform layer has one set of tensors (q38_moe_weights)");
+    *out = L->mixed_in;
     return Q38_OK;
 }
 

@@ -42,6 +42,13 @@ class MoeWeights(C.Structure):
                 ("codes", C.c_void_p * 3), ("scales", C.c_void_p * 3), ("books", C.c_void_p * 3)]
 
 
+class MoeMixedWeights(C.Structure):
+    _fields_ = [("router", C.c_void_p), ("shared_gate", C.c_void_p), ("codes_d4", C.c_void_p * 3),
+                ("scales_d4", C.c_void_p * 3), ("books_d4", C.c_void_p * 3), ("codes_d8", C.c_void_p * 3),
+                ("scales_d8", C.c_void_p * 3), ("books_d8", C.c_void_p * 3), ("book_scales_d8", C.c_uint16 * 3),
+                ("reserved", C.c_uint16)]
+
+
 class RouteOut(C.Structure):
     _fields_ = [("experts", C.c_void_p), ("weights", C.c_void_p), ("logits", C.c_void_p),
                 ("plan", C.c_void_p), ("x_norm", C.c_void_p)]
@@ -77,6 +84,8 @@ _sig("q38_moe_layer_destroy", None, P)
 _sig("q38_moe_layer_load", C.c_int, P, C.c_char_p, C.c_char_p, I32, C.POINTER(P))
 _sig("q38_checkpoint_inspect", C.c_int, C.c_char_p, C.c_char_p, C.POINTER(MoeDesc))
 _sig("q38_moe_layer_weights", C.c_int, P, C.POINTER(MoeWeights))
+_sig("q38_moe_layer_mixed_weights", C.c_int, P, C.POINTER(MoeMixedWeights))
+_sig("q38_moe_layer_create_mixed", C.c_int, P, C.POINTER(MoeDesc), C.POINTER(MoeMixedWeights), C.POINTER(P))
 _sig("q38_moe_layer_codebook", C.c_int, P, C.c_int, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P))
 _sig("q38_moe_layer_bytes", I64, P, I32, I32)
 _sig("q38_moe_workspace_size", SZ, C.POINTER(MoeDesc), I32)

@@ -111,3 +111,37 @@ def test_four_slots_chain_and_commit(mixed_stack, gpu, q38, orc):
     finally:
         for p in slots:
             q38.lib.q38_slot_destroy(p)
+
+
+@pytest.mark.parametrize("M", [4, 16])
+def test_explicit_mixed_layer_equals_synthetic(gpu, q38, mixed_stack, M):
+    """q38_moe_layer_create_mixed over caller-owned tensors: a layer built from the bank tensors
+    of a synthetic mixed layer (the generator the oracle reproduces, pinned by
+    test_mixed_layer_vs_oracle) gives the same routing and outputs bit for bit."""
+    src = mixed_stack[5]
+    w = q38.MoeMixedWeights()
+    q38.check(q38.lib.q38_moe_layer_mixed_weights(src.h, C.byref(w)))
+    assert all(w.codes_d4[p] and w.codes_d8[p] and w.books_d8[p] for p in range(3))
+    d = mixed_desc(q38)
+    h = C.c_void_p()
+    q38.check(q38.lib.q38_moe_layer_create_mixed(gpu.h, C.byref(d), C.byref(w), C.byref(h)))
+
+    class Explicit:
+        pass
+
+    ex_layer = Explicit()
+    ex_layer.h = h
+    try:
+        x = G.to_host(G.to_dev(np.random.default_rng(M).normal(0, 1, (M, 2048)).astype(np.float32)))
+        xb = (x.view(np.uint32) >> 16).astype(np.uint16)
+        a = run_forward(q38, src, d, xb)
+        b = run_forward(q38, ex_layer, d, xb)
+        for u, v in zip(a, b):
+            assert np.array_equal(u, v)
+        # the uniform-layer accessor refuses a mixed layer, and creation refuses a missing bank tensor
+        assert q38.lib.q38_moe_layer_weights(h, C.byref(q38.MoeWeights())) == q38.Q38_EINVAL
+        w.books_d8[1] = None
+        h2 = C.c_void_p()
+        assert q38.lib.q38_moe_layer_create_mixed(gpu.h, C.byref(d), C.byref(w), C.byref(h2)) == q38.Q38_EINVAL
+    finally:
+        q38.lib.q38_moe_layer_destroy(h)
