@@ -721,8 +721,8 @@ int q38_moe_route(q38_moe_layer* L, const uint16_t* x, int32_t rows, const q38_r
 static int run_prefill(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* x, uint16_t* y,
                        const q38_route_out* trace, hipEvent_t* ev, hipStream_t st) {
     if (int rc = route_prefill(L, w, rows, x, st, ev)) return rc;
-    LayerDev one = L->dev;  // the prefill kernels write a single plane per projection
-    one.gu_parts = one.d_parts = 1;
+    LayerDev one = L->dev;  // partial-sum planes of the prefill kernels
+    one.gu_parts = one.d_parts = prefill_planes(L->dev, rows);
     KernelTimer& kt = kernel_timer();
     if (ev) kt = {ev[6], ev[7]};
     Q38_HIP(launch_gate_up_pf(one, w, rows, st));

@@ -145,6 +145,9 @@ bool moe_supports_prefill(const LayerDev& L);
 hipError_t launch_router_rows(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st);
 hipError_t launch_topk_rows(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_plan_sort(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+// Partial-sum planes the prefill gate/up and down kernels write: 2 on the LDS-codebook
+// kernels (one per codebook chunk), 1 on the tile kernels.
+int prefill_planes(const LayerDev& L, int M);
 hipError_t launch_gate_up_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_swiglu_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);

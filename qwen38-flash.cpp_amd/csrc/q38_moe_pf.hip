@@ -32,8 +32,11 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 // [64 gy, 64 gy + 64), wave w taking rows 64 gy + w, + 4, ... Lane l accumulates
 // x*w over the columns 512t + 8l + j (t outer, j inner) with fmaf, then the xor butterfly
 // and BF16 rounding: the logits equal the verify router's bit for bit.
+// planar: the fp16 copy of x is stored chunk-planar ([2][M][H / 2]: dims 4c..4c+3 of every
+// subvector in plane c), the layout the LDS-codebook gate/up kernel reads its B operand from.
 template <int T, int NE>
-__global__ __launch_bounds__(256) void k_logits_rows(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ x) {
+__global__ __launch_bounds__(256) void k_logits_rows(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ x,
+                                                     int planar) {
     constexpr int H = 512 * T;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int e0 = blockIdx.x * NE;
@@ -103,7 +106,13 @@ __global__ __launch_bounds__(256) void k_logits_rows(LayerDev L, MoeBufs B, int 
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                     hq[k] = static_cast<uint32_t>(f2h(bflo(q[k]))) | (static_cast<uint32_t>(f2h(bfhi(q[k]))) << 16);
-                *reinterpret_cast<uint4*>(B.x16 + at) = make_uint4(hq[0], hq[1], hq[2], hq[3]);
+                if (planar) {
+                    const size_t pa = static_cast<size_t>(r) * (H / 2) + (64 * t + lane) * 4;
+                    *reinterpret_cast<uint2*>(B.x16 + pa) = make_uint2(hq[0], hq[1]);
+                    *reinterpret_cast<uint2*>(B.x16 + static_cast<size_t>(M) * (H / 2) + pa) = make_uint2(hq[2], hq[3]);
+                } else {
+                    *reinterpret_cast<uint4*>(B.x16 + at) = make_uint4(hq[0], hq[1], hq[2], hq[3]);
+                }
             }
         }
     }
@@ -414,11 +423,413 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// ============================================================== segmented GEMM on LDS codebook chunks (R9)
+// The same products with the codebook decode moved from the vector cache into LDS: a
+// workgroup holds one 4-dim chunk of one projection's codebook (128 KiB, d8/14-bit, at LDS
+// address 0) for the whole launch, so every decoded entry is an 8-byte LDS gather instead of
+// a 16-byte cache line read. Work units are (expert slot, pass of up to 16 of the slot's
+// routes); items are (unit, tile of output rows), and each workgroup walks a contiguous
+// range of items, so the B operand (the pass's 16 route rows, this chunk's dims) stays in
+// registers for all tiles of a unit. Wave (kh, rg): K part kh (lane quarter q owns one 16-
+// or 32-code span of each of its rows) x row group rg (32 rows = two 16-row MFMA tiles);
+// v_mfma_f32_16x16x32_f16 with A = the two gathered 4-dim entries of subvectors 2t, 2t + 1
+// of the lane's span and B = the same subvectors' dims of route c16, read as one 16-byte
+// word from the chunk-planar fp16 inputs. K parts are summed through LDS in part order.
+// Each chunk writes its own partial-sum plane (times the row scale); the consumers add the
+// two planes.
+// At entry the workgroup derives the units' first item (ustart, a scan over the slots) and
+// a table of its own units: expert, route count, first sorted position, first route, and
+// per route of the unit the row it reads (gate/up: the request row) or writes (down: the
+// route index), so a unit change costs LDS reads only. The code spans of item k + 1 are in
+// flight while item k computes (two register sets, the loop unrolled by two, no copies);
+// the next unit's B operand likewise.
+constexpr int kSegThreads = 512;
+constexpr int kSegRoutes = 16;                   // routes per unit (the MFMA's B columns)
+constexpr int kSegMaxSlots = kPlanExperts + 1;   // routed slots + the shared one
+constexpr int kSegKent = 1 << 14;                // d8/14-bit codebook entries
+constexpr int kSegTab = 64;                      // units one workgroup walks (checked on the host)
+
+struct SegTab {
+    int32_t ustart[kSegMaxSlots + 1];
+    int4 unit[kSegTab];                 // expert, route count, first sorted position, first route
+    int32_t row[kSegTab][kSegRoutes];   // per route of the unit (-1 past the slot's routes)
+};
+
+__device__ __forceinline__ void seg_wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ustart[s] = the first unit of slot s (ustart[ns] = the unit count): slot s has
+// ceil(n_s / 16) units. One wave, 64 slots per step (inclusive scan by shuffles).
+__device__ __forceinline__ void seg_unit_scan(const int32_t* plan, int M, int K, int has_shared, int32_t* ustart) {
+    const int lane = threadIdx.x & 63;
+    const int nu = plan[0], ns = nu + (has_shared ? 1 : 0), MK = M * K;
+    int base = 0;
+    for (int s0 = 0; s0 < ns; s0 += 64) {
+        const int s = s0 + lane;
+        int n = 0;
+        if (s < nu) n = plan[1 + MK + s + 1] - plan[1 + MK + s];
+        else if (s < ns) n = M;
+        int v = (n + kSegRoutes - 1) / kSegRoutes;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(v, o);
+            if (lane >= o) v += t;
+        }
+        if (s < ns) ustart[s + 1] = base + v;
+        base += __shfl(v, 63);
+    }
+    if (lane == 0) ustart[0] = 0;
+}
+
+// Slot of unit u: the last s with ustart[s] <= u (every slot has at least one unit).
+__device__ __forceinline__ int seg_slot(const int32_t* ustart, int ns, int u) {
+    int lo = 0, hi = ns;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (ustart[mid] <= u) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// The table of units [u0, u0 + nt) (every thread of the workgroup; ustart published).
+template <bool DOWN>
+__device__ __forceinline__ void seg_build_tab(const int32_t* plan, int M, int K, int has_shared, int E, int ns,
+                                              int u0, int nt, SegTab& T) {
+    const int MK = M * K, nu = plan[0];
+    for (int t = threadIdx.x; t < nt * kSegRoutes; t += kSegThreads) {
+        const int k = t / kSegRoutes, l = t % kSegRoutes;
+        const int u = u0 + k;
+        const int s = seg_slot(T.ustart, ns, u);
+        int expert, n, pos0;
+        slot_rows(plan, M, K, has_shared, s, E, &expert, &n, &pos0);
+        const int j0 = (u - T.ustart[s]) * kSegRoutes, j = j0 + l;
+        if (l == 0) T.unit[k] = make_int4(expert, n, pos0, j0);
+        int r = -1;
+        if (j < n) r = DOWN ? route_of_pos(plan, MK, pos0 + j) : route_row(plan, M, K, pos0, j, s == nu);
+        T.row[k][l] = r;
+    }
+}
+
+// Words [7 h, 7 h + 7) of the lane's 32-code block (h = half, for 16-code spans) or the
+// whole block (14 words), from the tiled code layout: tile64 = the row's 64-row tile,
+// rr = the row inside it; chunk c of a (tile, block) holds words 4c.. of its 64 rows.
+template <int SPL>
+__device__ __forceinline__ void seg_load_codes(const uint32_t* codes_t, int KS, size_t tile64, int rr, int blk,
+                                               int half, uint32_t (&w)[SPL == 32 ? 14 : 7]) {
+    const uint32_t* base = codes_t + (tile64 * KS + blk) * (14 * 64);
+    if constexpr (SPL == 32) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const uint4 v = *reinterpret_cast<const uint4*>(base + c * 256 + rr * 4);
+            w[4 * c] = v.x; w[4 * c + 1] = v.y; w[4 * c + 2] = v.z; w[4 * c + 3] = v.w;
+        }
+        const uint2 v = *reinterpret_cast<const uint2*>(base + 768 + rr * 2);
+        w[12] = v.x; w[13] = v.y;
+    } else {
+        // half 0: words 0..6 = chunk 0 + chunk 1 (three of four); half 1: words 7..13 =
+        // chunk 1's last word + chunk 2 + chunk 3. The same three loads for every lane.
+        const uint4 a = *reinterpret_cast<const uint4*>(base + (half ? 256 : 0) + rr * 4);
+        const uint4 b = *reinterpret_cast<const uint4*>(base + (half ? 512 : 256) + rr * 4);
+        const uint2 c = *reinterpret_cast<const uint2*>(base + 768 + rr * 2);
+        w[0] = half ? a.w : a.x;
+        w[1] = half ? b.x : a.y;
+        w[2] = half ? b.y : a.z;
+        w[3] = half ? b.z : a.w;
+        w[4] = half ? b.w : b.x;
+        w[5] = half ? c.x : b.y;
+        w[6] = half ? c.y : b.z;
+    }
+}
+
+// 8 x code q of a packed 32-code block (the LDS byte offset of its 4-dim entry): one shift
+// (or funnel shift, for a code that spans two words) and one mask.
+__device__ __forceinline__ uint32_t code14_x8(const uint32_t* w, int q) {
+    const int bit = q * 14;
+    const int wi = bit >> 5, sh = bit & 31;
+    uint32_t v;
+    if (sh < 3) v = w[wi] << (3 - sh);
+    else if (sh + 14 > 32) v = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh - 3);
+    else v = w[wi] >> (sh - 3);
+    return v & (((1u << 14) - 1u) << 3);
+}
+
+// Two 16-row tiles of one item: acc[i] += A(rows of w[i]) x B over NB16 16-byte B words (two
+// subvectors each). MFMA m (step m / 2, tile m % 2) uses the gathers issued LA MFMAs
+// earlier: scheduling barriers keep that order (left alone, the scheduler waits for each
+// MFMA's two gathers right before it, and the LDS latency is exposed on every step).
+template <int NB16, int NW>
+__device__ __forceinline__ void seg_mfma(const uint32_t (&w)[2][NW], const uint4 (&bx)[NB16],
+                                         const unsigned char* book, f4_t (&acc)[2]) {
+    constexpr int NM = 2 * NB16, LA = 4;
+    uint4 a[NM];
+    auto gather = [&](int m) {
+        const int t = m >> 1, i = m & 1;
+        const uint2 a0 = *reinterpret_cast<const uint2*>(book + code14_x8(w[i], 2 * t));
+        const uint2 a1 = *reinterpret_cast<const uint2*>(book + code14_x8(w[i], 2 * t + 1));
+        a[m] = make_uint4(a0.x, a0.y, a1.x, a1.y);
+    };
+#pragma unroll
+    for (int m = 0; m < LA; ++m) gather(m);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (m + LA < NM) gather(m + LA);
+        acc[m & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a[m]),
+                                                            __builtin_bit_cast(h8_t, bx[m >> 1]), acc[m & 1], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ float4 seg_scaled(uint2 sc, const f4_t& a) {
+    return make_float4(h2f(static_cast<uint16_t>(sc.x)) * a[0], h2f(static_cast<uint16_t>(sc.x >> 16)) * a[1],
+                       h2f(static_cast<uint16_t>(sc.y)) * a[2], h2f(static_cast<uint16_t>(sc.y >> 16)) * a[3]);
+}
+
+// Items [i0, i1) of this workgroup.
+__device__ __forceinline__ void seg_range(int n_items, int per_type, int idx, int& i0, int& i1) {
+    i0 = static_cast<int>(static_cast<int64_t>(idx) * n_items / per_type);
+    i1 = static_cast<int>(static_cast<int64_t>(idx + 1) * n_items / per_type);
+}
+
+// LDS of the kernels: the codebook chunk at 0, then (gate/up) the K-part partial sums, then
+// the unit table.
+template <int NSUB>
+constexpr size_t gu_seg_red_bytes() {
+    return size_t{2} * (NSUB / 128 - 1) * (8 / (NSUB / 128)) * 2 * 64 * 16;
+}
+
+// Gate/up (NSUB = H / 8 subvectors per row: 128, 256 or 512). Output rows of an item:
+// TR = 32 * RG rows of I; chunk `chunk` of projection `proj` per workgroup type. B = rows of
+// the chunk-planar fp16 inputs ([2][M][H / 2]).
+template <int NSUB>
+__global__ __launch_bounds__(kSegThreads) void k_gu_seg(LayerDev L, MoeBufs B, int M) {
+    constexpr int KP = NSUB / 128, RG = 8 / KP, TR = 32 * RG, KS = NSUB / 32;
+    static_assert(NSUB % 128 == 0 && KP * RG == 8, "8 waves = K parts x row groups");
+    extern __shared__ __align__(16) unsigned char lds[];
+    const unsigned char* book = lds;
+    f4_t* red = reinterpret_cast<f4_t*>(lds + kSegKent * 8);  // [2][KP - 1][RG][2][64]
+    SegTab& T = *reinterpret_cast<SegTab*>(lds + kSegKent * 8 + gu_seg_red_bytes<NSUB>());
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kh = wave % KP, rg = wave / KP;
+    const int r16 = lane & 15, q = lane >> 4;
+    const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
+    const int type = kk & 3, proj = type >> 1, chunk = type & 1;
+    const int per_type = (gridDim.x / 32) * 8;
+    const int idx = (kk >> 2) * 8 + x8;  // the chunk-0 and chunk-1 workgroups of an index share an XCD
+    const ProjDev& P = L.p[proj];
+    const int H = L.H, I = L.I, K = L.K, E = L.E, hs = L.has_shared;
+    const int32_t* plan = B.plan;
+    if (wave == 0) seg_unit_scan(plan, M, K, hs, T.ustart);
+    else dma_book<kSegKent>(P.book4 + static_cast<size_t>(chunk) * kSegKent * 4, lds, wave - 1, 7);
+    lds_barrier_dma_pending();  // ustart published; the codebook copy still in flight
+    const int ns = plan[0] + (hs ? 1 : 0);
+    const int tiles = I / TR;
+    int i0, i1;
+    seg_range(T.ustart[ns] * tiles, per_type, idx, i0, i1);
+    if (i0 >= i1) {
+        seg_wait_vm();  // (the copy into LDS ends before the workgroup does)
+        return;
+    }
+    const int u0 = i0 / tiles;
+    seg_build_tab<false>(plan, M, K, hs, E, ns, u0, (i1 - 1) / tiles - u0 + 1, T);
+    seg_wait_vm();
+    lds_barrier();
+    float* out = (proj == 0 ? B.g : B.u) + chunk * B.gu_plane;
+    const uint16_t* xplane = B.x16 + static_cast<size_t>(chunk) * M * (H / 2);
+
+    // B operand of unit k: request row T.row[k][r16], subvectors kh * 128 + 32 q + (0..31)
+    auto load_b = [&](int k, uint4 (&bx)[16]) {
+        const int row = T.row[k][r16];
+        if (row >= 0) {
+            const uint4* src = reinterpret_cast<const uint4*>(xplane + static_cast<size_t>(row) * (H / 2) +
+                                                              (kh * 128 + 32 * q) * 4);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) bx[i] = src[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) bx[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto load_codes = [&](int expert, int tile, uint32_t (&w)[2][14]) {
+        const size_t row0 = static_cast<size_t>(expert) * I + tile * TR + rg * 32;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            seg_load_codes<32>(P.codes_t, KS, row0 >> 6, static_cast<int>(row0 & 63) + 16 * i + r16, kh * 4 + q, 0,
+                               w[i]);
+    };
+    uint4 bx[16];
+    load_b(0, bx);
+    // (k, tile): the current item's unit (table index) and tile, advanced without divisions
+    int k = 0, tile = i0 - u0 * tiles;
+    auto body = [&](int item, const uint32_t (&w)[2][14], uint32_t (&wn)[2][14]) {
+        const int4 un = T.unit[k];  // expert, n, pos0, j0
+        const int o0 = tile * TR + rg * 32 + 4 * q;
+        // loads in the order they are needed: this item's row scales, the next unit's B
+        // operand (when the unit changes), the next item's code spans (the last item: its
+        // own again)
+        uint2 sc[2];
+        sc[0] = *reinterpret_cast<const uint2*>(P.scales + static_cast<size_t>(un.x) * I + o0);
+        sc[1] = *reinterpret_cast<const uint2*>(P.scales + static_cast<size_t>(un.x) * I + o0 + 16);
+        const bool last = item + 1 >= i1;
+        const bool new_unit = !last && tile + 1 == tiles;
+        load_codes(new_unit ? T.unit[k + 1].x : un.x, last ? tile : new_unit ? 0 : tile + 1, wn);
+        f4_t acc[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
+        seg_mfma<16, 14>(w, bx, book, acc);
+        // the next unit's B operand replaces this one as soon as the MFMAs have read it (a
+        // second register set would not fit), in flight through the reduction and stores
+        if (new_unit) load_b(k + 1, bx);
+        const int buf = item & 1;
+        if (KP > 1) {
+            if (kh > 0)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) red[(((buf * (KP - 1) + kh - 1) * RG + rg) * 2 + i) * 64 + lane] = acc[i];
+            lds_barrier();  // (the other buffer was read before the previous item's barrier)
+        }
+        if (kh == 0) {
+            const int j = un.w + r16;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                f4_t sum = acc[i];
+#pragma unroll
+                for (int p = 1; p < KP; ++p) sum += red[(((buf * (KP - 1) + p - 1) * RG + rg) * 2 + i) * 64 + lane];
+                if (j < un.y)
+                    *reinterpret_cast<float4*>(out + static_cast<size_t>(un.z + j) * I + o0 + 16 * i) =
+                        seg_scaled(sc[i], sum);
+            }
+        }
+        if (new_unit) {
+            ++k;
+            tile = 0;
+        } else {
+            ++tile;
+        }
+    };
+    uint32_t wa[2][14], wb[2][14];
+    load_codes(T.unit[0].x, tile, wa);
+    for (int item = i0; item < i1; item += 2) {
+        body(item, wa, wb);
+        if (item + 1 < i1) body(item + 1, wb, wa);
+    }
+}
+
+// Down (NSUB = I / 8 subvectors per row: 64 or 128; SPL = NSUB / 4 per lane quarter, 16 =
+// half a code block). One K part: wave rg owns rows 32 rg .. + 31 of a TR = 256-row tile of
+// H. B = the pass's SwiGLU rows (chunk-planar fp16 at sorted positions); outputs at the
+// route index.
+template <int NSUB>
+__global__ __launch_bounds__(kSegThreads) void k_dn_seg(LayerDev L, MoeBufs B, int M) {
+    constexpr int SPL = NSUB / 4, TR = 256, KS = NSUB / 32;
+    static_assert(SPL == 16 || SPL == 32, "16-code or 32-code lane spans");
+    constexpr int NW = SPL == 32 ? 14 : 7, NB = SPL / 2;
+    extern __shared__ __align__(16) unsigned char lds[];
+    const unsigned char* book = lds;
+    SegTab& T = *reinterpret_cast<SegTab*>(lds + kSegKent * 8);
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
+    const int tid = threadIdx.x, lane = tid & 63, rg = tid >> 6;
+    const int r16 = lane & 15, q = lane >> 4;
+    const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
+    const int chunk = kk & 1;
+    const int per_type = (gridDim.x / 16) * 8;
+    const int idx = (kk >> 1) * 8 + x8;
+    const ProjDev& P = L.p[2];
+    const int H = L.H, I = L.I, K = L.K, E = L.E, hs = L.has_shared;
+    const int32_t* plan = B.plan;
+    if (rg == 0) seg_unit_scan(plan, M, K, hs, T.ustart);
+    else dma_book<kSegKent>(P.book4 + static_cast<size_t>(chunk) * kSegKent * 4, lds, rg - 1, 7);
+    lds_barrier_dma_pending();
+    const int ns = plan[0] + (hs ? 1 : 0);
+    const int tiles = H / TR;
+    int i0, i1;
+    seg_range(T.ustart[ns] * tiles, per_type, idx, i0, i1);
+    if (i0 >= i1) {
+        seg_wait_vm();
+        return;
+    }
+    const int u0 = i0 / tiles;
+    seg_build_tab<true>(plan, M, K, hs, E, ns, u0, (i1 - 1) / tiles - u0 + 1, T);
+    seg_wait_vm();
+    lds_barrier();
+    float* dout = B.d + chunk * B.d_plane;
+    const int MKM = M * K + (hs ? M : 0);
+    const uint16_t* hplane = B.h16 + static_cast<size_t>(chunk) * MKM * (I / 2);
+    const int blk = SPL * q / 32, half = SPL == 16 ? (q & 1) : 0;
+
+    // B operand of unit k: SwiGLU row (sorted position) of route j0 + r16, subvectors
+    // SPL q + (0..SPL-1)
+    auto load_b = [&](int k, uint4 (&bx)[NB]) {
+        const int4 un = T.unit[k];
+        const int j = un.w + r16;
+        if (j < un.y) {
+            const uint4* src =
+                reinterpret_cast<const uint4*>(hplane + static_cast<size_t>(un.z + j) * (I / 2) + SPL * q * 4);
+#pragma unroll
+            for (int i = 0; i < NB; ++i) bx[i] = src[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) bx[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto load_codes = [&](int expert, int tile, uint32_t (&w)[2][NW]) {
+        const size_t row0 = static_cast<size_t>(expert) * H + tile * TR + rg * 32;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            seg_load_codes<SPL>(P.codes_t, KS, row0 >> 6, static_cast<int>(row0 & 63) + 16 * i + r16, blk, half,
+                                w[i]);
+    };
+    uint4 bx[NB];
+    load_b(0, bx);
+    int k = 0, tile = i0 - u0 * tiles;
+    auto body = [&](int item, const uint32_t (&w)[2][NW], uint32_t (&wn)[2][NW]) {
+        const int expert = T.unit[k].x;
+        const int rt = T.row[k][r16];  // route index of the lane's route (-1: none)
+        const int o0 = tile * TR + rg * 32 + 4 * q;
+        uint2 sc[2];
+        sc[0] = *reinterpret_cast<const uint2*>(P.scales + static_cast<size_t>(expert) * H + o0);
+        sc[1] = *reinterpret_cast<const uint2*>(P.scales + static_cast<size_t>(expert) * H + o0 + 16);
+        const bool last = item + 1 >= i1;
+        const bool new_unit = !last && tile + 1 == tiles;
+        load_codes(new_unit ? T.unit[k + 1].x : expert, last ? tile : new_unit ? 0 : tile + 1, wn);
+        f4_t acc[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
+        seg_mfma<NB, NW>(w, bx, book, acc);
+        if (new_unit) load_b(k + 1, bx);
+        if (rt >= 0)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                *reinterpret_cast<float4*>(dout + static_cast<size_t>(rt) * H + o0 + 16 * i) = seg_scaled(sc[i], acc[i]);
+        if (new_unit) {
+            ++k;
+            tile = 0;
+        } else {
+            ++tile;
+        }
+    };
+    uint32_t wa[2][NW], wb[2][NW];
+    load_codes(T.unit[0].x, tile, wa);
+    for (int item = i0; item < i1; item += 2) {
+        body(item, wa, wb);
+        if (item + 1 < i1) body(item + 1, wb, wa);
+    }
+}
+
+// SwiGLU of every route, the two chunk planes of g and u added; the output is chunk-planar
+// ([2][rows][I / 2]) for the down kernel's B operand.
+__global__ __launch_bounds__(256) void k_swiglu_seg(MoeBufs B, int I, int64_t total) {
+    const int64_t plane = total / 2;
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t pos = i / I;
+        const int o = static_cast<int>(i - pos * I);
+        const int64_t at = ((o >> 2) & 1) * plane + pos * (I / 2) + (o >> 3) * 4 + (o & 3);
+        B.h16[at] = f2h(swiglu(B.g[i] + B.g[B.gu_plane + i], B.u[i] + B.u[B.gu_plane + i]));
+    }
+}
+
 template <int T>
 hipError_t launch_router_rows_t(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st) {
     constexpr int NE = T <= 2 ? 8 : T <= 4 ? 4 : 2;  // router rows in registers: 16 T NE <= 128 VGPRs
     const int nr = L.E + (L.has_shared ? 1 : 0);
-    return launch(k_logits_rows<T, NE>, dim3((nr + NE - 1) / NE, (M + 63) / 64), dim3(256), 0, st, L, B, M, x);
+    const int planar = prefill_planes(L, M) == 2 ? 1 : 0;
+    return launch(k_logits_rows<T, NE>, dim3((nr + NE - 1) / NE, (M + 63) / 64), dim3(256), 0, st, L, B, M, x, planar);
 }
 
 } // namespace
@@ -460,16 +871,68 @@ static int pf_slots(const LayerDev& L, int M) {
     return (MK < L.E ? MK : L.E) + (L.has_shared ? 1 : 0);
 }
 
+// The LDS-codebook kernels serve layers with 4-dim codebook chunks and the tiled codes
+// (d8/14-bit, H / 8 = 128, 256 or 512, I / 8 = 64 or 128) when every workgroup's units fit
+// its table; others take the tile kernels.
+static int64_t seg_units_per_wg(const LayerDev& L, int M, int tiles, int per_type) {
+    const int64_t MK = static_cast<int64_t>(M) * L.K;
+    const int64_t ns = (MK < L.E ? MK : L.E) + (L.has_shared ? 1 : 0);
+    const int64_t units = (MK + (L.has_shared ? M : 0) + (kSegRoutes - 1) * ns) / kSegRoutes;  // >= sum ceil(n/16)
+    const int64_t items = (units * tiles + per_type - 1) / per_type;
+    return (items + tiles - 1) / tiles + 1;
+}
+
+int prefill_planes(const LayerDev& L, int M) {
+    for (int p = 0; p < 3; ++p)
+        if (!L.p[p].book4 || !L.p[p].codes_t) return 1;
+    const int gn = L.H / 8, dn = L.I / 8;
+    if ((gn != 128 && gn != 256 && gn != 512) || (dn != 64 && dn != 128)) return 1;
+    const int gu_rows = 32 * (8 / (gn / 128));  // output rows of a gate/up item
+    if (L.I % gu_rows || L.H % 256 || L.E + 1 > kSegMaxSlots) return 1;
+    const int grid = mfma_grid();
+    if (seg_units_per_wg(L, M, L.I / gu_rows, grid / 32 * 8) > kSegTab ||
+        seg_units_per_wg(L, M, L.H / 256, grid / 16 * 8) > kSegTab)
+        return 1;
+    return 2;
+}
+
+template <int NSUB>
+hipError_t launch_gu_seg_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    constexpr size_t lds = size_t{kSegKent} * 8 + gu_seg_red_bytes<NSUB>() + sizeof(SegTab);
+    if (const hipError_t e = ensure_lds<k_gu_seg<NSUB>>(lds); e != hipSuccess) return e;
+    return launch(k_gu_seg<NSUB>, dim3(mfma_grid()), dim3(kSegThreads), lds, st, L, B, M);
+}
+template <int NSUB>
+hipError_t launch_dn_seg_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    constexpr size_t lds = size_t{kSegKent} * 8 + sizeof(SegTab);
+    if (const hipError_t e = ensure_lds<k_dn_seg<NSUB>>(lds); e != hipSuccess) return e;
+    return launch(k_dn_seg<NSUB>, dim3(mfma_grid()), dim3(kSegThreads), lds, st, L, B, M);
+}
+
 hipError_t launch_gate_up_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    if (prefill_planes(L, M) == 2) {
+        switch (L.H / 8) {
+            case 128: return launch_gu_seg_t<128>(L, B, M, st);
+            case 256: return launch_gu_seg_t<256>(L, B, M, st);
+            case 512: return launch_gu_seg_t<512>(L, B, M, st);
+            default: return hipErrorInvalidValue;
+        }
+    }
     return launch(k_gu_pf, dim3(L.I / kPfRows, pf_slots(L, M), 2), dim3(256), 0, st, L, B, M);
 }
 
 hipError_t launch_swiglu_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     const int64_t total = static_cast<int64_t>(M * L.K + (L.has_shared ? M : 0)) * L.I;
+    if (prefill_planes(L, M) == 2) return launch(k_swiglu_seg, dim3(2048), dim3(256), 0, st, B, L.I, total);
     return launch(k_swiglu_pf, dim3(2048), dim3(256), 0, st, B, total);
 }
 
 hipError_t launch_down_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    if (prefill_planes(L, M) == 2) {
+        if (L.I / 8 == 64) return launch_dn_seg_t<64>(L, B, M, st);
+        if (L.I / 8 == 128) return launch_dn_seg_t<128>(L, B, M, st);
+        return hipErrorInvalidValue;
+    }
     return launch(k_dn_pf, dim3(L.H / kPfRows, pf_slots(L, M), 1), dim3(256), 0, st, L, B, M);
 }
 
