@@ -190,7 +190,10 @@ int q38_moe_route(q38_moe_layer* layer, const uint16_t* x, int32_t rows, const q
  * y = routed + shared for rows 1..2048 of x. Rows 1..16 take the verify kernels; wider
  * calls (SparseMoe::forward_prefill, include/qwen38/sparse_moe.hpp:68, S <= 2048) take the
  * segmented-GEMM kernels, which need d8/14-bit projections with per-row scales and
- * rows * top_k <= 32768. x, y: device [rows, H] bf16 (may not alias). */
+ * rows * top_k <= 32768. x, y: device [rows, H] bf16 (may not alias). The expert kernels
+ * take x as an fp16 MFMA operand: |x| must stay below 65504, and elements below 2^-14 lose
+ * relative precision (an RMSNorm output, as in the verify chain, is bounded by sqrt(H) and
+ * its small elements weigh nothing in the products). */
 int q38_moe_forward(q38_moe_layer* layer, const uint16_t* x, int32_t rows, uint16_t* y,
                     const q38_route_out* routes, void* workspace, size_t workspace_bytes, void* stream);
 

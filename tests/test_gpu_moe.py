@@ -31,6 +31,24 @@ def test_config0_layer(layer0, q38, orc, M):
     tol_check(orc, y, wy)
 
 
+@pytest.mark.parametrize("M", [4, 16])
+def test_fp16_operand_extremes(layer0, q38, orc, M):
+    """The expert kernels take x as an fp16 MFMA operand. RMSNorm outputs with one spike
+    per row reach sqrt(H) ~ 45 in one element and put the rest below fp16's normal range
+    (2^-14); the layer output stays within the MoE tolerance of the oracle, whose products
+    are in float."""
+    rng = np.random.default_rng(M)
+    h = rng.normal(0, 1e-4, (M, 2048))
+    h[np.arange(M), rng.integers(0, 2048, M)] = 1e3
+    x = orc.rmsnorm(orc.bf16(h))
+    xf = orc.bf16_to_f32(x)
+    assert np.abs(xf).max() > 40 and (np.abs(xf) < 2.0 ** -14).mean() > 0.9
+    y, ex, wt, lg, plan = run_forward(q38, layer0, layer0.desc, x)
+    wy, wex, wwt, wlg = orc.moe_layer_synth(oracle_lib.make_desc(), SEED, 0, x)
+    assert np.array_equal(ex, wex) and np.array_equal(wt, wwt)
+    tol_check(orc, y, wy)
+
+
 def test_sixteen_rows(layer0, q38, orc):
     x = orc.normal(orc.key(SEED, 0, 20), 7, 16 * 2048, 1.0).reshape(16, 2048)
     y, ex, wt, lg, plan = run_forward(q38, layer0, layer0.desc, x)
