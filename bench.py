@@ -378,50 +378,66 @@ def main():
         f"({100 * prefill_cfg['mfma_frac']:.2f}% of 2.5 PFLOP/s), {prefill_cfg['gbps']:.0f} GB/s, U={up}")
     Lp.close()
 
+    def chain_leg(desc_, Mc, NLc):
+        """us per layer (graph replays, median of 10), mean unique experts and bytes per layer
+        of Mc rows through NLc layers of desc_."""
+        lc = [q38.MoeLayer(ctx, desc_, seed=SEED, layer=l) for l in range(NLc)]
+        try:
+            larc = (C.c_void_p * NLc)(*[L.h.value for L in lc])
+            wsc = torch.empty(q38.lib.q38_moe_workspace_size(C.byref(desc_), Mc), dtype=torch.uint8, device=dev)
+            hc = torch.empty((Mc, H), dtype=torch.int16, device=dev)
+            toks_c = (C.c_uint32 * Mc)(*[11 + 7 * r for r in range(Mc)])
+            q38.check(q38.lib.q38_embed_synthetic(SEED, toks_c, Mc, H, hc.data_ptr(), sp))
+            hc0 = hc.clone()
+            plc = [torch.empty(2 + 4 * Mc * K, dtype=torch.int32, device=dev) for _ in lc]
+            trc = (q38.RouteOut * NLc)(*[q38.routes(plan=p) for p in plc])
+            q38.check(q38.lib.q38_verify_chain(larc, NLc, hc.data_ptr(), Mc, 1e-6, trc, wsc.data_ptr(), wsc.numel(),
+                                               sp))
+            torch.cuda.synchronize()
+            uc = [int(p[0].item()) for p in plc]
+
+            def run(sp_):
+                q38.check(q38.lib.q38_verify_chain(larc, NLc, hc.data_ptr(), Mc, 1e-6, None, wsc.data_ptr(),
+                                                   wsc.numel(), sp_))
+            gc = None
+            if not args.no_graph:
+                gc = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gc):
+                    run(torch.cuda.current_stream().cuda_stream)
+            tc = []
+            for _ in range(10):
+                hc.copy_(hc0)
+                ev0.record(stream)
+                if gc is not None:
+                    gc.replay()
+                else:
+                    run(sp)
+                ev1.record(stream)
+                torch.cuda.synchronize()
+                tc.append(ev0.elapsed_time(ev1))
+            us = 1e3 * float(np.median(tc)) / NLc
+            nb = sum(L.bytes(u, Mc) for L, u in zip(lc, uc)) / NLc
+            return us, float(np.mean(uc)), nb
+        finally:
+            for L in lc:
+                L.close()
+
     # ---------------------------------------------------------------- config 4: mixed VQ v2
     # 16 rows (4 slots x 4) through a chain of mixed layers (even experts d4/8-bit fp16 books,
     # odd experts d8/14-bit INT8 books with one scale per book), uniform routing.
     Mm, NLm = 16, 4
-    dm = q38.desc(mixed=1)
-    lm = [q38.MoeLayer(ctx, dm, seed=SEED, layer=l) for l in range(NLm)]
-    larm = (C.c_void_p * NLm)(*[L.h.value for L in lm])
-    wsm = torch.empty(q38.lib.q38_moe_workspace_size(C.byref(dm), Mm), dtype=torch.uint8, device=dev)
-    hm = torch.empty((Mm, H), dtype=torch.int16, device=dev)
-    toks = (C.c_uint32 * Mm)(*[11 + 7 * r for r in range(Mm)])
-    q38.check(q38.lib.q38_embed_synthetic(SEED, toks, Mm, H, hm.data_ptr(), sp))
-    hm0 = hm.clone()
-    plm = [torch.empty(2 + 4 * Mm * K, dtype=torch.int32, device=dev) for _ in lm]
-    trm = (q38.RouteOut * NLm)(*[q38.routes(plan=p) for p in plm])
-    q38.check(q38.lib.q38_verify_chain(larm, NLm, hm.data_ptr(), Mm, 1e-6, trm, wsm.data_ptr(), wsm.numel(), sp))
-    torch.cuda.synchronize()
-    um = [int(p[0].item()) for p in plm]
-
-    def mixed_chain(sp_):
-        q38.check(q38.lib.q38_verify_chain(larm, NLm, hm.data_ptr(), Mm, 1e-6, None, wsm.data_ptr(), wsm.numel(),
-                                           sp_))
-    gm = None
-    if not args.no_graph:
-        gm = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gm):
-            mixed_chain(torch.cuda.current_stream().cuda_stream)
-    mt = []
-    for _ in range(10):
-        hm.copy_(hm0)
-        ev0.record(stream)
-        if gm is not None:
-            gm.replay()
-        else:
-            mixed_chain(sp)
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        mt.append(ev0.elapsed_time(ev1))
-    m_us = 1e3 * float(np.median(mt)) / NLm
-    m_bytes = sum(L.bytes(u, Mm) for L, u in zip(lm, um)) / NLm
-    mixed_cfg = {"rows": Mm, "layers": NLm, "layer_us": m_us, "mean_unique_experts": float(np.mean(um)),
+    m_us, m_u, m_bytes = chain_leg(q38.desc(mixed=1), Mm, NLm)
+    mixed_cfg = {"rows": Mm, "layers": NLm, "layer_us": m_us, "mean_unique_experts": m_u,
                  "bytes_per_layer": m_bytes, "gbps": m_bytes / (m_us * 1e-6) / 1e9}
-    log(f"config 4 (mixed VQ v2, 16 rows): {m_us:.1f} us/layer, {mixed_cfg['gbps']:.0f} GB/s, U={np.mean(um):.1f}")
-    for L in lm:
-        L.close()
+    log(f"config 4 (mixed VQ v2, 16 rows): {m_us:.1f} us/layer, {mixed_cfg['gbps']:.0f} GB/s, U={m_u:.1f}")
+
+    # ---------------------------------------------------------------- checkpoint scale layout
+    # Config-1 layers with one fp16 scale per 64 inputs (the reference checkpoints' vq_scales
+    # layout) at the verify width: 4 rows through 8 layers.
+    g_us, g_u, g_bytes = chain_leg(q38.desc(gu_group=64, down_group=64), 4, 8)
+    g64_cfg = {"rows": 4, "layers": 8, "layer_us": g_us, "mean_unique_experts": g_u, "bytes_per_layer": g_bytes,
+               "gbps": g_bytes / (g_us * 1e-6) / 1e9}
+    log(f"config 1 with 64-input scale groups (4 rows): {g_us:.1f} us/layer, {g64_cfg['gbps']:.0f} GB/s, U={g_u:.1f}")
 
     if args.copy_calibration:
         # a plain device copy of known size for the FETCH_SIZE / WRITE_SIZE calibration runs
@@ -603,7 +619,7 @@ def main():
             "kernel_us_per_launch_m4": {k.split()[0]: 1e3 * v[0] / nl for k, v in kernels.items()},
             "algorithmic_bytes_per_launch_m4": {k.split()[0]: v[1] for k, v in kernels.items()},
             "config3_prefill": prefill_cfg,
-            "config4_mixed": mixed_cfg,
+            "config4_mixed": mixed_cfg, "config1_group64": g64_cfg,
             "config2_sampled": sampled_cfg,
             "config2_learned_drafts": learned_cfg,
         },

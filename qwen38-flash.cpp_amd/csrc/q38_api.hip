@@ -745,17 +745,18 @@ static int run_prefill(q38_moe_layer* L, const MoeBufs& w, int rows, const uint1
 // events recorded around the phases.
 static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* src, bool norm, float eps,
                      uint16_t* h_chain, uint16_t* y, const q38_route_out* trace, hipEvent_t* ev, hipStream_t st) {
+    const LayerDev dev = moe_call_dev(L->dev, rows);
     if (ev) Q38_HIP(hipEventRecord(ev[0], st));
-    Q38_HIP(launch_router(L->dev, w, rows, src, norm, eps, st));
-    if (!moe_plans_in_gate_up(L->dev)) Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
+    Q38_HIP(launch_router(dev, w, rows, src, norm, eps, st));
+    if (!moe_plans_in_gate_up(dev, rows)) Q38_HIP(launch_topk_plan(dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[1], st));
-    Q38_HIP(launch_gate_up(L->dev, w, rows, st));
+    Q38_HIP(launch_gate_up(dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[2], st));
     if (trace)
         if (int rc = copy_routes(L, rows, w, trace, st)) return rc;
-    Q38_HIP(launch_down(L->dev, w, rows, st));
+    Q38_HIP(launch_down(dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[3], st));
-    Q38_HIP(launch_combine(L->dev, w, rows, h_chain, y, st));
+    Q38_HIP(launch_combine(dev, w, rows, h_chain, y, st));
     if (ev) Q38_HIP(hipEventRecord(ev[4], st));
     return Q38_OK;
 }
@@ -870,23 +871,24 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
         moe_ws(layers[l]->desc, rows, &w, ws);
         hipEvent_t* E = &ev[static_cast<size_t>(l) * 8];
         const q38_moe_layer* L = layers[l];
+        const LayerDev dev = moe_call_dev(L->dev, rows);
         hipError_t e = hipSuccess;
         kt = {E[0], E[1]};
-        e = launch_router(L->dev, w, rows, h, true, eps, st);
-        if (e == hipSuccess && !moe_plans_in_gate_up(L->dev)) e = launch_topk_plan(L->dev, w, rows, st);
+        e = launch_router(dev, w, rows, h, true, eps, st);
+        if (e == hipSuccess && !moe_plans_in_gate_up(dev, rows)) e = launch_topk_plan(dev, w, rows, st);
         if (e == hipSuccess) {
             kt = {E[2], E[3]};
-            e = launch_gate_up(L->dev, w, rows, st);
+            e = launch_gate_up(dev, w, rows, st);
         }
         if (e == hipSuccess && traces)
             if (copy_routes(L, rows, w, &traces[l], st) != Q38_OK) e = hipErrorUnknown;
         if (e == hipSuccess) {
             kt = {E[4], E[5]};
-            e = launch_down(L->dev, w, rows, st);
+            e = launch_down(dev, w, rows, st);
         }
         if (e == hipSuccess) {
             kt = {E[6], E[7]};
-            e = launch_combine(L->dev, w, rows, h, nullptr, st);
+            e = launch_combine(dev, w, rows, h, nullptr, st);
         }
         kt = {};
         if (e != hipSuccess) rc = hip_fail(e, "profiled verify chain");

@@ -129,12 +129,18 @@ hipError_t launch_split_book_i8(const int8_t* book, float scale, int entries, in
 // codes [rows, words] (rows a multiple of 64) -> the tiled layout of ProjDev::codes_t
 hipError_t launch_tile_codes(const uint32_t* codes, int64_t rows, int words, int bits, uint32_t* out, hipStream_t st);
 bool moe_uses_mfma(const LayerDev& L);
+// The MFMA layers' geometry, whatever the scale groups.
+bool moe_uses_mfma_geometry(const LayerDev& L);
 // Mixed layer on the MFMA kernels (both banks prepared); the gate/up kernels of both the
 // uniform and the mixed MFMA paths route and build the plan themselves.
 bool moe_mixed_mfma(const LayerDev& L);
-bool moe_plans_in_gate_up(const LayerDev& L);
-// Verify widths of up to 4 rows on the 4x4x4 MFMA kernels (q38_moe4.hip).
+bool moe_plans_in_gate_up(const LayerDev& L, int M);
+// Verify widths of up to 4 rows on the 4x4x4 MFMA kernels (q38_moe4.hip): the MFMA layers,
+// and d8 layers of the same geometry with per-64-input scale groups. They write one partial-
+// sum plane per codebook chunk (gu_parts / d_parts of the call: moe_call_dev).
 bool moe_uses_narrow(const LayerDev& L, int M);
+// The layer view of a call of M rows: the partial-sum plane counts of the kernels it takes.
+LayerDev moe_call_dev(const LayerDev& L, int M);
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 int mfma_grid();  // persistent workgroups of the expert kernels (a multiple of 32)

@@ -1027,14 +1027,21 @@ bool moe_mixed_mfma(const LayerDev& L) {
     return true;
 }
 
-bool moe_plans_in_gate_up(const LayerDev& L) { return moe_uses_mfma(L) || moe_mixed_mfma(L); }
+bool moe_plans_in_gate_up(const LayerDev& L, int M) {
+    return moe_uses_mfma(L) || moe_mixed_mfma(L) || moe_uses_narrow(L, M);
+}
 
 bool moe_uses_mfma(const LayerDev& L) {
-    if (L.mixed) return false;
-    // MFMA tiles: per-row scales, 128-row tiles, and lane code spans of whole 16-code
-    // half-blocks (gate/up: d8 with H/8 in {256, 320} or d4 with H/4 = 512; down: d8 with
-    // I/8 = 64 or d4 with I/4 = 128).
+    // MFMA tiles: per-row scales and the geometry below
     if (L.p[0].ngrp != 1 || L.p[1].ngrp != 1 || L.p[2].ngrp != 1) return false;
+    return moe_uses_mfma_geometry(L);
+}
+
+bool moe_uses_mfma_geometry(const LayerDev& L) {
+    if (L.mixed) return false;
+    // 128-row tiles, and lane code spans of whole 16-code half-blocks (gate/up: d8 with H/8
+    // in {256, 320} or d4 with H/4 = 512; down: d8 with I/8 = 64 or d4 with I/4 = 128).
+    if (L.p[1].dim != L.p[0].dim || L.p[1].bits != L.p[0].bits) return false;
     if (L.I % kMfmaRowsPerItem || L.H % kMfmaRowsPerItem) return false;
     const int gd = L.p[0].dim, gb = L.p[0].bits, dd = L.p[2].dim, db = L.p[2].bits;
     const bool gu_ok = (gd == 8 && gb == 14 && (L.H == 2048 || L.H == 2560)) || (gd == 4 && gb == 8 && L.H == 2048);

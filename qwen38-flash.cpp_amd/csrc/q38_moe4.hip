@@ -76,6 +76,54 @@ __device__ __forceinline__ v4f_t slice_mfma(const uint32_t* cw, const uint2* boo
     return acc0 + acc1;
 }
 
+// The same 32 steps with one scale per 8 subvectors (64 inputs of d8 codes, the checkpoint
+// layout): the four groups of the slice accumulate separately (t within a group in order,
+// the groups interleaved), then each lane's rows (lane & ~3) + r are scaled per group and
+// the groups added in order: gs[r] holds row r's four fp16 group scales.
+template <int BITS>
+__device__ __forceinline__ v4f_t slice_mfma_g8(const uint32_t* cw, const uint2* book, const uint2* bops,
+                                               const uint2 (&gs)[4]) {
+    v4f_t acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint2 a = book[code_from<BITS>(cw, 8 * g + t)];
+            acc[g] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4_t, a),
+                                                        __builtin_bit_cast(h4_t, bops[8 * g + t]), acc[g], 0, 0, 0);
+        }
+    v4f_t out;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint16_t s4[4] = {static_cast<uint16_t>(gs[r].x), static_cast<uint16_t>(gs[r].x >> 16),
+                                static_cast<uint16_t>(gs[r].y), static_cast<uint16_t>(gs[r].y >> 16)};
+        float v = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) v = fmaf(h2f(s4[g]), acc[g][r], v);
+        out[r] = v;
+    }
+    return out;
+}
+
+// Scales an item needs. Per row (G8 = 0): k_gu4 keeps the aligned word holding its output
+// thread's row scale, k_dn4 the four rows' scales of its output lanes. Per group (G8 = 8):
+// the lane's rows (lane & ~3) + 0..3, the four groups of its wave's K slice.
+template <int G8>
+struct ItemScales {
+    uint2 g[4];
+};
+template <>
+struct ItemScales<0> {
+    uint2 w;
+};
+// Group scales of rows row0 + (lane & ~3) + 0..3, groups g0 .. g0 + 3 ([rows, ngrp] fp16).
+__device__ __forceinline__ void load_group_scales(const uint16_t* scales, size_t row0, int lane, int ngrp, int g0,
+                                                  uint2 (&gs)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        gs[r] = *reinterpret_cast<const uint2*>(scales + (row0 + (lane & ~3) + r) * ngrp + g0);
+}
+
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Gate and up projections. Workgroup type = (projection, codebook chunk); waves = K slices.
@@ -94,7 +142,7 @@ constexpr size_t gu4_lds_bytes() {
     return (size_t{1} << BITS) * 8 + 2 * (NSUB / 32) * 64 * 16;
 }
 
-template <int BITS, int NSUB, int NCHUNK, int D>
+template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
 __global__ __launch_bounds__(2 * NSUB) __attribute__((amdgpu_waves_per_eu(1, (NSUB / 32 + 3) / 4)))
 void k_gu4(LayerDev L, MoeBufs B, int M) {
     constexpr int KS = NSUB / 32;
@@ -183,17 +231,21 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     // unconditionally (past the end: the last item again, an L2 hit), so the compiler counts
     // them exactly and item k waits only for its own.
     const int my_n = n_items > idx ? (n_items - idx + per_type - 1) / per_type : 0;
-    auto load_item = [&](int j, uint32_t* cw, uint32_t& sc) {
+    auto load_item = [&](int j, uint32_t* cw, ItemScales<G8>& sc) {
         const int item = my_n > 0 ? idx + (j < my_n ? j : my_n - 1) * per_type : 0;
         const int expert = item_expert(item);
         const size_t row = static_cast<size_t>(expert) * I + (item % tiles) * 64;
         load_code_block_tiled<BITS>(P.codes_t + ((row >> 6) * KS + wave) * (BITS * 64), lane, cw);
-        // the aligned 32-bit word holding the row's fp16 scale (no 16-bit load to widen)
-        sc = *reinterpret_cast<const uint32_t*>(P.scales + ((row + r_out) & ~size_t{1}));
+        if constexpr (G8 == 0) {
+            // the aligned 32-bit word holding the row's fp16 scale (no 16-bit load to widen)
+            sc.w.x = *reinterpret_cast<const uint32_t*>(P.scales + ((row + r_out) & ~size_t{1}));
+        } else {
+            load_group_scales(P.scales, row, lane, P.ngrp, wave * (32 / G8), sc.g);
+        }
     };
     constexpr int PF = D < 3 ? D : 3;  // items in flight
     uint32_t cw[PF][BITS + 1];
-    uint32_t sc[PF];
+    ItemScales<G8> sc[PF];
 #pragma unroll
     for (int k = 0; k < PF; ++k) load_item(k, cw[k], sc[k]);  // (no items: item 0, unused)
     uint2 xb[32];
@@ -212,10 +264,12 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     //    the compute. Items past D (more per workgroup than the launch planned) take a loop.
     //    Output thread tid < 256: weight row r_out of the tile x request row tid & 3.
     float* out = (proj == 0 ? B.g : B.u) + chunk * B.gu_plane;
-    auto item_compute = [&](int j, const uint32_t* cwj, uint32_t scj, float& ov, int& oat) {
+    auto item_compute = [&](int j, const uint32_t* cwj, const ItemScales<G8>& scj, float& ov, int& oat) {
         const int item = idx + j * per_type;
         const int buf = j & 1;
-        const v4f_t acc = slice_mfma<BITS>(cwj, book, xb);
+        v4f_t acc;
+        if constexpr (G8 == 0) acc = slice_mfma<BITS>(cwj, book, xb);
+        else acc = slice_mfma_g8<BITS>(cwj, book, xb, scj.g);
         reinterpret_cast<v4f_t*>(red)[(buf * KS + wave) * 64 + lane] = acc;
         lds_barrier();  // (the other buffer's readers passed the previous item's barrier)
         oat = -1;
@@ -227,7 +281,8 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
                 float s = 0.0f;
 #pragma unroll
                 for (int w = 0; w < KS; ++w) s += red[((buf * KS + w) * 64 + src) * 4 + reg];
-                ov = h2f(static_cast<uint16_t>(scj >> (16 * (r_out & 1)))) * s;
+                if constexpr (G8 == 0) ov = h2f(static_cast<uint16_t>(scj.w.x >> (16 * (r_out & 1)))) * s;
+                else ov = s;  // (the group scales are applied in the slices)
                 oat = pos * I + (item % tiles) * 64 + r_out;
             }
         }
@@ -245,7 +300,8 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     for (int k = 0; k < D; ++k)
         if (oat[k] >= 0) out[oat[k]] = ov[k];
     for (int jj = D; jj < my_n; ++jj) {
-        uint32_t c1[BITS + 1], s1;
+        uint32_t c1[BITS + 1];
+        ItemScales<G8> s1;
         load_item(jj, c1, s1);
         float o1;
         int a1;
@@ -262,7 +318,7 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
 // items are (slot, TR = 64 RG rows of H). The B columns are the slot's routes: their SwiGLU
 // rows (this chunk's dims, fp16) are formed per item from the gate/up chunk planes, which
 // are requested with the item's code spans, D items ahead.
-template <int BITS, int NSUB, int NCHUNK, int D>
+template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_dn4(LayerDev L, MoeBufs B, int M) {
     constexpr int KS = NSUB / 32, RG = 8 / KS, TR = 64 * RG;
     constexpr int NT = 512, KENT = 1 << BITS;
@@ -333,12 +389,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             u[q][1] = B.u[(two ? B.gu_plane : 0) + at];
         }
     };
-    // row scales of the output lanes (kh == 0): rows (lane & ~3) + 0..3 of the row group
-    auto load_sc = [&](int item, uint2& sc) {
+    // row scales of the output lanes (kh == 0): rows (lane & ~3) + 0..3 of the row group; or
+    // the group scales of every lane's rows for its wave's K slice
+    auto load_sc = [&](int item, ItemScales<G8>& sc) {
         const int ui = item / tiles;
         const int expert = ui < nu ? plan[1 + ui] : L.E;
-        sc = *reinterpret_cast<const uint2*>(P.scales + static_cast<size_t>(expert) * H + (item % tiles) * TR +
-                                             rg * 64 + (lane & ~3));
+        const size_t row0 = static_cast<size_t>(expert) * H + (item % tiles) * TR + rg * 64;
+        if constexpr (G8 == 0) sc.w = *reinterpret_cast<const uint2*>(P.scales + row0 + (lane & ~3));
+        else load_group_scales(P.scales, row0, lane, P.ngrp, kh * (32 / G8), sc.g);
     };
     // Items j = idx + j * per_type (j < my_n); loads are unconditional (past the end: the last
     // item again) so the compiler counts them exactly.
@@ -347,7 +405,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     constexpr int PF = D;  // items in flight (all: the item loads are the ones that wait longest)
     uint32_t cw[PF][BITS + 1];
     float gq[PF][GQ][2], uq[PF][GQ][2];
-    uint2 sc[PF];
+    ItemScales<G8> sc[PF];
     auto load_slot = [&](int j, int k) {
         const int it = item_of(j);
         load_code_block_tiled<BITS>(code_src(it), lane, cw[k]);
@@ -369,7 +427,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     //    0..3 of the row group x route lane & 3.
     float* dout = B.d + chunk * B.d_plane;
     auto item_compute = [&](int jj, const uint32_t* cwj, const float (&g2)[GQ][2], const float (&u2)[GQ][2],
-                            uint2 scj, float (&o4)[4], int& oroute, int& obase) {
+                            const ItemScales<G8>& scj, float (&o4)[4], int& oroute, int& obase) {
         const int item = idx + jj * per_type;
         int expert, n, pos0;
         const int ui = item / tiles;
@@ -392,7 +450,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             bop[t] = make_uint2(v2.x, v2.y);
             bop[t + 1] = make_uint2(v2.z, v2.w);
         }
-        v4f_t acc = slice_mfma<BITS>(cwj, book, bop);
+        v4f_t acc;
+        if constexpr (G8 == 0) acc = slice_mfma<BITS>(cwj, book, bop);
+        else acc = slice_mfma_g8<BITS>(cwj, book, bop, scj.g);
         if (kh > 0) reinterpret_cast<v4f_t*>(red)[(rg * (KS - 1) + kh - 1) * 64 + lane] = acc;
         lds_barrier();  // (the next item's SwiGLU rows are written after this barrier)
         oroute = -1;
@@ -404,10 +464,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             if (jr < n) {
                 oroute = ui == nu ? MK + jr : plan[2 + 2 * MK + pos0 + jr];
                 obase = (item % tiles) * TR + rg * 64 + (lane & ~3);
-                const uint16_t s4[4] = {static_cast<uint16_t>(scj.x), static_cast<uint16_t>(scj.x >> 16),
-                                        static_cast<uint16_t>(scj.y), static_cast<uint16_t>(scj.y >> 16)};
+                if constexpr (G8 == 0) {
+                    const uint16_t s4[4] = {static_cast<uint16_t>(scj.w.x), static_cast<uint16_t>(scj.w.x >> 16),
+                                            static_cast<uint16_t>(scj.w.y), static_cast<uint16_t>(scj.w.y >> 16)};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) o4[r] = h2f(s4[r]) * acc[r];
+                    for (int r = 0; r < 4; ++r) o4[r] = h2f(s4[r]) * acc[r];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) o4[r] = acc[r];
+                }
             }
         }
     };
@@ -429,7 +494,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         const int it = item_of(jj);
         uint32_t c1[BITS + 1];
         float g1[GQ][2], u1[GQ][2];
-        uint2 s1;
+        ItemScales<G8> s1;
         load_code_block_tiled<BITS>(code_src(it), lane, c1);
         load_gu(it, g1, u1);
         load_sc(it, s1);
@@ -446,28 +511,50 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #endif
 }
 
-template <int BITS, int NSUB, int NCHUNK, int D>
+template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
 hipError_t launch_gu4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     constexpr size_t lds = gu4_lds_bytes<BITS, NSUB, NCHUNK>();
-    if (const hipError_t e = ensure_lds<k_gu4<BITS, NSUB, NCHUNK, D>>(lds); e != hipSuccess) return e;
-    return launch(k_gu4<BITS, NSUB, NCHUNK, D>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
+    if (const hipError_t e = ensure_lds<k_gu4<BITS, NSUB, NCHUNK, D, G8>>(lds); e != hipSuccess) return e;
+    return launch(k_gu4<BITS, NSUB, NCHUNK, D, G8>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
 }
-template <int BITS, int NSUB, int NCHUNK, int D>
+template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
 hipError_t launch_dn4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     constexpr int KS = NSUB / 32, RG = 8 / KS;
     constexpr size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(RG) * (KS - 1) * 64 * 16;
-    if (const hipError_t e = ensure_lds<k_dn4<BITS, NSUB, NCHUNK, D>>(lds); e != hipSuccess) return e;
-    return launch(k_dn4<BITS, NSUB, NCHUNK, D>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M);
+    if (const hipError_t e = ensure_lds<k_dn4<BITS, NSUB, NCHUNK, D, G8>>(lds); e != hipSuccess) return e;
+    return launch(k_dn4<BITS, NSUB, NCHUNK, D, G8>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M);
 }
+
+// Scales the four-row kernels take: one per output row, or one per 64 inputs for the d8
+// gate/up projections of H / 8 = 256 subvectors and the d8 down projection (the layout of the
+// reference's checkpoints, src/sparse_moe.cpp:641-647).
+bool gu_groups64(const LayerDev& L) {
+    return L.p[0].dim == 8 && L.H / 8 == 256 && L.p[0].ngrp == L.H / 64 && L.p[1].ngrp == L.H / 64;
+}
+bool dn_groups64(const LayerDev& L) { return L.p[2].dim == 8 && L.p[2].ngrp == L.I / 64; }
 } // namespace
 
 bool moe_uses_narrow(const LayerDev& L, int M) {
-    if (M < 1 || M > kNarrow || L.E != 512 || !moe_uses_mfma(L)) return false;
+    if (M < 1 || M > kNarrow || L.E != 512 || L.mixed) return false;
     if (M * L.K > 64) return false;  // the plan is built by one wave
+    // the MFMA layers' geometry (moe_uses_mfma), with per-64-input scale groups allowed
+    const bool rows = L.p[0].ngrp == 1 && L.p[1].ngrp == 1 && L.p[2].ngrp == 1;
+    if (rows ? !moe_uses_mfma(L) : !(moe_uses_mfma_geometry(L) && (L.p[0].ngrp == 1 ? L.p[1].ngrp == 1 : gu_groups64(L)) &&
+                                     (L.p[2].ngrp == 1 || dn_groups64(L))))
+        return false;
     const int gn = L.H / L.p[0].dim, dn = L.I / L.p[2].dim;
     const bool gu = (L.p[0].dim == 8 && (gn == 256 || gn == 320)) || (L.p[0].dim == 4 && gn == 512);
     const bool dw = (L.p[2].dim == 8 && dn == 64) || (L.p[2].dim == 4 && dn == 128);
     return gu && dw && L.I % 64 == 0 && L.H % 256 == 0;
+}
+
+LayerDev moe_call_dev(const LayerDev& L, int M) {
+    LayerDev d = L;
+    if (moe_uses_narrow(L, M)) {
+        d.gu_parts = L.p[0].dim / 4;
+        d.d_parts = L.p[2].dim / 4;
+    }
+    return d;
 }
 
 // Ring depth: the most items one workgroup can get (every route on its own expert, plus the
@@ -482,6 +569,14 @@ hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream
     const int nsub = L.H / L.p[0].dim;
     if (!L.p[0].codes_t || !L.p[1].codes_t) return hipErrorInvalidValue;
     const int grid = mfma_grid();
+    if (L.p[0].dim == 8 && nsub == 256 && gu_groups64(L)) {
+        const int c = ring_items(L, M, L.I / 64, grid / 32 * 8);
+        if (c <= 2) return launch_gu4_t<14, 256, 2, 2, 8>(L, B, M, st);
+        if (c <= 3) return launch_gu4_t<14, 256, 2, 3, 8>(L, B, M, st);
+        if (c <= 4) return launch_gu4_t<14, 256, 2, 4, 8>(L, B, M, st);
+        return launch_gu4_t<14, 256, 2, 6, 8>(L, B, M, st);
+    }
+    if (L.p[0].ngrp != 1 || L.p[1].ngrp != 1) return hipErrorInvalidValue;
     if (L.p[0].dim == 8 && nsub == 256) {
         const int c = ring_items(L, M, L.I / 64, grid / 32 * 8);
         if (c <= 2) return launch_gu4_t<14, 256, 2, 2>(L, B, M, st);
@@ -506,6 +601,13 @@ hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t 
     const int nsub = L.I / L.p[2].dim;
     if (!L.p[2].codes_t) return hipErrorInvalidValue;
     const int grid = mfma_grid();
+    if (L.p[2].dim == 8 && nsub == 64 && dn_groups64(L)) {
+        const int c = ring_items(L, M, L.H / 256, grid / 16 * 8);
+        if (c <= 1) return launch_dn4_t<14, 64, 2, 1, 8>(L, B, M, st);
+        if (c <= 2) return launch_dn4_t<14, 64, 2, 2, 8>(L, B, M, st);
+        return launch_dn4_t<14, 64, 2, 3, 8>(L, B, M, st);
+    }
+    if (L.p[2].ngrp != 1) return hipErrorInvalidValue;
     if (L.p[2].dim == 8 && nsub == 64) {
         const int c = ring_items(L, M, L.H / 256, grid / 16 * 8);
         if (c <= 1) return launch_dn4_t<14, 64, 2, 1>(L, B, M, st);

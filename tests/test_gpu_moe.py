@@ -31,6 +31,36 @@ def test_config0_layer(layer0, q38, orc, M):
     tol_check(orc, y, wy)
 
 
+@pytest.fixture(scope="module")
+def layer_g64(gpu, q38):
+    L = q38.MoeLayer(gpu, q38.desc(gu_group=64, down_group=64), seed=SEED, layer=5)
+    yield L
+    L.close()
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16])
+def test_group64_layer(layer_g64, q38, orc, M):
+    """One fp16 scale per 64 inputs (the reference checkpoints' layout) on the config-0
+    geometry: rows 1-4 take the four-row MFMA kernels, which scale each K slice's four group
+    partial sums; 16 rows take the grouped VALU kernels. Routing bit-exact, outputs within
+    the MoE tolerance of the oracle."""
+    x = orc.normal(orc.key(SEED, 5, 20), 31 * M, M * 2048, 1.0).reshape(M, 2048)
+    y, ex, wt, lg, plan = run_forward(q38, layer_g64, layer_g64.desc, x)
+    wy, wex, wwt, wlg = orc.moe_layer_synth(oracle_lib.make_desc(gu_group=64, down_group=64), SEED, 5, x)
+    assert np.array_equal(lg, wlg) and np.array_equal(ex, wex) and np.array_equal(wt, wwt)
+    plan_check(orc, plan, ex, 512)
+    tol_check(orc, y, wy)
+
+
+def test_group64_narrow_matches_grouped_kernels(layer_g64, q38, orc):
+    """The same four rows through the four-row kernels (a 4-row call) and the grouped VALU
+    kernels (rows 0-3 of a 5-row call) agree within the MoE tolerance."""
+    x = orc.normal(orc.key(SEED, 5, 21), 3, 5 * 2048, 1.0).reshape(5, 2048)
+    y4 = run_forward(q38, layer_g64, layer_g64.desc, x[:4])[0]
+    y5 = run_forward(q38, layer_g64, layer_g64.desc, x)[0]
+    tol_check(orc, y4, y5[:4])
+
+
 @pytest.mark.parametrize("M", [4, 16])
 def test_fp16_operand_extremes(layer0, q38, orc, M):
     """The expert kernels take x as an fp16 MFMA operand. RMSNorm outputs with one spike

@@ -1,6 +1,6 @@
 """q38_verify_chain_profiled: every phase kernel is timed (start at the phase's first kernel,
 stop at its last), on uniform, mixed (two bank kernels per phase) and per-64-input scale
-group (VALU kernels) stacks; the profiled pass computes the same values as the plain one."""
+group stacks; the profiled pass computes the same values as the plain one."""
 import ctypes as C
 
 import numpy as np
@@ -12,7 +12,7 @@ from moe_cases import SEED
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("kind,M", [("uniform", 4), ("uniform", 1), ("mixed", 16), ("group64", 4)])
+@pytest.mark.parametrize("kind,M", [("uniform", 4), ("uniform", 1), ("mixed", 16), ("group64", 4), ("group64", 8)])
 def test_profiled_chain(gpu, q38, orc, kind, M):
     import torch
     d = {"uniform": q38.desc(), "mixed": q38.desc(mixed=1), "group64": q38.desc(gu_group=64, down_group=64)}[kind]
