@@ -287,6 +287,17 @@ int q38_head_greedy(q38_head* head, const uint16_t* h, int32_t rows, uint32_t* a
 int q38_head_logits(q38_head* head, const uint16_t* h, int32_t rows, float* logits, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* Softmax of the head's logits at temperature T > 0: the probabilities sampling reads
+ * (logits.softmax_axis(-1), src/native_engine.cpp:116-118, at T = 1; the tempered target and
+ * draft distributions of rejection sampling otherwise). Per row, stats [rows][2] = (max
+ * logit, sum over the vocabulary of exp((l - max) / T)), summed in a fixed order; when probs
+ * (device [rows, V] float) is given it receives exp((l - max) / T) / sum, and the logits are
+ * computed into it first. Rows as for q38_head_logits (Q8: 1..16, Q4: 1..4); workspace:
+ * q38_head_probs_workspace_size bytes. */
+size_t q38_head_probs_workspace_size(const q38_head* head, int32_t max_rows);
+int q38_head_probs(q38_head* head, const uint16_t* h, int32_t rows, float temperature, float* probs, float* stats,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* greedy_from_logits (src/mtp_verifier.cpp:20-55) on device logits [rows, vocab] float:
  * per row the argmax, lowest index on ties (src/mlx_backend.cpp:78-85), and its value.
  * argmax, value: device [rows] (value may be null); rows 1..64; workspace: device, at least

@@ -3,6 +3,8 @@
 // Q38_E* code and leaves outputs untouched.
 #include "q38.h"
 
+#include <cmath>
+
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
 #include "q38_private.h"
@@ -1047,6 +1049,39 @@ int q38_head_logits(q38_head* hd, const uint16_t* h, int32_t rows, float* logits
         return fail(Q38_EINVAL, "Q4 head rows must be between 1 and 4 per call");
     }
     Q38_HIP(launch_head_logits(hd->dev, h, rows, w, logits, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+// q38_head_probs: [head logits workspace | logits (when probs is null) | softmax partials]
+static size_t head_probs_layout(const q38_head* hd, int rows, size_t* logits_off, size_t* part_off) {
+    const size_t hw = align256(q38_head_workspace_size(hd, rows));
+    const size_t lg = align256(static_cast<size_t>(rows) * static_cast<size_t>(hd->dev.V) * 4);
+    if (logits_off) *logits_off = hw;
+    if (part_off) *part_off = hw + lg;
+    return hw + lg + softmax_rows_workspace(rows, hd->dev.V);
+}
+
+size_t q38_head_probs_workspace_size(const q38_head* hd, int32_t max_rows) {
+    if (!hd || max_rows < 1 || q38_head_workspace_size(hd, max_rows) == 0) return 0;
+    return head_probs_layout(hd, max_rows, nullptr, nullptr);
+}
+
+int q38_head_probs(q38_head* hd, const uint16_t* h, int32_t rows, float temperature, float* probs, float* stats,
+                   void* ws, size_t ws_bytes, void* stream) {
+    if (!hd || !h || !stats) return fail(Q38_EINVAL, "q38_head_probs: null argument");
+    if (!(temperature > 0.0f) || !std::isfinite(temperature))
+        return fail(Q38_EINVAL, "q38_head_probs: temperature must be positive and finite");
+    if (q38_head_workspace_size(hd, rows) == 0)
+        return fail(Q38_EINVAL, hd->dev.kind == Q38_HEAD_Q8 ? "head rows must be between 1 and 16 per call"
+                                                            : "Q4 head rows must be between 1 and 4 per call");
+    size_t lo = 0, po = 0;
+    const size_t need = head_probs_layout(hd, rows, &lo, &po);
+    if (!ws || ws_bytes < need) return fail(Q38_ESPACE, "workspace too small");
+    char* base = static_cast<char*>(ws);
+    float* logits = probs ? probs : reinterpret_cast<float*>(base + lo);
+    if (int rc = q38_head_logits(hd, h, rows, logits, ws, lo, stream)) return rc;
+    Q38_HIP(launch_softmax_rows(logits, rows, hd->dev.V, temperature, stats, probs, base + po,
+                                static_cast<hipStream_t>(stream)));
     return Q38_OK;
 }
 

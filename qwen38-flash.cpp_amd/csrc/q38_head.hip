@@ -859,4 +859,53 @@ hipError_t launch_accept_sampled(const float* tl, const float* dl, const uint32_
     return e;
 }
 
+namespace {
+// Softmax rows: per row the chunk partials (k_samp_stats) merged in chunk order into
+// (max, sum of exp((l - max) / T)); then, when asked, the probabilities.
+__global__ __launch_bounds__(64) void k_softmax_stats(const float2* __restrict__ part, int nc, float invT,
+                                                      float* __restrict__ stats) {
+    if (threadIdx.x != 0) return;
+    const int r = blockIdx.x;
+    float m = -INFINITY, s = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+        const float2 v = part[static_cast<size_t>(r) * nc + c];
+        softmax_merge(m, s, v.x, v.y, invT);
+    }
+    stats[2 * r] = m;
+    stats[2 * r + 1] = s;
+}
+
+// probs[r][x] = exp((l[r][x] - max) / T) / sum (0 for a -inf logit); probs may be l.
+__global__ __launch_bounds__(256) void k_softmax_probs(const float* l, int64_t V, int64_t cs, float invT,
+                                                      const float* __restrict__ stats, float* probs) {
+    const int c = blockIdx.x, r = blockIdx.y;
+    const int64_t a = static_cast<int64_t>(c) * cs, b = a + cs < V ? a + cs : V;
+    const float m = stats[2 * r], s = stats[2 * r + 1];
+    for (int64_t x = a + threadIdx.x; x < b; x += 256) {
+        const float v = l[static_cast<int64_t>(r) * V + x];
+        probs[static_cast<int64_t>(r) * V + x] = v > -INFINITY ? expf((v - m) * invT) / s : 0.0f;
+    }
+}
+} // namespace
+
+size_t softmax_rows_workspace(int rows, int64_t V) {
+    const int nc = static_cast<int>(std::min<int64_t>(kSampChunks, (V + 255) / 256));
+    return a256(static_cast<size_t>(rows) * nc * sizeof(float2));
+}
+
+hipError_t launch_softmax_rows(const float* logits, int rows, int64_t V, float T, float* stats, float* probs, void* ws,
+                               hipStream_t st) {
+    const int nc = static_cast<int>(std::min<int64_t>(kSampChunks, (V + 255) / 256));
+    const int64_t cs = (V + nc - 1) / nc;
+    const float invT = 1.0f / T;
+    auto* part = static_cast<float2*>(ws);
+    hipError_t e = launch(k_samp_stats, dim3(nc, rows), dim3(256), 0, st, logits, logits, rows - 1, V, cs, invT, part);
+    if (e == hipSuccess)
+        e = launch(k_softmax_stats, dim3(rows), dim3(64), 0, st, static_cast<const float2*>(part), nc, invT, stats);
+    if (e == hipSuccess && probs)
+        e = launch(k_softmax_probs, dim3(nc, rows), dim3(256), 0, st, logits, V, cs, invT,
+                   static_cast<const float*>(stats), probs);
+    return e;
+}
+
 } // namespace q38

@@ -213,6 +213,12 @@ hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long lo
 // acceptance
 // k <= 24; ws: accept_sampled_workspace(k, V) bytes.
 size_t accept_sampled_workspace(int k, int64_t V);
+// Softmax of rows [rows, V] float at temperature T: stats [rows][2] = (max, sum of
+// exp((l - max) / T)) and, when probs is given (it may be logits), the probabilities.
+// ws: softmax_rows_workspace(rows, V) bytes.
+size_t softmax_rows_workspace(int rows, int64_t V);
+hipError_t launch_softmax_rows(const float* logits, int rows, int64_t V, float T, float* stats, float* probs, void* ws,
+                               hipStream_t st);
 hipError_t launch_accept_sampled(const float* tl, const float* dl, const uint32_t* drafts, int k, int64_t V,
                                  float T, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out, void* ws,
                                  hipStream_t st);

@@ -382,6 +382,41 @@ MtpTargetVerification verify_mtp_target_layer_major_reference(const QwenModel& m
     return v;
 }
 
+MtpTargetVerification verify_mtp_target_serial_oracle(const QwenModel& model, std::uint32_t current_token,
+                                                      std::span<const std::uint32_t> drafts, ModelDecodeState& origin) {
+    if (drafts.empty()) throw std::runtime_error("MTP verification requires at least one draft");
+    std::vector<std::uint32_t> tokens;
+    tokens.reserve(drafts.size() + 1);
+    tokens.push_back(current_token);
+    tokens.insert(tokens.end(), drafts.begin(), drafts.end());
+    const std::size_t H = model.hidden(), n = tokens.size();
+    const auto st = static_cast<hipStream_t>(model.context().stream());
+    DeviceTensor all({1, n, H}, DType::bf16);  // the rows' final hidden states, staged below
+    MtpTargetVerification v;
+    v.draft_count = drafts.size();
+    v.origin = &origin;
+    const std::size_t base = origin.token_count();
+    for (std::size_t i = 0; i < n; ++i) {
+        // (in the verify model a row's decode reads only its own token: no attention state)
+        MtpTargetVerifyRow row;
+        std::vector<GreedyStep> greedy;
+        model.forward_verify_layer_major(std::span<const std::uint32_t>(&tokens[i], 1), row.final_mixed, greedy,
+                                         nullptr, &row.pre_mixer_stream);
+        row.greedy = greedy.at(0);
+        check_hip(hipMemcpyAsync(static_cast<char*>(all.data()) + i * H * 2, row.final_mixed.data(), H * 2,
+                                 hipMemcpyDeviceToDevice, st),
+                  "serial verification row");
+        row.state_after = base + i + 1;
+        v.rows.push_back(std::move(row));
+    }
+    check(q38_slot_stage(origin.slot(), static_cast<int32_t>(drafts.size()), static_cast<const uint16_t*>(all.data()),
+                         model.context().stream()),
+          "verification checkpoints");
+    v.generation = q38_slot_generation(origin.slot());
+    model.context().synchronize();
+    return v;
+}
+
 void commit_mtp_target_verification(MtpTargetVerification&& verification, std::size_t accepted,
                                     ModelDecodeState& destination) {
     if (verification.rows.size() != verification.draft_count + 1)

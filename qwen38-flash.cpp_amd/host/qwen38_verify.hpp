@@ -249,6 +249,15 @@ struct MtpTargetVerification {
     std::uint64_t generation{0};         // the slot's staging generation of these rows
 };
 
+// The correctness oracle of the verification (include/qwen38/mtp_verifier.hpp:27-31,
+// src/mtp_verifier.cpp:59-82): one target decode per row, each row's state built on the
+// previous one; the rows are staged as checkpoints like the layer-major pass's. For up to
+// four rows (one kernel family) its results equal the layer-major pass's bit for bit.
+[[nodiscard]] MtpTargetVerification verify_mtp_target_serial_oracle(const QwenModel& model,
+                                                                   std::uint32_t current_token,
+                                                                   std::span<const std::uint32_t> drafts,
+                                                                   ModelDecodeState& origin);
+
 [[nodiscard]] MtpTargetVerification verify_mtp_target_layer_major_reference(const QwenModel& model,
                                                                            std::uint32_t current_token,
                                                                            std::span<const std::uint32_t> drafts,

@@ -108,6 +108,8 @@ _sig("q38_head_bytes", I64, P)
 _sig("q38_head_workspace_size", SZ, P, I32)
 _sig("q38_head_greedy", C.c_int, P, P, I32, P, P, P, SZ, P)
 _sig("q38_head_logits", C.c_int, P, P, I32, P, P, SZ, P)
+_sig("q38_head_probs_workspace_size", SZ, P, I32)
+_sig("q38_head_probs", C.c_int, P, P, I32, C.c_float, P, P, P, SZ, P)
 _sig("q38_argmax_rows", C.c_int, P, I32, I64, P, P, P, SZ, P)
 
 

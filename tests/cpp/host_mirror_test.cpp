@@ -462,6 +462,27 @@ static void gpu_tests() {
     qwen38::commit_mtp_target_verification(std::move(v3), 2, state);
     CHECK(v3.rows.empty() && state.token_count() == 105);
 
+    // the serial oracle (one decode per row) gives the layer-major rows bit for bit (up to
+    // four rows: one kernel family) and stages checkpoints that commit the same way
+    {
+        auto lm = qwen38::verify_mtp_target_layer_major_reference(model, 5, drafts, state);
+        auto so = qwen38::verify_mtp_target_serial_oracle(model, 5, drafts, state);
+        CHECK(so.draft_count == 3 && so.rows.size() == 4 && so.generation > lm.generation);
+        for (std::size_t i = 0; i < 4; ++i) {
+            CHECK(so.rows[i].greedy.token == lm.rows[i].greedy.token);
+            CHECK(so.rows[i].greedy.logit == lm.rows[i].greedy.logit);
+            CHECK(so.rows[i].state_after == lm.rows[i].state_after);
+            CHECK(so.rows[i].final_mixed.to_host<std::uint16_t>() == lm.rows[i].final_mixed.to_host<std::uint16_t>());
+            CHECK(so.rows[i].pre_mixer_stream.to_host<std::uint16_t>() ==
+                  lm.rows[i].pre_mixer_stream.to_host<std::uint16_t>());
+        }
+        CHECK(throws<std::runtime_error>([&] {
+            (void)qwen38::verify_mtp_target_serial_oracle(model, 5, std::vector<std::uint32_t>{}, state);
+        }));
+        qwen38::commit_mtp_target_verification(std::move(so), 1, state);
+        CHECK(state.token_count() == 107);
+    }
+
     // a full external-draft round with the target's own greedy continuation as drafts
     const std::uint32_t cur = 11;
     std::vector<std::uint32_t> greedy_drafts;

@@ -223,3 +223,70 @@ def test_head_planes_wide_dynamic_range(gpu, q38, orc):
         assert np.array_equal(am, wi) and np.array_equal(lg, wv)
     finally:
         hd.close()
+
+
+def head_probs(q38, hd, h_np, T, with_probs=True):
+    M = h_np.shape[0]
+    h = G.to_dev(h_np)
+    probs = G.empty((M, hd.vocab), np.float32) if with_probs else None
+    stats = G.empty((M, 2), np.float32)
+    ws = G.workspace(q38.lib.q38_head_probs_workspace_size(hd.h, M))
+    q38.check(q38.lib.q38_head_probs(hd.h, h.data_ptr(), M, T, probs.data_ptr() if with_probs else None,
+                                     stats.data_ptr(), ws.data_ptr(), ws.numel(), G.stream()))
+    return (G.to_host(probs) if with_probs else None), G.to_host(stats)
+
+
+def softmax64(L, T):
+    z = (L.astype(np.float64) - L.max(axis=1, keepdims=True)) / T
+    e = np.exp(z)
+    return e / e.sum(axis=1, keepdims=True), e.sum(axis=1)
+
+
+@pytest.mark.parametrize("kind,rows", [("q8", 4), ("q4", 3)])
+@pytest.mark.parametrize("T", [1.0, 0.7])
+def test_head_probs_full_vocab(gpu, q38, orc, kind, rows, T):
+    """q38_head_probs: the softmax of the head's own logits (q38_head_logits), against a float64
+    softmax of those logits; the per-row max is the logits' max bit for bit, the probabilities
+    sum to 1, and the stats-only call gives the same stats."""
+    k = q38.Q38_HEAD_Q8 if kind == "q8" else q38.Q38_HEAD_Q4G64
+    hd = q38.Head(gpu, k, 151936, 2048, seed=SEED)
+    try:
+        h = orc.rmsnorm(orc.embed(SEED, list(range(30, 30 + rows)), 2048))
+        L = logits(q38, hd, h)
+        p, st = head_probs(q38, hd, h, T)
+        want, wsum = softmax64(L, T)
+        assert np.array_equal(st[:, 0], L.max(axis=1))
+        assert np.allclose(st[:, 1], wsum, rtol=1e-5, atol=0)
+        assert np.abs(p - want).max() <= 1e-5 * want.max()
+        assert np.allclose(p.sum(axis=1, dtype=np.float64), 1.0, atol=1e-4)
+        _, st2 = head_probs(q38, hd, h, T, with_probs=False)
+        assert np.array_equal(st2.view(np.uint32), st.view(np.uint32))
+    finally:
+        hd.close()
+
+
+def test_head_probs_closed_forms_and_rejects(gpu, q38):
+    """h = 0 gives equal logits: every probability 1 / V, stats (0, V). Temperatures that are
+    not positive and finite, and row counts past the head's limit, are rejected."""
+    rng = np.random.default_rng(13)
+    V, H = 3000, 2048
+    W = rng.integers(-127, 128, (V, H)).astype(np.int8)
+    s = f16(rng.uniform(1e-4, 1e-3, V))
+    hd = explicit_head(q38, gpu, W, s)
+    try:
+        p, st = head_probs(q38, hd, np.zeros((2, H), np.uint16), 0.5)
+        assert np.allclose(p, 1.0 / V, rtol=1e-6) and st[:, 0].tolist() == [0.0, 0.0]
+        assert np.allclose(st[:, 1], V, rtol=1e-6)
+        h = G.to_dev(np.zeros((2, H), np.uint16))
+        stats = G.empty((17, 2), np.float32)
+        ws = G.workspace(q38.lib.q38_head_probs_workspace_size(hd.h, 16))
+        for T in (0.0, -1.0, float("nan"), float("inf")):
+            assert q38.lib.q38_head_probs(hd.h, h.data_ptr(), 2, T, None, stats.data_ptr(), ws.data_ptr(),
+                                          ws.numel(), G.stream()) == q38.Q38_EINVAL
+        assert q38.lib.q38_head_probs(hd.h, h.data_ptr(), 17, 1.0, None, stats.data_ptr(), ws.data_ptr(),
+                                      ws.numel(), G.stream()) == q38.Q38_EINVAL
+        assert q38.lib.q38_head_probs(hd.h, h.data_ptr(), 2, 1.0, None, stats.data_ptr(), ws.data_ptr(), 64,
+                                      G.stream()) == q38.Q38_ESPACE
+        assert q38.lib.q38_head_probs_workspace_size(hd.h, 17) == 0
+    finally:
+        hd.close()
