@@ -197,6 +197,61 @@ __device__ __forceinline__ double wave_sum_xor(double v) {
     v = v + xor_lane_d<1>(v);
     return v;
 }
+// wave_sum_xor of N values (N a power of two, 2..16), reduced and scattered: the xor-32 step
+// swaps the upper half of value i with the lower half of value i + N/2 (one lane swap and
+// one add per pair), the xor-16 step does the same for 16-lane rows when two or more values
+// are left, and the steps inside a row are DPP adds (row rotations by 8 and by 4, which equal
+// the xor partners once the previous step has made the row's halves, quarters, equal; then
+// the two quad permutations). Every add joins the same two partial sums as wave_sum_xor does
+// (float addition commutes exactly), so each total is bit-identical to wave_sum_xor of that
+// value. On return v[s] for s < scatter_slots<N>() holds in lane l the total of input value
+// scatter_value<N>(s, l >> 4); the other entries are dead.
+template <int N>
+__device__ constexpr int scatter_slots() { return N >= 4 ? N / 4 : 1; }
+template <int N>
+__device__ constexpr int scatter_value(int s, int row) {
+    return N >= 4 ? s + (row & 1) * (N / 4) + (row >> 1) * (N / 2) : (N == 2 ? (row >> 1) : 0);
+}
+// one lane per distinct (slot, value): the first lane of each 16-lane row (of each 32-lane
+// half when N = 2; lane 0 for N = 1, a plain wave_sum_xor)
+template <int N>
+__device__ __forceinline__ bool scatter_leader(int lane) {
+    return (lane & (N == 1 ? 63 : N == 2 ? 31 : 15)) == 0;
+}
+template <int N>
+__device__ __forceinline__ void wave_sum_xor_scatter(float (&v)[N]) {
+    static_assert(N >= 2 && N <= 16 && (N & (N - 1)) == 0, "N: a power of two in 2..16");
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + N / 2]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    constexpr int S = scatter_slots<N>();
+    if constexpr (N >= 4) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + N / 4]), false,
+                                                            false);
+            v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+    } else {
+        v[0] = v[0] + xor_lane_f<16>(v[0]);
+    }
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+        v[i] = v[i] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), 0x128, 0xF, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+        v[i] = v[i] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), 0x124, 0xF, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+        v[i] = v[i] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), 0x4E, 0xF, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+        v[i] = v[i] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), 0xB1, 0xF, 0xF, false));
+}
+
 // wave_sum_xor of N independent values, step by step across all of them (the exchanges of
 // one step are in flight together); each result equals wave_sum_xor of that value alone.
 template <int N>

@@ -257,10 +257,15 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
             for (int i = 0; i < 4; ++i) ss[r] = fmaf(v[r][i], v[r][i], ss[r]);
         }
         Q38_STAMPV(0, 4, ss[MR - 1]);
-        wave_sum_xor_n<MR>(ss);
+        if constexpr (MR == 1) {
+            ss[0] = wave_sum_xor(ss[0]);
+            if (lane == 0) red[0][wave] = ss[0];
+        } else {
+            wave_sum_xor_scatter<MR>(ss);
 #pragma unroll
-        for (int r = 0; r < MR; ++r)
-            if (lane == 0) red[r][wave] = ss[r];
+            for (int s = 0; s < scatter_slots<MR>(); ++s)
+                if (scatter_leader<MR>(lane)) red[scatter_value<MR>(s, lane >> 4)][wave] = ss[s];
+        }
         Q38_STAMPV(0, 5, ss[MR - 1]);
         lds_barrier();
         Q38_STAMP(0, 6);
@@ -329,11 +334,15 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
             }
         }
     }
-    wave_sum_xor_n<MR>(acc);
+    // the MR butterflies at once (MR > 1: 16-lane row q of acc[s] ends with request row
+    // scatter_value<MR>(s, q))
+    if constexpr (MR > 1) wave_sum_xor_scatter<MR>(acc);
+    else acc[0] = wave_sum_xor(acc[0]);
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-        const float sres = acc[r];
-        if (lane == 0 && r < M) {
+    for (int s = 0; s < scatter_slots<MR>(); ++s) {
+        const int r = MR > 1 ? scatter_value<MR>(s, lane >> 4) : 0;
+        const float sres = acc[s];
+        if (scatter_leader<MR>(lane) && r < M) {
             if (e < L.E) {
                 B.logits[r * L.E + e] = L.rbias ? rbf(sres) + L.rbias[e] : rbf(sres);
             } else {

@@ -84,17 +84,17 @@ __global__ __launch_bounds__(256) void k_logits_rows(LayerDev L, MoeBufs B, int 
                 }
             }
         }
-        float mine = 0.0f;
+        // the NE butterflies at once: 16-lane row q of acc[s] ends with router row
+        // e0 + scatter_value<NE>(s, q)
+        wave_sum_xor_scatter<NE>(acc);
 #pragma unroll
-        for (int n = 0; n < NE; ++n) {
-            const float s = wave_sum_xor(acc[n]);
-            if (lane == n) mine = s;
-        }
-        const int e = e0 + lane;
-        if (lane < NE && e < nr) {
-            const float lg = rbf(mine);
-            if (e < L.E) B.logits[static_cast<size_t>(r) * L.E + e] = L.rbias ? lg + L.rbias[e] : lg;
-            else B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
+        for (int s = 0; s < scatter_slots<NE>(); ++s) {
+            const int e = e0 + scatter_value<NE>(s, lane >> 4);
+            if ((lane & 15) == 0 && e < nr) {
+                const float lg = rbf(acc[s]);
+                if (e < L.E) B.logits[static_cast<size_t>(r) * L.E + e] = L.rbias ? lg + L.rbias[e] : lg;
+                else B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
+            }
         }
         if (store_x) {
 #pragma unroll
