@@ -409,6 +409,56 @@ const uint16_t* q38_slot_hidden(const q38_slot* slot);
  * reference consumes the verification's own rows, src/mtp_verifier.cpp:129-145). */
 uint64_t q38_slot_generation(const q38_slot* slot);
 
+/* ------------------------------------------------------------------ HyperConnection mixer
+ * The stream mixer around a decoder block (HyperConnection, include/qwen38/hyper_connection.hpp:18-40,
+ * src/hyper_connection.cpp:150-211 for the weights, :309-493 read, :692-709 write). A row's state
+ * is HC residual streams of H values ([rows, HC * H] bf16, stream s at columns s H ..). read()
+ * normalises each stream (RMSNorm, then the learned weight 1 + hc_norm.weight), projects the
+ * flat normalised row to the rank R (input_mix_weight_down) and back to HC x H
+ * (input_mix_weight_up) through x / HC, SiLU and sigmoid, and returns the block input
+ * mixed = mean over streams of sigmoid(up) * normalised stream, plus per-stream injection
+ * gates 2 sigmoid(block_inject_weight . normalised / HC) when the mixer has them. write() adds
+ * block_output * injection[s] to every stream s. Values are rounded to bf16 at the points of
+ * the reference's fused read kernels (src/hc_metal_kernels.hpp:10-36, 85-128, 270-308); the
+ * dot products accumulate in float. Projections are MLX affine-quantised: weight
+ * [out][in / (32 / bits)] uint32 (value j of a word at bits j*bits.., LSB first), scales and
+ * biases [out][in / group] bf16, value = q * scale + bias. */
+typedef struct q38_hc q38_hc;
+typedef struct q38_hc_desc {
+    int32_t hidden;          /* H: a multiple of 256, at most 4096                       */
+    int32_t streams;         /* HC: 1..16                                                 */
+    int32_t rank;            /* R: rows of input_mix_weight_down, a multiple of the group
+                                and of 128 / bits, at most 512                            */
+    int32_t bits;            /* 4 or 8                                                    */
+    int32_t group;           /* 32, 64 or 128                                             */
+    int32_t with_injection;  /* 1: block_inject_weight present (the decoder mixers)       */
+    float eps;               /* RMSNorm epsilon, > 0                                      */
+} q38_hc_desc;
+typedef struct q38_hc_weights {
+    const uint16_t* norm;                                  /* hc_norm.weight [HC * H]     */
+    const uint32_t* down_w; const uint16_t* down_s; const uint16_t* down_b;  /* [R][HC H] */
+    const uint32_t* up_w; const uint16_t* up_s; const uint16_t* up_b;        /* [HC H][R] */
+    const uint32_t* inj_w; const uint16_t* inj_s; const uint16_t* inj_b;     /* [HC][HC H] */
+} q38_hc_weights;
+/* HyperConnection::HyperConnection (src/hyper_connection.cpp:150-211): adopts the device
+ * weight pointers (they must stay alive) and forms 1 + hc_norm.weight once (bf16). */
+int q38_hc_create(q38_ctx* ctx, const q38_hc_desc* desc, const q38_hc_weights* weights, q38_hc** out);
+void q38_hc_destroy(q38_hc* hc);
+size_t q38_hc_workspace_size(const q38_hc_desc* desc, int32_t max_rows);
+/* HyperConnection::read (src/hyper_connection.cpp:309-493; the MLX graph at :461-493): stream [rows, HC H] bf16 ->
+ * mixed [rows, H] bf16 and, with injection, injection [rows, HC] bf16 (may be null
+ * otherwise). rows 1..16. */
+int q38_hc_read(q38_hc* hc, const uint16_t* stream, int32_t rows, uint16_t* mixed, uint16_t* injection, void* workspace,
+                size_t workspace_bytes, void* hip_stream);
+/* HyperConnection::write (src/hyper_connection.cpp:692-709): out = stream + block_output *
+ * injection per stream, rounded to bf16 at the product and the sum; out may be stream. */
+int q38_hc_write(const q38_hc* hc, const uint16_t* stream, const uint16_t* block_output, const uint16_t* injection,
+                 int32_t rows, uint16_t* out, void* hip_stream);
+/* HyperConnection::initialize_stream (src/hyper_connection.cpp:298-307): the embedding rows
+ * [rows, H] tiled to [rows, streams * H]. H a multiple of 8. */
+int q38_hc_initialize_stream(const uint16_t* embedding, int32_t rows, int32_t hidden, int32_t streams, uint16_t* out,
+                             void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,9 @@
 //   Q4 draft head          closed forms (nibble order, sign, group scales), numpy splitmix64
 //                          regeneration + float64 logits.
 //   RMSNorm                bit-exact float64 numpy restatement, closed forms, invariants.
+//   HyperConnection mixer  independent numpy restatement, closed forms (zero and bias-only
+//                          projections, packed-value order, the 1 + w norm weight, sign-only
+//                          streams, injection of 1 and 2 in the write).
 
 #include <pthread.h>
 #include <sched.h>
@@ -766,6 +769,102 @@ void rmsnorm(const uint16_t* h, int M, int H, double eps, uint16_t* out) {
     }
 }
 
+// ---------------------------------------------------------------- HyperConnection mixer
+// HyperConnection::read / write (src/hyper_connection.cpp:309-493, 692-709) at the rounding
+// points of the reference's fused read kernels (src/hc_metal_kernels.hpp:10-36 normalise,
+// :85-128 rank projection + SiLU, :270-308 expansion + mix); the default MLX graph
+// (src/hyper_connection.cpp:461-493) rounds to BF16 at the same points, and its injection
+// (raw = T(dot), T(raw * T(1/HC)), T(sigmoid), T(x2), :481-493) is the one stated here.
+// MLX affine weights: value j of a packed word at bits j*bits (LSB first), weight =
+// q * scale + bias with one BF16 scale and bias per `group` inputs. Dot products are taken
+// in double over exactly-widened operands and rounded once to float (a value every float
+// accumulation order approximates; the device is compared within tolerance); the norm
+// total likewise. Elementwise steps are float operations, as on the device.
+struct HcDesc {
+    int32_t hidden, streams, rank, bits, group, with_injection;
+    float eps;
+};
+
+double affine_dot(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x, int n, int bits, int group) {
+    const int vpw = 32 / bits;
+    const uint32_t mask = (1u << bits) - 1u;
+    double acc = 0.0;
+    for (int k = 0; k < n; ++k) {
+        const uint32_t q = (w[k / vpw] >> (bits * (k % vpw))) & mask;
+        const double wq = static_cast<double>(q) * bf16_to_f32(s[k / group]) + bf16_to_f32(b[k / group]);
+        acc += static_cast<double>(x[k]) * wq;
+    }
+    return acc;
+}
+
+inline float sigmoid_d(float v) { return static_cast<float>(1.0 / (1.0 + std::exp(-static_cast<double>(v)))); }
+
+void hc_read(const HcDesc& d, const uint16_t* norm, const uint32_t* dw, const uint16_t* ds, const uint16_t* db,
+             const uint32_t* uw, const uint16_t* us, const uint16_t* ub, const uint32_t* iw, const uint16_t* is,
+             const uint16_t* ib, const uint16_t* stream, int M, uint16_t* mixed, uint16_t* inj, uint16_t* xn_out,
+             float* act_out) {
+    const int H = d.hidden, HC = d.streams, R = d.rank, K = HC * H;
+    const int vpw = 32 / d.bits;
+    std::vector<float> xn(K), act(R);
+    for (int m = 0; m < M; ++m) {
+        const uint16_t* row = stream + static_cast<size_t>(m) * K;
+        for (int s = 0; s < HC; ++s) {
+            double ss = 0.0;
+            for (int k = 0; k < H; ++k) {
+                const double v = bf16_to_f32(row[s * H + k]);
+                ss += v * v;
+            }
+            const float inv = static_cast<float>(1.0 / std::sqrt(static_cast<double>(static_cast<float>(ss)) / H + d.eps));
+            for (int k = 0; k < H; ++k) {
+                const float t = rbf16(bf16_to_f32(row[s * H + k]) * inv);
+                const float wn = rbf16(bf16_to_f32(norm[s * H + k]) + 1.0f);
+                xn[s * H + k] = rbf16(t * wn);
+            }
+        }
+        for (int r = 0; r < R; ++r) {
+            const double dot = affine_dot(dw + static_cast<size_t>(r) * (K / vpw), ds + static_cast<size_t>(r) * (K / d.group),
+                                          db + static_cast<size_t>(r) * (K / d.group), xn.data(), K, d.bits, d.group);
+            const float v = rbf16(static_cast<float>(dot) / static_cast<float>(HC));
+            act[r] = rbf16(v * rbf16(sigmoid_d(v)));
+        }
+        if (d.with_injection && inj) {
+            for (int c = 0; c < HC; ++c) {
+                const double dot = affine_dot(iw + static_cast<size_t>(c) * (K / vpw), is + static_cast<size_t>(c) * (K / d.group),
+                                              ib + static_cast<size_t>(c) * (K / d.group), xn.data(), K, d.bits, d.group);
+                const float v = rbf16(rbf16(static_cast<float>(dot)) * rbf16(1.0f / static_cast<float>(HC)));
+                inj[static_cast<size_t>(m) * HC + c] = f32_to_bf16(rbf16(sigmoid_d(v)) * 2.0f);
+            }
+        }
+        for (int c = 0; c < H; ++c) {
+            float sum = 0.0f;
+            for (int s = 0; s < HC; ++s) {
+                const size_t wr = static_cast<size_t>(s) * H + c;
+                const double dot = affine_dot(uw + wr * (R / vpw), us + wr * (R / d.group), ub + wr * (R / d.group),
+                                              act.data(), R, d.bits, d.group);
+                const float u = rbf16(static_cast<float>(dot));
+                const float gate = rbf16(sigmoid_d(u));
+                sum += rbf16(gate * xn[s * H + c]);
+            }
+            mixed[static_cast<size_t>(m) * H + c] = f32_to_bf16(rbf16(sum) / static_cast<float>(HC));
+        }
+        if (xn_out)
+            for (int k = 0; k < K; ++k) xn_out[static_cast<size_t>(m) * K + k] = f32_to_bf16(xn[k]);
+        if (act_out)
+            for (int r = 0; r < R; ++r) act_out[static_cast<size_t>(m) * R + r] = act[r];
+    }
+}
+
+void hc_write(int H, int HC, int M, const uint16_t* stream, const uint16_t* block, const uint16_t* inj, uint16_t* out) {
+    for (int m = 0; m < M; ++m)
+        for (int s = 0; s < HC; ++s) {
+            const float g = bf16_to_f32(inj[static_cast<size_t>(m) * HC + s]);
+            for (int c = 0; c < H; ++c) {
+                const size_t at = (static_cast<size_t>(m) * HC + s) * H + c;
+                out[at] = f32_to_bf16(bf16_to_f32(stream[at]) + rbf16(bf16_to_f32(block[static_cast<size_t>(m) * H + c]) * g));
+            }
+        }
+}
+
 // ---------------------------------------------------------------- LM head (R12/R13)
 // Reference: batched quantized_matmul over the final rows (src/model.cpp:466-492) and
 // argmax_all + take (src/mtp_verifier.cpp:30-55), ties to the lowest index
@@ -1170,6 +1269,19 @@ int orc_accept_sampled(const float* target_logits, const float* draft_logits, co
     *accepted = k;
     *next = static_cast<uint32_t>(draw(p, v));
     return 0;
+}
+
+int orc_hc_read(const HcDesc* d, const uint16_t* norm, const uint32_t* dw, const uint16_t* ds, const uint16_t* db,
+                const uint32_t* uw, const uint16_t* us, const uint16_t* ub, const uint32_t* iw, const uint16_t* is,
+                const uint16_t* ib, const uint16_t* stream, int M, uint16_t* mixed, uint16_t* inj, uint16_t* xn_out,
+                float* act_out) {
+    if (!d || d->bits <= 0 || 32 % d->bits || d->group <= 0 || d->hidden % d->group || d->rank % d->group) return -1;
+    hc_read(*d, norm, dw, ds, db, uw, us, ub, iw, is, ib, stream, M, mixed, inj, xn_out, act_out);
+    return 0;
+}
+void orc_hc_write(int H, int HC, int M, const uint16_t* stream, const uint16_t* block, const uint16_t* inj,
+                  uint16_t* out) {
+    hc_write(H, HC, M, stream, block, inj, out);
 }
 
 } // extern "C"

@@ -1410,6 +1410,109 @@ int q38_slot_info(const q38_slot* s, uint64_t* token_count, int32_t* staged_rows
 const uint16_t* q38_slot_hidden(const q38_slot* s) { return s && s->has_hidden ? s->committed : nullptr; }
 uint64_t q38_slot_generation(const q38_slot* s) { return s && s->staged_rows > 0 ? s->stages : 0; }
 
+// ------------------------------------------------------------------ HyperConnection mixer
+struct q38_hc {
+    q38_ctx* ctx;
+    q38_hc_desc desc;
+    HcDev dev;
+    uint16_t* wn;  // 1 + hc_norm.weight (owned)
+};
+
+static int hc_validate(const q38_hc_desc* d) {
+    if (!d) return fail(Q38_EINVAL, "null HyperConnection description");
+    if (d->hidden <= 0 || d->hidden % 256 || d->hidden > 256 * kHcMaxPerThread)
+        return fail(Q38_EINVAL, "HyperConnection hidden size must be a positive multiple of 256, at most 4096");
+    if (d->streams < 1 || d->streams > kHcMaxStreams) return fail(Q38_EINVAL, "HyperConnection stream count must be 1..16");
+    if (d->bits != 4 && d->bits != 8) return fail(Q38_EINVAL, "HyperConnection projections must be 4- or 8-bit affine");
+    if (d->group != 32 && d->group != 64 && d->group != 128)
+        return fail(Q38_EINVAL, "HyperConnection quantization group must be 32, 64 or 128");
+    if (d->rank <= 0 || d->rank > kHcMaxRank || d->rank % d->group || d->rank % (128 / d->bits))
+        return fail(Q38_EINVAL, "HyperConnection rank must be a multiple of the group and of 128 / bits, at most 512");
+    if (!(d->eps > 0.0f)) return fail(Q38_EINVAL, "RMS norm epsilon must be positive");
+    return Q38_OK;
+}
+
+int q38_hc_create(q38_ctx* ctx, const q38_hc_desc* d, const q38_hc_weights* w, q38_hc** out) {
+    if (!ctx || !w || !out) return fail(Q38_EINVAL, "q38_hc_create: null argument");
+    if (int rc = hc_validate(d)) return rc;
+    if (!w->norm || !w->down_w || !w->down_s || !w->down_b || !w->up_w || !w->up_s || !w->up_b)
+        return fail(Q38_EINVAL, "q38_hc_create: norm, down and up tensors are required");
+    if (d->with_injection && (!w->inj_w || !w->inj_s || !w->inj_b))
+        return fail(Q38_EINVAL, "q38_hc_create: a mixer with injection needs block_inject_weight tensors");
+    const uintptr_t a = reinterpret_cast<uintptr_t>(w->up_w);
+    if (a % 16) return fail(Q38_EINVAL, "q38_hc_create: input_mix_weight_up must be 16-byte aligned");
+    const int n = d->streams * d->hidden;
+    uint16_t* wn = nullptr;
+    if (hipMalloc(&wn, static_cast<size_t>(n) * 2) != hipSuccess)
+        return fail(Q38_ENOMEM, "hipMalloc failed for the HyperConnection norm weight");
+    hipError_t e = launch_hc_norm_weight(w->norm, n, wn, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(wn);
+        return hip_fail(e, "HyperConnection norm weight");
+    }
+    auto* hc = new q38_hc{ctx, *d, {}, wn};
+    hc->dev = HcDev{d->hidden, d->streams, d->rank, d->bits, d->group, d->with_injection ? 1 : 0, d->eps, wn,
+                    w->down_w, w->down_s, w->down_b, w->up_w, w->up_s, w->up_b,
+                    d->with_injection ? w->inj_w : nullptr, d->with_injection ? w->inj_s : nullptr,
+                    d->with_injection ? w->inj_b : nullptr};
+    *out = hc;
+    return Q38_OK;
+}
+
+void q38_hc_destroy(q38_hc* hc) {
+    if (!hc) return;
+    (void)hipFree(hc->wn);
+    delete hc;
+}
+
+static size_t hc_workspace(const q38_hc_desc& d, int rows) {
+    return align256(static_cast<size_t>(rows) * d.streams * d.hidden * 2) + align256(static_cast<size_t>(rows) * d.rank * 4);
+}
+
+size_t q38_hc_workspace_size(const q38_hc_desc* d, int32_t max_rows) {
+    if (hc_validate(d) || max_rows < 1 || max_rows > kMaxRows) return 0;
+    return hc_workspace(*d, max_rows);
+}
+
+int q38_hc_read(q38_hc* hc, const uint16_t* stream, int32_t rows, uint16_t* mixed, uint16_t* injection, void* ws,
+                size_t ws_bytes, void* st) {
+    if (!hc || !stream || !mixed || !ws) return fail(Q38_EINVAL, "q38_hc_read: null argument");
+    if (rows < 1 || rows > kMaxRows) return fail(Q38_EINVAL, "q38_hc_read: rows must be 1..16");
+    if (hc->desc.with_injection && !injection) return fail(Q38_EINVAL, "q38_hc_read: this mixer returns an injection");
+    const size_t need = hc_workspace(hc->desc, rows);
+    if (ws_bytes < need) return fail(Q38_ESPACE, "q38_hc_read: workspace too small");
+    if (reinterpret_cast<uintptr_t>(stream) % 16) return fail(Q38_EINVAL, "q38_hc_read: stream must be 16-byte aligned");
+    auto* xn = static_cast<uint16_t*>(ws);
+    auto* act = reinterpret_cast<float*>(static_cast<char*>(ws) +
+                                         align256(static_cast<size_t>(rows) * hc->desc.streams * hc->desc.hidden * 2));
+    Q38_HIP(launch_hc_read(hc->dev, rows, stream, xn, act, mixed, injection, static_cast<hipStream_t>(st)));
+    return Q38_OK;
+}
+
+int q38_hc_write(const q38_hc* hc, const uint16_t* stream, const uint16_t* block_output, const uint16_t* injection,
+                 int32_t rows, uint16_t* out, void* st) {
+    if (!hc || !stream || !block_output || !injection || !out) return fail(Q38_EINVAL, "q38_hc_write: null argument");
+    if (rows < 1 || rows > kMaxPrefillRows) return fail(Q38_EINVAL, "q38_hc_write: rows must be 1..2048");
+    if ((reinterpret_cast<uintptr_t>(stream) | reinterpret_cast<uintptr_t>(block_output) |
+         reinterpret_cast<uintptr_t>(out)) % 16)
+        return fail(Q38_EINVAL, "q38_hc_write: stream, block output and out must be 16-byte aligned");
+    Q38_HIP(launch_hc_write(hc->desc.hidden, hc->desc.streams, rows, stream, block_output, injection, out,
+                            static_cast<hipStream_t>(st)));
+    return Q38_OK;
+}
+
+int q38_hc_initialize_stream(const uint16_t* embedding, int32_t rows, int32_t hidden, int32_t streams, uint16_t* out,
+                             void* st) {
+    if (!embedding || !out || rows < 1 || rows > kMaxPrefillRows || hidden < 8 || hidden % 8 || streams < 1 ||
+        streams > kHcMaxStreams)
+        return fail(Q38_EINVAL, "q38_hc_initialize_stream: bad arguments");
+    if ((reinterpret_cast<uintptr_t>(embedding) | reinterpret_cast<uintptr_t>(out)) % 16)
+        return fail(Q38_EINVAL, "q38_hc_initialize_stream: embedding and out must be 16-byte aligned");
+    Q38_HIP(launch_hc_tile(hidden, streams, rows, embedding, out, static_cast<hipStream_t>(st)));
+    return Q38_OK;
+}
+
 } // extern "C"
 
 #ifdef Q38_TRACE

@@ -223,4 +223,30 @@ hipError_t launch_accept_sampled(const float* tl, const float* dl, const uint32_
                                  float T, uint64_t seed, uint64_t slot, uint64_t round, int64_t* out, void* ws,
                                  hipStream_t st);
 
+// HyperConnection mixer (streams of H values per row; MLX affine-quantised projections with
+// 32 / bits values per packed word, one bf16 scale and bias per G inputs).
+constexpr int kHcMaxPerThread = 16;  // H <= 4096 (H / 256 values per normalisation thread)
+constexpr int kHcMaxRank = 512;
+constexpr int kHcMaxStreams = 16;
+struct HcDev {
+    int H, HC, R, bits, G, with_inj;
+    float eps;
+    const uint16_t* wn;                       // [HC * H] bf16: 1 + hc_norm.weight
+    const uint32_t* dw;                       // down [R][HC * H / vpw]
+    const uint16_t *ds, *db;                  //      [R][HC * H / G]
+    const uint32_t* uw;                       // up [HC * H][R / vpw]
+    const uint16_t *us, *ub;                  //    [HC * H][R / G]
+    const uint32_t* iw;                       // injection [HC][HC * H / vpw] (with_inj)
+    const uint16_t *is, *ib;                  //           [HC][HC * H / G]
+};
+size_t hc_up_lds_max();
+// xn: [M][HC * H] bf16 and act: [M][R] float of the workspace; mixed [M][H], inj [M][HC] bf16
+// (inj unused without injection).
+hipError_t launch_hc_read(const HcDev& D, int M, const uint16_t* stream, uint16_t* xn, float* act, uint16_t* mixed,
+                          uint16_t* inj, hipStream_t st);
+hipError_t launch_hc_write(int H, int HC, int M, const uint16_t* stream, const uint16_t* block_out,
+                           const uint16_t* inj, uint16_t* out, hipStream_t st);
+hipError_t launch_hc_tile(int H, int HC, int M, const uint16_t* emb, uint16_t* out, hipStream_t st);
+hipError_t launch_hc_norm_weight(const uint16_t* raw, int n, uint16_t* wn, hipStream_t st);
+
 } // namespace q38

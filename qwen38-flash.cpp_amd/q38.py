@@ -142,6 +142,24 @@ _sig("q38_slot_hidden", P, P)
 _sig("q38_slot_generation", C.c_uint64, P)
 
 
+class HcDesc(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("hidden", "streams", "rank", "bits", "group", "with_injection")] + [
+        ("eps", C.c_float)]
+
+
+class HcWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "norm", "down_w", "down_s", "down_b", "up_w", "up_s", "up_b", "inj_w", "inj_s", "inj_b")]
+
+
+_sig("q38_hc_create", C.c_int, P, C.POINTER(HcDesc), C.POINTER(HcWeights), C.POINTER(P))
+_sig("q38_hc_destroy", None, P)
+_sig("q38_hc_workspace_size", SZ, C.POINTER(HcDesc), I32)
+_sig("q38_hc_read", C.c_int, P, P, I32, P, P, P, SZ, P)
+_sig("q38_hc_write", C.c_int, P, P, P, P, I32, P, P)
+_sig("q38_hc_initialize_stream", C.c_int, P, I32, I32, I32, P, P)
+
+
 def check(rc: int) -> int:
     if rc != Q38_OK:
         raise Q38Error(rc, lib.q38_last_error().decode())
@@ -260,3 +278,33 @@ class MtpHead:
 def routes(experts=None, weights=None, logits=None, plan=None, x_norm=None) -> RouteOut:
     f = lambda t: None if t is None else ptr(t)
     return RouteOut(f(experts), f(weights), f(logits), f(plan), f(x_norm))
+
+
+class Hc:
+    """HyperConnection mixer over caller-owned device weights (torch tensors keyed by the
+    q38_hc_weights field names; the handle keeps references to them)."""
+
+    _FIELDS = ("norm", "down_w", "down_s", "down_b", "up_w", "up_s", "up_b", "inj_w", "inj_s", "inj_b")
+
+    def __init__(self, ctx: "Ctx", desc: HcDesc, tensors: dict):
+        self.desc = desc
+        self._keep = tensors
+        w = HcWeights(*[ptr(tensors[k]) if tensors.get(k) is not None else None for k in self._FIELDS])
+        h = P()
+        check(lib.q38_hc_create(ctx.h, C.byref(desc), C.byref(w), C.byref(h)))
+        self.h = h
+
+    def workspace_size(self, rows: int) -> int:
+        return lib.q38_hc_workspace_size(C.byref(self.desc), rows)
+
+    def read(self, stream, rows, mixed, injection, ws, st=None):
+        check(lib.q38_hc_read(self.h, ptr(stream), rows, ptr(mixed), ptr(injection) if injection is not None else None,
+                              ptr(ws), ws.numel() if hasattr(ws, "numel") else 0, st))
+
+    def write(self, stream, block, injection, rows, out, st=None):
+        check(lib.q38_hc_write(self.h, ptr(stream), ptr(block), ptr(injection), rows, ptr(out), st))
+
+    def close(self):
+        if self.h:
+            lib.q38_hc_destroy(self.h)
+            self.h = None

@@ -23,6 +23,11 @@ class Desc(C.Structure):  # field order of oracle/q38_oracle.cpp Desc
         "gu_group", "down_group", "normalize", "has_shared", "mixed", "book_format")]
 
 
+class HcDesc(C.Structure):  # field order of oracle/q38_oracle.cpp HcDesc
+    _fields_ = [(n, C.c_int32) for n in ("hidden", "streams", "rank", "bits", "group", "with_injection")] + [
+        ("eps", C.c_float)]
+
+
 def make_desc(hidden=2048, inter=512, experts=512, top_k=10, gu=(8, 14), down=(8, 14), gu_group=None,
               down_group=None, normalize=1, shared=1, mixed=0, book_format=0) -> Desc:
     return Desc(hidden, inter, experts, top_k, gu[0], gu[1], down[0], down[1], gu_group or hidden,
@@ -71,6 +76,8 @@ class Oracle:
             C.c_int, P)
         sig("orc_rmsnorm", None, P, C.c_int, C.c_int, F64, P)
         sig("orc_residual_add", None, P, P, I64, P)
+        sig("orc_hc_read", C.c_int, C.POINTER(HcDesc), *([P] * 10), P, C.c_int, P, P, P, P)
+        sig("orc_hc_write", None, C.c_int, C.c_int, C.c_int, P, P, P, P)
         sig("orc_head_q8_synth_logits", None, U64, C.c_int, I64, I64, P, C.c_int, P, C.c_int)
         sig("orc_head_q8_logits", None, P, P, I64, C.c_int, P, C.c_int, P, C.c_int)
         sig("orc_argmax", None, P, C.c_int, I64, P, P)
@@ -216,6 +223,32 @@ class Oracle:
         h = np.ascontiguousarray(h, np.uint16)
         out = np.empty_like(h)
         self.lib.orc_rmsnorm(_a(h), h.shape[0], h.shape[1], eps, _a(out))
+        return out
+
+    def hc_read(self, desc, w, stream):
+        """HyperConnection read: w holds numpy arrays norm, down_w/s/b, up_w/s/b and, with
+        injection, inj_w/s/b. Returns (mixed, injection or None, xn, act)."""
+        stream = np.ascontiguousarray(stream, np.uint16)
+        M = stream.shape[0]
+        H, HC, R = desc.hidden, desc.streams, desc.rank
+        mixed = np.empty((M, H), np.uint16)
+        inj = np.empty((M, HC), np.uint16) if desc.with_injection else None
+        xn = np.empty((M, HC * H), np.uint16)
+        act = np.empty((M, R), np.float32)
+        keep = [np.ascontiguousarray(w[k]) if w.get(k) is not None else None for k in (
+            "norm", "down_w", "down_s", "down_b", "up_w", "up_s", "up_b", "inj_w", "inj_s", "inj_b")]
+        ptrs = [_a(a) if a is not None else None for a in keep]
+        rc = self.lib.orc_hc_read(C.byref(desc), *ptrs, _a(stream), M, _a(mixed),
+                                  _a(inj) if inj is not None else None, _a(xn), _a(act))
+        assert rc == 0
+        return mixed, inj, xn, act
+
+    def hc_write(self, H, HC, stream, block, inj):
+        stream = np.ascontiguousarray(stream, np.uint16)
+        block = np.ascontiguousarray(block, np.uint16)
+        inj = np.ascontiguousarray(inj, np.uint16)
+        out = np.empty_like(stream)
+        self.lib.orc_hc_write(H, HC, stream.shape[0], _a(stream), _a(block), _a(inj), _a(out))
         return out
 
     def residual_add(self, h, y):
