@@ -10,7 +10,8 @@ synthetic (seeded, random-init) and resident in HBM before timing.
 Also reported (in "config"): per-layer microseconds and HBM GB/s of the 48-layer MoE chain for
 M = 1..4 rows, the phase split of a profiled pass, the roofline of the dominant kernel, config 3
 (512 prefill rows), config 4 (mixed VQ v2, 16 rows), config 2's sampled tail (Q8 logits, Q4 draft
-logits, device rejection sampling) and a round with drafts from the MTP draft head.
+logits, device rejection sampling), a round with drafts from the MTP draft head, and the decoder
+layer's MLP half with its HyperConnection mixers (mixer read -> MoE -> mixer write).
 The CPU baseline is the C++ oracle (oracle/q38_oracle.cpp) timed on this host's cores on a
 bounded sample (20 passes per M = 1..4 over 5 layers, and a row slice of the Q8 head + argmax,
 on the process's thread share and on 1 thread), scaled to a round.
@@ -439,6 +440,92 @@ def main():
                "gbps": g_bytes / (g_us * 1e-6) / 1e9}
     log(f"config 1 with 64-input scale groups (4 rows): {g_us:.1f} us/layer, {g64_cfg['gbps']:.0f} GB/s, U={g_u:.1f}")
 
+    # ---------------------------------------------------------------- decoder MLP half
+    # HyperConnection read -> MoE -> write (q38_verify_chain_hc) for 4 rows through 8 config-1
+    # layers with 4-stream mixers (rank 256, 4-bit affine weights in groups of 64, seeded
+    # random); and the mixers alone (read + write with the block input as block output).
+    def hc_tensors(gen, HCn, Rn):
+        K = HCn * H
+
+        def proj(o, n):
+            w = torch.randint(-2**31, 2**31 - 1, (o, n // 8), dtype=torch.int32, device=dev, generator=gen)
+            s = torch.rand((o, n // 64), device=dev, generator=gen) * (0.05 / 8)
+            b = -s * 7.5 + torch.randn((o, n // 64), device=dev, generator=gen) * 0.002
+            return w, s.to(torch.bfloat16).view(torch.int16), b.to(torch.bfloat16).view(torch.int16)
+        t = {"norm": (torch.randn(K, device=dev, generator=gen) * 0.1).to(torch.bfloat16).view(torch.int16)}
+        t["down_w"], t["down_s"], t["down_b"] = proj(Rn, K)
+        t["up_w"], t["up_s"], t["up_b"] = proj(K, Rn)
+        t["inj_w"], t["inj_s"], t["inj_b"] = proj(HCn, K)
+        return t
+
+    def hc_leg(Mh, NLh, HCn=4, Rn=256):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(SEED)
+        lh = [q38.MoeLayer(ctx, q38.desc(), seed=SEED, layer=l) for l in range(NLh)]
+        hdesc = q38.HcDesc(H, HCn, Rn, 4, 64, 1, 1e-6)
+        mixers = [q38.Hc(ctx, hdesc, hc_tensors(gen, HCn, Rn)) for _ in range(NLh)]
+        try:
+            emb = torch.empty((Mh, H), dtype=torch.int16, device=dev)
+            toks_h = (C.c_uint32 * Mh)(*[11 + 7 * r for r in range(Mh)])
+            q38.check(q38.lib.q38_embed_synthetic(SEED, toks_h, Mh, H, emb.data_ptr(), sp))
+            st0 = torch.empty((Mh, HCn * H), dtype=torch.int16, device=dev)
+            q38.check(q38.lib.q38_hc_initialize_stream(emb.data_ptr(), Mh, H, HCn, st0.data_ptr(), sp))
+            sth = st0.clone()
+            lar = (C.c_void_p * NLh)(*[L.h.value for L in lh])
+            mar = (C.c_void_p * NLh)(*[m.h.value for m in mixers])
+            wsh = torch.empty(q38.lib.q38_verify_chain_hc_workspace_size(C.byref(lh[0].desc), C.byref(hdesc), Mh),
+                              dtype=torch.uint8, device=dev)
+            mixed_h = torch.empty((Mh, H), dtype=torch.int16, device=dev)
+            inj_h = torch.empty((Mh, HCn), dtype=torch.int16, device=dev)
+            wsm = torch.empty(mixers[0].workspace_size(Mh), dtype=torch.uint8, device=dev)
+
+            def run_chain(sp_):
+                q38.check(q38.lib.q38_verify_chain_hc(lar, mar, NLh, sth.data_ptr(), Mh, wsh.data_ptr(), wsh.numel(),
+                                                      sp_))
+
+            def run_mixers(sp_):
+                for m in mixers:
+                    m.read(sth, Mh, mixed_h, inj_h, wsm, sp_)
+                    m.write(sth, mixed_h, inj_h, Mh, sth, sp_)
+
+            out = []
+            for fn in (run_chain, run_mixers):
+                g = None
+                if not args.no_graph:
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g):
+                        fn(torch.cuda.current_stream().cuda_stream)
+                tt = []
+                for _ in range(10):
+                    sth.copy_(st0)
+                    ev0.record(stream)
+                    if g is not None:
+                        g.replay()
+                    else:
+                        fn(sp)
+                    ev1.record(stream)
+                    torch.cuda.synchronize()
+                    tt.append(ev0.elapsed_time(ev1))
+                out.append(1e3 * float(np.median(tt)) / NLh)
+            # mixer bytes per layer: down, up and injection weights with their scales and
+            # biases, the streams read twice (normalisation, write) and written once
+            K = HCn * H
+            wbytes = (Rn * K // 2 + Rn * K // 64 * 4) * 2 + HCn * K // 2 + HCn * K // 64 * 4
+            sbytes = 3 * Mh * K * 2
+            return out[0], out[1], wbytes + sbytes
+        finally:
+            for L in lh:
+                L.close()
+            for m in mixers:
+                m.close()
+
+    hc_us, hcm_us, hc_bytes = hc_leg(4, 8)
+    hc_cfg = {"rows": 4, "layers": 8, "streams": 4, "rank": 256, "mixer_bits": 4, "mixer_group": 64,
+              "layer_us": hc_us, "mixer_us": hcm_us, "mixer_bytes": hc_bytes,
+              "mixer_gbps": hc_bytes / (hcm_us * 1e-6) / 1e9}
+    log(f"decoder MLP half (mixer read -> MoE -> mixer write, 4 rows): {hc_us:.1f} us/layer; "
+        f"mixers alone {hcm_us:.1f} us/layer ({hc_cfg['mixer_gbps']:.0f} GB/s of {hc_bytes / 1e6:.2f} MB)")
+
     if args.copy_calibration:
         # a plain device copy of known size for the FETCH_SIZE / WRITE_SIZE calibration runs
         nb = 256 << 20
@@ -619,7 +706,7 @@ def main():
             "kernel_us_per_launch_m4": {k.split()[0]: 1e3 * v[0] / nl for k, v in kernels.items()},
             "algorithmic_bytes_per_launch_m4": {k.split()[0]: v[1] for k, v in kernels.items()},
             "config3_prefill": prefill_cfg,
-            "config4_mixed": mixed_cfg, "config1_group64": g64_cfg,
+            "config4_mixed": mixed_cfg, "config1_group64": g64_cfg, "decoder_mlp_half_hc": hc_cfg,
             "config2_sampled": sampled_cfg,
             "config2_learned_drafts": learned_cfg,
         },

@@ -454,6 +454,16 @@ int q38_hc_read(q38_hc* hc, const uint16_t* stream, int32_t rows, uint16_t* mixe
  * injection per stream, rounded to bf16 at the product and the sum; out may be stream. */
 int q38_hc_write(const q38_hc* hc, const uint16_t* stream, const uint16_t* block_output, const uint16_t* injection,
                  int32_t rows, uint16_t* out, void* hip_stream);
+/* The MLP half of DecoderLayer::forward_verify_dense_batched (src/decoder_layer.cpp:494-497)
+ * over n_layers layers: per layer l, read = mixers[l].read(stream), y = MoE_l(read.mixed)
+ * (q38_moe_forward), stream = mixers[l].write(stream, y, read.injection). stream: device
+ * [rows, HC * H] bf16, updated in place; rows 1..16. Layers and mixers share H; every
+ * mixer has injection weights, the same streams and rank. The decoder's optional MLP output
+ * map (src/decoder_layer.cpp:198-210) is not applied. Workspace:
+ * q38_verify_chain_hc_workspace_size bytes for the largest layer description. */
+size_t q38_verify_chain_hc_workspace_size(const q38_moe_desc* desc, const q38_hc_desc* mixer, int32_t max_rows);
+int q38_verify_chain_hc(q38_moe_layer* const* layers, q38_hc* const* mixers, int32_t n_layers, uint16_t* stream,
+                        int32_t rows, void* workspace, size_t workspace_bytes, void* hip_stream);
 /* HyperConnection::initialize_stream (src/hyper_connection.cpp:298-307): the embedding rows
  * [rows, H] tiled to [rows, streams * H]. H a multiple of 8. */
 int q38_hc_initialize_stream(const uint16_t* embedding, int32_t rows, int32_t hidden, int32_t streams, uint16_t* out,

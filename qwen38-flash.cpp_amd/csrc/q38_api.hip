@@ -1502,6 +1502,66 @@ int q38_hc_write(const q38_hc* hc, const uint16_t* stream, const uint16_t* block
     return Q38_OK;
 }
 
+// Workspace of the mixer chain: the largest layer's MoE workspace, then the mixer's (xn,
+// act), the block input and the injection gates (the layer output goes straight into the
+// streams).
+static size_t chain_hc_ws(size_t moe_bytes, const q38_hc_desc& hd, int rows, char* base, uint16_t** mixed,
+                          uint16_t** inj, void** hcws) {
+    size_t off = align256(moe_bytes);
+    if (hcws) *hcws = base + off;
+    off += hc_workspace(hd, rows);
+    if (mixed) *mixed = reinterpret_cast<uint16_t*>(base + off);
+    off += align256(static_cast<size_t>(rows) * hd.hidden * 2);
+    if (inj) *inj = reinterpret_cast<uint16_t*>(base + off);
+    off += align256(static_cast<size_t>(rows) * hd.streams * 2);
+    return off;
+}
+
+size_t q38_verify_chain_hc_workspace_size(const q38_moe_desc* d, const q38_hc_desc* hd, int32_t max_rows) {
+    if (!d || hc_validate(hd) || max_rows < 1 || max_rows > kMaxRows) return 0;
+    return chain_hc_ws(moe_ws(*d, max_rows, nullptr, nullptr), *hd, max_rows, nullptr, nullptr, nullptr, nullptr);
+}
+
+int q38_verify_chain_hc(q38_moe_layer* const* layers, q38_hc* const* mixers, int32_t n_layers, uint16_t* stream,
+                        int32_t rows, void* ws, size_t ws_bytes, void* hip_stream) {
+    if (!layers || !mixers || n_layers < 1 || !stream || !ws) return fail(Q38_EINVAL, "q38_verify_chain_hc: bad arguments");
+    if (int rc = check_rows(rows)) return rc;
+    if (reinterpret_cast<uintptr_t>(stream) % 16) return fail(Q38_EINVAL, "q38_verify_chain_hc: stream must be 16-byte aligned");
+    size_t moe_need = 0;
+    for (int l = 0; l < n_layers; ++l) {
+        if (!layers[l] || !mixers[l]) return fail(Q38_EINVAL, "q38_verify_chain_hc: null layer or mixer");
+        const q38_hc_desc& hd = mixers[l]->desc;
+        if (layers[l]->desc.hidden != hd.hidden || hd.hidden != mixers[0]->desc.hidden ||
+            hd.streams != mixers[0]->desc.streams || hd.rank != mixers[0]->desc.rank)
+            return fail(Q38_EINVAL, "q38_verify_chain_hc: layers and mixers disagree on the hidden size, streams or rank");
+        if (!hd.with_injection) return fail(Q38_EINVAL, "q38_verify_chain_hc: a decoder mixer carries injection weights");
+        moe_need = std::max(moe_need, moe_ws(layers[l]->desc, rows, nullptr, nullptr));
+    }
+    char* base = static_cast<char*>(ws);
+    uint16_t *mixed = nullptr, *inj = nullptr;
+    void* hcws = nullptr;
+    if (ws_bytes < chain_hc_ws(moe_need, mixers[0]->desc, rows, base, &mixed, &inj, &hcws))
+        return fail(Q38_ESPACE, "workspace too small");
+    const hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    const q38_hc_desc& hd0 = mixers[0]->desc;
+    auto* xn = static_cast<uint16_t*>(hcws);
+    auto* act = reinterpret_cast<float*>(static_cast<char*>(hcws) +
+                                         align256(static_cast<size_t>(rows) * hd0.streams * hd0.hidden * 2));
+    for (int l = 0; l < n_layers; ++l) {
+        Q38_HIP(launch_hc_read(mixers[l]->dev, rows, stream, xn, act, mixed, inj, st));
+        MoeBufs w{};
+        moe_ws(layers[l]->desc, rows, &w, ws);
+        // the MoE layer on the block input; its combine writes the output into the streams
+        const LayerDev dev = moe_call_dev(layers[l]->dev, rows);
+        Q38_HIP(launch_router(dev, w, rows, mixed, false, 0.0f, st));
+        if (!moe_plans_in_gate_up(dev, rows)) Q38_HIP(launch_topk_plan(dev, w, rows, st));
+        Q38_HIP(launch_gate_up(dev, w, rows, st));
+        Q38_HIP(launch_down(dev, w, rows, st));
+        Q38_HIP(launch_combine_hc(dev, w, rows, stream, inj, hd0.streams, st));
+    }
+    return Q38_OK;
+}
+
 int q38_hc_initialize_stream(const uint16_t* embedding, int32_t rows, int32_t hidden, int32_t streams, uint16_t* out,
                              void* st) {
     if (!embedding || !out || rows < 1 || rows > kMaxPrefillRows || hidden < 8 || hidden % 8 || streams < 1 ||

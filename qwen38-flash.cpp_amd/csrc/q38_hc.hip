@@ -6,17 +6,17 @@
 //
 //   k_hc_norm   per (row, stream): RMSNorm over H and the learned norm weight,
 //               xn = T(T(x * inv_rms) * T(1 + w))                     (T = round to BF16)
-//   k_hc_down   one wave per output: the rank projection of the row's flat normalised
+//   k_hc_down   one workgroup per output: the rank projection of the row's flat normalised
 //               streams (MLX affine weights: q * scale + bias per group, 4 or 8 bits),
 //               a = T(v * T(sigmoid(v))) with v = T(dot / HC); the injection outputs in the
 //               same launch, inj = T(2 * T(sigmoid(T(T(dot) * T(1 / HC)))))
-//   k_hc_up     one lane per (stream, column): u = T(dot over the rank), gate = T(sigmoid(u)),
+//   k_hc_up     four lanes per (stream, column): u = T(dot over the rank), gate = T(sigmoid(u)),
 //               the stream's term T(gate * xn); the workgroup adds the HC terms in stream
 //               order in float: mixed = T(T(sum) / HC)
 //   k_hc_write  stream <- T(stream + T(block_output * inj[stream]))
 // Memory per call is tiny next to the MoE block (R x HC x H x bits / 8 bytes per projection:
 // 1 MiB each at H 2048, HC 4, R 256, 4 bits); the kernels are latency-bound, so each launch
-// spreads its weight rows over as many waves as there are outputs.
+// spreads its weight rows over many waves and issues a thread's loads before its products.
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
 
@@ -28,20 +28,33 @@ namespace {
 __device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
 
 // ------------------------------------------------------------------ read: normalisation
-// Workgroup (stream s, row m), 256 threads: thread t holds columns t + 256 i of the stream,
-// squares summed in i order with fmaf, the wave totals (xor butterfly) added in wave order.
+// Workgroup (stream s, row m), 256 threads: thread t holds the 8-column runs t + 256 i of the
+// stream (H / 8 runs; at most 2 per thread for H <= 4096), loaded with the matching norm
+// weights in one go; squares summed run by run with fmaf, the wave totals (xor butterfly)
+// added in wave order.
 __global__ __launch_bounds__(256) void k_hc_norm(HcDev D, const uint16_t* __restrict__ stream, uint16_t* __restrict__ xn) {
+    constexpr int kRuns = kHcMaxPerThread / 8;
     __shared__ float red[4];
     const int s = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
-    const int H = D.H, npt = H / 256;
+    const int H = D.H, runs = H / 8;
     const size_t base = (static_cast<size_t>(m) * D.HC + s) * H;
-    float v[kHcMaxPerThread];
+    uint4 xv[kRuns], wv[kRuns];
+#pragma unroll
+    for (int i = 0; i < kRuns; ++i) {
+        const int r = tid + 256 * i < runs ? tid + 256 * i : 0;  // (past the stream: run 0, unused)
+        xv[i] = *reinterpret_cast<const uint4*>(stream + base + 8 * r);
+        wv[i] = *reinterpret_cast<const uint4*>(D.wn + static_cast<size_t>(s) * H + 8 * r);
+    }
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kHcMaxPerThread; ++i)
-        if (i < npt) {
-            v[i] = bf2f(stream[base + tid + 256 * i]);
-            ss = fmaf(v[i], v[i], ss);
+    for (int i = 0; i < kRuns; ++i)
+        if (tid + 256 * i < runs) {
+            const uint32_t q[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                ss = fmaf(bflo(q[k]), bflo(q[k]), ss);
+                ss = fmaf(bfhi(q[k]), bfhi(q[k]), ss);
+            }
         }
     ss = wave_sum_xor(ss);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -49,10 +62,18 @@ __global__ __launch_bounds__(256) void k_hc_norm(HcDev D, const uint16_t* __rest
     const float total = ((red[0] + red[1]) + red[2]) + red[3];
     const float inv = 1.0f / sqrtf(total / static_cast<float>(H) + D.eps);
 #pragma unroll
-    for (int i = 0; i < kHcMaxPerThread; ++i)
-        if (i < npt) {
-            const size_t k = base + tid + 256 * i;
-            xn[k] = f2bf(rbf(v[i] * inv) * bf2f(D.wn[static_cast<size_t>(s) * H + tid + 256 * i]));
+    for (int i = 0; i < kRuns; ++i)
+        if (tid + 256 * i < runs) {
+            const uint32_t q[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            const uint32_t w[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = f2bf(rbf(bflo(q[k]) * inv) * bflo(w[k]));
+                const uint32_t hi = f2bf(rbf(bfhi(q[k]) * inv) * bfhi(w[k]));
+                o[k] = lo | (hi << 16);
+            }
+            *reinterpret_cast<uint4*>(xn + base + 8 * (tid + 256 * i)) = make_uint4(o[0], o[1], o[2], o[3]);
         }
 }
 
@@ -64,35 +85,18 @@ __device__ __forceinline__ void dequant_word(uint32_t w, float s, float b, float
         out[t] = fmaf(static_cast<float>((w >> (BITS * t)) & ((1u << BITS) - 1u)), s, b);
 }
 
-// 32 / BITS bf16 values of row m at column k0 (k0 a multiple of 32 / BITS).
-template <int BITS>
-__device__ __forceinline__ void load_bf16_run(const uint16_t* p, float (&x)[32 / BITS]) {
-    if constexpr (BITS == 4) {
-        const uint4 q = *reinterpret_cast<const uint4*>(p);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[2 * i] = bflo(w[i]);
-            x[2 * i + 1] = bfhi(w[i]);
-        }
-    } else {
-        const uint2 q = *reinterpret_cast<const uint2*>(p);
-        x[0] = bflo(q.x); x[1] = bfhi(q.x); x[2] = bflo(q.y); x[3] = bfhi(q.y);
-    }
-}
-
 // ------------------------------------------------------------------ read: rank projection
-// Wave w of workgroup b: output o = 4 b + w (o < R: a rank row; R <= o < R + HC: injection
-// row o - R). Lane l takes the packed words l + 64 j of the output's row and every row's
-// matching normalised inputs (read from L2: xn is M x HC x H x 2 bytes).
+// Workgroup o (256 threads): output o (o < R: a rank row; R <= o < R + HC: injection row
+// o - R). Thread t takes the packed words t + 256 i of the output's row and every row's
+// matching normalised inputs (read from L2: xn is M x HC x H x 2 bytes); UNR words' loads
+// are issued before their products. The four waves' totals are added in wave order.
 template <int BITS, int MR>
 __global__ __launch_bounds__(256) void k_hc_down(HcDev D, int M, const uint16_t* __restrict__ xn, float* __restrict__ act,
                                                  uint16_t* __restrict__ inj) {
-    constexpr int VPW = 32 / BITS;
-    const int lane = threadIdx.x & 63;
-    const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int n_out = D.R + (D.with_inj ? D.HC : 0);
-    if (o >= n_out) return;  // wave-uniform
+    constexpr int VPW = 32 / BITS, XW = VPW / 2, UNR = MR <= 4 ? 4 : MR <= 8 ? 2 : 1;
+    __shared__ float red[4][MR];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int o = blockIdx.x;
     const int K = D.HC * D.H, words = K / VPW, groups = K / D.G;
     const bool rank_row = o < D.R;
     const int row = rank_row ? o : o - D.R;
@@ -102,98 +106,143 @@ __global__ __launch_bounds__(256) void k_hc_down(HcDev D, int M, const uint16_t*
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
-    for (int j = lane; j < words; j += 64) {
-        const int k0 = j * VPW, g = k0 / D.G;
-        float wq[VPW];
-        dequant_word<BITS>(W[j], bf2f(S[g]), bf2f(Bi[g]), wq);
+    for (int j0 = tid; j0 < words; j0 += 256 * UNR) {
+        uint32_t wv[UNR], xr[UNR][MR][XW];
+        float sv[UNR], bv[UNR];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const int mm = m < M ? m : M - 1;  // (rows past M repeat the last one; unused)
-            float x[VPW];
-            load_bf16_run<BITS>(xn + static_cast<size_t>(mm) * K + k0, x);
+        for (int u = 0; u < UNR; ++u) {
+            const int j = j0 + 256 * u < words ? j0 + 256 * u : j0;  // (past the end: repeated, unused)
+            const int g = j * VPW / D.G;
+            wv[u] = W[j];
+            sv[u] = bf2f(S[g]);
+            bv[u] = bf2f(Bi[g]);
 #pragma unroll
-            for (int t = 0; t < VPW; ++t) acc[m] = fmaf(x[t], wq[t], acc[m]);
+            for (int m = 0; m < MR; ++m) {
+                const uint16_t* p = xn + static_cast<size_t>(m < M ? m : M - 1) * K + j * VPW;
+                if constexpr (XW == 4) {
+                    const uint4 q = *reinterpret_cast<const uint4*>(p);
+                    xr[u][m][0] = q.x; xr[u][m][1] = q.y; xr[u][m][2] = q.z; xr[u][m][3] = q.w;
+                } else {
+                    const uint2 q = *reinterpret_cast<const uint2*>(p);
+                    xr[u][m][0] = q.x; xr[u][m][1] = q.y;
+                }
+            }
         }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u)
+            if (j0 + 256 * u < words) {
+                float wq[VPW];
+                dequant_word<BITS>(wv[u], sv[u], bv[u], wq);
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+#pragma unroll
+                    for (int t = 0; t < XW; ++t) {
+                        acc[m] = fmaf(bflo(xr[u][m][t]), wq[2 * t], acc[m]);
+                        acc[m] = fmaf(bfhi(xr[u][m][t]), wq[2 * t + 1], acc[m]);
+                    }
+            }
     }
-    const float inv_hc = 1.0f / static_cast<float>(D.HC);
-    auto finish = [&](int m, float total) {
+    if constexpr (MR == 1) {
+        const float t = wave_sum_xor(acc[0]);
+        if (lane == 0) red[wave][0] = t;
+    } else {
+        wave_sum_xor_scatter<MR>(acc);
+#pragma unroll
+        for (int s = 0; s < scatter_slots<MR>(); ++s)
+            if (scatter_leader<MR>(lane)) red[wave][scatter_value<MR>(s, lane >> 4)] = acc[s];
+    }
+    lds_barrier();
+    if (tid < M) {
+        const int m = tid;
+        const float total = ((red[0][m] + red[1][m]) + red[2][m]) + red[3][m];
         if (rank_row) {
             const float v = rbf(total / static_cast<float>(D.HC));
             act[static_cast<size_t>(m) * D.R + row] = rbf(v * rbf(sigmoid_f(v)));
         } else {
-            const float v = rbf(rbf(total) * rbf(inv_hc));
+            const float v = rbf(rbf(total) * rbf(1.0f / static_cast<float>(D.HC)));
             inj[static_cast<size_t>(m) * D.HC + row] = f2bf(rbf(sigmoid_f(v)) * 2.0f);
-        }
-    };
-    if constexpr (MR == 1) {
-        const float t = wave_sum_xor(acc[0]);
-        if (lane == 0) finish(0, t);
-    } else {
-        wave_sum_xor_scatter<MR>(acc);
-#pragma unroll
-        for (int s = 0; s < scatter_slots<MR>(); ++s) {
-            const int m = scatter_value<MR>(s, lane >> 4);
-            if (scatter_leader<MR>(lane) && m < M) finish(m, acc[s]);
         }
     }
 }
 
 // ------------------------------------------------------------------ read: expansion + mix
-// Workgroup b, HC waves: wave h = stream h, lane l = column c = 64 b + l, whose weight row is
-// h H + c (R / VPW packed words, R / G groups). The rows' rank activations are staged in LDS
-// (every lane reads the same one: broadcast); the streams' terms meet in LDS and lane l of
-// wave 0 adds them in stream order.
+// Workgroup b, HC waves: wave h = stream h; lanes 4c' .. 4c' + 3 share column c = 16 b + c',
+// whose weight row is h H + c (R / VPW packed words, R / G groups), lane quarter q taking the
+// row's 16-byte quads q, q + 4, ... (each inside one scale group). The quarters' partial
+// sums meet by two DPP steps ((q0 + q1) + (q2 + q3)). The rows' rank activations are staged
+// in LDS; the streams' terms meet in LDS and are added in stream order.
 template <int BITS, int MR>
 __global__ __launch_bounds__(1024) void k_hc_up(HcDev D, int M, const uint16_t* __restrict__ xn,
                                                 const float* __restrict__ act, uint16_t* __restrict__ mixed) {
-    constexpr int VPW = 32 / BITS;
+    constexpr int VPW = 32 / BITS, QMAX = kHcMaxRank / VPW / 16;
     extern __shared__ __align__(16) float hc_lds[];
     float* acts = hc_lds;                                     // [M][R]
-    float* terms = hc_lds + static_cast<size_t>(MR) * D.R;    // [MR][HC][64]
+    float* terms = hc_lds + static_cast<size_t>(MR) * D.R;    // [MR][HC][16]
     const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
     const int H = D.H, R = D.R, HC = D.HC;
-    for (int i = tid; i < M * R; i += 64 * HC) acts[i] = act[i];
-    const int c = blockIdx.x * 64 + lane;
+    const int cl = lane >> 2, q = lane & 3;
+    const int c = blockIdx.x * 16 + cl;
     const size_t wrow = static_cast<size_t>(h) * H + c;
-    const int words = R / VPW, groups = R / D.G;
-    const uint32_t* W = D.uw + wrow * words;
+    const int nq = R / VPW / 4, groups = R / D.G;
+    const uint4* W4 = reinterpret_cast<const uint4*>(D.uw + wrow * (R / VPW));
     const uint16_t* S = D.us + wrow * groups;
     const uint16_t* Bi = D.ub + wrow * groups;
+    uint4 wv[QMAX];
+    float sv[QMAX], bv[QMAX];
+#pragma unroll
+    for (int i = 0; i < QMAX; ++i) {
+        const int qi = q + 4 * i < nq ? q + 4 * i : 0;  // (past the row's quads: quad 0, unused)
+        const int g = qi * 4 * VPW / D.G;
+        wv[i] = W4[qi];
+        sv[i] = bf2f(S[g]);
+        bv[i] = bf2f(Bi[g]);
+    }
+    // the epilogue's normalised stream values (lanes q == 0), requested with the weights
+    uint16_t xe[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) xe[m] = xn[(static_cast<size_t>(m < M ? m : M - 1) * HC + h) * H + c];
+    for (int i = tid; i < M * R; i += 64 * HC) acts[i] = act[i];
     lds_barrier();
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
-    for (int j4 = 0; j4 < words; j4 += 4) {
-        const uint4 q = *reinterpret_cast<const uint4*>(W + j4);
-        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r0 = (j4 + i) * VPW, g = r0 / D.G;
-            float wq[VPW];
-            dequant_word<BITS>(w4[i], bf2f(S[g]), bf2f(Bi[g]), wq);
+    for (int i = 0; i < QMAX; ++i)
+        if (q + 4 * i < nq) {
+            const uint32_t w4[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const int mm = m < M ? m : M - 1;
+            for (int k = 0; k < 4; ++k) {
+                const int r0 = ((q + 4 * i) * 4 + k) * VPW;
+                float wq[VPW];
+                dequant_word<BITS>(w4[k], sv[i], bv[i], wq);
 #pragma unroll
-                for (int t = 0; t < VPW; ++t) acc[m] = fmaf(acts[mm * R + r0 + t], wq[t], acc[m]);
+                for (int m = 0; m < MR; ++m) {
+                    const int mm = m < M ? m : M - 1;
+#pragma unroll
+                    for (int t = 0; t < VPW; ++t) acc[m] = fmaf(acts[mm * R + r0 + t], wq[t], acc[m]);
+                }
             }
         }
-    }
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-        if (m < M) {
-            const float u = rbf(acc[m]);
-            const float gate = rbf(sigmoid_f(u));
-            const float x = bf2f(xn[(static_cast<size_t>(m) * HC + h) * H + c]);
-            terms[(m * HC + h) * 64 + lane] = rbf(gate * x);
-        }
+    for (int m = 0; m < MR; ++m) {
+        acc[m] = acc[m] + xor_lane_f<1>(acc[m]);
+        acc[m] = acc[m] + xor_lane_f<2>(acc[m]);
+    }
+    if (q == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            if (m < M) {
+                const float u = rbf(acc[m]);
+                const float gate = rbf(sigmoid_f(u));
+                terms[(m * HC + h) * 16 + cl] = rbf(gate * bf2f(xe[m]));
+            }
+    }
     lds_barrier();
-    if (h == 0) {
-        for (int m = 0; m < M; ++m) {
-            float s = 0.0f;
-            for (int hh = 0; hh < HC; ++hh) s += terms[(m * HC + hh) * 64 + lane];
-            mixed[static_cast<size_t>(m) * H + c] = f2bf(rbf(s) / static_cast<float>(HC));
-        }
+    for (int i = tid; i < M * 16; i += 64 * HC) {
+        const int m = i >> 4, cc = i & 15;
+        float s = 0.0f;
+        for (int hh = 0; hh < HC; ++hh) s += terms[(m * HC + hh) * 16 + cc];
+        mixed[static_cast<size_t>(m) * H + blockIdx.x * 16 + cc] = f2bf(rbf(s) / static_cast<float>(HC));
     }
 }
 
@@ -244,11 +293,11 @@ hipError_t launch_hc_read_mr(const HcDev& D, int M, const uint16_t* stream, uint
     hipError_t e = launch(k_hc_norm, dim3(D.HC, M), dim3(256), 0, st, D, stream, xn);
     if (e != hipSuccess) return e;
     const int n_out = D.R + (D.with_inj ? D.HC : 0);
-    e = launch(k_hc_down<BITS, MR>, dim3((n_out + 3) / 4), dim3(256), 0, st, D, M, xn, act, inj);
+    e = launch(k_hc_down<BITS, MR>, dim3(n_out), dim3(256), 0, st, D, M, xn, act, inj);
     if (e != hipSuccess) return e;
-    const size_t lds = (static_cast<size_t>(MR) * D.R + static_cast<size_t>(MR) * D.HC * 64) * sizeof(float);
+    const size_t lds = (static_cast<size_t>(MR) * D.R + static_cast<size_t>(MR) * D.HC * 16) * sizeof(float);
     if ((e = ensure_lds<k_hc_up<BITS, MR>>(hc_up_lds_max())) != hipSuccess) return e;
-    return launch(k_hc_up<BITS, MR>, dim3(D.H / 64), dim3(64 * D.HC), lds, st, D, M, xn, act, mixed);
+    return launch(k_hc_up<BITS, MR>, dim3(D.H / 16), dim3(64 * D.HC), lds, st, D, M, xn, act, mixed);
 }
 
 template <int BITS>
@@ -264,7 +313,7 @@ hipError_t launch_hc_read_b(const HcDev& D, int M, const uint16_t* stream, uint1
 } // namespace
 
 size_t hc_up_lds_max() {
-    return (static_cast<size_t>(kMaxRows) * kHcMaxRank + static_cast<size_t>(kMaxRows) * kHcMaxStreams * 64) *
+    return (static_cast<size_t>(kMaxRows) * kHcMaxRank + static_cast<size_t>(kMaxRows) * kHcMaxStreams * 16) *
            sizeof(float);
 }
 

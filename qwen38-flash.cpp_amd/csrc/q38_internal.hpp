@@ -122,6 +122,10 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
 hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 // chain: h <- h + y (in place); otherwise out <- y. Down rows are read at the route index.
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);
+// The combine followed by the HyperConnection write of the layer output into hs ([M][HC][H]
+// bf16, in place) with the per-row stream gates inj ([M][HC] bf16).
+hipError_t launch_combine_hc(const LayerDev& L, const MoeBufs& B, int M, uint16_t* hs, const uint16_t* inj, int HC,
+                             hipStream_t st);
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st);
 hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_t* book4, hipStream_t st);
 hipError_t launch_split_book_i8(const int8_t* book, float scale, int entries, int dim, uint16_t* book4,

@@ -851,47 +851,89 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
 // r * k + s and the shared expert's row r at M * k + r, so every load here is independent
 // of the plan and all of them are issued before the first use.
 template <int KT, bool TWO>
-__global__ __launch_bounds__(256) void k_combine(LayerDev L, MoeBufs B, int M, uint16_t* h, uint16_t* out) {
-    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + 3 * sizeof(void*)>();
-    const int r = blockIdx.y;
-    const int o = blockIdx.x * 256 + threadIdx.x;
+struct CombineIn {
+    float wts[KT + 1];    // route weights in slot order, then the shared gate
+    float dv[KT + 1][2];  // the routes' (and the shared expert's) down outputs, both planes
+};
+
+// Every load is unconditional and issued up front, the row's route weights and gate first
+// (each wait below then covers only what it needs); with no shared expert the shared read
+// repeats route 0 (that route is opaque to the optimizer, so it cannot split the code on it).
+template <int KT, bool TWO>
+__device__ __forceinline__ void combine_load(const LayerDev& L, const MoeBufs& B, int M, int r, int o,
+                                             CombineIn<KT, TWO>& in) {
     const int H = L.H, MK = M * KT;
-    Q38_STAMP(24576, 0);
-    if (o >= H) return;
-    constexpr bool two = TWO;  // L.d_parts == 2
-    const bool shared = L.has_shared;
-    // Every load is unconditional and issued up front, the row's route weights and gate
-    // first (each wait below then covers only what it needs): the residual comes from the
-    // output row when there is none, and with no shared expert its read repeats route 0
-    // (that route is opaque to the optimizer, so it cannot split the code on it).
-    float wts[KT + 1];
 #pragma unroll
-    for (int s = 0; s < KT; ++s) wts[s] = B.weights[r * KT + s];
-    wts[KT] = B.sgate[r];
-    const uint16_t hraw = (h ? h : out)[static_cast<size_t>(r) * H + o];
-    int shared_route = shared ? MK + r : r * KT;  // (no shared expert: route 0 again, unused)
+    for (int s = 0; s < KT; ++s) in.wts[s] = B.weights[r * KT + s];
+    in.wts[KT] = B.sgate[r];
+    int shared_route = L.has_shared ? MK + r : r * KT;
     asm("" : "+s"(shared_route));
-    float dv[KT + 1][2];
 #pragma unroll
     for (int s = 0; s <= KT; ++s) {
         const int route = s < KT ? r * KT + s : shared_route;
         const size_t at = static_cast<size_t>(route) * H + o;
-        dv[s][0] = B.d[at];
-        dv[s][1] = two ? B.d[B.d_plane + at] : 0.0f;
+        in.dv[s][0] = B.d[at];
+        in.dv[s][1] = TWO ? B.d[B.d_plane + at] : 0.0f;
     }
-    const float hv = h ? bf2f(hraw) : 0.0f;
+}
+
+template <int KT, bool TWO>
+__device__ __forceinline__ float combine_value(const LayerDev& L, const CombineIn<KT, TWO>& in) {
     float routed = 0.0f;
 #pragma unroll
-    for (int s = 0; s < KT; ++s) routed = fmaf(wts[s], rbf(two ? dv[s][0] + dv[s][1] : dv[s][0]), routed);
+    for (int s = 0; s < KT; ++s) routed = fmaf(in.wts[s], rbf(TWO ? in.dv[s][0] + in.dv[s][1] : in.dv[s][0]), routed);
     float y = rbf(routed);
-    if (shared) {
-        const float sh = rbf(rbf(two ? dv[KT][0] + dv[KT][1] : dv[KT][0]) * wts[KT]);
+    if (L.has_shared) {
+        const float sh = rbf(rbf(TWO ? in.dv[KT][0] + in.dv[KT][1] : in.dv[KT][0]) * in.wts[KT]);
         y = rbf(y + sh);
     }
+    return y;
+}
+
+template <int KT, bool TWO>
+__global__ __launch_bounds__(256) void k_combine(LayerDev L, MoeBufs B, int M, uint16_t* h, uint16_t* out) {
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + 3 * sizeof(void*)>();
+    const int r = blockIdx.y;
+    const int o = blockIdx.x * 256 + threadIdx.x;
+    const int H = L.H;
+    Q38_STAMP(24576, 0);
+    if (o >= H) return;
+    CombineIn<KT, TWO> in;
+    combine_load<KT, TWO>(L, B, M, r, o, in);
+    // the residual comes from the output row when there is none (unused then)
+    const uint16_t hraw = (h ? h : out)[static_cast<size_t>(r) * H + o];
+    const float y = combine_value<KT, TWO>(L, in);
     const size_t i = static_cast<size_t>(r) * H + o;
-    if (h) h[i] = f2bf(rbf(hv + y));
+    if (h) h[i] = f2bf(rbf(bf2f(hraw) + y));
     else out[i] = f2bf(y);
     Q38_STAMP(24576, 1);
+}
+
+// The same combine followed by the HyperConnection write of the layer output into the row's
+// HC streams (HyperConnection::write, src/hyper_connection.cpp:692-709): stream s of row r
+// becomes T(stream + T(y * inj[r][s])), y never leaves registers.
+template <int KT, bool TWO>
+__global__ __launch_bounds__(256) void k_combine_hc(LayerDev L, MoeBufs B, int M, uint16_t* hs, const uint16_t* inj,
+                                                    int HC) {
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + 3 * sizeof(void*)>();
+    const int r = blockIdx.y;
+    const int o = blockIdx.x * 256 + threadIdx.x;
+    const int H = L.H;
+    if (o >= H) return;
+    CombineIn<KT, TWO> in;
+    combine_load<KT, TWO>(L, B, M, r, o, in);
+    uint16_t sv[kHcMaxStreams], gv[kHcMaxStreams];
+    const size_t row = static_cast<size_t>(r) * HC * H + o;
+#pragma unroll
+    for (int s = 0; s < kHcMaxStreams; ++s)
+        if (s < HC) {
+            sv[s] = hs[row + static_cast<size_t>(s) * H];
+            gv[s] = inj[r * HC + s];
+        }
+    const float y = combine_value<KT, TWO>(L, in);
+#pragma unroll
+    for (int s = 0; s < kHcMaxStreams; ++s)
+        if (s < HC) hs[row + static_cast<size_t>(s) * H] = f2bf(bf2f(sv[s]) + rbf(y * bf2f(gv[s])));
 }
 
 __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x, int H, float eps,
@@ -1158,31 +1200,47 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
 }
 
 template <int KT>
-hipError_t launch_combine_k(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
-    if (L.d_parts == 2) return launch(k_combine<KT, true>, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
-    return launch(k_combine<KT, false>, dim3((L.H + 255) / 256, M), dim3(256), 0, st, L, B, M, h, out);
+hipError_t launch_combine_k(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, const uint16_t* inj,
+                            int HC, hipStream_t st) {
+    const dim3 grid((L.H + 255) / 256, M);
+    if (inj) {
+        if (L.d_parts == 2) return launch(k_combine_hc<KT, true>, grid, dim3(256), 0, st, L, B, M, h, inj, HC);
+        return launch(k_combine_hc<KT, false>, grid, dim3(256), 0, st, L, B, M, h, inj, HC);
+    }
+    if (L.d_parts == 2) return launch(k_combine<KT, true>, grid, dim3(256), 0, st, L, B, M, h, out);
+    return launch(k_combine<KT, false>, grid, dim3(256), 0, st, L, B, M, h, out);
+}
+
+static hipError_t launch_combine_any(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out,
+                                     const uint16_t* inj, int HC, hipStream_t st) {
+    switch (L.K) {
+        case 1: return launch_combine_k<1>(L, B, M, h, out, inj, HC, st);
+        case 2: return launch_combine_k<2>(L, B, M, h, out, inj, HC, st);
+        case 3: return launch_combine_k<3>(L, B, M, h, out, inj, HC, st);
+        case 4: return launch_combine_k<4>(L, B, M, h, out, inj, HC, st);
+        case 5: return launch_combine_k<5>(L, B, M, h, out, inj, HC, st);
+        case 6: return launch_combine_k<6>(L, B, M, h, out, inj, HC, st);
+        case 7: return launch_combine_k<7>(L, B, M, h, out, inj, HC, st);
+        case 8: return launch_combine_k<8>(L, B, M, h, out, inj, HC, st);
+        case 9: return launch_combine_k<9>(L, B, M, h, out, inj, HC, st);
+        case 10: return launch_combine_k<10>(L, B, M, h, out, inj, HC, st);
+        case 11: return launch_combine_k<11>(L, B, M, h, out, inj, HC, st);
+        case 12: return launch_combine_k<12>(L, B, M, h, out, inj, HC, st);
+        case 13: return launch_combine_k<13>(L, B, M, h, out, inj, HC, st);
+        case 14: return launch_combine_k<14>(L, B, M, h, out, inj, HC, st);
+        case 15: return launch_combine_k<15>(L, B, M, h, out, inj, HC, st);
+        case 16: return launch_combine_k<16>(L, B, M, h, out, inj, HC, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
-    switch (L.K) {
-        case 1: return launch_combine_k<1>(L, B, M, h, out, st);
-        case 2: return launch_combine_k<2>(L, B, M, h, out, st);
-        case 3: return launch_combine_k<3>(L, B, M, h, out, st);
-        case 4: return launch_combine_k<4>(L, B, M, h, out, st);
-        case 5: return launch_combine_k<5>(L, B, M, h, out, st);
-        case 6: return launch_combine_k<6>(L, B, M, h, out, st);
-        case 7: return launch_combine_k<7>(L, B, M, h, out, st);
-        case 8: return launch_combine_k<8>(L, B, M, h, out, st);
-        case 9: return launch_combine_k<9>(L, B, M, h, out, st);
-        case 10: return launch_combine_k<10>(L, B, M, h, out, st);
-        case 11: return launch_combine_k<11>(L, B, M, h, out, st);
-        case 12: return launch_combine_k<12>(L, B, M, h, out, st);
-        case 13: return launch_combine_k<13>(L, B, M, h, out, st);
-        case 14: return launch_combine_k<14>(L, B, M, h, out, st);
-        case 15: return launch_combine_k<15>(L, B, M, h, out, st);
-        case 16: return launch_combine_k<16>(L, B, M, h, out, st);
-        default: return hipErrorInvalidValue;
-    }
+    return launch_combine_any(L, B, M, h, out, nullptr, 0, st);
+}
+
+hipError_t launch_combine_hc(const LayerDev& L, const MoeBufs& B, int M, uint16_t* hs, const uint16_t* inj, int HC,
+                             hipStream_t st) {
+    return launch_combine_any(L, B, M, hs, nullptr, inj, HC, st);
 }
 
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st) {

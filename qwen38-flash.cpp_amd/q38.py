@@ -158,6 +158,8 @@ _sig("q38_hc_workspace_size", SZ, C.POINTER(HcDesc), I32)
 _sig("q38_hc_read", C.c_int, P, P, I32, P, P, P, SZ, P)
 _sig("q38_hc_write", C.c_int, P, P, P, P, I32, P, P)
 _sig("q38_hc_initialize_stream", C.c_int, P, I32, I32, I32, P, P)
+_sig("q38_verify_chain_hc_workspace_size", SZ, C.POINTER(MoeDesc), C.POINTER(HcDesc), I32)
+_sig("q38_verify_chain_hc", C.c_int, P, P, I32, P, I32, P, SZ, P)
 
 
 def check(rc: int) -> int:

@@ -175,3 +175,68 @@ def test_hc_rejects(gpu, q38):
         assert e.value.code == q38.Q38_EINVAL
     finally:
         hc.close()
+
+
+def chain_hc(q38, layers, mixers, stream_np):
+    import ctypes as C
+    M = stream_np.shape[0]
+    st = G.to_dev(stream_np)
+    d, hd = layers[0].desc, mixers[0].desc
+    ws = G.workspace(q38.lib.q38_verify_chain_hc_workspace_size(C.byref(d), C.byref(hd), M))
+    la = (C.c_void_p * len(layers))(*[L.h.value for L in layers])
+    ma = (C.c_void_p * len(mixers))(*[h.h.value for h in mixers])
+    q38.check(q38.lib.q38_verify_chain_hc(la, ma, len(layers), st.data_ptr(), M, ws.data_ptr(), ws.numel(),
+                                          G.stream()))
+    return G.to_host(st, np.uint16)
+
+
+def test_chain_hc_layers(gpu, q38, orc):
+    """The decoder's MLP half over 3 layers (mixer read -> MoE -> mixer write) at 4 rows:
+    the fused chain equals the layer-by-layer composition of q38_hc_read, q38_moe_forward and
+    q38_hc_write bit for bit, and each layer, fed the GPU's own stream (teacher forcing),
+    matches the oracle's read -> MoE -> write: routing of the GPU's block input bit-exact,
+    the block input within one bf16 step, the new stream within the MoE bar."""
+    import ctypes as C
+    import oracle_lib
+    from moe_cases import SEED, tol_check
+    rng = np.random.default_rng(77)
+    M, NL = 4, 3
+    layers = [q38.MoeLayer(gpu, q38.desc(), seed=SEED, layer=l) for l in range(NL)]
+    built = [build(q38, gpu, rng) for _ in range(NL)]
+    mixers = [b[2] for b in built]
+    try:
+        d0, H, HC = built[0][0], 2048, 4
+        stream = to_bf16_bits(rng.normal(0, 1.0, (M, HC * H)).astype(np.float32))
+        fused = chain_hc(q38, layers, mixers, stream)
+        s = stream
+        od = oracle_lib.make_desc()
+        for l in range(NL):
+            d, w, hc = built[l]
+            mixed, inj, _, _ = gpu_read(q38, hc, d, s)
+            x_d = G.to_dev(mixed)
+            y = G.empty((M, H), np.uint16)
+            ex = G.empty(M * 10, np.int32)
+            wt = G.empty(M * 10, np.float32)
+            ws = G.workspace(q38.lib.q38_moe_workspace_size(C.byref(layers[l].desc), M))
+            r = q38.routes(experts=ex, weights=wt)
+            q38.check(q38.lib.q38_moe_forward(layers[l].h, x_d.data_ptr(), M, y.data_ptr(), C.byref(r),
+                                              ws.data_ptr(), ws.numel(), G.stream()))
+            out = G.empty((M, HC * H), np.uint16)
+            hc.write(G.to_dev(s), y, G.to_dev(inj), M, out, G.stream())
+            s_next = G.to_host(out, np.uint16)
+            # oracle, teacher-forced on the GPU's stream s
+            m_ref, i_ref, _, _ = orc.hc_read(d, w, s)
+            assert ulp_diff(mixed, m_ref).max() <= 1
+            assert ulp_diff(inj, i_ref).max() <= 1
+            y_ref, ex_ref, wt_ref, _ = orc.moe_layer_synth(od, SEED, l, mixed)
+            assert np.array_equal(G.to_host(ex).reshape(M, 10), ex_ref)
+            assert np.array_equal(G.to_host(wt).reshape(M, 10), wt_ref)
+            tol_check(orc, G.to_host(y, np.uint16), y_ref)
+            tol_check(orc, s_next, orc.hc_write(H, HC, s, y_ref, inj))
+            s = s_next
+        assert np.array_equal(fused, s)
+    finally:
+        for L in layers:
+            L.close()
+        for h in mixers:
+            h.close()
