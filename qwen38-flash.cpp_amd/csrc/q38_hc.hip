@@ -10,7 +10,7 @@
 //               streams (MLX affine weights: q * scale + bias per group, 4 or 8 bits),
 //               a = T(v * T(sigmoid(v))) with v = T(dot / HC); the injection outputs in the
 //               same launch, inj = T(2 * T(sigmoid(T(T(dot) * T(1 / HC)))))
-//   k_hc_up     four lanes per (stream, column): u = T(dot over the rank), gate = T(sigmoid(u)),
+//   k_hc_up     eight lanes per (stream, column): u = T(dot over the rank), gate = T(sigmoid(u)),
 //               the stream's term T(gate * xn); the workgroup adds the HC terms in stream
 //               order in float: mixed = T(T(sum) / HC)
 //   k_hc_write  stream <- T(stream + T(block_output * inj[stream]))
@@ -166,22 +166,23 @@ __global__ __launch_bounds__(256) void k_hc_down(HcDev D, int M, const uint16_t*
 }
 
 // ------------------------------------------------------------------ read: expansion + mix
-// Workgroup b, HC waves: wave h = stream h; lanes 4c' .. 4c' + 3 share column c = 16 b + c',
-// whose weight row is h H + c (R / VPW packed words, R / G groups), lane quarter q taking the
-// row's 16-byte quads q, q + 4, ... (each inside one scale group). The quarters' partial
-// sums meet by two DPP steps ((q0 + q1) + (q2 + q3)). The rows' rank activations are staged
-// in LDS; the streams' terms meet in LDS and are added in stream order.
+// Workgroup b, HC waves: wave h = stream h; lanes 8c' .. 8c' + 7 share column c = 8 b + c',
+// whose weight row is h H + c (R / VPW packed words, R / G groups), lane octant q taking the
+// row's 16-byte quads q, q + 8, ... (each inside one scale group). The octants' partial sums
+// meet by three DPP steps (((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7))). The rows' rank
+// activations are staged in LDS and read 16 bytes at a time (the 8 columns of a wave read
+// the same ones); the streams' terms meet in LDS and are added in stream order.
 template <int BITS, int MR>
 __global__ __launch_bounds__(1024) void k_hc_up(HcDev D, int M, const uint16_t* __restrict__ xn,
                                                 const float* __restrict__ act, uint16_t* __restrict__ mixed) {
-    constexpr int VPW = 32 / BITS, QMAX = kHcMaxRank / VPW / 16;
+    constexpr int VPW = 32 / BITS, QMAX = kHcMaxRank / VPW / 32;
     extern __shared__ __align__(16) float hc_lds[];
     float* acts = hc_lds;                                     // [M][R]
-    float* terms = hc_lds + static_cast<size_t>(MR) * D.R;    // [MR][HC][16]
+    float* terms = hc_lds + static_cast<size_t>(MR) * D.R;    // [MR][HC][8]
     const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
     const int H = D.H, R = D.R, HC = D.HC;
-    const int cl = lane >> 2, q = lane & 3;
-    const int c = blockIdx.x * 16 + cl;
+    const int cl = lane >> 3, q = lane & 7;
+    const int c = blockIdx.x * 8 + cl;
     const size_t wrow = static_cast<size_t>(h) * H + c;
     const int nq = R / VPW / 4, groups = R / D.G;
     const uint4* W4 = reinterpret_cast<const uint4*>(D.uw + wrow * (R / VPW));
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(1024) void k_hc_up(HcDev D, int M, const uint16_t* 
     float sv[QMAX], bv[QMAX];
 #pragma unroll
     for (int i = 0; i < QMAX; ++i) {
-        const int qi = q + 4 * i < nq ? q + 4 * i : 0;  // (past the row's quads: quad 0, unused)
+        const int qi = q + 8 * i < nq ? q + 8 * i : 0;  // (past the row's quads: quad 0, unused)
         const int g = qi * 4 * VPW / D.G;
         wv[i] = W4[qi];
         sv[i] = bf2f(S[g]);
@@ -201,25 +202,43 @@ __global__ __launch_bounds__(1024) void k_hc_up(HcDev D, int M, const uint16_t* 
     uint16_t xe[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) xe[m] = xn[(static_cast<size_t>(m < M ? m : M - 1) * HC + h) * H + c];
-    for (int i = tid; i < M * R; i += 64 * HC) acts[i] = act[i];
+    {   // the activations into LDS, 16 bytes a thread and four loads in flight before the stores
+        const int n4 = M * R / 4, nt = 64 * HC;
+        const uint4* src = reinterpret_cast<const uint4*>(act);
+        uint4* dst = reinterpret_cast<uint4*>(acts);
+        for (int b = tid; b < n4; b += 4 * nt) {
+            uint4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = src[b + u * nt < n4 ? b + u * nt : b];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (b + u * nt < n4) dst[b + u * nt] = v[u];
+        }
+    }
     lds_barrier();
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
 #pragma unroll
     for (int i = 0; i < QMAX; ++i)
-        if (q + 4 * i < nq) {
+        if (q + 8 * i < nq) {
             const uint32_t w4[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const int r0 = ((q + 4 * i) * 4 + k) * VPW;
+                const int r0 = ((q + 8 * i) * 4 + k) * VPW;
                 float wq[VPW];
                 dequant_word<BITS>(w4[k], sv[i], bv[i], wq);
 #pragma unroll
                 for (int m = 0; m < MR; ++m) {
-                    const int mm = m < M ? m : M - 1;
+                    const float4* a4 = reinterpret_cast<const float4*>(acts + (m < M ? m : M - 1) * R + r0);
 #pragma unroll
-                    for (int t = 0; t < VPW; ++t) acc[m] = fmaf(acts[mm * R + r0 + t], wq[t], acc[m]);
+                    for (int t4 = 0; t4 < VPW / 4; ++t4) {
+                        const float4 av = a4[t4];
+                        acc[m] = fmaf(av.x, wq[4 * t4], acc[m]);
+                        acc[m] = fmaf(av.y, wq[4 * t4 + 1], acc[m]);
+                        acc[m] = fmaf(av.z, wq[4 * t4 + 2], acc[m]);
+                        acc[m] = fmaf(av.w, wq[4 * t4 + 3], acc[m]);
+                    }
                 }
             }
         }
@@ -227,6 +246,7 @@ __global__ __launch_bounds__(1024) void k_hc_up(HcDev D, int M, const uint16_t* 
     for (int m = 0; m < MR; ++m) {
         acc[m] = acc[m] + xor_lane_f<1>(acc[m]);
         acc[m] = acc[m] + xor_lane_f<2>(acc[m]);
+        acc[m] = acc[m] + xor_lane_f<4>(acc[m]);
     }
     if (q == 0) {
 #pragma unroll
@@ -234,15 +254,15 @@ __global__ __launch_bounds__(1024) void k_hc_up(HcDev D, int M, const uint16_t* 
             if (m < M) {
                 const float u = rbf(acc[m]);
                 const float gate = rbf(sigmoid_f(u));
-                terms[(m * HC + h) * 16 + cl] = rbf(gate * bf2f(xe[m]));
+                terms[(m * HC + h) * 8 + cl] = rbf(gate * bf2f(xe[m]));
             }
     }
     lds_barrier();
-    for (int i = tid; i < M * 16; i += 64 * HC) {
-        const int m = i >> 4, cc = i & 15;
+    for (int i = tid; i < M * 8; i += 64 * HC) {
+        const int m = i >> 3, cc = i & 7;
         float s = 0.0f;
-        for (int hh = 0; hh < HC; ++hh) s += terms[(m * HC + hh) * 16 + cc];
-        mixed[static_cast<size_t>(m) * H + blockIdx.x * 16 + cc] = f2bf(rbf(s) / static_cast<float>(HC));
+        for (int hh = 0; hh < HC; ++hh) s += terms[(m * HC + hh) * 8 + cc];
+        mixed[static_cast<size_t>(m) * H + blockIdx.x * 8 + cc] = f2bf(rbf(s) / static_cast<float>(HC));
     }
 }
 
@@ -295,9 +315,9 @@ hipError_t launch_hc_read_mr(const HcDev& D, int M, const uint16_t* stream, uint
     const int n_out = D.R + (D.with_inj ? D.HC : 0);
     e = launch(k_hc_down<BITS, MR>, dim3(n_out), dim3(256), 0, st, D, M, xn, act, inj);
     if (e != hipSuccess) return e;
-    const size_t lds = (static_cast<size_t>(MR) * D.R + static_cast<size_t>(MR) * D.HC * 16) * sizeof(float);
+    const size_t lds = (static_cast<size_t>(MR) * D.R + static_cast<size_t>(MR) * D.HC * 8) * sizeof(float);
     if ((e = ensure_lds<k_hc_up<BITS, MR>>(hc_up_lds_max())) != hipSuccess) return e;
-    return launch(k_hc_up<BITS, MR>, dim3(D.H / 16), dim3(64 * D.HC), lds, st, D, M, xn, act, mixed);
+    return launch(k_hc_up<BITS, MR>, dim3(D.H / 8), dim3(64 * D.HC), lds, st, D, M, xn, act, mixed);
 }
 
 template <int BITS>
@@ -313,7 +333,7 @@ hipError_t launch_hc_read_b(const HcDev& D, int M, const uint16_t* stream, uint1
 } // namespace
 
 size_t hc_up_lds_max() {
-    return (static_cast<size_t>(kMaxRows) * kHcMaxRank + static_cast<size_t>(kMaxRows) * kHcMaxStreams * 16) *
+    return (static_cast<size_t>(kMaxRows) * kHcMaxRank + static_cast<size_t>(kMaxRows) * kHcMaxStreams * 8) *
            sizeof(float);
 }
 
