@@ -261,6 +261,89 @@ void SparseMoe::set_router_bias(const DeviceTensor& bias) {
     check(q38_moe_layer_set_router_bias(layer_, static_cast<const float*>(bias.data())), "set_router_bias");
 }
 
+// ------------------------------------------------------------------ HyperConnection mixer
+HyperConnection::HyperConnection(const Context& ctx, const q38_hc_weights& tensors, std::size_t hidden_size,
+                                 std::size_t stream_count, std::size_t rank, std::size_t quantization_bits,
+                                 std::size_t quantization_group_size, float rms_norm_epsilon, bool with_injection)
+    : ctx_(&ctx) {
+    if (!(rms_norm_epsilon > 0.0F)) throw std::runtime_error("RMS norm epsilon must be positive");
+    desc_ = q38_hc_desc{static_cast<int32_t>(hidden_size), static_cast<int32_t>(stream_count),
+                        static_cast<int32_t>(rank), static_cast<int32_t>(quantization_bits),
+                        static_cast<int32_t>(quantization_group_size), with_injection ? 1 : 0, rms_norm_epsilon};
+    check(q38_hc_create(ctx.handle(), &desc_, &tensors, &hc_), "HyperConnection");
+}
+HyperConnection::~HyperConnection() { q38_hc_destroy(hc_); }
+HyperConnection::HyperConnection(HyperConnection&& o) noexcept
+    : ctx_(o.ctx_), hc_(o.hc_), desc_(o.desc_), workspace_(std::move(o.workspace_)) {
+    o.hc_ = nullptr;
+}
+HyperConnection& HyperConnection::operator=(HyperConnection&& o) noexcept {
+    if (this != &o) {
+        q38_hc_destroy(hc_);
+        ctx_ = o.ctx_;
+        hc_ = o.hc_;
+        desc_ = o.desc_;
+        workspace_ = std::move(o.workspace_);
+        o.hc_ = nullptr;
+    }
+    return *this;
+}
+
+DeviceTensor HyperConnection::initialize_stream(const Context& ctx, const DeviceTensor& embedding,
+                                                std::size_t stream_count) {
+    const auto& s = embedding.shape();
+    if (s.size() != 3) throw std::runtime_error("hyper-connection embedding must have rank 3");
+    if (embedding.dtype() != DType::bf16) throw std::runtime_error("hyper-connection embedding must be bf16");
+    const std::size_t rows = s[0] * s[1];
+    DeviceTensor out({s[0], s[1], s[2] * stream_count}, DType::bf16);
+    check(q38_hc_initialize_stream(static_cast<const uint16_t*>(embedding.data()), static_cast<int32_t>(rows),
+                                   static_cast<int32_t>(s[2]), static_cast<int32_t>(stream_count),
+                                   static_cast<uint16_t*>(out.data()), ctx.stream()),
+          "initialize_stream");
+    return out;
+}
+
+HyperConnectionRead HyperConnection::read(const DeviceTensor& stream) const {
+    const auto& s = stream.shape();
+    const std::size_t width = static_cast<std::size_t>(desc_.hidden) * static_cast<std::size_t>(desc_.streams);
+    if (s.size() != 3 || s[2] != width || stream.dtype() != DType::bf16)
+        throw std::runtime_error("invalid hyper-connection stream shape");
+    const std::size_t rows = s[0] * s[1];
+    HyperConnectionRead out;
+    out.mixed = DeviceTensor({s[0], s[1], static_cast<std::size_t>(desc_.hidden)}, DType::bf16);
+    if (desc_.with_injection) {
+        out.injection = DeviceTensor({s[0], s[1], static_cast<std::size_t>(desc_.streams), 1}, DType::bf16);
+        out.has_injection = true;
+    }
+    std::lock_guard<std::mutex> lk(g_ws_mutex);
+    const std::size_t need = q38_hc_workspace_size(&desc_, static_cast<int32_t>(std::min<std::size_t>(rows, 16)));
+    if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
+    check(q38_hc_read(hc_, static_cast<const uint16_t*>(stream.data()), static_cast<int32_t>(rows),
+                      static_cast<uint16_t*>(out.mixed.data()),
+                      out.has_injection ? static_cast<uint16_t*>(out.injection.data()) : nullptr, workspace_.data(),
+                      workspace_.nbytes(), ctx_->stream()),
+          "HyperConnection::read");
+    return out;
+}
+
+DeviceTensor HyperConnection::write(const DeviceTensor& stream, const DeviceTensor& block_output,
+                                    const DeviceTensor& injection) const {
+    const auto& s = stream.shape();
+    if (s.size() != 3) throw std::runtime_error("hyper-connection stream must have rank 3");
+    const std::size_t rows = s[0] * s[1];
+    if (rows_of(block_output, static_cast<std::size_t>(desc_.hidden)) != rows ||
+        injection.numel() != rows * static_cast<std::size_t>(desc_.streams) ||
+        s[2] != static_cast<std::size_t>(desc_.hidden) * static_cast<std::size_t>(desc_.streams))
+        throw std::runtime_error("invalid hyper-connection write shapes");
+    DeviceTensor out(s, DType::bf16);
+    check(q38_hc_write(hc_, static_cast<const uint16_t*>(stream.data()),
+                       static_cast<const uint16_t*>(block_output.data()),
+                       static_cast<const uint16_t*>(injection.data()), static_cast<int32_t>(rows),
+                       static_cast<uint16_t*>(out.data()), ctx_->stream()),
+          "HyperConnection::write");
+    return out;
+}
+
 // ------------------------------------------------------------------ QwenModel (verify path)
 QwenModel::QwenModel(const Context& ctx, std::uint64_t seed, std::size_t layer_count, std::size_t vocab,
                      const MoeGeometry& geometry, std::size_t expert_count, std::size_t experts_per_token,

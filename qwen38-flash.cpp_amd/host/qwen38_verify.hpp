@@ -177,6 +177,49 @@ private:
     mutable DeviceTensor workspace_;
 };
 
+// ------------------------------------------------------------------ HyperConnection mixer
+// HyperConnectionRead (include/qwen38/hyper_connection.hpp:12-16).
+struct HyperConnectionRead {
+    DeviceTensor mixed;      // [B, S, H] bf16: the block input
+    DeviceTensor injection;  // [B, S, HC, 1] bf16 stream gates (empty without injection)
+    bool has_injection{false};
+};
+
+// HyperConnection (include/qwen38/hyper_connection.hpp:18-71) over device tensors in the
+// reference layout: hc_norm.weight [HC * H], input_mix_weight_down [R][HC * H] and
+// input_mix_weight_up [HC * H][R] (and block_inject_weight [HC][HC * H] when with_injection),
+// MLX affine-quantised (packed uint32 words, bf16 scales and biases per group). The reference
+// reads bits and group size from the manifest; here they are arguments.
+class HyperConnection final {
+public:
+    HyperConnection(const Context& ctx, const q38_hc_weights& tensors, std::size_t hidden_size,
+                    std::size_t stream_count, std::size_t rank, std::size_t quantization_bits,
+                    std::size_t quantization_group_size, float rms_norm_epsilon, bool with_injection);
+    ~HyperConnection();
+    HyperConnection(HyperConnection&&) noexcept;
+    HyperConnection& operator=(HyperConnection&&) noexcept;
+    HyperConnection(const HyperConnection&) = delete;
+    HyperConnection& operator=(const HyperConnection&) = delete;
+
+    // initialize_stream (src/hyper_connection.cpp:298-307): [B, S, H] -> [B, S, HC * H].
+    [[nodiscard]] static DeviceTensor initialize_stream(const Context& ctx, const DeviceTensor& embedding,
+                                                        std::size_t stream_count);
+    // read (src/hyper_connection.cpp:309-493): stream [B, S, HC * H] bf16, B * S in 1..16.
+    [[nodiscard]] HyperConnectionRead read(const DeviceTensor& stream) const;
+    // write (src/hyper_connection.cpp:692-709): stream + block_output * injection per stream.
+    [[nodiscard]] DeviceTensor write(const DeviceTensor& stream, const DeviceTensor& block_output,
+                                     const DeviceTensor& injection) const;
+
+    [[nodiscard]] q38_hc* handle() const noexcept { return hc_; }
+    [[nodiscard]] const q38_hc_desc& desc() const noexcept { return desc_; }
+
+private:
+    const Context* ctx_ = nullptr;
+    q38_hc* hc_ = nullptr;
+    q38_hc_desc desc_{};
+    mutable DeviceTensor workspace_;
+};
+
 // ------------------------------------------------------------------ verify model
 struct GreedyStep {
     std::uint32_t token{0};

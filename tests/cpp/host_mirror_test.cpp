@@ -207,6 +207,85 @@ static void batched_slot_tests(const qwen38::Context& ctx, const qwen38::QwenMod
 // advanced over the committed rows only, next stream = the correction row's pre-norm stream);
 // bad depths and positions throw with both states intact; the batched scheduler drafts
 // with the head once a slot has a committed stream.
+// HyperConnection mirror: initialize_stream tiles the embedding; read and write give the C
+// ABI's results bit for bit (one kernel family); shape errors throw as the reference does.
+static void hyper_connection_tests(const qwen38::Context& ctx) {
+    const std::size_t H = 2048, HC = 4, R = 256, G = 64, K = H * HC, M = 4;
+    std::uint64_t st = 0x9E3779B97F4A7C15ull;
+    auto next = [&] { st = st * 6364136223846793005ull + 1442695040888963407ull; return static_cast<std::uint32_t>(st >> 32); };
+    auto bf16 = [](float f) { std::uint32_t u; std::memcpy(&u, &f, 4); return static_cast<std::uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16); };
+    auto unit = [&] { return (static_cast<float>(next() >> 8) / 16777216.0f) - 0.5f; };
+    auto upload_u32 = [&](std::size_t n) {
+        std::vector<std::uint32_t> h(n);
+        for (auto& v : h) v = next();
+        qwen38::DeviceTensor t({n}, qwen38::DType::u32);
+        t.upload(h.data(), n * 4);
+        return t;
+    };
+    auto upload_bf16 = [&](std::size_t n, float scale, float offset) {
+        std::vector<std::uint16_t> h(n);
+        for (auto& v : h) v = bf16(offset + scale * unit());
+        qwen38::DeviceTensor t({n}, qwen38::DType::bf16);
+        t.upload(h.data(), n * 2);
+        return t;
+    };
+    // centred 4-bit groups: weight = q * s + b with b ~ -7.5 s
+    auto norm = upload_bf16(K, 0.2f, 0.0f);
+    auto dw = upload_u32(R * K / 8), ds = upload_bf16(R * K / G, 0.004f, 0.006f), db = upload_bf16(R * K / G, 0.002f, -0.045f);
+    auto uw = upload_u32(K * R / 8), us = upload_bf16(K * R / G, 0.004f, 0.006f), ub = upload_bf16(K * R / G, 0.002f, -0.045f);
+    auto iw = upload_u32(HC * K / 8), is = upload_bf16(HC * K / G, 0.004f, 0.006f), ib = upload_bf16(HC * K / G, 0.002f, -0.045f);
+    auto u16 = [](const qwen38::DeviceTensor& t) { return static_cast<const std::uint16_t*>(t.data()); };
+    auto u32 = [](const qwen38::DeviceTensor& t) { return static_cast<const std::uint32_t*>(t.data()); };
+    const q38_hc_weights w{u16(norm), u32(dw), u16(ds), u16(db), u32(uw), u16(us), u16(ub), u32(iw), u16(is), u16(ib)};
+    qwen38::HyperConnection hc(ctx, w, H, HC, R, 4, G, 1e-6f, true);
+
+    auto emb = upload_bf16(M * H, 2.0f, 0.0f);
+    qwen38::DeviceTensor emb3({1, M, H}, qwen38::DType::bf16);
+    CHECK(hipMemcpy(emb3.data(), emb.data(), M * H * 2, hipMemcpyDeviceToDevice) == hipSuccess);
+    const qwen38::DeviceTensor stream = qwen38::HyperConnection::initialize_stream(ctx, emb3, HC);
+    ctx.synchronize();
+    CHECK(stream.shape() == (std::vector<std::size_t>{1, M, K}));
+    {
+        const auto e = emb3.to_host<std::uint16_t>();
+        const auto s = stream.to_host<std::uint16_t>();
+        for (std::size_t r = 0; r < M; ++r)
+            for (std::size_t h = 0; h < HC; ++h)
+                CHECK(std::equal(e.begin() + static_cast<std::ptrdiff_t>(r * H), e.begin() + static_cast<std::ptrdiff_t>((r + 1) * H),
+                                 s.begin() + static_cast<std::ptrdiff_t>(r * K + h * H)));
+    }
+    const qwen38::HyperConnectionRead rd = hc.read(stream);
+    CHECK(rd.has_injection && rd.mixed.shape() == (std::vector<std::size_t>{1, M, H}) &&
+          rd.injection.shape() == (std::vector<std::size_t>{1, M, HC, 1}));
+    // the same read through the C ABI
+    qwen38::DeviceTensor mixed2({M, H}, qwen38::DType::bf16), inj2({M, HC}, qwen38::DType::bf16);
+    const std::size_t wsb = q38_hc_workspace_size(&hc.desc(), static_cast<int32_t>(M));
+    qwen38::DeviceTensor ws({wsb}, qwen38::DType::u32);
+    CHECK(q38_hc_read(hc.handle(), u16(stream), static_cast<int32_t>(M), static_cast<std::uint16_t*>(mixed2.data()),
+                      static_cast<std::uint16_t*>(inj2.data()), ws.data(), ws.nbytes(), ctx.stream()) == Q38_OK);
+    ctx.synchronize();
+    CHECK(rd.mixed.to_host<std::uint16_t>() == mixed2.to_host<std::uint16_t>());
+    CHECK(rd.injection.to_host<std::uint16_t>() == inj2.to_host<std::uint16_t>());
+    // write with the block input standing in for the block output
+    const qwen38::DeviceTensor out = hc.write(stream, rd.mixed, rd.injection);
+    qwen38::DeviceTensor out2({M, K}, qwen38::DType::bf16);
+    CHECK(q38_hc_write(hc.handle(), u16(stream), u16(rd.mixed), u16(rd.injection), static_cast<int32_t>(M),
+                       static_cast<std::uint16_t*>(out2.data()), ctx.stream()) == Q38_OK);
+    ctx.synchronize();
+    CHECK(out.to_host<std::uint16_t>() == out2.to_host<std::uint16_t>());
+    CHECK(out.to_host<std::uint16_t>() != stream.to_host<std::uint16_t>());
+    // shape and argument errors
+    qwen38::DeviceTensor bad({1, M, K - 8}, qwen38::DType::bf16);
+    CHECK(throws<std::runtime_error>([&] { (void)hc.read(bad); }));
+    CHECK(throws<std::runtime_error>([&] { (void)hc.write(stream, rd.injection, rd.injection); }));
+    CHECK(throws<std::runtime_error>([&] {
+        qwen38::HyperConnection bad_eps(ctx, w, H, HC, R, 4, G, 0.0f, true);
+    }));
+    CHECK(throws<std::runtime_error>([&] {
+        qwen38::HyperConnection bad_rank(ctx, w, H, HC, 100, 4, G, 1e-6f, true);
+    }));
+    std::printf("hyper connection: ok\n");
+}
+
 static void draft_head_tests(const qwen38::Context& ctx, const qwen38::QwenModel& model) {
     qwen38::MoeGeometry g;
     qwen38::QwenMtpHead head(ctx, model.seed(), model.vocab(), g);
@@ -502,6 +581,7 @@ static void gpu_tests() {
     std::printf("gpu section: ok (accepted %zu of 3 self-drafts)\n", step.accepted);
     batched_slot_tests(ctx, model);
     draft_head_tests(ctx, model);
+    hyper_connection_tests(ctx);
 }
 
 int main(int argc, char** argv) {

@@ -3,7 +3,8 @@ program tests/cpp/host_mirror_test.cpp, built with the library: host KATs and ex
 types on the CPU, the device section (SparseMoe vs the C ABI, verify + commit lifecycle,
 a greedy round, and the engine-side round driver with 3 requests sharing each batched
 verification, every batch recomputed row by row in the same kernel family; the MTP draft head,
-learned-draft rounds and the scheduler drafting with the head) on the GPU."""
+learned-draft rounds and the scheduler drafting with the head; the HyperConnection mixer
+against the C ABI) on the GPU."""
 import os
 import subprocess
 
@@ -30,3 +31,4 @@ def test_gpu_section():
     assert "gpu section: ok" in out, out
     assert "batched slots: ok" in out, out
     assert "draft head: ok" in out, out
+    assert "hyper connection: ok" in out, out
