@@ -117,7 +117,8 @@ typedef struct q38_route_out {
     float* weights;     /* [rows*k]                                                    */
     float* logits;      /* [rows*E] router logits (BF16 values widened to float)       */
     int32_t* plan;      /* [1 + 4*rows*k + 1]: n_unique, uexp[rows*k], uoff[rows*k+1],
-                           route_list[rows*k], route_pos[rows*k]                       */
+                           route_list[rows*k], route_pos[rows*k]; past n_unique, uexp
+                           holds -1 and uoff rows*k (verify widths)                    */
     uint16_t* x_norm;   /* [rows*H] the normalised layer input (chain mode)            */
 } q38_route_out;
 

@@ -328,15 +328,20 @@ __device__ __forceinline__ void topk_build_plan(int M, int K, int32_t* plan, Top
     lds_barrier();
     int rank = __popcll(bal & ((1ull << lane) - 1ull));
     for (int w = 0; w < wave; ++w) rank += t.wave_cnt[w];
+    int nu = 0;
+    for (int w = 0; w < waves; ++w) nu += t.wave_cnt[w];
     if (start) {
         plan[1 + rank] = t.sorted_e[tid];
         plan[1 + MK + rank] = tid;
     }
     if (tid == 0) {
-        int nu = 0;
-        for (int w = 0; w < waves; ++w) nu += t.wave_cnt[w];
         plan[0] = nu;
         plan[1 + MK + nu] = MK;
+    }
+    // entries past the unique experts: expert -1, offset MK (every entry is written)
+    if (tid < MK && tid >= nu) {
+        plan[1 + tid] = -1;
+        plan[1 + MK + tid + 1] = MK;
     }
     lds_barrier();
 }
@@ -427,6 +432,11 @@ __device__ __forceinline__ void plan_wave(int M, int K, const int32_t* ex, int32
     if (lane == 0) {
         plan[0] = nu;
         plan[1 + MK + nu] = MK;
+    }
+    // entries past the unique experts: expert -1, offset MK (every entry is written)
+    if (act && lane >= nu) {
+        plan[1 + lane] = -1;
+        plan[1 + MK + lane + 1] = MK;
     }
     if (slot_pos && lane < M) slot_pos[nu * 4 + lane] = MK + lane;  // the shared expert's slot
 }
