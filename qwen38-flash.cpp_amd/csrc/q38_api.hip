@@ -885,8 +885,14 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
         if (e == hipSuccess && traces)
             if (copy_routes(L, rows, w, &traces[l], st) != Q38_OK) e = hipErrorUnknown;
         if (e == hipSuccess) {
-            kt = {E[4], E[5]};
-            e = launch_down(dev, w, rows, st);
+            if (moe_uses_fused(dev, rows)) {  // the down half ran in the gate/up launch (down_ms 0)
+                kt = {};
+                e = hipEventRecord(E[4], st);
+                if (e == hipSuccess) e = hipEventRecord(E[5], st);
+            } else {
+                kt = {E[4], E[5]};
+                e = launch_down(dev, w, rows, st);
+            }
         }
         if (e == hipSuccess) {
             kt = {E[6], E[7]};

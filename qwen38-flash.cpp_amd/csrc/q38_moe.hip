@@ -207,13 +207,15 @@ __global__ __launch_bounds__(1024) void k_prepare_u8(const uint16_t* __restrict_
 // (t outer, j inner) with fmaf, then the xor butterfly and BF16 rounding; a router bias,
 // when set, is added to the rounded logit in float. Workgroup 0 stores x in the workspace
 // (bf16) with its fp16 copy (the MFMA operand) unless src already is that copy.
+// reset_gu: the gate/up chunk planes of the call ([2][M*K + M][I] each for g and u) are set
+// to the all-ones pattern that the fused gate/up + down kernel (k_gd4) waits on.
 template <int T, bool NORM, int MR>
 __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ src,
-                                                        float eps) {
+                                                        float eps, int reset_gu) {
     constexpr int H = 512 * T, NT = 128 * T, NW = NT / 64;
     extern __shared__ __align__(16) uint16_t xs[];  // [M][H] bf16
     __shared__ float red[MR][NW];
-    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + 2 * sizeof(void*) + sizeof(float)>();
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + 2 * sizeof(void*) + sizeof(float) + sizeof(int)>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nr = L.E + (L.has_shared ? 1 : 0);
     const int e = blockIdx.x * NW + wave;
@@ -315,6 +317,12 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
     }
     lds_barrier();
     Q38_STAMP(0, 2);
+    if (reset_gu) {
+        const size_t n4 = B.gu_plane / 2;  // 16-byte stores per [2][rows][I] block
+        const uint4 ones = make_uint4(~0u, ~0u, ~0u, ~0u);
+        for (size_t i = static_cast<size_t>(blockIdx.x) * NT + tid; i < 2 * n4; i += static_cast<size_t>(gridDim.x) * NT)
+            reinterpret_cast<uint4*>(i < n4 ? B.g : B.u)[i < n4 ? i : i - n4] = ones;
+    }
     if (e >= nr) return;
     // all rows' products first (independent chains), then the butterflies
     float acc[MR];
@@ -1023,7 +1031,9 @@ hipError_t launch_route_norm_t(const LayerDev& L, const MoeBufs& B, int M, const
     const size_t lds = static_cast<size_t>(M) * 512 * T * 2;
     if (const hipError_t e = ensure_lds<k_route_norm<T, NORM, MR>>(MR * 512 * T * 2); e != hipSuccess) return e;
     const int rows = L.E + (L.has_shared ? 1 : 0);
-    return launch(k_route_norm<T, NORM, MR>, dim3((rows + NW - 1) / NW), dim3(128 * T), lds, st, L, B, M, src, eps);
+    const int reset = moe_uses_fused(L, M) ? 1 : 0;
+    return launch(k_route_norm<T, NORM, MR>, dim3((rows + NW - 1) / NW), dim3(128 * T), lds, st, L, B, M, src, eps,
+                  reset);
 }
 template <int T, bool NORM>
 hipError_t launch_route_norm_m(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* src, float eps,
@@ -1137,6 +1147,7 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
         if (e != hipSuccess) return e;
         return launch_gu_mfma_g<14, 256, 2, 1>(L, B, M, st);
     }
+    if (moe_uses_fused(L, M)) return launch_gate_down4(L, B, M, st);
     if (moe_uses_narrow(L, M)) return launch_gate_up4(L, B, M, st);
     const int D = L.p[0].dim, BT = L.p[0].bits;
     if (moe_uses_mfma(L)) {
@@ -1173,6 +1184,7 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
         if (e != hipSuccess) return e;
         return launch_down_mfma_g<14, 64, 2, 1>(L, B, M, st);
     }
+    if (moe_uses_fused(L, M)) return hipSuccess;  // (the fused gate/up launch ran the down half)
     if (moe_uses_narrow(L, M)) return launch_down4(L, B, M, st);
     const int D = L.p[2].dim, BT = L.p[2].bits;
     if (moe_uses_mfma(L)) {

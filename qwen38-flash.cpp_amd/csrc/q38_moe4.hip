@@ -126,6 +126,22 @@ __device__ __forceinline__ void load_group_scales(const uint16_t* scales, size_t
 
 __device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Gate/up values inside k_gd4: agent-scope relaxed atomics (stores and loads that are
+// coherent across the XCDs' L2s), plain accesses in the two-kernel path.
+template <bool AGENT>
+__device__ __forceinline__ void store_f32(float* p, float v) {
+    if constexpr (AGENT) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+template <bool AGENT>
+__device__ __forceinline__ float load_f32(const float* p) {
+    if constexpr (AGENT) return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+}
+// The reset pattern of the gate/up planes (all ones: a NaN that no arithmetic produces).
+__device__ __forceinline__ bool gu_unset(float v) { return __float_as_uint(v) == 0xFFFFFFFFu; }
+constexpr int kGuSpinLimit = 1 << 16;
+
 // Gate and up projections. Workgroup type = (projection, codebook chunk); waves = K slices.
 // Items are 64-row tiles of I; the 4 B columns are the request rows (rows not routed to the
 // item's expert are computed and discarded). Output: partial sums of this chunk, times the
@@ -142,23 +158,23 @@ constexpr size_t gu4_lds_bytes() {
     return (size_t{1} << BITS) * 8 + 2 * (NSUB / 32) * 64 * 16;
 }
 
-template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
-__global__ __launch_bounds__(2 * NSUB) __attribute__((amdgpu_waves_per_eu(1, (NSUB / 32 + 3) / 4)))
-void k_gu4(LayerDev L, MoeBufs B, int M) {
+// FUSED: the gate/up half of k_gd4, whose outputs are read by the down half of other
+// workgroups of the same launch (agent-coherent stores, see k_gd4).
+// dn_fill (FUSED): receives the workgroup's down codebook chunk for the down half (16-byte
+// granules tid + NT q), requested a few granules per item behind the items' own loads, while
+// the items keep the CU's LDS busy and leave its memory path mostly idle.
+template <int BITS, int NSUB, int NCHUNK, int D, int G8, bool FUSED>
+__device__ __forceinline__ void gu4_body(const LayerDev& L, const MoeBufs& B, int M, unsigned char* lds,
+                                         int32_t* ex, int32_t* plan, int32_t* slot_pos, u4_t* dn_fill) {
     constexpr int KS = NSUB / 32;
     constexpr int NT = 64 * KS;
     constexpr int KENT = 1 << BITS;
     constexpr int TYPES = 2 * NCHUNK;
-    extern __shared__ __align__(16) unsigned char lds[];
-    __shared__ int32_t ex[kNarrowMaxRoutes];
-    __shared__ int32_t plan[kNarrowPlan];
-    __shared__ int32_t slot_pos[(kNarrowMaxRoutes + 1) * 4];
     static_assert(kNarrow * NSUB * 8 + kNarrow * 64 * 8 <= 2 * KS * 64 * 16, "staging fits the partial sums");
     const uint2* book = reinterpret_cast<const uint2*>(lds);
     float* red = reinterpret_cast<float*>(lds + KENT * 8);  // [2][KS][64][4]
     uint2* xs = reinterpret_cast<uint2*>(lds + KENT * 8);                       // [4][NSUB], in red
     uint64_t* cand = reinterpret_cast<uint64_t*>(lds + KENT * 8 + kNarrow * NSUB * 8);  // [4][64], in red
-    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
     const int type = kk % TYPES;
@@ -289,16 +305,24 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     };
     float ov[D];
     int oat[D];
+    // (FUSED: the down chunk has the gate/up geometry; its granules are spread over the first
+    // FI items, so that the last ones still have two items' time to arrive)
+    constexpr int NFILL = FUSED ? KENT / 2 / NT : 0, FI = D > 3 ? D - 2 : 1;
+    const u4_t* dsrc = reinterpret_cast<const u4_t*>(L.p[2].book4 + static_cast<size_t>(kk % NCHUNK) * KENT * 4);
 #pragma unroll
     for (int k = 0; k < D; ++k) {
         oat[k] = -1;
         if (k < my_n) item_compute(k, cw[k % PF], sc[k % PF], ov[k], oat[k]);
         if (k + PF < D) load_item(k + PF, cw[k % PF], sc[k % PF]);
+        if constexpr (FUSED) {
+#pragma unroll
+            for (int q = NFILL * k / FI; q < (k < FI ? NFILL * (k + 1) / FI : 0); ++q) dn_fill[q] = dsrc[tid + q * NT];
+        }
         if (k == 0) Q38_STAMP(8192, 8);
     }
 #pragma unroll
     for (int k = 0; k < D; ++k)
-        if (oat[k] >= 0) out[oat[k]] = ov[k];
+        if (oat[k] >= 0) store_f32<FUSED>(out + oat[k], ov[k]);
     for (int jj = D; jj < my_n; ++jj) {
         uint32_t c1[BITS + 1];
         ItemScales<G8> s1;
@@ -306,7 +330,7 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
         float o1;
         int a1;
         item_compute(jj, c1, s1, o1, a1);
-        if (a1 >= 0) out[a1] = o1;
+        if (a1 >= 0) store_f32<FUSED>(out + a1, o1);
     }
     Q38_STAMP(8192, 9);
 #ifdef Q38_TRACE
@@ -314,21 +338,33 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
 #endif
 }
 
+template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
+__global__ __launch_bounds__(2 * NSUB) __attribute__((amdgpu_waves_per_eu(1, (NSUB / 32 + 3) / 4)))
+void k_gu4(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ int32_t ex[kNarrowMaxRoutes];
+    __shared__ int32_t plan[kNarrowPlan];
+    __shared__ int32_t slot_pos[(kNarrowMaxRoutes + 1) * 4];
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
+    gu4_body<BITS, NSUB, NCHUNK, D, G8, false>(L, B, M, lds, ex, plan, slot_pos, nullptr);
+}
+
 // Down projection. Workgroup type = codebook chunk; 8 waves = KS K slices x RG row groups,
 // items are (slot, TR = 64 RG rows of H). The B columns are the slot's routes: their SwiGLU
 // rows (this chunk's dims, fp16) are formed per item from the gate/up chunk planes, which
 // are requested with the item's code spans, D items ahead.
-template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_dn4(LayerDev L, MoeBufs B, int M) {
+// FUSED: the down half of k_gd4. The plan is already in LDS (built by this workgroup's
+// gate/up half), and the gate/up values are read agent-coherent and re-read until none
+// holds the reset pattern (the gate/up half of another workgroup has not stored it yet).
+// hs: SwiGLU rows of the item's routes, [kNarrow][NSUB] fp16 quads.
+template <int BITS, int NSUB, int NCHUNK, int D, int G8, bool FUSED>
+__device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, int M, unsigned char* lds,
+                                         int32_t* plan, uint2* hs, const u4_t* pre_fill) {
     constexpr int KS = NSUB / 32, RG = 8 / KS, TR = 64 * RG;
     constexpr int NT = 512, KENT = 1 << BITS;
     static_assert(KS * RG == 8, "8 waves");
-    extern __shared__ __align__(16) unsigned char lds[];
-    __shared__ int32_t plan[kNarrowPlan];
-    __shared__ __align__(16) uint2 hs[kNarrow][NSUB];  // SwiGLU rows of the item's routes (fp16)
     const uint2* book = reinterpret_cast<const uint2*>(lds);
     float* red = reinterpret_cast<float*>(lds + KENT * 8);  // [RG][KS-1][64][4]
-    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
     const int chunk = kk % NCHUNK;
@@ -336,6 +372,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int idx = (kk / NCHUNK) * 8 + x8;
     const ProjDev& P = L.p[2];
     const int H = L.H, I = L.I, K = L.K, MK = M * K;
+    // (E as a register value: a select between an LDS plan entry and an argument held in
+    // memory would otherwise become one generic load, whose wait drains every load in flight)
+    const int E = __builtin_amdgcn_readfirstlane(L.E);
     const int kh = wave % KS, rg = wave / KS;
 
     // 1. The plan (written by the gate/up kernel) into LDS, then the codebook chunk loads
@@ -344,11 +383,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     //    every wait is on registers and the compiler counts it exactly.
     const int plan_n = 2 + 4 * MK;
     Q38_STAMP(16384, 0);
-    if (tid < plan_n) plan[tid] = B.plan[tid];
+    if (!FUSED && tid < plan_n) plan[tid] = B.plan[tid];
     constexpr int NG = KENT / 2;  // 16-byte granules of the chunk
     constexpr int NFILL = (NG + NT - 1) / NT;
     u4_t fv[NFILL];
-    {
+    if constexpr (FUSED) {  // (requested by the gate/up half)
+#pragma unroll
+        for (int q = 0; q < NFILL; ++q) fv[q] = pre_fill[q];
+    } else {
         const u4_t* src = reinterpret_cast<const u4_t*>(P.book4 + static_cast<size_t>(chunk) * KENT * 4);
 #pragma unroll
         for (int q = 0; q < NFILL; ++q) {
@@ -363,10 +405,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int nu = plan[0];
     const int tiles = H / TR;
     const int n_items = (nu + (L.has_shared ? 1 : 0)) * tiles;
-    const bool two = L.gu_parts == 2;
+    const bool two = FUSED || L.gu_parts == 2;  // (the fused layers' gate/up write two planes)
     auto code_src = [&](int item) {  // this wave's (64-row tile, block) in the tiled codes
         int expert, n, pos0;
-        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
+        slot_rows(plan, M, K, L.has_shared, item / tiles, E, &expert, &n, &pos0);
         const size_t row0 = static_cast<size_t>(expert) * H + (item % tiles) * TR + rg * 64;
         return P.codes_t + ((row0 >> 6) * KS + kh) * (BITS * 64);
     };
@@ -377,23 +419,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     constexpr int GQ = (kNarrow * NSUB * 4 + NT - 1) / NT;
     auto load_gu = [&](int item, float (&g)[GQ][2], float (&u)[GQ][2]) {
         int expert, n, pos0;
-        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
+        slot_rows(plan, M, K, L.has_shared, item / tiles, E, &expert, &n, &pos0);
 #pragma unroll
         for (int q = 0; q < GQ; ++q) {
             const int e = tid + NT * q < n * NSUB * 4 ? tid + NT * q : n * NSUB * 4 - 1;
             const size_t at = static_cast<size_t>(pos0 + e / (4 * NSUB)) * I + (e / 4 % NSUB) * (4 * NCHUNK) +
                               4 * chunk + (e & 3);
-            g[q][0] = B.g[at];
-            u[q][0] = B.u[at];
-            g[q][1] = B.g[(two ? B.gu_plane : 0) + at];
-            u[q][1] = B.u[(two ? B.gu_plane : 0) + at];
+            g[q][0] = load_f32<FUSED>(B.g + at);
+            u[q][0] = load_f32<FUSED>(B.u + at);
+            g[q][1] = load_f32<FUSED>(B.g + (two ? B.gu_plane : 0) + at);
+            u[q][1] = load_f32<FUSED>(B.u + (two ? B.gu_plane : 0) + at);
         }
     };
     // row scales of the output lanes (kh == 0): rows (lane & ~3) + 0..3 of the row group; or
     // the group scales of every lane's rows for its wave's K slice
     auto load_sc = [&](int item, ItemScales<G8>& sc) {
         const int ui = item / tiles;
-        const int expert = ui < nu ? plan[1 + ui] : L.E;
+        // (the plan entry is read before the value select, so that the select cannot become
+        // one generic load from either LDS or the kernel arguments)
+        const int pe = plan[1 + (ui < nu ? ui : 0)];
+        const int expert = ui < nu ? pe : E;
         const size_t row0 = static_cast<size_t>(expert) * H + (item % tiles) * TR + rg * 64;
         if constexpr (G8 == 0) sc.w = *reinterpret_cast<const uint2*>(P.scales + row0 + (lane & ~3));
         else load_group_scales(P.scales, row0, lane, P.ngrp, kh * (32 / G8), sc.g);
@@ -413,7 +458,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         load_sc(it, sc[k]);
     };
 #pragma unroll
-    for (int k = 0; k < PF; ++k) load_slot(k, k);  // (no items: item 0, unused)
+    for (int k = 0; k < PF; ++k) {
+        load_slot(k, k);  // (no items: item 0, unused)
+        if (k < 3) Q38_STAMP(16384, 6 + k);
+    }
 #pragma unroll
     for (int q = 0; q < NFILL; ++q) {
         const int i = tid + q * NT;
@@ -431,14 +479,42 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         const int item = idx + jj * per_type;
         int expert, n, pos0;
         const int ui = item / tiles;
-        slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
+        slot_rows(plan, M, K, L.has_shared, ui, E, &expert, &n, &pos0);
+        float gl[GQ][2], ul[GQ][2];
+#pragma unroll
+        for (int q = 0; q < GQ; ++q)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) gl[q][i] = g2[q][i], ul[q][i] = u2[q][i];
+        if constexpr (FUSED) {
+            auto pending = [&] {
+                bool p = false;
+#pragma unroll
+                for (int q = 0; q < GQ; ++q)
+                    if (tid + NT * q < n * NSUB * 4)
+#pragma unroll
+                        for (int i = 0; i < 2; ++i) p |= gu_unset(gl[q][i]) || gu_unset(ul[q][i]);
+                return p;
+            };
+            // (bounded: a value still unset at the limit stays NaN and so does the output)
+            int spin = 0;
+            for (; pending() && spin < kGuSpinLimit; ++spin) {
+                __builtin_amdgcn_s_sleep(2);
+                load_gu(item, gl, ul);
+            }
+#ifdef Q38_TRACE
+            if (jj == 0) {
+                Q38_STAMP(16384, 5);
+                if (threadIdx.x == 0) g_trace[16384 + 16 * blockIdx.x + 11] = spin;
+            }
+#endif
+        }
 #pragma unroll
         for (int q = 0; q < GQ; ++q) {
             const int e = tid + NT * q;
             if (e < n * NSUB * 4) {
-                const float g = two ? g2[q][0] + g2[q][1] : g2[q][0];
-                const float u = two ? u2[q][0] + u2[q][1] : u2[q][0];
-                reinterpret_cast<uint16_t*>(&hs[0][0])[e] = f2h(swiglu(g, u));
+                const float g = two ? gl[q][0] + gl[q][1] : gl[q][0];
+                const float u = two ? ul[q][0] + ul[q][1] : ul[q][0];
+                reinterpret_cast<uint16_t*>(hs)[e] = f2h(swiglu(g, u));
             }
         }
         lds_barrier();  // SwiGLU rows (and, the first time, the codebook chunk) in LDS
@@ -446,7 +522,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         uint2 bop[32];
 #pragma unroll
         for (int t = 0; t < 32; t += 2) {
-            const uint4 v2 = *reinterpret_cast<const uint4*>(&hs[jb][kh * 32 + t]);
+            const uint4 v2 = *reinterpret_cast<const uint4*>(&hs[jb * NSUB + kh * 32 + t]);
             bop[t] = make_uint2(v2.x, v2.y);
             bop[t + 1] = make_uint2(v2.z, v2.w);
         }
@@ -512,10 +588,55 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 }
 
 template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_dn4(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ int32_t plan[kNarrowPlan];
+    __shared__ __align__(16) uint2 hs[kNarrow * NSUB];
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
+    dn4_body<BITS, NSUB, NCHUNK, D, G8, false>(L, B, M, lds, plan, hs, nullptr);
+}
+
+// Gate/up and down of a verify layer in one launch (d8/14-bit, H / 8 = 256, I / 8 = 64,
+// per-row scales). Every workgroup first runs the gate/up half of k_gu4 (routing, plan,
+// its gate/up items), then replaces its LDS codebook chunk with a down chunk and runs the
+// down half of k_dn4: the down kernel's launch, plan read and first loads are gone from
+// the layer's latency chain, and each workgroup's down loads start as soon as its own
+// gate/up items are done.
+// Gate/up values cross workgroups (and XCDs) inside the launch. They are stored with
+// agent-scope atomic stores and read with agent-scope atomic loads, both coherent at the
+// device's memory side, so no L2 write-back is needed; the router kernel before this one
+// sets every value of the gate/up planes to the all-ones pattern (a NaN no arithmetic
+// produces), and a reader re-reads the values it needs until none holds it. The wait is
+// bounded (kGuSpinLimit re-reads, ~0.1 s): every workgroup of the grid is resident at once
+// (one per CU, grid <= CUs), so it ends long before that unless something is broken, and
+// then the affected outputs are NaN instead of the kernel hanging.
+template <int BITS, int NSUB_GU, int NSUB_DN, int NCHUNK, int DG, int DD>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gd4(LayerDev L, MoeBufs B, int M) {
+    static_assert(2 * NSUB_GU == 512, "the gate/up half uses the 8 waves of the down half");
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ int32_t ex[kNarrowMaxRoutes];
+    __shared__ int32_t plan[kNarrowPlan];
+    __shared__ int32_t slot_pos[(kNarrowMaxRoutes + 1) * 4];
+    __shared__ __align__(16) uint2 hs[kNarrow * NSUB_DN];
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
+    u4_t fill[(1 << BITS) / 2 / 512];  // the down codebook chunk, requested by the gate/up half
+    gu4_body<BITS, NSUB_GU, NCHUNK, DG, 0, true>(L, B, M, lds, ex, plan, slot_pos, fill);
+    lds_barrier();  // every wave is done with the gate/up codebook chunk
+    dn4_body<BITS, NSUB_DN, NCHUNK, DD, 0, true>(L, B, M, lds, plan, hs, fill);
+}
+
+template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
 hipError_t launch_gu4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     constexpr size_t lds = gu4_lds_bytes<BITS, NSUB, NCHUNK>();
     if (const hipError_t e = ensure_lds<k_gu4<BITS, NSUB, NCHUNK, D, G8>>(lds); e != hipSuccess) return e;
     return launch(k_gu4<BITS, NSUB, NCHUNK, D, G8>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
+}
+template <int DG, int DD>
+hipError_t launch_gd4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    constexpr size_t lds = gu4_lds_bytes<14, 256, 2>();
+    static_assert(lds >= (size_t{1} << 14) * 8 + 4 * 64 * 16, "the down half's LDS fits the gate/up half's");
+    if (const hipError_t e = ensure_lds<k_gd4<14, 256, 64, 2, DG, DD>>(lds); e != hipSuccess) return e;
+    return launch(k_gd4<14, 256, 64, 2, DG, DD>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M);
 }
 template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
 hipError_t launch_dn4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
@@ -563,6 +684,25 @@ LayerDev moe_call_dev(const LayerDev& L, int M) {
 // 6 (4 for the wider workgroups) and further items take the loop.
 static int ring_items(const LayerDev& L, int M, int tiles, int per_type) {
     return ((M * L.K + 1) * tiles + per_type - 1) / per_type;
+}
+
+bool moe_uses_fused(const LayerDev& L, int M) {
+    if (!moe_uses_narrow(L, M)) return false;
+    for (int p = 0; p < 3; ++p)
+        if (L.p[p].dim != 8 || L.p[p].bits != 14 || L.p[p].ngrp != 1 || !L.p[p].codes_t) return false;
+    return L.H == 2048 && L.I == 512;
+}
+
+// Ring depths of the two halves (as the two kernels pick them: every item's loads in flight
+// at once where registers allow; items beyond take the loop).
+hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    if (!moe_uses_fused(L, M)) return hipErrorInvalidValue;
+    const int grid = mfma_grid();
+    const int c = ring_items(L, M, L.I / 64, grid / 32 * 8);
+    if (c <= 2) return launch_gd4_t<2, 1>(L, B, M, st);
+    if (c <= 3) return launch_gd4_t<3, 2>(L, B, M, st);
+    if (c <= 4) return launch_gd4_t<4, 2>(L, B, M, st);
+    return launch_gd4_t<6, 3>(L, B, M, st);
 }
 
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {

@@ -481,9 +481,12 @@ __device__ __forceinline__ bool slot_rows(const int32_t* plan, int M, int K, int
                                           int* expert, int* n, int* first_pos) {
     const int nu = plan[0];
     const int MK = M * K;
+    // (the entries are read at a clamped index before any select, so that the compiler
+    // cannot merge the LDS read with the caller's E into one generic load)
+    const int uc = ui < nu ? ui : 0;
+    const int pe = plan[1 + uc], a = plan[1 + MK + uc], b = plan[1 + MK + uc + 1];
     if (ui < nu) {
-        *expert = plan[1 + ui];
-        const int a = plan[1 + MK + ui], b = plan[1 + MK + ui + 1];
+        *expert = pe;
         *n = b - a;
         *first_pos = a;
         return true;
