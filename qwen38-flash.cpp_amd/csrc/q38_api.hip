@@ -752,6 +752,12 @@ static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_
     Q38_HIP(launch_router(dev, w, rows, src, norm, eps, st));
     if (!moe_plans_in_gate_up(dev, rows)) Q38_HIP(launch_topk_plan(dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[1], st));
+    if (moe_uses_fused(dev, rows)) {  // gate/up, down and combine in one launch
+        Q38_HIP(launch_gate_down4(dev, w, rows, h_chain, h_chain ? nullptr : y, st));
+        if (ev)
+            for (int i = 2; i <= 4; ++i) Q38_HIP(hipEventRecord(ev[i], st));
+        return copy_routes(L, rows, w, trace, st);
+    }
     Q38_HIP(launch_gate_up(dev, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[2], st));
     if (trace)
@@ -878,23 +884,23 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
         kt = {E[0], E[1]};
         e = launch_router(dev, w, rows, h, true, eps, st);
         if (e == hipSuccess && !moe_plans_in_gate_up(dev, rows)) e = launch_topk_plan(dev, w, rows, st);
+        const bool fused = moe_uses_fused(dev, rows);  // (gate/up, down and combine in one launch)
         if (e == hipSuccess) {
             kt = {E[2], E[3]};
-            e = launch_gate_up(dev, w, rows, st);
+            e = fused ? launch_gate_down4(dev, w, rows, h, nullptr, st) : launch_gate_up(dev, w, rows, st);
         }
         if (e == hipSuccess && traces)
             if (copy_routes(L, rows, w, &traces[l], st) != Q38_OK) e = hipErrorUnknown;
         if (e == hipSuccess) {
-            if (moe_uses_fused(dev, rows)) {  // the down half ran in the gate/up launch (down_ms 0)
+            if (fused) {  // down and combine ran in the gate/up launch (down_ms, merge_ms 0)
                 kt = {};
-                e = hipEventRecord(E[4], st);
-                if (e == hipSuccess) e = hipEventRecord(E[5], st);
+                for (int i = 4; i < 8 && e == hipSuccess; ++i) e = hipEventRecord(E[i], st);
             } else {
                 kt = {E[4], E[5]};
                 e = launch_down(dev, w, rows, st);
             }
         }
-        if (e == hipSuccess) {
+        if (e == hipSuccess && !fused) {
             kt = {E[6], E[7]};
             e = launch_combine(dev, w, rows, h, nullptr, st);
         }

@@ -147,11 +147,12 @@ bool moe_uses_narrow(const LayerDev& L, int M);
 LayerDev moe_call_dev(const LayerDev& L, int M);
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
-// The d8/14-bit, H 2048, I 512, per-row-scale layers at up to 4 rows run gate/up and down in
-// one launch (k_gd4): launch_gate_up takes it, launch_down then has nothing to launch, and
-// the router kernel before it resets the gate/up planes the launch waits on.
+// The d8/14-bit, H 2048, I 512, top-10, per-row-scale layers at up to 4 rows run gate/up and
+// down in one launch (k_gd4), and with h or out set the combine too (h <- h + y in place, or
+// out <- y): launch_gate_up takes it without the combine, launch_down then has nothing to
+// launch. The router kernel before it resets the gate/up and down planes the launch waits on.
 bool moe_uses_fused(const LayerDev& L, int M);
-hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);
 int mfma_grid();  // persistent workgroups of the expert kernels (a multiple of 32)
 // Prefill widths, kMaxRows < M <= kMaxPrefillRows (q38_moe_pf.hip), one kernel each:
 // router logits, per-row top-k, sorted plan, segmented gate/up, SwiGLU, segmented down

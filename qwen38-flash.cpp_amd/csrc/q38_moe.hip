@@ -207,8 +207,9 @@ __global__ __launch_bounds__(1024) void k_prepare_u8(const uint16_t* __restrict_
 // (t outer, j inner) with fmaf, then the xor butterfly and BF16 rounding; a router bias,
 // when set, is added to the rounded logit in float. Workgroup 0 stores x in the workspace
 // (bf16) with its fp16 copy (the MFMA operand) unless src already is that copy.
-// reset_gu: the gate/up chunk planes of the call ([2][M*K + M][I] each for g and u) are set
-// to the all-ones pattern that the fused gate/up + down kernel (k_gd4) waits on.
+// reset_gu: the gate/up and down chunk planes of the call ([2][M*K + M][I] each for g and u,
+// [2][M*K + M][H] for d) are set to the all-ones pattern that the fused layer kernel (k_gd4)
+// waits on.
 template <int T, bool NORM, int MR>
 __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ src,
                                                         float eps, int reset_gu) {
@@ -318,10 +319,15 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
     lds_barrier();
     Q38_STAMP(0, 2);
     if (reset_gu) {
-        const size_t n4 = B.gu_plane / 2;  // 16-byte stores per [2][rows][I] block
+        const size_t n4 = B.gu_plane / 2, d4 = B.d_plane / 2;  // 16-byte stores per [2][rows][I or H] block
         const uint4 ones = make_uint4(~0u, ~0u, ~0u, ~0u);
-        for (size_t i = static_cast<size_t>(blockIdx.x) * NT + tid; i < 2 * n4; i += static_cast<size_t>(gridDim.x) * NT)
-            reinterpret_cast<uint4*>(i < n4 ? B.g : B.u)[i < n4 ? i : i - n4] = ones;
+        for (size_t i = static_cast<size_t>(blockIdx.x) * NT + tid; i < 2 * n4 + d4;
+             i += static_cast<size_t>(gridDim.x) * NT) {
+            uint4* dst = i < n4 ? reinterpret_cast<uint4*>(B.g) + i
+                                : i < 2 * n4 ? reinterpret_cast<uint4*>(B.u) + (i - n4)
+                                             : reinterpret_cast<uint4*>(B.d) + (i - 2 * n4);
+            *dst = ones;
+        }
     }
     if (e >= nr) return;
     // all rows' products first (independent chains), then the butterflies
@@ -858,11 +864,6 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
 // place (h <- T(h + y)), otherwise out <- y. The down kernels write route r * k + s at row
 // r * k + s and the shared expert's row r at M * k + r, so every load here is independent
 // of the plan and all of them are issued before the first use.
-template <int KT, bool TWO>
-struct CombineIn {
-    float wts[KT + 1];    // route weights in slot order, then the shared gate
-    float dv[KT + 1][2];  // the routes' (and the shared expert's) down outputs, both planes
-};
 
 // Every load is unconditional and issued up front, the row's route weights and gate first
 // (each wait below then covers only what it needs); with no shared expert the shared read
@@ -885,18 +886,6 @@ __device__ __forceinline__ void combine_load(const LayerDev& L, const MoeBufs& B
     }
 }
 
-template <int KT, bool TWO>
-__device__ __forceinline__ float combine_value(const LayerDev& L, const CombineIn<KT, TWO>& in) {
-    float routed = 0.0f;
-#pragma unroll
-    for (int s = 0; s < KT; ++s) routed = fmaf(in.wts[s], rbf(TWO ? in.dv[s][0] + in.dv[s][1] : in.dv[s][0]), routed);
-    float y = rbf(routed);
-    if (L.has_shared) {
-        const float sh = rbf(rbf(TWO ? in.dv[KT][0] + in.dv[KT][1] : in.dv[KT][0]) * in.wts[KT]);
-        y = rbf(y + sh);
-    }
-    return y;
-}
 
 template <int KT, bool TWO>
 __global__ __launch_bounds__(256) void k_combine(LayerDev L, MoeBufs B, int M, uint16_t* h, uint16_t* out) {
@@ -1147,7 +1136,7 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
         if (e != hipSuccess) return e;
         return launch_gu_mfma_g<14, 256, 2, 1>(L, B, M, st);
     }
-    if (moe_uses_fused(L, M)) return launch_gate_down4(L, B, M, st);
+    if (moe_uses_fused(L, M)) return launch_gate_down4(L, B, M, nullptr, nullptr, st);
     if (moe_uses_narrow(L, M)) return launch_gate_up4(L, B, M, st);
     const int D = L.p[0].dim, BT = L.p[0].bits;
     if (moe_uses_mfma(L)) {

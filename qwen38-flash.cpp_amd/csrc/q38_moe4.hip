@@ -163,9 +163,10 @@ constexpr size_t gu4_lds_bytes() {
 // dn_fill (FUSED): receives the workgroup's down codebook chunk for the down half (16-byte
 // granules tid + NT q), requested a few granules per item behind the items' own loads, while
 // the items keep the CU's LDS busy and leave its memory path mostly idle.
+// wt (FUSED): the rows' route weights in LDS, for the fused kernel's combine tail.
 template <int BITS, int NSUB, int NCHUNK, int D, int G8, bool FUSED>
 __device__ __forceinline__ void gu4_body(const LayerDev& L, const MoeBufs& B, int M, unsigned char* lds,
-                                         int32_t* ex, int32_t* plan, int32_t* slot_pos, u4_t* dn_fill) {
+                                         int32_t* ex, int32_t* plan, int32_t* slot_pos, u4_t* dn_fill, float* wt) {
     constexpr int KS = NSUB / 32;
     constexpr int NT = 64 * KS;
     constexpr int KENT = 1 << BITS;
@@ -210,7 +211,7 @@ __device__ __forceinline__ void gu4_body(const LayerDev& L, const MoeBufs& B, in
         for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(lg[j]));
         Q38_STAMP(8192, 1);
         Q38_STAMP(8192, 2);
-        topk_select_row_fast<8>(L, B, wave, lg, ex, blockIdx.x == 0, cand + 64 * wave);
+        topk_select_row_fast<8>(L, B, wave, lg, ex, blockIdx.x == 0, cand + 64 * wave, FUSED ? wt : nullptr);
 #pragma unroll
         for (int q = 0; q < XPW; ++q) xs[wave * NSUB + lane + 64 * q] = xv[q];
     }
@@ -346,7 +347,7 @@ void k_gu4(LayerDev L, MoeBufs B, int M) {
     __shared__ int32_t plan[kNarrowPlan];
     __shared__ int32_t slot_pos[(kNarrowMaxRoutes + 1) * 4];
     touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
-    gu4_body<BITS, NSUB, NCHUNK, D, G8, false>(L, B, M, lds, ex, plan, slot_pos, nullptr);
+    gu4_body<BITS, NSUB, NCHUNK, D, G8, false>(L, B, M, lds, ex, plan, slot_pos, nullptr, nullptr);
 }
 
 // Down projection. Workgroup type = codebook chunk; 8 waves = KS K slices x RG row groups,
@@ -403,13 +404,20 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
 
     // 2. Code spans and gate/up quads of the first D items.
     const int nu = plan[0];
-    const int tiles = H / TR;
+    const int tiles = FUSED ? 2048 / TR : H / TR;  // (the fused layers have H = 2048)
     const int n_items = (nu + (L.has_shared ? 1 : 0)) * tiles;
     const bool two = FUSED || L.gu_parts == 2;  // (the fused layers' gate/up write two planes)
-    auto code_src = [&](int item) {  // this wave's (64-row tile, block) in the tiled codes
+    // An item's slot (expert, route count, first route position), read from the plan once.
+    struct Slot {
         int expert, n, pos0;
-        slot_rows(plan, M, K, L.has_shared, item / tiles, E, &expert, &n, &pos0);
-        const size_t row0 = static_cast<size_t>(expert) * H + (item % tiles) * TR + rg * 64;
+    };
+    auto slot_of = [&](int item) {
+        Slot t;
+        slot_rows(plan, M, K, L.has_shared, item / tiles, E, &t.expert, &t.n, &t.pos0);
+        return t;
+    };
+    auto code_src = [&](int item, const Slot& t) {  // this wave's (64-row tile, block) in the tiled codes
+        const size_t row0 = static_cast<size_t>(t.expert) * H + (item % tiles) * TR + rg * 64;
         return P.codes_t + ((row0 >> 6) * KS + kh) * (BITS * 64);
     };
     // Gate/up chunk-plane values of the SwiGLU elements this thread forms: element e = tid
@@ -417,9 +425,8 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
     // (4 NSUB), subvector e / 4 % NSUB, dim e % 4). Loads are unconditional: elements past
     // the slot's routes repeat its last element, so the compiler counts every load.
     constexpr int GQ = (kNarrow * NSUB * 4 + NT - 1) / NT;
-    auto load_gu = [&](int item, float (&g)[GQ][2], float (&u)[GQ][2]) {
-        int expert, n, pos0;
-        slot_rows(plan, M, K, L.has_shared, item / tiles, E, &expert, &n, &pos0);
+    auto load_gu = [&](const Slot& t, float (&g)[GQ][2], float (&u)[GQ][2]) {
+        const int n = t.n, pos0 = t.pos0;
 #pragma unroll
         for (int q = 0; q < GQ; ++q) {
             const int e = tid + NT * q < n * NSUB * 4 ? tid + NT * q : n * NSUB * 4 - 1;
@@ -433,13 +440,8 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
     };
     // row scales of the output lanes (kh == 0): rows (lane & ~3) + 0..3 of the row group; or
     // the group scales of every lane's rows for its wave's K slice
-    auto load_sc = [&](int item, ItemScales<G8>& sc) {
-        const int ui = item / tiles;
-        // (the plan entry is read before the value select, so that the select cannot become
-        // one generic load from either LDS or the kernel arguments)
-        const int pe = plan[1 + (ui < nu ? ui : 0)];
-        const int expert = ui < nu ? pe : E;
-        const size_t row0 = static_cast<size_t>(expert) * H + (item % tiles) * TR + rg * 64;
+    auto load_sc = [&](int item, const Slot& t, ItemScales<G8>& sc) {
+        const size_t row0 = static_cast<size_t>(t.expert) * H + (item % tiles) * TR + rg * 64;
         if constexpr (G8 == 0) sc.w = *reinterpret_cast<const uint2*>(P.scales + row0 + (lane & ~3));
         else load_group_scales(P.scales, row0, lane, P.ngrp, kh * (32 / G8), sc.g);
     };
@@ -453,9 +455,10 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
     ItemScales<G8> sc[PF];
     auto load_slot = [&](int j, int k) {
         const int it = item_of(j);
-        load_code_block_tiled<BITS>(code_src(it), lane, cw[k]);
-        load_gu(it, gq[k], uq[k]);
-        load_sc(it, sc[k]);
+        const Slot t = slot_of(it);
+        load_code_block_tiled<BITS>(code_src(it, t), lane, cw[k]);
+        load_gu(t, gq[k], uq[k]);
+        load_sc(it, t, sc[k]);
     };
 #pragma unroll
     for (int k = 0; k < PF; ++k) {
@@ -499,7 +502,7 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
             int spin = 0;
             for (; pending() && spin < kGuSpinLimit; ++spin) {
                 __builtin_amdgcn_s_sleep(2);
-                load_gu(item, gl, ul);
+                load_gu(Slot{expert, n, pos0}, gl, ul);
             }
 #ifdef Q38_TRACE
             if (jj == 0) {
@@ -565,21 +568,22 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
     for (int k = 0; k < D; ++k)
         if (oroute[k] >= 0)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) dout[static_cast<size_t>(oroute[k]) * H + obase[k] + r] = o4[k][r];
+            for (int r = 0; r < 4; ++r) store_f32<FUSED>(dout + static_cast<size_t>(oroute[k]) * H + obase[k] + r, o4[k][r]);
     for (int jj = D; jj < my_n; ++jj) {
         const int it = item_of(jj);
         uint32_t c1[BITS + 1];
         float g1[GQ][2], u1[GQ][2];
         ItemScales<G8> s1;
-        load_code_block_tiled<BITS>(code_src(it), lane, c1);
-        load_gu(it, g1, u1);
-        load_sc(it, s1);
+        const Slot t = slot_of(it);
+        load_code_block_tiled<BITS>(code_src(it, t), lane, c1);
+        load_gu(t, g1, u1);
+        load_sc(it, t, s1);
         float p4[4];
         int rt, bs;
         item_compute(jj, c1, g1, u1, s1, p4, rt, bs);
         if (rt >= 0)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) dout[static_cast<size_t>(rt) * H + bs + r] = p4[r];
+            for (int r = 0; r < 4; ++r) store_f32<FUSED>(dout + static_cast<size_t>(rt) * H + bs + r, p4[r]);
     }
     Q38_STAMP(16384, 4);
 #ifdef Q38_TRACE
@@ -596,33 +600,79 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     dn4_body<BITS, NSUB, NCHUNK, D, G8, false>(L, B, M, lds, plan, hs, nullptr);
 }
 
-// Gate/up and down of a verify layer in one launch (d8/14-bit, H / 8 = 256, I / 8 = 64,
-// per-row scales). Every workgroup first runs the gate/up half of k_gu4 (routing, plan,
-// its gate/up items), then replaces its LDS codebook chunk with a down chunk and runs the
-// down half of k_dn4: the down kernel's launch, plan read and first loads are gone from
-// the layer's latency chain, and each workgroup's down loads start as soon as its own
-// gate/up items are done.
-// Gate/up values cross workgroups (and XCDs) inside the launch. They are stored with
-// agent-scope atomic stores and read with agent-scope atomic loads, both coherent at the
-// device's memory side, so no L2 write-back is needed; the router kernel before this one
-// sets every value of the gate/up planes to the all-ones pattern (a NaN no arithmetic
-// produces), and a reader re-reads the values it needs until none holds it. The wait is
-// bounded (kGuSpinLimit re-reads, ~0.1 s): every workgroup of the grid is resident at once
-// (one per CU, grid <= CUs), so it ends long before that unless something is broken, and
-// then the affected outputs are NaN instead of the kernel hanging.
-template <int BITS, int NSUB_GU, int NSUB_DN, int NCHUNK, int DG, int DD>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gd4(LayerDev L, MoeBufs B, int M) {
+// Gate/up and down of a verify layer in one launch (d8/14-bit, H 2048, I 512, top-10,
+// per-row scales), optionally with the combine. Every workgroup first runs the gate/up half
+// of k_gu4 (routing, plan, its gate/up items), then replaces its LDS codebook chunk with a
+// down chunk (requested during its gate/up items) and runs the down half of k_dn4: the down
+// kernel's launch, plan read and first loads are gone from the layer's latency chain. With
+// h or out set, the last kCombineWgs workgroups (those with the fewest down items) then form
+// the layer output: y = combine of the rows' routes and the shared expert (combine_value,
+// the combine kernel's arithmetic); h <- T(h + y) in place, or out <- y.
+// Values cross workgroups (and XCDs) inside the launch: the gate/up and down partial sums
+// are stored with agent-scope atomic stores and read with agent-scope atomic loads, both
+// coherent at the device's memory side, so no L2 write-back is needed. The router kernel
+// before this one sets every value of those planes to the all-ones pattern (a NaN that no
+// arithmetic produces), and a reader re-reads the values it needs until none holds it. The
+// wait is bounded (kGuSpinLimit re-reads, ~0.1 s): every workgroup of the grid is resident
+// at once (one per CU, grid <= CUs), so it ends long before that unless something is broken,
+// and then the affected outputs are NaN instead of the kernel hanging.
+constexpr int kCombineWgs = 32;
+template <int KT>
+__device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B, int M, const float* wt, uint16_t* h,
+                                             uint16_t* out) {
+    const int w = static_cast<int>(blockIdx.x) - static_cast<int>(gridDim.x - kCombineWgs);
+    const int H = L.H, MK = M * KT;
+    const int per = (M * H + kCombineWgs - 1) / kCombineWgs;  // (<= 512: M <= 4, H = 2048)
+    const int p = w * per + static_cast<int>(threadIdx.x);
+    if (w < 0 || static_cast<int>(threadIdx.x) >= per || p >= M * H) return;
+    const int r = p / H, o = p % H;
+    CombineIn<KT, true> in;
+#pragma unroll
+    for (int s = 0; s < KT; ++s) in.wts[s] = wt[r * KT + s];
+    in.wts[KT] = B.sgate[r];
+    const uint16_t hraw = (h ? h : out)[static_cast<size_t>(r) * H + o];  // (unused without h)
+    auto load = [&] {
+#pragma unroll
+        for (int s = 0; s <= KT; ++s) {
+            const int route = s < KT ? r * KT + s : (L.has_shared ? MK + r : r * KT);
+            const size_t at = static_cast<size_t>(route) * H + o;
+            in.dv[s][0] = load_f32<true>(B.d + at);
+            in.dv[s][1] = load_f32<true>(B.d + B.d_plane + at);
+        }
+    };
+    auto pending = [&] {
+        bool q = false;
+#pragma unroll
+        for (int s = 0; s <= KT; ++s) q |= gu_unset(in.dv[s][0]) || gu_unset(in.dv[s][1]);
+        return q;
+    };
+    load();
+    for (int spin = 0; pending() && spin < kGuSpinLimit; ++spin) {
+        __builtin_amdgcn_s_sleep(2);
+        load();
+    }
+    const float y = combine_value<KT, true>(L, in);
+    const size_t i = static_cast<size_t>(r) * H + o;
+    if (h) h[i] = f2bf(rbf(bf2f(hraw) + y));
+    else out[i] = f2bf(y);
+}
+
+template <int BITS, int NSUB_GU, int NSUB_DN, int NCHUNK, int DG, int DD, int KT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gd4(LayerDev L, MoeBufs B, int M,
+                                                                                         uint16_t* h, uint16_t* out) {
     static_assert(2 * NSUB_GU == 512, "the gate/up half uses the 8 waves of the down half");
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int32_t ex[kNarrowMaxRoutes];
+    __shared__ float wt[kNarrowMaxRoutes];
     __shared__ int32_t plan[kNarrowPlan];
     __shared__ int32_t slot_pos[(kNarrowMaxRoutes + 1) * 4];
     __shared__ __align__(16) uint2 hs[kNarrow * NSUB_DN];
-    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int) + 2 * sizeof(void*)>();
     u4_t fill[(1 << BITS) / 2 / 512];  // the down codebook chunk, requested by the gate/up half
-    gu4_body<BITS, NSUB_GU, NCHUNK, DG, 0, true>(L, B, M, lds, ex, plan, slot_pos, fill);
+    gu4_body<BITS, NSUB_GU, NCHUNK, DG, 0, true>(L, B, M, lds, ex, plan, slot_pos, fill, wt);
     lds_barrier();  // every wave is done with the gate/up codebook chunk
     dn4_body<BITS, NSUB_DN, NCHUNK, DD, 0, true>(L, B, M, lds, plan, hs, fill);
+    if (h || out) combine_tail<KT>(L, B, M, wt, h, out);
 }
 
 template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
@@ -632,11 +682,11 @@ hipError_t launch_gu4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t 
     return launch(k_gu4<BITS, NSUB, NCHUNK, D, G8>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
 }
 template <int DG, int DD>
-hipError_t launch_gd4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+hipError_t launch_gd4_t(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
     constexpr size_t lds = gu4_lds_bytes<14, 256, 2>();
     static_assert(lds >= (size_t{1} << 14) * 8 + 4 * 64 * 16, "the down half's LDS fits the gate/up half's");
-    if (const hipError_t e = ensure_lds<k_gd4<14, 256, 64, 2, DG, DD>>(lds); e != hipSuccess) return e;
-    return launch(k_gd4<14, 256, 64, 2, DG, DD>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M);
+    if (const hipError_t e = ensure_lds<k_gd4<14, 256, 64, 2, DG, DD, 10>>(lds); e != hipSuccess) return e;
+    return launch(k_gd4<14, 256, 64, 2, DG, DD, 10>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M, h, out);
 }
 template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
 hipError_t launch_dn4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
@@ -690,19 +740,19 @@ bool moe_uses_fused(const LayerDev& L, int M) {
     if (!moe_uses_narrow(L, M)) return false;
     for (int p = 0; p < 3; ++p)
         if (L.p[p].dim != 8 || L.p[p].bits != 14 || L.p[p].ngrp != 1 || !L.p[p].codes_t) return false;
-    return L.H == 2048 && L.I == 512;
+    return L.H == 2048 && L.I == 512 && L.K == 10 && mfma_grid() >= kCombineWgs;
 }
 
 // Ring depths of the two halves (as the two kernels pick them: every item's loads in flight
 // at once where registers allow; items beyond take the loop).
-hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
     if (!moe_uses_fused(L, M)) return hipErrorInvalidValue;
     const int grid = mfma_grid();
     const int c = ring_items(L, M, L.I / 64, grid / 32 * 8);
-    if (c <= 2) return launch_gd4_t<2, 1>(L, B, M, st);
-    if (c <= 3) return launch_gd4_t<3, 2>(L, B, M, st);
-    if (c <= 4) return launch_gd4_t<4, 2>(L, B, M, st);
-    return launch_gd4_t<6, 3>(L, B, M, st);
+    if (c <= 2) return launch_gd4_t<2, 1>(L, B, M, h, out, st);
+    if (c <= 3) return launch_gd4_t<3, 2>(L, B, M, h, out, st);
+    if (c <= 4) return launch_gd4_t<4, 2>(L, B, M, h, out, st);
+    return launch_gd4_t<6, 3>(L, B, M, h, out, st);
 }
 
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {

@@ -159,12 +159,15 @@ __device__ __forceinline__ void topk_keys_t(const LayerDev& L, const float* lg, 
 
 // Rank-ordered outputs of one row: lane s < K holds the s-th key (weight p / sum of the
 // selected p in rank order when normalising).
+// wt_lds (optional): the row's route weights in LDS beside ex_lds.
 __device__ __forceinline__ void topk_write_row(const LayerDev& L, const MoeBufs& B, int r, int32_t* ex_lds,
-                                               bool global_out, float psel, int isel, float sum) {
+                                               bool global_out, float psel, int isel, float sum,
+                                               float* wt_lds = nullptr) {
     const int lane = threadIdx.x & 63;
     const int K = L.K;
     if (lane < K) {
         if (ex_lds) ex_lds[r * K + lane] = isel;
+        if (wt_lds) wt_lds[r * K + lane] = L.normalize ? psel / sum : psel;
         if (global_out) {
             B.experts[r * K + lane] = isel;
             B.weights[r * K + lane] = L.normalize ? psel / sum : psel;
@@ -177,7 +180,7 @@ __device__ __forceinline__ void topk_write_row(const LayerDev& L, const MoeBufs&
 // keys in (p desc, index asc) order. key[] is consumed.
 template <int NJ>
 __device__ __forceinline__ void topk_tournament(const LayerDev& L, const MoeBufs& B, int r, uint64_t* key,
-                                                int32_t* ex_lds, bool global_out) {
+                                                int32_t* ex_lds, bool global_out, float* wt_lds = nullptr) {
     const int lane = threadIdx.x & 63;
     const int K = L.K;
 #pragma unroll
@@ -222,7 +225,7 @@ __device__ __forceinline__ void topk_tournament(const LayerDev& L, const MoeBufs
             isel = static_cast<int>(0xFFFFFFFFu - wlo);
         }
     }
-    topk_write_row(L, B, r, ex_lds, global_out, psel, isel, sum);
+    topk_write_row(L, B, r, ex_lds, global_out, psel, isel, sum, wt_lds);
 }
 
 template <int NJ, bool EXACT>
@@ -245,7 +248,8 @@ __device__ __forceinline__ void topk_select_row_t(const LayerDev& L, const MoeBu
 // LDS.
 template <int NJ>
 __device__ __forceinline__ void topk_select_row_fast(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
-                                                     int32_t* ex_lds, bool global_out, uint64_t* cand) {
+                                                     int32_t* ex_lds, bool global_out, uint64_t* cand,
+                                                     float* wt_lds = nullptr) {
     const int lane = threadIdx.x & 63;
     const int K = L.K;
     uint64_t key[NJ];
@@ -275,7 +279,7 @@ __device__ __forceinline__ void topk_select_row_fast(const LayerDev& L, const Mo
         total += __popcll(bj);
     }
     if (total > 64) {
-        topk_tournament<NJ>(L, B, r, key, ex_lds, global_out);
+        topk_tournament<NJ>(L, B, r, key, ex_lds, global_out, wt_lds);
         return;
     }
     // zero keys pad the list to a multiple of 16 (a zero key is below every real one); a
@@ -298,7 +302,8 @@ __device__ __forceinline__ void topk_select_row_fast(const LayerDev& L, const Mo
     Q38_STAMPV(8192, 13, hi);
     float sum = 0.0f;
     for (int s = 0; s < K; ++s) sum += __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(hi), s)));
-    topk_write_row(L, B, r, ex_lds, global_out, __uint_as_float(hi), static_cast<int>(0xFFFFFFFFu - lo), sum);
+    topk_write_row(L, B, r, ex_lds, global_out, __uint_as_float(hi), static_cast<int>(0xFFFFFFFFu - lo), sum,
+                   wt_lds);
 }
 __device__ __forceinline__ void topk_select_row(const LayerDev& L, const MoeBufs& B, int r, const float* lg,
                                                 int32_t* ex_lds, bool global_out) {
@@ -499,6 +504,28 @@ __device__ __forceinline__ bool slot_rows(const int32_t* plan, int M, int K, int
     }
     return false;
 }
+// The combine's inputs for one (row, column) and its arithmetic (R8 reduce, R10, R11):
+// routed = T(sum_slot w_slot * T(d_slot)) in slot order, shared = T(T(d_shared) * gate),
+// y = T(routed + shared). Shared by the combine kernels and the fused layer kernel's tail.
+template <int KT, bool TWO>
+struct CombineIn {
+    float wts[KT + 1];    // route weights in slot order, then the shared gate
+    float dv[KT + 1][2];  // the routes' (and the shared expert's) down outputs, both planes
+};
+
+template <int KT, bool TWO>
+__device__ __forceinline__ float combine_value(const LayerDev& L, const CombineIn<KT, TWO>& in) {
+    float routed = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KT; ++s) routed = fmaf(in.wts[s], rbf(TWO ? in.dv[s][0] + in.dv[s][1] : in.dv[s][0]), routed);
+    float y = rbf(routed);
+    if (L.has_shared) {
+        const float sh = rbf(rbf(TWO ? in.dv[KT][0] + in.dv[KT][1] : in.dv[KT][0]) * in.wts[KT]);
+        y = rbf(y + sh);
+    }
+    return y;
+}
+
 // The request row of the j-th route of slot ui.
 __device__ __forceinline__ int route_row(const int32_t* plan, int M, int K, int pos0, int j, bool shared) {
     return shared ? j : plan[2 + 2 * M * K + pos0 + j] / K;
