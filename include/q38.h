@@ -237,9 +237,11 @@ int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h
  * interval a kernel trace reports; launch gaps are not included). */
 typedef struct q38_moe_timings {
     double routing_ms;   /* router logits kernel */
-    double gate_up_ms;   /* gate/up projections (+ top-k + plan on the MFMA path) */
-    double down_ms;      /* down projection (+ SwiGLU on the narrow path) */
-    double merge_ms;     /* ordered route reduction + shared gate + residual + next RMSNorm */
+    double gate_up_ms;   /* gate/up projections (+ top-k + plan on the MFMA path); on layers
+                            that run gate/up, down and combine in one kernel (d8/14-bit, H
+                            2048, I 512, top-10, per-row scales, rows <= 4), that kernel */
+    double down_ms;      /* down projection (+ SwiGLU on the narrow path); 0 on those layers */
+    double merge_ms;     /* ordered route reduction + shared gate + residual; 0 on those layers */
     int32_t layers;
     int32_t reserved;
 } q38_moe_timings;

@@ -912,8 +912,10 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
         q38_moe_timings t{};
         for (int l = 0; l < n_layers && e == hipSuccess; ++l) {
             hipEvent_t* E = &ev[static_cast<size_t>(l) * 8];
-            float ms[4];
-            for (int i = 0; i < 4 && e == hipSuccess; ++i) e = hipEventElapsedTime(&ms[i], E[2 * i], E[2 * i + 1]);
+            float ms[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            // (a fused layer's down and combine phases ran inside its gate/up kernel: 0)
+            const int phases = moe_uses_fused(moe_call_dev(layers[l]->dev, rows), rows) ? 2 : 4;
+            for (int i = 0; i < phases && e == hipSuccess; ++i) e = hipEventElapsedTime(&ms[i], E[2 * i], E[2 * i + 1]);
             t.routing_ms += ms[0];
             t.gate_up_ms += ms[1];
             t.down_ms += ms[2];
