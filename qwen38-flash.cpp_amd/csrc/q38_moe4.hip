@@ -657,7 +657,9 @@ __device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B
     else out[i] = f2bf(y);
 }
 
-template <int BITS, int NSUB_GU, int NSUB_DN, int NCHUNK, int DG, int DD, int KT>
+// G8: per-row scales (0) or one scale per 64 inputs in both projections (8, the checkpoint
+// layout; the two kernels' G8 = 8 item code).
+template <int BITS, int NSUB_GU, int NSUB_DN, int NCHUNK, int DG, int DD, int KT, int G8 = 0>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gd4(LayerDev L, MoeBufs B, int M,
                                                                                          uint16_t* h, uint16_t* out) {
     static_assert(2 * NSUB_GU == 512, "the gate/up half uses the 8 waves of the down half");
@@ -669,9 +671,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     __shared__ __align__(16) uint2 hs[kNarrow * NSUB_DN];
     touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int) + 2 * sizeof(void*)>();
     u4_t fill[(1 << BITS) / 2 / 512];  // the down codebook chunk, requested by the gate/up half
-    gu4_body<BITS, NSUB_GU, NCHUNK, DG, 0, true>(L, B, M, lds, ex, plan, slot_pos, fill, wt);
+    gu4_body<BITS, NSUB_GU, NCHUNK, DG, G8, true>(L, B, M, lds, ex, plan, slot_pos, fill, wt);
     lds_barrier();  // every wave is done with the gate/up codebook chunk
-    dn4_body<BITS, NSUB_DN, NCHUNK, DD, 0, true>(L, B, M, lds, plan, hs, fill);
+    dn4_body<BITS, NSUB_DN, NCHUNK, DD, G8, true>(L, B, M, lds, plan, hs, fill);
     if (h || out) combine_tail<KT>(L, B, M, wt, h, out);
 }
 
@@ -681,12 +683,12 @@ hipError_t launch_gu4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t 
     if (const hipError_t e = ensure_lds<k_gu4<BITS, NSUB, NCHUNK, D, G8>>(lds); e != hipSuccess) return e;
     return launch(k_gu4<BITS, NSUB, NCHUNK, D, G8>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
 }
-template <int DG, int DD>
+template <int DG, int DD, int G8>
 hipError_t launch_gd4_t(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
     constexpr size_t lds = gu4_lds_bytes<14, 256, 2>();
     static_assert(lds >= (size_t{1} << 14) * 8 + 4 * 64 * 16, "the down half's LDS fits the gate/up half's");
-    if (const hipError_t e = ensure_lds<k_gd4<14, 256, 64, 2, DG, DD, 10>>(lds); e != hipSuccess) return e;
-    return launch(k_gd4<14, 256, 64, 2, DG, DD, 10>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M, h, out);
+    if (const hipError_t e = ensure_lds<k_gd4<14, 256, 64, 2, DG, DD, 10, G8>>(lds); e != hipSuccess) return e;
+    return launch(k_gd4<14, 256, 64, 2, DG, DD, 10, G8>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M, h, out);
 }
 template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
 hipError_t launch_dn4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
@@ -738,8 +740,11 @@ static int ring_items(const LayerDev& L, int M, int tiles, int per_type) {
 
 bool moe_uses_fused(const LayerDev& L, int M) {
     if (!moe_uses_narrow(L, M)) return false;
+    // per-row scales everywhere, or per-64-input groups in both projections
+    const bool rows = L.p[0].ngrp == 1 && L.p[1].ngrp == 1 && L.p[2].ngrp == 1;
+    if (!rows && !(gu_groups64(L) && dn_groups64(L))) return false;
     for (int p = 0; p < 3; ++p)
-        if (L.p[p].dim != 8 || L.p[p].bits != 14 || L.p[p].ngrp != 1 || !L.p[p].codes_t) return false;
+        if (L.p[p].dim != 8 || L.p[p].bits != 14 || !L.p[p].codes_t) return false;
     return L.H == 2048 && L.I == 512 && L.K == 10 && mfma_grid() >= kCombineWgs;
 }
 
@@ -749,10 +754,16 @@ hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, uint16_
     if (!moe_uses_fused(L, M)) return hipErrorInvalidValue;
     const int grid = mfma_grid();
     const int c = ring_items(L, M, L.I / 64, grid / 32 * 8);
-    if (c <= 2) return launch_gd4_t<2, 1>(L, B, M, h, out, st);
-    if (c <= 3) return launch_gd4_t<3, 2>(L, B, M, h, out, st);
-    if (c <= 4) return launch_gd4_t<4, 2>(L, B, M, h, out, st);
-    return launch_gd4_t<6, 3>(L, B, M, h, out, st);
+    if (L.p[0].ngrp != 1) {  // 64-input scale groups
+        if (c <= 2) return launch_gd4_t<2, 1, 8>(L, B, M, h, out, st);
+        if (c <= 3) return launch_gd4_t<3, 2, 8>(L, B, M, h, out, st);
+        if (c <= 4) return launch_gd4_t<4, 2, 8>(L, B, M, h, out, st);
+        return launch_gd4_t<6, 3, 8>(L, B, M, h, out, st);
+    }
+    if (c <= 2) return launch_gd4_t<2, 1, 0>(L, B, M, h, out, st);
+    if (c <= 3) return launch_gd4_t<3, 2, 0>(L, B, M, h, out, st);
+    if (c <= 4) return launch_gd4_t<4, 2, 0>(L, B, M, h, out, st);
+    return launch_gd4_t<6, 3, 0>(L, B, M, h, out, st);
 }
 
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {

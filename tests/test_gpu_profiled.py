@@ -1,5 +1,6 @@
 """q38_verify_chain_profiled: every phase kernel is timed (start at the phase's first kernel,
-stop at its last), on uniform (one fused gate/up + down + combine kernel at up to 4 rows),
+stop at its last), on uniform (one fused gate/up + down + combine kernel at up to 4 rows, as
+for the scale-group stacks),
 mixed (two bank kernels per phase) and per-64-input scale group stacks; the profiled pass
 computes the same values as the plain one."""
 import ctypes as C
@@ -37,9 +38,9 @@ def test_profiled_chain(gpu, q38, orc, kind, M):
         assert rc == q38.Q38_OK, q38.last_error()
         assert np.array_equal(G.to_host(hp, np.uint16), plain)
         phases = [tm.routing_ms, tm.gate_up_ms, tm.down_ms, tm.merge_ms]
-        # uniform config-1 layers at up to 4 rows run gate/up, down and the combine in one
-        # kernel: its time is gate_up_ms, and the down and merge phases are 0
-        fused = kind == "uniform" and M <= 4
+        # config-1 layers (per-row or 64-input scales) at up to 4 rows run gate/up, down and
+        # the combine in one kernel: its time is gate_up_ms, and the down and merge phases are 0
+        fused = kind in ("uniform", "group64") and M <= 4
         timed = phases[:2] if fused else phases
         assert tm.layers == 3 and all(np.isfinite(p) and p > 0 for p in timed), phases
         if fused:
