@@ -226,7 +226,10 @@ int q38_moe_layer_set_router_bias(q38_moe_layer* layer, const float* bias);
 /* The verify pass through a stack of MoE layers (QwenModel::forward_verify_layer_major_
  * reference, src/model.cpp:386-441, with the HyperConnection/attention parts replaced by
  * a pre-norm residual): for each layer h <- h + MoE(RMSNorm(h)). h: device [rows, H]
- * bf16, updated in place. traces (optional): per-layer route outputs, array of n_layers. */
+ * bf16, updated in place. traces (optional): per-layer route outputs, array of n_layers.
+ * At 1-4 rows on d8/14-bit H 2048 layers the experts and the combine run as one kernel whose
+ * workgroups (one per CU) wait for each other: it expects the device's CUs to itself while
+ * it runs (otherwise bounded waits expire and the affected outputs are NaN). */
 int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows,
                      float eps, const q38_route_out* traces, void* workspace, size_t workspace_bytes,
                      void* stream);
