@@ -429,6 +429,12 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
         const int n = t.n, pos0 = t.pos0;
 #pragma unroll
         for (int q = 0; q < GQ; ++q) {
+            // (FUSED: a pass wholly past the slot's routes is not loaded: its values are never
+            // used, and the load instructions are what the down half's start waits on)
+            if (FUSED && q > 0 && NT * q >= n * NSUB * 4) {
+                g[q][0] = u[q][0] = g[q][1] = u[q][1] = 0.0f;
+                continue;
+            }
             const int e = tid + NT * q < n * NSUB * 4 ? tid + NT * q : n * NSUB * 4 - 1;
             const size_t at = static_cast<size_t>(pos0 + e / (4 * NSUB)) * I + (e / 4 % NSUB) * (4 * NCHUNK) +
                               4 * chunk + (e & 3);
