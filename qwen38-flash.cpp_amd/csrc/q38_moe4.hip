@@ -25,6 +25,9 @@
 //          the plan is in LDS; the chunk is stored to LDS behind them.
 //          Down outputs are written at the route index (request row * k + slot; the
 //          shared expert's rows after the routed ones), so the combine needs no plan.
+//   k_gd4  both bodies in one launch, then the combine (the config-1 geometry): the down
+//          kernel's launch, plan read and first waits leave the layer's latency chain, and
+//          values cross workgroups through agent-coherent stores and polled loads.
 #include "q38_moe_dev.hpp"
 
 namespace q38 {
