@@ -22,8 +22,13 @@
 //                          one-hot / zero codebooks; dense numpy float64 recomputation.
 //   LM head                exact integer-product check vs numpy float64 + near-tie KAT.
 //   Philox4x32-10          Random123 known-answer vectors.
-//   rejection sampling     invariants (p == q accepts all; p(d) = 0 rejects) and a
-//                          chi-square test that the emitted token follows p.
+//   rejection sampling     invariants (p == q accepts all; p(d) = 0 rejects); chi-square
+//                          tests at k = 3 that every emitted position follows its p_i, that
+//                          the draw after a first rejection at i follows norm(max(0, p_i -
+//                          q_i)) and the all-accepted bonus follows p_k, and the acceptance
+//                          rate sum_x min(p_i, q_i); planted wrong-row draws fail them.
+//   residual add           float32 numpy restatement with its own RNE (ties, overflow,
+//                          signed zeros, subnormals).
 //   exp contract           error bound vs math.exp over the whole reduced range.
 //   per-dim INT8/U8 books  independent numpy restatement (bit-exact tables and decode),
 //                          closed forms (min/max round trip, lround ties away from zero,
@@ -1057,6 +1062,25 @@ int orc_moe_layer_synth(const Desc* d, uint64_t seed, int layer, const uint16_t*
     SynthSource src(*d, seed, static_cast<uint64_t>(layer));
     return moe_layer(*d, src, x, M, y, experts, weights, logits, threads);
 }
+// Routing alone (R1 + R2) of the synthetic layer (seed, layer): logits [M, E] (BF16-rounded
+// contract dot, plus the optional bias), experts / weights [M, k].
+int orc_route_synth(const Desc* d, uint64_t seed, int layer, const uint16_t* x, int M, const float* bias,
+                    int32_t* experts, float* weights, float* logits, int threads) {
+    const int H = d->hidden, E = d->experts;
+    if (H % 512 != 0 || E % 64 != 0 || d->top_k < 1 || d->top_k > E || M < 1) return -1;
+    SynthSource src(*d, seed, static_cast<uint64_t>(layer));
+    const uint16_t* Wr = src.router();
+    std::vector<float> lg(static_cast<size_t>(M) * E);
+    parallel_for(E, threads, [&](int e) {
+        for (int r = 0; r < M; ++r) {
+            const float v = rbf16(dot_contract(x + static_cast<size_t>(r) * H, Wr + static_cast<size_t>(e) * H, H));
+            lg[static_cast<size_t>(r) * E + e] = bias ? v + bias[e] : v;
+        }
+    });
+    route_rows(lg.data(), M, E, d->top_k, d->normalize, experts, weights);
+    if (logits) std::copy(lg.begin(), lg.end(), logits);
+    return 0;
+}
 // orc_moe_layer_synth with an additive router-logit bias (float, added to the BF16 logit).
 int orc_moe_layer_synth_bias(const Desc* d, uint64_t seed, int layer, const uint16_t* x, int M, const float* bias,
                              uint16_t* y, int32_t* experts, float* weights, float* logits, int threads) {
@@ -1244,6 +1268,12 @@ void orc_round_uniforms(uint64_t seed, uint64_t slot, uint64_t round, uint32_t p
 // d_i iff u_i * q_i(d_i) < p_i(d_i); at the first rejection emit a draw from
 // norm(max(0, p_i - q_i)) with v_i; if all k are accepted emit a draw from p_k with v_k.
 // p = softmax(target_logits/T) [k+1, V], q = softmax(draft_logits/T) [k, V].
+// Test-only fault injection for the sampler (0: none). 1: the all-accepted bonus token is
+// drawn from p_{k-1} instead of p_k. 2: after a first rejection at position i >= 1 the
+// residual is formed from rows i-1 instead of i. The distribution tests set it to show that
+// a wrong-row draw fails them; nothing else touches it.
+static int g_plant_fault = 0;
+void orc_plant_fault(int code) { g_plant_fault = code; }
 int orc_accept_sampled(const float* target_logits, const float* draft_logits, const uint32_t* drafts, int k,
                        int64_t V, float temperature, uint64_t seed, uint64_t slot, uint64_t round,
                        int64_t* accepted, uint32_t* next) {
@@ -1257,13 +1287,17 @@ int orc_accept_sampled(const float* target_logits, const float* draft_logits, co
         round_uniforms(seed, slot, round, static_cast<uint32_t>(i), &u, &v);
         const double pd = p[drafts[i]], qd = q[drafts[i]];
         if (static_cast<double>(u) * qd < pd) continue;
+        if (g_plant_fault == 2 && i >= 1) {
+            softmax_T(target_logits + static_cast<size_t>(i - 1) * V, V, temperature, p);
+            softmax_T(draft_logits + static_cast<size_t>(i - 1) * V, V, temperature, q);
+        }
         std::vector<double> res(V);
         for (int64_t x = 0; x < V; ++x) res[x] = std::max(0.0, p[x] - q[x]);
         *accepted = i;
         *next = static_cast<uint32_t>(draw(res, v));
         return 0;
     }
-    softmax_T(target_logits + static_cast<size_t>(k) * V, V, temperature, p);
+    softmax_T(target_logits + static_cast<size_t>(g_plant_fault == 1 ? k - 1 : k) * V, V, temperature, p);
     float u, v;
     round_uniforms(seed, slot, round, static_cast<uint32_t>(k), &u, &v);
     *accepted = k;

@@ -88,6 +88,8 @@ class Oracle:
         sig("orc_philox4x32_10", None, P, P, P)
         sig("orc_round_uniforms", None, U64, U64, U64, U32, P, P)
         sig("orc_accept_sampled", C.c_int, P, P, P, C.c_int, I64, F32, U64, U64, U64, P, P)
+        sig("orc_plant_fault", None, C.c_int)
+        sig("orc_route_synth", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, P, P, C.c_int)
 
     # ---- formats
     def bf16(self, x):
@@ -194,6 +196,19 @@ class Oracle:
                                                    _a(lg), threads)
         assert rc == 0
         return y, ex, wt, lg
+
+    def route_synth(self, d: Desc, seed, layer, x, threads=8, bias=None):
+        """Routing alone of the synthetic layer (seed, layer) on x -> (experts, weights, logits)."""
+        x = np.ascontiguousarray(x, np.uint16)
+        M = x.shape[0]
+        ex = np.empty((M, d.top_k), np.int32)
+        wt = np.empty((M, d.top_k), np.float32)
+        lg = np.empty((M, d.experts), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        rc = self.lib.orc_route_synth(C.byref(d), seed, layer, _a(x), M, None if b is None else _a(b), _a(ex),
+                                      _a(wt), _a(lg), threads)
+        assert rc == 0
+        return ex, wt, lg
 
     def moe_layer_synth_reps(self, d: Desc, seed, layer, x, threads=(8,), warm=2, reps=20):
         """Seconds per pass, [len(threads), reps], of one synthetic layer (experts generated once)."""

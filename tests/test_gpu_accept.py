@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 import gpu_util as G
+from sampling_cases import k3_case, k3_pvalues, softmax_T
 
 pytestmark = pytest.mark.gpu
 
@@ -35,6 +36,32 @@ def test_sampled_decisions_match(gpu, q38, orc):
         same += gpu_accept(q38, tl, dl, drafts, T, 77, 1, rnd) == orc.accept_sampled(tl, dl, drafts, T, 77, 1, rnd)
     print(f"sampled acceptance: {same}/{n} rounds identical to the oracle")
     assert same >= n - n // 1000, same
+
+
+def test_sampled_k3_distributions_on_device(gpu, q38):
+    """The device sampler's own output at k = 3, without the oracle: every emitted position
+    follows its target row, each first-rejection draw follows norm(max(0, p_i - q_i)), the
+    bonus token follows p_3, and the acceptance rates are sum_x min(p_i, q_i)."""
+    tl, dl, T = k3_case()
+    k, V = dl.shape
+    n = 12000
+    rng = np.random.default_rng(22)
+    q = softmax_T(dl, T)
+    drafts = np.stack([rng.choice(V, size=n, p=q[i]) for i in range(k)], 1)
+    t, d = G.to_dev(tl), G.to_dev(dl)
+    ws = G.workspace(q38.lib.q38_mtp_accept_workspace_size(k, V))
+    dr = G.to_dev(drafts.astype(np.uint32))
+    out = G.empty((n, 2), np.int64)
+    for r in range(n):
+        q38.check(q38.lib.q38_mtp_accept_sampled(t.data_ptr(), d.data_ptr(), dr.data_ptr() + 4 * k * r, k, V, T,
+                                                 0xBEEF, 2, r, out.data_ptr() + 16 * r, ws.data_ptr(), ws.numel(),
+                                                 G.stream()))
+    o = G.to_host(out)
+    pv, hist = k3_pvalues(tl, dl, T, drafts, o[:, 0], o[:, 1])
+    print("device k=3 sampling p-values:", {key: f"{v:.3g}" for key, v in pv.items()}, "accepted:", hist)
+    assert hist.min() >= 700, hist
+    bad = {key: v for key, v in pv.items() if v < 1e-4}
+    assert not bad, (bad, hist)
 
 
 def test_sampled_full_vocab(gpu, q38, orc):

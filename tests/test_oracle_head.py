@@ -4,6 +4,8 @@ import numpy as np
 import pytest
 from scipy import stats
 
+from sampling_cases import k3_case, k3_pvalues, softmax_T
+
 
 def test_head_contract_vs_float64(orc):
     rng = np.random.default_rng(0)
@@ -96,6 +98,113 @@ def test_sampling_output_follows_target(orc):
         counts[d if a == 1 else nxt] += 1
     chi = stats.chisquare(counts, p * n)
     assert chi.pvalue > 1e-4, (counts, p * n)
+
+
+def _run_rounds(orc, tl, dl, T, n, seed=21):
+    k, V = dl.shape
+    rng = np.random.default_rng(seed)
+    q = softmax_T(dl, T)
+    drafts = np.stack([rng.choice(V, size=n, p=q[i]) for i in range(k)], 1)
+    res = np.array([orc.accept_sampled(tl, dl, drafts[t], T, 0xC0FFEE, 3, t) for t in range(n)])
+    return drafts, res[:, 0], res[:, 1]
+
+
+def _k3_pvalues(orc, tl, dl, T, n):
+    """n oracle rounds of the k = 3 case, checked by sampling_cases.k3_pvalues."""
+    drafts, acc, nxt = _run_rounds(orc, tl, dl, T, n)
+    return k3_pvalues(tl, dl, T, drafts, acc, nxt)
+
+
+def test_sampling_k3_every_emitted_token(orc):
+    """k = 3: every position of the emitted sequence follows its target row, the residual
+    draw at each first rejection (positions 0, 1 and 2) follows norm(max(0, p_i - q_i)),
+    the bonus token after three acceptances follows p_3, and each acceptance happens with
+    probability sum_x min(p_i(x), q_i(x)) (Leviathan et al. 2023, Theorem 1)."""
+    tl, dl, T = k3_case()
+    pv, hist = _k3_pvalues(orc, tl, dl, T, 24000)
+    assert hist.min() >= 1500, hist          # every accepted count 0..3 is well represented
+    bad = {key: v for key, v in pv.items() if v < 1e-4}
+    assert not bad, (bad, hist)
+
+
+@pytest.mark.parametrize("fault,keys", [(1, ("bonus", "pos3")), (2, ("res1", "res2"))])
+def test_sampling_k3_planted_wrong_row_fails(orc, fault, keys):
+    """The same checks catch a sampler that draws from the wrong row: the bonus token from
+    p_{k-1} (fault 1), or the residual after a rejection at i >= 1 from row i - 1 (fault 2)."""
+    tl, dl, T = k3_case()
+    orc.lib.orc_plant_fault(fault)
+    try:
+        pv, _ = _k3_pvalues(orc, tl, dl, T, 24000)
+    finally:
+        orc.lib.orc_plant_fault(0)
+    for key in keys:
+        assert pv[key] < 1e-12, (key, pv[key])
+    # the rows the fault does not touch still pass
+    for key in ("res0", "acc0", "acc1", "acc2"):
+        assert pv[key] > 1e-4, (key, pv[key])
+
+
+def _rne_bf16_by_neighbours(f32):
+    """float32 -> bf16 bits by choosing the nearer of the two bf16 neighbours in float64
+    (ties to the even mantissa, beyond the largest finite value to infinity): a second,
+    independent formulation of round-to-nearest-even."""
+    out = np.empty(f32.shape, np.uint16)
+    for i, v in enumerate(f32.reshape(-1)):
+        v = np.float32(v)
+        if np.isnan(v):
+            out.flat[i] = 0x7FC0 if not np.signbit(v) else 0xFFC0
+            continue
+        sign = 0x8000 if np.signbit(v) else 0
+        a = abs(float(v))
+        lo = int(np.array(abs(v), np.float32).view(np.uint32)) >> 16          # truncation toward 0
+        lo_v = float(np.array(lo << 16, np.uint32).view(np.float32))
+        if lo_v == a:
+            out.flat[i] = sign | lo
+            continue
+        hi = lo + 1
+        hi_v = float(np.array(hi << 16, np.uint32).view(np.float32)) if hi < 0x7F80 else float("inf")
+        if hi == 0x7F80:   # above the largest finite bf16: halfway point is max + half an ulp
+            hi_v = 2.0 ** 128
+        dlo, dhi = a - lo_v, hi_v - a
+        pick = lo if (dlo < dhi or (dlo == dhi and lo % 2 == 0)) else hi
+        out.flat[i] = sign | (0x7F80 if pick >= 0x7F80 else pick)
+    return out
+
+
+def test_residual_add_float32_restatement(orc):
+    """orc_residual_add = bf16(float32(h) + float32(y)) with round-to-nearest-even, against
+    numpy's IEEE float32 add and a neighbour-comparison rounding; plus closed forms
+    (h + 0 = h, h + (-h) = +0, signed zeros, overflow to infinity, inf - inf = NaN, exact
+    halfway cases in both directions, subnormals)."""
+    rng = np.random.default_rng(33)
+    h = orc.bf16(rng.normal(0, 1, 4000) * 10.0 ** rng.integers(-30, 30, 4000))
+    y = orc.bf16(rng.normal(0, 1, 4000) * 10.0 ** rng.integers(-30, 30, 4000))
+    one = 0x3F80
+    special_h = [0x0000, 0x8000, 0x8000, 0x7F7F, 0xFF7F, 0x7F80, 0x0001, 0x8001, 0x0080, one, one, one, 0x4000]
+    special_y = [0x8000, 0x8000, 0x0000, 0x7F7F, 0xFF7F, 0xFF80, 0x0001, 0x0003, 0x8001, 0x3B80, 0x3BC0, 0x3C40,
+                 0x3C00]
+    # 1 + 2^-8 is halfway between 1 and 1 + 2^-7 (ties to 1, even); 1 + 3*2^-9 rounds up
+    # to 1 + 2^-7; 1 + 2^-7 + 2^-8 is the next tie (to the even 1 + 2^-6); 2 + 2^-7 is
+    # halfway between 2 and 2 + 2^-6 (to 2)
+    h = np.concatenate([h, np.array(special_h, np.uint16), h[:500]])
+    y = np.concatenate([y, np.array(special_y, np.uint16), (h[:500] ^ 0x8000).astype(np.uint16)])
+    got = orc.residual_add(h, y)
+    with np.errstate(over="ignore", invalid="ignore"):
+        s32 = orc.bf16_to_f32(h) + orc.bf16_to_f32(y)
+    want = _rne_bf16_by_neighbours(s32)
+    nan = np.isnan(s32)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.isnan(orc.bf16_to_f32(got[nan])).all()
+    n0 = 4000
+    g = got[n0:n0 + len(special_h)].tolist()
+    assert g[0] == 0x0000 and g[1] == 0x8000 and g[2] == 0x0000      # +0 + -0 = +0; -0 + -0 = -0
+    assert g[3] == 0x7F80 and g[4] == 0xFF80                          # overflow to +-inf
+    assert np.isnan(orc.bf16_to_f32(np.array([g[5]], np.uint16)))[0]  # inf + -inf
+    assert g[6] == 0x0002 and g[7] == 0x0002 and g[8] == 0x007F       # subnormal sums are exact
+    assert g[9] == one and g[10] == 0x3F81 and g[11] == 0x3F82 and g[12] == 0x4000
+    assert (got[-500:] == 0).all()                                   # h + (-h) = +0
+    assert np.array_equal(orc.residual_add(h[:4000], np.zeros(4000, np.uint16)),
+                          np.where((h[:4000] & 0x7FFF) == 0, 0, h[:4000]).astype(np.uint16))
 
 
 # ---------------------------------------------------------------- Q4 draft head (R14)
