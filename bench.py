@@ -118,6 +118,32 @@ def cpu_baseline(args, mean_acc):
     return out
 
 
+def chain_only(args, q38, torch, ctx, layers, larr, ws):
+    """Profiling driver: the MoE chain alone at M = args.chain_only rows (the layer kernels a
+    counter run collects), args.warmup untimed and args.steps event-timed passes, eager launches."""
+    M = args.chain_only
+    assert 1 <= M <= 4, "--chain-only takes 1..4 rows"
+    sp = torch.cuda.current_stream().cuda_stream
+    h = torch.empty((M, H), dtype=torch.int16, device="cuda")
+    toks = (C.c_uint32 * M)(*[11 + 7 * r for r in range(M)])
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ts = []
+    for i in range(args.warmup + args.steps):
+        q38.check(q38.lib.q38_embed_synthetic(SEED, toks, M, H, h.data_ptr(), sp))
+        ev0.record()
+        q38.check(q38.lib.q38_verify_chain(larr, len(layers), h.data_ptr(), M, 1e-6, None, ws.data_ptr(),
+                                           ws.numel(), sp))
+        ev1.record()
+        torch.cuda.synchronize()
+        if i >= args.warmup:
+            ts.append(1e3 * ev0.elapsed_time(ev1) / len(layers))
+    q38.check(q38.lib.q38_ctx_synchronize(ctx.h, sp))
+    log(f"chain only, M={M}: {np.median(ts):.2f} us/layer over {len(layers)} layers (median of {len(ts)} passes)")
+    for L in layers:
+        L.close()
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -128,6 +154,8 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=20, help="timed CPU passes per (M, thread count)")
     ap.add_argument("--cpu-layers", type=int, default=5, help="layers the CPU passes are spread over")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel from the host")
+    ap.add_argument("--chain-only", type=int, default=0, metavar="M",
+                    help="profiling driver: only the 48-layer MoE chain at M rows, --steps times, then exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (reference kernel for HBM counter calibration)")
     args = ap.parse_args()
@@ -148,9 +176,12 @@ def main():
     d = q38.desc()
     log("generating 48 synthetic layers + Q8 head")
     layers = [q38.MoeLayer(ctx, d, seed=SEED, layer=l) for l in range(args.layers)]
-    head = q38.Head(ctx, q38.Q38_HEAD_Q8, V, H, seed=SEED)
     larr = (C.c_void_p * len(layers))(*[L.h.value for L in layers])
     ws = torch.empty(q38.lib.q38_moe_workspace_size(C.byref(d), 4), dtype=torch.uint8, device=dev)
+    if args.chain_only:
+        chain_only(args, q38, torch, ctx, layers, larr, ws)
+        return
+    head = q38.Head(ctx, q38.Q38_HEAD_Q8, V, H, seed=SEED)
     wsh = torch.empty(head.workspace_size(4), dtype=torch.uint8, device=dev)
     h = torch.empty((4, H), dtype=torch.int16, device=dev)
     hf = torch.empty((4, H), dtype=torch.int16, device=dev)
@@ -240,6 +271,7 @@ def main():
         tokens += got[0] + 1
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    q38.check(q38.lib.q38_ctx_synchronize(ctx.h, sp))  # no bounded wait gave up in the timed rounds
     tok_s = tokens / elapsed
     ms_round = 1e3 * elapsed / args.steps
     mean_acc = tokens / args.steps - 1
@@ -300,23 +332,22 @@ def main():
     uniq = [int(p[0].item()) for p in plans]
     nl = len(layers)
     MK = M * K
-    # algorithmic bytes per launch: the weights a launch must read once (per-expert figures
-    # of the packed layout: gate/up codes 2 x 512 rows x 448 B, down 2048 rows x 112 B, one
-    # fp16 scale per row; the fp16 d8 codebooks once per launch, not once per CU) plus the
-    # activations it reads and writes as designed (gate/up partial sums and down outputs are
-    # two fp32 chunk planes per route, the router writes x as bf16 and fp16).
+    # Algorithmic bytes per launch (the per-unit figures of the packed layout): the weights a
+    # launch must read once -- per expert slot (the U routed experts and the shared one) the
+    # gate/up codes 2 x 512 rows x 448 B and down codes 2048 rows x 112 B with one fp16 scale
+    # per row (694,272 B), the three fp16 d8 codebooks once per launch (786,432 B) -- plus the
+    # activations the layer reads and writes: the router's logits and shared gate, x (fp16),
+    # and the residual stream h read and written. The kernel's fp32 partial-sum planes (two
+    # chunk planes per route for gate, up and down, written and read back inside the launch)
+    # are designed intermediates, reported separately and not counted.
     book = 16384 * 8 * 2
     routes = MK + M  # routed + shared
-    gu_bytes = sum((u + 1) * (2 * I * 448 + 2 * I * 2) + 2 * book + M * E * 4 + M * H * 2 + 2 * 2 * routes * I * 4
-                   for u in uniq) / nl
-    dn_bytes = sum((u + 1) * (H * 112 + H * 2) + book + 2 * 2 * routes * I * 4 + 2 * routes * H * 4
-                   for u in uniq) / nl
+    slot_bytes = 2 * I * 448 + 2 * I * 2 + H * 112 + H * 2
+    gd_alg = sum((u + 1) * slot_bytes for u in uniq) / nl + 3 * book + M * E * 4 + M * 4 + M * H * 2 + 2 * M * H * 2
+    gd_planes = 2 * (2 * 2 * routes * I * 4 + 2 * routes * H * 4)   # (written, then read)
     rt_bytes = E * H * 2 + H * 2 + M * H * 2 + 2 * M * H * 2 + M * (E + 1) * 4
-    mg_bytes = 2 * routes * H * 4 + M * K * 4 + M * 4 + 2 * M * H * 2
-    # config 1 at M = 4 runs gate/up, down and the combine in one kernel (k_gd4): its bytes
-    # are the three phases' (the partial-sum planes it writes and reads back included)
     kernels = {"k_gd4 (top-k, plan, gate/up, SwiGLU, down, route-order reduce, shared gate, residual)":
-               (tm.gate_up_ms, gu_bytes + dn_bytes + mg_bytes),
+               (tm.gate_up_ms, gd_alg),
                "k_route_norm (RMSNorm, router logits)": (tm.routing_ms, rt_bytes)}
     dom = max(kernels, key=lambda k: kernels[k][0])
     dom_us = 1e3 * kernels[dom][0] / nl
@@ -541,7 +572,9 @@ def main():
     # k = 3 at temperature 0.7: Q8 target logits of the 4 verify rows (fast pass), Q4/g64 draft
     # logits of the 3 draft rows, then rejection sampling on the device. Each call is timed
     # with events on the launch stream (median of 20, after a warm-up).
-    head_q4 = q38.Head(ctx, q38.Q38_HEAD_Q4G64, V, H, seed=SEED)
+    # two Q4 heads (165 MB each, 330 MB together, beyond the 256 MB MALL), alternated call by
+    # call, so that every timed Q4 call streams its head from HBM
+    head_q4s = [q38.Head(ctx, q38.Q38_HEAD_Q4G64, V, H, seed=SEED + i) for i in range(2)]
     tl = torch.empty((4, V), dtype=torch.float32, device=dev)
     dl = torch.empty((3, V), dtype=torch.float32, device=dev)
     acc_out = torch.empty(2, dtype=torch.int64, device=dev)
@@ -554,8 +587,8 @@ def main():
     calls = {
         "q8_logits_4rows": lambda: q38.check(q38.lib.q38_head_logits(head.h, hf.data_ptr(), 4, tl.data_ptr(),
                                                                      wsh.data_ptr(), wsh.numel(), sp)),
-        "q4_draft_logits_3rows": lambda: q38.check(q38.lib.q38_head_logits(head_q4.h, hf.data_ptr(), 3,
-                                                                           dl.data_ptr(), None, 0, sp)),
+        "q4_draft_logits_3rows": lambda: q38.check(q38.lib.q38_head_logits(head_q4s[rnd[0] & 1].h, hf.data_ptr(),
+                                                                           3, dl.data_ptr(), None, 0, sp)),
         "accept_sampled": lambda: q38.check(q38.lib.q38_mtp_accept_sampled(
             tl.data_ptr(), dl.data_ptr(), sdrafts.data_ptr(), 3, V, 0.7, SEED, 0, rnd[0], acc_out.data_ptr(),
             wsa.data_ptr(), wsa.numel(), sp)),
@@ -583,7 +616,8 @@ def main():
         "accept_gbps_one_pass": 7 * V * 4 / (samp_us["accept_sampled"] * 1e-6) / 1e9,
     }
     log("config 2 sampled tail (us): " + ", ".join(f"{k}={v:.1f}" for k, v in samp_us.items()))
-    head_q4.close()
+    for hq in head_q4s:
+        hq.close()
 
     # ---------------------------------------------------------------- config 2: learned drafts
     # The MTP draft head (seeded random-init, its block = layer 48) drafts 3 tokens on the
@@ -713,7 +747,8 @@ def main():
         },
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "launch_avg_us": dom_us,
-                     "algorithmic_bytes_per_launch": dom_bytes},
+                     "algorithmic_bytes_per_launch": dom_bytes,
+                     "intermediate_bytes_per_launch": gd_planes if dom.startswith("k_gd4") else 0},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

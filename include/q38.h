@@ -33,7 +33,8 @@ enum {
     Q38_EHIP = -3,    /* HIP runtime failure */
     Q38_ENOMEM = -4,  /* allocation failure */
     Q38_ESTATE = -5,  /* invalid lifecycle / commit request   (std::runtime_error) */
-    Q38_ESPACE = -6   /* workspace too small */
+    Q38_ESPACE = -6,  /* workspace too small */
+    Q38_EWAIT = -7    /* a bounded wait between workgroups gave up (q38_ctx_synchronize) */
 };
 
 typedef struct q38_ctx q38_ctx;
@@ -177,6 +178,29 @@ int q38_moe_layer_codebook(const q38_moe_layer* layer, int proj, const uint16_t*
                            const uint16_t** scales, const uint16_t** biases);
 /* Algorithmic HBM bytes of one forward that touches n_unique routed experts. */
 int64_t q38_moe_layer_bytes(const q38_moe_layer* layer, int32_t n_unique, int32_t rows);
+/* Completion check of the stream's work on the context's device. The one-launch verify
+ * layer (d8/14-bit, H 2048, I 512, top-10, 1-4 rows; see q38_verify_chain) passes values
+ * between its workgroups, which wait for each other with bounded waits; a wait that gives up
+ * (the grid was not resident at once: the device shared with other work) leaves NaN outputs
+ * and sets a status bit on the device. This call synchronises `stream`, then returns
+ * Q38_EWAIT if any such wait gave up on the device since the last check (and clears the
+ * bit), Q38_OK otherwise. No counterpart in the reference (its Metal dispatches do not wait
+ * on each other); the C++ mirror calls it wherever it reads tokens back
+ * (src/mtp_verifier.cpp:47-52). */
+int q38_ctx_synchronize(q38_ctx* ctx, void* stream);
+
+/* Process-wide switch (default on): 0 makes every later call take the multi-kernel layer
+ * (gate/up, down and combine as separate launches, no waits between workgroups) instead of
+ * the one-launch kernel. The one-launch kernel is also taken only where the device fits its
+ * grid at one workgroup per CU (checked once per device against the kernel's occupancy). */
+void q38_set_fused_layers(int enable);
+
+/* Test hook: the number of re-reads a bounded wait makes before it gives up (default 65536,
+ * about 0.1 s; a negative value restores it). A limit of 0 makes a wait give up at its first
+ * read of a value another workgroup has not stored yet, so tests can reach the give-up path
+ * while every kernel still runs to its end. */
+void q38_debug_set_wait_limit(int32_t spins);
+
 /* Workspace bytes needed by q38_moe_forward / q38_verify_chain for up to max_rows rows
  * (1..2048). */
 size_t q38_moe_workspace_size(const q38_moe_desc* desc, int32_t max_rows);
@@ -229,7 +253,8 @@ int q38_moe_layer_set_router_bias(q38_moe_layer* layer, const float* bias);
  * bf16, updated in place. traces (optional): per-layer route outputs, array of n_layers.
  * At 1-4 rows on d8/14-bit H 2048 layers the experts and the combine run as one kernel whose
  * workgroups (one per CU) wait for each other: it expects the device's CUs to itself while
- * it runs (otherwise bounded waits expire and the affected outputs are NaN). */
+ * it runs. Otherwise bounded waits give up, the affected outputs are NaN, and the next
+ * q38_ctx_synchronize returns Q38_EWAIT (q38_set_fused_layers(0) avoids the kernel). */
 int q38_verify_chain(q38_moe_layer* const* layers, int32_t n_layers, uint16_t* h, int32_t rows,
                      float eps, const q38_route_out* traces, void* workspace, size_t workspace_bytes,
                      void* stream);

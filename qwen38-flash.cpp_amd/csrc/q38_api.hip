@@ -126,6 +126,26 @@ int q38_ctx_create(int hip_device, q38_ctx** out) {
 }
 void q38_ctx_destroy(q38_ctx* ctx) { delete ctx; }
 
+int q38_ctx_synchronize(q38_ctx* ctx, void* stream) {
+    if (!ctx) return fail(Q38_EINVAL, "q38_ctx_synchronize: null context");
+    int prev = 0;
+    Q38_HIP(hipGetDevice(&prev));
+    if (prev != ctx->device) Q38_HIP(hipSetDevice(ctx->device));
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    uint32_t status = 0;
+    if (e == hipSuccess) e = read_wait_status(&status, true);
+    if (prev != ctx->device) (void)hipSetDevice(prev);
+    if (e != hipSuccess) return hip_fail(e, "q38_ctx_synchronize");
+    if (status)
+        return fail(Q38_EWAIT, "a bounded wait between workgroups of the one-launch verify layer gave up: the "
+                               "outputs of the calls since the last check are invalid (is the device shared?)");
+    return Q38_OK;
+}
+
+void q38_set_fused_layers(int enable) { set_fused_enabled(enable != 0); }
+
+void q38_debug_set_wait_limit(int32_t spins) { set_wait_limit(spins); }
+
 // ------------------------------------------------------------------ geometry
 int64_t q38_packed_vq_word_count(int64_t code_count, int bits) {
     if (bits <= 0 || bits > 31 || code_count < 0) {
@@ -650,6 +670,7 @@ static size_t moe_ws(const q38_moe_desc& d, int M, MoeBufs* w, void* base) {
     t.h16 = reinterpret_cast<uint16_t*>(take(gu * 2));
     t.gu_plane = gu;
     t.d_plane = dn;
+    t.wait_limit = wait_limit();
     if (w) *w = t;
     return off;
 }
@@ -922,7 +943,10 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
             t.merge_ms += ms[3];
         }
         t.layers = n_layers;
+        uint32_t status = 0;
+        if (e == hipSuccess) e = read_wait_status(&status, true);
         if (e != hipSuccess) rc = hip_fail(e, "profiled chain timing");
+        else if (status) rc = fail(Q38_EWAIT, "q38_verify_chain_profiled: a wait between workgroups gave up");
         else *tm = t;
     }
     for (auto& e : ev)

@@ -87,6 +87,9 @@ struct MoeBufs {
     uint16_t* h16;     // [M*K + M, I] fp16 SwiGLU rows (prefill path)
     size_t gu_plane;   // floats between the chunk planes of g and u
     size_t d_plane;    // floats between the chunk planes of d
+    // Re-reads a bounded wait between workgroups of one launch makes before it gives up
+    // (kWaitLimit; smaller only when a test forces the give-up path).
+    int wait_limit;
 };
 
 struct LayerDev {
@@ -101,6 +104,10 @@ struct LayerDev {
     int mixed;
     ProjDev pb[3][2];
     const float* rbias;      // [E] additive router-logit bias (device) or null
+    // The call's choice of the one-launch layer kernel (k_gd4), fixed by moe_call_dev so that
+    // the router (which resets the planes that kernel waits on) and the expert launch agree:
+    // 0 undecided (decided from the layer on each query), 1 fused, 2 not fused.
+    int fused_mode;
 };
 
 struct HeadDev {
@@ -152,6 +159,17 @@ hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t 
 // out <- y): launch_gate_up takes it without the combine, launch_down then has nothing to
 // launch. The router kernel before it resets the gate/up and down planes the launch waits on.
 bool moe_uses_fused(const LayerDev& L, int M);
+// The one-launch kernel's workgroups wait for each other, so it is taken only while it is
+// enabled (q38_set_fused_layers) and the compiled kernels fit one workgroup per CU with the
+// grid no larger than the CU count (checked once per device).
+void set_fused_enabled(bool on);
+// Bounded waits between workgroups: re-reads before a wait gives up, and the device status
+// word that a wait which gave up sets (bit 0). read_wait_status synchronises the device's
+// null stream with the copy (the caller synchronises its own stream first).
+constexpr int kWaitLimit = 1 << 16;
+void set_wait_limit(int spins);  // < 0: kWaitLimit
+int wait_limit();
+hipError_t read_wait_status(uint32_t* status, bool clear);
 hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);
 int mfma_grid();  // persistent workgroups of the expert kernels (a multiple of 32)
 // Prefill widths, kMaxRows < M <= kMaxPrefillRows (q38_moe_pf.hip), one kernel each:

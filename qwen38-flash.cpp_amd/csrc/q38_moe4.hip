@@ -143,7 +143,17 @@ __device__ __forceinline__ float load_f32(const float* p) {
 }
 // The reset pattern of the gate/up planes (all ones: a NaN that no arithmetic produces).
 __device__ __forceinline__ bool gu_unset(float v) { return __float_as_uint(v) == 0xFFFFFFFFu; }
-constexpr int kGuSpinLimit = 1 << 16;
+} // namespace
+
+// Status of the bounded waits between workgroups (one word per device, in the code object):
+// bit 0 is set by every thread whose wait gave up with a value still unset. The host reads
+// and clears it (read_wait_status).
+__device__ uint32_t g_wait_status;
+
+namespace {
+__device__ __forceinline__ void wait_gave_up() {
+    __hip_atomic_fetch_or(&g_wait_status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Gate and up projections. Workgroup type = (projection, codebook chunk); waves = K slices.
 // Items are 64-row tiles of I; the 4 B columns are the request rows (rows not routed to the
@@ -507,12 +517,14 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
                         for (int i = 0; i < 2; ++i) p |= gu_unset(gl[q][i]) || gu_unset(ul[q][i]);
                 return p;
             };
-            // (bounded: a value still unset at the limit stays NaN and so does the output)
+            // (bounded: a value still unset at the limit stays NaN, and so does the output, and
+            // the device's wait status records it)
             int spin = 0;
-            for (; pending() && spin < kGuSpinLimit; ++spin) {
+            for (; pending() && spin < B.wait_limit; ++spin) {
                 __builtin_amdgcn_s_sleep(2);
                 load_gu(Slot{expert, n, pos0}, gl, ul);
             }
+            if (pending()) wait_gave_up();
 #ifdef Q38_TRACE
             if (jj == 0) {
                 Q38_STAMP(16384, 5);
@@ -622,9 +634,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 // coherent at the device's memory side, so no L2 write-back is needed. The router kernel
 // before this one sets every value of those planes to the all-ones pattern (a NaN that no
 // arithmetic produces), and a reader re-reads the values it needs until none holds it. The
-// wait is bounded (kGuSpinLimit re-reads, ~0.1 s): every workgroup of the grid is resident
-// at once (one per CU, grid <= CUs), so it ends long before that unless something is broken,
-// and then the affected outputs are NaN instead of the kernel hanging.
+// wait is bounded (kWaitLimit re-reads, ~0.1 s): every workgroup of the grid is resident at
+// once (one per CU, grid <= CUs, checked against the kernel's occupancy before it is chosen),
+// so it ends long before that unless the device is shared with other work or something is
+// broken; then the affected outputs are NaN instead of the kernel hanging, and the device's
+// wait status records it for the API to report (q38_ctx_synchronize).
 constexpr int kCombineWgs = 32;
 template <int KT>
 __device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B, int M, const float* wt, uint16_t* h,
@@ -656,10 +670,11 @@ __device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B
         return q;
     };
     load();
-    for (int spin = 0; pending() && spin < kGuSpinLimit; ++spin) {
+    for (int spin = 0; pending() && spin < B.wait_limit; ++spin) {
         __builtin_amdgcn_s_sleep(2);
         load();
     }
+    if (pending()) wait_gave_up();
     const float y = combine_value<KT, true>(L, in);
     const size_t i = static_cast<size_t>(r) * H + o;
     if (h) h[i] = f2bf(rbf(bf2f(hraw) + y));
@@ -736,6 +751,8 @@ LayerDev moe_call_dev(const LayerDev& L, int M) {
         d.gu_parts = L.p[0].dim / 4;
         d.d_parts = L.p[2].dim / 4;
     }
+    d.fused_mode = 0;
+    d.fused_mode = moe_uses_fused(d, M) ? 1 : 2;
     return d;
 }
 
@@ -747,14 +764,64 @@ static int ring_items(const LayerDev& L, int M, int tiles, int per_type) {
     return ((M * L.K + 1) * tiles + per_type - 1) / per_type;
 }
 
+namespace {
+std::atomic<int> g_fused_enabled{1};
+std::atomic<int> g_wait_limit{kWaitLimit};
+
+// Occupancy of one k_gd4 instantiation: at least one workgroup of 512 threads with its LDS
+// per CU, and the planned grid no larger than the CUs that many workgroups cover.
+template <int DG, int DD, int G8>
+bool gd4_fits(int cus) {
+    constexpr size_t lds = gu4_lds_bytes<14, 256, 2>();
+    auto kern = k_gd4<14, 256, 64, 2, DG, DD, 10, G8>;
+    if (ensure_lds<k_gd4<14, 256, 64, 2, DG, DD, 10, G8>>(lds) != hipSuccess) return false;
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), 512, lds) != hipSuccess)
+        return false;
+    return nb >= 1 && static_cast<int64_t>(mfma_grid()) <= static_cast<int64_t>(cus) * nb;
+}
+
+// Whether every k_gd4 instantiation fits the current device as planned (once per device).
+bool fused_resident() {
+    static std::atomic<uint64_t> checked{0}, ok{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    const uint64_t bit = uint64_t{1} << (dev & 63);
+    if (checked.load(std::memory_order_acquire) & bit) return (ok.load(std::memory_order_acquire) & bit) != 0;
+    int cus = 0;
+    bool fits = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0;
+    fits = fits && gd4_fits<2, 1, 0>(cus) && gd4_fits<3, 2, 0>(cus) && gd4_fits<4, 2, 0>(cus) &&
+           gd4_fits<6, 3, 0>(cus) && gd4_fits<2, 1, 8>(cus) && gd4_fits<3, 2, 8>(cus) && gd4_fits<4, 2, 8>(cus) &&
+           gd4_fits<6, 3, 8>(cus);
+    (void)hipGetLastError();  // (a failed query leaves no error behind for the next launch)
+    if (fits) ok.fetch_or(bit, std::memory_order_acq_rel);
+    checked.fetch_or(bit, std::memory_order_acq_rel);
+    return fits;
+}
+} // namespace
+
+void set_fused_enabled(bool on) { g_fused_enabled.store(on ? 1 : 0, std::memory_order_relaxed); }
+void set_wait_limit(int spins) { g_wait_limit.store(spins < 0 ? kWaitLimit : spins, std::memory_order_relaxed); }
+int wait_limit() { return g_wait_limit.load(std::memory_order_relaxed); }
+hipError_t read_wait_status(uint32_t* status, bool clear) {
+    hipError_t e = hipMemcpyFromSymbol(status, HIP_SYMBOL(g_wait_status), sizeof(uint32_t), 0, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && clear && *status != 0) {
+        const uint32_t zero = 0;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(g_wait_status), &zero, sizeof(uint32_t), 0, hipMemcpyHostToDevice);
+    }
+    return e;
+}
+
 bool moe_uses_fused(const LayerDev& L, int M) {
+    if (L.fused_mode != 0) return L.fused_mode == 1;
+    if (!g_fused_enabled.load(std::memory_order_relaxed)) return false;
     if (!moe_uses_narrow(L, M)) return false;
     // per-row scales everywhere, or per-64-input groups in both projections
     const bool rows = L.p[0].ngrp == 1 && L.p[1].ngrp == 1 && L.p[2].ngrp == 1;
     if (!rows && !(gu_groups64(L) && dn_groups64(L))) return false;
     for (int p = 0; p < 3; ++p)
         if (L.p[p].dim != 8 || L.p[p].bits != 14 || !L.p[p].codes_t) return false;
-    return L.H == 2048 && L.I == 512 && L.K == 10 && mfma_grid() >= kCombineWgs;
+    return L.H == 2048 && L.I == 512 && L.K == 10 && mfma_grid() >= kCombineWgs && fused_resident();
 }
 
 // Ring depths of the two halves (as the two kernels pick them: every item's loads in flight

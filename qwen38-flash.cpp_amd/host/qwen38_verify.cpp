@@ -52,7 +52,10 @@ Context::~Context() {
     if (stream_) (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
     q38_ctx_destroy(ctx_);
 }
-void Context::synchronize() const { check_hip(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "sync"); }
+// Every read-back of the host interface waits here: the stream's work, then the device's
+// status of the one-launch layer kernel's bounded waits (a wait that gave up throws, as any
+// other failed verification does, instead of passing NaN rows on).
+void Context::synchronize() const { check(q38_ctx_synchronize(ctx_, stream_), "sync"); }
 
 std::size_t dtype_size(DType t) noexcept {
     switch (t) {

@@ -20,7 +20,7 @@ if not os.path.exists(LIB_PATH):
     raise ImportError(f"libq38.so is not built at {LIB_PATH}; run __graft_entry__.build()")
 lib = C.CDLL(LIB_PATH)
 
-Q38_OK, Q38_EINVAL, Q38_ERANGE, Q38_EHIP, Q38_ENOMEM, Q38_ESTATE, Q38_ESPACE = 0, -1, -2, -3, -4, -5, -6
+Q38_OK, Q38_EINVAL, Q38_ERANGE, Q38_EHIP, Q38_ENOMEM, Q38_ESTATE, Q38_ESPACE, Q38_EWAIT = 0, -1, -2, -3, -4, -5, -6, -7
 Q38_HEAD_Q8, Q38_HEAD_Q4G64 = 0, 1
 Q38_CB_FP16, Q38_CB_INT8_SCALED, Q38_CB_U8_PERDIM = 0, 1, 2
 
@@ -75,6 +75,9 @@ _sig("q38_last_error", C.c_char_p)
 _sig("q38_version", C.c_char_p)
 _sig("q38_ctx_create", C.c_int, C.c_int, C.POINTER(P))
 _sig("q38_ctx_destroy", None, P)
+_sig("q38_ctx_synchronize", C.c_int, P, P)
+_sig("q38_set_fused_layers", None, C.c_int)
+_sig("q38_debug_set_wait_limit", None, I32)
 _sig("q38_packed_vq_word_count", I64, I64, C.c_int)
 _sig("q38_unpack_vq_code", C.c_int, P, I64, I64, C.c_int, C.POINTER(U32))
 _sig("q38_supports_segmented_vq", C.c_int, C.c_int, C.c_int)
