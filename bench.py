@@ -139,6 +139,14 @@ def chain_only(args, q38, torch, ctx, layers, larr, ws):
             ts.append(1e3 * ev0.elapsed_time(ev1) / len(layers))
     q38.check(q38.lib.q38_ctx_synchronize(ctx.h, sp))
     log(f"chain only, M={M}: {np.median(ts):.2f} us/layer over {len(layers)} layers (median of {len(ts)} passes)")
+    if args.copy_calibration:
+        nb = 256 << 20
+        src = torch.ones(nb // 4, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: 4 x {nb} bytes read and written")
     for L in layers:
         L.close()
     ctx.close()

@@ -76,8 +76,9 @@ typedef struct q38_moe_desc {
  * later in-place change would make the two disagree. Expert index E is the shared expert.
  *   router       [E, H] bf16                      (SparseMoe::router_,  sparse_moe.hpp:201)
  *   shared_gate  [H] bf16 (w_sg)                  (shared_router_,       sparse_moe.hpp:209)
- *   codes[p]     [E+1, OUT_p, words_p] u32, words_p = ceil(IN_p/D/32)*BITS
- *   scales[p]    [E+1, OUT_p, IN_p/G_p] fp16
+ *   codes[p]     [E+1, OUT_p, words_p] u32, words_p = ceil(IN_p/D/32)*BITS (E rows without a
+ *                shared expert)
+ *   scales[p]    [E+1, OUT_p, IN_p/G_p] fp16 (E rows without a shared expert)
  *   books[p]     [2^BITS, D] fp16
  * p = 0 gate, 1 up, 2 down. */
 typedef struct q38_moe_weights {
@@ -200,6 +201,30 @@ void q38_set_fused_layers(int enable);
  * read of a value another workgroup has not stored yet, so tests can reach the give-up path
  * while every kernel still runs to its end. */
 void q38_debug_set_wait_limit(int32_t spins);
+
+/* Shared expert in MLX affine form: the only shared-expert format of the reference's
+ * checkpoints (SparseMoe::load_projection's affine branch, src/sparse_moe.cpp:474-480,
+ * 662-700, applied by SparseMoe::forward_shared, :1306-1313, through quantized_matmul).
+ * Projection p = gate, up (OUT = inter, IN = hidden), down (OUT = hidden, IN = inter):
+ *   weight[p]  [OUT, IN * bits / 32] u32, value j of a word at bits j * bits (LSB first)
+ *   scales[p], biases[p]  [OUT, IN / group], bf16 (scale_dtype 0) or fp16 (1)
+ * w[o, c] = scale[o, c / group] * q[o, c] + bias[o, c / group]. bits 2, 4 or 8; group 32, 64
+ * or 128; inter <= 4096 (its own size: SparseMoe's shared_expert_intermediate_size). Device
+ * pointers, adopted like q38_moe_weights. */
+typedef struct q38_affine_shared {
+    const uint32_t* weight[3];
+    const uint16_t* scales[3];
+    const uint16_t* biases[3];
+    int32_t bits, group, inter, scale_dtype;
+} q38_affine_shared;
+
+/* q38_moe_layer_create for a layer whose shared expert is affine (desc->has_shared = 1):
+ * weights->codes / scales hold the E routed experts only ([E, OUT, ...], no row for E), and
+ * weights->shared_gate is the BF16 w_sg. The shared expert then runs as two kernels of its own
+ * after the router; routing, the routed experts and the merge are those of q38_moe_layer_create
+ * (SparseMoe ctor, include/qwen38/sparse_moe.hpp:48-55). */
+int q38_moe_layer_create_affine_shared(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_weights* weights,
+                                       const q38_affine_shared* shared, q38_moe_layer** out);
 
 /* Workspace bytes needed by q38_moe_forward / q38_verify_chain for up to max_rows rows
  * (1..2048). */

@@ -348,11 +348,59 @@ void expert_forward(const ExpertWeights& W, const float* x, float* dout) {
     for (int o = 0; o < H; ++o) dout[o] = rbf16(proj_row_dot(W.down, o, h.data()));
 }
 
+// Shared expert in MLX affine form (the reference checkpoints' shared experts: the affine
+// branch of SparseMoe::load_projection, src/sparse_moe.cpp:662-700, applied by
+// SparseMoe::forward_shared, :1306-1313, through quantized_matmul). Row o of a [OUT, IN]
+// projection: values q in [0, 2^bits) packed LSB-first in 32-bit words (32 / bits per word),
+// w[o, c] = scale[o, c / G] * q[o, c] + bias[o, c / G] with bf16 (fmt 0) or fp16 (fmt 1) scales
+// and biases. The dot product is taken per group as scale * sum(q x) + bias * sum(x), in
+// double.
+struct AffineProj {
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+    int in, out, bits, group, fmt;
+};
+inline double affine_param(uint16_t v, int fmt) { return fmt ? f16_to_f32(v) : bf16_to_f32(v); }
+inline double affine_row_dot(const AffineProj& P, int o, const float* x) {
+    const int vpw = 32 / P.bits, ngrp = P.in / P.group;
+    const uint32_t mask = (1u << P.bits) - 1u;
+    const uint32_t* row = P.w + static_cast<size_t>(o) * (P.in / vpw);
+    double acc = 0.0;
+    for (int g = 0; g < ngrp; ++g) {
+        double qx = 0.0, sx = 0.0;
+        for (int c = g * P.group; c < (g + 1) * P.group; ++c) {
+            const uint32_t q = (row[c / vpw] >> ((c % vpw) * P.bits)) & mask;
+            qx += static_cast<double>(q) * x[c];
+            sx += x[c];
+        }
+        acc += affine_param(P.s[static_cast<size_t>(o) * ngrp + g], P.fmt) * qx +
+               affine_param(P.b[static_cast<size_t>(o) * ngrp + g], P.fmt) * sx;
+    }
+    return acc;
+}
+struct AffineExpert { AffineProj gate, up, down; };
+// forward_shared's rounding points: gate and up T (quantized_matmul outputs), T(silu), the
+// product T, the down projection T (the shared gate and the merge follow in moe_layer).
+void affine_expert_forward(const AffineExpert& W, const float* x, float* dout) {
+    const int I = W.gate.out, H = W.down.out;
+    std::vector<float> h(I);
+    for (int o = 0; o < I; ++o) {
+        const float g = rbf16(affine_row_dot(W.gate, o, x));
+        const float u = rbf16(affine_row_dot(W.up, o, x));
+        const float sg = rbf16(static_cast<double>(g) / (1.0 + std::exp(-static_cast<double>(g))));
+        h[o] = rbf16(static_cast<double>(sg) * u);
+    }
+    for (int o = 0; o < H; ++o) dout[o] = rbf16(affine_row_dot(W.down, o, h.data()));
+}
+
 struct LayerSource {
     virtual ~LayerSource() = default;
     virtual const uint16_t* router() = 0;       // [E, H] bf16
     virtual const uint16_t* wsg() = 0;          // [H] bf16 (may be null without shared)
     virtual ExpertWeights expert(int e) = 0;    // e == E: shared expert
+    // the shared expert in affine form instead of expert(E), when the layer has one
+    virtual const AffineExpert* shared_affine() { return nullptr; }
 };
 
 // Persistent worker pool: workers are created on first use, each pinned to one CPU of the
@@ -492,14 +540,18 @@ int moe_layer(const Desc& d, LayerSource& src, const uint16_t* x, int M, uint16_
     std::vector<int> uniq(ex.begin(), ex.end());
     std::sort(uniq.begin(), uniq.end());
     uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
-    if (d.has_shared) uniq.push_back(E);
+    const AffineExpert* sa = d.has_shared ? src.shared_affine() : nullptr;
+    if (d.has_shared && !sa) uniq.push_back(E);
     std::vector<ExpertWeights> ew(uniq.size());
     std::vector<int> slot_of(E + 1, -1);
     for (size_t u = 0; u < uniq.size(); ++u) { ew[u] = src.expert(uniq[u]); slot_of[uniq[u]] = static_cast<int>(u); }
     parallel_for(n_routes, threads, [&](int i) {
         const int r = i < M * k ? i / k : i - M * k;
         const int e = i < M * k ? ex[i] : E;
-        expert_forward(ew[slot_of[e]], xf.data() + static_cast<size_t>(r) * H, dout.data() + static_cast<size_t>(i) * H);
+        if (e == E && sa)
+            affine_expert_forward(*sa, xf.data() + static_cast<size_t>(r) * H, dout.data() + static_cast<size_t>(i) * H);
+        else
+            expert_forward(ew[slot_of[e]], xf.data() + static_cast<size_t>(r) * H, dout.data() + static_cast<size_t>(i) * H);
     });
     const uint16_t* wsg = d.has_shared ? src.wsg() : nullptr;
     for (int r = 0; r < M; ++r) {
@@ -731,6 +783,9 @@ struct DenseSource final : LayerSource {
     const uint16_t* wr; const uint16_t* ws;
     const uint32_t* codes[3]; const uint16_t* scales[3];
     std::vector<float> book[3];
+    bool has_sa = false;
+    AffineExpert sa{};
+    const AffineExpert* shared_affine() override { return has_sa ? &sa : nullptr; }
     DenseSource(const Desc& dd, const uint16_t* r, const uint16_t* w, const uint32_t* const* c,
                 const uint16_t* const* s, const uint16_t* const* b)
         : d(dd), wr(r), ws(w) {
@@ -1116,6 +1171,38 @@ int orc_moe_layer_dense(const Desc* d, const uint16_t* router, const uint16_t* w
     if (d->mixed) return -1;
     DenseSource src(*d, router, wsg, codes, scales, books);
     return moe_layer(*d, src, x, M, y, experts, weights, logits, threads);
+}
+// orc_moe_layer_dense with the shared expert in MLX affine form: codes / scales hold the E
+// routed experts only; sa_w / sa_s / sa_b: gate, up ([inter, H]) and down ([H, inter]) packed
+// words, scales and biases (fmt 0 bf16, 1 fp16).
+int orc_moe_layer_dense_affine_shared(const Desc* d, const uint16_t* router, const uint16_t* wsg,
+                                      const uint32_t* const* codes, const uint16_t* const* scales,
+                                      const uint16_t* const* books, const uint32_t* const* sa_w,
+                                      const uint16_t* const* sa_s, const uint16_t* const* sa_b, int bits, int group,
+                                      int inter, int fmt, const uint16_t* x, int M, uint16_t* y, int32_t* experts,
+                                      float* weights, float* logits, int threads) {
+    if (d->mixed || !d->has_shared || bits <= 0 || 32 % bits || group <= 0 || d->hidden % group || inter % group)
+        return -1;
+    DenseSource src(*d, router, wsg, codes, scales, books);
+    src.has_sa = true;
+    src.sa.gate = AffineProj{sa_w[0], sa_s[0], sa_b[0], d->hidden, inter, bits, group, fmt};
+    src.sa.up = AffineProj{sa_w[1], sa_s[1], sa_b[1], d->hidden, inter, bits, group, fmt};
+    src.sa.down = AffineProj{sa_w[2], sa_s[2], sa_b[2], inter, d->hidden, bits, group, fmt};
+    return moe_layer(*d, src, x, M, y, experts, weights, logits, threads);
+}
+// The affine shared expert alone on rows of x: dout [M, H] = T(down) per row (no gate).
+int orc_affine_expert(const uint32_t* const* sa_w, const uint16_t* const* sa_s, const uint16_t* const* sa_b, int H,
+                      int inter, int bits, int group, int fmt, const uint16_t* x, int M, float* dout) {
+    if (bits <= 0 || 32 % bits || group <= 0 || H % group || inter % group) return -1;
+    const AffineExpert W{AffineProj{sa_w[0], sa_s[0], sa_b[0], H, inter, bits, group, fmt},
+                         AffineProj{sa_w[1], sa_s[1], sa_b[1], H, inter, bits, group, fmt},
+                         AffineProj{sa_w[2], sa_s[2], sa_b[2], inter, H, bits, group, fmt}};
+    std::vector<float> xf(H);
+    for (int r = 0; r < M; ++r) {
+        for (int c = 0; c < H; ++c) xf[c] = bf16_to_f32(x[static_cast<size_t>(r) * H + c]);
+        affine_expert_forward(W, xf.data(), dout + static_cast<size_t>(r) * H);
+    }
+    return 0;
 }
 // One expert applied to rows of x (no routing); dout [M, H] = T(down) per row.
 int orc_expert_dense(const Desc* d, const uint32_t* const* codes, const uint16_t* const* scales,

@@ -258,7 +258,9 @@ static int prepare_layer(q38_moe_layer* L) {
     }
     int64_t rows[3] = {0, 0, 0};
     for (int p = 0; p < 3 && tiled; ++p) {
-        rows[p] = static_cast<int64_t>(L->desc.experts + 1) * (p < 2 ? L->desc.inter : L->desc.hidden);
+        // (the routed experts and the VQ shared expert E: the tensors hold no row E otherwise)
+        const int experts = L->desc.experts + (L->desc.has_shared && !L->dev.shared_affine ? 1 : 0);
+        rows[p] = static_cast<int64_t>(experts) * (p < 2 ? L->desc.inter : L->desc.hidden);
         toff[p] = total;
         total += align256(static_cast<size_t>(rows[p]) * L->dev.p[p].words * 4);
     }
@@ -315,6 +317,48 @@ int q38_moe_layer_create(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_w
             return fail(Q38_EINVAL, "every projection needs codes, scales and a codebook");
     auto* L = new q38_moe_layer{ctx, *desc, {}, nullptr, 0, nullptr};
     fill_dev(L, weights);
+    if (int rc = prepare_layer(L)) {
+        delete L;
+        return rc;
+    }
+    *out = L;
+    return Q38_OK;
+}
+
+int q38_moe_layer_create_affine_shared(q38_ctx* ctx, const q38_moe_desc* desc, const q38_moe_weights* weights,
+                                       const q38_affine_shared* shared, q38_moe_layer** out) {
+    if (!ctx || !out || !weights || !shared || !desc)
+        return fail(Q38_EINVAL, "q38_moe_layer_create_affine_shared: null argument");
+    if (desc->mixed || !desc->has_shared)
+        return fail(Q38_EINVAL, "q38_moe_layer_create_affine_shared: a uniform layer with a shared expert "
+                                "(has_shared = 1, mixed = 0)");
+    if (int rc = validate_desc(desc)) return rc;
+    const int bits = shared->bits, G = shared->group, Is = shared->inter;
+    if (bits != 2 && bits != 4 && bits != 8)
+        return fail(Q38_EINVAL, "affine shared expert: bits must be 2, 4 or 8 (values whole in 32-bit words)");
+    if (G != 32 && G != 64 && G != 128) return fail(Q38_EINVAL, "affine shared expert: group must be 32, 64 or 128");
+    if (Is < G || Is % G || desc->hidden % G || Is > 4096 || desc->hidden > 4096)
+        return fail(Q38_EINVAL, "affine shared expert: the group must divide hidden and inter (both <= 4096)");
+    if (static_cast<int64_t>(Is) > static_cast<int64_t>(desc->top_k + 1) * desc->inter)
+        return fail(Q38_EINVAL, "affine shared expert: its intermediate size may be at most (top_k + 1) x inter");
+    if (shared->scale_dtype != 0 && shared->scale_dtype != 1)
+        return fail(Q38_EINVAL, "affine shared expert: scale_dtype 0 (bf16) or 1 (fp16)");
+    if (!weights->router || !weights->shared_gate) return fail(Q38_EINVAL, "router / shared gate tensors are required");
+    for (int p = 0; p < 3; ++p) {
+        if (!weights->codes[p] || !weights->scales[p] || !weights->books[p])
+            return fail(Q38_EINVAL, "every projection needs codes, scales and a codebook");
+        if (!shared->weight[p] || !shared->scales[p] || !shared->biases[p])
+            return fail(Q38_EINVAL, "affine shared expert: every projection needs weight, scales and biases");
+    }
+    auto* L = new q38_moe_layer{ctx, *desc, {}, nullptr, 0, nullptr};
+    fill_dev(L, weights);
+    LayerDev& v = L->dev;
+    v.shared_affine = 1;
+    v.sa_bits = bits;
+    v.sa_group = G;
+    v.sa_inter = Is;
+    v.sa_f16 = shared->scale_dtype;
+    for (int p = 0; p < 3; ++p) v.sa[p] = AffineDev{shared->weight[p], shared->scales[p], shared->biases[p]};
     if (int rc = prepare_layer(L)) {
         delete L;
         return rc;
@@ -641,8 +685,12 @@ int64_t q38_moe_layer_bytes(const q38_moe_layer* L, int32_t n_unique, int32_t ro
         per_expert += static_cast<int64_t>(outd) * v.p[p].words * 4 + static_cast<int64_t>(outd) * v.p[p].ngrp * 2;
         books += (int64_t{1} << v.p[p].bits) * v.p[p].dim * 2;
     }
-    const int64_t experts = static_cast<int64_t>(n_unique) + (v.has_shared ? 1 : 0);
-    return experts * per_expert + books + static_cast<int64_t>(v.E) * v.H * 2 + (v.has_shared ? v.H * 2 : 0) +
+    const int64_t experts = static_cast<int64_t>(n_unique) + (v.has_shared && !v.shared_affine ? 1 : 0);
+    // an affine shared expert: 3 projections of sa_inter x H values, a scale and a bias per group
+    const int64_t sa = v.shared_affine ? 3 * (static_cast<int64_t>(v.sa_inter) * v.H * v.sa_bits / 8 +
+                                              static_cast<int64_t>(v.sa_inter) * v.H / v.sa_group * 4)
+                                       : 0;
+    return experts * per_expert + sa + books + static_cast<int64_t>(v.E) * v.H * 2 + (v.has_shared ? v.H * 2 : 0) +
            static_cast<int64_t>(2) * rows * v.H * 2;
 }
 
@@ -733,7 +781,7 @@ int q38_moe_route(q38_moe_layer* L, const uint16_t* x, int32_t rows, const q38_r
         if (int rc = route_prefill(L, w, rows, x, st, nullptr)) return rc;
     } else {
         Q38_HIP(launch_router(L->dev, w, rows, x, false, 0.0f, st));
-        Q38_HIP(launch_topk_plan(L->dev, w, rows, st));
+        Q38_HIP(launch_topk_plan(expert_view(L->dev), w, rows, st));
     }
     return copy_routes(L, rows, w, routes, st);
 }
@@ -744,7 +792,8 @@ int q38_moe_route(q38_moe_layer* L, const uint16_t* x, int32_t rows, const q38_r
 static int run_prefill(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* x, uint16_t* y,
                        const q38_route_out* trace, hipEvent_t* ev, hipStream_t st) {
     if (int rc = route_prefill(L, w, rows, x, st, ev)) return rc;
-    LayerDev one = L->dev;  // partial-sum planes of the prefill kernels
+    Q38_HIP(launch_shared_affine(L->dev, w, rows, st));
+    LayerDev one = expert_view(L->dev);  // partial-sum planes of the prefill kernels
     one.gu_parts = one.d_parts = prefill_planes(L->dev, rows);
     KernelTimer& kt = kernel_timer();
     if (ev) kt = {ev[6], ev[7]};
@@ -756,6 +805,7 @@ static int run_prefill(q38_moe_layer* L, const MoeBufs& w, int rows, const uint1
     if (ev) kt = {ev[10], ev[11]};
     Q38_HIP(launch_down_pf(one, w, rows, st));
     if (ev) kt = {ev[12], ev[13]};
+    one.has_shared = L->dev.has_shared;  // (the combine adds the shared expert, affine or not)
     Q38_HIP(launch_combine(one, w, rows, nullptr, y, st));
     kt = {};
     return Q38_OK;
@@ -769,21 +819,28 @@ static int run_prefill(q38_moe_layer* L, const MoeBufs& w, int rows, const uint1
 static int run_layer(q38_moe_layer* L, const MoeBufs& w, int rows, const uint16_t* src, bool norm, float eps,
                      uint16_t* h_chain, uint16_t* y, const q38_route_out* trace, hipEvent_t* ev, hipStream_t st) {
     const LayerDev dev = moe_call_dev(L->dev, rows);
+    const LayerDev ex = expert_view(dev);  // (without the shared slot when it is affine)
     if (ev) Q38_HIP(hipEventRecord(ev[0], st));
     Q38_HIP(launch_router(dev, w, rows, src, norm, eps, st));
-    if (!moe_plans_in_gate_up(dev, rows)) Q38_HIP(launch_topk_plan(dev, w, rows, st));
+    Q38_HIP(launch_shared_affine(dev, w, rows, st));
+    if (!moe_plans_in_gate_up(ex, rows)) Q38_HIP(launch_topk_plan(ex, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[1], st));
-    if (moe_uses_fused(dev, rows)) {  // gate/up, down and combine in one launch
-        Q38_HIP(launch_gate_down4(dev, w, rows, h_chain, h_chain ? nullptr : y, st));
+    if (moe_uses_fused(ex, rows)) {  // gate/up, down and combine in one launch
+        if (dev.shared_affine) {  // (the combine, with the affine shared rows, as its own kernel)
+            Q38_HIP(launch_gate_down4(ex, w, rows, nullptr, nullptr, st));
+            Q38_HIP(launch_combine(dev, w, rows, h_chain, y, st));
+        } else {
+            Q38_HIP(launch_gate_down4(ex, w, rows, h_chain, h_chain ? nullptr : y, st));
+        }
         if (ev)
             for (int i = 2; i <= 4; ++i) Q38_HIP(hipEventRecord(ev[i], st));
         return copy_routes(L, rows, w, trace, st);
     }
-    Q38_HIP(launch_gate_up(dev, w, rows, st));
+    Q38_HIP(launch_gate_up(ex, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[2], st));
     if (trace)
         if (int rc = copy_routes(L, rows, w, trace, st)) return rc;
-    Q38_HIP(launch_down(dev, w, rows, st));
+    Q38_HIP(launch_down(ex, w, rows, st));
     if (ev) Q38_HIP(hipEventRecord(ev[3], st));
     Q38_HIP(launch_combine(dev, w, rows, h_chain, y, st));
     if (ev) Q38_HIP(hipEventRecord(ev[4], st));
@@ -902,26 +959,31 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
         const q38_moe_layer* L = layers[l];
         const LayerDev dev = moe_call_dev(L->dev, rows);
         hipError_t e = hipSuccess;
+        const LayerDev ex = expert_view(dev);
         kt = {E[0], E[1]};
         e = launch_router(dev, w, rows, h, true, eps, st);
-        if (e == hipSuccess && !moe_plans_in_gate_up(dev, rows)) e = launch_topk_plan(dev, w, rows, st);
-        const bool fused = moe_uses_fused(dev, rows);  // (gate/up, down and combine in one launch)
+        if (e == hipSuccess) e = launch_shared_affine(dev, w, rows, st);
+        if (e == hipSuccess && !moe_plans_in_gate_up(ex, rows)) e = launch_topk_plan(ex, w, rows, st);
+        // (gate/up, down and combine in one launch; with an affine shared expert the combine is
+        // a kernel of its own)
+        const bool fused = moe_uses_fused(ex, rows), split_combine = !fused || dev.shared_affine;
         if (e == hipSuccess) {
             kt = {E[2], E[3]};
-            e = fused ? launch_gate_down4(dev, w, rows, h, nullptr, st) : launch_gate_up(dev, w, rows, st);
+            e = fused ? launch_gate_down4(ex, w, rows, dev.shared_affine ? nullptr : h, nullptr, st)
+                      : launch_gate_up(ex, w, rows, st);
         }
         if (e == hipSuccess && traces)
             if (copy_routes(L, rows, w, &traces[l], st) != Q38_OK) e = hipErrorUnknown;
         if (e == hipSuccess) {
-            if (fused) {  // down and combine ran in the gate/up launch (down_ms, merge_ms 0)
+            if (fused) {  // down (and the combine) ran in the gate/up launch (down_ms 0)
                 kt = {};
-                for (int i = 4; i < 8 && e == hipSuccess; ++i) e = hipEventRecord(E[i], st);
+                for (int i = 4; i < (split_combine ? 6 : 8) && e == hipSuccess; ++i) e = hipEventRecord(E[i], st);
             } else {
                 kt = {E[4], E[5]};
-                e = launch_down(dev, w, rows, st);
+                e = launch_down(ex, w, rows, st);
             }
         }
-        if (e == hipSuccess && !fused) {
+        if (e == hipSuccess && split_combine) {
             kt = {E[6], E[7]};
             e = launch_combine(dev, w, rows, h, nullptr, st);
         }
@@ -934,9 +996,12 @@ int q38_verify_chain_profiled(q38_moe_layer* const* layers, int32_t n_layers, ui
         for (int l = 0; l < n_layers && e == hipSuccess; ++l) {
             hipEvent_t* E = &ev[static_cast<size_t>(l) * 8];
             float ms[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            // (a fused layer's down and combine phases ran inside its gate/up kernel: 0)
-            const int phases = moe_uses_fused(moe_call_dev(layers[l]->dev, rows), rows) ? 2 : 4;
-            for (int i = 0; i < phases && e == hipSuccess; ++i) e = hipEventElapsedTime(&ms[i], E[2 * i], E[2 * i + 1]);
+            // (a fused layer's down and combine phases ran inside its gate/up kernel: 0; with an
+            // affine shared expert its combine is timed)
+            const LayerDev lv = moe_call_dev(layers[l]->dev, rows);
+            const bool fz = moe_uses_fused(expert_view(lv), rows);
+            for (int i = 0; i < 4 && e == hipSuccess; ++i)
+                if (!fz || i < 2 || (i == 3 && lv.shared_affine)) e = hipEventElapsedTime(&ms[i], E[2 * i], E[2 * i + 1]);
             t.routing_ms += ms[0];
             t.gate_up_ms += ms[1];
             t.down_ms += ms[2];
@@ -1591,10 +1656,12 @@ int q38_verify_chain_hc(q38_moe_layer* const* layers, q38_hc* const* mixers, int
         moe_ws(layers[l]->desc, rows, &w, ws);
         // the MoE layer on the block input; its combine writes the output into the streams
         const LayerDev dev = moe_call_dev(layers[l]->dev, rows);
+        const LayerDev ex = expert_view(dev);
         Q38_HIP(launch_router(dev, w, rows, mixed, false, 0.0f, st));
-        if (!moe_plans_in_gate_up(dev, rows)) Q38_HIP(launch_topk_plan(dev, w, rows, st));
-        Q38_HIP(launch_gate_up(dev, w, rows, st));
-        Q38_HIP(launch_down(dev, w, rows, st));
+        Q38_HIP(launch_shared_affine(dev, w, rows, st));
+        if (!moe_plans_in_gate_up(ex, rows)) Q38_HIP(launch_topk_plan(ex, w, rows, st));
+        Q38_HIP(launch_gate_up(ex, w, rows, st));
+        Q38_HIP(launch_down(ex, w, rows, st));
         Q38_HIP(launch_combine_hc(dev, w, rows, stream, inj, hd0.streams, st));
     }
     return Q38_OK;

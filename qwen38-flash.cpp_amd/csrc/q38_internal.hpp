@@ -92,6 +92,13 @@ struct MoeBufs {
     int wait_limit;
 };
 
+// A projection in MLX affine form: packed values, per-group scales and biases.
+struct AffineDev {
+    const uint32_t* w;  // [OUT][IN * bits / 32], value j of a word at bits j * bits
+    const uint16_t* s;  // [OUT][IN / group]
+    const uint16_t* b;  // [OUT][IN / group]
+};
+
 struct LayerDev {
     const uint16_t* router;  // [E, H] bf16
     const uint16_t* wsg;     // [H] bf16
@@ -108,7 +115,21 @@ struct LayerDev {
     // the router (which resets the planes that kernel waits on) and the expert launch agree:
     // 0 undecided (decided from the layer on each query), 1 fused, 2 not fused.
     int fused_mode;
+    // The shared expert in MLX affine form (shared_affine 1; the reference checkpoints'
+    // format): gate and up [sa_inter][H], down [H][sa_inter], sa_bits-bit values, one scale and
+    // bias per sa_group inputs, bf16 (sa_f16 0) or fp16. The expert kernels then take the layer
+    // without a shared slot (expert_view); the router (shared gate) and the combine keep it.
+    AffineDev sa[3];
+    int shared_affine, sa_bits, sa_group, sa_inter, sa_f16;
 };
+
+// The view of a layer the routed-expert kernels take: without the shared slot when the shared
+// expert is affine (its down rows come from launch_shared_affine).
+inline LayerDev expert_view(const LayerDev& L) {
+    LayerDev v = L;
+    if (L.shared_affine) v.has_shared = 0;
+    return v;
+}
 
 struct HeadDev {
     const int8_t* w;         // Q8: [V, H]; Q4: [V, H/2] packed nibbles
@@ -126,6 +147,13 @@ hipError_t launch_router(const LayerDev& L, const MoeBufs& B, int M, const uint1
                          hipStream_t st);
 hipError_t launch_topk_plan(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+// the grouped-scale (VALU) kernels of launch_gate_up / launch_down (q38_moe_grp.hip)
+hipError_t launch_gate_up_grouped(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+hipError_t launch_down_grouped(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+// The affine shared expert of the call's rows (q38_affine.hip): SwiGLU rows into B.h16, then
+// its down outputs into the shared rows of the down planes (plane 0; plane 1 cleared). Runs
+// after the router (it reads B.x) and before the combine; nothing without shared_affine.
+hipError_t launch_shared_affine(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 // chain: h <- h + y (in place); otherwise out <- y. Down rows are read at the route index.
 hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);

@@ -252,39 +252,14 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[r][i] = bf2f(hraw[r][i]);
         Q38_STAMPV(0, 1, v[0][0]);
-        float ss[MR];
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            ss[r] = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) ss[r] = fmaf(v[r][i], v[r][i], ss[r]);
-        }
-        Q38_STAMPV(0, 4, ss[MR - 1]);
-        if constexpr (MR == 1) {
-            ss[0] = wave_sum_xor(ss[0]);
-            if (lane == 0) red[0][wave] = ss[0];
-        } else {
-            wave_sum_xor_scatter<MR>(ss);
-#pragma unroll
-            for (int s = 0; s < scatter_slots<MR>(); ++s)
-                if (scatter_leader<MR>(lane)) red[scatter_value<MR>(s, lane >> 4)][wave] = ss[s];
-        }
-        Q38_STAMPV(0, 5, ss[MR - 1]);
+        norm_partials<NT, MR>(v, red);
         lds_barrier();
         Q38_STAMP(0, 6);
         // Lane r forms row r's total (wave totals in wave order) and 1 / rms, one chain for
         // all rows instead of MR chains in every lane (the phase is VALU-bound); the results
         // are read back from lanes 0..MR-1.
         float inv[MR];
-        {
-            const int rl = lane < MR ? lane : 0;
-            float t = 0.0f;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) t += red[rl][w];
-            const float il = 1.0f / sqrtf(t / static_cast<float>(H) + eps);
-#pragma unroll
-            for (int r = 0; r < MR; ++r) inv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(il), r));
-        }
+        norm_inv<NT, MR>(red, H, eps, inv);
 #pragma unroll
         for (int r = 0; r < MR; ++r)
             if (r < M) {
@@ -332,26 +307,7 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
     if (e >= nr) return;
     // all rows' products first (independent chains), then the butterflies
     float acc[MR];
-#pragma unroll
-    for (int r = 0; r < MR; ++r) {
-        acc[r] = 0.0f;
-        const int rr = r < M ? r : 0;
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(xs + static_cast<size_t>(rr) * H + 512 * t + 8 * lane);
-            const uint32_t xq[4] = {xv.x, xv.y, xv.z, xv.w};
-            const uint32_t wq[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                acc[r] = __builtin_fmaf(bflo(xq[k]), bflo(wq[k]), acc[r]);
-                acc[r] = __builtin_fmaf(bfhi(xq[k]), bfhi(wq[k]), acc[r]);
-            }
-        }
-    }
-    // the MR butterflies at once (MR > 1: 16-lane row q of acc[s] ends with request row
-    // scatter_value<MR>(s, q))
-    if constexpr (MR > 1) wave_sum_xor_scatter<MR>(acc);
-    else acc[0] = wave_sum_xor(acc[0]);
+    router_dots<T, MR>(xs, M, wv, acc);
 #pragma unroll
     for (int s = 0; s < scatter_slots<MR>(); ++s) {
         const int r = MR > 1 ? scatter_value<MR>(s, lane >> 4) : 0;
@@ -669,195 +625,6 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
     }
 }
 
-// ============================================================== grouped-scale path
-// Layers whose scales are per 64-input group (the reference checkpoint layout,
-// src/sparse_moe.cpp:641-647) take this path: VALU dot products with codebook reads
-// through the cache, per-group scaling in the lane. Same fp32 g/u/d outputs.
-template <int D>
-struct Vec;
-template <>
-struct Vec<8> {
-    // fp16 codebook, or INT8 codebook x one fp16 scale (value = q * scale, exact in float)
-    static __device__ __forceinline__ void load_book(const ProjDev& P, uint32_t code, float* v) {
-        if (P.book_i8) {
-            const uint2 b = *reinterpret_cast<const uint2*>(P.book_i8 + code * 8);
-            const uint32_t w[2] = {b.x, b.y};
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                v[i] = static_cast<float>(static_cast<int8_t>(w[i >> 2] >> (8 * (i & 3)))) * P.book_scale;
-            return;
-        }
-        const uint4 b = *reinterpret_cast<const uint4*>(P.book + code * 8);
-        const uint32_t w[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[2 * i] = h2f(static_cast<uint16_t>(w[i]));
-            v[2 * i + 1] = h2f(static_cast<uint16_t>(w[i] >> 16));
-        }
-    }
-};
-template <>
-struct Vec<4> {
-    static __device__ __forceinline__ void load_book(const ProjDev& P, uint32_t code, float* v) {
-        const uint2 b = *reinterpret_cast<const uint2*>(P.book + code * 4);
-        v[0] = h2f(static_cast<uint16_t>(b.x));
-        v[1] = h2f(static_cast<uint16_t>(b.x >> 16));
-        v[2] = h2f(static_cast<uint16_t>(b.y));
-        v[3] = h2f(static_cast<uint16_t>(b.y >> 16));
-    }
-};
-
-template <>
-struct Vec<2> {
-    // d2/K256: the byte codes of the reference checkpoint's first layers
-    static __device__ __forceinline__ void load_book(const ProjDev& P, uint32_t code, float* v) {
-        const uint32_t b = *reinterpret_cast<const uint32_t*>(P.book + code * 2);
-        v[0] = h2f(static_cast<uint16_t>(b));
-        v[1] = h2f(static_cast<uint16_t>(b >> 16));
-    }
-};
-
-constexpr int kGuRowsPerBlock = 64;
-constexpr int kDownRowsPerBlock = 128;
-
-// Staged input rows of the grouped kernels, fp16: row j, column c at fin_at(j, c, IN). Two
-// pad halves (one bank) after every 64 columns, so that the lanes of a row (16 codes each,
-// 64 or 128 columns apart) read different LDS banks instead of one. fp16 keeps 16 rows of
-// H = 2048 at 66.5 KiB, two workgroups per CU. (Inputs are bf16 values or SwiGLU outputs
-// rounded to bf16: fp16 holds them exactly in the normal range; the MFMA paths take the
-// same fp16 operand.)
-typedef _Float16 fin_t;
-__host__ __device__ constexpr int fin_stride(int IN) { return IN + 2 * (IN / 64); }
-constexpr size_t kFinLdsMax = 68 * 1024;  // 16 rows of H = 2048 (68,096 bytes)
-__device__ __forceinline__ int fin_at(int j, int c, int IN) { return j * fin_stride(IN) + c + 2 * (c / 64); }
-
-// Lane mapping: a lane owns 16 consecutive codes of a row (BITS/2 words); LPR lanes
-// (power of two, padded) cover one row; 64/LPR rows per wave. in_f: n rows staged at fin_at. Output row
-// pos0 + j, or its route index when rplan (the plan) is given (down projections).
-template <int D, int BITS, int LPR, int MAXN>
-__device__ __forceinline__ void grouped_rows(const ProjDev& P, int expert, int IN, int OUT, int o_base,
-                                             int rows_per_block, const fin_t* in_f, int n, float* out,
-                                             int pos0, int wave, int lane, const int32_t* rplan = nullptr,
-                                             int MK = 0) {
-    const int nsub = IN / D;
-    const int lanes_used = (nsub + 15) / 16;
-    const int sub_lane = lane % LPR;
-    const bool active = sub_lane < lanes_used;
-    const int s0 = sub_lane * 16;
-    const int spg = IN / P.ngrp / D;
-    const bool row_scale = P.ngrp == 1;
-    constexpr int WPL = BITS / 2;
-    constexpr int RPW = 64 / LPR;
-    for (int it = 0; it < rows_per_block / (4 * RPW); ++it) {
-        const int o = o_base + it * 4 * RPW + wave * RPW + lane / LPR;
-        float acc[MAXN];
-#pragma unroll
-        for (int j = 0; j < MAXN; ++j) acc[j] = 0.0f;
-        if (active && o < OUT) {
-            const size_t rowi = static_cast<size_t>(expert) * OUT + o;
-            const uint32_t* pw = P.codes + rowi * P.words + (s0 / 32) * BITS + ((s0 % 32) / 16) * WPL;
-            uint32_t wr[WPL + 1];
-#pragma unroll
-            for (int i = 0; i < WPL; ++i) wr[i] = pw[i];
-            wr[WPL] = 0;
-            float pp[MAXN];
-#pragma unroll
-            for (int j = 0; j < MAXN; ++j) pp[j] = 0.0f;
-#pragma unroll
-            for (int qq = 0; qq < 16; ++qq) {
-                const int s = s0 + qq;
-                const uint32_t c = code_from<BITS>(wr, qq);
-                float bk[D];
-                Vec<D>::load_book(P, c, bk);
-#pragma unroll
-                for (int j = 0; j < MAXN; ++j)
-                    if (j < n)
-#pragma unroll
-                        for (int dd = 0; dd < D; ++dd) pp[j] = fmaf(static_cast<float>(in_f[fin_at(j, s * D + dd, IN)]), bk[dd], pp[j]);
-                // a group ends here, or the lane's span ends inside a group of more than 16 codes
-                if (!row_scale && (((s + 1) % spg) == 0 || qq == 15)) {
-                    const float sc = h2f(P.scales[rowi * P.ngrp + s / spg]);
-#pragma unroll
-                    for (int j = 0; j < MAXN; ++j) {
-                        acc[j] = fmaf(sc, pp[j], acc[j]);
-                        pp[j] = 0.0f;
-                    }
-                }
-            }
-            if (row_scale) {
-#pragma unroll
-                for (int j = 0; j < MAXN; ++j) acc[j] = pp[j];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < MAXN; ++j) acc[j] = group_sum_xor<LPR>(acc[j]);
-        if (sub_lane == 0 && o < OUT) {
-            const float sc = row_scale ? h2f(P.scales[static_cast<size_t>(expert) * OUT + o]) : 1.0f;
-#pragma unroll
-            for (int j = 0; j < MAXN; ++j)
-                if (j < n) out[static_cast<size_t>(rplan ? route_of_pos(rplan, MK, pos0 + j) : pos0 + j) * OUT + o] = acc[j] * sc;
-        }
-    }
-}
-
-// grouped_rows for a slot of n routes, with the route loop sized for n (1, 2, 4 or up to
-// kMaxRows) rather than always unrolled to kMaxRows with a guard per route (most slots of
-// a 16-row call have one or two routes).
-template <int D, int BITS, int LPR>
-__device__ __forceinline__ void grouped_rows_n(const ProjDev& P, int expert, int IN, int OUT, int o_base,
-                                               int rows_per_block, const fin_t* in_f, int n, float* out, int pos0,
-                                               int wave, int lane, const int32_t* rplan = nullptr, int MK = 0) {
-    if (n <= 1)
-        grouped_rows<D, BITS, LPR, 1>(P, expert, IN, OUT, o_base, rows_per_block, in_f, n, out, pos0, wave, lane, rplan, MK);
-    else if (n <= 2)
-        grouped_rows<D, BITS, LPR, 2>(P, expert, IN, OUT, o_base, rows_per_block, in_f, n, out, pos0, wave, lane, rplan, MK);
-    else if (n <= 4)
-        grouped_rows<D, BITS, LPR, 4>(P, expert, IN, OUT, o_base, rows_per_block, in_f, n, out, pos0, wave, lane, rplan, MK);
-    else
-        grouped_rows<D, BITS, LPR, kMaxRows>(P, expert, IN, OUT, o_base, rows_per_block, in_f, n, out, pos0, wave, lane,
-                                             rplan, MK);
-}
-
-template <int D, int BITS, int LPR>
-__global__ __launch_bounds__(256) void k_gu_grouped(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) fin_t fin[];  // n rows of H, at fin_at
-    int expert, n, pos0;
-    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
-    const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
-    const int H = L.H, I = L.I;
-    for (int i = threadIdx.x; i < n * H; i += 256) {
-        const int j = i / H, c = i % H;
-        fin[fin_at(j, c, H)] = static_cast<fin_t>(bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]));
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int o_base = blockIdx.x * kGuRowsPerBlock;
-    grouped_rows_n<D, BITS, LPR>(L.p[0], expert, H, I, o_base, kGuRowsPerBlock, fin, n, B.g, pos0, wave, lane);
-    grouped_rows_n<D, BITS, LPR>(L.p[1], expert, H, I, o_base, kGuRowsPerBlock, fin, n, B.u, pos0, wave, lane);
-}
-
-template <int D, int BITS, int LPR>
-__global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int M) {
-    extern __shared__ __align__(16) fin_t fin[];  // n rows of I, at fin_at
-    int expert, n, pos0;
-    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
-    const int H = L.H, I = L.I;
-    for (int i = threadIdx.x; i < n * I; i += 256) {
-        const size_t at = static_cast<size_t>(pos0) * I + i;
-        float g = B.g[at], u = B.u[at];
-        if (L.gu_parts == 2) {
-            g += B.g[B.gu_plane + at];
-            u += B.u[B.gu_plane + at];
-        }
-        fin[fin_at(i / I, i % I, I)] = static_cast<fin_t>(swiglu(g, u));
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    grouped_rows_n<D, BITS, LPR>(L.p[2], expert, I, H, blockIdx.x * kDownRowsPerBlock, kDownRowsPerBlock,
-                                         fin, n, B.d, pos0, wave, lane, B.plan, M * L.K);
-}
-
-
 // ============================================================== combine (R8, R10, R11)
 // One thread per (row, column): routed = T(sum_slot w_slot * T(d_slot)) in slot order,
 // shared = T(T(d_shared) * gate), y = T(routed + shared); chain mode adds the residual in
@@ -994,11 +761,6 @@ __global__ void k_tile_codes(const uint32_t* __restrict__ codes, int64_t n_tiles
 
 // ============================================================== launchers
 namespace {
-int next_pow2(int v) {
-    int p = 1;
-    while (p < v) p <<= 1;
-    return p;
-}
 int g_mfma_grid = 256;  // one persistent workgroup per CU (set from the device at first use)
 
 void init_grid() {
@@ -1052,19 +814,6 @@ hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStr
     return launch(k_down_mfma<BITS, NSUB, NCHUNK, PAR>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
 
-template <int D, int BITS, int LPR>
-hipError_t launch_gu_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = static_cast<size_t>(M) * fin_stride(L.H) * sizeof(fin_t);
-    if (lds > kFinLdsMax) return hipErrorInvalidValue;
-    if (const hipError_t e = ensure_lds<k_gu_grouped<D, BITS, LPR>>(kFinLdsMax); e != hipSuccess) return e;
-    return launch(k_gu_grouped<D, BITS, LPR>, dim3(L.I / kGuRowsPerBlock, M * L.K + 1), dim3(256), lds, st, L, B, M);
-}
-template <int D, int BITS, int LPR>
-hipError_t launch_down_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = static_cast<size_t>(M) * fin_stride(L.I) * sizeof(fin_t);
-    return launch(k_down_grouped<D, BITS, LPR>, dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256), lds, st, L, B,
-                  M);
-}
 } // namespace
 
 // Mixed layers run their two banks on the MFMA kernels: H = 2048, I = 512, per-row scales,
@@ -1138,7 +887,7 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
     }
     if (moe_uses_fused(L, M)) return launch_gate_down4(L, B, M, nullptr, nullptr, st);
     if (moe_uses_narrow(L, M)) return launch_gate_up4(L, B, M, st);
-    const int D = L.p[0].dim, BT = L.p[0].bits;
+    const int D = L.p[0].dim;
     if (moe_uses_mfma(L)) {
         const int nsub = L.H / D;
         if (D == 8 && nsub == 256) return launch_gu_mfma_g<14, 256, 2>(L, B, M, st);
@@ -1146,23 +895,7 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
         if (D == 4 && nsub == 512) return launch_gu_mfma_g<8, 512, 1>(L, B, M, st);
         return hipErrorInvalidValue;
     }
-    const int lpr = next_pow2((L.H / D + 15) / 16);
-    if (D == 8 && BT == 14) {
-        if (lpr == 16) return launch_gu_grouped_g<8, 14, 16>(L, B, M, st);
-        if (lpr == 32) return launch_gu_grouped_g<8, 14, 32>(L, B, M, st);
-        if (lpr == 8) return launch_gu_grouped_g<8, 14, 8>(L, B, M, st);
-        if (lpr <= 4) return launch_gu_grouped_g<8, 14, 4>(L, B, M, st);
-    } else if (D == 4 && BT == 8) {
-        if (lpr == 32) return launch_gu_grouped_g<4, 8, 32>(L, B, M, st);
-        if (lpr == 64) return launch_gu_grouped_g<4, 8, 64>(L, B, M, st);
-        if (lpr == 16) return launch_gu_grouped_g<4, 8, 16>(L, B, M, st);
-        if (lpr <= 8) return launch_gu_grouped_g<4, 8, 8>(L, B, M, st);
-    } else if (D == 2 && BT == 8) {
-        if (lpr == 64) return launch_gu_grouped_g<2, 8, 64>(L, B, M, st);
-        if (lpr == 32) return launch_gu_grouped_g<2, 8, 32>(L, B, M, st);
-        if (lpr <= 16) return launch_gu_grouped_g<2, 8, 16>(L, B, M, st);
-    }
-    return hipErrorInvalidValue;
+    return launch_gate_up_grouped(L, B, M, st);
 }
 
 hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
@@ -1175,29 +908,14 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
     }
     if (moe_uses_fused(L, M)) return hipSuccess;  // (the fused gate/up launch ran the down half)
     if (moe_uses_narrow(L, M)) return launch_down4(L, B, M, st);
-    const int D = L.p[2].dim, BT = L.p[2].bits;
+    const int D = L.p[2].dim;
     if (moe_uses_mfma(L)) {
         const int nsub = L.I / D;
         if (D == 8 && nsub == 64) return launch_down_mfma_g<14, 64, 2>(L, B, M, st);
         if (D == 4 && nsub == 128) return launch_down_mfma_g<8, 128, 1>(L, B, M, st);
         return hipErrorInvalidValue;
     }
-    const int lpr = next_pow2((L.I / D + 15) / 16);
-    if (D == 8 && BT == 14) {
-        if (lpr == 4) return launch_down_grouped_g<8, 14, 4>(L, B, M, st);
-        if (lpr == 8) return launch_down_grouped_g<8, 14, 8>(L, B, M, st);
-        if (lpr <= 2) return launch_down_grouped_g<8, 14, 2>(L, B, M, st);
-    } else if (D == 4 && BT == 8) {
-        if (lpr == 8) return launch_down_grouped_g<4, 8, 8>(L, B, M, st);
-        if (lpr == 16) return launch_down_grouped_g<4, 8, 16>(L, B, M, st);
-        if (lpr == 4) return launch_down_grouped_g<4, 8, 4>(L, B, M, st);
-        if (lpr <= 2) return launch_down_grouped_g<4, 8, 2>(L, B, M, st);
-    } else if (D == 2 && BT == 8) {
-        if (lpr == 16) return launch_down_grouped_g<2, 8, 16>(L, B, M, st);
-        if (lpr == 32) return launch_down_grouped_g<2, 8, 32>(L, B, M, st);
-        if (lpr <= 8) return launch_down_grouped_g<2, 8, 8>(L, B, M, st);
-    }
-    return hipErrorInvalidValue;
+    return launch_down_grouped(L, B, M, st);
 }
 
 template <int KT>

@@ -235,7 +235,9 @@ __device__ __forceinline__ void gu4_body(const LayerDev& L, const MoeBufs& B, in
     //    before it waits for LDS writes only, the one after it for every wave's copy too.
     lds_barrier_dma_pending();
     if (wave == 0) plan_wave(M, K, ex, plan, slot_pos);
+    Q38_STAMP(8192, 14);
     wait_vm_all();
+    Q38_STAMP_T(8192, 15, 64 * M);
     lds_barrier();
     asm volatile("" ::"v"(warm));
     Q38_STAMP(8192, 4);
@@ -644,6 +646,7 @@ template <int KT>
 __device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B, int M, const float* wt, uint16_t* h,
                                              uint16_t* out) {
     const int w = static_cast<int>(blockIdx.x) - static_cast<int>(gridDim.x - kCombineWgs);
+    Q38_STAMP(24576, 0);
     const int H = L.H, MK = M * KT;
     const int per = (M * H + kCombineWgs - 1) / kCombineWgs;  // (<= 512: M <= 4, H = 2048)
     const int p = w * per + static_cast<int>(threadIdx.x);
@@ -670,15 +673,18 @@ __device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B
         return q;
     };
     load();
+    Q38_STAMPV(24576, 1, in.dv[0][0]);
     for (int spin = 0; pending() && spin < B.wait_limit; ++spin) {
         __builtin_amdgcn_s_sleep(2);
         load();
     }
     if (pending()) wait_gave_up();
+    Q38_STAMPV(24576, 2, in.dv[0][0]);
     const float y = combine_value<KT, true>(L, in);
     const size_t i = static_cast<size_t>(r) * H + o;
     if (h) h[i] = f2bf(rbf(bf2f(hraw) + y));
     else out[i] = f2bf(y);
+    Q38_STAMP(24576, 3);
 }
 
 // G8: per-row scales (0) or one scale per 64 inputs in both projections (8, the checkpoint
@@ -699,6 +705,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     lds_barrier();  // every wave is done with the gate/up codebook chunk
     dn4_body<BITS, NSUB_DN, NCHUNK, DD, G8, true>(L, B, M, lds, plan, hs, fill);
     if (h || out) combine_tail<KT>(L, B, M, wt, h, out);
+    Q38_STAMP(24576, 4);
 }
 
 template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>

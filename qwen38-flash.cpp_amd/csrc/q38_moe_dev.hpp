@@ -25,7 +25,16 @@ extern __device__ unsigned long long g_trace[32768];
         asm volatile("" ::"v"(v));      \
         Q38_STAMP(base, i);             \
     } while (0)
+#define Q38_STAMP_T(base, i, t)                                                                               \
+    do {                                                                                                      \
+        if (static_cast<int>(threadIdx.x) == (t))                                                             \
+            ::q38::g_trace[(base) + 16 * (blockIdx.y * gridDim.x + blockIdx.x) + (i)] =                       \
+                __builtin_amdgcn_s_memrealtime();                                                             \
+    } while (0)
 #else
+#define Q38_STAMP_T(base, i, t) \
+    do {                        \
+    } while (0)
 #define Q38_STAMP(base, i) \
     do {                   \
     } while (0)
@@ -547,6 +556,72 @@ __device__ __forceinline__ void fill_book(const uint16_t* src4, unsigned char* l
         for (int k = 0; k < G; ++k) dst[i + k * nthreads] = v[k];
     }
     for (; i < N; i += nthreads) dst[i] = src[i];
+}
+
+// ============================================================== router rows (R1) + layer-input RMSNorm
+// The arithmetic contracts of the router, shared by the router kernel (k_route_norm) and the
+// one-launch layer kernel (k_gd4 with its router) so that the two give the same bits. A
+// workgroup of NT = H / 4 threads forms the norm: thread t owns columns t + NT i (i < 4) of
+// every row and accumulates fmaf(v, v) in i order; the wave xor-butterfly totals (MR > 1:
+// reduced and scattered together) go to red[MR][NT / 64]; after a barrier, lane r of every
+// wave adds row r's wave totals in wave order and forms inv_rms = 1 / sqrt(total / H + eps),
+// which every lane reads back.
+template <int NT, int MR>
+__device__ __forceinline__ void norm_partials(const float (&v)[MR][4], float (*red)[NT / 64]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float ss[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        ss[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss[r] = fmaf(v[r][i], v[r][i], ss[r]);
+    }
+    if constexpr (MR == 1) {
+        ss[0] = wave_sum_xor(ss[0]);
+        if (lane == 0) red[0][wave] = ss[0];
+    } else {
+        wave_sum_xor_scatter<MR>(ss);
+#pragma unroll
+        for (int s = 0; s < scatter_slots<MR>(); ++s)
+            if (scatter_leader<MR>(lane)) red[scatter_value<MR>(s, lane >> 4)][wave] = ss[s];
+    }
+}
+template <int NT, int MR>
+__device__ __forceinline__ void norm_inv(const float (*red)[NT / 64], int H, float eps, float (&inv)[MR]) {
+    const int lane = threadIdx.x & 63;
+    const int rl = lane < MR ? lane : 0;
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) t += red[rl][w];
+    const float il = 1.0f / sqrtf(t / static_cast<float>(H) + eps);
+#pragma unroll
+    for (int r = 0; r < MR; ++r) inv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(il), r));
+}
+// Router logit contract: lane l holds the columns c = 512 t + 8 l + j of a router row (t < T
+// outer, j < 8 inner) and accumulates x * w with fmaf for each of the MR request rows (rows
+// past M repeat row 0); then the MR butterflies at once (reduced and scattered for MR > 1:
+// 16-lane row q of acc[s] ends with request row scatter_value<MR>(s, q)). xs: [M][512 T] bf16.
+template <int T, int MR>
+__device__ __forceinline__ void router_dots(const uint16_t* xs, int M, const uint4 (&wv)[T], float (&acc)[MR]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        acc[r] = 0.0f;
+        const int rr = r < M ? r : 0;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(xs + static_cast<size_t>(rr) * 512 * T + 512 * t + 8 * lane);
+            const uint32_t xq[4] = {xv.x, xv.y, xv.z, xv.w};
+            const uint32_t wq[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                acc[r] = __builtin_fmaf(bflo(xq[k]), bflo(wq[k]), acc[r]);
+                acc[r] = __builtin_fmaf(bfhi(xq[k]), bfhi(wq[k]), acc[r]);
+            }
+        }
+    }
+    if constexpr (MR > 1) wave_sum_xor_scatter<MR>(acc);
+    else acc[0] = wave_sum_xor(acc[0]);
 }
 
 // SwiGLU with the reference's rounding points (src/vq_metal_kernels.hpp:589-595):

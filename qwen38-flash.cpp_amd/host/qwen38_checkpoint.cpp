@@ -256,9 +256,31 @@ ModelManifest ModelManifest::parse(std::string_view config_json) {
     m.expert_count_ = cfg.at("num_experts").as_size("num_experts");
     m.experts_per_token_ = cfg.at("num_experts_per_tok").as_size("num_experts_per_tok");
     if (const Json* n = cfg.find("norm_topk_prob")) m.normalize_ = n->as_bool();
+    if (const Json* n = cfg.find("shared_expert_intermediate_size"))
+        m.shared_inter_ = n->as_size("shared_expert_intermediate_size");
+    // quantization metadata (src/model_manifest.cpp:188-208): model-wide bits and group_size,
+    // and per-module objects {bits, group_size} with bits 2..8.
+    const Json* quantization = root.find("quantization");
+    if (!quantization) quantization = root.find("quantization_config");
+    if (quantization) {
+        m.has_quantization_ = true;
+        m.quantization_.bits = quantization->at("bits").as_size("quantization.bits");
+        m.quantization_.group_size = quantization->at("group_size").as_size("quantization.group_size");
+        for (const auto& [module, value] : quantization->as_object()) {
+            if (!value.is_object()) continue;
+            const Json* bits = value.find("bits");
+            const Json* group = value.find("group_size");
+            if (!bits || !group) continue;
+            const QuantizationSpec spec{bits->as_size("quantization override bits"),
+                                        group->as_size("quantization override group_size")};
+            if (spec.bits < 2 || spec.bits > 8 || spec.group_size == 0)
+                throw std::runtime_error("invalid quantization override for " + module);
+            m.quantization_overrides_.emplace(module, spec);
+        }
+    }
     // vq_modules (src/model_manifest.cpp:210-230): every module must describe the model's
-    // expert count (shared-expert modules describe 1), a non-empty geometry whose input
-    // splits into whole vectors and scale groups, and packed codes of at most 31 bits.
+    // expert count, a non-empty geometry whose input splits into whole vectors and scale
+    // groups, and packed codes of at most 31 bits.
     if (const Json* modules = root.find("vq_modules")) {
         for (const auto& [module, value] : modules->as_object()) {
             VectorQuantizationSpec s;
@@ -270,8 +292,7 @@ ModelManifest ModelManifest::parse(std::string_view config_json) {
             s.group_size = value.at("group").as_size("vq_modules.group");
             if (const Json* pb = value.find("pack_bits"); pb && !pb->is_null())  // absent / null: byte codes
                 s.packed_bits = pb->as_size("vq_modules.pack_bits");
-            const bool shared_module = module.find(".shared_expert.") != std::string::npos;
-            if ((s.expert_count != m.expert_count_ && !(shared_module && s.expert_count == 1)) ||
+            if (s.expert_count != m.expert_count_ ||
                 s.output_dimension == 0 || s.input_dimension == 0 || s.codebook_size < 2 ||
                 s.vector_dimension == 0 || s.group_size == 0 || s.input_dimension % s.vector_dimension != 0 ||
                 s.input_dimension % s.group_size != 0 || (s.packed_bits != 0 && s.packed_bits > 31))
@@ -282,9 +303,26 @@ ModelManifest ModelManifest::parse(std::string_view config_json) {
     return m;
 }
 
+namespace {
+constexpr std::string_view kWrapper = "language_model.";
+// The name without the "language_model." wrapper, or empty when it has none.
+std::string_view flat_name(std::string_view name) {
+    return name.substr(0, kWrapper.size()) == kWrapper ? name.substr(kWrapper.size()) : std::string_view{};
+}
+} // namespace
+
 const VectorQuantizationSpec* ModelManifest::vector_quantization_for(std::string_view module) const {
-    const auto it = vq_.find(module);
+    auto it = vq_.find(module);
+    if (it == vq_.end() && !flat_name(module).empty()) it = vq_.find(flat_name(module));
     return it == vq_.end() ? nullptr : &it->second;
+}
+
+QuantizationSpec ModelManifest::quantization_for(std::string_view module) const {
+    if (!has_quantization_) throw std::runtime_error("model is missing quantization metadata");
+    auto it = quantization_overrides_.find(module);
+    if (it == quantization_overrides_.end() && !flat_name(module).empty())
+        it = quantization_overrides_.find(flat_name(module));
+    return it == quantization_overrides_.end() ? quantization_ : it->second;
 }
 
 // ------------------------------------------------------------------ safetensors
@@ -375,12 +413,53 @@ TensorStore::TensorStore(const std::string& directory) : manifest_(ModelManifest
 }
 TensorStore::~TensorStore() = default;
 
-bool TensorStore::has(std::string_view name) const { return tensors_.find(name) != tensors_.end(); }
+bool TensorStore::has(std::string_view name) const {
+    return tensors_.find(name) != tensors_.end() ||
+           (!flat_name(name).empty() && tensors_.find(flat_name(name)) != tensors_.end());
+}
 
 const TensorView& TensorStore::tensor(std::string_view name) const {
-    const auto it = tensors_.find(name);
+    auto it = tensors_.find(name);
+    if (it == tensors_.end() && !flat_name(name).empty()) it = tensors_.find(flat_name(name));
     if (it == tensors_.end()) throw std::runtime_error("missing tensor " + std::string(name));
     return it->second;
+}
+
+// ------------------------------------------------------------------ affine projections
+// infer_affine_quantization_bits (src/quantization_geometry.cpp:9-35) on the last dimensions.
+static std::size_t infer_affine_bits(const TensorView& weight, const TensorView& scales, std::size_t group,
+                                     const std::string& label) {
+    if (weight.shape.empty() || weight.shape.size() != scales.shape.size() || weight.shape.back() <= 0 ||
+        scales.shape.back() <= 0 || group == 0)
+        throw std::runtime_error("cannot infer " + label + " quantization geometry");
+    const auto packed = static_cast<std::size_t>(weight.shape.back());
+    const auto width = static_cast<std::size_t>(scales.shape.back()) * group;
+    if (width == 0 || packed * 32 % width != 0) throw std::runtime_error("non-integral " + label + " quantization bits");
+    const std::size_t bits = packed * 32 / width;
+    if (bits != 2 && bits != 3 && bits != 4 && bits != 5 && bits != 6 && bits != 8)
+        throw std::runtime_error(label + " projections must use affine Q2, Q3, Q4, Q5, Q6, or Q8");
+    return bits;
+}
+
+AffineProjectionTensors load_affine_projection(const TensorStore& store, std::string_view name) {
+    const std::string base(name);
+    AffineProjectionTensors p;
+    p.weight = &store.tensor(base + ".weight");
+    p.scales = &store.tensor(base + ".scales");
+    p.biases = &store.tensor(base + ".biases");
+    const QuantizationSpec q = store.manifest().quantization_for(base);
+    p.group_size = q.group_size;
+    p.bits = infer_affine_bits(*p.weight, *p.scales, q.group_size, "MoE");
+    // (src/sparse_moe.cpp:668-671; MTP-head modules may differ from the metadata)
+    if (p.bits != q.bits && base.find("language_model.mtp.") != 0)
+        throw std::runtime_error("MoE tensor disagrees with quantization metadata for " + base);
+    if (p.weight->dtype != "U32" || p.weight->shape.size() != 2 || p.scales->shape != p.biases->shape ||
+        p.scales->shape.size() != 2 || p.scales->shape[0] != p.weight->shape[0] ||
+        (p.scales->dtype != "BF16" && p.scales->dtype != "F16") || p.biases->dtype != p.scales->dtype)
+        throw std::runtime_error("invalid affine quantization tensors for " + base);
+    p.out = static_cast<std::size_t>(p.weight->shape[0]);
+    p.in = static_cast<std::size_t>(p.scales->shape[1]) * p.group_size;
+    return p;
 }
 
 // ------------------------------------------------------------------ VQ projections
@@ -443,13 +522,39 @@ q38_moe_desc checkpoint_layer_desc(const TensorStore& store, std::string_view pr
     desc.gu_group = static_cast<int32_t>(g.spec.group_size);
     desc.down_group = static_cast<int32_t>(d.spec.group_size);
     desc.normalize_topk = normalize ? 1 : 0;
-    const bool vq_shared = store.manifest().vector_quantization_for(pre + ".shared_expert.gate_proj") != nullptr;
-    const bool any_shared = vq_shared || store.has(pre + ".shared_expert_gate.weight") ||
+    // The shared expert: SparseMoe::forward_shared applies it with quantized_matmul, so the
+    // reference reads it in MLX affine form only (the VQ branch of load_projection would need a
+    // vq_modules entry for all routed experts).
+    if (store.manifest().vector_quantization_for(pre + ".shared_expert.gate_proj"))
+        throw std::runtime_error("shared expert of " + pre + " is VQ-coded; shared experts load in affine form");
+    const bool any_shared = store.has(pre + ".shared_expert_gate.weight") ||
                             store.has(pre + ".shared_expert.gate_proj.weight");
-    if (any_shared && !vq_shared)
-        throw std::runtime_error("shared expert of " + pre + " is not VQ-coded (only VQ shared experts load)");
-    desc.has_shared = vq_shared ? 1 : 0;
+    if (any_shared) (void)checkpoint_shared_expert(store, pre, g.spec.input_dimension);  // (its checks)
+    desc.has_shared = any_shared ? 1 : 0;
     return desc;
+}
+
+SharedExpertTensors checkpoint_shared_expert(const TensorStore& store, std::string_view prefix, std::size_t hidden) {
+    const std::string pre(prefix);
+    SharedExpertTensors s;
+    const char* names[3] = {".gate_proj", ".up_proj", ".down_proj"};
+    for (int p = 0; p < 3; ++p) s.proj[p] = load_affine_projection(store, pre + ".shared_expert" + names[p]);
+    const std::size_t Is = s.proj[0].out;
+    if (s.proj[0].in != hidden || s.proj[1].in != hidden || s.proj[1].out != Is || s.proj[2].in != Is ||
+        s.proj[2].out != hidden)
+        throw std::runtime_error("shared expert of " + pre + ": gate/up [inter, hidden] and down [hidden, inter]");
+    for (int p = 1; p < 3; ++p)
+        if (s.proj[p].bits != s.proj[0].bits || s.proj[p].group_size != s.proj[0].group_size ||
+            s.proj[p].scales->dtype != s.proj[0].scales->dtype)
+            throw std::runtime_error("shared expert of " + pre + ": the device kernels take one bits, group size "
+                                     "and scale dtype for its three projections");
+    const std::size_t cfg = store.manifest().shared_expert_intermediate_size();
+    if (cfg != 0 && cfg != Is)
+        throw std::runtime_error("shared expert of " + pre + " disagrees with shared_expert_intermediate_size");
+    s.gate = &store.tensor(pre + ".shared_expert_gate.weight");
+    if (s.gate->dtype != "BF16" || s.gate->nbytes != hidden * 2)
+        throw std::runtime_error("shared expert gate of " + pre + " must be BF16 [1, hidden]");
+    return s;
 }
 
 } // namespace qwen38
@@ -501,42 +606,40 @@ extern "C" int q38_moe_layer_load(q38_ctx* ctx, const char* checkpoint, const ch
                                                        store.manifest().normalize_topk_probability());
         d.book_format = book_format;
         const char* names[3] = {".gate_proj", ".up_proj", ".down_proj"};
-        qwen38::VqProjectionTensors routed[3], shared[3];
-        for (int p = 0; p < 3; ++p) {
-            routed[p] = qwen38::load_vq_projection(store, pre + ".switch_mlp" + names[p]);
-            if (d.has_shared) {
-                shared[p] = qwen38::load_vq_projection(store, pre + ".shared_expert" + names[p]);
-                const auto& a = routed[p].spec;
-                const auto& b = shared[p].spec;
-                if (b.expert_count != 1 || a.input_dimension != b.input_dimension ||
-                    a.output_dimension != b.output_dimension || a.vector_dimension != b.vector_dimension ||
-                    a.packed_bits != b.packed_bits || a.group_size != b.group_size ||
-                    routed[p].codebook->nbytes != shared[p].codebook->nbytes ||
-                    std::memcmp(routed[p].codebook->data, shared[p].codebook->data, shared[p].codebook->nbytes) != 0)
-                    throw std::runtime_error("shared expert of " + pre +
-                                             " must use the routed projection's geometry and codebook");
-            }
-        }
-        const int E = d.experts, rowsE = E + (d.has_shared ? 1 : 0);
+        qwen38::VqProjectionTensors routed[3];
+        for (int p = 0; p < 3; ++p) routed[p] = qwen38::load_vq_projection(store, pre + ".switch_mlp" + names[p]);
+        qwen38::SharedExpertTensors shared;
+        if (d.has_shared) shared = qwen38::checkpoint_shared_expert(store, pre, static_cast<std::size_t>(d.hidden));
+        const int E = d.experts;
         const int dims[3] = {d.gu_dim, d.gu_dim, d.down_dim}, bits[3] = {d.gu_bits, d.gu_bits, d.down_bits};
         const int ins[3] = {d.hidden, d.hidden, d.inter}, outs[3] = {d.inter, d.inter, d.hidden};
         const int grps[3] = {d.gu_group, d.gu_group, d.down_group};
-        // one device block: router, shared gate, then per projection codes, scales, book
+        // one device block: router, shared gate, per projection codes, scales, book, then the
+        // affine shared expert's weights, scales and biases
         auto a256 = [](std::size_t v) { return (v + 255) / 256 * 256; };
         std::size_t off = 0, o_router = off;
         off += a256(static_cast<std::size_t>(E) * d.hidden * 2);
         const std::size_t o_wsg = off;
         off += a256(static_cast<std::size_t>(d.hidden) * 2);
-        std::size_t o_codes[3], o_scales[3], o_book[3], words[3];
+        std::size_t o_codes[3], o_scales[3], o_book[3], words[3], o_sw[3] = {}, o_ss[3] = {}, o_sb[3] = {};
         for (int p = 0; p < 3; ++p) {
             words[p] = static_cast<std::size_t>(((ins[p] / dims[p] + 31) / 32) * bits[p]);
             o_codes[p] = off;
-            off += a256(static_cast<std::size_t>(rowsE) * outs[p] * words[p] * 4);
+            off += a256(static_cast<std::size_t>(E) * outs[p] * words[p] * 4);
             o_scales[p] = off;
-            off += a256(static_cast<std::size_t>(rowsE) * outs[p] * (ins[p] / grps[p]) * 2);
+            off += a256(static_cast<std::size_t>(E) * outs[p] * (ins[p] / grps[p]) * 2);
             o_book[p] = off;
             off += a256((std::size_t{1} << bits[p]) * dims[p] * 2);
         }
+        if (d.has_shared)
+            for (int p = 0; p < 3; ++p) {
+                o_sw[p] = off;
+                off += a256(shared.proj[p].weight->nbytes);
+                o_ss[p] = off;
+                off += a256(shared.proj[p].scales->nbytes);
+                o_sb[p] = off;
+                off += a256(shared.proj[p].biases->nbytes);
+            }
         char* base = nullptr;
         if (hipMalloc(&base, off) != hipSuccess) return ck_fail(Q38_ENOMEM, "hipMalloc failed for checkpoint tensors");
         auto up = [&](std::size_t o, const void* src, std::size_t n) {
@@ -546,36 +649,45 @@ extern "C" int q38_moe_layer_load(q38_ctx* ctx, const char* checkpoint, const ch
         try {
             if (hipMemset(base, 0, off) != hipSuccess) throw std::runtime_error("clearing checkpoint tensors failed");
             up(o_router, store.tensor(pre + ".gate.weight").data, static_cast<std::size_t>(E) * d.hidden * 2);
-            if (d.has_shared) {
-                const qwen38::TensorView& sg = store.tensor(pre + ".shared_expert_gate.weight");
-                if (sg.dtype != "BF16" || sg.nbytes != static_cast<std::size_t>(d.hidden) * 2)
-                    throw std::runtime_error("shared expert gate of " + pre + " must be BF16 [1, hidden]");
-                up(o_wsg, sg.data, sg.nbytes);
-            }
             for (int p = 0; p < 3; ++p) {
                 const std::int64_t rows = static_cast<std::int64_t>(E) * outs[p];
                 const std::vector<std::uint32_t> c = packed_codes(routed[p], rows, static_cast<int>(words[p]));
                 up(o_codes[p], c.data(), c.size() * 4);
                 up(o_scales[p], routed[p].scales->data, routed[p].scales->nbytes);
-                if (d.has_shared) {
-                    const std::vector<std::uint32_t> cs = packed_codes(shared[p], outs[p], static_cast<int>(words[p]));
-                    up(o_codes[p] + c.size() * 4, cs.data(), cs.size() * 4);
-                    up(o_scales[p] + routed[p].scales->nbytes, shared[p].scales->data, shared[p].scales->nbytes);
-                }
                 up(o_book[p], routed[p].codebook->data, routed[p].codebook->nbytes);  // unused entries stay 0
             }
             q38_moe_weights w{};
             w.router = reinterpret_cast<const uint16_t*>(base + o_router);
-            w.shared_gate = d.has_shared ? reinterpret_cast<const uint16_t*>(base + o_wsg) : nullptr;
             for (int p = 0; p < 3; ++p) {
                 w.codes[p] = reinterpret_cast<const uint32_t*>(base + o_codes[p]);
                 w.scales[p] = reinterpret_cast<const uint16_t*>(base + o_scales[p]);
                 w.books[p] = reinterpret_cast<const uint16_t*>(base + o_book[p]);
             }
             q38_moe_layer* layer = nullptr;
-            if (int rc = q38_moe_layer_create(ctx, &d, &w, &layer)) {
+            int rc = Q38_OK;
+            if (d.has_shared) {
+                up(o_wsg, shared.gate->data, shared.gate->nbytes);
+                w.shared_gate = reinterpret_cast<const uint16_t*>(base + o_wsg);
+                q38_affine_shared a{};
+                for (int p = 0; p < 3; ++p) {
+                    up(o_sw[p], shared.proj[p].weight->data, shared.proj[p].weight->nbytes);
+                    up(o_ss[p], shared.proj[p].scales->data, shared.proj[p].scales->nbytes);
+                    up(o_sb[p], shared.proj[p].biases->data, shared.proj[p].biases->nbytes);
+                    a.weight[p] = reinterpret_cast<const uint32_t*>(base + o_sw[p]);
+                    a.scales[p] = reinterpret_cast<const uint16_t*>(base + o_ss[p]);
+                    a.biases[p] = reinterpret_cast<const uint16_t*>(base + o_sb[p]);
+                }
+                a.bits = static_cast<int32_t>(shared.proj[0].bits);
+                a.group = static_cast<int32_t>(shared.proj[0].group_size);
+                a.inter = static_cast<int32_t>(shared.proj[0].out);
+                a.scale_dtype = shared.proj[0].scales->dtype == "F16" ? 1 : 0;
+                rc = q38_moe_layer_create_affine_shared(ctx, &d, &w, &a, &layer);
+            } else {
+                rc = q38_moe_layer_create(ctx, &d, &w, &layer);
+            }
+            if (rc) {
                 (void)hipFree(base);
-                return rc;  // q38_moe_layer_create set the message
+                return rc;  // the create call set the message
             }
             q38_private_layer_adopt(layer, base);
             *out = layer;
@@ -588,3 +700,4 @@ extern "C" int q38_moe_layer_load(q38_ctx* ctx, const char* checkpoint, const ch
         return ck_fail(Q38_EINVAL, e.what());
     }
 }
+

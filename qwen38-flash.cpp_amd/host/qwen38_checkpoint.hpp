@@ -17,8 +17,19 @@
 //                      base.vq_scales  [experts, out, in/group] F16
 //                    and per layer prefix: prefix.gate.weight [E, H] BF16 (the router,
 //                    src/sparse_moe.cpp:467) and, with a shared expert,
-//                    prefix.shared_expert_gate.weight [1, H] BF16 plus the VQ modules
-//                    prefix.shared_expert.{gate,up,down}_proj (experts = 1).
+//                    prefix.shared_expert_gate.weight [1, H] BF16 plus the MLX affine
+//                    projections prefix.shared_expert.{gate,up,down}_proj (the affine branch of
+//                    SparseMoe::load_projection, src/sparse_moe.cpp:662-700):
+//                      base.weight     [out, in * bits / 32] U32 (values LSB-first)
+//                      base.scales     [out, in / group] BF16 or F16
+//                      base.biases     [out, in / group] BF16 or F16
+//                    with bits inferred from the shapes (infer_affine_quantization_bits,
+//                    src/quantization_geometry.cpp:9-35) and checked against the manifest's
+//                    "quantization" (or "quantization_config") bits for the module, whose
+//                    group_size it takes (ModelManifest::quantization_for,
+//                    src/model_manifest.cpp:188-208, 470-482).
+// Module and tensor names resolve as the reference's do: a name under "language_model." that
+// is absent falls back to the name without it (src/model_manifest.cpp:484-500).
 // Byte codes (pack_bits 0) are the 8-bit packed layout when in/dim is a multiple of 32 (four
 // codes per word, lowest byte first); other widths are re-laid out into 32-code blocks.
 #pragma once
@@ -81,6 +92,12 @@ struct VectorQuantizationSpec {
     std::size_t packed_bits{0};  // 0: one code per byte
 };
 
+// QuantizationSpec (include/qwen38/model_manifest.hpp): affine bits and group size.
+struct QuantizationSpec {
+    std::size_t bits{0};
+    std::size_t group_size{0};
+};
+
 // The manifest subset the MoE layers need (config.json of a checkpoint directory).
 class ModelManifest {
 public:
@@ -89,11 +106,19 @@ public:
     [[nodiscard]] std::size_t expert_count() const noexcept { return expert_count_; }
     [[nodiscard]] std::size_t experts_per_token() const noexcept { return experts_per_token_; }
     [[nodiscard]] bool normalize_topk_probability() const noexcept { return normalize_; }
+    // The config's shared_expert_intermediate_size (0 when the config has none).
+    [[nodiscard]] std::size_t shared_expert_intermediate_size() const noexcept { return shared_inter_; }
     [[nodiscard]] const VectorQuantizationSpec* vector_quantization_for(std::string_view module) const;
+    // The module's override, else the model-wide bits and group size; throws when the config
+    // carries no quantization metadata (the reference requires it of every model).
+    [[nodiscard]] QuantizationSpec quantization_for(std::string_view module) const;
 
 private:
-    std::size_t expert_count_{0}, experts_per_token_{0};
+    std::size_t expert_count_{0}, experts_per_token_{0}, shared_inter_{0};
     bool normalize_{true};
+    bool has_quantization_{false};
+    QuantizationSpec quantization_{};
+    std::map<std::string, QuantizationSpec, std::less<>> quantization_overrides_;
     std::map<std::string, VectorQuantizationSpec, std::less<>> vq_;
 };
 
@@ -124,6 +149,16 @@ private:
     std::map<std::string, TensorView, std::less<>> tensors_;
 };
 
+// One MLX affine projection's host tensors after the reference's checks (bits inferred from
+// the shapes and equal to the manifest's; scales and biases of one dtype).
+struct AffineProjectionTensors {
+    std::size_t bits{0}, group_size{0}, out{0}, in{0};
+    const TensorView* weight{nullptr};
+    const TensorView* scales{nullptr};
+    const TensorView* biases{nullptr};
+};
+[[nodiscard]] AffineProjectionTensors load_affine_projection(const TensorStore& store, std::string_view base);
+
 // One VQ projection's host tensors after the reference's checks.
 struct VqProjectionTensors {
     VectorQuantizationSpec spec;
@@ -132,6 +167,14 @@ struct VqProjectionTensors {
     const TensorView* scales{nullptr};
 };
 [[nodiscard]] VqProjectionTensors load_vq_projection(const TensorStore& store, std::string_view base);
+
+// The affine shared expert of the layer at `prefix` and its BF16 gate row.
+struct SharedExpertTensors {
+    AffineProjectionTensors proj[3];  // gate, up, down
+    const TensorView* gate{nullptr};
+};
+[[nodiscard]] SharedExpertTensors checkpoint_shared_expert(const TensorStore& store, std::string_view prefix,
+                                                           std::size_t hidden);
 
 // The q38 layer description of the MoE layer at `prefix` (geometry from the VQ modules).
 [[nodiscard]] q38_moe_desc checkpoint_layer_desc(const TensorStore& store, std::string_view prefix,

@@ -49,6 +49,11 @@ class MoeMixedWeights(C.Structure):
                 ("reserved", C.c_uint16)]
 
 
+class AffineShared(C.Structure):
+    _fields_ = [("weight", C.c_void_p * 3), ("scales", C.c_void_p * 3), ("biases", C.c_void_p * 3),
+                ("bits", C.c_int32), ("group", C.c_int32), ("inter", C.c_int32), ("scale_dtype", C.c_int32)]
+
+
 class RouteOut(C.Structure):
     _fields_ = [("experts", C.c_void_p), ("weights", C.c_void_p), ("logits", C.c_void_p),
                 ("plan", C.c_void_p), ("x_norm", C.c_void_p)]
@@ -83,6 +88,8 @@ _sig("q38_unpack_vq_code", C.c_int, P, I64, I64, C.c_int, C.POINTER(U32))
 _sig("q38_supports_segmented_vq", C.c_int, C.c_int, C.c_int)
 _sig("q38_moe_layer_create", C.c_int, P, C.POINTER(MoeDesc), C.POINTER(MoeWeights), C.POINTER(P))
 _sig("q38_moe_layer_create_synthetic", C.c_int, P, C.POINTER(MoeDesc), U64, I32, C.POINTER(P))
+_sig("q38_moe_layer_create_affine_shared", C.c_int, P, C.POINTER(MoeDesc), C.POINTER(MoeWeights),
+     C.POINTER(AffineShared), C.POINTER(P))
 _sig("q38_moe_layer_destroy", None, P)
 _sig("q38_moe_layer_load", C.c_int, P, C.c_char_p, C.c_char_p, I32, C.POINTER(P))
 _sig("q38_checkpoint_inspect", C.c_int, C.c_char_p, C.c_char_p, C.POINTER(MoeDesc))

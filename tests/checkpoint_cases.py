@@ -8,6 +8,7 @@ import os
 import numpy as np
 
 PREFIX = "model.layers.0.mlp"
+PREFIX_WRAPPED = "language_model." + PREFIX  # (the reference's name; a flat store drops the wrapper)
 
 
 def f16(a):
@@ -36,16 +37,22 @@ def packed(codes, bits):
 
 
 class Checkpoint:
-    """One MoE layer: E routed experts (+ optional VQ shared expert sharing the codebooks),
-    gate/up (dim, bits) and down (dim, bits) geometry, scale groups gu_group / down_group.
-    bits 0 = byte codes (pack_bits null in the manifest)."""
+    """One MoE layer in the reference's on-disk layout: E routed VQ experts (gate/up (dim, bits)
+    and down (dim, bits) geometry, scale groups gu_group / down_group; bits 0 = byte codes,
+    pack_bits null in the manifest) and, with shared, an MLX affine shared expert
+    (shared_expert.{gate,up,down}_proj .weight / .scales / .biases, sa_bits values, sa_group
+    inputs per scale, sa_fmt 0 BF16 or 1 F16 scales, intermediate size shared_inter) with the
+    model-wide "quantization" metadata. flat: tensors and modules stored without the
+    "language_model." wrapper that the layer prefix PREFIX_WRAPPED carries."""
 
     def __init__(self, H=512, I=128, E=64, k=4, gu=(8, 14), down=(8, 14), gu_group=64, down_group=64,
-                 shared=True, seed=0, normalize=True):
+                 shared=True, seed=0, normalize=True, sa_bits=4, sa_group=64, sa_fmt=0, shared_inter=None,
+                 flat=False):
+        from affine_cases import random_affine
         rng = np.random.default_rng(seed)
         self.H, self.I, self.E, self.k, self.gu, self.down = H, I, E, k, gu, down
         self.groups = (gu_group, gu_group, down_group)
-        self.shared, self.normalize = shared, normalize
+        self.shared, self.normalize, self.flat = shared, normalize, flat
         geo = (gu, gu, down)
         ins, outs = (H, H, I), (I, I, H)
         self.router = bf16_bits(rng.normal(0, 0.02, (E, H)))
@@ -56,18 +63,24 @@ class Checkpoint:
             K = 256 if bits == 0 else 1 << bits
             self.books.append(f16(rng.normal(0, 1, (K, dim))))
             n = ins[p] // dim
-            rows = (E + 1) * outs[p]
+            rows = E * outs[p]
             self.codes.append(rng.integers(0, K, (rows, n)).astype(np.uint32))
             self.scales.append(f16(rng.uniform(0.005, 0.02, (rows, ins[p] // self.groups[p]))))
+        self.sa = random_affine(rng, H, shared_inter or I, sa_bits, sa_group, sa_fmt) if shared else None
 
     def kernel_geometry(self, p):
         dim, bits = (self.gu, self.gu, self.down)[p]
         return dim, (8 if bits == 0 else bits)
 
     def words(self, p):
-        """Codes in the q38 packed layout [(E+1)*OUT, words] (byte codes = 8-bit words)."""
+        """Codes in the q38 packed layout [E*OUT, words] (byte codes = 8-bit words)."""
         dim, bits = self.kernel_geometry(p)
         return packed(self.codes[p], bits)
+
+    @property
+    def prefix(self):
+        """The layer prefix a caller passes (the wrapped name when the store is flat)."""
+        return PREFIX_WRAPPED if self.flat else PREFIX
 
     def config(self, experts_field=None):
         mods = {}
@@ -80,11 +93,13 @@ class Checkpoint:
                     "k": int(self.books[p].shape[0]), "dim": dim, "group": self.groups[p],
                     "pack_bits": None if bits == 0 else bits}
             mods[f"{PREFIX}.switch_mlp.{names[p]}"] = spec
-            if self.shared:
-                mods[f"{PREFIX}.shared_expert.{names[p]}"] = dict(spec, experts=1)
-        return {"text_config": {"num_experts": self.E, "num_experts_per_tok": self.k,
-                                "norm_topk_prob": self.normalize, "hidden_size": self.H},
-                "vq_modules": mods}
+        text = {"num_experts": self.E, "num_experts_per_tok": self.k, "norm_topk_prob": self.normalize,
+                "hidden_size": self.H}
+        cfg = {"text_config": text, "vq_modules": mods}
+        if self.shared:
+            text["shared_expert_intermediate_size"] = self.sa["inter"]
+            cfg["quantization"] = {"group_size": self.sa["group"], "bits": self.sa["bits"]}
+        return cfg
 
     def tensors(self):
         t = {f"{PREFIX}.gate.weight": self.router}  # uint16 = BF16 bits
@@ -93,17 +108,17 @@ class Checkpoint:
         for p in range(3):
             dim, bits = (self.gu, self.gu, self.down)[p]
             E, O = self.E, outs[p]
-            c = self.codes[p].reshape(E + 1, O, -1)
+            c = self.codes[p].reshape(E, O, -1)
             enc = (lambda a: a.astype(np.uint8)) if bits == 0 else (lambda a: packed(a.reshape(-1, a.shape[-1]), bits)
                                                                       .reshape(a.shape[0], a.shape[1], -1))
-            s = self.scales[p].reshape(E + 1, O, -1)
-            t[f"{PREFIX}.switch_mlp.{names[p]}.codes"] = enc(c[:E])
+            t[f"{PREFIX}.switch_mlp.{names[p]}.codes"] = enc(c)
             t[f"{PREFIX}.switch_mlp.{names[p]}.codebook"] = self.books[p]
-            t[f"{PREFIX}.switch_mlp.{names[p]}.vq_scales"] = s[:E]
+            t[f"{PREFIX}.switch_mlp.{names[p]}.vq_scales"] = self.scales[p].reshape(E, O, -1)
             if self.shared:
-                t[f"{PREFIX}.shared_expert.{names[p]}.codes"] = enc(c[E:])
-                t[f"{PREFIX}.shared_expert.{names[p]}.codebook"] = self.books[p]
-                t[f"{PREFIX}.shared_expert.{names[p]}.vq_scales"] = s[E:]
+                sdt = np.float16 if self.sa["fmt"] == 1 else np.uint16  # (uint16 = BF16 bits)
+                t[f"{PREFIX}.shared_expert.{names[p]}.weight"] = self.sa["w"][p]
+                t[f"{PREFIX}.shared_expert.{names[p]}.scales"] = self.sa["s"][p].view(sdt)
+                t[f"{PREFIX}.shared_expert.{names[p]}.biases"] = self.sa["b"][p].view(sdt)
         if self.shared:
             t[f"{PREFIX}.shared_expert_gate.weight"] = self.wsg
         return t

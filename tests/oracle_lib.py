@@ -89,6 +89,11 @@ class Oracle:
         sig("orc_round_uniforms", None, U64, U64, U64, U32, P, P)
         sig("orc_accept_sampled", C.c_int, P, P, P, C.c_int, I64, F32, U64, U64, U64, P, P)
         sig("orc_plant_fault", None, C.c_int)
+        sig("orc_moe_layer_dense_affine_shared", C.c_int, C.POINTER(Desc), P, P, C.POINTER(P), C.POINTER(P),
+            C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P), C.c_int, C.c_int, C.c_int, C.c_int, P, C.c_int,
+            P, P, P, P, C.c_int)
+        sig("orc_affine_expert", C.c_int, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.c_int, C.c_int, C.c_int,
+            C.c_int, C.c_int, P, C.c_int, P)
         sig("orc_route_synth", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, P, P, C.c_int)
 
     # ---- formats
@@ -231,6 +236,39 @@ class Oracle:
         arr = lambda xs: (P * 3)(*[_a(a).value for a in xs])
         rc = self.lib.orc_moe_layer_dense(C.byref(d), _a(keep[0]), _a(keep[1]), arr(keep[2:5]), arr(keep[5:8]),
                                           arr(keep[8:11]), _a(x), M, _a(y), _a(ex), _a(wt), _a(lg), threads)
+        assert rc == 0
+        return y, ex, wt, lg
+
+    @staticmethod
+    def _ptrs(arrs):
+        return (P * 3)(*[_a(a) for a in arrs])
+
+    def affine_expert(self, sa, x):
+        """The affine shared expert (sa: dict with w, s, b lists of 3 arrays, bits, group, inter,
+        fmt) on rows of x -> T(down) [M, H] float32."""
+        x = np.ascontiguousarray(x, np.uint16)
+        M, H = x.shape
+        keep = [[np.ascontiguousarray(a) for a in sa[k]] for k in ("w", "s", "b")]
+        out = np.empty((M, H), np.float32)
+        rc = self.lib.orc_affine_expert(self._ptrs(keep[0]), self._ptrs(keep[1]), self._ptrs(keep[2]), H, sa["inter"],
+                                        sa["bits"], sa["group"], sa["fmt"], _a(x), M, _a(out))
+        assert rc == 0
+        return out
+
+    def moe_layer_dense_affine_shared(self, d: Desc, router, wsg, codes, scales, books, sa, x, threads=8):
+        x = np.ascontiguousarray(x, np.uint16)
+        M = x.shape[0]
+        y = np.empty_like(x)
+        ex = np.empty((M, d.top_k), np.int32)
+        wt = np.empty((M, d.top_k), np.float32)
+        lg = np.empty((M, d.experts), np.float32)
+        keep = [[np.ascontiguousarray(a) for a in grp] for grp in (codes, scales, books)]
+        sk = [[np.ascontiguousarray(a) for a in sa[k]] for k in ("w", "s", "b")]
+        r, w = np.ascontiguousarray(router, np.uint16), np.ascontiguousarray(wsg, np.uint16)
+        rc = self.lib.orc_moe_layer_dense_affine_shared(
+            C.byref(d), _a(r), _a(w), self._ptrs(keep[0]), self._ptrs(keep[1]), self._ptrs(keep[2]),
+            self._ptrs(sk[0]), self._ptrs(sk[1]), self._ptrs(sk[2]), sa["bits"], sa["group"], sa["inter"], sa["fmt"],
+            _a(x), M, _a(y), _a(ex), _a(wt), _a(lg), threads)
         assert rc == 0
         return y, ex, wt, lg
 

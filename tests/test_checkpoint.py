@@ -87,17 +87,80 @@ def test_layer_level_errors(q38, tmp_path):
     expect_error(q38, ck.write(str(tmp_path / "a"), tensors=t), f"missing tensor {PREFIX}.gate.weight")
     t = ck.tensors()
     t[f"{PREFIX}.shared_expert_gate.weight"] = np.zeros((1, 512), np.uint16)
-    expect_error(q38, ck.write(str(tmp_path / "b"), tensors=t), "is not VQ-coded")
+    expect_error(q38, ck.write(str(tmp_path / "b"), tensors=t),
+                 f"missing tensor {PREFIX}.shared_expert.gate_proj.weight")
     cfg = ck.config()
     del cfg["vq_modules"][f"{PREFIX}.switch_mlp.down_proj"]
     expect_error(q38, ck.write(str(tmp_path / "c"), config=cfg), "no vq_modules entry")
-    # a shared expert must share the routed codebook (one codebook per projection)
-    ck2 = Checkpoint(shared=True)
-    t = ck2.tensors()
-    t[f"{PREFIX}.shared_expert.up_proj.codebook"] = t[f"{PREFIX}.shared_expert.up_proj.codebook"] * 2
-    # inspect passes (geometry only); the loader itself compares the codebooks
-    rc, _, err = inspect(q38, ck2.write(str(tmp_path / "d"), tensors=t))
+
+
+def test_affine_shared_expert_checks(q38, tmp_path):
+    """The affine shared expert's checks: the reference's messages for a missing quantization
+    section, bits that disagree with it, non-integral bits and bad tensors
+    (src/sparse_moe.cpp:662-700, src/quantization_geometry.cpp:9-35, src/model_manifest.cpp:188-192);
+    a VQ module for a shared expert is refused (experts must be num_experts), and one covering
+    all experts is not a shared expert the reference can apply."""
+    ck = Checkpoint(shared=True, sa_bits=4, sa_group=64)
+    base = f"{PREFIX}.shared_expert.up_proj"
+    cfg = ck.config()
+    del cfg["quantization"]
+    expect_error(q38, ck.write(str(tmp_path / "q0"), config=cfg), "model is missing quantization metadata")
+    cfg = ck.config()
+    cfg["quantization"]["bits"] = 8
+    expect_error(q38, ck.write(str(tmp_path / "q1"), config=cfg),
+                 f"MoE tensor disagrees with quantization metadata for {PREFIX}.shared_expert.gate_proj")
+    cfg = ck.config()
+    cfg["quantization"][base] = {"bits": 4, "group_size": 48}
+    expect_error(q38, ck.write(str(tmp_path / "q2"), config=cfg), "non-integral MoE quantization bits")
+    cfg = ck.config()
+    cfg["quantization"][base] = {"bits": 9, "group_size": 64}
+    expect_error(q38, ck.write(str(tmp_path / "q3"), config=cfg), f"invalid quantization override for {base}")
+    for i, (key, f) in enumerate([(f"{base}.scales", lambda a: a.astype(np.float32)),
+                                  (f"{base}.biases", lambda a: a[:, :-1]),
+                                  (f"{base}.weight", lambda a: a.astype(np.int32))]):
+        t = ck.tensors()
+        t[key] = np.ascontiguousarray(f(t[key]))
+        rc, _, err = inspect(q38, ck.write(str(tmp_path / f"t{i}"), tensors=t))
+        assert rc == q38.Q38_EINVAL and ("invalid affine quantization tensors" in err or "quantization" in err), err
+    # a per-module override of the quantization is honoured (here: the same values)
+    cfg = ck.config()
+    cfg["quantization"][f"language_model.{base}"] = {"bits": 4, "group_size": 64}
+    rc, _, err = inspect(q38, ck.write(str(tmp_path / "ov"), config=cfg))
     assert rc == 0, err
+    cfg = ck.config()
+    cfg["text_config"]["shared_expert_intermediate_size"] = 256
+    expect_error(q38, ck.write(str(tmp_path / "si"), config=cfg), "disagrees with shared_expert_intermediate_size")
+    # VQ shared modules: experts 1 (the old exemption) and experts E
+    cfg = ck.config()
+    cfg["vq_modules"][f"{PREFIX}.shared_expert.gate_proj"] = dict(cfg["vq_modules"][f"{PREFIX}.switch_mlp.gate_proj"],
+                                                                   experts=1)
+    expect_error(q38, ck.write(str(tmp_path / "v1"), config=cfg),
+                 f"unsupported vector quantization geometry for {PREFIX}.shared_expert.gate_proj")
+    cfg["vq_modules"][f"{PREFIX}.shared_expert.gate_proj"]["experts"] = ck.E
+    expect_error(q38, ck.write(str(tmp_path / "v2"), config=cfg), "shared experts load in affine form")
+
+
+@pytest.mark.parametrize("shared_inter,sa_bits,sa_group,sa_fmt", [(128, 4, 64, 0), (256, 8, 32, 1), (64, 2, 64, 0)])
+def test_affine_shared_geometry(q38, tmp_path, shared_inter, sa_bits, sa_group, sa_fmt):
+    ck = Checkpoint(shared=True, shared_inter=shared_inter, sa_bits=sa_bits, sa_group=sa_group, sa_fmt=sa_fmt)
+    rc, d, err = inspect(q38, ck.write(str(tmp_path)))
+    assert rc == 0 and d.has_shared == 1, err
+
+
+def test_flat_names_resolve_under_the_wrapper(q38, tmp_path):
+    """Tensors and modules stored without "language_model." resolve when the layer is named
+    with it (ModelManifest::resolve_tensor_name / vector_quantization_for /
+    quantization_for, src/model_manifest.cpp:470-500)."""
+    ck = Checkpoint(shared=True, flat=True)
+    path = ck.write(str(tmp_path))
+    d = q38.MoeDesc()
+    rc = q38.lib.q38_checkpoint_inspect(path.encode(), ck.prefix.encode(), C.byref(d))
+    assert rc == 0, q38.lib.q38_last_error()
+    rc2, d2, err = inspect(q38, path)
+    assert rc2 == 0, err
+    assert bytes(d) == bytes(d2)
+    rc = q38.lib.q38_checkpoint_inspect(path.encode(), b"other_model." + PREFIX.encode(), C.byref(d))
+    assert rc == q38.Q38_EINVAL
 
 
 def test_safetensors_header_checks(q38, tmp_path):
