@@ -304,10 +304,12 @@ __global__ __launch_bounds__(128 * T) void k_route_norm(LayerDev L, MoeBufs B, i
             *dst = ones;
         }
     }
+    Q38_STAMP(0, 4);
     if (e >= nr) return;
     // all rows' products first (independent chains), then the butterflies
     float acc[MR];
     router_dots<T, MR>(xs, M, wv, acc);
+    Q38_STAMPV(0, 5, acc[0]);
 #pragma unroll
     for (int s = 0; s < scatter_slots<MR>(); ++s) {
         const int r = MR > 1 ? scatter_value<MR>(s, lane >> 4) : 0;

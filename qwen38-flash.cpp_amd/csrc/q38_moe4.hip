@@ -302,8 +302,10 @@ __device__ __forceinline__ void gu4_body(const LayerDev& L, const MoeBufs& B, in
         v4f_t acc;
         if constexpr (G8 == 0) acc = slice_mfma<BITS>(cwj, book, xb);
         else acc = slice_mfma_g8<BITS>(cwj, book, xb, scj.g);
+        if (j == 0) Q38_STAMPV(8192, 6, acc[0]);
         reinterpret_cast<v4f_t*>(red)[(buf * KS + wave) * 64 + lane] = acc;
         lds_barrier();  // (the other buffer's readers passed the previous item's barrier)
+        if (j == 0) Q38_STAMP(8192, 7);
         oat = -1;
         if (tid < 64 * kNarrow) {
             const int jr = tid & 3;  // request row
@@ -544,6 +546,7 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
             }
         }
         lds_barrier();  // SwiGLU rows (and, the first time, the codebook chunk) in LDS
+        if (jj == 0) Q38_STAMP(16384, 12);
         const int jb = (lane & 3) < n ? (lane & 3) : 0;
         uint2 bop[32];
 #pragma unroll
@@ -555,8 +558,10 @@ __device__ __forceinline__ void dn4_body(const LayerDev& L, const MoeBufs& B, in
         v4f_t acc;
         if constexpr (G8 == 0) acc = slice_mfma<BITS>(cwj, book, bop);
         else acc = slice_mfma_g8<BITS>(cwj, book, bop, scj.g);
+        if (jj == 0) Q38_STAMPV(16384, 13, acc[0]);
         if (kh > 0) reinterpret_cast<v4f_t*>(red)[(rg * (KS - 1) + kh - 1) * 64 + lane] = acc;
         lds_barrier();  // (the next item's SwiGLU rows are written after this barrier)
+        if (jj == 0) Q38_STAMP(16384, 14);
         oroute = -1;
         if (kh == 0) {
 #pragma unroll
