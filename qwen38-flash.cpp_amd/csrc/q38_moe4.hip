@@ -218,8 +218,10 @@ __device__ __forceinline__ void gu4_body(const LayerDev& L, const MoeBufs& B, in
         for (int q = 0; q < XPW; ++q)
             xv[q] = *reinterpret_cast<const uint2*>(B.x16 + static_cast<size_t>(wave) * H +
                                                     (lane + 64 * q) * (4 * NCHUNK) + 4 * chunk);
-        constexpr int kLines = NCHUNK * KENT * 8 / 128;
-        warm = reinterpret_cast<const uint32_t*>(L.p[2].book4)[(((kk * M + wave) * 64 + lane) % kLines) * 32];
+        // (lines of the down book itself: (1 << bits) entries of dim fp16 values; the gate/up
+        // book's geometry may differ, e.g. d8/14-bit gate/up over a d4/8-bit down)
+        const int lines = ((1 << L.p[2].bits) * L.p[2].dim * 2) >> 7;
+        warm = reinterpret_cast<const uint32_t*>(L.p[2].book4)[(((kk * M + wave) * 64 + lane) % lines) * 32];
 #pragma unroll
         for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(lg[j]));
         Q38_STAMP(8192, 1);

@@ -184,3 +184,22 @@ def test_hidden_2560_layers(gpu, q38, orc, H, I, M):
         tol_check(orc, y, wy)
     finally:
         L.close()
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_d8_gate_up_over_d4_down(gpu, q38, orc, M):
+    """A full-size layer whose gate/up (d8/14-bit, 256 KiB book) and down (d4/8-bit, 2 KiB
+    book) geometries differ takes the four-row kernels; the gate/up kernel's warm-up of the
+    down book stays inside the down book's own lines."""
+    d = q38.desc(gu=(8, 14), down=(4, 8))
+    L = q38.MoeLayer(gpu, d, seed=SEED, layer=9)
+    try:
+        x = orc.normal(orc.key(SEED, 9, 21), 29 * M, M * 2048, 1.0).reshape(M, 2048)
+        y, ex, wt, lg, plan = run_forward(q38, L, L.desc, x)
+        wy, wex, wwt, wlg = orc.moe_layer_synth(oracle_lib.make_desc(gu=(8, 14), down=(4, 8)), SEED, 9, x)
+        assert np.array_equal(lg, wlg), "router logits"
+        assert np.array_equal(ex, wex) and np.array_equal(wt, wwt), "routing"
+        plan_check(orc, plan, ex, 512)
+        tol_check(orc, y, wy)
+    finally:
+        L.close()
