@@ -17,6 +17,9 @@
 // Rows <= 4 take the narrow kernels of q38_moe4.hip instead of k_topk_plan + k_*_mfma.
 // Mixed layers (two codebook geometries by expert parity) run k_gu_mfma / k_down_mfma once
 // per bank. Layers with per-64-input scale groups use the k_*_grouped VALU kernels.
+#ifdef Q38_TRACE
+#define g_trace g_trace_route  // (each code object holds its own stamp buffer)
+#endif
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
 #include "q38_moe_dev.hpp"
@@ -1026,4 +1029,15 @@ hipError_t launch_book_to_int8(const uint16_t* book16, int n, int8_t* q8, uint16
     return hipGetLastError();
 }
 
+#ifdef Q38_TRACE
+__device__ unsigned long long g_trace_route[32768];
+#endif
 } // namespace q38
+
+#ifdef Q38_TRACE
+extern "C" int q38_trace_read_route(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(q38::g_trace_route), sizeof(unsigned long long) * 32768) == hipSuccess
+               ? 0
+               : -1;
+}
+#endif

@@ -914,4 +914,14 @@ hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t 
     return hipErrorInvalidValue;
 }
 
+#ifdef Q38_TRACE
+// The phase stamps of this code object (Q38_STAMP in q38_moe_dev.hpp) and their reader.
+__device__ unsigned long long g_trace[32768];
+#endif
 } // namespace q38
+
+#ifdef Q38_TRACE
+extern "C" int q38_trace_read(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(q38::g_trace), sizeof(unsigned long long) * 32768) == hipSuccess ? 0 : -1;
+}
+#endif

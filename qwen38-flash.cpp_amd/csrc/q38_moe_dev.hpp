@@ -6,8 +6,8 @@
 #include "q38_device.hpp"
 #include "q38_internal.hpp"
 
-// Phase stamps for timing a kernel from the inside: with Q38_TRACE defined (a separate
-// relocatable-device-code build), thread 0 of each workgroup records the 100 MHz real-time
+// Phase stamps for timing a kernel from the inside: with Q38_TRACE defined (the separate
+// build of the Makefile's trace target, read by trace/phases.py), thread 0 of each workgroup records the 100 MHz real-time
 // counter at a numbered point into q38::g_trace[base + 16 * workgroup + i]; Q38_STAMPV
 // first waits for value v. Without Q38_TRACE they compile to nothing.
 #ifdef Q38_TRACE

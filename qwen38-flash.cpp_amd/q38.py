@@ -14,7 +14,8 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libq38.so")
+# (Q38_LIB: another build of the same ABI, e.g. the phase-stamp build trace/libq38.so)
+LIB_PATH = os.environ.get("Q38_LIB") or os.path.join(_HERE, "libq38.so")
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"libq38.so is not built at {LIB_PATH}; run __graft_entry__.build()")
