@@ -753,8 +753,8 @@ static int check_forward_rows(const q38_moe_layer* L, int rows) {
     if (rows >= 1 && rows <= kMaxRows) return Q38_OK;
     if (rows < 1 || rows > kMaxPrefillRows) return fail(Q38_EINVAL, "rows must be between 1 and 2048");
     if (L->desc.top_k * rows > 32768) return fail(Q38_EINVAL, "rows x top_k must not exceed 32768");
-    if (!moe_supports_prefill(L->dev))
-        return fail(Q38_EINVAL, "prefill widths (rows > 16) need a d8/14-bit layer with per-row scales");
+    if (!moe_supports_prefill(L->dev) && !moe_supports_grouped_prefill(L->dev))
+        return fail(Q38_EINVAL, "prefill widths (rows > 16) need a uniform layer of d8/14, d4/8 or d2/8 codes");
     return Q38_OK;
 }
 
@@ -794,8 +794,29 @@ static int run_prefill(q38_moe_layer* L, const MoeBufs& w, int rows, const uint1
     if (int rc = route_prefill(L, w, rows, x, st, ev)) return rc;
     Q38_HIP(launch_shared_affine(L->dev, w, rows, st));
     LayerDev one = expert_view(L->dev);  // partial-sum planes of the prefill kernels
-    one.gu_parts = one.d_parts = prefill_planes(L->dev, rows);
     KernelTimer& kt = kernel_timer();
+    if (!moe_supports_prefill(L->dev)) {
+        // scale groups, d4 and d2 codes: the grouped kernels over 16-route passes of each slot
+        // (one partial-sum plane; SwiGLU inside the down kernel)
+        one.gu_parts = one.d_parts = 1;
+        if (ev) kt = {ev[6], ev[7]};
+        Q38_HIP(launch_gate_up_grouped(one, w, rows, st));
+        kt = {};
+        if (trace)
+            if (int rc = copy_routes(L, rows, w, trace, st)) return rc;
+        if (ev) {
+            Q38_HIP(hipEventRecord(ev[8], st));
+            Q38_HIP(hipEventRecord(ev[9], st));
+            kt = {ev[10], ev[11]};
+        }
+        Q38_HIP(launch_down_grouped(one, w, rows, st));
+        if (ev) kt = {ev[12], ev[13]};
+        one.has_shared = L->dev.has_shared;
+        Q38_HIP(launch_combine(one, w, rows, nullptr, y, st));
+        kt = {};
+        return Q38_OK;
+    }
+    one.gu_parts = one.d_parts = prefill_planes(L->dev, rows);
     if (ev) kt = {ev[6], ev[7]};
     Q38_HIP(launch_gate_up_pf(one, w, rows, st));
     if (trace)

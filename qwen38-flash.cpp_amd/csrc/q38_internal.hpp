@@ -150,6 +150,9 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
 // the grouped-scale (VALU) kernels of launch_gate_up / launch_down (q38_moe_grp.hip)
 hipError_t launch_gate_up_grouped(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down_grouped(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+// Prefill widths (kMaxRows < M) on the grouped kernels: layouts the segmented MFMA kernels
+// do not take (scale groups, d4 and d2 codes)
+bool moe_supports_grouped_prefill(const LayerDev& L);
 // The affine shared expert of the call's rows (q38_affine.hip): SwiGLU rows into B.h16, then
 // its down outputs into the shared rows of the down planes (plane 0; plane 1 cleared). Runs
 // after the router (it reads B.x) and before the combine; nothing without shared_affine.

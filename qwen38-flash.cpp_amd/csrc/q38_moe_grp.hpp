@@ -11,7 +11,7 @@
 namespace q38 {
 namespace {
 
-int next_pow2(int v) {
+inline int next_pow2(int v) {
     int p = 1;
     while (p < v) p <<= 1;
     return p;
@@ -166,16 +166,76 @@ __device__ __forceinline__ void grouped_rows_n(const ProjDev& P, int expert, int
                                              rplan, MK);
 }
 
+// Work units of a call. Up to kMaxRows rows, a unit is a slot of the plan (blockIdx.y). At
+// prefill widths (more rows, the plan of k_plan_sort, same layout) a slot can hold up to M
+// routes, more than the kMaxRows staged rows: a unit is then one pass over up to kMaxRows
+// of a slot's routes, the slots' passes in slot order (routed experts ascending, then the
+// shared expert). Block-wide (256 threads, uniform result); false past the last unit.
+constexpr int kUnitSlotsPerThread = 5;  // 256 x 5 >= 1025 slots (E <= 1024 + the shared expert)
+__device__ bool grouped_unit(const int32_t* plan, int M, int K, int has_shared, int u, int* slot, int* pass) {
+    __shared__ int wsum[4];
+    __shared__ int found[2];
+    const int MK = M * K, nu = plan[0];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int cnt[kUnitSlotsPerThread], tot = 0;
+#pragma unroll
+    for (int c = 0; c < kUnitSlotsPerThread; ++c) {
+        const int s = tid * kUnitSlotsPerThread + c;
+        const int n = s < nu ? plan[2 + MK + s] - plan[1 + MK + s] : (s == nu && has_shared ? M : 0);
+        cnt[c] = (n + kMaxRows - 1) / kMaxRows;
+        tot += cnt[c];
+    }
+    int incl = tot;  // inclusive scan over the wave, then the waves in order
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += t;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    if (tid == 0) found[0] = -1;
+    __syncthreads();
+    int start = incl - tot;
+    for (int w = 0; w < wave; ++w) start += wsum[w];
+    const int total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+#pragma unroll
+    for (int c = 0; c < kUnitSlotsPerThread; ++c) {
+        if (u >= start && u < start + cnt[c]) {
+            found[0] = tid * kUnitSlotsPerThread + c;
+            found[1] = u - start;
+        }
+        start += cnt[c];
+    }
+    __syncthreads();
+    *slot = found[0];
+    *pass = found[1];
+    return u < total && found[0] >= 0;
+}
+
+// The unit's expert, routes (n <= kMaxRows, from sorted position pos0) and its first route's
+// index j0 within the slot; false for no work.
+__device__ __forceinline__ bool grouped_routes(const LayerDev& L, const MoeBufs& B, int M, int* expert, int* n,
+                                               int* pos0, int* j0, bool* shared) {
+    int slot = static_cast<int>(blockIdx.y), pass = 0;
+    if (M > kMaxRows && !grouped_unit(B.plan, M, L.K, L.has_shared, slot, &slot, &pass)) return false;
+    if (!slot_rows(B.plan, M, L.K, L.has_shared, slot, L.E, expert, n, pos0)) return false;
+    *shared = slot == B.plan[0];
+    *j0 = pass * kMaxRows;
+    *n = *n - *j0 < kMaxRows ? *n - *j0 : kMaxRows;
+    *pos0 += *j0;
+    return *n > 0;
+}
+
 template <int D, int BITS, int LPR>
 __global__ __launch_bounds__(256) void k_gu_grouped(LayerDev L, MoeBufs B, int M) {
     extern __shared__ __align__(16) fin_t fin[];  // n rows of H, at fin_at
-    int expert, n, pos0;
-    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
-    const bool shared = static_cast<int>(blockIdx.y) == B.plan[0];
+    int expert, n, pos0, j0;
+    bool shared;
+    if (!grouped_routes(L, B, M, &expert, &n, &pos0, &j0, &shared)) return;
     const int H = L.H, I = L.I;
     for (int i = threadIdx.x; i < n * H; i += 256) {
         const int j = i / H, c = i % H;
-        fin[fin_at(j, c, H)] = static_cast<fin_t>(bf2f(B.x[static_cast<size_t>(route_row(B.plan, M, L.K, pos0, j, shared)) * H + c]));
+        const int row = shared ? j0 + j : route_row(B.plan, M, L.K, pos0, j, false);
+        fin[fin_at(j, c, H)] = static_cast<fin_t>(bf2f(B.x[static_cast<size_t>(row) * H + c]));
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -187,8 +247,9 @@ __global__ __launch_bounds__(256) void k_gu_grouped(LayerDev L, MoeBufs B, int M
 template <int D, int BITS, int LPR>
 __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int M) {
     extern __shared__ __align__(16) fin_t fin[];  // n rows of I, at fin_at
-    int expert, n, pos0;
-    if (!slot_rows(B.plan, M, L.K, L.has_shared, blockIdx.y, L.E, &expert, &n, &pos0)) return;
+    int expert, n, pos0, j0;
+    bool shared;
+    if (!grouped_routes(L, B, M, &expert, &n, &pos0, &j0, &shared)) return;
     const int H = L.H, I = L.I;
     for (int i = threadIdx.x; i < n * I; i += 256) {
         const size_t at = static_cast<size_t>(pos0) * I + i;
@@ -206,18 +267,33 @@ __global__ __launch_bounds__(256) void k_down_grouped(LayerDev L, MoeBufs B, int
 }
 
 
+// Units of a call (grid.y): its slots up to kMaxRows rows; at prefill widths a bound on the
+// passes, sum over slots of ceil(n / kMaxRows) <= MK / kMaxRows + slots + the shared
+// expert's passes (units past the last exit at once).
+inline int grouped_units(const LayerDev& L, int M) {
+    const int MK = M * L.K;
+    if (M <= kMaxRows) return MK + 1;
+    const int slots = MK < L.E ? MK : L.E;
+    return (MK + kMaxRows - 1) / kMaxRows + slots + (M + kMaxRows - 1) / kMaxRows + 1;
+}
+
 template <int D, int BITS, int LPR>
 hipError_t launch_gu_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = static_cast<size_t>(M) * fin_stride(L.H) * sizeof(fin_t);
+    const int rows = M < kMaxRows ? M : kMaxRows;
+    const size_t lds = static_cast<size_t>(rows) * fin_stride(L.H) * sizeof(fin_t);
     if (lds > kFinLdsMax) return hipErrorInvalidValue;
     if (const hipError_t e = ensure_lds<k_gu_grouped<D, BITS, LPR>>(kFinLdsMax); e != hipSuccess) return e;
-    return launch(k_gu_grouped<D, BITS, LPR>, dim3(L.I / kGuRowsPerBlock, M * L.K + 1), dim3(256), lds, st, L, B, M);
+    return launch(k_gu_grouped<D, BITS, LPR>, dim3(L.I / kGuRowsPerBlock, grouped_units(L, M)), dim3(256), lds, st, L,
+                  B, M);
 }
 template <int D, int BITS, int LPR>
 hipError_t launch_down_grouped_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = static_cast<size_t>(M) * fin_stride(L.I) * sizeof(fin_t);
-    return launch(k_down_grouped<D, BITS, LPR>, dim3(L.H / kDownRowsPerBlock, M * L.K + 1), dim3(256), lds, st, L, B,
-                  M);
+    const int rows = M < kMaxRows ? M : kMaxRows;
+    const size_t lds = static_cast<size_t>(rows) * fin_stride(L.I) * sizeof(fin_t);
+    if (lds > kFinLdsMax) return hipErrorInvalidValue;
+    if (const hipError_t e = ensure_lds<k_down_grouped<D, BITS, LPR>>(kFinLdsMax); e != hipSuccess) return e;
+    return launch(k_down_grouped<D, BITS, LPR>, dim3(L.H / kDownRowsPerBlock, grouped_units(L, M)), dim3(256), lds, st,
+                  L, B, M);
 }
 } // namespace
 } // namespace q38

@@ -148,8 +148,7 @@ def test_prefill_explicit_small_layer(gpu, q38, orc):
 def test_prefill_rejects(gpu, q38, orc):
     d = q38.desc()
     L = q38.MoeLayer(gpu, d, seed=SEED, layer=LAYER)
-    small = q38.MoeLayer(gpu, q38.desc(hidden=512, inter=128, experts=64, top_k=4, gu=(4, 8), down=(4, 8)),
-                         seed=SEED, layer=0)
+    mixed = q38.MoeLayer(gpu, q38.desc(mixed=1), seed=SEED, layer=0)
     try:
         ws = G.workspace(q38.lib.q38_moe_workspace_size(C.byref(d), 64))
         x = G.empty((2049, 2048), np.uint16)
@@ -158,10 +157,75 @@ def test_prefill_rejects(gpu, q38, orc):
                                        G.stream()) == q38.Q38_EINVAL
         assert q38.lib.q38_moe_forward(L.h, x.data_ptr(), 64, y.data_ptr(), None, ws.data_ptr(), 1024,
                                        G.stream()) == q38.Q38_ESPACE
-        # d4/8-bit projections have no prefill kernels
-        assert q38.lib.q38_moe_forward(small.h, x.data_ptr(), 32, y.data_ptr(), None, ws.data_ptr(), ws.numel(),
+        # the mixed VQ v2 layout has no prefill kernels
+        assert q38.lib.q38_moe_forward(mixed.h, x.data_ptr(), 32, y.data_ptr(), None, ws.data_ptr(), ws.numel(),
                                        G.stream()) == q38.Q38_EINVAL
         assert b"prefill" in q38.lib.q38_last_error()
     finally:
         L.close()
-        small.close()
+        mixed.close()
+
+
+# ---------------------------------------------------------------- grouped-scale layouts
+# Layouts the segmented MFMA kernels do not take run at prefill widths on the grouped VALU
+# kernels, in passes of up to 16 of a slot's routes (hot experts take many passes).
+
+def test_prefill_512_zipf_group64(gpu, q38, orc):
+    """The reference checkpoints' layout (d8/14-bit, one FP16 scale per 64 inputs) at 512 rows
+    with Zipf-skewed routing: logits, top-k, weights and the stable plan bit-exact, outputs
+    within the MoE tolerance of the oracle on sampled rows."""
+    M = 512
+    d = q38.desc(gu_group=64, down_group=64)
+    od = oracle_lib.make_desc(gu_group=64, down_group=64)
+    L = q38.MoeLayer(gpu, d, seed=SEED, layer=LAYER)
+    try:
+        bias = zipf_router_bias(512, SEED)
+        bias_dev = G.to_dev(bias)
+        q38.check(q38.lib.q38_moe_layer_set_router_bias(L.h, bias_dev.data_ptr()))
+        x = orc.rmsnorm(orc.embed(SEED, tokens(M), 2048))
+        y, ex, wt, lg, plan = run_forward(q38, L, d, x)
+        oex, owt = orc.route(lg, 10)
+        assert np.array_equal(ex, oex) and np.array_equal(wt.view(np.uint32), owt.view(np.uint32))
+        stable_plan_check(orc, plan, ex, 512)
+        counts = np.bincount(ex.reshape(-1), minlength=512)
+        assert counts.max() > 32  # some slots take several 16-route passes
+        check_rows_vs_oracle(orc, od, x, y, ex, wt, lg, sampled_rows(M, 16, 3), bias)
+        assert np.isfinite(orc.bf16_to_f32(y)).all()
+    finally:
+        L.close()
+
+
+@pytest.mark.parametrize("geo,M", [(dict(gu=(4, 8), down=(4, 8)), 40), (dict(gu=(2, 8), down=(2, 8), gu_group=64,
+                                                                            down_group=64), 100),
+                                   (dict(gu=(8, 14), down=(4, 8), gu_group=64, down_group=64), 33)])
+def test_prefill_grouped_small_layers(gpu, q38, orc, geo, M):
+    """d4/8 with row scales, d2/8 byte codes with 64-input groups, and d8 gate/up over a d4
+    down, at prefill widths on a small explicit layer (E = 64, k = 4: slots with up to ~M/4
+    routes, several passes each): every row against the oracle."""
+    lay = ExplicitLayer(q38, gpu, orc, H=512, I=256, E=64, k=4, seed=13 + M, **geo)
+    try:
+        x = orc.rmsnorm(orc.embed(SEED, tokens(M), 512))
+        y, ex, wt, lg, plan = run_forward(q38, lay.layer, lay.qdesc, x)
+        wy, wex, wwt, wlg = lay.oracle(orc, x)
+        assert np.array_equal(lg.view(np.uint32), wlg.view(np.uint32)) and np.array_equal(ex, wex)
+        assert np.array_equal(wt.view(np.uint32), wwt.view(np.uint32))
+        stable_plan_check(orc, plan, ex, 64)
+        tol_check(orc, y, wy)
+    finally:
+        lay.close()
+
+
+def test_prefill_grouped_matches_verify_rows(gpu, q38, orc):
+    """The same rows through the grouped kernels at prefill width (40 rows) and at verify
+    width (the first 16 rows alone): outputs within the MoE tolerance of each other, routing
+    identical."""
+    d = q38.desc(gu_group=64, down_group=64)
+    L = q38.MoeLayer(gpu, d, seed=SEED, layer=5)
+    try:
+        x = orc.rmsnorm(orc.embed(SEED, tokens(40), 2048))
+        y, ex, wt, lg, _ = run_forward(q38, L, d, x)
+        y16, ex16, wt16, lg16, _ = run_forward(q38, L, d, x[:16])
+        assert np.array_equal(ex[:16], ex16) and np.array_equal(wt[:16].view(np.uint32), wt16.view(np.uint32))
+        tol_check(orc, y[:16], y16)
+    finally:
+        L.close()
