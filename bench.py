@@ -169,7 +169,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
-                                   "(see DESIGN.md for how the round would shard)", "n_gpus": args.gpus}))
+                                   "(how the round would shard is described with the design)", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import torch

@@ -465,6 +465,58 @@ const uint16_t* q38_slot_hidden(const q38_slot* slot);
  * reference consumes the verification's own rows, src/mtp_verifier.cpp:129-145). */
 uint64_t q38_slot_generation(const q38_slot* slot);
 
+/* ---- GatedDeltaNet verify step (the linear-attention half of a decoder layer):
+ * GatedDeltaNet::forward_verify (src/gated_delta_net.cpp:657-834) for S rows
+ * (1..64) from an origin state, with the state after every row as that row's checkpoint; the
+ * caller commits a round by taking the checkpoint of its last accepted row as the next
+ * origin (q38_gdn_commit). Weights are the reference checkpoint's tensors as stored
+ * (src/gated_delta_net.cpp:138-178): in_proj_qkv [C, H], in_proj_z [HV DV, H], in_proj_b
+ * [HV, H], in_proj_a [HV, H] and out_proj [H, HV DV] MLX affine-quantized (packed u32 weight,
+ * scales and biases [out][in / group] bf16 or fp16), conv1d.weight [C, 4] bf16 (MLX
+ * [C, 4, 1]), A_log [HV] fp32, dt_bias [HV] bf16, norm.weight [DV] bf16; C = 2 HK DK + HV DV.
+ * A state (q38_gdn_state_bytes) is the convolution rows [3][C] bf16 followed by the
+ * recurrent state [HV][DV][DK] bf16 (GatedDeltaNetState's convolution and recurrent arrays,
+ * include/qwen38/gated_delta_net.hpp:28-37). */
+typedef struct q38_gdn q38_gdn;
+typedef struct q38_gdn_desc {
+    int32_t hidden;        /* H: a multiple of the group and of 32                          */
+    int32_t key_heads;     /* HK (linear_num_key_heads)                                     */
+    int32_t value_heads;   /* HV, a multiple of HK (value head h reads key head h / (HV/HK)) */
+    int32_t key_dim;       /* DK = DV: 64, 128 or 256                                       */
+    int32_t value_dim;     /* DV                                                            */
+    int32_t conv_kernel;   /* 4 (linear_conv_kernel_dim)                                    */
+    int32_t bits;          /* 2, 4 or 8                                                     */
+    int32_t group;         /* 32, 64 or 128                                                 */
+    int32_t scale_dtype;   /* 0 bf16, 1 fp16 scales and biases                              */
+    int32_t gate_silu;     /* output_gate_type: 0 "sigmoid", 1 "silu"                       */
+    float eps;             /* rms_norm_eps of the output norm                               */
+} q38_gdn_desc;
+typedef struct q38_gdn_weights {
+    const uint32_t* weight[5];  /* qkv, z, b, a, out                                         */
+    const uint16_t* scales[5];
+    const uint16_t* biases[5];
+    const uint16_t* conv;       /* [C][4] bf16                                               */
+    const float* a_log;         /* [HV]                                                      */
+    const uint16_t* dt_bias;    /* [HV] bf16                                                 */
+    const uint16_t* norm;       /* [DV] bf16                                                 */
+} q38_gdn_weights;
+/* GatedDeltaNet::GatedDeltaNet (src/gated_delta_net.cpp:138-178): adopts the device weight
+ * pointers (they must stay alive). */
+int q38_gdn_create(q38_ctx* ctx, const q38_gdn_desc* desc, const q38_gdn_weights* weights, q38_gdn** out);
+void q38_gdn_destroy(q38_gdn* gdn);
+/* Bytes of one state (the origin and each checkpoint). */
+size_t q38_gdn_state_bytes(const q38_gdn* gdn);
+size_t q38_gdn_workspace_size(const q38_gdn* gdn, int32_t max_rows);
+/* GatedDeltaNet::forward_verify: x [rows, H] bf16 -> out [rows, H] bf16; origin: a state, or
+ * null for the zero state of an uninitialised one; checkpoints: rows states, the state after
+ * each row (may be null when not needed). */
+int q38_gdn_verify(q38_gdn* gdn, const uint16_t* x, int32_t rows, const void* origin, void* checkpoints,
+                   uint16_t* out, void* workspace, size_t workspace_bytes, void* stream);
+/* The commit of a verify round for this layer's state (the checkpoint of the last accepted
+ * row becomes the state, src/gated_delta_net.cpp:825-831 with the verifier's commit,
+ * src/mtp_verifier.cpp:129-145): copies checkpoints[row] to state on the stream. */
+int q38_gdn_commit(const q38_gdn* gdn, const void* checkpoints, int32_t row, void* state, void* stream);
+
 /* ------------------------------------------------------------------ HyperConnection mixer
  * The stream mixer around a decoder block (HyperConnection, include/qwen38/hyper_connection.hpp:18-40,
  * src/hyper_connection.cpp:150-211 for the weights, :309-493 read, :692-709 write). A row's state

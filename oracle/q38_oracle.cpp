@@ -39,6 +39,11 @@
 //   HyperConnection mixer  independent numpy restatement, closed forms (zero and bias-only
 //                          projections, packed-value order, the 1 + w norm weight, sign-only
 //                          streams, injection of 1 and 2 in the write).
+//   GatedDeltaNet verify   independent numpy restatement (float64 state, vectorised per
+//                          head), closed forms (one row from a zero state: state = beta v k^T,
+//                          output beta v (k . q); beta 0: the state decays by g per row;
+//                          one-hot conv taps), S rows = S single-row calls chained through
+//                          the checkpoints; a planted wrong key-head mapping fails them.
 
 #include <pthread.h>
 #include <sched.h>
@@ -1013,6 +1018,177 @@ int64_t draw(const std::vector<double>& w, double v) {
     return last < 0 ? 0 : last;
 }
 
+
+// ---------------------------------------------------------------- GatedDeltaNet verify
+// GatedDeltaNet::forward_verify (src/gated_delta_net.cpp:657-834): the linear-attention half
+// of a decoder layer for S rows (1..64) from an origin state, with the state after every
+// row kept as that row's checkpoint. The rounding points restate the ops of that path:
+//   qkv, z, b, a   T(quantized_matmul) (affine_row_dot, double accumulation)
+//   conv1d         depthwise, width 4 over [origin conv rows ; qkv rows]: T(sum_j w[c][j] *
+//                  in[t + j][c]) (:691-692), then silu = T(c * T(sigmoid(c))) (MlxArray::silu,
+//                  src/mlx_backend.cpp:621-624)
+//   q, k           rms_norm with unit weight over the head dimension (:709-710):
+//                  T(x * 1/sqrt(mean(x^2) + 1e-6)), then q = T(q * bf16(1/DK)),
+//                  k = T(k * bf16(1/sqrt(DK))) (:711-716); value head h reads key head
+//                  h / (HV / HK) (repeat_axis, :717-719)
+//   beta           T(sigmoid(b)) (:721); decay T(exp(-(exp(A_log) * softplus(T(a + dt_bias)))))
+//                  with softplus = log1p(exp(.)) in float (:722-725)
+//   recurrence     the bf16-sum verify kernel (src/gdn_metal_kernels.hpp:498-562): per value
+//                  head and value row, 32 lanes of DK/32 state items, every product, lane sum,
+//                  residual, delta, update and state rounded to bf16 as there; the 32 lanes'
+//                  partial sums (simd_sum there) are added in float by an xor butterfly
+//                  (lane offsets 16, 8, 4, 2, 1) and rounded once — the order is this build's
+//                  contract (Metal's simd_sum order is not specified: parity unpinned there)
+//   output         rms_norm(y, norm_weight, eps) = T(w * T(y * inv)) per value head
+//                  (:809 / :824), gate T(sigmoid(z)) or silu T(z * T(sigmoid(z))), their product
+//                  T, then T(quantized_matmul(out_proj)) (:829-833)
+//   checkpoints    after row t: conv rows t+1..t+3 of [origin ; qkv] and the recurrent state
+//                  (:825-831).
+struct GdnDesc {
+    int hidden, hk, hv, dk, dv, conv, bits, group, fmt, gate_silu;
+    float eps;
+};
+struct GdnW {
+    AffineProj qkv, z, b, a, out;
+    const uint16_t* conv_w;  // [C][4] bf16
+    const float* a_log;      // [HV]
+    const uint16_t* dt_bias; // [HV] bf16
+    const uint16_t* norm_w;  // [DV] bf16
+};
+int g_gdn_fault;  // planted faults (tests only): 1 = value head h reads key head h % HK
+inline float tb(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+inline float sigmoid_t(float x) { return tb(static_cast<float>(1.0 / (1.0 + std::exp(-static_cast<double>(x))))); }
+
+// The recurrence of S rows (the bf16-sum kernel's rounding points, above): q, k [S][HK][DK],
+// v [S][HV][DV], decay / beta [S][HV] (bf16 values); state_in [HV][DV][DK] bf16 or null (zero);
+// y [S][HV][DV]; the state after row t at state_rows + t * row_stride when given.
+void gdn_recurrence(int HK, int HV, int DK, int DV, int S, const float* q, const float* k, const float* v,
+                    const float* decay, const float* beta, const uint16_t* state_in, float* y, uint16_t* state_rows,
+                    size_t row_stride) {
+    const int KW = HK * DK, VW = HV * DV, rep = HV / HK, items = DK / 32;
+    for (int h = 0; h < HV; ++h) {
+        const int hk = g_gdn_fault == 1 ? h % HK : h / rep;
+        for (int r = 0; r < DV; ++r) {
+            std::vector<float> st(DK);
+            for (int i = 0; i < DK; ++i)
+                st[i] = state_in ? bf16_to_f32(state_in[(static_cast<size_t>(h) * DV + r) * DK + i]) : 0.0f;
+            for (int t = 0; t < S; ++t) {
+                const float g = decay[static_cast<size_t>(t) * HV + h], bt = beta[static_cast<size_t>(t) * HV + h];
+                const float* kr = k + static_cast<size_t>(t) * KW + hk * DK;
+                const float* qr = q + static_cast<size_t>(t) * KW + hk * DK;
+                float part[32];
+                for (int l = 0; l < 32; ++l) {
+                    float acc = 0.0f;
+                    for (int i = 0; i < items; ++i) {
+                        const int ix = l * items + i;
+                        st[ix] = tb(st[ix] * g);
+                        acc = tb(acc + tb(st[ix] * kr[ix]));
+                    }
+                    part[l] = acc;
+                }
+                auto lane_sum = [&](float* pp) {
+                    for (int off = 16; off > 0; off >>= 1) {
+                        float nx[32];
+                        for (int l = 0; l < 32; ++l) nx[l] = pp[l] + pp[l ^ off];
+                        std::memcpy(pp, nx, sizeof(nx));
+                    }
+                    return tb(pp[0]);
+                };
+                const float recalled = lane_sum(part);
+                const float delta = tb(tb(v[static_cast<size_t>(t) * VW + h * DV + r] - recalled) * bt);
+                for (int l = 0; l < 32; ++l) {
+                    float acc = 0.0f;
+                    for (int i = 0; i < items; ++i) {
+                        const int ix = l * items + i;
+                        st[ix] = tb(st[ix] + tb(kr[ix] * delta));
+                        acc = tb(acc + tb(st[ix] * qr[ix]));
+                    }
+                    part[l] = acc;
+                }
+                y[static_cast<size_t>(t) * VW + h * DV + r] = lane_sum(part);
+                if (state_rows) {
+                    uint16_t* cs = state_rows + static_cast<size_t>(t) * row_stride + (static_cast<size_t>(h) * DV + r) * DK;
+                    for (int i = 0; i < DK; ++i) cs[i] = f32_to_bf16(st[i]);
+                }
+            }
+        }
+    }
+}
+
+// state: conv [3][C] bf16 then recurrent [HV][DV][DK] bf16
+void gdn_verify(const GdnDesc& d, const GdnW& W, const uint16_t* x, int S, const uint16_t* origin, uint16_t* out,
+                uint16_t* ckpt) {
+    const int H = d.hidden, HK = d.hk, HV = d.hv, DK = d.dk, DV = d.dv;
+    const int KW = HK * DK, VW = HV * DV, C = 2 * KW + VW;
+    const size_t state_elems = static_cast<size_t>(3) * C + static_cast<size_t>(HV) * DV * DK;
+    std::vector<float> xf(H), qkv(static_cast<size_t>(S + 3) * C), z(static_cast<size_t>(S) * VW),
+        beta(static_cast<size_t>(S) * HV), decay(static_cast<size_t>(S) * HV), q(static_cast<size_t>(S) * KW),
+        k(static_cast<size_t>(S) * KW), v(static_cast<size_t>(S) * VW), y(static_cast<size_t>(S) * VW),
+        gated(static_cast<size_t>(S) * VW);
+    for (int i = 0; i < 3 * C; ++i) qkv[i] = origin ? bf16_to_f32(origin[i]) : 0.0f;
+    for (int t = 0; t < S; ++t) {
+        for (int c = 0; c < H; ++c) xf[c] = bf16_to_f32(x[static_cast<size_t>(t) * H + c]);
+        for (int c = 0; c < C; ++c) qkv[static_cast<size_t>(t + 3) * C + c] = rbf16(affine_row_dot(W.qkv, c, xf.data()));
+        for (int c = 0; c < VW; ++c) z[static_cast<size_t>(t) * VW + c] = rbf16(affine_row_dot(W.z, c, xf.data()));
+        for (int h = 0; h < HV; ++h) {
+            const float b = rbf16(affine_row_dot(W.b, h, xf.data()));
+            const float a = rbf16(affine_row_dot(W.a, h, xf.data()));
+            beta[static_cast<size_t>(t) * HV + h] = sigmoid_t(b);
+            const float biased = tb(a + bf16_to_f32(W.dt_bias[h]));
+            const double softplus = std::log1p(std::exp(static_cast<double>(biased)));
+            const double rate = std::exp(static_cast<double>(W.a_log[h]));
+            decay[static_cast<size_t>(t) * HV + h] = rbf16(std::exp(-(static_cast<double>(static_cast<float>(rate)) *
+                                                                        static_cast<float>(softplus))));
+        }
+        // conv + silu, then the q / k norms per head
+        std::vector<float> act(C);
+        for (int c = 0; c < C; ++c) {
+            float acc = 0.0f;
+            for (int j = 0; j < 4; ++j)
+                acc = std::fma(bf16_to_f32(W.conv_w[static_cast<size_t>(c) * 4 + j]),
+                               qkv[static_cast<size_t>(t + j) * C + c], acc);
+            const float cv = tb(acc);
+            act[c] = tb(cv * sigmoid_t(cv));
+        }
+        const float ks = tb(static_cast<float>(1.0 / std::sqrt(static_cast<double>(DK))));
+        const float qs = tb(static_cast<float>(1.0 / DK));
+        for (int part = 0; part < 2; ++part)
+            for (int h = 0; h < HK; ++h) {
+                const float* a = act.data() + part * KW + h * DK;
+                double ss = 0.0;
+                for (int i = 0; i < DK; ++i) ss += static_cast<double>(a[i]) * a[i];
+                const float inv = static_cast<float>(1.0 / std::sqrt(ss / DK + 1e-6));
+                float* dst = (part ? k.data() : q.data()) + static_cast<size_t>(t) * KW + h * DK;
+                for (int i = 0; i < DK; ++i) dst[i] = tb(tb(a[i] * inv) * (part ? ks : qs));
+            }
+        for (int c = 0; c < VW; ++c) v[static_cast<size_t>(t) * VW + c] = act[2 * KW + c];
+    }
+    gdn_recurrence(HK, HV, DK, DV, S, q.data(), k.data(), v.data(), decay.data(), beta.data(),
+                   origin ? origin + static_cast<size_t>(3) * C : nullptr, y.data(),
+                   ckpt ? ckpt + static_cast<size_t>(3) * C : nullptr, state_elems);
+    // norm and gate per (row, value head), then the output projection
+    for (int t = 0; t < S; ++t) {
+        for (int h = 0; h < HV; ++h) {
+            const float* yr = y.data() + static_cast<size_t>(t) * VW + h * DV;
+            double ss = 0.0;
+            for (int i = 0; i < DV; ++i) ss += static_cast<double>(yr[i]) * yr[i];
+            const float inv = static_cast<float>(1.0 / std::sqrt(ss / DV + static_cast<double>(d.eps)));
+            for (int i = 0; i < DV; ++i) {
+                const float nrm = tb(bf16_to_f32(W.norm_w[i]) * tb(yr[i] * inv));
+                const float zz = z[static_cast<size_t>(t) * VW + h * DV + i];
+                const float gate = d.gate_silu ? tb(zz * sigmoid_t(zz)) : sigmoid_t(zz);
+                gated[static_cast<size_t>(t) * VW + h * DV + i] = tb(nrm * gate);
+            }
+        }
+        for (int o = 0; o < H; ++o)
+            out[static_cast<size_t>(t) * H + o] = f32_to_bf16(rbf16(affine_row_dot(W.out, o, gated.data() + static_cast<size_t>(t) * VW)));
+        if (ckpt) {
+            uint16_t* cc = ckpt + static_cast<size_t>(t) * state_elems;
+            for (int j = 0; j < 3; ++j)
+                for (int c = 0; c < C; ++c) cc[static_cast<size_t>(j) * C + c] = f32_to_bf16(qkv[static_cast<size_t>(t + 1 + j) * C + c]);
+        }
+    }
+}
 } // namespace
 
 // ======================================================================== C ABI
@@ -1403,6 +1579,38 @@ int orc_hc_read(const HcDesc* d, const uint16_t* norm, const uint32_t* dw, const
 void orc_hc_write(int H, int HC, int M, const uint16_t* stream, const uint16_t* block, const uint16_t* inj,
                   uint16_t* out) {
     hc_write(H, HC, M, stream, block, inj, out);
+}
+
+
+// ---- GatedDeltaNet verify (GdnDesc: hidden, hk, hv, dk, dv, conv, bits, group, fmt, gate_silu, eps)
+void orc_gdn_plant_fault(int code) { g_gdn_fault = code; }
+// The recurrence alone (bf16 values as floats; state_in / state_rows bf16 bits).
+int orc_gdn_recurrence(int HK, int HV, int DK, int DV, int S, const float* q, const float* k, const float* v,
+                       const float* decay, const float* beta, const uint16_t* state_in, float* y, uint16_t* state_rows) {
+    if (HK < 1 || HV % HK || DK % 32 || S < 1) return -1;
+    gdn_recurrence(HK, HV, DK, DV, S, q, k, v, decay, beta, state_in, y, state_rows,
+                   static_cast<size_t>(HV) * DV * DK);
+    return 0;
+}
+int orc_gdn_verify(const GdnDesc* d, const uint32_t* const* w, const uint16_t* const* sc, const uint16_t* const* bi,
+                   const uint16_t* conv_w, const float* a_log, const uint16_t* dt_bias, const uint16_t* norm_w,
+                   const uint16_t* x, int S, const uint16_t* origin, uint16_t* out, uint16_t* ckpt) {
+    if (!d || S < 1 || d->conv != 4 || d->dk % 32 || d->hv % d->hk || d->bits <= 0 || 32 % d->bits || d->group <= 0)
+        return -1;
+    const int KW = d->hk * d->dk, VW = d->hv * d->dv, C = 2 * KW + VW;
+    GdnW W{};
+    const int ins[5] = {d->hidden, d->hidden, d->hidden, d->hidden, VW}, outs[5] = {C, VW, d->hv, d->hv, d->hidden};
+    AffineProj* P[5] = {&W.qkv, &W.z, &W.b, &W.a, &W.out};
+    for (int p = 0; p < 5; ++p) {
+        if (ins[p] % d->group) return -1;
+        *P[p] = AffineProj{w[p], sc[p], bi[p], ins[p], outs[p], d->bits, d->group, d->fmt};
+    }
+    W.conv_w = conv_w;
+    W.a_log = a_log;
+    W.dt_bias = dt_bias;
+    W.norm_w = norm_w;
+    gdn_verify(*d, W, x, S, origin, out, ckpt);
+    return 0;
 }
 
 } // extern "C"

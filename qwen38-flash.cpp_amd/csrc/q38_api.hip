@@ -626,6 +626,116 @@ static int create_synthetic_mixed(q38_ctx* ctx, const q38_moe_desc& d, uint64_t 
     return Q38_OK;
 }
 
+// ------------------------------------------------------------------ GatedDeltaNet verify
+struct q38_gdn {
+    q38_ctx* ctx;
+    q38_gdn_desc desc;
+    GdnDev dev;
+    size_t state_elems;
+};
+
+int q38_gdn_create(q38_ctx* ctx, const q38_gdn_desc* desc, const q38_gdn_weights* w, q38_gdn** out) {
+    if (!ctx || !desc || !w || !out) return fail(Q38_EINVAL, "q38_gdn_create: null argument");
+    const q38_gdn_desc& d = *desc;
+    // the reference's own checks (src/gated_delta_net.cpp:169-177), then what the kernels take
+    if (d.key_heads <= 0 || d.value_heads <= 0 || d.key_dim <= 0 || d.value_dim <= 0 || d.hidden <= 0)
+        return fail(Q38_EINVAL, "GatedDeltaNet dimensions must be positive");
+    if (d.value_heads % d.key_heads != 0) return fail(Q38_EINVAL, "value heads must be divisible by key heads");
+    if (d.conv_kernel != 4)
+        return fail(Q38_EINVAL, "the retained Qwen3.8 checkpoint requires convolution width 4");
+    if (d.bits != 2 && d.bits != 4 && d.bits != 8) return fail(Q38_EINVAL, "GatedDeltaNet projections: bits must be 2, 4 or 8");
+    if (d.group != 32 && d.group != 64 && d.group != 128)
+        return fail(Q38_EINVAL, "GatedDeltaNet projections: group must be 32, 64 or 128");
+    if (d.scale_dtype != 0 && d.scale_dtype != 1) return fail(Q38_EINVAL, "scale_dtype must be 0 (bf16) or 1 (fp16)");
+    if (d.gate_silu != 0 && d.gate_silu != 1) return fail(Q38_EINVAL, "gate_silu must be 0 (sigmoid) or 1 (silu)");
+    if (!(d.eps > 0.0f)) return fail(Q38_EINVAL, "eps must be positive");
+    const int VW = d.value_heads * d.value_dim;
+    if (d.hidden % d.group || VW % d.group || d.hidden % 32 || d.hidden > 8192 || VW > 16384)
+        return fail(Q38_EINVAL, "hidden and HV * DV must be multiples of the group (hidden <= 8192, HV * DV <= 16384)");
+    GdnDev G{};
+    G.hidden = d.hidden;
+    G.hk = d.key_heads;
+    G.hv = d.value_heads;
+    G.dk = d.key_dim;
+    G.dv = d.value_dim;
+    G.bits = d.bits;
+    G.group = d.group;
+    G.f16 = d.scale_dtype;
+    G.gate_silu = d.gate_silu;
+    G.eps = d.eps;
+    if (!gdn_geometry_ok(G)) return fail(Q38_EINVAL, "GatedDeltaNet: key_dim = value_dim of 64, 128 or 256");
+    for (int p = 0; p < 5; ++p) {
+        if (!w->weight[p] || !w->scales[p] || !w->biases[p]) return fail(Q38_EINVAL, "q38_gdn_create: null projection");
+        G.w[p] = w->weight[p];
+        G.s[p] = w->scales[p];
+        G.b[p] = w->biases[p];
+    }
+    if (!w->conv || !w->a_log || !w->dt_bias || !w->norm) return fail(Q38_EINVAL, "q38_gdn_create: null tensor");
+    G.conv_w = w->conv;
+    G.a_log = w->a_log;
+    G.dt_bias = w->dt_bias;
+    G.norm_w = w->norm;
+    const size_t C = 2 * static_cast<size_t>(d.key_heads) * d.key_dim + static_cast<size_t>(VW);
+    *out = new q38_gdn{ctx, d, G, 3 * C + static_cast<size_t>(VW) * d.key_dim};
+    return Q38_OK;
+}
+
+void q38_gdn_destroy(q38_gdn* gdn) { delete gdn; }
+
+size_t q38_gdn_state_bytes(const q38_gdn* gdn) { return gdn ? gdn->state_elems * 2 : 0; }
+
+static size_t gdn_ws(const q38_gdn* g, int S, GdnBufs* b, void* base) {
+    const q38_gdn_desc& d = g->desc;
+    const size_t KW = static_cast<size_t>(d.key_heads) * d.key_dim, VW = static_cast<size_t>(d.value_heads) * d.value_dim;
+    const size_t C = 2 * KW + VW, HV = static_cast<size_t>(d.value_heads);
+    size_t off = 0;
+    char* p = static_cast<char*>(base);
+    auto take = [&](size_t bytes) {
+        char* q = p ? p + off : nullptr;
+        off += align256(bytes);
+        return q;
+    };
+    GdnBufs t{};
+    t.qkv = reinterpret_cast<uint16_t*>(take(S * C * 2));
+    t.z = reinterpret_cast<uint16_t*>(take(S * VW * 2));
+    t.bpr = reinterpret_cast<uint16_t*>(take(S * HV * 2));
+    t.apr = reinterpret_cast<uint16_t*>(take(S * HV * 2));
+    t.q = reinterpret_cast<uint16_t*>(take(S * KW * 2));
+    t.k = reinterpret_cast<uint16_t*>(take(S * KW * 2));
+    t.v = reinterpret_cast<uint16_t*>(take(S * VW * 2));
+    t.beta = reinterpret_cast<float*>(take(S * HV * 4));
+    t.decay = reinterpret_cast<float*>(take(S * HV * 4));
+    t.y = reinterpret_cast<uint16_t*>(take(S * VW * 2));
+    t.gated = reinterpret_cast<uint16_t*>(take(S * VW * 2));
+    if (b) *b = t;
+    return off;
+}
+
+size_t q38_gdn_workspace_size(const q38_gdn* gdn, int32_t max_rows) {
+    if (!gdn || max_rows < 1 || max_rows > 64) return 0;
+    return gdn_ws(gdn, max_rows, nullptr, nullptr);
+}
+
+int q38_gdn_verify(q38_gdn* gdn, const uint16_t* x, int32_t rows, const void* origin, void* checkpoints,
+                   uint16_t* out, void* ws, size_t ws_bytes, void* stream) {
+    if (!gdn || !x || !out) return fail(Q38_EINVAL, "q38_gdn_verify: null argument");
+    if (rows < 1 || rows > 64) return fail(Q38_EINVAL, "GatedDeltaNet batch requires shape [1,S,hidden], S=1..64");
+    GdnBufs b{};
+    if (!ws || ws_bytes < gdn_ws(gdn, rows, &b, ws)) return fail(Q38_ESPACE, "workspace too small");
+    Q38_HIP(launch_gdn_verify(gdn->dev, b, rows, x, static_cast<const uint16_t*>(origin),
+                              static_cast<uint16_t*>(checkpoints), out, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+int q38_gdn_commit(const q38_gdn* gdn, const void* checkpoints, int32_t row, void* state, void* stream) {
+    if (!gdn || !checkpoints || !state) return fail(Q38_EINVAL, "q38_gdn_commit: null argument");
+    if (row < 0 || row >= 64) return fail(Q38_EINVAL, "q38_gdn_commit: row must be 0..63");
+    const size_t bytes = gdn->state_elems * 2;
+    Q38_HIP(hipMemcpyAsync(state, static_cast<const char*>(checkpoints) + bytes * static_cast<size_t>(row), bytes,
+                           hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
 void q38_moe_layer_destroy(q38_moe_layer* layer) {
     if (!layer) return;
     if (layer->owned) (void)hipFree(layer->owned);

@@ -1,0 +1,304 @@
+// q38_gdn.hip — the GatedDeltaNet verify step: the linear-attention half of a decoder layer
+// for S verify rows (1..64) from an origin state, keeping the state after every row as that
+// row's checkpoint (GatedDeltaNet::forward_verify, src/gated_delta_net.cpp:657-834).
+//
+// Five launches:
+//   k_gdn_proj      the affine projections qkv, z, b (beta) and a (decay) of the S rows in
+//                   one launch: a workgroup takes a block of one projection's weight rows for
+//                   up to 16 staged rows; outputs rounded to bf16 (quantized_matmul's output);
+//   k_gdn_prework   per (row, head): the depthwise width-4 convolution over [origin conv rows ;
+//                   qkv rows] and SiLU (T(c * T(sigmoid c))), the q / k RMS norms with the
+//                   1/DK and 1/sqrt(DK) scales, v, and per value head beta = T(sigmoid b) and
+//                   decay = T(exp(-exp(A_log) * softplus(T(a + dt_bias)))); the conv rows of
+//                   every checkpoint;
+//   k_gdn_recur     the delta-rule recurrence with the reference's bf16-sum rounding points
+//                   (src/gdn_metal_kernels.hpp:498-562): one 64-lane wave per two value rows of
+//                   a value head, 32 lanes per row with DK / 32 state items each, the state in
+//                   registers across the S rows; every product, lane sum, residual, delta,
+//                   update and state value rounded to bf16, the 32 lanes' sums added in float
+//                   by an xor butterfly (offsets 16..1) and rounded once; writes y and the
+//                   recurrent part of every row's checkpoint;
+//   k_gdn_norm_gate per (row, value head): T(w * T(y / rms(y))) times the gate T(sigmoid z)
+//                   or SiLU T(z * T(sigmoid z)), rounded (:809, :824-833);
+//   k_gdn_proj      the output projection.
+// A state (q38_gdn_state_bytes) is the conv rows [3][C] bf16 followed by the recurrent state
+// [HV][DV][DK] bf16, C = 2 HK DK + HV DV; value head h reads key head h / (HV / HK).
+#include "q38_affine.hpp"
+
+namespace q38 {
+
+namespace {
+
+__device__ __forceinline__ float tbf(float v) { return bf2f(f2bf(v)); }
+__device__ __forceinline__ float sigmoid_bf(float x) { return tbf(1.0f / (1.0f + expf(-x))); }
+
+// One projection of a k_gdn_proj launch: weight rows [out, IN], destination rows of stride
+// dst_stride (bf16).
+struct GdnProj {
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+    uint16_t* dst;
+    int out, dst_stride, first_block;
+};
+struct GdnProjSet {
+    GdnProj p[4];
+    int n;
+};
+
+// Weight rows per workgroup: 4 waves x (64 / LPR) rows.
+template <int LPR>
+constexpr int proj_rows_per_wg() {
+    return kSaThreads / 64 * (64 / LPR);
+}
+
+template <int BITS, int LPR>
+__global__ __launch_bounds__(kSaThreads) void k_gdn_proj(GdnProjSet set, const uint16_t* __restrict__ x, int S,
+                                                         int IN, int G, int f16, int rows_wg) {
+    extern __shared__ __align__(16) uint16_t xs[];  // [rows_wg][IN]
+    const int r0 = blockIdx.y * rows_wg, nr = S - r0 < rows_wg ? S - r0 : rows_wg;
+    // the projection of this block (uniform selects over the argument block)
+    const int bx = static_cast<int>(blockIdx.x);
+    const int pi = set.n > 3 && bx >= set.p[3].first_block ? 3
+                   : set.n > 2 && bx >= set.p[2].first_block ? 2
+                   : set.n > 1 && bx >= set.p[1].first_block ? 1
+                                                             : 0;
+    const GdnProj P = pi == 3 ? set.p[3] : pi == 2 ? set.p[2] : pi == 1 ? set.p[1] : set.p[0];
+    sa_stage(x, IN, r0, nr, xs);
+    __syncthreads();
+    constexpr int OPW = 64 / LPR;
+    const int o = ((bx - P.first_block) * (kSaThreads / 64) + (threadIdx.x >> 6)) * OPW + (threadIdx.x & 63) / LPR;
+    if (o >= P.out) return;
+    const int wpr = IN * BITS / 32, ngrp = IN / G;
+    float acc[kSaRows];
+    sa_row_dot<BITS, LPR>(P.w + static_cast<size_t>(o) * wpr, P.s + static_cast<size_t>(o) * ngrp,
+                          P.b + static_cast<size_t>(o) * ngrp, IN, G, f16, xs, nr, acc);
+    if ((threadIdx.x & 63) % LPR == 0)
+#pragma unroll
+        for (int r = 0; r < kSaRows; ++r)
+            if (r < nr) P.dst[static_cast<size_t>(r0 + r) * P.dst_stride + o] = f2bf(acc[r]);
+}
+
+// conv + SiLU of row t, channels cb + lane * CPL + i; q / k heads normalised.
+template <int CPL>
+__global__ __launch_bounds__(64) void k_gdn_prework(GdnDev G, GdnBufs B, int S, const uint16_t* __restrict__ origin,
+                                                    uint16_t* __restrict__ ckpt, size_t state_elems) {
+    const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int HK = G.hk, HV = G.hv, DK = G.dk, DV = G.dv, KW = HK * DK, VW = HV * DV, C = 2 * KW + VW;
+    const int role = head < HK ? 0 : head < 2 * HK ? 1 : 2;  // q, k, v
+    const int h = role == 0 ? head : role == 1 ? head - HK : head - 2 * HK;
+    const int cb = role == 0 ? h * DK : role == 1 ? KW + h * DK : 2 * KW + h * DV;
+    auto cin = [&](int r, int c) {  // row r of [origin conv rows ; qkv rows]
+        if (r >= 3) return bf2f(B.qkv[static_cast<size_t>(r - 3) * C + c]);
+        return origin ? bf2f(origin[static_cast<size_t>(r) * C + c]) : 0.0f;
+    };
+    float act[CPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = cb + lane * CPL + i;
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = fmaf(bf2f(G.conv_w[static_cast<size_t>(c) * 4 + j]), cin(t + j, c), acc);
+        const float cv = tbf(acc);
+        act[i] = tbf(cv * sigmoid_bf(cv));
+        ss = fmaf(act[i], act[i], ss);
+        if (ckpt)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) ckpt[static_cast<size_t>(t) * state_elems + static_cast<size_t>(j) * C + c] =
+                                             f2bf(cin(t + 1 + j, c));
+    }
+    if (role < 2) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        const float inv = 1.0f / sqrtf(ss / static_cast<float>(DK) + 1e-6f);
+        const float scale = role == 0 ? tbf(1.0f / static_cast<float>(DK)) : tbf(1.0f / sqrtf(static_cast<float>(DK)));
+        uint16_t* dst = (role == 0 ? B.q : B.k) + static_cast<size_t>(t) * KW + h * DK + lane * CPL;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) dst[i] = f2bf(tbf(act[i] * inv) * scale);
+    } else {
+        uint16_t* dst = B.v + static_cast<size_t>(t) * VW + h * DV + lane * CPL;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) dst[i] = f2bf(act[i]);
+        if (lane == 0) {
+            const size_t at = static_cast<size_t>(t) * HV + h;
+            B.beta[at] = sigmoid_bf(bf2f(B.bpr[at]));
+            const float biased = tbf(bf2f(B.apr[at]) + bf2f(G.dt_bias[h]));
+            const float softplus = log1pf(expf(biased));
+            const float rate = expf(G.a_log[h]);
+            B.decay[at] = tbf(expf(-(rate * softplus)));
+        }
+    }
+}
+
+// Lane sum of the 32 lanes of each half-wave in float (xor butterfly 16..1), rounded.
+__device__ __forceinline__ float half_wave_sum(float v) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return tbf(v);
+}
+
+template <int ITEMS>
+__global__ __launch_bounds__(64) void k_gdn_recur(GdnDev G, GdnBufs B, int S, const uint16_t* __restrict__ origin,
+                                                  uint16_t* __restrict__ ckpt, size_t state_elems) {
+    const int HK = G.hk, HV = G.hv, DK = G.dk, DV = G.dv, KW = HK * DK, VW = HV * DV, C = 2 * KW + VW;
+    const int hv = blockIdx.y, lane = threadIdx.x, sl = lane & 31;
+    const int dv = blockIdx.x * 2 + (lane >> 5);
+    const int hk = hv / (HV / HK);
+    const size_t rec = static_cast<size_t>(3) * C + (static_cast<size_t>(hv) * DV + dv) * DK + sl * ITEMS;
+    float st[ITEMS];
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) st[i] = origin ? bf2f(origin[rec + i]) : 0.0f;
+    for (int t = 0; t < S; ++t) {
+        const float g = B.decay[static_cast<size_t>(t) * HV + hv], bt = B.beta[static_cast<size_t>(t) * HV + hv];
+        const uint16_t* kr = B.k + static_cast<size_t>(t) * KW + hk * DK + sl * ITEMS;
+        const uint16_t* qr = B.q + static_cast<size_t>(t) * KW + hk * DK + sl * ITEMS;
+        float kv[ITEMS], qv[ITEMS];
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) {
+            kv[i] = bf2f(kr[i]);
+            qv[i] = bf2f(qr[i]);
+        }
+        const float vv = bf2f(B.v[static_cast<size_t>(t) * VW + hv * DV + dv]);
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) {
+            st[i] = tbf(st[i] * g);
+            acc = tbf(acc + tbf(st[i] * kv[i]));
+        }
+        const float recalled = half_wave_sum(acc);
+        const float delta = tbf(tbf(vv - recalled) * bt);
+        acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) {
+            st[i] = tbf(st[i] + tbf(kv[i] * delta));
+            acc = tbf(acc + tbf(st[i] * qv[i]));
+        }
+        const float y = half_wave_sum(acc);
+        if (sl == 0) B.y[static_cast<size_t>(t) * VW + hv * DV + dv] = f2bf(y);
+        if (ckpt)
+#pragma unroll
+            for (int i = 0; i < ITEMS; ++i) ckpt[static_cast<size_t>(t) * state_elems + rec + i] = f2bf(st[i]);
+    }
+}
+
+template <int CPL>
+__global__ __launch_bounds__(64) void k_gdn_norm_gate(GdnDev G, GdnBufs B, int S) {
+    const int hv = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int DV = G.dv, VW = G.hv * DV;
+    const size_t base = static_cast<size_t>(t) * VW + hv * DV + lane * CPL;
+    float y[CPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        y[i] = bf2f(B.y[base + i]);
+        ss = fmaf(y[i], y[i], ss);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(DV) + G.eps);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const float nrm = tbf(bf2f(G.norm_w[lane * CPL + i]) * tbf(y[i] * inv));
+        const float z = bf2f(B.z[base + i]);
+        const float gate = G.gate_silu ? tbf(z * sigmoid_bf(z)) : sigmoid_bf(z);
+        B.gated[base + i] = f2bf(nrm * gate);
+    }
+}
+
+// Lanes per weight row: the row's 32-input chunks over at most 64 lanes.
+int proj_lpr(int IN) {
+    const int c = IN / 32;
+    return c >= 64 ? 64 : c >= 32 ? 32 : c >= 16 ? 16 : 8;
+}
+
+template <int BITS, int LPR>
+hipError_t launch_proj_t(GdnProjSet set, int blocks, const uint16_t* x, int S, int IN, int G, int f16,
+                         hipStream_t st) {
+    // staged rows: up to 16, fewer for wide inputs (the staging stays within 144 KiB of LDS)
+    int rows = static_cast<int>((144 * 1024) / (static_cast<size_t>(IN) * 2));
+    rows = rows > kSaRows ? kSaRows : rows;
+    if (rows < 1) return hipErrorInvalidValue;
+    const size_t lds = static_cast<size_t>(rows) * IN * 2;
+    if (const hipError_t e = ensure_lds<k_gdn_proj<BITS, LPR>>(lds); e != hipSuccess) return e;
+    return launch(k_gdn_proj<BITS, LPR>, dim3(blocks, (S + rows - 1) / rows), dim3(kSaThreads), lds, st, set, x, S, IN,
+                  G, f16, rows);
+}
+template <int BITS>
+hipError_t launch_proj_b(GdnProjSet set, const uint16_t* x, int S, int IN, int G, int f16, hipStream_t st) {
+    const int lpr = proj_lpr(IN);
+    int blocks = 0;
+    const int per = kSaThreads / 64 * (64 / lpr);
+    for (int i = 0; i < set.n; ++i) {
+        set.p[i].first_block = blocks;
+        blocks += (set.p[i].out + per - 1) / per;
+    }
+    switch (lpr) {
+        case 64: return launch_proj_t<BITS, 64>(set, blocks, x, S, IN, G, f16, st);
+        case 32: return launch_proj_t<BITS, 32>(set, blocks, x, S, IN, G, f16, st);
+        case 16: return launch_proj_t<BITS, 16>(set, blocks, x, S, IN, G, f16, st);
+        default: return launch_proj_t<BITS, 8>(set, blocks, x, S, IN, G, f16, st);
+    }
+}
+hipError_t launch_proj(const GdnProjSet& set, const uint16_t* x, int S, int IN, int G, int bits, int f16,
+                       hipStream_t st) {
+    switch (bits) {
+        case 2: return launch_proj_b<2>(set, x, S, IN, G, f16, st);
+        case 4: return launch_proj_b<4>(set, x, S, IN, G, f16, st);
+        case 8: return launch_proj_b<8>(set, x, S, IN, G, f16, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int CPL>
+hipError_t launch_prework_t(const GdnDev& G, const GdnBufs& B, int S, const uint16_t* origin, uint16_t* ckpt,
+                            size_t state_elems, hipStream_t st) {
+    return launch(k_gdn_prework<CPL>, dim3(2 * G.hk + G.hv, S), dim3(64), 0, st, G, B, S, origin, ckpt, state_elems);
+}
+template <int CPL>
+hipError_t launch_norm_gate_t(const GdnDev& G, const GdnBufs& B, int S, hipStream_t st) {
+    return launch(k_gdn_norm_gate<CPL>, dim3(G.hv, S), dim3(64), 0, st, G, B, S);
+}
+template <int ITEMS>
+hipError_t launch_recur_t(const GdnDev& G, const GdnBufs& B, int S, const uint16_t* origin, uint16_t* ckpt,
+                          size_t state_elems, hipStream_t st) {
+    return launch(k_gdn_recur<ITEMS>, dim3(G.dv / 2, G.hv), dim3(64), 0, st, G, B, S, origin, ckpt, state_elems);
+}
+} // namespace
+
+bool gdn_geometry_ok(const GdnDev& G) {
+    // (the prework gives a lane dk / 64 or dv / 64 channels; a recurrence lane dk / 32 items)
+    return (G.dk == 64 || G.dk == 128 || G.dk == 256) && G.dk == G.dv && G.hk > 0 && G.hv % G.hk == 0;
+}
+
+hipError_t launch_gdn_verify(const GdnDev& G, const GdnBufs& B, int S, const uint16_t* x, const uint16_t* origin,
+                             uint16_t* ckpt, uint16_t* out, hipStream_t st) {
+    if (!gdn_geometry_ok(G)) return hipErrorInvalidValue;
+    const int KW = G.hk * G.dk, VW = G.hv * G.dv, C = 2 * KW + VW;
+    const size_t state_elems = static_cast<size_t>(3) * C + static_cast<size_t>(G.hv) * G.dv * G.dk;
+    GdnProjSet in{};
+    in.n = 4;
+    in.p[0] = {G.w[0], G.s[0], G.b[0], B.qkv, C, C, 0};
+    in.p[1] = {G.w[1], G.s[1], G.b[1], B.z, VW, VW, 0};
+    in.p[2] = {G.w[2], G.s[2], G.b[2], B.bpr, G.hv, G.hv, 0};
+    in.p[3] = {G.w[3], G.s[3], G.b[3], B.apr, G.hv, G.hv, 0};
+    if (const hipError_t e = launch_proj(in, x, S, G.hidden, G.group, G.bits, G.f16, st); e != hipSuccess) return e;
+    hipError_t e = G.dk == 64    ? launch_prework_t<1>(G, B, S, origin, ckpt, state_elems, st)
+                   : G.dk == 128 ? launch_prework_t<2>(G, B, S, origin, ckpt, state_elems, st)
+                                 : launch_prework_t<4>(G, B, S, origin, ckpt, state_elems, st);
+    if (e != hipSuccess) return e;
+    e = G.dk == 64    ? launch_recur_t<2>(G, B, S, origin, ckpt, state_elems, st)
+        : G.dk == 128 ? launch_recur_t<4>(G, B, S, origin, ckpt, state_elems, st)
+                      : launch_recur_t<8>(G, B, S, origin, ckpt, state_elems, st);
+    if (e != hipSuccess) return e;
+    e = G.dv == 64 ? launch_norm_gate_t<1>(G, B, S, st)
+        : G.dv == 128 ? launch_norm_gate_t<2>(G, B, S, st)
+                      : launch_norm_gate_t<4>(G, B, S, st);
+    if (e != hipSuccess) return e;
+    GdnProjSet o{};
+    o.n = 1;
+    o.p[0] = {G.w[4], G.s[4], G.b[4], out, G.hidden, G.hidden, 0};
+    return launch_proj(o, B.gated, S, VW, G.group, G.bits, G.f16, st);
+}
+
+} // namespace q38

@@ -150,6 +150,30 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
 // the grouped-scale (VALU) kernels of launch_gate_up / launch_down (q38_moe_grp.hip)
 hipError_t launch_gate_up_grouped(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down_grouped(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
+// GatedDeltaNet verify step (q38_gdn.hip). Projections p: 0 qkv [C, H], 1 z [HV DV, H],
+// 2 b [HV, H], 3 a [HV, H], 4 out [H, HV DV], MLX affine (bits, group, bf16 / fp16 scales).
+struct GdnDev {
+    int hidden, hk, hv, dk, dv, bits, group, f16, gate_silu;
+    float eps;
+    const uint32_t* w[5];
+    const uint16_t* s[5];
+    const uint16_t* b[5];
+    const uint16_t* conv_w;   // [C][4] bf16
+    const float* a_log;       // [HV]
+    const uint16_t* dt_bias;  // [HV] bf16
+    const uint16_t* norm_w;   // [DV] bf16
+};
+// Workspace views of one verify call of S rows (bf16 unless noted).
+struct GdnBufs {
+    uint16_t *qkv, *z, *bpr, *apr;  // projections [S][C], [S][HV DV], [S][HV] x 2
+    uint16_t *q, *k, *v;            // [S][HK DK] x 2, [S][HV DV]
+    float *beta, *decay;            // [S][HV] (bf16 values)
+    uint16_t *y, *gated;            // [S][HV DV]
+};
+bool gdn_geometry_ok(const GdnDev& G);
+hipError_t launch_gdn_verify(const GdnDev& G, const GdnBufs& B, int S, const uint16_t* x, const uint16_t* origin,
+                             uint16_t* ckpt, uint16_t* out, hipStream_t st);
+
 // Prefill widths (kMaxRows < M) on the grouped kernels: layouts the segmented MFMA kernels
 // do not take (scale groups, d4 and d2 codes)
 bool moe_supports_grouped_prefill(const LayerDev& L);

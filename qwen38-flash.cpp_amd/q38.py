@@ -50,6 +50,16 @@ class MoeMixedWeights(C.Structure):
                 ("reserved", C.c_uint16)]
 
 
+class GdnDesc(C.Structure):  # include/q38.h q38_gdn_desc
+    _fields_ = [(n, C.c_int32) for n in ("hidden", "key_heads", "value_heads", "key_dim", "value_dim", "conv_kernel",
+                                         "bits", "group", "scale_dtype", "gate_silu")] + [("eps", C.c_float)]
+
+
+class GdnWeights(C.Structure):  # include/q38.h q38_gdn_weights
+    _fields_ = [("weight", C.c_void_p * 5), ("scales", C.c_void_p * 5), ("biases", C.c_void_p * 5),
+                ("conv", C.c_void_p), ("a_log", C.c_void_p), ("dt_bias", C.c_void_p), ("norm", C.c_void_p)]
+
+
 class AffineShared(C.Structure):
     _fields_ = [("weight", C.c_void_p * 3), ("scales", C.c_void_p * 3), ("biases", C.c_void_p * 3),
                 ("bits", C.c_int32), ("group", C.c_int32), ("inter", C.c_int32), ("scale_dtype", C.c_int32)]
@@ -84,6 +94,12 @@ _sig("q38_ctx_destroy", None, P)
 _sig("q38_ctx_synchronize", C.c_int, P, P)
 _sig("q38_set_fused_layers", None, C.c_int)
 _sig("q38_debug_set_wait_limit", None, I32)
+_sig("q38_gdn_create", C.c_int, P, C.POINTER(GdnDesc), C.POINTER(GdnWeights), C.POINTER(P))
+_sig("q38_gdn_destroy", None, P)
+_sig("q38_gdn_state_bytes", C.c_size_t, P)
+_sig("q38_gdn_workspace_size", C.c_size_t, P, I32)
+_sig("q38_gdn_verify", C.c_int, P, P, I32, P, P, P, P, C.c_size_t, P)
+_sig("q38_gdn_commit", C.c_int, P, P, I32, P, P)
 _sig("q38_packed_vq_word_count", I64, I64, C.c_int)
 _sig("q38_unpack_vq_code", C.c_int, P, I64, I64, C.c_int, C.POINTER(U32))
 _sig("q38_supports_segmented_vq", C.c_int, C.c_int, C.c_int)

@@ -23,6 +23,11 @@ class Desc(C.Structure):  # field order of oracle/q38_oracle.cpp Desc
         "gu_group", "down_group", "normalize", "has_shared", "mixed", "book_format")]
 
 
+class GdnDesc(C.Structure):  # field order of oracle/q38_oracle.cpp GdnDesc
+    _fields_ = [(n, C.c_int32) for n in ("hidden", "hk", "hv", "dk", "dv", "conv", "bits", "group", "fmt",
+                                         "gate_silu")] + [("eps", C.c_float)]
+
+
 class HcDesc(C.Structure):  # field order of oracle/q38_oracle.cpp HcDesc
     _fields_ = [(n, C.c_int32) for n in ("hidden", "streams", "rank", "bits", "group", "with_injection")] + [
         ("eps", C.c_float)]
@@ -92,6 +97,10 @@ class Oracle:
         sig("orc_moe_layer_dense_affine_shared", C.c_int, C.POINTER(Desc), P, P, C.POINTER(P), C.POINTER(P),
             C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P), C.c_int, C.c_int, C.c_int, C.c_int, P, C.c_int,
             P, P, P, P, C.c_int)
+        sig("orc_gdn_plant_fault", None, C.c_int)
+        sig("orc_gdn_recurrence", C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, P, P, P, P, P)
+        sig("orc_gdn_verify", C.c_int, C.POINTER(GdnDesc), C.POINTER(P), C.POINTER(P), C.POINTER(P), P, P, P, P, P,
+            C.c_int, P, P, P)
         sig("orc_affine_expert", C.c_int, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.c_int, C.c_int, C.c_int,
             C.c_int, C.c_int, P, C.c_int, P)
         sig("orc_route_synth", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, P, P, C.c_int)
@@ -240,8 +249,44 @@ class Oracle:
         return y, ex, wt, lg
 
     @staticmethod
-    def _ptrs(arrs):
-        return (P * 3)(*[_a(a) for a in arrs])
+    def _ptrs(arrs, n=3):
+        return (P * n)(*[_a(a) for a in arrs])
+
+    def gdn_plant_fault(self, code):
+        self.lib.orc_gdn_plant_fault(code)
+
+    def gdn_recurrence(self, HK, q, k, v, decay, beta, state=None):
+        """The GDN recurrence alone: q, k [S, HK, DK], v [S, HV, DV], decay / beta [S, HV] as
+        float32 (bf16 values), state [HV, DV, DK] bf16 bits or None -> (y [S, HV, DV] float32,
+        states [S, HV, DV, DK] bf16 bits)."""
+        q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+        decay, beta = np.ascontiguousarray(decay, np.float32), np.ascontiguousarray(beta, np.float32)
+        S, HV, DV = v.shape
+        DK = q.shape[2]
+        y = np.empty((S, HV, DV), np.float32)
+        st = np.empty((S, HV, DV, DK), np.uint16)
+        sp = None if state is None else np.ascontiguousarray(state, np.uint16)
+        rc = self.lib.orc_gdn_recurrence(HK, HV, DK, DV, S, _a(q), _a(k), _a(v), _a(decay), _a(beta),
+                                         None if sp is None else _a(sp), _a(y), _a(st))
+        assert rc == 0
+        return y, st
+
+    def gdn_verify(self, layer, x, origin=None):
+        """GatedDeltaNet::forward_verify on rows x [S, hidden] (bf16 bits) from origin (a state
+        of layer.state_elems bf16, or None for zeros) -> (out [S, hidden] bf16, checkpoints
+        [S, state_elems] bf16)."""
+        d = layer.odesc
+        x = np.ascontiguousarray(x, np.uint16)
+        S = x.shape[0]
+        keep = [[np.ascontiguousarray(a) for a in layer.proj[k]] for k in ("w", "s", "b")]
+        out = np.empty((S, d.hidden), np.uint16)
+        ck = np.empty((S, layer.state_elems), np.uint16)
+        org = None if origin is None else np.ascontiguousarray(origin, np.uint16)
+        rc = self.lib.orc_gdn_verify(C.byref(d), self._ptrs(keep[0], 5), self._ptrs(keep[1], 5),
+                                     self._ptrs(keep[2], 5), _a(layer.conv_w), _a(layer.a_log), _a(layer.dt_bias),
+                                     _a(layer.norm_w), _a(x), S, None if org is None else _a(org), _a(out), _a(ck))
+        assert rc == 0
+        return out, ck
 
     def affine_expert(self, sa, x):
         """The affine shared expert (sa: dict with w, s, b lists of 3 arrays, bits, group, inter,
