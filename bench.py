@@ -566,6 +566,77 @@ def main():
     log(f"decoder MLP half (mixer read -> MoE -> mixer write, 4 rows): {hc_us:.1f} us/layer; "
         f"mixers alone {hcm_us:.1f} us/layer ({hc_cfg['mixer_gbps']:.0f} GB/s of {hc_bytes / 1e6:.2f} MB)")
 
+    # ---------------------------------------------------------------- GDN verify step
+    # The linear-attention half of a decoder layer (GatedDeltaNet::forward_verify) at the
+    # family's geometry: hidden 2048, 16 key and 32 value heads of 128, Q8/g64 projections;
+    # 4 verify rows from an origin state, writing the 4 per-row checkpoints. Eight layers of
+    # random tensors (34 MB of weights each, 272 MB together, past the 256 MB MALL) are
+    # taken in turn; a pass over them is event-timed, median of 10 passes.
+    def gdn_leg(S=4, NLg=8, Hg=2048, HKg=16, HVg=32, Dg=128):
+        C_ = 2 * HKg * Dg + HVg * Dg
+        VWg = HVg * Dg
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(SEED)
+
+        def bf(shape, lo, hi):
+            return (torch.rand(shape, generator=gen, device=dev) * (hi - lo) + lo).to(torch.bfloat16).view(torch.int16)
+
+        layers_g, keep = [], []
+        wbytes = 0
+        for _ in range(NLg):
+            w = q38.GdnWeights()
+            for p_, (O, IN) in enumerate(((C_, Hg), (VWg, Hg), (HVg, Hg), (HVg, Hg), (Hg, VWg))):
+                wt = torch.randint(-2 ** 31, 2 ** 31 - 1, (O, IN // 4), generator=gen, device=dev, dtype=torch.int32)
+                sc = bf((O, IN // 64), 0.5e-4, 1.5e-4)
+                bi = bf((O, IN // 64), -0.02, -0.01)
+                keep += [wt, sc, bi]
+                w.weight[p_], w.scales[p_], w.biases[p_] = wt.data_ptr(), sc.data_ptr(), bi.data_ptr()
+                wbytes += wt.numel() * 4 + 2 * sc.numel() * 2
+            conv = bf((C_, 4), -0.5, 0.5)
+            alog = torch.rand(HVg, generator=gen, device=dev) * 2.0
+            dtb = bf((HVg,), -0.5, 0.5)
+            nrm = bf((Dg,), 0.5, 1.5)
+            keep += [conv, alog, dtb, nrm]
+            w.conv, w.a_log, w.dt_bias, w.norm = conv.data_ptr(), alog.data_ptr(), dtb.data_ptr(), nrm.data_ptr()
+            wbytes += conv.numel() * 2 + alog.numel() * 4 + dtb.numel() * 2 + nrm.numel() * 2
+            dsc = q38.GdnDesc(Hg, HKg, HVg, Dg, Dg, 4, 8, 64, 0, 0, 1e-6)
+            hg = C.c_void_p()
+            q38.check(q38.lib.q38_gdn_create(ctx.h, C.byref(dsc), C.byref(w), C.byref(hg)))
+            layers_g.append(hg)
+        try:
+            sb = q38.lib.q38_gdn_state_bytes(layers_g[0])
+            origins = [bf((sb // 2,), -0.05, 0.05) for _ in range(NLg)]
+            ck = torch.empty(S * sb, dtype=torch.uint8, device=dev)
+            xg = bf((S, Hg), -1.0, 1.0)
+            yg = torch.empty((S, Hg), dtype=torch.int16, device=dev)
+            wsg_ = torch.empty(q38.lib.q38_gdn_workspace_size(layers_g[0], S), dtype=torch.uint8, device=dev)
+
+            def one_pass():
+                for li, hg in enumerate(layers_g):
+                    q38.check(q38.lib.q38_gdn_verify(hg, xg.data_ptr(), S, origins[li].data_ptr(), ck.data_ptr(),
+                                                     yg.data_ptr(), wsg_.data_ptr(), wsg_.numel(), sp))
+            one_pass()
+            ts = []
+            for _ in range(10):
+                ev0.record(stream)
+                one_pass()
+                ev1.record(stream)
+                torch.cuda.synchronize()
+                ts.append(1e3 * ev0.elapsed_time(ev1) / NLg)
+            us = float(np.median(ts))
+            moved = wbytes // NLg + sb * (1 + S) + 2 * S * Hg * 2
+            return {"rows": S, "layers": NLg, "hidden": Hg, "key_heads": HKg, "value_heads": HVg, "head_dim": Dg,
+                    "bits": 8, "group": 64, "us_per_call": us, "bytes_per_call": moved,
+                    "gbps": moved / (us * 1e-6) / 1e9, "hbm_frac": moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                    "note": "eager launches (5 kernels per call); bytes = weights + origin state + S checkpoints + rows"}
+        finally:
+            for hg in layers_g:
+                q38.lib.q38_gdn_destroy(hg)
+
+    gdn_cfg = gdn_leg()
+    log(f"GDN verify step (4 rows, 2048 / 16 x 32 heads of 128, Q8/g64): {gdn_cfg['us_per_call']:.1f} us/call, "
+        f"{gdn_cfg['gbps']:.0f} GB/s of {gdn_cfg['bytes_per_call'] / 1e6:.1f} MB")
+
     if args.copy_calibration:
         # a plain device copy of known size for the FETCH_SIZE / WRITE_SIZE calibration runs
         nb = 256 << 20
@@ -750,6 +821,7 @@ def main():
             "algorithmic_bytes_per_launch_m4": {k.split()[0]: v[1] for k, v in kernels.items()},
             "config3_prefill": prefill_cfg,
             "config4_mixed": mixed_cfg, "config1_group64": g64_cfg, "decoder_mlp_half_hc": hc_cfg,
+            "gdn_verify_step": gdn_cfg,
             "config2_sampled": sampled_cfg,
             "config2_learned_drafts": learned_cfg,
         },

@@ -77,5 +77,71 @@ __device__ __forceinline__ void sa_row_dot(const uint32_t* wrow, const uint16_t*
         for (int r = 0; r < kSaRows; ++r) acc[r] += __shfl_xor(acc[r], m, 64);
 }
 
+// sa_row_dot with the staged rows' 32-input chunk sums given (sxs [nr][IN / 32], each the
+// same sequential float sum sa_row_dot forms): the sums are formed once per workgroup instead
+// of once per weight row; the results are the same bits.
+template <int BITS, int LPR>
+__device__ __forceinline__ void sa_row_dot_sx(const uint32_t* wrow, const uint16_t* srow, const uint16_t* brow, int IN,
+                                              int G, int f16, const uint16_t* xs, const float* sxs, int nr,
+                                              float (&acc)[kSaRows]) {
+    const int gl = (threadIdx.x & 63) % LPR;
+    constexpr uint32_t kMask = (1u << BITS) - 1u;
+    const int nc = IN / 32;
+#pragma unroll
+    for (int r = 0; r < kSaRows; ++r) acc[r] = 0.0f;
+    for (int c = gl; c < nc; c += LPR) {
+        uint32_t wq[BITS];
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) wq[k] = wrow[c * BITS + k];
+        const int g = c * 32 / G;
+        const float sc = sa_param(srow, g, f16), bi = sa_param(brow, g, f16);
+        float q[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+            q[j] = static_cast<float>((wq[j * BITS / 32] >> ((j * BITS) % 32)) & kMask);
+#pragma unroll
+        for (int r = 0; r < kSaRows; ++r) {
+            if (r >= nr) continue;
+            const uint4* x4 = reinterpret_cast<const uint4*>(xs + static_cast<size_t>(r) * IN + c * 32);
+            float qx = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint4 u = x4[v];
+                const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    qx = fmaf(q[8 * v + 2 * k], bflo(w4[k]), qx);
+                    qx = fmaf(q[8 * v + 2 * k + 1], bfhi(w4[k]), qx);
+                }
+            }
+            acc[r] = fmaf(sc, qx, fmaf(bi, sxs[r * nc + c], acc[r]));
+        }
+    }
+#pragma unroll
+    for (int m = LPR / 2; m > 0; m >>= 1)
+#pragma unroll
+        for (int r = 0; r < kSaRows; ++r) acc[r] += __shfl_xor(acc[r], m, 64);
+}
+
+// The chunk sums of nr staged rows (xs [nr][IN]) into sxs [nr][IN / 32], in sa_row_dot's order.
+__device__ __forceinline__ void sa_chunk_sums(const uint16_t* xs, int IN, int nr, float* sxs, int nthreads) {
+    const int nc = IN / 32;
+    for (int i = threadIdx.x; i < nr * nc; i += nthreads) {
+        const uint4* x4 = reinterpret_cast<const uint4*>(xs + static_cast<size_t>(i / nc) * IN + (i % nc) * 32);
+        float sx = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 u = x4[v];
+            const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                sx += bflo(w4[k]);
+                sx += bfhi(w4[k]);
+            }
+        }
+        sxs[i] = sx;
+    }
+}
+
 } // namespace
 } // namespace q38

@@ -46,17 +46,12 @@ struct GdnProjSet {
     int n;
 };
 
-// Weight rows per workgroup: 4 waves x (64 / LPR) rows.
-template <int LPR>
-constexpr int proj_rows_per_wg() {
-    return kSaThreads / 64 * (64 / LPR);
-}
-
 template <int BITS, int LPR>
 __global__ __launch_bounds__(kSaThreads) void k_gdn_proj(GdnProjSet set, const uint16_t* __restrict__ x, int S,
                                                          int IN, int G, int f16, int rows_wg) {
-    extern __shared__ __align__(16) uint16_t xs[];  // [rows_wg][IN]
+    extern __shared__ __align__(16) uint16_t xs[];  // [rows_wg][IN], then the chunk sums [rows_wg][IN / 32]
     const int r0 = blockIdx.y * rows_wg, nr = S - r0 < rows_wg ? S - r0 : rows_wg;
+    float* sxs = reinterpret_cast<float*>(xs + static_cast<size_t>(rows_wg) * IN);
     // the projection of this block (uniform selects over the argument block)
     const int bx = static_cast<int>(blockIdx.x);
     const int pi = set.n > 3 && bx >= set.p[3].first_block ? 3
@@ -66,13 +61,15 @@ __global__ __launch_bounds__(kSaThreads) void k_gdn_proj(GdnProjSet set, const u
     const GdnProj P = pi == 3 ? set.p[3] : pi == 2 ? set.p[2] : pi == 1 ? set.p[1] : set.p[0];
     sa_stage(x, IN, r0, nr, xs);
     __syncthreads();
+    sa_chunk_sums(xs, IN, nr, sxs, kSaThreads);
+    __syncthreads();
     constexpr int OPW = 64 / LPR;
     const int o = ((bx - P.first_block) * (kSaThreads / 64) + (threadIdx.x >> 6)) * OPW + (threadIdx.x & 63) / LPR;
     if (o >= P.out) return;
     const int wpr = IN * BITS / 32, ngrp = IN / G;
     float acc[kSaRows];
-    sa_row_dot<BITS, LPR>(P.w + static_cast<size_t>(o) * wpr, P.s + static_cast<size_t>(o) * ngrp,
-                          P.b + static_cast<size_t>(o) * ngrp, IN, G, f16, xs, nr, acc);
+    sa_row_dot_sx<BITS, LPR>(P.w + static_cast<size_t>(o) * wpr, P.s + static_cast<size_t>(o) * ngrp,
+                             P.b + static_cast<size_t>(o) * ngrp, IN, G, f16, xs, sxs, nr, acc);
     if ((threadIdx.x & 63) % LPR == 0)
 #pragma unroll
         for (int r = 0; r < kSaRows; ++r)
@@ -147,19 +144,43 @@ __global__ __launch_bounds__(64) void k_gdn_recur(GdnDev G, GdnBufs B, int S, co
     const int hk = hv / (HV / HK);
     const size_t rec = static_cast<size_t>(3) * C + (static_cast<size_t>(hv) * DV + dv) * DK + sl * ITEMS;
     float st[ITEMS];
+    {
+        typedef uint16_t items_t __attribute__((ext_vector_type(ITEMS)));
+        items_t o0 = {};
+        if (origin) o0 = *reinterpret_cast<const items_t*>(origin + rec);
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) st[i] = origin ? bf2f(origin[rec + i]) : 0.0f;
+        for (int i = 0; i < ITEMS; ++i) st[i] = bf2f(o0[i]);
+    }
+    // (row t + 1's inputs are requested before row t's arithmetic; a lane's DK / 32 items of
+    // k, q and the state are one vector access each)
+    static_assert(ITEMS == 2 || ITEMS == 4 || ITEMS == 8, "items per lane");
+    typedef uint16_t items_t __attribute__((ext_vector_type(ITEMS)));
+    struct RowIn {
+        items_t k, q;
+        uint16_t v;
+        float g, b;
+    };
+    auto load_row = [&](int t, RowIn& r) {
+        const int tt = t < S ? t : S - 1;
+        r.k = *reinterpret_cast<const items_t*>(B.k + static_cast<size_t>(tt) * KW + hk * DK + sl * ITEMS);
+        r.q = *reinterpret_cast<const items_t*>(B.q + static_cast<size_t>(tt) * KW + hk * DK + sl * ITEMS);
+        r.v = B.v[static_cast<size_t>(tt) * VW + hv * DV + dv];
+        r.g = B.decay[static_cast<size_t>(tt) * HV + hv];
+        r.b = B.beta[static_cast<size_t>(tt) * HV + hv];
+    };
+    RowIn nxt;
+    load_row(0, nxt);
     for (int t = 0; t < S; ++t) {
-        const float g = B.decay[static_cast<size_t>(t) * HV + hv], bt = B.beta[static_cast<size_t>(t) * HV + hv];
-        const uint16_t* kr = B.k + static_cast<size_t>(t) * KW + hk * DK + sl * ITEMS;
-        const uint16_t* qr = B.q + static_cast<size_t>(t) * KW + hk * DK + sl * ITEMS;
+        const RowIn cur = nxt;
+        load_row(t + 1, nxt);
+        const float g = cur.g, bt = cur.b;
         float kv[ITEMS], qv[ITEMS];
 #pragma unroll
         for (int i = 0; i < ITEMS; ++i) {
-            kv[i] = bf2f(kr[i]);
-            qv[i] = bf2f(qr[i]);
+            kv[i] = bf2f(cur.k[i]);
+            qv[i] = bf2f(cur.q[i]);
         }
-        const float vv = bf2f(B.v[static_cast<size_t>(t) * VW + hv * DV + dv]);
+        const float vv = bf2f(cur.v);
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < ITEMS; ++i) {
@@ -176,9 +197,13 @@ __global__ __launch_bounds__(64) void k_gdn_recur(GdnDev G, GdnBufs B, int S, co
         }
         const float y = half_wave_sum(acc);
         if (sl == 0) B.y[static_cast<size_t>(t) * VW + hv * DV + dv] = f2bf(y);
-        if (ckpt)
+        if (ckpt) {
+            typedef uint16_t items_t2 __attribute__((ext_vector_type(ITEMS)));
+            items_t2 o;
 #pragma unroll
-            for (int i = 0; i < ITEMS; ++i) ckpt[static_cast<size_t>(t) * state_elems + rec + i] = f2bf(st[i]);
+            for (int i = 0; i < ITEMS; ++i) o[i] = f2bf(st[i]);
+            *reinterpret_cast<items_t2*>(ckpt + static_cast<size_t>(t) * state_elems + rec) = o;
+        }
     }
 }
 
@@ -206,27 +231,34 @@ __global__ __launch_bounds__(64) void k_gdn_norm_gate(GdnDev G, GdnBufs B, int S
     }
 }
 
-// Lanes per weight row: the row's 32-input chunks over at most 64 lanes.
-int proj_lpr(int IN) {
+// Lanes per weight row: about four 32-input chunks per lane (16 weight rows per workgroup at
+// H = 2048), 8 to 64 lanes.
+int proj_lpr(int IN, int out) {
     const int c = IN / 32;
-    return c >= 64 ? 64 : c >= 32 ? 32 : c >= 16 ? 16 : 8;
+    const int lpr = c >= 256 ? 64 : c >= 128 ? 32 : c >= 64 ? 16 : 8;
+    // (fewer weight rows per workgroup where the projection has few rows: at least ~512
+    // workgroups for 256 CUs)
+    return out / (kSaThreads / 64 * (64 / lpr)) < 512 && lpr < 64 && c >= 2 * lpr ? 2 * lpr : lpr;
 }
 
 template <int BITS, int LPR>
 hipError_t launch_proj_t(GdnProjSet set, int blocks, const uint16_t* x, int S, int IN, int G, int f16,
                          hipStream_t st) {
     // staged rows: up to 16, fewer for wide inputs (the staging stays within 144 KiB of LDS)
-    int rows = static_cast<int>((144 * 1024) / (static_cast<size_t>(IN) * 2));
+    int rows = static_cast<int>((144 * 1024) / (static_cast<size_t>(IN) * 2 + static_cast<size_t>(IN) / 8));
     rows = rows > kSaRows ? kSaRows : rows;
+    rows = rows > S ? S : rows;
     if (rows < 1) return hipErrorInvalidValue;
-    const size_t lds = static_cast<size_t>(rows) * IN * 2;
+    const size_t lds = static_cast<size_t>(rows) * IN * 2 + static_cast<size_t>(rows) * (IN / 32) * 4;
     if (const hipError_t e = ensure_lds<k_gdn_proj<BITS, LPR>>(lds); e != hipSuccess) return e;
     return launch(k_gdn_proj<BITS, LPR>, dim3(blocks, (S + rows - 1) / rows), dim3(kSaThreads), lds, st, set, x, S, IN,
                   G, f16, rows);
 }
 template <int BITS>
 hipError_t launch_proj_b(GdnProjSet set, const uint16_t* x, int S, int IN, int G, int f16, hipStream_t st) {
-    const int lpr = proj_lpr(IN);
+    int rows_out = 0;
+    for (int i = 0; i < set.n; ++i) rows_out += set.p[i].out;
+    const int lpr = proj_lpr(IN, rows_out);
     int blocks = 0;
     const int per = kSaThreads / 64 * (64 / lpr);
     for (int i = 0; i < set.n; ++i) {
