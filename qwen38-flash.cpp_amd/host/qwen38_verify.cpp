@@ -292,6 +292,66 @@ HyperConnection& HyperConnection::operator=(HyperConnection&& o) noexcept {
     return *this;
 }
 
+// ------------------------------------------------------------------ GatedDeltaNet
+GatedDeltaNet::GatedDeltaNet(const Context& ctx, const q38_gdn_weights& tensors, std::size_t hidden_size,
+                             std::size_t key_head_count, std::size_t value_head_count, std::size_t key_head_dimension,
+                             std::size_t value_head_dimension, std::size_t convolution_kernel_size,
+                             int quantization_bits, int quantization_group_size, bool fp16_scales,
+                             const std::string& output_gate_type, float rms_norm_epsilon)
+    : ctx_(&ctx), hidden_(hidden_size) {
+    if (output_gate_type != "sigmoid" && output_gate_type != "silu")
+        throw std::runtime_error("unsupported output_gate_type");
+    const q38_gdn_desc d{static_cast<int32_t>(hidden_size), static_cast<int32_t>(key_head_count),
+                         static_cast<int32_t>(value_head_count), static_cast<int32_t>(key_head_dimension),
+                         static_cast<int32_t>(value_head_dimension), static_cast<int32_t>(convolution_kernel_size),
+                         quantization_bits, quantization_group_size, fp16_scales ? 1 : 0,
+                         output_gate_type == "silu" ? 1 : 0, rms_norm_epsilon};
+    check(q38_gdn_create(ctx.handle(), &d, &tensors, &gdn_), "GatedDeltaNet");
+}
+GatedDeltaNet::~GatedDeltaNet() { q38_gdn_destroy(gdn_); }
+GatedDeltaNet::GatedDeltaNet(GatedDeltaNet&& o) noexcept
+    : ctx_(o.ctx_), gdn_(o.gdn_), hidden_(o.hidden_), workspace_(std::move(o.workspace_)) {
+    o.gdn_ = nullptr;
+}
+GatedDeltaNet& GatedDeltaNet::operator=(GatedDeltaNet&& o) noexcept {
+    if (this != &o) {
+        q38_gdn_destroy(gdn_);
+        ctx_ = o.ctx_;
+        gdn_ = o.gdn_;
+        hidden_ = o.hidden_;
+        workspace_ = std::move(o.workspace_);
+        o.gdn_ = nullptr;
+    }
+    return *this;
+}
+std::size_t GatedDeltaNet::state_bytes() const noexcept { return q38_gdn_state_bytes(gdn_); }
+
+DeviceTensor GatedDeltaNet::forward_verify(const DeviceTensor& input, const GatedDeltaNetState& origin,
+                                           std::vector<GatedDeltaNetState>& checkpoints) const {
+    const auto& s = input.shape();
+    if (s.size() != 3 || s[0] != 1 || s[1] < 1 || s[1] > 64 || s[2] != hidden_ || input.dtype() != DType::bf16)
+        throw std::runtime_error("GatedDeltaNet batch requires shape [1,S,hidden], S=1..64");
+    if (origin.initialized && origin.block.empty()) throw std::runtime_error("GatedDeltaNet origin state has no data");
+    const std::size_t rows = s[1], sb = state_bytes();
+    DeviceTensor out({1, rows, hidden_}, DType::bf16);
+    DeviceTensor block({rows * sb / 2}, DType::bf16);
+    std::lock_guard<std::mutex> lk(g_ws_mutex);
+    const std::size_t need = q38_gdn_workspace_size(gdn_, static_cast<int32_t>(rows));
+    if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
+    check(q38_gdn_verify(gdn_, static_cast<const uint16_t*>(input.data()), static_cast<int32_t>(rows),
+                         origin.initialized ? origin.data() : nullptr, block.data(),
+                         static_cast<uint16_t*>(out.data()), workspace_.data(), workspace_.nbytes(), ctx_->stream()),
+          "GatedDeltaNet::forward_verify");
+    checkpoints.clear();
+    checkpoints.resize(rows);
+    for (std::size_t r = 0; r < rows; ++r) {
+        checkpoints[r].block = block.share();
+        checkpoints[r].offset = r * sb;
+        checkpoints[r].initialized = true;
+    }
+    return out;
+}
+
 DeviceTensor HyperConnection::initialize_stream(const Context& ctx, const DeviceTensor& embedding,
                                                 std::size_t stream_count) {
     const auto& s = embedding.shape();

@@ -220,6 +220,49 @@ private:
     mutable DeviceTensor workspace_;
 };
 
+// ------------------------------------------------------------------ GatedDeltaNet (verify)
+// GatedDeltaNetState (include/qwen38/gated_delta_net.hpp:28-37): the convolution rows and the
+// recurrent state of one layer and slot, one device block of GatedDeltaNet::state_bytes()
+// (conv [3][C] bf16, then recurrent [HV][DV][DK] bf16) at `offset` bytes into `block`; the
+// checkpoints of one verify call share one block, as the reference's slices share theirs.
+struct GatedDeltaNetState {
+    DeviceTensor block;
+    std::size_t offset{0};
+    bool initialized{false};
+    [[nodiscard]] void* data() const noexcept { return static_cast<char*>(block.data()) + offset; }
+};
+
+// GatedDeltaNet (include/qwen38/gated_delta_net.hpp:40-106) on the verify path: the
+// reference checkpoint's tensors (q38_gdn_weights) with the manifest's geometry.
+class GatedDeltaNet final {
+public:
+    GatedDeltaNet(const Context& ctx, const q38_gdn_weights& tensors, std::size_t hidden_size,
+                  std::size_t key_head_count, std::size_t value_head_count, std::size_t key_head_dimension,
+                  std::size_t value_head_dimension, std::size_t convolution_kernel_size, int quantization_bits,
+                  int quantization_group_size, bool fp16_scales, const std::string& output_gate_type,
+                  float rms_norm_epsilon);
+    ~GatedDeltaNet();
+    GatedDeltaNet(GatedDeltaNet&&) noexcept;
+    GatedDeltaNet& operator=(GatedDeltaNet&&) noexcept;
+    GatedDeltaNet(const GatedDeltaNet&) = delete;
+    GatedDeltaNet& operator=(const GatedDeltaNet&) = delete;
+
+    // forward_verify (src/gated_delta_net.cpp:657-834): input [1, S, hidden] bf16, S = 1..64,
+    // from origin (an uninitialised origin is the zero state); checkpoints receives the S
+    // states after each row. Throws on a deferred-rollback origin as the reference does (this
+    // build's states never defer).
+    [[nodiscard]] DeviceTensor forward_verify(const DeviceTensor& input, const GatedDeltaNetState& origin,
+                                              std::vector<GatedDeltaNetState>& checkpoints) const;
+    [[nodiscard]] std::size_t state_bytes() const noexcept;
+    [[nodiscard]] q38_gdn* handle() const noexcept { return gdn_; }
+
+private:
+    const Context* ctx_ = nullptr;
+    q38_gdn* gdn_ = nullptr;
+    std::size_t hidden_ = 0;
+    mutable DeviceTensor workspace_;
+};
+
 // ------------------------------------------------------------------ verify model
 struct GreedyStep {
     std::uint32_t token{0};

@@ -286,6 +286,106 @@ static void hyper_connection_tests(const qwen38::Context& ctx) {
     std::printf("hyper connection: ok\n");
 }
 
+// GatedDeltaNet mirror: forward_verify equals the C ABI call bit for bit (outputs and the
+// checkpoint block); S rows equal S one-row calls each from the previous call's last
+// checkpoint; shape and geometry errors throw with the reference's messages.
+static void gated_delta_net_tests(const qwen38::Context& ctx) {
+    const std::size_t H = 512, HK = 2, HV = 4, D = 128, C = 2 * HK * D + HV * D, VW = HV * D, S = 4, G = 64;
+    std::uint64_t st = 0x2545F4914F6CDD1Dull;
+    auto next = [&] { st = st * 6364136223846793005ull + 1442695040888963407ull; return static_cast<std::uint32_t>(st >> 32); };
+    auto bf16 = [](float f) { std::uint32_t u; std::memcpy(&u, &f, 4); return static_cast<std::uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16); };
+    auto unit = [&] { return (static_cast<float>(next() >> 8) / 16777216.0f) - 0.5f; };
+    auto upload_u32 = [&](std::size_t n) {
+        std::vector<std::uint32_t> h(n);
+        for (auto& v : h) v = next();
+        qwen38::DeviceTensor t({n}, qwen38::DType::u32);
+        t.upload(h.data(), n * 4);
+        return t;
+    };
+    auto upload_bf16 = [&](std::size_t n, float scale, float offset) {
+        std::vector<std::uint16_t> h(n);
+        for (auto& v : h) v = bf16(offset + scale * unit());
+        qwen38::DeviceTensor t({n}, qwen38::DType::bf16);
+        t.upload(h.data(), n * 2);
+        return t;
+    };
+    const std::size_t outs[5] = {C, VW, HV, HV, H}, ins[5] = {H, H, H, H, VW};
+    std::vector<qwen38::DeviceTensor> keep;
+    q38_gdn_weights w{};
+    for (int p = 0; p < 5; ++p) {  // 8-bit, centred: weight = q * s + b with b ~ -127.5 s
+        keep.push_back(upload_u32(outs[p] * ins[p] / 4));
+        keep.push_back(upload_bf16(outs[p] * ins[p] / G, 0.0001f, 0.00015f));
+        keep.push_back(upload_bf16(outs[p] * ins[p] / G, 0.002f, -0.019f));
+        w.weight[p] = static_cast<const std::uint32_t*>(keep[keep.size() - 3].data());
+        w.scales[p] = static_cast<const std::uint16_t*>(keep[keep.size() - 2].data());
+        w.biases[p] = static_cast<const std::uint16_t*>(keep[keep.size() - 1].data());
+    }
+    keep.push_back(upload_bf16(C * 4, 1.0f, 0.0f));
+    w.conv = static_cast<const std::uint16_t*>(keep.back().data());
+    std::vector<float> alog(HV, 0.5f);
+    qwen38::DeviceTensor alog_t({HV}, qwen38::DType::f32);
+    alog_t.upload(alog.data(), HV * 4);
+    w.a_log = static_cast<const float*>(alog_t.data());
+    keep.push_back(upload_bf16(HV, 1.0f, 0.0f));
+    w.dt_bias = static_cast<const std::uint16_t*>(keep.back().data());
+    keep.push_back(upload_bf16(D, 0.5f, 1.0f));
+    w.norm = static_cast<const std::uint16_t*>(keep.back().data());
+    qwen38::GatedDeltaNet gdn(ctx, w, H, HK, HV, D, D, 4, 8, static_cast<int>(G), false, "sigmoid", 1e-6f);
+    const std::size_t sb = gdn.state_bytes();
+    CHECK(sb == (3 * C + VW * D) * 2);
+
+    auto x = upload_bf16(S * H, 2.0f, 0.0f);
+    qwen38::DeviceTensor x3({1, S, H}, qwen38::DType::bf16);
+    CHECK(hipMemcpy(x3.data(), x.data(), S * H * 2, hipMemcpyDeviceToDevice) == hipSuccess);
+    qwen38::GatedDeltaNetState origin;
+    origin.block = upload_bf16(sb / 2, 0.1f, 0.0f);
+    origin.initialized = true;
+    std::vector<qwen38::GatedDeltaNetState> ck;
+    const qwen38::DeviceTensor out = gdn.forward_verify(x3, origin, ck);
+    CHECK(ck.size() == S && out.shape() == (std::vector<std::size_t>{1, S, H}));
+    // the same call through the C ABI
+    qwen38::DeviceTensor out2({S, H}, qwen38::DType::bf16), blk2({S * sb / 2}, qwen38::DType::bf16);
+    qwen38::DeviceTensor ws({q38_gdn_workspace_size(gdn.handle(), static_cast<int32_t>(S))}, qwen38::DType::u32);
+    CHECK(q38_gdn_verify(gdn.handle(), static_cast<const std::uint16_t*>(x3.data()), static_cast<int32_t>(S),
+                         origin.data(), blk2.data(), static_cast<std::uint16_t*>(out2.data()), ws.data(), ws.nbytes(),
+                         ctx.stream()) == Q38_OK);
+    ctx.synchronize();
+    CHECK(out.to_host<std::uint16_t>() == out2.to_host<std::uint16_t>());
+    CHECK(ck[0].block.to_host<std::uint16_t>() == blk2.to_host<std::uint16_t>());
+    // row by row from the previous call's checkpoint
+    qwen38::GatedDeltaNetState state;
+    state.block = origin.block.share();
+    state.initialized = true;
+    const auto want = out.to_host<std::uint16_t>();
+    for (std::size_t r = 0; r < S; ++r) {
+        qwen38::DeviceTensor xr({1, 1, H}, qwen38::DType::bf16);
+        CHECK(hipMemcpy(xr.data(), static_cast<const char*>(x3.data()) + r * H * 2, H * 2, hipMemcpyDeviceToDevice) ==
+              hipSuccess);
+        std::vector<qwen38::GatedDeltaNetState> c1;
+        const qwen38::DeviceTensor o1 = gdn.forward_verify(xr, state, c1);
+        ctx.synchronize();
+        const auto got = o1.to_host<std::uint16_t>();
+        CHECK(std::equal(got.begin(), got.end(), want.begin() + static_cast<std::ptrdiff_t>(r * H)));
+        state = std::move(c1[0]);
+    }
+    {
+        std::vector<std::uint16_t> a(sb / 2), b(sb / 2);
+        CHECK(hipMemcpy(a.data(), state.data(), sb, hipMemcpyDeviceToHost) == hipSuccess);
+        CHECK(hipMemcpy(b.data(), ck[S - 1].data(), sb, hipMemcpyDeviceToHost) == hipSuccess);
+        CHECK(a == b);
+    }
+    // errors
+    qwen38::DeviceTensor bad({1, 65, H}, qwen38::DType::bf16);
+    CHECK(throws<std::runtime_error>([&] { (void)gdn.forward_verify(bad, origin, ck); }));
+    CHECK(throws<std::runtime_error>([&] {
+        qwen38::GatedDeltaNet g3(ctx, w, H, HK, HV, D, D, 3, 8, static_cast<int>(G), false, "sigmoid", 1e-6f);
+    }));
+    CHECK(throws<std::runtime_error>([&] {
+        qwen38::GatedDeltaNet gx(ctx, w, H, HK, HV, D, D, 4, 8, static_cast<int>(G), false, "tanh", 1e-6f);
+    }));
+    std::printf("gated delta net: ok\n");
+}
+
 static void draft_head_tests(const qwen38::Context& ctx, const qwen38::QwenModel& model) {
     qwen38::MoeGeometry g;
     qwen38::QwenMtpHead head(ctx, model.seed(), model.vocab(), g);
@@ -582,6 +682,7 @@ static void gpu_tests() {
     batched_slot_tests(ctx, model);
     draft_head_tests(ctx, model);
     hyper_connection_tests(ctx);
+    gated_delta_net_tests(ctx);
 }
 
 int main(int argc, char** argv) {

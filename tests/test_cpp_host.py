@@ -4,7 +4,7 @@ types on the CPU, the device section (SparseMoe vs the C ABI, verify + commit li
 a greedy round, and the engine-side round driver with 3 requests sharing each batched
 verification, every batch recomputed row by row in the same kernel family; the MTP draft head,
 learned-draft rounds and the scheduler drafting with the head; the HyperConnection mixer
-against the C ABI) on the GPU."""
+and the GatedDeltaNet verify step against the C ABI) on the GPU."""
 import os
 import subprocess
 
@@ -32,3 +32,4 @@ def test_gpu_section():
     assert "batched slots: ok" in out, out
     assert "draft head: ok" in out, out
     assert "hyper connection: ok" in out, out
+    assert "gated delta net: ok" in out, out
