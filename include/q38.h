@@ -375,6 +375,7 @@ int q38_argmax_rows(const float* logits, int32_t rows, int64_t vocab, uint32_t* 
  * (pre_mixer_stream), the input of the next step of a draft chain. Rows 1..4 (the Q4 head's
  * row limit); hidden 2048. */
 typedef struct q38_mtp_head q38_mtp_head;
+typedef struct q38_hc q38_hc; /* the HyperConnection mixer (declared below) */
 /* Borrowed components (kept alive by the caller): layer (hidden H), fc_embedding and
  * fc_hidden (Q8 heads, vocab = hidden = H), draft_head (Q4, hidden H). */
 int q38_mtp_head_create(q38_ctx* ctx, q38_moe_layer* layer, q38_head* fc_embedding, q38_head* fc_hidden,
@@ -390,6 +391,31 @@ void q38_mtp_head_destroy(q38_mtp_head* head);
 /* The component handles (owned by the head when it was created synthetic). */
 int q38_mtp_head_parts(const q38_mtp_head* head, q38_moe_layer** layer, q38_head** fc_embedding,
                        q38_head** fc_hidden, q38_head** draft_head);
+/* HC streams (QwenMtpHead with hyper_connection_count streams, src/mtp_head.cpp:120-170,
+ * 223-267, 454-470). After this call a step maps the target's pre-mixer streams s (device
+ * [rows, HC * H] bf16) and the next token t to
+ *   ne = T(T(rms(embed(t))) * (1 + w_e))        pre_fc_norm_embedding, over H
+ *   nh = T(T(rms(s)) * (1 + w_h))               pre_fc_norm_hidden, over the row's HC * H
+ *   x[s] = T(T(W_e . ne) + T(W_h . nh[s]))      the hidden projection per stream, the
+ *                                               embedding projection added to every stream
+ *   x' = block mixer write(x, MoE(read(x).mixed), read(x).injection)   the head's block
+ *   logits = Q4 head(final mixer read(x').mixed)
+ * and x' is the step's output stream [rows, HC * H]. The mixers (q38_hc_create) are borrowed:
+ * the block mixer with injection weights, the final mixer without (the reference builds it
+ * with with_injection false), both of the head's hidden size and one stream count. The norm
+ * weights are the raw checkpoint tensors (bf16; null for zeros); 1 + w is formed once here.
+ * The trace's combined rows are then [rows, HC * H] and final_mixed is the final mixer's
+ * mixed row. Size workspaces after this call. A null streams argument returns to the
+ * single-stream head. */
+typedef struct q38_mtp_streams {
+    q38_hc* block_mixer;            /* language_model.mtp.layers.0's MLP mixer          */
+    q38_hc* final_mixer;            /* language_model.mtp.hyper_connection_mixer        */
+    const uint16_t* embedding_norm; /* pre_fc_norm_embedding.weight [H]                 */
+    const uint16_t* hidden_norm;    /* pre_fc_norm_hidden.weight [HC * H]               */
+} q38_mtp_streams;
+int q38_mtp_head_set_streams(q38_mtp_head* head, const q38_mtp_streams* streams);
+/* The head's stream count (1 for the single-stream head). */
+int q38_mtp_head_streams(const q38_mtp_head* head);
 /* Device workspace bytes for up to max_rows rows (1..4); 0 for an invalid count. */
 size_t q38_mtp_workspace_size(const q38_mtp_head* head, int32_t max_rows);
 /* Optional intermediate rows of a step (MtpTrace, include/qwen38/mtp_head.hpp:24-28):
@@ -531,7 +557,6 @@ int q38_gdn_commit(const q38_gdn* gdn, const void* checkpoints, int32_t row, voi
  * dot products accumulate in float. Projections are MLX affine-quantised: weight
  * [out][in / (32 / bits)] uint32 (value j of a word at bits j*bits.., LSB first), scales and
  * biases [out][in / group] bf16, value = q * scale + bias. */
-typedef struct q38_hc q38_hc;
 typedef struct q38_hc_desc {
     int32_t hidden;          /* H: a multiple of 256, at most 4096                       */
     int32_t streams;         /* HC: 1..16                                                 */

@@ -1331,6 +1331,13 @@ int q38_argmax_rows(const float* logits, int32_t rows, int64_t vocab, uint32_t* 
 }
 
 // ------------------------------------------------------------------ MTP draft head
+struct q38_hc {
+    q38_ctx* ctx;
+    q38_hc_desc desc;
+    HcDev dev;
+    uint16_t* wn;  // 1 + hc_norm.weight (owned)
+};
+
 struct q38_mtp_head {
     q38_ctx* ctx;
     q38_moe_layer* layer;
@@ -1340,6 +1347,12 @@ struct q38_mtp_head {
     uint64_t embed_seed;
     float eps;
     bool owned;
+    // HC streams (q38_mtp_head_set_streams); streams == 1 and no mixers: the single-stream head
+    int streams = 1;
+    q38_hc* block_hc = nullptr;
+    q38_hc* final_hc = nullptr;
+    uint16_t* emb_norm = nullptr;  // 1 + pre_fc_norm_embedding.weight [H] (owned; null: gain 1)
+    uint16_t* hid_norm = nullptr;  // 1 + pre_fc_norm_hidden.weight [HC * H] (owned; null: gain 1)
 };
 
 namespace {
@@ -1366,20 +1379,27 @@ size_t mtp_layout(const q38_mtp_head* m, int rows, MtpWork* w, void* base) {
         off += align256(bytes);
         return p;
     };
+    const size_t HC = static_cast<size_t>(m->streams);
+    const int fc_rows = std::min(kHeadMaxRows, rows * m->streams);  // the stream projections run in passes
     MtpWork t{};
     t.e16 = reinterpret_cast<uint16_t*>(take(rows * H * 2));
     t.ne = reinterpret_cast<uint16_t*>(take(rows * H * 2));
-    t.nh = reinterpret_cast<uint16_t*>(take(rows * H * 2));
-    t.x = reinterpret_cast<uint16_t*>(take(rows * H * 2));
+    t.nh = reinterpret_cast<uint16_t*>(take(rows * HC * H * 2));
+    t.x = reinterpret_cast<uint16_t*>(take(rows * HC * H * 2));
     t.f = reinterpret_cast<uint16_t*>(take(rows * H * 2));
     t.pe = reinterpret_cast<float*>(take(rows * H * 4));
-    t.ph = reinterpret_cast<float*>(take(rows * H * 4));
+    t.ph = reinterpret_cast<float*>(take(rows * HC * H * 4));
     t.logits = reinterpret_cast<float*>(take(rows * V * 4));
     t.best = reinterpret_cast<unsigned long long*>(take(rows * 8));
     t.tokens = reinterpret_cast<uint32_t*>(take(rows * 4));
-    t.head_ws_bytes = std::max(q38_head_workspace_size(m->fc_e, rows), q38_head_workspace_size(m->fc_h, rows));
+    t.head_ws_bytes = std::max(q38_head_workspace_size(m->fc_e, rows), q38_head_workspace_size(m->fc_h, fc_rows));
     t.head_ws = take(t.head_ws_bytes);
     t.moe_ws_bytes = q38_moe_workspace_size(&m->layer->desc, rows);
+    if (m->block_hc) {
+        t.moe_ws_bytes = std::max(t.moe_ws_bytes, q38_verify_chain_hc_workspace_size(&m->layer->desc,
+                                                                                     &m->block_hc->desc, rows));
+        t.moe_ws_bytes = std::max(t.moe_ws_bytes, q38_hc_workspace_size(&m->final_hc->desc, rows));
+    }
     t.moe_ws = take(t.moe_ws_bytes);
     if (w) *w = t;
     return off;
@@ -1398,20 +1418,36 @@ int mtp_validate(q38_moe_layer* layer, q38_head* fe, q38_head* fh, q38_head* dh)
 }
 
 // One draft step on rows (<= 4) requests; logits into `logits`, the output stream in w.x.
+// With HC streams (combine_inputs, src/mtp_head.cpp:258-266; forward_decode, :454-470): the
+// hidden norm runs over the row's HC * H values, the hidden projection over each stream, the
+// embedding projection is added to every stream, the block is the mixer read -> MoE ->
+// mixer write, and the final mixer's read gives the LM head's input.
 int mtp_step(q38_mtp_head* m, const MtpWork& w, const uint16_t* stream_in, const uint32_t* tokens, int rows,
              float* logits, const q38_mtp_trace* trace, hipStream_t st) {
-    const int H = m->layer->desc.hidden;
+    const int H = m->layer->desc.hidden, HC = m->streams;
     Q38_HIP(launch_gen_embed_dev(m->embed_seed, tokens, rows, H, w.e16, st));
-    Q38_HIP(launch_rmsnorm(w.e16, rows, H, m->eps, w.ne, st));
-    Q38_HIP(launch_rmsnorm(stream_in, rows, H, m->eps, w.nh, st));
+    Q38_HIP(launch_rmsnorm_w(w.e16, rows, H, m->eps, m->emb_norm, w.ne, st));
+    Q38_HIP(launch_rmsnorm_w(stream_in, rows, HC * H, m->eps, m->hid_norm, w.nh, st));
     if (int rc = q38_head_logits(m->fc_e, w.ne, rows, w.pe, w.head_ws, w.head_ws_bytes, st)) return rc;
-    if (int rc = q38_head_logits(m->fc_h, w.nh, rows, w.ph, w.head_ws, w.head_ws_bytes, st)) return rc;
-    Q38_HIP(launch_fc_join(w.pe, w.ph, rows * H, w.x, w.best, rows, st));
+    for (int r0 = 0; r0 < rows * HC; r0 += kHeadMaxRows) {
+        const int n = std::min(kHeadMaxRows, rows * HC - r0);
+        if (int rc = q38_head_logits(m->fc_h, w.nh + static_cast<size_t>(r0) * H, n, w.ph + static_cast<size_t>(r0) * H,
+                                     w.head_ws, w.head_ws_bytes, st))
+            return rc;
+    }
+    Q38_HIP(launch_fc_join(w.pe, w.ph, rows, HC, H, w.x, w.best, st));
     if (trace && trace->combined)
-        Q38_HIP(hipMemcpyAsync(trace->combined, w.x, static_cast<size_t>(rows) * H * 2, hipMemcpyDeviceToDevice, st));
+        Q38_HIP(hipMemcpyAsync(trace->combined, w.x, static_cast<size_t>(rows) * HC * H * 2, hipMemcpyDeviceToDevice,
+                               st));
     q38_moe_layer* layers[1] = {m->layer};
-    if (int rc = q38_verify_chain(layers, 1, w.x, rows, m->eps, nullptr, w.moe_ws, w.moe_ws_bytes, st)) return rc;
-    Q38_HIP(launch_rmsnorm(w.x, rows, H, m->eps, w.f, st));
+    if (m->block_hc) {
+        q38_hc* mixers[1] = {m->block_hc};
+        if (int rc = q38_verify_chain_hc(layers, mixers, 1, w.x, rows, w.moe_ws, w.moe_ws_bytes, st)) return rc;
+        if (int rc = q38_hc_read(m->final_hc, w.x, rows, w.f, nullptr, w.moe_ws, w.moe_ws_bytes, st)) return rc;
+    } else {
+        if (int rc = q38_verify_chain(layers, 1, w.x, rows, m->eps, nullptr, w.moe_ws, w.moe_ws_bytes, st)) return rc;
+        Q38_HIP(launch_rmsnorm(w.x, rows, H, m->eps, w.f, st));
+    }
     if (trace && trace->final_mixed)
         Q38_HIP(hipMemcpyAsync(trace->final_mixed, w.f, static_cast<size_t>(rows) * H * 2, hipMemcpyDeviceToDevice,
                                st));
@@ -1453,8 +1489,54 @@ int q38_mtp_head_create_synthetic(q38_ctx* ctx, const q38_moe_desc* desc, int64_
     return Q38_OK;
 }
 
+static void mtp_free_norms(q38_mtp_head* m) {
+    (void)hipFree(m->emb_norm);
+    (void)hipFree(m->hid_norm);
+    m->emb_norm = m->hid_norm = nullptr;
+}
+
+int q38_mtp_head_set_streams(q38_mtp_head* m, const q38_mtp_streams* s) {
+    if (!m) return fail(Q38_EINVAL, "q38_mtp_head_set_streams: null head");
+    const int H = m->layer->desc.hidden;
+    if (!s) {
+        mtp_free_norms(m);
+        m->streams = 1;
+        m->block_hc = m->final_hc = nullptr;
+        return Q38_OK;
+    }
+    if (!s->block_mixer || !s->final_mixer) return fail(Q38_EINVAL, "MTP streams need the block and final mixers");
+    const q38_hc_desc &b = s->block_mixer->desc, &f = s->final_mixer->desc;
+    if (b.hidden != H || f.hidden != H || b.streams != f.streams)
+        return fail(Q38_EINVAL, "MTP mixers must share the head's hidden size and stream count");
+    if (!b.with_injection) return fail(Q38_EINVAL, "the MTP block mixer carries injection weights");
+    if (f.with_injection) return fail(Q38_EINVAL, "the MTP final mixer is read without injection");
+    const int HC = b.streams;
+    uint16_t *en = nullptr, *hn = nullptr;
+    hipError_t e = hipSuccess;
+    if (s->embedding_norm && e == hipSuccess) e = hipMalloc(&en, static_cast<size_t>(H) * 2);
+    if (s->hidden_norm && e == hipSuccess) e = hipMalloc(&hn, static_cast<size_t>(HC) * H * 2);
+    if (e == hipSuccess && en) e = launch_hc_norm_weight(s->embedding_norm, H, en, nullptr);
+    if (e == hipSuccess && hn) e = launch_hc_norm_weight(s->hidden_norm, HC * H, hn, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(en);
+        (void)hipFree(hn);
+        return hip_fail(e, "MTP stream norm weights");
+    }
+    mtp_free_norms(m);
+    m->streams = HC;
+    m->block_hc = s->block_mixer;
+    m->final_hc = s->final_mixer;
+    m->emb_norm = en;
+    m->hid_norm = hn;
+    return Q38_OK;
+}
+
+int q38_mtp_head_streams(const q38_mtp_head* m) { return m ? m->streams : 0; }
+
 void q38_mtp_head_destroy(q38_mtp_head* m) {
     if (!m) return;
+    mtp_free_norms(m);
     if (m->owned) {
         q38_head_destroy(m->draft);
         q38_head_destroy(m->fc_h);
@@ -1490,7 +1572,7 @@ int q38_mtp_forward_decode(q38_mtp_head* m, const uint16_t* stream_in, const uin
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (int rc = mtp_step(m, w, stream_in, tokens, rows, logits ? logits : w.logits, trace, st)) return rc;
     if (stream_out)
-        Q38_HIP(hipMemcpyAsync(stream_out, w.x, static_cast<size_t>(rows) * m->layer->desc.hidden * 2,
+        Q38_HIP(hipMemcpyAsync(stream_out, w.x, static_cast<size_t>(rows) * m->streams * m->layer->desc.hidden * 2,
                                hipMemcpyDeviceToDevice, st));
     return Q38_OK;
 }
@@ -1516,7 +1598,7 @@ int q38_mtp_draft_greedy(q38_mtp_head* m, const uint16_t* stream_in, const uint3
         t_in = w.tokens;
     }
     if (stream_out)
-        Q38_HIP(hipMemcpyAsync(stream_out, w.x, static_cast<size_t>(rows) * m->layer->desc.hidden * 2,
+        Q38_HIP(hipMemcpyAsync(stream_out, w.x, static_cast<size_t>(rows) * m->streams * m->layer->desc.hidden * 2,
                                hipMemcpyDeviceToDevice, st));
     return Q38_OK;
 }
@@ -1645,13 +1727,6 @@ const uint16_t* q38_slot_hidden(const q38_slot* s) { return s && s->has_hidden ?
 uint64_t q38_slot_generation(const q38_slot* s) { return s && s->staged_rows > 0 ? s->stages : 0; }
 
 // ------------------------------------------------------------------ HyperConnection mixer
-struct q38_hc {
-    q38_ctx* ctx;
-    q38_hc_desc desc;
-    HcDev dev;
-    uint16_t* wn;  // 1 + hc_norm.weight (owned)
-};
-
 static int hc_validate(const q38_hc_desc* d) {
     if (!d) return fail(Q38_EINVAL, "null HyperConnection description");
     if (d->hidden <= 0 || d->hidden % 256 || d->hidden > 256 * kHcMaxPerThread)

@@ -747,11 +747,17 @@ hipError_t launch_scale_absmax(const uint16_t* scales, int64_t n, float* out, hi
 // projections, each rounded to bf16, added in bf16: src/mtp_head.cpp:258-266). The sum of two
 // bf16 values is exact in fp32 or below half a bf16 ulp of the larger, so one rounding of the
 // fp32 sum is the correctly rounded bf16 sum. Also clears best[0..M) for the step's argmax.
-__global__ __launch_bounds__(256) void k_fc_join(const float* __restrict__ a, const float* __restrict__ b, int n,
-                                                 uint16_t* __restrict__ x, unsigned long long* __restrict__ best,
-                                                 int M) {
+// With HC streams a row holds HC stream projections b [M][HC][H] and one embedding
+// projection a [M][H], added to every stream (the broadcast of src/mtp_head.cpp:261-266).
+__global__ __launch_bounds__(256) void k_fc_join(const float* __restrict__ a, const float* __restrict__ b, int M,
+                                                 int HC, int H, uint16_t* __restrict__ x,
+                                                 unsigned long long* __restrict__ best) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) x[i] = f2bf(rbf(a[i]) + rbf(b[i]));
+    const int n = M * HC * H;
+    if (i < n) {
+        const int r = i / (HC * H), c = i % H;
+        x[i] = f2bf(rbf(a[r * H + c]) + rbf(b[i]));
+    }
     if (best && i < M) best[i] = 0ull;
 }
 
@@ -790,9 +796,10 @@ __global__ void k_argmax_final(const unsigned long long* __restrict__ best, int 
     if (drafts) drafts[static_cast<size_t>(r) * depth + step] = t;
 }
 
-hipError_t launch_fc_join(const float* a, const float* b, int n, uint16_t* x, unsigned long long* best, int M,
+hipError_t launch_fc_join(const float* a, const float* b, int M, int HC, int H, uint16_t* x, unsigned long long* best,
                           hipStream_t st) {
-    return launch(k_fc_join, dim3((n + 255) / 256), dim3(256), 0, st, a, b, n, x, best, M);
+    const int n = M * HC * H;
+    return launch(k_fc_join, dim3((n + 255) / 256), dim3(256), 0, st, a, b, M, HC, H, x, best);
 }
 
 hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long long* best, bool clear,

@@ -189,6 +189,9 @@ hipError_t launch_combine(const LayerDev& L, const MoeBufs& B, int M, uint16_t* 
 hipError_t launch_combine_hc(const LayerDev& L, const MoeBufs& B, int M, uint16_t* hs, const uint16_t* inj, int HC,
                              hipStream_t st);
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st);
+// The same with a learned weight w [H] bf16: y = T(T(x * inv_rms) * w) (MLX rms_norm's rounding).
+hipError_t launch_rmsnorm_w(const uint16_t* x, int M, int H, float eps, const uint16_t* w, uint16_t* y,
+                            hipStream_t st);
 hipError_t launch_split_book(const uint16_t* book, int entries, int dim, uint16_t* book4, hipStream_t st);
 hipError_t launch_split_book_i8(const int8_t* book, float scale, int entries, int dim, uint16_t* book4,
                                 hipStream_t st);
@@ -285,7 +288,7 @@ hipError_t launch_head_logits(const HeadDev& hd, const uint16_t* h, int M, const
                               hipStream_t st);
 
 // draft head: x = T(T(a) + T(b)) over n values, clearing best[0..M) (best may be null)
-hipError_t launch_fc_join(const float* a, const float* b, int n, uint16_t* x, unsigned long long* best, int M,
+hipError_t launch_fc_join(const float* a, const float* b, int M, int HC, int H, uint16_t* x, unsigned long long* best,
                           hipStream_t st);
 // Row argmax of logits [M, V] (ties to the lowest index) into best[M] (cleared first when
 // `clear`, else it must hold 0), decoded into tokens / values / drafts[r * depth + step]

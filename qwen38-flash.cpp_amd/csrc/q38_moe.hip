@@ -706,7 +706,7 @@ __global__ __launch_bounds__(256) void k_combine_hc(LayerDev L, MoeBufs B, int M
 }
 
 __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x, int H, float eps,
-                                                 uint16_t* __restrict__ y) {
+                                                 const uint16_t* __restrict__ w, uint16_t* __restrict__ y) {
     __shared__ float red[4];
     const int r = blockIdx.x, tid = threadIdx.x;
     float ss = 0.0f;
@@ -719,8 +719,10 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x,
     __syncthreads();
     const float t = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.0f / sqrtf(t / static_cast<float>(H) + eps);
-    for (int c = tid; c < H; c += 256)
-        y[static_cast<size_t>(r) * H + c] = f2bf(bf2f(x[static_cast<size_t>(r) * H + c]) * inv);
+    for (int c = tid; c < H; c += 256) {
+        const float n = rbf(bf2f(x[static_cast<size_t>(r) * H + c]) * inv);
+        y[static_cast<size_t>(r) * H + c] = f2bf(w ? n * bf2f(w[c]) : n);
+    }
 }
 
 // Split a [entries, dim] fp16 codebook into [dim/4][entries][4] chunks.
@@ -968,7 +970,11 @@ hipError_t launch_combine_hc(const LayerDev& L, const MoeBufs& B, int M, uint16_
 }
 
 hipError_t launch_rmsnorm(const uint16_t* x, int M, int H, float eps, uint16_t* y, hipStream_t st) {
-    return launch(k_rmsnorm, dim3(M), dim3(256), 0, st, x, H, eps, y);
+    return launch(k_rmsnorm, dim3(M), dim3(256), 0, st, x, H, eps, static_cast<const uint16_t*>(nullptr), y);
+}
+hipError_t launch_rmsnorm_w(const uint16_t* x, int M, int H, float eps, const uint16_t* w, uint16_t* y,
+                            hipStream_t st) {
+    return launch(k_rmsnorm, dim3(M), dim3(256), 0, st, x, H, eps, w, y);
 }
 
 hipError_t launch_tile_codes(const uint32_t* codes, int64_t rows, int words, int bits, uint32_t* out, hipStream_t st) {

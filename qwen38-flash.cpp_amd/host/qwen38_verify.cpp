@@ -676,6 +676,21 @@ QwenMtpHead::QwenMtpHead(const Context& ctx, std::uint64_t seed, std::size_t voc
 }
 QwenMtpHead::~QwenMtpHead() { q38_mtp_head_destroy(head_); }
 
+void QwenMtpHead::attach_streams(const HyperConnection& block_mixer, const HyperConnection& final_mixer,
+                                 const DeviceTensor& embedding_norm, const DeviceTensor& hidden_norm) {
+    const std::size_t hc = static_cast<std::size_t>(block_mixer.desc().streams);
+    if ((!embedding_norm.empty() && (embedding_norm.numel() != hidden_ || embedding_norm.dtype() != DType::bf16)) ||
+        (!hidden_norm.empty() && (hidden_norm.numel() != hc * hidden_ || hidden_norm.dtype() != DType::bf16)))
+        throw std::runtime_error("MTP norm weights must be bf16 of the hidden size and the stream width");
+    const q38_mtp_streams s{block_mixer.handle(), final_mixer.handle(),
+                            embedding_norm.empty() ? nullptr : static_cast<const uint16_t*>(embedding_norm.data()),
+                            hidden_norm.empty() ? nullptr : static_cast<const uint16_t*>(hidden_norm.data())};
+    check(q38_mtp_head_set_streams(head_, &s), "MTP head streams");
+    streams_ = static_cast<std::size_t>(q38_mtp_head_streams(head_));
+    ws_ = DeviceTensor({q38_mtp_workspace_size(head_, 4)}, DType::u32);
+    streams_dev_ = DeviceTensor({4, width()}, DType::bf16);
+}
+
 void QwenMtpHead::advance(std::size_t query_position, std::size_t rows, MtpDecodeState& state) const {
     if (!state.position_base.has_value()) state.position_base = query_position;
     if (query_position != *state.position_base + state.row_count)
@@ -685,14 +700,14 @@ void QwenMtpHead::advance(std::size_t query_position, std::size_t rows, MtpDecod
 
 MtpDecodeStep QwenMtpHead::forward_decode(const DeviceTensor& stream, std::uint32_t next_token,
                                           std::size_t query_position, MtpDecodeState& state) const {
-    if (stream.shape() != std::vector<std::size_t>{1, 1, hidden_} || stream.dtype() != DType::bf16)
-        throw std::runtime_error("MTP target stream must have shape [1,1,hidden] bf16");
+    if (stream.shape() != std::vector<std::size_t>{1, 1, width()} || stream.dtype() != DType::bf16)
+        throw std::runtime_error("MTP target stream must have shape [1,1,stream width] bf16");
     if (next_token >= vocab_) throw std::runtime_error("MTP token id is out of range");
     MtpDecodeState next = state;
     advance(query_position, 1, next);
     const hipStream_t st = static_cast<hipStream_t>(ctx_->stream());
     check_hip(hipMemcpyAsync(tokens_dev_.data(), &next_token, 4, hipMemcpyHostToDevice, st), "MTP token");
-    MtpDecodeStep out{DeviceTensor({1, 1, vocab_}, DType::f32), DeviceTensor({1, 1, hidden_}, DType::bf16)};
+    MtpDecodeStep out{DeviceTensor({1, 1, vocab_}, DType::f32), DeviceTensor({1, 1, width()}, DType::bf16)};
     check(q38_mtp_forward_decode(head_, static_cast<const uint16_t*>(stream.data()),
                                  static_cast<const uint32_t*>(tokens_dev_.data()), 1, static_cast<float*>(out.logits.data()),
                                  static_cast<uint16_t*>(out.pre_mixer_stream.data()), nullptr, ws_.data(), ws_.nbytes(),
@@ -712,11 +727,11 @@ std::vector<std::vector<std::uint32_t>> QwenMtpHead::draft_greedy_rows(std::span
     if (depth < 1 || depth > 24) throw std::runtime_error("MTP draft depth must be between 1 and 24");
     const hipStream_t st = static_cast<hipStream_t>(ctx_->stream());
     for (std::size_t r = 0; r < rows; ++r) {
-        if (streams[r] == nullptr || streams[r]->numel() != hidden_ || streams[r]->dtype() != DType::bf16)
-            throw std::runtime_error("MTP target stream must have shape [1,1,hidden] bf16");
+        if (streams[r] == nullptr || streams[r]->numel() != width() || streams[r]->dtype() != DType::bf16)
+            throw std::runtime_error("MTP target stream must have shape [1,1,stream width] bf16");
         if (tokens[r] >= vocab_) throw std::runtime_error("MTP token id is out of range");
-        check_hip(hipMemcpyAsync(static_cast<char*>(streams_dev_.data()) + r * hidden_ * 2, streams[r]->data(),
-                                 hidden_ * 2, hipMemcpyDeviceToDevice, st),
+        check_hip(hipMemcpyAsync(static_cast<char*>(streams_dev_.data()) + r * width() * 2, streams[r]->data(),
+                                 width() * 2, hipMemcpyDeviceToDevice, st),
                   "MTP streams");
     }
     check_hip(hipMemcpyAsync(tokens_dev_.data(), tokens.data(), rows * 4, hipMemcpyHostToDevice, st), "MTP tokens");
@@ -746,7 +761,7 @@ std::vector<std::uint32_t> QwenMtpHead::draft_greedy(const DeviceTensor& stream,
 
 void QwenMtpHead::consume_decode(const DeviceTensor& stream, std::uint32_t next_token, std::size_t query_position,
                                  MtpDecodeState& state) const {
-    if (stream.numel() != hidden_) throw std::runtime_error("MTP target stream must have shape [1,1,hidden] bf16");
+    if (stream.numel() != width()) throw std::runtime_error("MTP target stream must have shape [1,1,stream width] bf16");
     if (next_token >= vocab_) throw std::runtime_error("MTP token id is out of range");
     advance(query_position, 1, state);
 }

@@ -431,7 +431,15 @@ public:
     [[nodiscard]] MtpDecodeState snapshot_state(const MtpDecodeState& state) const {
         return snapshot_mtp_decode_state(state);
     }
-    // forward_decode (src/mtp_head.cpp:454-470): target_pre_mixer_stream [1, 1, H] bf16.
+    // The reference head's HC streams (src/mtp_head.cpp:120-170, 223-267, 454-470): the
+    // block's MLP mixer (with injection weights), the final mixer (without), and the raw
+    // pre_fc_norm_embedding [H] and pre_fc_norm_hidden [HC * H] weights (empty: zeros).
+    // Afterwards target streams are [1, 1, HC * H]. The mixers must outlive the head's use.
+    void attach_streams(const HyperConnection& block_mixer, const HyperConnection& final_mixer,
+                        const DeviceTensor& embedding_norm = DeviceTensor(),
+                        const DeviceTensor& hidden_norm = DeviceTensor());
+    [[nodiscard]] std::size_t stream_count() const noexcept { return streams_; }
+    // forward_decode (src/mtp_head.cpp:454-470): target_pre_mixer_stream [1, 1, HC * H] bf16.
     [[nodiscard]] MtpDecodeStep forward_decode(const DeviceTensor& target_pre_mixer_stream, std::uint32_t next_token,
                                                std::size_t query_position, MtpDecodeState& state) const;
     // The greedy draft chain (draft_lazy_chain, src/mtp_runner.cpp:152-211): depth drafts on
@@ -455,7 +463,8 @@ private:
     void advance(std::size_t query_position, std::size_t rows, MtpDecodeState& state) const;
     const Context* ctx_ = nullptr;
     q38_mtp_head* head_ = nullptr;
-    std::size_t hidden_ = 0, vocab_ = 0;
+    [[nodiscard]] std::size_t width() const noexcept { return hidden_ * streams_; }
+    std::size_t hidden_ = 0, vocab_ = 0, streams_ = 1;
     mutable DeviceTensor ws_, tokens_dev_, streams_dev_, drafts_dev_;
 };
 

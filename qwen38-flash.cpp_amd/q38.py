@@ -185,6 +185,14 @@ _sig("q38_hc_workspace_size", SZ, C.POINTER(HcDesc), I32)
 _sig("q38_hc_read", C.c_int, P, P, I32, P, P, P, SZ, P)
 _sig("q38_hc_write", C.c_int, P, P, P, P, I32, P, P)
 _sig("q38_hc_initialize_stream", C.c_int, P, I32, I32, I32, P, P)
+
+
+class MtpStreams(C.Structure):
+    _fields_ = [("block_mixer", P), ("final_mixer", P), ("embedding_norm", P), ("hidden_norm", P)]
+
+
+_sig("q38_mtp_head_set_streams", C.c_int, P, C.POINTER(MtpStreams))
+_sig("q38_mtp_head_streams", C.c_int, P)
 _sig("q38_verify_chain_hc_workspace_size", SZ, C.POINTER(MoeDesc), C.POINTER(HcDesc), I32)
 _sig("q38_verify_chain_hc", C.c_int, P, P, I32, P, I32, P, SZ, P)
 
@@ -292,6 +300,18 @@ class MtpHead:
 
     def workspace_size(self, rows: int) -> int:
         return lib.q38_mtp_workspace_size(self.h, rows)
+
+    def set_streams(self, block: "Hc", final: "Hc", embedding_norm=None, hidden_norm=None):
+        """Run the head on HC streams (q38_mtp_head_set_streams); the mixers and norm tensors
+        must outlive the head's use of them."""
+        self._streams = (block, final, embedding_norm, hidden_norm)
+        s = MtpStreams(block.h, final.h, None if embedding_norm is None else ptr(embedding_norm),
+                       None if hidden_norm is None else ptr(hidden_norm))
+        check(lib.q38_mtp_head_set_streams(self.h, C.byref(s)))
+
+    def clear_streams(self):
+        check(lib.q38_mtp_head_set_streams(self.h, None))
+        self._streams = None
 
     def parts(self):
         layer, fe, fh, dh = P(), P(), P(), P()

@@ -386,6 +386,87 @@ static void gated_delta_net_tests(const qwen38::Context& ctx) {
     std::printf("gated delta net: ok\n");
 }
 
+// The draft head on HC streams (5 streams of the model's hidden size): forward_decode equals
+// the C ABI step bit for bit, the greedy chain equals a replay of single steps, and a
+// single-stream row is refused.
+static void mtp_stream_tests(const qwen38::Context& ctx, const qwen38::QwenModel& model) {
+    const std::size_t H = model.hidden(), HC = 5, R = 256, G = 64, K = H * HC;
+    std::uint64_t st = 0xD1B54A32D192ED03ull;
+    auto next = [&] { st = st * 6364136223846793005ull + 1442695040888963407ull; return static_cast<std::uint32_t>(st >> 32); };
+    auto bf16 = [](float f) { std::uint32_t u; std::memcpy(&u, &f, 4); return static_cast<std::uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16); };
+    auto unit = [&] { return (static_cast<float>(next() >> 8) / 16777216.0f) - 0.5f; };
+    std::vector<qwen38::DeviceTensor> keep;
+    auto u32t = [&](std::size_t n) {
+        std::vector<std::uint32_t> h(n);
+        for (auto& v : h) v = next();
+        keep.emplace_back(std::vector<std::size_t>{n}, qwen38::DType::u32);
+        keep.back().upload(h.data(), n * 4);
+        return static_cast<const std::uint32_t*>(keep.back().data());
+    };
+    auto bft = [&](std::size_t n, float scale, float offset) {
+        std::vector<std::uint16_t> h(n);
+        for (auto& v : h) v = bf16(offset + scale * unit());
+        keep.emplace_back(std::vector<std::size_t>{n}, qwen38::DType::bf16);
+        keep.back().upload(h.data(), n * 2);
+        return static_cast<const std::uint16_t*>(keep.back().data());
+    };
+    keep.reserve(32);
+    auto mixer = [&](bool inj) {
+        q38_hc_weights w{};
+        w.norm = bft(K, 0.2f, 0.0f);
+        w.down_w = u32t(R * K / 8), w.down_s = bft(R * K / G, 0.004f, 0.006f), w.down_b = bft(R * K / G, 0.002f, -0.045f);
+        w.up_w = u32t(K * R / 8), w.up_s = bft(K * R / G, 0.004f, 0.006f), w.up_b = bft(K * R / G, 0.002f, -0.045f);
+        if (inj) w.inj_w = u32t(HC * K / 8), w.inj_s = bft(HC * K / G, 0.004f, 0.006f), w.inj_b = bft(HC * K / G, 0.002f, -0.045f);
+        return qwen38::HyperConnection(ctx, w, H, HC, R, 4, G, 1e-6f, inj);
+    };
+    qwen38::HyperConnection block = mixer(true), final_mixer = mixer(false);
+    qwen38::DeviceTensor en({H}, qwen38::DType::bf16), hn({K}, qwen38::DType::bf16);
+    CHECK(hipMemcpy(en.data(), bft(H, 0.2f, 0.0f), H * 2, hipMemcpyDeviceToDevice) == hipSuccess);
+    CHECK(hipMemcpy(hn.data(), bft(K, 0.2f, 0.0f), K * 2, hipMemcpyDeviceToDevice) == hipSuccess);
+    qwen38::MoeGeometry g;
+    qwen38::QwenMtpHead head(ctx, model.seed(), model.vocab(), g);
+    head.attach_streams(block, final_mixer, en, hn);
+    CHECK(head.stream_count() == HC);
+    // target streams: a verified row tiled over the streams
+    qwen38::DeviceTensor fm, rows;
+    std::vector<qwen38::GreedyStep> gs;
+    model.forward_verify_layer_major(std::vector<std::uint32_t>{321}, fm, gs, nullptr, &rows);
+    qwen38::DeviceTensor one({1, 1, H}, qwen38::DType::bf16);
+    CHECK(hipMemcpy(one.data(), rows.data(), H * 2, hipMemcpyDeviceToDevice) == hipSuccess);
+    const qwen38::DeviceTensor prev = qwen38::HyperConnection::initialize_stream(ctx, one, HC);
+    CHECK(prev.shape() == (std::vector<std::size_t>{1, 1, K}));
+    const std::uint32_t cur = gs[0].token;
+    qwen38::MtpDecodeState rs = head.make_state();
+    const qwen38::MtpDecodeStep s0 = head.forward_decode(prev, cur, 10, rs);
+    CHECK(s0.pre_mixer_stream.shape() == (std::vector<std::size_t>{1, 1, K}));
+    {   // the same step through the C ABI
+        qwen38::DeviceTensor lg({1, model.vocab()}, qwen38::DType::f32), so({1, K}, qwen38::DType::bf16);
+        qwen38::DeviceTensor tok({1}, qwen38::DType::u32), ws({q38_mtp_workspace_size(head.handle(), 1)}, qwen38::DType::u32);
+        tok.upload(&cur, 4);
+        CHECK(q38_mtp_forward_decode(head.handle(), static_cast<const std::uint16_t*>(prev.data()),
+                                     static_cast<const std::uint32_t*>(tok.data()), 1, static_cast<float*>(lg.data()),
+                                     static_cast<std::uint16_t*>(so.data()), nullptr, ws.data(), ws.nbytes(),
+                                     ctx.stream()) == Q38_OK);
+        ctx.synchronize();
+        CHECK(lg.to_host<float>() == s0.logits.to_host<float>());
+        CHECK(so.to_host<std::uint16_t>() == s0.pre_mixer_stream.to_host<std::uint16_t>());
+    }
+    qwen38::MtpDecodeState cs = head.make_state();
+    const auto d = head.draft_greedy(prev, cur, 10, 3, cs);
+    qwen38::MtpDecodeState ps = head.make_state();
+    qwen38::DeviceTensor s = prev.share();
+    std::uint32_t t = cur;
+    for (std::size_t k = 0; k < 3; ++k) {
+        qwen38::MtpDecodeStep step = head.forward_decode(s, t, 10 + k, ps);
+        const auto lg = step.logits.to_host<float>();
+        t = static_cast<std::uint32_t>(std::max_element(lg.begin(), lg.end()) - lg.begin());
+        CHECK(t == d[k]);
+        s = std::move(step.pre_mixer_stream);
+    }
+    CHECK(throws<std::runtime_error>([&] { (void)head.forward_decode(one, cur, 13, ps); }));
+    std::printf("mtp streams: ok\n");
+}
+
 static void draft_head_tests(const qwen38::Context& ctx, const qwen38::QwenModel& model) {
     qwen38::MoeGeometry g;
     qwen38::QwenMtpHead head(ctx, model.seed(), model.vocab(), g);
@@ -683,6 +764,7 @@ static void gpu_tests() {
     draft_head_tests(ctx, model);
     hyper_connection_tests(ctx);
     gated_delta_net_tests(ctx);
+    mtp_stream_tests(ctx, model);
 }
 
 int main(int argc, char** argv) {

@@ -3,8 +3,8 @@ program tests/cpp/host_mirror_test.cpp, built with the library: host KATs and ex
 types on the CPU, the device section (SparseMoe vs the C ABI, verify + commit lifecycle,
 a greedy round, and the engine-side round driver with 3 requests sharing each batched
 verification, every batch recomputed row by row in the same kernel family; the MTP draft head,
-learned-draft rounds and the scheduler drafting with the head; the HyperConnection mixer
-and the GatedDeltaNet verify step against the C ABI) on the GPU."""
+learned-draft rounds and the scheduler drafting with the head; the HyperConnection mixer,
+the GatedDeltaNet verify step and the draft head on HC streams against the C ABI) on the GPU."""
 import os
 import subprocess
 
@@ -33,3 +33,4 @@ def test_gpu_section():
     assert "draft head: ok" in out, out
     assert "hyper connection: ok" in out, out
     assert "gated delta net: ok" in out, out
+    assert "mtp streams: ok" in out, out

@@ -70,6 +70,7 @@ def test_hc_read_rows(gpu, q38, orc, M):
     (2048, 4, 256, 8, 64, True, 4),     # 8-bit projections
     (2048, 4, 256, 4, 32, True, 3),     # 32-input groups
     (2560, 4, 128, 4, 64, True, 4),     # the reference family's hidden size
+    (2048, 5, 256, 4, 64, True, 4),     # 5 streams: the 10240-wide stream of the MTP head
     (2048, 4, 512, 4, 128, False, 2),   # widest rank, no injection (the final mixer)
     (1024, 1, 64, 8, 32, True, 16),     # one stream
     (4096, 8, 256, 4, 64, True, 5),     # widest stream (32768 values)
