@@ -543,6 +543,60 @@ int q38_gdn_verify(q38_gdn* gdn, const uint16_t* x, int32_t rows, const void* or
  * src/mtp_verifier.cpp:129-145): copies checkpoints[row] to state on the stream. */
 int q38_gdn_commit(const q38_gdn* gdn, const void* checkpoints, int32_t row, void* state, void* stream);
 
+/* ------------------------------------------------------------------ full attention (verify)
+ * SelfAttention::forward_verify (src/self_attention.cpp:1450-1720) on its dense path: the
+ * attention half of a full-attention decoder layer for S verify rows of one slot over the
+ * slot's KV cache. The call appends the rows' keys and values to the cache at tokens
+ * cache_tokens .. cache_tokens + S - 1, and row r attends tokens 0 .. cache_tokens + r. Row
+ * r's checkpoint (SelfAttentionState after the row, :1595-1610) is the cache prefix of
+ * cache_tokens + r + 1 tokens, so commit and rollback are the caller's token count: no
+ * device work, and a rejected suffix is overwritten by the next call. The arithmetic is the
+ * reference's explicit decode path (:1240-1305) with its bf16 rounding points: q_proj rows
+ * per head (D query values, then D gate values), k_proj, v_proj; RMS norms of q and k per head
+ * with the q_norm / k_norm weights (1 + w when norm_offset); RoPE on the first rotary_dim
+ * dims (the split-half rotation, cos / sin of position * theta^(-2i / R) rounded to bf16,
+ * :641-679); scores T(T(q . k) * T(1/sqrt D)); the softmax of the float32 scores rounded to
+ * bf16; T(P . V); the gate T(sigmoid); the output projection. Not part of this path: the QSA
+ * block selection (the reference builds its mask only once a context exceeds the indexer
+ * budget, :764-766; within the budget the results agree) and the Q8 KV cache. */
+typedef struct q38_attn q38_attn;
+typedef struct q38_attn_desc {
+    int32_t hidden;       /* H: a multiple of the group and of 32, at most 8192                */
+    int32_t q_heads;      /* HQ (num_attention_heads)                                         */
+    int32_t kv_heads;     /* HKV (num_key_value_heads); HQ a multiple of it                   */
+    int32_t head_dim;     /* D: 64, 128 or 256                                                */
+    int32_t rotary_dim;   /* R: even, 0 < R <= D (head_dim * partial_rotary_factor)            */
+    int32_t bits;         /* 2, 4 or 8                                                        */
+    int32_t group;        /* 32, 64 or 128                                                    */
+    int32_t scale_dtype;  /* 0 bf16, 1 fp16 scales and biases                                 */
+    int32_t norm_offset;  /* 1: the norms apply 1 + weight (attention_norm_has_offset)         */
+    float eps;            /* rms_norm_eps                                                     */
+    double rope_theta;
+} q38_attn_desc;
+typedef struct q38_attn_weights {
+    const uint32_t* weight[4];  /* q_proj [2 HQ D][H], k_proj [HKV D][H], v_proj, o_proj [H][HQ D] */
+    const uint16_t* scales[4];
+    const uint16_t* biases[4];
+    const uint16_t* q_norm;     /* [D] bf16                                                   */
+    const uint16_t* k_norm;     /* [D] bf16                                                   */
+} q38_attn_weights;
+/* SelfAttention::SelfAttention (src/self_attention.cpp:460-521): adopts the device weight
+ * pointers (they must stay alive); the norm weights are copied (1 + w formed when
+ * norm_offset). */
+int q38_attn_create(q38_ctx* ctx, const q38_attn_desc* desc, const q38_attn_weights* weights, q38_attn** out);
+void q38_attn_destroy(q38_attn* attn);
+/* Bytes of a KV cache of `capacity` tokens: keys [HKV][capacity][D] bf16, then values. */
+size_t q38_attn_cache_bytes(const q38_attn* attn, int64_t capacity);
+/* Workspace for calls of up to max_rows rows (1..64) with up to max_tokens tokens after the
+ * call (cache_tokens + rows). */
+size_t q38_attn_workspace_size(const q38_attn* attn, int32_t max_rows, int64_t max_tokens);
+/* x [rows, H] bf16 -> out [rows, H] bf16; cache: 16-byte aligned, q38_attn_cache_bytes(capacity)
+ * bytes, cache_tokens valid tokens; position: the position of row 0 (the state's position_base
+ * + token_count). Q38_ERANGE when cache_tokens + rows exceeds capacity. */
+int q38_attn_verify(q38_attn* attn, const uint16_t* x, int32_t rows, void* cache, int64_t capacity,
+                    int64_t cache_tokens, int64_t position, uint16_t* out, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* ------------------------------------------------------------------ HyperConnection mixer
  * The stream mixer around a decoder block (HyperConnection, include/qwen38/hyper_connection.hpp:18-40,
  * src/hyper_connection.cpp:150-211 for the weights, :309-493 read, :692-709 write). A row's state

@@ -1189,6 +1189,146 @@ void gdn_verify(const GdnDesc& d, const GdnW& W, const uint16_t* x, int S, const
         }
     }
 }
+// ---- full attention, verify (SelfAttention::forward_verify, src/self_attention.cpp:1450-1720,
+// on its dense path: no QSA mask, which the reference builds only once a context exceeds the
+// indexer budget, :764-766, and a bf16 KV cache). The rounding points are those of the
+// explicit decode path (:1240-1305), which the batched path computes in one pass:
+//   projections    qg = T(q_proj x) [HQ][2 D] (per head D query values, then D gate values,
+//                  :1464-1466 / :1481-1488), k = T(k_proj x), v = T(v_proj x) [HKV][D]
+//   q / k norms    rms_norm per head: T(wn * T(x * inv)), inv = 1 / sqrt(mean(x^2) + eps),
+//                  wn = w, or T(1 + w) with an offset norm (effective_norm_weight, :52-58)
+//   RoPE           (:641-679) on the first R dims at position p: c_i, s_i = bf16 of
+//                  float(cos / sin(p * theta^(-2i / R))) in double, i < R / 2, repeated for
+//                  the second half; x'_j = T(T(x_j * c_j) + T(rot_j * s_j)),
+//                  rot = (-x_{j + R/2} for j < R/2, x_{j - R/2} after); dims >= R unchanged
+//   cache          keys / values [HKV][T][D]: the origin's T0 tokens, then the S rows
+//   scores         row r, query head h (kv head h / (HQ / HKV)) over tokens t <= T0 + r:
+//                  s_t = T(T(q . k_t) * T(1 / sqrt D)) (:1299-1302)
+//   softmax        of the float32 scores: e_t = exp(s_t - max s), p_t = T(e_t / sum e) (:1303)
+//   output         attended = T(sum_t p_t v_t), gated = T(attended * T(sigmoid(gate)))
+//                  (:1321-1323), out = T(o_proj gated)
+// Positions: row r of the call is at position + r (origin.position_base + token_count, :1254).
+struct AttnDesc {
+    int hidden, q_heads, kv_heads, head_dim, rotary_dim, bits, group, fmt, norm_offset;
+    float eps;
+    double rope_theta;
+};
+struct AttnW {
+    AffineProj q, k, v, o;
+    const uint16_t* q_norm;  // [D] bf16
+    const uint16_t* k_norm;  // [D] bf16
+};
+int g_attn_fault;  // planted faults (tests only): 1 = RoPE on adjacent pairs, 2 = no causal mask within the rows
+
+// The bf16 RoPE table of one position: c[i], s[i] for i < R / 2.
+void rope_table(double theta, int R, int64_t pos, float* c, float* s) {
+    for (int i = 0; i < R / 2; ++i) {
+        const double freq = std::pow(theta, -2.0 * static_cast<double>(i) / static_cast<double>(R));
+        const double angle = static_cast<double>(pos) * freq;
+        c[i] = rbf16(static_cast<float>(std::cos(angle)));
+        s[i] = rbf16(static_cast<float>(std::sin(angle)));
+    }
+}
+
+// rms_norm of one head (T(wn * T(x * inv))) then RoPE at pos, in place on D values.
+void attn_norm_rope(float* x, int D, int R, const float* wn, float eps, double theta, int64_t pos) {
+    double ss = 0.0;
+    for (int i = 0; i < D; ++i) ss += static_cast<double>(x[i]) * x[i];
+    const float inv = static_cast<float>(1.0 / std::sqrt(ss / D + static_cast<double>(eps)));
+    for (int i = 0; i < D; ++i) x[i] = tb(wn[i] * tb(x[i] * inv));
+    std::vector<float> c(R / 2), sn(R / 2), y(R);
+    rope_table(theta, R, pos, c.data(), sn.data());
+    const int half = R / 2;
+    for (int j = 0; j < R; ++j) {
+        float rot, cj, sj;
+        if (g_attn_fault == 1) {  // interleaved pairs (2i, 2i + 1), the other RoPE convention
+            const int i = j / 2;
+            rot = (j % 2 == 0) ? -x[j + 1] : x[j - 1];
+            cj = c[i];
+            sj = sn[i];
+        } else {
+            rot = j < half ? -x[j + half] : x[j - half];
+            cj = c[j % half];
+            sj = sn[j % half];
+        }
+        y[j] = tb(tb(x[j] * cj) + tb(rot * sj));
+    }
+    for (int j = 0; j < R; ++j) x[j] = y[j];
+}
+
+// keys / values: [HKV][cap][D] bf16 with the origin's T0 tokens; the S new rows are written at
+// T0..T0+S-1 (the cache after the call); out [S][H].
+void attn_verify(const AttnDesc& d, const AttnW& W, const uint16_t* x, int S, uint16_t* keys, uint16_t* values,
+                 int64_t cap, int64_t T0, int64_t position, uint16_t* out) {
+    const int H = d.hidden, HQ = d.q_heads, HKV = d.kv_heads, D = d.head_dim, R = d.rotary_dim;
+    const int grp = HQ / HKV;
+    std::vector<float> qn(D), kn(D);
+    for (int i = 0; i < D; ++i) {
+        const float qw = bf16_to_f32(W.q_norm[i]), kw = bf16_to_f32(W.k_norm[i]);
+        qn[i] = d.norm_offset ? tb(1.0f + qw) : qw;
+        kn[i] = d.norm_offset ? tb(1.0f + kw) : kw;
+    }
+    std::vector<float> xf(H), q(static_cast<size_t>(S) * HQ * D), gate(static_cast<size_t>(S) * HQ * D);
+    for (int r = 0; r < S; ++r) {
+        for (int c = 0; c < H; ++c) xf[c] = bf16_to_f32(x[static_cast<size_t>(r) * H + c]);
+        const int64_t pos = position + r;
+        for (int h = 0; h < HQ; ++h) {
+            float* qh = q.data() + (static_cast<size_t>(r) * HQ + h) * D;
+            for (int i = 0; i < D; ++i) {
+                qh[i] = rbf16(affine_row_dot(W.q, h * 2 * D + i, xf.data()));
+                gate[(static_cast<size_t>(r) * HQ + h) * D + i] =
+                    sigmoid_t(rbf16(affine_row_dot(W.q, h * 2 * D + D + i, xf.data())));
+            }
+            attn_norm_rope(qh, D, R, qn.data(), d.eps, d.rope_theta, pos);
+        }
+        std::vector<float> kh(D);
+        for (int g = 0; g < HKV; ++g) {
+            for (int i = 0; i < D; ++i) kh[i] = rbf16(affine_row_dot(W.k, g * D + i, xf.data()));
+            attn_norm_rope(kh.data(), D, R, kn.data(), d.eps, d.rope_theta, pos);
+            uint16_t* kd = keys + (static_cast<size_t>(g) * cap + T0 + r) * D;
+            uint16_t* vd = values + (static_cast<size_t>(g) * cap + T0 + r) * D;
+            for (int i = 0; i < D; ++i) {
+                kd[i] = f32_to_bf16(kh[i]);
+                vd[i] = f32_to_bf16(rbf16(affine_row_dot(W.v, g * D + i, xf.data())));
+            }
+        }
+    }
+    const float scale = tb(static_cast<float>(1.0 / std::sqrt(static_cast<double>(D))));
+    std::vector<float> gated(static_cast<size_t>(HQ) * D);
+    for (int r = 0; r < S; ++r) {
+        const int64_t T = g_attn_fault == 2 ? T0 + S : T0 + r + 1;
+        for (int h = 0; h < HQ; ++h) {
+            const int g = h / grp;
+            const float* qh = q.data() + (static_cast<size_t>(r) * HQ + h) * D;
+            std::vector<float> sc(static_cast<size_t>(T));
+            float m = -INFINITY;
+            for (int64_t t = 0; t < T; ++t) {
+                const uint16_t* kt = keys + (static_cast<size_t>(g) * cap + t) * D;
+                double dot = 0.0;
+                for (int i = 0; i < D; ++i) dot += static_cast<double>(qh[i]) * bf16_to_f32(kt[i]);
+                sc[t] = tb(rbf16(dot) * scale);
+                m = std::max(m, sc[t]);
+            }
+            double sum = 0.0;
+            std::vector<float> e(static_cast<size_t>(T));
+            for (int64_t t = 0; t < T; ++t) {
+                e[t] = static_cast<float>(std::exp(static_cast<double>(sc[t] - m)));
+                sum += e[t];
+            }
+            std::vector<double> acc(D, 0.0);
+            for (int64_t t = 0; t < T; ++t) {
+                const float pt = rbf16(static_cast<double>(e[t]) / static_cast<double>(static_cast<float>(sum)));
+                const uint16_t* vt = values + (static_cast<size_t>(g) * cap + t) * D;
+                for (int i = 0; i < D; ++i) acc[i] += static_cast<double>(pt) * bf16_to_f32(vt[i]);
+            }
+            for (int i = 0; i < D; ++i)
+                gated[static_cast<size_t>(h) * D + i] = tb(rbf16(acc[i]) * gate[(static_cast<size_t>(r) * HQ + h) * D + i]);
+        }
+        for (int o = 0; o < H; ++o)
+            out[static_cast<size_t>(r) * H + o] = f32_to_bf16(rbf16(affine_row_dot(W.o, o, gated.data())));
+    }
+}
+
 } // namespace
 
 // ======================================================================== C ABI
@@ -1610,6 +1750,28 @@ int orc_gdn_verify(const GdnDesc* d, const uint32_t* const* w, const uint16_t* c
     W.dt_bias = dt_bias;
     W.norm_w = norm_w;
     gdn_verify(*d, W, x, S, origin, out, ckpt);
+    return 0;
+}
+
+void orc_attn_plant_fault(int f) { g_attn_fault = f; }
+void orc_rope_table(double theta, int R, int64_t pos, float* c, float* s) { rope_table(theta, R, pos, c, s); }
+int orc_attn_verify(const AttnDesc* d, const uint32_t* const* w, const uint16_t* const* sc, const uint16_t* const* bi,
+                    const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* x, int S, uint16_t* keys,
+                    uint16_t* values, int64_t cap, int64_t T0, int64_t position, uint16_t* out) {
+    if (!d || S < 1 || d->q_heads % d->kv_heads || d->rotary_dim <= 0 || d->rotary_dim % 2 ||
+        d->rotary_dim > d->head_dim || d->bits <= 0 || 32 % d->bits || d->group <= 0 || T0 < 0 || T0 + S > cap)
+        return -1;
+    const int QW = d->q_heads * d->head_dim, KW = d->kv_heads * d->head_dim;
+    const int ins[4] = {d->hidden, d->hidden, d->hidden, QW}, outs[4] = {2 * QW, KW, KW, d->hidden};
+    AttnW W{};
+    AffineProj* P[4] = {&W.q, &W.k, &W.v, &W.o};
+    for (int p = 0; p < 4; ++p) {
+        if (ins[p] % d->group) return -1;
+        *P[p] = AffineProj{w[p], sc[p], bi[p], ins[p], outs[p], d->bits, d->group, d->fmt};
+    }
+    W.q_norm = q_norm;
+    W.k_norm = k_norm;
+    attn_verify(*d, W, x, S, keys, values, cap, T0, position, out);
     return 0;
 }
 

@@ -93,6 +93,78 @@ hipError_t launch_sa(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st)
            : cd >= 16 ? launch_sa_dn_t<BITS, 16>(L, B, M, st)
                       : launch_sa_dn_t<BITS, 8>(L, B, M, st);
 }
+// Rows of several affine projections of the same S input rows in one launch: workgroup
+// blocks [p.first_block, next first_block) take projection p's weight rows, a lane group of
+// LPR lanes per weight row, up to 16 input rows staged in LDS with their 32-input sums.
+template <int BITS, int LPR>
+__global__ __launch_bounds__(kSaThreads) void k_affine_rows(AffineRowSet set, const uint16_t* __restrict__ x, int S,
+                                                         int IN, int G, int f16, int rows_wg) {
+    extern __shared__ __align__(16) uint16_t xs[];  // [rows_wg][IN], then the chunk sums [rows_wg][IN / 32]
+    const int r0 = blockIdx.y * rows_wg, nr = S - r0 < rows_wg ? S - r0 : rows_wg;
+    float* sxs = reinterpret_cast<float*>(xs + static_cast<size_t>(rows_wg) * IN);
+    // the projection of this block (uniform selects over the argument block)
+    const int bx = static_cast<int>(blockIdx.x);
+    const int pi = set.n > 3 && bx >= set.p[3].first_block ? 3
+                   : set.n > 2 && bx >= set.p[2].first_block ? 2
+                   : set.n > 1 && bx >= set.p[1].first_block ? 1
+                                                             : 0;
+    const AffineRows P = pi == 3 ? set.p[3] : pi == 2 ? set.p[2] : pi == 1 ? set.p[1] : set.p[0];
+    sa_stage(x, IN, r0, nr, xs);
+    __syncthreads();
+    sa_chunk_sums(xs, IN, nr, sxs, kSaThreads);
+    __syncthreads();
+    constexpr int OPW = 64 / LPR;
+    const int o = ((bx - P.first_block) * (kSaThreads / 64) + (threadIdx.x >> 6)) * OPW + (threadIdx.x & 63) / LPR;
+    if (o >= P.out) return;
+    const int wpr = IN * BITS / 32, ngrp = IN / G;
+    float acc[kSaRows];
+    sa_row_dot_sx<BITS, LPR>(P.w + static_cast<size_t>(o) * wpr, P.s + static_cast<size_t>(o) * ngrp,
+                             P.b + static_cast<size_t>(o) * ngrp, IN, G, f16, xs, sxs, nr, acc);
+    if ((threadIdx.x & 63) % LPR == 0)
+#pragma unroll
+        for (int r = 0; r < kSaRows; ++r)
+            if (r < nr) P.dst[static_cast<size_t>(r0 + r) * P.dst_stride + o] = f2bf(acc[r]);
+}
+
+int proj_lpr(int IN, int out) {
+    const int c = IN / 32;
+    const int lpr = c >= 256 ? 64 : c >= 128 ? 32 : c >= 64 ? 16 : 8;
+    // (fewer weight rows per workgroup where the projection has few rows: at least ~512
+    // workgroups for 256 CUs)
+    return out / (kSaThreads / 64 * (64 / lpr)) < 512 && lpr < 64 && c >= 2 * lpr ? 2 * lpr : lpr;
+}
+
+template <int BITS, int LPR>
+hipError_t launch_proj_t(AffineRowSet set, int blocks, const uint16_t* x, int S, int IN, int G, int f16,
+                         hipStream_t st) {
+    // staged rows: up to 16, fewer for wide inputs (the staging stays within 144 KiB of LDS)
+    int rows = static_cast<int>((144 * 1024) / (static_cast<size_t>(IN) * 2 + static_cast<size_t>(IN) / 8));
+    rows = rows > kSaRows ? kSaRows : rows;
+    rows = rows > S ? S : rows;
+    if (rows < 1) return hipErrorInvalidValue;
+    const size_t lds = static_cast<size_t>(rows) * IN * 2 + static_cast<size_t>(rows) * (IN / 32) * 4;
+    if (const hipError_t e = ensure_lds<k_affine_rows<BITS, LPR>>(lds); e != hipSuccess) return e;
+    return launch(k_affine_rows<BITS, LPR>, dim3(blocks, (S + rows - 1) / rows), dim3(kSaThreads), lds, st, set, x, S, IN,
+                  G, f16, rows);
+}
+template <int BITS>
+hipError_t launch_proj_b(AffineRowSet set, const uint16_t* x, int S, int IN, int G, int f16, hipStream_t st) {
+    int rows_out = 0;
+    for (int i = 0; i < set.n; ++i) rows_out += set.p[i].out;
+    const int lpr = proj_lpr(IN, rows_out);
+    int blocks = 0;
+    const int per = kSaThreads / 64 * (64 / lpr);
+    for (int i = 0; i < set.n; ++i) {
+        set.p[i].first_block = blocks;
+        blocks += (set.p[i].out + per - 1) / per;
+    }
+    switch (lpr) {
+        case 64: return launch_proj_t<BITS, 64>(set, blocks, x, S, IN, G, f16, st);
+        case 32: return launch_proj_t<BITS, 32>(set, blocks, x, S, IN, G, f16, st);
+        case 16: return launch_proj_t<BITS, 16>(set, blocks, x, S, IN, G, f16, st);
+        default: return launch_proj_t<BITS, 8>(set, blocks, x, S, IN, G, f16, st);
+    }
+}
 } // namespace
 
 hipError_t launch_shared_affine(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
@@ -101,6 +173,16 @@ hipError_t launch_shared_affine(const LayerDev& L, const MoeBufs& B, int M, hipS
         case 2: return launch_sa<2>(L, B, M, st);
         case 4: return launch_sa<4>(L, B, M, st);
         case 8: return launch_sa<8>(L, B, M, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_affine_rows(const AffineRowSet& set, const uint16_t* x, int S, int IN, int G, int bits, int f16,
+                              hipStream_t st) {
+    switch (bits) {
+        case 2: return launch_proj_b<2>(set, x, S, IN, G, f16, st);
+        case 4: return launch_proj_b<4>(set, x, S, IN, G, f16, st);
+        case 8: return launch_proj_b<8>(set, x, S, IN, G, f16, st);
         default: return hipErrorInvalidValue;
     }
 }

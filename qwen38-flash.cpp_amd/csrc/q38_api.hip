@@ -736,6 +736,132 @@ int q38_gdn_commit(const q38_gdn* gdn, const void* checkpoints, int32_t row, voi
     return Q38_OK;
 }
 
+// ------------------------------------------------------------------ full attention verify
+struct q38_attn {
+    q38_ctx* ctx;
+    q38_attn_desc desc;
+    AttnDev dev;
+    uint16_t* norms;  // effective q and k norm weights [2][D] (owned)
+};
+
+int q38_attn_create(q38_ctx* ctx, const q38_attn_desc* desc, const q38_attn_weights* w, q38_attn** out) {
+    if (!ctx || !desc || !w || !out) return fail(Q38_EINVAL, "q38_attn_create: null argument");
+    const q38_attn_desc& d = *desc;
+    // the reference's check (src/self_attention.cpp:515-520), then what the kernels take
+    if (d.hidden <= 0 || d.q_heads <= 0 || d.kv_heads <= 0 || d.head_dim <= 0)
+        return fail(Q38_EINVAL, "attention dimensions must be positive");
+    if (d.q_heads % d.kv_heads != 0 || d.rotary_dim <= 0 || d.rotary_dim % 2 != 0 || d.rotary_dim > d.head_dim)
+        return fail(Q38_EINVAL, "unsupported attention head/rotary configuration");
+    if (!attn_geometry_ok(d.hidden, d.q_heads, d.kv_heads, d.head_dim, d.rotary_dim))
+        return fail(Q38_EINVAL, "attention head dimension must be 64, 128 or 256");
+    if (d.bits != 2 && d.bits != 4 && d.bits != 8) return fail(Q38_EINVAL, "attention projections: bits must be 2, 4 or 8");
+    if (d.group != 32 && d.group != 64 && d.group != 128)
+        return fail(Q38_EINVAL, "attention projections: group must be 32, 64 or 128");
+    if (d.scale_dtype != 0 && d.scale_dtype != 1) return fail(Q38_EINVAL, "scale_dtype must be 0 (bf16) or 1 (fp16)");
+    if (d.norm_offset != 0 && d.norm_offset != 1) return fail(Q38_EINVAL, "norm_offset must be 0 or 1");
+    if (!(d.eps > 0.0f) || !(d.rope_theta > 0.0)) return fail(Q38_EINVAL, "eps and rope_theta must be positive");
+    const int QW = d.q_heads * d.head_dim;
+    if (d.hidden % d.group || QW % d.group || d.hidden % 32 || d.hidden > 8192 || QW > 16384)
+        return fail(Q38_EINVAL, "hidden and HQ * D must be multiples of the group (hidden <= 8192, HQ * D <= 16384)");
+    AttnDev A{};
+    A.hidden = d.hidden;
+    A.hq = d.q_heads;
+    A.hkv = d.kv_heads;
+    A.d = d.head_dim;
+    A.rot = d.rotary_dim;
+    A.bits = d.bits;
+    A.group = d.group;
+    A.f16 = d.scale_dtype;
+    A.eps = d.eps;
+    A.theta = d.rope_theta;
+    for (int p = 0; p < 4; ++p) {
+        if (!w->weight[p] || !w->scales[p] || !w->biases[p]) return fail(Q38_EINVAL, "q38_attn_create: null projection");
+        A.w[p] = w->weight[p];
+        A.s[p] = w->scales[p];
+        A.b[p] = w->biases[p];
+    }
+    if (!w->q_norm || !w->k_norm) return fail(Q38_EINVAL, "q38_attn_create: null norm weight");
+    uint16_t* norms = nullptr;
+    const size_t D = static_cast<size_t>(d.head_dim);
+    if (hipMalloc(&norms, 2 * D * 2) != hipSuccess) return fail(Q38_ENOMEM, "hipMalloc failed for the attention norms");
+    hipError_t e = hipSuccess;
+    if (d.norm_offset) {
+        e = launch_hc_norm_weight(w->q_norm, static_cast<int>(D), norms, nullptr);
+        if (e == hipSuccess) e = launch_hc_norm_weight(w->k_norm, static_cast<int>(D), norms + D, nullptr);
+    } else {
+        e = hipMemcpy(norms, w->q_norm, D * 2, hipMemcpyDeviceToDevice);
+        if (e == hipSuccess) e = hipMemcpy(norms + D, w->k_norm, D * 2, hipMemcpyDeviceToDevice);
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(norms);
+        return hip_fail(e, "attention norm weights");
+    }
+    A.qn = norms;
+    A.kn = norms + D;
+    *out = new q38_attn{ctx, d, A, norms};
+    return Q38_OK;
+}
+
+void q38_attn_destroy(q38_attn* a) {
+    if (!a) return;
+    (void)hipFree(a->norms);
+    delete a;
+}
+
+size_t q38_attn_cache_bytes(const q38_attn* a, int64_t capacity) {
+    if (!a || capacity < 1) return 0;
+    return 2 * static_cast<size_t>(a->desc.kv_heads) * static_cast<size_t>(capacity) * a->desc.head_dim * 2;
+}
+
+static size_t attn_ws(const q38_attn* a, int S, int64_t tokens, AttnBufs* b, void* base) {
+    const q38_attn_desc& d = a->desc;
+    const size_t QW = static_cast<size_t>(d.q_heads) * d.head_dim, KW = static_cast<size_t>(d.kv_heads) * d.head_dim;
+    const size_t NQ = static_cast<size_t>(S) * d.q_heads;
+    size_t off = 0;
+    char* p = static_cast<char*>(base);
+    auto take = [&](size_t bytes) {
+        char* q = p ? p + off : nullptr;
+        off += align256(bytes);
+        return q;
+    };
+    AttnBufs t{};
+    t.qg = reinterpret_cast<uint16_t*>(take(S * 2 * QW * 2));
+    t.kr = reinterpret_cast<uint16_t*>(take(S * KW * 2));
+    t.vr = reinterpret_cast<uint16_t*>(take(S * KW * 2));
+    t.q = reinterpret_cast<uint16_t*>(take(S * QW * 2));
+    t.gs = reinterpret_cast<uint16_t*>(take(S * QW * 2));
+    t.sc = reinterpret_cast<uint16_t*>(take(NQ * static_cast<size_t>(attn_score_stride(tokens)) * 2));
+    t.mx = reinterpret_cast<float*>(take(NQ * 4));
+    t.sm = reinterpret_cast<float*>(take(NQ * 4));
+    t.part = reinterpret_cast<float*>(take(static_cast<size_t>(attn_pv_tiles(tokens)) * NQ * d.head_dim * 4));
+    t.gated = reinterpret_cast<uint16_t*>(take(S * QW * 2));
+    if (b) *b = t;
+    return off;
+}
+
+size_t q38_attn_workspace_size(const q38_attn* a, int32_t max_rows, int64_t max_tokens) {
+    if (!a || max_rows < 1 || max_rows > 64 || max_tokens < max_rows) return 0;
+    return attn_ws(a, max_rows, max_tokens, nullptr, nullptr);
+}
+
+int q38_attn_verify(q38_attn* a, const uint16_t* x, int32_t rows, void* cache, int64_t capacity, int64_t cache_tokens,
+                    int64_t position, uint16_t* out, void* ws, size_t ws_bytes, void* stream) {
+    if (!a || !x || !cache || !out || !ws) return fail(Q38_EINVAL, "q38_attn_verify: null argument");
+    if (rows < 1 || rows > 64) return fail(Q38_EINVAL, "attention batch requires shape [1,S,hidden], S=1..64");
+    if (cache_tokens < 0 || position < 0 || capacity < 1)
+        return fail(Q38_EINVAL, "attention cache tokens and position must not be negative");
+    if (cache_tokens + rows > capacity) return fail(Q38_ERANGE, "attention cache capacity exceeded");
+    if (reinterpret_cast<uintptr_t>(cache) % 16) return fail(Q38_EINVAL, "q38_attn_verify: cache must be 16-byte aligned");
+    AttnBufs b{};
+    if (ws_bytes < attn_ws(a, rows, cache_tokens + rows, &b, ws)) return fail(Q38_ESPACE, "workspace too small");
+    uint16_t* keys = static_cast<uint16_t*>(cache);
+    uint16_t* values = keys + static_cast<size_t>(a->desc.kv_heads) * static_cast<size_t>(capacity) * a->desc.head_dim;
+    Q38_HIP(launch_attn_verify(a->dev, b, rows, x, keys, values, capacity, cache_tokens, position, out,
+                               static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
 void q38_moe_layer_destroy(q38_moe_layer* layer) {
     if (!layer) return;
     if (layer->owned) (void)hipFree(layer->owned);

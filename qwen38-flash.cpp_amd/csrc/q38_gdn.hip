@@ -3,9 +3,10 @@
 // row's checkpoint (GatedDeltaNet::forward_verify, src/gated_delta_net.cpp:657-834).
 //
 // Five launches:
-//   k_gdn_proj      the affine projections qkv, z, b (beta) and a (decay) of the S rows in
-//                   one launch: a workgroup takes a block of one projection's weight rows for
-//                   up to 16 staged rows; outputs rounded to bf16 (quantized_matmul's output);
+//   k_affine_rows   the affine projections qkv, z, b (beta) and a (decay) of the S rows in
+//                   one launch (q38_affine.hip): a workgroup takes a block of one projection's
+//                   weight rows for up to 16 staged rows; outputs rounded to bf16
+//                   (quantized_matmul's output);
 //   k_gdn_prework   per (row, head): the depthwise width-4 convolution over [origin conv rows ;
 //                   qkv rows] and SiLU (T(c * T(sigmoid c))), the q / k RMS norms with the
 //                   1/DK and 1/sqrt(DK) scales, v, and per value head beta = T(sigmoid b) and
@@ -20,7 +21,7 @@
 //                   recurrent part of every row's checkpoint;
 //   k_gdn_norm_gate per (row, value head): T(w * T(y / rms(y))) times the gate T(sigmoid z)
 //                   or SiLU T(z * T(sigmoid z)), rounded (:809, :824-833);
-//   k_gdn_proj      the output projection.
+//   k_affine_rows   the output projection.
 // A state (q38_gdn_state_bytes) is the conv rows [3][C] bf16 followed by the recurrent state
 // [HV][DV][DK] bf16, C = 2 HK DK + HV DV; value head h reads key head h / (HV / HK).
 #include "q38_affine.hpp"
@@ -31,50 +32,6 @@ namespace {
 
 __device__ __forceinline__ float tbf(float v) { return bf2f(f2bf(v)); }
 __device__ __forceinline__ float sigmoid_bf(float x) { return tbf(1.0f / (1.0f + expf(-x))); }
-
-// One projection of a k_gdn_proj launch: weight rows [out, IN], destination rows of stride
-// dst_stride (bf16).
-struct GdnProj {
-    const uint32_t* w;
-    const uint16_t* s;
-    const uint16_t* b;
-    uint16_t* dst;
-    int out, dst_stride, first_block;
-};
-struct GdnProjSet {
-    GdnProj p[4];
-    int n;
-};
-
-template <int BITS, int LPR>
-__global__ __launch_bounds__(kSaThreads) void k_gdn_proj(GdnProjSet set, const uint16_t* __restrict__ x, int S,
-                                                         int IN, int G, int f16, int rows_wg) {
-    extern __shared__ __align__(16) uint16_t xs[];  // [rows_wg][IN], then the chunk sums [rows_wg][IN / 32]
-    const int r0 = blockIdx.y * rows_wg, nr = S - r0 < rows_wg ? S - r0 : rows_wg;
-    float* sxs = reinterpret_cast<float*>(xs + static_cast<size_t>(rows_wg) * IN);
-    // the projection of this block (uniform selects over the argument block)
-    const int bx = static_cast<int>(blockIdx.x);
-    const int pi = set.n > 3 && bx >= set.p[3].first_block ? 3
-                   : set.n > 2 && bx >= set.p[2].first_block ? 2
-                   : set.n > 1 && bx >= set.p[1].first_block ? 1
-                                                             : 0;
-    const GdnProj P = pi == 3 ? set.p[3] : pi == 2 ? set.p[2] : pi == 1 ? set.p[1] : set.p[0];
-    sa_stage(x, IN, r0, nr, xs);
-    __syncthreads();
-    sa_chunk_sums(xs, IN, nr, sxs, kSaThreads);
-    __syncthreads();
-    constexpr int OPW = 64 / LPR;
-    const int o = ((bx - P.first_block) * (kSaThreads / 64) + (threadIdx.x >> 6)) * OPW + (threadIdx.x & 63) / LPR;
-    if (o >= P.out) return;
-    const int wpr = IN * BITS / 32, ngrp = IN / G;
-    float acc[kSaRows];
-    sa_row_dot_sx<BITS, LPR>(P.w + static_cast<size_t>(o) * wpr, P.s + static_cast<size_t>(o) * ngrp,
-                             P.b + static_cast<size_t>(o) * ngrp, IN, G, f16, xs, sxs, nr, acc);
-    if ((threadIdx.x & 63) % LPR == 0)
-#pragma unroll
-        for (int r = 0; r < kSaRows; ++r)
-            if (r < nr) P.dst[static_cast<size_t>(r0 + r) * P.dst_stride + o] = f2bf(acc[r]);
-}
 
 // conv + SiLU of row t, channels cb + lane * CPL + i; q / k heads normalised.
 template <int CPL>
@@ -233,55 +190,6 @@ __global__ __launch_bounds__(64) void k_gdn_norm_gate(GdnDev G, GdnBufs B, int S
 
 // Lanes per weight row: about four 32-input chunks per lane (16 weight rows per workgroup at
 // H = 2048), 8 to 64 lanes.
-int proj_lpr(int IN, int out) {
-    const int c = IN / 32;
-    const int lpr = c >= 256 ? 64 : c >= 128 ? 32 : c >= 64 ? 16 : 8;
-    // (fewer weight rows per workgroup where the projection has few rows: at least ~512
-    // workgroups for 256 CUs)
-    return out / (kSaThreads / 64 * (64 / lpr)) < 512 && lpr < 64 && c >= 2 * lpr ? 2 * lpr : lpr;
-}
-
-template <int BITS, int LPR>
-hipError_t launch_proj_t(GdnProjSet set, int blocks, const uint16_t* x, int S, int IN, int G, int f16,
-                         hipStream_t st) {
-    // staged rows: up to 16, fewer for wide inputs (the staging stays within 144 KiB of LDS)
-    int rows = static_cast<int>((144 * 1024) / (static_cast<size_t>(IN) * 2 + static_cast<size_t>(IN) / 8));
-    rows = rows > kSaRows ? kSaRows : rows;
-    rows = rows > S ? S : rows;
-    if (rows < 1) return hipErrorInvalidValue;
-    const size_t lds = static_cast<size_t>(rows) * IN * 2 + static_cast<size_t>(rows) * (IN / 32) * 4;
-    if (const hipError_t e = ensure_lds<k_gdn_proj<BITS, LPR>>(lds); e != hipSuccess) return e;
-    return launch(k_gdn_proj<BITS, LPR>, dim3(blocks, (S + rows - 1) / rows), dim3(kSaThreads), lds, st, set, x, S, IN,
-                  G, f16, rows);
-}
-template <int BITS>
-hipError_t launch_proj_b(GdnProjSet set, const uint16_t* x, int S, int IN, int G, int f16, hipStream_t st) {
-    int rows_out = 0;
-    for (int i = 0; i < set.n; ++i) rows_out += set.p[i].out;
-    const int lpr = proj_lpr(IN, rows_out);
-    int blocks = 0;
-    const int per = kSaThreads / 64 * (64 / lpr);
-    for (int i = 0; i < set.n; ++i) {
-        set.p[i].first_block = blocks;
-        blocks += (set.p[i].out + per - 1) / per;
-    }
-    switch (lpr) {
-        case 64: return launch_proj_t<BITS, 64>(set, blocks, x, S, IN, G, f16, st);
-        case 32: return launch_proj_t<BITS, 32>(set, blocks, x, S, IN, G, f16, st);
-        case 16: return launch_proj_t<BITS, 16>(set, blocks, x, S, IN, G, f16, st);
-        default: return launch_proj_t<BITS, 8>(set, blocks, x, S, IN, G, f16, st);
-    }
-}
-hipError_t launch_proj(const GdnProjSet& set, const uint16_t* x, int S, int IN, int G, int bits, int f16,
-                       hipStream_t st) {
-    switch (bits) {
-        case 2: return launch_proj_b<2>(set, x, S, IN, G, f16, st);
-        case 4: return launch_proj_b<4>(set, x, S, IN, G, f16, st);
-        case 8: return launch_proj_b<8>(set, x, S, IN, G, f16, st);
-        default: return hipErrorInvalidValue;
-    }
-}
-
 template <int CPL>
 hipError_t launch_prework_t(const GdnDev& G, const GdnBufs& B, int S, const uint16_t* origin, uint16_t* ckpt,
                             size_t state_elems, hipStream_t st) {
@@ -308,13 +216,13 @@ hipError_t launch_gdn_verify(const GdnDev& G, const GdnBufs& B, int S, const uin
     if (!gdn_geometry_ok(G)) return hipErrorInvalidValue;
     const int KW = G.hk * G.dk, VW = G.hv * G.dv, C = 2 * KW + VW;
     const size_t state_elems = static_cast<size_t>(3) * C + static_cast<size_t>(G.hv) * G.dv * G.dk;
-    GdnProjSet in{};
+    AffineRowSet in{};
     in.n = 4;
     in.p[0] = {G.w[0], G.s[0], G.b[0], B.qkv, C, C, 0};
     in.p[1] = {G.w[1], G.s[1], G.b[1], B.z, VW, VW, 0};
     in.p[2] = {G.w[2], G.s[2], G.b[2], B.bpr, G.hv, G.hv, 0};
     in.p[3] = {G.w[3], G.s[3], G.b[3], B.apr, G.hv, G.hv, 0};
-    if (const hipError_t e = launch_proj(in, x, S, G.hidden, G.group, G.bits, G.f16, st); e != hipSuccess) return e;
+    if (const hipError_t e = launch_affine_rows(in, x, S, G.hidden, G.group, G.bits, G.f16, st); e != hipSuccess) return e;
     hipError_t e = G.dk == 64    ? launch_prework_t<1>(G, B, S, origin, ckpt, state_elems, st)
                    : G.dk == 128 ? launch_prework_t<2>(G, B, S, origin, ckpt, state_elems, st)
                                  : launch_prework_t<4>(G, B, S, origin, ckpt, state_elems, st);
@@ -327,10 +235,10 @@ hipError_t launch_gdn_verify(const GdnDev& G, const GdnBufs& B, int S, const uin
         : G.dv == 128 ? launch_norm_gate_t<2>(G, B, S, st)
                       : launch_norm_gate_t<4>(G, B, S, st);
     if (e != hipSuccess) return e;
-    GdnProjSet o{};
+    AffineRowSet o{};
     o.n = 1;
     o.p[0] = {G.w[4], G.s[4], G.b[4], out, G.hidden, G.hidden, 0};
-    return launch_proj(o, B.gated, S, VW, G.group, G.bits, G.f16, st);
+    return launch_affine_rows(o, B.gated, S, VW, G.group, G.bits, G.f16, st);
 }
 
 } // namespace q38

@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <mutex>
 
 namespace q38 {
 
@@ -33,19 +34,24 @@ hipError_t launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, A
     return hipGetLastError();
 }
 
-// Dynamic-LDS limit of kernel KERN, raised once per device (thread-safe: a device bit is
-// set only after the attribute call succeeded; a race sets the same value twice).
+// Dynamic-LDS limit of kernel KERN on the current device, raised to `bytes` when a call needs
+// more than any call before it (the limit only grows, so calls with smaller needs keep
+// working; the raise is serialised, and the recorded size is updated only after the
+// attribute call succeeded).
 template <auto KERN>
 hipError_t ensure_lds(size_t bytes) {
-    static std::atomic<uint64_t> done{0};
+    static std::atomic<uint32_t> limit[64];
+    static std::mutex mu;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    const uint64_t bit = uint64_t{1} << (dev & 63);
-    if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+    std::atomic<uint32_t>& cur = limit[dev & 63];
+    if (cur.load(std::memory_order_acquire) >= bytes) return hipSuccess;
+    std::lock_guard<std::mutex> lk(mu);
+    if (cur.load(std::memory_order_acquire) >= bytes) return hipSuccess;
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(KERN), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(bytes));
-    if (e == hipSuccess) done.fetch_or(bit, std::memory_order_acq_rel);
+    if (e == hipSuccess) cur.store(static_cast<uint32_t>(bytes), std::memory_order_release);
     return e;
 }
 
@@ -152,6 +158,50 @@ hipError_t launch_gate_up_grouped(const LayerDev& L, const MoeBufs& B, int M, hi
 hipError_t launch_down_grouped(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 // GatedDeltaNet verify step (q38_gdn.hip). Projections p: 0 qkv [C, H], 1 z [HV DV, H],
 // 2 b [HV, H], 3 a [HV, H], 4 out [H, HV DV], MLX affine (bits, group, bf16 / fp16 scales).
+// Several MLX affine projections of the same rows in one launch (k_affine_rows): weight rows
+// [out, IN] (packed values, scales and biases [out][IN / group]), outputs rounded to bf16 into
+// dst rows of stride dst_stride.
+struct AffineRows {
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+    uint16_t* dst;
+    int out, dst_stride, first_block;
+};
+struct AffineRowSet {
+    AffineRows p[4];
+    int n;
+};
+hipError_t launch_affine_rows(const AffineRowSet& set, const uint16_t* x, int S, int IN, int G, int bits, int f16,
+                              hipStream_t st);
+
+// Full attention, verify (q38_attn.hip): geometry, the projections' tensors (q, k, v, o), the
+// effective q / k norm weights [D] (1 + w formed at creation for offset norms).
+struct AttnDev {
+    int hidden, hq, hkv, d, rot, bits, group, f16;
+    float eps;
+    double theta;
+    const uint32_t* w[4];
+    const uint16_t* s[4];
+    const uint16_t* b[4];
+    const uint16_t* qn;
+    const uint16_t* kn;
+};
+// Workspace of one call: projection outputs qg [S][2 HQ D], kr / vr [S][HKV D]; queries q and
+// gates gs [S][HQ][D]; scores sc [S HQ][score stride]; per-query max and sum; P.V partials
+// [tiles][S HQ][D]; gated rows [S][HQ D].
+struct AttnBufs {
+    uint16_t *qg, *kr, *vr, *q, *gs, *sc;
+    float *mx, *sm, *part;
+    uint16_t* gated;
+};
+bool attn_geometry_ok(int hidden, int hq, int hkv, int d, int rot);
+int64_t attn_score_stride(int64_t tokens);
+int64_t attn_pv_tiles(int64_t tokens);
+hipError_t launch_attn_verify(const AttnDev& A, const AttnBufs& B, int S, const uint16_t* x, uint16_t* keys,
+                              uint16_t* values, int64_t cap, int64_t T0, int64_t position, uint16_t* out,
+                              hipStream_t st);
+
 struct GdnDev {
     int hidden, hk, hv, dk, dv, bits, group, f16, gate_silu;
     float eps;

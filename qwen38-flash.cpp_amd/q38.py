@@ -60,6 +60,17 @@ class GdnWeights(C.Structure):  # include/q38.h q38_gdn_weights
                 ("conv", C.c_void_p), ("a_log", C.c_void_p), ("dt_bias", C.c_void_p), ("norm", C.c_void_p)]
 
 
+class AttnDesc(C.Structure):  # include/q38.h q38_attn_desc
+    _fields_ = [(n, C.c_int32) for n in ("hidden", "q_heads", "kv_heads", "head_dim", "rotary_dim", "bits", "group",
+                                         "scale_dtype", "norm_offset")] + [("eps", C.c_float),
+                                                                            ("rope_theta", C.c_double)]
+
+
+class AttnWeights(C.Structure):  # include/q38.h q38_attn_weights
+    _fields_ = [("weight", C.c_void_p * 4), ("scales", C.c_void_p * 4), ("biases", C.c_void_p * 4),
+                ("q_norm", C.c_void_p), ("k_norm", C.c_void_p)]
+
+
 class AffineShared(C.Structure):
     _fields_ = [("weight", C.c_void_p * 3), ("scales", C.c_void_p * 3), ("biases", C.c_void_p * 3),
                 ("bits", C.c_int32), ("group", C.c_int32), ("inter", C.c_int32), ("scale_dtype", C.c_int32)]
@@ -100,6 +111,11 @@ _sig("q38_gdn_state_bytes", C.c_size_t, P)
 _sig("q38_gdn_workspace_size", C.c_size_t, P, I32)
 _sig("q38_gdn_verify", C.c_int, P, P, I32, P, P, P, P, C.c_size_t, P)
 _sig("q38_gdn_commit", C.c_int, P, P, I32, P, P)
+_sig("q38_attn_create", C.c_int, P, C.POINTER(AttnDesc), C.POINTER(AttnWeights), C.POINTER(P))
+_sig("q38_attn_destroy", None, P)
+_sig("q38_attn_cache_bytes", C.c_size_t, P, I64)
+_sig("q38_attn_workspace_size", C.c_size_t, P, I32, I64)
+_sig("q38_attn_verify", C.c_int, P, P, I32, P, I64, I64, I64, P, P, C.c_size_t, P)
 _sig("q38_packed_vq_word_count", I64, I64, C.c_int)
 _sig("q38_unpack_vq_code", C.c_int, P, I64, I64, C.c_int, C.POINTER(U32))
 _sig("q38_supports_segmented_vq", C.c_int, C.c_int, C.c_int)

@@ -28,6 +28,11 @@ class GdnDesc(C.Structure):  # field order of oracle/q38_oracle.cpp GdnDesc
                                          "gate_silu")] + [("eps", C.c_float)]
 
 
+class AttnDesc(C.Structure):  # field order of oracle/q38_oracle.cpp AttnDesc
+    _fields_ = [(n, C.c_int32) for n in ("hidden", "q_heads", "kv_heads", "head_dim", "rotary_dim", "bits", "group",
+                                         "fmt", "norm_offset")] + [("eps", C.c_float), ("rope_theta", C.c_double)]
+
+
 class HcDesc(C.Structure):  # field order of oracle/q38_oracle.cpp HcDesc
     _fields_ = [(n, C.c_int32) for n in ("hidden", "streams", "rank", "bits", "group", "with_injection")] + [
         ("eps", C.c_float)]
@@ -101,6 +106,10 @@ class Oracle:
         sig("orc_gdn_recurrence", C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, P, P, P, P, P)
         sig("orc_gdn_verify", C.c_int, C.POINTER(GdnDesc), C.POINTER(P), C.POINTER(P), C.POINTER(P), P, P, P, P, P,
             C.c_int, P, P, P)
+        sig("orc_attn_plant_fault", None, C.c_int)
+        sig("orc_rope_table", None, C.c_double, C.c_int, I64, P, P)
+        sig("orc_attn_verify", C.c_int, C.POINTER(AttnDesc), C.POINTER(P), C.POINTER(P), C.POINTER(P), P, P, P,
+            C.c_int, P, P, I64, I64, I64, P)
         sig("orc_affine_expert", C.c_int, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.c_int, C.c_int, C.c_int,
             C.c_int, C.c_int, P, C.c_int, P)
         sig("orc_route_synth", C.c_int, C.POINTER(Desc), U64, C.c_int, P, C.c_int, P, P, P, P, C.c_int)
@@ -287,6 +296,32 @@ class Oracle:
                                      _a(layer.norm_w), _a(x), S, None if org is None else _a(org), _a(out), _a(ck))
         assert rc == 0
         return out, ck
+
+    def attn_plant_fault(self, code):
+        self.lib.orc_attn_plant_fault(code)
+
+    def rope_table(self, theta, R, pos):
+        c = np.empty(R // 2, np.float32)
+        sn = np.empty(R // 2, np.float32)
+        self.lib.orc_rope_table(theta, R, pos, _a(c), _a(sn))
+        return c, sn
+
+    def attn_verify(self, layer, x, keys, values, T0, position):
+        """SelfAttention::forward_verify (dense) on rows x [S, hidden] (bf16 bits) over a cache
+        keys / values [HKV, cap, D] (bf16 bits, T0 tokens valid) -> (out [S, hidden] bf16,
+        keys, values after the call: copies with the S new rows at T0..T0+S-1)."""
+        d = layer.odesc
+        x = np.ascontiguousarray(x, np.uint16)
+        S = x.shape[0]
+        k2, v2 = np.array(keys, np.uint16, copy=True, order="C"), np.array(values, np.uint16, copy=True, order="C")
+        cap = k2.shape[1]
+        keep = [[np.ascontiguousarray(a) for a in layer.proj[k]] for k in ("w", "s", "b")]
+        out = np.empty((S, d.hidden), np.uint16)
+        rc = self.lib.orc_attn_verify(C.byref(d), self._ptrs(keep[0], 4), self._ptrs(keep[1], 4),
+                                      self._ptrs(keep[2], 4), _a(layer.q_norm), _a(layer.k_norm), _a(x), S,
+                                      _a(k2), _a(v2), cap, T0, position, _a(out))
+        assert rc == 0
+        return out, k2, v2
 
     def affine_expert(self, sa, x):
         """The affine shared expert (sa: dict with w, s, b lists of 3 arrays, bits, group, inter,
