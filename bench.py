@@ -637,6 +637,72 @@ def main():
     log(f"GDN verify step (4 rows, 2048 / 16 x 32 heads of 128, Q8/g64): {gdn_cfg['us_per_call']:.1f} us/call, "
         f"{gdn_cfg['gbps']:.0f} GB/s of {gdn_cfg['bytes_per_call'] / 1e6:.1f} MB")
 
+    # ---------------------------------------------------------------- full-attention verify step
+    # 4 verify rows over a cached context through NLa layers in turn (H 2048, 16 query and 2 kv
+    # heads of 256, rotary 64, Q8/g64 projections), each with its own KV cache, so that the
+    # timed calls stream weights and caches from HBM.
+    def attn_leg(S=4, T0=4096, NLa=4, Hg=2048, HQ=16, HKV=2, Dg=256):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(SEED + T0)
+
+        def bf(shape, lo, hi):
+            return (torch.rand(shape, generator=gen, device=dev) * (hi - lo) + lo).to(torch.bfloat16).view(torch.int16)
+
+        QW, KW = HQ * Dg, HKV * Dg
+        handles, keep, wbytes = [], [], 0
+        cap = T0 + 64
+        for _ in range(NLa):
+            w = q38.AttnWeights()
+            for p_, (O, IN) in enumerate(((2 * QW, Hg), (KW, Hg), (KW, Hg), (Hg, QW))):
+                wt = torch.randint(-2 ** 31, 2 ** 31 - 1, (O, IN // 4), generator=gen, device=dev, dtype=torch.int32)
+                sc = bf((O, IN // 64), 0.5e-4, 1.5e-4)
+                bi = bf((O, IN // 64), -0.02, -0.01)
+                keep += [wt, sc, bi]
+                w.weight[p_], w.scales[p_], w.biases[p_] = wt.data_ptr(), sc.data_ptr(), bi.data_ptr()
+                wbytes += wt.numel() * 4 + 2 * sc.numel() * 2
+            qn, kn = bf((Dg,), 0.5, 1.5), bf((Dg,), 0.5, 1.5)
+            keep += [qn, kn]
+            w.q_norm, w.k_norm = qn.data_ptr(), kn.data_ptr()
+            dsc = q38.AttnDesc(Hg, HQ, HKV, Dg, 64, 8, 64, 0, 0, 1e-6, 1e7)
+            ha = C.c_void_p()
+            q38.check(q38.lib.q38_attn_create(ctx.h, C.byref(dsc), C.byref(w), C.byref(ha)))
+            handles.append(ha)
+        try:
+            cb = q38.lib.q38_attn_cache_bytes(handles[0], cap)
+            caches = [bf((cb // 2,), -1.0, 1.0) for _ in range(NLa)]
+            xa = bf((S, Hg), -1.0, 1.0)
+            ya = torch.empty((S, Hg), dtype=torch.int16, device=dev)
+            wsa = torch.empty(q38.lib.q38_attn_workspace_size(handles[0], S, T0 + S), dtype=torch.uint8, device=dev)
+
+            def one_pass():
+                for li, ha in enumerate(handles):
+                    q38.check(q38.lib.q38_attn_verify(ha, xa.data_ptr(), S, caches[li].data_ptr(), cap, T0, T0,
+                                                      ya.data_ptr(), wsa.data_ptr(), wsa.numel(), sp))
+            one_pass()
+            ts = []
+            for _ in range(10):
+                ev0.record(stream)
+                one_pass()
+                ev1.record(stream)
+                torch.cuda.synchronize()
+                ts.append(1e3 * ev0.elapsed_time(ev1) / NLa)
+            us = float(np.median(ts))
+            cache_read = 2 * HKV * (T0 + S) * Dg * 2
+            moved = wbytes // NLa + cache_read + 2 * S * Hg * 2
+            return {"rows": S, "cached_tokens": T0, "layers": NLa, "hidden": Hg, "q_heads": HQ, "kv_heads": HKV,
+                    "head_dim": Dg, "rotary_dim": 64, "bits": 8, "group": 64, "us_per_call": us,
+                    "bytes_per_call": moved, "gbps": moved / (us * 1e-6) / 1e9,
+                    "hbm_frac": moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                    "note": "eager launches (7 kernels per call); bytes = weights + the KV cache read + rows"}
+        finally:
+            for ha in handles:
+                q38.lib.q38_attn_destroy(ha)
+
+    attn_cfg = {f"ctx{t}": attn_leg(T0=t) for t in (4096, 32768)}
+    for k_, v_ in attn_cfg.items():
+        log(f"attention verify step (4 rows, {k_}, 2048 / 16 + 2 heads of 256, Q8/g64): {v_['us_per_call']:.1f} "
+            f"us/call, {v_['gbps']:.0f} GB/s of {v_['bytes_per_call'] / 1e6:.1f} MB")
+
     if args.copy_calibration:
         # a plain device copy of known size for the FETCH_SIZE / WRITE_SIZE calibration runs
         nb = 256 << 20
@@ -784,6 +850,49 @@ def main():
                    "note": "seeded random-init draft head: drafts are uncorrelated with the target"}
     log(f"config 2 learned drafts: draft chain {learned_cfg['draft_chain_us']:.1f} us (depth 3), round "
         f"{learned_cfg['round_ms']:.3f} ms, mean accepted {learned_cfg['mean_accepted']:.2f}")
+
+    # The same depth-3 chain on the reference head's HC streams: 5 streams of H (the 10240-wide
+    # target stream), the block as mixer read -> MoE -> write and the final mixer's read before
+    # the Q4 head (4-bit g64 mixers of rank 256, random pre-FC norm weights).
+    HCs = 5
+    gen_s = torch.Generator(device=dev)
+    gen_s.manual_seed(SEED + HCs)
+    blk = q38.Hc(ctx, q38.HcDesc(H, HCs, 256, 4, 64, 1, 1e-6), hc_tensors(gen_s, HCs, 256))
+    fin = q38.Hc(ctx, q38.HcDesc(H, HCs, 256, 4, 64, 0, 1e-6), hc_tensors(gen_s, HCs, 256))
+    n_e = (torch.randn(H, device=dev, generator=gen_s) * 0.1).to(torch.bfloat16).view(torch.int16)
+    n_h = (torch.randn(HCs * H, device=dev, generator=gen_s) * 0.1).to(torch.bfloat16).view(torch.int16)
+    mtp.set_streams(blk, fin, n_e, n_h)
+    wss = torch.empty(mtp.workspace_size(1), dtype=torch.uint8, device=dev)
+    ssb = torch.empty((1, HCs * H), dtype=torch.int16, device=dev)
+    q38.check(q38.lib.q38_hc_initialize_stream(sbuf.data_ptr(), 1, H, HCs, ssb.data_ptr(), sp))
+
+    def stream_chain(sp_):
+        q38.check(q38.lib.q38_mtp_draft_greedy(mtp.h, ssb.data_ptr(), tok_dev.data_ptr(), 1, 3, ddev.data_ptr(),
+                                               None, wss.data_ptr(), wss.numel(), sp_))
+
+    gs_ = None
+    if not args.no_graph:
+        stream_chain(sp)
+        torch.cuda.synchronize()
+        gs_ = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gs_):
+            stream_chain(torch.cuda.current_stream().cuda_stream)
+    dts = []
+    for _ in range(20):
+        ev0.record(stream)
+        if gs_ is not None:
+            gs_.replay()
+        else:
+            stream_chain(sp)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        dts.append(1e3 * ev0.elapsed_time(ev1))
+    learned_cfg["draft_chain_hc5_us"] = float(np.median(dts))
+    log(f"config 2 learned drafts on 5 HC streams: draft chain {learned_cfg['draft_chain_hc5_us']:.1f} us (depth 3)")
+    del gs_
+    mtp.clear_streams()
+    blk.close()
+    fin.close()
     mtp.close()
 
     # ---------------------------------------------------------------- CPU baseline
@@ -822,6 +931,7 @@ def main():
             "config3_prefill": prefill_cfg,
             "config4_mixed": mixed_cfg, "config1_group64": g64_cfg, "decoder_mlp_half_hc": hc_cfg,
             "gdn_verify_step": gdn_cfg,
+            "attention_verify_step": attn_cfg,
             "config2_sampled": sampled_cfg,
             "config2_learned_drafts": learned_cfg,
         },

@@ -832,6 +832,7 @@ static size_t attn_ws(const q38_attn* a, int S, int64_t tokens, AttnBufs* b, voi
     t.q = reinterpret_cast<uint16_t*>(take(S * QW * 2));
     t.gs = reinterpret_cast<uint16_t*>(take(S * QW * 2));
     t.sc = reinterpret_cast<uint16_t*>(take(NQ * static_cast<size_t>(attn_score_stride(tokens)) * 2));
+    t.stats = reinterpret_cast<float2*>(take(static_cast<size_t>(attn_score_tiles(tokens)) * NQ * 8));
     t.mx = reinterpret_cast<float*>(take(NQ * 4));
     t.sm = reinterpret_cast<float*>(take(NQ * 4));
     t.part = reinterpret_cast<float*>(take(static_cast<size_t>(attn_pv_tiles(tokens)) * NQ * d.head_dim * 4));

@@ -12,15 +12,15 @@
 //                    R dims with the bf16 cos / sin of position * theta^(-2i / R) formed in
 //                    double (:641-679), T(sigmoid(gate)), and the new keys and values written
 //                    into the cache at the row's token;
-//   k_attn_scores    per (64-token tile, kv head, chunk of 32 queries): the tile's keys staged
-//                    in LDS (rows padded by 16 bytes), the queries as float; one lane per token,
-//                    the waves splitting the queries; s = T(T(q . k) * T(1 / sqrt D)) for every
-//                    token the query sees (t <= T0 + r);
-//   k_attn_softmax   per query: the max and the float sum of exp(s - max) over its tokens;
-//   k_attn_pv        per (256-token tile, kv head, chunk of 32 queries): p = T(e / sum) into
-//                    LDS, then per dimension the tile's sum of p * v in float (token groups
-//                    added in order), one partial row per (tile, query);
-//   k_attn_combine   per query: the tiles' partials added in tile order, rounded, times the
+//   k_attn_scores    per (64-token tile, kv head): s = T(T(q . k) * T(1 / sqrt D)) for every
+//                    token a query sees (t <= T0 + r) on bf16 MFMA (exact products, float
+//                    sums), and per query the tile's max and float sum of exp(s - max);
+//   k_attn_stats     per query: the max over its tiles and the sum of the tiles' sums scaled
+//                    to it;
+//   k_attn_pv        per (256-token tile, kv head, 64 queries): p = T(exp(s - max) / sum) as
+//                    the A operand of bf16 MFMA against the tile's values (staged transposed in
+//                    LDS, 64 tokens at a time), one float partial row per (tile, query);
+//   k_attn_combine   per query: the tiles' partials added in a fixed order, rounded, times the
 //                    gate, rounded;
 //   k_affine_rows    the output projection.
 // Tiles start at multiples of their size from token 0, so a query's sums do not depend on how
@@ -33,9 +33,9 @@ namespace q38 {
 
 namespace {
 
-constexpr int kTok = 64;     // tokens per score tile
+constexpr int kTok = 64;     // tokens per score tile (and per P.V sub-tile)
 constexpr int kPvTok = 256;  // tokens per P.V tile
-constexpr int kQc = 32;      // queries per chunk
+constexpr int kPvMt = 4;     // 16-query M-tiles per P.V workgroup
 
 __device__ __forceinline__ float tbf(float v) { return bf2f(f2bf(v)); }
 __device__ __forceinline__ float sigmoid_bf(float x) { return tbf(1.0f / (1.0f + expf(-x))); }
@@ -101,83 +101,98 @@ __global__ __launch_bounds__(64) void k_attn_prework(AttnDev A, AttnBufs B, uint
     }
 }
 
-// Scores of one 64-token tile of kv head g for queries j0 .. j0 + 31 of the head's group
-// (query j: row j / G, head g G + j % G).
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f4_t mfma_bf16(uint4 a, uint4 b, f4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8_t, a), __builtin_bit_cast(bf8_t, b), c, 0,
+                                                   0, 0);
+}
+
+// Scores and tile statistics of one 64-token tile of kv head g for all S * G queries of the
+// head's group (query j: row j / G, head g G + j % G), on v_mfma_f32_16x16x32_bf16: wave w
+// takes tokens 16 w .. 16 w + 15 of the tile; per 16-query M-tile, A = the queries (lane
+// (c, q): query row c, dims 8 q .. 8 q + 7 of each 32-dim step), B = the keys (lane (c, q):
+// token c, the same dims), both read as 16-byte runs; the products are exact and the sums
+// float. The lane then holds queries 4 q .. 4 q + 3 of the M-tile for token c. Per query the
+// tile's max and the float sum of exp(s - max) over the tokens it sees go to B.stats.
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_scores(AttnDev A, AttnBufs B, int S, const uint16_t* __restrict__ keys,
                                                      int64_t cap, int64_t T0, int64_t tpad) {
-    constexpr int KS = D + 8;  // padded key row (bf16): rows start 4 banks apart
-    extern __shared__ __align__(16) char lds[];
-    uint16_t* kt = reinterpret_cast<uint16_t*>(lds);                        // [64][KS]
-    float* qs = reinterpret_cast<float*>(lds + kTok * KS * sizeof(uint16_t));  // [32][D]
-    const int tile = blockIdx.x, g = blockIdx.y;
-    const int G = A.hq / A.hkv, NQ = S * G, j0 = blockIdx.z * kQc;
-    const int nq = NQ - j0 < kQc ? NQ - j0 : kQc;
-    const int64_t t0 = static_cast<int64_t>(tile) * kTok, Ttot = T0 + S;
-    constexpr int WPR = D / 8;  // 16-byte words per key row
-    for (int w = threadIdx.x; w < kTok * WPR; w += 256) {
-        const int tt = w / WPR, c = w % WPR;
-        const int64_t t = t0 + tt < Ttot ? t0 + tt : Ttot - 1;
-        *reinterpret_cast<uint4*>(kt + tt * KS + c * 8) =
-            *reinterpret_cast<const uint4*>(keys + (static_cast<int64_t>(g) * cap + t) * D + c * 8);
-    }
-    for (int e = threadIdx.x; e < nq * D; e += 256) {
-        const int jj = e / D, i = e % D, j = j0 + jj;
-        qs[jj * D + i] = bf2f(B.q[(static_cast<size_t>(j / G) * A.hq + g * G + j % G) * D + i]);
-    }
-    __syncthreads();
-    const int tt = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    constexpr int QPW = kQc / 4;  // queries per wave: jj = wv + 4 k
-    float acc[QPW];
+    constexpr int KS = D / 32;
+    __shared__ float red_m[4][16], red_s[4][16];
+    const int tile = blockIdx.x, g = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int c = lane & 15, q = lane >> 4;
+    const int HQ = A.hq, G = HQ / A.hkv, NQ = S * G;
+    const int64_t Ttot = T0 + S, tk = static_cast<int64_t>(tile) * kTok + 16 * w + c;
+    const uint16_t* krow = keys + (static_cast<int64_t>(g) * cap + (tk < Ttot ? tk : Ttot - 1)) * D + 8 * q;
+    uint4 kb[KS];
 #pragma unroll
-    for (int k = 0; k < QPW; ++k) acc[k] = 0.0f;
-    for (int c = 0; c < D; c += 8) {
-        const uint4 kw = *reinterpret_cast<const uint4*>(kt + tt * KS + c);
-        const uint32_t u[4] = {kw.x, kw.y, kw.z, kw.w};
-        float kf[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            kf[2 * e] = __uint_as_float(u[e] << 16);
-            kf[2 * e + 1] = __uint_as_float(u[e] & 0xFFFF0000u);
-        }
-#pragma unroll
-        for (int k = 0; k < QPW; ++k) {
-            const int jj = wv + 4 * k;
-            if (jj < nq) {
-                const float4 a = *reinterpret_cast<const float4*>(qs + jj * D + c);
-                const float4 b = *reinterpret_cast<const float4*>(qs + jj * D + c + 4);
-                float s = acc[k];
-                s = fmaf(a.x, kf[0], s);
-                s = fmaf(a.y, kf[1], s);
-                s = fmaf(a.z, kf[2], s);
-                s = fmaf(a.w, kf[3], s);
-                s = fmaf(b.x, kf[4], s);
-                s = fmaf(b.y, kf[5], s);
-                s = fmaf(b.z, kf[6], s);
-                s = fmaf(b.w, kf[7], s);
-                acc[k] = s;
-            }
-        }
-    }
+    for (int ks = 0; ks < KS; ++ks) kb[ks] = *reinterpret_cast<const uint4*>(krow + 32 * ks);
     const float scale = tbf(static_cast<float>(1.0 / sqrt(static_cast<double>(D))));
-    const int64_t t = t0 + tt;
+    const size_t NQall = static_cast<size_t>(S) * HQ;
+    const int nmt = (NQ + 15) / 16;
+    for (int mt = 0; mt < nmt; ++mt) {
+        const int jr = mt * 16 + c;  // this lane's A row
+        uint4 qa[KS];
+        if (jr < NQ) {
+            const uint16_t* qrow = B.q + (static_cast<size_t>(jr / G) * HQ + g * G + jr % G) * D + 8 * q;
 #pragma unroll
-    for (int k = 0; k < QPW; ++k) {
-        const int jj = wv + 4 * k;
-        if (jj >= nq) continue;
-        const int j = j0 + jj, r = j / G;
-        if (t <= T0 + r) B.sc[(static_cast<size_t>(r) * A.hq + g * G + j % G) * tpad + t] = f2bf(tbf(acc[k]) * scale);
+            for (int ks = 0; ks < KS; ++ks) qa[ks] = *reinterpret_cast<const uint4*>(qrow + 32 * ks);
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) qa[ks] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) acc = mfma_bf16(qa[ks], kb[ks], acc);
+        float sv[4], mm[4];
+        bool ok[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = mt * 16 + 4 * q + i, r = j / G;
+            ok[i] = j < NQ && tk <= T0 + r;
+            sv[i] = ok[i] ? tbf(tbf(acc[i]) * scale) : -INFINITY;
+            if (ok[i]) B.sc[(static_cast<size_t>(r) * HQ + g * G + j % G) * tpad + tk] = f2bf(sv[i]);
+            float m = sv[i];
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+            mm[i] = m;
+        }
+        if (c == 0)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red_m[w][4 * q + i] = mm[i];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * q + i;
+            mm[i] = fmaxf(fmaxf(red_m[0][row], red_m[1][row]), fmaxf(red_m[2][row], red_m[3][row]));
+            float e = ok[i] ? expf(sv[i] - mm[i]) : 0.0f;
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) e += __shfl_xor(e, off, 64);
+            if (c == 0) red_s[w][row] = e;
+        }
+        __syncthreads();
+        if (w == 0 && c == 0)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = mt * 16 + 4 * q + i, row = 4 * q + i;
+                if (j >= NQ) continue;
+                const size_t qi = static_cast<size_t>(j / G) * HQ + g * G + j % G;
+                B.stats[static_cast<size_t>(tile) * NQall + qi] =
+                    make_float2(mm[i], (red_s[0][row] + red_s[1][row]) + (red_s[2][row] + red_s[3][row]));
+            }
+        __syncthreads();
     }
 }
 
-// Max and sum of exp(s - max) of one query's scores (row r: tokens 0 .. T0 + r).
-__global__ __launch_bounds__(256) void k_attn_softmax(AttnDev A, AttnBufs B, int64_t T0, int64_t tpad) {
+// Per query: max and sum over its tiles' statistics (m = max m_t, sum = sum s_t exp(m_t - m)).
+__global__ __launch_bounds__(256) void k_attn_stats(AttnDev A, AttnBufs B, int S, int64_t T0) {
     __shared__ float red[4];
     const int qi = blockIdx.x, r = qi / A.hq, tid = threadIdx.x;
-    const int64_t T = T0 + r + 1;
-    const uint16_t* row = B.sc + static_cast<size_t>(qi) * tpad;
+    const size_t NQall = static_cast<size_t>(S) * A.hq;
+    const int64_t nt = (T0 + r + 1 + kTok - 1) / kTok;
     float m = -INFINITY;
-    for (int64_t t = tid; t < T; t += 256) m = fmaxf(m, bf2f(row[t]));
+    for (int64_t k = tid; k < nt; k += 256) m = fmaxf(m, B.stats[static_cast<size_t>(k) * NQall + qi].x);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if ((tid & 63) == 0) red[tid >> 6] = m;
@@ -185,7 +200,10 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnDev A, AttnBufs B, int
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     float s = 0.0f;
-    for (int64_t t = tid; t < T; t += 256) s += expf(bf2f(row[t]) - m);
+    for (int64_t k = tid; k < nt; k += 256) {
+        const float2 st = B.stats[static_cast<size_t>(k) * NQall + qi];
+        s += st.y * expf(st.x - m);
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
     if ((tid & 63) == 0) red[tid >> 6] = s;
@@ -196,72 +214,143 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnDev A, AttnBufs B, int
     }
 }
 
-// Partial P.V rows of one 256-token tile of kv head g for queries j0 .. j0 + 31.
+// P.V of one 256-token tile (four 64-token sub-tiles) of kv head g for M-tiles
+// mt0 .. mt0 + kPvMt - 1 of the group's queries, on v_mfma_f32_16x16x32_bf16: the sub-tile's
+// values are staged transposed in LDS ([dim][token], rows padded by 16 bytes; the next
+// sub-tile's loads are in flight while the current one computes); A = p = T(exp(s - m) / sum)
+// of 8 tokens of one query (0 for tokens the query does not see), B = 8 tokens of one dim;
+// wave w owns dims 16 NTW w .. One partial row per (tile, query) in float.
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_pv(AttnDev A, AttnBufs B, int S, const uint16_t* __restrict__ values,
                                                  int64_t cap, int64_t T0, int64_t tpad) {
-    constexpr int TPD = 256 / D;  // token groups
-    extern __shared__ __align__(16) char lds[];
-    float* ps = reinterpret_cast<float*>(lds);           // [32][256]
-    float* red = ps + kQc * kPvTok;                      // [TPD][32][D]
-    const int tile = blockIdx.x, g = blockIdx.y;
-    const int G = A.hq / A.hkv, NQ = S * G, j0 = blockIdx.z * kQc;
-    const int nq = NQ - j0 < kQc ? NQ - j0 : kQc;
-    const int64_t t0 = static_cast<int64_t>(tile) * kPvTok, Ttot = T0 + S;
-    for (int e = threadIdx.x; e < nq * kPvTok; e += 256) {
-        const int jj = e / kPvTok, tt = e % kPvTok, j = j0 + jj, r = j / G;
-        const int64_t t = t0 + tt;
-        const size_t qi = static_cast<size_t>(r) * A.hq + g * G + j % G;
-        float p = 0.0f;
-        if (t <= T0 + r) p = tbf(expf(bf2f(B.sc[qi * tpad + t]) - B.mx[qi]) / B.sm[qi]);
-        ps[jj * kPvTok + tt] = p;
-    }
-    __syncthreads();
-    const int tg = threadIdx.x / D, d = threadIdx.x % D;
-    float acc[kQc];
+    constexpr int VS = kTok + 8;        // transposed row (bf16)
+    constexpr int NTW = D / 16 / 4;     // 16-dim N-tiles per wave
+    constexpr int CPT = D / 64;         // 8-dim chunks a thread stages per sub-tile (two tokens each)
+    __shared__ __align__(16) uint16_t vt[D * VS];
+    const int tile = blockIdx.x, g = blockIdx.y, mt0 = blockIdx.z * kPvMt;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 15, q = lane >> 4;
+    const int HQ = A.hq, G = HQ / A.hkv, NQ = S * G;
+    const int nmt = (NQ + 15) / 16 - mt0 < kPvMt ? (NQ + 15) / 16 - mt0 : kPvMt;
+    const int64_t Ttot = T0 + S, tb = static_cast<int64_t>(tile) * kPvTok;
+    const int64_t left = Ttot - tb;
+    const int nsub = static_cast<int>(left >= kPvTok ? kPvTok / kTok : (left + kTok - 1) / kTok);
+    const int tp = tid & 31, dc0 = tid >> 5;
+    uint4 va[CPT], vb[CPT];
+    auto load = [&](int64_t ts) {
+        const int64_t t = ts + 2 * tp;
 #pragma unroll
-    for (int jj = 0; jj < kQc; ++jj) acc[jj] = 0.0f;
-    for (int tt = tg; tt < kPvTok; tt += TPD) {
-        const int64_t t = t0 + tt;
-        if (t >= Ttot) break;
-        const float v = bf2f(values[(static_cast<int64_t>(g) * cap + t) * D + d]);
+        for (int k = 0; k < CPT; ++k) {
+            const int dc = dc0 + 8 * k;
+            const uint16_t* src = values + (static_cast<int64_t>(g) * cap + t) * D + 8 * dc;
+            va[k] = t < Ttot ? *reinterpret_cast<const uint4*>(src) : make_uint4(0u, 0u, 0u, 0u);
+            vb[k] = t + 1 < Ttot ? *reinterpret_cast<const uint4*>(src + D) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto store = [&]() {
 #pragma unroll
-        for (int jj = 0; jj < kQc; ++jj)
-            if (jj < nq) acc[jj] = fmaf(ps[jj * kPvTok + tt], v, acc[jj]);
-    }
-    if constexpr (TPD > 1) {
+        for (int k = 0; k < CPT; ++k) {
+            const int dc = dc0 + 8 * k;
+            const uint32_t a[4] = {va[k].x, va[k].y, va[k].z, va[k].w}, b[4] = {vb[k].x, vb[k].y, vb[k].z, vb[k].w};
 #pragma unroll
-        for (int jj = 0; jj < kQc; ++jj)
-            if (jj < nq) red[(tg * kQc + jj) * D + d] = acc[jj];
+            for (int e = 0; e < 4; ++e) {
+                const int d = 8 * dc + 2 * e;
+                *reinterpret_cast<uint32_t*>(vt + d * VS + 2 * tp) = (a[e] & 0xFFFFu) | (b[e] << 16);
+                *reinterpret_cast<uint32_t*>(vt + (d + 1) * VS + 2 * tp) = (a[e] >> 16) | (b[e] & 0xFFFF0000u);
+            }
+        }
+    };
+    f4_t acc[kPvMt][NTW];
+#pragma unroll
+    for (int mt = 0; mt < kPvMt; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    load(tb);
+    for (int s = 0; s < nsub; ++s) {
+        const int64_t ts = tb + static_cast<int64_t>(kTok) * s;
+        __syncthreads();  // the previous sub-tile's reads are done
+        store();
         __syncthreads();
-        if (tg != 0) return;
+        if (s + 1 < nsub) load(ts + kTok);
 #pragma unroll
-        for (int jj = 0; jj < kQc; ++jj) {
-            if (jj >= nq) continue;
-            float s = red[jj * D + d];
-            for (int k = 1; k < TPD; ++k) s += red[(k * kQc + jj) * D + d];
-            acc[jj] = s;
+        for (int mt = 0; mt < kPvMt; ++mt) {
+            if (mt >= nmt) break;
+            const int j = (mt0 + mt) * 16 + c;
+            uint4 pa[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+            if (j < NQ) {
+                const int r = j / G;
+                const size_t qi = static_cast<size_t>(r) * HQ + g * G + j % G;
+                const float m = B.mx[qi], sum = B.sm[qi];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const int64_t t = ts + 32 * ks + 8 * q;
+                    const uint4 sv = *reinterpret_cast<const uint4*>(B.sc + qi * tpad + t);
+                    const uint32_t u[4] = {sv.x, sv.y, sv.z, sv.w};
+                    uint32_t pk[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float s0 = __uint_as_float(u[e] << 16), s1 = __uint_as_float(u[e] & 0xFFFF0000u);
+                        const uint32_t p0 = t + 2 * e <= T0 + r ? f2bf(expf(s0 - m) / sum) : 0u;
+                        const uint32_t p1 = t + 2 * e + 1 <= T0 + r ? f2bf(expf(s1 - m) / sum) : 0u;
+                        pk[e] = p0 | (p1 << 16);
+                    }
+                    pa[ks] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                }
+            }
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) {
+                const uint16_t* col = vt + ((w * NTW + nt) * 16 + c) * VS + 8 * q;
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    acc[mt][nt] = mfma_bf16(pa[ks], *reinterpret_cast<const uint4*>(col + 32 * ks), acc[mt][nt]);
+            }
         }
     }
-    const size_t NQall = static_cast<size_t>(S) * A.hq;
-    for (int jj = 0; jj < nq; ++jj) {
-        const int j = j0 + jj, r = j / G;
-        const size_t qi = static_cast<size_t>(r) * A.hq + g * G + j % G;
-        B.part[(static_cast<size_t>(tile) * NQall + qi) * D + d] = acc[jj];
+    const size_t NQall = static_cast<size_t>(S) * HQ;
+#pragma unroll
+    for (int mt = 0; mt < kPvMt; ++mt) {
+        if (mt >= nmt) break;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = (mt0 + mt) * 16 + 4 * q + i;
+            if (j >= NQ) continue;
+            const size_t qi = static_cast<size_t>(j / G) * HQ + g * G + j % G;
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt)
+                B.part[(static_cast<size_t>(tile) * NQall + qi) * D + (w * NTW + nt) * 16 + c] = acc[mt][nt][i];
+        }
     }
 }
 
-// attended = T(sum of the tiles' partials, tile order), gated = T(attended * gate).
-__global__ __launch_bounds__(256) void k_attn_combine(AttnDev A, AttnBufs B, int S, int64_t T0) {
-    const int qi = blockIdx.x, d = threadIdx.x, D = A.d;
-    if (d >= D) return;
+// attended = T(sum of the tiles' partials), gated = T(attended * gate): TG groups of D
+// threads, group k adds tiles k, k + TG, .. (8 loads in flight), the groups added in order.
+template <int D>
+__global__ __launch_bounds__(1024) void k_attn_combine(AttnDev A, AttnBufs B, int S, int64_t T0) {
+    constexpr int TG = 1024 / D;
+    __shared__ float red[1024];
+    const int qi = blockIdx.x, d = threadIdx.x % D, k = threadIdx.x / D;
     const int r = qi / A.hq, h = qi % A.hq;
     const int64_t ntile = (T0 + r + 1 + kPvTok - 1) / kPvTok;
     const size_t NQall = static_cast<size_t>(S) * A.hq;
+    const float* src = B.part + static_cast<size_t>(qi) * D + d;
+    const size_t step = NQall * D;
     float a = 0.0f;
-    for (int64_t tile = 0; tile < ntile; ++tile) a += B.part[(static_cast<size_t>(tile) * NQall + qi) * D + d];
+    int64_t t = k;
+    for (; t + 7 * TG < ntile; t += 8 * TG) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[static_cast<size_t>(t + u * TG) * step];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a += v[u];
+    }
+    for (; t < ntile; t += TG) a += src[static_cast<size_t>(t) * step];
+    red[threadIdx.x] = a;
+    __syncthreads();
+    if (k != 0) return;
+    float s = red[d];
+#pragma unroll
+    for (int kk = 1; kk < TG; ++kk) s += red[kk * D + d];
     B.gated[static_cast<size_t>(r) * A.hq * D + static_cast<size_t>(h) * D + d] =
-        f2bf(tbf(a) * bf2f(B.gs[static_cast<size_t>(qi) * D + d]));
+        f2bf(tbf(s) * bf2f(B.gs[static_cast<size_t>(qi) * D + d]));
 }
 
 template <int D>
@@ -269,23 +358,19 @@ hipError_t launch_attn_core(const AttnDev& A, const AttnBufs& B, int S, uint16_t
                             int64_t T0, int64_t position, int64_t tpad, hipStream_t st) {
     const int HQ = A.hq, HKV = A.hkv, G = HQ / HKV;
     const int64_t Ttot = T0 + S;
-    const unsigned qchunks = static_cast<unsigned>((S * G + kQc - 1) / kQc);
     hipError_t e = launch(k_attn_prework<D / 64>, dim3(HQ + 2 * HKV, S), dim3(64), 0, st, A, B, keys, values, cap, T0,
                           position);
     if (e != hipSuccess) return e;
-    const size_t lds_s = static_cast<size_t>(kTok) * (D + 8) * 2 + static_cast<size_t>(kQc) * D * 4;
-    if ((e = ensure_lds<k_attn_scores<D>>(lds_s)) != hipSuccess) return e;
-    e = launch(k_attn_scores<D>, dim3(static_cast<unsigned>((Ttot + kTok - 1) / kTok), HKV, qchunks), dim3(256), lds_s,
-               st, A, B, S, static_cast<const uint16_t*>(keys), cap, T0, tpad);
+    e = launch(k_attn_scores<D>, dim3(static_cast<unsigned>((Ttot + kTok - 1) / kTok), HKV), dim3(256), 0, st, A, B, S,
+               static_cast<const uint16_t*>(keys), cap, T0, tpad);
     if (e != hipSuccess) return e;
-    e = launch(k_attn_softmax, dim3(S * HQ), dim3(256), 0, st, A, B, T0, tpad);
+    e = launch(k_attn_stats, dim3(S * HQ), dim3(256), 0, st, A, B, S, T0);
     if (e != hipSuccess) return e;
-    const size_t lds_p = static_cast<size_t>(kQc) * kPvTok * 4 + static_cast<size_t>(256) * kQc * 4;
-    if ((e = ensure_lds<k_attn_pv<D>>(lds_p)) != hipSuccess) return e;
-    e = launch(k_attn_pv<D>, dim3(static_cast<unsigned>((Ttot + kPvTok - 1) / kPvTok), HKV, qchunks), dim3(256), lds_p,
+    const unsigned mchunks = static_cast<unsigned>(((S * G + 15) / 16 + kPvMt - 1) / kPvMt);
+    e = launch(k_attn_pv<D>, dim3(static_cast<unsigned>((Ttot + kPvTok - 1) / kPvTok), HKV, mchunks), dim3(256), 0,
                st, A, B, S, static_cast<const uint16_t*>(values), cap, T0, tpad);
     if (e != hipSuccess) return e;
-    return launch(k_attn_combine, dim3(S * HQ), dim3(256), 0, st, A, B, S, T0);
+    return launch(k_attn_combine<D>, dim3(S * HQ), dim3(1024), 0, st, A, B, S, T0);
 }
 
 } // namespace
@@ -297,6 +382,7 @@ bool attn_geometry_ok(int hidden, int hq, int hkv, int d, int rot) {
 
 int64_t attn_score_stride(int64_t tokens) { return (tokens + kTok - 1) / kTok * kTok; }
 int64_t attn_pv_tiles(int64_t tokens) { return (tokens + kPvTok - 1) / kPvTok; }
+int64_t attn_score_tiles(int64_t tokens) { return (tokens + kTok - 1) / kTok; }
 
 hipError_t launch_attn_verify(const AttnDev& A, const AttnBufs& B, int S, const uint16_t* x, uint16_t* keys,
                               uint16_t* values, int64_t cap, int64_t T0, int64_t position, uint16_t* out,

@@ -188,16 +188,18 @@ struct AttnDev {
     const uint16_t* kn;
 };
 // Workspace of one call: projection outputs qg [S][2 HQ D], kr / vr [S][HKV D]; queries q and
-// gates gs [S][HQ][D]; scores sc [S HQ][score stride]; per-query max and sum; P.V partials
-// [tiles][S HQ][D]; gated rows [S][HQ D].
+// gates gs [S][HQ][D]; scores sc [S HQ][score stride]; per (score tile, query) max and sum
+// stats; per-query max and sum; P.V partials [tiles][S HQ][D]; gated rows [S][HQ D].
 struct AttnBufs {
     uint16_t *qg, *kr, *vr, *q, *gs, *sc;
+    float2* stats;
     float *mx, *sm, *part;
     uint16_t* gated;
 };
 bool attn_geometry_ok(int hidden, int hq, int hkv, int d, int rot);
 int64_t attn_score_stride(int64_t tokens);
 int64_t attn_pv_tiles(int64_t tokens);
+int64_t attn_score_tiles(int64_t tokens);
 hipError_t launch_attn_verify(const AttnDev& A, const AttnBufs& B, int S, const uint16_t* x, uint16_t* keys,
                               uint16_t* values, int64_t cap, int64_t T0, int64_t position, uint16_t* out,
                               hipStream_t st);
