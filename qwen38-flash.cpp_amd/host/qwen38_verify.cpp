@@ -352,6 +352,73 @@ DeviceTensor GatedDeltaNet::forward_verify(const DeviceTensor& input, const Gate
     return out;
 }
 
+// ------------------------------------------------------------------ SelfAttention
+SelfAttention::SelfAttention(const Context& ctx, const q38_attn_weights& tensors, std::size_t hidden_size,
+                             std::size_t attention_heads, std::size_t key_value_heads, std::size_t head_dimension,
+                             std::size_t rotary_dimension, int quantization_bits, int quantization_group_size,
+                             bool fp16_scales, bool norm_has_offset, float rms_norm_epsilon, double rope_theta)
+    : ctx_(&ctx), hidden_(hidden_size) {
+    const q38_attn_desc d{static_cast<int32_t>(hidden_size), static_cast<int32_t>(attention_heads),
+                          static_cast<int32_t>(key_value_heads), static_cast<int32_t>(head_dimension),
+                          static_cast<int32_t>(rotary_dimension), quantization_bits, quantization_group_size,
+                          fp16_scales ? 1 : 0, norm_has_offset ? 1 : 0, rms_norm_epsilon, rope_theta};
+    check(q38_attn_create(ctx.handle(), &d, &tensors, &attn_), "SelfAttention");
+}
+SelfAttention::~SelfAttention() { q38_attn_destroy(attn_); }
+SelfAttention::SelfAttention(SelfAttention&& o) noexcept
+    : ctx_(o.ctx_), attn_(o.attn_), hidden_(o.hidden_), workspace_(std::move(o.workspace_)) {
+    o.attn_ = nullptr;
+}
+SelfAttention& SelfAttention::operator=(SelfAttention&& o) noexcept {
+    if (this != &o) {
+        q38_attn_destroy(attn_);
+        ctx_ = o.ctx_;
+        attn_ = o.attn_;
+        hidden_ = o.hidden_;
+        workspace_ = std::move(o.workspace_);
+        o.attn_ = nullptr;
+    }
+    return *this;
+}
+
+SelfAttentionState SelfAttention::make_state(std::size_t capacity, std::size_t position_base) const {
+    const std::size_t bytes = q38_attn_cache_bytes(attn_, static_cast<int64_t>(capacity));
+    if (bytes == 0) throw std::runtime_error("attention cache capacity must be positive");
+    SelfAttentionState s;
+    s.cache = DeviceTensor({bytes / 2}, DType::bf16);
+    s.capacity = capacity;
+    s.position_base = position_base;
+    return s;
+}
+
+DeviceTensor SelfAttention::forward_verify(const DeviceTensor& input, const SelfAttentionState& origin,
+                                           std::vector<SelfAttentionState>& checkpoints) const {
+    const auto& s = input.shape();
+    if (s.size() != 3 || s[0] != 1 || s[1] < 1 || s[1] > 64 || s[2] != hidden_ || input.dtype() != DType::bf16)
+        throw std::runtime_error("attention batch requires shape [1,S,hidden], S=1..64");
+    if (origin.cache.empty()) throw std::runtime_error("attention state has no cache");
+    const std::size_t rows = s[1], tokens = origin.token_count + rows;
+    DeviceTensor out({1, rows, hidden_}, DType::bf16);
+    std::lock_guard<std::mutex> lk(g_ws_mutex);
+    const std::size_t need = q38_attn_workspace_size(attn_, static_cast<int32_t>(rows), static_cast<int64_t>(tokens));
+    if (workspace_.nbytes() < need) workspace_ = DeviceTensor({(need + 3) / 4}, DType::u32);
+    check(q38_attn_verify(attn_, static_cast<const uint16_t*>(input.data()), static_cast<int32_t>(rows),
+                          origin.cache.data(), static_cast<int64_t>(origin.capacity),
+                          static_cast<int64_t>(origin.token_count),
+                          static_cast<int64_t>(origin.position_base + origin.token_count),
+                          static_cast<uint16_t*>(out.data()), workspace_.data(), workspace_.nbytes(), ctx_->stream()),
+          "SelfAttention::forward_verify");
+    checkpoints.clear();
+    checkpoints.resize(rows);
+    for (std::size_t r = 0; r < rows; ++r) {
+        checkpoints[r].cache = origin.cache.share();
+        checkpoints[r].capacity = origin.capacity;
+        checkpoints[r].token_count = origin.token_count + r + 1;
+        checkpoints[r].position_base = origin.position_base;
+    }
+    return out;
+}
+
 DeviceTensor HyperConnection::initialize_stream(const Context& ctx, const DeviceTensor& embedding,
                                                 std::size_t stream_count) {
     const auto& s = embedding.shape();

@@ -263,6 +263,48 @@ private:
     mutable DeviceTensor workspace_;
 };
 
+// ------------------------------------------------------------------ SelfAttention (verify)
+// SelfAttentionState (include/qwen38/self_attention.hpp:12-30) on the dense path: a KV cache of
+// `capacity` tokens (keys [HKV][capacity][D] bf16, then values) holding token_count tokens,
+// the first at position_base. The checkpoints of a verify call share the cache and differ in
+// token_count, so committing a row is adopting its checkpoint and rolling back is keeping the
+// origin.
+struct SelfAttentionState {
+    DeviceTensor cache;
+    std::size_t capacity{0};
+    std::size_t token_count{0};
+    std::size_t position_base{0};
+};
+
+// SelfAttention (include/qwen38/self_attention.hpp:32-128) on the verify path: the reference
+// checkpoint's tensors (q38_attn_weights) with the manifest's geometry.
+class SelfAttention final {
+public:
+    SelfAttention(const Context& ctx, const q38_attn_weights& tensors, std::size_t hidden_size,
+                  std::size_t attention_heads, std::size_t key_value_heads, std::size_t head_dimension,
+                  std::size_t rotary_dimension, int quantization_bits, int quantization_group_size, bool fp16_scales,
+                  bool norm_has_offset, float rms_norm_epsilon, double rope_theta);
+    ~SelfAttention();
+    SelfAttention(SelfAttention&&) noexcept;
+    SelfAttention& operator=(SelfAttention&&) noexcept;
+    SelfAttention(const SelfAttention&) = delete;
+    SelfAttention& operator=(const SelfAttention&) = delete;
+
+    // An empty state with a cache of `capacity` tokens.
+    [[nodiscard]] SelfAttentionState make_state(std::size_t capacity, std::size_t position_base = 0) const;
+    // forward_verify (src/self_attention.cpp:1450-1720): input [1, S, hidden] bf16, S = 1..64;
+    // appends the rows to origin's cache (shared with the returned checkpoints).
+    [[nodiscard]] DeviceTensor forward_verify(const DeviceTensor& input, const SelfAttentionState& origin,
+                                              std::vector<SelfAttentionState>& checkpoints) const;
+    [[nodiscard]] q38_attn* handle() const noexcept { return attn_; }
+
+private:
+    const Context* ctx_ = nullptr;
+    q38_attn* attn_ = nullptr;
+    std::size_t hidden_ = 0;
+    mutable DeviceTensor workspace_;
+};
+
 // ------------------------------------------------------------------ verify model
 struct GreedyStep {
     std::uint32_t token{0};

@@ -386,6 +386,103 @@ static void gated_delta_net_tests(const qwen38::Context& ctx) {
     std::printf("gated delta net: ok\n");
 }
 
+// SelfAttention mirror: forward_verify equals the C ABI call bit for bit (outputs and cache),
+// the checkpoints share the cache with token counts origin + r + 1, S rows equal S one-row
+// calls chained through the checkpoints, and a full cache throws std::out_of_range.
+static void self_attention_tests(const qwen38::Context& ctx) {
+    const std::size_t H = 512, HQ = 4, HKV = 2, D = 128, R = 32, G = 64, QW = HQ * D, KW = HKV * D, S = 4, CAP = 40;
+    std::uint64_t st = 0x6A09E667F3BCC909ull;
+    auto next = [&] { st = st * 6364136223846793005ull + 1442695040888963407ull; return static_cast<std::uint32_t>(st >> 32); };
+    auto bf16 = [](float f) { std::uint32_t u; std::memcpy(&u, &f, 4); return static_cast<std::uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16); };
+    auto unit = [&] { return (static_cast<float>(next() >> 8) / 16777216.0f) - 0.5f; };
+    std::vector<qwen38::DeviceTensor> keep;
+    keep.reserve(16);
+    auto u32t = [&](std::size_t n) {
+        std::vector<std::uint32_t> h(n);
+        for (auto& v : h) v = next();
+        keep.emplace_back(std::vector<std::size_t>{n}, qwen38::DType::u32);
+        keep.back().upload(h.data(), n * 4);
+        return static_cast<const std::uint32_t*>(keep.back().data());
+    };
+    auto bft = [&](std::size_t n, float scale, float offset) {
+        std::vector<std::uint16_t> h(n);
+        for (auto& v : h) v = bf16(offset + scale * unit());
+        keep.emplace_back(std::vector<std::size_t>{n}, qwen38::DType::bf16);
+        keep.back().upload(h.data(), n * 2);
+        return static_cast<const std::uint16_t*>(keep.back().data());
+    };
+    const std::size_t outs[4] = {2 * QW, KW, KW, H}, ins[4] = {H, H, H, QW};
+    q38_attn_weights w{};
+    for (int p = 0; p < 4; ++p) {  // 8-bit, centred: weight = q * s + b with b ~ -127.5 s
+        w.weight[p] = u32t(outs[p] * ins[p] / 4);
+        w.scales[p] = bft(outs[p] * ins[p] / G, 0.0001f, 0.00015f);
+        w.biases[p] = bft(outs[p] * ins[p] / G, 0.002f, -0.019f);
+    }
+    w.q_norm = bft(D, 0.5f, 1.0f);
+    w.k_norm = bft(D, 0.5f, 1.0f);
+    qwen38::SelfAttention attn(ctx, w, H, HQ, HKV, D, R, 8, static_cast<int>(G), false, false, 1e-6f, 1e6);
+    // an origin holding 20 tokens (random cache contents), at position 100
+    qwen38::SelfAttentionState origin = attn.make_state(CAP, 100);
+    {
+        std::vector<std::uint16_t> h(origin.cache.numel());
+        for (auto& v : h) v = bf16(unit());
+        origin.cache.upload(h.data(), h.size() * 2);
+        origin.token_count = 20;
+    }
+    auto copy_state = [&](const qwen38::SelfAttentionState& a) {
+        qwen38::SelfAttentionState b = attn.make_state(a.capacity, a.position_base);
+        CHECK(hipMemcpy(b.cache.data(), a.cache.data(), a.cache.nbytes(), hipMemcpyDeviceToDevice) == hipSuccess);
+        b.token_count = a.token_count;
+        return b;
+    };
+    const qwen38::SelfAttentionState base = copy_state(origin);
+    auto x = bft(S * H, 2.0f, 0.0f);
+    qwen38::DeviceTensor x3({1, S, H}, qwen38::DType::bf16);
+    CHECK(hipMemcpy(x3.data(), x, S * H * 2, hipMemcpyDeviceToDevice) == hipSuccess);
+    std::vector<qwen38::SelfAttentionState> ck;
+    const qwen38::DeviceTensor out = attn.forward_verify(x3, origin, ck);
+    ctx.synchronize();
+    CHECK(ck.size() == S);
+    for (std::size_t r = 0; r < S; ++r)
+        CHECK(ck[r].token_count == 21 + r && ck[r].cache.data() == origin.cache.data() && ck[r].position_base == 100);
+    {   // the C ABI on a copy of the origin
+        qwen38::SelfAttentionState o2 = copy_state(base);
+        qwen38::DeviceTensor out2({S, H}, qwen38::DType::bf16);
+        qwen38::DeviceTensor ws({q38_attn_workspace_size(attn.handle(), S, CAP)}, qwen38::DType::u32);
+        CHECK(q38_attn_verify(attn.handle(), static_cast<const std::uint16_t*>(x3.data()), S, o2.cache.data(), CAP, 20,
+                              120, static_cast<std::uint16_t*>(out2.data()), ws.data(), ws.nbytes(), ctx.stream()) == Q38_OK);
+        ctx.synchronize();
+        CHECK(out.to_host<std::uint16_t>() == out2.to_host<std::uint16_t>());
+        CHECK(origin.cache.to_host<std::uint16_t>() == o2.cache.to_host<std::uint16_t>());
+    }
+    {   // row by row through the checkpoints
+        qwen38::SelfAttentionState s = copy_state(base);
+        const auto want = out.to_host<std::uint16_t>();
+        for (std::size_t r = 0; r < S; ++r) {
+            qwen38::DeviceTensor xr({1, 1, H}, qwen38::DType::bf16);
+            CHECK(hipMemcpy(xr.data(), static_cast<const char*>(x3.data()) + r * H * 2, H * 2,
+                            hipMemcpyDeviceToDevice) == hipSuccess);
+            std::vector<qwen38::SelfAttentionState> c1;
+            const qwen38::DeviceTensor o1 = attn.forward_verify(xr, s, c1);
+            ctx.synchronize();
+            const auto got = o1.to_host<std::uint16_t>();
+            CHECK(std::equal(got.begin(), got.end(), want.begin() + static_cast<std::ptrdiff_t>(r * H)));
+            s = std::move(c1[0]);
+        }
+        CHECK(s.token_count == 24 && s.cache.to_host<std::uint16_t>() == origin.cache.to_host<std::uint16_t>());
+    }
+    // a full cache
+    qwen38::SelfAttentionState full = copy_state(base);
+    full.token_count = CAP - 2;
+    CHECK(throws<std::out_of_range>([&] { (void)attn.forward_verify(x3, full, ck); }));
+    qwen38::DeviceTensor bad({1, 65, H}, qwen38::DType::bf16);
+    CHECK(throws<std::runtime_error>([&] { (void)attn.forward_verify(bad, origin, ck); }));
+    CHECK(throws<std::runtime_error>([&] {
+        qwen38::SelfAttention a3(ctx, w, H, 3, HKV, D, R, 8, static_cast<int>(G), false, false, 1e-6f, 1e6);
+    }));
+    std::printf("self attention: ok\n");
+}
+
 // The draft head on HC streams (5 streams of the model's hidden size): forward_decode equals
 // the C ABI step bit for bit, the greedy chain equals a replay of single steps, and a
 // single-stream row is refused.
@@ -765,6 +862,7 @@ static void gpu_tests() {
     hyper_connection_tests(ctx);
     gated_delta_net_tests(ctx);
     mtp_stream_tests(ctx, model);
+    self_attention_tests(ctx);
 }
 
 int main(int argc, char** argv) {

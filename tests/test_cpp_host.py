@@ -4,7 +4,8 @@ types on the CPU, the device section (SparseMoe vs the C ABI, verify + commit li
 a greedy round, and the engine-side round driver with 3 requests sharing each batched
 verification, every batch recomputed row by row in the same kernel family; the MTP draft head,
 learned-draft rounds and the scheduler drafting with the head; the HyperConnection mixer,
-the GatedDeltaNet verify step and the draft head on HC streams against the C ABI) on the GPU."""
+the GatedDeltaNet and full-attention verify steps and the draft head on HC streams against
+the C ABI) on the GPU."""
 import os
 import subprocess
 
@@ -34,3 +35,4 @@ def test_gpu_section():
     assert "hyper connection: ok" in out, out
     assert "gated delta net: ok" in out, out
     assert "mtp streams: ok" in out, out
+    assert "self attention: ok" in out, out
