@@ -108,16 +108,16 @@ __device__ __forceinline__ f4_t mfma_bf16(uint4 a, uint4 b, f4_t c) {
                                                    0, 0);
 }
 
-// Scores and tile statistics of one 64-token tile of kv head g for all S * G queries of the
-// head's group (query j: row j / G, head g G + j % G), on v_mfma_f32_16x16x32_bf16: wave w
-// takes tokens 16 w .. 16 w + 15 of the tile; per 16-query M-tile, A = the queries (lane
+// Scores and tile statistics of one 64-token tile of kv head g for mt_per_wg 16-query M-tiles
+// (from blockIdx.z * mt_per_wg) of the head's group (query j: row j / G, head g G + j % G), on
+// v_mfma_f32_16x16x32_bf16: wave w takes tokens 16 w .. 16 w + 15 of the tile; A = the queries (lane
 // (c, q): query row c, dims 8 q .. 8 q + 7 of each 32-dim step), B = the keys (lane (c, q):
 // token c, the same dims), both read as 16-byte runs; the products are exact and the sums
 // float. The lane then holds queries 4 q .. 4 q + 3 of the M-tile for token c. Per query the
 // tile's max and the float sum of exp(s - max) over the tokens it sees go to B.stats.
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_scores(AttnDev A, AttnBufs B, int S, const uint16_t* __restrict__ keys,
-                                                     int64_t cap, int64_t T0, int64_t tpad) {
+                                                     int64_t cap, int64_t T0, int64_t tpad, int mt_per_wg) {
     constexpr int KS = D / 32;
     __shared__ float red_m[4][16], red_s[4][16];
     const int tile = blockIdx.x, g = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -130,8 +130,8 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnDev A, AttnBufs B, int 
     for (int ks = 0; ks < KS; ++ks) kb[ks] = *reinterpret_cast<const uint4*>(krow + 32 * ks);
     const float scale = tbf(static_cast<float>(1.0 / sqrt(static_cast<double>(D))));
     const size_t NQall = static_cast<size_t>(S) * HQ;
-    const int nmt = (NQ + 15) / 16;
-    for (int mt = 0; mt < nmt; ++mt) {
+    const int mt_lo = blockIdx.z * mt_per_wg, mt_hi = min(mt_lo + mt_per_wg, (NQ + 15) / 16);
+    for (int mt = mt_lo; mt < mt_hi; ++mt) {
         const int jr = mt * 16 + c;  // this lane's A row
         uint4 qa[KS];
         if (jr < NQ) {
@@ -214,34 +214,36 @@ __global__ __launch_bounds__(256) void k_attn_stats(AttnDev A, AttnBufs B, int S
     }
 }
 
-// P.V of one 256-token tile (four 64-token sub-tiles) of kv head g for M-tiles
-// mt0 .. mt0 + kPvMt - 1 of the group's queries, on v_mfma_f32_16x16x32_bf16: the sub-tile's
-// values are staged transposed in LDS ([dim][token], rows padded by 16 bytes; the next
-// sub-tile's loads are in flight while the current one computes); A = p = T(exp(s - m) / sum)
-// of 8 tokens of one query (0 for tokens the query does not see), B = 8 tokens of one dim;
-// wave w owns dims 16 NTW w .. One partial row per (tile, query) in float.
-template <int D>
+// P.V of one 256-token tile (four 64-token sub-tiles) of kv head g for a DW-dim slice and
+// M-tiles mt0 .. mt0 + kPvMt - 1 of the group's queries, on v_mfma_f32_16x16x32_bf16: the
+// sub-tile's values of the slice are staged transposed in LDS ([dim][token], rows padded by 16
+// bytes; the next sub-tile's loads are in flight while the current one computes); A = p =
+// T(exp(s - m) / sum) of 8 tokens of one query (0 for tokens the query does not see), B = 8
+// tokens of one dim; wave w owns dims 16 NTW w .. 16 NTW (w + 1) - 1 of the slice. One float
+// partial per (tile, query, dim).
+template <int D, int DW>
 __global__ __launch_bounds__(256) void k_attn_pv(AttnDev A, AttnBufs B, int S, const uint16_t* __restrict__ values,
                                                  int64_t cap, int64_t T0, int64_t tpad) {
     constexpr int VS = kTok + 8;        // transposed row (bf16)
-    constexpr int NTW = D / 16 / 4;     // 16-dim N-tiles per wave
-    constexpr int CPT = D / 64;         // 8-dim chunks a thread stages per sub-tile (two tokens each)
-    __shared__ __align__(16) uint16_t vt[D * VS];
-    const int tile = blockIdx.x, g = blockIdx.y, mt0 = blockIdx.z * kPvMt;
+    constexpr int NSL = D / DW;         // dim slices (DW dims per workgroup)
+    constexpr int NTW = DW / 64;        // 16-dim N-tiles per wave
+    constexpr int CPT = DW / 64;        // 8-dim chunks a thread stages per sub-tile (two tokens each)
+    __shared__ __align__(16) uint16_t vt[DW * VS];
+    const int tile = blockIdx.x, g = blockIdx.y, mt0 = (blockIdx.z / NSL) * kPvMt, d0 = (blockIdx.z % NSL) * DW;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 15, q = lane >> 4;
     const int HQ = A.hq, G = HQ / A.hkv, NQ = S * G;
     const int nmt = (NQ + 15) / 16 - mt0 < kPvMt ? (NQ + 15) / 16 - mt0 : kPvMt;
     const int64_t Ttot = T0 + S, tb = static_cast<int64_t>(tile) * kPvTok;
     const int64_t left = Ttot - tb;
     const int nsub = static_cast<int>(left >= kPvTok ? kPvTok / kTok : (left + kTok - 1) / kTok);
+    // staging: thread (token pair tp, 8-dim chunks dc0 + 8 k) of the slice
     const int tp = tid & 31, dc0 = tid >> 5;
     uint4 va[CPT], vb[CPT];
     auto load = [&](int64_t ts) {
         const int64_t t = ts + 2 * tp;
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
-            const int dc = dc0 + 8 * k;
-            const uint16_t* src = values + (static_cast<int64_t>(g) * cap + t) * D + 8 * dc;
+            const uint16_t* src = values + (static_cast<int64_t>(g) * cap + t) * D + d0 + 8 * (dc0 + 8 * k);
             va[k] = t < Ttot ? *reinterpret_cast<const uint4*>(src) : make_uint4(0u, 0u, 0u, 0u);
             vb[k] = t + 1 < Ttot ? *reinterpret_cast<const uint4*>(src + D) : make_uint4(0u, 0u, 0u, 0u);
         }
@@ -249,11 +251,10 @@ __global__ __launch_bounds__(256) void k_attn_pv(AttnDev A, AttnBufs B, int S, c
     auto store = [&]() {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
-            const int dc = dc0 + 8 * k;
             const uint32_t a[4] = {va[k].x, va[k].y, va[k].z, va[k].w}, b[4] = {vb[k].x, vb[k].y, vb[k].z, vb[k].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int d = 8 * dc + 2 * e;
+                const int d = 8 * (dc0 + 8 * k) + 2 * e;
                 *reinterpret_cast<uint32_t*>(vt + d * VS + 2 * tp) = (a[e] & 0xFFFFu) | (b[e] << 16);
                 *reinterpret_cast<uint32_t*>(vt + (d + 1) * VS + 2 * tp) = (a[e] >> 16) | (b[e] & 0xFFFF0000u);
             }
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(AttnDev A, AttnBufs B, int S, c
             const size_t qi = static_cast<size_t>(j / G) * HQ + g * G + j % G;
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt)
-                B.part[(static_cast<size_t>(tile) * NQall + qi) * D + (w * NTW + nt) * 16 + c] = acc[mt][nt][i];
+                B.part[(static_cast<size_t>(tile) * NQall + qi) * D + d0 + (w * NTW + nt) * 16 + c] = acc[mt][nt][i];
         }
     }
 }
@@ -361,14 +362,24 @@ hipError_t launch_attn_core(const AttnDev& A, const AttnBufs& B, int S, uint16_t
     hipError_t e = launch(k_attn_prework<D / 64>, dim3(HQ + 2 * HKV, S), dim3(64), 0, st, A, B, keys, values, cap, T0,
                           position);
     if (e != hipSuccess) return e;
-    e = launch(k_attn_scores<D>, dim3(static_cast<unsigned>((Ttot + kTok - 1) / kTok), HKV), dim3(256), 0, st, A, B, S,
-               static_cast<const uint16_t*>(keys), cap, T0, tpad);
+    // short contexts: one M-tile per workgroup for parallelism; long ones: the workgroup takes
+    // every M-tile of its tile (the keys are read once)
+    const int nmt = (S * G + 15) / 16;
+    const int64_t ntile = (Ttot + kTok - 1) / kTok;
+    const int mt_per_wg = ntile * HKV < 1024 ? 1 : nmt;
+    e = launch(k_attn_scores<D>, dim3(static_cast<unsigned>(ntile), HKV, (nmt + mt_per_wg - 1) / mt_per_wg), dim3(256),
+               0, st, A, B, S, static_cast<const uint16_t*>(keys), cap, T0, tpad, mt_per_wg);
     if (e != hipSuccess) return e;
     e = launch(k_attn_stats, dim3(S * HQ), dim3(256), 0, st, A, B, S, T0);
     if (e != hipSuccess) return e;
-    const unsigned mchunks = static_cast<unsigned>(((S * G + 15) / 16 + kPvMt - 1) / kPvMt);
-    e = launch(k_attn_pv<D>, dim3(static_cast<unsigned>((Ttot + kPvTok - 1) / kPvTok), HKV, mchunks), dim3(256), 0,
-               st, A, B, S, static_cast<const uint16_t*>(values), cap, T0, tpad);
+    const unsigned mchunks = static_cast<unsigned>((nmt + kPvMt - 1) / kPvMt);
+    const unsigned npv = static_cast<unsigned>((Ttot + kPvTok - 1) / kPvTok);
+    if (npv * HKV * mchunks < 128)  // few tiles: 64-dim slices per workgroup for parallelism
+        e = launch(k_attn_pv<D, 64>, dim3(npv, HKV, mchunks * (D / 64)), dim3(256), 0, st, A, B, S,
+                   static_cast<const uint16_t*>(values), cap, T0, tpad);
+    else
+        e = launch(k_attn_pv<D, D>, dim3(npv, HKV, mchunks), dim3(256), 0, st, A, B, S,
+                   static_cast<const uint16_t*>(values), cap, T0, tpad);
     if (e != hipSuccess) return e;
     return launch(k_attn_combine<D>, dim3(S * HQ), dim3(1024), 0, st, A, B, S, T0);
 }
