@@ -2,7 +2,8 @@
 SelfAttention::forward_verify, src/self_attention.cpp:1450-1720) against the oracle on the
 same weights, rows and cache:
 - outputs within the MoE tolerance (rel L2 <= 1e-2, max-abs <= 2e-2);
-- the new keys and values in the cache within one bf16 step on almost every element;
+- the new keys and values in the cache within two bf16 steps of the larger of the element and
+  its head vector's RMS, and within one step on almost every element;
 - the rest of the cache untouched, bit for bit; unused cache slots hold 65536.0 and are never
   read (a read would show in the outputs);
 - S rows in one call equal S one-row calls through the cache, bit for bit (the checkpoint of
@@ -65,9 +66,16 @@ class DevAttn:
 
 
 def check_cache(keys, values, k2, v2, wk, wv, T0, S):
+    """New rows within two bf16 steps of the larger of the element and its head vector's RMS
+    (an element much smaller than its vector carries the absolute error of the vector's sums),
+    one step or less on almost all elements; the rest of the cache bit for bit."""
     for got, want, old in ((k2, wk, keys), (v2, wv, values)):
+        g, wnt = bf(got[:, T0:T0 + S]).astype(np.float64), bf(want[:, T0:T0 + S]).astype(np.float64)
+        rms = np.sqrt((wnt * wnt).mean(-1, keepdims=True))
+        scale = np.maximum(np.abs(wnt), rms)
+        assert (np.abs(g - wnt) <= scale * 2.0 ** -7).all(), np.abs(g - wnt).max()
         u = ulp_diff(got[:, T0:T0 + S], want[:, T0:T0 + S])
-        assert u.max() <= 2 and (u > 0).mean() <= 1e-2, (u.max(), (u > 0).mean())
+        assert (u > 1).mean() <= 1e-3, (u > 1).mean()
         assert np.array_equal(got[:, :T0], old[:, :T0]) and np.array_equal(got[:, T0 + S:], old[:, T0 + S:])
 
 
