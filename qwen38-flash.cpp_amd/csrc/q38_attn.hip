@@ -265,44 +265,72 @@ __global__ __launch_bounds__(256) void k_attn_pv(AttnDev A, AttnBufs B, int S, c
     for (int mt = 0; mt < kPvMt; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // per M-tile: this lane's A-row query, its softmax max and sum (read once)
+    size_t qrow[kPvMt];
+    int rrow[kPvMt];
+    float mrow[kPvMt], srow[kPvMt];
+#pragma unroll
+    for (int mt = 0; mt < kPvMt; ++mt) {
+        const int j = (mt0 + mt) * 16 + c;
+        rrow[mt] = -1;
+        if (mt < nmt && j < NQ) {
+            rrow[mt] = j / G;
+            qrow[mt] = static_cast<size_t>(rrow[mt]) * HQ + g * G + j % G;
+            mrow[mt] = B.mx[qrow[mt]];
+            srow[mt] = B.sm[qrow[mt]];
+        }
+    }
+    // the scores of the lane's 2 x 8 tokens of a sub-tile, per M-tile (loaded with the values)
+    uint4 scv[kPvMt][2];
+    auto load_sc = [&](int64_t ts) {
+#pragma unroll
+        for (int mt = 0; mt < kPvMt; ++mt)
+            if (rrow[mt] >= 0)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    scv[mt][ks] = *reinterpret_cast<const uint4*>(B.sc + qrow[mt] * tpad + ts + 32 * ks + 8 * q);
+    };
     load(tb);
+    load_sc(tb);
     for (int s = 0; s < nsub; ++s) {
         const int64_t ts = tb + static_cast<int64_t>(kTok) * s;
         __syncthreads();  // the previous sub-tile's reads are done
         store();
         __syncthreads();
-        if (s + 1 < nsub) load(ts + kTok);
+        uint4 pa[kPvMt][2];
+#pragma unroll
+        for (int mt = 0; mt < kPvMt; ++mt) {
+            pa[mt][0] = pa[mt][1] = make_uint4(0u, 0u, 0u, 0u);
+            if (rrow[mt] < 0) continue;
+            const int64_t last = T0 + rrow[mt];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int64_t t = ts + 32 * ks + 8 * q;
+                const uint32_t u[4] = {scv[mt][ks].x, scv[mt][ks].y, scv[mt][ks].z, scv[mt][ks].w};
+                uint32_t pk[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float s0 = __uint_as_float(u[e] << 16), s1 = __uint_as_float(u[e] & 0xFFFF0000u);
+                    const uint32_t p0 = t + 2 * e <= last ? f2bf(expf(s0 - mrow[mt]) / srow[mt]) : 0u;
+                    const uint32_t p1 = t + 2 * e + 1 <= last ? f2bf(expf(s1 - mrow[mt]) / srow[mt]) : 0u;
+                    pk[e] = p0 | (p1 << 16);
+                }
+                pa[mt][ks] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            }
+        }
+        if (s + 1 < nsub) {  // the next sub-tile's values and scores are in flight during the MFMAs
+            load(ts + kTok);
+            load_sc(ts + kTok);
+        }
 #pragma unroll
         for (int mt = 0; mt < kPvMt; ++mt) {
             if (mt >= nmt) break;
-            const int j = (mt0 + mt) * 16 + c;
-            uint4 pa[2] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
-            if (j < NQ) {
-                const int r = j / G;
-                const size_t qi = static_cast<size_t>(r) * HQ + g * G + j % G;
-                const float m = B.mx[qi], sum = B.sm[qi];
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const int64_t t = ts + 32 * ks + 8 * q;
-                    const uint4 sv = *reinterpret_cast<const uint4*>(B.sc + qi * tpad + t);
-                    const uint32_t u[4] = {sv.x, sv.y, sv.z, sv.w};
-                    uint32_t pk[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float s0 = __uint_as_float(u[e] << 16), s1 = __uint_as_float(u[e] & 0xFFFF0000u);
-                        const uint32_t p0 = t + 2 * e <= T0 + r ? f2bf(expf(s0 - m) / sum) : 0u;
-                        const uint32_t p1 = t + 2 * e + 1 <= T0 + r ? f2bf(expf(s1 - m) / sum) : 0u;
-                        pk[e] = p0 | (p1 << 16);
-                    }
-                    pa[ks] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-                }
-            }
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt) {
                 const uint16_t* col = vt + ((w * NTW + nt) * 16 + c) * VS + 8 * q;
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks)
-                    acc[mt][nt] = mfma_bf16(pa[ks], *reinterpret_cast<const uint4*>(col + 32 * ks), acc[mt][nt]);
+                    acc[mt][nt] = mfma_bf16(pa[mt][ks], *reinterpret_cast<const uint4*>(col + 32 * ks), acc[mt][nt]);
             }
         }
     }
