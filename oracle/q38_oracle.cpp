@@ -42,8 +42,16 @@
 //   GatedDeltaNet verify   independent numpy restatement (float64 state, vectorised per
 //                          head), closed forms (one row from a zero state: state = beta v k^T,
 //                          output beta v (k . q); beta 0: the state decays by g per row;
-//                          one-hot conv taps), S rows = S single-row calls chained through
-//                          the checkpoints; a planted wrong key-head mapping fails them.
+//                          decay 1, beta 1 and a one-hot key: the delta rule replaces that
+//                          column of the state by v), S rows = S single-row calls chained
+//                          through the checkpoints; a planted wrong key-head mapping fails them.
+//   attention verify       independent numpy restatement (float64, numpy cos / sin, the
+//                          rotation as a 2 x 2 matrix per pair), closed forms (the bf16 RoPE
+//                          table at position 0 and at R = 2; with an identity o_proj and zero
+//                          gates: a zero query gives the mean of the visible values / 2, a
+//                          one-hot query matched by one large key reads that token's value),
+//                          S rows = S single-row calls through the cache; planted RoPE-pairing
+//                          and causal-mask faults fail them.
 
 #include <pthread.h>
 #include <sched.h>
