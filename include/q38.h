@@ -646,11 +646,35 @@ int q38_hc_write(const q38_hc* hc, const uint16_t* stream, const uint16_t* block
  * (q38_moe_forward), stream = mixers[l].write(stream, y, read.injection). stream: device
  * [rows, HC * H] bf16, updated in place; rows 1..16. Layers and mixers share H; every
  * mixer has injection weights, the same streams and rank. The decoder's optional MLP output
- * map (src/decoder_layer.cpp:198-210) is not applied. Workspace:
+ * map (src/decoder_layer.cpp:198-210) is applied by q38_verify_chain_hc_mapped. Workspace:
  * q38_verify_chain_hc_workspace_size bytes for the largest layer description. */
 size_t q38_verify_chain_hc_workspace_size(const q38_moe_desc* desc, const q38_hc_desc* mixer, int32_t max_rows);
 int q38_verify_chain_hc(q38_moe_layer* const* layers, q38_hc* const* mixers, int32_t n_layers, uint16_t* stream,
                         int32_t rows, void* workspace, size_t workspace_bytes, void* hip_stream);
+/* The decoder's optional MLP output map (DecoderLayer::apply_mlp_output_map,
+ * src/decoder_layer.cpp:198-210, tensors loaded at :158-182): rank 0 takes the full map mlp.T
+ * [H][H] bf16 (out = T(y . T)); rank R > 0 the low-rank pair mlp.T_delta_left [H][R] and
+ * mlp.T_delta_right [R][H] bf16 (out = T(y + T(T(y . left) . right))). Each product sums in
+ * float over 128-input slices in ascending order, the slices added in order. */
+typedef struct q38_mlp_map {
+    int32_t hidden;
+    int32_t rank;          /* 0: full map                                                    */
+    const uint16_t* full;  /* [H][H] bf16 (rank 0)                                           */
+    const uint16_t* left;  /* [H][rank] bf16                                                 */
+    const uint16_t* right; /* [rank][H] bf16                                                 */
+} q38_mlp_map;
+size_t q38_mlp_map_workspace_size(const q38_mlp_map* map, int32_t max_rows);
+/* y [rows, H] bf16 -> out [rows, H] bf16 (out must not alias y); rows 1..16. */
+int q38_mlp_output_map(const q38_mlp_map* map, const uint16_t* y, int32_t rows, uint16_t* out, void* workspace,
+                       size_t workspace_bytes, void* stream);
+/* q38_verify_chain_hc with the MLP output map of each layer (maps[l], or null for a layer
+ * without one; maps itself may be null): per layer read, MoE, map, write
+ * (src/decoder_layer.cpp:494-497). Workspace: q38_verify_chain_hc_mapped_workspace_size for
+ * the largest layer description. */
+size_t q38_verify_chain_hc_mapped_workspace_size(const q38_moe_desc* desc, const q38_hc_desc* mixer, int32_t max_rows);
+int q38_verify_chain_hc_mapped(q38_moe_layer* const* layers, q38_hc* const* mixers, const q38_mlp_map* const* maps,
+                               int32_t n_layers, uint16_t* stream, int32_t rows, void* workspace,
+                               size_t workspace_bytes, void* hip_stream);
 /* HyperConnection::initialize_stream (src/hyper_connection.cpp:298-307): the embedding rows
  * [rows, H] tiled to [rows, streams * H]. H a multiple of 8. */
 int q38_hc_initialize_stream(const uint16_t* embedding, int32_t rows, int32_t hidden, int32_t streams, uint16_t* out,

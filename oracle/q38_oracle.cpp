@@ -52,6 +52,9 @@
 //                          one-hot query matched by one large key reads that token's value),
 //                          S rows = S single-row calls through the cache; planted RoPE-pairing
 //                          and causal-mask faults fail them.
+//   MLP output map         closed forms (identity full map: out = y; zero right factor: out = y;
+//                          rank-1 one-hot factors: column b gains column a, a transposed factor
+//                          fails), float64 numpy within tolerance.
 
 #include <pthread.h>
 #include <sched.h>
@@ -1337,6 +1340,25 @@ void attn_verify(const AttnDesc& d, const AttnW& W, const uint16_t* x, int S, ui
     }
 }
 
+// ---- the decoder's MLP output map (DecoderLayer::apply_mlp_output_map,
+// src/decoder_layer.cpp:198-210): out = T(y . T), or T(y + T(T(y . L) . R)) with the low-rank
+// pair. MLX's bf16 matmul order is not specified (parity unpinned there); this build's contract:
+// per output element, float fmaf over 128-input slices in ascending order, the slices' sums
+// added in slice order, then rounded to bf16.
+void map_product(const float* a, int rows, int K, const uint16_t* W, int N, float* out) {
+    for (int r = 0; r < rows; ++r)
+        for (int n = 0; n < N; ++n) {
+            float total = 0.0f;
+            for (int k0 = 0; k0 < K; k0 += 128) {
+                float acc = 0.0f;
+                for (int k = k0; k < std::min(K, k0 + 128); ++k)
+                    acc = std::fma(a[static_cast<size_t>(r) * K + k], bf16_to_f32(W[static_cast<size_t>(k) * N + n]), acc);
+                total += acc;
+            }
+            out[static_cast<size_t>(r) * N + n] = rbf16(total);
+        }
+}
+
 } // namespace
 
 // ======================================================================== C ABI
@@ -1761,6 +1783,20 @@ int orc_gdn_verify(const GdnDesc* d, const uint32_t* const* w, const uint16_t* c
     return 0;
 }
 
+void orc_mlp_map(int H, int rank, const uint16_t* full, const uint16_t* left, const uint16_t* right,
+                 const uint16_t* y, int rows, uint16_t* out) {
+    std::vector<float> yf(static_cast<size_t>(rows) * H), o(static_cast<size_t>(rows) * H);
+    for (size_t i = 0; i < yf.size(); ++i) yf[i] = bf16_to_f32(y[i]);
+    if (rank == 0) {
+        map_product(yf.data(), rows, H, full, H, o.data());
+    } else {
+        std::vector<float> t(static_cast<size_t>(rows) * rank);
+        map_product(yf.data(), rows, H, left, rank, t.data());
+        map_product(t.data(), rows, rank, right, H, o.data());
+        for (size_t i = 0; i < o.size(); ++i) o[i] = rbf16(yf[i] + o[i]);
+    }
+    for (size_t i = 0; i < o.size(); ++i) out[i] = f32_to_bf16(o[i]);
+}
 void orc_attn_plant_fault(int f) { g_attn_fault = f; }
 void orc_rope_table(double theta, int R, int64_t pos, float* c, float* s) { rope_table(theta, R, pos, c, s); }
 int orc_attn_verify(const AttnDesc* d, const uint32_t* const* w, const uint16_t* const* sc, const uint16_t* const* bi,

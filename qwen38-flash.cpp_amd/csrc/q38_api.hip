@@ -2000,6 +2000,100 @@ int q38_verify_chain_hc(q38_moe_layer* const* layers, q38_hc* const* mixers, int
     return Q38_OK;
 }
 
+static int map_check(const q38_mlp_map* m, int hidden) {
+    if (!m) return fail(Q38_EINVAL, "null MLP output map");
+    if (m->hidden != hidden || hidden <= 0) return fail(Q38_EINVAL, "MLP output map hidden size mismatch");
+    if (m->rank < 0 || m->rank > hidden) return fail(Q38_EINVAL, "invalid Niwaki low-rank map geometry");
+    if (m->rank == 0 ? !m->full : (!m->left || !m->right)) return fail(Q38_EINVAL, "incomplete Niwaki low-rank map pair");
+    return Q38_OK;
+}
+static MlpMapDev map_dev(const q38_mlp_map* m) { return MlpMapDev{m->hidden, m->rank, m->full, m->left, m->right}; }
+
+size_t q38_mlp_map_workspace_size(const q38_mlp_map* map, int32_t max_rows) {
+    if (!map || max_rows < 1 || max_rows > kMaxRows || map->hidden <= 0 || map->rank < 0 || map->rank > map->hidden)
+        return 0;
+    return mlp_map_workspace(map->hidden, map->rank, max_rows);
+}
+
+int q38_mlp_output_map(const q38_mlp_map* map, const uint16_t* y, int32_t rows, uint16_t* out, void* ws,
+                       size_t ws_bytes, void* stream) {
+    if (!map || !y || !out || !ws) return fail(Q38_EINVAL, "q38_mlp_output_map: null argument");
+    if (int rc = map_check(map, map->hidden)) return rc;
+    if (int rc = check_rows(rows)) return rc;
+    if (out == y) return fail(Q38_EINVAL, "q38_mlp_output_map: out must not alias y");
+    if (ws_bytes < mlp_map_workspace(map->hidden, map->rank, rows)) return fail(Q38_ESPACE, "workspace too small");
+    Q38_HIP(launch_mlp_map(map_dev(map), y, rows, out, ws, static_cast<hipStream_t>(stream)));
+    return Q38_OK;
+}
+
+size_t q38_verify_chain_hc_mapped_workspace_size(const q38_moe_desc* d, const q38_hc_desc* hd, int32_t max_rows) {
+    const size_t base = q38_verify_chain_hc_workspace_size(d, hd, max_rows);
+    if (!base) return 0;
+    // the MoE output, the mapped output and the map's scratch (a full map is the largest)
+    const size_t H = static_cast<size_t>(hd->hidden), R = static_cast<size_t>(max_rows);
+    return base + 2 * align256(R * H * 2) + mlp_map_workspace(hd->hidden, 0, max_rows);
+}
+
+int q38_verify_chain_hc_mapped(q38_moe_layer* const* layers, q38_hc* const* mixers, const q38_mlp_map* const* maps,
+                               int32_t n_layers, uint16_t* stream, int32_t rows, void* ws, size_t ws_bytes,
+                               void* hip_stream) {
+    if (!maps) return q38_verify_chain_hc(layers, mixers, n_layers, stream, rows, ws, ws_bytes, hip_stream);
+    if (!layers || !mixers || n_layers < 1 || !stream || !ws) return fail(Q38_EINVAL, "q38_verify_chain_hc: bad arguments");
+    if (int rc = check_rows(rows)) return rc;
+    if (!mixers[0] || !layers[0]) return fail(Q38_EINVAL, "q38_verify_chain_hc: null layer or mixer");
+    for (int l = 0; l < n_layers; ++l)
+        if (maps[l])
+            if (int rc = map_check(maps[l], mixers[0]->desc.hidden)) return rc;
+    const size_t need = q38_verify_chain_hc_mapped_workspace_size(&layers[0]->desc, &mixers[0]->desc, rows);
+    size_t chain_need = 0;
+    for (int l = 0; l < n_layers; ++l) {
+        if (!layers[l]) return fail(Q38_EINVAL, "q38_verify_chain_hc: null layer or mixer");
+        chain_need = std::max(chain_need, q38_verify_chain_hc_workspace_size(&layers[l]->desc, &mixers[0]->desc, rows));
+    }
+    const size_t H = static_cast<size_t>(mixers[0]->desc.hidden);
+    const size_t extra = 2 * align256(static_cast<size_t>(rows) * H * 2) + mlp_map_workspace(static_cast<int>(H), 0, rows);
+    if (ws_bytes < std::max(need, chain_need + extra)) return fail(Q38_ESPACE, "workspace too small");
+    char* base = static_cast<char*>(ws);
+    const size_t chain_bytes = align256(chain_need);
+    uint16_t* y = reinterpret_cast<uint16_t*>(base + chain_bytes);
+    uint16_t* ym = reinterpret_cast<uint16_t*>(base + chain_bytes + align256(static_cast<size_t>(rows) * H * 2));
+    void* mws = base + chain_bytes + 2 * align256(static_cast<size_t>(rows) * H * 2);
+    const hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    for (int l = 0; l < n_layers; ++l) {
+        if (!maps[l]) {  // the fused path for this layer
+            if (int rc = q38_verify_chain_hc(layers + l, mixers + l, 1, stream, rows, ws, chain_bytes, hip_stream))
+                return rc;
+            continue;
+        }
+        if (!mixers[l]) return fail(Q38_EINVAL, "q38_verify_chain_hc: null layer or mixer");
+        const q38_hc_desc& hd = mixers[l]->desc;
+        if (layers[l]->desc.hidden != hd.hidden || hd.hidden != mixers[0]->desc.hidden ||
+            hd.streams != mixers[0]->desc.streams || hd.rank != mixers[0]->desc.rank || !hd.with_injection)
+            return fail(Q38_EINVAL, "q38_verify_chain_hc: layers and mixers disagree on the hidden size, streams or rank");
+        uint16_t *mixed = nullptr, *inj = nullptr;
+        void* hcws = nullptr;
+        const size_t moe_need = moe_ws(layers[l]->desc, rows, nullptr, nullptr);
+        chain_hc_ws(moe_need, hd, rows, base, &mixed, &inj, &hcws);
+        auto* xn = static_cast<uint16_t*>(hcws);
+        auto* act = reinterpret_cast<float*>(static_cast<char*>(hcws) +
+                                             align256(static_cast<size_t>(rows) * hd.streams * hd.hidden * 2));
+        Q38_HIP(launch_hc_read(mixers[l]->dev, rows, stream, xn, act, mixed, inj, st));
+        MoeBufs w{};
+        moe_ws(layers[l]->desc, rows, &w, ws);
+        const LayerDev dev = moe_call_dev(layers[l]->dev, rows);
+        const LayerDev ex = expert_view(dev);
+        Q38_HIP(launch_router(dev, w, rows, mixed, false, 0.0f, st));
+        Q38_HIP(launch_shared_affine(dev, w, rows, st));
+        if (!moe_plans_in_gate_up(ex, rows)) Q38_HIP(launch_topk_plan(ex, w, rows, st));
+        Q38_HIP(launch_gate_up(ex, w, rows, st));
+        Q38_HIP(launch_down(ex, w, rows, st));
+        Q38_HIP(launch_combine(dev, w, rows, nullptr, y, st));
+        Q38_HIP(launch_mlp_map(map_dev(maps[l]), y, rows, ym, mws, st));
+        Q38_HIP(launch_hc_write(hd.hidden, hd.streams, rows, stream, ym, inj, stream, st));
+    }
+    return Q38_OK;
+}
+
 int q38_hc_initialize_stream(const uint16_t* embedding, int32_t rows, int32_t hidden, int32_t streams, uint16_t* out,
                              void* st) {
     if (!embedding || !out || rows < 1 || rows > kMaxPrefillRows || hidden < 8 || hidden % 8 || streams < 1 ||

@@ -204,6 +204,17 @@ hipError_t launch_attn_verify(const AttnDev& A, const AttnBufs& B, int S, const 
                               uint16_t* values, int64_t cap, int64_t T0, int64_t position, uint16_t* out,
                               hipStream_t st);
 
+// The decoder's MLP output map (q38_map.hip): rank 0 = the full map full [H][H]; otherwise
+// the low-rank pair left [H][rank], right [rank][H]; bf16.
+struct MlpMapDev {
+    int hidden, rank;
+    const uint16_t* full;
+    const uint16_t* left;
+    const uint16_t* right;
+};
+size_t mlp_map_workspace(int hidden, int rank, int rows);
+hipError_t launch_mlp_map(const MlpMapDev& m, const uint16_t* y, int rows, uint16_t* out, void* ws, hipStream_t st);
+
 struct GdnDev {
     int hidden, hk, hv, dk, dv, bits, group, f16, gate_silu;
     float eps;

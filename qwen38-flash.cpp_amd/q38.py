@@ -203,6 +203,18 @@ _sig("q38_hc_write", C.c_int, P, P, P, P, I32, P, P)
 _sig("q38_hc_initialize_stream", C.c_int, P, I32, I32, I32, P, P)
 
 
+class MlpMap(C.Structure):  # include/q38.h q38_mlp_map
+    _fields_ = [("hidden", C.c_int32), ("rank", C.c_int32), ("full", C.c_void_p), ("left", C.c_void_p),
+                ("right", C.c_void_p)]
+
+
+_sig("q38_mlp_map_workspace_size", SZ, C.POINTER(MlpMap), I32)
+_sig("q38_mlp_output_map", C.c_int, C.POINTER(MlpMap), P, I32, P, P, SZ, P)
+_sig("q38_verify_chain_hc_mapped_workspace_size", SZ, C.POINTER(MoeDesc), C.POINTER(HcDesc), I32)
+_sig("q38_verify_chain_hc_mapped", C.c_int, C.POINTER(P), C.POINTER(P), C.POINTER(C.POINTER(MlpMap)), I32, P, I32, P,
+     SZ, P)
+
+
 class MtpStreams(C.Structure):
     _fields_ = [("block_mixer", P), ("final_mixer", P), ("embedding_norm", P), ("hidden_norm", P)]
 

@@ -106,6 +106,7 @@ class Oracle:
         sig("orc_gdn_recurrence", C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, P, P, P, P, P)
         sig("orc_gdn_verify", C.c_int, C.POINTER(GdnDesc), C.POINTER(P), C.POINTER(P), C.POINTER(P), P, P, P, P, P,
             C.c_int, P, P, P)
+        sig("orc_mlp_map", None, C.c_int, C.c_int, P, P, P, P, C.c_int, P)
         sig("orc_attn_plant_fault", None, C.c_int)
         sig("orc_rope_table", None, C.c_double, C.c_int, I64, P, P)
         sig("orc_attn_verify", C.c_int, C.POINTER(AttnDesc), C.POINTER(P), C.POINTER(P), C.POINTER(P), P, P, P,
@@ -296,6 +297,17 @@ class Oracle:
                                      _a(layer.norm_w), _a(x), S, None if org is None else _a(org), _a(out), _a(ck))
         assert rc == 0
         return out, ck
+
+    def mlp_map(self, y, full=None, left=None, right=None):
+        """The decoder's MLP output map on rows y [rows, H] (bf16 bits): the full map [H, H] or the
+        low-rank pair left [H, R], right [R, H] (bf16 bits) -> out [rows, H] bf16 bits."""
+        y = np.ascontiguousarray(y, np.uint16)
+        rows, H = y.shape
+        rank = 0 if full is not None else left.shape[1]
+        keep = [None if a is None else np.ascontiguousarray(a, np.uint16) for a in (full, left, right)]
+        out = np.empty_like(y)
+        self.lib.orc_mlp_map(H, rank, *[None if a is None else _a(a) for a in keep], _a(y), rows, _a(out))
+        return out
 
     def attn_plant_fault(self, code):
         self.lib.orc_attn_plant_fault(code)
