@@ -473,16 +473,24 @@ __global__ __launch_bounds__(256) void k_samp_stats(const float* __restrict__ tl
     const float* l = r <= k ? tl + static_cast<int64_t>(r) * V : dl + static_cast<int64_t>(r - k - 1) * V;
     const int64_t a = static_cast<int64_t>(c) * cs, b = a + cs < V ? a + cs : V;
     float m = -INFINITY, s = 0.0f;
-    for (int64_t x = a + tid; x < b; x += 256) {
-        const float v = l[x];
-        if (!(v > -INFINITY)) continue;  // a -inf logit has probability 0
+    auto take = [&](float v) {
+        if (!(v > -INFINITY)) return;  // a -inf logit has probability 0
         if (v > m) {
             s = (m == -INFINITY ? 0.0f : s * expf((m - v) * invT)) + 1.0f;
             m = v;
         } else {
             s += expf((v - m) * invT);
         }
+    };
+    int64_t x = a + tid;
+    for (; x + 3 * 256 < b; x += 4 * 256) {  // four loads in flight, taken in index order
+        const float v0 = l[x], v1 = l[x + 256], v2 = l[x + 512], v3 = l[x + 768];
+        take(v0);
+        take(v1);
+        take(v2);
+        take(v3);
     }
+    for (; x < b; x += 256) take(l[x]);
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
         const float m2 = __shfl_xor(m, off, kWave), s2 = __shfl_xor(s, off, kWave);
@@ -518,33 +526,60 @@ __global__ __launch_bounds__(64) void k_samp_decide(const float* __restrict__ tl
         if (lane == 0) st[r] = make_float2(m, s);
     }
     __syncthreads();
+    // lane i: position i's uniforms and p(d_i), q(d_i) (all positions at once), then lane 0
+    // walks the accept chain in order
+    __shared__ float su[25], sv[25], spd[24], sqd[24];
+    if (lane <= k) {
+        float u, v;
+        round_uniforms(seed, slot, round, static_cast<uint32_t>(lane), &u, &v);
+        su[lane] = u;
+        sv[lane] = v;
+        if (lane < k) {
+            const float2 ps = st[lane], qs = st[k + 1 + lane];
+            const uint32_t d = drafts[lane];
+            // an out-of-vocabulary draft is rejected (never read out of bounds)
+            spd[lane] = d < V ? expf((tl[static_cast<int64_t>(lane) * V + d] - ps.x) * invT) / ps.y : 0.0f;
+            sqd[lane] = d < V ? expf((dl[static_cast<int64_t>(lane) * V + d] - qs.x) * invT) / qs.y : 1.0f;
+        }
+    }
+    __syncthreads();
     if (lane != 0) return;
     for (int i = 0; i <= k; ++i) {
-        float u, v;
-        round_uniforms(seed, slot, round, static_cast<uint32_t>(i), &u, &v);
         const float2 ps = st[i];
         if (i == k) {
-            *ctl = SampCtl{k, v, ps.x, ps.y, 0.0f, 1.0f};
+            *ctl = SampCtl{k, sv[i], ps.x, ps.y, 0.0f, 1.0f};
             return;
         }
+        if (su[i] * sqd[i] < spd[i]) continue;
         const float2 qs = st[k + 1 + i];
-        const uint32_t d = drafts[i];
-        // an out-of-vocabulary draft is rejected (never read out of bounds)
-        const float pd = d < V ? expf((tl[static_cast<int64_t>(i) * V + d] - ps.x) * invT) / ps.y : 0.0f;
-        const float qd = d < V ? expf((dl[static_cast<int64_t>(i) * V + d] - qs.x) * invT) / qs.y : 1.0f;
-        if (u * qd < pd) continue;
-        *ctl = SampCtl{i, v, ps.x, ps.y, qs.x, qs.y};
+        *ctl = SampCtl{i, sv[i], ps.x, ps.y, qs.x, qs.y};
         return;
     }
 }
 
-// Residual weight of index x under the control block's row.
-__device__ __forceinline__ float samp_weight(const float* tl, const float* dl, int k, int64_t V, const SampCtl& c,
-                                             float invT, int64_t x) {
-    const float p = expf((tl[static_cast<int64_t>(c.row) * V + x] - c.pm) * invT) / c.ps;
-    if (c.row == k) return p;
-    const float q = expf((dl[static_cast<int64_t>(c.row) * V + x] - c.qm) * invT) / c.qs;
-    return fmaxf(0.0f, p - q);
+// The residual weights of indices x0 .. x1 - 1 in index order, 8 indices' logits loaded at a
+// time; f(x, w) returns true to stop.
+template <typename F>
+__device__ __forceinline__ void samp_weights(const float* tl, const float* dl, int k, int64_t V, const SampCtl& c,
+                                             float invT, int64_t x0, int64_t x1, F&& f) {
+    const float* pr = tl + static_cast<int64_t>(c.row) * V;
+    const float* qr = c.row == k ? pr : dl + static_cast<int64_t>(c.row) * V;
+    for (int64_t x = x0; x < x1; x += 8) {
+        float pl[8], ql[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int64_t xi = x + j < x1 ? x + j : x1 - 1;
+            pl[j] = pr[xi];
+            ql[j] = qr[xi];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (x + j >= x1) return;
+            const float p = expf((pl[j] - c.pm) * invT) / c.ps;
+            const float w = c.row == k ? p : fmaxf(0.0f, p - expf((ql[j] - c.qm) * invT) / c.qs);
+            if (f(x + j, w)) return;
+        }
+    }
 }
 
 // Thread t of a chunk owns the contiguous sub-range [a + t * sub, a + (t + 1) * sub).
@@ -576,11 +611,11 @@ __global__ __launch_bounds__(256) void k_samp_mass(const float* __restrict__ tl,
     __syncthreads();
     float s = 0.0f;
     int64_t lp = -1;
-    for (int64_t x = x0; x < x1; ++x) {
-        const float w = samp_weight(tl, dl, k, V, c, invT, x);
+    samp_weights(tl, dl, k, V, c, invT, x0, x1, [&](int64_t x, float w) {
         s += w;
         if (w > 0.0f) lp = x;
-    }
+        return false;
+    });
     if (lp >= 0) atomicMax(&last, static_cast<unsigned long long>(lp + 1));
     const float t = block_sum_ordered(s, sh);
     if (threadIdx.x == 0) {
@@ -594,23 +629,26 @@ __global__ __launch_bounds__(256) void k_samp_draw(const float* __restrict__ tl,
                                                    const SampCtl* __restrict__ ctl, const float* __restrict__ csum,
                                                    const int64_t* __restrict__ clast, int64_t* __restrict__ out) {
     __shared__ float pre[256];
+    __shared__ float cs_l[kSampChunks];
     __shared__ int chunk;
     __shared__ float base, target;
     __shared__ unsigned long long found;
     const SampCtl c = *ctl;
     const int tid = threadIdx.x;
+    if (tid < nc) cs_l[tid] = csum[tid];
+    __syncthreads();
     if (tid == 0) {
         float total = 0.0f;
-        for (int i = 0; i < nc; ++i) total += csum[i];
+        for (int i = 0; i < nc; ++i) total += cs_l[i];
         const float tg = c.v * total;
         float run = 0.0f;
         int ch = -1;
         for (int i = 0; i < nc; ++i) {
-            if (csum[i] > 0.0f && run <= tg && tg < run + csum[i]) {
+            if (cs_l[i] > 0.0f && run <= tg && tg < run + cs_l[i]) {
                 ch = i;
                 break;
             }
-            run += csum[i];
+            run += cs_l[i];
         }
         chunk = ch;
         base = run;
@@ -625,7 +663,10 @@ __global__ __launch_bounds__(256) void k_samp_draw(const float* __restrict__ tl,
         int64_t x0, x1;
         samp_range(a, b, sub, tid, x0, x1);
         float s = 0.0f;
-        for (int64_t x = x0; x < x1; ++x) s += samp_weight(tl, dl, k, V, c, invT, x);
+        samp_weights(tl, dl, k, V, c, invT, x0, x1, [&](int64_t, float w) {
+            s += w;
+            return false;
+        });
         pre[tid] = s;
         __syncthreads();
         if (tid == 0) {  // exclusive prefix over the threads, in index order
@@ -641,12 +682,11 @@ __global__ __launch_bounds__(256) void k_samp_draw(const float* __restrict__ tl,
         if (s > 0.0f && excl <= target && target < excl + s) {
             float run = excl;
             int64_t p = -1;
-            for (int64_t x = x0; x < x1; ++x) {
-                const float w = samp_weight(tl, dl, k, V, c, invT, x);
+            samp_weights(tl, dl, k, V, c, invT, x0, x1, [&](int64_t x, float w) {
                 run += w;
                 if (w > 0.0f) p = x;  // the last positive so far: the fallback of this range
-                if (run > target && w > 0.0f) break;
-            }
+                return run > target && w > 0.0f;
+            });
             if (p >= 0) atomicMin(&found, static_cast<unsigned long long>(p));
         }
         __syncthreads();
