@@ -1486,12 +1486,12 @@ namespace {
 constexpr int kMtpMaxRows = 4;
 
 struct MtpWork {
-    uint16_t *e16, *ne, *nh, *x, *f;
+    uint16_t *x, *f;
     float *pe, *ph, *logits;
     unsigned long long* best;
     uint32_t* tokens;
-    void* head_ws;
-    size_t head_ws_bytes;
+    HeadWork we, wh[4];  // the FC projections' prepared rows (the stream projection in passes)
+    int mh[4], passes;
     void* moe_ws;
     size_t moe_ws_bytes;
 };
@@ -1507,11 +1507,7 @@ size_t mtp_layout(const q38_mtp_head* m, int rows, MtpWork* w, void* base) {
         return p;
     };
     const size_t HC = static_cast<size_t>(m->streams);
-    const int fc_rows = std::min(kHeadMaxRows, rows * m->streams);  // the stream projections run in passes
     MtpWork t{};
-    t.e16 = reinterpret_cast<uint16_t*>(take(rows * H * 2));
-    t.ne = reinterpret_cast<uint16_t*>(take(rows * H * 2));
-    t.nh = reinterpret_cast<uint16_t*>(take(rows * HC * H * 2));
     t.x = reinterpret_cast<uint16_t*>(take(rows * HC * H * 2));
     t.f = reinterpret_cast<uint16_t*>(take(rows * H * 2));
     t.pe = reinterpret_cast<float*>(take(rows * H * 4));
@@ -1519,8 +1515,13 @@ size_t mtp_layout(const q38_mtp_head* m, int rows, MtpWork* w, void* base) {
     t.logits = reinterpret_cast<float*>(take(rows * V * 4));
     t.best = reinterpret_cast<unsigned long long*>(take(rows * 8));
     t.tokens = reinterpret_cast<uint32_t*>(take(rows * 4));
-    t.head_ws_bytes = std::max(q38_head_workspace_size(m->fc_e, rows), q38_head_workspace_size(m->fc_h, fc_rows));
-    t.head_ws = take(t.head_ws_bytes);
+    t.we = head_work_carve(take(head_work_bytes(m->fc_e->dev, rows, false)), m->fc_e->dev, rows, false);
+    const int nrows = rows * m->streams;  // the stream projection's rows, in passes of up to 16
+    t.passes = (nrows + kHeadMaxRows - 1) / kHeadMaxRows;
+    for (int p = 0; p < t.passes; ++p) {
+        t.mh[p] = std::min(kHeadMaxRows, nrows - p * kHeadMaxRows);
+        t.wh[p] = head_work_carve(take(head_work_bytes(m->fc_h->dev, t.mh[p], false)), m->fc_h->dev, t.mh[p], false);
+    }
     t.moe_ws_bytes = q38_moe_workspace_size(&m->layer->desc, rows);
     if (m->block_hc) {
         t.moe_ws_bytes = std::max(t.moe_ws_bytes, q38_verify_chain_hc_workspace_size(&m->layer->desc,
@@ -1549,19 +1550,36 @@ int mtp_validate(q38_moe_layer* layer, q38_head* fe, q38_head* fh, q38_head* dh)
 // hidden norm runs over the row's HC * H values, the hidden projection over each stream, the
 // embedding projection is added to every stream, the block is the mixer read -> MoE ->
 // mixer write, and the final mixer's read gives the LM head's input.
-int mtp_step(q38_mtp_head* m, const MtpWork& w, const uint16_t* stream_in, const uint32_t* tokens, int rows,
-             float* logits, const q38_mtp_trace* trace, hipStream_t st) {
+// tokens: the step's tokens, or null in a chain: the previous step's argmax keys in w.best,
+// whose tokens the prologue also records as drafts[., prev_step].
+int mtp_step(q38_mtp_head* m, const MtpWork& w, const uint16_t* stream_in, const uint32_t* tokens, uint32_t* drafts,
+             int depth, int prev_step, int rows, float* logits, const q38_mtp_trace* trace, hipStream_t st) {
     const int H = m->layer->desc.hidden, HC = m->streams;
-    Q38_HIP(launch_gen_embed_dev(m->embed_seed, tokens, rows, H, w.e16, st));
-    Q38_HIP(launch_rmsnorm_w(w.e16, rows, H, m->eps, m->emb_norm, w.ne, st));
-    Q38_HIP(launch_rmsnorm_w(stream_in, rows, HC * H, m->eps, m->hid_norm, w.nh, st));
-    if (int rc = q38_head_logits(m->fc_e, w.ne, rows, w.pe, w.head_ws, w.head_ws_bytes, st)) return rc;
-    for (int r0 = 0; r0 < rows * HC; r0 += kHeadMaxRows) {
-        const int n = std::min(kHeadMaxRows, rows * HC - r0);
-        if (int rc = q38_head_logits(m->fc_h, w.nh + static_cast<size_t>(r0) * H, n, w.ph + static_cast<size_t>(r0) * H,
-                                     w.head_ws, w.head_ws_bytes, st))
-            return rc;
+    DraftPro P{};
+    P.embed_key = stream_key(m->embed_seed, kEmbedLayer, T_EMBED);
+    P.toks = tokens;
+    P.best = w.best;
+    P.drafts = drafts;
+    P.tokens_out = w.tokens;
+    P.depth = depth;
+    P.prev_step = prev_step;
+    P.stream = stream_in;
+    P.H = H;
+    P.HC = HC;
+    P.M = rows;
+    P.eps = m->eps;
+    P.emb_norm = m->emb_norm;
+    P.hid_norm = m->hid_norm;
+    P.we = w.we;
+    for (int p = 0; p < w.passes; ++p) {
+        P.wh[p] = w.wh[p];
+        P.mh[p] = w.mh[p];
     }
+    Q38_HIP(launch_draft_prologue(P, st));
+    Q38_HIP(launch_head_logits_prepared(m->fc_e->dev, rows, w.we, w.pe, st));
+    for (int p = 0; p < w.passes; ++p)
+        Q38_HIP(launch_head_logits_prepared(m->fc_h->dev, w.mh[p], w.wh[p],
+                                            w.ph + static_cast<size_t>(p) * kHeadMaxRows * H, st));
     Q38_HIP(launch_fc_join(w.pe, w.ph, rows, HC, H, w.x, w.best, st));
     if (trace && trace->combined)
         Q38_HIP(hipMemcpyAsync(trace->combined, w.x, static_cast<size_t>(rows) * HC * H * 2, hipMemcpyDeviceToDevice,
@@ -1697,7 +1715,8 @@ int q38_mtp_forward_decode(q38_mtp_head* m, const uint16_t* stream_in, const uin
     MtpWork w{};
     mtp_layout(m, rows, &w, ws);
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    if (int rc = mtp_step(m, w, stream_in, tokens, rows, logits ? logits : w.logits, trace, st)) return rc;
+    if (int rc = mtp_step(m, w, stream_in, tokens, nullptr, 0, 0, rows, logits ? logits : w.logits, trace, st))
+        return rc;
     if (stream_out)
         Q38_HIP(hipMemcpyAsync(stream_out, w.x, static_cast<size_t>(rows) * m->streams * m->layer->desc.hidden * 2,
                                hipMemcpyDeviceToDevice, st));
@@ -1717,12 +1736,17 @@ int q38_mtp_draft_greedy(q38_mtp_head* m, const uint16_t* stream_in, const uint3
     const uint16_t* s_in = stream_in;
     const uint32_t* t_in = tokens;
     for (int step = 0; step < depth; ++step) {
-        // the step's join clears w.best; its argmax feeds the next step's token and stream
-        if (int rc = mtp_step(m, w, s_in, t_in, rows, w.logits, nullptr, st)) return rc;
-        Q38_HIP(launch_argmax(w.logits, rows, m->draft->dev.V, w.best, false, w.tokens, nullptr, drafts, depth, step,
-                              st));
+        // the step's join clears w.best; its argmax keys feed the next step's prologue (which
+        // records this step's drafts), the last step's are finished here
+        if (int rc = mtp_step(m, w, s_in, step == 0 ? t_in : nullptr, drafts, depth, step - 1, rows, w.logits, nullptr,
+                              st))
+            return rc;
+        if (step + 1 == depth)
+            Q38_HIP(launch_argmax(w.logits, rows, m->draft->dev.V, w.best, false, w.tokens, nullptr, drafts, depth,
+                                  step, st));
+        else
+            Q38_HIP(launch_argmax_rows(w.logits, rows, m->draft->dev.V, w.best, st));
         s_in = w.x;
-        t_in = w.tokens;
     }
     if (stream_out)
         Q38_HIP(hipMemcpyAsync(stream_out, w.x, static_cast<size_t>(rows) * m->streams * m->layer->desc.hidden * 2,

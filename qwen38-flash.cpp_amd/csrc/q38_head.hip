@@ -57,14 +57,14 @@ HeadWork head_work_carve(void* base, const HeadDev& hd, int M, bool greedy) {
     return w;
 }
 
-// One block per request row: the int8 planes of h, its plane scale, the residual R and
-// sum|h| (double, fixed order), and the reset of the pass state (kernel stores, no memset
-// nodes, so the sequence can be captured in a graph).
-__global__ __launch_bounds__(256) void k_head_prep(const uint16_t* __restrict__ h, int H, int M, HeadWork w) {
+// The int8 planes of one request row hr (H values, global or LDS), its plane scale, the
+// residual R and sum|h| (double, fixed order), and the reset of the pass state for row r of
+// an M-row call (kernel stores, no memset nodes, so the sequence can be captured in a graph).
+// Called by all 256 threads of a workgroup; may be called repeatedly in one workgroup.
+__device__ void head_prep_row(const uint16_t* hr, int H, int M, int r, const HeadWork& w) {
     __shared__ float redm[4];
     __shared__ double redt[4], redr[4];
-    const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const uint16_t* hr = h + static_cast<size_t>(r) * H;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     float m = 0.0f;
     for (int c = tid; c < H; c += 256) m = fmaxf(m, fabsf(bf2f(hr[c])));
     m = wave_max(m);
@@ -103,6 +103,12 @@ __global__ __launch_bounds__(256) void k_head_prep(const uint16_t* __restrict__ 
         w.cnt[r] = 0;
         w.best[r] = 0ull;
     }
+    __syncthreads();
+}
+
+// One block per request row.
+__global__ __launch_bounds__(256) void k_head_prep(const uint16_t* __restrict__ h, int H, int M, HeadWork w) {
+    head_prep_row(h + static_cast<size_t>(blockIdx.x) * H, H, M, blockIdx.x, w);
 }
 
 // Fast pass on v_mfma_i32_16x16x64_i8. A tile is 16 vocab rows; the TB groups of four
@@ -842,6 +848,13 @@ hipError_t launch_fc_join(const float* a, const float* b, int M, int HC, int H, 
     return launch(k_fc_join, dim3((n + 255) / 256), dim3(256), 0, st, a, b, M, HC, H, x, best);
 }
 
+// The row argmax keys alone (best must start at 0; no k_argmax_final).
+hipError_t launch_argmax_rows(const float* logits, int M, int64_t V, unsigned long long* best, hipStream_t st) {
+    if (M < 1 || M > 64 || V < 1) return hipErrorInvalidValue;
+    const int64_t blocks = std::min<int64_t>(128, (V + 255) / 256);
+    return launch(k_argmax_rows, dim3(static_cast<unsigned>(blocks), M), dim3(256), 0, st, logits, V, best);
+}
+
 hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long long* best, bool clear,
                          uint32_t* tokens, float* values, uint32_t* drafts, int depth, int step, hipStream_t st) {
     if (M < 1 || M > 64 || V < 1) return hipErrorInvalidValue;
@@ -853,6 +866,76 @@ hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long lo
     hipError_t e = launch(k_argmax_rows, dim3(static_cast<unsigned>(blocks), M), dim3(256), 0, st, logits, V, best);
     if (e != hipSuccess) return e;
     return launch(k_argmax_final, dim3(1), dim3(64), 0, st, best, M, tokens, values, drafts, depth, step);
+}
+
+// The draft step's inputs of its two FC projections in one launch (the embedding, the two
+// RMSNorms and the Q8 planes of both projections' rows): workgroup (r, 0) forms request r's
+// embedding row (token toks[r], or, in a chain, the previous step's argmax best[r], whose
+// token it also records), (r, 1) loads its stream row; each RMS-normalises its row (H or
+// HC * H values in k_rmsnorm's order, with the offset weight when given) in LDS and prepares
+// the Q8 planes of the resulting head rows: the embedding row as row r of we, the stream's HC
+// rows as the rows g = r HC + s of the stream projection's passes (pass g / 16, row g % 16).
+__global__ __launch_bounds__(256) void k_draft_prologue(DraftPro P) {
+    extern __shared__ __align__(16) uint16_t row[];  // [HC * H] bf16
+    __shared__ float red[4];
+    const int r = blockIdx.x, which = blockIdx.y, tid = threadIdx.x;
+    const int H = P.H, W = which ? P.HC * H : H;
+    float ss = 0.0f;
+    if (which == 0) {
+        uint32_t t;
+        if (P.toks) {
+            t = P.toks[r];
+        } else {
+            t = 0xFFFFFFFFu - static_cast<uint32_t>(P.best[r]);
+            if (tid == 0) {
+                if (P.tokens_out) P.tokens_out[r] = t;
+                if (P.drafts) P.drafts[static_cast<size_t>(r) * P.depth + P.prev_step] = t;
+            }
+        }
+        for (int c = tid; c < W; c += 256) {
+            const uint16_t e = f2bf(static_cast<float>(normal_at(P.embed_key, static_cast<uint64_t>(t) * H + c)));
+            const float v = bf2f(e);
+            ss = fmaf(v, v, ss);
+            row[c] = e;
+        }
+    } else {
+        for (int c = tid; c < W; c += 256) {
+            const uint16_t e = P.stream[static_cast<size_t>(r) * W + c];
+            const float v = bf2f(e);
+            ss = fmaf(v, v, ss);
+            row[c] = e;
+        }
+    }
+    ss = wave_sum_xor(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / sqrtf(tot / static_cast<float>(W) + P.eps);
+    const uint16_t* wn = which ? P.hid_norm : P.emb_norm;
+    for (int c = tid; c < W; c += 256) {
+        const float n = rbf(bf2f(row[c]) * inv);
+        row[c] = f2bf(wn ? n * bf2f(wn[c]) : n);
+    }
+    __syncthreads();
+    if (which == 0) {
+        head_prep_row(row, H, P.M, r, P.we);
+    } else {
+        for (int sidx = 0; sidx < P.HC; ++sidx) {
+            const int g = r * P.HC + sidx, pass = g / kHeadMaxRows;
+            head_prep_row(row + static_cast<size_t>(sidx) * H, H, P.mh[pass], g % kHeadMaxRows, P.wh[pass]);
+        }
+    }
+}
+
+hipError_t launch_draft_prologue(const DraftPro& P, hipStream_t st) {
+    const size_t lds = static_cast<size_t>(P.HC) * P.H * 2;
+    if (const hipError_t e = ensure_lds<k_draft_prologue>(lds); e != hipSuccess) return e;
+    return launch(k_draft_prologue, dim3(P.M, 2), dim3(256), lds, st, P);
+}
+
+hipError_t launch_head_logits_prepared(const HeadDev& hd, int M, const HeadWork& w, float* logits, hipStream_t st) {
+    if (hd.kind != 0) return hipErrorInvalidValue;
+    return launch_i8(hd, M, w, logits, st);
 }
 
 namespace {

@@ -342,6 +342,27 @@ struct HeadWork {
     float* fast;        // [M, V] (greedy)
 };
 constexpr int kHeadMaxRows = 16;
+// The draft step's prologue (k_draft_prologue): embedding / stream rows, their RMSNorms and
+// the Q8 planes of the FC projections' rows.
+struct DraftPro {
+    uint64_t embed_key;
+    const uint32_t* toks;               // step tokens, or null: take them from best
+    const unsigned long long* best;     // the previous step's argmax keys
+    uint32_t* drafts;                   // (chain) the previous step's drafts [M][depth]
+    uint32_t* tokens_out;
+    int depth, prev_step;
+    const uint16_t* stream;             // [M][HC * H]
+    int H, HC, M;
+    float eps;
+    const uint16_t* emb_norm;           // [H] or null
+    const uint16_t* hid_norm;           // [HC * H] or null
+    HeadWork we;                        // the embedding projection's rows
+    HeadWork wh[4];                     // the stream projection's passes of up to 16 rows
+    int mh[4];
+};
+hipError_t launch_draft_prologue(const DraftPro& P, hipStream_t st);
+hipError_t launch_argmax_rows(const float* logits, int M, int64_t V, unsigned long long* best, hipStream_t st);
+hipError_t launch_head_logits_prepared(const HeadDev& hd, int M, const HeadWork& w, float* logits, hipStream_t st);
 size_t head_work_bytes(const HeadDev& hd, int M, bool greedy);
 HeadWork head_work_carve(void* base, const HeadDev& hd, int M, bool greedy);
 hipError_t head_init_attrs();
