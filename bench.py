@@ -480,6 +480,23 @@ def main():
                "gbps": g_bytes / (g_us * 1e-6) / 1e9}
     log(f"config 1 with 64-input scale groups (4 rows): {g_us:.1f} us/layer, {g64_cfg['gbps']:.0f} GB/s, U={g_u:.1f}")
 
+    # ---------------------------------------------------------------- per-dimension U8 books
+    # Config-1 layers with the reference's verify-width INT8/U8 books (Q38_CB_U8_PERDIM): the
+    # kernels that read the books themselves (q38_set_u8_native(2)), and the decoded fp16 book
+    # on the other verify kernels (mode 0; the one-launch layer at 1-4 rows); 8 layers. The
+    # default mode takes the faster of the two per width.
+    u8_cfg = {"layers": 8}
+    for Mu in (1, 4, 16):
+        for native in (2, 0):
+            q38.lib.q38_set_u8_native(native)
+            u_us, u_u, u_bytes = chain_leg(q38.desc(book_format=q38.Q38_CB_U8_PERDIM), Mu, 8)
+            u8_cfg[f"m{Mu}_{'u8_kernels' if native else 'decoded_book'}_us"] = u_us
+            u8_cfg[f"m{Mu}_unique_experts"] = u_u
+    q38.lib.q38_set_u8_native(1)
+    log("config 1 with U8 books, us/layer (U8 kernels / decoded book): " +
+        ", ".join(f"M={Mu}: {u8_cfg[f'm{Mu}_u8_kernels_us']:.1f} / {u8_cfg[f'm{Mu}_decoded_book_us']:.1f}"
+                  for Mu in (1, 4, 16)))
+
     # ---------------------------------------------------------------- decoder MLP half
     # HyperConnection read -> MoE -> write (q38_verify_chain_hc) for 4 rows through 8 config-1
     # layers with 4-stream mixers (rank 256, 4-bit affine weights in groups of 64, seeded
@@ -929,7 +946,7 @@ def main():
             "kernel_us_per_launch_m4": {k.split()[0]: 1e3 * v[0] / nl for k, v in kernels.items()},
             "algorithmic_bytes_per_launch_m4": {k.split()[0]: v[1] for k, v in kernels.items()},
             "config3_prefill": prefill_cfg,
-            "config4_mixed": mixed_cfg, "config1_group64": g64_cfg, "decoder_mlp_half_hc": hc_cfg,
+            "config4_mixed": mixed_cfg, "config1_group64": g64_cfg, "config1_u8_books": u8_cfg, "decoder_mlp_half_hc": hc_cfg,
             "gdn_verify_step": gdn_cfg,
             "attention_verify_step": attn_cfg,
             "config2_sampled": sampled_cfg,

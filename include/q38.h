@@ -196,6 +196,17 @@ int q38_ctx_synchronize(q38_ctx* ctx, void* stream);
  * grid at one workgroup per CU (checked once per device against the kernel's occupancy). */
 void q38_set_fused_layers(int enable);
 
+/* Process-wide mode for layers with Q38_CB_U8_PERDIM books whose three projections are
+ * d8/14-bit with per-row scales (H 2048, I 512, no affine shared expert): which verify widths
+ * run on the kernels that read the per-dimension INT8/U8 books themselves (the reference's
+ * verify-width decode, src/vq_metal_kernels.hpp:564-579, which forms w = q * scale (+ bias)
+ * per weight): one 8-byte entry per subvector from a book held whole in LDS, the
+ * per-dimension scale applied to the inputs and the bias as a per-row sum. 0: none (the
+ * decoded fp16 book on the other kernels); 1 (default): 5-16 rows, and 1-4 rows where the
+ * one-launch layer kernel is not taken (it is faster at those widths); 2: 1-16 rows.
+ * No counterpart in the reference. */
+void q38_set_u8_native(int mode);
+
 /* Test hook: the number of re-reads a bounded wait makes before it gives up (default 65536,
  * about 0.1 s; a negative value restores it). A limit of 0 makes a wait give up at its first
  * read of a value another workgroup has not stored yet, so tests can reach the give-up path

@@ -143,6 +143,7 @@ int q38_ctx_synchronize(q38_ctx* ctx, void* stream) {
 }
 
 void q38_set_fused_layers(int enable) { set_fused_enabled(enable != 0); }
+void q38_set_u8_native(int mode) { set_u8_native(mode); }
 
 void q38_debug_set_wait_limit(int32_t spins) { set_wait_limit(spins); }
 
@@ -254,7 +255,9 @@ static int prepare_layer(q38_moe_layer* L) {
         total += align256((static_cast<size_t>(1) << L->dev.p[p].bits) * L->dev.p[p].dim * 2);
         u8[p] = L->desc.book_format == Q38_CB_U8_PERDIM && L->dev.p[p].dim == 8 && L->dev.p[p].bits == 14;
         uoff[p] = total;
-        if (u8[p]) total += align256(size_t{16384} * 8) + 256 + align256(size_t{16384} * 8 * 2);
+        // q, scales + biases, the decoded book, then the U8 kernels' operands (u, 16 floats)
+        if (u8[p]) total += align256(size_t{16384} * 8) + 256 + align256(size_t{16384} * 8 * 2) +
+                            align256(size_t{16384} * 8) + 256;
     }
     int64_t rows[3] = {0, 0, 0};
     for (int p = 0; p < 3 && tiled; ++p) {
@@ -273,6 +276,12 @@ static int prepare_layer(q38_moe_layer* L) {
         auto* sb = reinterpret_cast<uint16_t*>(base + uoff[p] + align256(size_t{16384} * 8));
         auto* dec = reinterpret_cast<uint16_t*>(base + uoff[p] + align256(size_t{16384} * 8) + 256);
         e = launch_prepare_u8(L->dev.p[p].book, 16384, p == 0 ? 1 : 0, q, sb, sb + 8, dec, nullptr);
+        char* ops = base + uoff[p] + align256(size_t{16384} * 8) + 256 + align256(size_t{16384} * 8 * 2);
+        if (e == hipSuccess)
+            e = launch_u8_operands(q, 16384, p == 0 ? 1 : 0, sb, sb + 8, reinterpret_cast<uint8_t*>(ops),
+                                   reinterpret_cast<float*>(ops + align256(size_t{16384} * 8)), nullptr);
+        L->dev.p[p].book_u8 = reinterpret_cast<const uint8_t*>(ops);
+        L->dev.p[p].u8_sb = reinterpret_cast<const float*>(ops + align256(size_t{16384} * 8));
         L->u8q[p] = q;
         L->u8s[p] = sb;
         L->u8b[p] = sb + 8;
@@ -300,6 +309,9 @@ static int prepare_layer(q38_moe_layer* L) {
         return hip_fail(e, "codebook preparation");
     }
     L->prepared = base;
+    // the U8 verify kernels: all three books U8, H 2048, I 512, per-row scales
+    L->dev.u8_native = u8[0] && u8[1] && u8[2] && !L->dev.mixed && L->dev.H == 2048 && L->dev.I == 512 &&
+                       L->dev.p[0].ngrp == 1 && L->dev.p[1].ngrp == 1 && L->dev.p[2].ngrp == 1;
     return Q38_OK;
 }
 
@@ -953,6 +965,7 @@ static size_t moe_ws(const q38_moe_desc& d, int M, MoeBufs* w, void* base) {
     t.u = reinterpret_cast<float*>(take(2 * gu * 4));
     t.d = reinterpret_cast<float*>(take(2 * dn * 4));
     t.h16 = reinterpret_cast<uint16_t*>(take(gu * 2));
+    t.dcorr = t.g ? t.g + gu : nullptr;  // (g's second plane: unused by the U8 kernels' calls)
     t.gu_plane = gu;
     t.d_plane = dn;
     t.wait_limit = wait_limit();

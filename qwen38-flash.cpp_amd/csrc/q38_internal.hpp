@@ -73,6 +73,12 @@ struct ProjDev {
     // chunks of 4 words (the last chunk BITS % 4 wide when not 0) with the 64 rows
     // interleaved inside each chunk, so one 16-byte load per lane reads 1 KiB contiguously.
     const uint32_t* codes_t;
+    // A per-dimension INT8/U8 book in the form the U8 verify kernels read (or null): [2^bits][8]
+    // bytes u (the centred book's codes offset by 128, u = q + 128), and u8_sb = 16 floats,
+    // the per-dimension scale s[8] then the offset b[8] (the affine book's min, -128 s for the
+    // centred book), so that the decoded weight is u * s[d] + b[d].
+    const uint8_t* book_u8;
+    const float* u8_sb;
 };
 
 // Workspace views of one MoE call (rows <= kMaxRows).
@@ -90,7 +96,10 @@ struct MoeBufs {
     float* g;          // [2][M*K + M, I] gate
     float* u;          // [2][M*K + M, I] up
     float* d;          // [2][M*K + M, H] down
-    uint16_t* h16;     // [M*K + M, I] fp16 SwiGLU rows (prefill path)
+    uint16_t* h16;     // [M*K + M, I] fp16 SwiGLU rows (prefill path; the U8 down operand)
+    // [M*K + M] per-route correction of the U8 down kernel; it shares the storage of g's second
+    // plane, which the U8 path (one plane) leaves unused.
+    float* dcorr;
     size_t gu_plane;   // floats between the chunk planes of g and u
     size_t d_plane;    // floats between the chunk planes of d
     // Re-reads a bounded wait between workgroups of one launch makes before it gives up
@@ -127,6 +136,10 @@ struct LayerDev {
     // without a shared slot (expert_view); the router (shared gate) and the combine keep it.
     AffineDev sa[3];
     int shared_affine, sa_bits, sa_group, sa_inter, sa_f16;
+    // u8_native: the three projections carry U8 books the U8 verify kernels read (d8/14-bit,
+    // H 2048, I 512, per-row scales, no affine shared expert). u8_call: this call runs them
+    // (moe_call_dev: 1-16 rows while they are enabled); it then writes one partial-sum plane.
+    int u8_native, u8_call;
 };
 
 // The view of a layer the routed-expert kernels take: without the shared slot when the shared
@@ -273,6 +286,16 @@ bool moe_plans_in_gate_up(const LayerDev& L, int M);
 bool moe_uses_narrow(const LayerDev& L, int M);
 // The layer view of a call of M rows: the partial-sum plane counts of the kernels it takes.
 LayerDev moe_call_dev(const LayerDev& L, int M);
+// Verify widths (1-16 rows) of layers with U8 books on the kernels that read the books
+// themselves (k_gu_u8, k_swiglu_u8, k_dn_u8), by mode: 0 never (the decoded fp16 books on the
+// other verify kernels), 1 (default) at 5-16 rows and at 1-4 rows where the one-launch layer
+// is not taken, 2 at every verify width.
+bool moe_u8_call(const LayerDev& L, int M);
+void set_u8_native(int mode);
+// The U8 kernels' operands of a per-dimension book: u = q (+ 128 when centred) as bytes and
+// the 16 floats s[8], b[8] (ProjDev::book_u8, u8_sb).
+hipError_t launch_u8_operands(const void* q, int K, int centered, const uint16_t* s16, const uint16_t* b16,
+                              uint8_t* u, float* sb, hipStream_t st);
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 hipError_t launch_down4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st);
 // The d8/14-bit, H 2048, I 512, top-10, per-row-scale layers at up to 4 rows run gate/up and

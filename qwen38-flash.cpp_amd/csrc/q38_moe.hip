@@ -630,6 +630,340 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
     }
 }
 
+// ============================================================== U8 books (R6, verify widths)
+// The reference's verify-width decode (src/vq_metal_kernels.hpp:564-579) reads a d8
+// projection's per-dimension INT8/U8 book: w = q s[d] (+ b[d]), s and b fp16 per dimension.
+// Here the book is kept as bytes u = q + 128 (centred gate book) or u = q (affine books), so
+// that w = (u - 128) s[d] + c[d] with c = 0 (centred) or b + 128 s (affine). One 8-byte entry
+// holds all 8 dims, so the whole book (16384 x 8 bytes) sits in one workgroup's LDS: one
+// gather per subvector, where the fp16 book takes two (one per 4-dim chunk, in two
+// workgroups). v_mfma_f32_16x16x32_f16 takes A = u - 128, exact in fp16 (v_perm pairs two
+// bytes with the exponent byte of 1024, giving 1024 + u, then a packed fp16 add of -1152),
+// and B = x' = fp16(s[d] x) per input, so for each B column (input row or route)
+//   sum_k w_k x_k = sum_k (u_k - 128) x'_k + sum_k c[d_k] x_k
+// up to the rounding of x' (relative 2^-12 per input, carried by |u - 128| s, about |w|).
+// The second sum is formed once per column in a fixed order. Lane (c, q) of a 16-row tile:
+// A = row c's entry for subvector q S4 + t, B = column c's x' of that subvector (8 fp16),
+// t = 0 .. S4 - 1 (S4 = subvectors / 4).
+__device__ __forceinline__ void wait_vm_all_moe() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+constexpr int kU8Cols = 4;  // gate/up: request rows staged per pass (the book leaves room for 4)
+constexpr uint32_t kF16Exp1024 = 0x64646464u;
+
+__device__ __forceinline__ h8_t u8_entry_f16(uint2 e) {
+    // bytes u0..u7 -> fp16 1024 + u0 .. 1024 + u7 (dims in order) -> u - 128, exact
+    const uint4 v = make_uint4(__builtin_amdgcn_perm(kF16Exp1024, e.x, 0x04010400u),
+                               __builtin_amdgcn_perm(kF16Exp1024, e.x, 0x04030402u),
+                               __builtin_amdgcn_perm(kF16Exp1024, e.y, 0x04010400u),
+                               __builtin_amdgcn_perm(kF16Exp1024, e.y, 0x04030402u));
+    return __builtin_bit_cast(h8_t, v) - static_cast<_Float16>(1152.0f);
+}
+
+// x' of one subvector (8 fp16 inputs) and its share of the column sum sum_k c[d_k] x_k (in c,
+// dimension order).
+__device__ __forceinline__ uint4 u8_scale_sub(uint4 xv, const float (&s)[8], const float (&b)[8], float& c) {
+    const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t pr = 0;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int d = 2 * i + k;
+            const float x = h2f(static_cast<uint16_t>(w[i] >> (16 * k)));
+            const uint16_t xp = f2h(x * s[d]);
+            c = fmaf(b[d], x, c);
+            pr |= static_cast<uint32_t>(xp) << (16 * k);
+        }
+        o[i] = pr;
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__device__ __forceinline__ void u8_load_sb(const float* sb, float (&s)[8], float (&b)[8]) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        s[d] = sb[d];
+        b[d] = sb[8 + d];
+    }
+}
+
+// One 16-row tile over all NSUB subvectors: A from the U8 book, B = xlane[t] (this lane's
+// column, q block) from LDS or registers. Two accumulators (even and odd steps), added.
+template <int NSUB, typename XB>
+__device__ __forceinline__ f4_t mfma_tile_u8(const uint32_t* w, const uint2* book, const XB& xlane) {
+    constexpr int S4 = NSUB / 4;
+    f4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < S4; t += 2) {
+        const h8_t a0 = u8_entry_f16(book[code_from<14>(w, t)]);
+        const h8_t a1 = u8_entry_f16(book[code_from<14>(w, t + 1)]);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8_t, xlane[t]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8_t, xlane[t + 1]), acc1, 0, 0, 0);
+    }
+    return acc0 + acc1;
+}
+
+// Gate and up from the U8 books: workgroup type = projection (the whole book in LDS), items
+// (slot, 128-row tile of I). Waves 0-3 copy the book into LDS over the direct global-to-LDS
+// path while waves 4-7 stage x' of the request rows (M <= kU8Cols: lane l of those 256
+// threads takes subvector l of every row) with their shares of each row's column sum C =
+// sum_k c[d_k] x_k (wave butterflies, then the four waves' sums in order); then routing and
+// the plan as in k_gu_mfma, and the first item's codes are requested before the copy is
+// waited for. Wider calls stage x' per pass of up to kU8Cols of a slot's routes, and C comes
+// from one wave per row. The x' rows are padded per q block (S4 + 1 entries), so the 16
+// columns x 4 blocks of one B read fall in different LDS banks. Output: one plane,
+// scale * (acc + C), at the route's sorted position.
+template <int NSUB>
+__global__ __launch_bounds__(kMfmaThreads) void k_gu_u8(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ TopkLds tk;
+    __shared__ int32_t plan[kPlanInts];
+    __shared__ float cx[kMaxRows];          // C of each request row (this projection)
+    __shared__ float cpart[4][kU8Cols];     // staging waves' shares of C
+    __shared__ int32_t exf[kNarrowMaxRoutes];          // (fast routing) the rows' experts
+    __shared__ uint64_t cand[kU8Cols][64];             // (fast routing) candidates per row wave
+    constexpr int KENT = 1 << 14;
+    constexpr int S4 = NSUB / 4, WPL = S4 * 14 / 32, XR = 4 * (S4 + 1);
+    static_assert(NSUB == 256, "one staging thread per subvector");
+    const uint2* book = reinterpret_cast<const uint2*>(lds);
+    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);  // [kU8Cols + 1 zero][4][S4 + 1] x'
+    auto xat = [](int row, int sv) { return row * XR + (sv / S4) * (S4 + 1) + sv % S4; };
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
+    const int proj = kk & 1;
+    const int per_type = (gridDim.x / 16) * 8;
+    const int idx = (kk >> 1) * 8 + x8;
+    const ProjDev& P = L.p[proj];
+    const int H = L.H, I = L.I, K = L.K;
+    float s[8], b[8];
+    u8_load_sb(P.u8_sb, s, b);
+    const bool stage_all = M <= kU8Cols;
+    if (wave < 4) {
+        dma_book<KENT>(reinterpret_cast<const uint16_t*>(P.book_u8), lds, wave, 4);
+    } else if (stage_all) {
+        const int sv = tid - 256;
+        uint4 xv[kU8Cols];
+#pragma unroll
+        for (int r = 0; r < kU8Cols; ++r)
+            if (r < M) xv[r] = *reinterpret_cast<const uint4*>(B.x16 + static_cast<size_t>(r) * H + 8 * sv);
+#pragma unroll
+        for (int r = 0; r < kU8Cols; ++r)
+            if (r < M) {
+                float c = 0.0f;
+                xs[xat(r, sv)] = u8_scale_sub(xv[r], s, b, c);
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
+                if (lane == 0) cpart[wave - 4][r] = c;
+            }
+    }
+    // Routing: up to 4 rows of E = 512 by the one-wave routines of the four-row kernels
+    // (row r on wave 4 + r, the plan by wave 4), otherwise the block routine.
+    if (stage_all && L.E == 512 && M * K <= kNarrowMaxRoutes) {
+        if (wave >= 4 && wave - 4 < M) {
+            float lg[8];
+            topk_load_row_t<8, true>(L, B, wave - 4, lg);
+            topk_select_row_fast<8>(L, B, wave - 4, lg, exf, blockIdx.x == 0, cand[wave - 4]);
+        }
+        lds_barrier();
+        if (wave == 4) plan_wave(M, K, exf, plan);
+        lds_barrier();
+    } else {
+        topk_plan_block(L, B, M, blockIdx.x == 0, plan, tk, 4);
+    }
+    if (blockIdx.x == 0)
+        for (int i = tid; i < 2 + 4 * M * L.K; i += kMfmaThreads) B.plan[i] = plan[i];
+    if (stage_all) {
+        if (tid < M) cx[tid] = ((cpart[0][tid] + cpart[1][tid]) + cpart[2][tid]) + cpart[3][tid];
+    } else {
+        for (int r = wave; r < M; r += 8) {
+            float c = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NSUB / 64; ++i) {
+                const uint4 xv = *reinterpret_cast<const uint4*>(B.x16 + static_cast<size_t>(r) * H + 8 * (lane + 64 * i));
+                (void)u8_scale_sub(xv, s, b, c);
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
+            if (lane == 0) cx[r] = c;
+        }
+    }
+    for (int i = tid; i < XR; i += kMfmaThreads) xs[kU8Cols * XR + i] = make_uint4(0u, 0u, 0u, 0u);
+    const int nu = plan[0];
+    const int nslots = nu + (L.has_shared ? 1 : 0);
+    const int tiles = I / kMfmaRowsPerItem;
+    const int n_items = nslots * tiles;
+    float* out = proj == 0 ? B.g : B.u;
+    const int r16 = lane & 15, q = lane >> 4;
+    auto code_src = [&](int item) {
+        int expert, n, pos0;
+        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
+        const size_t rowi = static_cast<size_t>(expert) * I + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
+        return P.codes + rowi * P.words + q * WPL;
+    };
+    uint32_t w[WPL + 1], wn[WPL + 1];
+    if (idx < n_items) load_lane_words<14, NSUB>(code_src(idx), w);
+    wait_vm_all_moe();  // (the book copy of waves 0-3)
+    lds_barrier();
+    for (int item = idx; item < n_items; item += per_type) {
+        if (item + per_type < n_items) load_lane_words<14, NSUB>(code_src(item + per_type), wn);
+        const int ui = item / tiles, tile = item % tiles;
+        int expert, n, pos0;
+        slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
+        const bool shared = ui == nu;
+        const int o0 = tile * kMfmaRowsPerItem + wave * 16;
+        for (int j0 = 0; j0 < n; j0 += kU8Cols) {
+            const int nj = n - j0 < kU8Cols ? n - j0 : kU8Cols;
+            const int crow = r16 < nj ? route_row(plan, M, K, pos0, j0 + r16, shared) : 0;
+            const int xrow = stage_all ? crow : r16;
+            if (!stage_all) {
+                lds_barrier();
+                for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
+                    const int jj = i / NSUB, sv = i % NSUB;
+                    const int row = route_row(plan, M, K, pos0, j0 + jj, shared);
+                    float c = 0.0f;
+                    xs[xat(jj, sv)] = u8_scale_sub(
+                        *reinterpret_cast<const uint4*>(B.x16 + static_cast<size_t>(row) * H + 8 * sv), s, b, c);
+                }
+                lds_barrier();
+            }
+            const uint4* xlane = xs + (r16 < nj ? xrow : kU8Cols) * XR + q * (S4 + 1);
+            const f4_t acc = mfma_tile_u8<NSUB>(w, book, xlane);
+            if (r16 < nj) {
+                const float c = cx[crow];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int o = o0 + 4 * q + rr;
+                    const float sc = h2f(P.scales[static_cast<size_t>(expert) * I + o]);
+                    out[static_cast<size_t>(pos0 + j0 + r16) * I + o] = sc * (acc[rr] + c);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i <= WPL; ++i) w[i] = wn[i];
+    }
+}
+
+// SwiGLU rows of every route as the U8 down kernel's B operand: one wave per sorted position
+// (I = 512: lane l = subvector l), h = fp16(swiglu(g, u)) as on the fp16-book path, then
+// h' = fp16(s[d] h) into B.h16 ([position][I], subvector-major) and the route's column sum
+// C = sum_k c[d_k] h_k into B.dcorr (lane order, then a fixed butterfly).
+__global__ __launch_bounds__(256) void k_swiglu_u8(LayerDev L, MoeBufs B, int n_routes) {
+    const int pos = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (pos >= n_routes) return;
+    float s[8], b[8];
+    u8_load_sb(L.p[2].u8_sb, s, b);
+    const size_t at = static_cast<size_t>(pos) * L.I + 8 * lane;
+    const float4 g0 = *reinterpret_cast<const float4*>(B.g + at), g1 = *reinterpret_cast<const float4*>(B.g + at + 4);
+    const float4 u0 = *reinterpret_cast<const float4*>(B.u + at), u1 = *reinterpret_cast<const float4*>(B.u + at + 4);
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    uint32_t hw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        hw[i] = static_cast<uint32_t>(f2h(swiglu(gv[2 * i], uv[2 * i]))) |
+                (static_cast<uint32_t>(f2h(swiglu(gv[2 * i + 1], uv[2 * i + 1]))) << 16);
+    float c = 0.0f;
+    const uint4 hp = u8_scale_sub(make_uint4(hw[0], hw[1], hw[2], hw[3]), s, b, c);
+    *reinterpret_cast<uint4*>(B.h16 + at) = hp;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
+    if (lane == 0) B.dcorr[pos] = c;
+}
+
+// Down from the U8 book: every workgroup holds the book; items (slot, 128-row tile of H); B =
+// the slot's h' rows straight from the workspace (lane (c, q): 16 x 16 bytes of route c's row),
+// loaded with the item's codes one item ahead. Routes in passes of 16 (one pass at <= 16 rows).
+// Output: one plane, scale * (acc + C), at the route index.
+template <int NSUB>
+__global__ __launch_bounds__(kMfmaThreads) void k_dn_u8(LayerDev L, MoeBufs B, int M) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ int32_t plan[kPlanInts];
+    constexpr int KENT = 1 << 14;
+    constexpr int S4 = NSUB / 4, WPL = S4 * 14 / 32;
+    static_assert(NSUB == 64, "I = 512");
+    const uint2* book = reinterpret_cast<const uint2*>(lds);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int idx = blockIdx.x, per_type = gridDim.x;
+    const ProjDev& P = L.p[2];
+    const int H = L.H, I = L.I, K = L.K, MK = M * K;
+    // the plan first (a wave's loads complete in order), then the book over the direct
+    // global-to-LDS path; the first item's loads go out before the copy is waited for
+    constexpr int PV = (kPlanInts + kMfmaThreads - 1) / kMfmaThreads;
+    const int plan_n = 2 + 4 * MK;
+    int pv[PV];
+#pragma unroll
+    for (int k = 0; k < PV; ++k) pv[k] = tid + k * kMfmaThreads < plan_n ? B.plan[tid + k * kMfmaThreads] : 0;
+    dma_book<KENT>(reinterpret_cast<const uint16_t*>(P.book_u8), lds, wave, 8);
+#pragma unroll
+    for (int k = 0; k < PV; ++k)
+        if (tid + k * kMfmaThreads < plan_n) plan[tid + k * kMfmaThreads] = pv[k];
+    lds_barrier();
+    const int nu = plan[0];
+    const int tiles = H / kMfmaRowsPerItem;
+    const int n_items = (nu + (L.has_shared ? 1 : 0)) * tiles;
+    const int r16 = lane & 15, q = lane >> 4;
+    struct Item {
+        uint32_t w[WPL + 1];
+        uint4 bx[S4];
+    };
+    auto load = [&](int item, int j0, Item& it) {
+        int expert, n, pos0;
+        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
+        const size_t rowi = static_cast<size_t>(expert) * H + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
+        load_lane_words<14, NSUB>(P.codes + rowi * P.words + q * WPL, it.w);
+        if (j0 + r16 < n) {
+            const uint4* src = reinterpret_cast<const uint4*>(B.h16 + static_cast<size_t>(pos0 + j0 + r16) * I) + q * S4;
+#pragma unroll
+            for (int t = 0; t < S4; ++t) it.bx[t] = src[t];
+        } else {
+#pragma unroll
+            for (int t = 0; t < S4; ++t) it.bx[t] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    Item cur, nxt;
+    if (idx < n_items) load(idx, 0, cur);
+    wait_vm_all_moe();  // (the book copy)
+    lds_barrier();
+    for (int item = idx; item < n_items; item += per_type) {
+        int expert, n, pos0;
+        slot_rows(plan, M, K, L.has_shared, item / tiles, L.E, &expert, &n, &pos0);
+        const int o0 = (item % tiles) * kMfmaRowsPerItem + wave * 16;
+        for (int j0 = 0; j0 < n; j0 += 16) {
+            // the next load: this item's next pass, else the next item's first
+            const bool more = j0 + 16 < n;
+            if (more) load(item, j0 + 16, nxt);
+            else if (item + per_type < n_items) load(item + per_type, 0, nxt);
+            const f4_t acc = mfma_tile_u8<NSUB>(cur.w, book, cur.bx);
+            if (j0 + r16 < n) {
+                const int pos = pos0 + j0 + r16;
+                const float c = B.dcorr[pos];
+                const size_t rt = static_cast<size_t>(route_of_pos(plan, MK, pos)) * H;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int o = o0 + 4 * q + rr;
+                    const float sc = h2f(P.scales[static_cast<size_t>(expert) * H + o]);
+                    B.d[rt + o] = sc * (acc[rr] + c);
+                }
+            }
+            cur = nxt;
+        }
+    }
+}
+
+// u = q (+ 128 when centred) and the 16 floats s[8], c[8] of one per-dimension book (c = 0
+// centred, bias + 128 s affine).
+__global__ void k_u8_operands(const uint8_t* __restrict__ q, int n, int centered, const uint16_t* __restrict__ s16,
+                              const uint16_t* __restrict__ b16, uint8_t* __restrict__ u, float* __restrict__ sb) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) u[i] = static_cast<uint8_t>(q[i] ^ (centered ? 0x80u : 0u));
+    if (i < 8) {
+        const float sv = h2f(s16[i]);
+        sb[i] = sv;
+        sb[8 + i] = centered ? 0.0f : h2f(b16[i]) + 128.0f * sv;
+    }
+}
+
 // ============================================================== combine (R8, R10, R11)
 // One thread per (row, column): routed = T(sum_slot w_slot * T(d_slot)) in slot order,
 // shared = T(T(d_shared) * gate), y = T(routed + shared); chain mode adds the residual in
@@ -821,7 +1155,48 @@ hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStr
     return launch(k_down_mfma<BITS, NSUB, NCHUNK, PAR>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
 
+hipError_t launch_gu_u8(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    constexpr int NSUB = 256;
+    constexpr size_t lds = (size_t{1} << 14) * 8 + static_cast<size_t>(kU8Cols + 1) * (NSUB + 4) * 16;
+    if (L.H != 8 * NSUB || L.I % kMfmaRowsPerItem) return hipErrorInvalidValue;
+    if (const hipError_t e = ensure_lds<k_gu_u8<NSUB>>(lds); e != hipSuccess) return e;
+    return launch(k_gu_u8<NSUB>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
+}
+
+hipError_t launch_down_u8(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
+    constexpr size_t lds = (size_t{1} << 14) * 8;
+    if (L.I != 512 || L.H % kMfmaRowsPerItem) return hipErrorInvalidValue;
+    const int n_routes = M * L.K + (L.has_shared ? M : 0);
+    hipError_t e = launch(k_swiglu_u8, dim3((n_routes + 3) / 4), dim3(256), 0, st, L, B, n_routes);
+    if (e != hipSuccess) return e;
+    if ((e = ensure_lds<k_dn_u8<64>>(lds)) != hipSuccess) return e;
+    return launch(k_dn_u8<64>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
+}
+
+std::atomic<int> g_u8_native{1};
+
 } // namespace
+
+void set_u8_native(int mode) { g_u8_native.store(mode < 0 ? 0 : mode > 2 ? 2 : mode, std::memory_order_relaxed); }
+
+bool moe_u8_call(const LayerDev& L, int M) {
+    if (!L.u8_native || L.shared_affine || L.mixed || M < 1 || M > kMaxRows) return false;
+    const int mode = g_u8_native.load(std::memory_order_relaxed);
+    if (mode == 0) return false;
+    if (mode == 2 || M > 4) return true;
+    // 1-4 rows: the one-launch layer on the decoded book is faster wherever it is taken
+    LayerDev d = L;
+    d.fused_mode = 0;
+    return !moe_uses_fused(d, M);
+}
+
+hipError_t launch_u8_operands(const void* q, int K, int centered, const uint16_t* s16, const uint16_t* b16,
+                              uint8_t* u, float* sb, hipStream_t st) {
+    const int n = K * 8;
+    hipLaunchKernelGGL(k_u8_operands, dim3((n + 255) / 256), dim3(256), 0, st, static_cast<const uint8_t*>(q), n,
+                       centered, s16, b16, u, sb);
+    return hipGetLastError();
+}
 
 // Mixed layers run their two banks on the MFMA kernels: H = 2048, I = 512, per-row scales,
 // chunked fp16 codebooks prepared for both banks.
@@ -892,6 +1267,7 @@ hipError_t launch_gate_up(const LayerDev& L, const MoeBufs& B, int M, hipStream_
         if (e != hipSuccess) return e;
         return launch_gu_mfma_g<14, 256, 2, 1>(L, B, M, st);
     }
+    if (L.u8_call) return launch_gu_u8(L, B, M, st);
     if (moe_uses_fused(L, M)) return launch_gate_down4(L, B, M, nullptr, nullptr, st);
     if (moe_uses_narrow(L, M)) return launch_gate_up4(L, B, M, st);
     const int D = L.p[0].dim;
@@ -913,6 +1289,7 @@ hipError_t launch_down(const LayerDev& L, const MoeBufs& B, int M, hipStream_t s
         if (e != hipSuccess) return e;
         return launch_down_mfma_g<14, 64, 2, 1>(L, B, M, st);
     }
+    if (L.u8_call) return launch_down_u8(L, B, M, st);
     if (moe_uses_fused(L, M)) return hipSuccess;  // (the fused gate/up launch ran the down half)
     if (moe_uses_narrow(L, M)) return launch_down4(L, B, M, st);
     const int D = L.p[2].dim;

@@ -761,6 +761,13 @@ bool moe_uses_narrow(const LayerDev& L, int M) {
 
 LayerDev moe_call_dev(const LayerDev& L, int M) {
     LayerDev d = L;
+    d.u8_call = 0;
+    if (moe_u8_call(L, M)) {  // the U8 kernels: one plane each, no one-launch layer
+        d.u8_call = 1;
+        d.gu_parts = d.d_parts = 1;
+        d.fused_mode = 2;
+        return d;
+    }
     if (moe_uses_narrow(L, M)) {
         d.gu_parts = L.p[0].dim / 4;
         d.d_parts = L.p[2].dim / 4;

@@ -104,6 +104,7 @@ _sig("q38_ctx_create", C.c_int, C.c_int, C.POINTER(P))
 _sig("q38_ctx_destroy", None, P)
 _sig("q38_ctx_synchronize", C.c_int, P, P)
 _sig("q38_set_fused_layers", None, C.c_int)
+_sig("q38_set_u8_native", None, C.c_int)
 _sig("q38_debug_set_wait_limit", None, I32)
 _sig("q38_gdn_create", C.c_int, P, C.POINTER(GdnDesc), C.POINTER(GdnWeights), C.POINTER(P))
 _sig("q38_gdn_destroy", None, P)

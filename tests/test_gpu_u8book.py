@@ -1,7 +1,12 @@
 """Per-dimension INT8/U8 codebooks (R6, Q38_CB_U8_PERDIM) on the GPU: the tables the device
 derives at layer creation equal the oracle's restatement of SparseMoe::prepare_u8_codebook
 (src/sparse_moe.cpp:750-804) bit for bit, and layers using them match the oracle at verify
-widths (1, 4, 16 rows), prefill width and with per-64-input scale groups."""
+widths (1, 4, 16 rows), prefill width and with per-64-input scale groups.
+
+At 1-16 rows such layers run on the kernels that read the U8 books themselves (the reference's
+verify-width decode, src/vq_metal_kernels.hpp:564-579): checked against the oracle's float
+decode and against the decoded-fp16-book kernels (q38_set_u8_native(0)) on the same rows
+(mode 2 takes them at 1-4 rows too; the default takes them at 5-16)."""
 import ctypes as C
 
 import numpy as np
@@ -66,3 +71,39 @@ def test_book_format_validation(gpu, q38):
     assert q38.lib.q38_moe_layer_create_synthetic(gpu.h, C.byref(d), SEED, 0, C.byref(h)) == q38.Q38_EINVAL
     d = q38.desc(book_format=5)
     assert q38.lib.q38_moe_layer_create_synthetic(gpu.h, C.byref(d), SEED, 0, C.byref(h)) == q38.Q38_EINVAL
+
+
+@pytest.fixture
+def restore_u8_native(q38):
+    yield
+    q38.lib.q38_set_u8_native(1)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 9, 16])
+def test_u8_kernels_vs_decoded_book(u8layer, q38, orc, restore_u8_native, M):
+    """Routing identical on both paths; both within the MoE tolerance of the oracle's float
+    decode; the outputs differ (the U8 kernels' arithmetic, not the decoded book, ran)."""
+    x = orc.rmsnorm(orc.embed(SEED, [900 + 7 * i for i in range(M)], 2048))
+    q38.lib.q38_set_u8_native(2)
+    y1, ex1, wt1, lg1, plan1 = run_forward(q38, u8layer, u8layer.desc, x)
+    q38.lib.q38_set_u8_native(0)
+    y0, ex0, wt0, lg0, plan0 = run_forward(q38, u8layer, u8layer.desc, x)
+    wy, wex, wwt, wlg = orc.moe_layer_synth(oracle_lib.make_desc(book_format=2), SEED, 9, x)
+    assert np.array_equal(ex1, wex) and np.array_equal(wt1, wwt) and np.array_equal(plan1, plan0)
+    assert np.array_equal(ex0, wex) and np.array_equal(wt0, wwt)
+    r1 = tol_check(orc, y1, wy)
+    r0 = tol_check(orc, y0, wy)
+    print(f"M={M}: U8 kernels rel {r1[0]:.2e} max {r1[1]:.2e}; decoded book rel {r0[0]:.2e} max {r0[1]:.2e}")
+    assert not np.array_equal(y1, y0)
+
+
+def test_u8_kernels_repeat_and_width_change(u8layer, q38, orc, restore_u8_native):
+    """The same call twice gives the same bits; a 16-row call in between (other staging and
+    passes) leaves no state behind."""
+    q38.lib.q38_set_u8_native(2)
+    x4 = orc.rmsnorm(orc.embed(SEED, [11, 12, 13, 14], 2048))
+    x16 = orc.rmsnorm(orc.embed(SEED, list(range(500, 516)), 2048))
+    a = run_forward(q38, u8layer, u8layer.desc, x4)[0]
+    run_forward(q38, u8layer, u8layer.desc, x16)
+    b = run_forward(q38, u8layer, u8layer.desc, x4)[0]
+    assert np.array_equal(a, b)
