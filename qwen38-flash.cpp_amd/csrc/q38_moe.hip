@@ -390,10 +390,27 @@ __device__ __forceinline__ f4_t mfma_tile(const uint32_t* w, const uint2* book, 
     }
     return acc;
 }
+// Staged B rows: row r, lane quarter q (subvectors q S4 .. q S4 + S4 - 1, 8 bytes each) at
+// byte r * RB + q * QB. The strides are padded so that one B read of the MFMA loop (16
+// columns x 4 quarters, 16 bytes each) spreads over the LDS banks: with unpadded rows every
+// lane of it lands in the same 16-byte bank group. Row strides are 16 mod 256 bytes and
+// quarter strides 64 or 192 mod 256 (128 for 16-subvector quarters), so distinct rows and
+// quarters take distinct 16-byte slots of a 256-byte bank cycle, four lanes per slot.
+template <int NSUB>
+struct XsLayout {
+    static constexpr int S4 = NSUB / 4;
+    static constexpr int QB = S4 * 8 >= 256 ? S4 * 8 + 64 : S4 * 8;
+    static constexpr int RB = 4 * QB + 16;
+    __device__ static uint2* at(uint4* xs, int row, int sv) {
+        return reinterpret_cast<uint2*>(reinterpret_cast<unsigned char*>(xs) + row * RB + (sv / S4) * QB +
+                                        (sv % S4) * 8);
+    }
+};
 // B row base for lane (row xrow, block q) or the zero row when inactive.
 template <int NSUB>
 __device__ __forceinline__ const uint4* xs_lane(const uint4* xs, int xrow, int zero_row, int q, bool active) {
-    return xs + ((active ? xrow : zero_row) * NSUB + q * (NSUB / 4)) / 2;
+    return reinterpret_cast<const uint4*>(reinterpret_cast<const unsigned char*>(xs) +
+                                          (active ? xrow : zero_row) * XsLayout<NSUB>::RB + q * XsLayout<NSUB>::QB);
 }
 
 constexpr int kPlanSlots = kMaxRows * kMaxTopK + 1;  // unique-expert slots + the shared one
@@ -441,7 +458,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     constexpr int KENT = 1 << BITS;
     constexpr int MAXC = gu_mfma_cols(BITS);
     const uint2* book = reinterpret_cast<const uint2*>(lds);       // [KENT] x 4 fp16
-    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);          // [8 + 1 zero][NSUB][4] fp16
+    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);          // [MAXC + 1 zero] rows (XsLayout), 4 fp16 per subvector
     constexpr int TYPES = 2 * NCHUNK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
@@ -481,12 +498,12 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
     if (stage_all) {
         for (int i = tid; i < M * NSUB; i += kMfmaThreads) {
             const int row = i / NSUB, sv = i % NSUB;
-            reinterpret_cast<uint2*>(xs)[i] =
+            *XsLayout<NSUB>::at(xs, row, sv) =
                 *reinterpret_cast<const uint2*>(B.x16 + static_cast<size_t>(row) * H + sv * (4 * NCHUNK) + 4 * chunk);
         }
     }
     for (int i = tid; i < NSUB; i += kMfmaThreads)
-        reinterpret_cast<uint2*>(xs)[MAXC * NSUB + i] = make_uint2(0u, 0u);
+        *XsLayout<NSUB>::at(xs, MAXC, i) = make_uint2(0u, 0u);
     lds_barrier();
     auto code_src = [&](int item) {
         int expert, n, pos0;
@@ -514,7 +531,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
                 for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
                     const int jj = i / NSUB, sv = i % NSUB;
                     const int row = route_row(plan, M, K, pos0, j0 + jj, shared);
-                    reinterpret_cast<uint2*>(xs)[jj * NSUB + sv] = *reinterpret_cast<const uint2*>(
+                    *XsLayout<NSUB>::at(xs, jj, sv) = *reinterpret_cast<const uint2*>(
                         B.x16 + static_cast<size_t>(row) * H + sv * (4 * NCHUNK) + 4 * chunk);
                 }
                 lds_barrier();
@@ -545,7 +562,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
     __shared__ int32_t pslots[PAR < 0 ? 1 : kPlanSlots];
     constexpr int KENT = 1 << BITS;
     const uint2* book = reinterpret_cast<const uint2*>(lds);
-    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);   // [routes][NSUB][4] fp16 SwiGLU rows
+    uint4* xs = reinterpret_cast<uint4*>(lds + KENT * 8);   // [routes + 1 zero] SwiGLU rows (XsLayout), 4 fp16 each
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x8 = blockIdx.x & 7, kk = blockIdx.x >> 3;
     const int chunk = kk % NCHUNK;
@@ -572,12 +589,12 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
             }
             const uint32_t h0 = f2h(swiglu(gv.x, uv.x)), h1 = f2h(swiglu(gv.y, uv.y));
             const uint32_t h2 = f2h(swiglu(gv.z, uv.z)), h3 = f2h(swiglu(gv.w, uv.w));
-            reinterpret_cast<uint2*>(xs)[j * NSUB + sv] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+            *XsLayout<NSUB>::at(xs, j, sv) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
         }
     };
     if (stage_all) stage(0, n_routes);
     for (int i = tid; i < NSUB; i += kMfmaThreads)
-        reinterpret_cast<uint2*>(xs)[kDownStageRoutes * NSUB + i] = make_uint2(0u, 0u);
+        *XsLayout<NSUB>::at(xs, kDownStageRoutes, i) = make_uint2(0u, 0u);
     lds_barrier();
     float* dout = B.d + chunk * B.d_plane;
     const int nu = plan[0];
@@ -1144,13 +1161,13 @@ hipError_t launch_route_norm_h(const LayerDev& L, const MoeBufs& B, int M, const
 
 template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 hipError_t launch_gu_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(gu_mfma_cols(BITS) + 1) * NSUB * 8;
+    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(gu_mfma_cols(BITS) + 1) * XsLayout<NSUB>::RB;
     if (const hipError_t e = ensure_lds<k_gu_mfma<BITS, NSUB, NCHUNK, PAR>>(lds); e != hipSuccess) return e;
     return launch(k_gu_mfma<BITS, NSUB, NCHUNK, PAR>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
 template <int BITS, int NSUB, int NCHUNK, int PAR = -1>
 hipError_t launch_down_mfma_g(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kDownStageRoutes + 1) * NSUB * 8;
+    const size_t lds = (size_t{1} << BITS) * 8 + static_cast<size_t>(kDownStageRoutes + 1) * XsLayout<NSUB>::RB;
     if (const hipError_t e = ensure_lds<k_down_mfma<BITS, NSUB, NCHUNK, PAR>>(lds); e != hipSuccess) return e;
     return launch(k_down_mfma<BITS, NSUB, NCHUNK, PAR>, dim3(g_mfma_grid), dim3(kMfmaThreads), lds, st, L, B, M);
 }
