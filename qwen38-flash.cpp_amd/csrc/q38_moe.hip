@@ -512,10 +512,19 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
             static_cast<size_t>(bank_index<PAR>(expert)) * I + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
         return P.codes + rowi * P.words + q * WPL;
     };
+    // Mixed banks: a contiguous range of items, so that consecutive items mostly share a slot
+    // and its staged rows (restaged only when the slot or the pass changes). Uniform layers:
+    // items strided over the workgroups (the shared slot's 16 rows take two passes per tile,
+    // and a contiguous range would put all its tiles on one workgroup).
+    constexpr bool CONTIG = PAR >= 0;
+    const int i0 = CONTIG ? static_cast<int>(static_cast<int64_t>(idx) * n_items / per_type) : idx;
+    const int i1 = CONTIG ? static_cast<int>(static_cast<int64_t>(idx + 1) * n_items / per_type) : n_items;
+    const int istep = CONTIG ? 1 : per_type;
+    int staged_slot = -1, staged_j0 = -1;
     uint32_t w[WPL + 1], wn[WPL + 1];
-    if (idx < n_items) load_lane_words<BITS, NSUB>(code_src(idx), w);
-    for (int item = idx; item < n_items; item += per_type) {
-        if (item + per_type < n_items) load_lane_words<BITS, NSUB>(code_src(item + per_type), wn);
+    if (i0 < i1) load_lane_words<BITS, NSUB>(code_src(i0), w);
+    for (int item = i0; item < i1; item += istep) {
+        if (item + istep < i1) load_lane_words<BITS, NSUB>(code_src(item + istep), wn);
         const int ui = slot_of(item), tile = item % tiles;
         int expert, n, pos0;
         slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
@@ -526,7 +535,9 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_mfma(LayerDev L, MoeBufs B,
             int xrow = r16;
             if (stage_all) {
                 if (r16 < nj) xrow = route_row(plan, M, K, pos0, j0 + r16, shared);
-            } else {
+            } else if (ui != staged_slot || j0 != staged_j0) {
+                staged_slot = ui;
+                staged_j0 = j0;
                 lds_barrier();
                 for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
                     const int jj = i / NSUB, sv = i % NSUB;
@@ -612,23 +623,35 @@ __global__ __launch_bounds__(kMfmaThreads) void k_down_mfma(LayerDev L, MoeBufs 
             static_cast<size_t>(bank_index<PAR>(expert)) * H + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
         return P.codes + rowi * P.words + q * WPL;
     };
+    // a contiguous range of items (see k_gu_mfma): a slot's routes (all of them when they fit
+    // the staging rows) are staged once for its consecutive items
+    const int i0 = static_cast<int>(static_cast<int64_t>(idx) * n_items / per_type);
+    const int i1 = static_cast<int>(static_cast<int64_t>(idx + 1) * n_items / per_type);
+    int staged_slot = -1, staged_j0 = -1;
     uint32_t w[WPL + 1], wn[WPL + 1];
-    if (idx < n_items) load_lane_words<BITS, NSUB>(code_src(idx), w);
-    for (int item = idx; item < n_items; item += per_type) {
-        if (item + per_type < n_items) load_lane_words<BITS, NSUB>(code_src(item + per_type), wn);
+    if (i0 < i1) load_lane_words<BITS, NSUB>(code_src(i0), w);
+    for (int item = i0; item < i1; ++item) {
+        if (item + 1 < i1) load_lane_words<BITS, NSUB>(code_src(item + 1), wn);
         const int ui = slot_of(item), tile = item % tiles;
         int expert, n, pos0;
         slot_rows(plan, M, K, L.has_shared, ui, L.E, &expert, &n, &pos0);
         const int o0 = tile * kMfmaRowsPerItem + wave * 16;
+        const bool whole = n <= kDownStageRoutes;  // (always at verify widths: n <= 16)
         for (int j0 = 0; j0 < n; j0 += kMfmaMaxCols) {
             const int nj = n - j0 < kMfmaMaxCols ? n - j0 : kMfmaMaxCols;
             int xrow = r16;
             if (stage_all) {
                 xrow = pos0 + j0 + r16;
             } else {
-                lds_barrier();
-                stage(pos0 + j0, nj);
-                lds_barrier();
+                const int sj0 = whole ? 0 : j0;
+                if (ui != staged_slot || sj0 != staged_j0) {
+                    staged_slot = ui;
+                    staged_j0 = sj0;
+                    lds_barrier();
+                    stage(pos0 + sj0, whole ? n : nj);
+                    lds_barrier();
+                }
+                xrow = j0 - sj0 + r16;
             }
             const f4_t acc = mfma_tile<BITS, NSUB>(w, book, xs_lane<NSUB>(xs, xrow, kDownStageRoutes, q, r16 < nj));
             if (r16 < nj) {
@@ -818,6 +841,9 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_u8(LayerDev L, MoeBufs B, i
         const size_t rowi = static_cast<size_t>(expert) * I + (item % tiles) * kMfmaRowsPerItem + wave * 16 + r16;
         return P.codes + rowi * P.words + q * WPL;
     };
+    // items strided over the workgroups (as k_gu_mfma's uniform layers); wider calls restage
+    // x' only when the slot or the pass changes
+    int staged_slot = -1, staged_j0 = -1;
     uint32_t w[WPL + 1], wn[WPL + 1];
     if (idx < n_items) load_lane_words<14, NSUB>(code_src(idx), w);
     wait_vm_all_moe();  // (the book copy of waves 0-3)
@@ -833,7 +859,9 @@ __global__ __launch_bounds__(kMfmaThreads) void k_gu_u8(LayerDev L, MoeBufs B, i
             const int nj = n - j0 < kU8Cols ? n - j0 : kU8Cols;
             const int crow = r16 < nj ? route_row(plan, M, K, pos0, j0 + r16, shared) : 0;
             const int xrow = stage_all ? crow : r16;
-            if (!stage_all) {
+            if (!stage_all && (ui != staged_slot || j0 != staged_j0)) {
+                staged_slot = ui;
+                staged_j0 = j0;
                 lds_barrier();
                 for (int i = tid; i < nj * NSUB; i += kMfmaThreads) {
                     const int jj = i / NSUB, sv = i % NSUB;
