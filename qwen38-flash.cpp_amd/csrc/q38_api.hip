@@ -1502,6 +1502,8 @@ struct MtpWork {
     uint16_t *x, *f;
     float *pe, *ph, *logits;
     unsigned long long* best;
+    unsigned long long* part;  // the Q4 draft head's partial argmax keys [rows][nparts]
+    int nparts;
     uint32_t* tokens;
     HeadWork we, wh[4];  // the FC projections' prepared rows (the stream projection in passes)
     int mh[4], passes;
@@ -1527,6 +1529,8 @@ size_t mtp_layout(const q38_mtp_head* m, int rows, MtpWork* w, void* base) {
     t.ph = reinterpret_cast<float*>(take(rows * HC * H * 4));
     t.logits = reinterpret_cast<float*>(take(rows * V * 4));
     t.best = reinterpret_cast<unsigned long long*>(take(rows * 8));
+    t.part = reinterpret_cast<unsigned long long*>(take(static_cast<size_t>(rows) * kQ4MaxBlocks * 8));
+    t.nparts = b ? q4_blocks(rows) : 0;
     t.tokens = reinterpret_cast<uint32_t*>(take(rows * 4));
     t.we = head_work_carve(take(head_work_bytes(m->fc_e->dev, rows, false)), m->fc_e->dev, rows, false);
     const int nrows = rows * m->streams;  // the stream projection's rows, in passes of up to 16
@@ -1566,12 +1570,16 @@ int mtp_validate(q38_moe_layer* layer, q38_head* fe, q38_head* fh, q38_head* dh)
 // tokens: the step's tokens, or null in a chain: the previous step's argmax keys in w.best,
 // whose tokens the prologue also records as drafts[., prev_step].
 int mtp_step(q38_mtp_head* m, const MtpWork& w, const uint16_t* stream_in, const uint32_t* tokens, uint32_t* drafts,
-             int depth, int prev_step, int rows, float* logits, const q38_mtp_trace* trace, hipStream_t st) {
+             int depth, int prev_step, int rows, float* logits, const q38_mtp_trace* trace, hipStream_t st,
+             bool argmax = false) {
     const int H = m->layer->desc.hidden, HC = m->streams;
     DraftPro P{};
     P.embed_key = stream_key(m->embed_seed, kEmbedLayer, T_EMBED);
     P.toks = tokens;
     P.best = w.best;
+    // (a chain step after the first takes its token from the previous Q4 head's partial keys)
+    P.part = m->draft->dev.kind != Q38_HEAD_Q8 ? w.part : nullptr;
+    P.nparts = w.nparts;
     P.drafts = drafts;
     P.tokens_out = w.tokens;
     P.depth = depth;
@@ -1609,6 +1617,11 @@ int mtp_step(q38_mtp_head* m, const MtpWork& w, const uint16_t* stream_in, const
     if (trace && trace->final_mixed)
         Q38_HIP(hipMemcpyAsync(trace->final_mixed, w.f, static_cast<size_t>(rows) * H * 2, hipMemcpyDeviceToDevice,
                                st));
+    // (argmax: a Q4 draft head also forms its workgroups' argmax keys in w.part)
+    if (argmax && m->draft->dev.kind != Q38_HEAD_Q8) {
+        Q38_HIP(launch_head_q4_part(m->draft->dev, w.f, rows, logits, w.part, st));
+        return Q38_OK;
+    }
     return q38_head_logits(m->draft, w.f, rows, logits, nullptr, 0, st);
 }
 } // namespace
@@ -1751,14 +1764,19 @@ int q38_mtp_draft_greedy(q38_mtp_head* m, const uint16_t* stream_in, const uint3
     for (int step = 0; step < depth; ++step) {
         // the step's join clears w.best; its argmax keys feed the next step's prologue (which
         // records this step's drafts), the last step's are finished here
+        const bool fused = m->draft->dev.kind != Q38_HEAD_Q8;  // (the Q4 head merges the keys itself)
         if (int rc = mtp_step(m, w, s_in, step == 0 ? t_in : nullptr, drafts, depth, step - 1, rows, w.logits, nullptr,
-                              st))
+                              st, true))
             return rc;
-        if (step + 1 == depth)
-            Q38_HIP(launch_argmax(w.logits, rows, m->draft->dev.V, w.best, false, w.tokens, nullptr, drafts, depth,
-                                  step, st));
-        else
+        if (step + 1 == depth) {
+            if (fused)
+                Q38_HIP(launch_argmax_part_final(w.part, w.nparts, rows, w.tokens, nullptr, drafts, depth, step, st));
+            else
+                Q38_HIP(launch_argmax(w.logits, rows, m->draft->dev.V, w.best, false, w.tokens, nullptr, drafts,
+                                      depth, step, st));
+        } else if (!fused) {
             Q38_HIP(launch_argmax_rows(w.logits, rows, m->draft->dev.V, w.best, st));
+        }
         s_in = w.x;
     }
     if (stream_out)

@@ -309,9 +309,12 @@ __device__ __forceinline__ void reduce_scatter(float (&part)[NP]) {
     }
 }
 
+// part (or null): also each workgroup's argmax key per row, orderable(logit) << 32 | ~index
+// as k_argmax_rows forms them (0: none), at part[r * gridDim.x + block]; the consumer takes
+// the maximum (no atomics: one address per row would serialise the grid's waves).
 template <int M>
 __global__ __launch_bounds__(256) void k_head_q4(HeadDev hd, const uint16_t* __restrict__ h,
-                                                 float* __restrict__ out_logits) {
+                                                 float* __restrict__ out_logits, unsigned long long* __restrict__ part) {
     constexpr int CPL = 32, RPS = 8;            // columns per lane, rows per step
     constexpr int N = RPS * M;                  // partials per lane per step
     constexpr int NP = N <= 8 ? 8 : N <= 16 ? 16 : 32;  // padded to a power of two
@@ -351,6 +354,7 @@ __global__ __launch_bounds__(256) void k_head_q4(HeadDev hd, const uint16_t* __r
         }
     };
     int64_t base = gw * RPS;
+    uint64_t kbest = 0;  // this lane's best key (its values all belong to one row)
     if (base < V) load(base, wq, sq);
     for (; base < V; base += nw * RPS) {
         if (base + nw * RPS < V) load(base + nw * RPS, wn, sn);
@@ -392,7 +396,12 @@ __global__ __launch_bounds__(256) void k_head_q4(HeadDev hd, const uint16_t* __r
         const int lsb = 64 / NP;  // lanes sharing an index: the low log2(64 / NP) lane bits
         if ((lane & (lsb - 1)) == 0 && idx < N) {
             const int j = idx / M, r = idx % M;
-            if (base + j < V) out_logits[static_cast<size_t>(r) * V + base + j] = part[0];
+            if (base + j < V) {
+                out_logits[static_cast<size_t>(r) * V + base + j] = part[0];
+                const uint64_t k = (static_cast<uint64_t>(orderable(part[0])) << 32) |
+                                   (0xFFFFFFFFu - static_cast<uint32_t>(base + j));
+                kbest = k > kbest ? k : kbest;
+            }
         }
 #pragma unroll
         for (int j = 0; j < RPS; ++j) {
@@ -400,6 +409,54 @@ __global__ __launch_bounds__(256) void k_head_q4(HeadDev hd, const uint16_t* __r
             sq[j] = sn[j];
         }
     }
+    if (part) {
+        __shared__ uint64_t wk[4][M];
+        int idx = 0;
+        {
+            int bitv = NP / 2;
+            for (int o = 32; bitv >= 1; o >>= 1, bitv >>= 1)
+                if (lane & o) idx += bitv;
+        }
+#pragma unroll
+        for (int r = 0; r < M; ++r) {
+            const uint64_t k = wave_max_u64(idx % M == r ? kbest : 0);
+            if (lane == 0) wk[threadIdx.x >> 6][r] = k;
+        }
+        __syncthreads();
+        if (threadIdx.x < M) {
+            const int r = threadIdx.x;
+            uint64_t k = wk[0][r];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) k = wk[w][r] > k ? wk[w][r] : k;
+            part[static_cast<size_t>(r) * gridDim.x + blockIdx.x] = k;
+        }
+    }
+}
+
+// The maximum of n partial keys (block-wide; every thread gets it).
+__device__ __forceinline__ uint64_t max_keys(const unsigned long long* p, int n) {
+    __shared__ uint64_t wk[4];
+    uint64_t k = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) k = p[i] > k ? p[i] : k;
+    k = wave_max_u64(k);
+    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = k;
+    __syncthreads();
+    k = wk[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) k = wk[w] > k ? wk[w] : k;
+    return k;
+}
+
+// Row r's key from the Q4 head's partials, decoded as k_argmax_final does.
+__global__ __launch_bounds__(256) void k_argmax_part_final(const unsigned long long* __restrict__ part, int n,
+                                                           uint32_t* __restrict__ tokens, float* __restrict__ values,
+                                                           uint32_t* __restrict__ drafts, int depth, int step) {
+    const int r = blockIdx.x;
+    const uint64_t b = max_keys(part + static_cast<size_t>(r) * n, n);
+    if (threadIdx.x != 0) return;
+    const uint32_t t = 0xFFFFFFFFu - static_cast<uint32_t>(b);
+    if (tokens) tokens[r] = t;
+    if (values) values[r] = from_orderable(static_cast<uint32_t>(b >> 32));
+    if (drafts) drafts[static_cast<size_t>(r) * depth + step] = t;
 }
 
 __global__ void k_gen_head(HeadDev hd, uint64_t wkey, uint64_t skey, int8_t* __restrict__ w,
@@ -739,11 +796,12 @@ hipError_t launch_i8(const HeadDev& hd, int M, const HeadWork& w, float* out, hi
     }
 }
 template <int M>
-hipError_t launch_q4_m(const HeadDev& hd, const uint16_t* h, float* out, hipStream_t st) {
+hipError_t launch_q4_m(const HeadDev& hd, const uint16_t* h, float* out, hipStream_t st,
+                       unsigned long long* part = nullptr) {
     // one resident wave per SIMD slot (the kernel holds 4 waves per SIMD at M = 1, 3 at M = 2
     // and 3, 2 at M = 4): every wave streams
     // many 8-row steps, so its prologue (M rows of h) is paid once per ~9 steps
-    return launch(k_head_q4<M>, dim3(cu_count() * (M == 1 ? 4 : M == 4 ? 2 : 3)), dim3(256), 0, st, hd, h, out);
+    return launch(k_head_q4<M>, dim3(q4_blocks(M)), dim3(256), 0, st, hd, h, out, part);
 }
 } // namespace
 
@@ -772,6 +830,23 @@ hipError_t launch_head_logits(const HeadDev& hd, const uint16_t* h, int M, const
         case 2: return launch_q4_m<2>(hd, h, logits, st);
         case 3: return launch_q4_m<3>(hd, h, logits, st);
         case 4: return launch_q4_m<4>(hd, h, logits, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+int q4_blocks(int M) {
+    const int n = cu_count() * (M == 1 ? 4 : M == 4 ? 2 : 3);
+    return n < kQ4MaxBlocks ? n : kQ4MaxBlocks;
+}
+
+hipError_t launch_head_q4_part(const HeadDev& hd, const uint16_t* h, int M, float* logits, unsigned long long* part,
+                               hipStream_t st) {
+    if (hd.kind == 0 || hd.H != 2048) return hipErrorInvalidValue;
+    switch (M) {
+        case 1: return launch_q4_m<1>(hd, h, logits, st, part);
+        case 2: return launch_q4_m<2>(hd, h, logits, st, part);
+        case 3: return launch_q4_m<3>(hd, h, logits, st, part);
+        case 4: return launch_q4_m<4>(hd, h, logits, st, part);
         default: return hipErrorInvalidValue;
     }
 }
@@ -855,6 +930,12 @@ hipError_t launch_argmax_rows(const float* logits, int M, int64_t V, unsigned lo
     return launch(k_argmax_rows, dim3(static_cast<unsigned>(blocks), M), dim3(256), 0, st, logits, V, best);
 }
 
+hipError_t launch_argmax_part_final(const unsigned long long* part, int n, int M, uint32_t* tokens, float* values,
+                                    uint32_t* drafts, int depth, int step, hipStream_t st) {
+    if (M < 1 || M > 64 || n < 1) return hipErrorInvalidValue;
+    return launch(k_argmax_part_final, dim3(M), dim3(256), 0, st, part, n, tokens, values, drafts, depth, step);
+}
+
 hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long long* best, bool clear,
                          uint32_t* tokens, float* values, uint32_t* drafts, int depth, int step, hipStream_t st) {
     if (M < 1 || M > 64 || V < 1) return hipErrorInvalidValue;
@@ -869,14 +950,17 @@ hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long lo
 }
 
 // The draft step's inputs of its two FC projections in one launch (the embedding, the two
-// RMSNorms and the Q8 planes of both projections' rows): workgroup (r, 0) forms request r's
-// embedding row (token toks[r], or, in a chain, the previous step's argmax best[r], whose
-// token it also records), (r, 1) loads its stream row; each RMS-normalises its row (H or
-// HC * H values in k_rmsnorm's order, with the offset weight when given) in LDS and prepares
-// the Q8 planes of the resulting head rows: the embedding row as row r of we, the stream's HC
-// rows as the rows g = r HC + s of the stream projection's passes (pass g / 16, row g % 16).
+// RMSNorms and the Q8 planes of both projections' rows), one workgroup per projection row:
+// (r, 0) forms request r's embedding row (token toks[r], or, in a chain, the previous step's
+// argmax best[r], whose token it also records); (r, 1 + s) takes stream s of request r. Each
+// RMS-normalises its row in k_rmsnorm's order (thread t sums the squares of values t, t + 256,
+// ... of the whole H or HC * H row in order, then the wave and workgroup sums), the stream
+// workgroups each over the whole stream row (read again from L2) but normalising only their
+// own H values, with the offset weight when given, and prepares the Q8 planes of that row:
+// the embedding row as row r of we, stream s as row g = r HC + s of the stream projection's
+// passes (pass g / 16, row g % 16).
 __global__ __launch_bounds__(256) void k_draft_prologue(DraftPro P) {
-    extern __shared__ __align__(16) uint16_t row[];  // [HC * H] bf16
+    extern __shared__ __align__(16) uint16_t row[];  // [H] bf16
     __shared__ float red[4];
     const int r = blockIdx.x, which = blockIdx.y, tid = threadIdx.x;
     const int H = P.H, W = which ? P.HC * H : H;
@@ -886,7 +970,8 @@ __global__ __launch_bounds__(256) void k_draft_prologue(DraftPro P) {
         if (P.toks) {
             t = P.toks[r];
         } else {
-            t = 0xFFFFFFFFu - static_cast<uint32_t>(P.best[r]);
+            const uint64_t b = P.part ? max_keys(P.part + static_cast<size_t>(r) * P.nparts, P.nparts) : P.best[r];
+            t = 0xFFFFFFFFu - static_cast<uint32_t>(b);
             if (tid == 0) {
                 if (P.tokens_out) P.tokens_out[r] = t;
                 if (P.drafts) P.drafts[static_cast<size_t>(r) * P.depth + P.prev_step] = t;
@@ -899,11 +984,26 @@ __global__ __launch_bounds__(256) void k_draft_prologue(DraftPro P) {
             row[c] = e;
         }
     } else {
-        for (int c = tid; c < W; c += 256) {
-            const uint16_t e = P.stream[static_cast<size_t>(r) * W + c];
-            const float v = bf2f(e);
-            ss = fmaf(v, v, ss);
-            row[c] = e;
+        // the whole stream row, 16 values per thread in flight, summed in order
+        const int s0 = (which - 1) * H;
+        const uint16_t* src = P.stream + static_cast<size_t>(r) * W;
+        constexpr int B16 = 16;
+        for (int c0 = 0; c0 < W; c0 += 256 * B16) {
+            uint16_t e[B16];
+#pragma unroll
+            for (int k = 0; k < B16; ++k) {
+                const int c = c0 + tid + 256 * k;
+                e[k] = c < W ? src[c] : 0;
+            }
+#pragma unroll
+            for (int k = 0; k < B16; ++k) {
+                const int c = c0 + tid + 256 * k;
+                if (c < W) {
+                    const float v = bf2f(e[k]);
+                    ss = fmaf(v, v, ss);
+                    if (c >= s0 && c < s0 + H) row[c - s0] = e[k];
+                }
+            }
         }
     }
     ss = wave_sum_xor(ss);
@@ -911,26 +1011,24 @@ __global__ __launch_bounds__(256) void k_draft_prologue(DraftPro P) {
     __syncthreads();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.0f / sqrtf(tot / static_cast<float>(W) + P.eps);
-    const uint16_t* wn = which ? P.hid_norm : P.emb_norm;
-    for (int c = tid; c < W; c += 256) {
+    const uint16_t* wn = which ? P.hid_norm + (which - 1) * H : P.emb_norm;
+    for (int c = tid; c < H; c += 256) {
         const float n = rbf(bf2f(row[c]) * inv);
-        row[c] = f2bf(wn ? n * bf2f(wn[c]) : n);
+        row[c] = f2bf((which ? P.hid_norm : P.emb_norm) ? n * bf2f(wn[c]) : n);
     }
     __syncthreads();
     if (which == 0) {
         head_prep_row(row, H, P.M, r, P.we);
     } else {
-        for (int sidx = 0; sidx < P.HC; ++sidx) {
-            const int g = r * P.HC + sidx, pass = g / kHeadMaxRows;
-            head_prep_row(row + static_cast<size_t>(sidx) * H, H, P.mh[pass], g % kHeadMaxRows, P.wh[pass]);
-        }
+        const int g = r * P.HC + which - 1, pass = g / kHeadMaxRows;
+        head_prep_row(row, H, P.mh[pass], g % kHeadMaxRows, P.wh[pass]);
     }
 }
 
 hipError_t launch_draft_prologue(const DraftPro& P, hipStream_t st) {
-    const size_t lds = static_cast<size_t>(P.HC) * P.H * 2;
+    const size_t lds = static_cast<size_t>(P.H) * 2;
     if (const hipError_t e = ensure_lds<k_draft_prologue>(lds); e != hipSuccess) return e;
-    return launch(k_draft_prologue, dim3(P.M, 2), dim3(256), lds, st, P);
+    return launch(k_draft_prologue, dim3(P.M, 1 + P.HC), dim3(256), lds, st, P);
 }
 
 hipError_t launch_head_logits_prepared(const HeadDev& hd, int M, const HeadWork& w, float* logits, hipStream_t st) {

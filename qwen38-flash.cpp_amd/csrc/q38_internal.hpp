@@ -371,6 +371,8 @@ struct DraftPro {
     uint64_t embed_key;
     const uint32_t* toks;               // step tokens, or null: take them from best
     const unsigned long long* best;     // the previous step's argmax keys
+    const unsigned long long* part;     // or (non-null) its Q4 head's partial keys [M][nparts]
+    int nparts;
     uint32_t* drafts;                   // (chain) the previous step's drafts [M][depth]
     uint32_t* tokens_out;
     int depth, prev_step;
@@ -385,6 +387,15 @@ struct DraftPro {
 };
 hipError_t launch_draft_prologue(const DraftPro& P, hipStream_t st);
 hipError_t launch_argmax_rows(const float* logits, int M, int64_t V, unsigned long long* best, hipStream_t st);
+// The Q4 head's logits with each workgroup's argmax key per row in part ([M][q4_blocks(M)]
+// u64), and the decode of row r's maximum of such keys into tokens / values /
+// drafts[r * depth + step] (each may be null).
+constexpr int kQ4MaxBlocks = 2048;
+int q4_blocks(int M);
+hipError_t launch_head_q4_part(const HeadDev& hd, const uint16_t* h, int M, float* logits, unsigned long long* part,
+                               hipStream_t st);
+hipError_t launch_argmax_part_final(const unsigned long long* part, int n, int M, uint32_t* tokens, float* values,
+                                    uint32_t* drafts, int depth, int step, hipStream_t st);
 hipError_t launch_head_logits_prepared(const HeadDev& hd, int M, const HeadWork& w, float* logits, hipStream_t st);
 size_t head_work_bytes(const HeadDev& hd, int M, bool greedy);
 HeadWork head_work_carve(void* base, const HeadDev& hd, int M, bool greedy);
