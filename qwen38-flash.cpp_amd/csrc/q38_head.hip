@@ -60,15 +60,17 @@ HeadWork head_work_carve(void* base, const HeadDev& hd, int M, bool greedy) {
 // The int8 planes of one request row hr (H values, global or LDS), its plane scale, the
 // residual R and sum|h| (double, fixed order), and the reset of the pass state for row r of
 // an M-row call (kernel stores, no memset nodes, so the sequence can be captured in a graph).
-// Called by all 256 threads of a workgroup; may be called repeatedly in one workgroup.
+// Called by every thread of a workgroup of 256 or more (threads past 256 take no part but
+// the barriers); may be called repeatedly in one workgroup.
 __device__ void head_prep_row(const uint16_t* hr, int H, int M, int r, const HeadWork& w) {
     __shared__ float redm[4];
     __shared__ double redt[4], redr[4];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int cend = tid < 256 ? H : 0;
     float m = 0.0f;
-    for (int c = tid; c < H; c += 256) m = fmaxf(m, fabsf(bf2f(hr[c])));
+    for (int c = tid; c < cend; c += 256) m = fmaxf(m, fabsf(bf2f(hr[c])));
     m = wave_max(m);
-    if (lane == 0) redm[wv] = m;
+    if (lane == 0 && wv < 4) redm[wv] = m;
     __syncthreads();
     m = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
     int e = 0;
@@ -76,7 +78,7 @@ __device__ void head_prep_row(const uint16_t* hr, int H, int M, int r, const Hea
     const float s = m > 0.0f ? ldexpf(1.0f, e - 6) : 1.0f;
     const double sd = s;
     double tsum = 0.0, res = 0.0;
-    for (int c = tid; c < H; c += 256) {
+    for (int c = tid; c < cend; c += 256) {
         const double x = bf2f(hr[c]);
         const double y = x / sd;                  // exact: power-of-two scale, |y| < 64
         const double a = rint(y);
@@ -92,7 +94,7 @@ __device__ void head_prep_row(const uint16_t* hr, int H, int M, int r, const Hea
     }
     tsum = wave_sum_xor(tsum);
     res = wave_sum_xor(res);
-    if (lane == 0) { redt[wv] = tsum; redr[wv] = res; }
+    if (lane == 0 && wv < 4) { redt[wv] = tsum; redr[wv] = res; }
     __syncthreads();
     if (tid == 0) {
         // rounded up so that the window bound stays an upper bound
@@ -435,7 +437,7 @@ __global__ __launch_bounds__(256) void k_head_q4(HeadDev hd, const uint16_t* __r
 
 // The maximum of n partial keys (block-wide; every thread gets it).
 __device__ __forceinline__ uint64_t max_keys(const unsigned long long* p, int n) {
-    __shared__ uint64_t wk[4];
+    __shared__ uint64_t wk[16];  // (up to 1024 threads)
     uint64_t k = 0;
     for (int i = threadIdx.x; i < n; i += blockDim.x) k = p[i] > k ? p[i] : k;
     k = wave_max_u64(k);
@@ -959,13 +961,14 @@ hipError_t launch_argmax(const float* logits, int M, int64_t V, unsigned long lo
 // own H values, with the offset weight when given, and prepares the Q8 planes of that row:
 // the embedding row as row r of we, stream s as row g = r HC + s of the stream projection's
 // passes (pass g / 16, row g % 16).
-__global__ __launch_bounds__(256) void k_draft_prologue(DraftPro P) {
+__global__ __launch_bounds__(1024) void k_draft_prologue(DraftPro P) {
     extern __shared__ __align__(16) uint16_t row[];  // [H] bf16
     __shared__ float red[4];
     const int r = blockIdx.x, which = blockIdx.y, tid = threadIdx.x;
     const int H = P.H, W = which ? P.HC * H : H;
     float ss = 0.0f;
     if (which == 0) {
+        // (the 1024 threads generate the row; its sums stay on the first 256 in k_rmsnorm's order)
         uint32_t t;
         if (P.toks) {
             t = P.toks[r];
@@ -977,13 +980,15 @@ __global__ __launch_bounds__(256) void k_draft_prologue(DraftPro P) {
                 if (P.drafts) P.drafts[static_cast<size_t>(r) * P.depth + P.prev_step] = t;
             }
         }
-        for (int c = tid; c < W; c += 256) {
-            const uint16_t e = f2bf(static_cast<float>(normal_at(P.embed_key, static_cast<uint64_t>(t) * H + c)));
-            const float v = bf2f(e);
-            ss = fmaf(v, v, ss);
-            row[c] = e;
-        }
-    } else {
+        for (int c = tid; c < H; c += 1024)
+            row[c] = f2bf(static_cast<float>(normal_at(P.embed_key, static_cast<uint64_t>(t) * H + c)));
+        __syncthreads();
+        if (tid < 256)
+            for (int c = tid; c < W; c += 256) {
+                const float v = bf2f(row[c]);
+                ss = fmaf(v, v, ss);
+            }
+    } else if (tid < 256) {
         // the whole stream row, 16 values per thread in flight, summed in order
         const int s0 = (which - 1) * H;
         const uint16_t* src = P.stream + static_cast<size_t>(r) * W;
@@ -1007,12 +1012,12 @@ __global__ __launch_bounds__(256) void k_draft_prologue(DraftPro P) {
         }
     }
     ss = wave_sum_xor(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    if ((tid & 63) == 0 && tid < 256) red[tid >> 6] = ss;
     __syncthreads();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.0f / sqrtf(tot / static_cast<float>(W) + P.eps);
     const uint16_t* wn = which ? P.hid_norm + (which - 1) * H : P.emb_norm;
-    for (int c = tid; c < H; c += 256) {
+    for (int c = tid; c < H; c += 1024) {
         const float n = rbf(bf2f(row[c]) * inv);
         row[c] = f2bf((which ? P.hid_norm : P.emb_norm) ? n * bf2f(wn[c]) : n);
     }
@@ -1028,7 +1033,7 @@ __global__ __launch_bounds__(256) void k_draft_prologue(DraftPro P) {
 hipError_t launch_draft_prologue(const DraftPro& P, hipStream_t st) {
     const size_t lds = static_cast<size_t>(P.H) * 2;
     if (const hipError_t e = ensure_lds<k_draft_prologue>(lds); e != hipSuccess) return e;
-    return launch(k_draft_prologue, dim3(P.M, 1 + P.HC), dim3(256), lds, st, P);
+    return launch(k_draft_prologue, dim3(P.M, 1 + P.HC), dim3(1024), lds, st, P);
 }
 
 hipError_t launch_head_logits_prepared(const HeadDev& hd, int M, const HeadWork& w, float* logits, hipStream_t st) {
