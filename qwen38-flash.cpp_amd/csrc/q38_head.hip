@@ -210,7 +210,13 @@ void k_head_i8(HeadDev hd, int M, HeadWork w, float* __restrict__ out_logits) {
         }
         buf ^= 1;  // the other buffer is free: its readers passed this iteration's barrier
     }
-    if (wave == 0 && jact && !out_logits) atomicMax(&w.rowmax[i16], orderable(mx));
+    if (!out_logits) {
+        // one atomic per request row and group: the four lanes of a row (q) merged first
+        // (same-address atomics from every lane of the grid serialise at the kernel's end)
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if (wave == 0 && jact && q == 0) atomicMax(&w.rowmax[i16], orderable(mx));
+    }
 }
 
 // Window: fast >= max - 2E with E = 2 * s_max * 128 * (R + 2^-22 (sum|h| + R)), twice the
