@@ -122,8 +122,9 @@ def chain_only(args, q38, torch, ctx, layers, larr, ws):
     """Profiling driver: the MoE chain alone at M = args.chain_only rows (the layer kernels a
     counter run collects), args.warmup untimed and args.steps event-timed passes, eager launches."""
     M = args.chain_only
-    assert 1 <= M <= 4, "--chain-only takes 1..4 rows"
+    assert 1 <= M <= 16, "--chain-only takes 1..16 rows"
     sp = torch.cuda.current_stream().cuda_stream
+    ws = torch.empty(q38.lib.q38_moe_workspace_size(C.byref(layers[0].desc), M), dtype=torch.uint8, device="cuda")
     h = torch.empty((M, H), dtype=torch.int16, device="cuda")
     toks = (C.c_uint32 * M)(*[11 + 7 * r for r in range(M)])
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -166,6 +167,8 @@ def main():
                     help="profiling driver: only the 48-layer MoE chain at M rows, --steps times, then exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (reference kernel for HBM counter calibration)")
+    ap.add_argument("--u8-books", type=int, default=-1, metavar="MODE",
+                    help="with --chain-only: layers with per-dimension INT8/U8 books, q38_set_u8_native(MODE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it "
@@ -182,6 +185,9 @@ def main():
 
     ctx = q38.Ctx(0)
     d = q38.desc()
+    if args.chain_only and args.u8_books >= 0:
+        d = q38.desc(book_format=q38.Q38_CB_U8_PERDIM)
+        q38.lib.q38_set_u8_native(args.u8_books)
     log("generating 48 synthetic layers + Q8 head")
     layers = [q38.MoeLayer(ctx, d, seed=SEED, layer=l) for l in range(args.layers)]
     larr = (C.c_void_p * len(layers))(*[L.h.value for L in layers])
