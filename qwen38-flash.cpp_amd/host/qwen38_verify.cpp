@@ -474,6 +474,54 @@ DeviceTensor HyperConnection::write(const DeviceTensor& stream, const DeviceTens
     return out;
 }
 
+// ------------------------------------------------------------------ DecoderLayer (verify)
+DecoderLayer::DecoderLayer(const HyperConnection& attention_mixer, const GatedDeltaNet& linear_attention,
+                           const HyperConnection& mlp_mixer, const SparseMoe& mlp, const q38_mlp_map* output_map)
+    : attention_mixer_(&attention_mixer), linear_(&linear_attention), mlp_mixer_(&mlp_mixer), mlp_(&mlp),
+      map_(output_map) {}
+
+DecoderLayer::DecoderLayer(const HyperConnection& attention_mixer, const SelfAttention& full_attention,
+                           const HyperConnection& mlp_mixer, const SparseMoe& mlp, const q38_mlp_map* output_map)
+    : attention_mixer_(&attention_mixer), full_(&full_attention), mlp_mixer_(&mlp_mixer), mlp_(&mlp),
+      map_(output_map) {}
+
+DeviceTensor DecoderLayer::forward_verify_dense_batched(const DeviceTensor& streams, const DecoderLayerState& origin,
+                                                        std::vector<DecoderLayerState>& checkpoints) const {
+    const auto& s = streams.shape();
+    if (s.size() != 3 || s[0] != 1 || s[1] < 1 || s[1] > 16)
+        throw std::runtime_error("decoder batch must contain 1 to 16 matching rows");
+    const std::size_t rows = s[1];
+    checkpoints.clear();
+    checkpoints.resize(rows);
+    // attention half (src/decoder_layer.cpp:469-491)
+    const HyperConnectionRead attention = attention_mixer_->read(streams);
+    DeviceTensor outputs;
+    if (linear_) {
+        std::vector<GatedDeltaNetState> cps;
+        outputs = linear_->forward_verify(attention.mixed, origin.linear_attention, cps);
+        for (std::size_t r = 0; r < rows; ++r) checkpoints[r].linear_attention = std::move(cps[r]);
+    } else {
+        std::vector<SelfAttentionState> cps;
+        outputs = full_->forward_verify(attention.mixed, origin.full_attention, cps);
+        for (std::size_t r = 0; r < rows; ++r) checkpoints[r].full_attention = std::move(cps[r]);
+    }
+    DeviceTensor post = attention_mixer_->write(streams, outputs, attention.injection);
+    // MLP half (:493-497): read, MoE, output map, write, in place on the post-attention streams
+    std::lock_guard<std::mutex> lk(g_ws_mutex);
+    const std::size_t need = q38_verify_chain_hc_mapped_workspace_size(&mlp_->desc(), &mlp_mixer_->desc(),
+                                                                       static_cast<int32_t>(rows));
+    if (need == 0) throw std::runtime_error("decoder layer: no MLP-half workspace for these shapes");
+    if (workspace_.nbytes() < need) workspace_ = DeviceTensor({need}, DType::u32);
+    q38_moe_layer* layer = mlp_->handle();
+    q38_hc* mixer = mlp_mixer_->handle();
+    const q38_mlp_map* map = map_;
+    check(q38_verify_chain_hc_mapped(&layer, &mixer, &map, 1, static_cast<uint16_t*>(post.data()),
+                                     static_cast<int32_t>(rows), workspace_.data(), workspace_.nbytes(),
+                                     mlp_mixer_->context().stream()),
+          "DecoderLayer::forward_verify_dense_batched");
+    return post;
+}
+
 // ------------------------------------------------------------------ QwenModel (verify path)
 QwenModel::QwenModel(const Context& ctx, std::uint64_t seed, std::size_t layer_count, std::size_t vocab,
                      const MoeGeometry& geometry, std::size_t expert_count, std::size_t experts_per_token,

@@ -212,6 +212,7 @@ public:
 
     [[nodiscard]] q38_hc* handle() const noexcept { return hc_; }
     [[nodiscard]] const q38_hc_desc& desc() const noexcept { return desc_; }
+    [[nodiscard]] const Context& context() const noexcept { return *ctx_; }
 
 private:
     const Context* ctx_ = nullptr;
@@ -302,6 +303,43 @@ private:
     const Context* ctx_ = nullptr;
     q38_attn* attn_ = nullptr;
     std::size_t hidden_ = 0;
+    mutable DeviceTensor workspace_;
+};
+
+// ------------------------------------------------------------------ DecoderLayer (verify)
+// DecoderLayerState (include/qwen38/decoder_layer.hpp): the attention half's state of one
+// layer and slot, the linear-attention state or the full-attention KV cache (by layer kind).
+struct DecoderLayerState {
+    GatedDeltaNetState linear_attention;
+    SelfAttentionState full_attention;
+};
+
+// DecoderLayer::forward_verify_dense_batched (src/decoder_layer.cpp:447-504) over one layer's
+// components, referenced (the caller keeps them alive): the attention mixer, a GatedDeltaNet
+// or a SelfAttention, the MLP mixer, the SparseMoe and the optional MLP output map. The
+// per-layer embeddings (PLE, :457-467) are not part of this build.
+class DecoderLayer final {
+public:
+    DecoderLayer(const HyperConnection& attention_mixer, const GatedDeltaNet& linear_attention,
+                 const HyperConnection& mlp_mixer, const SparseMoe& mlp, const q38_mlp_map* output_map = nullptr);
+    DecoderLayer(const HyperConnection& attention_mixer, const SelfAttention& full_attention,
+                 const HyperConnection& mlp_mixer, const SparseMoe& mlp, const q38_mlp_map* output_map = nullptr);
+
+    // streams [1, S, HC * H] bf16, S = 1..16 (the mixers' row limit): attention mixer read,
+    // the attention step from origin (checkpoints receive the state after each row), the
+    // attention mixer's write, then the MLP half (mixer read, MoE, output map, mixer write).
+    // Returns the layer's output streams.
+    [[nodiscard]] DeviceTensor forward_verify_dense_batched(const DeviceTensor& streams, const DecoderLayerState& origin,
+                                                            std::vector<DecoderLayerState>& checkpoints) const;
+    [[nodiscard]] bool linear() const noexcept { return linear_ != nullptr; }
+
+private:
+    const HyperConnection* attention_mixer_ = nullptr;
+    const GatedDeltaNet* linear_ = nullptr;
+    const SelfAttention* full_ = nullptr;
+    const HyperConnection* mlp_mixer_ = nullptr;
+    const SparseMoe* mlp_ = nullptr;
+    const q38_mlp_map* map_ = nullptr;
     mutable DeviceTensor workspace_;
 };
 

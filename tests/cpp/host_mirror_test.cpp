@@ -483,6 +483,195 @@ static void self_attention_tests(const qwen38::Context& ctx) {
     std::printf("self attention: ok\n");
 }
 
+// DecoderLayer mirror (forward_verify_dense_batched) on a linear-attention layer and a
+// full-attention layer: the output equals the C ABI composition (mixer read, attention step,
+// mixer write, then the MLP half through q38_verify_chain_hc_mapped) bit for bit, the
+// checkpoints are the attention step's, and rows split over two calls chained through a
+// checkpoint equal the rows of one call.
+static void decoder_layer_tests(const qwen38::Context& ctx) {
+    const std::size_t H = 512, HCN = 4, R = 64, G = 64, K = H * HCN, S = 4;
+    std::uint64_t st = 0xBB67AE8584CAA73Bull;
+    auto next = [&] { st = st * 6364136223846793005ull + 1442695040888963407ull; return static_cast<std::uint32_t>(st >> 32); };
+    auto bf16 = [](float f) { std::uint32_t u; std::memcpy(&u, &f, 4); return static_cast<std::uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16); };
+    auto unit = [&] { return (static_cast<float>(next() >> 8) / 16777216.0f) - 0.5f; };
+    std::vector<qwen38::DeviceTensor> keep;
+    keep.reserve(64);
+    auto u32t = [&](std::size_t n) {
+        std::vector<std::uint32_t> h(n);
+        for (auto& v : h) v = next();
+        keep.emplace_back(std::vector<std::size_t>{n}, qwen38::DType::u32);
+        keep.back().upload(h.data(), n * 4);
+        return static_cast<const std::uint32_t*>(keep.back().data());
+    };
+    auto bft = [&](std::size_t n, float scale, float offset) {
+        std::vector<std::uint16_t> h(n);
+        for (auto& v : h) v = bf16(offset + scale * unit());
+        keep.emplace_back(std::vector<std::size_t>{n}, qwen38::DType::bf16);
+        keep.back().upload(h.data(), n * 2);
+        return static_cast<const std::uint16_t*>(keep.back().data());
+    };
+    auto mixer_weights = [&] {  // 4-bit centred groups, as in the mixer test
+        return q38_hc_weights{bft(K, 0.2f, 0.0f),
+                              u32t(R * K / 8), bft(R * K / G, 0.004f, 0.006f), bft(R * K / G, 0.002f, -0.045f),
+                              u32t(K * R / 8), bft(K * R / G, 0.004f, 0.006f), bft(K * R / G, 0.002f, -0.045f),
+                              u32t(HCN * K / 8), bft(HCN * K / G, 0.004f, 0.006f), bft(HCN * K / G, 0.002f, -0.045f)};
+    };
+    const q38_hc_weights aw = mixer_weights(), mw = mixer_weights();
+    qwen38::HyperConnection amix(ctx, aw, H, HCN, R, 4, G, 1e-6f, true);
+    qwen38::HyperConnection mmix(ctx, mw, H, HCN, R, 4, G, 1e-6f, true);
+    qwen38::MoeGeometry g;
+    g.hidden = H;
+    g.intermediate = 128;
+    qwen38::SparseMoe moe(ctx, 0x5EEDull, 7, 64, 4, true, g);
+    // a linear-attention block (the GatedDeltaNet test's geometry)
+    const std::size_t HK = 2, HV = 4, D = 128, C = 2 * HK * D + HV * D, VW = HV * D;
+    q38_gdn_weights gw{};
+    {
+        const std::size_t outs[5] = {C, VW, HV, HV, H}, ins[5] = {H, H, H, H, VW};
+        for (int p = 0; p < 5; ++p) {
+            gw.weight[p] = u32t(outs[p] * ins[p] / 4);
+            gw.scales[p] = bft(outs[p] * ins[p] / G, 0.0001f, 0.00015f);
+            gw.biases[p] = bft(outs[p] * ins[p] / G, 0.002f, -0.019f);
+        }
+        gw.conv = bft(C * 4, 1.0f, 0.0f);
+        gw.dt_bias = bft(HV, 1.0f, 0.0f);
+        gw.norm = bft(D, 0.5f, 1.0f);
+    }
+    std::vector<float> alog(HV, 0.5f);
+    qwen38::DeviceTensor alog_t({HV}, qwen38::DType::f32);
+    alog_t.upload(alog.data(), HV * 4);
+    gw.a_log = static_cast<const float*>(alog_t.data());
+    qwen38::GatedDeltaNet gdn(ctx, gw, H, HK, HV, D, D, 4, 8, static_cast<int>(G), false, "sigmoid", 1e-6f);
+    // a full-attention block (the SelfAttention test's geometry)
+    const std::size_t HQ = 4, HKV = 2, RD = 32, QW = HQ * D, KW = HKV * D, CAP = 40;
+    q38_attn_weights tw{};
+    {
+        const std::size_t outs[4] = {2 * QW, KW, KW, H}, ins[4] = {H, H, H, QW};
+        for (int p = 0; p < 4; ++p) {
+            tw.weight[p] = u32t(outs[p] * ins[p] / 4);
+            tw.scales[p] = bft(outs[p] * ins[p] / G, 0.0001f, 0.00015f);
+            tw.biases[p] = bft(outs[p] * ins[p] / G, 0.002f, -0.019f);
+        }
+        tw.q_norm = bft(D, 0.5f, 1.0f);
+        tw.k_norm = bft(D, 0.5f, 1.0f);
+    }
+    qwen38::SelfAttention attn(ctx, tw, H, HQ, HKV, D, RD, 8, static_cast<int>(G), false, false, 1e-6f, 1e6);
+
+    // streams of S rows
+    const std::uint16_t* emb = bft(S * H, 2.0f, 0.0f);
+    qwen38::DeviceTensor emb3({1, S, H}, qwen38::DType::bf16);
+    CHECK(hipMemcpy(emb3.data(), emb, S * H * 2, hipMemcpyDeviceToDevice) == hipSuccess);
+    const qwen38::DeviceTensor streams = qwen38::HyperConnection::initialize_stream(ctx, emb3, HCN);
+    auto rows_of = [&](const qwen38::DeviceTensor& t, std::size_t r0, std::size_t n) {
+        qwen38::DeviceTensor o({1, n, K}, qwen38::DType::bf16);
+        CHECK(hipMemcpy(o.data(), static_cast<const char*>(t.data()) + r0 * K * 2, n * K * 2,
+                        hipMemcpyDeviceToDevice) == hipSuccess);
+        return o;
+    };
+    // the MLP half through the C ABI, in place
+    auto mlp_half = [&](qwen38::DeviceTensor& x, std::size_t rows) {
+        qwen38::DeviceTensor ws({q38_verify_chain_hc_mapped_workspace_size(&moe.desc(), &mmix.desc(),
+                                                                            static_cast<int32_t>(rows))},
+                                qwen38::DType::u32);
+        q38_moe_layer* l = moe.handle();
+        q38_hc* m = mmix.handle();
+        CHECK(q38_verify_chain_hc_mapped(&l, &m, nullptr, 1, static_cast<std::uint16_t*>(x.data()),
+                                         static_cast<int32_t>(rows), ws.data(), ws.nbytes(), ctx.stream()) == Q38_OK);
+    };
+
+    {   // linear-attention layer
+        qwen38::DecoderLayer layer(amix, gdn, mmix, moe);
+        CHECK(layer.linear());
+        qwen38::DecoderLayerState origin;
+        origin.linear_attention.block = qwen38::DeviceTensor({gdn.state_bytes() / 2}, qwen38::DType::bf16);
+        {
+            std::vector<std::uint16_t> h(gdn.state_bytes() / 2);
+            for (auto& v : h) v = bf16(0.1f * unit());
+            origin.linear_attention.block.upload(h.data(), h.size() * 2);
+        }
+        origin.linear_attention.initialized = true;
+        std::vector<qwen38::DecoderLayerState> ck;
+        const qwen38::DeviceTensor out = layer.forward_verify_dense_batched(streams, origin, ck);
+        ctx.synchronize();
+        CHECK(ck.size() == S && out.shape() == streams.shape());
+        // the composition through the components and the C ABI
+        const qwen38::HyperConnectionRead rd = amix.read(streams);
+        std::vector<qwen38::GatedDeltaNetState> gck;
+        const qwen38::DeviceTensor go = gdn.forward_verify(rd.mixed, origin.linear_attention, gck);
+        qwen38::DeviceTensor post = amix.write(streams, go, rd.injection);
+        mlp_half(post, S);
+        ctx.synchronize();
+        const auto want = post.to_host<std::uint16_t>();
+        CHECK(out.to_host<std::uint16_t>() == want);
+        CHECK(out.to_host<std::uint16_t>() != streams.to_host<std::uint16_t>());
+        for (std::size_t r = 0; r < S; ++r) {
+            std::vector<std::uint16_t> a(gdn.state_bytes() / 2), b(gdn.state_bytes() / 2);
+            CHECK(hipMemcpy(a.data(), ck[r].linear_attention.data(), gdn.state_bytes(), hipMemcpyDeviceToHost) ==
+                  hipSuccess);
+            CHECK(hipMemcpy(b.data(), gck[r].data(), gdn.state_bytes(), hipMemcpyDeviceToHost) == hipSuccess);
+            CHECK(a == b);
+        }
+        // rows 0-1, then rows 2-3 from the checkpoint of row 1
+        std::vector<qwen38::DecoderLayerState> c1, c2;
+        const qwen38::DeviceTensor o1 = layer.forward_verify_dense_batched(rows_of(streams, 0, 2), origin, c1);
+        const qwen38::DeviceTensor o2 = layer.forward_verify_dense_batched(rows_of(streams, 2, 2), c1[1], c2);
+        ctx.synchronize();
+        const auto a1 = o1.to_host<std::uint16_t>(), a2 = o2.to_host<std::uint16_t>();
+        CHECK(std::equal(a1.begin(), a1.end(), want.begin()));
+        CHECK(std::equal(a2.begin(), a2.end(), want.begin() + static_cast<std::ptrdiff_t>(2 * K)));
+    }
+    {   // full-attention layer over a cache holding 20 tokens at position 100
+        qwen38::DecoderLayer layer(amix, attn, mmix, moe);
+        CHECK(!layer.linear());
+        auto fresh = [&] {
+            qwen38::DecoderLayerState o;
+            o.full_attention = attn.make_state(CAP, 100);
+            std::uint64_t s2 = 0x3C6EF372FE94F82Bull;
+            std::vector<std::uint16_t> h(o.full_attention.cache.numel());
+            for (auto& v : h) {
+                s2 = s2 * 6364136223846793005ull + 1442695040888963407ull;
+                v = bf16(static_cast<float>(static_cast<std::uint32_t>(s2 >> 40)) / 16777216.0f - 0.5f);
+            }
+            o.full_attention.cache.upload(h.data(), h.size() * 2);
+            o.full_attention.token_count = 20;
+            return o;
+        };
+        qwen38::DecoderLayerState origin = fresh();
+        std::vector<qwen38::DecoderLayerState> ck;
+        const qwen38::DeviceTensor out = layer.forward_verify_dense_batched(streams, origin, ck);
+        ctx.synchronize();
+        CHECK(ck.size() == S);
+        for (std::size_t r = 0; r < S; ++r) CHECK(ck[r].full_attention.token_count == 21 + r);
+        qwen38::DecoderLayerState o2 = fresh();
+        const qwen38::HyperConnectionRead rd = amix.read(streams);
+        std::vector<qwen38::SelfAttentionState> ack;
+        const qwen38::DeviceTensor ao = attn.forward_verify(rd.mixed, o2.full_attention, ack);
+        qwen38::DeviceTensor post = amix.write(streams, ao, rd.injection);
+        mlp_half(post, S);
+        ctx.synchronize();
+        const auto want = post.to_host<std::uint16_t>();
+        CHECK(out.to_host<std::uint16_t>() == want);
+        CHECK(origin.full_attention.cache.to_host<std::uint16_t>() == o2.full_attention.cache.to_host<std::uint16_t>());
+        // rows 0-1, then rows 2-3 from the checkpoint of row 1
+        qwen38::DecoderLayerState o3 = fresh();
+        std::vector<qwen38::DecoderLayerState> c1, c2;
+        const qwen38::DeviceTensor p1 = layer.forward_verify_dense_batched(rows_of(streams, 0, 2), o3, c1);
+        const qwen38::DeviceTensor p2 = layer.forward_verify_dense_batched(rows_of(streams, 2, 2), c1[1], c2);
+        ctx.synchronize();
+        const auto a1 = p1.to_host<std::uint16_t>(), a2 = p2.to_host<std::uint16_t>();
+        CHECK(std::equal(a1.begin(), a1.end(), want.begin()));
+        CHECK(std::equal(a2.begin(), a2.end(), want.begin() + static_cast<std::ptrdiff_t>(2 * K)));
+        CHECK(c2[1].full_attention.token_count == 24);
+    }
+    qwen38::DeviceTensor bad({1, 17, K}, qwen38::DType::bf16);
+    std::vector<qwen38::DecoderLayerState> ck;
+    qwen38::DecoderLayerState none;
+    CHECK(throws<std::runtime_error>([&] {
+        (void)qwen38::DecoderLayer(amix, gdn, mmix, moe).forward_verify_dense_batched(bad, none, ck);
+    }));
+    std::printf("decoder layer: ok\n");
+}
+
 // The draft head on HC streams (5 streams of the model's hidden size): forward_decode equals
 // the C ABI step bit for bit, the greedy chain equals a replay of single steps, and a
 // single-stream row is refused.
@@ -863,6 +1052,7 @@ static void gpu_tests() {
     gated_delta_net_tests(ctx);
     mtp_stream_tests(ctx, model);
     self_attention_tests(ctx);
+    decoder_layer_tests(ctx);
 }
 
 int main(int argc, char** argv) {

@@ -36,3 +36,4 @@ def test_gpu_section():
     assert "gated delta net: ok" in out, out
     assert "mtp streams: ok" in out, out
     assert "self attention: ok" in out, out
+    assert "decoder layer: ok" in out, out
