@@ -726,6 +726,125 @@ def main():
         log(f"attention verify step (4 rows, {k_}, 2048 / 16 + 2 heads of 256, Q8/g64): {v_['us_per_call']:.1f} "
             f"us/call, {v_['gbps']:.0f} GB/s of {v_['bytes_per_call'] / 1e6:.1f} MB")
 
+    # ---------------------------------------------------------------- full decoder layer
+    # DecoderLayer::forward_verify_dense_batched (src/decoder_layer.cpp:447-504) at 4 rows:
+    # attention mixer read -> the attention step (a GatedDeltaNet layer from an origin state
+    # with 4 checkpoints, or full attention over 4,096 cached tokens) -> mixer write -> the
+    # MLP half (mixer read -> config-1 MoE -> mixer write), the streams carried through NLd
+    # layers of one kind (4 streams, rank-256 4-bit mixers, the GDN / attention legs'
+    # geometries); eager launches, median of 10 passes.
+    def decoder_leg(kind, S=4, NLd=4, HCn=4, Rn=256, T0=4096):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(SEED + 17)
+
+        def bf(shape, lo, hi):
+            return (torch.rand(shape, generator=gen, device=dev) * (hi - lo) + lo).to(torch.bfloat16).view(torch.int16)
+
+        def affine(pairs, keep):
+            ws_, ss_, bs_ = [], [], []
+            for O, IN in pairs:
+                wt = torch.randint(-2 ** 31, 2 ** 31 - 1, (O, IN // 4), generator=gen, device=dev, dtype=torch.int32)
+                sc, bi = bf((O, IN // 64), 0.5e-4, 1.5e-4), bf((O, IN // 64), -0.02, -0.01)
+                keep += [wt, sc, bi]
+                ws_.append(wt.data_ptr())
+                ss_.append(sc.data_ptr())
+                bs_.append(bi.data_ptr())
+            return ws_, ss_, bs_
+
+        hdesc = q38.HcDesc(H, HCn, Rn, 4, 64, 1, 1e-6)
+        amix = [q38.Hc(ctx, hdesc, hc_tensors(gen, HCn, Rn)) for _ in range(NLd)]
+        mmix = [q38.Hc(ctx, hdesc, hc_tensors(gen, HCn, Rn)) for _ in range(NLd)]
+        moes = [q38.MoeLayer(ctx, q38.desc(), seed=SEED, layer=l) for l in range(NLd)]
+        keep, blocks, states = [], [], []
+        cap = T0 + 64
+        for _ in range(NLd):
+            hb = C.c_void_p()
+            if kind == "linear":
+                HKg, HVg, Dg = 16, 32, 128
+                C_ = 2 * HKg * Dg + HVg * Dg
+                w = q38.GdnWeights()
+                ws_, ss_, bs_ = affine(((C_, H), (HVg * Dg, H), (HVg, H), (HVg, H), (H, HVg * Dg)), keep)
+                for p_ in range(5):
+                    w.weight[p_], w.scales[p_], w.biases[p_] = ws_[p_], ss_[p_], bs_[p_]
+                conv, alog, dtb, nrm = bf((C_, 4), -0.5, 0.5), torch.rand(HVg, generator=gen, device=dev) * 2.0, \
+                    bf((HVg,), -0.5, 0.5), bf((Dg,), 0.5, 1.5)
+                keep += [conv, alog, dtb, nrm]
+                w.conv, w.a_log, w.dt_bias, w.norm = conv.data_ptr(), alog.data_ptr(), dtb.data_ptr(), nrm.data_ptr()
+                dsc = q38.GdnDesc(H, HKg, HVg, Dg, Dg, 4, 8, 64, 0, 0, 1e-6)
+                q38.check(q38.lib.q38_gdn_create(ctx.h, C.byref(dsc), C.byref(w), C.byref(hb)))
+                states.append(bf((q38.lib.q38_gdn_state_bytes(hb) // 2,), -0.05, 0.05))
+            else:
+                HQ, HKV, Dg = 16, 2, 256
+                w = q38.AttnWeights()
+                ws_, ss_, bs_ = affine(((2 * HQ * Dg, H), (HKV * Dg, H), (HKV * Dg, H), (H, HQ * Dg)), keep)
+                for p_ in range(4):
+                    w.weight[p_], w.scales[p_], w.biases[p_] = ws_[p_], ss_[p_], bs_[p_]
+                qn, kn = bf((Dg,), 0.5, 1.5), bf((Dg,), 0.5, 1.5)
+                keep += [qn, kn]
+                w.q_norm, w.k_norm = qn.data_ptr(), kn.data_ptr()
+                dsc = q38.AttnDesc(H, HQ, HKV, Dg, 64, 8, 64, 0, 0, 1e-6, 1e7)
+                q38.check(q38.lib.q38_attn_create(ctx.h, C.byref(dsc), C.byref(w), C.byref(hb)))
+                states.append(bf((q38.lib.q38_attn_cache_bytes(hb, cap) // 2,), -1.0, 1.0))
+            blocks.append(hb)
+        try:
+            emb = torch.empty((S, H), dtype=torch.int16, device=dev)
+            toks_d = (C.c_uint32 * S)(*[11 + 7 * r for r in range(S)])
+            q38.check(q38.lib.q38_embed_synthetic(SEED, toks_d, S, H, emb.data_ptr(), sp))
+            st0 = torch.empty((S, HCn * H), dtype=torch.int16, device=dev)
+            q38.check(q38.lib.q38_hc_initialize_stream(emb.data_ptr(), S, H, HCn, st0.data_ptr(), sp))
+            sth = st0.clone()
+            mixed_d = torch.empty((S, H), dtype=torch.int16, device=dev)
+            inj_d = torch.empty((S, HCn), dtype=torch.int16, device=dev)
+            y_d = torch.empty((S, H), dtype=torch.int16, device=dev)
+            wsm = torch.empty(amix[0].workspace_size(S), dtype=torch.uint8, device=dev)
+            wsc = torch.empty(q38.lib.q38_verify_chain_hc_mapped_workspace_size(C.byref(moes[0].desc), C.byref(hdesc),
+                                                                                S), dtype=torch.uint8, device=dev)
+            if kind == "linear":
+                sbytes = q38.lib.q38_gdn_state_bytes(blocks[0])
+                ck = torch.empty(S * sbytes, dtype=torch.uint8, device=dev)
+                wsb = torch.empty(q38.lib.q38_gdn_workspace_size(blocks[0], S), dtype=torch.uint8, device=dev)
+            else:
+                wsb = torch.empty(q38.lib.q38_attn_workspace_size(blocks[0], S, T0 + S), dtype=torch.uint8, device=dev)
+
+            def one_pass():
+                for li in range(NLd):
+                    amix[li].read(sth, S, mixed_d, inj_d, wsm, sp)
+                    if kind == "linear":
+                        q38.check(q38.lib.q38_gdn_verify(blocks[li], mixed_d.data_ptr(), S, states[li].data_ptr(),
+                                                         ck.data_ptr(), y_d.data_ptr(), wsb.data_ptr(), wsb.numel(), sp))
+                    else:
+                        q38.check(q38.lib.q38_attn_verify(blocks[li], mixed_d.data_ptr(), S, states[li].data_ptr(), cap,
+                                                          T0, T0, y_d.data_ptr(), wsb.data_ptr(), wsb.numel(), sp))
+                    amix[li].write(sth, y_d, inj_d, S, sth, sp)
+                    lar = (C.c_void_p * 1)(moes[li].h.value)
+                    mar = (C.c_void_p * 1)(mmix[li].h.value)
+                    q38.check(q38.lib.q38_verify_chain_hc_mapped(lar, mar, None, 1, sth.data_ptr(), S, wsc.data_ptr(),
+                                                                 wsc.numel(), sp))
+            sth.copy_(st0)
+            one_pass()
+            ts = []
+            for _ in range(10):
+                sth.copy_(st0)
+                ev0.record(stream)
+                one_pass()
+                ev1.record(stream)
+                torch.cuda.synchronize()
+                ts.append(1e3 * ev0.elapsed_time(ev1) / NLd)
+            return float(np.median(ts))
+        finally:
+            for hb in blocks:
+                (q38.lib.q38_gdn_destroy if kind == "linear" else q38.lib.q38_attn_destroy)(hb)
+            for m in amix + mmix:
+                m.close()
+            for L in moes:
+                L.close()
+
+    dec_cfg = {"rows": 4, "layers": 4, "streams": 4, "mixer_rank": 256,
+               "linear_layer_us": decoder_leg("linear"), "full_attention_layer_us_ctx4096": decoder_leg("full"),
+               "note": "eager launches; attention mixer read, GDN or attention step, mixer write, MLP half"}
+    log(f"full decoder layer verify (4 rows): GDN layer {dec_cfg['linear_layer_us']:.1f} us, attention layer "
+        f"(4,096 cached tokens) {dec_cfg['full_attention_layer_us_ctx4096']:.1f} us")
+
     if args.copy_calibration:
         # a plain device copy of known size for the FETCH_SIZE / WRITE_SIZE calibration runs
         nb = 256 << 20
@@ -953,7 +1072,7 @@ def main():
             "algorithmic_bytes_per_launch_m4": {k.split()[0]: v[1] for k, v in kernels.items()},
             "config3_prefill": prefill_cfg,
             "config4_mixed": mixed_cfg, "config1_group64": g64_cfg, "config1_u8_books": u8_cfg, "decoder_mlp_half_hc": hc_cfg,
-            "gdn_verify_step": gdn_cfg,
+            "gdn_verify_step": gdn_cfg, "decoder_layer_verify": dec_cfg,
             "attention_verify_step": attn_cfg,
             "config2_sampled": sampled_cfg,
             "config2_learned_drafts": learned_cfg,
