@@ -2,7 +2,8 @@
 // SparseMoe::forward_prefill_impl segmented path (src/sparse_moe.cpp:2199-2624).
 //
 //   k_logits_rows  router logits, NE router rows per workgroup held in registers across
-//                  64 request rows (the per-lane summation contract of the verify router)
+//                  the workgroup's request rows (the per-lane summation contract of the
+//                  verify router), and the shared expert's gate
 //   k_topk_rows    softmax + top-k of every row (one wave per row, R2)
 //   k_plan_sort    gather-by-expert plan of all routes (R3, the stable sort of
 //                  src/sparse_moe.cpp:2260-2271): a counting sort by expert in one
@@ -28,46 +29,85 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 // ============================================================== router (R1)
-// Workgroup (gx, gy): router rows [NE gx, NE gx + NE) (row E is w_sg) against request rows
-// [64 gy, 64 gy + 64), wave w taking rows 64 gy + w, + 4, ... Lane l accumulates
+// Workgroup (gx, gy): routed router rows [NE gx, NE gx + NE) against request rows
+// [rpw gy, rpw gy + rpw), wave w taking rows rpw gy + w, + 8, ... Lane l accumulates
 // x*w over the columns 512t + 8l + j (t outer, j inner) with fmaf, then the xor butterfly
-// and BF16 rounding: the logits equal the verify router's bit for bit.
+// and BF16 rounding: the logits equal the verify router's bit for bit. The launch sizes rpw
+// so that the grid is resident at once (one pass of workgroups per CU slot, no partial
+// second pass).
 // planar: the fp16 copy of x is stored chunk-planar ([2][M][H / 2]: dims 4c..4c+3 of every
 // subvector in plane c), the layout the LDS-codebook gate/up kernel reads its B operand from.
+constexpr int kLogitsWaves = 8;
+
 template <int T, int NE>
-__global__ __launch_bounds__(256) void k_logits_rows(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ x,
-                                                     int planar) {
+__global__ __launch_bounds__(64 * kLogitsWaves) void k_logits_rows(LayerDev L, MoeBufs B, int M, const uint16_t* __restrict__ x,
+                                                     int planar, int rpw) {
     constexpr int H = 512 * T;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int e0 = blockIdx.x * NE;
-    const int nr = L.E + (L.has_shared ? 1 : 0);
+    const int nr = L.E;
     uint4 wv[NE][T];
 #pragma unroll
     for (int n = 0; n < NE; ++n) {
         const int e = e0 + n < nr ? e0 + n : nr - 1;
-        const uint16_t* w = e < L.E ? L.router + static_cast<size_t>(e) * H : L.wsg;
+        const uint16_t* w = L.router + static_cast<size_t>(e) * H;
 #pragma unroll
         for (int t = 0; t < T; ++t) wv[n][t] = *reinterpret_cast<const uint4*>(w + 512 * t + 8 * lane);
     }
     const bool store_x = blockIdx.x == 0 && x != B.x;
-    const int r1 = (static_cast<int>(blockIdx.y) + 1) * 64 < M ? (blockIdx.y + 1) * 64 : M;
-    // the next request row's inputs are loaded while this row's dot products run (the
-    // prefetch of the last row repeats it: always in bounds)
-    uint4 xn[T];
-    {
-        const int r0 = blockIdx.y * 64 + wave < r1 ? blockIdx.y * 64 + wave : r1 - 1;
+    const int rb = static_cast<int>(blockIdx.y) * rpw;
+    const int r1 = rb + rpw < M ? rb + rpw : M;
+    if (rb >= r1) return;
+    auto load_row = [&](int r, uint4 (&v)[T]) {
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-            xn[t] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(r0) * H + 512 * t + 8 * lane);
+        for (int t = 0; t < T; ++t) v[t] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(r) * H + 512 * t + 8 * lane);
+    };
+    // the request rows two and one steps ahead are in flight while a row's dot products run
+    // (past the end the last row again: always in bounds)
+    uint4 xa[T], xb[T];
+    load_row(rb + wave < r1 ? rb + wave : r1 - 1, xa);
+    load_row(rb + wave + kLogitsWaves < r1 ? rb + wave + kLogitsWaves : r1 - 1, xb);
+    // the router bias of the lane's logits (loop-invariant: loaded once, so that no load in the
+    // loop waits behind the prefetches)
+    float rbias[scatter_slots<NE>()];
+#pragma unroll
+    for (int s = 0; s < scatter_slots<NE>(); ++s) {
+        const int e = e0 + scatter_value<NE>(s, lane >> 4);
+        rbias[s] = L.rbias ? L.rbias[e < nr ? e : nr - 1] : 0.0f;
     }
-    for (int r = blockIdx.y * 64 + wave; r < r1; r += 4) {
+    // The shared expert's gate row (w_sg), spread over the grid's columns: wave 0 of column gx
+    // takes request rows rb + gx, rb + gx + gridDim.x, ... of its range, with the same lane
+    // contract; sgate = T(sigmoid(T(logit))).
+    if (L.has_shared && wave == 0) {
+        uint4 ws[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) ws[t] = *reinterpret_cast<const uint4*>(L.wsg + 512 * t + 8 * lane);
+        for (int r = rb + static_cast<int>(blockIdx.x); r < r1; r += gridDim.x) {
+            uint4 xs[T];
+            load_row(r, xs);
+            float a = 0.0f;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const uint32_t xq[4] = {xs[t].x, xs[t].y, xs[t].z, xs[t].w};
+                const uint32_t wq[4] = {ws[t].x, ws[t].y, ws[t].z, ws[t].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    a = __builtin_fmaf(bflo(xq[k]), bflo(wq[k]), a);
+                    a = __builtin_fmaf(bfhi(xq[k]), bfhi(wq[k]), a);
+                }
+            }
+            a = wave_sum_xor(a);
+            if (lane == 0) B.sgate[r] = rbf(1.0f / (1.0f + expf(-rbf(a))));
+        }
+    }
+    for (int r = rb + wave; r < r1; r += kLogitsWaves) {
         uint4 xv[T];
 #pragma unroll
-        for (int t = 0; t < T; ++t) xv[t] = xn[t];
-        const int rn = r + 4 < r1 ? r + 4 : r;
-#pragma unroll
-        for (int t = 0; t < T; ++t)
-            xn[t] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(rn) * H + 512 * t + 8 * lane);
+        for (int t = 0; t < T; ++t) {
+            xv[t] = xa[t];
+            xa[t] = xb[t];
+        }
+        load_row(r + 2 * kLogitsWaves < r1 ? r + 2 * kLogitsWaves : r1 - 1, xb);
         float acc[NE];
 #pragma unroll
         for (int n = 0; n < NE; ++n) acc[n] = 0.0f;
@@ -92,8 +132,7 @@ __global__ __launch_bounds__(256) void k_logits_rows(LayerDev L, MoeBufs B, int 
             const int e = e0 + scatter_value<NE>(s, lane >> 4);
             if ((lane & 15) == 0 && e < nr) {
                 const float lg = rbf(acc[s]);
-                if (e < L.E) B.logits[static_cast<size_t>(r) * L.E + e] = L.rbias ? lg + L.rbias[e] : lg;
-                else B.sgate[r] = rbf(1.0f / (1.0f + expf(-lg)));
+                B.logits[static_cast<size_t>(r) * L.E + e] = L.rbias ? lg + rbias[s] : lg;
             }
         }
         if (store_x) {
@@ -135,13 +174,15 @@ constexpr int kSortMax = 32768;  // routes per call (rows x k); route ids fit 16
 // [2 + 2MK + i] route at sorted position i, [2 + 3MK + route] its sorted position.
 //
 // The plan is a stable counting sort of the routes by expert (routes keep ascending order
-// within an expert), in one workgroup of 16 waves. Wave w owns the contiguous routes
+// within an expert), in one workgroup of 16 waves; the routes' experts are first copied into
+// LDS (every load in flight at once), so neither walk waits on memory. Wave w owns the contiguous routes
 // [w c, w c + c) and walks them 64 at a time in order; within such a batch, lanes with the
 // same expert find each other with one ballot per expert-id bit, and a lane's rank is the
 // number of lower lanes in its group.
 //   A: every group's last lane adds the group size to cnt[w][e];
 //   B: per expert, a scan over experts of the totals (and of the nonzero flags: the slot
-//      numbers) gives its first position, and a scan over waves turns cnt[w][e] into wave
+//      numbers; shuffles within a wave, then the wave totals) gives its first position,
+//      and a scan over waves turns cnt[w][e] into wave
 //      w's first position within the expert;
 //   C: the walk again: position = cnt[w][e] + rank, the group's last lane advances cnt.
 // Counts and positions are below 2^16 (MK <= kSortMax), so cnt holds 16-bit values.
@@ -162,35 +203,55 @@ __device__ __forceinline__ void plan_group(int e, bool valid, int lane, int& ran
 
 __global__ __launch_bounds__(1024) void k_plan_sort(MoeBufs B, int MK, int E) {
     __shared__ uint16_t cnt[kPlanWaves][kPlanExperts];
-    __shared__ uint32_t scan[kPlanExperts];
+    __shared__ uint32_t wtot[kPlanWaves];
+    extern __shared__ uint16_t ex[];  // [MK] expert of every route
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    for (int i = tid; i < kPlanWaves * kPlanExperts; i += 1024) (&cnt[0][0])[i] = 0;
+    // Every route's expert into LDS at once (all loads in flight before the first store), the
+    // counters cleared behind them; the walks then read LDS only.
+    {
+        constexpr int PT = kSortMax / 1024;
+        int v[PT];
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            const int i = tid + 1024 * k;
+            v[k] = i < MK ? B.experts[i] : 0;
+        }
+        for (int i = tid; i < kPlanWaves * kPlanExperts / 8; i += 1024)
+            reinterpret_cast<uint4*>(&cnt[0][0])[i] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            const int i = tid + 1024 * k;
+            if (i < MK) ex[i] = static_cast<uint16_t>(v[k]);
+        }
+    }
     __syncthreads();
     const int c = (MK + kPlanWaves - 1) / kPlanWaves;
     const int r0 = w * c < MK ? w * c : MK, r1 = r0 + c < MK ? r0 + c : MK;
     for (int b = r0; b < r1; b += 64) {  // A
         const int i = b + lane;
         const bool valid = i < r1;
-        const int e = valid ? B.experts[i] : 0;
+        const int e = valid ? ex[i] : 0;
         int rank, n;
         plan_group(e, valid, lane, rank, n);
         if (valid && rank == n - 1) cnt[w][e] = static_cast<uint16_t>(cnt[w][e] + n);
     }
     __syncthreads();
-    // B: tid = expert. scan holds total | (total > 0) << 16 (totals sum to MK < 2^16).
+    // B: tid = expert. The scanned value is total | (total > 0) << 16 (totals sum to MK <
+    // 2^16): an inclusive scan within each wave by shuffles, then the wave totals in order.
     uint32_t tot = 0;
     if (tid < E)
         for (int v = 0; v < kPlanWaves; ++v) tot += cnt[v][tid];
     const uint32_t own = tot | (tot ? 1u << 16 : 0u);
-    scan[tid] = own;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {  // inclusive scan
-        const uint32_t t = tid >= off ? scan[tid - off] : 0u;
-        __syncthreads();
-        scan[tid] += t;
-        __syncthreads();
+    uint32_t incl = own;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
     }
-    const uint32_t excl = scan[tid] - own;
+    if (lane == 63) wtot[w] = incl;
+    __syncthreads();
+    for (int v = 0; v < w; ++v) incl += wtot[v];
+    const uint32_t excl = incl - own;
     int32_t* plan = B.plan;
     if (tid < E && tot) {
         const int slot = static_cast<int>(excl >> 16);
@@ -198,7 +259,7 @@ __global__ __launch_bounds__(1024) void k_plan_sort(MoeBufs B, int MK, int E) {
         plan[1 + MK + slot] = static_cast<int>(excl & 0xFFFFu);
     }
     if (tid == 1023) {
-        const int nu = static_cast<int>(scan[1023] >> 16);
+        const int nu = static_cast<int>(incl >> 16);
         plan[0] = nu;
         plan[1 + MK + nu] = MK;
     }
@@ -214,7 +275,7 @@ __global__ __launch_bounds__(1024) void k_plan_sort(MoeBufs B, int MK, int E) {
     for (int b = r0; b < r1; b += 64) {  // C
         const int i = b + lane;
         const bool valid = i < r1;
-        const int e = valid ? B.experts[i] : 0;
+        const int e = valid ? ex[i] : 0;
         int rank, n;
         plan_group(e, valid, lane, rank, n);
         if (valid) {
@@ -824,12 +885,37 @@ __global__ __launch_bounds__(256) void k_swiglu_seg(MoeBufs B, int I, int64_t to
     }
 }
 
+int router_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+        n = 256;
+    return n;
+}
+
 template <int T>
 hipError_t launch_router_rows_t(const LayerDev& L, const MoeBufs& B, int M, const uint16_t* x, hipStream_t st) {
     constexpr int NE = T <= 2 ? 8 : T <= 4 ? 4 : 2;  // router rows in registers: 16 T NE <= 128 VGPRs
-    const int nr = L.E + (L.has_shared ? 1 : 0);
+    // workgroups resident at once (per instantiation; every device here is the same part)
+    static std::atomic<int> resident{0};
+    int slots = resident.load(std::memory_order_relaxed);
+    if (slots == 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(k_logits_rows<T, NE>),
+                                                         64 * kLogitsWaves, 0) != hipSuccess || nb < 1)
+            nb = 1;
+        slots = nb * router_cus();
+        resident.store(slots, std::memory_order_relaxed);
+    }
+    // request rows per workgroup: the grid fills the resident slots once (at least one row
+    // per wave)
+    const int gx = (L.E + NE - 1) / NE;
+    int gy = slots / gx;
+    gy = gy < 1 ? 1 : gy > (M + kLogitsWaves - 1) / kLogitsWaves ? (M + kLogitsWaves - 1) / kLogitsWaves : gy;
+    const int rpw = (M + gy - 1) / gy;
+    gy = (M + rpw - 1) / rpw;
     const int planar = prefill_planes(L, M) == 2 ? 1 : 0;
-    return launch(k_logits_rows<T, NE>, dim3((nr + NE - 1) / NE, (M + 63) / 64), dim3(256), 0, st, L, B, M, x, planar);
+    return launch(k_logits_rows<T, NE>, dim3(gx, gy), dim3(64 * kLogitsWaves), 0, st, L, B, M, x, planar, rpw);
 }
 
 } // namespace
@@ -863,7 +949,9 @@ hipError_t launch_topk_rows(const LayerDev& L, const MoeBufs& B, int M, hipStrea
 
 hipError_t launch_plan_sort(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
     if (M * L.K > kSortMax || L.E > kPlanExperts) return hipErrorInvalidValue;
-    return launch(k_plan_sort, dim3(1), dim3(1024), 0, st, B, M * L.K, L.E);
+    const size_t lds = static_cast<size_t>(M * L.K) * 2;
+    if (const hipError_t e = ensure_lds<k_plan_sort>(kSortMax * 2); e != hipSuccess) return e;
+    return launch(k_plan_sort, dim3(1), dim3(1024), lds, st, B, M * L.K, L.E);
 }
 
 static int pf_slots(const LayerDev& L, int M) {
