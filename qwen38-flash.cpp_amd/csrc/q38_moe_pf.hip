@@ -652,24 +652,28 @@ __device__ __forceinline__ void seg_range(int n_items, int per_type, int idx, in
     i1 = static_cast<int>(static_cast<int64_t>(idx + 1) * n_items / per_type);
 }
 
-// LDS of the kernels: the codebook chunk at 0, then (gate/up) the K-part partial sums, then
-// the unit table.
-template <int NSUB>
-constexpr size_t gu_seg_red_bytes() {
-    return size_t{2} * (NSUB / 128 - 1) * (8 / (NSUB / 128)) * 2 * 64 * 16;
-}
-
-// Gate/up (NSUB = H / 8 subvectors per row: 128, 256 or 512). Output rows of an item:
+// Gate/up (NSUB = H / 8 subvectors per row: 128 or 256; at 512 the K-part partial sums of
+// four K parts would not fit in LDS beside the 128 KiB codebook chunk). Output rows of an item:
 // TR = 32 * RG rows of I; chunk `chunk` of projection `proj` per workgroup type. B = rows of
 // the chunk-planar fp16 inputs ([2][M][H / 2]).
 template <int NSUB>
 __global__ __launch_bounds__(kSegThreads) void k_gu_seg(LayerDev L, MoeBufs B, int M) {
     constexpr int KP = NSUB / 128, RG = 8 / KP, TR = 32 * RG, KS = NSUB / 32;
     static_assert(NSUB % 128 == 0 && KP * RG == 8, "8 waves = K parts x row groups");
-    extern __shared__ __align__(16) unsigned char lds[];
+    // One static LDS block (the codebook chunk at offset 0, known when compiling, so a gather's
+    // address is its code offset alone), the K-part partial sums ([2][KP - 1][RG][2][64]) and
+    // the unit table.
+    constexpr int RED = 2 * (KP - 1) * RG * 2 * 64;
+    struct Lds {
+        uint2 book[kSegKent];
+        f4_t red[RED > 0 ? RED : 1];
+        SegTab T;
+    };
+    __shared__ Lds S;
+    unsigned char* lds = reinterpret_cast<unsigned char*>(S.book);
     const unsigned char* book = lds;
-    f4_t* red = reinterpret_cast<f4_t*>(lds + kSegKent * 8);  // [2][KP - 1][RG][2][64]
-    SegTab& T = *reinterpret_cast<SegTab*>(lds + kSegKent * 8 + gu_seg_red_bytes<NSUB>());
+    f4_t* red = S.red;
+    SegTab& T = S.T;
     touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kh = wave % KP, rg = wave / KP;
@@ -783,9 +787,16 @@ __global__ __launch_bounds__(kSegThreads) void k_dn_seg(LayerDev L, MoeBufs B, i
     constexpr int SPL = NSUB / 4, TR = 256, KS = NSUB / 32;
     static_assert(SPL == 16 || SPL == 32, "16-code or 32-code lane spans");
     constexpr int NW = SPL == 32 ? 14 : 7, NB = SPL / 2;
-    extern __shared__ __align__(16) unsigned char lds[];
+    // one static LDS block: the codebook chunk at offset 0 (a gather's address is its code
+    // offset alone), then the unit table
+    struct Lds {
+        uint2 book[kSegKent];
+        SegTab T;
+    };
+    __shared__ Lds S;
+    unsigned char* lds = reinterpret_cast<unsigned char*>(S.book);
     const unsigned char* book = lds;
-    SegTab& T = *reinterpret_cast<SegTab*>(lds + kSegKent * 8);
+    SegTab& T = S.T;
     touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int)>();
     const int tid = threadIdx.x, lane = tid & 63, rg = tid >> 6;
     const int r16 = lane & 15, q = lane >> 4;
@@ -960,7 +971,7 @@ static int pf_slots(const LayerDev& L, int M) {
 }
 
 // The LDS-codebook kernels serve layers with 4-dim codebook chunks and the tiled codes
-// (d8/14-bit, H / 8 = 128, 256 or 512, I / 8 = 64 or 128) when every workgroup's units fit
+// (d8/14-bit, H / 8 = 128 or 256, I / 8 = 64 or 128) when every workgroup's units fit
 // its table; others take the tile kernels.
 static int64_t seg_units_per_wg(const LayerDev& L, int M, int tiles, int per_type) {
     const int64_t MK = static_cast<int64_t>(M) * L.K;
@@ -974,7 +985,7 @@ int prefill_planes(const LayerDev& L, int M) {
     for (int p = 0; p < 3; ++p)
         if (!L.p[p].book4 || !L.p[p].codes_t) return 1;
     const int gn = L.H / 8, dn = L.I / 8;
-    if ((gn != 128 && gn != 256 && gn != 512) || (dn != 64 && dn != 128)) return 1;
+    if ((gn != 128 && gn != 256) || (dn != 64 && dn != 128)) return 1;
     const int gu_rows = 32 * (8 / (gn / 128));  // output rows of a gate/up item
     if (L.I % gu_rows || L.H % 256 || L.E + 1 > kSegMaxSlots) return 1;
     const int grid = mfma_grid();
@@ -986,15 +997,11 @@ int prefill_planes(const LayerDev& L, int M) {
 
 template <int NSUB>
 hipError_t launch_gu_seg_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    constexpr size_t lds = size_t{kSegKent} * 8 + gu_seg_red_bytes<NSUB>() + sizeof(SegTab);
-    if (const hipError_t e = ensure_lds<k_gu_seg<NSUB>>(lds); e != hipSuccess) return e;
-    return launch(k_gu_seg<NSUB>, dim3(mfma_grid()), dim3(kSegThreads), lds, st, L, B, M);
+    return launch(k_gu_seg<NSUB>, dim3(mfma_grid()), dim3(kSegThreads), 0, st, L, B, M);
 }
 template <int NSUB>
 hipError_t launch_dn_seg_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
-    constexpr size_t lds = size_t{kSegKent} * 8 + sizeof(SegTab);
-    if (const hipError_t e = ensure_lds<k_dn_seg<NSUB>>(lds); e != hipSuccess) return e;
-    return launch(k_dn_seg<NSUB>, dim3(mfma_grid()), dim3(kSegThreads), lds, st, L, B, M);
+    return launch(k_dn_seg<NSUB>, dim3(mfma_grid()), dim3(kSegThreads), 0, st, L, B, M);
 }
 
 hipError_t launch_gate_up_pf(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
@@ -1002,7 +1009,6 @@ hipError_t launch_gate_up_pf(const LayerDev& L, const MoeBufs& B, int M, hipStre
         switch (L.H / 8) {
             case 128: return launch_gu_seg_t<128>(L, B, M, st);
             case 256: return launch_gu_seg_t<256>(L, B, M, st);
-            case 512: return launch_gu_seg_t<512>(L, B, M, st);
             default: return hipErrorInvalidValue;
         }
     }
