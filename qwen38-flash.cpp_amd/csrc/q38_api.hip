@@ -2048,6 +2048,11 @@ int q38_verify_chain_hc(q38_moe_layer* const* layers, q38_hc* const* mixers, int
         Q38_HIP(launch_router(dev, w, rows, mixed, false, 0.0f, st));
         Q38_HIP(launch_shared_affine(dev, w, rows, st));
         if (!moe_plans_in_gate_up(ex, rows)) Q38_HIP(launch_topk_plan(ex, w, rows, st));
+        if (moe_uses_fused(ex, rows) && !dev.shared_affine) {
+            // gate/up, down and the combine into the streams in one launch
+            Q38_HIP(launch_gate_down4(ex, w, rows, stream, nullptr, st, inj, hd0.streams));
+            continue;
+        }
         Q38_HIP(launch_gate_up(ex, w, rows, st));
         Q38_HIP(launch_down(ex, w, rows, st));
         Q38_HIP(launch_combine_hc(dev, w, rows, stream, inj, hd0.streams, st));

@@ -314,7 +314,10 @@ constexpr int kWaitLimit = 1 << 16;
 void set_wait_limit(int spins);  // < 0: kWaitLimit
 int wait_limit();
 hipError_t read_wait_status(uint32_t* status, bool clear);
-hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st);
+// HC > 0: h holds the rows' HC streams, and the combine writes the output into every stream
+// with the injection weights inj ([M][HC]) as k_combine_hc does.
+hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st,
+                             const uint16_t* inj = nullptr, int HC = 0);
 int mfma_grid();  // persistent workgroups of the expert kernels (a multiple of 32)
 // Prefill widths, kMaxRows < M <= kMaxPrefillRows (q38_moe_pf.hip), one kernel each:
 // router logits, per-row top-k, sorted plan, segmented gate/up, SwiGLU, segmented down

@@ -649,9 +649,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 // broken; then the affected outputs are NaN instead of the kernel hanging, and the device's
 // wait status records it for the API to report (q38_ctx_synchronize).
 constexpr int kCombineWgs = 32;
+// HC > 0: h is the rows' HyperConnection streams ([M][HC][H]) and the output goes into every
+// stream as k_combine_hc writes it, T(stream + T(y * inj[r][s])), instead of h <- T(h + y).
 template <int KT>
 __device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B, int M, const float* wt, uint16_t* h,
-                                             uint16_t* out) {
+                                             uint16_t* out, const uint16_t* inj, int HC) {
     const int w = static_cast<int>(blockIdx.x) - static_cast<int>(gridDim.x - kCombineWgs);
     Q38_STAMP(24576, 0);
     const int H = L.H, MK = M * KT;
@@ -663,7 +665,17 @@ __device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B
 #pragma unroll
     for (int s = 0; s < KT; ++s) in.wts[s] = wt[r * KT + s];
     in.wts[KT] = B.sgate[r];
-    const uint16_t hraw = (h ? h : out)[static_cast<size_t>(r) * H + o];  // (unused without h)
+    const uint16_t hraw = HC > 0 ? 0 : (h ? h : out)[static_cast<size_t>(r) * H + o];  // (unused without h)
+    uint16_t sv[kHcMaxStreams], gv[kHcMaxStreams];
+    const size_t srow = (static_cast<size_t>(r) * HC) * H + o;
+    if (HC > 0) {
+#pragma unroll
+        for (int s = 0; s < kHcMaxStreams; ++s)
+            if (s < HC) {
+                sv[s] = h[srow + static_cast<size_t>(s) * H];
+                gv[s] = inj[r * HC + s];
+            }
+    }
     auto load = [&] {
 #pragma unroll
         for (int s = 0; s <= KT; ++s) {
@@ -689,8 +701,15 @@ __device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B
     Q38_STAMPV(24576, 2, in.dv[0][0]);
     const float y = combine_value<KT, true>(L, in);
     const size_t i = static_cast<size_t>(r) * H + o;
-    if (h) h[i] = f2bf(rbf(bf2f(hraw) + y));
-    else out[i] = f2bf(y);
+    if (HC > 0) {
+#pragma unroll
+        for (int s = 0; s < kHcMaxStreams; ++s)
+            if (s < HC) h[srow + static_cast<size_t>(s) * H] = f2bf(bf2f(sv[s]) + rbf(y * bf2f(gv[s])));
+    } else if (h) {
+        h[i] = f2bf(rbf(bf2f(hraw) + y));
+    } else {
+        out[i] = f2bf(y);
+    }
     Q38_STAMP(24576, 3);
 }
 
@@ -698,7 +717,8 @@ __device__ __forceinline__ void combine_tail(const LayerDev& L, const MoeBufs& B
 // layout; the two kernels' G8 = 8 item code).
 template <int BITS, int NSUB_GU, int NSUB_DN, int NCHUNK, int DG, int DD, int KT, int G8 = 0>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gd4(LayerDev L, MoeBufs B, int M,
-                                                                                         uint16_t* h, uint16_t* out) {
+                                                                                         uint16_t* h, uint16_t* out,
+                                                                                         const uint16_t* inj, int HC) {
     static_assert(2 * NSUB_GU == 512, "the gate/up half uses the 8 waves of the down half");
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int32_t ex[kNarrowMaxRoutes];
@@ -706,12 +726,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     __shared__ int32_t plan[kNarrowPlan];
     __shared__ int32_t slot_pos[(kNarrowMaxRoutes + 1) * 4];
     __shared__ __align__(16) uint2 hs[kNarrow * NSUB_DN];
-    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + sizeof(int) + 2 * sizeof(void*)>();
+    touch_kernargs<sizeof(LayerDev) + sizeof(MoeBufs) + 2 * sizeof(int) + 3 * sizeof(void*)>();
     u4_t fill[(1 << BITS) / 2 / 512];  // the down codebook chunk, requested by the gate/up half
     gu4_body<BITS, NSUB_GU, NCHUNK, DG, G8, true>(L, B, M, lds, ex, plan, slot_pos, fill, wt);
     lds_barrier();  // every wave is done with the gate/up codebook chunk
     dn4_body<BITS, NSUB_DN, NCHUNK, DD, G8, true>(L, B, M, lds, plan, hs, fill);
-    if (h || out) combine_tail<KT>(L, B, M, wt, h, out);
+    if (h || out) combine_tail<KT>(L, B, M, wt, h, out, inj, HC);
     Q38_STAMP(24576, 4);
 }
 
@@ -722,11 +742,13 @@ hipError_t launch_gu4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t 
     return launch(k_gu4<BITS, NSUB, NCHUNK, D, G8>, dim3(mfma_grid()), dim3(2 * NSUB), lds, st, L, B, M);
 }
 template <int DG, int DD, int G8>
-hipError_t launch_gd4_t(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
+hipError_t launch_gd4_t(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st,
+                        const uint16_t* inj, int HC) {
     constexpr size_t lds = gu4_lds_bytes<14, 256, 2>();
     static_assert(lds >= (size_t{1} << 14) * 8 + 4 * 64 * 16, "the down half's LDS fits the gate/up half's");
     if (const hipError_t e = ensure_lds<k_gd4<14, 256, 64, 2, DG, DD, 10, G8>>(lds); e != hipSuccess) return e;
-    return launch(k_gd4<14, 256, 64, 2, DG, DD, 10, G8>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M, h, out);
+    return launch(k_gd4<14, 256, 64, 2, DG, DD, 10, G8>, dim3(mfma_grid()), dim3(512), lds, st, L, B, M, h, out, inj,
+                  HC);
 }
 template <int BITS, int NSUB, int NCHUNK, int D, int G8 = 0>
 hipError_t launch_dn4_t(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
@@ -847,20 +869,22 @@ bool moe_uses_fused(const LayerDev& L, int M) {
 
 // Ring depths of the two halves (as the two kernels pick them: every item's loads in flight
 // at once where registers allow; items beyond take the loop).
-hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st) {
+hipError_t launch_gate_down4(const LayerDev& L, const MoeBufs& B, int M, uint16_t* h, uint16_t* out, hipStream_t st,
+                             const uint16_t* inj, int HC) {
     if (!moe_uses_fused(L, M)) return hipErrorInvalidValue;
+    if (HC < 0 || HC > kHcMaxStreams || (HC > 0 && (!h || !inj || out))) return hipErrorInvalidValue;
     const int grid = mfma_grid();
     const int c = ring_items(L, M, L.I / 64, grid / 32 * 8);
     if (L.p[0].ngrp != 1) {  // 64-input scale groups
-        if (c <= 2) return launch_gd4_t<2, 1, 8>(L, B, M, h, out, st);
-        if (c <= 3) return launch_gd4_t<3, 2, 8>(L, B, M, h, out, st);
-        if (c <= 4) return launch_gd4_t<4, 2, 8>(L, B, M, h, out, st);
-        return launch_gd4_t<6, 3, 8>(L, B, M, h, out, st);
+        if (c <= 2) return launch_gd4_t<2, 1, 8>(L, B, M, h, out, st, inj, HC);
+        if (c <= 3) return launch_gd4_t<3, 2, 8>(L, B, M, h, out, st, inj, HC);
+        if (c <= 4) return launch_gd4_t<4, 2, 8>(L, B, M, h, out, st, inj, HC);
+        return launch_gd4_t<6, 3, 8>(L, B, M, h, out, st, inj, HC);
     }
-    if (c <= 2) return launch_gd4_t<2, 1, 0>(L, B, M, h, out, st);
-    if (c <= 3) return launch_gd4_t<3, 2, 0>(L, B, M, h, out, st);
-    if (c <= 4) return launch_gd4_t<4, 2, 0>(L, B, M, h, out, st);
-    return launch_gd4_t<6, 3, 0>(L, B, M, h, out, st);
+    if (c <= 2) return launch_gd4_t<2, 1, 0>(L, B, M, h, out, st, inj, HC);
+    if (c <= 3) return launch_gd4_t<3, 2, 0>(L, B, M, h, out, st, inj, HC);
+    if (c <= 4) return launch_gd4_t<4, 2, 0>(L, B, M, h, out, st, inj, HC);
+    return launch_gd4_t<6, 3, 0>(L, B, M, h, out, st, inj, HC);
 }
 
 hipError_t launch_gate_up4(const LayerDev& L, const MoeBufs& B, int M, hipStream_t st) {
