@@ -191,6 +191,33 @@ def chain_hc(q38, layers, mixers, stream_np):
     return G.to_host(st, np.uint16)
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_chain_hc_fused_tail_equals_split_path(gpu, q38, M):
+    """At 1-4 rows the HC chain's MoE is the fused gate/up + down kernel whose combine tail
+    writes the streams; with the fused kernel switched off the same chain takes the split
+    kernels and k_combine_hc. Both give the same streams bit for bit over 2 layers."""
+    from moe_cases import SEED
+    rng = np.random.default_rng(90 + M)
+    layers = [q38.MoeLayer(gpu, q38.desc(), seed=SEED, layer=l) for l in range(2)]
+    built = [build(q38, gpu, rng) for _ in range(2)]
+    mixers = [b[2] for b in built]
+    try:
+        stream = to_bf16_bits(rng.normal(0, 1.0, (M, 4 * 2048)).astype(np.float32))
+        fused = chain_hc(q38, layers, mixers, stream)
+        q38.lib.q38_set_fused_layers(0)
+        try:
+            split = chain_hc(q38, layers, mixers, stream)
+        finally:
+            q38.lib.q38_set_fused_layers(1)
+        assert np.array_equal(fused, split)
+        assert not np.array_equal(fused, stream)
+    finally:
+        for L in layers:
+            L.close()
+        for h in mixers:
+            h.close()
+
+
 def test_chain_hc_layers(gpu, q38, orc):
     """The decoder's MLP half over 3 layers (mixer read -> MoE -> mixer write) at 4 rows:
     the fused chain equals the layer-by-layer composition of q38_hc_read, q38_moe_forward and
