@@ -17,7 +17,7 @@
 //                    sums), and per query the tile's max and float sum of exp(s - max);
 //   k_attn_stats     per query: the max over its tiles and the sum of the tiles' sums scaled
 //                    to it;
-//   k_attn_pv        per (256-token tile, kv head, 64 queries): p = T(exp(s - max) / sum) as
+//   k_attn_pv        per (128-token tile, kv head, 64 queries): p = T(exp(s - max) / sum) as
 //                    the A operand of bf16 MFMA against the tile's values (staged transposed in
 //                    LDS, 64 tokens at a time), one float partial row per (tile, query);
 //   k_attn_combine   per query: the tiles' partials added in a fixed order, rounded, times the
@@ -34,7 +34,7 @@ namespace q38 {
 namespace {
 
 constexpr int kTok = 64;     // tokens per score tile (and per P.V sub-tile)
-constexpr int kPvTok = 256;  // tokens per P.V tile
+constexpr int kPvTok = 128;  // tokens per P.V tile (256: 70.6 -> 63.9 us per 4-row call at 4K tokens)
 constexpr int kPvMt = 4;     // 16-query M-tiles per P.V workgroup
 
 __device__ __forceinline__ float tbf(float v) { return bf2f(f2bf(v)); }
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void k_attn_stats(AttnDev A, AttnBufs B, int S
     }
 }
 
-// P.V of one 256-token tile (four 64-token sub-tiles) of kv head g for a DW-dim slice and
+// P.V of one 128-token tile (two 64-token sub-tiles) of kv head g for a DW-dim slice and
 // M-tiles mt0 .. mt0 + kPvMt - 1 of the group's queries, on v_mfma_f32_16x16x32_bf16: the
 // sub-tile's values of the slice are staged transposed in LDS ([dim][token], rows padded by 16
 // bytes; the next sub-tile's loads are in flight while the current one computes); A = p =

@@ -131,7 +131,7 @@ def test_full_size_layer(gpu, q38, orc):
 def test_rows_chain_through_the_cache(gpu, q38):
     L = AttnLayer(seed=5)
     rng = np.random.default_rng(5)
-    T0, S, cap = 290, 6, 300   # the rows cross a 256-token tile
+    T0, S, cap = 380, 6, 390   # the rows cross a 128-token P.V tile and a 64-token score tile
     keys, values = L.random_cache(rng, cap, T0)
     x = to16(rng.normal(0, 1, (S, L.hidden)), 0)
     dev = DevAttn(q38, gpu, L, cap)
