@@ -46,6 +46,7 @@ __global__ __launch_bounds__(64) void k_attn_prework(AttnDev A, AttnBufs B, uint
                                                      uint16_t* __restrict__ values, int64_t cap, int64_t T0,
                                                      int64_t position) {
     __shared__ float nv[64 * CPL];
+    __shared__ float csk[32 * CPL], snk[32 * CPL];  // the rotary table of this row: pair k's T(cos), T(sin)
     const int head = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
     const int HQ = A.hq, HKV = A.hkv, D = A.d, R = A.rot, half = R / 2;
     const int QW = HQ * D, KW = HKV * D;
@@ -78,16 +79,22 @@ __global__ __launch_bounds__(64) void k_attn_prework(AttnDev A, AttnBufs B, uint
         const int i = lane * CPL + c;
         nv[i] = tbf(bf2f(wn[i]) * tbf(x[c] * inv));
     }
-    __syncthreads();
+    // one rotary pair per lane (the two elements of a pair share its angle), in double as
+    // before: pos * theta^(-2k / R)
     const double pos = static_cast<double>(position + r);
+    for (int k = lane; k < half; k += 64) {
+        const double ang = pos * pow(A.theta, -2.0 * static_cast<double>(k) / static_cast<double>(R));
+        csk[k] = tbf(static_cast<float>(cos(ang)));
+        snk[k] = tbf(static_cast<float>(sin(ang)));
+    }
+    __syncthreads();
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int i = lane * CPL + c;
         float y = nv[i];
         if (i < R) {
             const int k = i < half ? i : i - half;
-            const double ang = pos * pow(A.theta, -2.0 * static_cast<double>(k) / static_cast<double>(R));
-            const float cs = tbf(static_cast<float>(cos(ang))), sn = tbf(static_cast<float>(sin(ang)));
+            const float cs = csk[k], sn = snk[k];
             const float rot = i < half ? -nv[i + half] : nv[i - half];
             y = tbf(tbf(nv[i] * cs) + tbf(rot * sn));
         }
